@@ -1,0 +1,129 @@
+/*
+ * refcpu — CPU restatement of GoNeuron's pure-Go float32 training step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity oracle: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and only
+ * as the checker or the timed CPU baseline.  The product (libgoneuron_hip.so)
+ * never links, loads or calls it.
+ *
+ * It follows the reference per-sample algorithm line by line (file:line
+ * citations point into the GoNeuron tree):
+ *   Network.trainBatchSequential      internal/net/net.go:721-784
+ *   Network.trainBatchParallel        internal/net/net.go:588-717 (W workers)
+ *   Dense                             internal/layer/layer.go:224-667
+ *   matMulOptimized (summation order) internal/layer/matmul_optimized.go:18-152
+ *   activations                       internal/activations/activations.go:22-236,345-352
+ *   CrossEntropy / MSE                internal/loss/loss.go:53-178
+ *   Adam                              internal/opt/opt.go:117-258
+ *   Dropout                           internal/layer/dropout.go:47-401
+ *   Conv2D                            internal/layer/conv2d.go:114-1174
+ *   MaxPool2D                         internal/layer/maxpool2d.go:106-410,508-513
+ *   Flatten                           internal/layer/reshape.go:64-96
+ *   RNG                               internal/layer/layer.go:61-81
+ * Built with -O2 -ffp-contract=off (Go amd64 GOAMD64=v1 emits no FMA).
+ */
+#ifndef GN_REFCPU_H
+#define GN_REFCPU_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Activation object kinds (activations.go).  `is_ptr` mirrors Go's value vs
+ * pointer receiver distinction that cacheActivationType (layer.go:183-205)
+ * depends on. */
+enum {
+  GNO_ACT_NIL = 0,
+  GNO_ACT_RELU = 1,
+  GNO_ACT_SIGMOID = 2,
+  GNO_ACT_TANH = 3,
+  GNO_ACT_SOFTMAX = 4,
+  GNO_ACT_LOGSOFTMAX = 5,
+  GNO_ACT_LINEAR = 6,
+};
+
+enum {
+  GNO_LAYER_DENSE = 1,
+  GNO_LAYER_DROPOUT = 2,
+  GNO_LAYER_CONV2D = 3,
+  GNO_LAYER_MAXPOOL2D = 4,
+  GNO_LAYER_FLATTEN = 5,
+  GNO_LAYER_EMBEDDING = 6,
+  GNO_LAYER_POSENC = 7,
+  GNO_LAYER_TRANSFORMER = 8,
+  GNO_LAYER_CLSPOOL = 9,
+  GNO_LAYER_LSTM_UNROLLER = 10,
+};
+
+enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
+
+typedef struct gno_layer_spec {
+  int32_t kind;
+  int32_t in_size;      /* Dense in / Dropout size / Flatten size / LSTM input */
+  int32_t out_size;     /* Dense out / LSTM hidden */
+  int32_t act;          /* GNO_ACT_* */
+  int32_t act_is_ptr;   /* 1: &activations.X{} ; 0: activations.X{} value */
+  int32_t in_channels;  /* Conv2D / MaxPool2D (-1 = lazy) */
+  int32_t out_channels;
+  int32_t kernel, stride, padding;
+  float p;              /* Dropout */
+  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim;
+  int32_t return_sequences;
+} gno_layer_spec;
+
+typedef struct gno_net gno_net;
+
+/* LCG (layer.go:61-81). */
+float gno_rand_float(uint64_t *state);
+/* Synthetic data: uniform U[0,1) stream, N(0,1) Box-Muller pairs, class ids. */
+void gno_fill_uniform(float *dst, int64_t n, uint64_t seed);
+void gno_fill_normal(float *dst, int64_t n, uint64_t seed);
+void gno_fill_class_ids(int32_t *dst, int64_t n, int32_t nclass, uint64_t seed);
+
+gno_net *gno_net_create(const gno_layer_spec *specs, int32_t nlayers,
+                        int32_t loss_kind, float lr, int32_t workers);
+void gno_net_destroy(gno_net *n);
+int64_t gno_net_nparams(const gno_net *n);
+int64_t gno_net_layer_param_offset(const gno_net *n, int32_t layer);
+int64_t gno_net_layer_param_count(const gno_net *n, int32_t layer);
+float *gno_net_params(gno_net *n);
+float *gno_net_grads(gno_net *n);
+float *gno_net_adam_m(gno_net *n);
+float *gno_net_adam_v(gno_net *n);
+int32_t gno_net_adam_timestep(const gno_net *n);
+/* One TrainBatch: x is B x in (row major), y is B x out. Returns mean loss.
+ * workers==1 -> trainBatchSequential; >1 -> trainBatchParallel chunking. */
+float gno_net_train_batch(gno_net *n, const float *x, const float *y, int32_t B);
+/* Same as train_batch but stops before Step (grads hold the averaged batch
+ * gradient), for gradient parity checks. */
+float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32_t B);
+void gno_net_step(gno_net *n);
+/* Forward of one sample (training flag as set); writes out, returns out len. */
+int32_t gno_net_forward(gno_net *n, const float *x, float *out);
+void gno_net_set_training(gno_net *n, int32_t training);
+int32_t gno_net_out_size(const gno_net *n);
+/* Per-layer probes for unit tests: argmax of a MaxPool2D layer after the last
+ * forward (count returned), last saved pre-activation of layer `layer`. */
+int32_t gno_net_layer_argmax(gno_net *n, int32_t layer, int32_t *dst, int32_t cap);
+int32_t gno_net_layer_preact(gno_net *n, int32_t layer, float *dst, int32_t cap);
+
+/* Stand-alone kernels of the reference (for golden-vector checks). */
+void gno_activate_batch(int32_t act, float *x, int32_t n);            /* softmax/logsoftmax */
+float gno_activate(int32_t act, float x);
+float gno_derivative(int32_t act, float x);
+float gno_loss_forward(int32_t loss_kind, const float *pred, const float *y, int32_t n);
+void gno_loss_backward(int32_t loss_kind, const float *pred, const float *y, float *grad, int32_t n);
+/* Adam.StepInPlace with the optimizer's timestep already advanced to `timestep`
+ * (NewStep increments before the update; opt.go:237-258). */
+void gno_adam_step_inplace(float *params, const float *grads, float *m, float *v,
+                           int64_t n, float lr, float beta1, float beta2, float eps,
+                           int32_t timestep);
+/* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
+void gno_matmul(const float *in, const float *w, const float *bias, float *out,
+                int32_t batch, int32_t in_size, int32_t out_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,356 @@
+"""Pins the CPU oracle against the reference's own fixtures and known answers,
+and against what the mathematics fixes (closed forms, brute force, autograd).
+
+Fixtures: tests/golden/pytorch_refs/* are the data files the reference keeps in
+scripts/pytorch_validation/test_data/pytorch_refs (consumed by
+internal/validation/pytorch_validation_test.go:164-346).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "pytorch_refs")
+
+
+def fx(name, f):
+    return np.fromfile(os.path.join(GOLD, name, f + ".bin"), dtype="<f4")
+
+
+def meta(name):
+    with open(os.path.join(GOLD, name, "metadata.json")) as fh:
+        return json.load(fh)
+
+
+# ---------------------------------------------------------------- fixtures
+@pytest.mark.parametrize("name", ["dense_simple", "dense_batch"])
+def test_dense_forward_fixture(oracle, name):
+    m = meta(name)
+    B, I = m["inputs"]["input"]["shape"]
+    O = m["inputs"]["weights"]["shape"][0]
+    x = fx(name, "input").reshape(B, I)
+    w = fx(name, "weights").reshape(O, I)
+    b = fx(name, "biases")
+    out = oracle.matmul(x, w, b)
+    np.testing.assert_allclose(out, fx(name, "output").reshape(B, O), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("name,act", [("activation_softmax", 4), ("activation_log_softmax", 5)])
+def test_softmax_fixtures(oracle, name, act):
+    x = fx(name, "input").reshape(2, 3)
+    exp = fx(name, "output").reshape(2, 3)
+    for r in range(2):
+        np.testing.assert_allclose(oracle.activate_batch(act, x[r]), exp[r], atol=1e-6)
+
+
+@pytest.mark.parametrize("name,act", [("activation_relu", 1), ("activation_sigmoid", 2),
+                                      ("activation_tanh", 3)])
+def test_scalar_activation_fixtures(oracle, name, act):
+    x = fx(name, "input")
+    got = np.array([oracle.lib().gno_activate(act, float(v)) for v in x], np.float32)
+    np.testing.assert_allclose(got, fx(name, "output"), atol=1e-6)
+
+
+def test_softmax_known_answers(oracle):
+    # activations_pytorch_test.go:92-150
+    cases = [([1, 2, 3], [0.09003057317, 0.2447284710, 0.6652409558]),
+             ([0, 0, 0], [1 / 3] * 3), ([-1, 0, 1], [0.09003057317, 0.2447284710, 0.6652409558]),
+             ([2.0], [1.0])]
+    for x, e in cases:
+        np.testing.assert_allclose(oracle.activate_batch(oracle.ACT_SOFTMAX, x), e, atol=1e-6)
+    cases = [([1, 2, 3], [-2.407605964, -1.407605964, -0.4076059643]),
+             ([0, 0, 0], [-1.098612289] * 3), ([2.0], [0.0])]
+    for x, e in cases:
+        np.testing.assert_allclose(oracle.activate_batch(oracle.ACT_LOGSOFTMAX, x), e, atol=1e-6)
+
+
+def test_mse_fixture(oracle):
+    got = oracle.loss_forward(oracle.LOSS_MSE, fx("loss_mse", "y_pred"), fx("loss_mse", "y_true"))
+    assert abs(got - fx("loss_mse", "loss")[0]) <= 1e-6
+    g = oracle.loss_backward(oracle.LOSS_MSE, fx("loss_mse", "y_pred"), fx("loss_mse", "y_true"))
+    np.testing.assert_allclose(g, 0.5 * (fx("loss_mse", "y_pred") - fx("loss_mse", "y_true")), rtol=1e-6)
+
+
+def test_cross_entropy_probability_semantics(oracle):
+    # The fixture is PyTorch logits-CE; the reference's CE takes probabilities
+    # (loss.go:120-141).  softmax(logits) fed to the reference CE must give the
+    # fixture's per-row mean.
+    logits = fx("loss_cross_entropy", "logits").reshape(2, 3)
+    tgt = fx("loss_cross_entropy", "targets").astype(int)
+    total = 0.0
+    for r in range(2):
+        p = oracle.activate_batch(oracle.ACT_SOFTMAX, logits[r])
+        y = np.zeros(3, np.float32)
+        y[tgt[r]] = 1
+        total += oracle.loss_forward(oracle.LOSS_CE, p, y)
+    assert abs(total / 2 - fx("loss_cross_entropy", "loss")[0]) < 1e-6
+
+
+def test_cross_entropy_clip_constant(oracle):
+    # Q5: CE over log-probabilities clips at 1e-10 -> -log(1e-10) per sample.
+    logp = oracle.activate_batch(oracle.ACT_LOGSOFTMAX, np.random.default_rng(0).normal(size=50))
+    y = np.zeros(50, np.float32)
+    y[7] = 1
+    assert abs(oracle.loss_forward(oracle.LOSS_CE, logp, y) - 23.02585) < 1e-4
+
+
+def test_adam_fixture_t1(oracle):
+    # optimizer_adam_step stores the t=1 update; StepInPlace with timestep 0.
+    p = fx("optimizer_adam_step", "param").copy()
+    g = fx("optimizer_adam_step", "grad")
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    oracle.adam_step(p, g, m, v, float(fx("optimizer_adam_step", "lr")[0]),
+                     float(fx("optimizer_adam_step", "beta1")[0]),
+                     float(fx("optimizer_adam_step", "beta2")[0]),
+                     float(fx("optimizer_adam_step", "eps")[0]), 0)
+    np.testing.assert_allclose(p, fx("optimizer_adam_step", "param_updated"), rtol=1e-6)
+
+
+def test_adam_network_first_step_closed_form(oracle):
+    # Q1: Network.Step calls NewStep first, so the first update uses t = 2.
+    # Closed form in float64: dp = lr*sqrt(1-b2^2)/(1-b1^2) * (1-b1) g / (sqrt((1-b2) g^2) + eps)
+    rng = np.random.default_rng(1)
+    g = rng.normal(size=1000).astype(np.float32)
+    p = np.zeros(1000, np.float32)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    oracle.adam_step(p, g, m, v, lr, b1, b2, eps, 1)
+    gd = g.astype(np.float64)
+    b1f, b2f = float(np.float32(b1)), float(np.float32(b2))
+    eff = lr * math.sqrt(1 - b2f ** 2) / (1 - b1f ** 2)
+    exp = -eff * (1 - b1f) * gd / (np.sqrt((1 - b2f) * gd * gd) + eps)
+    np.testing.assert_allclose(p, exp, rtol=2e-5, atol=1e-9)
+
+
+# ---------------------------------------------------------------- layer known answers
+def test_maxpool_known_answer(oracle):
+    # maxpool2d_test.go:8-35, 152-173
+    net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
+                     oracle.LOSS_MSE)
+    out = net.forward(np.arange(1, 17, dtype=np.float32))
+    np.testing.assert_array_equal(out, [6, 8, 14, 16])
+    np.testing.assert_array_equal(net.argmax(0), [5, 7, 13, 15])
+
+
+def test_maxpool_tie_first_wins(oracle):
+    net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
+                     oracle.LOSS_MSE)
+    net.forward(np.ones(16, np.float32))
+    np.testing.assert_array_equal(net.argmax(0), [0, 2, 8, 10])
+
+
+def test_dense_tanh_identity(oracle):
+    # layer_test.go:15-45
+    net = oracle.Net([oracle.spec(oracle.LAYER_DENSE, in_size=2, out_size=2, act=oracle.ACT_TANH)],
+                     oracle.LOSS_MSE)
+    net.params[:] = [1, 0, 0, 1, 0, 0]
+    out = net.forward(np.array([1, 2], np.float32))
+    np.testing.assert_allclose(out, [math.tanh(1), math.tanh(2)], atol=1e-6)
+
+
+def test_dense_init_closed_form(oracle):
+    # Dense.Build layer.go:300-320: RNG(in*1000+out*100+42), W then b.
+    net = oracle.Net([oracle.spec(oracle.LAYER_DENSE, in_size=3, out_size=2, act=oracle.ACT_RELU)],
+                     oracle.LOSS_MSE)
+    s = (3 * 1000 + 2 * 100 + 42)
+    vals = []
+    for _ in range(8):
+        s = (s * 6364136223846793005 + 1) % (1 << 64)
+        vals.append(np.float32(s >> 33) / np.float32(2 ** 31))
+    scale = np.float32(math.sqrt(2 / 5))
+    exp = [np.float32(np.float32(u * np.float32(2)) * scale) - scale for u in vals[:6]]
+    exp += [np.float32(u * np.float32(0.2)) - np.float32(0.1) for u in vals[6:]]
+    np.testing.assert_array_equal(net.params, np.array(exp, np.float32))
+
+
+def test_dropout_mask_reset_determinism(oracle):
+    # dropout_test.go:134-161 (Reset => identical mask); Q9 closed form.
+    net = oracle.Net([oracle.spec(oracle.LAYER_DROPOUT, in_size=128, p=0.2)], oracle.LOSS_MSE)
+    x = np.ones(128, np.float32)
+    a = net.forward(x)
+    b = net.forward(x)
+    np.testing.assert_array_equal(a, b)
+    s = 42
+    keep = []
+    for _ in range(128):
+        s = (s * 6364136223846793005 + 1) % (1 << 64)
+        keep.append(not (np.float32(s >> 33) / np.float32(2 ** 31) < np.float32(0.2)))
+    scale = np.float32(1) / (np.float32(1) - np.float32(0.2))
+    np.testing.assert_array_equal(a, np.where(keep, scale, 0).astype(np.float32))
+
+
+def _direct_conv(x, w, b, stride, pad):
+    C, H, W = x.shape
+    O, _, K, _ = w.shape
+    oH = (H + 2 * pad - K) // stride + 1
+    oW = (W + 2 * pad - K) // stride + 1
+    xp = np.zeros((C, H + 2 * pad, W + 2 * pad), np.float64)
+    xp[:, pad:pad + H, pad:pad + W] = x
+    out = np.zeros((O, oH, oW), np.float64)
+    for o in range(O):
+        for i in range(oH):
+            for j in range(oW):
+                out[o, i, j] = (xp[:, i * stride:i * stride + K, j * stride:j * stride + K] * w[o]).sum() + b[o]
+    return out
+
+
+def test_conv_generic_matches_brute_force(oracle):
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(2, 6, 6)).astype(np.float32)
+    net = oracle.Net([oracle.spec(oracle.LAYER_CONV2D, in_size=72, in_channels=2, out_channels=3, kernel=3,
+                                  stride=2, padding=1, act=oracle.ACT_LINEAR)], oracle.LOSS_MSE)
+    w = net.params[:54].reshape(3, 2, 3, 3)
+    b = net.params[54:57]
+    out = net.forward(x.ravel())
+    np.testing.assert_allclose(out, _direct_conv(x, w, b, 2, 1).ravel(), rtol=1e-5, atol=1e-5)
+
+
+def test_conv3x3_fast_path_quirk(oracle):
+    # Q7 (conv2d.go:265-357): interior rows skip columns 0 and W-1 -> bias only;
+    # every other position is the true convolution.
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(3, 8, 8)).astype(np.float32)
+    net = oracle.Net([oracle.spec(oracle.LAYER_CONV2D, in_size=192, in_channels=3, out_channels=4, kernel=3,
+                                  stride=1, padding=1, act=oracle.ACT_LINEAR)], oracle.LOSS_MSE)
+    w = net.params[:108].reshape(4, 3, 3, 3)
+    b = net.params[108:112]
+    out = net.forward(x.ravel()).reshape(4, 8, 8)
+    ref = _direct_conv(x, w, b, 1, 1)
+    mask = np.ones((8, 8), bool)
+    mask[1:7, 0] = False
+    mask[1:7, 7] = False
+    np.testing.assert_allclose(out[:, mask], ref[:, mask], rtol=1e-5, atol=1e-5)
+    for o in range(4):
+        np.testing.assert_array_equal(out[o, 1:7, 0], np.full(6, b[o], np.float32))
+        np.testing.assert_array_equal(out[o, 1:7, 7], np.full(6, b[o], np.float32))
+
+
+# ---------------------------------------------------------------- gradients vs autograd
+torch = pytest.importorskip("torch")
+
+
+def _torch_dense_stack(params, sizes, acts, x, y, out_kind):
+    """Autograd of the per-sample reference step, expressed in float64 torch.
+
+    out_kind 'softmax_ce' / 'logsoftmax_ce' reproduces Q4: the loss gradient
+    p - y is fed through the activation's Jacobian (z -> p), exactly what
+    Dense.Backward does with CrossEntropy.BackwardInPlace's output."""
+    P = torch.tensor(params.astype(np.float64), requires_grad=True)
+    off = 0
+    h = torch.tensor(x.astype(np.float64))
+    for (i, o), a in zip(sizes, acts):
+        W = P[off:off + i * o].view(o, i)
+        b = P[off + i * o: off + i * o + o]
+        off += i * o + o
+        z = h @ W.T + b
+        if a == "relu":
+            h = torch.relu(z)
+        elif a == "softmax":
+            h = torch.softmax(z, dim=1)
+        elif a == "logsoftmax":
+            h = torch.log_softmax(z, dim=1)
+        else:
+            h = z
+    yt = torch.tensor(y.astype(np.float64))
+    B = x.shape[0]
+    if out_kind == "mse":
+        loss = ((h - yt) ** 2).mean(dim=1).sum() / B
+        loss.backward()
+    else:
+        g = (h - yt).detach() / B
+        h.backward(g)
+    return P.grad.numpy()
+
+
+@pytest.mark.parametrize("out_act,act_code", [("softmax", 4), ("logsoftmax", 5)])
+def test_dense_stack_grads_vs_autograd(oracle, out_act, act_code):
+    rng = np.random.default_rng(5)
+    sizes = [(12, 16), (16, 16), (16, 7)]
+    specs = [oracle.spec(oracle.LAYER_DENSE, in_size=12, out_size=16, act=oracle.ACT_RELU),
+             oracle.spec(oracle.LAYER_DENSE, in_size=16, out_size=16, act=oracle.ACT_RELU),
+             oracle.spec(oracle.LAYER_DENSE, in_size=16, out_size=7, act=act_code, act_is_ptr=1)]
+    net = oracle.Net(specs, oracle.LOSS_CE)
+    B = 8
+    x = rng.normal(size=(B, 12)).astype(np.float32)
+    y = np.eye(7, dtype=np.float32)[rng.integers(0, 7, B)]
+    p0 = net.params.copy()
+    net.accumulate_batch(x, y, B)
+    exp = _torch_dense_stack(p0, sizes, ["relu", "relu", out_act], x, y, "ce")
+    got = net.grads
+    assert np.abs(got - exp).max() / np.abs(exp).max() < 1e-5
+
+
+def test_dense_mse_grads_vs_autograd(oracle):
+    rng = np.random.default_rng(6)
+    sizes = [(10, 9), (9, 3)]
+    specs = [oracle.spec(oracle.LAYER_DENSE, in_size=10, out_size=9, act=oracle.ACT_RELU),
+             oracle.spec(oracle.LAYER_DENSE, in_size=9, out_size=3, act=oracle.ACT_LINEAR)]
+    net = oracle.Net(specs, oracle.LOSS_MSE, workers=3)
+    B = 7
+    x = rng.normal(size=(B, 10)).astype(np.float32)
+    y = rng.normal(size=(B, 3)).astype(np.float32)
+    p0 = net.params.copy()
+    net.accumulate_batch(x, y, B)
+    exp = _torch_dense_stack(p0, sizes, ["relu", "linear"], x, y, "mse")
+    assert np.abs(net.grads - exp).max() / np.abs(exp).max() < 1e-5
+
+
+def test_conv_pool_grads_vs_autograd(oracle):
+    # Conv (generic path, k3 s2 p1 so Q7 does not apply) -> MaxPool -> Flatten -> Dense.
+    rng = np.random.default_rng(7)
+    C, H = 2, 8
+    specs = [oracle.spec(oracle.LAYER_CONV2D, in_size=C * H * H, in_channels=C, out_channels=3, kernel=3,
+                         stride=2, padding=1, act=oracle.ACT_RELU),
+             oracle.spec(oracle.LAYER_MAXPOOL2D, in_channels=3, kernel=2, stride=2),
+             oracle.spec(oracle.LAYER_FLATTEN),
+             oracle.spec(oracle.LAYER_DENSE, in_size=12, out_size=5, act=oracle.ACT_SOFTMAX, act_is_ptr=1)]
+    net = oracle.Net(specs, oracle.LOSS_CE)
+    B = 4
+    x = rng.normal(size=(B, C, H, H)).astype(np.float32)
+    y = np.eye(5, dtype=np.float32)[rng.integers(0, 5, B)]
+    p0 = net.params.copy().astype(np.float64)
+    net.accumulate_batch(x.reshape(B, -1), y, B)
+    P = torch.tensor(p0, requires_grad=True)
+    w = P[:54].view(3, 2, 3, 3)
+    b = P[54:57]
+    W = P[57:57 + 60].view(5, 12)
+    bb = P[117:122]
+    z = torch.nn.functional.conv2d(torch.tensor(x.astype(np.float64)), w, b, stride=2, padding=1)
+    a = torch.relu(z)
+    pooled = torch.nn.functional.max_pool2d(a, 2, 2)
+    logits = pooled.reshape(B, -1) @ W.T + bb
+    p = torch.softmax(logits, dim=1)
+    p.backward((p - torch.tensor(y.astype(np.float64))).detach() / B)
+    exp = P.grad.numpy()
+    assert np.abs(net.grads - exp).max() / np.abs(exp).max() < 1e-5
+
+
+def test_sequential_vs_parallel_workers_agree(oracle):
+    # A2: W-worker chunking only changes summation order for Dense stacks.
+    rng = np.random.default_rng(8)
+    mk = lambda w: oracle.Net([oracle.spec(oracle.LAYER_DENSE, in_size=20, out_size=30, act=oracle.ACT_RELU),
+                               oracle.spec(oracle.LAYER_DENSE, in_size=30, out_size=5, act=oracle.ACT_SOFTMAX,
+                                           act_is_ptr=1)], oracle.LOSS_CE, workers=w)
+    x = rng.normal(size=(16, 20)).astype(np.float32)
+    y = np.eye(5, dtype=np.float32)[rng.integers(0, 5, 16)]
+    a, b = mk(1), mk(4)
+    la = a.train_batch(x, y, 16)
+    lb = b.train_batch(x, y, 16)
+    assert abs(la - lb) < 1e-5
+    np.testing.assert_allclose(a.params, b.params, rtol=1e-5, atol=1e-6)
+
+
+def test_facade_softmax_value_gives_nan(oracle):
+    # Q3: a Softmax *value* is ActTypeNone: identity forward, NaN derivative.
+    net = oracle.Net([oracle.spec(oracle.LAYER_DENSE, in_size=4, out_size=3, act=oracle.ACT_SOFTMAX,
+                                  act_is_ptr=0)], oracle.LOSS_CE)
+    x = np.ones((1, 4), np.float32)
+    out = net.forward(x[0])
+    pre = net.preact(0)
+    np.testing.assert_array_equal(out, pre)
+    net.accumulate_batch(x, np.eye(3, dtype=np.float32)[:1], 1)
+    assert np.isnan(net.grads).all()
