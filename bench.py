@@ -1,0 +1,171 @@
+"""Throughput of GoNeuron's fp32 training step (forward + backward + Adam) on
+one MI355X, with the roofline fraction of the dominant kernel and the CPU
+reference path timed beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wide]
+
+Prints ONE JSON line.  `value` is samples/s with inputs resident in HBM; the
+GEMM family's achieved TFLOP/s comes from HIP events recorded around every
+GEMM launch on the library's stream during the timed steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+
+
+def gemm_flops(cfg, B):
+    """Algorithmic GEMM FLOPs of one step: forward 2*B*in*out per Dense,
+    dW the same, dX for every Dense but the first (its dX is discarded)."""
+    f = 0
+    dense = [d for d in cfg["layers"] if d["kind"] == "dense"]
+    for i, d in enumerate(dense):
+        mac = B * d["in"] * d["out"]
+        f += 2 * mac + 2 * mac + (2 * mac if i > 0 else 0)
+    return f
+
+
+def cpu_baseline(cfg, x, y, budget_s=15.0):
+    """The CPU oracle (reference-semantics restatement, 1 thread) on a bounded
+    sample: per-sample fwd+bwd of n samples plus one Adam pass over the arena,
+    scaled to samples/s = n / (t_samples + t_adam * n / B)."""
+    from oracle import refcpu
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from cfgutil import oracle_net
+    refcpu.build()
+    net = oracle_net(refcpu, cfg)
+    B = cfg["B"]
+    # calibrate with one sample, then fill the budget
+    t0 = time.perf_counter()
+    net.accumulate_batch(x[:1], y[:1], 1)
+    t1 = time.perf_counter() - t0
+    n = int(max(1, min(B, budget_s / max(t1, 1e-6))))
+    t0 = time.perf_counter()
+    net.accumulate_batch(x[:n], y[:n], n)
+    ts = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    net.step()
+    ta = time.perf_counter() - t0
+    per_sample = (ts + ta * n / B) / n
+    return {"value": 1.0 / per_sample, "unit": "samples/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/refcpu (C restatement of net.go:721-784, -O2 -ffp-contract=off, 1 thread): "
+                      f"{n} of {B} samples fwd+bwd ({ts:.2f} s) + one Adam pass over the "
+                      f"{net.n}-param arena ({ta:.3f} s) scaled by n/B"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the data-parallel "
+              "sharding across GPUs is a design (DESIGN.md), not built here.", file=sys.stderr)
+        sys.exit(2)
+
+    import ctypes as C
+    import goneuron_amd as gn
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib, check
+
+    cfg = configs.CONFIGS[args.config]()
+    B = cfg["B"]
+    dev = gn.GetDefaultDevice()
+    x, y = configs.inputs(cfg)
+    model = configs.build(cfg, device=dev)
+
+    def dbuf(a):
+        p = C.c_void_p()
+        check(dev.h, lib().gn_malloc(dev.h, a.nbytes, C.byref(p)))
+        check(dev.h, lib().gn_memcpy_h2d(dev.h, p, a.ctypes.data, a.nbytes))
+        return p
+
+    dx, dy = dbuf(x), dbuf(y)
+    step = lambda: check(dev.h, lib().gn_model_train_step_device(model.h, dx, dy, B))
+    for _ in range(args.warmup):
+        step()
+    dev.sync()
+    check(dev.h, lib().gn_timing_enable(dev.h, 1))
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.sync()
+    elapsed = time.perf_counter() - t0
+    res = {}
+    for cls, name in ((0, "gemm"), (1, "adam"), (2, "other")):
+        n = C.c_int64()
+        ms = C.c_double()
+        check(dev.h, lib().gn_timing_report(dev.h, cls, C.byref(n), C.byref(ms)))
+        res[name] = (n.value, ms.value)
+    check(dev.h, lib().gn_timing_enable(dev.h, 0))
+    loss = C.c_float()
+    check(dev.h, lib().gn_model_read_loss(model.h, C.byref(loss)))
+
+    K = args.steps
+    samples_per_s = B * K / elapsed
+    ms_per_step = elapsed * 1e3 / K
+    flops = gemm_flops(cfg, B)
+    g_n, g_ms = res["gemm"]
+    a_n, a_ms = res["adam"]
+    gemm_tflops = flops * K / (g_ms * 1e-3) / 1e12 if g_ms > 0 else None
+    per_launch_flops = flops * K / g_n if g_n else None
+    adam_bytes = 28 * model.nparams
+    adam_gbps = adam_bytes * a_n / (a_ms * 1e-3) / 1e9 if a_ms > 0 else None
+
+    line = {
+        "metric": "train samples/s (fwd+bwd+Adam) on 1 MI355X; % of fp32 MFMA / HBM roofline",
+        "value": samples_per_s,
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (reference LCG, seeds 1000+cfg / 2000+cfg), reference LCG weight init",
+        "config": {"workload": cfg["name"], "batch": B,
+                   "layers": [d["kind"] + (f"{d['in']}->{d['out']}" if d["kind"] == "dense" else "")
+                              for d in cfg["layers"]],
+                   "loss": cfg["loss"], "optimizer": "Adam lr=1e-3"},
+        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": (gemm_tflops / PEAK_FP32_MFMA_TFLOPS) if gemm_tflops else None,
+                     "traffic": None, "kernel": "gemm_f32_mfma (all instantiations)",
+                     "flops_per_launch": per_launch_flops,
+                     "avg_launch_ms": g_ms / g_n if g_n else None},
+        "kernels": {
+            "gemm": {"launches_per_step": g_n / K, "ms_per_step": g_ms / K},
+            "adam": {"launches_per_step": a_n / K, "ms_per_step": a_ms / K, "bound": "hbm",
+                     "achieved_gbps": adam_gbps, "peak_gbps": PEAK_HBM_GBPS,
+                     "frac": adam_gbps / PEAK_HBM_GBPS if adam_gbps else None,
+                     "bytes_per_launch": adam_bytes},
+            "other": {"launches_per_step": res["other"][0] / K, "ms_per_step": res["other"][1] / K},
+        },
+        "loss": loss.value,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,125 @@
+"""The five BASELINE training-step configurations and their synthetic inputs.
+
+Layers are described neutrally (dicts) so that the same description builds the
+GPU model (``build``) and, in tests, the CPU oracle.  Inputs come from the
+reference's LCG (layer.go:61-81) with seeds 1000 + config number (inputs) and
+2000 + config number (targets).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, Flatten, Embedding,
+               PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
+               Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal, fill_uniform,
+               fill_class_ids)
+
+_ACTS = {"relu": ReLU, "linear": Linear, "softmax": Softmax, "logsoftmax": LogSoftmax}
+
+
+def dense(i, o, act, ptr=False):
+    return {"kind": "dense", "in": i, "out": o, "act": act, "ptr": ptr}
+
+
+def mlp(hidden=128):
+    return dict(num=1, name="mlp", B=64, loss="ce", lr=1e-3, x="uniform", in_len=784,
+                classes=10,
+                layers=[dense(784, hidden, "relu"), {"kind": "dropout", "p": 0.2, "n": hidden},
+                        dense(hidden, 10, "softmax", True)])
+
+
+def cnn(B=128):
+    return dict(num=2, name="cnn", B=B, loss="ce", lr=1e-3, x="normal", in_len=3 * 32 * 32,
+                classes=10,
+                layers=[{"kind": "conv2d", "inC": 3, "outC": 16, "k": 3, "s": 1, "p": 1, "act": "relu"},
+                        {"kind": "maxpool2d", "k": 2, "s": 2, "p": 0, "inC": 16},
+                        {"kind": "flatten", "n": 4096},
+                        dense(4096, 10, "softmax", True)])
+
+
+def wide(width=4096, classes=1000, depth=4, B=1024):
+    ls = [dense(width, width, "relu") for _ in range(depth)]
+    ls.append(dense(width, classes, "logsoftmax", True))
+    return dict(num=3, name="wide", B=B, loss="ce", lr=1e-3, x="normal", in_len=width,
+                classes=classes, layers=ls)
+
+
+def gpt(B=32, T=128, vocab=8000, dim=256, heads=8, ff=1024):
+    return dict(num=4, name="gpt", B=B, loss="ce", lr=1e-3, x="ids", in_len=T, classes=vocab,
+                layers=[{"kind": "embedding", "vocab": vocab, "dim": dim},
+                        {"kind": "posenc", "T": T, "dim": dim},
+                        {"kind": "transformer", "dim": dim, "heads": heads, "T": T, "ff": ff,
+                         "causal": True},
+                        {"kind": "clspool", "T": T, "dim": dim},
+                        dense(dim, vocab, "logsoftmax", True)])
+
+
+def lstm(B=64, T=100, inp=64, hidden=256):
+    return dict(num=5, name="lstm", B=B, loss="mse", lr=1e-3, x="normal", in_len=T * inp,
+                classes=None, targets="normal",
+                layers=[{"kind": "lstm", "in": inp, "hidden": hidden, "T": T},
+                        dense(hidden, 1, "linear")])
+
+
+CONFIGS = {"mlp": mlp, "cnn": cnn, "wide": wide, "gpt": gpt, "lstm": lstm}
+
+
+def inputs(cfg, B=None):
+    """(x, y) float32 arrays, B x in_len and B x out_len."""
+    B = B or cfg["B"]
+    n = B * cfg["in_len"]
+    seed_x, seed_y = 1000 + cfg["num"], 2000 + cfg["num"]
+    if cfg["x"] == "uniform":
+        x = fill_uniform(n, seed_x)
+    elif cfg["x"] == "normal":
+        x = fill_normal(n, seed_x)
+    else:
+        x = fill_class_ids(n, cfg["classes"], seed_x).astype(np.float32)
+    x = x.reshape(B, cfg["in_len"])
+    if cfg.get("targets") == "normal":
+        y = fill_normal(B, seed_y).reshape(B, 1)
+    else:
+        ids = fill_class_ids(B, cfg["classes"], seed_y)
+        y = np.zeros((B, cfg["classes"]), np.float32)
+        y[np.arange(B), ids] = 1.0
+    return x, y
+
+
+def product_layers(cfg):
+    out = []
+    for d in cfg["layers"]:
+        k = d["kind"]
+        if k == "dense":
+            act = _ACTS[d["act"]]
+            out.append(Dense(d["in"], d["out"], Ref(act) if d["ptr"] else act))
+        elif k == "dropout":
+            out.append(Dropout(d["p"], d["n"]))
+        elif k == "flatten":
+            out.append(Flatten(d["n"]))
+        elif k == "conv2d":
+            out.append(Conv2D(d["inC"], d["outC"], d["k"], d["s"], d["p"], _ACTS[d["act"]]))
+        elif k == "maxpool2d":
+            out.append(MaxPool2D(d["k"], d["s"], d["p"], d["inC"]))
+        elif k == "embedding":
+            out.append(Embedding(d["vocab"], d["dim"]))
+        elif k == "posenc":
+            out.append(PositionalEncoding(d["T"], d["dim"]))
+        elif k == "transformer":
+            out.append(TransformerBlock(d["dim"], d["heads"], d["T"], d["ff"], d["causal"]))
+        elif k == "clspool":
+            out.append(CLSPooling(d["T"], d["dim"]))
+        elif k == "lstm":
+            out.append(SequenceUnroller(LSTM(d["hidden"], d["in"]), d["T"], False))
+        else:
+            raise ValueError(k)
+    # the first layer carries the per-sample input length
+    out[0].desc.in_size = cfg["in_len"] if out[0].desc.in_size <= 0 or cfg["layers"][0]["kind"] in (
+        "conv2d", "embedding", "lstm") else out[0].desc.in_size
+    return out
+
+
+def build(cfg, device=None, workers=1, max_batch=None):
+    m = NewSequential(*product_layers(cfg), device=device)
+    m.Compile(Adam(cfg["lr"]), CrossEntropy if cfg["loss"] == "ce" else MSE,
+              max_batch=max_batch or cfg["B"], workers=workers)
+    return m

@@ -1,0 +1,87 @@
+// Internal declarations shared by the runtime and the kernel files of
+// libgoneuron_hip.so.  Kernels are gfx950-only (64-wide wavefronts, fp32 MFMA).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/goneuron_hip.h"
+
+namespace gn {
+
+// Activation derivative kinds used by kernels.  Computed from the saved
+// *output* of the layer: out = act(pre) is deterministic, so relu'(pre) ==
+// (out > 0), sigmoid'(pre) == out*(1-out), tanh'(pre) == 1-out*out exactly as
+// the reference recomputes them from the pre-activation.
+enum DerivKind : int32_t {
+  D_ONE = 0,      // Linear: derivative 1
+  D_RELU = 1,
+  D_SIGMOID = 2,
+  D_TANH = 3,
+  D_NAN = 4,      // Softmax/LogSoftmax *values*: Derivative returns NaN (Q3)
+};
+
+// Forward activation kinds applied elementwise in GEMM epilogues.
+enum FwdKind : int32_t {
+  F_IDENTITY = 0,
+  F_RELU = 1,
+  F_SIGMOID = 2,
+  F_TANH = 3,
+  F_NAN = 4,      // scalar Activate of Softmax/LogSoftmax values (Conv2D only)
+};
+
+struct GemmArgs {
+  int M, N, K;
+  const float *A;
+  int lda;
+  const float *B;
+  int ldb;
+  float *C;
+  int ldc;
+  float alpha;
+  const float *bias;  // EPI_BIAS_ACT: per-column bias (may be null)
+  const float *aux;   // EPI_DACT: saved output used for act'
+  int ldaux;
+  int act;            // FwdKind or DerivKind
+};
+
+enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
+
+// op(A) layout: 'N' = A[m*lda+k] (K contiguous), 'T' = A[k*lda+m].
+// op(B) layout: 'N' = B[k*ldb+n] (N contiguous), 'T' = B[n*ldb+k].
+hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t s);
+
+hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,
+                       float beta1, float beta2, float omb1, float omb2, float eps, hipStream_t s);
+
+// db[o] = scale * sum_b dz[b*ld + o]
+hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
+                         float *scratch, size_t scratch_cap, hipStream_t s);
+
+// dz = g * act'(out) elementwise (optionally with dropout mask/scale fused)
+hipError_t launch_dact(const float *g, const float *out, float *dz, int64_t n, int deriv,
+                       hipStream_t s);
+
+// Output-layer row kernel: forward row activation (softmax/logsoftmax/none),
+// per-sample loss, loss gradient, and dz through the activation's Jacobian
+// (Q4).  z holds pre-activations [B,C]; out receives the activation output.
+hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz, float *loss_rows,
+                           int B, int C, int row_act, int deriv, int loss_kind, hipStream_t s);
+enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMWISE = 3 };
+
+// Row activation only (forward/predict)
+hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s);
+
+// mean loss: loss = (sum_b rows[b] in sample order) / B
+hipError_t launch_loss_mean(const float *rows, int B, int workers, float *loss, hipStream_t s);
+
+// dropout: out = x*scale where mask else 0 (mask is per-feature, Q9)
+hipError_t launch_dropout(const float *x, const float *mask, float scale, float *out, int B, int n,
+                          hipStream_t s);
+
+// Elementwise forward activation in place.
+hipError_t launch_act_inplace(float *x, int64_t n, int fwd, hipStream_t s);
+
+}  // namespace gn

@@ -1,0 +1,885 @@
+// Host runtime of libgoneuron_hip.so: context, device-resident flat arena,
+// the Sequential model plan and the batched training step.
+//
+// The step keeps the reference's per-sample semantics (Network.
+// trainBatchSequential, internal/net/net.go:721-784: per-sample forward,
+// backward accumulated into the flat grads, grads *= 1/B, Adam) but runs each
+// layer once over the whole batch: per-sample mat-vecs become fp32 MFMA GEMMs,
+// the gradient sums over samples become the K dimension of those GEMMs, and
+// the 1/B average is folded into the dW/db writes.  Parameters, gradients and
+// Adam moments live in one HBM allocation; nothing crosses PCIe inside a step.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gn_common.h"
+
+using namespace gn;
+
+struct gn_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  int fail_next = 0;
+  hipDeviceProp_t props{};
+  float *scratch = nullptr;  // colsum partials
+  size_t scratch_floats = 0;
+  // kernel timing (gn_timing_enable)
+  bool timing = false;
+  struct Rec { int cls; hipEvent_t a, b; };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> pool;
+  size_t pool_used = 0;
+};
+
+static hipEvent_t ev_get(gn_ctx *c) {
+  if (c->pool_used == c->pool.size()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    c->pool.push_back(e);
+  }
+  return c->pool[c->pool_used++];
+}
+
+// Brackets the kernels launched in its scope with events when timing is on.
+struct KTimer {
+  gn_ctx *c;
+  int cls;
+  hipEvent_t a = nullptr, b = nullptr;
+  KTimer(gn_ctx *c_, int cls_) : c(c_), cls(cls_) {
+    if (c->timing) {
+      a = ev_get(c);
+      b = ev_get(c);
+      if (a && b) (void)hipEventRecord(a, c->stream);
+      else a = b = nullptr;
+    }
+  }
+  ~KTimer() {
+    if (a) {
+      (void)hipEventRecord(b, c->stream);
+      c->recs.push_back({cls, a, b});
+    }
+  }
+};
+
+static int set_err(gn_ctx *c, int code, const char *fmt, ...) {
+  if (c) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+  }
+  return code;
+}
+
+#define HIP_OK(ctx, expr)                                                                  \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      return set_err((ctx), GN_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                     __FILE__, __LINE__);                                                  \
+  } while (0)
+
+static int check_fail(gn_ctx *c) {
+  if (c && c->fail_next) {
+    int code = c->fail_next;
+    c->fail_next = 0;
+    return set_err(c, code, "injected failure (gn_debug_fail_next)");
+  }
+  return GN_OK;
+}
+
+#define ENTRY(ctx)                              \
+  do {                                          \
+    if (!(ctx)) return GN_ERR_INVALID;          \
+    int f_ = check_fail(ctx);                   \
+    if (f_) return f_;                          \
+    (void)hipSetDevice((ctx)->device);          \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// LCG of the reference (layer.go:61-81) and synthetic data
+// ---------------------------------------------------------------------------
+static inline float lcg_float(uint64_t &s) {
+  s = s * 6364136223846793005ULL + 1ULL;
+  return (float)(s >> 33) / (float)(1u << 31);
+}
+
+extern "C" int gn_fill_uniform(float *dst, int64_t n, uint64_t seed) {
+  if (!dst && n) return GN_ERR_INVALID;
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) dst[i] = lcg_float(s);
+  return GN_OK;
+}
+
+extern "C" int gn_fill_normal(float *dst, int64_t n, uint64_t seed) {
+  if (!dst && n) return GN_ERR_INVALID;
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) {
+    double u1 = (double)lcg_float(s);
+    double u2 = (double)lcg_float(s);
+    if (u1 < 1e-7) u1 = 1e-7;
+    dst[i] = (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+  }
+  return GN_OK;
+}
+
+extern "C" int gn_fill_class_ids(int32_t *dst, int64_t n, int32_t nclass, uint64_t seed) {
+  if ((!dst && n) || nclass <= 0) return GN_ERR_INVALID;
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t c = (int32_t)(lcg_float(s) * (float)nclass);
+    dst[i] = c >= nclass ? nclass - 1 : c;
+  }
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+extern "C" int gn_available(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n > 0 ? 1 : 0;
+}
+
+extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
+  if (!out) return GN_ERR_INVALID;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return GN_ERR_NO_DEVICE;
+  if (device_ordinal < 0 || device_ordinal >= n) return GN_ERR_INVALID;
+  std::unique_ptr<gn_ctx> c(new gn_ctx);
+  c->device = device_ordinal;
+  if (hipSetDevice(device_ordinal) != hipSuccess) return GN_ERR_HIP;
+  if (hipGetDeviceProperties(&c->props, device_ordinal) != hipSuccess) return GN_ERR_HIP;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return GN_ERR_HIP;
+  c->scratch_floats = (size_t)64 * 65536;
+  if (hipMalloc(&c->scratch, c->scratch_floats * sizeof(float)) != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    return GN_ERR_OOM;
+  }
+  *out = c.release();
+  return GN_OK;
+}
+
+extern "C" void gn_shutdown(gn_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
+  (void)hipFree(c->scratch);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+extern "C" const char *gn_last_error(const gn_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+extern "C" int gn_device_info(gn_ctx *c, gn_info *info) {
+  ENTRY(c);
+  if (!info) return set_err(c, GN_ERR_INVALID, "info is null");
+  memset(info, 0, sizeof *info);
+  snprintf(info->arch, sizeof info->arch, "%s", c->props.gcnArchName);
+  info->cu_count = c->props.multiProcessorCount;
+  info->hbm_bytes = (int64_t)c->props.totalGlobalMem;
+  info->peak_fp32_mfma_tflops = 157.3;  // MI355X dense fp32 matrix
+  info->peak_hbm_gbps = 8000.0;         // MI355X HBM3E
+  return GN_OK;
+}
+
+extern "C" int gn_sync(gn_ctx *c) {
+  ENTRY(c);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_debug_fail_next(gn_ctx *c, int code) {
+  if (!c) return GN_ERR_INVALID;
+  c->fail_next = code < 0 ? code : GN_ERR_INJECTED;
+  return GN_OK;
+}
+
+extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
+  ENTRY(c);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  c->timing = enable != 0;
+  c->recs.clear();
+  c->pool_used = 0;
+  return GN_OK;
+}
+
+extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *total_ms) {
+  ENTRY(c);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  int64_t n = 0;
+  double ms = 0;
+  for (const auto &r : c->recs) {
+    if (r.cls != cls) continue;
+    float t = 0;
+    HIP_OK(c, hipEventElapsedTime(&t, r.a, r.b));
+    ms += t;
+    ++n;
+  }
+  if (launches) *launches = n;
+  if (total_ms) *total_ms = ms;
+  return GN_OK;
+}
+
+extern "C" int gn_malloc(gn_ctx *c, size_t bytes, void **dptr) {
+  ENTRY(c);
+  if (!dptr) return set_err(c, GN_ERR_INVALID, "dptr is null");
+  *dptr = nullptr;
+  if (hipMalloc(dptr, bytes ? bytes : 4) != hipSuccess)
+    return set_err(c, GN_ERR_OOM, "hipMalloc(%zu) failed", bytes);
+  return GN_OK;
+}
+
+extern "C" int gn_free(gn_ctx *c, void *p) {
+  ENTRY(c);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipFree(p));
+  return GN_OK;
+}
+
+extern "C" int gn_memcpy_h2d(gn_ctx *c, void *dst, const void *src, size_t bytes) {
+  ENTRY(c);
+  if ((!dst || !src) && bytes) return set_err(c, GN_ERR_INVALID, "null pointer");
+  HIP_OK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_memcpy_d2h(gn_ctx *c, void *dst, const void *src, size_t bytes) {
+  ENTRY(c);
+  if ((!dst || !src) && bytes) return set_err(c, GN_ERR_INVALID, "null pointer");
+  HIP_OK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_memset_zero(gn_ctx *c, void *dst, size_t bytes) {
+  ENTRY(c);
+  HIP_OK(c, hipMemsetAsync(dst, 0, bytes, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Per-layer operators
+// ---------------------------------------------------------------------------
+struct ActPlan {
+  int row_act;  // RowAct (with fwd kind in bits 8.. for ROW_ELEMWISE)
+  int fwd;      // FwdKind for elementwise forward
+  int deriv;    // DerivKind
+  bool jac;     // Softmax/LogSoftmax Jacobian backward
+};
+
+// cacheActivationType (layer.go:183-205) + the Activate/Derivative methods of
+// activations.go: pointer Softmax/LogSoftmax get the row activation and the
+// Jacobian; the values fall through to identity forward / NaN derivative.
+static int plan_act(int act, int is_ptr, ActPlan &p) {
+  p = ActPlan{ROW_NONE, F_IDENTITY, D_ONE, false};
+  switch (act) {
+    case GN_ACT_RELU: p.fwd = F_RELU; p.deriv = D_RELU; break;
+    case GN_ACT_SIGMOID: p.fwd = F_SIGMOID; p.deriv = D_SIGMOID; break;
+    case GN_ACT_TANH: p.fwd = F_TANH; p.deriv = D_TANH; break;
+    case GN_ACT_LINEAR: break;
+    case GN_ACT_SOFTMAX:
+    case GN_ACT_LOGSOFTMAX:
+      if (is_ptr) {
+        p.row_act = act == GN_ACT_SOFTMAX ? ROW_SOFTMAX : ROW_LOGSOFTMAX;
+        p.jac = true;
+      } else {
+        p.deriv = D_NAN;
+      }
+      break;
+    default: return GN_ERR_INVALID;  // nil activation: the reference panics in Derivative
+  }
+  if (p.row_act == ROW_NONE && p.fwd != F_IDENTITY) p.row_act = ROW_ELEMWISE | (p.fwd << 8);
+  return GN_OK;
+}
+
+static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const float *b, float *out,
+                            int B, int in, int out_n, int fwd) {
+  GemmArgs a{};
+  a.M = B; a.N = out_n; a.K = in;
+  a.A = x; a.lda = in;
+  a.B = W; a.ldb = in;
+  a.C = out; a.ldc = out_n;
+  a.bias = b; a.act = fwd; a.alpha = 1.f;
+  KTimer kt(c, GN_KCLASS_GEMM);
+  return launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream);
+}
+
+// gradW = scale * dz^T x ; gradB = scale * colsum(dz) ; gin = dz W (optionally * act'(aux))
+static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz,
+                                 float *gW, float *gB, float *gin, int B, int in, int out_n,
+                                 float scale, const float *gin_aux, int gin_deriv) {
+  hipError_t e;
+  if (gB) {
+    KTimer kt(c, GN_KCLASS_OTHER);
+    e = launch_colsum(dz, B, out_n, out_n, scale, gB, c->scratch, c->scratch_floats, c->stream);
+    if (e != hipSuccess) return e;
+  }
+  GemmArgs a{};
+  a.M = out_n; a.N = in; a.K = B;
+  a.A = dz; a.lda = out_n;
+  a.B = x; a.ldb = in;
+  a.C = gW; a.ldc = in;
+  a.alpha = scale;
+  {
+    KTimer kt(c, GN_KCLASS_GEMM);
+    e = launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
+  }
+  if (e != hipSuccess) return e;
+  if (gin) {
+    GemmArgs d{};
+    d.M = B; d.N = in; d.K = out_n;
+    d.A = dz; d.lda = out_n;
+    d.B = W; d.ldb = in;
+    d.C = gin; d.ldc = in;
+    d.alpha = 1.f;
+    KTimer kt(c, GN_KCLASS_GEMM);
+    if (gin_aux) {
+      d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv;
+      e = launch_gemm('N', 'N', EPI_DACT, d, c->stream);
+    } else {
+      e = launch_gemm('N', 'N', EPI_SCALE, d, c->stream);
+    }
+  }
+  return e;
+}
+
+extern "C" int gn_gemm(gn_ctx *c, int32_t transA, int32_t transB, int32_t M, int32_t N, int32_t K,
+                       float alpha, const float *A, int32_t lda, const float *B, int32_t ldb,
+                       float *Cm, int32_t ldc) {
+  ENTRY(c);
+  if (M < 0 || N < 0 || K < 0 || !A || !B || !Cm) return set_err(c, GN_ERR_INVALID, "bad gemm args");
+  if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N)
+    return set_err(c, GN_ERR_INVALID, "leading dimension too small");
+  GemmArgs a{};
+  a.M = M; a.N = N; a.K = K;
+  a.A = A; a.lda = lda; a.B = B; a.ldb = ldb; a.C = Cm; a.ldc = ldc; a.alpha = alpha;
+  HIP_OK(c, launch_gemm(transA ? 'T' : 'N', transB ? 'T' : 'N', EPI_SCALE, a, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_dense_forward(gn_ctx *c, const float *x, const float *W, const float *bias,
+                                float *out, int32_t B, int32_t in, int32_t out_n, int32_t act,
+                                int32_t act_is_ptr) {
+  ENTRY(c);
+  if (!x || !W || !out || B < 0 || in <= 0 || out_n <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad dense_forward args");
+  ActPlan ap;
+  if (plan_act(act, act_is_ptr, ap)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
+  HIP_OK(c, dense_fwd(c, x, W, bias, out, B, in, out_n, ap.jac ? F_IDENTITY : ap.fwd));
+  if (ap.jac) HIP_OK(c, launch_row_act(out, B, out_n, ap.row_act, c->stream));
+  return GN_OK;
+}
+
+__global__ void jac_rows_kernel(const float *__restrict__ o, const float *__restrict__ g,
+                                float *__restrict__ dz, int C, int logsm) {
+  __shared__ float sh[4];
+  const int b = blockIdx.x, t = threadIdx.x;
+  const float *orow = o + (size_t)b * C, *grow = g + (size_t)b * C;
+  float *d = dz + (size_t)b * C;
+  float s = 0.f;
+  for (int i = t; i < C; i += 256) s += logsm ? grow[i] : grow[i] * orow[i];
+  // block reduce
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((t & 63) == 0) sh[t >> 6] = s;
+  __syncthreads();
+  s = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  for (int i = t; i < C; i += 256)
+    d[i] = logsm ? grow[i] - (float)exp((double)orow[i]) * s : grow[i] * orow[i] - orow[i] * s;
+}
+
+extern "C" int gn_dense_backward(gn_ctx *c, const float *x, const float *W, const float *out,
+                                 const float *gout, float *gradW, float *gradB, float *gin,
+                                 float *dz, int32_t B, int32_t in, int32_t out_n, int32_t act,
+                                 int32_t act_is_ptr, float scale) {
+  ENTRY(c);
+  if (!x || !W || !out || !gout || !gradW || !dz || B <= 0 || in <= 0 || out_n <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad dense_backward args");
+  ActPlan ap;
+  if (plan_act(act, act_is_ptr, ap)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
+  if (ap.jac) {
+    hipLaunchKernelGGL(jac_rows_kernel, dim3(B), dim3(256), 0, c->stream, out, gout, dz, out_n,
+                       ap.row_act == ROW_LOGSOFTMAX ? 1 : 0);
+    HIP_OK(c, hipGetLastError());
+  } else {
+    HIP_OK(c, launch_dact(gout, out, dz, (int64_t)B * out_n, ap.deriv, c->stream));
+  }
+  HIP_OK(c, dense_bwd_core(c, x, W, dz, gradW, gradB, gin, B, in, out_n, scale, nullptr, 0));
+  return GN_OK;
+}
+
+extern "C" int gn_adam_step(gn_ctx *c, float *p, const float *g, float *m, float *v, int64_t n,
+                            float lr, float b1, float b2, float eps, int32_t timestep) {
+  ENTRY(c);
+  if ((!p || !g || !m || !v) && n) return set_err(c, GN_ERR_INVALID, "null arena pointer");
+  if ((((uintptr_t)p | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15) != 0)
+    return set_err(c, GN_ERR_INVALID, "arena pointers must be 16-byte aligned");
+  if (b1 == 0) b1 = 0.9f;
+  if (b2 == 0) b2 = 0.999f;
+  if (eps == 0) eps = 1e-8f;
+  // opt.go:237-242: bias corrections in float64 then rounded
+  const double ts = (double)(timestep + 1);
+  const float bias1 = (float)(1.0 - pow((double)b1, ts));
+  const float bias2 = (float)(1.0 - pow((double)b2, ts));
+  const float efflr = lr * (float)sqrt((double)bias2) / bias1;
+  HIP_OK(c, launch_adam(p, g, m, v, n, efflr, b1, b2, 1.0f - b1, 1.0f - b2, eps, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Model
+// ---------------------------------------------------------------------------
+struct LayerRT {
+  gn_layer_desc d{};
+  int64_t poff = 0, pcount = 0;
+  int in_len = 0, out_len = 0;  // per-sample feature counts
+  float *out = nullptr;         // [maxB, out_len] activation output (owned unless alias)
+  bool out_alias = false;       // Flatten: out is the input buffer
+  float *gout = nullptr;        // dL/d(out) [maxB, out_len] (owned unless alias)
+  bool gout_alias = false;
+  ActPlan ap{};
+  float *mask = nullptr;        // Dropout per-feature mask (Q9)
+  float scale = 1.f;
+};
+
+struct gn_model {
+  gn_ctx *ctx = nullptr;
+  std::vector<LayerRT> L;
+  int loss_kind = 0;
+  gn_adam_desc adam{};
+  int maxB = 0, workers = 1;
+  int64_t nparams = 0, region = 0;
+  float *arena = nullptr, *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
+  int timestep = 0;
+  float *loss_rows = nullptr, *loss_dev = nullptr;
+  float *xin = nullptr, *yin = nullptr;  // staging for host inputs
+  int training = 1;
+  int last_B = 0;
+  std::vector<void *> owned;
+};
+
+static int model_alloc(gn_model *M, size_t floats, float **p) {
+  void *q = nullptr;
+  if (hipMalloc(&q, std::max<size_t>(floats, 1) * sizeof(float)) != hipSuccess) {
+    *p = nullptr;
+    return set_err(M->ctx, GN_ERR_OOM, "hipMalloc(%zu floats) failed", floats);
+  }
+  M->owned.push_back(q);
+  *p = (float *)q;
+  return GN_OK;
+}
+
+extern "C" void gn_model_destroy(gn_model *M) {
+  if (!M) return;
+  (void)hipSetDevice(M->ctx->device);
+  (void)hipStreamSynchronize(M->ctx->stream);
+  for (void *p : M->owned) (void)hipFree(p);
+  delete M;
+}
+
+// Reference initialisation into the host copy of the arena.
+static void init_dense(float *p, int in, int out) {  // Dense.Build layer.go:300-320
+  const float scale = (float)sqrt(2.0 / ((double)in + (double)out));
+  uint64_t s = (uint64_t)(in * 1000 + out * 100 + 42);
+  const int64_t nw = (int64_t)in * out;
+  for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
+  for (int i = 0; i < out; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
+}
+
+extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t nlayers,
+                               int32_t loss_kind, const gn_adam_desc *adam, int32_t max_batch,
+                               int32_t workers, gn_model **out) {
+  ENTRY(c);
+  if (!layers || nlayers <= 0 || !out || max_batch <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad model_create args");
+  if (loss_kind != GN_LOSS_MSE && loss_kind != GN_LOSS_CE)
+    return set_err(c, GN_ERR_INVALID, "unknown loss %d", loss_kind);
+  *out = nullptr;
+  std::unique_ptr<gn_model> M(new gn_model);
+  M->ctx = c;
+  M->loss_kind = loss_kind;
+  M->maxB = max_batch;
+  M->workers = workers < 1 ? 1 : workers;
+  if (adam) M->adam = *adam;
+  if (M->adam.beta1 == 0) M->adam.beta1 = 0.9f;
+  if (M->adam.beta2 == 0) M->adam.beta2 = 0.999f;
+  if (M->adam.eps == 0) M->adam.eps = 1e-8f;
+  M->L.resize(nlayers);
+
+  // Shape propagation (the reference infers per-sample lengths at forward time)
+  int len = layers[0].in_size;
+  if (len <= 0) return set_err(c, GN_ERR_INVALID, "first layer needs in_size (input length)");
+  int64_t off = 0;
+  for (int i = 0; i < nlayers; ++i) {
+    LayerRT &R = M->L[i];
+    R.d = layers[i];
+    R.in_len = len;
+    switch (R.d.kind) {
+      case GN_LAYER_DENSE:
+        if (R.d.in_size != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: Dense in %d != incoming %d", i, R.d.in_size, len);
+        if (R.d.out_size <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: Dense out <= 0", i);
+        if (plan_act(R.d.act, R.d.act_is_ptr, R.ap))
+          return set_err(c, GN_ERR_INVALID, "layer %d: activation %d not supported", i, R.d.act);
+        if (R.ap.jac && i != nlayers - 1)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: Softmax/LogSoftmax only on the output layer", i);
+        R.pcount = (int64_t)R.d.in_size * R.d.out_size + R.d.out_size;
+        R.out_len = R.d.out_size;
+        break;
+      case GN_LAYER_DROPOUT:
+        if (R.d.in_size != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: Dropout size %d != incoming %d", i, R.d.in_size, len);
+        if (R.d.p < 0 || R.d.p > 1) return set_err(c, GN_ERR_INVALID, "dropout p out of [0,1]");
+        R.out_len = len;
+        break;
+      case GN_LAYER_FLATTEN:
+        R.out_len = len;
+        break;
+      default:
+        return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: kind %d not built in this library", i,
+                       R.d.kind);
+    }
+    R.poff = off;
+    off += R.pcount;
+    len = R.out_len;
+  }
+  if (M->L.back().d.kind != GN_LAYER_DENSE)
+    return set_err(c, GN_ERR_UNSUPPORTED, "the output layer must be Dense");
+  M->nparams = off;
+  M->region = (off + 63) / 64 * 64;
+
+  // Arena: params | grads | m | v (each region 256 B aligned)
+  int rc = model_alloc(M.get(), (size_t)M->region * 4, &M->arena);
+  if (rc) return rc;
+  M->params = M->arena;
+  M->grads = M->arena + M->region;
+  M->m = M->arena + 2 * M->region;
+  M->v = M->arena + 3 * M->region;
+  HIP_OK(c, hipMemsetAsync(M->arena, 0, (size_t)M->region * 4 * sizeof(float), c->stream));
+
+  std::vector<float> host((size_t)std::max<int64_t>(off, 1), 0.f);
+  int maxw = 0;
+  for (int i = 0; i < nlayers; ++i) {
+    LayerRT &R = M->L[i];
+    maxw = std::max(maxw, std::max(R.in_len, R.out_len));
+    if (R.d.kind == GN_LAYER_DENSE) init_dense(host.data() + R.poff, R.d.in_size, R.d.out_size);
+    if (R.d.kind == GN_LAYER_FLATTEN) {
+      // reshape.go:64-96: identity both ways; share the neighbours' buffers
+      R.out_alias = true;
+      R.gout_alias = true;
+      R.gout = i > 0 ? M->L[i - 1].gout : nullptr;
+      continue;
+    }
+    if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.out))) return rc;
+    if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.gout))) return rc;
+    if (R.d.kind == GN_LAYER_DROPOUT) {
+      // Q9: Dropout.Reset reseeds RNG(42) before every sample (dropout.go:399-401),
+      // so one mask of the first `size` draws serves every sample and step.
+      std::vector<float> mk(R.d.in_size);
+      uint64_t s = 42;
+      for (int k = 0; k < R.d.in_size; ++k) mk[k] = lcg_float(s) < R.d.p ? 0.f : 1.f;
+      const float keep = 1.0f - R.d.p;
+      R.scale = 1.0f / keep;
+      if ((rc = model_alloc(M.get(), R.d.in_size, &R.mask))) return rc;
+      HIP_OK(c, hipMemcpyAsync(R.mask, mk.data(), mk.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+    }
+  }
+  HIP_OK(c, hipMemcpyAsync(M->params, host.data(), (size_t)off * sizeof(float),
+                           hipMemcpyHostToDevice, c->stream));
+  if ((rc = model_alloc(M.get(), (size_t)max_batch, &M->loss_rows))) return rc;
+  if ((rc = model_alloc(M.get(), 64, &M->loss_dev))) return rc;
+  if ((rc = model_alloc(M.get(), (size_t)max_batch * M->L[0].in_len, &M->xin))) return rc;
+  if ((rc = model_alloc(M.get(), (size_t)max_batch * M->L.back().out_len, &M->yin))) return rc;
+  HIP_OK(c, hipMemsetAsync(M->loss_dev, 0, 64 * sizeof(float), c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  (void)maxw;
+  *out = M.release();
+  return GN_OK;
+}
+
+extern "C" int gn_model_nparams(gn_model *M, int64_t *n) {
+  if (!M || !n) return GN_ERR_INVALID;
+  *n = M->nparams;
+  return GN_OK;
+}
+
+extern "C" int gn_model_layer_params(gn_model *M, int32_t layer, int64_t *offset, int64_t *count) {
+  if (!M || layer < 0 || layer >= (int)M->L.size()) return GN_ERR_INVALID;
+  if (offset) *offset = M->L[layer].poff;
+  if (count) *count = M->L[layer].pcount;
+  return GN_OK;
+}
+
+extern "C" int gn_model_out_size(gn_model *M, int32_t *n) {
+  if (!M || !n) return GN_ERR_INVALID;
+  *n = M->L.back().out_len;
+  return GN_OK;
+}
+
+static int arena_copy(gn_model *M, float *region, float *host, int64_t off, int64_t n, bool d2h) {
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  if (off < 0 || n < 0 || off + n > M->nparams || (!host && n))
+    return set_err(c, GN_ERR_INVALID, "arena range [%lld,+%lld) outside %lld", (long long)off,
+                   (long long)n, (long long)M->nparams);
+  if (d2h)
+    HIP_OK(c, hipMemcpyAsync(host, region + off, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  else
+    HIP_OK(c, hipMemcpyAsync(region + off, host, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_get_params(gn_model *M, float *dst, int64_t off, int64_t n) {
+  if (!M) return GN_ERR_INVALID;
+  return arena_copy(M, M->params, dst, off, n, true);
+}
+extern "C" int gn_model_set_params(gn_model *M, const float *src, int64_t off, int64_t n) {
+  if (!M) return GN_ERR_INVALID;
+  return arena_copy(M, M->params, const_cast<float *>(src), off, n, false);
+}
+extern "C" int gn_model_get_grads(gn_model *M, float *dst, int64_t off, int64_t n) {
+  if (!M) return GN_ERR_INVALID;
+  return arena_copy(M, M->grads, dst, off, n, true);
+}
+extern "C" int gn_model_get_adam(gn_model *M, float *mdst, float *vdst, int64_t off, int64_t n,
+                                 int32_t *timestep) {
+  if (!M) return GN_ERR_INVALID;
+  int rc = GN_OK;
+  if (mdst && (rc = arena_copy(M, M->m, mdst, off, n, true))) return rc;
+  if (vdst && (rc = arena_copy(M, M->v, vdst, off, n, true))) return rc;
+  if (timestep) *timestep = M->timestep;
+  return GN_OK;
+}
+extern "C" int gn_model_arena(gn_model *M, float **p, float **g, float **m, float **v) {
+  if (!M) return GN_ERR_INVALID;
+  if (p) *p = M->params;
+  if (g) *g = M->grads;
+  if (m) *m = M->m;
+  if (v) *v = M->v;
+  return GN_OK;
+}
+
+extern "C" int gn_model_set_training(gn_model *M, int32_t t) {
+  if (!M) return GN_ERR_INVALID;
+  M->training = t ? 1 : 0;
+  return GN_OK;
+}
+
+// Forward over B samples.  Returns the output pointer of the last layer.
+// `for_loss`: the output layer keeps pre-activations for the row kernel.
+static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
+  gn_ctx *c = M->ctx;
+  const float *cur = x;
+  const int n = (int)M->L.size();
+  for (int i = 0; i < n; ++i) {
+    LayerRT &R = M->L[i];
+    switch (R.d.kind) {
+      case GN_LAYER_DENSE: {
+        const float *W = M->params + R.poff;
+        const float *b = W + (int64_t)R.d.in_size * R.d.out_size;
+        const bool last = (i == n - 1);
+        int fwd = R.ap.fwd;
+        if (R.ap.jac || (last && for_loss)) fwd = F_IDENTITY;  // row kernel finishes it
+        HIP_OK(c, dense_fwd(c, cur, W, b, R.out, B, R.d.in_size, R.d.out_size, fwd));
+        if (last && !for_loss && R.ap.jac)
+          HIP_OK(c, launch_row_act(R.out, B, R.out_len, R.ap.row_act, c->stream));
+        break;
+      }
+      case GN_LAYER_DROPOUT:
+        if (M->training)
+          HIP_OK(c, launch_dropout(cur, R.mask, R.scale, R.out, B, R.out_len, c->stream));
+        else
+          HIP_OK(c, hipMemcpyAsync(R.out, cur, (size_t)B * R.out_len * sizeof(float),
+                                   hipMemcpyDeviceToDevice, c->stream));
+        break;
+      case GN_LAYER_FLATTEN:
+        R.out = const_cast<float *>(cur);
+        break;
+      default:
+        return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
+    }
+    cur = R.out;
+  }
+  return GN_OK;
+}
+
+// Backward over B samples.  The output layer's dz is in L.back().gout.
+static int model_backward(gn_model *M, const float *x, int B, float scale) {
+  gn_ctx *c = M->ctx;
+  const int n = (int)M->L.size();
+  bool is_dz = true;  // gout of the current layer already holds dz
+  for (int i = n - 1; i >= 0; --i) {
+    LayerRT &R = M->L[i];
+    const float *in = i == 0 ? x : M->L[i - 1].out;
+    LayerRT *below = i > 0 ? &M->L[i - 1] : nullptr;
+    // Layers below that are Flatten alias their gout to ours.
+    switch (R.d.kind) {
+      case GN_LAYER_DENSE: {
+        const float *W = M->params + R.poff;
+        float *gW = M->grads + R.poff;
+        float *gB = gW + (int64_t)R.d.in_size * R.d.out_size;
+        float *dz = R.gout;
+        if (!is_dz) HIP_OK(c, launch_dact(R.gout, R.out, dz, (int64_t)B * R.out_len, R.ap.deriv, c->stream));
+        float *gin = nullptr;
+        const float *aux = nullptr;
+        int deriv = 0;
+        bool next_dz = false;
+        if (below) {
+          gin = below->gout;  // Flatten's gout aliases the buffer of the layer under it
+          if (below->d.kind == GN_LAYER_DENSE && !below->ap.jac) {
+            aux = below->out;  // fuse act' of the layer below into the dX epilogue
+            deriv = below->ap.deriv;
+            next_dz = true;
+          }
+        }
+        HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, gB, gin, B, R.d.in_size, R.d.out_size, scale,
+                                 aux, deriv));
+        is_dz = next_dz;
+        break;
+      }
+      case GN_LAYER_DROPOUT: {
+        // dropout.go:283-290; the training flag is on during TrainBatch
+        if (below && below->d.kind != GN_LAYER_FLATTEN)
+          HIP_OK(c, launch_dropout(R.gout, R.mask, R.scale, below->gout, B, R.out_len, c->stream));
+        else if (below)
+          return set_err(c, GN_ERR_UNSUPPORTED, "Flatten below Dropout");
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_FLATTEN:
+        break;  // gout aliased by the layer above
+      default:
+        return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
+    }
+  }
+  return GN_OK;
+}
+
+static int model_accumulate(gn_model *M, const float *x, const float *y, int B) {
+  gn_ctx *c = M->ctx;
+  if (B <= 0 || B > M->maxB) return set_err(c, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
+  if (!x || !y) return set_err(c, GN_ERR_INVALID, "null input");
+  int rc = model_forward(M, x, B, true);
+  if (rc) return rc;
+  LayerRT &O = M->L.back();
+  int row_act = O.ap.row_act;
+  HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
+                            O.ap.deriv, M->loss_kind, c->stream));
+  HIP_OK(c, launch_loss_mean(M->loss_rows, B, M->workers, M->loss_dev, c->stream));
+  // grads *= 1/B: float32 reciprocal (net.go:767-770), float32(1/float64(B))
+  // for the W-worker path (net.go:703-706).
+  const float scale = M->workers > 1 ? (float)(1.0 / (double)B) : 1.0f / (float)B;
+  rc = model_backward(M, x, B, scale);
+  if (rc) return rc;
+  M->last_B = B;
+  return GN_OK;
+}
+
+extern "C" int gn_model_step(gn_model *M) {
+  if (!M) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  M->timestep++;  // Adam.NewStep (opt.go:254-258)
+  const float b1 = M->adam.beta1, b2 = M->adam.beta2, eps = M->adam.eps;
+  const double ts = (double)(M->timestep + 1);
+  const float bias1 = (float)(1.0 - pow((double)b1, ts));
+  const float bias2 = (float)(1.0 - pow((double)b2, ts));
+  const float efflr = M->adam.lr * (float)sqrt((double)bias2) / bias1;
+  KTimer kt(c, GN_KCLASS_ADAM);
+  HIP_OK(c, launch_adam(M->params, M->grads, M->m, M->v, M->nparams, efflr, b1, b2, 1.0f - b1,
+                        1.0f - b2, eps, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_accumulate_device(gn_model *M, const float *x, const float *y, int32_t B) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  return model_accumulate(M, x, y, B);
+}
+
+extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const float *y, int32_t B) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  int rc = model_accumulate(M, x, y, B);
+  if (rc) return rc;
+  return gn_model_step(M);
+}
+
+extern "C" int gn_model_train_step(gn_model *M, const float *x, const float *y, int32_t B,
+                                   float *loss_out) {
+  if (!M) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  if (B <= 0 || B > M->maxB) return set_err(c, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
+  if (!x || !y) return set_err(c, GN_ERR_INVALID, "null input");
+  HIP_OK(c, hipMemcpyAsync(M->xin, x, (size_t)B * M->L[0].in_len * sizeof(float),
+                           hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipMemcpyAsync(M->yin, y, (size_t)B * M->L.back().out_len * sizeof(float),
+                           hipMemcpyHostToDevice, c->stream));
+  int rc = model_accumulate(M, M->xin, M->yin, B);
+  if (rc) return rc;
+  if ((rc = gn_model_step(M))) return rc;
+  if (loss_out) return gn_model_read_loss(M, loss_out);
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
+  if (!M || !loss) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  HIP_OK(c, hipMemcpyAsync(loss, M->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *out) {
+  if (!M) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  if (B <= 0 || B > M->maxB || !x || !out) return set_err(c, GN_ERR_INVALID, "bad predict args");
+  const int saved = M->training;
+  M->training = 0;  // Sequential.Predict sets training=false (sequential.go:118-122)
+  HIP_OK(c, hipMemcpyAsync(M->xin, x, (size_t)B * M->L[0].in_len * sizeof(float),
+                           hipMemcpyHostToDevice, c->stream));
+  int rc = model_forward(M, M->xin, B, false);
+  M->training = saved;
+  if (rc) return rc;
+  LayerRT &O = M->L.back();
+  HIP_OK(c, hipMemcpyAsync(out, O.out, (size_t)B * O.out_len * sizeof(float),
+                           hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_layer_output(gn_model *M, int32_t layer, float *dst, int64_t n) {
+  if (!M || layer < 0 || layer >= (int)M->L.size() || !dst) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  LayerRT &R = M->L[layer];
+  const int64_t have = (int64_t)M->last_B * R.out_len;
+  if (n > have) return set_err(c, GN_ERR_INVALID, "asked %lld > %lld", (long long)n, (long long)have);
+  HIP_OK(c, hipMemcpyAsync(dst, R.out, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_layer_argmax(gn_model *M, int32_t layer, int32_t *dst, int64_t n) {
+  if (!M || layer < 0 || layer >= (int)M->L.size() || !dst) return GN_ERR_INVALID;
+  return set_err(M->ctx, GN_ERR_UNSUPPORTED, "layer %d has no argmax switches", layer);
+}

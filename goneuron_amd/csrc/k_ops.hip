@@ -1,0 +1,362 @@
+// Memory-bound kernels of the training step: Adam over the flat arena, bias
+// gradient column sums, activation derivatives, the output-layer row kernel
+// (row activation + loss + loss gradient + activation Jacobian), dropout and
+// the batch-mean loss.
+//
+// Rounding follows the reference's float32 expression order (the library is
+// built with -ffp-contract=off; divisions and square roots are the correctly
+// rounded __fdiv_rn / __fsqrt_rn), and transcendentals go through double
+// precision exactly where the Go code calls math.Exp / math.Log / math.Tanh
+// on float64 arguments.
+#include "gn_common.h"
+
+namespace gn {
+
+constexpr int TPB = 256;
+
+// ---------------------------------------------------------------------------
+// Adam.StepInPlace, opt.go:244-251:
+//   m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; p -= effLR*m/(sqrt(v)+eps)
+// 28 bytes of HBM traffic per parameter (read p,g,m,v; write p,m,v).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float efflr, float b1,
+                                      float b2, float omb1, float omb2, float eps) {
+  const float mi = __fadd_rn(__fmul_rn(b1, m), __fmul_rn(omb1, g));
+  const float vi = __fadd_rn(__fmul_rn(b2, v), __fmul_rn(__fmul_rn(omb2, g), g));
+  m = mi;
+  v = vi;
+  p = __fsub_rn(p, __fdiv_rn(__fmul_rn(efflr, mi), __fadd_rn(__fsqrt_rn(vi), eps)));
+}
+
+__global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
+                                                   const float *__restrict__ g,
+                                                   float *__restrict__ m, float *__restrict__ v,
+                                                   int64_t n, float efflr, float b1, float b2,
+                                                   float omb1, float omb2, float eps) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const int64_t n4 = n >> 2;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  f4v *p4 = reinterpret_cast<f4v *>(p);
+  const f4v *g4 = reinterpret_cast<const f4v *>(g);
+  f4v *m4 = reinterpret_cast<f4v *>(m);
+  f4v *v4 = reinterpret_cast<f4v *>(v);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    f4v pp = __builtin_nontemporal_load(p4 + i);
+    const f4v gg = __builtin_nontemporal_load(g4 + i);
+    f4v mm = __builtin_nontemporal_load(m4 + i);
+    f4v vv = __builtin_nontemporal_load(v4 + i);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float pq = pp[q], mq = mm[q], vq = vv[q];
+      adam1(pq, gg[q], mq, vq, efflr, b1, b2, omb1, omb2, eps);
+      pp[q] = pq;
+      mm[q] = mq;
+      vv[q] = vq;
+    }
+    __builtin_nontemporal_store(pp, p4 + i);
+    __builtin_nontemporal_store(mm, m4 + i);
+    __builtin_nontemporal_store(vv, v4 + i);
+  }
+  // scalar tail (n % 4 elements), handled by the first threads of block 0
+  if (blockIdx.x == 0) {
+    const int64_t i = (n4 << 2) + threadIdx.x;
+    if (i < n) adam1(p[i], g[i], m[i], v[i], efflr, b1, b2, omb1, omb2, eps);
+  }
+}
+
+hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,
+                       float b1, float b2, float omb1, float omb2, float eps, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const int64_t n4 = n >> 2;
+  int64_t blocks = (n4 + TPB - 1) / TPB;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(adam_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
+                     b1, b2, omb1, omb2, eps);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Bias gradient: db[o] = scale * sum_b dz[b, o]   (gradB += dz, layer.go:566;
+// averaged by grads *= 1/B, net.go:767-770).  Two passes: 64-column strips x
+// row chunks -> partials (one per chunk), then an in-order sum of partials.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(TPB) void colsum_partial(const float *__restrict__ dz, int rows,
+                                                      int cols, int ld, int rows_per_chunk,
+                                                      float *__restrict__ part) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  const int r0 = blockIdx.y * rows_per_chunk;
+  const int r1 = min(rows, r0 + rows_per_chunk);
+  float s = 0.f;
+  if (col < cols)
+    for (int r = r0 + w; r < r1; r += 4) s += dz[(size_t)r * ld + col];
+  red[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && col < cols)
+    part[(size_t)blockIdx.y * cols + col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+__global__ __launch_bounds__(TPB) void colsum_final(const float *__restrict__ part, int chunks,
+                                                    int cols, float scale, float *__restrict__ out) {
+  const int col = blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= cols) return;
+  float s = 0.f;
+  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols + col];
+  out[col] = s * scale;
+}
+
+hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
+                         float *scratch, size_t scratch_cap, hipStream_t s) {
+  if (cols <= 0) return hipSuccess;
+  if ((size_t)cols > scratch_cap) return hipErrorInvalidValue;
+  int chunks = (rows + 63) / 64;
+  if (chunks > 64) chunks = 64;
+  if ((size_t)chunks * cols > scratch_cap) chunks = (int)(scratch_cap / cols);
+  if (chunks < 1) chunks = 1;
+  const int rpc = (rows + chunks - 1) / chunks;
+  dim3 g1((cols + 63) / 64, chunks);
+  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, dz, rows, cols, ld, rpc, scratch);
+  hipLaunchKernelGGL(colsum_final, dim3((cols + TPB - 1) / TPB), dim3(TPB), 0, s, scratch, chunks,
+                     cols, scale, out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Activation derivative from the saved output (Dense/Conv default branch:
+// dz = grad * act.Derivative(preAct), layer.go:561-567).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float deriv_of(float out, int kind) {
+  switch (kind) {
+    case D_RELU: return out > 0.0f ? 1.0f : 0.0f;
+    case D_SIGMOID: return out * (1.0f - out);
+    case D_TANH: return 1.0f - out * out;
+    case D_NAN: return __builtin_nanf("");
+    default: return 1.0f;
+  }
+}
+
+__device__ __forceinline__ float fwd_of(float v, int kind) {
+  switch (kind) {
+    case F_RELU: return v > 0.0f ? v : 0.0f;
+    case F_SIGMOID: return 1.0f / (1.0f + (float)exp((double)(-v)));
+    case F_TANH: return (float)tanh((double)v);
+    case F_NAN: return __builtin_nanf("");
+    default: return v;
+  }
+}
+
+__global__ __launch_bounds__(TPB) void dact_kernel(const float *__restrict__ g,
+                                                   const float *__restrict__ out,
+                                                   float *__restrict__ dz, int64_t n, int kind) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dz[i] = g[i] * deriv_of(out[i], kind);
+}
+
+hipError_t launch_dact(const float *g, const float *out, float *dz, int64_t n, int kind,
+                       hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + TPB - 1) / TPB;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(dact_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, g, out, dz, n, kind);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(TPB) void act_kernel(float *__restrict__ x, int64_t n, int kind) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = fwd_of(x[i], kind);
+}
+
+hipError_t launch_act_inplace(float *x, int64_t n, int kind, hipStream_t s) {
+  if (n <= 0 || kind == F_IDENTITY) return hipSuccess;
+  int64_t blocks = (n + TPB - 1) / TPB;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(act_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, x, n, kind);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Block reductions (256 threads = 4 wave64s).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float block_sum(float v, float *sh) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+__device__ __forceinline__ float block_max(float v, float *sh) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+
+// Row activation (Softmax.ActivateBatch activations.go:161-183 /
+// LogSoftmax.ActivateBatch :204-236), in place over one row.
+__device__ void row_activate(float *row, int C, int row_act, int fwd, float *sh) {
+  const int t = threadIdx.x;
+  if (row_act == ROW_SOFTMAX || row_act == ROW_LOGSOFTMAX) {
+    float mx = -__builtin_inff();
+    for (int i = t; i < C; i += TPB) mx = fmaxf(mx, row[i]);
+    mx = block_max(mx, sh);
+    float s = 0.f;
+    for (int i = t; i < C; i += TPB) s += (float)exp((double)(row[i] - mx));
+    s = block_sum(s, sh);
+    if (row_act == ROW_SOFTMAX) {
+      for (int i = t; i < C; i += TPB) row[i] = __fdiv_rn((float)exp((double)(row[i] - mx)), s);
+    } else {
+      const float ls = (float)log((double)s);
+      for (int i = t; i < C; i += TPB) row[i] = row[i] - mx - ls;
+    }
+  } else if (row_act == ROW_ELEMWISE) {
+    for (int i = t; i < C; i += TPB) row[i] = fwd_of(row[i], fwd);
+  }
+}
+
+// Output layer: z (pre-activations, overwritten by the activation output),
+// per-sample loss (loss.go:53-67 MSE, :120-141 CE), loss gradient
+// (loss.go:90-105, :165-178) and dz through the activation (Q4):
+//   Softmax    dz_k = sum_i g_i p_i (d_ik - p_k) = p_k g_k - p_k sum_i g_i p_i  (layer.go:504-529)
+//   LogSoftmax dz_k = sum_i g_i (d_ik - exp(o_k)) = g_k - exp(o_k) sum_i g_i     (layer.go:530-560)
+//   otherwise  dz_k = g_k * Derivative                                          (layer.go:561-567)
+__global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
+                                                       const float *__restrict__ y,
+                                                       float *__restrict__ dz,
+                                                       float *__restrict__ loss_rows, int C,
+                                                       int row_act, int fwd, int deriv,
+                                                       int loss_kind) {
+  __shared__ float sh[4];
+  const int b = blockIdx.x, t = threadIdx.x;
+  float *o = zo + (size_t)b * C;
+  const float *yr = y + (size_t)b * C;
+  float *d = dz + (size_t)b * C;
+  row_activate(o, C, row_act, fwd, sh);
+  __syncthreads();
+  // loss and its gradient g (kept in d)
+  float l = 0.f;
+  if (loss_kind == GN_LOSS_MSE) {
+    const float factor = __fdiv_rn(2.0f, (float)C);
+    for (int i = t; i < C; i += TPB) {
+      const float df = o[i] - yr[i];
+      l += df * df;
+      d[i] = factor * df;
+    }
+    l = block_sum(l, sh);
+    l = __fdiv_rn(l, (float)C);
+  } else {
+    for (int i = t; i < C; i += TPB) {
+      float pv = o[i];
+      if (pv < 1e-10f) pv = 1e-10f;
+      const float yi = yr[i];
+      l -= yi * (float)log((double)pv);
+      d[i] = o[i] - yi;
+    }
+    l = block_sum(l, sh);
+  }
+  if (t == 0) loss_rows[b] = l;
+  // Jacobian / derivative
+  if (row_act == ROW_SOFTMAX) {
+    float s1 = 0.f;
+    for (int i = t; i < C; i += TPB) s1 += d[i] * o[i];
+    s1 = block_sum(s1, sh);
+    for (int i = t; i < C; i += TPB) d[i] = d[i] * o[i] - o[i] * s1;
+  } else if (row_act == ROW_LOGSOFTMAX) {
+    float s1 = 0.f;
+    for (int i = t; i < C; i += TPB) s1 += d[i];
+    s1 = block_sum(s1, sh);
+    for (int i = t; i < C; i += TPB) d[i] = d[i] - (float)exp((double)o[i]) * s1;
+  } else {
+    for (int i = t; i < C; i += TPB) d[i] = d[i] * deriv_of(o[i], deriv);
+  }
+}
+
+hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz, float *loss_rows,
+                           int B, int C, int row_act, int deriv, int loss_kind, hipStream_t s) {
+  (void)z;  // activation is computed in place on `out` (which holds z)
+  if (B <= 0) return hipSuccess;
+  // fwd kind for ROW_ELEMWISE rides in the high bits of row_act
+  const int fwd = row_act >> 8;
+  hipLaunchKernelGGL(out_rows_kernel, dim3(B), dim3(TPB), 0, s, out, y, dz, loss_rows, C,
+                     row_act & 0xff, fwd, deriv, loss_kind);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(TPB) void row_act_kernel(float *__restrict__ x, int C, int row_act,
+                                                      int fwd) {
+  __shared__ float sh[4];
+  row_activate(x + (size_t)blockIdx.x * C, C, row_act, fwd, sh);
+}
+
+hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) {
+  if (B <= 0 || (row_act & 0xff) == ROW_NONE) return hipSuccess;
+  hipLaunchKernelGGL(row_act_kernel, dim3(B), dim3(TPB), 0, s, out, C, row_act & 0xff,
+                     row_act >> 8);
+  return hipGetLastError();
+}
+
+// Batch loss: totalLoss accumulates per sample in order (net.go:744), per
+// worker chunk then in worker order for W > 1 (net.go:679-716); / B.
+__global__ void loss_mean_kernel(const float *__restrict__ rows, int B, int W,
+                                 float *__restrict__ loss) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float total = 0.f;
+  if (W <= 1) {
+    for (int i = 0; i < B; ++i) total += rows[i];
+  } else {
+    const int chunk = (B + W - 1) / W;
+    for (int w = 0; w < W; ++w) {
+      float local = 0.f;
+      for (int i = w * chunk; i < min(B, (w + 1) * chunk); ++i) local += rows[i];
+      total += local;
+    }
+  }
+  *loss = __fdiv_rn(total, (float)B);
+}
+
+hipError_t launch_loss_mean(const float *rows, int B, int W, float *loss, hipStream_t s) {
+  hipLaunchKernelGGL(loss_mean_kernel, dim3(1), dim3(64), 0, s, rows, B, W, loss);
+  return hipGetLastError();
+}
+
+// Dropout with the per-feature mask of Q9 (dropout.go:138-150 forward,
+// :283-290 backward): out = mask ? x*scale : 0.
+__global__ __launch_bounds__(TPB) void dropout_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ mask, float scale,
+                                                      float *__restrict__ out, int64_t total,
+                                                      int n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float mk = mask[i % n];
+    out[i] = mk > 0.f ? x[i] * scale : 0.0f;
+  }
+}
+
+hipError_t launch_dropout(const float *x, const float *mask, float scale, float *out, int B, int n,
+                          hipStream_t s) {
+  const int64_t total = (int64_t)B * n;
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + TPB - 1) / TPB;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(dropout_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, x, mask, scale, out,
+                     total, n);
+  return hipGetLastError();
+}
+
+}  // namespace gn

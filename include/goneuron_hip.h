@@ -1,0 +1,207 @@
+/*
+ * goneuron_hip.h — C ABI of libgoneuron_hip.so, the MI355X (gfx950) training
+ * backend for GoNeuron's fp32 training step (forward + backward + Adam).
+ *
+ * The library replaces the reference's per-sample CPU loop and its Metal cgo
+ * bridge.  Every entry point below names the reference interface it stands in
+ * for (paths relative to the GoNeuron tree).  Conventions:
+ *   - every call returns an int status: GN_OK (0) or a negative GN_ERR_* code;
+ *     gn_last_error() gives the message of the last failure on a context
+ *     (the reference's Metal ABI returns void and drops errors,
+ *     internal/layer/metal.go:270-274);
+ *   - host pointers are read or written only during the call, never retained;
+ *   - "_device" entry points take device pointers (HBM-resident inputs);
+ *   - one HIP stream per context; a context is not thread-safe (the Go side
+ *     serialises calls with a mutex, as MetalDevice.mu does, metal.go:70).
+ */
+#ifndef GONEURON_HIP_H
+#define GONEURON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define GN_OK 0
+#define GN_ERR_INVALID (-1)     /* bad argument (null, size, kind) */
+#define GN_ERR_HIP (-2)         /* HIP runtime error */
+#define GN_ERR_OOM (-3)         /* device allocation failed */
+#define GN_ERR_UNSUPPORTED (-4) /* layer/activation combination not built */
+#define GN_ERR_SHAPE (-5)       /* input size mismatch (layer.go:347-349) */
+#define GN_ERR_INJECTED (-6)    /* forced by gn_debug_fail_next */
+#define GN_ERR_NO_DEVICE (-7)   /* no HIP device */
+#define GN_ERR_INDEX (-8)       /* index out of range (embedding.go:126-128) */
+
+/* ---- activation codes ---------------------------------------------------
+ * A layer carries the activation *object* the Go code was given and whether it
+ * was a pointer (&activations.Softmax{}) or a value (activations.Softmax{}),
+ * because Dense dispatches on cacheActivationType (layer.go:183-205), which
+ * only recognises pointer Softmax/LogSoftmax: the facade's values run as
+ * identity forward and NaN derivative (activations.go:150-158). */
+#define GN_ACT_NIL 0
+#define GN_ACT_RELU 1
+#define GN_ACT_SIGMOID 2
+#define GN_ACT_TANH 3
+#define GN_ACT_SOFTMAX 4
+#define GN_ACT_LOGSOFTMAX 5
+#define GN_ACT_LINEAR 6
+
+/* ---- layer kinds (the []layer.Layer given to goneuron.NewSequential) ----- */
+#define GN_LAYER_DENSE 1         /* layer.NewDense            layer.go:267 */
+#define GN_LAYER_DROPOUT 2       /* layer.NewDropout          dropout.go:47 */
+#define GN_LAYER_CONV2D 3        /* layer.NewConv2D           conv2d.go:74 */
+#define GN_LAYER_MAXPOOL2D 4     /* layer.NewMaxPool2D        maxpool2d.go:45 */
+#define GN_LAYER_FLATTEN 5       /* layer.NewFlatten          reshape.go:29 */
+#define GN_LAYER_EMBEDDING 6     /* layer.NewEmbedding        embedding.go */
+#define GN_LAYER_POSENC 7        /* layer.NewPositionalEncoding transformer.go:51 */
+#define GN_LAYER_TRANSFORMER 8   /* layer.NewTransformerBlockE transformer.go:908 */
+#define GN_LAYER_CLSPOOL 9       /* layer.NewCLSPooling       transformer.go:1679 */
+#define GN_LAYER_LSTM_UNROLLER 10 /* SequenceUnroller(LSTM)   unroller.go:57, lstm.go */
+
+#define GN_LOSS_MSE 1            /* loss.MSE          loss.go:38-105 */
+#define GN_LOSS_CE 2             /* loss.CrossEntropy loss.go:108-178 */
+
+typedef struct gn_layer_desc {
+  int32_t kind;
+  int32_t in_size;      /* Dense in / Dropout & Flatten size / first-layer input length */
+  int32_t out_size;     /* Dense out / LSTM hidden */
+  int32_t act;          /* GN_ACT_* */
+  int32_t act_is_ptr;   /* 1 when the Go activation is a pointer */
+  int32_t in_channels;  /* Conv2D / MaxPool2D; -1 = lazy (MaxPool runs as 1 channel) */
+  int32_t out_channels;
+  int32_t kernel, stride, padding;
+  float p;              /* Dropout probability */
+  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim;
+  int32_t return_sequences;
+} gn_layer_desc;
+
+typedef struct gn_adam_desc {   /* opt.NewAdam opt.go:117-126 */
+  float lr, beta1, beta2, eps;  /* zeros select the reference defaults */
+} gn_adam_desc;
+
+typedef struct gn_info {
+  char arch[64];
+  int32_t cu_count;
+  int64_t hbm_bytes;
+  double peak_fp32_mfma_tflops; /* dense fp32 matrix peak */
+  double peak_hbm_gbps;
+} gn_info;
+
+typedef struct gn_ctx gn_ctx;
+typedef struct gn_model gn_model;
+
+/* ---- context -------------------------------------------------------------
+ * Replaces layer.GetDefaultDevice / MetalDevice construction
+ * (internal/layer/device.go:39-48, metal.go:76-98). */
+int gn_available(void);                      /* 1 when a HIP device is present */
+int gn_init(int device_ordinal, gn_ctx **out);
+void gn_shutdown(gn_ctx *ctx);
+const char *gn_last_error(const gn_ctx *ctx);
+int gn_device_info(gn_ctx *ctx, gn_info *info);
+int gn_sync(gn_ctx *ctx);                    /* waitForMetal, metal_ops.m:1002-1007 */
+/* Test hook: the next entry point that takes this context fails with `code`. */
+int gn_debug_fail_next(gn_ctx *ctx, int code);
+
+/* ---- device buffers (createMetalBuffer / update / read, metal.go:6-50) --- */
+int gn_malloc(gn_ctx *ctx, size_t bytes, void **dptr);
+int gn_free(gn_ctx *ctx, void *dptr);
+int gn_memcpy_h2d(gn_ctx *ctx, void *dst, const void *src, size_t bytes);
+int gn_memcpy_d2h(gn_ctx *ctx, void *dst, const void *src, size_t bytes);
+int gn_memset_zero(gn_ctx *ctx, void *dst, size_t bytes);
+
+/* ---- model: Sequential.Compile + Network.initBuffers --------------------
+ * sequential.go:26-87, net.go:91-127: layers are built with the reference's
+ * seeded LCG initialisation into one device-resident flat arena
+ * (params | grads | Adam m | Adam v).  `workers` is the trainBatchParallel
+ * worker count W (net.go:588-608; 1 = trainBatchSequential). */
+int gn_model_create(gn_ctx *ctx, const gn_layer_desc *layers, int32_t nlayers,
+                    int32_t loss_kind, const gn_adam_desc *adam, int32_t max_batch,
+                    int32_t workers, gn_model **out);
+void gn_model_destroy(gn_model *m);
+int gn_model_nparams(gn_model *m, int64_t *n);
+int gn_model_layer_params(gn_model *m, int32_t layer, int64_t *offset, int64_t *count);
+int gn_model_out_size(gn_model *m, int32_t *n);
+/* Network.Params / SetParams / Gradients (net.go:549-572, 787-846). */
+int gn_model_get_params(gn_model *m, float *dst, int64_t offset, int64_t n);
+int gn_model_set_params(gn_model *m, const float *src, int64_t offset, int64_t n);
+int gn_model_get_grads(gn_model *m, float *dst, int64_t offset, int64_t n);
+int gn_model_get_adam(gn_model *m, float *m_dst, float *v_dst, int64_t offset, int64_t n,
+                      int32_t *timestep);
+/* Device pointers of the arena regions (for zero-copy callers). */
+int gn_model_arena(gn_model *m, float **params, float **grads, float **adam_m, float **adam_v);
+
+/* Network.TrainBatch (net.go:412-436): one fwd+bwd over B samples, gradient
+ * average, Adam step.  Host inputs: x is B x in_size, y is B x out_size
+ * (row major, the [][]float32 batches flattened).  loss_out may be NULL. */
+int gn_model_train_step(gn_model *m, const float *x, const float *y, int32_t B, float *loss_out);
+/* Same with HBM-resident x / y; the mean loss stays on the device (read it
+ * with gn_model_read_loss).  No host synchronisation. */
+int gn_model_train_step_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
+/* Forward + backward + average only (grads valid, no Adam step). */
+int gn_model_accumulate_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
+/* Network.Step (net.go:260-284): Adam.NewStep + StepInPlace on the arena. */
+int gn_model_step(gn_model *m);
+int gn_model_read_loss(gn_model *m, float *loss);
+/* Sequential.Predict / PredictBatch (sequential.go:118-160): inference mode
+ * forward of B samples; out is B x out_size. */
+int gn_model_predict(gn_model *m, const float *x, int32_t B, float *out);
+int gn_model_set_training(gn_model *m, int32_t training);
+/* Layer probes for parity tests: saved output of `layer` for the last batch
+ * (B x out_len), MaxPool2D argmax switches (B x out_len, int32). */
+int gn_model_layer_output(gn_model *m, int32_t layer, float *dst, int64_t n);
+int gn_model_layer_argmax(gn_model *m, int32_t layer, int32_t *dst, int64_t n);
+
+/* ---- per-layer operators on device pointers -----------------------------
+ * Batched stand-ins for the per-sample Layer.Forward / Backward calls and the
+ * Metal entry points listed next to each. */
+
+/* matMulFusedPersistent + bias_activation (metal_ops.m:1235-1249, 171-195) /
+ * Dense.ForwardWithArena (layer.go:346-456): out[b,o] = act(b[o] + x[b,:].W[o,:]).
+ * Softmax/LogSoftmax pointers apply the row activation. */
+int gn_dense_forward(gn_ctx *ctx, const float *x, const float *W, const float *bias, float *out,
+                     int32_t B, int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr);
+/* Dense.Backward (layer.go:488-667) for a batch: dz from gout and the saved
+ * output, gradW = scale*dz^T x, gradB = scale*colsum(dz) (overwrite), and
+ * gin = dz W when gin != NULL. */
+int gn_dense_backward(gn_ctx *ctx, const float *x, const float *W, const float *out,
+                      const float *gout, float *gradW, float *gradB, float *gin, float *dz_scratch,
+                      int32_t B, int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr,
+                      float scale);
+/* Generic fp32 MFMA GEMM: C[M,N] = alpha * op(A) op(B); trans flags as BLAS
+ * (A is M x K row-major when transA == 0, K x M when 1; B is K x N when
+ * transB == 0, N x K when 1).  Stands in for matMulMPSPersistent
+ * (metal_ops.m:1220-1233). */
+int gn_gemm(gn_ctx *ctx, int32_t transA, int32_t transB, int32_t M, int32_t N, int32_t K,
+            float alpha, const float *A, int32_t lda, const float *B, int32_t ldb, float *C,
+            int32_t ldc);
+/* Adam.StepInPlace (opt.go:207-252) over n elements of the flat arena, with
+ * the optimizer timestep already advanced (first Network.Step => 1). */
+int gn_adam_step(gn_ctx *ctx, float *params, const float *grads, float *m, float *v, int64_t n,
+                 float lr, float beta1, float beta2, float eps, int32_t timestep);
+
+/* ---- kernel timing (measurement hook; no reference counterpart) ---------
+ * While enabled, every kernel launch of the library is bracketed by HIP events
+ * on the context stream and attributed to a class.  gn_timing_report
+ * synchronises the stream and returns the launch count and summed kernel time
+ * of a class since the last enable. */
+#define GN_KCLASS_GEMM 0   /* gemm_f32_mfma (Dense fwd / dX / dW) */
+#define GN_KCLASS_ADAM 1   /* adam_kernel */
+#define GN_KCLASS_OTHER 2  /* row kernels, column sums, dropout, ... */
+int gn_timing_enable(gn_ctx *ctx, int enable);
+int gn_timing_report(gn_ctx *ctx, int kclass, int64_t *launches, double *total_ms);
+
+/* ---- synthetic inputs (host side; harness utility) ----------------------
+ * The reference's LCG (layer.go:61-81): U[0,1) stream, N(0,1) by one
+ * Box-Muller cosine per two draws (u1 clamped to 1e-7, f64 math), class ids
+ * floor(U*nclass) clamped to nclass-1. */
+int gn_fill_uniform(float *dst, int64_t n, uint64_t seed);
+int gn_fill_normal(float *dst, int64_t n, uint64_t seed);
+int gn_fill_class_ids(int32_t *dst, int64_t n, int32_t nclass, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GONEURON_HIP_H */

@@ -1,0 +1,51 @@
+"""Test helpers: build the CPU oracle network for a neutral config description
+(goneuron_amd.configs) and compare tensors by the BASELINE tolerances."""
+import numpy as np
+
+ACT = {"relu": 1, "sigmoid": 2, "tanh": 3, "softmax": 4, "logsoftmax": 5, "linear": 6}
+
+
+def oracle_specs(refcpu, cfg):
+    specs = []
+    for i, d in enumerate(cfg["layers"]):
+        k = d["kind"]
+        if k == "dense":
+            specs.append(refcpu.spec(refcpu.LAYER_DENSE, in_size=d["in"], out_size=d["out"],
+                                     act=ACT[d["act"]], act_is_ptr=int(d["ptr"])))
+        elif k == "dropout":
+            specs.append(refcpu.spec(refcpu.LAYER_DROPOUT, in_size=d["n"], p=d["p"]))
+        elif k == "flatten":
+            specs.append(refcpu.spec(refcpu.LAYER_FLATTEN, in_size=d["n"]))
+        elif k == "conv2d":
+            specs.append(refcpu.spec(refcpu.LAYER_CONV2D, in_size=cfg["in_len"], in_channels=d["inC"],
+                                     out_channels=d["outC"], kernel=d["k"], stride=d["s"],
+                                     padding=d["p"], act=ACT[d["act"]]))
+        elif k == "maxpool2d":
+            specs.append(refcpu.spec(refcpu.LAYER_MAXPOOL2D, in_channels=d["inC"], kernel=d["k"],
+                                     stride=d["s"], padding=d["p"]))
+        else:
+            raise NotImplementedError(k)
+    return specs
+
+
+def oracle_net(refcpu, cfg, workers=1):
+    return refcpu.Net(oracle_specs(refcpu, cfg), refcpu.LOSS_CE if cfg["loss"] == "ce" else refcpu.LOSS_MSE,
+                      lr=cfg["lr"], workers=workers)
+
+
+def max_rel(a, r):
+    """max|a - r| / max|r| (BASELINE per-tensor gradient tolerance)."""
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    den = np.abs(r).max()
+    if den == 0:
+        return float(np.abs(a).max())
+    return float(np.abs(a - r).max() / den)
+
+
+def norm_rel(a, r):
+    """||a - r||_2 / ||r||_2 (BASELINE updated-weight tolerance)."""
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    den = np.linalg.norm(r)
+    return float(np.linalg.norm(a - r) / den) if den else float(np.linalg.norm(a))

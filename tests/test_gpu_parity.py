@@ -1,0 +1,241 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the
+same seeded inputs, and against torch fp32 for full-size GEMM work.
+
+Tolerances: gradients and loss max|a-r|/max|r| <= 1e-4 per
+tensor; updated weights ||a-r||/||r|| <= 1e-4; Adam on identical inputs and
+argmax switches bit-exact.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from cfgutil import max_rel, norm_rel, oracle_net
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gn():
+    import goneuron_amd as gn
+    gn.GetDefaultDevice()
+    return gn
+
+
+@pytest.fixture(scope="module")
+def dev(gn):
+    return gn.GetDefaultDevice()
+
+
+class DBuf:
+    """A device buffer holding a numpy array (float32 or int32)."""
+
+    def __init__(self, dev, arr):
+        from goneuron_amd._lib import lib, check
+        self.lib, self.check, self.dev = lib(), check, dev
+        self.arr = np.ascontiguousarray(arr)
+        self.p = C.c_void_p()
+        check(dev.h, self.lib.gn_malloc(dev.h, max(self.arr.nbytes, 4), C.byref(self.p)))
+        if self.arr.nbytes:
+            check(dev.h, self.lib.gn_memcpy_h2d(dev.h, self.p, self.arr.ctypes.data, self.arr.nbytes))
+
+    def get(self):
+        out = np.empty_like(self.arr)
+        self.check(self.dev.h, self.lib.gn_memcpy_d2h(self.dev.h, out.ctypes.data, self.p, out.nbytes))
+        return out
+
+    def __del__(self):
+        try:
+            self.lib.gn_free(self.dev.h, self.p)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K,pad", [(128, 128, 32, 0), (200, 136, 72, 0), (37, 91, 53, 0),
+                                       (256, 384, 1000, 4), (10, 128, 64, 0), (64, 10, 128, 1),
+                                       (1, 7, 5, 0)])
+def test_gemm_layouts(gn, dev, ta, tb, M, N, K, pad):
+    log(f"gemm ta={ta} tb={tb} M={M} N={N} K={K} pad={pad}")
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    A = rng.normal(size=(K, M) if ta else (M, K)).astype(np.float32)
+    Bm = rng.normal(size=(N, K) if tb else (K, N)).astype(np.float32)
+    lda = A.shape[1] + pad
+    ldb = Bm.shape[1] + pad
+    Ap = np.zeros((A.shape[0], lda), np.float32)
+    Ap[:, :A.shape[1]] = A
+    Bp = np.zeros((Bm.shape[0], ldb), np.float32)
+    Bp[:, :Bm.shape[1]] = Bm
+    dA, dB = DBuf(dev, Ap), DBuf(dev, Bp)
+    dC = DBuf(dev, np.zeros((M, N), np.float32))
+    from goneuron_amd._lib import lib, check
+    check(dev.h, lib().gn_gemm(dev.h, ta, tb, M, N, K, 0.5, dA.p, lda, dB.p, ldb, dC.p, N))
+    opA = A.T.astype(np.float64) if ta else A.astype(np.float64)
+    opB = Bm.T.astype(np.float64) if tb else Bm.astype(np.float64)
+    ref = 0.5 * opA @ opB
+    got = dC.get()
+    scale = 0.5 * np.abs(opA) @ np.abs(opB)
+    assert (np.abs(got - ref) <= 2e-6 * scale + 1e-30).all()
+
+
+# ------------------------------------------------------------------ Adam
+def test_adam_bit_exact(gn, dev, oracle):
+    rng = np.random.default_rng(11)
+    n = 100003
+    p = rng.normal(size=n).astype(np.float32)
+    g = (rng.normal(size=n) * 10.0 ** rng.integers(-9, 1, n)).astype(np.float32)
+    m = (rng.normal(size=n) * 1e-3).astype(np.float32)
+    v = np.abs(rng.normal(size=n) * 1e-6).astype(np.float32)
+    dp, dg, dm, dv = DBuf(dev, p), DBuf(dev, g), DBuf(dev, m), DBuf(dev, v)
+    from goneuron_amd._lib import lib, check
+    for t in (1, 2, 7):
+        check(dev.h, lib().gn_adam_step(dev.h, dp.p, dg.p, dm.p, dv.p, n, 1e-3, 0.9, 0.999, 1e-8, t))
+        oracle.adam_step(p, g, m, v, 1e-3, 0.9, 0.999, 1e-8, t)
+    np.testing.assert_array_equal(dp.get(), p)
+    np.testing.assert_array_equal(dm.get(), m)
+    np.testing.assert_array_equal(dv.get(), v)
+
+
+# ------------------------------------------------------------------ model parity vs oracle
+def _compare_step(gn, oracle, cfg, steps=1, workers=1):
+    from goneuron_amd import configs
+    log(f"model parity {cfg['name']} B={cfg['B']} steps={steps} W={workers}")
+    x, y = configs.inputs(cfg)
+    B = cfg["B"]
+    model = configs.build(cfg, workers=workers)
+    net = oracle_net(oracle, cfg, workers=workers)
+    np.testing.assert_array_equal(model.Params(), net.params)  # LCG init is exact
+    for s in range(steps):
+        lg = model.TrainBatch(x, y)
+        lo = net.accumulate_batch(x, y, B)
+        g_gpu = model.Gradients()
+        g_ref = net.grads.copy()
+        assert abs(lg - lo) <= TOL * max(abs(lo), 1e-30), (s, lg, lo)
+        for i in range(len(cfg["layers"])):
+            sl = model.LayerParams(i)
+            if sl.stop > sl.start:
+                assert max_rel(g_gpu[sl], g_ref[sl]) <= TOL, (s, i, max_rel(g_gpu[sl], g_ref[sl]))
+        net.step()
+        p_gpu = model.Params()
+        for i in range(len(cfg["layers"])):
+            sl = model.LayerParams(i)
+            if sl.stop > sl.start:
+                assert norm_rel(p_gpu[sl], net.params[sl]) <= TOL, (s, i)
+        # keep the two runs on identical weights so each step is checked alone
+        net.params[:] = p_gpu
+    m_gpu, v_gpu, t = model.AdamState()
+    assert t == net.timestep
+    assert norm_rel(m_gpu, net.adam_m) <= TOL
+    assert norm_rel(v_gpu, net.adam_v) <= TOL
+    return model, net
+
+
+def test_mlp_full_config(gn, oracle):
+    from goneuron_amd import configs
+    _compare_step(gn, oracle, configs.mlp(), steps=3)
+
+
+def test_mlp_predict(gn, oracle):
+    from goneuron_amd import configs
+    cfg = configs.mlp()
+    x, _ = configs.inputs(cfg)
+    model = configs.build(cfg)
+    net = oracle_net(oracle, cfg)
+    net.set_training(False)
+    out = model.PredictBatch(x[:16])
+    for b in range(16):
+        np.testing.assert_allclose(out[b], net.forward(x[b]), rtol=1e-5, atol=1e-6)
+
+
+def test_wide_reduced(gn, oracle):
+    from goneuron_amd import configs
+    _compare_step(gn, oracle, configs.wide(width=256, classes=100, B=64), steps=2)
+
+
+def test_wide_reduced_workers(gn, oracle):
+    from goneuron_amd import configs
+    _compare_step(gn, oracle, configs.wide(width=128, classes=37, depth=2, B=48), steps=1, workers=4)
+
+
+def test_odd_batch_and_sizes(gn, oracle):
+    from goneuron_amd import configs
+    cfg = configs.wide(width=72, classes=13, depth=2, B=19)
+    cfg["layers"][0]["in"] = 72
+    _compare_step(gn, oracle, cfg, steps=2)
+
+
+# ------------------------------------------------------------------ full-size C3 vs torch fp32
+def test_wide_full_size_vs_torch(gn):
+    """C3 at BASELINE size: one step against torch fp32 autograd (Q4 Jacobian
+    fed through p.backward), on the same initial weights."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("torch has no GPU")
+    from goneuron_amd import configs
+    cfg = configs.wide()
+    log("wide full-size vs torch")
+    x, y = configs.inputs(cfg)
+    B = cfg["B"]
+    model = configs.build(cfg)
+    p0 = model.Params()
+    lg = model.TrainBatch(x, y)
+    g_gpu = model.Gradients()
+    p1 = model.Params()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    P = torch.tensor(p0, device=dev, requires_grad=True)
+    h = torch.tensor(x, device=dev)
+    off = 0
+    sl = []
+    for i, d in enumerate(cfg["layers"]):
+        n_w = d["in"] * d["out"]
+        W = P[off:off + n_w].view(d["out"], d["in"])
+        b = P[off + n_w:off + n_w + d["out"]]
+        sl.append(slice(off, off + n_w + d["out"]))
+        off += n_w + d["out"]
+        z = h @ W.T + b
+        h = torch.relu(z) if d["act"] == "relu" else torch.log_softmax(z, dim=1)
+    yt = torch.tensor(y, device=dev)
+    h.backward(((h - yt) / B).detach())
+    g_ref = P.grad.detach().cpu().numpy()
+    for i, s in enumerate(sl):
+        r = max_rel(g_gpu[s], g_ref[s])
+        log(f"  layer {i} grad max_rel {r:.3e}")
+        assert r <= TOL, (i, r)
+    # loss: CE of log-probabilities is the constant -log(1e-10) per sample (Q5)
+    assert abs(lg - 23.02585) < 1e-3
+    # Adam at t = 2 from zero moments, in float64 from the torch gradient
+    g = g_ref.astype(np.float64)
+    b1, b2 = float(np.float32(0.9)), float(np.float32(0.999))
+    eff = 1e-3 * np.sqrt(1 - b2 ** 2) / (1 - b1 ** 2)
+    p_ref = p0 - eff * (1 - b1) * g / (np.sqrt((1 - b2) * g * g) + 1e-8)
+    for i, s in enumerate(sl):
+        r = norm_rel(p1[s], p_ref[s])
+        log(f"  layer {i} param norm_rel {r:.3e}")
+        assert r <= TOL, (i, r)
+
+
+# ------------------------------------------------------------------ error paths
+def test_errors_are_reported(gn, dev):
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib
+    cfg = configs.mlp()
+    model = configs.build(cfg)
+    x, y = configs.inputs(cfg)
+    with pytest.raises(gn.GNError):
+        model._ck(lib().gn_model_train_step(model.h, None, None, 4, None))
+    lib().gn_debug_fail_next(dev.h, -6)
+    with pytest.raises(gn.GNError) as e:
+        model.TrainBatch(x, y)
+    assert e.value.code == -6
+    # the model still works after the injected failure
+    assert np.isfinite(model.TrainBatch(x, y))
