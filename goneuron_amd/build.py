@@ -5,6 +5,8 @@ Each ``csrc/*.hip`` file is compiled to an object in parallel, then linked into
   --offload-arch=gfx950                 MI355X only
   -ffp-contract=off                     keep the reference's float32 rounding
                                         order in elementwise code (no FMA)
+  -fhip-fp32-correctly-rounded-divide-sqrt  IEEE fp32 '/' and sqrtf, matching
+                                        Go's float32 '/' and float32(math.Sqrt(x))
   -target-feature -packed-fp32-ops      no packed fp32 VALU ops
 """
 from __future__ import annotations
@@ -22,6 +24,7 @@ LIB = os.path.join(HERE, "libgoneuron_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "-O3", "--offload-arch=gfx950", "-fPIC", "-std=c++17", "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]

@@ -4,8 +4,8 @@
 // the batch-mean loss.
 //
 // Rounding follows the reference's float32 expression order (the library is
-// built with -ffp-contract=off; divisions and square roots are the correctly
-// rounded __fdiv_rn / __fsqrt_rn), and transcendentals go through double
+// built with -ffp-contract=off and correctly rounded fp32 division and square
+// root), and transcendentals go through double
 // precision exactly where the Go code calls math.Exp / math.Log / math.Tanh
 // on float64 arguments.
 #include "gn_common.h"
@@ -21,11 +21,14 @@ constexpr int TPB = 256;
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float efflr, float b1,
                                       float b2, float omb1, float omb2, float eps) {
-  const float mi = __fadd_rn(__fmul_rn(b1, m), __fmul_rn(omb1, g));
-  const float vi = __fadd_rn(__fmul_rn(b2, v), __fmul_rn(__fmul_rn(omb2, g), g));
+  // -ffp-contract=off keeps every product and sum separately rounded;
+  // '/' and sqrtf are IEEE correctly rounded under
+  // -fhip-fp32-correctly-rounded-divide-sqrt (== float32(math.Sqrt(float64(v))))
+  const float mi = b1 * m + omb1 * g;
+  const float vi = b2 * v + omb2 * g * g;
   m = mi;
   v = vi;
-  p = __fsub_rn(p, __fdiv_rn(__fmul_rn(efflr, mi), __fadd_rn(__fsqrt_rn(vi), eps)));
+  p = p - efflr * mi / (__builtin_sqrtf(vi) + eps);
 }
 
 __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
@@ -220,7 +223,7 @@ __device__ void row_activate(float *row, int C, int row_act, int fwd, float *sh)
     for (int i = t; i < C; i += TPB) s += (float)exp((double)(row[i] - mx));
     s = block_sum(s, sh);
     if (row_act == ROW_SOFTMAX) {
-      for (int i = t; i < C; i += TPB) row[i] = __fdiv_rn((float)exp((double)(row[i] - mx)), s);
+      for (int i = t; i < C; i += TPB) row[i] = (float)exp((double)(row[i] - mx)) / s;
     } else {
       const float ls = (float)log((double)s);
       for (int i = t; i < C; i += TPB) row[i] = row[i] - mx - ls;
@@ -252,14 +255,14 @@ __global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
   // loss and its gradient g (kept in d)
   float l = 0.f;
   if (loss_kind == GN_LOSS_MSE) {
-    const float factor = __fdiv_rn(2.0f, (float)C);
+    const float factor = 2.0f / (float)C;
     for (int i = t; i < C; i += TPB) {
       const float df = o[i] - yr[i];
       l += df * df;
       d[i] = factor * df;
     }
     l = block_sum(l, sh);
-    l = __fdiv_rn(l, (float)C);
+    l = l / (float)C;
   } else {
     for (int i = t; i < C; i += TPB) {
       float pv = o[i];
@@ -327,7 +330,7 @@ __global__ void loss_mean_kernel(const float *__restrict__ rows, int B, int W,
       total += local;
     }
   }
-  *loss = __fdiv_rn(total, (float)B);
+  *loss = total / (float)B;
 }
 
 hipError_t launch_loss_mean(const float *rows, int B, int W, float *loss, hipStream_t s) {

@@ -175,14 +175,18 @@ def test_odd_batch_and_sizes(gn, oracle):
 
 # ------------------------------------------------------------------ full-size C3 vs torch fp32
 def test_wide_full_size_vs_torch(gn):
-    """C3 at BASELINE size: one step against torch fp32 autograd (Q4 Jacobian
-    fed through p.backward), on the same initial weights."""
+    """C3 at BASELINE size: one step against torch autograd in float64 (Q4
+    Jacobian fed through p.backward) on the same initial weights.  ReLU is a
+    branch: pre-activations within fp32 rounding of 0 may take either side in
+    any two fp32 summation orders, so the float64 reference takes each unit's
+    branch from the GPU forward (out > 0) and the number of units whose float64
+    pre-activation lies on the other side is reported."""
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("torch has no GPU")
     from goneuron_amd import configs
     cfg = configs.wide()
-    log("wide full-size vs torch")
+    log("wide full-size vs torch float64")
     x, y = configs.inputs(cfg)
     B = cfg["B"]
     model = configs.build(cfg)
@@ -190,12 +194,13 @@ def test_wide_full_size_vs_torch(gn):
     lg = model.TrainBatch(x, y)
     g_gpu = model.Gradients()
     p1 = model.Params()
-    torch.backends.cuda.matmul.allow_tf32 = False
+    outs = [model.LayerOutput(i, B * d["out"]).reshape(B, d["out"]) for i, d in enumerate(cfg["layers"])]
     dev = torch.device("cuda:0")
-    P = torch.tensor(p0, device=dev, requires_grad=True)
-    h = torch.tensor(x, device=dev)
+    P = torch.tensor(p0.astype(np.float64), device=dev, requires_grad=True)
+    h = torch.tensor(x.astype(np.float64), device=dev)
     off = 0
     sl = []
+    flips = []
     for i, d in enumerate(cfg["layers"]):
         n_w = d["in"] * d["out"]
         W = P[off:off + n_w].view(d["out"], d["in"])
@@ -203,25 +208,32 @@ def test_wide_full_size_vs_torch(gn):
         sl.append(slice(off, off + n_w + d["out"]))
         off += n_w + d["out"]
         z = h @ W.T + b
-        h = torch.relu(z) if d["act"] == "relu" else torch.log_softmax(z, dim=1)
-    yt = torch.tensor(y, device=dev)
+        if d["act"] == "relu":
+            mask = torch.tensor(outs[i] > 0, device=dev)
+            flips.append(int(((z > 0) != mask).sum()))
+            h = z * mask
+        else:
+            h = torch.log_softmax(z, dim=1)
+            lp = h.detach().cpu().numpy()
+    log(f"  relu branch disagreements fp32 vs fp64 per layer: {flips}")
+    log(f"  logp max_rel {max_rel(outs[-1], lp):.3e}")
+    assert max_rel(outs[-1], lp) <= TOL
+    yt = torch.tensor(y.astype(np.float64), device=dev)
     h.backward(((h - yt) / B).detach())
     g_ref = P.grad.detach().cpu().numpy()
-    for i, s in enumerate(sl):
-        r = max_rel(g_gpu[s], g_ref[s])
-        log(f"  layer {i} grad max_rel {r:.3e}")
-        assert r <= TOL, (i, r)
+    errs = [max_rel(g_gpu[s], g_ref[s]) for s in sl]
+    log("  grad max_rel per layer: " + " ".join(f"{e:.3e}" for e in errs))
     # loss: CE of log-probabilities is the constant -log(1e-10) per sample (Q5)
     assert abs(lg - 23.02585) < 1e-3
-    # Adam at t = 2 from zero moments, in float64 from the torch gradient
+    # Adam at t = 2 from zero moments, in float64 from the float64 gradient
     g = g_ref.astype(np.float64)
     b1, b2 = float(np.float32(0.9)), float(np.float32(0.999))
     eff = 1e-3 * np.sqrt(1 - b2 ** 2) / (1 - b1 ** 2)
     p_ref = p0 - eff * (1 - b1) * g / (np.sqrt((1 - b2) * g * g) + 1e-8)
-    for i, s in enumerate(sl):
-        r = norm_rel(p1[s], p_ref[s])
-        log(f"  layer {i} param norm_rel {r:.3e}")
-        assert r <= TOL, (i, r)
+    perrs = [norm_rel(p1[s], p_ref[s]) for s in sl]
+    log("  param norm_rel per layer: " + " ".join(f"{e:.3e}" for e in perrs))
+    assert max(errs) <= TOL, errs
+    assert max(perrs) <= TOL, perrs
 
 
 # ------------------------------------------------------------------ error paths
