@@ -45,6 +45,8 @@ struct GemmArgs {
   const float *aux;   // EPI_DACT: saved output used for act'
   int ldaux;
   int act;            // FwdKind or DerivKind
+  float *ws;          // split-K workspace (may be null: no split)
+  size_t ws_cap;      // floats
 };
 
 enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };

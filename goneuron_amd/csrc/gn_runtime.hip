@@ -162,7 +162,7 @@ extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
   if (hipSetDevice(device_ordinal) != hipSuccess) return GN_ERR_HIP;
   if (hipGetDeviceProperties(&c->props, device_ordinal) != hipSuccess) return GN_ERR_HIP;
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return GN_ERR_HIP;
-  c->scratch_floats = (size_t)64 * 65536;
+  c->scratch_floats = (size_t)16 << 20;  // 64 MiB: colsum partials, split-K partials
   if (hipMalloc(&c->scratch, c->scratch_floats * sizeof(float)) != hipSuccess) {
     (void)hipStreamDestroy(c->stream);
     return GN_ERR_OOM;
@@ -314,6 +314,7 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
   a.B = W; a.ldb = in;
   a.C = out; a.ldc = out_n;
   a.bias = b; a.act = fwd; a.alpha = 1.f;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
   KTimer kt(c, GN_KCLASS_GEMM);
   return launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream);
 }
@@ -334,6 +335,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
   a.B = x; a.ldb = in;
   a.C = gW; a.ldc = in;
   a.alpha = scale;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
   {
     KTimer kt(c, GN_KCLASS_GEMM);
     e = launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
@@ -346,6 +348,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
     d.B = W; d.ldb = in;
     d.C = gin; d.ldc = in;
     d.alpha = 1.f;
+    d.ws = c->scratch; d.ws_cap = c->scratch_floats;
     KTimer kt(c, GN_KCLASS_GEMM);
     if (gin_aux) {
       d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv;
@@ -367,6 +370,7 @@ extern "C" int gn_gemm(gn_ctx *c, int32_t transA, int32_t transB, int32_t M, int
   GemmArgs a{};
   a.M = M; a.N = N; a.K = K;
   a.A = A; a.lda = lda; a.B = B; a.ldb = ldb; a.C = Cm; a.ldc = ldc; a.alpha = alpha;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
   HIP_OK(c, launch_gemm(transA ? 'T' : 'N', transB ? 'T' : 'N', EPI_SCALE, a, c->stream));
   return GN_OK;
 }

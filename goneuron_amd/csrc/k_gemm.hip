@@ -1,16 +1,24 @@
 // fp32 MFMA GEMM family for gfx950 (CDNA4).
 //
 // C[M,N] = epilogue( sum_k opA[m,k] * opB[k,n] ) with both operands staged
-// through LDS in a K-contiguous, padded layout so every lane fetches its MFMA
-// operands with ds_read_b128.
+// through LDS.  A K-contiguous operand is stored [row][k] (padded) and each lane
+// fetches its 16 MFMA operands per K tile with 4 ds_read_b128; an M/N-contiguous
+// operand keeps its global layout in LDS (no transposing scalar stores) and is
+// read with ds_read_b32 by consecutive lanes.
 //
-// Tiling: 128x128 block tile, BK = 32, 256 threads = 4 wave64s in a 2x2 grid,
-// each wave owns a 64x64 sub-tile = 2x2 v_mfma_f32_32x32x2_f32 accumulators
-// (64 fp32 accumulators per lane).  Within a K tile, lane half h (lanes 32-63)
-// feeds k = 16h + s at MFMA step s, so each lane's 16 operand values per tile
-// row are contiguous in LDS.  Two LDS stages: global loads for tile k+1 are
-// issued into registers before the MFMAs of tile k and written to the other
-// stage afterwards, one barrier per K tile.
+// Tiling: 128x128 block tile, 64-wide K stages, 512 threads = 8 wave64s in
+// two K-groups.  Group g owns k in [32g, 32g+32) of every stage; inside a
+// group the 4 waves tile the block 2x2, each wave a 64x64 sub-tile = 2x2
+// v_mfma_f32_32x32x2_f32 accumulators (64 fp32 accumulators per lane).  The
+// two groups' partial sums are added through LDS before the epilogue.  With a
+// 1024-row batch a 4096-wide layer has exactly 256 tiles (one per CU): the
+// K-groups give every SIMD two waves to hide LDS and barrier latency.  Lane
+// half h feeds k = 16h + s at MFMA step s, so each lane's 16 operand values per
+// slab are contiguous for a K-contiguous operand.  Two LDS stages: global loads
+// for stage k+1 are issued into registers before the MFMAs of stage k and
+// written to the other stage afterwards, one barrier per stage.  When the tile grid cannot fill
+// the 256 CUs the K range is split across blocks; the partial sums are added
+// in split order by a second kernel that also applies the epilogue.
 //
 // Used by Dense forward (NT: X[B,in] * W[out,in]^T, fused bias + activation),
 // Dense dX (NN: dZ[B,out] * W[out,in], fused activation derivative of the layer
@@ -18,15 +26,17 @@
 // the per-sample mat-vecs in layer.go:406, :591-663.
 #include "gn_common.h"
 
+#include <algorithm>
+
 namespace gn {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 32;
-constexpr int PITCH = BK + 4;  // floats; 16 B pad keeps b128 row reads conflict-free
-constexpr int NT = 256;
+constexpr int BK = 64;          // K staged per iteration (two 32-wide halves)
+constexpr int PITCH = BK + 4;   // floats; 16 B pad keeps b128 row reads conflict-free
+constexpr int NT = 512;         // 8 wave64s: 2 K-groups x (2 x 2) waves
 
 __device__ __forceinline__ float apply_fwd(float v, int kind) {
   switch (kind) {
@@ -51,40 +61,41 @@ __device__ __forceinline__ float apply_deriv(float out, int kind) {
 // Global -> register staging of one operand tile.  KC: the operand's K index
 // is contiguous in memory (rows x K, row pitch ld); otherwise it is stored
 // K x rows.  VEC: float4 accesses are legal (16 B aligned, sizes % 4 == 0).
+// Only k in [k0, kend) is read; everything else is zero-filled.
 template <bool KC, bool VEC>
-__device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld, int rows, int K,
+__device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld, int rows, int kend,
                                           int r0, int k0, float4 (&reg)[4]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int f = t + NT * j;
     if (KC) {
-      const int r = f >> 3, k4 = (f & 7) << 2;
+      const int r = f >> 4, k4 = (f & 15) << 2;
       const int gr = r0 + r, gk = k0 + k4;
       if (VEC) {
-        if (gr < rows && gk < K)
+        if (gr < rows && gk < kend)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gr * ld + gk);
         else
           reg[j] = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         const float *p = base + (size_t)gr * ld + gk;
         const bool ok = gr < rows;
-        reg[j].x = (ok && gk + 0 < K) ? p[0] : 0.f;
-        reg[j].y = (ok && gk + 1 < K) ? p[1] : 0.f;
-        reg[j].z = (ok && gk + 2 < K) ? p[2] : 0.f;
-        reg[j].w = (ok && gk + 3 < K) ? p[3] : 0.f;
+        reg[j].x = (ok && gk + 0 < kend) ? p[0] : 0.f;
+        reg[j].y = (ok && gk + 1 < kend) ? p[1] : 0.f;
+        reg[j].z = (ok && gk + 2 < kend) ? p[2] : 0.f;
+        reg[j].w = (ok && gk + 3 < kend) ? p[3] : 0.f;
       }
     } else {
       const int k = f >> 5, r4 = (f & 31) << 2;
       const int gk = k0 + k, gr = r0 + r4;
       if (VEC) {
-        if (gk < K && gr < rows)
+        if (gk < kend && gr < rows)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gk * ld + gr);
         else
           reg[j] = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
         const float *p = base + (size_t)gk * ld + gr;
-        const bool ok = gk < K;
+        const bool ok = gk < kend;
         reg[j].x = (ok && gr + 0 < rows) ? p[0] : 0.f;
         reg[j].y = (ok && gr + 1 < rows) ? p[1] : 0.f;
         reg[j].z = (ok && gr + 2 < rows) ? p[2] : 0.f;
@@ -94,22 +105,49 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
   }
 }
 
+// LDS layouts.  K-contiguous operands: [128 rows][68] (k fastest, 16 B pad),
+// read as 4 x ds_read_b128 per lane.  M/N-contiguous operands keep their
+// global layout, [64 k][132] (row fastest), written with ds_write_b128 and
+// read as 16 x ds_read_b32 per lane (consecutive lanes, consecutive rows).
+constexpr int RP = BM + 4;
+constexpr int STAGE = BM * PITCH;  // floats per operand stage (>= BK * RP)
+static_assert(BK * RP <= STAGE, "stage size");
+
 template <bool KC>
-__device__ __forceinline__ void store_tile(float (*S)[PITCH], const float4 (&reg)[4]) {
+__device__ __forceinline__ void store_tile(float *S, const float4 (&reg)[4]) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int f = t + NT * j;
     if (KC) {
-      const int r = f >> 3, k4 = (f & 7) << 2;
-      *reinterpret_cast<float4 *>(&S[r][k4]) = reg[j];
+      const int r = f >> 4, k4 = (f & 15) << 2;
+      *reinterpret_cast<float4 *>(S + r * PITCH + k4) = reg[j];
     } else {
       const int k = f >> 5, r4 = (f & 31) << 2;
-      S[r4 + 0][k] = reg[j].x;
-      S[r4 + 1][k] = reg[j].y;
-      S[r4 + 2][k] = reg[j].z;
-      S[r4 + 3][k] = reg[j].w;
+      *reinterpret_cast<float4 *>(S + k * RP + r4) = reg[j];
     }
+  }
+}
+
+// MFMA operand fragment of one 32-row slab for K-group g: lane half h
+// supplies k = 32g + 16h + s at step s (s = 0..15), row = rowbase + lane % 32.
+template <bool KC>
+__device__ __forceinline__ void read_frag(const float *S, int rowbase, int koff, int l32,
+                                          float (&a)[16]) {
+  if (KC) {
+    const float *src = S + (rowbase + l32) * PITCH + koff;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 x = *reinterpret_cast<const float4 *>(src + 4 * q);
+      a[4 * q + 0] = x.x;
+      a[4 * q + 1] = x.y;
+      a[4 * q + 2] = x.z;
+      a[4 * q + 3] = x.w;
+    }
+  } else {
+    const float *src = S + koff * RP + rowbase + l32;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) a[s] = src[s * RP];
   }
 }
 
@@ -135,23 +173,39 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int &tm,
   tn = (pid % width) / gsz;
 }
 
+__device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, int row, int col) {
+  if (epi == EPI_SCALE) return v * p.alpha;
+  if (epi == EPI_BIAS_ACT) return apply_fwd(v + (p.bias ? p.bias[col] : 0.f), p.act);
+  return v * apply_deriv(p.aux[(size_t)row * p.ldaux + col], p.act);
+}
+
+// EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
+constexpr int EPI_PARTIAL = 3;
+
 template <bool AK, bool BKC, bool VEC, int EPI>
-__global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(16))) float As[2][BM][PITCH];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN][PITCH];
+__global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n,
+                                                    int kchunk) {
+  __shared__ __attribute__((aligned(16))) float As[2][STAGE];
+  __shared__ __attribute__((aligned(16))) float Bs[2][STAGE];
 
   int tm, tn;
   tile_of_block(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int wm = w >> 1, wn = w & 1;
+  // waves 0-3 take k in [0,32) of every stage, waves 4-7 take [32,64); within
+  // a group the 4 waves tile the 128x128 block as 2x2 sub-tiles of 64x64.
+  const int g = w >> 2, w4 = w & 3;
+  const int wm = w4 >> 1, wn = w4 & 1;
   const int half = lane >> 5, l32 = lane & 31;
-  const int M = p.M, N = p.N, K = p.K;
-  const int nk = (K + BK - 1) / BK;
+  const int koff = g * 32 + half * 16;
+  const int M = p.M, N = p.N;
+  const int kbeg = blockIdx.y * kchunk;
+  const int kend = min(p.K, kbeg + kchunk);
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
   float4 ra[4], rb[4];
-  load_tile<AK, VEC>(p.A, p.lda, M, K, m0, 0, ra);
-  load_tile<BKC, VEC>(p.B, p.ldb, N, K, n0, 0, rb);
+  load_tile<AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
+  load_tile<BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
   store_tile<AK>(As[0], ra);
   store_tile<BKC>(Bs[0], rb);
   __syncthreads();
@@ -168,34 +222,14 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_tile<AK, VEC>(p.A, p.lda, M, K, m0, (kt + 1) * BK, ra);
-      load_tile<BKC, VEC>(p.B, p.ldb, N, K, n0, (kt + 1) * BK, rb);
+      load_tile<AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
+      load_tile<BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
     }
     float a[2][16], b[2][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float *src = &As[cur][wm * 64 + i * 32 + l32][half * 16];
+    for (int i = 0; i < 2; ++i) read_frag<AK>(As[cur], wm * 64 + i * 32, koff, l32, a[i]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 x = *reinterpret_cast<const float4 *>(src + 4 * q);
-        a[i][4 * q + 0] = x.x;
-        a[i][4 * q + 1] = x.y;
-        a[i][4 * q + 2] = x.z;
-        a[i][4 * q + 3] = x.w;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const float *src = &Bs[cur][wn * 64 + j * 32 + l32][half * 16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 x = *reinterpret_cast<const float4 *>(src + 4 * q);
-        b[j][4 * q + 0] = x.x;
-        b[j][4 * q + 1] = x.y;
-        b[j][4 * q + 2] = x.z;
-        b[j][4 * q + 3] = x.w;
-      }
-    }
+    for (int j = 0; j < 2; ++j) read_frag<BKC>(Bs[cur], wn * 64 + j * 32, koff, l32, b[j]);
 #pragma unroll
     for (int s = 0; s < 16; ++s)
 #pragma unroll
@@ -210,53 +244,85 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
     __syncthreads();
   }
 
-  // Epilogue.  v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r
-  // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
+  // K-group 1 hands its accumulators to group 0 through LDS (the operand
+  // stages are free after the last barrier): 4 waves x 64 lanes x 64 floats.
+  float *red = &As[0][0];
+  static_assert(4 * 64 * 64 <= 2 * STAGE, "reduction buffer");
+  if (g == 1) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int ij = q >> 2, r4 = (q & 3) << 2;
+      const floatx16 &v = acc[ij >> 1][ij & 1];
+      *reinterpret_cast<float4 *>(red + ((w4 * 16 + q) * 64 + lane) * 4) =
+          make_float4(v[r4], v[r4 + 1], v[r4 + 2], v[r4 + 3]);
+    }
+  }
+  __syncthreads();
+  if (g == 1) return;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int ij = q >> 2, r4 = (q & 3) << 2;
+    const float4 o = *reinterpret_cast<const float4 *>(red + ((w4 * 16 + q) * 64 + lane) * 4);
+    floatx16 &v = acc[ij >> 1][ij & 1];
+    v[r4] += o.x;
+    v[r4 + 1] += o.y;
+    v[r4 + 2] += o.z;
+    v[r4 + 3] += o.w;
+  }
+
+  // v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
+  float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = n0 + wn * 64 + j * 32 + l32;
       if (col >= N) continue;
-      float bias = 0.f;
-      if (EPI == EPI_BIAS_ACT && p.bias) bias = p.bias[col];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
         if (row >= M) continue;
-        float v = acc[i][j][r];
-        if (EPI == EPI_SCALE) {
-          v *= p.alpha;
-        } else if (EPI == EPI_BIAS_ACT) {
-          v = apply_fwd(v + bias, p.act);
-        } else {
-          v *= apply_deriv(p.aux[(size_t)row * p.ldaux + col], p.act);
-        }
-        p.C[(size_t)row * p.ldc + col] = v;
+        if (EPI == EPI_PARTIAL)
+          ws[(size_t)row * N + col] = acc[i][j][r];
+        else
+          p.C[(size_t)row * p.ldc + col] = epilogue(acc[i][j][r], EPI, p, row, col);
       }
     }
 }
 
+// Split-K reduction: partials summed in split order, then the epilogue.
+__global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits, int epi) {
+  const size_t MN = (size_t)p.M * p.N;
+  for (size_t idx = (size_t)blockIdx.x * NT + threadIdx.x; idx < MN; idx += (size_t)gridDim.x * NT) {
+    float v = p.ws[idx];
+    for (int s = 1; s < splits; ++s) v += p.ws[s * MN + idx];
+    const int row = (int)(idx / p.N), col = (int)(idx % p.N);
+    p.C[(size_t)row * p.ldc + col] = epilogue(v, epi, p, row, col);
+  }
+}
+
 template <bool AK, bool BKC, int EPI>
-static hipError_t launch_t(bool vec, const GemmArgs &a, hipStream_t s) {
-  const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-  dim3 grid(tm * tn), block(NT);
+static hipError_t launch_t(bool vec, const GemmArgs &a, int tm, int tn, int splits, int kchunk,
+                           hipStream_t s) {
+  dim3 grid(tm * tn, splits), block(NT);
   if (vec)
-    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, true, EPI>), grid, block, 0, s, a, tm, tn);
+    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, true, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, false, EPI>), grid, block, 0, s, a, tm, tn);
+    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, false, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
   return hipGetLastError();
 }
 
 template <int EPI>
-static hipError_t launch_e(char ta, char tb, bool vec, const GemmArgs &a, hipStream_t s) {
+static hipError_t launch_e(char ta, char tb, bool vec, const GemmArgs &a, int tm, int tn,
+                           int splits, int kchunk, hipStream_t s) {
   // op(A) 'N' -> A is M x K, K contiguous.  op(B) 'T' -> B is N x K, K contiguous.
   const bool ak = (ta == 'N');
   const bool bk = (tb == 'T');
-  if (ak && bk) return launch_t<true, true, EPI>(vec, a, s);
-  if (ak && !bk) return launch_t<true, false, EPI>(vec, a, s);
-  if (!ak && bk) return launch_t<false, true, EPI>(vec, a, s);
-  return launch_t<false, false, EPI>(vec, a, s);
+  if (ak && bk) return launch_t<true, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (ak && !bk) return launch_t<true, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (!ak && bk) return launch_t<false, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  return launch_t<false, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -268,9 +334,32 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0);
   vec = vec && (ak ? (a.K % 4 == 0) : (a.M % 4 == 0));
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
-  if (epi == EPI_BIAS_ACT) return launch_e<EPI_BIAS_ACT>(ta, tb, vec, a, s);
-  if (epi == EPI_DACT) return launch_e<EPI_DACT>(ta, tb, vec, a, s);
-  return launch_e<EPI_SCALE>(ta, tb, vec, a, s);
+  const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+  // Split K when the tile grid cannot fill the 256 CUs, keeping >= 8 K tiles
+  // per split; partials go to the workspace and are summed in split order.
+  int splits = 1;
+  const int tiles = tm * tn;
+  if (tiles < 160 && a.K >= 16 * BK && a.ws) {
+    splits = std::min((256 + tiles - 1) / tiles, a.K / (8 * BK));
+    while (splits > 1 && (size_t)splits * a.M * a.N > a.ws_cap) --splits;
+  }
+  int kchunk = a.K;
+  if (splits > 1) {
+    kchunk = ((a.K + splits - 1) / splits + BK - 1) / BK * BK;
+    splits = (a.K + kchunk - 1) / kchunk;
+  }
+  if (splits <= 1) {
+    kchunk = a.K > 0 ? a.K : 1;
+    if (epi == EPI_BIAS_ACT) return launch_e<EPI_BIAS_ACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+    if (epi == EPI_DACT) return launch_e<EPI_DACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+    return launch_e<EPI_SCALE>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+  }
+  hipError_t e = launch_e<EPI_PARTIAL>(ta, tb, vec, a, tm, tn, splits, kchunk, s);
+  if (e != hipSuccess) return e;
+  const size_t MN = (size_t)a.M * a.N;
+  const unsigned blocks = (unsigned)std::min<size_t>((MN + NT - 1) / NT, 4096);
+  hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+  return hipGetLastError();
 }
 
 }  // namespace gn

@@ -316,25 +316,43 @@ hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) 
 
 // Batch loss: totalLoss accumulates per sample in order (net.go:744), per
 // worker chunk then in worker order for W > 1 (net.go:679-716); / B.
-__global__ void loss_mean_kernel(const float *__restrict__ rows, int B, int W,
-                                 float *__restrict__ loss) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  float total = 0.f;
-  if (W <= 1) {
-    for (int i = 0; i < B; ++i) total += rows[i];
-  } else {
-    const int chunk = (B + W - 1) / W;
-    for (int w = 0; w < W; ++w) {
-      float local = 0.f;
-      for (int i = w * chunk; i < min(B, (w + 1) * chunk); ++i) local += rows[i];
-      total += local;
+__global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict__ rows, int B,
+                                                        int W, float *__restrict__ loss) {
+  __shared__ __attribute__((aligned(16))) float buf[1024 + 32];
+  const int chunk = W > 1 ? (B + W - 1) / W : B;
+  float total = 0.f, local = 0.f;
+  for (int base = 0; base < B; base += 1024) {
+    const int n = min(1024, B - base);
+    for (int i = threadIdx.x; i < n; i += TPB) buf[i] = rows[base + i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // registers in groups of 32 (8 x ds_read_b128 in flight), then the
+      // sequential float32 adds of the reference
+      for (int i0 = 0; i0 < n; i0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float4 x = *reinterpret_cast<const float4 *>(&buf[i0 + 4 * q]);
+          v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+        }
+        const int m = min(32, n - i0);
+        for (int q = 0; q < m; ++q) {
+          local += v[q];
+          const int gi = base + i0 + q + 1;
+          if (gi % chunk == 0 || gi == B) {  // end of a worker chunk
+            total += local;
+            local = 0.f;
+          }
+        }
+      }
     }
+    __syncthreads();
   }
-  *loss = total / (float)B;
+  if (threadIdx.x == 0) *loss = total / (float)B;
 }
 
 hipError_t launch_loss_mean(const float *rows, int B, int W, float *loss, hipStream_t s) {
-  hipLaunchKernelGGL(loss_mean_kernel, dim3(1), dim3(64), 0, s, rows, B, W, loss);
+  hipLaunchKernelGGL(loss_mean_kernel, dim3(1), dim3(TPB), 0, s, rows, B, W, loss);
   return hipGetLastError();
 }
 
