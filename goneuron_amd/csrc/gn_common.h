@@ -86,4 +86,24 @@ hipError_t launch_dropout(const float *x, const float *mask, float scale, float 
 // Elementwise forward activation in place.
 hipError_t launch_act_inplace(float *x, int64_t n, int fwd, hipStream_t s);
 
+// ---- Conv2D / MaxPool2D (per-sample NCHW, samples contiguous) ----
+struct ConvShape {
+  int inC, outC, k, stride, pad, H, W, oH, oW;
+};
+struct PoolShape {
+  int C, k, stride, pad, H, W, oH, oW;
+};
+hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, float *out,
+                           const ConvShape &s, int B, int fwd, hipStream_t st);
+// grad = [dW | db] (scaled), dz = gout * act'(out) formed on the fly
+hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
+                             const ConvShape &s, int B, int deriv, float scale, float *ws,
+                             size_t ws_cap, hipStream_t st);
+hipError_t launch_conv_dgrad(const float *gout, const float *out, const float *w, float *gin,
+                             const ConvShape &s, int B, int deriv, hipStream_t st);
+hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const PoolShape &s,
+                              int B, hipStream_t st);
+hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
+                              const PoolShape &s, int B, hipStream_t st);
+
 }  // namespace gn

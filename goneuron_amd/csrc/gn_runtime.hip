@@ -457,6 +457,10 @@ struct LayerRT {
   ActPlan ap{};
   float *mask = nullptr;        // Dropout per-feature mask (Q9)
   float scale = 1.f;
+  ConvShape cs{};               // Conv2D
+  PoolShape ps{};               // MaxPool2D
+  int32_t *argmax = nullptr;    // MaxPool2D switches [maxB, out_len]
+  int cfwd = 0, cderiv = 0;     // Conv2D scalar Activate / Derivative kinds
 };
 
 struct gn_model {
@@ -501,6 +505,35 @@ static void init_dense(float *p, int in, int out) {  // Dense.Build layer.go:300
   const int64_t nw = (int64_t)in * out;
   for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
   for (int i = 0; i < out; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
+}
+
+static void init_conv(float *p, int inC, int outC, int k) {  // Conv2D.Build conv2d.go:114-135
+  const float scale = (float)sqrt(2.0 / (double)(inC * k * k));
+  uint64_t s = 42;
+  const int64_t nw = (int64_t)outC * inC * k * k;
+  for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
+  for (int i = 0; i < outC; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
+}
+
+// Conv2D calls the activation's scalar Activate / Derivative methods directly
+// (conv2d.go:950, :1140): Softmax/LogSoftmax give NaN there.
+static int plan_scalar_act(int act, int &fwd, int &deriv) {
+  switch (act) {
+    case GN_ACT_RELU: fwd = F_RELU; deriv = D_RELU; return GN_OK;
+    case GN_ACT_SIGMOID: fwd = F_SIGMOID; deriv = D_SIGMOID; return GN_OK;
+    case GN_ACT_TANH: fwd = F_TANH; deriv = D_TANH; return GN_OK;
+    case GN_ACT_LINEAR: fwd = F_IDENTITY; deriv = D_ONE; return GN_OK;
+    case GN_ACT_SOFTMAX:
+    case GN_ACT_LOGSOFTMAX: fwd = F_NAN; deriv = D_NAN; return GN_OK;
+    default: return GN_ERR_INVALID;
+  }
+}
+
+// Square-first dimension inference of Conv2D / MaxPool2D forward
+// (conv2d.go:733-746, maxpool2d.go:117-126).
+static void infer_hw(int channel_size, int &H, int &W) {
+  H = (int)sqrt((double)channel_size);
+  W = (H * H == channel_size) ? H : (H > 0 ? channel_size / H : 0);
 }
 
 extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t nlayers,
@@ -552,6 +585,45 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       case GN_LAYER_FLATTEN:
         R.out_len = len;
         break;
+      case GN_LAYER_CONV2D: {
+        ConvShape &cs = R.cs;
+        cs.inC = R.d.in_channels;
+        cs.outC = R.d.out_channels;
+        cs.k = R.d.kernel;
+        cs.stride = R.d.stride;
+        cs.pad = R.d.padding;
+        if (cs.inC <= 0 || cs.outC <= 0 || cs.k <= 0 || cs.stride <= 0 || cs.pad < 0)
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad Conv2D geometry", i);
+        if (len % cs.inC)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: input %d not divisible by inChannels %d", i, len,
+                         cs.inC);
+        infer_hw(len / cs.inC, cs.H, cs.W);
+        cs.oH = (cs.H + 2 * cs.pad - cs.k) / cs.stride + 1;
+        cs.oW = (cs.W + 2 * cs.pad - cs.k) / cs.stride + 1;
+        if (cs.H * cs.W * cs.inC != len || cs.oH <= 0 || cs.oW <= 0)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: Conv2D input %d is not C x H x W", i, len);
+        if (plan_scalar_act(R.d.act, R.cfwd, R.cderiv))
+          return set_err(c, GN_ERR_INVALID, "layer %d: activation %d not supported", i, R.d.act);
+        R.pcount = (int64_t)cs.outC * cs.inC * cs.k * cs.k + cs.outC;
+        R.out_len = cs.outC * cs.oH * cs.oW;
+        break;
+      }
+      case GN_LAYER_MAXPOOL2D: {
+        PoolShape &ps = R.ps;
+        ps.C = R.d.in_channels <= 0 ? 1 : R.d.in_channels;  // maxpool2d.go:112-114 (Q8)
+        ps.k = R.d.kernel;
+        ps.stride = R.d.stride;
+        ps.pad = R.d.padding;
+        if (ps.k <= 0 || ps.stride <= 0 || ps.pad < 0)
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad MaxPool2D geometry", i);
+        infer_hw(len / ps.C, ps.H, ps.W);
+        ps.oH = (ps.H + 2 * ps.pad - ps.k) / ps.stride + 1;
+        ps.oW = (ps.W + 2 * ps.pad - ps.k) / ps.stride + 1;
+        if (ps.C * ps.H * ps.W != len || ps.oH <= 0 || ps.oW <= 0)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: MaxPool2D input %d is not C x H x W", i, len);
+        R.out_len = ps.C * ps.oH * ps.oW;
+        break;
+      }
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: kind %d not built in this library", i,
                        R.d.kind);
@@ -580,6 +652,12 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     LayerRT &R = M->L[i];
     maxw = std::max(maxw, std::max(R.in_len, R.out_len));
     if (R.d.kind == GN_LAYER_DENSE) init_dense(host.data() + R.poff, R.d.in_size, R.d.out_size);
+    if (R.d.kind == GN_LAYER_CONV2D) init_conv(host.data() + R.poff, R.cs.inC, R.cs.outC, R.cs.k);
+    if (R.d.kind == GN_LAYER_MAXPOOL2D) {
+      float *am = nullptr;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &am))) return rc;
+      R.argmax = reinterpret_cast<int32_t *>(am);
+    }
     if (R.d.kind == GN_LAYER_FLATTEN) {
       // reshape.go:64-96: identity both ways; share the neighbours' buffers
       R.out_alias = true;
@@ -714,6 +792,18 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_FLATTEN:
         R.out = const_cast<float *>(cur);
         break;
+      case GN_LAYER_CONV2D: {
+        const float *W = M->params + R.poff;
+        const float *b = W + (int64_t)R.cs.outC * R.cs.inC * R.cs.k * R.cs.k;
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_conv_fwd(cur, W, b, R.out, R.cs, B, R.cfwd, c->stream));
+        break;
+      }
+      case GN_LAYER_MAXPOOL2D: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
+        break;
+      }
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
     }
@@ -767,6 +857,26 @@ static int model_backward(gn_model *M, const float *x, int B, float scale) {
       }
       case GN_LAYER_FLATTEN:
         break;  // gout aliased by the layer above
+      case GN_LAYER_MAXPOOL2D:
+        if (below && below->gout) {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_maxpool_bwd(R.gout, R.argmax, below->gout, R.ps, B, c->stream));
+        }
+        is_dz = false;
+        break;
+      case GN_LAYER_CONV2D: {
+        // Conv2D.Backward (conv2d.go:1117-1168): the layer's own Derivative
+        // is applied to gout here, so it never receives a fused dz.
+        if (is_dz && i != n - 1) return set_err(c, GN_ERR_UNSUPPORTED, "fused dz into Conv2D");
+        const float *W = M->params + R.poff;
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_conv_wgrad(in, R.gout, R.out, M->grads + R.poff, R.cs, B, R.cderiv, scale,
+                                    c->scratch, c->scratch_floats, c->stream));
+        if (below && below->gout)
+          HIP_OK(c, launch_conv_dgrad(R.gout, R.out, W, below->gout, R.cs, B, R.cderiv, c->stream));
+        is_dz = false;
+        break;
+      }
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
     }
@@ -864,6 +974,7 @@ extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *o
   int rc = model_forward(M, M->xin, B, false);
   M->training = saved;
   if (rc) return rc;
+  M->last_B = B;
   LayerRT &O = M->L.back();
   HIP_OK(c, hipMemcpyAsync(out, O.out, (size_t)B * O.out_len * sizeof(float),
                            hipMemcpyDeviceToHost, c->stream));
@@ -885,5 +996,13 @@ extern "C" int gn_model_layer_output(gn_model *M, int32_t layer, float *dst, int
 
 extern "C" int gn_model_layer_argmax(gn_model *M, int32_t layer, int32_t *dst, int64_t n) {
   if (!M || layer < 0 || layer >= (int)M->L.size() || !dst) return GN_ERR_INVALID;
-  return set_err(M->ctx, GN_ERR_UNSUPPORTED, "layer %d has no argmax switches", layer);
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  LayerRT &R = M->L[layer];
+  if (!R.argmax) return set_err(c, GN_ERR_UNSUPPORTED, "layer %d has no argmax switches", layer);
+  const int64_t have = (int64_t)M->last_B * R.out_len;
+  if (n > have) return set_err(c, GN_ERR_INVALID, "asked %lld > %lld", (long long)n, (long long)have);
+  HIP_OK(c, hipMemcpyAsync(dst, R.argmax, n * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
 }

@@ -1,0 +1,305 @@
+// Conv2D and MaxPool2D kernels (NCHW per sample, samples contiguous).
+//
+// Conv2D forward reproduces the reference's float32 summation order exactly so
+// that pre-activations -- and the MaxPool argmax switches computed from them --
+// are bit-identical to the per-sample CPU path:
+//   k3 s1 p1 (conv2D3x3Optimized, conv2d.go:224-360): interior positions add,
+//     per input channel, three row sums ((w0*a + w1*b) + w2*c); columns 0 and
+//     W-1 of interior rows are never accumulated (pre = bias there, Q7); the
+//     first and last rows add tap by tap with bounds checks; bias last.
+//   other shapes (generic loop, conv2d.go:875-921): taps in (ic, kh, kw) order.
+// MaxPool2D forward (maxpool2d.go:186-219): strict '>' scan of the window in
+// (kh, kw) order from -Inf; the argmax is the flat index inside the sample.
+// MaxPool2D backward (maxpool2d.go:392-408) is done as a gather: every input
+// element sums the gradients of the windows whose argmax points at it, in
+// increasing output position -- the order the reference's scatter adds them.
+// Conv2D weight/bias gradients are an implicit GEMM over (sample, position)
+// reduced per block and then across blocks in a fixed order.
+#include "gn_common.h"
+
+namespace gn {
+
+constexpr int CT = 256;
+
+__device__ __forceinline__ float act_fwd(float v, int kind) {
+  switch (kind) {
+    case F_RELU: return v > 0.0f ? v : 0.0f;
+    case F_SIGMOID: return 1.0f / (1.0f + (float)exp((double)(-v)));
+    case F_TANH: return (float)tanh((double)v);
+    case F_NAN: return __builtin_nanf("");
+    default: return v;
+  }
+}
+
+__device__ __forceinline__ float act_deriv(float out, int kind) {
+  switch (kind) {
+    case D_RELU: return out > 0.0f ? 1.0f : 0.0f;
+    case D_SIGMOID: return out * (1.0f - out);
+    case D_TANH: return 1.0f - out * out;
+    case D_NAN: return __builtin_nanf("");
+    default: return 1.0f;
+  }
+}
+
+__global__ __launch_bounds__(CT) void conv2d_fwd_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ w,
+                                                        const float *__restrict__ bias,
+                                                        float *__restrict__ out, ConvShape s,
+                                                        int B, int fwd) {
+  const int osz = s.oH * s.oW;
+  const int64_t total = (int64_t)B * s.outC * osz;
+  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * CT) {
+    const int pos = (int)(idx % osz);
+    const int oc = (int)((idx / osz) % s.outC);
+    const int b = (int)(idx / ((int64_t)osz * s.outC));
+    const int oh = pos / s.oW, ow = pos % s.oW;
+    const int H = s.H, W = s.W;
+    const float *xs = x + (int64_t)b * s.inC * H * W;
+    const float *wo = w + (int64_t)oc * s.inC * s.k * s.k;
+    float p = 0.0f;
+    const bool fast = (s.k == 3 && s.stride == 1 && s.pad == 1);
+    if (fast && oh >= 1 && oh < s.oH - 1) {
+      if (ow >= 1 && ow < s.oW - 1) {
+        for (int ic = 0; ic < s.inC; ++ic) {
+          const float *wk = wo + ic * 9;
+          const float *top = xs + ic * H * W + (oh - 1) * W + ow;
+          const float *mid = top + W, *bot = mid + W;
+          p += wk[0] * top[-1] + wk[1] * top[0] + wk[2] * top[1];
+          p += wk[3] * mid[-1] + wk[4] * mid[0] + wk[5] * mid[1];
+          p += wk[6] * bot[-1] + wk[7] * bot[0] + wk[8] * bot[1];
+        }
+      }  // else: Q7, the interior-row edge columns keep 0
+    } else {
+      for (int ic = 0; ic < s.inC; ++ic)
+        for (int kh = 0; kh < s.k; ++kh) {
+          const int ih = oh * s.stride + kh - s.pad;
+          if (ih < 0 || ih >= H) continue;
+          for (int kw = 0; kw < s.k; ++kw) {
+            const int iw = ow * s.stride + kw - s.pad;
+            if (iw < 0 || iw >= W) continue;
+            p += wo[(ic * s.k + kh) * s.k + kw] * xs[(ic * H + ih) * W + iw];
+          }
+        }
+    }
+    out[idx] = act_fwd(p + bias[oc], fwd);
+  }
+}
+
+__global__ __launch_bounds__(CT) void maxpool_fwd_kernel(const float *__restrict__ x,
+                                                         float *__restrict__ out,
+                                                         int32_t *__restrict__ argmax,
+                                                         PoolShape s, int B) {
+  const int osz = s.oH * s.oW;
+  const int64_t total = (int64_t)B * s.C * osz;
+  const int in_len = s.C * s.H * s.W;
+  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * CT) {
+    const int pos = (int)(idx % osz);
+    const int c = (int)((idx / osz) % s.C);
+    const int b = (int)(idx / ((int64_t)osz * s.C));
+    const int oh = pos / s.oW, ow = pos % s.oW;
+    const float *xs = x + (int64_t)b * in_len;
+    float mv = -__builtin_inff();
+    int mi = -1;
+    for (int kh = 0; kh < s.k; ++kh)
+      for (int kw = 0; kw < s.k; ++kw) {
+        const int ih = oh * s.stride + kh - s.pad, iw = ow * s.stride + kw - s.pad;
+        if (ih >= 0 && ih < s.H && iw >= 0 && iw < s.W) {
+          const int i = (c * s.H + ih) * s.W + iw;
+          const float v = xs[i];
+          if (v > mv) {
+            mv = v;
+            mi = i;
+          }
+        }
+      }
+    out[idx] = mv;
+    argmax[idx] = mi;
+  }
+}
+
+// gin[b, i] = sum over output positions whose window holds input i and whose
+// argmax == i, visited in increasing output position.
+__global__ __launch_bounds__(CT) void maxpool_bwd_kernel(const float *__restrict__ gout,
+                                                         const int32_t *__restrict__ argmax,
+                                                         float *__restrict__ gin, PoolShape s,
+                                                         int B) {
+  const int in_len = s.C * s.H * s.W;
+  const int osz = s.oH * s.oW;
+  const int64_t total = (int64_t)B * in_len;
+  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * CT) {
+    const int i = (int)(idx % in_len);
+    const int b = (int)(idx / in_len);
+    const int c = i / (s.H * s.W), ih = (i / s.W) % s.H, iw = i % s.W;
+    // output rows/cols whose window covers (ih, iw)
+    int oh0 = ih + s.pad - s.k + 1, oh1 = ih + s.pad;
+    int ow0 = iw + s.pad - s.k + 1, ow1 = iw + s.pad;
+    oh0 = oh0 <= 0 ? 0 : (oh0 + s.stride - 1) / s.stride;
+    ow0 = ow0 <= 0 ? 0 : (ow0 + s.stride - 1) / s.stride;
+    oh1 = min(oh1 / s.stride, s.oH - 1);
+    ow1 = min(ow1 / s.stride, s.oW - 1);
+    const int64_t ob = ((int64_t)b * s.C + c) * osz;
+    float g = 0.0f;
+    for (int oh = oh0; oh <= oh1; ++oh)
+      for (int ow = ow0; ow <= ow1; ++ow) {
+        const int64_t o = ob + oh * s.oW + ow;
+        if (argmax[o] == i) g += gout[o];
+      }
+    gin[idx] = g;
+  }
+}
+
+// Conv2D weight + bias gradient partials.  Block (b, band): positions of one
+// band of output rows of one sample; dz = gout * act'(out) is formed on the
+// fly.  Output slot o < outC*inC*k*k is dW (oc, ic, kh, kw), the last outC
+// slots are db.  part[block][slot] = sum over the band's positions.
+__global__ __launch_bounds__(CT) void conv2d_wgrad_partial(const float *__restrict__ x,
+                                                           const float *__restrict__ gout,
+                                                           const float *__restrict__ out,
+                                                           float *__restrict__ part, ConvShape s,
+                                                           int band_rows, int deriv) {
+  extern __shared__ float sm[];
+  const int bands = (s.oH + band_rows - 1) / band_rows;
+  const int b = blockIdx.x / bands, band = blockIdx.x % bands;
+  const int oh0 = band * band_rows, oh1 = min(s.oH, oh0 + band_rows);
+  const int rows = oh1 - oh0;
+  const int P = rows * s.oW;
+  const int osz = s.oH * s.oW;
+  // dz tile [outC][P]
+  float *dz = sm;
+  for (int e = threadIdx.x; e < s.outC * P; e += CT) {
+    const int oc = e / P, q = e % P;
+    const int64_t gi = ((int64_t)b * s.outC + oc) * osz + oh0 * s.oW + q;
+    dz[e] = gout[gi] * act_deriv(out[gi], deriv);
+  }
+  __syncthreads();
+  const int nw = s.outC * s.inC * s.k * s.k;
+  const int nslots = nw + s.outC;
+  const float *xs = x + (int64_t)b * s.inC * s.H * s.W;
+  for (int o = threadIdx.x; o < nslots; o += CT) {
+    float acc = 0.0f;
+    if (o < nw) {
+      const int kw = o % s.k, kh = (o / s.k) % s.k, ic = (o / (s.k * s.k)) % s.inC,
+                oc = o / (s.k * s.k * s.inC);
+      const float *dzo = dz + oc * P;
+      for (int r = 0; r < rows; ++r) {
+        const int ih = (oh0 + r) * s.stride + kh - s.pad;
+        if (ih < 0 || ih >= s.H) continue;
+        const float *xr = xs + (ic * s.H + ih) * s.W;
+        for (int ow = 0; ow < s.oW; ++ow) {
+          const int iw = ow * s.stride + kw - s.pad;
+          if (iw < 0 || iw >= s.W) continue;
+          acc += dzo[r * s.oW + ow] * xr[iw];
+        }
+      }
+    } else {
+      const float *dzo = dz + (o - nw) * P;
+      for (int q = 0; q < P; ++q) acc += dzo[q];
+    }
+    part[(int64_t)blockIdx.x * nslots + o] = acc;
+  }
+}
+
+__global__ __launch_bounds__(CT) void conv2d_wgrad_final(const float *__restrict__ part, int nblocks,
+                                                         int nslots, float scale,
+                                                         float *__restrict__ grad) {
+  const int o = blockIdx.x * CT + threadIdx.x;
+  if (o >= nslots) return;
+  float s = 0.0f;
+  for (int i = 0; i < nblocks; ++i) s += part[(int64_t)i * nslots + o];
+  grad[o] = s * scale;  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)
+}
+
+// dX gather: gin[b, ic, ih, iw] = sum over (oc, kh, kw) of dz * w, dz formed
+// from gout and the saved output.
+__global__ __launch_bounds__(CT) void conv2d_dgrad_kernel(const float *__restrict__ gout,
+                                                          const float *__restrict__ out,
+                                                          const float *__restrict__ w,
+                                                          float *__restrict__ gin, ConvShape s,
+                                                          int B, int deriv) {
+  const int in_len = s.inC * s.H * s.W;
+  const int osz = s.oH * s.oW;
+  const int64_t total = (int64_t)B * in_len;
+  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * CT) {
+    const int i = (int)(idx % in_len);
+    const int b = (int)(idx / in_len);
+    const int ic = i / (s.H * s.W), ih = (i / s.W) % s.H, iw = i % s.W;
+    float g = 0.0f;
+    for (int oc = 0; oc < s.outC; ++oc)
+      for (int kh = 0; kh < s.k; ++kh) {
+        const int t = ih + s.pad - kh;
+        if (t < 0 || t % s.stride) continue;
+        const int oh = t / s.stride;
+        if (oh >= s.oH) continue;
+        for (int kw = 0; kw < s.k; ++kw) {
+          const int u = iw + s.pad - kw;
+          if (u < 0 || u % s.stride) continue;
+          const int ow = u / s.stride;
+          if (ow >= s.oW) continue;
+          const int64_t o = ((int64_t)b * s.outC + oc) * osz + oh * s.oW + ow;
+          g += gout[o] * act_deriv(out[o], deriv) * w[((oc * s.inC + ic) * s.k + kh) * s.k + kw];
+        }
+      }
+    gin[idx] = g;
+  }
+}
+
+static unsigned grid_for(int64_t n) {
+  int64_t b = (n + CT - 1) / CT;
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, float *out,
+                           const ConvShape &s, int B, int fwd, hipStream_t st) {
+  const int64_t n = (int64_t)B * s.outC * s.oH * s.oW;
+  hipLaunchKernelGGL(conv2d_fwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, x, w, bias, out, s, B,
+                     fwd);
+  return hipGetLastError();
+}
+
+hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const PoolShape &s,
+                              int B, hipStream_t st) {
+  const int64_t n = (int64_t)B * s.C * s.oH * s.oW;
+  hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, x, out, argmax, s, B);
+  return hipGetLastError();
+}
+
+hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
+                              const PoolShape &s, int B, hipStream_t st) {
+  const int64_t n = (int64_t)B * s.C * s.H * s.W;
+  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, gout, argmax, gin, s,
+                     B);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
+                             const ConvShape &s, int B, int deriv, float scale, float *ws,
+                             size_t ws_cap, hipStream_t st) {
+  // bands of output rows: keep the dz tile (outC x rows x oW floats) <= 32 KiB
+  int band = s.oH;
+  while (band > 1 && (size_t)s.outC * band * s.oW * sizeof(float) > 32768) band = (band + 1) / 2;
+  const int bands = (s.oH + band - 1) / band;
+  const int nblocks = B * bands;
+  const int nslots = s.outC * s.inC * s.k * s.k + s.outC;
+  if ((size_t)nblocks * nslots > ws_cap) return hipErrorInvalidValue;
+  const size_t shm = (size_t)s.outC * band * s.oW * sizeof(float);
+  hipLaunchKernelGGL(conv2d_wgrad_partial, dim3(nblocks), dim3(CT), shm, st, x, gout, out, ws, s,
+                     band, deriv);
+  hipLaunchKernelGGL(conv2d_wgrad_final, dim3((nslots + CT - 1) / CT), dim3(CT), 0, st, ws, nblocks,
+                     nslots, scale, grad);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_dgrad(const float *gout, const float *out, const float *w, float *gin,
+                             const ConvShape &s, int B, int deriv, hipStream_t st) {
+  const int64_t n = (int64_t)B * s.inC * s.H * s.W;
+  hipLaunchKernelGGL(conv2d_dgrad_kernel, dim3(grid_for(n)), dim3(CT), 0, st, gout, out, w, gin, s,
+                     B, deriv);
+  return hipGetLastError();
+}
+
+}  // namespace gn

@@ -173,6 +173,42 @@ def test_odd_batch_and_sizes(gn, oracle):
     _compare_step(gn, oracle, cfg, steps=2)
 
 
+def test_cnn_full_config(gn, oracle):
+    """C2 at BASELINE size: gradients to 1e-4, and the Conv2D outputs (hence
+    pre-activations) and MaxPool argmax switches bit-exact per sample."""
+    from goneuron_amd import configs
+    cfg = configs.cnn()
+    model, net = _compare_step(gn, oracle, cfg, steps=1)
+    # after the step both hold the same weights again: compare one forward
+    x, y = configs.inputs(cfg)
+    B = cfg["B"]
+    model.SetParams(net.params)
+    model.TrainBatch(x, y)  # runs the forward on the device with these weights
+    conv_out = model.LayerOutput(0, B * 16 * 1024).reshape(B, -1)
+    am = model.LayerArgmax(1, B * 4096).reshape(B, -1)
+    bad_conv = bad_am = 0
+    for b in range(B):
+        net.forward(x[b])
+        pre = net.preact(0)
+        bad_conv += int((np.maximum(pre, 0) != conv_out[b]).sum())
+        bad_am += int((net.argmax(1) != am[b]).sum())
+    log(f"  cnn: conv mismatches {bad_conv}, argmax mismatches {bad_am}")
+    assert bad_conv == 0
+    assert bad_am == 0
+
+
+def test_conv_generic_path_and_predict(gn, oracle):
+    """Conv2D k3 s2 p1 (generic loop order) + MaxPool k2 s1 (overlapping
+    windows, gather backward) + Dense, small shapes, 2 steps."""
+    cfg = dict(num=9, name="conv_generic", B=6, loss="ce", lr=1e-3, x="normal", in_len=2 * 9 * 9,
+               classes=5,
+               layers=[{"kind": "conv2d", "inC": 2, "outC": 3, "k": 3, "s": 2, "p": 1, "act": "relu"},
+                       {"kind": "maxpool2d", "k": 2, "s": 1, "p": 0, "inC": 3},
+                       {"kind": "flatten", "n": 48},
+                       {"kind": "dense", "in": 48, "out": 5, "act": "softmax", "ptr": True}])
+    _compare_step(gn, oracle, cfg, steps=2)
+
+
 # ------------------------------------------------------------------ full-size C3 vs torch fp32
 def test_wide_full_size_vs_torch(gn):
     """C3 at BASELINE size: one step against torch autograd in float64 (Q4
