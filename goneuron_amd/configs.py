@@ -112,9 +112,10 @@ def product_layers(cfg):
             out.append(SequenceUnroller(LSTM(d["hidden"], d["in"]), d["T"], False))
         else:
             raise ValueError(k)
-    # the first layer carries the per-sample input length
-    out[0].desc.in_size = cfg["in_len"] if out[0].desc.in_size <= 0 or cfg["layers"][0]["kind"] in (
-        "conv2d", "embedding", "lstm") else out[0].desc.in_size
+    # the first layer carries the per-sample input length (an LSTM carries its
+    # per-step input size and sequence length instead)
+    if cfg["layers"][0]["kind"] in ("conv2d", "embedding") or out[0].desc.in_size <= 0:
+        out[0].desc.in_size = cfg["in_len"]
     return out
 
 

@@ -106,4 +106,17 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st);
 
+// ---- SequenceUnroller(LSTM) ----
+hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hipStream_t s);
+hipError_t launch_lstm_fwd(const float *x, const float *WxT, const float *WhT, const float *bias,
+                           float *pre_i, float *cbuf, float *hbuf, float *out, int B, int T, int I,
+                           int H, hipStream_t s);
+hipError_t launch_lstm_bwd(const float *gh, const float *pre_i, const float *cbuf, const float *Wh,
+                           const float *bias, float *D, int B, int T, int H, hipStream_t s);
+hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
+                                    double *coef, float *w, int B, int T, int I, int H, int W,
+                                    hipStream_t s);
+hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, int H,
+                              hipStream_t s);
+
 }  // namespace gn

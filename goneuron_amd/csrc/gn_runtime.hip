@@ -461,6 +461,12 @@ struct LayerRT {
   PoolShape ps{};               // MaxPool2D
   int32_t *argmax = nullptr;    // MaxPool2D switches [maxB, out_len]
   int cfwd = 0, cderiv = 0;     // Conv2D scalar Activate / Derivative kinds
+  // SequenceUnroller(LSTM): T steps of I inputs, H hidden
+  int T = 0, I = 0, H = 0;
+  float *WxT = nullptr, *WhT = nullptr;          // transposed input-gate blocks
+  float *pre_i = nullptr, *cbuf = nullptr, *hbuf = nullptr;
+  float *Dg = nullptr, *S = nullptr, *wts = nullptr;
+  double *gram = nullptr, *coef = nullptr;
 };
 
 struct gn_model {
@@ -529,6 +535,18 @@ static int plan_scalar_act(int act, int &fwd, int &deriv) {
   }
 }
 
+static void init_lstm(float *p, int in, int H) {  // LSTM.Build lstm.go:175-196
+  const float sin_ = (float)sqrt(2.0 / (double)(in + 4 * H));
+  const float srec = (float)sqrt(2.0 / (double)(H + 4 * H));
+  float *wx = p, *wh = wx + (int64_t)4 * H * in, *b = wh + (int64_t)4 * H * H;
+  uint64_t s = (uint64_t)(in * 1000 + H * 100 + 142);
+  for (int i = 0; i < 4 * H; ++i) {
+    b[i] = (i >= H && i < 2 * H) ? 1.0f : 0.0f;
+    for (int j = 0; j < in; ++j) wx[(int64_t)i * in + j] = lcg_float(s) * 2 * sin_ - sin_;
+    for (int j = 0; j < H; ++j) wh[(int64_t)i * H + j] = lcg_float(s) * 2 * srec - srec;
+  }
+}
+
 // Square-first dimension inference of Conv2D / MaxPool2D forward
 // (conv2d.go:733-746, maxpool2d.go:117-126).
 static void infer_hw(int channel_size, int &H, int &W) {
@@ -558,6 +576,7 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
 
   // Shape propagation (the reference infers per-sample lengths at forward time)
   int len = layers[0].in_size;
+  if (layers[0].kind == GN_LAYER_LSTM_UNROLLER) len = layers[0].in_size * layers[0].seq_len;
   if (len <= 0) return set_err(c, GN_ERR_INVALID, "first layer needs in_size (input length)");
   int64_t off = 0;
   for (int i = 0; i < nlayers; ++i) {
@@ -624,6 +643,22 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.out_len = ps.C * ps.oH * ps.oW;
         break;
       }
+      case GN_LAYER_LSTM_UNROLLER: {
+        R.T = R.d.seq_len;
+        R.I = R.d.in_size;
+        R.H = R.d.out_size;
+        if (R.T <= 0 || R.I <= 0 || R.H <= 0 || R.H > 1024)
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(LSTM) sizes", i);
+        if (R.d.return_sequences)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
+        if (i != 0)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: SequenceUnroller only as the first layer", i);
+        R.in_len = R.T * R.I;  // the first layer's in_size is the per-step input size here
+        len = R.in_len;
+        R.pcount = (int64_t)4 * R.H * R.I + (int64_t)4 * R.H * R.H + 4 * R.H;
+        R.out_len = R.H;
+        break;
+      }
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: kind %d not built in this library", i,
                        R.d.kind);
@@ -653,6 +688,26 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     maxw = std::max(maxw, std::max(R.in_len, R.out_len));
     if (R.d.kind == GN_LAYER_DENSE) init_dense(host.data() + R.poff, R.d.in_size, R.d.out_size);
     if (R.d.kind == GN_LAYER_CONV2D) init_conv(host.data() + R.poff, R.cs.inC, R.cs.outC, R.cs.k);
+    if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
+      init_lstm(host.data() + R.poff, R.I, R.H);
+      const size_t Bm = max_batch, T = R.T, H = R.H;
+      if ((rc = model_alloc(M.get(), (size_t)R.I * H, &R.WxT))) return rc;
+      if ((rc = model_alloc(M.get(), H * H, &R.WhT))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * T * H, &R.pre_i))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * T * H, &R.cbuf))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * (T + 1) * H, &R.hbuf))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * (T + 1) * 4 * H, &R.Dg))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * 4 * H, &R.S))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * (T + 1), &R.wts))) return rc;
+      const int Wc = std::min(std::max(M->workers, 1), max_batch);
+      const size_t chunk = (max_batch + Wc - 1) / Wc, nmax = chunk * T;
+      const size_t nchains = (max_batch + chunk - 1) / chunk;
+      float *g = nullptr, *cf = nullptr;
+      if ((rc = model_alloc(M.get(), 2 * nchains * nmax * nmax, &g))) return rc;
+      if ((rc = model_alloc(M.get(), 2 * nchains * nmax, &cf))) return rc;
+      R.gram = reinterpret_cast<double *>(g);
+      R.coef = reinterpret_cast<double *>(cf);
+    }
     if (R.d.kind == GN_LAYER_MAXPOOL2D) {
       float *am = nullptr;
       if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &am))) return rc;
@@ -804,6 +859,18 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
         break;
       }
+      case GN_LAYER_LSTM_UNROLLER: {
+        const float *Wx = M->params + R.poff;
+        const float *Wh = Wx + (int64_t)4 * R.H * R.I;
+        const float *bias = Wh + (int64_t)4 * R.H * R.H;
+        KTimer kt(c, GN_KCLASS_OTHER);
+        // input-gate blocks only (Q13), transposed for coalesced per-unit reads
+        HIP_OK(c, launch_transpose(Wx, R.WxT, R.H, R.I, c->stream));
+        HIP_OK(c, launch_transpose(Wh, R.WhT, R.H, R.H, c->stream));
+        HIP_OK(c, launch_lstm_fwd(cur, R.WxT, R.WhT, bias, R.pre_i, R.cbuf, R.hbuf, R.out, B, R.T,
+                                  R.I, R.H, c->stream));
+        break;
+      }
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
     }
@@ -874,6 +941,38 @@ static int model_backward(gn_model *M, const float *x, int B, float scale) {
                                     c->scratch, c->scratch_floats, c->stream));
         if (below && below->gout)
           HIP_OK(c, launch_conv_dgrad(R.gout, R.out, W, below->gout, R.cs, B, R.cderiv, c->stream));
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_LSTM_UNROLLER: {
+        const int H = R.H, T = R.T, I = R.I, G4 = 4 * H;
+        const float *Wx = M->params + R.poff;
+        const float *Wh = Wx + (int64_t)G4 * I;
+        const float *bias = Wh + (int64_t)G4 * H;
+        float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
+        {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_lstm_bwd(R.gout, R.pre_i, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
+          HIP_OK(c, launch_lstm_clip_weights(R.Dg, R.hbuf, in, R.gram, R.coef, R.wts, B, T, I, H,
+                                             M->workers, c->stream));
+          HIP_OK(c, launch_lstm_weight(R.Dg, R.wts, R.S, B, T, H, c->stream));
+          HIP_OK(c, launch_colsum(R.S, B, G4, G4, scale, gb, c->scratch, c->scratch_floats, c->stream));
+        }
+        KTimer kt(c, GN_KCLASS_GEMM);
+        GemmArgs a{};  // dWx = scale * S^T x_last
+        a.M = G4; a.N = I; a.K = B;
+        a.A = R.S; a.lda = G4;
+        a.B = in + (int64_t)(T - 1) * I; a.ldb = T * I;
+        a.C = gWx; a.ldc = I; a.alpha = scale;
+        a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+        HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+        GemmArgs h{};  // dWh = scale * (w dG)^T hPrev, K over (sample, step)
+        h.M = G4; h.N = H; h.K = B * (T + 1);
+        h.A = R.Dg; h.lda = G4;
+        h.B = R.hbuf; h.ldb = H;
+        h.C = gWh; h.ldc = H; h.alpha = scale;
+        h.ws = c->scratch; h.ws_cap = c->scratch_floats;
+        HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, h, c->stream));
         is_dz = false;
         break;
       }

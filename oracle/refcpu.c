@@ -210,6 +210,12 @@ struct layer {
   int32_t inC, outC, k, stride, pad, inH, inW, outH, outW;
   int32_t *argmax;
   float *savedInput;
+  /* LSTM (base of a SequenceUnroller) */
+  int32_t T, H, timeStep;
+  float *cellBuf, *hiddenBuf, *dcNext, *gateI, *gateF, *gateC, *gateO, *dI, *dF, *dC, *dO, *dc,
+      *dx, *dhPrev, *cPrev, *hPrev, *lstmIn;
+  float *savedC, *savedH, *savedPre; /* T x H, T x H, T x 4H */
+  float *curGrad, *dhNextU, *gradInU, *outU;
 };
 
 struct gno_net {
@@ -598,6 +604,190 @@ static const float *maxpool_backward(layer *L, const float *g) {
   return L->gradInBuf;
 }
 
+
+/* ------------------------------------------------------------------------ */
+/* LSTM (lstm.go) wrapped by SequenceUnroller (unroller.go)                  */
+/* ------------------------------------------------------------------------ */
+/* LSTM.Build lstm.go:144-256: params = [Wx (4H x in) | Wh (4H x H) | b (4H)],
+ * RNG(in*1000 + out*100 + 142); per gate row i: in input weights then H
+ * recurrent weights; bias 1 on rows [H, 2H). */
+static void lstm_build(layer *L) {
+  int32_t in = L->spec.in_size, H = L->spec.out_size, T = L->spec.seq_len;
+  L->H = H;
+  L->T = T;
+  L->nparams = (int64_t)4 * H * in + (int64_t)4 * H * H + 4 * H;
+  L->lstmIn = zalloc(in);
+  L->cellBuf = zalloc(H); L->hiddenBuf = zalloc(H); L->dcNext = zalloc(H);
+  L->gateI = zalloc(H); L->gateF = zalloc(H); L->gateC = zalloc(H); L->gateO = zalloc(H);
+  L->dI = zalloc(H); L->dF = zalloc(H); L->dC = zalloc(H); L->dO = zalloc(H);
+  L->dc = zalloc(H); L->dx = zalloc(in); L->dhPrev = zalloc(H); L->cPrev = zalloc(H);
+  L->hPrev = zalloc(H);
+  L->savedC = zalloc((int64_t)T * H);
+  L->savedH = zalloc((int64_t)T * H);
+  L->savedPre = zalloc((int64_t)T * 4 * H);
+  L->curGrad = zalloc(H);
+  L->dhNextU = zalloc(H);
+  L->gradInU = zalloc((int64_t)T * in);
+  L->outU = zalloc(H);
+  L->in_len = T * in;
+  L->out_len = H;
+}
+
+static void lstm_init_params(layer *L) {
+  int32_t in = L->spec.in_size, H = L->H;
+  float sin_ = (float)sqrt(2.0 / (double)(in + 4 * H));
+  float srec = (float)sqrt(2.0 / (double)(H + 4 * H));
+  float *wx = L->params, *wh = wx + (int64_t)4 * H * in, *b = wh + (int64_t)4 * H * H;
+  uint64_t rng = (uint64_t)(in * 1000 + H * 100 + 142);
+  for (int32_t i = 0; i < 4 * H; i++) {
+    if (i >= H && i < 2 * H) b[i] = 1.0f;
+    for (int32_t j = 0; j < in; j++) wx[(int64_t)i * in + j] = gno_rand_float(&rng) * 2 * sin_ - sin_;
+    for (int32_t j = 0; j < H; j++) wh[(int64_t)i * H + j] = gno_rand_float(&rng) * 2 * srec - srec;
+  }
+}
+
+/* LSTM.Reset lstm.go:258-274 */
+static void lstm_reset(layer *L) {
+  L->timeStep = 0;
+  for (int32_t i = 0; i < L->H; i++) L->cellBuf[i] = L->hiddenBuf[i] = L->dcNext[i] = 0;
+}
+
+/* LSTM.ForwardWithArena (CPU branch) lstm.go:276-407 for one time step. */
+static void lstm_step_forward(layer *L, const float *x) {
+  int32_t in = L->spec.in_size, H = L->H, t = L->timeStep;
+  const float *wx = L->params, *wh = wx + (int64_t)4 * H * in, *b = wh + (int64_t)4 * H * H;
+  float *pre = L->savedPre + (int64_t)t * 4 * H;
+  memcpy(L->lstmIn, x, sizeof(float) * in);
+  memcpy(pre, b, sizeof(float) * 4 * H);
+  /* Q13: the gate helpers run over outSize rows only (lstm.go:1065-1101) */
+  if (in >= 64) {
+    for (int32_t i = 0; i < H; i++)
+      for (int32_t j = 0; j < in; j++) pre[i] += wx[(int64_t)i * in + j] * x[j];
+  } else {
+    for (int32_t i = 0; i < H; i++) {
+      float sum = 0.0f;
+      for (int32_t j = 0; j < in; j++) sum += wx[(int64_t)i * in + j] * x[j];
+      pre[i] += sum;
+    }
+  }
+  for (int32_t i = 0; i < H; i++)
+    for (int32_t j = 0; j < H; j++) pre[i] += wh[(int64_t)i * H + j] * L->hiddenBuf[j];
+  for (int32_t i = 0; i < H; i++) {
+    L->gateI[i] = gno_activate(GNO_ACT_SIGMOID, pre[i]);
+    L->gateF[i] = gno_activate(GNO_ACT_SIGMOID, pre[H + i]);
+    L->gateC[i] = gno_activate(GNO_ACT_TANH, pre[2 * H + i]);
+    L->gateO[i] = gno_activate(GNO_ACT_SIGMOID, pre[3 * H + i]);
+  }
+  if (t > 0) memcpy(L->cellBuf, L->savedC + (int64_t)(t - 1) * H, sizeof(float) * H);
+  else for (int32_t i = 0; i < H; i++) L->cellBuf[i] = 0;
+  for (int32_t i = 0; i < H; i++) L->cellBuf[i] = L->gateF[i] * L->cellBuf[i] + L->gateI[i] * L->gateC[i];
+  for (int32_t i = 0; i < H; i++) L->hiddenBuf[i] = L->gateO[i] * (float)tanh((double)L->cellBuf[i]);
+  memcpy(L->savedC + (int64_t)t * H, L->cellBuf, sizeof(float) * H);
+  memcpy(L->savedH + (int64_t)t * H, L->hiddenBuf, sizeof(float) * H);
+  L->timeStep++;
+}
+
+/* LSTM.clipGradients lstm.go:725-751 (Q14) */
+static void lstm_clip(layer *L) {
+  float ns = 0.0f;
+  for (int64_t i = 0; i < L->nparams; i++) ns += L->grads[i] * L->grads[i];
+  float norm = (float)sqrt((double)ns);
+  if (norm > 1.0f) {
+    float scale = 1.0f / norm;
+    for (int64_t i = 0; i < L->nparams; i++) L->grads[i] *= scale;
+  }
+}
+
+/* LSTM.Backward lstm.go:476-698 for the latest remaining time step; `grad`
+ * is updated in place with dhPrev (Q15).  Returns dx. */
+static const float *lstm_step_backward(layer *L, float *grad) {
+  int32_t in = L->spec.in_size, H = L->H;
+  int32_t ts = L->timeStep - 1;
+  if (ts < 0) {
+    for (int32_t i = 0; i < in; i++) L->lstmIn[i] = 0;
+    return L->lstmIn;
+  }
+  const float *wx = L->params, *wh = wx + (int64_t)4 * H * in;
+  float *gwx = L->grads, *gwh = gwx + (int64_t)4 * H * in, *gb = gwh + (int64_t)4 * H * H;
+  const float *c = L->savedC + (int64_t)ts * H;
+  const float *pre = L->savedPre + (int64_t)ts * 4 * H;
+  if (ts > 0) {
+    memcpy(L->cPrev, L->savedC + (int64_t)(ts - 1) * H, sizeof(float) * H);
+    memcpy(L->hPrev, L->savedH + (int64_t)(ts - 1) * H, sizeof(float) * H);
+  } else {
+    for (int32_t i = 0; i < H; i++) L->cPrev[i] = L->hPrev[i] = 0;
+  }
+  for (int32_t i = 0; i < H; i++) {
+    L->gateI[i] = gno_activate(GNO_ACT_SIGMOID, pre[i]);
+    L->gateF[i] = gno_activate(GNO_ACT_SIGMOID, pre[H + i]);
+    L->gateC[i] = gno_activate(GNO_ACT_TANH, pre[2 * H + i]);
+    L->gateO[i] = gno_activate(GNO_ACT_SIGMOID, pre[3 * H + i]);
+  }
+  for (int32_t i = 0; i < H; i++) {
+    float tc = (float)tanh((double)c[i]);
+    L->dc[i] = grad[i] * L->gateO[i] * (1 - tc * tc) + L->dcNext[i];
+  }
+  for (int32_t i = 0; i < H; i++) L->dI[i] = L->dc[i] * L->gateC[i] * gno_derivative(GNO_ACT_SIGMOID, pre[i]);
+  for (int32_t i = 0; i < H; i++) L->dF[i] = L->dc[i] * L->cPrev[i] * gno_derivative(GNO_ACT_SIGMOID, pre[H + i]);
+  for (int32_t i = 0; i < H; i++) L->dC[i] = L->dc[i] * L->gateI[i] * gno_derivative(GNO_ACT_TANH, pre[2 * H + i]);
+  for (int32_t i = 0; i < H; i++)
+    L->dO[i] = grad[i] * (float)tanh((double)c[i]) * gno_derivative(GNO_ACT_SIGMOID, pre[3 * H + i]);
+  for (int32_t i = 0; i < H; i++) L->dcNext[i] = L->dc[i] * L->gateF[i];
+  const float *dg[4] = {L->dI, L->dF, L->dC, L->dO};
+  /* Q10: inputBuf holds the last forward step's x */
+  for (int32_t g = 0; g < 4; g++)
+    for (int32_t i = 0; i < H; i++) {
+      int64_t row = (int64_t)g * H + i;
+      for (int32_t j = 0; j < in; j++) gwx[row * in + j] += dg[g][i] * L->lstmIn[j];
+      gb[row] += dg[g][i];
+    }
+  for (int32_t g = 0; g < 4; g++)
+    for (int32_t i = 0; i < H; i++) {
+      int64_t row = (int64_t)g * H + i;
+      for (int32_t j = 0; j < H; j++) gwh[row * H + j] += dg[g][i] * L->hPrev[j];
+    }
+  for (int32_t i = 0; i < in; i++) {
+    float sum = 0.0f;
+    for (int32_t g = 0; g < 4; g++)
+      for (int32_t j = 0; j < H; j++) sum += wx[((int64_t)g * H + j) * in + i] * dg[g][j];
+    L->dx[i] = sum;
+  }
+  for (int32_t i = 0; i < H; i++) {
+    float sum = 0.0f;
+    for (int32_t g = 0; g < 4; g++)
+      for (int32_t j = 0; j < H; j++) sum += wh[((int64_t)g * H + j) * H + i] * dg[g][j];
+    L->dhPrev[i] = sum;
+  }
+  for (int32_t i = 0; i < H; i++) grad[i] += L->dhPrev[i];
+  lstm_clip(L);
+  L->timeStep--;
+  return L->dx;
+}
+
+/* SequenceUnroller.ForwardWithArena unroller.go:57-127 (LSTM base, last state) */
+static const float *unroller_forward(layer *L, const float *x) {
+  int32_t in = L->spec.in_size;
+  lstm_reset(L);
+  for (int32_t t = 0; t < L->T; t++) lstm_step_forward(L, x + (int64_t)t * in);
+  memcpy(L->outU, L->hiddenBuf, sizeof(float) * L->H);
+  return L->outU;
+}
+
+/* SequenceUnroller.Backward unroller.go:133-213 (non-bidirectional branch) */
+static const float *unroller_backward(layer *L, const float *grad) {
+  int32_t in = L->spec.in_size, H = L->H;
+  for (int32_t i = 0; i < H; i++) L->dhNextU[i] = 0;
+  for (int32_t t = L->T - 1; t >= 0; t--) {
+    memcpy(L->curGrad, L->dhNextU, sizeof(float) * H);
+    if (t == L->T - 1)
+      for (int32_t i = 0; i < H; i++) L->curGrad[i] += grad[i];
+    const float *dx = lstm_step_backward(L, L->curGrad);
+    memcpy(L->gradInU + (int64_t)t * in, dx, sizeof(float) * in);
+    memcpy(L->dhNextU, L->curGrad, sizeof(float) * H);
+  }
+  return L->gradInU;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Generic layer dispatch                                                     */
 /* ------------------------------------------------------------------------ */
@@ -613,16 +803,19 @@ static void layer_build(layer *L) {
       L->pad = L->spec.padding;
       break;
     case GNO_LAYER_FLATTEN: break;
+    case GNO_LAYER_LSTM_UNROLLER: lstm_build(L); break;
     default: break;
   }
 }
 static void layer_init_params(layer *L) {
   if (L->kind == GNO_LAYER_DENSE) dense_init_params(L);
   else if (L->kind == GNO_LAYER_CONV2D) conv_init_params(L);
+  else if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_init_params(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
   if (L->kind == GNO_LAYER_MAXPOOL2D) { L->inH = L->inW = 0; }                      /* maxpool2d.go:508-513 */
+  if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_reset(L);                             /* unroller.go:268 */
 }
 /* *len_io: input length in, output length out */
 static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
@@ -633,6 +826,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_CONV2D: o = conv_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_MAXPOOL2D: o = maxpool_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_FLATTEN: o = x; L->in_len = L->out_len = *len_io; break; /* reshape.go:64-80 */
+    case GNO_LAYER_LSTM_UNROLLER: o = unroller_forward(L, x); *len_io = L->H; break;
     default: o = x;
   }
   return o;
@@ -644,6 +838,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_CONV2D: return conv_backward(L, g);
     case GNO_LAYER_MAXPOOL2D: return maxpool_backward(L, g);
     case GNO_LAYER_FLATTEN: return g; /* reshape.go:83-86 */
+    case GNO_LAYER_LSTM_UNROLLER: return unroller_backward(L, g);
     default: return g;
   }
 }
@@ -692,6 +887,11 @@ void gno_net_destroy(gno_net *n) {
     layer *L = &n->layers[i];
     free(L->inputBuf); free(L->preActBuf); free(L->outputBuf); free(L->savedOutput);
     free(L->gradInBuf); free(L->dzBuf); free(L->maskBuf); free(L->argmax); free(L->savedInput);
+    float *lb[] = {L->cellBuf, L->hiddenBuf, L->dcNext, L->gateI, L->gateF, L->gateC, L->gateO,
+                   L->dI, L->dF, L->dC, L->dO, L->dc, L->dx, L->dhPrev, L->cPrev, L->hPrev,
+                   L->lstmIn, L->savedC, L->savedH, L->savedPre, L->curGrad, L->dhNextU,
+                   L->gradInU, L->outU};
+    for (size_t k = 0; k < sizeof lb / sizeof lb[0]; k++) free(lb[k]);
   }
   free(n->layers);
   free(n->params); free(n->grads); free(n->m); free(n->v); free(n->worker_grads); free(n->lossGrad);
@@ -719,6 +919,7 @@ static int32_t in_len_of(const gno_net *n) {
   switch (L->kind) {
     case GNO_LAYER_DENSE: return L->spec.in_size;
     case GNO_LAYER_DROPOUT: return L->spec.in_size;
+    case GNO_LAYER_LSTM_UNROLLER: return L->T * L->spec.in_size;
     default: return L->spec.in_size;
   }
 }

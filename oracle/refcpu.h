@@ -19,6 +19,8 @@
  *   Conv2D                            internal/layer/conv2d.go:114-1174
  *   MaxPool2D                         internal/layer/maxpool2d.go:106-410,508-513
  *   Flatten                           internal/layer/reshape.go:64-96
+ *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
+ *   SequenceUnroller                  internal/layer/unroller.go:57-213
  *   RNG                               internal/layer/layer.go:61-81
  * Built with -O2 -ffp-contract=off (Go amd64 GOAMD64=v1 emits no FMA).
  */

@@ -23,6 +23,9 @@ def oracle_specs(refcpu, cfg):
         elif k == "maxpool2d":
             specs.append(refcpu.spec(refcpu.LAYER_MAXPOOL2D, in_channels=d["inC"], kernel=d["k"],
                                      stride=d["s"], padding=d["p"]))
+        elif k == "lstm":
+            specs.append(refcpu.spec(refcpu.LAYER_LSTM_UNROLLER, in_size=d["in"], out_size=d["hidden"],
+                                     seq_len=d["T"]))
         else:
             raise NotImplementedError(k)
     return specs

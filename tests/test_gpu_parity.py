@@ -209,6 +209,25 @@ def test_conv_generic_path_and_predict(gn, oracle):
     _compare_step(gn, oracle, cfg, steps=2)
 
 
+@pytest.mark.parametrize("workers,steps", [(64, 2), (4, 1), (1, 1)])
+def test_lstm_full_config(gn, oracle, workers, steps):
+    """C5 at BASELINE size (LSTM 64->256, T=100, B=64, MSE): the per-step
+    clip couples the samples of each worker chain, so W is part of the
+    semantics (trainBatchParallel, net.go:588-717)."""
+    from goneuron_amd import configs
+    _compare_step(gn, oracle, configs.lstm(), steps=steps, workers=workers)
+
+
+@pytest.mark.parametrize("workers", [1, 3])
+def test_lstm_small_unrolled_path(gn, oracle, workers):
+    """in < 64 takes the sum-then-add input-gate helper; odd sizes; 3 steps
+    (after the first Adam step every gate carries gradient)."""
+    from goneuron_amd import configs
+    cfg = configs.lstm(B=7, T=9, inp=5, hidden=24)
+    x, y = configs.inputs(cfg)
+    _compare_step(gn, oracle, cfg, steps=3, workers=workers)
+
+
 # ------------------------------------------------------------------ full-size C3 vs torch fp32
 def test_wide_full_size_vs_torch(gn):
     """C3 at BASELINE size: one step against torch autograd in float64 (Q4

@@ -354,3 +354,125 @@ def test_facade_softmax_value_gives_nan(oracle):
     np.testing.assert_array_equal(out, pre)
     net.accumulate_batch(x, np.eye(3, dtype=np.float32)[:1], 1)
     assert np.isnan(net.grads).all()
+
+
+# ---------------------------------------------------------------- LSTM (C5 semantics)
+def _lstm_cfg(B=4, T=5, inp=6, H=8):
+    from goneuron_amd import configs
+    return configs.lstm(B=B, T=T, inp=inp, hidden=H)
+
+
+def test_lstm_init_closed_form(oracle):
+    # LSTM.Build lstm.go:175-196: per gate row, inSize input draws then H recurrent draws
+    from cfgutil import oracle_net
+    cfg = _lstm_cfg(T=2, inp=3, H=2)
+    net = oracle_net(oracle, cfg)
+    p = net.params
+    inp, H = 3, 2
+    s = inp * 1000 + H * 100 + 142
+    si = np.float32(math.sqrt(2.0 / (inp + 4 * H)))
+    sr = np.float32(math.sqrt(2.0 / (H + 4 * H)))
+    wx = np.zeros((4 * H, inp), np.float32)
+    wh = np.zeros((4 * H, H), np.float32)
+
+    def u():
+        nonlocal s
+        s = (s * 6364136223846793005 + 1) % (1 << 64)
+        return np.float32(s >> 33) / np.float32(2 ** 31)
+    for i in range(4 * H):
+        for j in range(inp):
+            wx[i, j] = np.float32(np.float32(u() * np.float32(2)) * si) - si
+        for j in range(H):
+            wh[i, j] = np.float32(np.float32(u() * np.float32(2)) * sr) - sr
+    b = np.zeros(4 * H, np.float32)
+    b[H:2 * H] = 1
+    np.testing.assert_array_equal(p[:4 * H * inp], wx.ravel())
+    np.testing.assert_array_equal(p[4 * H * inp:4 * H * (inp + H)], wh.ravel())
+    np.testing.assert_array_equal(p[4 * H * (inp + H):4 * H * (inp + H) + 4 * H], b)
+
+
+@pytest.mark.parametrize("workers", [1, 4])
+def test_lstm_first_step_structure(oracle, workers):
+    """At initialisation the cell-gate bias is 0, so g = tanh(0) = 0, c and h stay
+    0 (Q13 leaves f, g, o without Wx x + Wh h): the Dense sees h = 0, the loss
+    is mean (b_d - y)^2, and only the cell-gate rows of Wx and b get gradient,
+    each row a multiple of the LAST step's input (Q10); Wh gets none."""
+    from cfgutil import oracle_net
+    from goneuron_amd import configs
+    B, T, inp, H = 4, 5, 6, 8
+    cfg = _lstm_cfg(B, T, inp, H)
+    net = oracle_net(oracle, cfg, workers=workers)
+    x, y = configs.inputs(cfg)
+    p = net.params.copy()
+    loss = net.accumulate_batch(x, y, B)
+    g = net.grads
+    nwx, nwh = 4 * H * inp, 4 * H * H
+    bd = p[nwx + nwh + 4 * H + H]
+    np.testing.assert_allclose(loss, np.mean((bd - y[:, 0]) ** 2), rtol=1e-6)
+    gwx = g[:nwx].reshape(4 * H, inp)
+    gwh = g[nwx:nwx + nwh]
+    gb = g[nwx + nwh:nwx + nwh + 4 * H]
+    assert not gwh.any()
+    for gate in (0, 1, 3):
+        assert not gwx[gate * H:(gate + 1) * H].any()
+        assert not gb[gate * H:(gate + 1) * H].any()
+    assert np.abs(gwx[2 * H:3 * H]).max() > 0
+    # dense: gradW = 0 (h = 0), gradB = mean 2 (b_d - y)
+    assert not g[nwx + nwh + 4 * H:nwx + nwh + 4 * H + H].any()
+    np.testing.assert_allclose(g[-1], np.mean(2 * (bd - y[:, 0])), rtol=1e-5)
+    # one sample alone: every cell row of dWx is a multiple of x_{T-1}
+    cfg1 = _lstm_cfg(1, T, inp, H)
+    net1 = oracle_net(oracle, cfg1)
+    net1.accumulate_batch(x[:1], y[:1], 1)
+    g1 = net1.grads[:nwx].reshape(4 * H, inp)
+    xl = x[0].reshape(T, inp)[-1]
+    for r in range(2 * H, 3 * H):
+        cos = g1[r] @ xl / (np.linalg.norm(g1[r]) * np.linalg.norm(xl) + 1e-30)
+        assert abs(abs(cos) - 1) < 1e-5
+
+
+@pytest.mark.parametrize("workers", [1, 2, 6])
+def test_lstm_clip_bounds_each_chain(oracle, workers):
+    """Q14: each worker's LSTM gradient is clipped to norm <= 1 after every step,
+    so the averaged LSTM gradient has norm <= W/B."""
+    from cfgutil import oracle_net
+    from goneuron_amd import configs
+    B, T, inp, H = 6, 7, 5, 8
+    cfg = _lstm_cfg(B, T, inp, H)
+    net = oracle_net(oracle, cfg, workers=workers)
+    x, y = configs.inputs(cfg)
+    y = y * 50  # large targets: the clip is active
+    for _ in range(3):   # later steps: all gates carry gradient
+        net.accumulate_batch(x, y, B)
+        nl = 4 * H * (inp + H) + 4 * H
+        assert np.linalg.norm(net.grads[:nl]) <= workers / B * (1 + 1e-5)
+        net.step()
+
+
+def _lstm_clip_gram(deltas):
+    """Independent restatement of the per-step clip G <- clip(G + D_t) through the
+    Gram matrix of the contributions: G_T = sum_t w_t D_t (float64)."""
+    n = len(deltas)
+    D = np.stack([d.astype(np.float64) for d in deltas])
+    Gm = D @ D.T
+    w = np.zeros(n)
+    nrm2 = 0.0
+    for t in range(n):
+        N2 = nrm2 + 2 * (w[:t] @ Gm[:t, t]) + Gm[t, t]
+        c = 1.0 / math.sqrt(N2) if math.sqrt(N2) > 1 else 1.0
+        w[:t] *= c
+        w[t] = c
+        nrm2 = c * c * N2
+    return w @ D
+
+
+def test_clip_gram_restatement_matches_sequential():
+    rng = np.random.default_rng(9)
+    deltas = [rng.normal(size=300).astype(np.float32) * s for s in (0.1, 2, 0.3, 5, 0.01, 1.5)]
+    G = np.zeros(300, np.float32)
+    for d in deltas:
+        G += d
+        nrm = np.float32(math.sqrt(float(np.sum(G.astype(np.float64) ** 2))))
+        if nrm > 1:
+            G *= np.float32(1) / nrm
+    np.testing.assert_allclose(_lstm_clip_gram(deltas), G, rtol=1e-5, atol=1e-7)
