@@ -192,6 +192,7 @@ void gno_matmul(const float *in, const float *w, const float *bias, float *out,
 /* Layers                                                                    */
 /* ------------------------------------------------------------------------ */
 typedef struct layer layer;
+typedef struct lnorm lnorm;
 struct layer {
   gno_layer_spec spec;
   int32_t kind;
@@ -216,6 +217,13 @@ struct layer {
       *dx, *dhPrev, *cPrev, *hPrev, *lstmIn;
   float *savedC, *savedH, *savedPre; /* T x H, T x H, T x 4H */
   float *curGrad, *dhNextU, *gradInU, *outU;
+  /* Embedding / PositionalEncoding / CLSPooling / TransformerBlock */
+  int32_t V, D, NH, FF;
+  int32_t *ids;
+  struct layer *sub;       /* block: wQ, wK, wV, wOut, ff1, ff2 (Dense) */
+  struct lnorm *ln;        /* block: norm1, norm2 */
+  float *aq, *ak, *av, *scores, *fin, *gfin, *gq, *gk, *gv, *attOut, *res1, *n1, *ffOut, *res2,
+      *blkOut, *gRes2, *gN1ff, *comb, *gRes1, *gInAtt, *tmpRow, *probs, *dpre;
 };
 
 struct gno_net {
@@ -788,6 +796,388 @@ static const float *unroller_backward(layer *L, const float *grad) {
   return L->gradInU;
 }
 
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm (layernorm.go:83-441), used inside TransformerBlock             */
+/* ------------------------------------------------------------------------ */
+struct lnorm {
+  int32_t N, rows;
+  float eps;
+  float *gamma, *beta, *ggamma, *gbeta; /* views */
+  float *savedInput, *means, *stds, *out, *gin, *gp;
+};
+
+static void ln_build(lnorm *L, int32_t N, int32_t rows) {
+  L->N = N;
+  L->rows = rows;
+  L->eps = 1e-5f;
+  L->savedInput = zalloc((int64_t)N * rows);
+  L->means = zalloc(rows);
+  L->stds = zalloc(rows);
+  L->out = zalloc((int64_t)N * rows);
+  L->gin = zalloc((int64_t)N * rows);
+  L->gp = zalloc(N);
+}
+
+static void ln_free(lnorm *L) {
+  free(L->savedInput); free(L->means); free(L->stds); free(L->out); free(L->gin); free(L->gp);
+}
+
+/* LayerNorm.ForwardWithArena (arena-less) layernorm.go:193-304 */
+static const float *ln_forward(lnorm *L, const float *x) {
+  int32_t N = L->N;
+  memcpy(L->savedInput, x, sizeof(float) * N * L->rows);
+  for (int32_t s = 0; s < L->rows; s++) {
+    const float *r = x + (int64_t)s * N;
+    float sum = 0.0f;
+    for (int32_t i = 0; i < N; i++) sum += r[i];
+    float mean = sum / (float)N;
+    L->means[s] = mean;
+    float ss = 0.0f;
+    for (int32_t i = 0; i < N; i++) {
+      float d = r[i] - mean;
+      ss += d * d;
+    }
+    float var = ss / (float)N;
+    float std = (float)sqrt((double)(var + L->eps));
+    L->stds[s] = std;
+    for (int32_t i = 0; i < N; i++) {
+      float nrm = (r[i] - mean) / std;
+      L->out[(int64_t)s * N + i] = L->gamma[i] * nrm + L->beta[i];
+    }
+  }
+  return L->out;
+}
+
+/* LayerNorm.Backward (CPU branch) layernorm.go:334-441 */
+static const float *ln_backward(lnorm *L, const float *g) {
+  int32_t N = L->N;
+  for (int32_t s = 0; s < L->rows; s++) {
+    const float *gr = g + (int64_t)s * N;
+    const float *xr = L->savedInput + (int64_t)s * N;
+    float mean = L->means[s], std = L->stds[s];
+    for (int32_t i = 0; i < N; i++) L->gp[i] = gr[i] * L->gamma[i];
+    float sumGrad = 0.0f, sumGX = 0.0f;
+    for (int32_t i = 0; i < N; i++) {
+      float diff = xr[i] - mean;
+      sumGrad += L->gp[i];
+      sumGX += L->gp[i] * diff;
+    }
+    for (int32_t i = 0; i < N; i++) {
+      float diff = xr[i] - mean;
+      float v = (L->gp[i] - sumGrad / (float)N) / std;
+      v -= (diff * sumGX) / ((float)N * std * std);
+      L->gin[(int64_t)s * N + i] = v;
+    }
+  }
+  for (int32_t s = 0; s < L->rows; s++) {
+    const float *gr = g + (int64_t)s * N;
+    const float *xr = L->savedInput + (int64_t)s * N;
+    float mean = L->means[s], std = L->stds[s];
+    for (int32_t i = 0; i < N; i++) {
+      float nrm = (xr[i] - mean) / std;
+      L->ggamma[i] += gr[i] * nrm;
+      L->gbeta[i] += gr[i];
+    }
+  }
+  return L->gin;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Embedding (embedding.go:42-183)                                            */
+/* ------------------------------------------------------------------------ */
+static void emb_build(layer *L) {
+  L->V = L->spec.vocab;
+  L->D = L->spec.dim;
+  L->T = L->spec.in_size; /* tokens per sample */
+  L->nparams = (int64_t)L->V * L->D;
+  L->ids = (int32_t *)calloc((size_t)L->T, sizeof(int32_t));
+  L->outputBuf = zalloc((int64_t)L->T * L->D);
+  L->gradInBuf = zalloc(L->T);
+  L->in_len = L->T;
+  L->out_len = L->T * L->D;
+}
+static void emb_init(layer *L) {
+  float scale = (float)sqrt(3.0 / (double)L->D);
+  uint64_t rng = 42;
+  for (int64_t i = 0; i < L->nparams; i++) L->params[i] = scale * (2 * gno_rand_float(&rng) - 1);
+}
+static const float *emb_forward(layer *L, const float *x) {
+  for (int32_t b = 0; b < L->T; b++) {
+    int32_t idx = (int32_t)floor((double)x[b]);
+    L->ids[b] = (int32_t)x[b];
+    if (idx < 0 || idx >= L->V) idx = 0; /* the reference errors out (sample skipped) */
+    memcpy(L->outputBuf + (int64_t)b * L->D, L->params + (int64_t)idx * L->D, sizeof(float) * L->D);
+  }
+  return L->outputBuf;
+}
+/* Q12: the whole embedding gradient view is zeroed before the scatter */
+static const float *emb_backward(layer *L, const float *g) {
+  for (int64_t i = 0; i < L->nparams; i++) L->grads[i] = 0;
+  for (int32_t b = 0; b < L->T; b++) {
+    int32_t idx = L->ids[b];
+    if (idx < 0 || idx >= L->V) continue;
+    for (int32_t d = 0; d < L->D; d++) L->grads[(int64_t)idx * L->D + d] += g[(int64_t)b * L->D + d];
+  }
+  for (int32_t b = 0; b < L->T; b++) L->gradInBuf[b] = 0;
+  return L->gradInBuf;
+}
+
+/* PositionalEncoding (transformer.go:51-120) */
+static void pe_build(layer *L) {
+  L->T = L->spec.seq_len;
+  L->D = L->spec.dim;
+  L->nparams = (int64_t)L->T * L->D;
+  L->outputBuf = zalloc(L->nparams);
+  L->in_len = L->out_len = L->T * L->D;
+}
+static void pe_init(layer *L) {
+  uint64_t rng = (uint64_t)(L->T + L->D + 42);
+  float scale = (float)sqrt(1.0 / (double)L->D);
+  for (int64_t i = 0; i < L->nparams; i++) L->params[i] = gno_rand_float(&rng) * 2 * scale - scale;
+}
+static const float *pe_forward(layer *L, const float *x) {
+  for (int64_t i = 0; i < L->nparams; i++) L->outputBuf[i] = x[i] + L->params[i];
+  return L->outputBuf;
+}
+static const float *pe_backward(layer *L, const float *g) {
+  for (int64_t i = 0; i < L->nparams; i++) L->grads[i] += g[i];
+  return g;
+}
+
+/* CLSPooling (transformer.go:1679-1725) */
+static void cls_build(layer *L) {
+  L->T = L->spec.seq_len;
+  L->D = L->spec.dim;
+  L->outputBuf = zalloc(L->D);
+  L->gradInBuf = zalloc((int64_t)L->T * L->D);
+  L->in_len = L->T * L->D;
+  L->out_len = L->D;
+}
+static const float *cls_forward(layer *L, const float *x) {
+  memcpy(L->outputBuf, x, sizeof(float) * L->D);
+  return L->outputBuf;
+}
+static const float *cls_backward(layer *L, const float *g) {
+  for (int64_t i = 0; i < (int64_t)L->T * L->D; i++) L->gradInBuf[i] = 0;
+  memcpy(L->gradInBuf, g, sizeof(float) * L->D);
+  return L->gradInBuf;
+}
+
+/* ------------------------------------------------------------------------ */
+/* TransformerBlock (transformer.go:908-1279) with MultiHeadAttention        */
+/* (:318-690).  Sub-layer flat order: wQ, wK, wV, wOut (W then b), norm1     */
+/* (gamma, beta), norm2, ff1 (W [ff][dim], b), ff2 (W [dim][ff], b).         */
+/* ------------------------------------------------------------------------ */
+static void dense_sub_build(layer *S, int32_t in, int32_t out, int32_t act) {
+  memset(S, 0, sizeof *S);
+  S->kind = GNO_LAYER_DENSE;
+  S->spec.kind = GNO_LAYER_DENSE;
+  S->spec.in_size = in;
+  S->spec.out_size = out;
+  S->spec.act = act;
+  S->training = 1;
+  dense_build(S);
+}
+
+static void tb_build(layer *L) {
+  int32_t d = L->spec.dim, T = L->spec.seq_len, ff = L->spec.ff_dim;
+  L->D = d;
+  L->T = T;
+  L->NH = L->spec.num_heads;
+  L->FF = ff;
+  L->sub = (layer *)calloc(6, sizeof(layer));
+  for (int i = 0; i < 4; i++) dense_sub_build(&L->sub[i], d, d, GNO_ACT_LINEAR);
+  dense_sub_build(&L->sub[4], d, ff, GNO_ACT_RELU);
+  dense_sub_build(&L->sub[5], ff, d, GNO_ACT_LINEAR);
+  L->ln = (lnorm *)calloc(2, sizeof(lnorm));
+  ln_build(&L->ln[0], d, T);
+  ln_build(&L->ln[1], d, T);
+  int64_t nd = (int64_t)d * d + d;
+  L->nparams = 4 * nd + 4 * (int64_t)d + ((int64_t)ff * d + ff) + ((int64_t)d * ff + d);
+  int64_t td = (int64_t)T * d;
+  L->aq = zalloc(td); L->ak = zalloc(td); L->av = zalloc(td); L->scores = zalloc((int64_t)T * T);
+  L->fin = zalloc(td); L->gfin = zalloc(td); L->gq = zalloc(td); L->gk = zalloc(td); L->gv = zalloc(td);
+  L->attOut = zalloc(td); L->res1 = zalloc(td); L->n1 = zalloc(td); L->ffOut = zalloc(td);
+  L->res2 = zalloc(td); L->blkOut = zalloc(td); L->gRes2 = zalloc(td); L->gN1ff = zalloc(td);
+  L->comb = zalloc(td); L->gRes1 = zalloc(td); L->gInAtt = zalloc(td);
+  L->tmpRow = zalloc(T); L->probs = zalloc(T); L->dpre = zalloc(T);
+  L->in_len = L->out_len = (int32_t)td;
+}
+
+/* bind sub-layer params / grads to the block's slices of the flat arena */
+static void tb_bind(layer *L) {
+  int32_t d = L->D, ff = L->FF;
+  int64_t nd = (int64_t)d * d + d, off = 0;
+  for (int i = 0; i < 4; i++) {
+    L->sub[i].params = L->params + off;
+    L->sub[i].grads = L->grads + off;
+    off += nd;
+  }
+  for (int i = 0; i < 2; i++) {
+    L->ln[i].gamma = L->params + off;
+    L->ln[i].beta = L->params + off + d;
+    L->ln[i].ggamma = L->grads + off;
+    L->ln[i].gbeta = L->grads + off + d;
+    off += 2 * d;
+  }
+  L->sub[4].params = L->params + off;
+  L->sub[4].grads = L->grads + off;
+  off += (int64_t)ff * d + ff;
+  L->sub[5].params = L->params + off;
+  L->sub[5].grads = L->grads + off;
+}
+
+/* Q11: TransformerBlock.Build and MultiHeadAttention.Build rebind every
+ * sub-layer to freshly allocated (zero) slices: all block parameters start 0. */
+static void tb_init(layer *L) {
+  for (int64_t i = 0; i < L->nparams; i++) L->params[i] = 0.0f;
+}
+
+/* MultiHeadAttention.ForwardWithArena (arena-less) transformer.go:405-527 */
+static const float *mha_forward(layer *L, const float *x) {
+  int32_t T = L->T, d = L->D, nh = L->NH, hd = d / nh;
+  for (int32_t t = 0; t < T; t++) {
+    memcpy(L->aq + (int64_t)t * d, dense_forward(&L->sub[0], x + (int64_t)t * d), sizeof(float) * d);
+    memcpy(L->ak + (int64_t)t * d, dense_forward(&L->sub[1], x + (int64_t)t * d), sizeof(float) * d);
+    memcpy(L->av + (int64_t)t * d, dense_forward(&L->sub[2], x + (int64_t)t * d), sizeof(float) * d);
+  }
+  float scale = (float)sqrt((double)hd);
+  for (int32_t h = 0; h < nh; h++) {
+    for (int32_t i = 0; i < T; i++)
+      for (int32_t j = 0; j < T; j++) {
+        if (L->spec.causal && j > i) {
+          L->scores[i * T + j] = -1e9f;
+          continue;
+        }
+        float dot = 0.0f;
+        for (int32_t e = 0; e < hd; e++) dot += L->aq[i * d + h * hd + e] * L->ak[j * d + h * hd + e];
+        L->scores[i * T + j] = dot / scale;
+      }
+    for (int32_t i = 0; i < T; i++) gno_activate_batch(GNO_ACT_SOFTMAX, L->scores + (int64_t)i * T, T);
+    for (int32_t i = 0; i < T; i++)
+      for (int32_t e = 0; e < hd; e++) {
+        float sum = 0.0f;
+        for (int32_t j = 0; j < T; j++) sum += L->scores[i * T + j] * L->av[j * d + h * hd + e];
+        L->fin[i * d + h * hd + e] = sum;
+      }
+  }
+  for (int32_t t = 0; t < T; t++)
+    memcpy(L->attOut + (int64_t)t * d, dense_forward(&L->sub[3], L->fin + (int64_t)t * d), sizeof(float) * d);
+  return L->attOut;
+}
+
+/* MultiHeadAttention.Backward transformer.go:557-690 */
+static const float *mha_backward(layer *L, const float *g) {
+  int32_t T = L->T, d = L->D, nh = L->NH, hd = d / nh;
+  float scale = (float)sqrt((double)hd);
+  for (int32_t t = 0; t < T; t++)
+    memcpy(L->gfin + (int64_t)t * d, dense_backward(&L->sub[3], g + (int64_t)t * d), sizeof(float) * d);
+  for (int64_t i = 0; i < (int64_t)T * d; i++) L->gq[i] = L->gk[i] = L->gv[i] = 0;
+  for (int32_t h = 0; h < nh; h++)
+    for (int32_t i = 0; i < T; i++) {
+      float *gradRow = L->tmpRow;
+      for (int32_t j = 0; j < T; j++) gradRow[j] = 0; /* make([]float32, seqLen) */
+      for (int32_t j = 0; j < T; j++) {
+        if (L->spec.causal && j > i) continue;
+        float dot = 0.0f;
+        for (int32_t e = 0; e < hd; e++) dot += L->gfin[i * d + h * hd + e] * L->av[j * d + h * hd + e];
+        gradRow[j] = dot;
+      }
+      float *row = L->probs;
+      for (int32_t j = 0; j < T; j++) {
+        if (L->spec.causal && j > i) row[j] = -1e9f;
+        else {
+          float dot = 0.0f;
+          for (int32_t e = 0; e < hd; e++) dot += L->aq[i * d + h * hd + e] * L->ak[j * d + h * hd + e];
+          row[j] = dot / scale;
+        }
+      }
+      gno_activate_batch(GNO_ACT_SOFTMAX, row, T);
+      for (int32_t j = 0; j < T; j++) {
+        float sum = 0.0f;
+        for (int32_t kk = 0; kk < T; kk++) {
+          float delta = (j == kk) ? 1.0f : 0.0f;
+          sum += gradRow[kk] * row[kk] * (delta - row[j]);
+        }
+        L->dpre[j] = sum;
+      }
+      for (int32_t j = 0; j < T; j++) {
+        if (L->spec.causal && j > i) continue;
+        float gs = L->dpre[j] / scale;
+        for (int32_t e = 0; e < hd; e++) {
+          L->gq[i * d + h * hd + e] += gs * L->ak[j * d + h * hd + e];
+          L->gk[j * d + h * hd + e] += gs * L->aq[i * d + h * hd + e];
+        }
+      }
+      for (int32_t j = 0; j < T; j++) {
+        float sc = row[j];
+        for (int32_t e = 0; e < hd; e++) L->gv[j * d + h * hd + e] += sc * L->gfin[i * d + h * hd + e];
+      }
+    }
+  for (int32_t t = 0; t < T; t++) {
+    const float *dq = dense_backward(&L->sub[0], L->gq + (int64_t)t * d);
+    float tq[4096], tk[4096];
+    memcpy(tq, dq, sizeof(float) * d);
+    const float *dk = dense_backward(&L->sub[1], L->gk + (int64_t)t * d);
+    memcpy(tk, dk, sizeof(float) * d);
+    const float *dv = dense_backward(&L->sub[2], L->gv + (int64_t)t * d);
+    for (int32_t i = 0; i < d; i++) L->gInAtt[(int64_t)t * d + i] = tq[i] + tk[i] + dv[i];
+  }
+  return L->gInAtt;
+}
+
+/* TransformerBlock.ForwardWithArena (arena-less) transformer.go:1080-1184 */
+static const float *tb_forward(layer *L, const float *x) {
+  int32_t T = L->T, d = L->D;
+  int64_t td = (int64_t)T * d;
+  const float *att = mha_forward(L, x);
+  for (int64_t i = 0; i < td; i++) L->res1[i] = x[i] + att[i];
+  memcpy(L->n1, ln_forward(&L->ln[0], L->res1), sizeof(float) * td);
+  for (int32_t s = 0; s < T; s++) {
+    const float *mid = dense_forward(&L->sub[4], L->n1 + (int64_t)s * d);
+    const float *fo = dense_forward(&L->sub[5], mid);
+    memcpy(L->ffOut + (int64_t)s * d, fo, sizeof(float) * d);
+  }
+  for (int64_t i = 0; i < td; i++) L->res2[i] = L->n1[i] + L->ffOut[i];
+  memcpy(L->blkOut, ln_forward(&L->ln[1], L->res2), sizeof(float) * td);
+  return L->blkOut;
+}
+
+/* TransformerBlock.Backward transformer.go:1220-1279 */
+static const float *tb_backward(layer *L, const float *g) {
+  int32_t T = L->T, d = L->D;
+  int64_t td = (int64_t)T * d;
+  memcpy(L->gRes2, ln_backward(&L->ln[1], g), sizeof(float) * td);
+  for (int32_t s = 0; s < T; s++) {
+    const float *mg = dense_backward(&L->sub[5], L->gRes2 + (int64_t)s * d);
+    const float *g1 = dense_backward(&L->sub[4], mg);
+    memcpy(L->gN1ff + (int64_t)s * d, g1, sizeof(float) * d);
+  }
+  for (int64_t i = 0; i < td; i++) L->comb[i] = L->gRes2[i] + L->gN1ff[i];
+  memcpy(L->gRes1, ln_backward(&L->ln[0], L->comb), sizeof(float) * td);
+  const float *ga = mha_backward(L, L->gRes1);
+  for (int64_t i = 0; i < td; i++) L->gInAtt[i] = L->gRes1[i] + ga[i];
+  return L->gInAtt;
+}
+
+static void tb_free(layer *L) {
+  if (!L->sub) return;
+  for (int i = 0; i < 6; i++) {
+    layer *S = &L->sub[i];
+    free(S->inputBuf); free(S->preActBuf); free(S->outputBuf); free(S->savedOutput);
+    free(S->gradInBuf); free(S->dzBuf);
+  }
+  free(L->sub);
+  ln_free(&L->ln[0]);
+  ln_free(&L->ln[1]);
+  free(L->ln);
+  float *bufs[] = {L->aq, L->ak, L->av, L->scores, L->fin, L->gfin, L->gq, L->gk, L->gv, L->attOut,
+                   L->res1, L->n1, L->ffOut, L->res2, L->blkOut, L->gRes2, L->gN1ff, L->comb,
+                   L->gRes1, L->gInAtt, L->tmpRow, L->probs, L->dpre};
+  for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) free(bufs[i]);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Generic layer dispatch                                                     */
 /* ------------------------------------------------------------------------ */
@@ -804,6 +1194,10 @@ static void layer_build(layer *L) {
       break;
     case GNO_LAYER_FLATTEN: break;
     case GNO_LAYER_LSTM_UNROLLER: lstm_build(L); break;
+    case GNO_LAYER_EMBEDDING: emb_build(L); break;
+    case GNO_LAYER_POSENC: pe_build(L); break;
+    case GNO_LAYER_CLSPOOL: cls_build(L); break;
+    case GNO_LAYER_TRANSFORMER: tb_build(L); break;
     default: break;
   }
 }
@@ -811,6 +1205,9 @@ static void layer_init_params(layer *L) {
   if (L->kind == GNO_LAYER_DENSE) dense_init_params(L);
   else if (L->kind == GNO_LAYER_CONV2D) conv_init_params(L);
   else if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_init_params(L);
+  else if (L->kind == GNO_LAYER_EMBEDDING) emb_init(L);
+  else if (L->kind == GNO_LAYER_POSENC) pe_init(L);
+  else if (L->kind == GNO_LAYER_TRANSFORMER) tb_init(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -827,6 +1224,10 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_MAXPOOL2D: o = maxpool_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_FLATTEN: o = x; L->in_len = L->out_len = *len_io; break; /* reshape.go:64-80 */
     case GNO_LAYER_LSTM_UNROLLER: o = unroller_forward(L, x); *len_io = L->H; break;
+    case GNO_LAYER_EMBEDDING: o = emb_forward(L, x); *len_io = L->out_len; break;
+    case GNO_LAYER_POSENC: o = pe_forward(L, x); break;
+    case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
+    case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
     default: o = x;
   }
   return o;
@@ -839,6 +1240,10 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_MAXPOOL2D: return maxpool_backward(L, g);
     case GNO_LAYER_FLATTEN: return g; /* reshape.go:83-86 */
     case GNO_LAYER_LSTM_UNROLLER: return unroller_backward(L, g);
+    case GNO_LAYER_EMBEDDING: return emb_backward(L, g);
+    case GNO_LAYER_POSENC: return pe_backward(L, g);
+    case GNO_LAYER_CLSPOOL: return cls_backward(L, g);
+    case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
     default: return g;
   }
 }
@@ -874,6 +1279,7 @@ gno_net *gno_net_create(const gno_layer_spec *specs, int32_t nlayers, int32_t lo
     layer *L = &n->layers[i];
     L->params = n->params + off;
     L->grads = n->grads + off;
+    if (L->kind == GNO_LAYER_TRANSFORMER) tb_bind(L);
     layer_init_params(L);
     off += L->nparams;
   }
@@ -892,6 +1298,8 @@ void gno_net_destroy(gno_net *n) {
                    L->lstmIn, L->savedC, L->savedH, L->savedPre, L->curGrad, L->dhNextU,
                    L->gradInU, L->outU};
     for (size_t k = 0; k < sizeof lb / sizeof lb[0]; k++) free(lb[k]);
+    free(L->ids);
+    if (L->kind == GNO_LAYER_TRANSFORMER) tb_free(L);
   }
   free(n->layers);
   free(n->params); free(n->grads); free(n->m); free(n->v); free(n->worker_grads); free(n->lossGrad);
@@ -920,6 +1328,7 @@ static int32_t in_len_of(const gno_net *n) {
     case GNO_LAYER_DENSE: return L->spec.in_size;
     case GNO_LAYER_DROPOUT: return L->spec.in_size;
     case GNO_LAYER_LSTM_UNROLLER: return L->T * L->spec.in_size;
+    case GNO_LAYER_EMBEDDING: return L->T;
     default: return L->spec.in_size;
   }
 }
@@ -928,6 +1337,7 @@ static void bind_grads(gno_net *n, float *buf) {
   int64_t off = 0;
   for (int32_t i = 0; i < n->nlayers; i++) {
     n->layers[i].grads = buf + off;
+    if (n->layers[i].kind == GNO_LAYER_TRANSFORMER) tb_bind(&n->layers[i]);
     off += n->layers[i].nparams;
   }
 }

@@ -21,6 +21,12 @@
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
+ *   Embedding                         internal/layer/embedding.go:42-183
+ *   PositionalEncoding                internal/layer/transformer.go:51-120
+ *   MultiHeadAttention                internal/layer/transformer.go:318-690
+ *   TransformerBlock                  internal/layer/transformer.go:908-1279
+ *   LayerNorm                         internal/layer/layernorm.go:83-441
+ *   CLSPooling                        internal/layer/transformer.go:1679-1725
  *   RNG                               internal/layer/layer.go:61-81
  * Built with -O2 -ffp-contract=off (Go amd64 GOAMD64=v1 emits no FMA).
  */

@@ -23,6 +23,16 @@ def oracle_specs(refcpu, cfg):
         elif k == "maxpool2d":
             specs.append(refcpu.spec(refcpu.LAYER_MAXPOOL2D, in_channels=d["inC"], kernel=d["k"],
                                      stride=d["s"], padding=d["p"]))
+        elif k == "embedding":
+            specs.append(refcpu.spec(refcpu.LAYER_EMBEDDING, in_size=cfg["in_len"], vocab=d["vocab"],
+                                     dim=d["dim"]))
+        elif k == "posenc":
+            specs.append(refcpu.spec(refcpu.LAYER_POSENC, seq_len=d["T"], dim=d["dim"]))
+        elif k == "transformer":
+            specs.append(refcpu.spec(refcpu.LAYER_TRANSFORMER, dim=d["dim"], num_heads=d["heads"],
+                                     seq_len=d["T"], ff_dim=d["ff"], causal=int(d["causal"])))
+        elif k == "clspool":
+            specs.append(refcpu.spec(refcpu.LAYER_CLSPOOL, seq_len=d["T"], dim=d["dim"]))
         elif k == "lstm":
             specs.append(refcpu.spec(refcpu.LAYER_LSTM_UNROLLER, in_size=d["in"], out_size=d["hidden"],
                                      seq_len=d["T"]))

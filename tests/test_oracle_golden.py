@@ -476,3 +476,217 @@ def test_clip_gram_restatement_matches_sequential():
         if nrm > 1:
             G *= np.float32(1) / nrm
     np.testing.assert_allclose(_lstm_clip_gram(deltas), G, rtol=1e-5, atol=1e-7)
+
+
+# ---------------------------------------------------------------- GPT (C4 semantics)
+def _gpt_small(B=3, T=6, V=11, D=8, NH=2, FF=12):
+    from goneuron_amd import configs
+    return configs.gpt(B=B, T=T, vocab=V, dim=D, heads=NH, ff=FF)
+
+
+def _block_slices(D, FF):
+    nd = D * D + D
+    off = 0
+    out = {}
+    for name in ("wq", "wk", "wv", "wo"):
+        out[name] = (off, off + D * D, off + nd)
+        off += nd
+    for name in ("ln1", "ln2"):
+        out[name] = (off, off + D, off + 2 * D)
+        off += 2 * D
+    out["ff1"] = (off, off + FF * D, off + FF * D + FF)
+    off += FF * D + FF
+    out["ff2"] = (off, off + D * FF, off + D * FF + D)
+    off += D * FF + D
+    return out, off
+
+
+def test_gpt_init_closed_form(oracle):
+    from cfgutil import oracle_net
+    cfg = _gpt_small()
+    net = oracle_net(oracle, cfg)
+    V, D, T = 11, 8, 6
+    p = net.params
+    s = 42
+    sc = np.float32(math.sqrt(3.0 / D))
+    exp = []
+    for _ in range(V * D):
+        s = (s * 6364136223846793005 + 1) % (1 << 64)
+        u = np.float32(s >> 33) / np.float32(2 ** 31)
+        exp.append(sc * (np.float32(np.float32(2) * u) - np.float32(1)))
+    np.testing.assert_array_equal(p[:V * D], np.array(exp, np.float32))
+    # Q11: every TransformerBlock parameter is zero after Build
+    blk = net.layer_slice(2)
+    assert not p[blk].any()
+
+
+def test_gpt_reference_init_step_structure(oracle):
+    """With the reference's zero block, the block output is LN2's beta (= 0 at
+    step 1) for every token: only the head bias and LN2 beta receive gradient."""
+    from cfgutil import oracle_net
+    from goneuron_amd import configs
+    cfg = _gpt_small()
+    net = oracle_net(oracle, cfg)
+    x, y = configs.inputs(cfg)
+    net.accumulate_batch(x, y, cfg["B"])
+    g = net.grads
+    D, FF, V = 8, 12, 11
+    sl, nb = _block_slices(D, FF)
+    blk0 = net.layer_slice(2).start
+    ln2b = slice(blk0 + sl["ln2"][1], blk0 + sl["ln2"][2])
+    head = net.layer_slice(4)
+    head_b = slice(head.start + D * V, head.stop)
+    nz = np.zeros_like(g, bool)
+    nz[ln2b] = True
+    nz[head_b] = True
+    assert not g[~nz].any()
+    assert np.abs(g[ln2b]).max() > 0 and np.abs(g[head_b]).max() > 0
+
+
+def _torch_gpt_grads(torch, cfg, p0, x, y):
+    """float64 torch model of the reference GPT step; autograd provides the
+    attention / softmax / LayerNorm / residual gradients, custom functions the
+    per-token quirks."""
+    B, T = x.shape
+    V, D = cfg["classes"], cfg["layers"][0]["dim"]
+    NH, FF = cfg["layers"][2]["heads"], cfg["layers"][2]["ff"]
+    hd = D // NH
+
+    class PTDense(torch.autograd.Function):   # Q10: dW from the last token's input
+        @staticmethod
+        def forward(ctx, xx, W, b):
+            ctx.save_for_backward(xx, W)
+            return xx @ W.T + b
+
+        @staticmethod
+        def backward(ctx, g):
+            xx, W = ctx.saved_tensors
+            s = g.sum(0)
+            return g @ W, s[:, None] * xx[-1][None, :], s
+
+    class QReLU(torch.autograd.Function):     # Q10: the last token's ReLU mask
+        @staticmethod
+        def forward(ctx, z):
+            ctx.save_for_backward(z)
+            return torch.relu(z)
+
+        @staticmethod
+        def backward(ctx, g):
+            (z,) = ctx.saved_tensors
+            return g * (z[-1] > 0).to(g.dtype)
+
+    class QLayerNorm(torch.autograd.Function):
+        """Q18: LayerNorm.Backward (layernorm.go:411-423) computes
+        dx = (gp - mean(gp))/std - (x-mu) * sum(gp*(x-mu)) / (N*std^2):
+        the exact gradient has N*std^3 in the last term."""
+        @staticmethod
+        def forward(ctx, xx, gam, bet):
+            mu = xx.mean(1, keepdim=True)
+            var = ((xx - mu) ** 2).mean(1, keepdim=True)
+            std = torch.sqrt(var + 1e-5)
+            ctx.save_for_backward(xx, mu, std, gam)
+            return gam * (xx - mu) / std + bet
+
+        @staticmethod
+        def backward(ctx, g):
+            xx, mu, std, gam = ctx.saved_tensors
+            N = xx.shape[1]
+            gp = g * gam
+            diff = xx - mu
+            dx = (gp - gp.sum(1, keepdim=True) / N) / std - diff * (gp * diff).sum(1, keepdim=True) / (N * std * std)
+            return dx, (g * diff / std).sum(0), g.sum(0)
+
+    P = torch.tensor(p0.astype(np.float64), requires_grad=True)
+    nE, nP = V * D, T * D
+    E = P[:nE].view(V, D)
+    PE = P[nE:nE + nP].view(T, D)
+    sl, nb = _block_slices(D, FF)
+    b0 = nE + nP
+
+    def W(name, rows, cols):
+        a, bsplit, c = sl[name]
+        return P[b0 + a:b0 + bsplit].view(rows, cols), P[b0 + bsplit:b0 + c]
+    Wq, bq = W("wq", D, D)
+    Wk, bk = W("wk", D, D)
+    Wv, bv = W("wv", D, D)
+    Wo, bo = W("wo", D, D)
+    g1, be1 = W("ln1", 1, D)
+    g2, be2 = W("ln2", 1, D)
+    W1, c1 = W("ff1", FF, D)
+    W2, c2 = W("ff2", D, FF)
+    h0 = b0 + nb
+    Wh = P[h0:h0 + V * D].view(V, D)
+    bh = P[h0 + V * D:h0 + V * D + V]
+    mask = torch.triu(torch.ones(T, T, dtype=torch.bool), 1)
+    emb_grad_rows = None
+    for b in range(B):
+        ids = x[b].astype(np.int64)
+        e = E[ids]
+        e_leaf = e.detach().requires_grad_(True)
+        h = e_leaf + PE
+        q, k, v = PTDense.apply(h, Wq, bq), PTDense.apply(h, Wk, bk), PTDense.apply(h, Wv, bv)
+        outs = []
+        for hh in range(NH):
+            sl_ = slice(hh * hd, (hh + 1) * hd)
+            s_ = (q[:, sl_] @ k[:, sl_].T) / math.sqrt(hd)
+            s_ = s_.masked_fill(mask, -1e9)
+            outs.append(torch.softmax(s_, dim=1) @ v[:, sl_])
+        att = PTDense.apply(torch.cat(outs, 1), Wo, bo)
+        n1 = QLayerNorm.apply(h + att, g1.view(D), be1)
+        mid = QReLU.apply(PTDense.apply(n1, W1, c1))
+        ff = PTDense.apply(mid, W2, c2)
+        out = QLayerNorm.apply(n1 + ff, g2.view(D), be2)
+        logits = out[0] @ Wh.T + bh
+        lp = torch.log_softmax(logits, 0)
+        lp.backward((lp - torch.tensor(y[b].astype(np.float64))).detach() / B)
+        if b == B - 1:                         # Q12: only the last sample's scatter survives
+            emb_grad_rows = (ids, e_leaf.grad.clone())
+    G = P.grad.clone().numpy()
+    G[:nE] = 0
+    ids, ge = emb_grad_rows
+    Ge = np.zeros((V, D))
+    for t in range(T):
+        Ge[ids[t]] += ge[t].numpy() / 1.0
+    G[:nE] = Ge.ravel()
+    return G
+
+
+def test_layernorm_quirk_formula_vs_exact():
+    """Q18 pinned against autograd: the reference's LayerNorm dx equals the
+    exact gradient with its variance term multiplied by std."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(13)
+    x = torch.tensor(rng.normal(size=(5, 7)) * 3, requires_grad=True)
+    gam = torch.tensor(rng.normal(size=7))
+    g = torch.tensor(rng.normal(size=(5, 7)))
+    y = torch.nn.functional.layer_norm(x, (7,), gam, None, 1e-5)
+    y.backward(g)
+    mu = x.detach().mean(1, keepdim=True)
+    diff = x.detach() - mu
+    std = torch.sqrt((diff ** 2).mean(1, keepdim=True) + 1e-5)
+    gp = g * gam
+    term = diff * (gp * diff).sum(1, keepdim=True) / (7 * std ** 3)
+    ref_formula = (gp - gp.mean(1, keepdim=True)) / std - term * std
+    exact = (gp - gp.mean(1, keepdim=True)) / std - term
+    np.testing.assert_allclose(x.grad.numpy(), exact.numpy(), rtol=1e-10, atol=1e-12)
+    assert not np.allclose(ref_formula.numpy(), exact.numpy())
+
+
+def test_gpt_grads_vs_torch_autograd(oracle):
+    torch = pytest.importorskip("torch")
+    from cfgutil import oracle_net, max_rel
+    from goneuron_amd import configs
+    cfg = _gpt_small()
+    net = oracle_net(oracle, cfg)
+    rng = np.random.default_rng(12)
+    blk = net.layer_slice(2)
+    net.params[blk] = (rng.normal(size=blk.stop - blk.start) * 0.4).astype(np.float32)
+    x, y = configs.inputs(cfg)
+    p0 = net.params.copy()
+    net.accumulate_batch(x, y, cfg["B"])
+    ref = _torch_gpt_grads(torch, cfg, p0, x, y)
+    got = net.grads
+    for i in range(5):
+        s = net.layer_slice(i)
+        if s.stop > s.start:
+            assert max_rel(got[s], ref[s]) < 1e-5, (i, max_rel(got[s], ref[s]))
