@@ -47,9 +47,14 @@ struct GemmArgs {
   int act;            // FwdKind or DerivKind
   float *ws;          // split-K workspace (may be null: no split)
   size_t ws_cap;      // floats
+  int aux_div;        // EPI_DACT: > 1 reads aux row (row/aux_div)*aux_div + aux_div-1
 };
 
-enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2 };
+// EPI_SCALE    C = alpha*acc
+// EPI_BIAS_ACT C = act(acc + bias[col])
+// EPI_DACT     C = acc * act'(aux[r', col])  (r' = row, or the last row of its group)
+// EPI_BIAS_ADD C = alpha*acc + bias[col] + aux[row, col]  (aux may alias C)
+enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2, EPI_BIAS_ADD = 4 };
 
 // op(A) layout: 'N' = A[m*lda+k] (K contiguous), 'T' = A[k*lda+m].
 // op(B) layout: 'N' = B[k*ldb+n] (N contiguous), 'T' = B[n*ldb+k].
@@ -118,5 +123,25 @@ hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const flo
                                     hipStream_t s);
 hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, int H,
                               hipStream_t s);
+
+// ---- Transformer path ----
+hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int rows, int V,
+                        int D, int *err, hipStream_t s);
+hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int TD, hipStream_t s);
+hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
+                             int D, int W, float scale, hipStream_t s);
+hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
+hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipStream_t s);
+hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s);
+hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
+                         int rows, int N, hipStream_t s);
+hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
+                         float *dx, float *gx, int rows, int N, hipStream_t s);
+bool attn_supported(int T, int D, int NH);
+hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *P, float *O, int B,
+                           int T, int D, int NH, int causal, hipStream_t s);
+hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *P,
+                           const float *GO, float *GQ, float *GK, float *GV, int B, int T, int D,
+                           int NH, int causal, hipStream_t s);
 
 }  // namespace gn

@@ -467,6 +467,14 @@ struct LayerRT {
   float *pre_i = nullptr, *cbuf = nullptr, *hbuf = nullptr;
   float *Dg = nullptr, *S = nullptr, *wts = nullptr;
   double *gram = nullptr, *coef = nullptr;
+  // Embedding / PositionalEncoding / TransformerBlock / CLSPooling
+  int V = 0, D = 0, NH = 0, FF = 0, causal = 0;
+  int32_t *ids = nullptr;
+  int *err = nullptr;
+  struct Tb {
+    float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *P, *st1, *st2;
+    float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
+  } tb{};
 };
 
 struct gn_model {
@@ -545,6 +553,41 @@ static void init_lstm(float *p, int in, int H) {  // LSTM.Build lstm.go:175-196
     for (int j = 0; j < in; ++j) wx[(int64_t)i * in + j] = lcg_float(s) * 2 * sin_ - sin_;
     for (int j = 0; j < H; ++j) wh[(int64_t)i * H + j] = lcg_float(s) * 2 * srec - srec;
   }
+}
+
+static void init_embedding(float *p, int V, int D) {  // NewEmbedding embedding.go:51-57
+  const float scale = (float)sqrt(3.0 / (double)D);
+  uint64_t s = 42;
+  for (int64_t i = 0; i < (int64_t)V * D; ++i) p[i] = scale * (2 * lcg_float(s) - 1);
+}
+
+static void init_posenc(float *p, int T, int D) {  // PositionalEncoding.Build transformer.go:50-66
+  uint64_t s = (uint64_t)(T + D + 42);
+  const float scale = (float)sqrt(1.0 / (double)D);
+  for (int64_t i = 0; i < (int64_t)T * D; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
+}
+
+// TransformerBlock flat layout (transformer.go:1035-1056): wQ, wK, wV, wOut
+// (W [D][D] then b [D]), norm1 (gamma, beta), norm2, ff1 (W [FF][D], b),
+// ff2 (W [D][FF], b).  Build rebinds every sub-layer to fresh zero slices, so
+// the reference starts the block at all-zero parameters.
+struct TbOff {
+  int64_t wq, bq, wk, bk, wv, bv, wo, bo, g1, be1, g2, be2, w1, b1, w2, b2, total;
+};
+static TbOff tb_offsets(int D, int FF) {
+  TbOff o{};
+  int64_t off = 0;
+  const int64_t dd = (int64_t)D * D;
+  o.wq = off; o.bq = off + dd; off += dd + D;
+  o.wk = off; o.bk = off + dd; off += dd + D;
+  o.wv = off; o.bv = off + dd; off += dd + D;
+  o.wo = off; o.bo = off + dd; off += dd + D;
+  o.g1 = off; o.be1 = off + D; off += 2 * D;
+  o.g2 = off; o.be2 = off + D; off += 2 * D;
+  o.w1 = off; o.b1 = off + (int64_t)FF * D; off += (int64_t)FF * D + FF;
+  o.w2 = off; o.b2 = off + (int64_t)D * FF; off += (int64_t)D * FF + D;
+  o.total = off;
+  return o;
 }
 
 // Square-first dimension inference of Conv2D / MaxPool2D forward
@@ -643,6 +686,43 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.out_len = ps.C * ps.oH * ps.oW;
         break;
       }
+      case GN_LAYER_EMBEDDING:
+        R.V = R.d.vocab;
+        R.D = R.d.dim;
+        R.T = len;  // tokens per sample
+        if (R.V <= 0 || R.D <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: bad Embedding", i);
+        if (i != 0) return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: Embedding only as the first layer", i);
+        R.pcount = (int64_t)R.V * R.D;
+        R.out_len = R.T * R.D;
+        break;
+      case GN_LAYER_POSENC:
+        R.T = R.d.seq_len;
+        R.D = R.d.dim > 0 ? R.d.dim : (R.T > 0 ? len / R.T : 0);
+        if (R.T <= 0 || R.D <= 0 || R.T * R.D != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: PositionalEncoding %dx%d != input %d", i, R.T, R.D, len);
+        R.pcount = (int64_t)R.T * R.D;
+        R.out_len = len;
+        break;
+      case GN_LAYER_TRANSFORMER:
+        R.T = R.d.seq_len;
+        R.D = R.d.dim;
+        R.NH = R.d.num_heads;
+        R.FF = R.d.ff_dim;
+        R.causal = R.d.causal;
+        if (R.T <= 0 || R.D <= 0 || R.FF <= 0 || R.T * R.D != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: TransformerBlock %dx%d != input %d", i, R.T, R.D, len);
+        if (!attn_supported(R.T, R.D, R.NH))
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: attention needs T <= 128, D/heads <= 32", i);
+        R.pcount = tb_offsets(R.D, R.FF).total;
+        R.out_len = len;
+        break;
+      case GN_LAYER_CLSPOOL:
+        R.T = R.d.seq_len;
+        R.D = R.d.dim;
+        if (R.T <= 0 || R.D <= 0 || R.T * R.D != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: CLSPooling %dx%d != input %d", i, R.T, R.D, len);
+        R.out_len = R.D;
+        break;
       case GN_LAYER_LSTM_UNROLLER: {
         R.T = R.d.seq_len;
         R.I = R.d.in_size;
@@ -688,6 +768,31 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     maxw = std::max(maxw, std::max(R.in_len, R.out_len));
     if (R.d.kind == GN_LAYER_DENSE) init_dense(host.data() + R.poff, R.d.in_size, R.d.out_size);
     if (R.d.kind == GN_LAYER_CONV2D) init_conv(host.data() + R.poff, R.cs.inC, R.cs.outC, R.cs.k);
+    if (R.d.kind == GN_LAYER_EMBEDDING) {
+      init_embedding(host.data() + R.poff, R.V, R.D);
+      float *tmp = nullptr;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.T, &tmp))) return rc;
+      R.ids = reinterpret_cast<int32_t *>(tmp);
+      if ((rc = model_alloc(M.get(), 64, &tmp))) return rc;
+      R.err = reinterpret_cast<int *>(tmp);
+      HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
+    }
+    if (R.d.kind == GN_LAYER_POSENC) init_posenc(host.data() + R.poff, R.T, R.D);
+    if (R.d.kind == GN_LAYER_TRANSFORMER) {
+      // parameters stay 0 (Q11); activations and gradients of the block
+      const size_t rows = (size_t)max_batch * R.T, D = R.D, FF = R.FF;
+      LayerRT::Tb &t = R.tb;
+      float **dbufs[] = {&t.Q, &t.K, &t.V, &t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2,
+                         &t.GO, &t.GQ, &t.GK, &t.GV, &t.GX};
+      for (float **b : dbufs)
+        if ((rc = model_alloc(M.get(), rows * D, b))) return rc;
+      if ((rc = model_alloc(M.get(), rows * FF, &t.MID))) return rc;
+      if ((rc = model_alloc(M.get(), rows * FF, &t.DZ1))) return rc;
+      if ((rc = model_alloc(M.get(), rows * 2, &t.st1))) return rc;
+      if ((rc = model_alloc(M.get(), rows * 2, &t.st2))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.NH * R.T * R.T, &t.P))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
+    }
     if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
       init_lstm(host.data() + R.poff, R.I, R.H);
       const size_t Bm = max_batch, T = R.T, H = R.H;
@@ -721,7 +826,14 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       continue;
     }
     if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.out))) return rc;
-    if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.gout))) return rc;
+    if (R.d.kind == GN_LAYER_POSENC && i > 0) {
+      // PositionalEncoding.Backward returns its input gradient unchanged
+      // (transformer.go:112-118): share the buffer with the layer below
+      R.gout = M->L[i - 1].gout;
+      R.gout_alias = true;
+    } else if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.gout))) {
+      return rc;
+    }
     if (R.d.kind == GN_LAYER_DROPOUT) {
       // Q9: Dropout.Reset reseeds RNG(42) before every sample (dropout.go:399-401),
       // so one mask of the first `size` draws serves every sample and step.
@@ -817,6 +929,139 @@ extern "C" int gn_model_set_training(gn_model *M, int32_t t) {
   return GN_OK;
 }
 
+// ---------------------------------------------------------------------------
+// TransformerBlock (post-norm, transformer.go:1080-1279) over B samples.
+// ---------------------------------------------------------------------------
+static hipError_t gemm_nt(gn_ctx *c, const float *A, const float *Bw, const float *bias, float *C,
+                          int M, int N, int K, int epi, int act, const float *aux) {
+  GemmArgs a{};
+  a.M = M; a.N = N; a.K = K;
+  a.A = A; a.lda = K; a.B = Bw; a.ldb = K;
+  a.C = C; a.ldc = N; a.alpha = 1.f; a.bias = bias; a.act = act;
+  a.aux = aux; a.ldaux = N;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM);
+  return launch_gemm('N', 'T', epi, a, c->stream);
+}
+
+// C[M,N] = A[M,K] W[K,N] (+ epilogue)
+static hipError_t gemm_nn(gn_ctx *c, const float *A, const float *Wm, float *C, int M, int N, int K,
+                          int epi, int act, const float *aux, int aux_div) {
+  GemmArgs a{};
+  a.M = M; a.N = N; a.K = K;
+  a.A = A; a.lda = K; a.B = Wm; a.ldb = N;
+  a.C = C; a.ldc = N; a.alpha = 1.f; a.act = act;
+  a.aux = aux; a.ldaux = N; a.aux_div = aux_div;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM);
+  return launch_gemm('N', 'N', epi, a, c->stream);
+}
+
+// Q10 weight gradient of a per-token Dense: dW[M,N] = scale * S^T Xlast, with
+// S [B, M] the per-sample token sums of dz and Xlast the last token's input
+// row of every sample (row stride T*N).
+static hipError_t gemm_dw_last(gn_ctx *c, const float *S, const float *X, float *dW, int B, int T,
+                               int M, int N, float scale) {
+  GemmArgs a{};
+  a.M = M; a.N = N; a.K = B;
+  a.A = S; a.lda = M;
+  a.B = X + (int64_t)(T - 1) * N; a.ldb = T * N;
+  a.C = dW; a.ldc = N; a.alpha = scale;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM);
+  return launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
+}
+
+static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
+  gn_ctx *c = M->ctx;
+  const int D = R.D, FF = R.FF, rows = B * R.T;
+  const TbOff o = tb_offsets(D, FF);
+  const float *P = M->params + R.poff;
+  LayerRT::Tb &t = R.tb;
+  // per-token projections: Q/K/V = X W^T + b (Dense with Linear activation)
+  HIP_OK(c, gemm_nt(c, X, P + o.wq, P + o.bq, t.Q, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
+  HIP_OK(c, gemm_nt(c, X, P + o.wk, P + o.bk, t.K, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
+  HIP_OK(c, gemm_nt(c, X, P + o.wv, P + o.bv, t.V, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
+  {
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.P, t.O, B, R.T, D, R.NH, R.causal, c->stream));
+  }
+  // res1 = x + wOut(o): the residual add rides in the GEMM epilogue
+  HIP_OK(c, gemm_nt(c, t.O, P + o.wo, P + o.bo, t.RES1, rows, D, D, EPI_BIAS_ADD, 0, X));
+  {
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_ln_fwd(t.RES1, P + o.g1, P + o.be1, t.N1, t.st1, rows, D, c->stream));
+  }
+  HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, P + o.b1, t.MID, rows, FF, D, EPI_BIAS_ACT, F_RELU, nullptr));
+  HIP_OK(c, gemm_nt(c, t.MID, P + o.w2, P + o.b2, t.RES2, rows, D, FF, EPI_BIAS_ADD, 0, t.N1));
+  KTimer kt(c, GN_KCLASS_OTHER);
+  HIP_OK(c, launch_ln_fwd(t.RES2, P + o.g2, P + o.be2, R.out, t.st2, rows, D, c->stream));
+  return GN_OK;
+}
+
+static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int B, float scale) {
+  gn_ctx *c = M->ctx;
+  const int D = R.D, FF = R.FF, T = R.T, rows = B * T;
+  const TbOff o = tb_offsets(D, FF);
+  const float *P = M->params + R.poff;
+  float *G = M->grads + R.poff;
+  LayerRT::Tb &t = R.tb;
+  float *cs = c->scratch;
+  const size_t cap = c->scratch_floats;
+  {  // LayerNorm 2 (Q18 formula), dgamma / dbeta column sums
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_ln_bwd(R.gout, t.RES2, P + o.g2, t.st2, t.G1, t.GX, rows, D, c->stream));
+    HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g2, cs, cap, c->stream));
+    HIP_OK(c, launch_colsum(R.gout, rows, D, D, scale, G + o.be2, cs, cap, c->stream));
+    // ff2 (Linear): dz2 = dRES2
+    HIP_OK(c, launch_colsum(t.G1, rows, D, D, scale, G + o.b2, cs, cap, c->stream));
+    HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
+  }
+  HIP_OK(c, gemm_dw_last(c, t.S, t.MID, G + o.w2, B, T, D, FF, scale));
+  // ff1 (ReLU): dz1 = (dz2 W2) * relu'(last token's pre-activation)  (Q10)
+  HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, D_RELU, t.MID, T));
+  {
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_colsum(t.DZ1, rows, FF, FF, scale, G + o.b1, cs, cap, c->stream));
+    HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
+  }
+  HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
+  // combined = dRES2 + dz1 W1
+  HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
+  {  // LayerNorm 1
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_ln_bwd(t.COMB, t.RES1, P + o.g1, t.st1, t.G2, t.GX, rows, D, c->stream));
+    HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g1, cs, cap, c->stream));
+    HIP_OK(c, launch_colsum(t.COMB, rows, D, D, scale, G + o.be1, cs, cap, c->stream));
+    // wOut (Linear): dz = dRES1
+    HIP_OK(c, launch_colsum(t.G2, rows, D, D, scale, G + o.bo, cs, cap, c->stream));
+    HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
+  }
+  HIP_OK(c, gemm_dw_last(c, t.S, t.O, G + o.wo, B, T, D, D, scale));
+  HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
+  {
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.P, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
+                              c->stream));
+  }
+  const float *gs[3] = {t.GQ, t.GK, t.GV};
+  const int64_t wo[3] = {o.wq, o.wk, o.wv}, bo[3] = {o.bq, o.bk, o.bv};
+  for (int k = 0; k < 3; ++k) {
+    {
+      KTimer kt(c, GN_KCLASS_OTHER);
+      HIP_OK(c, launch_colsum(gs[k], rows, D, D, scale, G + bo[k], cs, cap, c->stream));
+      HIP_OK(c, launch_token_sum(gs[k], t.S, B, T, D, c->stream));
+    }
+    HIP_OK(c, gemm_dw_last(c, t.S, X, G + wo[k], B, T, D, D, scale));
+  }
+  if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
+    HIP_OK(c, gemm_nn(c, t.GQ, P + o.wq, gin, rows, D, D, EPI_BIAS_ADD, 0, t.G2, 0));
+    HIP_OK(c, gemm_nn(c, t.GK, P + o.wk, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
+    HIP_OK(c, gemm_nn(c, t.GV, P + o.wv, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
+  }
+  return GN_OK;
+}
+
 // Forward over B samples.  Returns the output pointer of the last layer.
 // `for_loss`: the output layer keeps pre-activations for the row kernel.
 static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
@@ -857,6 +1102,27 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_MAXPOOL2D: {
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
+        break;
+      }
+      case GN_LAYER_EMBEDDING: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B * R.T, R.V, R.D, R.err,
+                               c->stream));
+        break;
+      }
+      case GN_LAYER_POSENC: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_pe_add(cur, M->params + R.poff, R.out, B, R.T * R.D, c->stream));
+        break;
+      }
+      case GN_LAYER_CLSPOOL: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_cls_fwd(cur, R.out, B, R.T * R.D, R.D, c->stream));
+        break;
+      }
+      case GN_LAYER_TRANSFORMER: {
+        int r = tb_forward(M, R, cur, B);
+        if (r) return r;
         break;
       }
       case GN_LAYER_LSTM_UNROLLER: {
@@ -942,6 +1208,32 @@ static int model_backward(gn_model *M, const float *x, int B, float scale) {
         if (below && below->gout)
           HIP_OK(c, launch_conv_dgrad(R.gout, R.out, W, below->gout, R.cs, B, R.cderiv, c->stream));
         is_dz = false;
+        break;
+      }
+      case GN_LAYER_CLSPOOL:
+        if (below && below->gout) {  // transformer.go:1714-1723: row 0 gets g, the rest 0
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_cls_bwd(R.gout, below->gout, B, R.T * R.D, R.D, c->stream));
+        }
+        is_dz = false;
+        break;
+      case GN_LAYER_TRANSFORMER: {
+        int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale);
+        if (r) return r;
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_POSENC: {  // gradW += g (transformer.go:112-118), summed over samples
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_colsum(R.gout, B, R.T * R.D, R.T * R.D, scale, M->grads + R.poff,
+                                c->scratch, c->scratch_floats, c->stream));
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_EMBEDDING: {  // Q12: last sample of each worker chunk only
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
+                                    scale, c->stream));
         break;
       }
       case GN_LAYER_LSTM_UNROLLER: {
@@ -1033,6 +1325,21 @@ extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const flo
   return gn_model_step(M);
 }
 
+// Out-of-range embedding ids raised a device flag (embedding.go:126-128 errors
+// on them); report and clear it once the stream has drained.
+static int check_embed_err(gn_model *M) {
+  gn_ctx *c = M->ctx;
+  if (M->L.empty() || M->L[0].d.kind != GN_LAYER_EMBEDDING) return GN_OK;
+  int flag = 0;
+  HIP_OK(c, hipMemcpyAsync(&flag, M->L[0].err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  if (flag) {
+    HIP_OK(c, hipMemsetAsync(M->L[0].err, 0, sizeof(int), c->stream));
+    return set_err(c, GN_ERR_INDEX, "embedding index out of bounds [0, %d)", M->L[0].V);
+  }
+  return GN_OK;
+}
+
 extern "C" int gn_model_train_step(gn_model *M, const float *x, const float *y, int32_t B,
                                    float *loss_out) {
   if (!M) return GN_ERR_INVALID;
@@ -1049,7 +1356,7 @@ extern "C" int gn_model_train_step(gn_model *M, const float *x, const float *y, 
   if ((rc = gn_model_step(M))) return rc;
   if (loss_out) return gn_model_read_loss(M, loss_out);
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  return GN_OK;
+  return check_embed_err(M);
 }
 
 extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
@@ -1058,7 +1365,7 @@ extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
   ENTRY(c);
   HIP_OK(c, hipMemcpyAsync(loss, M->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  return GN_OK;
+  return check_embed_err(M);
 }
 
 extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *out) {

@@ -176,7 +176,10 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int &tm,
 __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, int row, int col) {
   if (epi == EPI_SCALE) return v * p.alpha;
   if (epi == EPI_BIAS_ACT) return apply_fwd(v + (p.bias ? p.bias[col] : 0.f), p.act);
-  return v * apply_deriv(p.aux[(size_t)row * p.ldaux + col], p.act);
+  if (epi == EPI_BIAS_ADD)
+    return v * p.alpha + (p.bias ? p.bias[col] : 0.f) + p.aux[(size_t)row * p.ldaux + col];
+  const int ar = p.aux_div > 1 ? (row / p.aux_div) * p.aux_div + p.aux_div - 1 : row;
+  return v * apply_deriv(p.aux[(size_t)ar * p.ldaux + col], p.act);
 }
 
 // EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
@@ -352,6 +355,7 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
     kchunk = a.K > 0 ? a.K : 1;
     if (epi == EPI_BIAS_ACT) return launch_e<EPI_BIAS_ACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
     if (epi == EPI_DACT) return launch_e<EPI_DACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+    if (epi == EPI_BIAS_ADD) return launch_e<EPI_BIAS_ADD>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
     return launch_e<EPI_SCALE>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
   }
   hipError_t e = launch_e<EPI_PARTIAL>(ta, tb, vec, a, tm, tn, splits, kchunk, s);

@@ -106,7 +106,9 @@ def test_adam_bit_exact(gn, dev, oracle):
 
 
 # ------------------------------------------------------------------ model parity vs oracle
-def _compare_step(gn, oracle, cfg, steps=1, workers=1):
+def _compare_step(gn, oracle, cfg, steps=1, workers=1, perturb=None):
+    """perturb(params) -> params: optional replacement of the initial weights,
+    loaded into both implementations (e.g. non-zero TransformerBlock weights)."""
     from goneuron_amd import configs
     log(f"model parity {cfg['name']} B={cfg['B']} steps={steps} W={workers}")
     x, y = configs.inputs(cfg)
@@ -114,6 +116,10 @@ def _compare_step(gn, oracle, cfg, steps=1, workers=1):
     model = configs.build(cfg, workers=workers)
     net = oracle_net(oracle, cfg, workers=workers)
     np.testing.assert_array_equal(model.Params(), net.params)  # LCG init is exact
+    if perturb is not None:
+        p = perturb(net.params.copy())
+        net.params[:] = p
+        model.SetParams(p)
     for s in range(steps):
         lg = model.TrainBatch(x, y)
         lo = net.accumulate_batch(x, y, B)
@@ -226,6 +232,57 @@ def test_lstm_small_unrolled_path(gn, oracle, workers):
     cfg = configs.lstm(B=7, T=9, inp=5, hidden=24)
     x, y = configs.inputs(cfg)
     _compare_step(gn, oracle, cfg, steps=3, workers=workers)
+
+
+def _random_block(cfg, scale=0.2, seed=21):
+    """Non-zero TransformerBlock weights (the reference starts it at 0, Q11),
+    so attention, LayerNorm and the FF path carry gradient."""
+    from goneuron_amd import configs
+    d = cfg["layers"][2]
+    D, FF, T, V = d["dim"], d["ff"], d["T"], cfg["classes"]
+    start = V * D + T * D
+    n = 4 * (D * D + D) + 4 * D + (FF * D + FF) + (D * FF + D)
+
+    def f(p):
+        rng = np.random.default_rng(seed)
+        p[start:start + n] = (rng.normal(size=n) * scale).astype(np.float32)
+        g1 = start + 4 * (D * D + D)
+        p[g1:g1 + D] += 1.0          # LayerNorm gammas around 1
+        p[g1 + 2 * D:g1 + 3 * D] += 1.0
+        return p
+    return f
+
+
+@pytest.mark.parametrize("workers", [1, 2])
+def test_gpt_small_random_block(gn, oracle, workers):
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=5, T=12, vocab=37, dim=32, heads=4, ff=48)
+    _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
+
+
+def test_gpt_small_reference_init(gn, oracle):
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=4, T=16, vocab=50, dim=32, heads=2, ff=40)
+    _compare_step(gn, oracle, cfg, steps=3)
+
+
+def test_gpt_full_config_random_block(gn, oracle):
+    """C4 at BASELINE size (Emb 8000x256, PE 128, block 256/8 heads/ff 1024
+    causal, CLS, Dense 256->8000 LogSoftmax, B=32) with a non-zero block."""
+    from goneuron_amd import configs
+    cfg = configs.gpt()
+    _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg, scale=0.05))
+
+
+def test_gpt_embedding_index_error(gn, oracle):
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=2, T=4, vocab=10, dim=8, heads=2, ff=8)
+    model = configs.build(cfg)
+    x, y = configs.inputs(cfg)
+    x[1, 2] = 10  # out of range
+    with pytest.raises(gn.GNError) as e:
+        model.TrainBatch(x, y)
+    assert e.value.code == -8
 
 
 # ------------------------------------------------------------------ full-size C3 vs torch fp32
