@@ -24,6 +24,12 @@ sys.path.insert(0, ROOT)
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBPS = 8000.0
 
+# HBM bytes per training step moved by the GEMM family, from rocprofv3 --pmc
+# FETCH_SIZE (x2.000) and WRITE_SIZE (x1.000) passes, each scaled by what the
+# counter reads for a 1 GiB device-to-device copy (bench.py --copy-probe 1024).
+# Keyed by workload; a changed GEMM kernel needs a new measurement.
+GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2947.4e6}
+
 
 def gemm_flops(cfg, B):
     """Algorithmic GEMM FLOPs of one step: forward 2*B*in*out per Dense,
@@ -36,7 +42,7 @@ def gemm_flops(cfg, B):
     return f
 
 
-def cpu_baseline(cfg, x, y, budget_s=15.0):
+def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1):
     """The CPU oracle (reference-semantics restatement, 1 thread) on a bounded
     sample: per-sample fwd+bwd of n samples plus one Adam pass over the arena,
     scaled to samples/s = n / (t_samples + t_adam * n / B)."""
@@ -44,7 +50,7 @@ def cpu_baseline(cfg, x, y, budget_s=15.0):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from cfgutil import oracle_net
     refcpu.build()
-    net = oracle_net(refcpu, cfg)
+    net = oracle_net(refcpu, cfg, workers=workers)
     B = cfg["B"]
     # calibrate with one sample, then fill the budget
     t0 = time.perf_counter()
@@ -64,6 +70,19 @@ def cpu_baseline(cfg, x, y, budget_s=15.0):
                       f"{net.n}-param arena ({ta:.3f} s) scaled by n/B"}
 
 
+def copy_probe(mib):
+    """A copy kernel of known size: reads and writes mib MiB per launch."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_per_launch": n * 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,11 +91,18 @@ def main():
     ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
+                         "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the data-parallel "
               "sharding across GPUs is a design (DESIGN.md), not built here.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     import ctypes as C
     import goneuron_amd as gn
@@ -87,7 +113,8 @@ def main():
     B = cfg["B"]
     dev = gn.GetDefaultDevice()
     x, y = configs.inputs(cfg)
-    model = configs.build(cfg, device=dev)
+    workers = configs.gpu_workers(B)
+    model = configs.build(cfg, device=dev, workers=workers)
 
     def dbuf(a):
         p = C.c_void_p()
@@ -100,13 +127,21 @@ def main():
     for _ in range(args.warmup):
         step()
     dev.sync()
+    # timed region: K steps, no instrumentation -> value
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.sync()
+    elapsed = time.perf_counter() - t0
+    # the same K steps again with a HIP event pair around every kernel launch
+    # on the library's stream -> per-class kernel time for the roofline
     check(dev.h, lib().gn_timing_enable(dev.h, 1))
     dev.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     dev.sync()
-    elapsed = time.perf_counter() - t0
+    elapsed_ev = time.perf_counter() - t0
     res = {}
     for cls, name in ((0, "gemm"), (1, "adam"), (2, "other")):
         n = C.c_int64()
@@ -141,13 +176,15 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (reference LCG, seeds 1000+cfg / 2000+cfg), reference LCG weight init",
-        "config": {"workload": cfg["name"], "batch": B,
+        "config": {"workload": cfg["name"], "batch": B, "workers": workers,
                    "layers": [d["kind"] + (f"{d['in']}->{d['out']}" if d["kind"] == "dense" else "")
                               for d in cfg["layers"]],
                    "loss": cfg["loss"], "optimizer": "Adam lr=1e-3"},
         "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": (gemm_tflops / PEAK_FP32_MFMA_TFLOPS) if gemm_tflops else None,
-                     "traffic": None, "kernel": "gemm_f32_mfma (all instantiations)",
+                     "traffic": (GEMM_TRAFFIC_BYTES_PER_STEP[cfg["name"]] * K / g_n
+                                 if cfg["name"] in GEMM_TRAFFIC_BYTES_PER_STEP and g_n else None),
+                     "kernel": "gemm_f32_mfma (all instantiations)",
                      "flops_per_launch": per_launch_flops,
                      "avg_launch_ms": g_ms / g_n if g_n else None},
         "kernels": {
@@ -157,11 +194,12 @@ def main():
                      "frac": adam_gbps / PEAK_HBM_GBPS if adam_gbps else None,
                      "bytes_per_launch": adam_bytes},
             "other": {"launches_per_step": res["other"][0] / K, "ms_per_step": res["other"][1] / K},
+            "instrumented_ms_per_step": elapsed_ev * 1e3 / K,
         },
         "loss": loss.value,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget)
+        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget, workers)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -119,7 +119,18 @@ def product_layers(cfg):
     return out
 
 
-def build(cfg, device=None, workers=1, max_batch=None):
+def gpu_workers(B):
+    """The worker count Network.TrainBatch gives a device of Type() == GPU:
+    trainBatchParallel for B >= 64 (net.go:425-433) with at most 4 workers
+    (net.go:594-604), trainBatchSequential (W = 1) below that."""
+    return min(4, B) if B >= 64 else 1
+
+
+def build(cfg, device=None, workers=None, max_batch=None):
+    """workers=None selects gpu_workers(cfg["B"]), the reference's own
+    semantics for a GPU device."""
+    if workers is None:
+        workers = gpu_workers(cfg["B"])
     m = NewSequential(*product_layers(cfg), device=device)
     m.Compile(Adam(cfg["lr"]), CrossEntropy if cfg["loss"] == "ce" else MSE,
               max_batch=max_batch or cfg["B"], workers=workers)

@@ -113,11 +113,12 @@ hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *g
 
 // ---- SequenceUnroller(LSTM) ----
 hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hipStream_t s);
-hipError_t launch_lstm_fwd(const float *x, const float *WxT, const float *WhT, const float *bias,
-                           float *pre_i, float *cbuf, float *hbuf, float *out, int B, int T, int I,
-                           int H, hipStream_t s);
-hipError_t launch_lstm_bwd(const float *gh, const float *pre_i, const float *cbuf, const float *Wh,
-                           const float *bias, float *D, int B, int T, int H, hipStream_t s);
+hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,
+                           float *tcb, float *cbuf, float *hbuf, float *out, int B, int T, int H,
+                           hipStream_t s);
+hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
+                           const float *Wh, const float *bias, float *D, int B, int T, int H,
+                           hipStream_t s);
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
                                     double *coef, float *w, int B, int T, int I, int H, int W,
                                     hipStream_t s);

@@ -463,8 +463,9 @@ struct LayerRT {
   int cfwd = 0, cderiv = 0;     // Conv2D scalar Activate / Derivative kinds
   // SequenceUnroller(LSTM): T steps of I inputs, H hidden
   int T = 0, I = 0, H = 0;
-  float *WxT = nullptr, *WhT = nullptr;          // transposed input-gate blocks
-  float *pre_i = nullptr, *cbuf = nullptr, *hbuf = nullptr;
+  float *WhT = nullptr;                          // transposed input-gate block of Wh
+  float *xw = nullptr;                           // x_t . Wx_i for every (sample, step)
+  float *igb = nullptr, *tcb = nullptr, *cbuf = nullptr, *hbuf = nullptr;
   float *Dg = nullptr, *S = nullptr, *wts = nullptr;
   double *gram = nullptr, *coef = nullptr;
   // Embedding / PositionalEncoding / TransformerBlock / CLSPooling
@@ -796,9 +797,10 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
       init_lstm(host.data() + R.poff, R.I, R.H);
       const size_t Bm = max_batch, T = R.T, H = R.H;
-      if ((rc = model_alloc(M.get(), (size_t)R.I * H, &R.WxT))) return rc;
       if ((rc = model_alloc(M.get(), H * H, &R.WhT))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * T * H, &R.pre_i))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * T * H, &R.xw))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * T * H, &R.igb))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * T * H, &R.tcb))) return rc;
       if ((rc = model_alloc(M.get(), Bm * T * H, &R.cbuf))) return rc;
       if ((rc = model_alloc(M.get(), Bm * (T + 1) * H, &R.hbuf))) return rc;
       if ((rc = model_alloc(M.get(), Bm * (T + 1) * 4 * H, &R.Dg))) return rc;
@@ -1129,12 +1131,20 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         const float *Wx = M->params + R.poff;
         const float *Wh = Wx + (int64_t)4 * R.H * R.I;
         const float *bias = Wh + (int64_t)4 * R.H * R.H;
+        {
+          KTimer kt(c, GN_KCLASS_GEMM);
+          GemmArgs g{};  // xw[b*T + t][i] = x[b, t, :] . Wx[i, :] (input-gate rows, Q13)
+          g.M = B * R.T; g.N = R.H; g.K = R.I;
+          g.A = cur; g.lda = R.I;
+          g.B = Wx; g.ldb = R.I;
+          g.C = R.xw; g.ldc = R.H; g.alpha = 1.0f;
+          g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+          HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
+        }
         KTimer kt(c, GN_KCLASS_OTHER);
-        // input-gate blocks only (Q13), transposed for coalesced per-unit reads
-        HIP_OK(c, launch_transpose(Wx, R.WxT, R.H, R.I, c->stream));
         HIP_OK(c, launch_transpose(Wh, R.WhT, R.H, R.H, c->stream));
-        HIP_OK(c, launch_lstm_fwd(cur, R.WxT, R.WhT, bias, R.pre_i, R.cbuf, R.hbuf, R.out, B, R.T,
-                                  R.I, R.H, c->stream));
+        HIP_OK(c, launch_lstm_fwd(R.xw, R.WhT, bias, R.igb, R.tcb, R.cbuf, R.hbuf, R.out, B, R.T,
+                                  R.H, c->stream));
         break;
       }
       default:
@@ -1244,7 +1254,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale) {
         float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
         {
           KTimer kt(c, GN_KCLASS_OTHER);
-          HIP_OK(c, launch_lstm_bwd(R.gout, R.pre_i, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
+          HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
           HIP_OK(c, launch_lstm_clip_weights(R.Dg, R.hbuf, in, R.gram, R.coef, R.wts, B, T, I, H,
                                              M->workers, c->stream));
           HIP_OK(c, launch_lstm_weight(R.Dg, R.wts, R.S, B, T, H, c->stream));

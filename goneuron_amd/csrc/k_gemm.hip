@@ -338,12 +338,13 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   vec = vec && (ak ? (a.K % 4 == 0) : (a.M % 4 == 0));
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
   const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-  // Split K when the tile grid cannot fill the 256 CUs, keeping >= 8 K tiles
-  // per split; partials go to the workspace and are summed in split order.
+  // Split K when the tile grid cannot fill the 256 CUs (down to one K stage
+  // per split: a lone 128x128 tile runs at 1/256 of the chip); partials go to
+  // the workspace and are summed in split order.
   int splits = 1;
   const int tiles = tm * tn;
-  if (tiles < 160 && a.K >= 16 * BK && a.ws) {
-    splits = std::min((256 + tiles - 1) / tiles, a.K / (8 * BK));
+  if (tiles < 160 && a.K >= 2 * BK && a.ws) {
+    splits = std::min((256 + tiles - 1) / tiles, a.K / BK);
     while (splits > 1 && (size_t)splits * a.M * a.N > a.ws_cap) --splits;
   }
   int kchunk = a.K;

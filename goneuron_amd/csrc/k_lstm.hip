@@ -45,88 +45,132 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *__restrict_
   }
 }
 
-// Forward over T steps, one workgroup per sample, thread i = hidden unit i.
-// WxT [I][H] and WhT [H][H] are the transposed input-gate blocks.
-// Saves pre_i [B][T][H], c [B][T][H], hbuf [B][T+1][H] (hbuf[b][0] = 0,
-// hbuf[b][t+1] = h_t) and writes h_{T-1} to out [B][H].
-__global__ void lstm_fwd_kernel(const float *__restrict__ x, const float *__restrict__ WxT,
-                                const float *__restrict__ WhT, const float *__restrict__ bias,
-                                float *__restrict__ pre_i, float *__restrict__ cbuf,
-                                float *__restrict__ hbuf, float *__restrict__ out, int T, int I,
-                                int H) {
+// s = sum_{j0 <= j < j1} W[j * stride] * v[j], with U loads issued together
+// (the weights come from L2 every step; batching them hides its latency).
+template <int U>
+__device__ __forceinline__ float dot_strided(const float *__restrict__ W, int stride,
+                                             const float *v, int j0, int j1) {
+  float s = 0.f;
+  int j = j0;
+  for (; j + U <= j1; j += U) {
+    float w[U];
+#pragma unroll
+    for (int e = 0; e < U; ++e) w[e] = W[(size_t)(j + e) * stride];
+#pragma unroll
+    for (int e = 0; e < U; ++e) s += w[e] * v[j + e];
+  }
+  for (; j < j1; ++j) s += W[(size_t)j * stride] * v[j];
+  return s;
+}
+
+// Forward over T steps, one workgroup per sample.  xw [B][T][H] holds the
+// input-gate x projections x_t . Wx_i (one GEMM before the recurrence), so a
+// step only needs Wh_i h_{t-1}: NQ threads per hidden unit (up to LSTM_Q)
+// split that dot product and add their partials through LDS.
+// WhT [H][H] is the transposed input-gate block of Wh.
+// Saves ig = sigmoid(pre_i), tc = tanh(c), c [B][T][H] and hbuf [B][T+1][H]
+// (hbuf[b][0] = 0, hbuf[b][t+1] = h_t), and writes h_{T-1} to out [B][H].
+constexpr int LSTM_Q = 4;
+
+__global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict__ xw,
+                                                        const float *__restrict__ WhT,
+                                                        const float *__restrict__ bias,
+                                                        float *__restrict__ igb,
+                                                        float *__restrict__ tcb,
+                                                        float *__restrict__ cbuf,
+                                                        float *__restrict__ hbuf,
+                                                        float *__restrict__ out, int T, int H,
+                                                        int HB, int NQ) {
   extern __shared__ float sm[];
-  float *hs = sm, *xs = sm + H;
-  const int b = blockIdx.x, i = threadIdx.x;
-  const bool act = i < H;
-  const float *xb = x + (size_t)b * T * I;
-  float bi = 0.f, fg = 0.f, gg = 0.f, og = 0.f;
-  if (act) {
+  float *hs = sm, *part = sm + H;  // part[NQ][HB]
+  const int b = blockIdx.x;
+  const int i = threadIdx.x % HB, q = threadIdx.x / HB;
+  const bool act = i < H, own = act && q == 0;
+  const int jh0 = (H * q) / NQ, jh1 = (H * (q + 1)) / NQ;
+  const float *xwb = xw + (size_t)b * T * H;
+  float bi = 0.f, fg = 0.f, gg = 0.f, og = 0.f, xwn = 0.f;
+  if (own) {
     hs[i] = 0.f;
     hbuf[(size_t)b * (T + 1) * H + i] = 0.f;
     bi = bias[i];
     fg = sigm(bias[H + i]);       // Q13: f, g, o pre-activations are the biases
     gg = tanh32(bias[2 * H + i]);
     og = sigm(bias[3 * H + i]);
+    xwn = xwb[i];
   }
+  __syncthreads();
   float c = 0.f, hnew = 0.f;
   for (int t = 0; t < T; ++t) {
-    for (int j = i; j < I; j += blockDim.x) xs[j] = xb[(size_t)t * I + j];
+    const float xwc = xwn;
+    if (own && t + 1 < T) xwn = xwb[(size_t)(t + 1) * H + i];  // next step's, in flight
+    if (act) part[q * HB + i] = dot_strided<32>(WhT + i, H, hs, jh0, jh1);
     __syncthreads();
-    if (act) {
-      float a = bi;
-      if (I >= 64) {  // lstmComputeInputGates: direct accumulation
-        for (int j = 0; j < I; ++j) a += WxT[(size_t)j * H + i] * xs[j];
-      } else {        // lstmComputeInputGatesUnrolled4x: sum, then add
-        float s = 0.f;
-        for (int j = 0; j < I; ++j) s += WxT[(size_t)j * H + i] * xs[j];
-        a += s;
-      }
-      for (int j = 0; j < H; ++j) a += WhT[(size_t)j * H + i] * hs[j];
+    if (own) {
+      float sh = 0.f;
+      for (int r = 0; r < NQ; ++r) sh += part[r * HB + i];
+      const float a = (bi + xwc) + sh;  // bias, then Wx x, then Wh h (lstm.go:1065-1101)
       const size_t o = ((size_t)b * T + t) * H + i;
-      pre_i[o] = a;
       const float ig = sigm(a);
       c = fg * c + ig * gg;
-      hnew = og * tanh32(c);
+      const float tc = tanh32(c);
+      hnew = og * tc;
+      igb[o] = ig;
+      tcb[o] = tc;
       cbuf[o] = c;
       hbuf[((size_t)b * (T + 1) + t + 1) * H + i] = hnew;
+      hs[i] = hnew;
     }
     __syncthreads();
-    if (act) hs[i] = hnew;
   }
-  if (act) out[(size_t)b * H + i] = hnew;
+  if (own) out[(size_t)b * H + i] = hnew;
 }
 
 // BPTT deltas, one workgroup per sample.  gh = dL/dh_{T-1} [B][H].
 // D [B][T+1][4H]: row t = (dI, dF, dC, dO) of step t; row T = 0 (padding that
-// lines D up with hbuf for the dWh GEMM).
-__global__ void lstm_bwd_kernel(const float *__restrict__ gh, const float *__restrict__ pre_i,
-                                const float *__restrict__ cbuf, const float *__restrict__ Wh,
-                                const float *__restrict__ bias, float *__restrict__ D, int T,
-                                int H) {
-  extern __shared__ float dG[];  // 4H
-  const int b = blockIdx.x, i = threadIdx.x;
-  const bool act = i < H;
+// lines D up with hbuf for the dWh GEMM).  dhPrev = Wh^T dG is split over
+// NQ threads per unit (a 1/NQ share of the 4H rows each) and summed in LDS;
+// the saved gate values of step t-1 are fetched while step t runs.
+__global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict__ gh,
+                                                        const float *__restrict__ igb,
+                                                        const float *__restrict__ tcb,
+                                                        const float *__restrict__ cbuf,
+                                                        const float *__restrict__ Wh,
+                                                        const float *__restrict__ bias,
+                                                        float *__restrict__ D, int T, int H,
+                                                        int HB, int NQ) {
+  extern __shared__ float dG[];  // 4H, then part[NQ][HB]
+  float *part = dG + 4 * H;
+  const int b = blockIdx.x;
+  const int i = threadIdx.x % HB, q = threadIdx.x / HB;
+  const bool act = i < H, own = act && q == 0;
   const int G4 = 4 * H;
+  const int k0 = (G4 * q) / NQ, k1 = (G4 * (q + 1)) / NQ;
   float *Db = D + (size_t)b * (T + 1) * G4;
-  for (int k = i; k < G4; k += blockDim.x) Db[(size_t)T * G4 + k] = 0.f;
-  float cur = act ? gh[(size_t)b * H + i] : 0.f, dcn = 0.f;
+  for (int k = threadIdx.x; k < G4; k += blockDim.x) Db[(size_t)T * G4 + k] = 0.f;
+  float cur = own ? gh[(size_t)b * H + i] : 0.f, dcn = 0.f;
   float fg = 0.f, gg = 0.f, og = 0.f, dfd = 0.f, dgd = 0.f, dod = 0.f;
-  if (act) {
+  float ign = 0.f, tcn = 0.f, cpn = 0.f;  // step t's saved values, fetched one step early
+  const size_t ob = (size_t)b * T * H + i;
+  if (own) {
     fg = sigm(bias[H + i]);
     gg = tanh32(bias[2 * H + i]);
     og = sigm(bias[3 * H + i]);
     dfd = fg * (1.0f - fg);   // Sigmoid.Derivative(pre_f) recomputes sigmoid(pre_f)
     dgd = 1.0f - gg * gg;     // Tanh.Derivative
     dod = og * (1.0f - og);
+    ign = igb[ob + (size_t)(T - 1) * H];
+    tcn = tcb[ob + (size_t)(T - 1) * H];
+    cpn = T > 1 ? cbuf[ob + (size_t)(T - 2) * H] : 0.f;
   }
   for (int t = T - 1; t >= 0; --t) {
-    if (act) {
-      const size_t o = ((size_t)b * T + t) * H + i;
-      const float ig = sigm(pre_i[o]);
+    if (own) {
+      const float ig = ign, tc = tcn, cp = cpn;
+      if (t > 0) {
+        ign = igb[ob + (size_t)(t - 1) * H];
+        tcn = tcb[ob + (size_t)(t - 1) * H];
+        cpn = t > 1 ? cbuf[ob + (size_t)(t - 2) * H] : 0.f;
+      }
       const float did = ig * (1.0f - ig);
-      const float ct = cbuf[o];
-      const float cp = t > 0 ? cbuf[o - H] : 0.f;
-      const float tc = tanh32(ct);
       const float dc = cur * og * (1 - tc * tc) + dcn;
       const float dI = dc * gg * did;
       const float dF = dc * cp * dfd;
@@ -144,12 +188,13 @@ __global__ void lstm_bwd_kernel(const float *__restrict__ gh, const float *__res
       row[3 * H + i] = dO;
     }
     __syncthreads();
-    if (act) {
-      float s = 0.f;  // dhPrev = Wh^T dG, gates then units in order
-      for (int k = 0; k < G4; ++k) s += Wh[(size_t)k * H + i] * dG[k];
+    if (act) part[q * HB + i] = dot_strided<32>(Wh + i, H, dG, k0, k1);
+    __syncthreads();
+    if (own) {
+      float s = 0.f;
+      for (int r = 0; r < NQ; ++r) s += part[r * HB + i];
       cur += s;
     }
-    __syncthreads();
   }
 }
 
@@ -166,15 +211,24 @@ struct ChainMap {
   }
 };
 
-// Lower-triangular Gram of one chain, Gm[ch][v][u] (u <= v), in double:
+// Gram of one chain in double, stored by columns: GT[ch][u][v] = <D_u, D_v>
+// for u <= v (so the clip's per-block products read consecutive v),
 // <D_u, D_v> = (dG_u . dG_v) * (x_u . x_v + h_u . h_v + 1).
-// Block = 16x16 entries, LDS tiles of 32 k.
+// One block = a 64x64 tile pair (tv >= tu); 4 waves of 32x32, each 2x2
+// v_mfma_f64_16x16x4_f64 tiles with one accumulator set for the dG segment and
+// one for the [x | hPrev] segments; the MFMA rows are u and its columns v, so
+// the stores run along v.  K is staged 16 at a time through LDS as doubles
+// ([k][row], so a lane's operand read is one 8-byte word).
+// f64 16x16x4 operand layout: A[m = l%16][k = l/16], B[k = l/16][n = l%16];
+// result element i of lane l is row 4*i + l/16, column l%16.
+typedef double d4v __attribute__((ext_vector_type(4)));
+
 __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict__ D,
                                                         const float *__restrict__ hbuf,
                                                         const float *__restrict__ x,
                                                         double *__restrict__ Gm, ChainMap cm,
                                                         int I, int H, int nmax) {
-  __shared__ float su[16][33], sv[16][33];
+  __shared__ double sv[16][64], su[16][64];
   const int ch = blockIdx.y;
   const int n = cm.len(ch);
   // tile (tv, tu) with tu <= tv from the linear block index
@@ -184,84 +238,199 @@ __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict_
     ++tv;
   }
   const int tu = lin;
-  const int ntile = (n + 15) / 16;
-  if (tv >= ntile) return;
-  const int r = threadIdx.x >> 4, s = threadIdx.x & 15;
-  const int v = tv * 16 + r, u = tu * 16 + s;
+  const int ntile = (n + 63) / 64;
+  if (tv >= ntile) return;  // whole block leaves before any barrier
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
   const int G4 = 4 * H;
-  double acc[3] = {0.0, 0.0, 0.0};
-  // segments: 0 = dG (4H), 1 = hPrev (H), 2 = x_last (I)
+  // staging: thread -> row rr (0..63) and a quarter kq of the 16 k
+  const int rr = tid >> 2, kq = (tid & 3) * 4;
+  const int iv = tv * 64 + rr, iu = tu * 64 + rr;
+  int bv = 0, tvv = 0, bu = 0, tuu = 0;
+  if (iv < n) cm.at(ch, iv, bv, tvv);
+  if (iu < n) cm.at(ch, iu, bu, tuu);
+  d4v acc[2][2][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[q][i][j] = d4v{0.0, 0.0, 0.0, 0.0};
   for (int seg = 0; seg < 3; ++seg) {
     const int K = seg == 0 ? G4 : (seg == 1 ? H : I);
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      // load 16 rows x 32 k for the v-rows and the u-rows
-      for (int e = threadIdx.x; e < 2 * 16 * 32; e += 256) {
-        const int which = e / 512, rr = (e / 32) % 16, kk = e % 32;
-        const int idx = (which ? tv : tu) * 16 + rr;
-        float val = 0.f;
-        if (idx < n && k0 + kk < K) {
-          int bb, tt;
-          cm.at(ch, idx, bb, tt);
-          if (seg == 0)
-            val = D[((size_t)bb * (cm.T + 1) + tt) * G4 + k0 + kk];
-          else if (seg == 1)
-            val = hbuf[((size_t)bb * (cm.T + 1) + tt) * H + k0 + kk];
-          else
-            val = x[((size_t)bb * cm.T + cm.T - 1) * I + k0 + kk];
-        }
-        if (which) sv[rr][kk] = val;
-        else su[rr][kk] = val;
+    const float *pv, *pu;
+    if (seg == 0) {
+      pv = D + ((size_t)bv * (cm.T + 1) + tvv) * G4;
+      pu = D + ((size_t)bu * (cm.T + 1) + tuu) * G4;
+    } else if (seg == 1) {
+      pv = hbuf + ((size_t)bv * (cm.T + 1) + tvv) * H;
+      pu = hbuf + ((size_t)bu * (cm.T + 1) + tuu) * H;
+    } else {
+      pv = x + ((size_t)bv * cm.T + cm.T - 1) * I;
+      pu = x + ((size_t)bu * cm.T + cm.T - 1) * I;
+    }
+    const int q = seg == 0 ? 0 : 1;
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      float fv[4], fu[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = k0 + kq + e;
+        fv[e] = (iv < n && k < K) ? pv[k] : 0.f;
+        fu[e] = (iu < n && k < K) ? pu[k] : 0.f;
       }
       __syncthreads();
-      double a = 0.0;
-#pragma unroll 8
-      for (int kk = 0; kk < 32; ++kk) a += (double)sv[r][kk] * (double)su[s][kk];
-      acc[seg] += a;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sv[kq + e][rr] = (double)fv[e];
+        su[kq + e][rr] = (double)fu[e];
+      }
       __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int k = kk * 4 + (lane >> 4);
+        double a[2], b[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) a[i] = su[k][wm * 32 + i * 16 + (lane & 15)];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) b[j] = sv[k][wn * 32 + j * 16 + (lane & 15)];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[q][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[q][i][j], 0, 0, 0);
+      }
     }
   }
-  if (v < n && u <= v && u < n)
-    Gm[(size_t)ch * nmax * nmax + (size_t)v * nmax + u] = acc[0] * (acc[2] + acc[1] + 1.0);
+  double *Gc = Gm + (size_t)ch * nmax * nmax;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = tu * 64 + wm * 32 + i * 16 + 4 * r + (lane >> 4);
+        const int v = tv * 64 + wn * 32 + j * 16 + (lane & 15);
+        if (v < n && u <= v) Gc[(size_t)u * nmax + v] = acc[0][i][j][r] * (acc[1][i][j][r] + 1.0);
+      }
 }
 
 // Sequential clip of one chain from its Gram matrix; one workgroup per chain.
-// w_u = P * a_u; at step v: N^2 = |G|^2 + 2 P sum_{u<v} a_u <D_u,D_v> + <D_v,D_v>,
-// c = N > 1 ? 1/N : 1 (clipGradients), P *= c, a_v = c / P, |G|^2 = c^2 N^2.
+// With a_u = 1/P_{u-1} (P_v = c_0 ... c_v) the clipped sum is G_v = P_v sum_{u<=v} a_u D_u,
+// and step v needs s_v = sum_{u<v} a_u <D_u,D_v>:
+//   N^2 = |G|^2 + 2 P s_v + <D_v,D_v>,  c = N > 1 ? 1/N : 1 (clipGradients),
+//   P *= c,  a_v = c / P,  |G|^2 = c^2 N^2.
+// Blocked by CLIP_BLK steps: the part of s_v from earlier blocks is a matrix-
+// vector product that all waves compute; the in-block recursion runs in wave 0
+// with lane r holding row r's running s and the block's Gram tile in LDS, so a
+// step costs a few lane reads and one fused update instead of a block-wide
+// reduction.  Whenever P falls below 1e-150 the coefficients are rescaled by P
+// (exact: everything is linear in the a's), in-block at once and for earlier
+// blocks at the end of the block.
+constexpr int CLIP_BLK = 64;
+constexpr int CLIP_UNR = 8;
+
+__device__ __forceinline__ double readlane_d(double x, int l) {
+  const int lo = __builtin_amdgcn_readlane(__double2loint(x), l);
+  const int hi = __builtin_amdgcn_readlane(__double2hiint(x), l);
+  return __hiloint2double(hi, lo);
+}
+
 __global__ __launch_bounds__(256) void lstm_clip_kernel(const double *__restrict__ Gm,
                                                         double *__restrict__ a,
                                                         float *__restrict__ w, ChainMap cm,
                                                         int nmax) {
-  __shared__ double red[4];
+  __shared__ double tile[CLIP_BLK][CLIP_BLK + 1];  // tile[u][r] = <D_{v0+u}, D_{v0+r}>, u <= r
+  __shared__ double sold[CLIP_BLK], part4[4][CLIP_BLK];
+  __shared__ double bcast[2];                       // P at the end, pending rescale factor
   const int ch = blockIdx.x;
   const int n = cm.len(ch);
-  const double *G = Gm + (size_t)ch * nmax * nmax;
+  const double *G = Gm + (size_t)ch * nmax * nmax;  // GT[u][v]
   double *ac = a + (size_t)ch * nmax;
-  double P = 1.0, nrm2 = 0.0;
-  for (int v = 0; v < n; ++v) {
-    const double *row = G + (size_t)v * nmax;
-    double s = 0.0;
-    for (int u = threadIdx.x; u < v; u += 256) s += ac[u] * row[u];
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  double P = 1.0, Q = 1.0, nrm2 = 0.0;  // wave 0 only; Q = 1/P
+  for (int v0 = 0; v0 < n; v0 += CLIP_BLK) {
+    const int nb = min(CLIP_BLK, n - v0);
     __syncthreads();
-    s = (red[0] + red[1]) + (red[2] + red[3]);
-    const double N2 = nrm2 + 2.0 * P * s + row[v];
-    const double N = sqrt(N2 > 0.0 ? N2 : 0.0);
-    const double c = N > 1.0 ? 1.0 / N : 1.0;
-    P *= c;
-    if (threadIdx.x == 0) ac[v] = c / P;
-    nrm2 = c * c * N2;
-    if (P < 1e-200) {  // fold P into the coefficients before it underflows
-      __syncthreads();
-      for (int u = threadIdx.x; u <= v; u += 256) ac[u] *= P;
-      P = 1.0;
+    // s from earlier blocks: sold[r] = sum_{u < v0} a_u GT[u][v0 + r]; thread
+    // (r, q) takes u = q mod 4 with CLIP_UNR loads in flight, then the four
+    // partials are added in LDS
+    {
+      const int r = lane, q = wv;
+      double s = 0.0;
+      if (r < nb) {
+        const double *col = G + v0 + r;
+        int u = q;
+        for (; u + 4 * (CLIP_UNR - 1) < v0; u += 4 * CLIP_UNR) {
+          double gv[CLIP_UNR], av[CLIP_UNR];
+#pragma unroll
+          for (int e = 0; e < CLIP_UNR; ++e) {
+            gv[e] = col[(size_t)(u + 4 * e) * nmax];
+            av[e] = ac[u + 4 * e];
+          }
+#pragma unroll
+          for (int e = 0; e < CLIP_UNR; ++e) s += av[e] * gv[e];
+        }
+        for (; u < v0; u += 4) s += ac[u] * col[(size_t)u * nmax];
+      }
+      part4[q][r] = s;
+    }
+    for (int e = threadIdx.x; e < CLIP_BLK * CLIP_BLK; e += 256) {
+      const int u = e / CLIP_BLK, r = e % CLIP_BLK;
+      tile[u][r] = (r < nb && u <= r) ? G[(size_t)(v0 + u) * nmax + v0 + r] : 0.0;
     }
     __syncthreads();
+    if (threadIdx.x < CLIP_BLK)
+      sold[threadIdx.x] = (part4[0][threadIdx.x] + part4[1][threadIdx.x]) +
+                          (part4[2][threadIdx.x] + part4[3][threadIdx.x]);
+    __syncthreads();
+    if (wv == 0) {
+      // Per step only the norm recursion is serial: a_j = 1/P_{j-1} = Q is
+      // known when the step starts, so the running-s update of the later rows
+      // overlaps it, and 1/N comes from a refined reciprocal square root.
+      double sl = lane < nb ? sold[lane] : 0.0;  // running s of row v0 + lane
+      double al = 0.0;                            // a_{v0 + lane} once known
+      double blkscale = 1.0;
+      for (int j = 0; j < nb; ++j) {
+        const double aj = Q;
+        const double sj = readlane_d(sl, j);
+        if (lane == j) al = aj;
+        if (lane > j) sl += aj * tile[j][lane];
+        const double N2 = nrm2 + 2.0 * P * sj + tile[j][j];
+        if (N2 > 1.0) {  // clipGradients: scale by 1/N
+          double y = __builtin_amdgcn_rsq(N2);
+          y = y * (1.5 - 0.5 * N2 * y * y);
+          y = y * (1.5 - 0.5 * N2 * y * y);
+          P *= y;
+          Q *= N2 * y;
+          nrm2 = y * y * N2;
+        } else {
+          nrm2 = N2 > 0.0 ? N2 : 0.0;
+        }
+        if (P < 1e-150) {  // fold P into every coefficient so far
+          sl *= P;
+          al *= P;
+          blkscale *= P;
+          Q *= P;
+          P = 1.0;
+        }
+      }
+      if (lane < nb) ac[v0 + lane] = al;
+      if (lane == 0) {
+        bcast[0] = P;
+        bcast[1] = blkscale;
+      }
+    }
+    __syncthreads();
+    const double bs = bcast[1];  // rescale owed by the earlier blocks' coefficients
+    if (bs != 1.0)
+      for (int u = threadIdx.x; u < v0; u += 256) ac[u] *= bs;
   }
+  __syncthreads();
+  const double Pf = n > 0 ? bcast[0] : 1.0;
   for (int u = threadIdx.x; u < n; u += 256) {
     int b, t;
     cm.at(ch, u, b, t);
-    w[(size_t)b * (cm.T + 1) + t] = (float)(P * ac[u]);
+    w[(size_t)b * (cm.T + 1) + t] = (float)(Pf * ac[u]);
   }
 }
 
@@ -290,22 +459,28 @@ hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hip
   return hipGetLastError();
 }
 
-static int lstm_block(int H) { return ((H + 63) / 64) * 64; }
+static int lstm_hb(int H) { return ((H + 63) / 64) * 64; }
+static int lstm_nq(int hb) { return std::max(1, std::min(LSTM_Q, 1024 / hb)); }
 
-hipError_t launch_lstm_fwd(const float *x, const float *WxT, const float *WhT, const float *bias,
-                           float *pre_i, float *cbuf, float *hbuf, float *out, int B, int T, int I,
-                           int H, hipStream_t s) {
-  const size_t shm = (size_t)(H + I) * sizeof(float);
-  hipLaunchKernelGGL(lstm_fwd_kernel, dim3(B), dim3(lstm_block(H)), shm, s, x, WxT, WhT, bias, pre_i,
-                     cbuf, hbuf, out, T, I, H);
+hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,
+                           float *tcb, float *cbuf, float *hbuf, float *out, int B, int T, int H,
+                           hipStream_t s) {
+  const int hb = lstm_hb(H), nq = lstm_nq(hb);
+  if (hb > 1024) return hipErrorInvalidValue;
+  const size_t shm = (size_t)(H + nq * hb) * sizeof(float);
+  hipLaunchKernelGGL(lstm_fwd_kernel, dim3(B), dim3(hb * nq), shm, s, xw, WhT, bias, igb, tcb, cbuf,
+                     hbuf, out, T, H, hb, nq);
   return hipGetLastError();
 }
 
-hipError_t launch_lstm_bwd(const float *gh, const float *pre_i, const float *cbuf, const float *Wh,
-                           const float *bias, float *D, int B, int T, int H, hipStream_t s) {
-  const size_t shm = (size_t)4 * H * sizeof(float);
-  hipLaunchKernelGGL(lstm_bwd_kernel, dim3(B), dim3(lstm_block(H)), shm, s, gh, pre_i, cbuf, Wh,
-                     bias, D, T, H);
+hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
+                           const float *Wh, const float *bias, float *D, int B, int T, int H,
+                           hipStream_t s) {
+  const int hb = lstm_hb(H), nq = lstm_nq(hb);
+  if (hb > 1024) return hipErrorInvalidValue;
+  const size_t shm = (size_t)(4 * H + nq * hb) * sizeof(float);
+  hipLaunchKernelGGL(lstm_bwd_kernel, dim3(B), dim3(hb * nq), shm, s, gh, igb, tcb, cbuf, Wh, bias,
+                     D, T, H, hb, nq);
   return hipGetLastError();
 }
 
@@ -316,7 +491,7 @@ hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const flo
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
   const int nmax = cm.chunk * T;
-  const int ntile = (nmax + 15) / 16;
+  const int ntile = (nmax + 63) / 64;
   dim3 g(ntile * (ntile + 1) / 2, nchains);
   hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
   hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(256), 0, s, gram, coef, w, cm, nmax);

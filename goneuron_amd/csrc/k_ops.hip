@@ -31,6 +31,12 @@ __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, flo
   p = p - efflr * mi / (__builtin_sqrtf(vi) + eps);
 }
 
+// Each thread handles ADAM_U float4 groups per iteration (spaced one block
+// apart, so every load instruction stays coalesced) and issues all 4*ADAM_U
+// loads before the arithmetic, which keeps enough bytes in flight per CU to
+// run near the HBM limit.
+constexpr int ADAM_U = 4;
+
 __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
                                                    const float *__restrict__ g,
                                                    float *__restrict__ m, float *__restrict__ v,
@@ -38,27 +44,40 @@ __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
                                                    float omb1, float omb2, float eps) {
   typedef float f4v __attribute__((ext_vector_type(4)));
   const int64_t n4 = n >> 2;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t stride = (int64_t)gridDim.x * TPB * ADAM_U;
   f4v *p4 = reinterpret_cast<f4v *>(p);
   const f4v *g4 = reinterpret_cast<const f4v *>(g);
   f4v *m4 = reinterpret_cast<f4v *>(m);
   f4v *v4 = reinterpret_cast<f4v *>(v);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    f4v pp = __builtin_nontemporal_load(p4 + i);
-    const f4v gg = __builtin_nontemporal_load(g4 + i);
-    f4v mm = __builtin_nontemporal_load(m4 + i);
-    f4v vv = __builtin_nontemporal_load(v4 + i);
+  for (int64_t i0 = (int64_t)blockIdx.x * TPB * ADAM_U + threadIdx.x; i0 < n4; i0 += stride) {
+    f4v pp[ADAM_U], gg[ADAM_U], mm[ADAM_U], vv[ADAM_U];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float pq = pp[q], mq = mm[q], vq = vv[q];
-      adam1(pq, gg[q], mq, vq, efflr, b1, b2, omb1, omb2, eps);
-      pp[q] = pq;
-      mm[q] = mq;
-      vv[q] = vq;
+    for (int u = 0; u < ADAM_U; ++u) {
+      const int64_t i = i0 + (int64_t)u * TPB;
+      if (i < n4) {
+        pp[u] = __builtin_nontemporal_load(p4 + i);
+        gg[u] = __builtin_nontemporal_load(g4 + i);
+        mm[u] = __builtin_nontemporal_load(m4 + i);
+        vv[u] = __builtin_nontemporal_load(v4 + i);
+      }
     }
-    __builtin_nontemporal_store(pp, p4 + i);
-    __builtin_nontemporal_store(mm, m4 + i);
-    __builtin_nontemporal_store(vv, v4 + i);
+#pragma unroll
+    for (int u = 0; u < ADAM_U; ++u) {
+      const int64_t i = i0 + (int64_t)u * TPB;
+      if (i < n4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float pq = pp[u][q], mq = mm[u][q], vq = vv[u][q];
+          adam1(pq, gg[u][q], mq, vq, efflr, b1, b2, omb1, omb2, eps);
+          pp[u][q] = pq;
+          mm[u][q] = mq;
+          vv[u][q] = vq;
+        }
+        __builtin_nontemporal_store(pp[u], p4 + i);
+        __builtin_nontemporal_store(mm[u], m4 + i);
+        __builtin_nontemporal_store(vv[u], v4 + i);
+      }
+    }
   }
   // scalar tail (n % 4 elements), handled by the first threads of block 0
   if (blockIdx.x == 0) {
@@ -71,8 +90,8 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
                        float b1, float b2, float omb1, float omb2, float eps, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const int64_t n4 = n >> 2;
-  int64_t blocks = (n4 + TPB - 1) / TPB;
-  if (blocks > 256 * 32) blocks = 256 * 32;
+  int64_t blocks = (n4 + TPB * ADAM_U - 1) / (TPB * ADAM_U);
+  if (blocks > 16384) blocks = 16384;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(adam_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
                      b1, b2, omb1, omb2, eps);
