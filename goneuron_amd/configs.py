@@ -44,12 +44,12 @@ def wide(width=4096, classes=1000, depth=4, B=1024):
                 classes=classes, layers=ls)
 
 
-def gpt(B=32, T=128, vocab=8000, dim=256, heads=8, ff=1024):
+def gpt(B=32, T=128, vocab=8000, dim=256, heads=8, ff=1024, causal=True):
     return dict(num=4, name="gpt", B=B, loss="ce", lr=1e-3, x="ids", in_len=T, classes=vocab,
                 layers=[{"kind": "embedding", "vocab": vocab, "dim": dim},
                         {"kind": "posenc", "T": T, "dim": dim},
                         {"kind": "transformer", "dim": dim, "heads": heads, "T": T, "ff": ff,
-                         "causal": True},
+                         "causal": causal},
                         {"kind": "clspool", "T": T, "dim": dim},
                         dense(dim, vocab, "logsoftmax", True)])
 

@@ -66,22 +66,38 @@ __global__ __launch_bounds__(256) void pe_add_kernel(const float *__restrict__ x
     out[e] = x[e] + pe[e % TD];
 }
 
-// grad[E] = 0, then for each worker chunk's last sample, in order: rows of its
-// tokens scatter-added in token order (one block: a deterministic sequence).
+// grad[E] = 0 (hipMemsetAsync before the launch), then the token rows of each
+// worker chunk's last sample are scatter-added in (chunk, token) order.  Block
+// l takes contributing row l: if l is the first row carrying its id it sums,
+// in order, every row with that id and writes the row of gradE; rows whose id
+// appeared earlier write nothing, so all writes are to distinct rows.
+constexpr int EG_MAXL = 2048;  // contributing rows held in LDS
+
+__device__ __forceinline__ int eg_sample(int l, int T, int chunk, int B) {
+  return min((l / T + 1) * chunk - 1, B - 1);
+}
+
 __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict__ g,
                                                          const int32_t *__restrict__ ids,
                                                          float *__restrict__ gradE, int B, int T,
-                                                         int D, int W, float scale) {
-  const int Wc = W < 1 ? 1 : (W > B ? B : W);
-  const int chunk = (B + Wc - 1) / Wc;
-  for (int s = chunk - 1; s < B + chunk - 1; s += chunk) {
-    const int b = min(s, B - 1);
-    for (int t = 0; t < T; ++t) {
-      const int idx = ids[(int64_t)b * T + t];
-      for (int d = threadIdx.x; d < D; d += 256)  // thread d owns column d: ordered adds
-        gradE[(int64_t)idx * D + d] += g[((int64_t)b * T + t) * D + d] * scale;
-    }
-    if (s >= B - 1) break;
+                                                         int D, int chunk, int L, float scale) {
+  __shared__ int sid[EG_MAXL];
+  __shared__ int first;
+  const int l = blockIdx.x;
+  for (int e = threadIdx.x; e < L; e += 256)
+    sid[e] = ids[(int64_t)eg_sample(e, T, chunk, B) * T + e % T];
+  if (threadIdx.x == 0) first = 1;
+  __syncthreads();
+  const int my = sid[l];
+  for (int e = threadIdx.x; e < l; e += 256)
+    if (sid[e] == my) first = 0;  // benign race: every writer stores 0
+  __syncthreads();
+  if (!first) return;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    for (int e = l; e < L; ++e)
+      if (sid[e] == my) acc += g[((int64_t)eg_sample(e, T, chunk, B) * T + e % T) * D + d];
+    gradE[(int64_t)my * D + d] = acc * scale;
   }
 }
 
@@ -104,17 +120,21 @@ __global__ __launch_bounds__(256) void cls_bwd_kernel(const float *__restrict__ 
 }
 
 // S[b, :] = sum_t X[b, t, :]   (per-sample token sums for the Q10 dW outer products)
+// Block = 64 columns x 4 token groups of sample blockIdx.y; partials added in LDS.
 __global__ __launch_bounds__(256) void token_sum_kernel(const float *__restrict__ X,
                                                         float *__restrict__ S, int B, int T, int N) {
-  const int64_t n = (int64_t)B * N;
-  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
-    const int64_t b = e / N;
-    const int c = (int)(e % N);
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int64_t b = blockIdx.y;
+  float s = 0.f;
+  if (c < N) {
     const float *p = X + b * T * N + c;
-    float s = 0.f;
-    for (int t = 0; t < T; ++t) s += p[(int64_t)t * N];
-    S[e] = s;
+    for (int t = grp; t < T; t += 4) s += p[(int64_t)t * N];
   }
+  red[grp][lane] = s;
+  __syncthreads();
+  if (grp == 0 && c < N) S[b * N + c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
 // ---------------------------------------------------------------------------
@@ -177,10 +197,51 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 }
 
 // ---------------------------------------------------------------------------
-// Causal multi-head attention, one workgroup per (sample, head)
-// Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd).
-// P [B, NH, T, T] keeps the probabilities for the backward pass.
+// Causal multi-head attention on fp32 MFMA, one workgroup per (sample, head).
+// Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd); T <= 128 and
+// hd <= 32 are held in LDS (zero-padded to 128 x 32).  P [B, NH, T, T] keeps
+// the probabilities for the backward pass.  Wave w owns rows [32w, 32w+32) of
+// every T x T matrix.  v_mfma_f32_32x32x2_f32 operands: A[m = l%32][k = l/32],
+// B[k = l/32][n = l%32]; result register r of lane l is row
+// 8*(r/4) + 4*(l/32) + r%4, column l%32.
 // ---------------------------------------------------------------------------
+typedef float fx16 __attribute__((ext_vector_type(16)));
+constexpr int AT_SP = AT_T + 1;  // row pitch of the T x T LDS matrix
+
+__device__ __forceinline__ int mrow(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// row-wise max / sum over the 32 lanes that share lane/32
+__device__ __forceinline__ float hmax32(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float hsum32(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Stage rows [0, 128) x cols [0, 32) of head h into LDS (pitch AT_HP), zero padded.
+__device__ __forceinline__ void stage_head(float *dst, const float *__restrict__ src, int b, int h,
+                                           int T, int D, int hd) {
+  for (int e = threadIdx.x; e < AT_T * AT_HD; e += 256) {
+    const int t = e / AT_HD, d = e % AT_HD;
+    dst[t * AT_HP + d] = (t < T && d < hd) ? src[((int64_t)b * T + t) * D + h * hd + d] : 0.f;
+  }
+}
+
+// acc += A_rows[32 rows from r0] . B_rows[32 rows from c0]^T over k in [0, kn)
+// with A and B both stored [row][k] at pitch AT_HP (S = Q K^T, dP = gO V^T).
+__device__ __forceinline__ void mm_nt(fx16 &acc, const float *A, const float *Bm, int r0, int c0,
+                                      int kn, int lane) {
+  for (int k = 0; k < kn; k += 2) {
+    const float a = A[(r0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
+    const float b = Bm[(c0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+  }
+}
+
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__ Q,
                                                        const float *__restrict__ K,
                                                        const float *__restrict__ V,
@@ -188,61 +249,80 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
                                                        float *__restrict__ O, int T, int D,
                                                        int NH, int causal) {
   __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP];
-  __shared__ float prow[4][AT_T];
+  __shared__ float sp[AT_T * AT_SP];
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < T * hd; e += 256) {
-    const int t = e / hd, d = e % hd;
-    const int64_t gi = ((int64_t)b * T + t) * D + h * hd + d;
-    sq[t * AT_HP + d] = Q[gi];
-    sk[t * AT_HP + d] = K[gi];
-    sv[t * AT_HP + d] = V[gi];
-  }
+  stage_head(sq, Q, b, h, T, D, hd);
+  stage_head(sk, K, b, h, T, D, hd);
+  stage_head(sv, V, b, h, T, D, hd);
   __syncthreads();
   const float scale = (float)sqrt((double)hd);
+  const int r0 = 32 * w;
+  // scores for the 4 column tiles; fully masked causal tiles are skipped
+  fx16 acc[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    acc[jt] = fx16{};
+    if (!(causal && jt > w)) mm_nt(acc[jt], sq, sk, r0, 32 * jt, hd + (hd & 1), lane);
+  }
+  // row softmax: -1e9 on causal-masked entries (as the reference), columns
+  // >= T do not exist; exp in float64 (activations.go:161-183)
+  const int cl = lane & 31;
+  float mx[16], sum[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) mx[r] = -__builtin_inff();
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
+      float sc;
+      if (j >= T) sc = -__builtin_inff();
+      else if (causal && j > i) sc = -1e9f;
+      else sc = acc[jt][r] / scale;
+      acc[jt][r] = sc;
+      mx[r] = fmaxf(mx[r], sc);
+    }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    mx[r] = hmax32(mx[r]);
+    sum[r] = 0.f;
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 32 * jt + cl;
+      const float e = j < T ? (float)exp((double)(acc[jt][r] - mx[r])) : 0.f;
+      acc[jt][r] = e;
+      sum[r] += e;
+    }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sum[r] = hsum32(sum[r]);
   float *Pb = P + ((int64_t)b * NH + h) * T * T;
-  for (int i0 = 0; i0 < T; i0 += 4) {  // uniform trip count: barriers below are legal
-    const int i = i0 + w;
-    const bool ok = i < T;
-    if (ok) {
-      // scores (lanes over j), masked entries -1e9 as in the reference
-      float mx = -__builtin_inff();
-      for (int j = lane; j < T; j += 64) {
-        float sc;
-        if (causal && j > i) {
-          sc = -1e9f;
-        } else {
-          float dot = 0.f;
-          for (int d = 0; d < hd; ++d) dot += sq[i * AT_HP + d] * sk[j * AT_HP + d];
-          sc = dot / scale;
-        }
-        prow[w][j] = sc;
-        mx = fmaxf(mx, sc);
-      }
-      mx = wmax(mx);
-      float s = 0.f;
-      for (int j = lane; j < T; j += 64) {
-        const float e = (float)exp((double)(prow[w][j] - mx));
-        prow[w][j] = e;
-        s += e;
-      }
-      s = wsum(s);
-      for (int j = lane; j < T; j += 64) {
-        const float p = prow[w][j] / s;
-        prow[w][j] = p;
-        Pb[(int64_t)i * T + j] = p;
-      }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
+      const float p = acc[jt][r] / sum[r];
+      sp[i * AT_SP + j] = p;
+      if (i < T && j < T) Pb[(int64_t)i * T + j] = p;
     }
-    __syncthreads();
-    if (ok) {
-      for (int d = lane; d < hd; d += 64) {
-        float acc = 0.f;
-        for (int j = 0; j < T; ++j) acc += prow[w][j] * sv[j * AT_HP + d];
-        O[((int64_t)b * T + i) * D + h * hd + d] = acc;
-      }
-    }
-    __syncthreads();
+  __syncthreads();
+  // O = P V over j < min(T, rows of this wave + 1 under the causal mask)
+  fx16 o = fx16{};
+  const int kend = causal ? min(T, r0 + 32) : T;
+  for (int j = 0; j < kend; j += 2) {
+    const float a = sp[(r0 + (lane & 31)) * AT_SP + j + (lane >> 5)];
+    const float bv = sv[(j + (lane >> 5)) * AT_HP + (lane & 31)];
+    o = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, o, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = r0 + mrow(r, lane), d = cl;
+    if (i < T && d < hd) O[((int64_t)b * T + i) * D + h * hd + d] = o[r];
   }
 }
 
@@ -256,52 +336,97 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__
                                                        float *__restrict__ GV, int T, int D,
                                                        int NH, int causal) {
   __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP], sg[AT_T * AT_HP];
-  __shared__ float ds[AT_T * (AT_T + 1)];
+  __shared__ float sp[AT_T * AT_SP];  // P, then dS
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int TP = AT_T + 1;
-  for (int e = threadIdx.x; e < T * hd; e += 256) {
-    const int t = e / hd, d = e % hd;
-    const int64_t gi = ((int64_t)b * T + t) * D + h * hd + d;
-    sq[t * AT_HP + d] = Q[gi];
-    sk[t * AT_HP + d] = K[gi];
-    sv[t * AT_HP + d] = V[gi];
-    sg[t * AT_HP + d] = GO[gi];
+  const int cl = lane & 31;
+  stage_head(sq, Q, b, h, T, D, hd);
+  stage_head(sk, K, b, h, T, D, hd);
+  stage_head(sv, V, b, h, T, D, hd);
+  stage_head(sg, GO, b, h, T, D, hd);
+  const float *Pb = P + ((int64_t)b * NH + h) * T * T;
+  for (int e = threadIdx.x; e < AT_T * AT_T; e += 256) {
+    const int i = e / AT_T, j = e % AT_T;
+    sp[i * AT_SP + j] = (i < T && j < T) ? Pb[(int64_t)i * T + j] : 0.f;
   }
   __syncthreads();
   const float scale = (float)sqrt((double)hd);
-  const float *Pb = P + ((int64_t)b * NH + h) * T * T;
-  // dS rows (one wave per row)
-  for (int i = w; i < T; i += 4) {
-    float r = 0.f;
-    for (int j = lane; j < T; j += 64) {
-      float dp = 0.f;
-      if (!(causal && j > i))
-        for (int d = 0; d < hd; ++d) dp += sg[i * AT_HP + d] * sv[j * AT_HP + d];
-      ds[i * TP + j] = dp;
-      r += dp * Pb[(int64_t)i * T + j];
+  const int r0 = 32 * w;
+  const int kpad = hd + (hd & 1);
+  auto store = [&](float *G, const fx16 &v) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = r0 + mrow(r, lane), d = cl;
+      if (t < T && d < hd) G[((int64_t)b * T + t) * D + h * hd + d] = v[r];
     }
-    r = wsum(r);
-    for (int j = lane; j < T; j += 64) {
-      const float p = Pb[(int64_t)i * T + j];
-      ds[i * TP + j] = (causal && j > i) ? 0.f : (ds[i * TP + j] * p - p * r) / scale;
+  };
+  // gV_j = sum_i p_ij gO_i  (rows j of this wave; p_ij = 0 for i < j when causal)
+  {
+    fx16 acc = fx16{};
+    for (int i = causal ? r0 : 0; i < T; i += 2) {
+      const float a = sp[(i + (lane >> 5)) * AT_SP + r0 + (lane & 31)];
+      const float bv = sg[(i + (lane >> 5)) * AT_HP + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
     }
+    store(GV, acc);
   }
-  __syncthreads();
-  // gQ_i = sum_j dS_ij k_j ; gK_j = sum_i dS_ij q_i ; gV_j = sum_i p_ij gO_i
-  for (int e = threadIdx.x; e < T * hd; e += 256) {
-    const int t = e / hd, d = e % hd;
-    float gq = 0.f, gk = 0.f, gv = 0.f;
-    for (int j = 0; j < T; ++j) gq += ds[t * TP + j] * sk[j * AT_HP + d];
-    for (int i = 0; i < T; ++i) {
-      gk += ds[i * TP + t] * sq[i * AT_HP + d];
-      gv += Pb[(int64_t)i * T + t] * sg[i * AT_HP + d];
+  // dP_ij = gO_i . v_j ; r_i = sum_j dP_ij p_ij ; dS = (dP p - p r) / sqrt(hd)
+  fx16 dp[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    dp[jt] = fx16{};
+    if (!(causal && jt > w)) mm_nt(dp[jt], sg, sv, r0, 32 * jt, kpad, lane);
+  }
+  float rs[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) rs[r] = 0.f;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
+      const bool live = j < T && !(causal && j > i);
+      if (!live) dp[jt][r] = 0.f;
+      rs[r] += dp[jt][r] * sp[i * AT_SP + j];
     }
-    const int64_t gi = ((int64_t)b * T + t) * D + h * hd + d;
-    GQ[gi] = gq;
-    GK[gi] = gk;
-    GV[gi] = gv;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) rs[r] = hsum32(rs[r]);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
+      const bool live = j < T && !(causal && j > i);
+      const float p = sp[i * AT_SP + j];
+      dp[jt][r] = live ? (dp[jt][r] * p - p * rs[r]) / scale : 0.f;
+    }
+  __syncthreads();  // every wave has read P (gV and r): overwrite it with dS
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sp[(r0 + mrow(r, lane)) * AT_SP + 32 * jt + cl] = dp[jt][r];
+  __syncthreads();
+  // gQ_i = sum_j dS_ij k_j  (j <= i when causal)
+  {
+    fx16 acc = fx16{};
+    const int kend = causal ? min(T, r0 + 32) : T;
+    for (int j = 0; j < kend; j += 2) {
+      const float a = sp[(r0 + (lane & 31)) * AT_SP + j + (lane >> 5)];
+      const float bv = sk[(j + (lane >> 5)) * AT_HP + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
+    }
+    store(GQ, acc);
+  }
+  // gK_j = sum_i dS_ij q_i  (i >= j when causal)
+  {
+    fx16 acc = fx16{};
+    for (int i = causal ? r0 : 0; i < T; i += 2) {
+      const float a = sp[(i + (lane >> 5)) * AT_SP + r0 + (lane & 31)];
+      const float bv = sq[(i + (lane >> 5)) * AT_HP + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
+    }
+    store(GK, acc);
   }
 }
 
@@ -326,9 +451,15 @@ hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int
 
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
                              int D, int W, float scale, hipStream_t s) {
+  const int Wc = W < 1 ? 1 : (W > B ? B : W);
+  const int chunk = (B + Wc - 1) / Wc;
+  const int nsamp = (B + chunk - 1) / chunk;  // one contributing sample per chunk
+  const int L = nsamp * T;
+  if (L > EG_MAXL) return hipErrorInvalidValue;
   hipError_t e = hipMemsetAsync(gradE, 0, (size_t)V * D * sizeof(float), s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(embed_grad_kernel, dim3(1), dim3(256), 0, s, g, ids, gradE, B, T, D, W, scale);
+  hipLaunchKernelGGL(embed_grad_kernel, dim3(L), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
+                     scale);
   return hipGetLastError();
 }
 
@@ -345,8 +476,7 @@ hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipS
 }
 
 hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s) {
-  hipLaunchKernelGGL(token_sum_kernel, dim3(blocks_for((int64_t)B * N)), dim3(256), 0, s, X, S, B, T,
-                     N);
+  hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B), dim3(256), 0, s, X, S, B, T, N);
   return hipGetLastError();
 }
 

@@ -6,11 +6,13 @@
 // operand keeps its global layout in LDS (no transposing scalar stores) and is
 // read with ds_read_b32 by consecutive lanes.
 //
-// Tiling: 128x128 block tile, 64-wide K stages, 512 threads = 8 wave64s in
-// two K-groups.  Group g owns k in [32g, 32g+32) of every stage; inside a
-// group the 4 waves tile the block 2x2, each wave a 64x64 sub-tile = 2x2
-// v_mfma_f32_32x32x2_f32 accumulators (64 fp32 accumulators per lane).  The
-// two groups' partial sums are added through LDS before the epilogue.  With a
+// Tiling: R x R block tile (R = 128, or 64 for grids that 128-wide tiles
+// cannot fill), 64-wide K stages, 512 threads = 8 wave64s in two K-groups.
+// Group g owns k in [32g, 32g+32) of every stage; inside a group the 4 waves
+// tile the block 2x2, each wave an (R/2)x(R/2) sub-tile of
+// v_mfma_f32_32x32x2_f32 accumulators (2x2 of them, 64 fp32 per lane, at
+// R = 128).  The two groups' partial sums are added through LDS before the
+// epilogue.  With a
 // 1024-row batch a 4096-wide layer has exactly 256 tiles (one per CU): the
 // K-groups give every SIMD two waves to hide LDS and barrier latency.  Lane
 // half h feeds k = 16h + s at MFMA step s, so each lane's 16 operand values per
@@ -32,11 +34,19 @@ namespace gn {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 64;          // K staged per iteration (two 32-wide halves)
 constexpr int PITCH = BK + 4;   // floats; 16 B pad keeps b128 row reads conflict-free
 constexpr int NT = 512;         // 8 wave64s: 2 K-groups x (2 x 2) waves
+
+// Per-tile-size constants: R rows (and columns) per block tile.
+template <int R>
+struct Tile {
+  static constexpr int T = R / 64;            // 32x32 MFMA tiles per wave per dimension
+  static constexpr int RP = R + 4;            // pitch of an M/N-contiguous operand in LDS
+  static constexpr int STAGE = (R * PITCH > BK * RP) ? R * PITCH : BK * RP;  // floats
+  static constexpr int NLD = R / 32;          // float4 loads per thread per operand tile
+  static constexpr int QPL = T * T * 4;       // float4 accumulator groups per lane
+};
 
 __device__ __forceinline__ float apply_fwd(float v, int kind) {
   switch (kind) {
@@ -58,16 +68,16 @@ __device__ __forceinline__ float apply_deriv(float out, int kind) {
   }
 }
 
-// Global -> register staging of one operand tile.  KC: the operand's K index
-// is contiguous in memory (rows x K, row pitch ld); otherwise it is stored
-// K x rows.  VEC: float4 accesses are legal (16 B aligned, sizes % 4 == 0).
-// Only k in [k0, kend) is read; everything else is zero-filled.
-template <bool KC, bool VEC>
+// Global -> register staging of one R-row operand tile.  KC: the operand's K
+// index is contiguous in memory (rows x K, row pitch ld); otherwise it is
+// stored K x rows.  VEC: float4 accesses are legal (16 B aligned, sizes % 4 ==
+// 0).  Only k in [k0, kend) is read; everything else is zero-filled.
+template <int R, bool KC, bool VEC>
 __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld, int rows, int kend,
-                                          int r0, int k0, float4 (&reg)[4]) {
+                                          int r0, int k0, float4 (&reg)[Tile<R>::NLD]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < Tile<R>::NLD; ++j) {
     const int f = t + NT * j;
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
@@ -86,7 +96,7 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
         reg[j].w = (ok && gk + 3 < kend) ? p[3] : 0.f;
       }
     } else {
-      const int k = f >> 5, r4 = (f & 31) << 2;
+      const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
       const int gk = k0 + k, gr = r0 + r4;
       if (VEC) {
         if (gk < kend && gr < rows)
@@ -105,33 +115,29 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
   }
 }
 
-// LDS layouts.  K-contiguous operands: [128 rows][68] (k fastest, 16 B pad),
+// LDS layouts.  K-contiguous operands: [R rows][68] (k fastest, 16 B pad),
 // read as 4 x ds_read_b128 per lane.  M/N-contiguous operands keep their
-// global layout, [64 k][132] (row fastest), written with ds_write_b128 and
+// global layout, [64 k][R + 4] (row fastest), written with ds_write_b128 and
 // read as 16 x ds_read_b32 per lane (consecutive lanes, consecutive rows).
-constexpr int RP = BM + 4;
-constexpr int STAGE = BM * PITCH;  // floats per operand stage (>= BK * RP)
-static_assert(BK * RP <= STAGE, "stage size");
-
-template <bool KC>
-__device__ __forceinline__ void store_tile(float *S, const float4 (&reg)[4]) {
+template <int R, bool KC>
+__device__ __forceinline__ void store_tile(float *S, const float4 (&reg)[Tile<R>::NLD]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < Tile<R>::NLD; ++j) {
     const int f = t + NT * j;
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
       *reinterpret_cast<float4 *>(S + r * PITCH + k4) = reg[j];
     } else {
-      const int k = f >> 5, r4 = (f & 31) << 2;
-      *reinterpret_cast<float4 *>(S + k * RP + r4) = reg[j];
+      const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
+      *reinterpret_cast<float4 *>(S + k * Tile<R>::RP + r4) = reg[j];
     }
   }
 }
 
 // MFMA operand fragment of one 32-row slab for K-group g: lane half h
 // supplies k = 32g + 16h + s at step s (s = 0..15), row = rowbase + lane % 32.
-template <bool KC>
+template <int R, bool KC>
 __device__ __forceinline__ void read_frag(const float *S, int rowbase, int koff, int l32,
                                           float (&a)[16]) {
   if (KC) {
@@ -145,9 +151,9 @@ __device__ __forceinline__ void read_frag(const float *S, int rowbase, int koff,
       a[4 * q + 3] = x.w;
     }
   } else {
-    const float *src = S + koff * RP + rowbase + l32;
+    const float *src = S + koff * Tile<R>::RP + rowbase + l32;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) a[s] = src[s * RP];
+    for (int s = 0; s < 16; ++s) a[s] = src[s * Tile<R>::RP];
   }
 }
 
@@ -185,18 +191,20 @@ __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, i
 // EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
 constexpr int EPI_PARTIAL = 3;
 
-template <bool AK, bool BKC, bool VEC, int EPI>
+template <int R, bool AK, bool BKC, bool VEC, int EPI>
 __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n,
                                                     int kchunk) {
-  __shared__ __attribute__((aligned(16))) float As[2][STAGE];
-  __shared__ __attribute__((aligned(16))) float Bs[2][STAGE];
+  using TL = Tile<R>;
+  constexpr int T = TL::T;
+  __shared__ __attribute__((aligned(16))) float As[2][TL::STAGE];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TL::STAGE];
 
   int tm, tn;
   tile_of_block(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * R, n0 = tn * R;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   // waves 0-3 take k in [0,32) of every stage, waves 4-7 take [32,64); within
-  // a group the 4 waves tile the 128x128 block as 2x2 sub-tiles of 64x64.
+  // a group the 4 waves tile the R x R block as 2x2 sub-tiles of R/2 x R/2.
   const int g = w >> 2, w4 = w & 3;
   const int wm = w4 >> 1, wn = w4 & 1;
   const int half = lane >> 5, l32 = lane & 31;
@@ -206,18 +214,18 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
   const int kend = min(p.K, kbeg + kchunk);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
-  float4 ra[4], rb[4];
-  load_tile<AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
-  load_tile<BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
-  store_tile<AK>(As[0], ra);
-  store_tile<BKC>(Bs[0], rb);
+  float4 ra[TL::NLD], rb[TL::NLD];
+  load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
+  load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+  store_tile<R, AK>(As[0], ra);
+  store_tile<R, BKC>(Bs[0], rb);
   __syncthreads();
 
-  floatx16 acc[2][2];
+  floatx16 acc[T][T];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < T; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < T; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -225,48 +233,48 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_tile<AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
-      load_tile<BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
+      load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
+      load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
     }
-    float a[2][16], b[2][16];
+    float a[T][16], b[T][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) read_frag<AK>(As[cur], wm * 64 + i * 32, koff, l32, a[i]);
+    for (int i = 0; i < T; ++i) read_frag<R, AK>(As[cur], wm * (R / 2) + i * 32, koff, l32, a[i]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) read_frag<BKC>(Bs[cur], wn * 64 + j * 32, koff, l32, b[j]);
+    for (int j = 0; j < T; ++j) read_frag<R, BKC>(Bs[cur], wn * (R / 2) + j * 32, koff, l32, b[j]);
 #pragma unroll
     for (int s = 0; s < 16; ++s)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < T; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < T; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
     if (more) {
-      store_tile<AK>(As[cur ^ 1], ra);
-      store_tile<BKC>(Bs[cur ^ 1], rb);
+      store_tile<R, AK>(As[cur ^ 1], ra);
+      store_tile<R, BKC>(Bs[cur ^ 1], rb);
     }
     __syncthreads();
   }
 
   // K-group 1 hands its accumulators to group 0 through LDS (the operand
-  // stages are free after the last barrier): 4 waves x 64 lanes x 64 floats.
+  // stages are free after the last barrier): 4 waves x 64 lanes x T*T*16 floats.
   float *red = &As[0][0];
-  static_assert(4 * 64 * 64 <= 2 * STAGE, "reduction buffer");
+  static_assert(4 * 64 * TL::QPL * 4 <= 2 * TL::STAGE, "reduction buffer");
   if (g == 1) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < TL::QPL; ++q) {
       const int ij = q >> 2, r4 = (q & 3) << 2;
-      const floatx16 &v = acc[ij >> 1][ij & 1];
-      *reinterpret_cast<float4 *>(red + ((w4 * 16 + q) * 64 + lane) * 4) =
+      const floatx16 &v = acc[ij / T][ij % T];
+      *reinterpret_cast<float4 *>(red + ((w4 * TL::QPL + q) * 64 + lane) * 4) =
           make_float4(v[r4], v[r4 + 1], v[r4 + 2], v[r4 + 3]);
     }
   }
   __syncthreads();
   if (g == 1) return;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
+  for (int q = 0; q < TL::QPL; ++q) {
     const int ij = q >> 2, r4 = (q & 3) << 2;
-    const float4 o = *reinterpret_cast<const float4 *>(red + ((w4 * 16 + q) * 64 + lane) * 4);
-    floatx16 &v = acc[ij >> 1][ij & 1];
+    const float4 o = *reinterpret_cast<const float4 *>(red + ((w4 * TL::QPL + q) * 64 + lane) * 4);
+    floatx16 &v = acc[ij / T][ij % T];
     v[r4] += o.x;
     v[r4 + 1] += o.y;
     v[r4 + 2] += o.z;
@@ -277,14 +285,14 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
   // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < T; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + l32;
+    for (int j = 0; j < T; ++j) {
+      const int col = n0 + wn * (R / 2) + j * 32 + l32;
       if (col >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        const int row = m0 + wm * (R / 2) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
         if (row >= M) continue;
         if (EPI == EPI_PARTIAL)
           ws[(size_t)row * N + col] = acc[i][j][r];
@@ -305,27 +313,38 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits,
   }
 }
 
-template <bool AK, bool BKC, int EPI>
+template <int R, bool AK, bool BKC, int EPI>
 static hipError_t launch_t(bool vec, const GemmArgs &a, int tm, int tn, int splits, int kchunk,
                            hipStream_t s) {
   dim3 grid(tm * tn, splits), block(NT);
   if (vec)
-    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, true, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma<AK, BKC, false, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, false, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
   return hipGetLastError();
 }
 
-template <int EPI>
+template <int R, int EPI>
 static hipError_t launch_e(char ta, char tb, bool vec, const GemmArgs &a, int tm, int tn,
                            int splits, int kchunk, hipStream_t s) {
   // op(A) 'N' -> A is M x K, K contiguous.  op(B) 'T' -> B is N x K, K contiguous.
   const bool ak = (ta == 'N');
   const bool bk = (tb == 'T');
-  if (ak && bk) return launch_t<true, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  if (ak && !bk) return launch_t<true, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  if (!ak && bk) return launch_t<false, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  return launch_t<false, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (ak && bk) return launch_t<R, true, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (ak && !bk) return launch_t<R, true, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (!ak && bk) return launch_t<R, false, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  return launch_t<R, false, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
+}
+
+template <int R>
+static hipError_t launch_r(char ta, char tb, int epi, bool vec, const GemmArgs &a, int splits,
+                           int kchunk, hipStream_t s) {
+  const int tm = (a.M + R - 1) / R, tn = (a.N + R - 1) / R;
+  if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, a, tm, tn, splits, kchunk, s);
+  if (epi == EPI_BIAS_ACT) return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+  if (epi == EPI_DACT) return launch_e<R, EPI_DACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+  if (epi == EPI_BIAS_ADD) return launch_e<R, EPI_BIAS_ADD>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+  return launch_e<R, EPI_SCALE>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -337,30 +356,27 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0);
   vec = vec && (ak ? (a.K % 4 == 0) : (a.M % 4 == 0));
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
-  const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-  // Split K when the tile grid cannot fill the 256 CUs (down to one K stage
-  // per split: a lone 128x128 tile runs at 1/256 of the chip); partials go to
-  // the workspace and are summed in split order.
+  // 128-wide tiles when they fill the 256 CUs, else 64-wide tiles; when even
+  // those cannot fill the chip, split K (down to one K stage per split: a lone
+  // tile runs at 1/256 of the chip).  Partials go to the workspace and are
+  // summed in split order.
+  const int t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  const int t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+  const bool big = t128 >= 160;
+  const int tiles = big ? t128 : t64;
   int splits = 1;
-  const int tiles = tm * tn;
   if (tiles < 160 && a.K >= 2 * BK && a.ws) {
     splits = std::min((256 + tiles - 1) / tiles, a.K / BK);
     while (splits > 1 && (size_t)splits * a.M * a.N > a.ws_cap) --splits;
   }
-  int kchunk = a.K;
+  int kchunk = a.K > 0 ? a.K : 1;
   if (splits > 1) {
     kchunk = ((a.K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (a.K + kchunk - 1) / kchunk;
   }
-  if (splits <= 1) {
-    kchunk = a.K > 0 ? a.K : 1;
-    if (epi == EPI_BIAS_ACT) return launch_e<EPI_BIAS_ACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-    if (epi == EPI_DACT) return launch_e<EPI_DACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-    if (epi == EPI_BIAS_ADD) return launch_e<EPI_BIAS_ADD>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-    return launch_e<EPI_SCALE>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-  }
-  hipError_t e = launch_e<EPI_PARTIAL>(ta, tb, vec, a, tm, tn, splits, kchunk, s);
-  if (e != hipSuccess) return e;
+  hipError_t e = big ? launch_r<128>(ta, tb, epi, vec, a, splits, kchunk, s)
+                     : launch_r<64>(ta, tb, epi, vec, a, splits, kchunk, s);
+  if (e != hipSuccess || splits <= 1) return e;
   const size_t MN = (size_t)a.M * a.N;
   const unsigned blocks = (unsigned)std::min<size_t>((MN + NT - 1) / NT, 4096);
   hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(NT), 0, s, a, splits, epi);

@@ -105,7 +105,8 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(TPB) void colsum_partial(const float *__restrict__ dz, int rows,
                                                       int cols, int ld, int rows_per_chunk,
-                                                      float *__restrict__ part) {
+                                                      float *__restrict__ part, float scale,
+                                                      float *__restrict__ out) {
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
@@ -116,32 +117,40 @@ __global__ __launch_bounds__(TPB) void colsum_partial(const float *__restrict__ 
     for (int r = r0 + w; r < r1; r += 4) s += dz[(size_t)r * ld + col];
   red[w][lane] = s;
   __syncthreads();
-  if (w == 0 && col < cols)
-    part[(size_t)blockIdx.y * cols + col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  if (w == 0 && col < cols) {
+    const float v = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    if (gridDim.y == 1) out[col] = v * scale;  // a single chunk is the whole sum
+    else part[(size_t)blockIdx.y * cols + col] = v;
+  }
 }
 
+// One wave per column: lanes take the chunks, then a wave reduction.
 __global__ __launch_bounds__(TPB) void colsum_final(const float *__restrict__ part, int chunks,
                                                     int cols, float scale, float *__restrict__ out) {
-  const int col = blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (col >= cols) return;
   float s = 0.f;
-  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols + col];
-  out[col] = s * scale;
+  for (int c = lane; c < chunks; c += 64) s += part[(size_t)c * cols + col];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if (lane == 0) out[col] = s * scale;
 }
 
 hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
                          float *scratch, size_t scratch_cap, hipStream_t s) {
   if (cols <= 0) return hipSuccess;
-  if ((size_t)cols > scratch_cap) return hipErrorInvalidValue;
   int chunks = (rows + 63) / 64;
   if (chunks > 64) chunks = 64;
   if ((size_t)chunks * cols > scratch_cap) chunks = (int)(scratch_cap / cols);
   if (chunks < 1) chunks = 1;
   const int rpc = (rows + chunks - 1) / chunks;
   dim3 g1((cols + 63) / 64, chunks);
-  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, dz, rows, cols, ld, rpc, scratch);
-  hipLaunchKernelGGL(colsum_final, dim3((cols + TPB - 1) / TPB), dim3(TPB), 0, s, scratch, chunks,
-                     cols, scale, out);
+  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, dz, rows, cols, ld, rpc, scratch, scale,
+                     out);
+  if (chunks > 1)
+    hipLaunchKernelGGL(colsum_final, dim3((cols + 3) / 4), dim3(TPB), 0, s, scratch, chunks, cols,
+                       scale, out);
   return hipGetLastError();
 }
 
@@ -201,7 +210,7 @@ hipError_t launch_act_inplace(float *x, int64_t n, int kind, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Block reductions (256 threads = 4 wave64s).
+// Block reductions over blockDim.x / 64 wave64s (at most 16).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -215,42 +224,49 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 __device__ __forceinline__ float block_sum(float v, float *sh) {
   v = wave_sum(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if (lane == 0) sh[w] = v;
   __syncthreads();
-  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  float s = 0.f;
+  for (int i = 0; i < nw; ++i) s += sh[i];
+  return s;
 }
 __device__ __forceinline__ float block_max(float v, float *sh) {
   v = wave_max(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if (lane == 0) sh[w] = v;
   __syncthreads();
-  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+  float m = sh[0];
+  for (int i = 1; i < nw; ++i) m = fmaxf(m, sh[i]);
+  return m;
 }
 
 // Row activation (Softmax.ActivateBatch activations.go:161-183 /
 // LogSoftmax.ActivateBatch :204-236), in place over one row.
 __device__ void row_activate(float *row, int C, int row_act, int fwd, float *sh) {
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, nt = blockDim.x;
   if (row_act == ROW_SOFTMAX || row_act == ROW_LOGSOFTMAX) {
     float mx = -__builtin_inff();
-    for (int i = t; i < C; i += TPB) mx = fmaxf(mx, row[i]);
+    for (int i = t; i < C; i += nt) mx = fmaxf(mx, row[i]);
     mx = block_max(mx, sh);
     float s = 0.f;
-    for (int i = t; i < C; i += TPB) s += (float)exp((double)(row[i] - mx));
+    for (int i = t; i < C; i += nt) s += (float)exp((double)(row[i] - mx));
     s = block_sum(s, sh);
     if (row_act == ROW_SOFTMAX) {
-      for (int i = t; i < C; i += TPB) row[i] = (float)exp((double)(row[i] - mx)) / s;
+      for (int i = t; i < C; i += nt) row[i] = (float)exp((double)(row[i] - mx)) / s;
     } else {
       const float ls = (float)log((double)s);
-      for (int i = t; i < C; i += TPB) row[i] = row[i] - mx - ls;
+      for (int i = t; i < C; i += nt) row[i] = row[i] - mx - ls;
     }
   } else if (row_act == ROW_ELEMWISE) {
-    for (int i = t; i < C; i += TPB) row[i] = fwd_of(row[i], fwd);
+    for (int i = t; i < C; i += nt) row[i] = fwd_of(row[i], fwd);
   }
 }
+
+// Threads per row for the row kernels: long rows get 16 waves.
+static int row_threads(int C) { return C >= 4096 ? 1024 : TPB; }
 
 // Output layer: z (pre-activations, overwritten by the activation output),
 // per-sample loss (loss.go:53-67 MSE, :120-141 CE), loss gradient
@@ -258,14 +274,14 @@ __device__ void row_activate(float *row, int C, int row_act, int fwd, float *sh)
 //   Softmax    dz_k = sum_i g_i p_i (d_ik - p_k) = p_k g_k - p_k sum_i g_i p_i  (layer.go:504-529)
 //   LogSoftmax dz_k = sum_i g_i (d_ik - exp(o_k)) = g_k - exp(o_k) sum_i g_i     (layer.go:530-560)
 //   otherwise  dz_k = g_k * Derivative                                          (layer.go:561-567)
-__global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
+__global__ __launch_bounds__(1024) void out_rows_kernel(float *__restrict__ zo,
                                                        const float *__restrict__ y,
                                                        float *__restrict__ dz,
                                                        float *__restrict__ loss_rows, int C,
                                                        int row_act, int fwd, int deriv,
                                                        int loss_kind) {
-  __shared__ float sh[4];
-  const int b = blockIdx.x, t = threadIdx.x;
+  __shared__ float sh[16];
+  const int b = blockIdx.x, t = threadIdx.x, nt = blockDim.x;
   float *o = zo + (size_t)b * C;
   const float *yr = y + (size_t)b * C;
   float *d = dz + (size_t)b * C;
@@ -275,7 +291,7 @@ __global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
   float l = 0.f;
   if (loss_kind == GN_LOSS_MSE) {
     const float factor = 2.0f / (float)C;
-    for (int i = t; i < C; i += TPB) {
+    for (int i = t; i < C; i += nt) {
       const float df = o[i] - yr[i];
       l += df * df;
       d[i] = factor * df;
@@ -283,7 +299,7 @@ __global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
     l = block_sum(l, sh);
     l = l / (float)C;
   } else {
-    for (int i = t; i < C; i += TPB) {
+    for (int i = t; i < C; i += nt) {
       float pv = o[i];
       if (pv < 1e-10f) pv = 1e-10f;
       const float yi = yr[i];
@@ -296,16 +312,16 @@ __global__ __launch_bounds__(TPB) void out_rows_kernel(float *__restrict__ zo,
   // Jacobian / derivative
   if (row_act == ROW_SOFTMAX) {
     float s1 = 0.f;
-    for (int i = t; i < C; i += TPB) s1 += d[i] * o[i];
+    for (int i = t; i < C; i += nt) s1 += d[i] * o[i];
     s1 = block_sum(s1, sh);
-    for (int i = t; i < C; i += TPB) d[i] = d[i] * o[i] - o[i] * s1;
+    for (int i = t; i < C; i += nt) d[i] = d[i] * o[i] - o[i] * s1;
   } else if (row_act == ROW_LOGSOFTMAX) {
     float s1 = 0.f;
-    for (int i = t; i < C; i += TPB) s1 += d[i];
+    for (int i = t; i < C; i += nt) s1 += d[i];
     s1 = block_sum(s1, sh);
-    for (int i = t; i < C; i += TPB) d[i] = d[i] - (float)exp((double)o[i]) * s1;
+    for (int i = t; i < C; i += nt) d[i] = d[i] - (float)exp((double)o[i]) * s1;
   } else {
-    for (int i = t; i < C; i += TPB) d[i] = d[i] * deriv_of(o[i], deriv);
+    for (int i = t; i < C; i += nt) d[i] = d[i] * deriv_of(o[i], deriv);
   }
 }
 
@@ -315,20 +331,20 @@ hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz
   if (B <= 0) return hipSuccess;
   // fwd kind for ROW_ELEMWISE rides in the high bits of row_act
   const int fwd = row_act >> 8;
-  hipLaunchKernelGGL(out_rows_kernel, dim3(B), dim3(TPB), 0, s, out, y, dz, loss_rows, C,
+  hipLaunchKernelGGL(out_rows_kernel, dim3(B), dim3(row_threads(C)), 0, s, out, y, dz, loss_rows, C,
                      row_act & 0xff, fwd, deriv, loss_kind);
   return hipGetLastError();
 }
 
-__global__ __launch_bounds__(TPB) void row_act_kernel(float *__restrict__ x, int C, int row_act,
-                                                      int fwd) {
-  __shared__ float sh[4];
+__global__ __launch_bounds__(1024) void row_act_kernel(float *__restrict__ x, int C, int row_act,
+                                                       int fwd) {
+  __shared__ float sh[16];
   row_activate(x + (size_t)blockIdx.x * C, C, row_act, fwd, sh);
 }
 
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) {
   if (B <= 0 || (row_act & 0xff) == ROW_NONE) return hipSuccess;
-  hipLaunchKernelGGL(row_act_kernel, dim3(B), dim3(TPB), 0, s, out, C, row_act & 0xff,
+  hipLaunchKernelGGL(row_act_kernel, dim3(B), dim3(row_threads(C)), 0, s, out, C, row_act & 0xff,
                      row_act >> 8);
   return hipGetLastError();
 }
@@ -340,6 +356,7 @@ __global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict_
   __shared__ __attribute__((aligned(16))) float buf[1024 + 32];
   const int chunk = W > 1 ? (B + W - 1) / W : B;
   float total = 0.f, local = 0.f;
+  int left = chunk;  // samples still to add in the current worker chunk
   for (int base = 0; base < B; base += 1024) {
     const int n = min(1024, B - base);
     for (int i = threadIdx.x; i < n; i += TPB) buf[i] = rows[base + i];
@@ -357,10 +374,10 @@ __global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict_
         const int m = min(32, n - i0);
         for (int q = 0; q < m; ++q) {
           local += v[q];
-          const int gi = base + i0 + q + 1;
-          if (gi % chunk == 0 || gi == B) {  // end of a worker chunk
+          if (--left == 0 || base + i0 + q + 1 == B) {  // end of a worker chunk
             total += local;
             local = 0.f;
+            left = chunk;
           }
         }
       }

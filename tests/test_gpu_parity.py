@@ -260,6 +260,15 @@ def test_gpt_small_random_block(gn, oracle, workers):
     _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
 
 
+@pytest.mark.parametrize("T,dim,heads,causal", [(13, 30, 2, False), (33, 64, 2, True), (97, 16, 1, False)])
+def test_gpt_attention_shapes(gn, oracle, T, dim, heads, causal):
+    """Odd sequence lengths and head dims (LDS zero padding), the non-causal
+    path and a block-crossing causal mask, with a random block."""
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=3, T=T, vocab=29, dim=dim, heads=heads, ff=24, causal=causal)
+    _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg))
+
+
 def test_gpt_small_reference_init(gn, oracle):
     from goneuron_amd import configs
     cfg = configs.gpt(B=4, T=16, vocab=50, dim=32, heads=2, ff=40)
