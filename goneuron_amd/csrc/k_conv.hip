@@ -17,6 +17,8 @@
 // reduced per block and then across blocks in a fixed order.
 #include "gn_common.h"
 
+#include <algorithm>
+
 namespace gn {
 
 constexpr int CT = 256;
@@ -46,17 +48,16 @@ __global__ __launch_bounds__(CT) void conv2d_fwd_kernel(const float *__restrict_
                                                         const float *__restrict__ bias,
                                                         float *__restrict__ out, ConvShape s,
                                                         int B, int fwd) {
+  // blockIdx.y = b * outC + oc: one output plane, threads over its positions
   const int osz = s.oH * s.oW;
-  const int64_t total = (int64_t)B * s.outC * osz;
-  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * CT) {
-    const int pos = (int)(idx % osz);
-    const int oc = (int)((idx / osz) % s.outC);
-    const int b = (int)(idx / ((int64_t)osz * s.outC));
-    const int oh = pos / s.oW, ow = pos % s.oW;
-    const int H = s.H, W = s.W;
-    const float *xs = x + (int64_t)b * s.inC * H * W;
-    const float *wo = w + (int64_t)oc * s.inC * s.k * s.k;
+  const int plane = blockIdx.y;
+  const int oc = plane % s.outC, b = plane / s.outC;
+  const int H = s.H, W = s.W;
+  const float *xs = x + (int64_t)b * s.inC * H * W;
+  const float *wo = w + (int64_t)oc * s.inC * s.k * s.k;
+  for (int pos = blockIdx.x * CT + threadIdx.x; pos < osz; pos += gridDim.x * CT) {
+    const int oh = pos / s.oW, ow = pos - oh * s.oW;
+    const int64_t idx = (int64_t)plane * osz + pos;
     float p = 0.0f;
     const bool fast = (s.k == 3 && s.stride == 1 && s.pad == 1);
     if (fast && oh >= 1 && oh < s.oH - 1) {
@@ -120,19 +121,19 @@ __global__ __launch_bounds__(CT) void maxpool_fwd_kernel(const float *__restrict
 }
 
 // gin[b, i] = sum over output positions whose window holds input i and whose
-// argmax == i, visited in increasing output position.
+// argmax == i, visited in increasing output position.  Block = one (sample,
+// channel) plane, so a thread derives (ih, iw) with a single division.
 __global__ __launch_bounds__(CT) void maxpool_bwd_kernel(const float *__restrict__ gout,
                                                          const int32_t *__restrict__ argmax,
-                                                         float *__restrict__ gin, PoolShape s,
-                                                         int B) {
-  const int in_len = s.C * s.H * s.W;
-  const int osz = s.oH * s.oW;
-  const int64_t total = (int64_t)B * in_len;
-  for (int64_t idx = (int64_t)blockIdx.x * CT + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * CT) {
-    const int i = (int)(idx % in_len);
-    const int b = (int)(idx / in_len);
-    const int c = i / (s.H * s.W), ih = (i / s.W) % s.H, iw = i % s.W;
+                                                         float *__restrict__ gin, PoolShape s) {
+  const int plane = blockIdx.x;  // b * C + c
+  const int c = plane % s.C;
+  const int hw = s.H * s.W, osz = s.oH * s.oW;
+  const int64_t ob = (int64_t)plane * osz;
+  const int ibase = c * hw;      // flat index of the plane inside its sample
+  for (int e = threadIdx.x; e < hw; e += CT) {
+    const int ih = e / s.W, iw = e - ih * s.W;
+    const int i = ibase + e;
     // output rows/cols whose window covers (ih, iw)
     int oh0 = ih + s.pad - s.k + 1, oh1 = ih + s.pad;
     int ow0 = iw + s.pad - s.k + 1, ow1 = iw + s.pad;
@@ -140,14 +141,13 @@ __global__ __launch_bounds__(CT) void maxpool_bwd_kernel(const float *__restrict
     ow0 = ow0 <= 0 ? 0 : (ow0 + s.stride - 1) / s.stride;
     oh1 = min(oh1 / s.stride, s.oH - 1);
     ow1 = min(ow1 / s.stride, s.oW - 1);
-    const int64_t ob = ((int64_t)b * s.C + c) * osz;
     float g = 0.0f;
     for (int oh = oh0; oh <= oh1; ++oh)
       for (int ow = ow0; ow <= ow1; ++ow) {
         const int64_t o = ob + oh * s.oW + ow;
         if (argmax[o] == i) g += gout[o];
       }
-    gin[idx] = g;
+    gin[(int64_t)plane * hw + e] = g;
   }
 }
 
@@ -202,14 +202,100 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_partial(const float *__restri
   }
 }
 
-__global__ __launch_bounds__(CT) void conv2d_wgrad_final(const float *__restrict__ part, int nblocks,
-                                                         int nslots, float scale,
-                                                         float *__restrict__ grad) {
-  const int o = blockIdx.x * CT + threadIdx.x;
+// The same partials on fp32 MFMA: per block an implicit GEMM
+//   part[oc][tap] = sum_pos dz[oc][pos] * xcol[pos][tap],
+// tap = (ic, kh, kw) plus one all-ones column that yields the bias gradient.
+// dz and the block's input rows (zero padded by `pad` on every side) sit in
+// LDS; each of the 4 waves takes a quarter of the positions and the waves'
+// 32x32 results are added in LDS in wave order.
+typedef float cfx16 __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict__ x,
+                                                        const float *__restrict__ gout,
+                                                        const float *__restrict__ out,
+                                                        float *__restrict__ part, ConvShape s,
+                                                        int band_rows, int deriv) {
+  extern __shared__ float sm[];
+  const int bands = (s.oH + band_rows - 1) / band_rows;
+  const int b = blockIdx.x / bands, band = blockIdx.x % bands;
+  const int oh0 = band * band_rows, oh1 = min(s.oH, oh0 + band_rows);
+  const int P = (oh1 - oh0) * s.oW;
+  const int Pp = (P + 1) & ~1;
+  const int osz = s.oH * s.oW;
+  const int Rin = (band_rows - 1) * s.stride + s.k;  // input rows one band touches
+  const int Wp = s.W + 2 * s.pad;
+  float *dz = sm;                                    // [outC][Pp]
+  float *xb = dz + s.outC * Pp;                      // [inC][Rin][Wp]
+  int *poff = reinterpret_cast<int *>(xb + s.inC * Rin * Wp);  // [Pp] LDS offset of a position
+  float *red = reinterpret_cast<float *>(poff + Pp);           // [4][32*32]
+  for (int e = threadIdx.x; e < s.outC * Pp; e += CT) {
+    const int oc = e / Pp, q = e % Pp;
+    float v = 0.f;
+    if (q < P) {
+      const int64_t gi = ((int64_t)b * s.outC + oc) * osz + oh0 * s.oW + q;
+      v = gout[gi] * act_deriv(out[gi], deriv);
+    }
+    dz[e] = v;
+  }
+  const int ih0 = oh0 * s.stride - s.pad;
+  const float *xs = x + (int64_t)b * s.inC * s.H * s.W;
+  for (int e = threadIdx.x; e < s.inC * Rin * Wp; e += CT) {
+    const int c = e % Wp, r = (e / Wp) % Rin, ic = e / (Wp * Rin);
+    const int ih = ih0 + r, iw = c - s.pad;
+    xb[e] = (ih >= 0 && ih < s.H && iw >= 0 && iw < s.W) ? xs[(ic * s.H + ih) * s.W + iw] : 0.f;
+  }
+  for (int q = threadIdx.x; q < Pp; q += CT)
+    poff[q] = q < P ? (q / s.oW) * s.stride * Wp + (q % s.oW) * s.stride : 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ntap = s.inC * s.k * s.k;
+  const int nw = s.outC * ntap, nslots = nw + s.outC;
+  const int kq = ((Pp / 2 + 3) / 4) * 2;  // positions per wave (even)
+  const int kb = w * kq, ke = min(Pp, kb + kq);
+  for (int mt = 0; mt * 32 < s.outC; ++mt)
+    for (int nt = 0; nt * 32 <= ntap; ++nt) {
+      const int oc = mt * 32 + (lane & 31);
+      const int tap = nt * 32 + (lane & 31);
+      int toff = -1;  // -1: zero column, -2: ones column (bias)
+      if (tap < ntap) {
+        const int kw = tap % s.k, kh = (tap / s.k) % s.k, ic = tap / (s.k * s.k);
+        toff = (ic * Rin + kh) * Wp + kw;
+      } else if (tap == ntap) {
+        toff = -2;
+      }
+      cfx16 acc = cfx16{};
+      for (int q0 = kb; q0 < ke; q0 += 2) {
+        const int q = q0 + (lane >> 5);
+        const float a = oc < s.outC ? dz[oc * Pp + q] : 0.f;
+        const float bv = toff >= 0 ? xb[toff + poff[q]] : (toff == -2 && q < P ? 1.f : 0.f);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        red[w * 1024 + (8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 32 + (lane & 31)] = acc[r];
+      __syncthreads();
+      for (int e = threadIdx.x; e < 1024; e += CT) {
+        const int o = mt * 32 + e / 32, t = nt * 32 + e % 32;
+        const float v = (red[e] + red[1024 + e]) + (red[2048 + e] + red[3072 + e]);
+        if (o < s.outC && t < ntap) part[(int64_t)blockIdx.x * nslots + o * ntap + t] = v;
+        else if (o < s.outC && t == ntap) part[(int64_t)blockIdx.x * nslots + nw + o] = v;
+      }
+      __syncthreads();
+    }
+}
+
+// One wave per slot: lanes take the blocks, then a wave reduction.
+__global__ __launch_bounds__(CT) void conv2d_wgrad_reduce(const float *__restrict__ part,
+                                                          int nblocks, int nslots, float scale,
+                                                          float *__restrict__ grad) {
+  const int lane = threadIdx.x & 63;
+  const int o = blockIdx.x * (CT / 64) + (threadIdx.x >> 6);
   if (o >= nslots) return;
-  float s = 0.0f;
-  for (int i = 0; i < nblocks; ++i) s += part[(int64_t)i * nslots + o];
-  grad[o] = s * scale;  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)
+  float s = 0.f;
+  for (int i = lane; i < nblocks; i += 64) s += part[(int64_t)i * nslots + o];
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
+  if (lane == 0) grad[o] = s * scale;  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)
 }
 
 // dX gather: gin[b, ic, ih, iw] = sum over (oc, kh, kw) of dz * w, dz formed
@@ -255,8 +341,9 @@ static unsigned grid_for(int64_t n) {
 
 hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, float *out,
                            const ConvShape &s, int B, int fwd, hipStream_t st) {
-  const int64_t n = (int64_t)B * s.outC * s.oH * s.oW;
-  hipLaunchKernelGGL(conv2d_fwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, x, w, bias, out, s, B,
+  const int osz = s.oH * s.oW;
+  const int gx = std::min((osz + CT - 1) / CT, 64);
+  hipLaunchKernelGGL(conv2d_fwd_kernel, dim3(gx, B * s.outC), dim3(CT), 0, st, x, w, bias, out, s, B,
                      fwd);
   return hipGetLastError();
 }
@@ -270,26 +357,43 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
 
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st) {
-  const int64_t n = (int64_t)B * s.C * s.H * s.W;
-  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, gout, argmax, gin, s,
-                     B);
+  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(B * s.C), dim3(CT), 0, st, gout, argmax, gin, s);
   return hipGetLastError();
 }
 
 hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
                              const ConvShape &s, int B, int deriv, float scale, float *ws,
                              size_t ws_cap, hipStream_t st) {
-  // bands of output rows: keep the dz tile (outC x rows x oW floats) <= 32 KiB
+  const int nslots = s.outC * s.inC * s.k * s.k + s.outC;
+  const int Wp = s.W + 2 * s.pad;
+  // MFMA path: bands of output rows whose dz tile, input rows and tables fit
+  // in 64 KiB of LDS
+  auto mfma_lds = [&](int band) {
+    const int P = band * s.oW, Pp = (P + 1) & ~1, Rin = (band - 1) * s.stride + s.k;
+    return ((size_t)s.outC * Pp + (size_t)s.inC * Rin * Wp + Pp + 4 * 1024) * sizeof(float);
+  };
   int band = s.oH;
+  while (band > 1 && mfma_lds(band) > 32768) band = (band + 1) / 2;
+  if (mfma_lds(band) <= 65536) {
+    const int bands = (s.oH + band - 1) / band;
+    const int nblocks = B * bands;
+    if ((size_t)nblocks * nslots > ws_cap) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv2d_wgrad_mfma, dim3(nblocks), dim3(CT), mfma_lds(band), st, x, gout, out,
+                       ws, s, band, deriv);
+    hipLaunchKernelGGL(conv2d_wgrad_reduce, dim3((nslots + 3) / 4), dim3(CT), 0, st, ws, nblocks,
+                       nslots, scale, grad);
+    return hipGetLastError();
+  }
+  // scalar path for shapes whose input rows do not fit: dz tile <= 32 KiB
+  band = s.oH;
   while (band > 1 && (size_t)s.outC * band * s.oW * sizeof(float) > 32768) band = (band + 1) / 2;
   const int bands = (s.oH + band - 1) / band;
   const int nblocks = B * bands;
-  const int nslots = s.outC * s.inC * s.k * s.k + s.outC;
   if ((size_t)nblocks * nslots > ws_cap) return hipErrorInvalidValue;
   const size_t shm = (size_t)s.outC * band * s.oW * sizeof(float);
   hipLaunchKernelGGL(conv2d_wgrad_partial, dim3(nblocks), dim3(CT), shm, st, x, gout, out, ws, s,
                      band, deriv);
-  hipLaunchKernelGGL(conv2d_wgrad_final, dim3((nslots + CT - 1) / CT), dim3(CT), 0, st, ws, nblocks,
+  hipLaunchKernelGGL(conv2d_wgrad_reduce, dim3((nslots + 3) / 4), dim3(CT), 0, st, ws, nblocks,
                      nslots, scale, grad);
   return hipGetLastError();
 }

@@ -313,6 +313,23 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits,
   }
 }
 
+// Small outputs with many splits: one wave per element, lanes over the splits
+// (a fixed tree order), so the sum is not a chain of `splits` dependent loads.
+__global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int splits, int epi) {
+  const size_t MN = (size_t)p.M * p.N;
+  const size_t idx = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (idx >= MN) return;
+  float v = 0.f;
+  for (int s = lane; s < splits; s += 64) v += p.ws[s * MN + idx];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if (lane == 0) {
+    const int row = (int)(idx / p.N), col = (int)(idx % p.N);
+    p.C[(size_t)row * p.ldc + col] = epilogue(v, epi, p, row, col);
+  }
+}
+
 template <int R, bool AK, bool BKC, int EPI>
 static hipError_t launch_t(bool vec, const GemmArgs &a, int tm, int tn, int splits, int kchunk,
                            hipStream_t s) {
@@ -378,8 +395,13 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
                      : launch_r<64>(ta, tb, epi, vec, a, splits, kchunk, s);
   if (e != hipSuccess || splits <= 1) return e;
   const size_t MN = (size_t)a.M * a.N;
-  const unsigned blocks = (unsigned)std::min<size_t>((MN + NT - 1) / NT, 4096);
-  hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+  if (splits >= 16 && MN <= 65536) {
+    const unsigned blocks = (unsigned)((MN + NT / 64 - 1) / (NT / 64));
+    hipLaunchKernelGGL(gemm_splitk_reduce_wave, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+  } else {
+    const unsigned blocks = (unsigned)std::min<size_t>((MN + NT - 1) / NT, 4096);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+  }
   return hipGetLastError();
 }
 

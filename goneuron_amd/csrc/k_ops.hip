@@ -372,12 +372,15 @@ __global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict_
           v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
         }
         const int m = min(32, n - i0);
-        for (int q = 0; q < m; ++q) {
-          local += v[q];
-          if (--left == 0 || base + i0 + q + 1 == B) {  // end of a worker chunk
-            total += local;
-            local = 0.f;
-            left = chunk;
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {  // fully unrolled: v[] stays in registers
+          if (q < m) {
+            local += v[q];
+            if (--left == 0 || base + i0 + q + 1 == B) {  // end of a worker chunk
+              total += local;
+              local = 0.f;
+              left = chunk;
+            }
           }
         }
       }
