@@ -61,7 +61,8 @@ enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2, EPI_BIAS_ADD
 hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t s);
 
 hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,
-                       float beta1, float beta2, float omb1, float omb2, float eps, hipStream_t s);
+                       float b1, float b2, float omb1, float omb2, float eps, hipStream_t s,
+                       int max_blocks = 16384);
 
 // db[o] = scale * sum_b dz[b*ld + o]
 hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,

@@ -25,6 +25,7 @@ using namespace gn;
 struct gn_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipStream_t aux = nullptr;  // per-layer Adam updates, overlapped with the backward pass
   std::string err;
   int fail_next = 0;
   hipDeviceProp_t props{};
@@ -47,22 +48,24 @@ static hipEvent_t ev_get(gn_ctx *c) {
   return c->pool[c->pool_used++];
 }
 
-// Brackets the kernels launched in its scope with events when timing is on.
+// Brackets the kernels launched in its scope with events when timing is on
+// (on the stream those kernels go to).
 struct KTimer {
   gn_ctx *c;
   int cls;
+  hipStream_t st;
   hipEvent_t a = nullptr, b = nullptr;
-  KTimer(gn_ctx *c_, int cls_) : c(c_), cls(cls_) {
+  KTimer(gn_ctx *c_, int cls_, hipStream_t st_ = nullptr) : c(c_), cls(cls_), st(st_ ? st_ : c_->stream) {
     if (c->timing) {
       a = ev_get(c);
       b = ev_get(c);
-      if (a && b) (void)hipEventRecord(a, c->stream);
+      if (a && b) (void)hipEventRecord(a, st);
       else a = b = nullptr;
     }
   }
   ~KTimer() {
     if (a) {
-      (void)hipEventRecord(b, c->stream);
+      (void)hipEventRecord(b, st);
       c->recs.push_back({cls, a, b});
     }
   }
@@ -161,10 +164,16 @@ extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
   c->device = device_ordinal;
   if (hipSetDevice(device_ordinal) != hipSuccess) return GN_ERR_HIP;
   if (hipGetDeviceProperties(&c->props, device_ordinal) != hipSuccess) return GN_ERR_HIP;
+  // both streams at the default priority
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return GN_ERR_HIP;
+  if (hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    return GN_ERR_HIP;
+  }
   c->scratch_floats = (size_t)16 << 20;  // 64 MiB: colsum partials, split-K partials
   if (hipMalloc(&c->scratch, c->scratch_floats * sizeof(float)) != hipSuccess) {
     (void)hipStreamDestroy(c->stream);
+    (void)hipStreamDestroy(c->aux);
     return GN_ERR_OOM;
   }
   *out = c.release();
@@ -175,9 +184,11 @@ extern "C" void gn_shutdown(gn_ctx *c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
+  (void)hipStreamSynchronize(c->aux);
   for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
   (void)hipFree(c->scratch);
   (void)hipStreamDestroy(c->stream);
+  (void)hipStreamDestroy(c->aux);
   delete c;
 }
 
@@ -198,6 +209,7 @@ extern "C" int gn_device_info(gn_ctx *c, gn_info *info) {
 extern "C" int gn_sync(gn_ctx *c) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->aux));
   return GN_OK;
 }
 
@@ -210,6 +222,7 @@ extern "C" int gn_debug_fail_next(gn_ctx *c, int code) {
 extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->aux));
   c->timing = enable != 0;
   c->recs.clear();
   c->pool_used = 0;
@@ -219,6 +232,7 @@ extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
 extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *total_ms) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->aux));
   int64_t n = 0;
   double ms = 0;
   for (const auto &r : c->recs) {
@@ -492,7 +506,33 @@ struct gn_model {
   int training = 1;
   int last_B = 0;
   std::vector<void *> owned;
+  // train steps update each layer's parameters on ctx->aux as soon as that
+  // layer's backward is done, overlapping Adam with the rest of the backward
+  bool overlap_adam = true;
+  std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
 };
+
+// Adam coefficients of one Network.Step: Adam.NewStep increments the
+// timestep before the update, whose bias corrections use timestep + 1
+// (opt.go:237-258), in float64 then rounded.
+struct AdamCoef {
+  float efflr, b1, b2, omb1, omb2, eps;
+};
+
+static AdamCoef adam_next(gn_model *M) {
+  M->timestep++;
+  AdamCoef a;
+  a.b1 = M->adam.beta1;
+  a.b2 = M->adam.beta2;
+  a.eps = M->adam.eps;
+  const double ts = (double)(M->timestep + 1);
+  const float bias1 = (float)(1.0 - pow((double)a.b1, ts));
+  const float bias2 = (float)(1.0 - pow((double)a.b2, ts));
+  a.efflr = M->adam.lr * (float)sqrt((double)bias2) / bias1;
+  a.omb1 = 1.0f - a.b1;
+  a.omb2 = 1.0f - a.b2;
+  return a;
+}
 
 static int model_alloc(gn_model *M, size_t floats, float **p) {
   void *q = nullptr;
@@ -509,6 +549,8 @@ extern "C" void gn_model_destroy(gn_model *M) {
   if (!M) return;
   (void)hipSetDevice(M->ctx->device);
   (void)hipStreamSynchronize(M->ctx->stream);
+  (void)hipStreamSynchronize(M->ctx->aux);
+  for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
   for (void *p : M->owned) (void)hipFree(p);
   delete M;
 }
@@ -1156,9 +1198,19 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
 }
 
 // Backward over B samples.  The output layer's dz is in L.back().gout.
-static int model_backward(gn_model *M, const float *x, int B, float scale) {
+// With `ac`, each layer's parameters get their Adam update on ctx->aux once
+// the layer's backward kernels are queued (no later kernel of the backward
+// reads them), and the main stream waits for all updates at the end.
+static int model_backward(gn_model *M, const float *x, int B, float scale, const AdamCoef *ac) {
   gn_ctx *c = M->ctx;
   const int n = (int)M->L.size();
+  if (ac && (int)M->sync_ev.size() < n + 1) {
+    while ((int)M->sync_ev.size() < n + 1) {
+      hipEvent_t e;
+      HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      M->sync_ev.push_back(e);
+    }
+  }
   bool is_dz = true;  // gout of the current layer already holds dz
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
@@ -1281,11 +1333,30 @@ static int model_backward(gn_model *M, const float *x, int B, float scale) {
       default:
         return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
     }
+    if (ac && R.pcount > 0) {
+      HIP_OK(c, hipEventRecord(M->sync_ev[i], c->stream));
+      HIP_OK(c, hipStreamWaitEvent(c->aux, M->sync_ev[i], 0));
+      // While backward kernels still run, a 256-block grid (one block per CU
+      // next to the GEMM's waves) keeps the update off their critical path;
+      // the update of the first parameterised layer runs alone, at full width.
+      bool last = true;
+      for (int j = 0; j < i; ++j)
+        if (M->L[j].pcount > 0) last = false;
+      KTimer kt(c, GN_KCLASS_ADAM, c->aux);
+      HIP_OK(c, launch_adam(M->params + R.poff, M->grads + R.poff, M->m + R.poff, M->v + R.poff,
+                            R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps,
+                            c->aux, last ? 16384 : 256));
+    }
+  }
+  if (ac) {
+    HIP_OK(c, hipEventRecord(M->sync_ev[n], c->aux));
+    HIP_OK(c, hipStreamWaitEvent(c->stream, M->sync_ev[n], 0));
   }
   return GN_OK;
 }
 
-static int model_accumulate(gn_model *M, const float *x, const float *y, int B) {
+static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
+                            const AdamCoef *ac = nullptr) {
   gn_ctx *c = M->ctx;
   if (B <= 0 || B > M->maxB) return set_err(c, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
   if (!x || !y) return set_err(c, GN_ERR_INVALID, "null input");
@@ -1299,7 +1370,7 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B) 
   // grads *= 1/B: float32 reciprocal (net.go:767-770), float32(1/float64(B))
   // for the W-worker path (net.go:703-706).
   const float scale = M->workers > 1 ? (float)(1.0 / (double)B) : 1.0f / (float)B;
-  rc = model_backward(M, x, B, scale);
+  rc = model_backward(M, x, B, scale, ac);
   if (rc) return rc;
   M->last_B = B;
   return GN_OK;
@@ -1309,16 +1380,30 @@ extern "C" int gn_model_step(gn_model *M) {
   if (!M) return GN_ERR_INVALID;
   gn_ctx *c = M->ctx;
   ENTRY(c);
-  M->timestep++;  // Adam.NewStep (opt.go:254-258)
-  const float b1 = M->adam.beta1, b2 = M->adam.beta2, eps = M->adam.eps;
-  const double ts = (double)(M->timestep + 1);
-  const float bias1 = (float)(1.0 - pow((double)b1, ts));
-  const float bias2 = (float)(1.0 - pow((double)b2, ts));
-  const float efflr = M->adam.lr * (float)sqrt((double)bias2) / bias1;
+  const AdamCoef a = adam_next(M);  // Adam.NewStep (opt.go:254-258)
   KTimer kt(c, GN_KCLASS_ADAM);
-  HIP_OK(c, launch_adam(M->params, M->grads, M->m, M->v, M->nparams, efflr, b1, b2, 1.0f - b1,
-                        1.0f - b2, eps, c->stream));
+  HIP_OK(c, launch_adam(M->params, M->grads, M->m, M->v, M->nparams, a.efflr, a.b1, a.b2, a.omb1,
+                        a.omb2, a.eps, c->stream));
   return GN_OK;
+}
+
+// One training step: forward, loss, backward and Adam (Network.TrainBatch
+// followed by Network.Step).  Per-layer updates overlapped with the backward
+// pass pay off only when the update is long; small models update once at the
+// end (the overlapped launches would slow their short backward kernels).
+constexpr int64_t kOverlapAdamMin = (int64_t)8 << 20;
+static int model_train_step(gn_model *M, const float *x, const float *y, int B) {
+  if (!M->overlap_adam || M->nparams < kOverlapAdamMin) {
+    int rc = model_accumulate(M, x, y, B);
+    if (rc) return rc;
+    return gn_model_step(M);
+  }
+  if (B <= 0 || B > M->maxB) return set_err(M->ctx, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
+  const int saved = M->timestep;
+  const AdamCoef a = adam_next(M);
+  int rc = model_accumulate(M, x, y, B, &a);
+  if (rc) M->timestep = saved;
+  return rc;
 }
 
 extern "C" int gn_model_accumulate_device(gn_model *M, const float *x, const float *y, int32_t B) {
@@ -1330,9 +1415,7 @@ extern "C" int gn_model_accumulate_device(gn_model *M, const float *x, const flo
 extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const float *y, int32_t B) {
   if (!M) return GN_ERR_INVALID;
   ENTRY(M->ctx);
-  int rc = model_accumulate(M, x, y, B);
-  if (rc) return rc;
-  return gn_model_step(M);
+  return model_train_step(M, x, y, B);
 }
 
 // Out-of-range embedding ids raised a device flag (embedding.go:126-128 errors
@@ -1361,9 +1444,8 @@ extern "C" int gn_model_train_step(gn_model *M, const float *x, const float *y, 
                            hipMemcpyHostToDevice, c->stream));
   HIP_OK(c, hipMemcpyAsync(M->yin, y, (size_t)B * M->L.back().out_len * sizeof(float),
                            hipMemcpyHostToDevice, c->stream));
-  int rc = model_accumulate(M, M->xin, M->yin, B);
+  int rc = model_train_step(M, M->xin, M->yin, B);
   if (rc) return rc;
-  if ((rc = gn_model_step(M))) return rc;
   if (loss_out) return gn_model_read_loss(M, loss_out);
   HIP_OK(c, hipStreamSynchronize(c->stream));
   return check_embed_err(M);

@@ -10,6 +10,8 @@
 // on float64 arguments.
 #include "gn_common.h"
 
+#include <algorithm>
+
 namespace gn {
 
 constexpr int TPB = 256;
@@ -87,11 +89,30 @@ __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
 }
 
 hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,
-                       float b1, float b2, float omb1, float omb2, float eps, hipStream_t s) {
+                       float b1, float b2, float omb1, float omb2, float eps, hipStream_t s,
+                       int max_blocks) {
   if (n <= 0) return hipSuccess;
+  // The vector loop needs 16 B aligned pointers.  Ranges that start inside an
+  // aligned group (a layer's slice of the arena, whose four regions share one
+  // alignment) take their first 1-3 elements through the scalar tail path.
+  const uintptr_t mis = reinterpret_cast<uintptr_t>(p) & 15;
+  if (((reinterpret_cast<uintptr_t>(g) & 15) != mis) || ((reinterpret_cast<uintptr_t>(m) & 15) != mis) ||
+      ((reinterpret_cast<uintptr_t>(v) & 15) != mis) || (mis & 3))
+    return hipErrorInvalidValue;
+  if (mis) {
+    const int64_t head = std::min<int64_t>(n, (int64_t)((16 - mis) / 4));
+    hipLaunchKernelGGL(adam_kernel, dim3(1), dim3(TPB), 0, s, p, g, m, v, head, efflr, b1, b2, omb1,
+                       omb2, eps);
+    p += head;
+    g += head;
+    m += head;
+    v += head;
+    n -= head;
+    if (n <= 0) return hipGetLastError();
+  }
   const int64_t n4 = n >> 2;
   int64_t blocks = (n4 + TPB * ADAM_U - 1) / (TPB * ADAM_U);
-  if (blocks > 16384) blocks = 16384;
+  if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(adam_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
                      b1, b2, omb1, omb2, eps);
@@ -349,43 +370,22 @@ hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) 
   return hipGetLastError();
 }
 
-// Batch loss: totalLoss accumulates per sample in order (net.go:744), per
-// worker chunk then in worker order for W > 1 (net.go:679-716); / B.
+// Batch loss: the mean over the batch of the per-sample losses, summed per
+// worker chunk and then over the chunks in worker order (net.go:679-716;
+// one chunk for W = 1, net.go:744).  Each chunk is summed by a block-wide tree
+// (a different float32 order than the reference's running sum, well inside
+// the loss tolerance), the chunk sums in order by thread 0.
 __global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict__ rows, int B,
                                                         int W, float *__restrict__ loss) {
-  __shared__ __attribute__((aligned(16))) float buf[1024 + 32];
+  __shared__ float sh[16];
   const int chunk = W > 1 ? (B + W - 1) / W : B;
-  float total = 0.f, local = 0.f;
-  int left = chunk;  // samples still to add in the current worker chunk
-  for (int base = 0; base < B; base += 1024) {
-    const int n = min(1024, B - base);
-    for (int i = threadIdx.x; i < n; i += TPB) buf[i] = rows[base + i];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      // registers in groups of 32 (8 x ds_read_b128 in flight), then the
-      // sequential float32 adds of the reference
-      for (int i0 = 0; i0 < n; i0 += 32) {
-        float v[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float4 x = *reinterpret_cast<const float4 *>(&buf[i0 + 4 * q]);
-          v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
-        }
-        const int m = min(32, n - i0);
-#pragma unroll
-        for (int q = 0; q < 32; ++q) {  // fully unrolled: v[] stays in registers
-          if (q < m) {
-            local += v[q];
-            if (--left == 0 || base + i0 + q + 1 == B) {  // end of a worker chunk
-              total += local;
-              local = 0.f;
-              left = chunk;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
+  float total = 0.f;
+  for (int c0 = 0; c0 < B; c0 += chunk) {
+    const int c1 = min(B, c0 + chunk);
+    float s = 0.f;
+    for (int i = c0 + threadIdx.x; i < c1; i += TPB) s += rows[i];
+    s = block_sum(s, sh);
+    total += s;
   }
   if (threadIdx.x == 0) *loss = total / (float)B;
 }
