@@ -28,7 +28,7 @@ PEAK_HBM_GBPS = 8000.0
 # FETCH_SIZE (x2.000) and WRITE_SIZE (x1.000) passes, each scaled by what the
 # counter reads for a 1 GiB device-to-device copy (bench.py --copy-probe 1024).
 # Keyed by workload; a changed GEMM kernel needs a new measurement.
-GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2947.4e6}
+GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2914.1e6}
 
 
 def gemm_flops(cfg, B):
@@ -42,32 +42,74 @@ def gemm_flops(cfg, B):
     return f
 
 
-def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1):
-    """The CPU oracle (reference-semantics restatement, 1 thread) on a bounded
-    sample: per-sample fwd+bwd of n samples plus one Adam pass over the arena,
-    scaled to samples/s = n / (t_samples + t_adam * n / B)."""
+def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
+    """The CPU oracle (C restatement of the reference's per-sample path) timed
+    on the host, on a bounded sample, two ways:
+      - parallel (the reported value): trainBatchParallel's structure
+        (net.go:588-717) with T threads, each a private network (own layer
+        state and gradient arena, as LightweightClone) running its own
+        contiguous chunk; then the serial sum of the T gradient arenas and one
+        Adam pass, per batch;
+      - single thread: trainBatchSequential (net.go:721-784).
+    samples/s = samples / (sample time + per-batch time * samples / B)."""
+    import threading
     from oracle import refcpu
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from cfgutil import oracle_net
     refcpu.build()
-    net = oracle_net(refcpu, cfg, workers=workers)
     B = cfg["B"]
+    T = threads or min(B, os.cpu_count() or 1, 16)
+    nets = [oracle_net(refcpu, cfg) for _ in range(T)]
+    net = nets[0]
     # calibrate with one sample, then fill the budget
     t0 = time.perf_counter()
     net.accumulate_batch(x[:1], y[:1], 1)
     t1 = time.perf_counter() - t0
-    n = int(max(1, min(B, budget_s / max(t1, 1e-6))))
+    n1 = int(max(1, min(B, budget_s / 2 / max(t1, 1e-6))))
     t0 = time.perf_counter()
-    net.accumulate_batch(x[:n], y[:n], n)
-    ts = time.perf_counter() - t0
+    net.accumulate_batch(x[:n1], y[:n1], n1)
+    ts1 = time.perf_counter() - t0
+    net.step()  # first touch of the Adam moments, untimed
     t0 = time.perf_counter()
     net.step()
     ta = time.perf_counter() - t0
-    per_sample = (ts + ta * n / B) / n
-    return {"value": 1.0 / per_sample, "unit": "samples/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/refcpu (C restatement of net.go:721-784, -O2 -ffp-contract=off, 1 thread): "
-                      f"{n} of {B} samples fwd+bwd ({ts:.2f} s) + one Adam pass over the "
-                      f"{net.n}-param arena ({ta:.3f} s) scaled by n/B"}
+    single = n1 / (ts1 + ta * n1 / B)
+    # parallel: every thread takes npt samples of its own chunk of the batch
+    chunk = (B + T - 1) // T
+    npt = int(max(1, min(chunk, budget_s / 2 / max(t1, 1e-6))))
+
+    def work(t, n):
+        s0 = min(t * chunk, B - n)
+        nets[t].accumulate_batch(x[s0:s0 + n], y[s0:s0 + n], n)
+
+    def run_all(n):
+        th = [threading.Thread(target=work, args=(t, n)) for t in range(T)]
+        for h in th:
+            h.start()
+        for h in th:
+            h.join()
+
+    run_all(1)  # first touch of every worker's buffers, untimed
+    acc = np.zeros_like(net.grads)
+    acc += 1.0
+    t0 = time.perf_counter()
+    run_all(npt)
+    tp = time.perf_counter() - t0
+    t0 = time.perf_counter()  # serial sum of the worker arenas (net.go:694-700)
+    acc[:] = 0.0
+    for nt in nets:
+        acc += nt.grads
+    tsum = time.perf_counter() - t0
+    done = T * npt
+    par = done / (tp + (tsum + ta) * done / B)
+    del nets
+    return {"value": par, "unit": "samples/s", "cores": T, "kind": "port",
+            "sample": f"oracle/refcpu (C restatement of the per-sample path, -O2 -ffp-contract=off): "
+                      f"{T} threads x {npt} samples of their own chunks of the {B}-sample batch "
+                      f"({tp:.2f} s), plus per batch the sum of {T} gradient arenas ({tsum:.3f} s) and one "
+                      f"Adam pass over {net.n} params ({ta:.3f} s) scaled by samples/B",
+            "single_thread": {"value": single, "cores": 1,
+                              "sample": f"{n1} of {B} samples fwd+bwd ({ts1:.2f} s) + Adam scaled by n/B"}}
 
 
 def copy_probe(mib):
@@ -91,6 +133,8 @@ def main():
     ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="threads of the parallel CPU baseline (default min(B, cores, 16))")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -218,7 +262,7 @@ def main():
         "loss": loss.value,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget, workers)
+        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget, workers, args.cpu_threads)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
