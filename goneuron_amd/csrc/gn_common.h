@@ -120,6 +120,7 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
 hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
                            const float *Wh, const float *bias, float *D, int B, int T, int H,
                            hipStream_t s);
+int lstm_gram_pitch(int n);
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
                                     double *coef, float *w, int B, int T, int I, int H, int W,
                                     hipStream_t s);

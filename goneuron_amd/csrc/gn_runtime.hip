@@ -849,7 +849,8 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), Bm * 4 * H, &R.S))) return rc;
       if ((rc = model_alloc(M.get(), Bm * (T + 1), &R.wts))) return rc;
       const int Wc = std::min(std::max(M->workers, 1), max_batch);
-      const size_t chunk = (max_batch + Wc - 1) / Wc, nmax = chunk * T;
+      const size_t chunk = (max_batch + Wc - 1) / Wc;
+      const size_t nmax = (size_t)lstm_gram_pitch((int)(chunk * T));
       const size_t nchains = (max_batch + chunk - 1) / chunk;
       float *g = nullptr, *cf = nullptr;
       if ((rc = model_alloc(M.get(), 2 * nchains * nmax * nmax, &g))) return rc;

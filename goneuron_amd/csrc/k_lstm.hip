@@ -63,15 +63,65 @@ __device__ __forceinline__ float dot_strided(const float *__restrict__ W, int st
   return s;
 }
 
+// The same for four consecutive columns at once (16-byte loads: a CU streams
+// L2-resident weights about twice as fast with dwordx4 as with dword loads).
+template <int U>
+__device__ __forceinline__ float4 dot4_strided(const float4 *__restrict__ W, int stride4,
+                                               const float *v, int j0, int j1) {
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  int j = j0;
+  for (; j + U <= j1; j += U) {
+    float4 w[U];
+#pragma unroll
+    for (int e = 0; e < U; ++e) w[e] = W[(size_t)(j + e) * stride4];
+#pragma unroll
+    for (int e = 0; e < U; ++e) {
+      const float x = v[j + e];
+      s.x += w[e].x * x;
+      s.y += w[e].y * x;
+      s.z += w[e].z * x;
+      s.w += w[e].w * x;
+    }
+  }
+  for (; j < j1; ++j) {
+    const float4 w = W[(size_t)j * stride4];
+    const float x = v[j];
+    s.x += w.x * x;
+    s.y += w.y * x;
+    s.z += w.z * x;
+    s.w += w.w * x;
+  }
+  return s;
+}
+
+// Recurrent mat-vec of one step: part[q][c] = sum over the q-th share of k of
+// W[k][c] * v[k] (W is K x H row-major).  V4: thread (g, q) owns columns
+// 4g..4g+3 (H % 4 == 0, W 16-byte aligned); otherwise thread (i, q) owns
+// column i.  GB = threads per share (a multiple of 64), NQ shares.
+template <bool V4>
+__device__ __forceinline__ void step_matvec(const float *__restrict__ W, const float *v, int K,
+                                            int H, int GB, int NQ, float *part) {
+  const int c = threadIdx.x % GB, q = threadIdx.x / GB;
+  if (q >= NQ) return;
+  const int k0 = (K * q) / NQ, k1 = (K * (q + 1)) / NQ;
+  if (V4) {
+    if (4 * c < H) {
+      const float4 s = dot4_strided<16>(reinterpret_cast<const float4 *>(W) + c, H / 4, v, k0, k1);
+      *reinterpret_cast<float4 *>(part + q * H + 4 * c) = s;
+    }
+  } else if (c < H) {
+    part[q * H + c] = dot_strided<32>(W + c, H, v, k0, k1);
+  }
+}
+
 // Forward over T steps, one workgroup per sample.  xw [B][T][H] holds the
 // input-gate x projections x_t . Wx_i (one GEMM before the recurrence), so a
-// step only needs Wh_i h_{t-1}: NQ threads per hidden unit (up to LSTM_Q)
-// split that dot product and add their partials through LDS.
-// WhT [H][H] is the transposed input-gate block of Wh.
+// step only needs Wh_i h_{t-1}, split over NQ shares of j and summed in LDS.
+// WhT [H][H] is the transposed input-gate block of Wh.  Thread i < H owns
+// hidden unit i's state.
 // Saves ig = sigmoid(pre_i), tc = tanh(c), c [B][T][H] and hbuf [B][T+1][H]
 // (hbuf[b][0] = 0, hbuf[b][t+1] = h_t), and writes h_{T-1} to out [B][H].
-constexpr int LSTM_Q = 4;
-
+template <bool V4>
 __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict__ xw,
                                                         const float *__restrict__ WhT,
                                                         const float *__restrict__ bias,
@@ -80,13 +130,12 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
                                                         float *__restrict__ cbuf,
                                                         float *__restrict__ hbuf,
                                                         float *__restrict__ out, int T, int H,
-                                                        int HB, int NQ) {
+                                                        int GB, int NQ) {
   extern __shared__ float sm[];
-  float *hs = sm, *part = sm + H;  // part[NQ][HB]
+  float *hs = sm, *part = sm + ((H + 3) & ~3);  // part[NQ][H], 16-byte aligned
   const int b = blockIdx.x;
-  const int i = threadIdx.x % HB, q = threadIdx.x / HB;
-  const bool act = i < H, own = act && q == 0;
-  const int jh0 = (H * q) / NQ, jh1 = (H * (q + 1)) / NQ;
+  const int i = threadIdx.x;
+  const bool own = i < H;
   const float *xwb = xw + (size_t)b * T * H;
   float bi = 0.f, fg = 0.f, gg = 0.f, og = 0.f, xwn = 0.f;
   if (own) {
@@ -103,11 +152,11 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
   for (int t = 0; t < T; ++t) {
     const float xwc = xwn;
     if (own && t + 1 < T) xwn = xwb[(size_t)(t + 1) * H + i];  // next step's, in flight
-    if (act) part[q * HB + i] = dot_strided<32>(WhT + i, H, hs, jh0, jh1);
+    step_matvec<V4>(WhT, hs, H, H, GB, NQ, part);
     __syncthreads();
     if (own) {
       float sh = 0.f;
-      for (int r = 0; r < NQ; ++r) sh += part[r * HB + i];
+      for (int r = 0; r < NQ; ++r) sh += part[r * H + i];
       const float a = (bi + xwc) + sh;  // bias, then Wx x, then Wh h (lstm.go:1065-1101)
       const size_t o = ((size_t)b * T + t) * H + i;
       const float ig = sigm(a);
@@ -127,9 +176,10 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
 
 // BPTT deltas, one workgroup per sample.  gh = dL/dh_{T-1} [B][H].
 // D [B][T+1][4H]: row t = (dI, dF, dC, dO) of step t; row T = 0 (padding that
-// lines D up with hbuf for the dWh GEMM).  dhPrev = Wh^T dG is split over
-// NQ threads per unit (a 1/NQ share of the 4H rows each) and summed in LDS;
-// the saved gate values of step t-1 are fetched while step t runs.
+// lines D up with hbuf for the dWh GEMM).  dhPrev = Wh^T dG is split over NQ
+// shares of the 4H rows and summed in LDS; the saved gate values of step t-1
+// are fetched while step t runs.  Thread i < H owns hidden unit i.
+template <bool V4>
 __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict__ gh,
                                                         const float *__restrict__ igb,
                                                         const float *__restrict__ tcb,
@@ -137,14 +187,13 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
                                                         const float *__restrict__ Wh,
                                                         const float *__restrict__ bias,
                                                         float *__restrict__ D, int T, int H,
-                                                        int HB, int NQ) {
-  extern __shared__ float dG[];  // 4H, then part[NQ][HB]
+                                                        int GB, int NQ) {
+  extern __shared__ float dG[];  // 4H, then part[NQ][H]
   float *part = dG + 4 * H;
   const int b = blockIdx.x;
-  const int i = threadIdx.x % HB, q = threadIdx.x / HB;
-  const bool act = i < H, own = act && q == 0;
+  const int i = threadIdx.x;
+  const bool own = i < H;
   const int G4 = 4 * H;
-  const int k0 = (G4 * q) / NQ, k1 = (G4 * (q + 1)) / NQ;
   float *Db = D + (size_t)b * (T + 1) * G4;
   for (int k = threadIdx.x; k < G4; k += blockDim.x) Db[(size_t)T * G4 + k] = 0.f;
   float cur = own ? gh[(size_t)b * H + i] : 0.f, dcn = 0.f;
@@ -188,11 +237,11 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
       row[3 * H + i] = dO;
     }
     __syncthreads();
-    if (act) part[q * HB + i] = dot_strided<32>(Wh + i, H, dG, k0, k1);
+    step_matvec<V4>(Wh, dG, G4, H, GB, NQ, part);
     __syncthreads();
     if (own) {
       float s = 0.f;
-      for (int r = 0; r < NQ; ++r) s += part[r * HB + i];
+      for (int r = 0; r < NQ; ++r) s += part[r * H + i];
       cur += s;
     }
   }
@@ -314,20 +363,134 @@ __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict_
       }
 }
 
+// The same Gram with 16-byte staging loads, 32-wide K stages and the next
+// stage prefetched into registers while the current one runs on MFMA (H % 8
+// == 0, I % 4 == 0 and 16-byte aligned rows).  K runs over [dG | hPrev | x_last]:
+// the first 4H go to the dG accumulators, the rest (zero padded to a multiple
+// of 32) to the [x | hPrev] ones.
+__device__ __forceinline__ float4 gram_row4(const float *__restrict__ D,
+                                            const float *__restrict__ hbuf,
+                                            const float *__restrict__ x, int b, int t, int T,
+                                            int I, int H, int k) {
+  const int G4 = 4 * H;
+  if (k < G4) return *reinterpret_cast<const float4 *>(D + ((size_t)b * (T + 1) + t) * G4 + k);
+  k -= G4;
+  if (k < H) return *reinterpret_cast<const float4 *>(hbuf + ((size_t)b * (T + 1) + t) * H + k);
+  k -= H;
+  if (k < I) return *reinterpret_cast<const float4 *>(x + ((size_t)b * T + T - 1) * I + k);
+  return make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restrict__ D,
+                                                           const float *__restrict__ hbuf,
+                                                           const float *__restrict__ x,
+                                                           double *__restrict__ Gm, ChainMap cm,
+                                                           int I, int H, int nmax) {
+  constexpr int KS = 32;
+  __shared__ double sv[KS][64], su[KS][64];
+  const int ch = blockIdx.y;
+  const int n = cm.len(ch);
+  int lin = blockIdx.x, tv = 0;
+  while (lin > tv) {
+    lin -= tv + 1;
+    ++tv;
+  }
+  const int tu = lin;
+  if (tv >= (n + 63) / 64) return;  // whole block leaves before any barrier
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int G4 = 4 * H;
+  const int Kz = G4 + ((H + I + KS - 1) / KS) * KS;  // padded K
+  // staging: thread -> row rr (0..63), float4 column groups kq and kq + 16
+  const int rr = tid >> 2, kq = (tid & 3) * 4;
+  const int iv = tv * 64 + rr, iu = tu * 64 + rr;
+  const bool okv = iv < n, oku = iu < n;
+  int bv = 0, tvv = 0, bu = 0, tuu = 0;
+  if (okv) cm.at(ch, iv, bv, tvv);
+  if (oku) cm.at(ch, iu, bu, tuu);
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 rv[2], ru[2];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = k0 + kq + 16 * h;
+      rv[h] = okv ? gram_row4(D, hbuf, x, bv, tvv, cm.T, I, H, k) : z4;
+      ru[h] = oku ? gram_row4(D, hbuf, x, bu, tuu, cm.T, I, H, k) : z4;
+    }
+  };
+  d4v acc[2][2][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[q][i][j] = d4v{0.0, 0.0, 0.0, 0.0};
+  load(0);
+  for (int k0 = 0; k0 < Kz; k0 += KS) {
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kk = kq + 16 * h;
+      sv[kk][rr] = rv[h].x; sv[kk + 1][rr] = rv[h].y; sv[kk + 2][rr] = rv[h].z; sv[kk + 3][rr] = rv[h].w;
+      su[kk][rr] = ru[h].x; su[kk + 1][rr] = ru[h].y; su[kk + 2][rr] = ru[h].z; su[kk + 3][rr] = ru[h].w;
+    }
+    __syncthreads();
+    if (k0 + KS < Kz) load(k0 + KS);  // next stage in flight during the MFMAs
+    const int q = k0 < G4 ? 0 : 1;
+#pragma unroll
+    for (int ks = 0; ks < KS / 4; ++ks) {
+      const int k = ks * 4 + (lane >> 4);
+      double av[2], bvv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = su[k][wm * 32 + i * 16 + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bvv[j] = sv[k][wn * 32 + j * 16 + (lane & 15)];
+      if (q == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[0][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bvv[j], acc[0][i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[1][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bvv[j], acc[1][i][j], 0, 0, 0);
+      }
+    }
+  }
+  double *Gc = Gm + (size_t)ch * nmax * nmax;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = tu * 64 + wm * 32 + i * 16 + 4 * r + (lane >> 4);
+        const int v = tv * 64 + wn * 32 + j * 16 + (lane & 15);
+        if (v < n && u <= v) Gc[(size_t)u * nmax + v] = acc[0][i][j][r] * (acc[1][i][j][r] + 1.0);
+      }
+}
+
 // Sequential clip of one chain from its Gram matrix; one workgroup per chain.
 // With a_u = 1/P_{u-1} (P_v = c_0 ... c_v) the clipped sum is G_v = P_v sum_{u<=v} a_u D_u,
 // and step v needs s_v = sum_{u<v} a_u <D_u,D_v>:
 //   N^2 = |G|^2 + 2 P s_v + <D_v,D_v>,  c = N > 1 ? 1/N : 1 (clipGradients),
 //   P *= c,  a_v = c / P,  |G|^2 = c^2 N^2.
-// Blocked by CLIP_BLK steps: the part of s_v from earlier blocks is a matrix-
-// vector product that all waves compute; the in-block recursion runs in wave 0
-// with lane r holding row r's running s and the block's Gram tile in LDS, so a
-// step costs a few lane reads and one fused update instead of a block-wide
-// reduction.  Whenever P falls below 1e-150 the coefficients are rescaled by P
-// (exact: everything is linear in the a's), in-block at once and for earlier
-// blocks at the end of the block.
+// Blocked by CLIP_BLK steps: the in-block recursion runs in wave 0 with lane r
+// holding row r's running s and the block's Gram tile in LDS, so a step costs a
+// few lane reads and one fused update instead of a block-wide reduction; while
+// it runs, waves 1-15 compute the next block's share of s from all earlier
+// blocks (a matrix-vector product over the Gram columns) and stage its tiles,
+// and the current block's own share is added from a 64x64 cross tile after.
+// Whenever P falls below 1e-150 the coefficients are rescaled by P (exact:
+// everything is linear in the a's), in-block at once and for earlier blocks
+// (and the next block's partial s) at the end of the block.
 constexpr int CLIP_BLK = 64;
-constexpr int CLIP_UNR = 8;
+constexpr int CLIP_UNR = 16;
+constexpr int CLIP_NT = 1024;               // wave 0: recursion; waves 1..15: next block
+constexpr int CLIP_NS = (CLIP_NT - 64) / 32;  // shares of the next block's matrix-vector product
 
 __device__ __forceinline__ double readlane_d(double x, int l) {
   const int lo = __builtin_amdgcn_readlane(__double2loint(x), l);
@@ -335,74 +498,62 @@ __device__ __forceinline__ double readlane_d(double x, int l) {
   return __hiloint2double(hi, lo);
 }
 
-__global__ __launch_bounds__(256) void lstm_clip_kernel(const double *__restrict__ Gm,
+__global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__restrict__ Gm,
                                                         double *__restrict__ a,
                                                         float *__restrict__ w, ChainMap cm,
                                                         int nmax) {
-  __shared__ double tile[CLIP_BLK][CLIP_BLK + 1];  // tile[u][r] = <D_{v0+u}, D_{v0+r}>, u <= r
-  __shared__ double sold[CLIP_BLK], part4[4][CLIP_BLK];
-  __shared__ double bcast[2];                       // P at the end, pending rescale factor
+  // tile[buf][u][r] = <D_{v0+u}, D_{v0+r}> (u <= r) of the current / next block;
+  // cross[u][r] = <D_{v0+u}, D_{v1+r}>: current block rows x next block columns
+  __shared__ double tile[2][CLIP_BLK][CLIP_BLK + 1];
+  __shared__ double cross[CLIP_BLK][CLIP_BLK + 1];
+  __shared__ double sold[CLIP_BLK], partq[CLIP_NS][CLIP_BLK], ablk[CLIP_BLK];
+  __shared__ double bcast[2];  // P after the block, rescale applied during the block
   const int ch = blockIdx.x;
   const int n = cm.len(ch);
   const double *G = Gm + (size_t)ch * nmax * nmax;  // GT[u][v]
   double *ac = a + (size_t)ch * nmax;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  double P = 1.0, Q = 1.0, nrm2 = 0.0;  // wave 0 only; Q = 1/P
-  for (int v0 = 0; v0 < n; v0 += CLIP_BLK) {
-    const int nb = min(CLIP_BLK, n - v0);
-    __syncthreads();
-    // s from earlier blocks: sold[r] = sum_{u < v0} a_u GT[u][v0 + r]; thread
-    // (r, q) takes u = q mod 4 with CLIP_UNR loads in flight, then the four
-    // partials are added in LDS
-    {
-      const int r = lane, q = wv;
-      double s = 0.0;
-      if (r < nb) {
-        const double *col = G + v0 + r;
-        int u = q;
-        for (; u + 4 * (CLIP_UNR - 1) < v0; u += 4 * CLIP_UNR) {
-          double gv[CLIP_UNR], av[CLIP_UNR];
-#pragma unroll
-          for (int e = 0; e < CLIP_UNR; ++e) {
-            gv[e] = col[(size_t)(u + 4 * e) * nmax];
-            av[e] = ac[u + 4 * e];
-          }
-#pragma unroll
-          for (int e = 0; e < CLIP_UNR; ++e) s += av[e] * gv[e];
-        }
-        for (; u < v0; u += 4) s += ac[u] * col[(size_t)u * nmax];
-      }
-      part4[q][r] = s;
-    }
-    for (int e = threadIdx.x; e < CLIP_BLK * CLIP_BLK; e += 256) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int nblk = (n + CLIP_BLK - 1) / CLIP_BLK;
+  {
+    const int nb0 = min(CLIP_BLK, n);
+    for (int e = tid; e < CLIP_BLK * CLIP_BLK; e += CLIP_NT) {
       const int u = e / CLIP_BLK, r = e % CLIP_BLK;
-      tile[u][r] = (r < nb && u <= r) ? G[(size_t)(v0 + u) * nmax + v0 + r] : 0.0;
+      tile[0][u][r] = (r < nb0 && u <= r) ? G[(size_t)u * nmax + r] : 0.0;
     }
-    __syncthreads();
-    if (threadIdx.x < CLIP_BLK)
-      sold[threadIdx.x] = (part4[0][threadIdx.x] + part4[1][threadIdx.x]) +
-                          (part4[2][threadIdx.x] + part4[3][threadIdx.x]);
-    __syncthreads();
+    if (tid < CLIP_BLK) sold[tid] = 0.0;
+    if (tid == 0) bcast[0] = 1.0;
+  }
+  __syncthreads();
+  double P = 1.0, Q = 1.0, nrm2 = 0.0;  // wave 0 only; Q = 1/P
+  for (int k = 0; k < nblk; ++k) {
+    const int v0 = k * CLIP_BLK, nb = min(CLIP_BLK, n - v0);
+    const int v1 = v0 + CLIP_BLK, nb1 = k + 1 < nblk ? min(CLIP_BLK, n - v1) : 0;
     if (wv == 0) {
       // Per step only the norm recursion is serial: a_j = 1/P_{j-1} = Q is
       // known when the step starts, so the running-s update of the later rows
       // overlaps it, and 1/N comes from a refined reciprocal square root.
+      double(*T)[CLIP_BLK + 1] = tile[k & 1];
       double sl = lane < nb ? sold[lane] : 0.0;  // running s of row v0 + lane
       double al = 0.0;                            // a_{v0 + lane} once known
       double blkscale = 1.0;
+      double tjl = T[0][lane], tjj = T[0][0];    // step j's tile values, read a step early
       for (int j = 0; j < nb; ++j) {
+        double tnl = 0.0, tnj = 0.0;
+        if (j + 1 < nb) {
+          tnl = T[j + 1][lane];
+          tnj = T[j + 1][j + 1];
+        }
         const double aj = Q;
         const double sj = readlane_d(sl, j);
-        if (lane == j) al = aj;
-        if (lane > j) sl += aj * tile[j][lane];
-        const double N2 = nrm2 + 2.0 * P * sj + tile[j][j];
-        if (N2 > 1.0) {  // clipGradients: scale by 1/N
+        al = lane == j ? aj : al;
+        sl = lane > j ? fma(aj, tjl, sl) : sl;
+        const double N2 = fma(2.0 * P, sj, nrm2) + tjj;
+        if (N2 > 1.0) {  // clipGradients: scale by 1/N (rsq + one Newton step)
           double y = __builtin_amdgcn_rsq(N2);
-          y = y * (1.5 - 0.5 * N2 * y * y);
-          y = y * (1.5 - 0.5 * N2 * y * y);
+          y = y * (1.5 - 0.5 * N2 * (y * y));
           P *= y;
           Q *= N2 * y;
-          nrm2 = y * y * N2;
+          nrm2 = (y * y) * N2;
         } else {
           nrm2 = N2 > 0.0 ? N2 : 0.0;
         }
@@ -413,21 +564,71 @@ __global__ __launch_bounds__(256) void lstm_clip_kernel(const double *__restrict
           Q *= P;
           P = 1.0;
         }
+        tjl = tnl;
+        tjj = tnj;
       }
+      ablk[lane] = lane < nb ? al : 0.0;
       if (lane < nb) ac[v0 + lane] = al;
       if (lane == 0) {
         bcast[0] = P;
         bcast[1] = blkscale;
       }
+    } else if (nb1 > 0) {
+      // meanwhile the other three waves prepare the next block: the part of
+      // its s from blocks before this one (a's final up to this block's
+      // rescale, applied below), its diagonal tile and the cross tile
+      // thread (pair of rows 2p, 2p+1; share q of CLIP_NS) reads 16-byte pairs
+      const int t = tid - 64, pr = t & 31, q = t >> 5;
+      double s0 = 0.0, s1 = 0.0;
+      if (2 * pr < nb1) {
+        const double2 *col = reinterpret_cast<const double2 *>(G + v1 + 2 * pr);
+        const int ld2 = nmax / 2;  // nmax is even (the Gram's pitch)
+        constexpr int S = CLIP_NS;
+        int u = q;
+        for (; u + S * (CLIP_UNR - 1) < v0; u += S * CLIP_UNR) {
+          double2 gv[CLIP_UNR];
+          double av[CLIP_UNR];
+#pragma unroll
+          for (int e = 0; e < CLIP_UNR; ++e) {
+            gv[e] = col[(size_t)(u + S * e) * ld2];
+            av[e] = ac[u + S * e];
+          }
+#pragma unroll
+          for (int e = 0; e < CLIP_UNR; ++e) {
+            s0 += av[e] * gv[e].x;
+            s1 += av[e] * gv[e].y;
+          }
+        }
+        for (; u < v0; u += S) {
+          const double2 g2 = col[(size_t)u * ld2];
+          s0 += ac[u] * g2.x;
+          s1 += ac[u] * g2.y;
+        }
+      }
+      partq[q][2 * pr] = s0;
+      partq[q][2 * pr + 1] = s1;
+      double(*Tn)[CLIP_BLK + 1] = tile[(k + 1) & 1];
+      for (int e = t; e < CLIP_BLK * CLIP_BLK; e += CLIP_NT - 64) {
+        const int u = e / CLIP_BLK, rr = e % CLIP_BLK;
+        Tn[u][rr] = (rr < nb1 && u <= rr) ? G[(size_t)(v1 + u) * nmax + v1 + rr] : 0.0;
+        cross[u][rr] = (u < nb && rr < nb1) ? G[(size_t)(v0 + u) * nmax + v1 + rr] : 0.0;
+      }
     }
     __syncthreads();
-    const double bs = bcast[1];  // rescale owed by the earlier blocks' coefficients
-    if (bs != 1.0)
-      for (int u = threadIdx.x; u < v0; u += 256) ac[u] *= bs;
+    const double bs = bcast[1];
+    if (nb1 > 0 && tid < CLIP_BLK) {
+      double sn = 0.0;
+      for (int r = 0; r < CLIP_NS; ++r) sn += partq[r][tid];
+      sn *= bs;
+      for (int u = 0; u < nb; ++u) sn += ablk[u] * cross[u][tid];
+      sold[tid] = sn;
+    }
+    if (bs != 1.0)  // rescale owed by the earlier blocks' coefficients
+      for (int u = tid; u < v0; u += CLIP_NT) ac[u] *= bs;
+    __syncthreads();
   }
-  __syncthreads();
-  const double Pf = n > 0 ? bcast[0] : 1.0;
-  for (int u = threadIdx.x; u < n; u += 256) {
+  const double Pf = bcast[0];
+  for (int u = tid; u < n; u += CLIP_NT) {
     int b, t;
     cm.at(ch, u, b, t);
     w[(size_t)b * (cm.T + 1) + t] = (float)(Pf * ac[u]);
@@ -459,28 +660,53 @@ hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hip
   return hipGetLastError();
 }
 
-static int lstm_hb(int H) { return ((H + 63) / 64) * 64; }
-static int lstm_nq(int hb) { return std::max(1, std::min(LSTM_Q, 1024 / hb)); }
+// Thread layout of the recurrent mat-vec: GB threads per share of K (one per
+// column, or per 4 columns with 16-byte loads), as many shares as fit 1024.
+// Pitch of one chain's Gram matrix (rows of doubles): even, so the clip can
+// read 16-byte pairs.
+int lstm_gram_pitch(int n) { return (n + 1) & ~1; }
+
+struct LstmLayout {
+  bool v4;
+  int GB, NQ;
+};
+static LstmLayout lstm_layout(int H, const float *W) {
+  LstmLayout L;
+  L.v4 = (H % 4 == 0) && ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
+  const int cols = L.v4 ? H / 4 : H;
+  L.GB = ((cols + 63) / 64) * 64;
+  L.NQ = std::max(1, std::min(16, 1024 / L.GB));
+  return L;
+}
+static bool lstm_fits(int H) { return H >= 1 && H <= 1024; }
 
 hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,
                            float *tcb, float *cbuf, float *hbuf, float *out, int B, int T, int H,
                            hipStream_t s) {
-  const int hb = lstm_hb(H), nq = lstm_nq(hb);
-  if (hb > 1024) return hipErrorInvalidValue;
-  const size_t shm = (size_t)(H + nq * hb) * sizeof(float);
-  hipLaunchKernelGGL(lstm_fwd_kernel, dim3(B), dim3(hb * nq), shm, s, xw, WhT, bias, igb, tcb, cbuf,
-                     hbuf, out, T, H, hb, nq);
+  if (!lstm_fits(H)) return hipErrorInvalidValue;
+  const LstmLayout L = lstm_layout(H, WhT);
+  const size_t shm = (size_t)(((H + 3) & ~3) + L.NQ * H) * sizeof(float);
+  if (L.v4)
+    hipLaunchKernelGGL(lstm_fwd_kernel<true>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
+  else
+    hipLaunchKernelGGL(lstm_fwd_kernel<false>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
   return hipGetLastError();
 }
 
 hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
                            const float *Wh, const float *bias, float *D, int B, int T, int H,
                            hipStream_t s) {
-  const int hb = lstm_hb(H), nq = lstm_nq(hb);
-  if (hb > 1024) return hipErrorInvalidValue;
-  const size_t shm = (size_t)(4 * H + nq * hb) * sizeof(float);
-  hipLaunchKernelGGL(lstm_bwd_kernel, dim3(B), dim3(hb * nq), shm, s, gh, igb, tcb, cbuf, Wh, bias,
-                     D, T, H, hb, nq);
+  if (!lstm_fits(H)) return hipErrorInvalidValue;
+  const LstmLayout L = lstm_layout(H, Wh);
+  const size_t shm = (size_t)(4 * H + L.NQ * H) * sizeof(float);
+  if (L.v4)
+    hipLaunchKernelGGL(lstm_bwd_kernel<true>, dim3(B), dim3(1024), shm, s, gh, igb, tcb, cbuf, Wh,
+                       bias, D, T, H, L.GB, L.NQ);
+  else
+    hipLaunchKernelGGL(lstm_bwd_kernel<false>, dim3(B), dim3(1024), shm, s, gh, igb, tcb, cbuf, Wh,
+                       bias, D, T, H, L.GB, L.NQ);
   return hipGetLastError();
 }
 
@@ -490,11 +716,17 @@ hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const flo
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
-  const int nmax = cm.chunk * T;
+  const int nmax = lstm_gram_pitch(cm.chunk * T);
   const int ntile = (nmax + 63) / 64;
   dim3 g(ntile * (ntile + 1) / 2, nchains);
-  hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
-  hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(256), 0, s, gram, coef, w, cm, nmax);
+  const bool v4 = H % 8 == 0 && I % 4 == 0 &&
+                  (((reinterpret_cast<uintptr_t>(D) | reinterpret_cast<uintptr_t>(hbuf) |
+                     reinterpret_cast<uintptr_t>(x)) & 15) == 0);
+  if (v4)
+    hipLaunchKernelGGL(lstm_gram_v4_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+  else
+    hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+  hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), 0, s, gram, coef, w, cm, nmax);
   return hipGetLastError();
 }
 
