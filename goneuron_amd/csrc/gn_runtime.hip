@@ -487,7 +487,7 @@ struct LayerRT {
   int32_t *ids = nullptr;
   int *err = nullptr;
   struct Tb {
-    float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *P, *st1, *st2;
+    float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
   } tb{};
 };
@@ -833,7 +833,6 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), rows * FF, &t.DZ1))) return rc;
       if ((rc = model_alloc(M.get(), rows * 2, &t.st1))) return rc;
       if ((rc = model_alloc(M.get(), rows * 2, &t.st2))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.NH * R.T * R.T, &t.P))) return rc;
       if ((rc = model_alloc(M.get(), (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
     }
     if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
@@ -1029,7 +1028,7 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   HIP_OK(c, gemm_nt(c, X, P + o.wv, P + o.bv, t.V, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
   {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.P, t.O, B, R.T, D, R.NH, R.causal, c->stream));
+    HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, c->stream));
   }
   // res1 = x + wOut(o): the residual add rides in the GEMM epilogue
   HIP_OK(c, gemm_nt(c, t.O, P + o.wo, P + o.bo, t.RES1, rows, D, D, EPI_BIAS_ADD, 0, X));
@@ -1058,17 +1057,18 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     HIP_OK(c, launch_ln_bwd(R.gout, t.RES2, P + o.g2, t.st2, t.G1, t.GX, rows, D, c->stream));
     HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g2, cs, cap, c->stream));
     HIP_OK(c, launch_colsum(R.gout, rows, D, D, scale, G + o.be2, cs, cap, c->stream));
-    // ff2 (Linear): dz2 = dRES2
-    HIP_OK(c, launch_colsum(t.G1, rows, D, D, scale, G + o.b2, cs, cap, c->stream));
+    // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
+    // per-sample token sums S that the Q10 weight gradient needs anyway
     HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
+    HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.b2, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.MID, G + o.w2, B, T, D, FF, scale));
   // ff1 (ReLU): dz1 = (dz2 W2) * relu'(last token's pre-activation)  (Q10)
   HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, D_RELU, t.MID, T));
   {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_colsum(t.DZ1, rows, FF, FF, scale, G + o.b1, cs, cap, c->stream));
     HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
+    HIP_OK(c, launch_colsum(t.S, B, FF, FF, scale, G + o.b1, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
   // combined = dRES2 + dz1 W1
@@ -1079,14 +1079,14 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g1, cs, cap, c->stream));
     HIP_OK(c, launch_colsum(t.COMB, rows, D, D, scale, G + o.be1, cs, cap, c->stream));
     // wOut (Linear): dz = dRES1
-    HIP_OK(c, launch_colsum(t.G2, rows, D, D, scale, G + o.bo, cs, cap, c->stream));
     HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
+    HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.bo, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.O, G + o.wo, B, T, D, D, scale));
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
   {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.P, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
+    HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
                               c->stream));
   }
   const float *gs[3] = {t.GQ, t.GK, t.GV};
@@ -1094,8 +1094,8 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   for (int k = 0; k < 3; ++k) {
     {
       KTimer kt(c, GN_KCLASS_OTHER);
-      HIP_OK(c, launch_colsum(gs[k], rows, D, D, scale, G + bo[k], cs, cap, c->stream));
       HIP_OK(c, launch_token_sum(gs[k], t.S, B, T, D, c->stream));
+      HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + bo[k], cs, cap, c->stream));
     }
     HIP_OK(c, gemm_dw_last(c, t.S, X, G + wo[k], B, T, D, D, scale));
   }

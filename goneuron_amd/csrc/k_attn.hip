@@ -5,8 +5,8 @@
 // Semantics follow the reference per sample (transformer.go, layernorm.go,
 // embedding.go):
 //  - scores s_ij = (q_i . k_j) / sqrt(hd), -1e9 where j > i under the causal
-//    mask, row softmax with exp in float64 (activations.go:161-183),
-//    o_i = sum_j p_ij v_j (transformer.go:466-503);
+//    mask, row softmax (activations.go:161-183; exp in float32 here, see
+//    attn_probs), o_i = sum_j p_ij v_j (transformer.go:466-503);
 //  - backward dP_ij = gO_i . v_j, dS_ij = p_ij (dP_ij - sum_k dP_ik p_ik),
 //    gradScore = dS / sqrt(hd), gQ += gradScore k, gK += gradScore q,
 //    gV += p gO (transformer.go:583-648);
@@ -120,21 +120,26 @@ __global__ __launch_bounds__(256) void cls_bwd_kernel(const float *__restrict__ 
 }
 
 // S[b, :] = sum_t X[b, t, :]   (per-sample token sums for the Q10 dW outer products)
-// Block = 64 columns x 4 token groups of sample blockIdx.y; partials added in LDS.
-__global__ __launch_bounds__(256) void token_sum_kernel(const float *__restrict__ X,
-                                                        float *__restrict__ S, int B, int T, int N) {
-  __shared__ float red[4][64];
+// Block = 64 columns x 16 token groups of sample blockIdx.y; partials added in LDS.
+__global__ __launch_bounds__(1024) void token_sum_kernel(const float *__restrict__ X,
+                                                         float *__restrict__ S, int B, int T, int N) {
+  __shared__ float red[16][64];
   const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   const int64_t b = blockIdx.y;
   float s = 0.f;
   if (c < N) {
     const float *p = X + b * T * N + c;
-    for (int t = grp; t < T; t += 4) s += p[(int64_t)t * N];
+    for (int t = grp; t < T; t += 16) s += p[(int64_t)t * N];
   }
   red[grp][lane] = s;
   __syncthreads();
-  if (grp == 0 && c < N) S[b * N + c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  if (grp == 0 && c < N) {
+    float v = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) v += red[g][lane];
+    S[b * N + c] = v;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -199,57 +204,140 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 // ---------------------------------------------------------------------------
 // Causal multi-head attention on fp32 MFMA, one workgroup per (sample, head).
 // Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd); T <= 128 and
-// hd <= 32 are held in LDS (zero-padded to 128 x 32).  P [B, NH, T, T] keeps
-// the probabilities for the backward pass.  Wave w owns rows [32w, 32w+32) of
-// every T x T matrix.  v_mfma_f32_32x32x2_f32 operands: A[m = l%32][k = l/32],
-// B[k = l/32][n = l%32]; result register r of lane l is row
-// 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// hd <= 32 are held in LDS (zero-padded to 128 x 32).  Wave w owns queries
+// i in [32w, 32w+32) and works on transposed scores S^T[j][i] = k_j . q_i, so
+// each lane holds one query's column: the softmax over keys j is a reduction
+// inside the lane plus one exchange with lane l^32, and the probabilities stay
+// in registers in exactly the order the next MFMA consumes them (below).  The
+// backward pass recomputes them from Q and K instead of storing B*NH*T*T.
+// v_mfma_f32_32x32x2_f32 operands: A[m = l%32][k = l/32], B[k = l/32][n = l%32];
+// result register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// A product X[.][i] = sum_j Y[.][j] Z[j][i] whose Z^T comes from such a result
+// takes, at MFMA step s, key j = 8*(s/4) + 4*(l/32) + s%4 of the 32-key tile:
+// lane l then supplies Z register s as its B operand.
 // ---------------------------------------------------------------------------
 typedef float fx16 __attribute__((ext_vector_type(16)));
 constexpr int AT_SP = AT_T + 1;  // row pitch of the T x T LDS matrix
 
 __device__ __forceinline__ int mrow(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// row-wise max / sum over the 32 lanes that share lane/32
-__device__ __forceinline__ float hmax32(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float hsum32(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-// Stage rows [0, 128) x cols [0, 32) of head h into LDS (pitch AT_HP), zero padded.
+// Stage rows [0, 128) x cols [0, 32) of head h into LDS (pitch AT_HP), zero
+// padded.  With hd, D and the head offset multiples of 4 every thread issues
+// its four 16-byte loads before any store; otherwise element by element.
 __device__ __forceinline__ void stage_head(float *dst, const float *__restrict__ src, int b, int h,
                                            int T, int D, int hd) {
+  if ((hd & 3) == 0 && (D & 3) == 0 && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
+    float4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = threadIdx.x + 256 * q;  // 128 rows x 8 float4
+      const int t = f >> 3, d = (f & 7) << 2;
+      v[q] = (t < T && d < hd)
+                 ? *reinterpret_cast<const float4 *>(src + ((int64_t)b * T + t) * D + h * hd + d)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = threadIdx.x + 256 * q;
+      float *o = dst + (f >> 3) * AT_HP + ((f & 7) << 2);
+      o[0] = v[q].x;
+      o[1] = v[q].y;
+      o[2] = v[q].z;
+      o[3] = v[q].w;
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < AT_T * AT_HD; e += 256) {
     const int t = e / AT_HD, d = e % AT_HD;
     dst[t * AT_HP + d] = (t < T && d < hd) ? src[((int64_t)b * T + t) * D + h * hd + d] : 0.f;
   }
 }
 
-// acc += A_rows[32 rows from r0] . B_rows[32 rows from c0]^T over k in [0, kn)
-// with A and B both stored [row][k] at pitch AT_HP (S = Q K^T, dP = gO V^T).
+// acc += A_rows[32 rows from r0] . B_rows[32 rows from c0]^T over k in [0, 32),
+// both stored [row][k] at pitch AT_HP (the padding columns are zero).
 __device__ __forceinline__ void mm_nt(fx16 &acc, const float *A, const float *Bm, int r0, int c0,
-                                      int kn, int lane) {
-  for (int k = 0; k < kn; k += 2) {
+                                      int lane) {
+#pragma unroll
+  for (int k = 0; k < AT_HD; k += 2) {
     const float a = A[(r0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
     const float b = Bm[(c0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
   }
 }
 
+// acc[d][i] += sum over the 32 keys of tile jt of Y[j][d] * Zt[j][i], with Y in
+// LDS ([j][d], pitch AT_HP) and Zt the transposed-score-layout registers.
+__device__ __forceinline__ void mm_keys(fx16 &acc, const float *Y, const fx16 &Zt, int jt, int lane) {
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const int j = 32 * jt + 8 * (s >> 2) + 4 * (lane >> 5) + (s & 3);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Y[j * AT_HP + (lane & 31)], Zt[s], acc, 0, 0, 0);
+  }
+}
+
+// Probabilities P^T[j][i] of the wave's 32 queries in registers: scores /
+// sqrt(hd), -1e9 on causal-masked entries (as the reference), columns j >= T do
+// not exist; row softmax (activations.go:161-183) with a float32 exp: the
+// reference rounds a float64 exp to float32, expf is within 1 ulp of that and
+// the float64 exp of 64 entries per lane dominated the kernel.
+// Tiles jt > w are fully masked under the causal mask and are left at 0.
+__device__ __forceinline__ void attn_probs(fx16 (&pt)[4], const float *sq, const float *sk, int T,
+                                           int causal, float scale, int w, int lane) {
+  const int i = 32 * w + (lane & 31);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    pt[jt] = fx16{};
+    if (!(causal && jt > w)) mm_nt(pt[jt], sk, sq, 32 * jt, 32 * w, lane);
+  }
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 32 * jt + mrow(r, lane);
+      float sc;
+      if (j >= T) sc = -__builtin_inff();
+      else if (causal && j > i) sc = -1e9f;
+      else sc = pt[jt][r] / scale;
+      pt[jt][r] = sc;
+      mx = fmaxf(mx, sc);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 32 * jt + mrow(r, lane);
+      const float e = j < T ? expf(pt[jt][r] - mx) : 0.f;
+      pt[jt][r] = e;
+      sum += e;
+    }
+  sum += __shfl_xor(sum, 32, 64);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pt[jt][r] = pt[jt][r] / sum;
+}
+
+// Store a [d][i] (transposed) accumulator as head-h columns of G [B*T, D].
+__device__ __forceinline__ void store_t(float *G, const fx16 &v, int b, int h, int T, int D, int hd,
+                                        int w, int lane) {
+  const int i = 32 * w + (lane & 31);
+  if (i >= T) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int d = mrow(r, lane);
+    if (d < hd) G[((int64_t)b * T + i) * D + h * hd + d] = v[r];
+  }
+}
+
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__ Q,
                                                        const float *__restrict__ K,
                                                        const float *__restrict__ V,
-                                                       float *__restrict__ P,
                                                        float *__restrict__ O, int T, int D,
                                                        int NH, int causal) {
   __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP];
-  __shared__ float sp[AT_T * AT_SP];
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -258,176 +346,101 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
   stage_head(sv, V, b, h, T, D, hd);
   __syncthreads();
   const float scale = (float)sqrt((double)hd);
-  const int r0 = 32 * w;
-  // scores for the 4 column tiles; fully masked causal tiles are skipped
-  fx16 acc[4];
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-    acc[jt] = fx16{};
-    if (!(causal && jt > w)) mm_nt(acc[jt], sq, sk, r0, 32 * jt, hd + (hd & 1), lane);
-  }
-  // row softmax: -1e9 on causal-masked entries (as the reference), columns
-  // >= T do not exist; exp in float64 (activations.go:161-183)
-  const int cl = lane & 31;
-  float mx[16], sum[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) mx[r] = -__builtin_inff();
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
-      float sc;
-      if (j >= T) sc = -__builtin_inff();
-      else if (causal && j > i) sc = -1e9f;
-      else sc = acc[jt][r] / scale;
-      acc[jt][r] = sc;
-      mx[r] = fmaxf(mx[r], sc);
-    }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    mx[r] = hmax32(mx[r]);
-    sum[r] = 0.f;
-  }
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 32 * jt + cl;
-      const float e = j < T ? (float)exp((double)(acc[jt][r] - mx[r])) : 0.f;
-      acc[jt][r] = e;
-      sum[r] += e;
-    }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) sum[r] = hsum32(sum[r]);
-  float *Pb = P + ((int64_t)b * NH + h) * T * T;
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
-      const float p = acc[jt][r] / sum[r];
-      sp[i * AT_SP + j] = p;
-      if (i < T && j < T) Pb[(int64_t)i * T + j] = p;
-    }
-  __syncthreads();
-  // O = P V over j < min(T, rows of this wave + 1 under the causal mask)
+  fx16 pt[4];
+  attn_probs(pt, sq, sk, T, causal, scale, w, lane);
+  // O^T[d][i] = sum_j V[j][d] P[i][j]
   fx16 o = fx16{};
-  const int kend = causal ? min(T, r0 + 32) : T;
-  for (int j = 0; j < kend; j += 2) {
-    const float a = sp[(r0 + (lane & 31)) * AT_SP + j + (lane >> 5)];
-    const float bv = sv[(j + (lane >> 5)) * AT_HP + (lane & 31)];
-    o = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, o, 0, 0, 0);
-  }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int i = r0 + mrow(r, lane), d = cl;
-    if (i < T && d < hd) O[((int64_t)b * T + i) * D + h * hd + d] = o[r];
-  }
+  for (int jt = 0; jt < 4; ++jt)
+    if (!(causal && jt > w) && 32 * jt < T) mm_keys(o, sv, pt[jt], jt, lane);
+  store_t(O, o, b, h, T, D, hd, w, lane);
 }
 
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__ Q,
                                                        const float *__restrict__ K,
                                                        const float *__restrict__ V,
-                                                       const float *__restrict__ P,
                                                        const float *__restrict__ GO,
                                                        float *__restrict__ GQ,
                                                        float *__restrict__ GK,
                                                        float *__restrict__ GV, int T, int D,
                                                        int NH, int causal) {
   __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP], sg[AT_T * AT_HP];
-  __shared__ float sp[AT_T * AT_SP];  // P, then dS
+  __shared__ float sp[AT_T * AT_SP];  // P^T, then dS^T, as [j][i]
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int cl = lane & 31;
   stage_head(sq, Q, b, h, T, D, hd);
   stage_head(sk, K, b, h, T, D, hd);
   stage_head(sv, V, b, h, T, D, hd);
   stage_head(sg, GO, b, h, T, D, hd);
-  const float *Pb = P + ((int64_t)b * NH + h) * T * T;
-  for (int e = threadIdx.x; e < AT_T * AT_T; e += 256) {
-    const int i = e / AT_T, j = e % AT_T;
-    sp[i * AT_SP + j] = (i < T && j < T) ? Pb[(int64_t)i * T + j] : 0.f;
-  }
   __syncthreads();
   const float scale = (float)sqrt((double)hd);
-  const int r0 = 32 * w;
-  const int kpad = hd + (hd & 1);
-  auto store = [&](float *G, const fx16 &v) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = r0 + mrow(r, lane), d = cl;
-      if (t < T && d < hd) G[((int64_t)b * T + t) * D + h * hd + d] = v[r];
-    }
-  };
-  // gV_j = sum_i p_ij gO_i  (rows j of this wave; p_ij = 0 for i < j when causal)
-  {
-    fx16 acc = fx16{};
-    for (int i = causal ? r0 : 0; i < T; i += 2) {
-      const float a = sp[(i + (lane >> 5)) * AT_SP + r0 + (lane & 31)];
-      const float bv = sg[(i + (lane >> 5)) * AT_HP + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
-    }
-    store(GV, acc);
-  }
-  // dP_ij = gO_i . v_j ; r_i = sum_j dP_ij p_ij ; dS = (dP p - p r) / sqrt(hd)
-  fx16 dp[4];
+  const int i = 32 * w + (lane & 31);
+  fx16 pt[4];
+  attn_probs(pt, sq, sk, T, causal, scale, w, lane);
+  // dP^T[j][i] = v_j . gO_i ; r_i = sum_j dP_ij p_ij ; dS = (dP p - p r) / sqrt(hd)
+  fx16 ds[4];
+  float rs = 0.f;
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
-    dp[jt] = fx16{};
-    if (!(causal && jt > w)) mm_nt(dp[jt], sg, sv, r0, 32 * jt, kpad, lane);
+    ds[jt] = fx16{};
+    if (!(causal && jt > w)) mm_nt(ds[jt], sv, sg, 32 * jt, 32 * w, lane);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 32 * jt + mrow(r, lane);
+      const bool live = j < T && !(causal && j > i);
+      if (!live) ds[jt][r] = 0.f;
+      rs += ds[jt][r] * pt[jt][r];
+    }
   }
-  float rs[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) rs[r] = 0.f;
+  rs += __shfl_xor(rs, 32, 64);
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
+      const int j = 32 * jt + mrow(r, lane);
       const bool live = j < T && !(causal && j > i);
-      if (!live) dp[jt][r] = 0.f;
-      rs[r] += dp[jt][r] * sp[i * AT_SP + j];
+      const float p = pt[jt][r];
+      ds[jt][r] = live ? (ds[jt][r] * p - p * rs) / scale : 0.f;
     }
+  // gQ^T[d][i] = sum_j K[j][d] dS[i][j]
+  {
+    fx16 acc = fx16{};
 #pragma unroll
-  for (int r = 0; r < 16; ++r) rs[r] = hsum32(rs[r]);
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+    for (int jt = 0; jt < 4; ++jt)
+      if (!(causal && jt > w) && 32 * jt < T) mm_keys(acc, sk, ds[jt], jt, lane);
+    store_t(GQ, acc, b, h, T, D, hd, w, lane);
+  }
+  // the key-side products sum over queries of every wave: P^T and then dS^T
+  // go through LDS as [j][i], and wave w takes keys j in [32w, 32w+32)
+  const int j0 = 32 * w;
+  auto keyside = [&](const float *Yq, float *G) {
+    fx16 acc = fx16{};
+    // X[j][d] = sum_i Zt[j][i] Yq[i][d]; Zt[j][i] = 0 for i < j under the mask
+    for (int ii = causal ? j0 : 0; ii < T; ii += 2) {
+      const float a = sp[(j0 + (lane & 31)) * AT_SP + ii + (lane >> 5)];
+      const float bv = Yq[(ii + (lane >> 5)) * AT_HP + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int i = r0 + mrow(r, lane), j = 32 * jt + cl;
-      const bool live = j < T && !(causal && j > i);
-      const float p = sp[i * AT_SP + j];
-      dp[jt][r] = live ? (dp[jt][r] * p - p * rs[r]) / scale : 0.f;
+      const int j = j0 + mrow(r, lane), d = lane & 31;
+      if (j < T && d < hd) G[((int64_t)b * T + j) * D + h * hd + d] = acc[r];
     }
-  __syncthreads();  // every wave has read P (gV and r): overwrite it with dS
+  };
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sp[(r0 + mrow(r, lane)) * AT_SP + 32 * jt + cl] = dp[jt][r];
+    for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = pt[jt][r];
   __syncthreads();
-  // gQ_i = sum_j dS_ij k_j  (j <= i when causal)
-  {
-    fx16 acc = fx16{};
-    const int kend = causal ? min(T, r0 + 32) : T;
-    for (int j = 0; j < kend; j += 2) {
-      const float a = sp[(r0 + (lane & 31)) * AT_SP + j + (lane >> 5)];
-      const float bv = sk[(j + (lane >> 5)) * AT_HP + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
-    }
-    store(GQ, acc);
-  }
-  // gK_j = sum_i dS_ij q_i  (i >= j when causal)
-  {
-    fx16 acc = fx16{};
-    for (int i = causal ? r0 : 0; i < T; i += 2) {
-      const float a = sp[(i + (lane >> 5)) * AT_SP + r0 + (lane & 31)];
-      const float bv = sq[(i + (lane >> 5)) * AT_HP + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
-    }
-    store(GK, acc);
-  }
+  keyside(sg, GV);  // gV_j = sum_i p_ij gO_i
+  __syncthreads();
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = ds[jt][r];
+  __syncthreads();
+  keyside(sq, GK);  // gK_j = sum_i dS_ij q_i
 }
 
 static unsigned blocks_for(int64_t n) {
@@ -476,7 +489,7 @@ hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipS
 }
 
 hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s) {
-  hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B), dim3(256), 0, s, X, S, B, T, N);
+  hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B), dim3(1024), 0, s, X, S, B, T, N);
   return hipGetLastError();
 }
 
@@ -498,16 +511,16 @@ bool attn_supported(int T, int D, int NH) {
   return NH > 0 && D % NH == 0 && T >= 1 && T <= AT_T && D / NH <= AT_HD;
 }
 
-hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *P, float *O, int B,
-                           int T, int D, int NH, int causal, hipStream_t s) {
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, P, O, T, D, NH, causal);
+hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
+                           int D, int NH, int causal, hipStream_t s) {
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, O, T, D, NH, causal);
   return hipGetLastError();
 }
 
-hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *P,
-                           const float *GO, float *GQ, float *GK, float *GV, int B, int T, int D,
-                           int NH, int causal, hipStream_t s) {
-  hipLaunchKernelGGL(attn_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, P, GO, GQ, GK, GV, T, D,
+hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *GO,
+                           float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(attn_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, GO, GQ, GK, GV, T, D,
                      NH, causal);
   return hipGetLastError();
 }
