@@ -112,6 +112,22 @@ def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
                               "sample": f"{n1} of {B} samples fwd+bwd ({ts1:.2f} s) + Adam scaled by n/B"}}
 
 
+def mfma_probe():
+    """The fp32 MFMA rate the part sustains: gn_probe_mfma at 4, 8 and 16 waves
+    per CU and 4-11 ms per launch."""
+    import ctypes as C
+    import goneuron_amd as gn
+    from goneuron_amd._lib import lib, check
+    dev = gn.GetDefaultDevice()
+    for blocks, iters in ((512, 20000), (512, 20000), (1024, 20000), (1024, 20000), (512, 50000),
+                          (256, 100000)):
+        ms, tf = C.c_double(), C.c_double()
+        check(dev.h, lib().gn_probe_mfma(dev.h, blocks, iters, C.byref(ms), C.byref(tf)))
+        print(json.dumps({"mfma_probe_blocks": blocks, "iters": iters, "ms": ms.value,
+                          "tflops": tf.value, "frac_of_peak": tf.value / PEAK_FP32_MFMA_TFLOPS}),
+              flush=True)
+
+
 def copy_probe(mib):
     """A copy kernel of known size: reads and writes mib MiB per launch."""
     import torch
@@ -135,6 +151,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="threads of the parallel CPU baseline (default min(B, cores, 16))")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only run the matrix-core probe (back-to-back fp32 MFMA at 2, 4 and 8 "
+                         "waves per SIMD, short and sustained) and print its rates")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -146,6 +165,9 @@ def main():
 
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.mfma_probe:
+        mfma_probe()
         return
 
     import ctypes as C

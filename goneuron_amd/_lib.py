@@ -97,6 +97,7 @@ SIGNATURES = {
     "gn_fill_class_ids": (C.c_int, [i32p, C.c_int64, C.c_int32, C.c_uint64]),
     "gn_timing_enable": (C.c_int, [vp, C.c_int]),
     "gn_timing_report": (C.c_int, [vp, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+    "gn_probe_mfma": (C.c_int, [vp, C.c_int32, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
 _lib = None

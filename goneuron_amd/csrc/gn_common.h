@@ -147,4 +147,7 @@ hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
                            hipStream_t s);
 
+// ---- measurement probe ----
+hipError_t launch_mfma_probe(float *out, int blocks, int iters, hipStream_t s);
+
 }  // namespace gn

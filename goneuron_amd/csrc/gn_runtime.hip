@@ -229,6 +229,32 @@ extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
   return GN_OK;
 }
 
+extern "C" int gn_probe_mfma(gn_ctx *c, int32_t blocks, int32_t iters, double *ms, double *tflops) {
+  ENTRY(c);
+  if (blocks <= 0 || iters <= 0 || !ms || !tflops) return set_err(c, GN_ERR_INVALID, "bad probe args");
+  float *out = nullptr;
+  if (hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) != hipSuccess)
+    return set_err(c, GN_ERR_OOM, "probe buffer");
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t e = hipEventCreate(&a);
+  if (e == hipSuccess) e = hipEventCreate(&b);
+  if (e == hipSuccess) e = launch_mfma_probe(out, blocks, 16, c->stream);  // warm-up
+  if (e == hipSuccess) e = hipEventRecord(a, c->stream);
+  if (e == hipSuccess) e = launch_mfma_probe(out, blocks, iters, c->stream);
+  if (e == hipSuccess) e = hipEventRecord(b, c->stream);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float t = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t, a, b);
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipFree(out);
+  HIP_OK(c, e);
+  *ms = t;
+  // 4 waves per block, 4 MFMAs of 32x32x2 (4096 FLOP) per wave and iteration
+  *tflops = (double)blocks * 4 * 4 * 4096.0 * iters / (t * 1e-3) / 1e12;
+  return GN_OK;
+}
+
 extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *total_ms) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));

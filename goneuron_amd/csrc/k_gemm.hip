@@ -71,8 +71,9 @@ __device__ __forceinline__ float apply_deriv(float out, int kind) {
 // Global -> register staging of one R-row operand tile.  KC: the operand's K
 // index is contiguous in memory (rows x K, row pitch ld); otherwise it is
 // stored K x rows.  VEC: float4 accesses are legal (16 B aligned, sizes % 4 ==
-// 0).  Only k in [k0, kend) is read; everything else is zero-filled.
-template <int R, bool KC, bool VEC>
+// 0).  Only k in [k0, kend) is read; everything else is zero-filled.  FULL:
+// the tile lies inside the matrix (no checks, no zero fill).
+template <int R, bool KC, bool VEC, bool FULL = false>
 __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld, int rows, int kend,
                                           int r0, int k0, float4 (&reg)[Tile<R>::NLD]) {
   const int t = threadIdx.x;
@@ -82,7 +83,9 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
       const int gr = r0 + r, gk = k0 + k4;
-      if (VEC) {
+      if (FULL) {
+        reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gr * ld + gk);
+      } else if (VEC) {
         if (gr < rows && gk < kend)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gr * ld + gk);
         else
@@ -98,7 +101,9 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
     } else {
       const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
       const int gk = k0 + k, gr = r0 + r4;
-      if (VEC) {
+      if (FULL) {
+        reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gk * ld + gr);
+      } else if (VEC) {
         if (gk < kend && gr < rows)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gk * ld + gr);
         else
@@ -191,7 +196,7 @@ __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, i
 // EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
 constexpr int EPI_PARTIAL = 3;
 
-template <int R, bool AK, bool BKC, bool VEC, int EPI>
+template <int R, bool AK, bool BKC, bool VEC, int EPI, bool FULL>
 __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n,
                                                     int kchunk) {
   using TL = Tile<R>;
@@ -215,8 +220,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
   float4 ra[TL::NLD], rb[TL::NLD];
-  load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
-  load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+  load_tile<R, AK, VEC, FULL>(p.A, p.lda, M, kend, m0, kbeg, ra);
+  load_tile<R, BKC, VEC, FULL>(p.B, p.ldb, N, kend, n0, kbeg, rb);
   store_tile<R, AK>(As[0], ra);
   store_tile<R, BKC>(Bs[0], rb);
   __syncthreads();
@@ -232,7 +237,13 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
-    if (more) {
+    if (FULL) {
+      // One basic block per stage: the last stage re-loads itself into the
+      // idle buffer, so no branch splits the schedule below.
+      const int kn = kbeg + min(kt + 1, nk - 1) * BK;
+      load_tile<R, AK, VEC, true>(p.A, p.lda, M, kend, m0, kn, ra);
+      load_tile<R, BKC, VEC, true>(p.B, p.ldb, N, kend, n0, kn, rb);
+    } else if (more) {
       load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
       load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
     }
@@ -248,9 +259,30 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
 #pragma unroll
         for (int j = 0; j < T; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
-    if (more) {
+    if (FULL || more) {
       store_tile<R, AK>(As[cur ^ 1], ra);
       store_tile<R, BKC>(Bs[cur ^ 1], rb);
+    }
+    if (FULL && T == 2) {
+      // Interleave the stage's memory traffic with its 64 MFMAs: the first
+      // half's fragment reads, the next stage's global loads one per 2 MFMAs,
+      // 16 MFMAs, the second half's fragment reads, the LDS writes of the
+      // next stage one per 2 MFMAs, the last 16 MFMAs.
+      constexpr int DSR = (AK ? 4 : 16) + (BKC ? 4 : 16);  // fragment reads per half
+      __builtin_amdgcn_sched_group_barrier(0x100, DSR, 0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, DSR, 0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
     }
     __syncthreads();
   }
@@ -331,37 +363,46 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int sp
 }
 
 template <int R, bool AK, bool BKC, int EPI>
-static hipError_t launch_t(bool vec, const GemmArgs &a, int tm, int tn, int splits, int kchunk,
-                           hipStream_t s) {
+static hipError_t launch_t(bool vec, bool full, const GemmArgs &a, int tm, int tn, int splits,
+                          int kchunk, hipStream_t s) {
   dim3 grid(tm * tn, splits), block(NT);
-  if (vec)
-    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
+  if (vec && full)
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, true>), grid, block, 0, s, a, tm, tn,
+                       kchunk);
+  else if (vec)
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, false>), grid, block, 0, s, a, tm, tn,
+                       kchunk);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, false, EPI>), grid, block, 0, s, a, tm, tn, kchunk);
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, false, EPI, false>), grid, block, 0, s, a, tm, tn,
+                       kchunk);
   return hipGetLastError();
 }
 
 template <int R, int EPI>
-static hipError_t launch_e(char ta, char tb, bool vec, const GemmArgs &a, int tm, int tn,
+static hipError_t launch_e(char ta, char tb, bool vec, bool full, const GemmArgs &a, int tm, int tn,
                            int splits, int kchunk, hipStream_t s) {
   // op(A) 'N' -> A is M x K, K contiguous.  op(B) 'T' -> B is N x K, K contiguous.
   const bool ak = (ta == 'N');
   const bool bk = (tb == 'T');
-  if (ak && bk) return launch_t<R, true, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  if (ak && !bk) return launch_t<R, true, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  if (!ak && bk) return launch_t<R, false, true, EPI>(vec, a, tm, tn, splits, kchunk, s);
-  return launch_t<R, false, false, EPI>(vec, a, tm, tn, splits, kchunk, s);
+  if (ak && bk) return launch_t<R, true, true, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
+  if (ak && !bk) return launch_t<R, true, false, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
+  if (!ak && bk) return launch_t<R, false, true, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
+  return launch_t<R, false, false, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
 }
 
 template <int R>
 static hipError_t launch_r(char ta, char tb, int epi, bool vec, const GemmArgs &a, int splits,
                            int kchunk, hipStream_t s) {
   const int tm = (a.M + R - 1) / R, tn = (a.N + R - 1) / R;
-  if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, a, tm, tn, splits, kchunk, s);
-  if (epi == EPI_BIAS_ACT) return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-  if (epi == EPI_DACT) return launch_e<R, EPI_DACT>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-  if (epi == EPI_BIAS_ADD) return launch_e<R, EPI_BIAS_ADD>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
-  return launch_e<R, EPI_SCALE>(ta, tb, vec, a, tm, tn, 1, kchunk, s);
+  // every tile and K stage inside the matrices: the unchecked, scheduled loop
+  const bool full = vec && a.M % R == 0 && a.N % R == 0 && a.K % BK == 0;
+  if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, full, a, tm, tn, splits, kchunk, s);
+  if (epi == EPI_BIAS_ACT)
+    return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
+  if (epi == EPI_DACT) return launch_e<R, EPI_DACT>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
+  if (epi == EPI_BIAS_ADD)
+    return launch_e<R, EPI_BIAS_ADD>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
+  return launch_e<R, EPI_SCALE>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

@@ -192,6 +192,10 @@ int gn_adam_step(gn_ctx *ctx, float *params, const float *grads, float *m, float
 #define GN_KCLASS_OTHER 2  /* row kernels, column sums, dropout, ... */
 int gn_timing_enable(gn_ctx *ctx, int enable);
 int gn_timing_report(gn_ctx *ctx, int kclass, int64_t *launches, double *total_ms);
+/* Matrix-core probe (measurement hook; no reference counterpart): `blocks`
+ * workgroups of 4 wave64s issue `iters` x 4 back-to-back
+ * v_mfma_f32_32x32x2_f32 each; returns the kernel time and its FLOP rate. */
+int gn_probe_mfma(gn_ctx *ctx, int32_t blocks, int32_t iters, double *ms, double *tflops);
 
 /* ---- synthetic inputs (host side; harness utility) ----------------------
  * The reference's LCG (layer.go:61-81): U[0,1) stream, N(0,1) by one
