@@ -128,6 +128,31 @@ def mfma_probe():
               flush=True)
 
 
+def library_sgemm():
+    """The vendor library (torch.mm, fp32) on the C3 forward shape: a practical
+    ceiling for the hand-written GEMM, run in a process of its own because
+    torch ships its own HIP runtime. The library never calls it."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(1024, 4096, generator=g).to("cuda:0")
+    b = torch.randn(4096, 4096, generator=g).to("cuda:0")
+    c = torch.empty(1024, 4096, device="cuda:0")
+    for _ in range(5):
+        torch.mm(a, b, out=c)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 50
+    e0.record()
+    for _ in range(reps):
+        torch.mm(a, b, out=c)
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tf = 2 * 1024 * 4096 * 4096 / (ms * 1e-3) / 1e12
+    print(json.dumps({"library_sgemm": "torch.mm fp32 1024x4096 @ 4096x4096", "ms": ms,
+                      "tflops": tf, "frac_of_peak": tf / PEAK_FP32_MFMA_TFLOPS}), flush=True)
+
+
 def copy_probe(mib):
     """A copy kernel of known size: reads and writes mib MiB per launch."""
     import torch
@@ -154,6 +179,8 @@ def main():
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only run the matrix-core probe (back-to-back fp32 MFMA at 2, 4 and 8 "
                          "waves per SIMD, short and sustained) and print its rates")
+    ap.add_argument("--library-sgemm", action="store_true",
+                    help="only time torch.mm (fp32) on the C3 forward GEMM shape, as a reference point")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -168,6 +195,9 @@ def main():
         return
     if args.mfma_probe:
         mfma_probe()
+        return
+    if args.library_sgemm:
+        library_sgemm()
         return
 
     import ctypes as C
