@@ -16,11 +16,16 @@
 // 1024-row batch a 4096-wide layer has exactly 256 tiles (one per CU): the
 // K-groups give every SIMD two waves to hide LDS and barrier latency.  Lane
 // half h feeds k = 16h + s at MFMA step s, so each lane's 16 operand values per
-// slab are contiguous for a K-contiguous operand.  Two LDS stages: global loads
-// for stage k+1 are issued into registers before the MFMAs of stage k and
-// written to the other stage afterwards, one barrier per stage.  When the tile grid cannot fill
-// the 256 CUs the K range is split across blocks; the partial sums are added
-// in split order by a second kernel that also applies the epilogue.
+// slab are contiguous for a K-contiguous operand.  Two LDS stages, one
+// barrier per stage.  When every tile and K stage lies inside the matrices the
+// main loop is software-pipelined (the barrier sits before the last quarter
+// of a stage's MFMAs, fragment halves are double-buffered in registers, global
+// loads are issued about one stage before their LDS writes, and
+// __builtin_amdgcn_sched_group_barrier fixes the interleave); otherwise a
+// bounds-checked loop prefetches one stage into registers.  When the tile
+// grid cannot fill the 256 CUs the K range is split across blocks; the partial
+// sums are added in split order by a second kernel that also applies the
+// epilogue.
 //
 // Used by Dense forward (NT: X[B,in] * W[out,in]^T, fused bias + activation),
 // Dense dX (NN: dZ[B,out] * W[out,in], fused activation derivative of the layer
@@ -71,9 +76,8 @@ __device__ __forceinline__ float apply_deriv(float out, int kind) {
 // Global -> register staging of one R-row operand tile.  KC: the operand's K
 // index is contiguous in memory (rows x K, row pitch ld); otherwise it is
 // stored K x rows.  VEC: float4 accesses are legal (16 B aligned, sizes % 4 ==
-// 0).  Only k in [k0, kend) is read; everything else is zero-filled.  FULL:
-// the tile lies inside the matrix (no checks, no zero fill).
-template <int R, bool KC, bool VEC, bool FULL = false>
+// 0).  Only k in [k0, kend) is read; everything else is zero-filled.
+template <int R, bool KC, bool VEC>
 __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld, int rows, int kend,
                                           int r0, int k0, float4 (&reg)[Tile<R>::NLD]) {
   const int t = threadIdx.x;
@@ -83,9 +87,7 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
       const int gr = r0 + r, gk = k0 + k4;
-      if (FULL) {
-        reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gr * ld + gk);
-      } else if (VEC) {
+      if (VEC) {
         if (gr < rows && gk < kend)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gr * ld + gk);
         else
@@ -101,9 +103,7 @@ __device__ __forceinline__ void load_tile(const float *__restrict__ base, int ld
     } else {
       const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
       const int gk = k0 + k, gr = r0 + r4;
-      if (FULL) {
-        reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gk * ld + gr);
-      } else if (VEC) {
+      if (VEC) {
         if (gk < kend && gr < rows)
           reg[j] = *reinterpret_cast<const float4 *>(base + (size_t)gk * ld + gr);
         else
@@ -162,6 +162,64 @@ __device__ __forceinline__ void read_frag(const float *S, int rowbase, int koff,
   }
 }
 
+// Full-tile staging for the pipelined loop, in native vector types (a float4
+// struct copy through a register array can leave the array in scratch memory).
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int R, bool KC>
+__device__ __forceinline__ void load_tile_full(const float *__restrict__ base, int ld, int r0, int k0,
+                                               floatx4 (&reg)[Tile<R>::NLD]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < Tile<R>::NLD; ++j) {
+    const int f = t + NT * j;
+    if (KC) {
+      const int r = f >> 4, k4 = (f & 15) << 2;
+      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)(r0 + r) * ld + k0 + k4);
+    } else {
+      const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
+      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)(k0 + k) * ld + r0 + r4);
+    }
+  }
+}
+
+template <int R, bool KC>
+__device__ __forceinline__ void store_tile_full(float *S, const floatx4 (&reg)[Tile<R>::NLD]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < Tile<R>::NLD; ++j) {
+    const int f = t + NT * j;
+    if (KC) {
+      const int r = f >> 4, k4 = (f & 15) << 2;
+      *reinterpret_cast<floatx4 *>(S + r * PITCH + k4) = reg[j];
+    } else {
+      const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
+      *reinterpret_cast<floatx4 *>(S + k * Tile<R>::RP + r4) = reg[j];
+    }
+  }
+}
+
+// Half a fragment: MFMA steps s = 8h .. 8h+7 of read_frag (koff advanced by 8h).
+template <int R, bool KC>
+__device__ __forceinline__ void read_frag_half(const float *S, int rowbase, int koff, int l32,
+                                               float (&a)[8]) {
+  if (KC) {
+    const float *src = S + (rowbase + l32) * PITCH + koff;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const floatx4 x = *reinterpret_cast<const floatx4 *>(src + 4 * q);
+      a[4 * q + 0] = x[0];
+      a[4 * q + 1] = x[1];
+      a[4 * q + 2] = x[2];
+      a[4 * q + 3] = x[3];
+    }
+  } else {
+    const float *src = S + koff * Tile<R>::RP + rowbase + l32;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) a[s] = src[s * Tile<R>::RP];
+  }
+}
+
 // Block -> tile mapping.  Workgroups are dispatched round-robin over the 8
 // XCDs (each with its own L2), so consecutive block ids land on different
 // XCDs.  Remap so that each XCD receives a contiguous range of tile ids, and
@@ -196,9 +254,11 @@ __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, i
 // EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
 constexpr int EPI_PARTIAL = 3;
 
+// R = 128 runs one block per CU (139 KB of LDS), so two waves per SIMD and
+// the full 256-register budget; R = 64 fits two blocks per CU.
 template <int R, bool AK, bool BKC, bool VEC, int EPI, bool FULL>
-__global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n,
-                                                    int kchunk) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, R == 128 ? 2 : 4)))
+void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   using TL = Tile<R>;
   constexpr int T = TL::T;
   __shared__ __attribute__((aligned(16))) float As[2][TL::STAGE];
@@ -219,13 +279,6 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
   const int kend = min(p.K, kbeg + kchunk);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
-  float4 ra[TL::NLD], rb[TL::NLD];
-  load_tile<R, AK, VEC, FULL>(p.A, p.lda, M, kend, m0, kbeg, ra);
-  load_tile<R, BKC, VEC, FULL>(p.B, p.ldb, N, kend, n0, kbeg, rb);
-  store_tile<R, AK>(As[0], ra);
-  store_tile<R, BKC>(Bs[0], rb);
-  __syncthreads();
-
   floatx16 acc[T][T];
 #pragma unroll
   for (int i = 0; i < T; ++i)
@@ -234,57 +287,126 @@ __global__ __launch_bounds__(NT) void gemm_f32_mfma(GemmArgs p, int tiles_m, int
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (FULL) {
-      // One basic block per stage: the last stage re-loads itself into the
-      // idle buffer, so no branch splits the schedule below.
-      const int kn = kbeg + min(kt + 1, nk - 1) * BK;
-      load_tile<R, AK, VEC, true>(p.A, p.lda, M, kend, m0, kn, ra);
-      load_tile<R, BKC, VEC, true>(p.B, p.ldb, N, kend, n0, kn, rb);
-    } else if (more) {
-      load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
-      load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
-    }
-    float a[T][16], b[T][16];
-#pragma unroll
-    for (int i = 0; i < T; ++i) read_frag<R, AK>(As[cur], wm * (R / 2) + i * 32, koff, l32, a[i]);
-#pragma unroll
-    for (int j = 0; j < T; ++j) read_frag<R, BKC>(Bs[cur], wn * (R / 2) + j * 32, koff, l32, b[j]);
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-#pragma unroll
-      for (int i = 0; i < T; ++i)
-#pragma unroll
-        for (int j = 0; j < T; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
-    if (FULL || more) {
-      store_tile<R, AK>(As[cur ^ 1], ra);
-      store_tile<R, BKC>(Bs[cur ^ 1], rb);
-    }
-    if (FULL && T == 2) {
-      // Interleave the stage's memory traffic with its 64 MFMAs: the first
-      // half's fragment reads, the next stage's global loads one per 2 MFMAs,
-      // 16 MFMAs, the second half's fragment reads, the LDS writes of the
-      // next stage one per 2 MFMAs, the last 16 MFMAs.
-      constexpr int DSR = (AK ? 4 : 16) + (BKC ? 4 : 16);  // fragment reads per half
-      __builtin_amdgcn_sched_group_barrier(0x100, DSR, 0);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, DSR, 0);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  if constexpr (FULL) {
+    // Every tile and K stage lies inside the matrices (nk >= 1).  Software
+    // pipeline, one barrier per stage, each stage's 16 MFMA steps in halves
+    // f0 (s < 8) and f1 (s >= 8):
+    //   f1 fragment reads | MFMAs s = 0..7 | MFMAs s = 8..11 with the LDS
+    //   writes of the next stage | barrier | next stage's f0 fragment reads
+    //   and the global loads of the stage after next | MFMAs s = 12..15.
+    // The barrier sits before the stage's last quarter of MFMAs, so the
+    // fragment reads after it are covered by MFMAs on registers; global loads
+    // are issued about one stage before their LDS writes.  Loads and writes
+    // beyond the last stage re-read it into the idle buffer.
+    const int mrow = wm * (R / 2), ncol = wn * (R / 2);
+    floatx4 ra[TL::NLD], rb[TL::NLD];
+    load_tile_full<R, AK>(p.A, p.lda, m0, kbeg, ra);
+    load_tile_full<R, BKC>(p.B, p.ldb, n0, kbeg, rb);
+    store_tile_full<R, AK>(As[0], ra);
+    store_tile_full<R, BKC>(Bs[0], rb);
+    {
+      const int k1 = kbeg + min(1, nk - 1) * BK;
+      load_tile_full<R, AK>(p.A, p.lda, m0, k1, ra);
+      load_tile_full<R, BKC>(p.B, p.ldb, n0, k1, rb);
     }
     __syncthreads();
+    float f0a[T][8], f0b[T][8];
+#pragma unroll
+    for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[0], mrow + i * 32, koff, l32, f0a[i]);
+#pragma unroll
+    for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[0], ncol + j * 32, koff, l32, f0b[j]);
+    constexpr int DSRH = T * ((AK ? 2 : 8) + (BKC ? 2 : 8));  // fragment reads per half stage
+    constexpr int NW = 2 * TL::NLD;                            // loads (= LDS writes) per stage
+    constexpr int MQ = 4 * T * T;                              // MFMAs per quarter stage
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      float f1a[T][8], f1b[T][8];
+#pragma unroll
+      for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[cur], mrow + i * 32, koff + 8, l32, f1a[i]);
+#pragma unroll
+      for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[cur], ncol + j * 32, koff + 8, l32, f1b[j]);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int j = 0; j < T; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f0a[i][s], f0b[j][s], acc[i][j], 0, 0, 0);
+      store_tile_full<R, AK>(As[cur ^ 1], ra);
+      store_tile_full<R, BKC>(Bs[cur ^ 1], rb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int j = 0; j < T; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f1a[i][s], f1b[j][s], acc[i][j], 0, 0, 0);
+      // group masks: 0x008 MFMA, 0x020 global load, 0x100 LDS read, 0x200 LDS write
+      __builtin_amdgcn_sched_group_barrier(0x100, DSRH, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * MQ, 0);
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MQ / NW, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[cur ^ 1], mrow + i * 32, koff, l32, f0a[i]);
+#pragma unroll
+      for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[cur ^ 1], ncol + j * 32, koff, l32, f0b[j]);
+      {
+        const int k2 = kbeg + min(kt + 2, nk - 1) * BK;
+        load_tile_full<R, AK>(p.A, p.lda, m0, k2, ra);
+        load_tile_full<R, BKC>(p.B, p.ldb, n0, k2, rb);
+      }
+#pragma unroll
+      for (int s = 4; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int j = 0; j < T; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f1a[i][s], f1b[j][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, DSRH, 0);
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MQ / NW, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+    }
+    // the last iteration's fragment reads target LDS the reduction reuses
+    __syncthreads();
+  } else {
+    float4 ra[TL::NLD], rb[TL::NLD];
+    load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
+    load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+    store_tile<R, AK>(As[0], ra);
+    store_tile<R, BKC>(Bs[0], rb);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
+        load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
+      }
+      float a[T][16], b[T][16];
+#pragma unroll
+      for (int i = 0; i < T; ++i) read_frag<R, AK>(As[cur], wm * (R / 2) + i * 32, koff, l32, a[i]);
+#pragma unroll
+      for (int j = 0; j < T; ++j) read_frag<R, BKC>(Bs[cur], wn * (R / 2) + j * 32, koff, l32, b[j]);
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int j = 0; j < T; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+      if (more) {
+        store_tile<R, AK>(As[cur ^ 1], ra);
+        store_tile<R, BKC>(Bs[cur ^ 1], rb);
+      }
+      __syncthreads();
+    }
   }
 
   // K-group 1 hands its accumulators to group 0 through LDS (the operand
@@ -395,7 +517,7 @@ static hipError_t launch_r(char ta, char tb, int epi, bool vec, const GemmArgs &
                            int kchunk, hipStream_t s) {
   const int tm = (a.M + R - 1) / R, tn = (a.N + R - 1) / R;
   // every tile and K stage inside the matrices: the unchecked, scheduled loop
-  const bool full = vec && a.M % R == 0 && a.N % R == 0 && a.K % BK == 0;
+  const bool full = vec && a.K > 0 && a.M % R == 0 && a.N % R == 0 && a.K % BK == 0;
   if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, full, a, tm, tn, splits, kchunk, s);
   if (epi == EPI_BIAS_ACT)
     return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
