@@ -220,6 +220,29 @@ __device__ __forceinline__ void read_frag_half(const float *S, int rowbase, int 
   }
 }
 
+// Both fragment halves' slabs of a wave (T slabs).  With T = 2 an
+// M/N-contiguous operand is read pairwise: lane l takes rows 2*(l%32) and
+// 2*(l%32)+1 with one ds_read_b64, the even row feeding slab 0 and the odd row
+// slab 1, so a slab holds every other row of the wave's 64 (the epilogue maps
+// rows back; each output's K order is unchanged).
+template <int R, bool KC>
+__device__ __forceinline__ void read_frags(const float *S, int rowbase, int koff, int l32,
+                                           float (&a)[Tile<R>::T][8]) {
+  constexpr int T = Tile<R>::T;
+  if (KC || T != 2) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) read_frag_half<R, KC>(S, rowbase + i * 32, koff, l32, a[i]);
+  } else {
+    const float *src = S + koff * Tile<R>::RP + rowbase + 2 * l32;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float2 x = *reinterpret_cast<const float2 *>(src + s * Tile<R>::RP);
+      a[0][s] = x.x;
+      a[T - 1][s] = x.y;
+    }
+  }
+}
+
 // Block -> tile mapping.  Workgroups are dispatched round-robin over the 8
 // XCDs (each with its own L2), so consecutive block ids land on different
 // XCDs.  Remap so that each XCD receives a contiguous range of tile ids, and
@@ -311,20 +334,18 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     }
     __syncthreads();
     float f0a[T][8], f0b[T][8];
-#pragma unroll
-    for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[0], mrow + i * 32, koff, l32, f0a[i]);
-#pragma unroll
-    for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[0], ncol + j * 32, koff, l32, f0b[j]);
-    constexpr int DSRH = T * ((AK ? 2 : 8) + (BKC ? 2 : 8));  // fragment reads per half stage
+    read_frags<R, AK>(As[0], mrow, koff, l32, f0a);
+    read_frags<R, BKC>(Bs[0], ncol, koff, l32, f0b);
+    // fragment reads per half stage: 2 b128 per slab (K-contiguous), else 8
+    // (b64 pairs at T = 2, b32 at T = 1)
+    constexpr int DSRH = (AK ? 2 * T : 8) + (BKC ? 2 * T : 8);
     constexpr int NW = 2 * TL::NLD;                            // loads (= LDS writes) per stage
     constexpr int MQ = 4 * T * T;                              // MFMAs per quarter stage
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
       float f1a[T][8], f1b[T][8];
-#pragma unroll
-      for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[cur], mrow + i * 32, koff + 8, l32, f1a[i]);
-#pragma unroll
-      for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[cur], ncol + j * 32, koff + 8, l32, f1b[j]);
+      read_frags<R, AK>(As[cur], mrow, koff + 8, l32, f1a);
+      read_frags<R, BKC>(Bs[cur], ncol, koff + 8, l32, f1b);
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
@@ -350,10 +371,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       }
       __syncthreads();
-#pragma unroll
-      for (int i = 0; i < T; ++i) read_frag_half<R, AK>(As[cur ^ 1], mrow + i * 32, koff, l32, f0a[i]);
-#pragma unroll
-      for (int j = 0; j < T; ++j) read_frag_half<R, BKC>(Bs[cur ^ 1], ncol + j * 32, koff, l32, f0b[j]);
+      read_frags<R, AK>(As[cur ^ 1], mrow, koff, l32, f0a);
+      read_frags<R, BKC>(Bs[cur ^ 1], ncol, koff, l32, f0b);
       {
         const int k2 = kbeg + min(kt + 2, nk - 1) * BK;
         load_tile_full<R, AK>(p.A, p.lda, m0, k2, ra);
@@ -436,17 +455,20 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   }
 
   // v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
-  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile.
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile; slab rows are
+  // every other row when the operand was read pairwise (read_frags).
+  constexpr bool PAIR_A = FULL && !AK && T == 2, PAIR_B = FULL && !BKC && T == 2;
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
   for (int i = 0; i < T; ++i)
 #pragma unroll
     for (int j = 0; j < T; ++j) {
-      const int col = n0 + wn * (R / 2) + j * 32 + l32;
+      const int col = n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32);
       if (col >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (R / 2) + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
+        const int row = m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
         if (row >= M) continue;
         if (EPI == EPI_PARTIAL)
           ws[(size_t)row * N + col] = acc[i][j][r];
