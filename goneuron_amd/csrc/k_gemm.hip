@@ -162,12 +162,19 @@ __device__ __forceinline__ void read_frag(const float *S, int rowbase, int koff,
   }
 }
 
-// Full-tile staging for the pipelined loop, in native vector types (a float4
-// struct copy through a register array can leave the array in scratch memory).
+// Staging for the pipelined loop, in native vector types (a float4 struct
+// copy through a register array can leave the array in scratch memory).
+// Rows past the matrix edge re-read its last valid row or float4 (their
+// results are never stored).  With KT, k past kend reads a valid address and
+// the store replaces it by zeros (the select waits at the store, where the
+// load has to be complete anyway), which adds exact zeros to every sum like
+// the checked loop.  Needs the float4 legality of the checked loop's VEC case
+// (16 B aligned rows, contiguous extent % 4 == 0).
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int R, bool KC>
-__device__ __forceinline__ void load_tile_full(const float *__restrict__ base, int ld, int r0, int k0,
+template <int R, bool KC, bool KT>
+__device__ __forceinline__ void load_tile_pipe(const float *__restrict__ base, int ld, int rows,
+                                               int kend, int r0, int k0,
                                                floatx4 (&reg)[Tile<R>::NLD]) {
   const int t = threadIdx.x;
 #pragma unroll
@@ -175,26 +182,30 @@ __device__ __forceinline__ void load_tile_full(const float *__restrict__ base, i
     const int f = t + NT * j;
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
-      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)(r0 + r) * ld + k0 + k4);
+      const int gr = min(r0 + r, rows - 1), gk = KT ? min(k0 + k4, kend - 4) : k0 + k4;
+      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)gr * ld + gk);
     } else {
       const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
-      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)(k0 + k) * ld + r0 + r4);
+      const int gr = min(r0 + r4, rows - 4), gk = KT ? min(k0 + k, kend - 1) : k0 + k;
+      reg[j] = *reinterpret_cast<const floatx4 *>(base + (size_t)gk * ld + gr);
     }
   }
 }
 
-template <int R, bool KC>
-__device__ __forceinline__ void store_tile_full(float *S, const floatx4 (&reg)[Tile<R>::NLD]) {
+template <int R, bool KC, bool KT>
+__device__ __forceinline__ void store_tile_pipe(float *S, const floatx4 (&reg)[Tile<R>::NLD], int k0,
+                                                int kend) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < Tile<R>::NLD; ++j) {
     const int f = t + NT * j;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     if (KC) {
       const int r = f >> 4, k4 = (f & 15) << 2;
-      *reinterpret_cast<floatx4 *>(S + r * PITCH + k4) = reg[j];
+      *reinterpret_cast<floatx4 *>(S + r * PITCH + k4) = (!KT || k0 + k4 < kend) ? reg[j] : zero;
     } else {
       const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
-      *reinterpret_cast<floatx4 *>(S + k * Tile<R>::RP + r4) = reg[j];
+      *reinterpret_cast<floatx4 *>(S + k * Tile<R>::RP + r4) = (!KT || k0 + k < kend) ? reg[j] : zero;
     }
   }
 }
@@ -279,7 +290,9 @@ constexpr int EPI_PARTIAL = 3;
 
 // R = 128 runs one block per CU (139 KB of LDS), so two waves per SIMD and
 // the full 256-register budget; R = 64 fits two blocks per CU.
-template <int R, bool AK, bool BKC, bool VEC, int EPI, bool FULL>
+// PIPE: 0 = bounds-checked loop, 1 = pipelined loop (K range a multiple of
+// BK), 2 = pipelined loop with a partial last K stage.
+template <int R, bool AK, bool BKC, bool VEC, int EPI, int PIPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, R == 128 ? 2 : 4)))
 void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   using TL = Tile<R>;
@@ -310,8 +323,9 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  if constexpr (FULL) {
-    // Every tile and K stage lies inside the matrices (nk >= 1).  Software
+  if constexpr (PIPE != 0) {
+    // Operands are float4-legal and nk >= 1; tile edges are clamped (see
+    // load_tile_pipe).  Software
     // pipeline, one barrier per stage, each stage's 16 MFMA steps in halves
     // f0 (s < 8) and f1 (s >= 8):
     //   f1 fragment reads | MFMAs s = 0..7 | MFMAs s = 8..11 with the LDS
@@ -321,16 +335,17 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     // fragment reads after it are covered by MFMAs on registers; global loads
     // are issued about one stage before their LDS writes.  Loads and writes
     // beyond the last stage re-read it into the idle buffer.
+    constexpr bool KT = PIPE == 2;
     const int mrow = wm * (R / 2), ncol = wn * (R / 2);
     floatx4 ra[TL::NLD], rb[TL::NLD];
-    load_tile_full<R, AK>(p.A, p.lda, m0, kbeg, ra);
-    load_tile_full<R, BKC>(p.B, p.ldb, n0, kbeg, rb);
-    store_tile_full<R, AK>(As[0], ra);
-    store_tile_full<R, BKC>(Bs[0], rb);
+    load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, kbeg, ra);
+    load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+    store_tile_pipe<R, AK, KT>(As[0], ra, kbeg, kend);
+    store_tile_pipe<R, BKC, KT>(Bs[0], rb, kbeg, kend);
     {
       const int k1 = kbeg + min(1, nk - 1) * BK;
-      load_tile_full<R, AK>(p.A, p.lda, m0, k1, ra);
-      load_tile_full<R, BKC>(p.B, p.ldb, n0, k1, rb);
+      load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, k1, ra);
+      load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, k1, rb);
     }
     __syncthreads();
     float f0a[T][8], f0b[T][8];
@@ -353,8 +368,11 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
 #pragma unroll
           for (int j = 0; j < T; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f0a[i][s], f0b[j][s], acc[i][j], 0, 0, 0);
-      store_tile_full<R, AK>(As[cur ^ 1], ra);
-      store_tile_full<R, BKC>(Bs[cur ^ 1], rb);
+      {
+        const int k1 = kbeg + min(kt + 1, nk - 1) * BK;  // the stage ra, rb hold
+        store_tile_pipe<R, AK, KT>(As[cur ^ 1], ra, k1, kend);
+        store_tile_pipe<R, BKC, KT>(Bs[cur ^ 1], rb, k1, kend);
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -375,8 +393,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
       read_frags<R, BKC>(Bs[cur ^ 1], ncol, koff, l32, f0b);
       {
         const int k2 = kbeg + min(kt + 2, nk - 1) * BK;
-        load_tile_full<R, AK>(p.A, p.lda, m0, k2, ra);
-        load_tile_full<R, BKC>(p.B, p.ldb, n0, k2, rb);
+        load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, k2, ra);
+        load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, k2, rb);
       }
 #pragma unroll
       for (int s = 4; s < 8; ++s)
@@ -457,7 +475,7 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   // v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
   // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile; slab rows are
   // every other row when the operand was read pairwise (read_frags).
-  constexpr bool PAIR_A = FULL && !AK && T == 2, PAIR_B = FULL && !BKC && T == 2;
+  constexpr bool PAIR_A = PIPE != 0 && !AK && T == 2, PAIR_B = PIPE != 0 && !BKC && T == 2;
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
 #pragma unroll
   for (int i = 0; i < T; ++i)
@@ -507,46 +525,47 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int sp
 }
 
 template <int R, bool AK, bool BKC, int EPI>
-static hipError_t launch_t(bool vec, bool full, const GemmArgs &a, int tm, int tn, int splits,
+static hipError_t launch_t(bool vec, bool ktail, const GemmArgs &a, int tm, int tn, int splits,
                           int kchunk, hipStream_t s) {
   dim3 grid(tm * tn, splits), block(NT);
-  if (vec && full)
-    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, true>), grid, block, 0, s, a, tm, tn,
+  if (vec && !ktail)
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, 1>), grid, block, 0, s, a, tm, tn,
                        kchunk);
   else if (vec)
-    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, false>), grid, block, 0, s, a, tm, tn,
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, 2>), grid, block, 0, s, a, tm, tn,
                        kchunk);
   else
-    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, false, EPI, false>), grid, block, 0, s, a, tm, tn,
+    hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, false, EPI, 0>), grid, block, 0, s, a, tm, tn,
                        kchunk);
   return hipGetLastError();
 }
 
 template <int R, int EPI>
-static hipError_t launch_e(char ta, char tb, bool vec, bool full, const GemmArgs &a, int tm, int tn,
+static hipError_t launch_e(char ta, char tb, bool vec, bool ktail, const GemmArgs &a, int tm, int tn,
                            int splits, int kchunk, hipStream_t s) {
   // op(A) 'N' -> A is M x K, K contiguous.  op(B) 'T' -> B is N x K, K contiguous.
   const bool ak = (ta == 'N');
   const bool bk = (tb == 'T');
-  if (ak && bk) return launch_t<R, true, true, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
-  if (ak && !bk) return launch_t<R, true, false, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
-  if (!ak && bk) return launch_t<R, false, true, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
-  return launch_t<R, false, false, EPI>(vec, full, a, tm, tn, splits, kchunk, s);
+  if (ak && bk) return launch_t<R, true, true, EPI>(vec, ktail, a, tm, tn, splits, kchunk, s);
+  if (ak && !bk) return launch_t<R, true, false, EPI>(vec, ktail, a, tm, tn, splits, kchunk, s);
+  if (!ak && bk) return launch_t<R, false, true, EPI>(vec, ktail, a, tm, tn, splits, kchunk, s);
+  return launch_t<R, false, false, EPI>(vec, ktail, a, tm, tn, splits, kchunk, s);
 }
 
 template <int R>
 static hipError_t launch_r(char ta, char tb, int epi, bool vec, const GemmArgs &a, int splits,
                            int kchunk, hipStream_t s) {
   const int tm = (a.M + R - 1) / R, tn = (a.N + R - 1) / R;
-  // every tile and K stage inside the matrices: the unchecked, scheduled loop
-  const bool full = vec && a.K > 0 && a.M % R == 0 && a.N % R == 0 && a.K % BK == 0;
-  if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, full, a, tm, tn, splits, kchunk, s);
+  // float4-legal operands take the pipelined loop; it checks k only when the
+  // last K stage is partial
+  const bool ktail = a.K % BK != 0;
+  if (splits > 1) return launch_e<R, EPI_PARTIAL>(ta, tb, vec, ktail, a, tm, tn, splits, kchunk, s);
   if (epi == EPI_BIAS_ACT)
-    return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
-  if (epi == EPI_DACT) return launch_e<R, EPI_DACT>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
+    return launch_e<R, EPI_BIAS_ACT>(ta, tb, vec, ktail, a, tm, tn, 1, kchunk, s);
+  if (epi == EPI_DACT) return launch_e<R, EPI_DACT>(ta, tb, vec, ktail, a, tm, tn, 1, kchunk, s);
   if (epi == EPI_BIAS_ADD)
-    return launch_e<R, EPI_BIAS_ADD>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
-  return launch_e<R, EPI_SCALE>(ta, tb, vec, full, a, tm, tn, 1, kchunk, s);
+    return launch_e<R, EPI_BIAS_ADD>(ta, tb, vec, ktail, a, tm, tn, 1, kchunk, s);
+  return launch_e<R, EPI_SCALE>(ta, tb, vec, ktail, a, tm, tn, 1, kchunk, s);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -558,6 +577,7 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0);
   vec = vec && (ak ? (a.K % 4 == 0) : (a.M % 4 == 0));
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
+  vec = vec && a.K > 0;  // the pipelined loop assumes at least one K stage
   // 128-wide tiles when they fill the 256 CUs, else 64-wide tiles; when even
   // those cannot fill the chip, split K (down to one K stage per split: a lone
   // tile runs at 1/256 of the chip).  Partials go to the workspace and are

@@ -64,9 +64,11 @@ class DBuf:
 @pytest.mark.parametrize("M,N,K,pad", [(128, 128, 32, 0), (200, 136, 72, 0), (37, 91, 53, 0),
                                        (256, 384, 1000, 4), (10, 128, 64, 0), (64, 10, 128, 1),
                                        (1, 7, 5, 0), (64, 128, 784, 0), (100, 60, 300, 3),
-                                       # unchecked full-tile loop: 128-wide tiles, 64-wide
-                                       # tiles, and 64-wide tiles with split K
-                                       (2048, 2560, 128, 0), (512, 640, 64, 4), (128, 192, 4096, 0)])
+                                       # pipelined loop, K a multiple of 64: 128-wide tiles,
+                                       # 64-wide tiles, and 64-wide tiles with split K
+                                       (2048, 2560, 128, 0), (512, 640, 64, 4), (128, 192, 4096, 0),
+                                       # pipelined loop with a partial last K stage (and split K)
+                                       (128, 192, 4000, 0), (4, 8, 68, 0), (1032, 1000, 4100, 0)])
 def test_gemm_layouts(gn, dev, ta, tb, M, N, K, pad):
     log(f"gemm ta={ta} tb={tb} M={M} N={N} K={K} pad={pad}")
     rng = np.random.default_rng(M * 7 + N * 3 + K)
