@@ -11,10 +11,11 @@ import numpy as np
 
 from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, Flatten, Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
-               Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal, fill_uniform,
-               fill_class_ids)
+               Sigmoid, Tanh, Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
+               fill_uniform, fill_class_ids)
 
-_ACTS = {"relu": ReLU, "linear": Linear, "softmax": Softmax, "logsoftmax": LogSoftmax}
+_ACTS = {"relu": ReLU, "sigmoid": Sigmoid, "tanh": Tanh, "linear": Linear, "softmax": Softmax,
+         "logsoftmax": LogSoftmax}
 
 
 def dense(i, o, act, ptr=False):

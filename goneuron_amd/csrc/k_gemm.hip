@@ -276,6 +276,10 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int &tm,
   tn = (pid % width) / gsz;
 }
 
+// Out-of-line activation for the GEMM epilogue's rare kinds.
+__device__ __noinline__ float apply_fwd_call(float v, int kind) { return apply_fwd(v, kind); }
+__device__ __noinline__ float apply_deriv_call(float out, int kind) { return apply_deriv(out, kind); }
+
 __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, int row, int col) {
   if (epi == EPI_SCALE) return v * p.alpha;
   if (epi == EPI_BIAS_ACT) return apply_fwd(v + (p.bias ? p.bias[col] : 0.f), p.act);
@@ -477,23 +481,68 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   // every other row when the operand was read pairwise (read_frags).
   constexpr bool PAIR_A = PIPE != 0 && !AK && T == 2, PAIR_B = PIPE != 0 && !BKC && T == 2;
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
+  auto store_all = [&](auto f) {
 #pragma unroll
-  for (int i = 0; i < T; ++i)
+    for (int i = 0; i < T; ++i)
 #pragma unroll
-    for (int j = 0; j < T; ++j) {
-      const int col = n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32);
-      if (col >= N) continue;
+      for (int j = 0; j < T; ++j) {
+        const int col = n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32);
+        if (col >= N) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
-        const int row = m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
-        if (row >= M) continue;
-        if (EPI == EPI_PARTIAL)
-          ws[(size_t)row * N + col] = acc[i][j][r];
-        else
-          p.C[(size_t)row * p.ldc + col] = epilogue(acc[i][j][r], EPI, p, row, col);
+        for (int r = 0; r < 16; ++r) {
+          const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
+          const int row = m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
+          if (row >= M) continue;
+          if (EPI == EPI_PARTIAL)
+            ws[(size_t)row * N + col] = acc[i][j][r];
+          else
+            p.C[(size_t)row * p.ldc + col] = f(acc[i][j][r], row, col);
+        }
       }
-    }
+  };
+  // The activation is chosen once per block: identity and ReLU inline, the
+  // rest through an out-of-line call, so the 64-value-per-lane epilogue stays
+  // small (inlining the float64 sigmoid / tanh into it blew the code past the
+  // instruction cache).
+  if constexpr (EPI == EPI_BIAS_ACT) {
+    const float *bias = p.bias;
+    if (p.act == F_IDENTITY)
+      store_all([&](float v, int, int col) { return v + (bias ? bias[col] : 0.f); });
+    else if (p.act == F_RELU)
+      store_all([&](float v, int, int col) {
+        const float z = v + (bias ? bias[col] : 0.f);
+        return z > 0.0f ? z : 0.0f;
+      });
+    else
+      store_all([&](float v, int, int col) {
+        return apply_fwd_call(v + (bias ? bias[col] : 0.f), p.act);
+      });
+  } else if constexpr (EPI == EPI_DACT) {
+    // aux row of an output row: itself, or the last row of its group of
+    // aux_div rows (Q10), found with a multiply-high by ceil(2^32 / d), exact
+    // while rows * d < 2^32 (else the division).
+    const float *aux = p.aux;
+    const int ldaux = p.ldaux;
+    const unsigned d = p.aux_div > 1 ? (unsigned)p.aux_div : 1u;
+    const bool magic_ok = (unsigned long long)M * d < (1ull << 32);
+    const unsigned magic = d > 1 ? (unsigned)(0xFFFFFFFFull / d + 1) : 0u;
+    auto saved = [&](int row, int col) {
+      int ar = row;
+      if (d > 1) {
+        const unsigned q = magic_ok ? __umulhi((unsigned)row, magic) : (unsigned)row / d;
+        ar = (int)(q * d + d - 1);
+      }
+      return aux[(size_t)ar * ldaux + col];
+    };
+    if (p.act == D_ONE)
+      store_all([&](float v, int, int) { return v * 1.0f; });
+    else if (p.act == D_RELU)
+      store_all([&](float v, int row, int col) { return v * (saved(row, col) > 0.0f ? 1.0f : 0.0f); });
+    else
+      store_all([&](float v, int row, int col) { return v * apply_deriv_call(saved(row, col), p.act); });
+  } else {
+    store_all([&](float v, int row, int col) { return epilogue(v, EPI, p, row, col); });
+  }
 }
 
 // Split-K reduction: partials summed in split order, then the epilogue.

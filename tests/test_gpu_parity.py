@@ -177,6 +177,17 @@ def test_wide_reduced_workers(gn, oracle):
     _compare_step(gn, oracle, configs.wide(width=128, classes=37, depth=2, B=48), steps=1, workers=4)
 
 
+def test_sigmoid_tanh_dense_epilogues(gn, oracle):
+    """Sigmoid and Tanh Dense layers large enough that their GEMMs run
+    unsplit, so the activation (forward) and its derivative (dX of the layer
+    above) are applied in the GEMM kernel's own epilogue; MSE loss."""
+    from goneuron_amd.configs import dense
+    cfg = dict(num=6, name="acts", B=2048, loss="mse", lr=1e-3, x="normal", in_len=96,
+               classes=None, targets="normal",
+               layers=[dense(96, 640, "sigmoid"), dense(640, 640, "tanh"), dense(640, 1, "linear")])
+    _compare_step(gn, oracle, cfg, steps=1)
+
+
 def test_odd_batch_and_sizes(gn, oracle):
     from goneuron_amd import configs
     cfg = configs.wide(width=72, classes=13, depth=2, B=19)
