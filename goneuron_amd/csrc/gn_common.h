@@ -120,6 +120,17 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
 hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
                            const float *Wh, const float *bias, float *D, int B, int T, int H,
                            hipStream_t s);
+// Cooperative BPTT (see k_lstm.hip): eligibility, the sync buffer it needs
+// (flags + exchange, zeroed once at allocation), and the launch.  Returns an
+// error without launching when not eligible or when the cooperative launch is
+// refused (then lstm_bwd_kernel is the fallback).  *epoch carries the flag
+// base across launches; spin_limit < 0 makes every wait time out at once.
+bool lstm_coop_eligible(int B, int H);
+size_t lstm_coop_sync_bytes(int B, int H);
+hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *tcb,
+                                const float *cbuf, const float *Wh, const float *bias, float *D,
+                                void *sync, int *err, unsigned *epoch, int B, int T, int H,
+                                int spin_limit, hipStream_t s);
 int lstm_gram_pitch(int n);
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
                                     double *coef, float *w, int B, int T, int I, int H, int W,

@@ -508,10 +508,13 @@ struct LayerRT {
   float *igb = nullptr, *tcb = nullptr, *cbuf = nullptr, *hbuf = nullptr;
   float *Dg = nullptr, *S = nullptr, *wts = nullptr;
   double *gram = nullptr, *coef = nullptr;
+  void *lsync = nullptr;                         // cooperative BPTT flags + exchange
+  unsigned lepoch = 0;                           // its flag base
+  bool lcoop = false;                            // cooperative BPTT usable
   // Embedding / PositionalEncoding / TransformerBlock / CLSPooling
   int V = 0, D = 0, NH = 0, FF = 0, causal = 0;
   int32_t *ids = nullptr;
-  int *err = nullptr;
+  int *err = nullptr;  // device error flag (Embedding: bad id; LSTM: cooperative wait timeout)
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -520,6 +523,7 @@ struct LayerRT {
 
 struct gn_model {
   gn_ctx *ctx = nullptr;
+  int lstm_spin_limit = 1 << 18;  // polls per cooperative BPTT wait (see gn_debug_lstm_spin_limit)
   std::vector<LayerRT> L;
   int loss_kind = 0;
   gn_adam_desc adam{};
@@ -882,6 +886,17 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), 2 * nchains * nmax, &cf))) return rc;
       R.gram = reinterpret_cast<double *>(g);
       R.coef = reinterpret_cast<double *>(cf);
+      if (lstm_coop_eligible(max_batch, (int)H)) {
+        const size_t bytes = lstm_coop_sync_bytes(max_batch, (int)H);
+        float *sy = nullptr, *er = nullptr;
+        if ((rc = model_alloc(M.get(), (bytes + 3) / 4, &sy))) return rc;
+        if ((rc = model_alloc(M.get(), 64, &er))) return rc;
+        HIP_OK(c, hipMemsetAsync(sy, 0, bytes, c->stream));
+        HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
+        R.lsync = sy;
+        R.err = reinterpret_cast<int *>(er);
+        R.lcoop = true;
+      }
     }
     if (R.d.kind == GN_LAYER_MAXPOOL2D) {
       float *am = nullptr;
@@ -1333,7 +1348,20 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
         {
           KTimer kt(c, GN_KCLASS_OTHER);
-          HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
+          bool done = false;
+          if (R.lcoop && lstm_coop_eligible(B, H)) {
+            const hipError_t e = launch_lstm_bwd_coop(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg,
+                                                      R.lsync, R.err, &R.lepoch, B, T, H,
+                                                      M->lstm_spin_limit, c->stream);
+            if (e == hipSuccess) {
+              done = true;
+            } else {  // refused (e.g. fewer free CUs than workgroups): per-sample kernel from now on
+              (void)hipGetLastError();
+              R.lcoop = false;
+            }
+          }
+          if (!done)
+            HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
           HIP_OK(c, launch_lstm_clip_weights(R.Dg, R.hbuf, in, R.gram, R.coef, R.wts, B, T, I, H,
                                              M->workers, c->stream));
           HIP_OK(c, launch_lstm_weight(R.Dg, R.wts, R.S, B, T, H, c->stream));
@@ -1445,18 +1473,29 @@ extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const flo
   return model_train_step(M, x, y, B);
 }
 
-// Out-of-range embedding ids raised a device flag (embedding.go:126-128 errors
-// on them); report and clear it once the stream has drained.
+// Device error flags, reported and cleared once the stream has drained:
+// out-of-range embedding ids (embedding.go:126-128 errors on them) and a
+// cooperative BPTT wait that timed out (its gradients are then invalid).
 static int check_embed_err(gn_model *M) {
   gn_ctx *c = M->ctx;
-  if (M->L.empty() || M->L[0].d.kind != GN_LAYER_EMBEDDING) return GN_OK;
+  if (M->L.empty()) return GN_OK;
+  const LayerRT &R = M->L[0];
+  const bool emb = R.d.kind == GN_LAYER_EMBEDDING, lstm = R.d.kind == GN_LAYER_LSTM_UNROLLER;
+  if ((!emb && !lstm) || !R.err) return GN_OK;
   int flag = 0;
-  HIP_OK(c, hipMemcpyAsync(&flag, M->L[0].err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipMemcpyAsync(&flag, R.err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
   if (flag) {
-    HIP_OK(c, hipMemsetAsync(M->L[0].err, 0, sizeof(int), c->stream));
-    return set_err(c, GN_ERR_INDEX, "embedding index out of bounds [0, %d)", M->L[0].V);
+    HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
+    if (emb) return set_err(c, GN_ERR_INDEX, "embedding index out of bounds [0, %d)", R.V);
+    return set_err(c, GN_ERR_HIP, "LSTM cooperative BPTT: a workgroup wait timed out");
   }
+  return GN_OK;
+}
+
+extern "C" int gn_debug_lstm_spin_limit(gn_model *M, int32_t polls) {
+  if (!M) return GN_ERR_INVALID;
+  M->lstm_spin_limit = polls;
   return GN_OK;
 }
 

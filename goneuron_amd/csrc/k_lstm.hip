@@ -247,6 +247,175 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
   }
 }
 
+// Cooperative BPTT (H = 32, 64, 128 or 256, B <= 64): the per-sample
+// recurrence of lstm_bwd_kernel is bound by every step re-reading the 4H x H
+// recurrent weights from L2 into one CU (1 MB per step at H = 256).  Here a
+// group of LC_KM workgroups shares LC_SPG samples; member m keeps columns
+// [m*U, (m+1)*U) of Wh (U = H / LC_KM) in LDS for the whole sequence, owns
+// those hidden units' state and gate deltas, and computes their dhPrev from
+// the group's full dG.  Per step each member publishes its units' dG through
+// an exchange buffer (double-buffered by step parity) and a flag (agent-scope
+// release / acquire), waits for the other members' flags, reads the full dG
+// and does its share of Wh^T dG from LDS.  All shared words are agent-scope
+// atomics (device-coherent loads and stores, no cache flushes); a member
+// waits for its exchange stores to complete before raising its flag, and
+// reads the exchange only after every flag of the step is up.  Every wait is
+// bounded by
+// spin_limit polls; a timeout sets *err and the kernel runs to its end
+// without further waits (results are then invalid and the caller reports
+// the error).  All workgroups must be resident together: launched
+// cooperatively, one per CU.  Workgroup ids map to XCDs round-robin, so a
+// group's members are given ids of one residue mod 8 (one XCD, one L2).
+constexpr int LC_KM = 8;
+constexpr int LC_SPG = 2;
+constexpr int LC_NT = 1024;
+
+__host__ __device__ inline int lstm_coop_groups(int B) { return (B + LC_SPG - 1) / LC_SPG; }
+__host__ __device__ inline int lstm_coop_grid(int B) {
+  return (lstm_coop_groups(B) + 7) / 8 * 8 * LC_KM;
+}
+static inline size_t lstm_coop_lds(int H) {
+  const int U = H / LC_KM;
+  return ((size_t)4 * H * (U + 4) + (size_t)LC_SPG * 4 * H + (size_t)(LC_NT / 64) * LC_SPG * U) *
+         sizeof(float);
+}
+
+__global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
+    const float *__restrict__ gh, const float *__restrict__ igb, const float *__restrict__ tcb,
+    const float *__restrict__ cbuf, const float *__restrict__ Wh, const float *__restrict__ bias,
+    float *__restrict__ D, unsigned *flags, float *X, int *err, int B, int T, int H, unsigned base,
+    int spin_limit) {
+  extern __shared__ float sm[];
+  const int U = H / LC_KM, UP = U + 4, G4 = 4 * H;
+  float *Wsl = sm;                          // [4H][UP]: Wh[r][u0 + u]
+  float *dGs = Wsl + (size_t)G4 * UP;       // [SPG][4H]: the group's dG of this step
+  float *part = dGs + LC_SPG * G4;          // [waves][SPG][U]
+  const int wg = blockIdx.x, xcd = wg & 7, rest = wg >> 3;
+  const int m = rest % LC_KM, g = (rest / LC_KM) * 8 + xcd;
+  const int ngroups = lstm_coop_groups(B);
+  if (g >= ngroups) return;  // every member of a group computes the same g
+  const int Bp = ngroups * LC_SPG;
+  const int u0 = m * U;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int idx = tid; idx < G4 * U; idx += LC_NT) {
+    const int r = idx / U, u = idx - r * U;
+    Wsl[r * UP + u] = Wh[(size_t)r * H + u0 + u];
+  }
+  // owner lanes: thread s * U + u (wave 0) holds unit u0 + u of sample g*SPG + s
+  const bool own = tid < LC_SPG * U;
+  const int so = tid / U, uo = tid - so * U;
+  const int bo = g * LC_SPG + so, io = u0 + uo;
+  const bool valid = own && bo < B;
+  float cur = 0.f, dcn = 0.f, fg = 0.f, gg = 0.f, og = 0.f, dfd = 0.f, dgd = 0.f, dod = 0.f;
+  float ign = 0.f, tcn = 0.f, cpn = 0.f;
+  const size_t ob = (size_t)bo * T * H + io;
+  if (valid) {
+    cur = gh[(size_t)bo * H + io];
+    fg = sigm(bias[H + io]);
+    gg = tanh32(bias[2 * H + io]);
+    og = sigm(bias[3 * H + io]);
+    dfd = fg * (1.0f - fg);
+    dgd = 1.0f - gg * gg;
+    dod = og * (1.0f - og);
+    ign = igb[ob + (size_t)(T - 1) * H];
+    tcn = tcb[ob + (size_t)(T - 1) * H];
+    cpn = T > 1 ? cbuf[ob + (size_t)(T - 2) * H] : 0.f;
+    float *padrow = D + ((size_t)bo * (T + 1) + T) * G4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) padrow[q * H + io] = 0.f;
+  }
+  // partial products: thread (share, c4) sums rows of its share for units
+  // 4*c4 .. 4*c4+3 of both samples
+  const int C4 = U / 4;                     // 1, 2, 4 or 8: divides 64
+  const int c4 = tid % C4, share = tid / C4;
+  const int nshare = LC_NT / C4;
+  const int rps = (G4 + nshare - 1) / nshare;
+  const int r0 = min(share * rps, G4), r1 = min(r0 + rps, G4);
+  bool bad = false;
+  for (int step = 0; step < T; ++step) {
+    const int t = T - 1 - step, par = t & 1;
+    if (own) {
+      const float ig = ign, tc = tcn, cp = cpn;
+      if (valid && t > 0) {
+        ign = igb[ob + (size_t)(t - 1) * H];
+        tcn = tcb[ob + (size_t)(t - 1) * H];
+        cpn = t > 1 ? cbuf[ob + (size_t)(t - 2) * H] : 0.f;
+      }
+      const float did = ig * (1.0f - ig);
+      const float dc = cur * og * (1 - tc * tc) + dcn;
+      const float dv[4] = {dc * gg * did, dc * cp * dfd, dc * ig * dgd, cur * tc * dod};
+      dcn = dc * fg;
+      float *xrow = X + ((size_t)par * Bp + bo) * G4;
+      if (valid) {
+        float *row = D + ((size_t)bo * (T + 1) + t) * G4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) row[q * H + io] = dv[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        __hip_atomic_store(xrow + q * H + io, valid ? dv[q] : 0.f, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      // the exchange stores must have completed (device-coherent) before the
+      // flag is raised: s_waitcnt vmcnt(0)
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const unsigned want = base + (unsigned)step + 1u;
+      if (lane == 0)
+        __hip_atomic_store(flags + g * LC_KM + m, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // lanes 0..KM-1 poll the members' flags together
+      if (!bad) {
+        int spins = 0;
+        while (true) {
+          bool ready = true;
+          if (lane < LC_KM)
+            ready = (int)(__hip_atomic_load(flags + g * LC_KM + lane, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) - want) >= 0;
+          if (__all(ready)) break;
+          if (spin_limit < 0 || ++spins > spin_limit) {
+            bad = true;
+            if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < LC_SPG * G4; idx += LC_NT) {
+      const int s = idx / G4;
+      dGs[idx] = __hip_atomic_load(X + ((size_t)par * Bp + g * LC_SPG + s) * G4 + (idx - s * G4),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+    for (int r = r0; r < r1; ++r) {
+      const float4 w = *reinterpret_cast<const float4 *>(Wsl + r * UP + 4 * c4);
+      const float g0 = dGs[r], g1 = dGs[G4 + r];
+      a0.x += w.x * g0; a0.y += w.y * g0; a0.z += w.z * g0; a0.w += w.w * g0;
+      a1.x += w.x * g1; a1.y += w.y * g1; a1.z += w.z * g1; a1.w += w.w * g1;
+    }
+    for (int o = C4; o < 64; o <<= 1) {
+      a0.x += __shfl_xor(a0.x, o, 64); a0.y += __shfl_xor(a0.y, o, 64);
+      a0.z += __shfl_xor(a0.z, o, 64); a0.w += __shfl_xor(a0.w, o, 64);
+      a1.x += __shfl_xor(a1.x, o, 64); a1.y += __shfl_xor(a1.y, o, 64);
+      a1.z += __shfl_xor(a1.z, o, 64); a1.w += __shfl_xor(a1.w, o, 64);
+    }
+    if (lane < C4) {
+      float *p0 = part + (size_t)wave * LC_SPG * U + 4 * lane;
+      *reinterpret_cast<float4 *>(p0) = a0;
+      *reinterpret_cast<float4 *>(p0 + U) = a1;
+    }
+    __syncthreads();
+    if (own) {
+      float sum = 0.f;
+      for (int w = 0; w < LC_NT / 64; ++w) sum += part[(size_t)w * LC_SPG * U + so * U + uo];
+      cur += sum;
+    }
+  }
+}
+
 // Contribution u of chain ch: sample b = b0 + u / T, backward step t = T-1 - u % T.
 struct ChainMap {
   int T, chunk, B;
@@ -708,6 +877,47 @@ hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, 
     hipLaunchKernelGGL(lstm_bwd_kernel<false>, dim3(B), dim3(1024), shm, s, gh, igb, tcb, cbuf, Wh,
                        bias, D, T, H, L.GB, L.NQ);
   return hipGetLastError();
+}
+
+bool lstm_coop_eligible(int B, int H) {
+  // U = H / 8 units per member, handled 4 at a time by U / 4 lanes whose
+  // shuffle reduction needs a power of two
+  return B >= 1 && B <= 64 && (H == 32 || H == 64 || H == 128 || H == 256);
+}
+
+size_t lstm_coop_sync_bytes(int B, int H) {
+  const int Bp = lstm_coop_groups(B) * LC_SPG;
+  return (size_t)lstm_coop_groups(B) * LC_KM * sizeof(unsigned) + 256 +
+         (size_t)2 * Bp * 4 * H * sizeof(float);
+}
+
+// sync: lstm_coop_sync_bytes(B, H) bytes, 256-byte aligned; flags first (their
+// values only ever grow: each launch passes base = the previous launch's last
+// flag value), then the exchange buffer.  err: device int, 0 on success.
+hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *tcb,
+                                const float *cbuf, const float *Wh, const float *bias, float *D,
+                                void *sync, int *err, unsigned *epoch, int B, int T, int H,
+                                int spin_limit, hipStream_t s) {
+  if (!lstm_coop_eligible(B, H)) return hipErrorInvalidValue;
+  unsigned *flags = reinterpret_cast<unsigned *>(sync);
+  float *X = reinterpret_cast<float *>(reinterpret_cast<char *>(sync) +
+                                       (((size_t)lstm_coop_groups(B) * LC_KM * sizeof(unsigned) + 255) & ~(size_t)255));
+  const size_t shm = lstm_coop_lds(H);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_bwd_coop_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  unsigned base = *epoch;
+  void *args[] = {(void *)&gh, (void *)&igb, (void *)&tcb, (void *)&cbuf, (void *)&Wh,
+                  (void *)&bias, (void *)&D, (void *)&flags, (void *)&X, (void *)&err,
+                  (void *)&B, (void *)&T, (void *)&H, (void *)&base, (void *)&spin_limit};
+  hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(lstm_bwd_coop_kernel),
+                                            dim3(lstm_coop_grid(B)), dim3(LC_NT), args, shm, s);
+  if (e == hipSuccess) *epoch = base + (unsigned)T;
+  return e;
 }
 
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,

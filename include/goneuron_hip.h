@@ -140,6 +140,12 @@ int gn_model_train_step(gn_model *m, const float *x, const float *y, int32_t B, 
 /* Same with HBM-resident x / y; the mean loss stays on the device (read it
  * with gn_model_read_loss).  No host synchronisation. */
 int gn_model_train_step_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
+/* Test hook (no counterpart in the reference): polls per wait of the
+ * cooperative LSTM BPTT kernel before it reports a timeout (default 2^18);
+ * a negative value makes every wait time out at once, so the error path
+ * (GN_ERR_HIP at the next gn_model_read_loss / gn_model_train_step) can be
+ * tested without a fault. */
+int gn_debug_lstm_spin_limit(gn_model *model, int32_t polls);
 /* Forward + backward + average only (grads valid, no Adam step). */
 int gn_model_accumulate_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
 /* Network.Step (net.go:260-284): Adam.NewStep + StepInPlace on the arena. */

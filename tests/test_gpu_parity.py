@@ -250,6 +250,32 @@ def test_lstm_small_unrolled_path(gn, oracle, workers):
     _compare_step(gn, oracle, cfg, steps=3, workers=workers)
 
 
+@pytest.mark.parametrize("workers", [1, 3])
+def test_lstm_coop_odd_batch(gn, oracle, workers):
+    """The cooperative BPTT path (hidden 64: eight workgroups of 8 units per
+    pair of samples) with an odd batch, so the last pair has one sample."""
+    from goneuron_amd import configs
+    cfg = configs.lstm(B=11, T=12, inp=16, hidden=64)
+    _compare_step(gn, oracle, cfg, steps=2, workers=workers)
+
+
+def test_lstm_coop_timeout_is_reported(gn):
+    """A cooperative BPTT wait that times out (forced from the host: negative
+    poll limit, every wait gives up at once) surfaces as an error at the next
+    synchronising call; with the limit restored the next step is clean."""
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib, GNError
+    cfg = configs.lstm(B=8, T=6, inp=8, hidden=64)
+    x, y = configs.inputs(cfg)
+    model = configs.build(cfg)
+    model.TrainBatch(x, y)
+    assert lib().gn_debug_lstm_spin_limit(model.h, -1) == 0
+    with pytest.raises(GNError, match="timed out"):
+        model.TrainBatch(x, y)
+    assert lib().gn_debug_lstm_spin_limit(model.h, 1 << 18) == 0
+    model.TrainBatch(x, y)  # raises if the error were still pending
+
+
 def _random_block(cfg, scale=0.2, seed=21):
     """Non-zero TransformerBlock weights (the reference starts it at 0, Q11),
     so attention, LayerNorm and the FF path carry gradient."""
