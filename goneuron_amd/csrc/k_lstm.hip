@@ -97,20 +97,24 @@ __device__ __forceinline__ float4 dot4_strided(const float4 *__restrict__ W, int
 // Recurrent mat-vec of one step: part[q][c] = sum over the q-th share of k of
 // W[k][c] * v[k] (W is K x H row-major).  V4: thread (g, q) owns columns
 // 4g..4g+3 (H % 4 == 0, W 16-byte aligned); otherwise thread (i, q) owns
-// column i.  GB = threads per share (a multiple of 64), NQ shares.
+// column i.  GB = threads per share (a multiple of 64), NQ shares.  Shares
+// q < QL read their rows from Wl, a copy of W's leading rows in LDS (the rest
+// stream from L2 every step).
 template <bool V4>
-__device__ __forceinline__ void step_matvec(const float *__restrict__ W, const float *v, int K,
-                                            int H, int GB, int NQ, float *part) {
+__device__ __forceinline__ void step_matvec(const float *__restrict__ W, const float *Wl, int QL,
+                                            const float *v, int K, int H, int GB, int NQ,
+                                            float *part) {
   const int c = threadIdx.x % GB, q = threadIdx.x / GB;
   if (q >= NQ) return;
   const int k0 = (K * q) / NQ, k1 = (K * (q + 1)) / NQ;
   if (V4) {
     if (4 * c < H) {
-      const float4 s = dot4_strided<16>(reinterpret_cast<const float4 *>(W) + c, H / 4, v, k0, k1);
+      const float4 s = q < QL ? dot4_strided<16>(reinterpret_cast<const float4 *>(Wl) + c, H / 4, v, k0, k1)
+                              : dot4_strided<16>(reinterpret_cast<const float4 *>(W) + c, H / 4, v, k0, k1);
       *reinterpret_cast<float4 *>(part + q * H + 4 * c) = s;
     }
   } else if (c < H) {
-    part[q * H + c] = dot_strided<32>(W + c, H, v, k0, k1);
+    part[q * H + c] = q < QL ? dot_strided<32>(Wl + c, H, v, k0, k1) : dot_strided<32>(W + c, H, v, k0, k1);
   }
 }
 
@@ -130,9 +134,15 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
                                                         float *__restrict__ cbuf,
                                                         float *__restrict__ hbuf,
                                                         float *__restrict__ out, int T, int H,
-                                                        int GB, int NQ) {
+                                                        int GB, int NQ, int QL) {
   extern __shared__ float sm[];
   float *hs = sm, *part = sm + ((H + 3) & ~3);  // part[NQ][H], 16-byte aligned
+  float *Wl = part + NQ * H;                    // WhT rows [0, H*QL/NQ), 16-byte aligned
+  {
+    const int nl = (H * QL / NQ) * H;
+    for (int e = threadIdx.x * 4; e < nl; e += blockDim.x * 4)
+      *reinterpret_cast<float4 *>(Wl + e) = *reinterpret_cast<const float4 *>(WhT + e);
+  }
   const int b = blockIdx.x;
   const int i = threadIdx.x;
   const bool own = i < H;
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
   for (int t = 0; t < T; ++t) {
     const float xwc = xwn;
     if (own && t + 1 < T) xwn = xwb[(size_t)(t + 1) * H + i];  // next step's, in flight
-    step_matvec<V4>(WhT, hs, H, H, GB, NQ, part);
+    step_matvec<V4>(WhT, Wl, QL, hs, H, H, GB, NQ, part);
     __syncthreads();
     if (own) {
       float sh = 0.f;
@@ -237,7 +247,7 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
       row[3 * H + i] = dO;
     }
     __syncthreads();
-    step_matvec<V4>(Wh, dG, G4, H, GB, NQ, part);
+    step_matvec<V4>(Wh, nullptr, 0, dG, G4, H, GB, NQ, part);
     __syncthreads();
     if (own) {
       float s = 0.f;
@@ -365,6 +375,10 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
       if (lane == 0)
         __hip_atomic_store(flags + g * LC_KM + m, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // lanes 0..KM-1 poll the members' flags together
+      if (!bad && spin_limit < 0) {  // forced timeout (test hook): give up without polling
+        bad = true;
+        if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       if (!bad) {
         int spins = 0;
         while (true) {
@@ -373,7 +387,7 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
             ready = (int)(__hip_atomic_load(flags + g * LC_KM + lane, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT) - want) >= 0;
           if (__all(ready)) break;
-          if (spin_limit < 0 || ++spins > spin_limit) {
+          if (++spins > spin_limit) {
             bad = true;
             if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
@@ -556,7 +570,10 @@ __global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restri
                                                            double *__restrict__ Gm, ChainMap cm,
                                                            int I, int H, int nmax) {
   constexpr int KS = 32;
-  __shared__ double sv[KS][64], su[KS][64];
+  // row pitch 80 doubles (640 B = 128 B mod 256 B): the four k-rows one
+  // operand read touches (16 lanes each, 128 B) fall in alternate bank halves
+  constexpr int GP = 80;
+  __shared__ double sv[KS][GP], su[KS][GP];
   const int ch = blockIdx.y;
   const int n = cm.len(ch);
   int lin = blockIdx.x, tv = 0;
@@ -570,8 +587,10 @@ __global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restri
   const int wm = wv >> 1, wn = wv & 1;
   const int G4 = 4 * H;
   const int Kz = G4 + ((H + I + KS - 1) / KS) * KS;  // padded K
-  // staging: thread -> row rr (0..63), float4 column groups kq and kq + 16
-  const int rr = tid >> 2, kq = (tid & 3) * 4;
+  // staging: thread -> row rr (0..63), float4 column groups kq and kq + 16;
+  // a wave holds one kq, so each LDS store writes 64 consecutive doubles of a
+  // k-row (no bank conflicts)
+  const int rr = tid & 63, kq = (tid >> 6) * 4;
   const int iv = tv * 64 + rr, iu = tu * 64 + rr;
   const bool okv = iv < n, oku = iu < n;
   int bv = 0, tvv = 0, bu = 0, tuu = 0;
@@ -854,13 +873,26 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
                            hipStream_t s) {
   if (!lstm_fits(H)) return hipErrorInvalidValue;
   const LstmLayout L = lstm_layout(H, WhT);
-  const size_t shm = (size_t)(((H + 3) & ~3) + L.NQ * H) * sizeof(float);
+  const size_t base = (size_t)(((H + 3) & ~3) + L.NQ * H) * sizeof(float);
+  // as many leading shares of WhT in LDS as fit 128 KB (whole float4 rows:
+  // the V4 layout only; the copy needs 16-byte aligned WhT)
+  int QL = 0;
+  if (L.v4 && H % 4 == 0)
+    while (QL < L.NQ && (size_t)(H * (QL + 1) / L.NQ) * H * sizeof(float) <= (128u << 10)) ++QL;
+  const size_t shm = base + (size_t)(H * QL / L.NQ) * H * sizeof(float);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_fwd_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
   if (L.v4)
     hipLaunchKernelGGL(lstm_fwd_kernel<true>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
-                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ, QL);
   else
     hipLaunchKernelGGL(lstm_fwd_kernel<false>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
-                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ, 0);
   return hipGetLastError();
 }
 
