@@ -724,27 +724,28 @@ __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__rest
       double sl = lane < nb ? sold[lane] : 0.0;  // running s of row v0 + lane
       double al = 0.0;                            // a_{v0 + lane} once known
       double blkscale = 1.0;
-      double tjl = T[0][lane], tjj = T[0][0];    // step j's tile values, read a step early
+      // the lane's tile column and the diagonal, read two steps ahead
+      double t0 = T[0][lane], d0 = T[0][0];
+      double t1 = nb > 1 ? T[1][lane] : 0.0, d1 = nb > 1 ? T[1][1] : 0.0;
       for (int j = 0; j < nb; ++j) {
-        double tnl = 0.0, tnj = 0.0;
-        if (j + 1 < nb) {
-          tnl = T[j + 1][lane];
-          tnj = T[j + 1][j + 1];
+        double t2 = 0.0, d2 = 0.0;
+        if (j + 2 < nb) {
+          t2 = T[j + 2][lane];
+          d2 = T[j + 2][j + 2];
         }
         const double aj = Q;
         const double sj = readlane_d(sl, j);
         al = lane == j ? aj : al;
-        sl = lane > j ? fma(aj, tjl, sl) : sl;
-        const double N2 = fma(2.0 * P, sj, nrm2) + tjj;
-        if (N2 > 1.0) {  // clipGradients: scale by 1/N (rsq + one Newton step)
-          double y = __builtin_amdgcn_rsq(N2);
-          y = y * (1.5 - 0.5 * N2 * (y * y));
-          P *= y;
-          Q *= N2 * y;
-          nrm2 = (y * y) * N2;
-        } else {
-          nrm2 = N2 > 0.0 ? N2 : 0.0;
-        }
+        sl = lane > j ? fma(aj, t0, sl) : sl;
+        const double N2 = fma(2.0 * P, sj, nrm2) + d0;
+        // clipGradients: scale by 1/N when N > 1 (rsq + one Newton step);
+        // both outcomes are computed and selected, no branch on the chain
+        double y = __builtin_amdgcn_rsq(N2);
+        y = y * (1.5 - 0.5 * N2 * (y * y));
+        const bool clip = N2 > 1.0;
+        P = clip ? P * y : P;
+        Q = clip ? Q * (N2 * y) : Q;
+        nrm2 = clip ? (y * y) * N2 : (N2 > 0.0 ? N2 : 0.0);
         if (P < 1e-150) {  // fold P into every coefficient so far
           sl *= P;
           al *= P;
@@ -752,8 +753,10 @@ __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__rest
           Q *= P;
           P = 1.0;
         }
-        tjl = tnl;
-        tjj = tnj;
+        t0 = t1;
+        t1 = t2;
+        d0 = d1;
+        d1 = d2;
       }
       ablk[lane] = lane < nb ? al : 0.0;
       if (lane < nb) ac[v0 + lane] = al;
