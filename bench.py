@@ -153,6 +153,30 @@ def library_sgemm():
                       "tflops": tf, "frac_of_peak": tf / PEAK_FP32_MFMA_TFLOPS}), flush=True)
 
 
+def predict_bench(args, cfg, model, dev, dx, B, workers):
+    """Inference throughput (f3): K forward passes in inference mode over the
+    config's batch, inputs and outputs in HBM."""
+    import ctypes as C
+    from goneuron_amd._lib import lib, check
+    out = C.c_void_p()
+    check(dev.h, lib().gn_malloc(dev.h, B * model.out_size * 4, C.byref(out)))
+    run = lambda: check(dev.h, lib().gn_model_predict_device(model.h, dx, B, out))
+    for _ in range(args.warmup):
+        run()
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    dev.sync()
+    el = time.perf_counter() - t0
+    print(json.dumps({"metric": "predict samples/s (inference forward) on 1 MI355X", "value": args.steps * B / el,
+                      "unit": "samples/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "ms_per_step": 1e3 * el / args.steps, "higher_is_better": True,
+                      "dtype": "f32", "data": "synthetic",
+                      "config": {"workload": cfg["name"], "batch": B, "mode": "inference"}}), flush=True)
+    check(dev.h, lib().gn_free(dev.h, out))
+
+
 def copy_probe(mib):
     """A copy kernel of known size: reads and writes mib MiB per launch."""
     import torch
@@ -181,6 +205,9 @@ def main():
                          "waves per SIMD, short and sustained) and print its rates")
     ap.add_argument("--library-sgemm", action="store_true",
                     help="only time torch.mm (fp32) on the C3 forward GEMM shape, as a reference point")
+    ap.add_argument("--predict", action="store_true",
+                    help="time the inference path instead (Sequential.PredictBatch: forward in "
+                         "inference mode on HBM-resident inputs, gn_model_predict_device)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
@@ -219,6 +246,9 @@ def main():
         return p
 
     dx, dy = dbuf(x), dbuf(y)
+    if args.predict:
+        predict_bench(args, cfg, model, dev, dx, B, workers)
+        return
     step = lambda: check(dev.h, lib().gn_model_train_step_device(model.h, dx, dy, B))
     for _ in range(args.warmup):
         step()

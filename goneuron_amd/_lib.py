@@ -82,6 +82,7 @@ SIGNATURES = {
     "gn_model_step": (C.c_int, [vp]),
     "gn_model_read_loss": (C.c_int, [vp, f32p]),
     "gn_model_predict": (C.c_int, [vp, f32p, C.c_int32, f32p]),
+    "gn_model_predict_device": (C.c_int, [vp, vp, C.c_int32, vp]),
     "gn_model_set_training": (C.c_int, [vp, C.c_int32]),
     "gn_model_layer_output": (C.c_int, [vp, C.c_int32, f32p, C.c_int64]),
     "gn_model_layer_argmax": (C.c_int, [vp, C.c_int32, i32p, C.c_int64]),

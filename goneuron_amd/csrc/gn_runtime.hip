@@ -1543,6 +1543,23 @@ extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *o
   HIP_OK(c, hipMemcpyAsync(out, O.out, (size_t)B * O.out_len * sizeof(float),
                            hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  return check_embed_err(M);
+}
+
+extern "C" int gn_model_predict_device(gn_model *M, const float *x, int32_t B, float *out) {
+  if (!M) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  if (B <= 0 || B > M->maxB || !x || !out) return set_err(c, GN_ERR_INVALID, "bad predict args");
+  const int saved = M->training;
+  M->training = 0;
+  int rc = model_forward(M, x, B, false);
+  M->training = saved;
+  if (rc) return rc;
+  M->last_B = B;
+  LayerRT &O = M->L.back();
+  HIP_OK(c, hipMemcpyAsync(out, O.out, (size_t)B * O.out_len * sizeof(float),
+                           hipMemcpyDeviceToDevice, c->stream));
   return GN_OK;
 }
 

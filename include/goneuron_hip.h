@@ -154,6 +154,9 @@ int gn_model_read_loss(gn_model *m, float *loss);
 /* Sequential.Predict / PredictBatch (sequential.go:118-160): inference mode
  * forward of B samples; out is B x out_size. */
 int gn_model_predict(gn_model *m, const float *x, int32_t B, float *out);
+/* The same with HBM-resident x (B x in_size) and output (B x out_size); no
+ * host synchronisation (the device-side ForwardBatch of sequential.go:145-160). */
+int gn_model_predict_device(gn_model *m, const float *x_dev, int32_t B, float *out_dev);
 int gn_model_set_training(gn_model *m, int32_t training);
 /* Layer probes for parity tests: saved output of `layer` for the last batch
  * (B x out_len), MaxPool2D argmax switches (B x out_len, int32). */

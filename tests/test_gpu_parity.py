@@ -167,6 +167,51 @@ def test_mlp_predict(gn, oracle):
         np.testing.assert_allclose(out[b], net.forward(x[b]), rtol=1e-5, atol=1e-6)
 
 
+def _predict_cases():
+    from goneuron_amd import configs
+    return {
+        "cnn": (configs.cnn(B=16), None),
+        "wide": (configs.wide(width=256, classes=100, B=32), None),
+        "gpt": (configs.gpt(B=4, T=16, vocab=50, dim=32, heads=2, ff=64), "block"),
+        "lstm": (configs.lstm(B=8, T=12, inp=16, hidden=64), None),
+    }
+
+
+@pytest.mark.parametrize("name", ["cnn", "wide", "gpt", "lstm"])
+def test_predict_matches_oracle_after_training(gn, oracle, name):
+    """Sequential.PredictBatch (inference mode) on the host entry and on the
+    device-pointer entry, after one training step, against the oracle's
+    per-sample forward on the same weights."""
+    import ctypes as C
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib, check
+    cfg, extra = _predict_cases()[name]
+    x, y = configs.inputs(cfg)
+    B = cfg["B"]
+    model = configs.build(cfg)
+    if extra == "block":
+        p = _random_block(cfg)(model.Params().copy())
+        model.SetParams(p)
+    model.TrainBatch(x, y)
+    net = oracle_net(oracle, cfg)
+    net.params[:] = model.Params()
+    net.set_training(False)
+    out = model.PredictBatch(x)
+    ref = np.stack([net.forward(x[b])[:out.shape[1]] for b in range(B)])
+    assert max_rel(out, ref) <= TOL, max_rel(out, ref)
+    dev = model.device
+    dx, dout = C.c_void_p(), C.c_void_p()
+    check(dev.h, lib().gn_malloc(dev.h, x.nbytes, C.byref(dx)))
+    check(dev.h, lib().gn_malloc(dev.h, out.nbytes, C.byref(dout)))
+    check(dev.h, lib().gn_memcpy_h2d(dev.h, dx, x.ctypes.data, x.nbytes))
+    check(dev.h, lib().gn_model_predict_device(model.h, dx, B, dout))
+    got = np.empty_like(out)
+    check(dev.h, lib().gn_memcpy_d2h(dev.h, got.ctypes.data, dout, got.nbytes))
+    np.testing.assert_array_equal(got, out)
+    check(dev.h, lib().gn_free(dev.h, dx))
+    check(dev.h, lib().gn_free(dev.h, dout))
+
+
 def test_wide_reduced(gn, oracle):
     from goneuron_amd import configs
     _compare_step(gn, oracle, configs.wide(width=256, classes=100, B=64), steps=2)
