@@ -22,7 +22,7 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
+    "AvgPool2D", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "Ref", "Adam", "MSE",
     "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
 ]
@@ -61,7 +61,7 @@ def Ref(act: Activation) -> Activation:
 
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
- LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER) = range(1, 11)
+ LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D) = range(1, 12)
 
 
 class Layer:
@@ -134,6 +134,13 @@ def Conv2D(*args):
 
 def MaxPool2D(kernel, stride, padding, *in_channels):
     return Layer(LAYER_MAXPOOL2D, kernel=kernel, stride=stride, padding=padding,
+                 in_channels=in_channels[0] if in_channels else -1)
+
+
+def AvgPool2D(kernel, stride, padding, *in_channels):
+    """goneuron.AvgPool2D (goneuron.go:256): average over the in-bounds cells of
+    each window (padding not counted)."""
+    return Layer(LAYER_AVGPOOL2D, kernel=kernel, stride=stride, padding=padding,
                  in_channels=in_channels[0] if in_channels else -1)
 
 

@@ -9,7 +9,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, Flatten, Embedding,
+from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, Flatten,
+               Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
                Sigmoid, Tanh, Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
                fill_uniform, fill_class_ids)
@@ -101,6 +102,8 @@ def product_layers(cfg):
             out.append(Conv2D(d["inC"], d["outC"], d["k"], d["s"], d["p"], _ACTS[d["act"]]))
         elif k == "maxpool2d":
             out.append(MaxPool2D(d["k"], d["s"], d["p"], d["inC"]))
+        elif k == "avgpool2d":
+            out.append(AvgPool2D(d["k"], d["s"], d["p"], d["inC"]))
         elif k == "embedding":
             out.append(Embedding(d["vocab"], d["dim"]))
         elif k == "posenc":

@@ -111,6 +111,8 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
                               int B, hipStream_t st);
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st);
+hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
+hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
 
 // ---- SequenceUnroller(LSTM) ----
 hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hipStream_t s);

@@ -743,19 +743,20 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.out_len = cs.outC * cs.oH * cs.oW;
         break;
       }
-      case GN_LAYER_MAXPOOL2D: {
+      case GN_LAYER_MAXPOOL2D:
+      case GN_LAYER_AVGPOOL2D: {  // avgpool2d.go:86-126 infers H, W the same way
         PoolShape &ps = R.ps;
         ps.C = R.d.in_channels <= 0 ? 1 : R.d.in_channels;  // maxpool2d.go:112-114 (Q8)
         ps.k = R.d.kernel;
         ps.stride = R.d.stride;
         ps.pad = R.d.padding;
         if (ps.k <= 0 || ps.stride <= 0 || ps.pad < 0)
-          return set_err(c, GN_ERR_INVALID, "layer %d: bad MaxPool2D geometry", i);
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad pooling geometry", i);
         infer_hw(len / ps.C, ps.H, ps.W);
         ps.oH = (ps.H + 2 * ps.pad - ps.k) / ps.stride + 1;
         ps.oW = (ps.W + 2 * ps.pad - ps.k) / ps.stride + 1;
         if (ps.C * ps.H * ps.W != len || ps.oH <= 0 || ps.oW <= 0)
-          return set_err(c, GN_ERR_SHAPE, "layer %d: MaxPool2D input %d is not C x H x W", i, len);
+          return set_err(c, GN_ERR_SHAPE, "layer %d: pooling input %d is not C x H x W", i, len);
         R.out_len = ps.C * ps.oH * ps.oW;
         break;
       }
@@ -1190,6 +1191,11 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
         break;
       }
+      case GN_LAYER_AVGPOOL2D: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_avgpool_fwd(cur, R.out, R.ps, B, c->stream));
+        break;
+      }
       case GN_LAYER_EMBEDDING: {
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B * R.T, R.V, R.D, R.err,
@@ -1298,6 +1304,13 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         if (below && below->gout) {
           KTimer kt(c, GN_KCLASS_OTHER);
           HIP_OK(c, launch_maxpool_bwd(R.gout, R.argmax, below->gout, R.ps, B, c->stream));
+        }
+        is_dz = false;
+        break;
+      case GN_LAYER_AVGPOOL2D:  // avgpool2d.go:401-474
+        if (below && below->gout) {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_avgpool_bwd(R.gout, below->gout, R.ps, B, c->stream));
         }
         is_dz = false;
         break;

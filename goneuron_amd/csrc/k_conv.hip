@@ -348,6 +348,65 @@ hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, fl
   return hipGetLastError();
 }
 
+// AvgPool2D (avgpool2d.go:98-220, 401-474): count = in-bounds cells of the
+// window (padding excluded), out = sum in (kh, kw) order * float32(1 / count).
+__device__ __forceinline__ int avgpool_count(const PoolShape &s, int oh, int ow) {
+  const int h0 = oh * s.stride - s.pad, w0 = ow * s.stride - s.pad;
+  const int nh = min(h0 + s.k, s.H) - max(h0, 0), nw = min(w0 + s.k, s.W) - max(w0, 0);
+  return (nh > 0 && nw > 0) ? nh * nw : 0;
+}
+
+__global__ __launch_bounds__(CT) void avgpool_fwd_kernel(const float *__restrict__ x,
+                                                         float *__restrict__ out, PoolShape s,
+                                                         int64_t n) {
+  for (int64_t o = (int64_t)blockIdx.x * CT + threadIdx.x; o < n; o += (int64_t)gridDim.x * CT) {
+    const int ow = (int)(o % s.oW), oh = (int)((o / s.oW) % s.oH);
+    const int64_t plane = o / ((int64_t)s.oH * s.oW);  // b * C + c
+    const float *xp = x + plane * s.H * s.W;
+    const int count = avgpool_count(s, oh, ow);
+    float v = 0.0f;
+    if (count > 0) {
+      float sum = 0.0f;
+      for (int kh = 0; kh < s.k; ++kh) {
+        const int ih = oh * s.stride + kh - s.pad;
+        if (ih < 0 || ih >= s.H) continue;
+        for (int kw = 0; kw < s.k; ++kw) {
+          const int iw = ow * s.stride + kw - s.pad;
+          if (iw >= 0 && iw < s.W) sum += xp[ih * s.W + iw];
+        }
+      }
+      v = sum * (1.0f / (float)count);
+    }
+    out[o] = v;
+  }
+}
+
+// Backward as a gather: input cell (ih, iw) adds g * float32(1 / count) of
+// every window that holds it in increasing (oh, ow) order, the order in which
+// the reference scatters them onto a zeroed gradient.  One block per plane.
+__global__ __launch_bounds__(CT) void avgpool_bwd_kernel(const float *__restrict__ gout,
+                                                         float *__restrict__ gin, PoolShape s) {
+  const int64_t plane = blockIdx.x;
+  const int hw = s.H * s.W, osz = s.oH * s.oW;
+  const float *gp = gout + plane * osz;
+  for (int e = threadIdx.x; e < hw; e += CT) {
+    const int ih = e / s.W, iw = e - ih * s.W;
+    int oh0 = ih + s.pad - s.k + 1, oh1 = ih + s.pad;
+    int ow0 = iw + s.pad - s.k + 1, ow1 = iw + s.pad;
+    oh0 = oh0 <= 0 ? 0 : (oh0 + s.stride - 1) / s.stride;
+    ow0 = ow0 <= 0 ? 0 : (ow0 + s.stride - 1) / s.stride;
+    oh1 = min(oh1 / s.stride, s.oH - 1);
+    ow1 = min(ow1 / s.stride, s.oW - 1);
+    float g = 0.0f;
+    for (int oh = oh0; oh <= oh1; ++oh)
+      for (int ow = ow0; ow <= ow1; ++ow) {
+        const int count = avgpool_count(s, oh, ow);
+        if (count > 0) g += gp[oh * s.oW + ow] * (1.0f / (float)count);
+      }
+    gin[plane * hw + e] = g;
+  }
+}
+
 hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const PoolShape &s,
                               int B, hipStream_t st) {
   const int64_t n = (int64_t)B * s.C * s.oH * s.oW;
@@ -358,6 +417,17 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st) {
   hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(B * s.C), dim3(CT), 0, st, gout, argmax, gin, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st) {
+  const int64_t n = (int64_t)B * s.C * s.oH * s.oW;
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(grid_for(n)), dim3(CT), 0, st, x, out, s, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st) {
+  hipLaunchKernelGGL(avgpool_bwd_kernel, dim3(B * s.C), dim3(CT), 0, st, gout, gin, s);
   return hipGetLastError();
 }
 

@@ -613,6 +613,87 @@ static const float *maxpool_backward(layer *L, const float *g) {
 }
 
 
+/* AvgPool2D avgpool2d.go:98-220 (per-sample forward), :401-474 (backward):
+ * count = in-bounds window positions (padding excluded), out = sum (kh, kw
+ * order) * float32(1/count); backward scatters g * float32(1/count) over the
+ * window in output order (oh, ow), channel, kh, kw.  Input dims are inferred
+ * from the per-channel size on every forward (sqrt, then width = size / h). */
+static const float *avgpool_forward(layer *L, const float *x, int32_t total) {
+  if (L->inC <= 0) L->inC = 1;
+  int32_t cs = total / L->inC;
+  L->inH = (int32_t)sqrt((double)cs);
+  L->inW = (L->inH * L->inH == cs) ? L->inH : cs / L->inH;
+  L->outH = (L->inH + 2 * L->pad - L->k) / L->stride + 1;
+  L->outW = (L->inW + 2 * L->pad - L->k) / L->stride + 1;
+  int32_t osz = L->outH * L->outW, req = L->inC * osz;
+  if (req > L->out_len || total > L->in_len) {
+    free(L->outputBuf); free(L->argmax); free(L->gradInBuf);
+    L->outputBuf = zalloc(req);
+    L->argmax = (int32_t *)calloc((size_t)osz, sizeof(int32_t)); /* countBuf */
+    L->gradInBuf = zalloc(total);
+  }
+  L->out_len = req;
+  L->in_len = total;
+  int32_t H = L->inH, W = L->inW;
+  for (int32_t oh = 0; oh < L->outH; oh++)
+    for (int32_t ow = 0; ow < L->outW; ow++) {
+      int32_t pos = oh * L->outW + ow, count = 0;
+      for (int32_t kh = 0; kh < L->k; kh++)
+        for (int32_t kw = 0; kw < L->k; kw++) {
+          int32_t ih = oh * L->stride + kh - L->pad, iw = ow * L->stride + kw - L->pad;
+          if (ih >= 0 && ih < H && iw >= 0 && iw < W) count++;
+        }
+      L->argmax[pos] = count;
+      for (int32_t c = 0; c < L->inC; c++) {
+        float v = 0.0f;
+        if (count > 0) {
+          float inv = 1.0f / (float)count, sum = 0.0f;
+          for (int32_t kh = 0; kh < L->k; kh++)
+            for (int32_t kw = 0; kw < L->k; kw++) {
+              int32_t ih = oh * L->stride + kh - L->pad, iw = ow * L->stride + kw - L->pad;
+              if (ih >= 0 && ih < H && iw >= 0 && iw < W) sum += x[c * H * W + ih * W + iw];
+            }
+          v = sum * inv;
+        }
+        L->outputBuf[c * osz + pos] = v;
+      }
+    }
+  return L->outputBuf;
+}
+static const float *avgpool_backward(layer *L, const float *g) {
+  int32_t H = L->inH, W = L->inW, osz = L->outH * L->outW;
+  for (int32_t i = 0; i < L->in_len; i++) L->gradInBuf[i] = 0;
+  for (int32_t oh = 0; oh < L->outH; oh++)
+    for (int32_t ow = 0; ow < L->outW; ow++) {
+      int32_t pos = oh * L->outW + ow, count = L->argmax[pos];
+      if (count <= 0) continue;
+      float per = 1.0f / (float)count;
+      for (int32_t c = 0; c < L->inC; c++) {
+        float gv = g[c * osz + pos] * per;
+        for (int32_t kh = 0; kh < L->k; kh++)
+          for (int32_t kw = 0; kw < L->k; kw++) {
+            int32_t ih = oh * L->stride + kh - L->pad, iw = ow * L->stride + kw - L->pad;
+            if (ih >= 0 && ih < H && iw >= 0 && iw < W) L->gradInBuf[c * H * W + ih * W + iw] += gv;
+          }
+      }
+    }
+  return L->gradInBuf;
+}
+
+int32_t gno_avgpool2d(const float *x, int32_t total, int32_t inC, int32_t k, int32_t stride,
+                      int32_t pad, float *out, const float *g, float *gin) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_AVGPOOL2D;
+  L.inC = inC; L.k = k; L.stride = stride; L.pad = pad;
+  const float *o = avgpool_forward(&L, x, total);
+  memcpy(out, o, sizeof(float) * L.out_len);
+  if (g && gin) memcpy(gin, avgpool_backward(&L, g), sizeof(float) * L.in_len);
+  int32_t n = L.out_len;
+  free(L.outputBuf); free(L.argmax); free(L.gradInBuf);
+  return n;
+}
+
 /* ------------------------------------------------------------------------ */
 /* LSTM (lstm.go) wrapped by SequenceUnroller (unroller.go)                  */
 /* ------------------------------------------------------------------------ */
@@ -1187,6 +1268,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_DROPOUT: dropout_build(L); break;
     case GNO_LAYER_CONV2D: conv_build(L); break;
     case GNO_LAYER_MAXPOOL2D:
+    case GNO_LAYER_AVGPOOL2D:
       L->inC = L->spec.in_channels;
       L->k = L->spec.kernel;
       L->stride = L->spec.stride;
@@ -1212,6 +1294,7 @@ static void layer_init_params(layer *L) {
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
   if (L->kind == GNO_LAYER_MAXPOOL2D) { L->inH = L->inW = 0; }                      /* maxpool2d.go:508-513 */
+  if (L->kind == GNO_LAYER_AVGPOOL2D) { L->inH = L->inW = 0; }                      /* avgpool2d.go:560-565 */
   if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_reset(L);                             /* unroller.go:268 */
 }
 /* *len_io: input length in, output length out */
@@ -1222,6 +1305,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_DROPOUT: o = dropout_forward(L, x); break;
     case GNO_LAYER_CONV2D: o = conv_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_MAXPOOL2D: o = maxpool_forward(L, x, *len_io); *len_io = L->out_len; break;
+    case GNO_LAYER_AVGPOOL2D: o = avgpool_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_FLATTEN: o = x; L->in_len = L->out_len = *len_io; break; /* reshape.go:64-80 */
     case GNO_LAYER_LSTM_UNROLLER: o = unroller_forward(L, x); *len_io = L->H; break;
     case GNO_LAYER_EMBEDDING: o = emb_forward(L, x); *len_io = L->out_len; break;
@@ -1238,6 +1322,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_DROPOUT: return dropout_backward(L, g);
     case GNO_LAYER_CONV2D: return conv_backward(L, g);
     case GNO_LAYER_MAXPOOL2D: return maxpool_backward(L, g);
+    case GNO_LAYER_AVGPOOL2D: return avgpool_backward(L, g);
     case GNO_LAYER_FLATTEN: return g; /* reshape.go:83-86 */
     case GNO_LAYER_LSTM_UNROLLER: return unroller_backward(L, g);
     case GNO_LAYER_EMBEDDING: return emb_backward(L, g);

@@ -18,6 +18,7 @@
  *   Dropout                           internal/layer/dropout.go:47-401
  *   Conv2D                            internal/layer/conv2d.go:114-1174
  *   MaxPool2D                         internal/layer/maxpool2d.go:106-410,508-513
+ *   AvgPool2D                         internal/layer/avgpool2d.go:98-220,401-474,560-565
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -62,6 +63,7 @@ enum {
   GNO_LAYER_TRANSFORMER = 8,
   GNO_LAYER_CLSPOOL = 9,
   GNO_LAYER_LSTM_UNROLLER = 10,
+  GNO_LAYER_AVGPOOL2D = 11,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -127,6 +129,10 @@ void gno_loss_backward(int32_t loss_kind, const float *pred, const float *y, flo
 void gno_adam_step_inplace(float *params, const float *grads, float *m, float *v,
                            int64_t n, float lr, float beta1, float beta2, float eps,
                            int32_t timestep);
+/* AvgPool2D forward of one sample (out, returns its length) and, when g and
+ * gin are given, the backward of g into gin. */
+int32_t gno_avgpool2d(const float *x, int32_t total, int32_t inC, int32_t k, int32_t stride,
+                      int32_t pad, float *out, const float *g, float *gin);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

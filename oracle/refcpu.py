@@ -20,7 +20,7 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 
 ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR = range(7)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
- LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER) = range(1, 11)
+ LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D) = range(1, 12)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -97,6 +97,9 @@ def lib():
         L.gno_adam_step_inplace.argtypes = [f32p, f32p, f32p, f32p, C.c_int64, C.c_float, C.c_float,
                                             C.c_float, C.c_float, C.c_int32]
         L.gno_matmul.argtypes = [f32p, f32p, f32p, f32p, C.c_int32, C.c_int32, C.c_int32]
+        L.gno_avgpool2d.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                    f32p, f32p, f32p]
+        L.gno_avgpool2d.restype = C.c_int32
         _lib = L
     return _lib
 
@@ -214,6 +217,21 @@ class Net:
             lib().gno_net_destroy(self.h)
         except Exception:
             pass
+
+
+def avgpool2d(x, in_channels, kernel, stride, padding, g=None):
+    """AvgPool2D of one sample; returns out, or (out, grad_in) when g is given."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size, np.float32)
+    if g is None:
+        n = lib().gno_avgpool2d(fptr(x), x.size, in_channels, kernel, stride, padding, fptr(out),
+                                None, None)
+        return out[:n].copy()
+    g = np.ascontiguousarray(g, np.float32)
+    gin = np.empty(x.size, np.float32)
+    n = lib().gno_avgpool2d(fptr(x), x.size, in_channels, kernel, stride, padding, fptr(out),
+                            fptr(g), fptr(gin))
+    return out[:n].copy(), gin
 
 
 def matmul(x, w, b):

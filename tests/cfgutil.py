@@ -14,6 +14,9 @@ def oracle_specs(refcpu, cfg):
                                      act=ACT[d["act"]], act_is_ptr=int(d["ptr"])))
         elif k == "dropout":
             specs.append(refcpu.spec(refcpu.LAYER_DROPOUT, in_size=d["n"], p=d["p"]))
+        elif k == "avgpool2d":
+            specs.append(refcpu.spec(refcpu.LAYER_AVGPOOL2D, in_channels=d["inC"], kernel=d["k"],
+                                     stride=d["s"], padding=d["p"]))
         elif k == "flatten":
             specs.append(refcpu.spec(refcpu.LAYER_FLATTEN, in_size=d["n"]))
         elif k == "conv2d":

@@ -276,6 +276,35 @@ def test_conv_generic_path_and_predict(gn, oracle):
     _compare_step(gn, oracle, cfg, steps=2)
 
 
+@pytest.mark.parametrize("k,s,p", [(2, 2, 0), (3, 1, 1), (3, 2, 1)])
+def test_avgpool_cnn(gn, oracle, k, s, p):
+    """Conv2D -> AvgPool2D -> Flatten -> Dense: the pooled output is
+    bit-identical to the oracle's AvgPool2D of the GPU conv output (windows
+    that overlap or cross the padding included); gradients and updated
+    weights through the pooling backward to the oracle's bar."""
+    cin, H, cout = 3, 12, 4
+    oh = (H + 2 * p - k) // s + 1
+    cfg = dict(num=9, name="avgpool_cnn", B=10, loss="ce", lr=1e-3, x="normal", in_len=cin * H * H,
+               classes=6,
+               layers=[{"kind": "conv2d", "inC": cin, "outC": cout, "k": 3, "s": 1, "p": 1, "act": "relu"},
+                       {"kind": "avgpool2d", "k": k, "s": s, "p": p, "inC": cout},
+                       {"kind": "flatten", "n": cout * oh * oh},
+                       {"kind": "dense", "in": cout * oh * oh, "out": 6, "act": "softmax", "ptr": True}])
+    model, _ = _compare_step(gn, oracle, cfg, steps=2)
+    x, _ = configs_inputs(cfg)
+    model.PredictBatch(x)
+    B = cfg["B"]
+    conv = model.LayerOutput(0, B * cout * H * H).reshape(B, -1)
+    pooled = model.LayerOutput(1, B * cout * oh * oh).reshape(B, -1)
+    for b in range(B):
+        np.testing.assert_array_equal(pooled[b], oracle.avgpool2d(conv[b], cout, k, s, p))
+
+
+def configs_inputs(cfg):
+    from goneuron_amd import configs
+    return configs.inputs(cfg)
+
+
 @pytest.mark.parametrize("workers,steps", [(64, 2), (4, 1), (1, 1)])
 def test_lstm_full_config(gn, oracle, workers, steps):
     """C5 at BASELINE size (LSTM 64->256, T=100, B=64, MSE): the per-step

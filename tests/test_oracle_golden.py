@@ -136,6 +136,41 @@ def test_maxpool_known_answer(oracle):
     np.testing.assert_array_equal(net.argmax(0), [5, 7, 13, 15])
 
 
+def test_avgpool_known_answers(oracle):
+    # avgpool2d_test.go:8-35 (k2 s2), :37-64 (k2 s1), :94-131 (backward of ones)
+    x16 = np.arange(1, 17, dtype=np.float32)
+    np.testing.assert_array_equal(oracle.avgpool2d(x16, 1, 2, 2, 0), [3.5, 5.5, 11.5, 13.5])
+    x9 = np.arange(1, 10, dtype=np.float32)
+    np.testing.assert_array_equal(oracle.avgpool2d(x9, 1, 2, 1, 0), [3, 4, 6, 7])
+    _, gin = oracle.avgpool2d(x16, 1, 2, 2, 0, g=np.ones(4, np.float32))
+    np.testing.assert_array_equal(gin, np.full(16, 0.25, np.float32))
+
+
+def test_avgpool_padding_excluded_and_overlap(oracle):
+    """:66-92 (k2 s2 p1 on 3x3 gives 2x2); padded cells do not count
+    (avgpool2d.go:184-196), so the corner windows average 1 or 2 values; with
+    overlapping windows (k3 s1 p1) every input collects g/count from each
+    window that holds it: the adjoint of the forward."""
+    x9 = np.arange(1, 10, dtype=np.float32)
+    out = oracle.avgpool2d(x9, 1, 2, 2, 1)
+    np.testing.assert_array_equal(out, [1.0, 2.5, 5.5, 7.0])
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=2 * 5 * 5).astype(np.float32)
+    g = rng.normal(size=2 * 5 * 5).astype(np.float32)
+    out, gin = oracle.avgpool2d(x, 2, 3, 1, 1, g=g)
+    # brute force: the forward as a matrix A (out = A x) in float64, gin = A^T g
+    A = np.zeros((50, 50))
+    for c in range(2):
+        for oh in range(5):
+            for ow in range(5):
+                cells = [(ih, iw) for ih in range(oh - 1, oh + 2) for iw in range(ow - 1, ow + 2)
+                         if 0 <= ih < 5 and 0 <= iw < 5]
+                for ih, iw in cells:
+                    A[c * 25 + oh * 5 + ow, c * 25 + ih * 5 + iw] = 1.0 / len(cells)
+    np.testing.assert_allclose(out, A @ x, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(gin, A.T @ g, rtol=1e-6, atol=1e-6)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
