@@ -22,7 +22,7 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "AvgPool2D", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
+    "AvgPool2D", "RMSNorm", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "Ref", "Adam", "MSE",
     "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
 ]
@@ -61,7 +61,8 @@ def Ref(act: Activation) -> Activation:
 
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
- LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D) = range(1, 12)
+ LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
+ LAYER_RMSNORM) = range(1, 13)
 
 
 class Layer:
@@ -142,6 +143,18 @@ def AvgPool2D(kernel, stride, padding, *in_channels):
     each window (padding not counted)."""
     return Layer(LAYER_AVGPOOL2D, kernel=kernel, stride=stride, padding=padding,
                  in_channels=in_channels[0] if in_channels else -1)
+
+
+def RMSNorm(*normalized_shape, eps=1e-5):
+    """goneuron.RMSNorm (goneuron.go:229-236): y = x / sqrt(mean(x^2) + eps) *
+    gamma over rows of normalizedShape, gamma starting at 1 (rmsnorm.go:73-96).
+    The lazy form RMSNorm() is rejected: RMSNorm.Build has no error return, so
+    Sequential.Build (sequential.go:68-73) never resolves its size."""
+    if not normalized_shape or normalized_shape[0] <= 0:
+        raise GNError(-1, "RMSNorm needs normalizedShape > 0 (the lazy form is never built)")
+    if eps < 0:
+        raise GNError(-1, f"invalid eps {eps}: must be >= 0")
+    return Layer(LAYER_RMSNORM, dim=int(normalized_shape[0]), eps=float(eps) if eps > 0 else 0.0)
 
 
 def Embedding(num, dim):

@@ -9,7 +9,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, Flatten,
+from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, RMSNorm,
+               Flatten,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
                Sigmoid, Tanh, Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
@@ -104,6 +105,8 @@ def product_layers(cfg):
             out.append(MaxPool2D(d["k"], d["s"], d["p"], d["inC"]))
         elif k == "avgpool2d":
             out.append(AvgPool2D(d["k"], d["s"], d["p"], d["inC"]))
+        elif k == "rmsnorm":
+            out.append(RMSNorm(d["n"]))
         elif k == "embedding":
             out.append(Embedding(d["vocab"], d["dim"]))
         elif k == "posenc":

@@ -153,6 +153,10 @@ hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, flo
                          int rows, int N, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
+hipError_t launch_rms_fwd(const float *x, const float *gam, float *y, float *rms, int rows, int N,
+                          float eps, hipStream_t s);
+hipError_t launch_rms_bwd(const float *g, const float *x, const float *gam, const float *rms,
+                          float *dx, float *gx, int rows, int N, hipStream_t s);
 bool attn_supported(int T, int D, int NH);
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s);

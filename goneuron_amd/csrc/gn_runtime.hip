@@ -515,6 +515,9 @@ struct LayerRT {
   int V = 0, D = 0, NH = 0, FF = 0, causal = 0;
   int32_t *ids = nullptr;
   int *err = nullptr;  // device error flag (Embedding: bad id; LSTM: cooperative wait timeout)
+  // RMSNorm over rows of D: per-row rms and g * x / rms for the gamma sums
+  float *rmsv = nullptr, *gx = nullptr;
+  float eps = 0.f;
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -797,6 +800,16 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
           return set_err(c, GN_ERR_SHAPE, "layer %d: CLSPooling %dx%d != input %d", i, R.T, R.D, len);
         R.out_len = R.D;
         break;
+      case GN_LAYER_RMSNORM:  // rmsnorm.go:222-240: rows of normalizedShape
+        R.D = R.d.dim;
+        if (R.D <= 0 || len % R.D)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: RMSNorm normalizedShape %d does not divide input %d",
+                         i, R.D, len);
+        if (!(R.d.eps >= 0)) return set_err(c, GN_ERR_INVALID, "layer %d: RMSNorm eps < 0", i);
+        R.eps = R.d.eps > 0 ? R.d.eps : 1e-5f;  // the facade's eps (goneuron.go:234)
+        R.pcount = R.D;
+        R.out_len = len;
+        break;
       case GN_LAYER_LSTM_UNROLLER: {
         R.T = R.d.seq_len;
         R.I = R.d.in_size;
@@ -898,6 +911,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
+    }
+    if (R.d.kind == GN_LAYER_RMSNORM) {
+      std::fill(host.begin() + R.poff, host.begin() + R.poff + R.D, 1.0f);  // rmsnorm.go:80-82
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * (R.in_len / R.D), &R.rmsv))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.in_len, &R.gx))) return rc;
     }
     if (R.d.kind == GN_LAYER_MAXPOOL2D) {
       float *am = nullptr;
@@ -1217,6 +1235,12 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         if (r) return r;
         break;
       }
+      case GN_LAYER_RMSNORM: {
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_rms_fwd(cur, M->params + R.poff, R.out, R.rmsv, B * (R.in_len / R.D), R.D,
+                                 R.eps, c->stream));
+        break;
+      }
       case GN_LAYER_LSTM_UNROLLER: {
         const float *Wx = M->params + R.poff;
         const float *Wh = Wx + (int64_t)4 * R.H * R.I;
@@ -1337,6 +1361,16 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_TRANSFORMER: {
         int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale);
         if (r) return r;
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_RMSNORM: {  // rmsnorm.go:301-329: dx, then gamma += g * (x / rms)
+        KTimer kt(c, GN_KCLASS_OTHER);
+        const int rows = B * (R.in_len / R.D);
+        HIP_OK(c, launch_rms_bwd(R.gout, in, M->params + R.poff, R.rmsv, below ? below->gout : nullptr,
+                                 R.gx, rows, R.D, c->stream));
+        HIP_OK(c, launch_colsum(R.gx, rows, R.D, R.D, scale, M->grads + R.poff, c->scratch,
+                                c->scratch_floats, c->stream));
         is_dz = false;
         break;
       }

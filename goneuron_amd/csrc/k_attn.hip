@@ -202,6 +202,48 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 }
 
 // ---------------------------------------------------------------------------
+// RMSNorm over rows of N (rmsnorm.go:222-240, 301-329), one wave64 per row:
+// rms = sqrt(sum x^2 / N + eps) rounded from float64, y = (x / rms) * gamma;
+// dx = (gamma / rms) (g - x sum(g gamma x) / (N rms rms)); gx = g (x / rms)
+// feeds the gamma column sums.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rms_fwd_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ gam,
+                                                      float *__restrict__ y, float *__restrict__ rmsv,
+                                                      int rows, int N, float eps) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float *xr = x + (int64_t)r * N;
+  float ss = 0.f;
+  for (int i = lane; i < N; i += 64) ss += xr[i] * xr[i];
+  ss = wsum(ss);
+  const float rms = (float)sqrt((double)(ss / (float)N + eps));
+  for (int i = lane; i < N; i += 64) y[(int64_t)r * N + i] = (xr[i] / rms) * gam[i];
+  if (lane == 0) rmsv[r] = rms;
+}
+
+__global__ __launch_bounds__(256) void rms_bwd_kernel(const float *__restrict__ g,
+                                                      const float *__restrict__ x,
+                                                      const float *__restrict__ gam,
+                                                      const float *__restrict__ rmsv,
+                                                      float *__restrict__ dx,
+                                                      float *__restrict__ gx, int rows, int N) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float *gr = g + (int64_t)r * N, *xr = x + (int64_t)r * N;
+  const float rms = rmsv[r], inv = 1.0f / rms;
+  float s = 0.f;
+  for (int i = lane; i < N; i += 64) s += gr[i] * gam[i] * xr[i];
+  s = wsum(s);
+  const float factor = s / ((float)N * rms * rms);
+  for (int i = lane; i < N; i += 64) {
+    const float xi = xr[i], gi = gr[i];
+    if (dx) dx[(int64_t)r * N + i] = (gam[i] * inv) * (gi - xi * factor);
+    gx[(int64_t)r * N + i] = gi * (xi * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Causal multi-head attention on fp32 MFMA, one workgroup per (sample, head).
 // Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd); T <= 128 and
 // hd <= 32 are held in LDS (zero-padded to 128 x 32).  Wave w owns queries
@@ -503,6 +545,22 @@ hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, flo
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s) {
   hipLaunchKernelGGL(ln_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, g, x, gam, stats, dx, gx,
+                     rows, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_fwd(const float *x, const float *gam, float *y, float *rms, int rows, int N,
+                          float eps, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gam, y, rms, rows, N,
+                     eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms_bwd(const float *g, const float *x, const float *gam, const float *rms,
+                          float *dx, float *gx, int rows, int N, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rms_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, g, x, gam, rms, dx, gx,
                      rows, N);
   return hipGetLastError();
 }

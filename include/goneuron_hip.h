@@ -61,6 +61,7 @@ extern "C" {
 #define GN_LAYER_CLSPOOL 9       /* layer.NewCLSPooling       transformer.go:1679 */
 #define GN_LAYER_LSTM_UNROLLER 10 /* SequenceUnroller(LSTM)   unroller.go:57, lstm.go */
 #define GN_LAYER_AVGPOOL2D 11    /* layer.NewAvgPool2D        avgpool2d.go:50 */
+#define GN_LAYER_RMSNORM 12      /* layer.NewRMSNorm          rmsnorm.go:49 */
 
 #define GN_LOSS_MSE 1            /* loss.MSE          loss.go:38-105 */
 #define GN_LOSS_CE 2             /* loss.CrossEntropy loss.go:108-178 */
@@ -75,8 +76,9 @@ typedef struct gn_layer_desc {
   int32_t out_channels;
   int32_t kernel, stride, padding;
   float p;              /* Dropout probability */
-  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim;
+  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim; /* RMSNorm: dim = normalizedShape */
   int32_t return_sequences;
+  float eps;            /* RMSNorm eps; 0 selects the facade's 1e-5 (goneuron.go:234) */
 } gn_layer_desc;
 
 typedef struct gn_adam_desc {   /* opt.NewAdam opt.go:117-126 */

@@ -694,6 +694,78 @@ int32_t gno_avgpool2d(const float *x, int32_t total, int32_t inC, int32_t k, int
   return n;
 }
 
+/* RMSNorm rmsnorm.go:73-96 (Build: gamma = 1, normalizedShape floats),
+ * :222-240 (forward over rows of normalizedShape: sumSq sequential,
+ * rms = float32(sqrt(float64(sumSq / n + eps))), out = (x / rms) * gamma),
+ * :301-318 (dx = (gamma * (1/rms)) * (g - x * sum(g gamma x) / (n rms rms))),
+ * :321-329 (gamma grad += g * (x * (1/rms))).  The input copy and the per-row
+ * rms are the saved state of the one Forward each sample runs. */
+static void rms_build(layer *L) {
+  L->D = L->spec.dim;
+  L->nparams = L->D > 0 ? L->D : 0;
+}
+static void rms_init(layer *L) {
+  for (int32_t i = 0; i < L->D; i++) L->params[i] = 1.0f;
+}
+static float rms_eps(const layer *L) { return L->spec.eps > 0 ? L->spec.eps : 1e-5f; }
+static const float *rms_forward(layer *L, const float *x, int32_t total) {
+  int32_t n = L->D, rows = total / n;
+  if (total > L->in_len) {
+    free(L->outputBuf); free(L->savedInput); free(L->gradInBuf); free(L->tmpRow);
+    L->outputBuf = zalloc(total);
+    L->savedInput = zalloc(total);
+    L->gradInBuf = zalloc(total);
+    L->tmpRow = zalloc(rows);
+  }
+  L->in_len = L->out_len = total;
+  memcpy(L->savedInput, x, sizeof(float) * total);
+  const float eps = rms_eps(L);
+  for (int32_t s = 0; s < rows; s++) {
+    const float *xr = x + (int64_t)s * n;
+    float sumSq = 0.0f;
+    for (int32_t i = 0; i < n; i++) sumSq += xr[i] * xr[i];
+    float rms = (float)sqrt((double)(sumSq / (float)n + eps));
+    L->tmpRow[s] = rms;
+    for (int32_t i = 0; i < n; i++) L->outputBuf[(int64_t)s * n + i] = (xr[i] / rms) * L->params[i];
+  }
+  return L->outputBuf;
+}
+static const float *rms_backward(layer *L, const float *g) {
+  int32_t n = L->D, rows = L->in_len / n;
+  const float *x = L->savedInput;
+  for (int32_t s = 0; s < rows; s++) {
+    const float *gr = g + (int64_t)s * n, *xr = x + (int64_t)s * n;
+    float rms = L->tmpRow[s], invRMS = 1.0f / rms, sum = 0.0f;
+    for (int32_t i = 0; i < n; i++) sum += gr[i] * L->params[i] * xr[i];
+    float factor = sum / ((float)n * rms * rms);
+    for (int32_t i = 0; i < n; i++)
+      L->gradInBuf[(int64_t)s * n + i] = (L->params[i] * invRMS) * (gr[i] - xr[i] * factor);
+  }
+  for (int32_t s = 0; s < rows; s++) {
+    const float *gr = g + (int64_t)s * n, *xr = x + (int64_t)s * n;
+    float invRMS = 1.0f / L->tmpRow[s];
+    for (int32_t i = 0; i < n; i++) L->grads[i] += gr[i] * (xr[i] * invRMS);
+  }
+  return L->gradInBuf;
+}
+
+int32_t gno_rmsnorm(const float *x, int32_t total, int32_t n, float eps, const float *gamma,
+                    float *out, const float *g, float *gin, float *ggamma) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_RMSNORM;
+  L.spec.dim = n;
+  L.spec.eps = eps;
+  rms_build(&L);
+  if (n <= 0 || total % n) return -1;
+  L.params = (float *)gamma;
+  L.grads = ggamma;
+  memcpy(out, rms_forward(&L, x, total), sizeof(float) * total);
+  if (g && gin && ggamma) memcpy(gin, rms_backward(&L, g), sizeof(float) * total);
+  free(L.outputBuf); free(L.savedInput); free(L.gradInBuf); free(L.tmpRow);
+  return total / n;
+}
+
 /* ------------------------------------------------------------------------ */
 /* LSTM (lstm.go) wrapped by SequenceUnroller (unroller.go)                  */
 /* ------------------------------------------------------------------------ */
@@ -1280,6 +1352,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_POSENC: pe_build(L); break;
     case GNO_LAYER_CLSPOOL: cls_build(L); break;
     case GNO_LAYER_TRANSFORMER: tb_build(L); break;
+    case GNO_LAYER_RMSNORM: rms_build(L); break;
     default: break;
   }
 }
@@ -1290,6 +1363,7 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_EMBEDDING) emb_init(L);
   else if (L->kind == GNO_LAYER_POSENC) pe_init(L);
   else if (L->kind == GNO_LAYER_TRANSFORMER) tb_init(L);
+  else if (L->kind == GNO_LAYER_RMSNORM) rms_init(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -1312,6 +1386,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_POSENC: o = pe_forward(L, x); break;
     case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
     case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
+    case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
     default: o = x;
   }
   return o;
@@ -1329,6 +1404,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_POSENC: return pe_backward(L, g);
     case GNO_LAYER_CLSPOOL: return cls_backward(L, g);
     case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
+    case GNO_LAYER_RMSNORM: return rms_backward(L, g);
     default: return g;
   }
 }
@@ -1385,6 +1461,7 @@ void gno_net_destroy(gno_net *n) {
     for (size_t k = 0; k < sizeof lb / sizeof lb[0]; k++) free(lb[k]);
     free(L->ids);
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_free(L);
+    if (L->kind == GNO_LAYER_RMSNORM) free(L->tmpRow);
   }
   free(n->layers);
   free(n->params); free(n->grads); free(n->m); free(n->v); free(n->worker_grads); free(n->lossGrad);

@@ -19,6 +19,7 @@
  *   Conv2D                            internal/layer/conv2d.go:114-1174
  *   MaxPool2D                         internal/layer/maxpool2d.go:106-410,508-513
  *   AvgPool2D                         internal/layer/avgpool2d.go:98-220,401-474,560-565
+ *   RMSNorm                           internal/layer/rmsnorm.go:73-96,222-240,301-335
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -64,6 +65,7 @@ enum {
   GNO_LAYER_CLSPOOL = 9,
   GNO_LAYER_LSTM_UNROLLER = 10,
   GNO_LAYER_AVGPOOL2D = 11,
+  GNO_LAYER_RMSNORM = 12,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -78,8 +80,9 @@ typedef struct gno_layer_spec {
   int32_t out_channels;
   int32_t kernel, stride, padding;
   float p;              /* Dropout */
-  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim;
+  int32_t seq_len, num_heads, ff_dim, causal, vocab, dim; /* RMSNorm: dim = normalizedShape */
   int32_t return_sequences;
+  float eps;            /* RMSNorm eps (0 = 1e-5) */
 } gno_layer_spec;
 
 typedef struct gno_net gno_net;
@@ -133,6 +136,11 @@ void gno_adam_step_inplace(float *params, const float *grads, float *m, float *v
  * gin are given, the backward of g into gin. */
 int32_t gno_avgpool2d(const float *x, int32_t total, int32_t inC, int32_t k, int32_t stride,
                       int32_t pad, float *out, const float *g, float *gin);
+/* RMSNorm of one sample (total = rows x n) with the given gamma into out;
+ * with g, gin and ggamma also the backward (ggamma accumulates).  Returns the
+ * row count, -1 when n does not divide total. */
+int32_t gno_rmsnorm(const float *x, int32_t total, int32_t n, float eps, const float *gamma,
+                    float *out, const float *g, float *gin, float *ggamma);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

@@ -20,7 +20,8 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 
 ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR = range(7)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
- LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D) = range(1, 12)
+ LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
+ LAYER_RMSNORM) = range(1, 13)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -33,7 +34,7 @@ class LayerSpec(C.Structure):
         ("p", C.c_float),
         ("seq_len", C.c_int32), ("num_heads", C.c_int32), ("ff_dim", C.c_int32),
         ("causal", C.c_int32), ("vocab", C.c_int32), ("dim", C.c_int32),
-        ("return_sequences", C.c_int32),
+        ("return_sequences", C.c_int32), ("eps", C.c_float),
     ]
 
 
@@ -100,6 +101,9 @@ def lib():
         L.gno_avgpool2d.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                     f32p, f32p, f32p]
         L.gno_avgpool2d.restype = C.c_int32
+        L.gno_rmsnorm.argtypes = [f32p, C.c_int32, C.c_int32, C.c_float, f32p, f32p, f32p, f32p,
+                                  f32p]
+        L.gno_rmsnorm.restype = C.c_int32
         _lib = L
     return _lib
 
@@ -232,6 +236,25 @@ def avgpool2d(x, in_channels, kernel, stride, padding, g=None):
     n = lib().gno_avgpool2d(fptr(x), x.size, in_channels, kernel, stride, padding, fptr(out),
                             fptr(g), fptr(gin))
     return out[:n].copy(), gin
+
+
+def rmsnorm(x, n, gamma=None, g=None, eps=1e-5):
+    """RMSNorm of one sample over rows of n; returns out, or (out, grad_in,
+    grad_gamma) when g is given (grad_gamma accumulated from zero)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    gamma = np.ones(n, np.float32) if gamma is None else np.ascontiguousarray(gamma, np.float32)
+    out = np.empty(x.size, np.float32)
+    if g is None:
+        if lib().gno_rmsnorm(fptr(x), x.size, n, eps, fptr(gamma), fptr(out), None, None, None) < 0:
+            raise ValueError("n must divide the input length")
+        return out
+    g = np.ascontiguousarray(g, np.float32).ravel()
+    gin = np.empty(x.size, np.float32)
+    gg = np.zeros(n, np.float32)
+    if lib().gno_rmsnorm(fptr(x), x.size, n, eps, fptr(gamma), fptr(out), fptr(g), fptr(gin),
+                         fptr(gg)) < 0:
+        raise ValueError("n must divide the input length")
+    return out, gin, gg
 
 
 def matmul(x, w, b):

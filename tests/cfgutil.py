@@ -19,6 +19,9 @@ def oracle_specs(refcpu, cfg):
                                      stride=d["s"], padding=d["p"]))
         elif k == "flatten":
             specs.append(refcpu.spec(refcpu.LAYER_FLATTEN, in_size=d["n"]))
+        elif k == "rmsnorm":
+            specs.append(refcpu.spec(refcpu.LAYER_RMSNORM, dim=d["n"],
+                                     in_size=cfg["in_len"] if i == 0 else 0))
         elif k == "conv2d":
             specs.append(refcpu.spec(refcpu.LAYER_CONV2D, in_size=cfg["in_len"], in_channels=d["inC"],
                                      out_channels=d["outC"], kernel=d["k"], stride=d["s"],

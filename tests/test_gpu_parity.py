@@ -300,6 +300,51 @@ def test_avgpool_cnn(gn, oracle, k, s, p):
         np.testing.assert_array_equal(pooled[b], oracle.avgpool2d(conv[b], cout, k, s, p))
 
 
+_RMS_CASES = {
+    # Dense -> RMSNorm(width) -> Dense softmax, one row per sample
+    "dense_rms_dense": dict(B=33, in_len=48, classes=10, loss="ce", layers=[
+        {"kind": "dense", "in": 48, "out": 64, "act": "tanh", "ptr": False},
+        {"kind": "rmsnorm", "n": 64},
+        {"kind": "dense", "in": 64, "out": 10, "act": "softmax", "ptr": True}]),
+    # four rows of 24 per sample, MSE on one-hot targets
+    "rows_of_24": dict(B=17, in_len=40, classes=7, loss="mse", layers=[
+        {"kind": "dense", "in": 40, "out": 96, "act": "relu", "ptr": False},
+        {"kind": "rmsnorm", "n": 24},
+        {"kind": "dense", "in": 96, "out": 7, "act": "linear", "ptr": False}]),
+    # RMSNorm as the first layer (no input gradient), 4 rows of 32
+    "first_layer": dict(B=9, in_len=128, classes=5, loss="ce", layers=[
+        {"kind": "rmsnorm", "n": 32},
+        {"kind": "dense", "in": 128, "out": 5, "act": "softmax", "ptr": True}]),
+    # wide rows and a larger batch
+    "wide_1024": dict(B=256, in_len=256, classes=100, loss="ce", layers=[
+        {"kind": "dense", "in": 256, "out": 1024, "act": "relu", "ptr": False},
+        {"kind": "rmsnorm", "n": 1024},
+        {"kind": "dense", "in": 1024, "out": 100, "act": "logsoftmax", "ptr": True}]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_RMS_CASES))
+def test_rmsnorm_net(gn, oracle, case):
+    """RMSNorm (rmsnorm.go) inside a net: gradients, Adam state and updated
+    weights against the oracle over 3 steps (gamma leaves 1 after the first,
+    which exercises the reference's gamma-scaled dx); then the forward rows
+    of the trained model against the oracle's RMSNorm of the GPU's own input."""
+    cfg = dict(num=12, name="rms_" + case, lr=1e-3, x="normal", **_RMS_CASES[case])
+    model, _ = _compare_step(gn, oracle, cfg, steps=3)
+    x, _ = configs_inputs(cfg)
+    model.PredictBatch(x)
+    B, li = cfg["B"], [d["kind"] for d in cfg["layers"]].index("rmsnorm")
+    n = cfg["layers"][li]["n"]
+    width = cfg["in_len"] if li == 0 else cfg["layers"][li - 1]["out"]
+    xin = x if li == 0 else model.LayerOutput(li - 1, B * width).reshape(B, -1)
+    got = model.LayerOutput(li, B * width).reshape(B, -1)
+    sl = model.LayerParams(li)
+    gamma = model.Params()[sl]
+    for b in range(B):
+        ref = oracle.rmsnorm(xin[b], n, gamma=gamma)
+        assert max_rel(got[b], ref) <= 1e-6, (b, max_rel(got[b], ref))
+
+
 def configs_inputs(cfg):
     from goneuron_amd import configs
     return configs.inputs(cfg)

@@ -171,6 +171,93 @@ def test_avgpool_padding_excluded_and_overlap(oracle):
     np.testing.assert_allclose(gin, A.T @ g, rtol=1e-6, atol=1e-6)
 
 
+def _rms_f64(x, n, gamma, eps):
+    """RMSNorm in float64 from its definition, rows of n."""
+    xr = np.asarray(x, np.float64).reshape(-1, n)
+    rms = np.sqrt((xr * xr).mean(axis=1, keepdims=True) + eps)
+    return (xr / rms * np.asarray(gamma, np.float64)).ravel()
+
+
+def test_rmsnorm_known_answers(oracle):
+    """rmsnorm_test.go:8-37 (x = 1..4: y = x / sqrt(30/4 + 1e-5)), backward of
+    the same sample has the input's length; stability_test.go:301-318 (a zero
+    row gives zeros, no NaN: eps keeps rms > 0)."""
+    x = np.arange(1, 5, dtype=np.float32)
+    rms = np.float32(math.sqrt(float(np.float32(30.0) / np.float32(4.0) + np.float32(1e-5))))
+    y = oracle.rmsnorm(x, 4)
+    np.testing.assert_allclose(y, x / rms, rtol=0, atol=1e-5)
+    _, gin, _ = oracle.rmsnorm(x, 4, g=np.array([0.1, 0.2, 0.3, 0.4], np.float32))
+    assert gin.shape == (4,)
+    z = oracle.rmsnorm(np.zeros(4, np.float32), 4)
+    assert not np.isnan(z).any() and (z == 0).all()
+    # rmsnorm_test.go:39-69: 1..8 with unit grads gives a nonzero input gradient
+    _, gin8, _ = oracle.rmsnorm(np.arange(1, 9, dtype=np.float32), 8, g=np.ones(8, np.float32))
+    assert (gin8 != 0).any()
+
+
+def test_rmsnorm_gradients_by_finite_differences(oracle):
+    """gradient_check_test.go:955-1003 (gamma = 1 + 0.1 (2u - 1) from RNG(42),
+    x = [0.1, -0.2, 0.15, -0.1], g = 0.1, analytic within 5e-3 of numeric),
+    then three rows of 7 with random gamma.  Central differences of sum(g y)
+    over the float64 definition pin dgamma and, at gamma = 1, dx.  The
+    reference's dx (rmsnorm.go:314-316) multiplies the projection term by
+    gamma_j as well: dx_j = gamma_j/r (g_j - x_j S / (n r^2)), S = sum g gamma x,
+    where the exact gradient has x_j S / (n r^3) without gamma_j; so for gamma != 1
+    dx - numeric must equal (1 - gamma_j) x_j S / (n r^3)."""
+    seed = 42
+    gam4 = []
+    for _ in range(4):  # RNG.RandFloat (layer.go:72-75)
+        seed = (seed * 6364136223846793005 + 1) & (2**64 - 1)
+        gam4.append(np.float32(1.0) + (np.float32(seed >> 33) / np.float32(2**31) * np.float32(2)
+                                      - np.float32(1)) * np.float32(0.1))
+    x4 = np.array([0.1, -0.2, 0.15, -0.1], np.float32)
+    cases = [(x4, 4, np.array(gam4, np.float32), np.full(4, 0.1, np.float32)),
+             (x4, 4, np.ones(4, np.float32), np.full(4, 0.1, np.float32))]
+    rng = np.random.default_rng(11)
+    x21, g21 = rng.normal(size=21).astype(np.float32), rng.normal(size=21).astype(np.float32)
+    cases.append((x21, 7, (1 + 0.3 * rng.normal(size=7)).astype(np.float32), g21))
+    cases.append((x21, 7, np.ones(7, np.float32), g21))
+    h = 1e-6
+    for x, n, gam, g in cases:
+        y, gin, gg = oracle.rmsnorm(x, n, gamma=gam, g=g)
+        np.testing.assert_allclose(y, _rms_f64(x, n, gam, 1e-5), rtol=1e-6, atol=1e-7)
+        f = lambda xx, gg_: g.astype(np.float64) @ _rms_f64(xx, n, gg_, 1e-5)
+        num_dx = np.empty(x.size)
+        for i in range(x.size):
+            e = np.zeros(x.size); e[i] = h
+            num_dx[i] = (f(x + e, gam) - f(x - e, gam)) / (2 * h)
+        num_dg = np.empty(n)
+        for j in range(n):
+            e = np.zeros(n); e[j] = h
+            num_dg[j] = (f(x, gam + e) - f(x, gam - e)) / (2 * h)
+        np.testing.assert_allclose(gg, num_dg, rtol=1e-4, atol=1e-5)
+        xr = x.astype(np.float64).reshape(-1, n)
+        gr = g.astype(np.float64).reshape(-1, n)
+        r = np.sqrt((xr * xr).mean(axis=1, keepdims=True) + 1e-5)
+        S = (gr * gam * xr).sum(axis=1, keepdims=True)
+        quirk = ((1 - gam.astype(np.float64)) * xr * S / (n * r ** 3)).ravel()
+        np.testing.assert_allclose(gin, num_dx + quirk, rtol=1e-4, atol=1e-5)
+        if n == 4 and (gam != 1).any():  # the reference test's own bar
+            assert np.abs(gin - num_dx).max() <= 5e-3
+
+
+def test_rmsnorm_rows_are_independent(oracle):
+    """A sample of several rows normalises each row alone (rmsnorm.go:222-240):
+    bit-identical to the rows run one by one, gamma grads summed over rows."""
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=5 * 6).astype(np.float32)
+    g = rng.normal(size=5 * 6).astype(np.float32)
+    gam = rng.uniform(0.5, 1.5, size=6).astype(np.float32)
+    y, gin, gg = oracle.rmsnorm(x, 6, gamma=gam, g=g)
+    acc = np.zeros(6, np.float32)
+    for r in range(5):
+        yr, gr, ggr = oracle.rmsnorm(x[6 * r:6 * r + 6], 6, gamma=gam, g=g[6 * r:6 * r + 6])
+        np.testing.assert_array_equal(y[6 * r:6 * r + 6], yr)
+        np.testing.assert_array_equal(gin[6 * r:6 * r + 6], gr)
+        acc += ggr
+    np.testing.assert_allclose(gg, acc, rtol=1e-6, atol=1e-7)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
