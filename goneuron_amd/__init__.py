@@ -22,7 +22,7 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "AvgPool2D", "RMSNorm", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
+    "AvgPool2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "Ref", "Adam", "MSE",
     "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
 ]
@@ -62,7 +62,7 @@ def Ref(act: Activation) -> Activation:
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM) = range(1, 13)
+ LAYER_RMSNORM, LAYER_SWIGLU) = range(1, 14)
 
 
 class Layer:
@@ -155,6 +155,17 @@ def RMSNorm(*normalized_shape, eps=1e-5):
     if eps < 0:
         raise GNError(-1, f"invalid eps {eps}: must be >= 0")
     return Layer(LAYER_RMSNORM, dim=int(normalized_shape[0]), eps=float(eps) if eps > 0 else 0.0)
+
+
+def SwiGLU(out, *in_size):
+    """goneuron.SwiGLU (goneuron.go:238-245): y = swish(W x) * (V x), no
+    biases.  The lazy form SwiGLU(out) is rejected: SwiGLU.Build has no error
+    return, so Sequential.Build (sequential.go:68-73) never resolves its size."""
+    if not in_size or in_size[0] <= 0:
+        raise GNError(-1, "SwiGLU needs an input size (the lazy form is never built)")
+    if out <= 0:
+        raise GNError(-1, f"invalid outSize {out}: must be > 0")
+    return Layer(LAYER_SWIGLU, in_size=int(in_size[0]), out_size=int(out))
 
 
 def Embedding(num, dim):

@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 
 from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, RMSNorm,
-               Flatten,
+               SwiGLU, Flatten,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
                Sigmoid, Tanh, Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
@@ -107,6 +107,8 @@ def product_layers(cfg):
             out.append(AvgPool2D(d["k"], d["s"], d["p"], d["inC"]))
         elif k == "rmsnorm":
             out.append(RMSNorm(d["n"]))
+        elif k == "swiglu":
+            out.append(SwiGLU(d["out"], d["in"]))
         elif k == "embedding":
             out.append(Embedding(d["vocab"], d["dim"]))
         elif k == "posenc":

@@ -68,6 +68,11 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
 hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
                          float *scratch, size_t scratch_cap, hipStream_t s);
 
+// SwiGLU gating on Z = [gate | up] rows (2*out wide) and its backward into dZ
+hipError_t launch_swiglu_fwd(const float *Z, float *y, int B, int out, hipStream_t s);
+hipError_t launch_swiglu_bwd(const float *dy, const float *Z, float *dZ, int B, int out,
+                             hipStream_t s);
+
 // dz = g * act'(out) elementwise (optionally with dropout mask/scale fused)
 hipError_t launch_dact(const float *g, const float *out, float *dz, int64_t n, int deriv,
                        hipStream_t s);

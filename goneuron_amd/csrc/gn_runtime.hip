@@ -518,6 +518,8 @@ struct LayerRT {
   // RMSNorm over rows of D: per-row rms and g * x / rms for the gamma sums
   float *rmsv = nullptr, *gx = nullptr;
   float eps = 0.f;
+  // SwiGLU: projections Z = [gate | up] and their gradients, [maxB, 2*out] each
+  float *zbuf = nullptr, *dzbuf = nullptr;
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -595,6 +597,13 @@ static void init_dense(float *p, int in, int out) {  // Dense.Build layer.go:300
   const int64_t nw = (int64_t)in * out;
   for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
   for (int i = 0; i < out; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
+}
+
+static void init_swiglu(float *p, int in, int out) {  // SwiGLU.Build swiglu.go:82-88
+  const float scale = (float)sqrt(2.0 / ((double)in + (double)out));
+  uint64_t s = (uint64_t)(in * 100 + out + 42);
+  const int64_t n = 2 * (int64_t)in * out;
+  for (int64_t i = 0; i < n; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
 }
 
 static void init_conv(float *p, int inC, int outC, int k) {  // Conv2D.Build conv2d.go:114-135
@@ -810,6 +819,13 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.pcount = R.D;
         R.out_len = len;
         break;
+      case GN_LAYER_SWIGLU:  // swiglu.go:73-100: [W | V], each out x in, no biases
+        if (R.d.in_size != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: SwiGLU in %d != incoming %d", i, R.d.in_size, len);
+        if (R.d.out_size <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: SwiGLU out <= 0", i);
+        R.pcount = 2 * (int64_t)R.d.in_size * R.d.out_size;
+        R.out_len = R.d.out_size;
+        break;
       case GN_LAYER_LSTM_UNROLLER: {
         R.T = R.d.seq_len;
         R.I = R.d.in_size;
@@ -911,6 +927,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
+    }
+    if (R.d.kind == GN_LAYER_SWIGLU) {
+      init_swiglu(host.data() + R.poff, R.d.in_size, R.d.out_size);
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * R.out_len, &R.zbuf))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * R.out_len, &R.dzbuf))) return rc;
     }
     if (R.d.kind == GN_LAYER_RMSNORM) {
       std::fill(host.begin() + R.poff, host.begin() + R.poff + R.D, 1.0f);  // rmsnorm.go:80-82
@@ -1235,6 +1256,22 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         if (r) return r;
         break;
       }
+      case GN_LAYER_SWIGLU: {
+        const int out2 = 2 * R.d.out_size;
+        {
+          KTimer kt(c, GN_KCLASS_GEMM);
+          GemmArgs g{};  // Z[b] = [W x_b | V x_b]
+          g.M = B; g.N = out2; g.K = R.d.in_size;
+          g.A = cur; g.lda = R.d.in_size;
+          g.B = M->params + R.poff; g.ldb = R.d.in_size;
+          g.C = R.zbuf; g.ldc = out2; g.alpha = 1.0f;
+          g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+          HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
+        }
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_swiglu_fwd(R.zbuf, R.out, B, R.d.out_size, c->stream));
+        break;
+      }
       case GN_LAYER_RMSNORM: {
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_rms_fwd(cur, M->params + R.poff, R.out, R.rmsv, B * (R.in_len / R.D), R.D,
@@ -1362,6 +1399,28 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale);
         if (r) return r;
         is_dz = false;
+        break;
+      }
+      case GN_LAYER_SWIGLU: {  // swiglu.go:196-232
+        {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_swiglu_bwd(R.gout, R.zbuf, R.dzbuf, B, R.d.out_size, c->stream));
+        }
+        float *gin = nullptr;
+        const float *aux = nullptr;
+        int deriv = 0;
+        bool next_dz = false;
+        if (below) {
+          gin = below->gout;
+          if (below->d.kind == GN_LAYER_DENSE && !below->ap.jac) {
+            aux = below->out;  // act' of the Dense below fused into the dX epilogue
+            deriv = below->ap.deriv;
+            next_dz = true;
+          }
+        }
+        HIP_OK(c, dense_bwd_core(c, in, M->params + R.poff, R.dzbuf, M->grads + R.poff, nullptr, gin,
+                                 B, R.d.in_size, 2 * R.d.out_size, scale, aux, deriv));
+        is_dz = next_dz;
         break;
       }
       case GN_LAYER_RMSNORM: {  // rmsnorm.go:301-329: dx, then gamma += g * (x / rms)

@@ -419,4 +419,59 @@ hipError_t launch_dropout(const float *x, const float *mask, float scale, float 
   return hipGetLastError();
 }
 
+// SwiGLU gating (swiglu.go:165-171 forward, :206-216 backward) on the
+// projections Z = [gate | up] of each row (2*out wide, from one GEMM against
+// the parameter block [W | V]): y = (g sig(g)) u with sig(g) = 1/(1 +
+// float32(exp(float64(-g)))); dUp = dy swish, dGate = dy (swish + sig (1 -
+// swish)) u, written back as dZ = [dGate | dUp] for the parameter and input GEMMs.
+__device__ __forceinline__ float swiglu_sig(float g) { return 1.0f / (1.0f + (float)exp((double)(-g))); }
+
+__global__ __launch_bounds__(TPB) void swiglu_fwd_kernel(const float *__restrict__ Z,
+                                                         float *__restrict__ y, int64_t total,
+                                                         int out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / out;
+    const int o = (int)(i - r * out);
+    const float g = Z[r * 2 * out + o], u = Z[r * 2 * out + out + o];
+    y[i] = (g * swiglu_sig(g)) * u;
+  }
+}
+
+__global__ __launch_bounds__(TPB) void swiglu_bwd_kernel(const float *__restrict__ dy,
+                                                         const float *__restrict__ Z,
+                                                         float *__restrict__ dZ, int64_t total,
+                                                         int out) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / out;
+    const int o = (int)(i - r * out);
+    const float g = Z[r * 2 * out + o], u = Z[r * 2 * out + out + o];
+    const float sig = swiglu_sig(g), swish = g * sig;
+    dZ[r * 2 * out + out + o] = dy[i] * swish;
+    const float dswish = swish + sig * (1.0f - swish);
+    dZ[r * 2 * out + o] = dy[i] * dswish * u;
+  }
+}
+
+hipError_t launch_swiglu_fwd(const float *Z, float *y, int B, int out, hipStream_t s) {
+  const int64_t total = (int64_t)B * out;
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + TPB - 1) / TPB;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, Z, y, total, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_bwd(const float *dy, const float *Z, float *dZ, int B, int out,
+                             hipStream_t s) {
+  const int64_t total = (int64_t)B * out;
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + TPB - 1) / TPB;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, dy, Z, dZ, total,
+                     out);
+  return hipGetLastError();
+}
+
 }  // namespace gn

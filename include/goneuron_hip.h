@@ -62,6 +62,7 @@ extern "C" {
 #define GN_LAYER_LSTM_UNROLLER 10 /* SequenceUnroller(LSTM)   unroller.go:57, lstm.go */
 #define GN_LAYER_AVGPOOL2D 11    /* layer.NewAvgPool2D        avgpool2d.go:50 */
 #define GN_LAYER_RMSNORM 12      /* layer.NewRMSNorm          rmsnorm.go:49 */
+#define GN_LAYER_SWIGLU 13       /* layer.NewSwiGLU           swiglu.go:47 */
 
 #define GN_LOSS_MSE 1            /* loss.MSE          loss.go:38-105 */
 #define GN_LOSS_CE 2             /* loss.CrossEntropy loss.go:108-178 */

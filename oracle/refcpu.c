@@ -766,6 +766,88 @@ int32_t gno_rmsnorm(const float *x, int32_t total, int32_t n, float eps, const f
   return total / n;
 }
 
+/* SwiGLU swiglu.go:73-100 (Build: params [W | V], each out x in, one LCG
+ * stream seeded in*100 + out + 42, Xavier scale), :102-171 (forward of one
+ * sample: gate = W x, up = V x as sequential sums, out = (g sig(g)) up with
+ * sig = 1 / (1 + float32(exp(float64(-g))))), :174-232 (backward: dUp =
+ * grad swish, dGate = grad (swish + sig (1 - swish)) up; for each output o in
+ * turn gradW += dGate x, gradV += dUp x, gradIn += dGate W + dUp V). */
+static void swiglu_build(layer *L) {
+  int32_t in = L->spec.in_size, out = L->spec.out_size;
+  L->nparams = 2 * (int64_t)in * out;
+  L->in_len = in;
+  L->out_len = out;
+  L->inputBuf = zalloc(in);
+  L->preActBuf = zalloc(2 * (int64_t)out); /* gate | up */
+  L->outputBuf = zalloc(out);
+  L->gradInBuf = zalloc(in);
+  L->dzBuf = zalloc(2 * (int64_t)out);     /* dGate | dUp */
+}
+static void swiglu_init(layer *L) {
+  int32_t in = L->spec.in_size, out = L->spec.out_size;
+  float scale = (float)sqrt(2.0 / ((double)in + (double)out));
+  uint64_t rng = (uint64_t)(in * 100 + out + 42);
+  for (int64_t i = 0; i < L->nparams; i++) L->params[i] = gno_rand_float(&rng) * 2 * scale - scale;
+}
+static float swiglu_sig(float g) { return 1.0f / (1.0f + (float)exp((double)(-g))); }
+static const float *swiglu_forward(layer *L, const float *x) {
+  int32_t in = L->spec.in_size, out = L->spec.out_size;
+  const float *w = L->params, *v = L->params + (int64_t)in * out;
+  memcpy(L->inputBuf, x, sizeof(float) * in);
+  for (int32_t o = 0; o < out; o++) {
+    float sw = 0.0f, sv = 0.0f;
+    for (int32_t i = 0; i < in; i++) {
+      sw += w[(int64_t)o * in + i] * x[i];
+      sv += v[(int64_t)o * in + i] * x[i];
+    }
+    L->preActBuf[o] = sw;
+    L->preActBuf[out + o] = sv;
+  }
+  for (int32_t o = 0; o < out; o++) {
+    float g = L->preActBuf[o];
+    L->outputBuf[o] = (g * swiglu_sig(g)) * L->preActBuf[out + o];
+  }
+  return L->outputBuf;
+}
+static const float *swiglu_backward(layer *L, const float *grad) {
+  int32_t in = L->spec.in_size, out = L->spec.out_size;
+  const float *w = L->params, *v = L->params + (int64_t)in * out;
+  float *gw = L->grads, *gv = L->grads + (int64_t)in * out;
+  const float *x = L->inputBuf;
+  for (int32_t o = 0; o < out; o++) {
+    float g = L->preActBuf[o], u = L->preActBuf[out + o];
+    float sig = swiglu_sig(g), swish = g * sig;
+    L->dzBuf[out + o] = grad[o] * swish;
+    float dSwish = swish + sig * (1.0f - swish);
+    L->dzBuf[o] = grad[o] * dSwish * u;
+  }
+  for (int32_t i = 0; i < in; i++) L->gradInBuf[i] = 0.0f;
+  for (int32_t o = 0; o < out; o++) {
+    float dg = L->dzBuf[o], du = L->dzBuf[out + o];
+    for (int32_t i = 0; i < in; i++) {
+      gw[(int64_t)o * in + i] += dg * x[i];
+      gv[(int64_t)o * in + i] += du * x[i];
+      L->gradInBuf[i] += dg * w[(int64_t)o * in + i] + du * v[(int64_t)o * in + i];
+    }
+  }
+  return L->gradInBuf;
+}
+
+void gno_swiglu(const float *x, int32_t in, int32_t out, const float *params, float *y,
+                const float *g, float *gin, float *gparams) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_SWIGLU;
+  L.spec.in_size = in;
+  L.spec.out_size = out;
+  swiglu_build(&L);
+  L.params = (float *)params;
+  L.grads = gparams;
+  memcpy(y, swiglu_forward(&L, x), sizeof(float) * out);
+  if (g && gin && gparams) memcpy(gin, swiglu_backward(&L, g), sizeof(float) * in);
+  free(L.inputBuf); free(L.preActBuf); free(L.outputBuf); free(L.gradInBuf); free(L.dzBuf);
+}
+
 /* ------------------------------------------------------------------------ */
 /* LSTM (lstm.go) wrapped by SequenceUnroller (unroller.go)                  */
 /* ------------------------------------------------------------------------ */
@@ -1353,6 +1435,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_CLSPOOL: cls_build(L); break;
     case GNO_LAYER_TRANSFORMER: tb_build(L); break;
     case GNO_LAYER_RMSNORM: rms_build(L); break;
+    case GNO_LAYER_SWIGLU: swiglu_build(L); break;
     default: break;
   }
 }
@@ -1364,6 +1447,7 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_POSENC) pe_init(L);
   else if (L->kind == GNO_LAYER_TRANSFORMER) tb_init(L);
   else if (L->kind == GNO_LAYER_RMSNORM) rms_init(L);
+  else if (L->kind == GNO_LAYER_SWIGLU) swiglu_init(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -1387,6 +1471,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
     case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
     case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
+    case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
     default: o = x;
   }
   return o;
@@ -1405,6 +1490,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_CLSPOOL: return cls_backward(L, g);
     case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
     case GNO_LAYER_RMSNORM: return rms_backward(L, g);
+    case GNO_LAYER_SWIGLU: return swiglu_backward(L, g);
     default: return g;
   }
 }

@@ -20,6 +20,7 @@
  *   MaxPool2D                         internal/layer/maxpool2d.go:106-410,508-513
  *   AvgPool2D                         internal/layer/avgpool2d.go:98-220,401-474,560-565
  *   RMSNorm                           internal/layer/rmsnorm.go:73-96,222-240,301-335
+ *   SwiGLU                            internal/layer/swiglu.go:73-232
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -66,6 +67,7 @@ enum {
   GNO_LAYER_LSTM_UNROLLER = 10,
   GNO_LAYER_AVGPOOL2D = 11,
   GNO_LAYER_RMSNORM = 12,
+  GNO_LAYER_SWIGLU = 13,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -141,6 +143,10 @@ int32_t gno_avgpool2d(const float *x, int32_t total, int32_t inC, int32_t k, int
  * row count, -1 when n does not divide total. */
 int32_t gno_rmsnorm(const float *x, int32_t total, int32_t n, float eps, const float *gamma,
                     float *out, const float *g, float *gin, float *ggamma);
+/* SwiGLU of one sample with params [W | V] (each out x in) into y; with g,
+ * gin and gparams also the backward (gparams accumulates). */
+void gno_swiglu(const float *x, int32_t in, int32_t out, const float *params, float *y,
+                const float *g, float *gin, float *gparams);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR = range(7)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM) = range(1, 13)
+ LAYER_RMSNORM, LAYER_SWIGLU) = range(1, 14)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -104,6 +104,7 @@ def lib():
         L.gno_rmsnorm.argtypes = [f32p, C.c_int32, C.c_int32, C.c_float, f32p, f32p, f32p, f32p,
                                   f32p]
         L.gno_rmsnorm.restype = C.c_int32
+        L.gno_swiglu.argtypes = [f32p, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p, f32p]
         _lib = L
     return _lib
 
@@ -255,6 +256,23 @@ def rmsnorm(x, n, gamma=None, g=None, eps=1e-5):
                          fptr(gg)) < 0:
         raise ValueError("n must divide the input length")
     return out, gin, gg
+
+
+def swiglu(x, out, params, g=None):
+    """SwiGLU of one sample (params [W | V], each out x in); returns y, or
+    (y, grad_in, grad_params) when g is given (grad_params from zero)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    params = np.ascontiguousarray(params, np.float32).ravel()
+    assert params.size == 2 * x.size * out
+    y = np.empty(out, np.float32)
+    if g is None:
+        lib().gno_swiglu(fptr(x), x.size, out, fptr(params), fptr(y), None, None, None)
+        return y
+    g = np.ascontiguousarray(g, np.float32).ravel()
+    gin = np.empty(x.size, np.float32)
+    gp = np.zeros(params.size, np.float32)
+    lib().gno_swiglu(fptr(x), x.size, out, fptr(params), fptr(y), fptr(g), fptr(gin), fptr(gp))
+    return y, gin, gp
 
 
 def matmul(x, w, b):

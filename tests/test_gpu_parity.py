@@ -345,6 +345,43 @@ def test_rmsnorm_net(gn, oracle, case):
         assert max_rel(got[b], ref) <= 1e-6, (b, max_rel(got[b], ref))
 
 
+_SWIGLU_CASES = {
+    # Dense -> SwiGLU -> Dense: the Dense below gets its act' fused into dX
+    "dense_swiglu_dense": dict(B=33, in_len=32, classes=10, loss="ce", layers=[
+        {"kind": "dense", "in": 32, "out": 64, "act": "relu", "ptr": False},
+        {"kind": "swiglu", "in": 64, "out": 48},
+        {"kind": "dense", "in": 48, "out": 10, "act": "softmax", "ptr": True}]),
+    # SwiGLU as the first layer (no input gradient), MSE
+    "first_layer": dict(B=17, in_len=40, classes=5, loss="mse", layers=[
+        {"kind": "swiglu", "in": 40, "out": 24},
+        {"kind": "dense", "in": 24, "out": 5, "act": "linear", "ptr": False}]),
+    # RMSNorm -> SwiGLU feed-forward at transformer widths
+    "rms_swiglu_1024": dict(B=128, in_len=256, classes=100, loss="ce", layers=[
+        {"kind": "rmsnorm", "n": 256},
+        {"kind": "swiglu", "in": 256, "out": 1024},
+        {"kind": "dense", "in": 1024, "out": 100, "act": "logsoftmax", "ptr": True}]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_SWIGLU_CASES))
+def test_swiglu_net(gn, oracle, case):
+    """SwiGLU (swiglu.go) inside a net: gradients of [W | V], Adam state and
+    updated weights against the oracle over 3 steps; then the gated output of
+    the trained model against the oracle's SwiGLU of the GPU's own input."""
+    cfg = dict(num=13, name="swiglu_" + case, lr=1e-3, x="normal", **_SWIGLU_CASES[case])
+    model, _ = _compare_step(gn, oracle, cfg, steps=3)
+    x, _ = configs_inputs(cfg)
+    model.PredictBatch(x)
+    B, li = cfg["B"], [d["kind"] for d in cfg["layers"]].index("swiglu")
+    d = cfg["layers"][li]
+    xin = x if li == 0 else model.LayerOutput(li - 1, B * d["in"]).reshape(B, -1)
+    got = model.LayerOutput(li, B * d["out"]).reshape(B, -1)
+    params = model.Params()[model.LayerParams(li)]
+    for b in range(B):
+        ref = oracle.swiglu(xin[b], d["out"], params)
+        assert max_rel(got[b], ref) <= TOL, (b, max_rel(got[b], ref))
+
+
 def configs_inputs(cfg):
     from goneuron_amd import configs
     return configs.inputs(cfg)

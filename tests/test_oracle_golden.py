@@ -258,6 +258,53 @@ def test_rmsnorm_rows_are_independent(oracle):
     np.testing.assert_allclose(gg, acc, rtol=1e-6, atol=1e-7)
 
 
+def test_swiglu_known_answer_and_init(oracle):
+    """swiglu_test.go:31-51 (w = 2, v = 3, x = 1: y = 2 sig(2) 3 = 5.284782);
+    swiglu_test.go:8-29 shapes; Build (swiglu.go:73-100): one LCG stream over
+    [W | V] seeded in*100 + out + 42 with the Xavier scale."""
+    y = oracle.swiglu(np.ones(1, np.float32), 1, np.array([2, 3], np.float32))
+    assert abs(float(y[0]) - 5.284782) <= 1e-5
+    net = oracle.Net([oracle.spec(oracle.LAYER_SWIGLU, in_size=4, out_size=2)], oracle.LOSS_MSE)
+    seed, scale = 4 * 100 + 2 + 42, np.float32(math.sqrt(2.0 / 6.0))
+    want = []
+    for _ in range(16):
+        seed = (seed * 6364136223846793005 + 1) & (2**64 - 1)
+        want.append(np.float32(seed >> 33) / np.float32(2**31) * np.float32(2) * scale - scale)
+    np.testing.assert_array_equal(net.params, np.array(want, np.float32))
+    y, gin, gp = oracle.swiglu(np.arange(1, 5, dtype=np.float32), 2, net.params,
+                               g=np.array([0.1, 0.2], np.float32))
+    assert y.shape == (2,) and gin.shape == (4,) and gp.shape == (16,)
+
+
+def test_swiglu_gradients_by_finite_differences(oracle):
+    """dx, dW and dV of sum(g * y) against central differences of the float64
+    definition y = (Wx) sig(Wx) (Vx): a wrong swish derivative, a swapped
+    gate/up or a dropped term fails."""
+    rng = np.random.default_rng(21)
+    n_in, n_out = 5, 3
+    x = rng.normal(size=n_in).astype(np.float32)
+    p = (0.7 * rng.normal(size=2 * n_in * n_out)).astype(np.float32)
+    g = rng.normal(size=n_out).astype(np.float32)
+
+    def f(xx, pp):
+        W = pp[:n_in * n_out].reshape(n_out, n_in)
+        V = pp[n_in * n_out:].reshape(n_out, n_in)
+        a, u = W @ xx, V @ xx
+        return float(g.astype(np.float64) @ (a / (1 + np.exp(-a)) * u))
+
+    y, gin, gp = oracle.swiglu(x, n_out, p, g=g)
+    x64, p64 = x.astype(np.float64), p.astype(np.float64)
+    W = p64[:n_in * n_out].reshape(n_out, n_in)
+    V = p64[n_in * n_out:].reshape(n_out, n_in)
+    a = W @ x64
+    np.testing.assert_allclose(y, a / (1 + np.exp(-a)) * (V @ x64), rtol=1e-5, atol=1e-6)
+    h = 1e-6
+    num_x = [(f(x64 + h * e, p64) - f(x64 - h * e, p64)) / (2 * h) for e in np.eye(n_in)]
+    num_p = [(f(x64, p64 + h * e) - f(x64, p64 - h * e)) / (2 * h) for e in np.eye(p.size)]
+    np.testing.assert_allclose(gin, num_x, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(gp, num_p, rtol=1e-4, atol=1e-5)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
