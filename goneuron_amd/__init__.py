@@ -22,13 +22,15 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "AvgPool2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock", "CLSPooling", "LSTM", "SequenceUnroller",
-    "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "Ref", "Adam", "MSE",
+    "AvgPool2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock",
+    "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
+    "LSTM", "SequenceUnroller",
+    "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
     "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
 ]
 
 # ---------------------------------------------------------------- activations
-ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR = range(7)
+ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU = range(8)
 
 
 class Activation:
@@ -52,6 +54,7 @@ Tanh = Activation(ACT_TANH, False, "Tanh")
 Softmax = Activation(ACT_SOFTMAX, False, "Softmax")
 LogSoftmax = Activation(ACT_LOGSOFTMAX, False, "LogSoftmax")
 Linear = Activation(ACT_LINEAR, False, "Linear")
+GELU = Activation(ACT_GELU, False, "GELU")
 
 
 def Ref(act: Activation) -> Activation:
@@ -179,6 +182,28 @@ def PositionalEncoding(seq_len, *dim):
 def TransformerBlock(dim, heads, seq_len, ff_dim, causal):
     return Layer(LAYER_TRANSFORMER, dim=dim, num_heads=heads, seq_len=seq_len, ff_dim=ff_dim,
                  causal=int(causal))
+
+
+# TransformerBlockExt options (goneuron.go:352-358, transformer.go:199-210)
+ActReLU, ActSwiGLU, ActGELU = 0, 1, 2
+NormLN, NormRMS = 0, 1
+
+
+def TransformerBlockExt(heads, seq_len, ff_dim, causal, act_type, norm_type, use_rope, *dim):
+    """goneuron.TransformerBlockExt (goneuron.go:342-350): feed-forward ReLU,
+    SwiGLU or GELU, LayerNorm or RMSNorm, optional rotary embeddings on Q and
+    K.  The model dimension is required: with dim = -1 the reference leaves
+    the RMSNorm and SwiGLU sub-layers unbuilt (their Build has no error
+    return, transformer.go:987-1005)."""
+    if not dim or dim[0] <= 0:
+        raise GNError(-1, "TransformerBlockExt needs the model dimension")
+    if act_type not in (ActReLU, ActSwiGLU, ActGELU):
+        raise GNError(-1, f"unknown activation type {act_type}")
+    if norm_type not in (NormLN, NormRMS):
+        raise GNError(-1, f"unknown norm type {norm_type}")
+    return Layer(LAYER_TRANSFORMER, dim=int(dim[0]), num_heads=heads, seq_len=seq_len, ff_dim=ff_dim,
+                 causal=int(causal), block_act=int(act_type), block_norm=int(norm_type),
+                 use_rope=int(bool(use_rope)))
 
 
 def CLSPooling(seq_len, dim):

@@ -34,6 +34,7 @@ class LayerDesc(C.Structure):
         ("seq_len", C.c_int32), ("num_heads", C.c_int32), ("ff_dim", C.c_int32),
         ("causal", C.c_int32), ("vocab", C.c_int32), ("dim", C.c_int32),
         ("return_sequences", C.c_int32), ("eps", C.c_float),
+        ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
     ]
 
 

@@ -10,14 +10,16 @@ from __future__ import annotations
 import numpy as np
 
 from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, RMSNorm,
-               SwiGLU, Flatten,
+               SwiGLU, Flatten, TransformerBlockExt, ActReLU, ActSwiGLU, ActGELU, NormLN, NormRMS,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
-               Sigmoid, Tanh, Linear, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
+               Sigmoid, Tanh, Linear, GELU, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
                fill_uniform, fill_class_ids)
 
+BLOCK_ACTS = {"relu": ActReLU, "swiglu": ActSwiGLU, "gelu": ActGELU}
+BLOCK_NORMS = {"ln": NormLN, "rms": NormRMS}
 _ACTS = {"relu": ReLU, "sigmoid": Sigmoid, "tanh": Tanh, "linear": Linear, "softmax": Softmax,
-         "logsoftmax": LogSoftmax}
+         "logsoftmax": LogSoftmax, "gelu": GELU}
 
 
 def dense(i, o, act, ptr=False):
@@ -47,12 +49,15 @@ def wide(width=4096, classes=1000, depth=4, B=1024):
                 classes=classes, layers=ls)
 
 
-def gpt(B=32, T=128, vocab=8000, dim=256, heads=8, ff=1024, causal=True):
+def gpt(B=32, T=128, vocab=8000, dim=256, heads=8, ff=1024, causal=True, act="relu", norm="ln",
+        rope=False):
+    """C4; act / norm / rope select TransformerBlockExt's feed-forward
+    ("relu", "swiglu", "gelu"), norms ("ln", "rms") and rotary embeddings."""
     return dict(num=4, name="gpt", B=B, loss="ce", lr=1e-3, x="ids", in_len=T, classes=vocab,
                 layers=[{"kind": "embedding", "vocab": vocab, "dim": dim},
                         {"kind": "posenc", "T": T, "dim": dim},
                         {"kind": "transformer", "dim": dim, "heads": heads, "T": T, "ff": ff,
-                         "causal": causal},
+                         "causal": causal, "act": act, "norm": norm, "rope": rope},
                         {"kind": "clspool", "T": T, "dim": dim},
                         dense(dim, vocab, "logsoftmax", True)])
 
@@ -114,7 +119,13 @@ def product_layers(cfg):
         elif k == "posenc":
             out.append(PositionalEncoding(d["T"], d["dim"]))
         elif k == "transformer":
-            out.append(TransformerBlock(d["dim"], d["heads"], d["T"], d["ff"], d["causal"]))
+            if d.get("act", "relu") == "relu" and d.get("norm", "ln") == "ln" and not d.get("rope"):
+                out.append(TransformerBlock(d["dim"], d["heads"], d["T"], d["ff"], d["causal"]))
+            else:
+                out.append(TransformerBlockExt(d["heads"], d["T"], d["ff"], d["causal"],
+                                               BLOCK_ACTS[d.get("act", "relu")],
+                                               BLOCK_NORMS[d.get("norm", "ln")], d.get("rope", False),
+                                               d["dim"]))
         elif k == "clspool":
             out.append(CLSPooling(d["T"], d["dim"]))
         elif k == "lstm":

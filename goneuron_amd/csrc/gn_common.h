@@ -21,7 +21,19 @@ enum DerivKind : int32_t {
   D_SIGMOID = 2,
   D_TANH = 3,
   D_NAN = 4,      // Softmax/LogSoftmax *values*: Derivative returns NaN (Q3)
+  D_GELU = 5,     // GELU'(x) in float64 of the saved value, which must be the
+                  // pre-activation (GELU *values* run as identity forward)
 };
+
+// GELU'(x) as activations.go:258-272 computes it, in float64.
+__host__ __device__ __forceinline__ float gelu_deriv(float x) {
+  const double xd = (double)x, x2 = xd * xd, x3 = xd * x2;
+  const double arg = 0.7978845608028654 * (xd + 0.044715 * x3);
+  const double tv = tanh(arg);
+  const double t1 = 0.5 * (1.0 + tv);
+  const double t2 = 0.5 * xd * (1.0 - tv * tv) * 0.7978845608028654 * (1.0 + 0.134145 * x2);
+  return (float)(t1 + t2);
+}
 
 // Forward activation kinds applied elementwise in GEMM epilogues.
 enum FwdKind : int32_t {
@@ -70,7 +82,7 @@ hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scal
 
 // SwiGLU gating on Z = [gate | up] rows (2*out wide) and its backward into dZ
 hipError_t launch_swiglu_fwd(const float *Z, float *y, int B, int out, hipStream_t s);
-hipError_t launch_swiglu_bwd(const float *dy, const float *Z, float *dZ, int B, int out,
+hipError_t launch_swiglu_bwd(const float *dy, const float *Z, int ldz, float *dZ, int B, int out,
                              hipStream_t s);
 
 // dz = g * act'(out) elementwise (optionally with dropout mask/scale fused)
@@ -158,6 +170,10 @@ hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, flo
                          int rows, int N, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
+// Rotary embedding of rows [rows, NH*hd] in place; position = row % T; cs/sn
+// are [T][hd/2] tables; conj rotates the other way.
+hipError_t launch_rope(float *x, const float *cs, const float *sn, int rows, int T, int NH, int hd,
+                       int conj, hipStream_t s);
 hipError_t launch_rms_fwd(const float *x, const float *gam, float *y, float *rms, int rows, int N,
                           float eps, hipStream_t s);
 hipError_t launch_rms_bwd(const float *g, const float *x, const float *gam, const float *rms,

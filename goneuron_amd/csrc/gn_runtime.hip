@@ -331,6 +331,13 @@ static int plan_act(int act, int is_ptr, ActPlan &p) {
     case GN_ACT_SIGMOID: p.fwd = F_SIGMOID; p.deriv = D_SIGMOID; break;
     case GN_ACT_TANH: p.fwd = F_TANH; p.deriv = D_TANH; break;
     case GN_ACT_LINEAR: break;
+    case GN_ACT_GELU:
+      // only *activations.GELU is ActTypeGELU (layer.go:196-197); the value
+      // runs as ActTypeNone: identity forward, Derivative(preAct) backward,
+      // and the identity output is the pre-activation D_GELU needs
+      if (is_ptr) return GN_ERR_UNSUPPORTED;
+      p.deriv = D_GELU;
+      break;
     case GN_ACT_SOFTMAX:
     case GN_ACT_LOGSOFTMAX:
       if (is_ptr) {
@@ -523,6 +530,8 @@ struct LayerRT {
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
+    float *Z, *MG, *DZS;     // SwiGLU ff1: [gate | up] per token, token-0 mid grad, its dZ
+    float *rcos, *rsin;      // RoPE angle tables [T][hd/2]
   } tb{};
 };
 
@@ -653,23 +662,26 @@ static void init_posenc(float *p, int T, int D) {  // PositionalEncoding.Build t
 }
 
 // TransformerBlock flat layout (transformer.go:1035-1056): wQ, wK, wV, wOut
-// (W [D][D] then b [D]), norm1 (gamma, beta), norm2, ff1 (W [FF][D], b),
-// ff2 (W [D][FF], b).  Build rebinds every sub-layer to fresh zero slices, so
-// the reference starts the block at all-zero parameters.
+// (W [D][D] then b [D]), norm1, norm2 (LayerNorm: gamma, beta; RMSNorm:
+// gamma), ff1 (Dense: W [FF][D], b; SwiGLU: W [FF][D] then V [FF][D], here
+// at b1), ff2 (W [D][FF], b).  Build rebinds every sub-layer to fresh zero
+// slices, so the reference starts the block at all-zero parameters.
 struct TbOff {
   int64_t wq, bq, wk, bk, wv, bv, wo, bo, g1, be1, g2, be2, w1, b1, w2, b2, total;
 };
-static TbOff tb_offsets(int D, int FF) {
+static TbOff tb_offsets(int D, int FF, int act = GN_BLOCK_ACT_RELU, int norm = GN_BLOCK_NORM_LN) {
   TbOff o{};
   int64_t off = 0;
   const int64_t dd = (int64_t)D * D;
+  const int64_t nn = norm == GN_BLOCK_NORM_RMS ? D : 2 * (int64_t)D;
   o.wq = off; o.bq = off + dd; off += dd + D;
   o.wk = off; o.bk = off + dd; off += dd + D;
   o.wv = off; o.bv = off + dd; off += dd + D;
   o.wo = off; o.bo = off + dd; off += dd + D;
-  o.g1 = off; o.be1 = off + D; off += 2 * D;
-  o.g2 = off; o.be2 = off + D; off += 2 * D;
-  o.w1 = off; o.b1 = off + (int64_t)FF * D; off += (int64_t)FF * D + FF;
+  o.g1 = off; o.be1 = off + D; off += nn;
+  o.g2 = off; o.be2 = off + D; off += nn;
+  o.w1 = off; o.b1 = off + (int64_t)FF * D;
+  off += act == GN_BLOCK_ACT_SWIGLU ? 2 * (int64_t)FF * D : (int64_t)FF * D + FF;
   o.w2 = off; o.b2 = off + (int64_t)D * FF; off += (int64_t)D * FF + D;
   o.total = off;
   return o;
@@ -799,7 +811,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
           return set_err(c, GN_ERR_SHAPE, "layer %d: TransformerBlock %dx%d != input %d", i, R.T, R.D, len);
         if (!attn_supported(R.T, R.D, R.NH))
           return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: attention needs T <= 128, D/heads <= 32", i);
-        R.pcount = tb_offsets(R.D, R.FF).total;
+        if (R.d.block_act < GN_BLOCK_ACT_RELU || R.d.block_act > GN_BLOCK_ACT_GELU ||
+            R.d.block_norm < GN_BLOCK_NORM_LN || R.d.block_norm > GN_BLOCK_NORM_RMS)
+          return set_err(c, GN_ERR_INVALID, "layer %d: unknown TransformerBlock act %d / norm %d", i,
+                         R.d.block_act, R.d.block_norm);
+        R.pcount = tb_offsets(R.D, R.FF, R.d.block_act, R.d.block_norm).total;
         R.out_len = len;
         break;
       case GN_LAYER_CLSPOOL:
@@ -894,6 +910,31 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), rows * 2, &t.st1))) return rc;
       if ((rc = model_alloc(M.get(), rows * 2, &t.st2))) return rc;
       if ((rc = model_alloc(M.get(), (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
+      if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
+        if ((rc = model_alloc(M.get(), rows * 2 * FF, &t.Z))) return rc;
+        if ((rc = model_alloc(M.get(), (size_t)max_batch * FF, &t.MG))) return rc;
+        if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * FF, &t.DZS))) return rc;
+      }
+      if (R.d.use_rope) {
+        // applyRoPE's angles (transformer.go:215-221) in float32, computed once
+        const int hd = R.D / R.NH, half = hd / 2;
+        std::vector<float> cs((size_t)R.T * std::max(half, 1)), sn(cs.size());
+        for (int tt = 0; tt < R.T; ++tt)
+          for (int k = 0; k < half; ++k) {
+            const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
+            const float m = (float)tt * theta;
+            cs[(size_t)tt * half + k] = (float)cos((double)m);
+            sn[(size_t)tt * half + k] = (float)sin((double)m);
+          }
+        if ((rc = model_alloc(M.get(), cs.size(), &t.rcos))) return rc;
+        if ((rc = model_alloc(M.get(), sn.size(), &t.rsin))) return rc;
+        HIP_OK(c, hipMemcpyAsync(t.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice,
+                                 c->stream));
+        HIP_OK(c, hipMemcpyAsync(t.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice,
+                                 c->stream));
+        // the host vectors go out of scope: finish the copies first
+        HIP_OK(c, hipStreamSynchronize(c->stream));
+      }
     }
     if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
       init_lstm(host.data() + R.poff, R.I, R.H);
@@ -1097,10 +1138,40 @@ static hipError_t gemm_dw_last(gn_ctx *c, const float *S, const float *X, float 
   return launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
 }
 
+// Block norm k (0: norm1, 1: norm2) forward: LayerNorm (stats = mean, std)
+// or RMSNorm(dim, 1e-5) (stats = rms), transformer.go:928-934.
+static hipError_t tb_norm_fwd(gn_ctx *c, const LayerRT &R, const float *P, const TbOff &o, int k,
+                              const float *x, float *y, float *st, int rows) {
+  const float *g = P + (k == 0 ? o.g1 : o.g2), *be = P + (k == 0 ? o.be1 : o.be2);
+  KTimer kt(c, GN_KCLASS_OTHER);
+  if (R.d.block_norm == GN_BLOCK_NORM_RMS) return launch_rms_fwd(x, g, y, st, rows, R.D, 1e-5f, c->stream);
+  return launch_ln_fwd(x, g, be, y, st, rows, R.D, c->stream);
+}
+
+// Block norm backward: dx into dx, gamma (and LayerNorm beta) gradients.
+static hipError_t tb_norm_bwd(gn_ctx *c, const LayerRT &R, const float *P, float *G, const TbOff &o,
+                              int k, const float *g, const float *x, const float *st, float *dx,
+                              int rows, float scale) {
+  const int D = R.D;
+  const int64_t og = k == 0 ? o.g1 : o.g2, ob = k == 0 ? o.be1 : o.be2;
+  LayerRT::Tb &t = const_cast<LayerRT &>(R).tb;
+  KTimer kt(c, GN_KCLASS_OTHER);
+  hipError_t e;
+  if (R.d.block_norm == GN_BLOCK_NORM_RMS) {
+    e = launch_rms_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
+  } else {
+    e = launch_ln_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
+  }
+  if (e != hipSuccess) return e;
+  e = launch_colsum(t.GX, rows, D, D, scale, G + og, c->scratch, c->scratch_floats, c->stream);
+  if (e != hipSuccess || R.d.block_norm == GN_BLOCK_NORM_RMS) return e;
+  return launch_colsum(g, rows, D, D, scale, G + ob, c->scratch, c->scratch_floats, c->stream);
+}
+
 static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   gn_ctx *c = M->ctx;
   const int D = R.D, FF = R.FF, rows = B * R.T;
-  const TbOff o = tb_offsets(D, FF);
+  const TbOff o = tb_offsets(D, FF, R.d.block_act, R.d.block_norm);
   const float *P = M->params + R.poff;
   LayerRT::Tb &t = R.tb;
   // per-token projections: Q/K/V = X W^T + b (Dense with Linear activation)
@@ -1109,56 +1180,111 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   HIP_OK(c, gemm_nt(c, X, P + o.wv, P + o.bv, t.V, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
   {
     KTimer kt(c, GN_KCLASS_OTHER);
+    if (R.d.use_rope) {  // transformer.go:457-461; the backward reads the rotated Q, K too
+      HIP_OK(c, launch_rope(t.Q, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
+      HIP_OK(c, launch_rope(t.K, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
+    }
     HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, c->stream));
   }
   // res1 = x + wOut(o): the residual add rides in the GEMM epilogue
   HIP_OK(c, gemm_nt(c, t.O, P + o.wo, P + o.bo, t.RES1, rows, D, D, EPI_BIAS_ADD, 0, X));
-  {
+  HIP_OK(c, tb_norm_fwd(c, R, P, o, 0, t.RES1, t.N1, t.st1, rows));
+  if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
+    // Z = [gate | up] for every token (one GEMM against [W | V]), MID = swish(gate) * up
+    HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, nullptr, t.Z, rows, 2 * FF, D, EPI_BIAS_ACT, F_IDENTITY,
+                      nullptr));
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_ln_fwd(t.RES1, P + o.g1, P + o.be1, t.N1, t.st1, rows, D, c->stream));
+    HIP_OK(c, launch_swiglu_fwd(t.Z, t.MID, rows, FF, c->stream));
+  } else {
+    // ReLU, or GELU as a value activation: identity forward (ActTypeNone)
+    const int f = R.d.block_act == GN_BLOCK_ACT_GELU ? F_IDENTITY : F_RELU;
+    HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, P + o.b1, t.MID, rows, FF, D, EPI_BIAS_ACT, f, nullptr));
   }
-  HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, P + o.b1, t.MID, rows, FF, D, EPI_BIAS_ACT, F_RELU, nullptr));
   HIP_OK(c, gemm_nt(c, t.MID, P + o.w2, P + o.b2, t.RES2, rows, D, FF, EPI_BIAS_ADD, 0, t.N1));
-  KTimer kt(c, GN_KCLASS_OTHER);
-  HIP_OK(c, launch_ln_fwd(t.RES2, P + o.g2, P + o.be2, R.out, t.st2, rows, D, c->stream));
+  HIP_OK(c, tb_norm_fwd(c, R, P, o, 1, t.RES2, R.out, t.st2, rows));
   return GN_OK;
 }
 
 static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int B, float scale) {
   gn_ctx *c = M->ctx;
   const int D = R.D, FF = R.FF, T = R.T, rows = B * T;
-  const TbOff o = tb_offsets(D, FF);
+  const TbOff o = tb_offsets(D, FF, R.d.block_act, R.d.block_norm);
   const float *P = M->params + R.poff;
   float *G = M->grads + R.poff;
   LayerRT::Tb &t = R.tb;
   float *cs = c->scratch;
   const size_t cap = c->scratch_floats;
-  {  // LayerNorm 2 (Q18 formula), dgamma / dbeta column sums
+  // norm 2 (LayerNorm: Q18 formula; RMSNorm: Q19), gamma / beta column sums
+  HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 1, R.gout, t.RES2, t.st2, t.G1, rows, scale));
+  {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_ln_bwd(R.gout, t.RES2, P + o.g2, t.st2, t.G1, t.GX, rows, D, c->stream));
-    HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g2, cs, cap, c->stream));
-    HIP_OK(c, launch_colsum(R.gout, rows, D, D, scale, G + o.be2, cs, cap, c->stream));
     // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
     // per-sample token sums S that the Q10 weight gradient needs anyway
     HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
     HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.b2, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.MID, G + o.w2, B, T, D, FF, scale));
-  // ff1 (ReLU): dz1 = (dz2 W2) * relu'(last token's pre-activation)  (Q10)
-  HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, D_RELU, t.MID, T));
+  if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
+    // ff1 = SwiGLU called per token: its one saved entry (the last token's
+    // input, gate and up) serves the first Backward (token 0); the later ones
+    // return nil, so tokens 1.. get no feed-forward gradient (swiglu.go:126-133,
+    // 175-179).  mg = dRES2[token 0] W2; dZ from the last token's Z.
+    GemmArgs a{};
+    a.M = B; a.N = FF; a.K = D;
+    a.A = t.G1; a.lda = T * D;
+    a.B = P + o.w2; a.ldb = FF;
+    a.C = t.MG; a.ldc = FF; a.alpha = 1.f;
+    a.ws = cs; a.ws_cap = cap;
+    {
+      KTimer kt(c, GN_KCLASS_GEMM);
+      HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+    }
+    {
+      KTimer kt(c, GN_KCLASS_OTHER);
+      HIP_OK(c, launch_swiglu_bwd(t.MG, t.Z + (int64_t)(T - 1) * 2 * FF, T * 2 * FF, t.DZS, B, FF,
+                                  c->stream));
+    }
+    // [dW | dV] = scale * dZ^T x_last
+    GemmArgs w{};
+    w.M = 2 * FF; w.N = D; w.K = B;
+    w.A = t.DZS; w.lda = 2 * FF;
+    w.B = t.N1 + (int64_t)(T - 1) * D; w.ldb = T * D;
+    w.C = G + o.w1; w.ldc = D; w.alpha = scale;
+    w.ws = cs; w.ws_cap = cap;
+    {
+      KTimer kt(c, GN_KCLASS_GEMM);
+      HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, w, c->stream));
+    }
+    // combined = dRES2, plus dZ [W; V] on each sample's token 0
+    HIP_OK(c, hipMemcpyAsync(t.COMB, t.G1, (size_t)rows * D * sizeof(float), hipMemcpyDeviceToDevice,
+                             c->stream));
+    GemmArgs d{};
+    d.M = B; d.N = D; d.K = 2 * FF;
+    d.A = t.DZS; d.lda = 2 * FF;
+    d.B = P + o.w1; d.ldb = D;
+    d.C = t.COMB; d.ldc = T * D; d.alpha = 1.f;
+    d.aux = t.G1; d.ldaux = T * D;
+    d.ws = cs; d.ws_cap = cap;
+    KTimer kt(c, GN_KCLASS_GEMM);
+    HIP_OK(c, launch_gemm('N', 'N', EPI_BIAS_ADD, d, c->stream));
+  } else {
+    // ff1: dz1 = (dz2 W2) * act'(last token's pre-activation) (Q10); ReLU from
+    // its output, GELU (identity forward) from MID, which is the pre-activation
+    const int dk = R.d.block_act == GN_BLOCK_ACT_GELU ? D_GELU : D_RELU;
+    HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, dk, t.MID, T));
+    {
+      KTimer kt(c, GN_KCLASS_OTHER);
+      HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
+      HIP_OK(c, launch_colsum(t.S, B, FF, FF, scale, G + o.b1, cs, cap, c->stream));
+    }
+    HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
+    // combined = dRES2 + dz1 W1
+    HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
+  }
+  // norm 1
+  HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));
   {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
-    HIP_OK(c, launch_colsum(t.S, B, FF, FF, scale, G + o.b1, cs, cap, c->stream));
-  }
-  HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
-  // combined = dRES2 + dz1 W1
-  HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
-  {  // LayerNorm 1
-    KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_ln_bwd(t.COMB, t.RES1, P + o.g1, t.st1, t.G2, t.GX, rows, D, c->stream));
-    HIP_OK(c, launch_colsum(t.GX, rows, D, D, scale, G + o.g1, cs, cap, c->stream));
-    HIP_OK(c, launch_colsum(t.COMB, rows, D, D, scale, G + o.be1, cs, cap, c->stream));
     // wOut (Linear): dz = dRES1
     HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
     HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.bo, cs, cap, c->stream));
@@ -1169,6 +1295,10 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     KTimer kt(c, GN_KCLASS_OTHER);
     HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
                               c->stream));
+    if (R.d.use_rope) {  // transformer.go:660-664: conjugate rotation before wQ/wK
+      HIP_OK(c, launch_rope(t.GQ, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
+      HIP_OK(c, launch_rope(t.GK, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
+    }
   }
   const float *gs[3] = {t.GQ, t.GK, t.GV};
   const int64_t wo[3] = {o.wq, o.wk, o.wv}, bo[3] = {o.bq, o.bk, o.bv};
@@ -1404,7 +1534,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_SWIGLU: {  // swiglu.go:196-232
         {
           KTimer kt(c, GN_KCLASS_OTHER);
-          HIP_OK(c, launch_swiglu_bwd(R.gout, R.zbuf, R.dzbuf, B, R.d.out_size, c->stream));
+          HIP_OK(c, launch_swiglu_bwd(R.gout, R.zbuf, 2 * R.d.out_size, R.dzbuf, B, R.d.out_size,
+                                      c->stream));
         }
         float *gin = nullptr;
         const float *aux = nullptr;

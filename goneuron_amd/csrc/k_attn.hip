@@ -202,6 +202,30 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 }
 
 // ---------------------------------------------------------------------------
+// Rotary embeddings (applyRoPE, transformer.go:212-236): the pair (i, i+hd/2)
+// of head h of the token at position t = row % T turns by the float32 angle
+// tables (cos, sin)[t][i] built on the host as the reference computes them;
+// products and sums are rounded one by one as in the reference (no fused
+// multiply-add).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_kernel(float *__restrict__ x, const float *__restrict__ cs,
+                                                   const float *__restrict__ sn, int64_t total,
+                                                   int T, int NH, int hd, int conj) {
+  const int half = hd >> 1;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / (NH * half);
+    const int rem = (int)(e - r * (NH * half)), h = rem / half, i = rem - h * half;
+    const int t = (int)(r % T);
+    const float c = cs[t * half + i], s = conj ? -sn[t * half + i] : sn[t * half + i];
+    float *p = x + r * NH * hd + h * hd;
+    const float v1 = p[i], v2 = p[i + half];
+    p[i] = __fsub_rn(__fmul_rn(v1, c), __fmul_rn(v2, s));
+    p[i + half] = __fadd_rn(__fmul_rn(v1, s), __fmul_rn(v2, c));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm over rows of N (rmsnorm.go:222-240, 301-329), one wave64 per row:
 // rms = sqrt(sum x^2 / N + eps) rounded from float64, y = (x / rms) * gamma;
 // dx = (gamma / rms) (g - x sum(g gamma x) / (N rms rms)); gx = g (x / rms)
@@ -546,6 +570,17 @@ hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const
                          float *dx, float *gx, int rows, int N, hipStream_t s) {
   hipLaunchKernelGGL(ln_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, g, x, gam, stats, dx, gx,
                      rows, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope(float *x, const float *cs, const float *sn, int rows, int T, int NH, int hd,
+                       int conj, hipStream_t s) {
+  const int64_t total = (int64_t)rows * NH * (hd / 2);
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, cs, sn, total, T, NH, hd,
+                     conj);
   return hipGetLastError();
 }
 

@@ -69,6 +69,7 @@ __device__ __forceinline__ float apply_deriv(float out, int kind) {
     case D_SIGMOID: return out * (1.0f - out);
     case D_TANH: return 1.0f - out * out;
     case D_NAN: return __builtin_nanf("");
+    case D_GELU: return gelu_deriv(out);
     default: return 1.0f;
   }
 }

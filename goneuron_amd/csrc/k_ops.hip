@@ -185,6 +185,7 @@ __device__ __forceinline__ float deriv_of(float out, int kind) {
     case D_SIGMOID: return out * (1.0f - out);
     case D_TANH: return 1.0f - out * out;
     case D_NAN: return __builtin_nanf("");
+    case D_GELU: return gelu_deriv(out);
     default: return 1.0f;
   }
 }
@@ -439,14 +440,14 @@ __global__ __launch_bounds__(TPB) void swiglu_fwd_kernel(const float *__restrict
 }
 
 __global__ __launch_bounds__(TPB) void swiglu_bwd_kernel(const float *__restrict__ dy,
-                                                         const float *__restrict__ Z,
+                                                         const float *__restrict__ Z, int64_t ldz,
                                                          float *__restrict__ dZ, int64_t total,
                                                          int out) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / out;
     const int o = (int)(i - r * out);
-    const float g = Z[r * 2 * out + o], u = Z[r * 2 * out + out + o];
+    const float g = Z[r * ldz + o], u = Z[r * ldz + out + o];
     const float sig = swiglu_sig(g), swish = g * sig;
     dZ[r * 2 * out + out + o] = dy[i] * swish;
     const float dswish = swish + sig * (1.0f - swish);
@@ -463,14 +464,14 @@ hipError_t launch_swiglu_fwd(const float *Z, float *y, int B, int out, hipStream
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_bwd(const float *dy, const float *Z, float *dZ, int B, int out,
+hipError_t launch_swiglu_bwd(const float *dy, const float *Z, int ldz, float *dZ, int B, int out,
                              hipStream_t s) {
   const int64_t total = (int64_t)B * out;
   if (total <= 0) return hipSuccess;
   int64_t blocks = (total + TPB - 1) / TPB;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, dy, Z, dZ, total,
-                     out);
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, dy, Z, (int64_t)ldz,
+                     dZ, total, out);
   return hipGetLastError();
 }
 

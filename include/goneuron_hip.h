@@ -48,6 +48,7 @@ extern "C" {
 #define GN_ACT_SOFTMAX 4
 #define GN_ACT_LOGSOFTMAX 5
 #define GN_ACT_LINEAR 6
+#define GN_ACT_GELU 7   /* value activations.GELU{}: identity forward, GELU' backward */
 
 /* ---- layer kinds (the []layer.Layer given to goneuron.NewSequential) ----- */
 #define GN_LAYER_DENSE 1         /* layer.NewDense            layer.go:267 */
@@ -63,6 +64,13 @@ extern "C" {
 #define GN_LAYER_AVGPOOL2D 11    /* layer.NewAvgPool2D        avgpool2d.go:50 */
 #define GN_LAYER_RMSNORM 12      /* layer.NewRMSNorm          rmsnorm.go:49 */
 #define GN_LAYER_SWIGLU 13       /* layer.NewSwiGLU           swiglu.go:47 */
+
+/* TransformerBlockExt options (layer.ActivationType, layer.NormType) */
+#define GN_BLOCK_ACT_RELU 0
+#define GN_BLOCK_ACT_SWIGLU 1
+#define GN_BLOCK_ACT_GELU 2
+#define GN_BLOCK_NORM_LN 0
+#define GN_BLOCK_NORM_RMS 1
 
 #define GN_LOSS_MSE 1            /* loss.MSE          loss.go:38-105 */
 #define GN_LOSS_CE 2             /* loss.CrossEntropy loss.go:108-178 */
@@ -80,6 +88,9 @@ typedef struct gn_layer_desc {
   int32_t seq_len, num_heads, ff_dim, causal, vocab, dim; /* RMSNorm: dim = normalizedShape */
   int32_t return_sequences;
   float eps;            /* RMSNorm eps; 0 selects the facade's 1e-5 (goneuron.go:234) */
+  int32_t block_act;    /* TransformerBlock ff1: GN_BLOCK_ACT_* (transformer.go:199-203) */
+  int32_t block_norm;   /* TransformerBlock norms: GN_BLOCK_NORM_* (transformer.go:205-210) */
+  int32_t use_rope;     /* TransformerBlock: rotary embeddings on Q and K (transformer.go:212-236) */
 } gn_layer_desc;
 
 typedef struct gn_adam_desc {   /* opt.NewAdam opt.go:117-126 */

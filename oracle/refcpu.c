@@ -65,6 +65,12 @@ float gno_activate(int32_t act, float x) {
     case GNO_ACT_SOFTMAX:                                 /* :150-152 */
     case GNO_ACT_LOGSOFTMAX: return NAN;                  /* :192-194 */
     case GNO_ACT_LINEAR: return x;                        /* :345-347 */
+    case GNO_ACT_GELU: {                                  /* :244-254 */
+      float x3 = x * x * x;
+      float arg = (float)0.7978845608028654 * (x + 0.044715f * x3);
+      float tv = (float)tanh((double)arg);
+      return 0.5f * x * (1 + tv);
+    }
     default: return NAN;
   }
 }
@@ -83,6 +89,15 @@ float gno_derivative(int32_t act, float x) {
     case GNO_ACT_SOFTMAX:
     case GNO_ACT_LOGSOFTMAX: return NAN;                  /* :156-158, :198-200 */
     case GNO_ACT_LINEAR: return 1.0f;                     /* :350-352 */
+    case GNO_ACT_GELU: {                                  /* :258-272, in float64 */
+      double xd = (double)x, x2 = xd * xd, x3 = xd * x2;
+      double arg = 0.7978845608028654 * (xd + 0.044715 * x3);
+      double tv = tanh(arg);
+      double t1 = 0.5 * (1.0 + tv);
+      /* 3.0*c folds to the exact constant 0.134145 in Go */
+      double t2 = 0.5 * xd * (1.0 - tv * tv) * 0.7978845608028654 * (1.0 + 0.134145 * x2);
+      return (float)(t1 + t2);
+    }
     default: return NAN;
   }
 }
@@ -109,7 +124,7 @@ void gno_activate_batch(int32_t act, float *x, int32_t n) {
 
 /* cacheActivationType layer.go:183-205: pointer-only cases for Softmax and
  * LogSoftmax; everything else not listed is ActTypeNone. */
-enum { AT_NONE = 0, AT_RELU, AT_SIGMOID, AT_TANH, AT_SOFTMAX, AT_LOGSOFTMAX };
+enum { AT_NONE = 0, AT_RELU, AT_SIGMOID, AT_TANH, AT_SOFTMAX, AT_LOGSOFTMAX, AT_GELU };
 static int cache_act_type(int32_t act, int32_t is_ptr) {
   switch (act) {
     case GNO_ACT_RELU: return AT_RELU;
@@ -117,6 +132,7 @@ static int cache_act_type(int32_t act, int32_t is_ptr) {
     case GNO_ACT_TANH: return AT_TANH;
     case GNO_ACT_SOFTMAX: return is_ptr ? AT_SOFTMAX : AT_NONE;
     case GNO_ACT_LOGSOFTMAX: return is_ptr ? AT_LOGSOFTMAX : AT_NONE;
+    case GNO_ACT_GELU: return is_ptr ? AT_GELU : AT_NONE; /* only *activations.GELU */
     default: return AT_NONE;
   }
 }
@@ -221,7 +237,8 @@ struct layer {
   int32_t V, D, NH, FF;
   int32_t *ids;
   struct layer *sub;       /* block: wQ, wK, wV, wOut, ff1, ff2 (Dense) */
-  struct lnorm *ln;        /* block: norm1, norm2 */
+  struct lnorm *ln;        /* block: norm1, norm2 (LayerNorm) */
+  struct layer *rn;        /* block: norm1, norm2 (RMSNorm) */
   float *aq, *ak, *av, *scores, *fin, *gfin, *gq, *gk, *gv, *attOut, *res1, *n1, *ffOut, *res2,
       *blkOut, *gRes2, *gN1ff, *comb, *gRes1, *gInAtt, *tmpRow, *probs, *dpre;
 };
@@ -807,10 +824,15 @@ static const float *swiglu_forward(layer *L, const float *x) {
     float g = L->preActBuf[o];
     L->outputBuf[o] = (g * swiglu_sig(g)) * L->preActBuf[out + o];
   }
+  L->timeStep = 1; /* arena-less: savedInputOffsets = [0] (swiglu.go:126-133) */
   return L->outputBuf;
 }
 static const float *swiglu_backward(layer *L, const float *grad) {
   int32_t in = L->spec.in_size, out = L->spec.out_size;
+  /* swiglu.go:175-179, 228-230: one saved entry per Forward, popped here; a
+   * second Backward after one Forward returns nil */
+  if (L->timeStep == 0) return NULL;
+  L->timeStep = 0;
   const float *w = L->params, *v = L->params + (int64_t)in * out;
   float *gw = L->grads, *gv = L->grads + (int64_t)in * out;
   const float *x = L->inputBuf;
@@ -1215,6 +1237,19 @@ static void dense_sub_build(layer *S, int32_t in, int32_t out, int32_t act) {
   dense_build(S);
 }
 
+/* NewTransformerBlockExtE transformer.go:908-960: norms are LayerNorm or
+ * RMSNorm(dim, 1e-5); ff1 is Dense(dim, ff, ReLU{}), Dense(dim, ff, GELU{})
+ * (a value: ActTypeNone, identity forward and GELU' backward, layer.go:183-205)
+ * or SwiGLU(dim, ff); ff2 is Dense(ff, dim, Linear{}). */
+enum { TB_ACT_RELU = 0, TB_ACT_SWIGLU = 1, TB_ACT_GELU = 2 };
+enum { TB_NORM_LN = 0, TB_NORM_RMS = 1 };
+static int64_t tb_norm_size(const layer *L) {
+  return L->spec.block_norm == TB_NORM_RMS ? L->D : 2 * (int64_t)L->D;
+}
+static int64_t tb_ff1_size(const layer *L) {
+  int64_t d = L->D, ff = L->FF;
+  return L->spec.block_act == TB_ACT_SWIGLU ? 2 * d * ff : ff * d + ff;
+}
 static void tb_build(layer *L) {
   int32_t d = L->spec.dim, T = L->spec.seq_len, ff = L->spec.ff_dim;
   L->D = d;
@@ -1223,13 +1258,31 @@ static void tb_build(layer *L) {
   L->FF = ff;
   L->sub = (layer *)calloc(6, sizeof(layer));
   for (int i = 0; i < 4; i++) dense_sub_build(&L->sub[i], d, d, GNO_ACT_LINEAR);
-  dense_sub_build(&L->sub[4], d, ff, GNO_ACT_RELU);
+  if (L->spec.block_act == TB_ACT_SWIGLU) {
+    layer *S = &L->sub[4];
+    S->kind = S->spec.kind = GNO_LAYER_SWIGLU;
+    S->spec.in_size = d;
+    S->spec.out_size = ff;
+    S->training = 1;
+    swiglu_build(S);
+  } else {
+    dense_sub_build(&L->sub[4], d, ff, L->spec.block_act == TB_ACT_GELU ? GNO_ACT_GELU : GNO_ACT_RELU);
+  }
   dense_sub_build(&L->sub[5], ff, d, GNO_ACT_LINEAR);
-  L->ln = (lnorm *)calloc(2, sizeof(lnorm));
-  ln_build(&L->ln[0], d, T);
-  ln_build(&L->ln[1], d, T);
+  if (L->spec.block_norm == TB_NORM_RMS) {
+    L->rn = (layer *)calloc(2, sizeof(layer));
+    for (int i = 0; i < 2; i++) {
+      L->rn[i].kind = L->rn[i].spec.kind = GNO_LAYER_RMSNORM;
+      L->rn[i].spec.dim = d;
+      rms_build(&L->rn[i]);
+    }
+  } else {
+    L->ln = (lnorm *)calloc(2, sizeof(lnorm));
+    ln_build(&L->ln[0], d, T);
+    ln_build(&L->ln[1], d, T);
+  }
   int64_t nd = (int64_t)d * d + d;
-  L->nparams = 4 * nd + 4 * (int64_t)d + ((int64_t)ff * d + ff) + ((int64_t)d * ff + d);
+  L->nparams = 4 * nd + 2 * tb_norm_size(L) + tb_ff1_size(L) + ((int64_t)d * ff + d);
   int64_t td = (int64_t)T * d;
   L->aq = zalloc(td); L->ak = zalloc(td); L->av = zalloc(td); L->scores = zalloc((int64_t)T * T);
   L->fin = zalloc(td); L->gfin = zalloc(td); L->gq = zalloc(td); L->gk = zalloc(td); L->gv = zalloc(td);
@@ -1250,15 +1303,21 @@ static void tb_bind(layer *L) {
     off += nd;
   }
   for (int i = 0; i < 2; i++) {
-    L->ln[i].gamma = L->params + off;
-    L->ln[i].beta = L->params + off + d;
-    L->ln[i].ggamma = L->grads + off;
-    L->ln[i].gbeta = L->grads + off + d;
-    off += 2 * d;
+    if (L->rn) {
+      L->rn[i].params = L->params + off;
+      L->rn[i].grads = L->grads + off;
+    } else {
+      L->ln[i].gamma = L->params + off;
+      L->ln[i].beta = L->params + off + d;
+      L->ln[i].ggamma = L->grads + off;
+      L->ln[i].gbeta = L->grads + off + d;
+    }
+    off += tb_norm_size(L);
   }
   L->sub[4].params = L->params + off;
   L->sub[4].grads = L->grads + off;
-  off += (int64_t)ff * d + ff;
+  off += tb_ff1_size(L);
+  (void)ff;
   L->sub[5].params = L->params + off;
   L->sub[5].grads = L->grads + off;
 }
@@ -1269,6 +1328,28 @@ static void tb_init(layer *L) {
   for (int64_t i = 0; i < L->nparams; i++) L->params[i] = 0.0f;
 }
 
+/* applyRoPE transformer.go:212-236: rotate the pairs (i, i + hd/2) of every
+ * head of token t by t * 10000^(-2i/hd); conjugate (the backward) turns the
+ * other way. */
+static void rope_apply(float *x, int32_t T, int32_t nh, int32_t hd, int conj) {
+  for (int32_t t = 0; t < T; t++)
+    for (int32_t h = 0; h < nh; h++)
+      for (int32_t i = 0; i < hd / 2; i++) {
+        float theta = (float)pow(10000.0, -(double)(2 * i) / (double)hd);
+        float mTheta = (float)t * theta;
+        float c = (float)cos((double)mTheta), sn = (float)sin((double)mTheta);
+        if (conj) sn = -sn;
+        int64_t i1 = (int64_t)t * nh * hd + h * hd + i, i2 = i1 + hd / 2;
+        float v1 = x[i1], v2 = x[i2];
+        x[i1] = v1 * c - v2 * sn;
+        x[i2] = v1 * sn + v2 * c;
+      }
+}
+
+void gno_rope(float *x, int32_t T, int32_t nh, int32_t hd, int32_t conj) {
+  rope_apply(x, T, nh, hd, conj);
+}
+
 /* MultiHeadAttention.ForwardWithArena (arena-less) transformer.go:405-527 */
 static const float *mha_forward(layer *L, const float *x) {
   int32_t T = L->T, d = L->D, nh = L->NH, hd = d / nh;
@@ -1276,6 +1357,10 @@ static const float *mha_forward(layer *L, const float *x) {
     memcpy(L->aq + (int64_t)t * d, dense_forward(&L->sub[0], x + (int64_t)t * d), sizeof(float) * d);
     memcpy(L->ak + (int64_t)t * d, dense_forward(&L->sub[1], x + (int64_t)t * d), sizeof(float) * d);
     memcpy(L->av + (int64_t)t * d, dense_forward(&L->sub[2], x + (int64_t)t * d), sizeof(float) * d);
+  }
+  if (L->spec.use_rope) { /* transformer.go:457-461 */
+    rope_apply(L->aq, T, nh, hd, 0);
+    rope_apply(L->ak, T, nh, hd, 0);
   }
   float scale = (float)sqrt((double)hd);
   for (int32_t h = 0; h < nh; h++) {
@@ -1350,6 +1435,10 @@ static const float *mha_backward(layer *L, const float *g) {
         for (int32_t e = 0; e < hd; e++) L->gv[j * d + h * hd + e] += sc * L->gfin[i * d + h * hd + e];
       }
     }
+  if (L->spec.use_rope) { /* transformer.go:660-664 */
+    rope_apply(L->gq, T, nh, hd, 1);
+    rope_apply(L->gk, T, nh, hd, 1);
+  }
   for (int32_t t = 0; t < T; t++) {
     const float *dq = dense_backward(&L->sub[0], L->gq + (int64_t)t * d);
     float tq[4096], tk[4096];
@@ -1363,19 +1452,26 @@ static const float *mha_backward(layer *L, const float *g) {
 }
 
 /* TransformerBlock.ForwardWithArena (arena-less) transformer.go:1080-1184 */
+static const float *tb_norm_forward(layer *L, int k, const float *x) {
+  return L->rn ? rms_forward(&L->rn[k], x, L->T * L->D) : ln_forward(&L->ln[k], x);
+}
+static const float *tb_norm_backward(layer *L, int k, const float *g) {
+  return L->rn ? rms_backward(&L->rn[k], g) : ln_backward(&L->ln[k], g);
+}
 static const float *tb_forward(layer *L, const float *x) {
   int32_t T = L->T, d = L->D;
   int64_t td = (int64_t)T * d;
   const float *att = mha_forward(L, x);
   for (int64_t i = 0; i < td; i++) L->res1[i] = x[i] + att[i];
-  memcpy(L->n1, ln_forward(&L->ln[0], L->res1), sizeof(float) * td);
+  memcpy(L->n1, tb_norm_forward(L, 0, L->res1), sizeof(float) * td);
   for (int32_t s = 0; s < T; s++) {
-    const float *mid = dense_forward(&L->sub[4], L->n1 + (int64_t)s * d);
+    const float *mid = L->sub[4].kind == GNO_LAYER_SWIGLU ? swiglu_forward(&L->sub[4], L->n1 + (int64_t)s * d)
+                                                         : dense_forward(&L->sub[4], L->n1 + (int64_t)s * d);
     const float *fo = dense_forward(&L->sub[5], mid);
     memcpy(L->ffOut + (int64_t)s * d, fo, sizeof(float) * d);
   }
   for (int64_t i = 0; i < td; i++) L->res2[i] = L->n1[i] + L->ffOut[i];
-  memcpy(L->blkOut, ln_forward(&L->ln[1], L->res2), sizeof(float) * td);
+  memcpy(L->blkOut, tb_norm_forward(L, 1, L->res2), sizeof(float) * td);
   return L->blkOut;
 }
 
@@ -1383,14 +1479,16 @@ static const float *tb_forward(layer *L, const float *x) {
 static const float *tb_backward(layer *L, const float *g) {
   int32_t T = L->T, d = L->D;
   int64_t td = (int64_t)T * d;
-  memcpy(L->gRes2, ln_backward(&L->ln[1], g), sizeof(float) * td);
+  memcpy(L->gRes2, tb_norm_backward(L, 1, g), sizeof(float) * td);
   for (int32_t s = 0; s < T; s++) {
     const float *mg = dense_backward(&L->sub[5], L->gRes2 + (int64_t)s * d);
-    const float *g1 = dense_backward(&L->sub[4], mg);
-    memcpy(L->gN1ff + (int64_t)s * d, g1, sizeof(float) * d);
+    const float *g1 = L->sub[4].kind == GNO_LAYER_SWIGLU ? swiglu_backward(&L->sub[4], mg)
+                                                        : dense_backward(&L->sub[4], mg);
+    /* a nil slice copies nothing: the token keeps what the buffer held */
+    if (g1) memcpy(L->gN1ff + (int64_t)s * d, g1, sizeof(float) * d);
   }
   for (int64_t i = 0; i < td; i++) L->comb[i] = L->gRes2[i] + L->gN1ff[i];
-  memcpy(L->gRes1, ln_backward(&L->ln[0], L->comb), sizeof(float) * td);
+  memcpy(L->gRes1, tb_norm_backward(L, 0, L->comb), sizeof(float) * td);
   const float *ga = mha_backward(L, L->gRes1);
   for (int64_t i = 0; i < td; i++) L->gInAtt[i] = L->gRes1[i] + ga[i];
   return L->gInAtt;
@@ -1404,9 +1502,18 @@ static void tb_free(layer *L) {
     free(S->gradInBuf); free(S->dzBuf);
   }
   free(L->sub);
-  ln_free(&L->ln[0]);
-  ln_free(&L->ln[1]);
-  free(L->ln);
+  if (L->ln) {
+    ln_free(&L->ln[0]);
+    ln_free(&L->ln[1]);
+    free(L->ln);
+  }
+  if (L->rn) {
+    for (int i = 0; i < 2; i++) {
+      free(L->rn[i].outputBuf); free(L->rn[i].savedInput); free(L->rn[i].gradInBuf);
+      free(L->rn[i].tmpRow);
+    }
+    free(L->rn);
+  }
   float *bufs[] = {L->aq, L->ak, L->av, L->scores, L->fin, L->gfin, L->gq, L->gk, L->gv, L->attOut,
                    L->res1, L->n1, L->ffOut, L->res2, L->blkOut, L->gRes2, L->gN1ff, L->comb,
                    L->gRes1, L->gInAtt, L->tmpRow, L->probs, L->dpre};
@@ -1454,6 +1561,9 @@ static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_MAXPOOL2D) { L->inH = L->inW = 0; }                      /* maxpool2d.go:508-513 */
   if (L->kind == GNO_LAYER_AVGPOOL2D) { L->inH = L->inW = 0; }                      /* avgpool2d.go:560-565 */
   if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_reset(L);                             /* unroller.go:268 */
+  if (L->kind == GNO_LAYER_SWIGLU) L->timeStep = 0;                                  /* swiglu.go:362-366 */
+  if (L->kind == GNO_LAYER_TRANSFORMER && L->sub[4].kind == GNO_LAYER_SWIGLU)
+    L->sub[4].timeStep = 0;                                                          /* Reset of ff1 */
 }
 /* *len_io: input length in, output length out */
 static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {

@@ -52,6 +52,7 @@ enum {
   GNO_ACT_SOFTMAX = 4,
   GNO_ACT_LOGSOFTMAX = 5,
   GNO_ACT_LINEAR = 6,
+  GNO_ACT_GELU = 7,
 };
 
 enum {
@@ -85,6 +86,9 @@ typedef struct gno_layer_spec {
   int32_t seq_len, num_heads, ff_dim, causal, vocab, dim; /* RMSNorm: dim = normalizedShape */
   int32_t return_sequences;
   float eps;            /* RMSNorm eps (0 = 1e-5) */
+  int32_t block_act;    /* TransformerBlock ff1: 0 ReLU, 1 SwiGLU, 2 GELU (transformer.go:199-203) */
+  int32_t block_norm;   /* TransformerBlock norms: 0 LayerNorm, 1 RMSNorm (transformer.go:205-210) */
+  int32_t use_rope;     /* TransformerBlock attention: rotary embeddings on Q and K */
 } gno_layer_spec;
 
 typedef struct gno_net gno_net;
@@ -147,6 +151,8 @@ int32_t gno_rmsnorm(const float *x, int32_t total, int32_t n, float eps, const f
  * gin and gparams also the backward (gparams accumulates). */
 void gno_swiglu(const float *x, int32_t in, int32_t out, const float *params, float *y,
                 const float *g, float *gin, float *gparams);
+/* applyRoPE over T tokens of nh heads of hd, in place (conj: the inverse). */
+void gno_rope(float *x, int32_t T, int32_t nh, int32_t hd, int32_t conj);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

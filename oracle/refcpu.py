@@ -18,7 +18,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 
-ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR = range(7)
+ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU = range(8)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
  LAYER_RMSNORM, LAYER_SWIGLU) = range(1, 14)
@@ -35,6 +35,7 @@ class LayerSpec(C.Structure):
         ("seq_len", C.c_int32), ("num_heads", C.c_int32), ("ff_dim", C.c_int32),
         ("causal", C.c_int32), ("vocab", C.c_int32), ("dim", C.c_int32),
         ("return_sequences", C.c_int32), ("eps", C.c_float),
+        ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
     ]
 
 
@@ -105,6 +106,7 @@ def lib():
                                   f32p]
         L.gno_rmsnorm.restype = C.c_int32
         L.gno_swiglu.argtypes = [f32p, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p, f32p]
+        L.gno_rope.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32]
         _lib = L
     return _lib
 
@@ -273,6 +275,13 @@ def swiglu(x, out, params, g=None):
     gp = np.zeros(params.size, np.float32)
     lib().gno_swiglu(fptr(x), x.size, out, fptr(params), fptr(y), fptr(g), fptr(gin), fptr(gp))
     return y, gin, gp
+
+
+def rope(x, T, nh, hd, conj=False):
+    """applyRoPE of x ([T, nh*hd] row major) into a new array."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().gno_rope(fptr(y), T, nh, hd, int(conj))
+    return y
 
 
 def matmul(x, w, b):

@@ -2,7 +2,7 @@
 (goneuron_amd.configs) and compare tensors by the BASELINE tolerances."""
 import numpy as np
 
-ACT = {"relu": 1, "sigmoid": 2, "tanh": 3, "softmax": 4, "logsoftmax": 5, "linear": 6}
+ACT = {"relu": 1, "sigmoid": 2, "tanh": 3, "softmax": 4, "logsoftmax": 5, "linear": 6, "gelu": 7}
 
 
 def oracle_specs(refcpu, cfg):
@@ -38,7 +38,10 @@ def oracle_specs(refcpu, cfg):
             specs.append(refcpu.spec(refcpu.LAYER_POSENC, seq_len=d["T"], dim=d["dim"]))
         elif k == "transformer":
             specs.append(refcpu.spec(refcpu.LAYER_TRANSFORMER, dim=d["dim"], num_heads=d["heads"],
-                                     seq_len=d["T"], ff_dim=d["ff"], causal=int(d["causal"])))
+                                     seq_len=d["T"], ff_dim=d["ff"], causal=int(d["causal"]),
+                                     block_act={"relu": 0, "swiglu": 1, "gelu": 2}[d.get("act", "relu")],
+                                     block_norm={"ln": 0, "rms": 1}[d.get("norm", "ln")],
+                                     use_rope=int(bool(d.get("rope", False)))))
         elif k == "clspool":
             specs.append(refcpu.spec(refcpu.LAYER_CLSPOOL, seq_len=d["T"], dim=d["dim"]))
         elif k == "lstm":

@@ -435,18 +435,19 @@ def test_lstm_coop_timeout_is_reported(gn):
 def _random_block(cfg, scale=0.2, seed=21):
     """Non-zero TransformerBlock weights (the reference starts it at 0, Q11),
     so attention, LayerNorm and the FF path carry gradient."""
-    from goneuron_amd import configs
     d = cfg["layers"][2]
     D, FF, T, V = d["dim"], d["ff"], d["T"], cfg["classes"]
     start = V * D + T * D
-    n = 4 * (D * D + D) + 4 * D + (FF * D + FF) + (D * FF + D)
+    nn = D if d.get("norm", "ln") == "rms" else 2 * D
+    n1 = 2 * FF * D if d.get("act", "relu") == "swiglu" else FF * D + FF
+    n = 4 * (D * D + D) + 2 * nn + n1 + (D * FF + D)
 
     def f(p):
         rng = np.random.default_rng(seed)
         p[start:start + n] = (rng.normal(size=n) * scale).astype(np.float32)
         g1 = start + 4 * (D * D + D)
-        p[g1:g1 + D] += 1.0          # LayerNorm gammas around 1
-        p[g1 + 2 * D:g1 + 3 * D] += 1.0
+        p[g1:g1 + D] += 1.0          # norm gammas around 1
+        p[g1 + nn:g1 + nn + D] += 1.0
         return p
     return f
 
@@ -465,6 +466,40 @@ def test_gpt_attention_shapes(gn, oracle, T, dim, heads, causal):
     from goneuron_amd import configs
     cfg = configs.gpt(B=3, T=T, vocab=29, dim=dim, heads=heads, ff=24, causal=causal)
     _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg))
+
+
+@pytest.mark.parametrize("act,norm,rope,causal,workers", [
+    ("relu", "rms", True, False, 1), ("gelu", "ln", True, False, 2), ("gelu", "rms", False, True, 1),
+    ("swiglu", "rms", True, False, 1), ("swiglu", "ln", False, True, 2)])
+def test_gpt_block_ext(gn, oracle, act, norm, rope, causal, workers):
+    """TransformerBlockExt (transformer.go:908-960): RMSNorm norms (Q19),
+    GELU feed-forward (value activation: identity forward, GELU' from the last
+    token's pre-activation), SwiGLU feed-forward (token 0's gradient only,
+    from the last token's saved state) and rotary Q/K, with a random block;
+    2 steps."""
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=5, T=12, vocab=37, dim=32, heads=4, ff=48, act=act, norm=norm, rope=rope,
+                      causal=causal)
+    _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
+
+
+def test_gpt_block_ext_c4_size(gn, oracle):
+    """The reference's TransformerBlockExt test combination (SwiGLU, RMSNorm,
+    RoPE; goneuron_test.go:471-477) at C4's size: D 256, 8 heads, ff 1024,
+    T 128, B 32, causal."""
+    from goneuron_amd import configs
+    cfg = configs.gpt(act="swiglu", norm="rms", rope=True)
+    _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg, scale=0.05))
+
+
+def test_dense_gelu_value_activation(gn, oracle):
+    """Dense(.., GELU{}) with the value activation: ActTypeNone (layer.go:183-205)
+    runs the identity forward and GELU'(pre-activation) backward."""
+    cfg = dict(num=14, name="dense_gelu", B=40, loss="ce", lr=1e-3, x="normal", in_len=24, classes=6,
+               layers=[{"kind": "dense", "in": 24, "out": 40, "act": "gelu", "ptr": False},
+                       {"kind": "dense", "in": 40, "out": 32, "act": "gelu", "ptr": False},
+                       {"kind": "dense", "in": 32, "out": 6, "act": "softmax", "ptr": True}])
+    _compare_step(gn, oracle, cfg, steps=2)
 
 
 def test_gpt_small_reference_init(gn, oracle):

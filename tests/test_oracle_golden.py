@@ -305,6 +305,43 @@ def test_swiglu_gradients_by_finite_differences(oracle):
     np.testing.assert_allclose(gp, num_p, rtol=1e-4, atol=1e-5)
 
 
+def test_gelu_known_answers(oracle):
+    """activations_pytorch_test.go:151-204 (tanh-form GELU and its float64
+    derivative, 1e-6)."""
+    act = [(-2.0, -0.04540230591), (-1.0, -0.15880800939), (-0.5, -0.15428599017), (0.0, 0.0),
+           (0.5, 0.34571400982), (1.0, 0.84119199060), (2.0, 1.95459769408)]
+    der = [(-2.0, -0.08609925685), (-1.0, -0.08296408407), (-0.5, 0.13263009635), (0.0, 0.5),
+           (0.5, 0.86736990312), (1.0, 1.08296408396), (2.0, 1.08609925608)]
+    for x, e in act:
+        assert abs(oracle.lib().gno_activate(oracle.ACT_GELU, x) - e) <= 1e-6, x
+    for x, e in der:
+        assert abs(oracle.lib().gno_derivative(oracle.ACT_GELU, x) - e) <= 1e-6, x
+
+
+def test_rope_known_answers_and_inverse(oracle):
+    """rope_test.go:8-49 (t = 0 is the identity; t = 1, i = 0 rotates (x4, x6)
+    by 1 rad), :51-75 (conjugate undoes the rotation, 1e-3); every pair keeps
+    its length and the angle t * 10000^(-2i/hd) is the float64 rotation's."""
+    x = np.array([1, 2, 3, 4, 1, 2, 3, 4], np.float32)
+    y = oracle.rope(x, 2, 1, 4)
+    np.testing.assert_array_equal(y[:4], x[:4])
+    c0, s0 = np.float32(math.cos(1.0)), np.float32(math.sin(1.0))
+    assert abs(y[4] - (1 * c0 - 3 * s0)) <= 1e-5 and abs(y[6] - (1 * s0 + 3 * c0)) <= 1e-5
+    x = np.arange(10 * 4 * 32, dtype=np.float32)
+    back = oracle.rope(oracle.rope(x, 10, 4, 32), 10, 4, 32, conj=True)
+    np.testing.assert_allclose(back, x, atol=1e-3)
+    rng = np.random.default_rng(4)
+    T, nh, hd = 7, 3, 10
+    x = rng.normal(size=T * nh * hd).astype(np.float32)
+    y = oracle.rope(x, T, nh, hd)
+    xr, yr = x.reshape(T, nh, hd).astype(np.float64), y.reshape(T, nh, hd).astype(np.float64)
+    ang = np.array([[t * 10000.0 ** (-2 * i / hd) for i in range(hd // 2)] for t in range(T)])
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    a, b = xr[:, :, :hd // 2], xr[:, :, hd // 2:]
+    np.testing.assert_allclose(yr[:, :, :hd // 2], a * c - b * s, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(yr[:, :, hd // 2:], a * s + b * c, rtol=1e-5, atol=1e-5)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
@@ -653,18 +690,22 @@ def _gpt_small(B=3, T=6, V=11, D=8, NH=2, FF=12):
     return configs.gpt(B=B, T=T, vocab=V, dim=D, heads=NH, ff=FF)
 
 
-def _block_slices(D, FF):
+def _block_slices(D, FF, act="relu", norm="ln"):
+    """(start, split, end) of each block part: W then b; LayerNorm gamma then
+    beta; RMSNorm gamma only (split = end); SwiGLU W then V."""
     nd = D * D + D
     off = 0
     out = {}
     for name in ("wq", "wk", "wv", "wo"):
         out[name] = (off, off + D * D, off + nd)
         off += nd
+    nn = D if norm == "rms" else 2 * D
     for name in ("ln1", "ln2"):
-        out[name] = (off, off + D, off + 2 * D)
-        off += 2 * D
-    out["ff1"] = (off, off + FF * D, off + FF * D + FF)
-    off += FF * D + FF
+        out[name] = (off, off + D, off + nn)
+        off += nn
+    n1 = 2 * FF * D if act == "swiglu" else FF * D + FF
+    out["ff1"] = (off, off + FF * D, off + n1)
+    off += n1
     out["ff2"] = (off, off + D * FF, off + D * FF + D)
     off += D * FF + D
     return out, off
@@ -718,7 +759,9 @@ def _torch_gpt_grads(torch, cfg, p0, x, y):
     per-token quirks."""
     B, T = x.shape
     V, D = cfg["classes"], cfg["layers"][0]["dim"]
-    NH, FF = cfg["layers"][2]["heads"], cfg["layers"][2]["ff"]
+    blk = cfg["layers"][2]
+    NH, FF = blk["heads"], blk["ff"]
+    act, norm, rope = blk.get("act", "relu"), blk.get("norm", "ln"), blk.get("rope", False)
     hd = D // NH
 
     class PTDense(torch.autograd.Function):   # Q10: dW from the last token's input
@@ -765,11 +808,85 @@ def _torch_gpt_grads(torch, cfg, p0, x, y):
             dx = (gp - gp.sum(1, keepdim=True) / N) / std - diff * (gp * diff).sum(1, keepdim=True) / (N * std * std)
             return dx, (g * diff / std).sum(0), g.sum(0)
 
+    class QRMSNorm(torch.autograd.Function):
+        """Q19: RMSNorm.Backward (rmsnorm.go:309-316) scales the projection
+        term by gamma too: dx = gamma/r (g - x sum(g gamma x) / (N r^2))."""
+        @staticmethod
+        def forward(ctx, xx, gam):
+            r = torch.sqrt((xx * xx).mean(1, keepdim=True) + 1e-5)
+            ctx.save_for_backward(xx, r, gam)
+            return xx / r * gam
+
+        @staticmethod
+        def backward(ctx, g):
+            xx, r, gam = ctx.saved_tensors
+            N = xx.shape[1]
+            S = (g * gam * xx).sum(1, keepdim=True)
+            return gam / r * (g - xx * S / (N * r * r)), (g * xx / r).sum(0)
+
+    class QGELU(torch.autograd.Function):
+        """Dense(dim, ff, GELU{}) with a value activation: identity forward
+        (ActTypeNone, layer.go:183-205), GELU'(pre-activation) backward from
+        the last token's saved pre-activation (Q10)."""
+        @staticmethod
+        def forward(ctx, z):
+            ctx.save_for_backward(z)
+            return z.clone()
+
+        @staticmethod
+        def backward(ctx, g):
+            (z,) = ctx.saved_tensors
+            zz = z[-1]
+            c = 0.7978845608028654
+            tv = torch.tanh(c * (zz + 0.044715 * zz ** 3))
+            d = 0.5 * (1 + tv) + 0.5 * zz * (1 - tv * tv) * c * (1 + 3 * 0.044715 * zz ** 2)
+            return g * d
+
+    class QSwiGLU(torch.autograd.Function):
+        """SwiGLU called per token (swiglu.go): each Forward replaces the one
+        saved entry, so the first Backward (token 0) runs on the last token's
+        input, gate and up, and the later ones return nil (no gradient)."""
+        @staticmethod
+        def forward(ctx, xx, Wg, Vu):
+            ctx.save_for_backward(xx, Wg, Vu)
+            a, u = xx @ Wg.T, xx @ Vu.T
+            return a * torch.sigmoid(a) * u
+
+        @staticmethod
+        def backward(ctx, gm):
+            xx, Wg, Vu = ctx.saved_tensors
+            xl = xx[-1]
+            a, u = xl @ Wg.T, xl @ Vu.T
+            sig = torch.sigmoid(a)
+            sw = a * sig
+            d_up = gm[0] * sw
+            d_gate = gm[0] * (sw + sig * (1 - sw)) * u
+            dx = torch.zeros_like(xx)
+            dx[0] = d_gate @ Wg + d_up @ Vu
+            return dx, torch.outer(d_gate, xl), torch.outer(d_up, xl)
+
+    if rope:  # applyRoPE's float32 angles (transformer.go:215-221)
+        half = hd // 2
+        cs = np.zeros((T, half)); sn = np.zeros((T, half))
+        for t in range(T):
+            for i in range(half):
+                th = np.float32(math.pow(10000.0, -float(2 * i) / float(hd)))
+                m = np.float32(np.float32(t) * th)
+                cs[t, i] = np.float32(math.cos(float(m)))
+                sn[t, i] = np.float32(math.sin(float(m)))
+        cs_t, sn_t = torch.tensor(cs), torch.tensor(sn)
+
+    def rot(z):
+        zz = z.view(T, NH, hd)
+        a_, b_ = zz[:, :, :hd // 2], zz[:, :, hd // 2:]
+        c_, s_ = cs_t[:, None, :], sn_t[:, None, :]
+        return torch.cat([a_ * c_ - b_ * s_, a_ * s_ + b_ * c_], 2).reshape(T, NH * hd)
+
     P = torch.tensor(p0.astype(np.float64), requires_grad=True)
     nE, nP = V * D, T * D
     E = P[:nE].view(V, D)
     PE = P[nE:nE + nP].view(T, D)
-    sl, nb = _block_slices(D, FF)
+    sl, nb = _block_slices(D, FF, act, norm)
     b0 = nE + nP
 
     def W(name, rows, cols):
@@ -794,17 +911,33 @@ def _torch_gpt_grads(torch, cfg, p0, x, y):
         e_leaf = e.detach().requires_grad_(True)
         h = e_leaf + PE
         q, k, v = PTDense.apply(h, Wq, bq), PTDense.apply(h, Wk, bk), PTDense.apply(h, Wv, bv)
+        if rope:
+            q, k = rot(q), rot(k)
         outs = []
         for hh in range(NH):
             sl_ = slice(hh * hd, (hh + 1) * hd)
             s_ = (q[:, sl_] @ k[:, sl_].T) / math.sqrt(hd)
-            s_ = s_.masked_fill(mask, -1e9)
+            if blk["causal"]:
+                s_ = s_.masked_fill(mask, -1e9)
             outs.append(torch.softmax(s_, dim=1) @ v[:, sl_])
         att = PTDense.apply(torch.cat(outs, 1), Wo, bo)
-        n1 = QLayerNorm.apply(h + att, g1.view(D), be1)
-        mid = QReLU.apply(PTDense.apply(n1, W1, c1))
+        if norm == "rms":
+            n1 = QRMSNorm.apply(h + att, g1.view(D))
+        else:
+            n1 = QLayerNorm.apply(h + att, g1.view(D), be1)
+        if act == "swiglu":
+            a0, _, a1 = sl["ff1"]
+            mid = QSwiGLU.apply(n1, P[b0 + a0:b0 + a0 + FF * D].view(FF, D),
+                                P[b0 + a0 + FF * D:b0 + a1].view(FF, D))
+        elif act == "gelu":
+            mid = QGELU.apply(PTDense.apply(n1, W1, c1))
+        else:
+            mid = QReLU.apply(PTDense.apply(n1, W1, c1))
         ff = PTDense.apply(mid, W2, c2)
-        out = QLayerNorm.apply(n1 + ff, g2.view(D), be2)
+        if norm == "rms":
+            out = QRMSNorm.apply(n1 + ff, g2.view(D))
+        else:
+            out = QLayerNorm.apply(n1 + ff, g2.view(D), be2)
         logits = out[0] @ Wh.T + bh
         lp = torch.log_softmax(logits, 0)
         lp.backward((lp - torch.tensor(y[b].astype(np.float64))).detach() / B)
@@ -841,11 +974,22 @@ def test_layernorm_quirk_formula_vs_exact():
     assert not np.allclose(ref_formula.numpy(), exact.numpy())
 
 
-def test_gpt_grads_vs_torch_autograd(oracle):
+@pytest.mark.parametrize("act,norm,rope,causal", [("relu", "ln", False, True),
+                                                  ("relu", "ln", False, False),
+                                                  ("relu", "rms", True, False),
+                                                  ("gelu", "ln", True, False),
+                                                  ("swiglu", "rms", False, True),
+                                                  ("swiglu", "rms", True, False)])
+def test_gpt_grads_vs_torch_autograd(oracle, act, norm, rope, causal):
+    """The GPT step (C4 shape, small) against a float64 torch model whose
+    autograd covers attention, softmax, residuals and rotary embeddings, and
+    whose custom functions restate each reference quirk; with the
+    TransformerBlockExt variants (transformer.go:908-960)."""
     torch = pytest.importorskip("torch")
     from cfgutil import oracle_net, max_rel
     from goneuron_amd import configs
-    cfg = _gpt_small()
+    cfg = configs.gpt(B=3, T=6, vocab=11, dim=8, heads=2, ff=12, act=act, norm=norm, rope=rope,
+                      causal=causal)
     net = oracle_net(oracle, cfg)
     rng = np.random.default_rng(12)
     blk = net.layer_slice(2)
@@ -859,3 +1003,18 @@ def test_gpt_grads_vs_torch_autograd(oracle):
         s = net.layer_slice(i)
         if s.stop > s.start:
             assert max_rel(got[s], ref[s]) < 1e-5, (i, max_rel(got[s], ref[s]))
+    # each part of the block on its own scale.  With a causal mask the CLS
+    # token attends to itself only (no Q/K gradient); without RoPE the key
+    # gradients of each query row sum to zero over the keys, so Wk's Q10
+    # gradient (token sum times the last input) vanishes up to rounding.
+    b0 = net.layer_slice(2).start
+    for name, (a0, _, a1) in _block_slices(8, 12, act, norm)[0].items():
+        part = slice(b0 + a0, b0 + a1)
+        if causal and name in ("wq", "wk"):
+            assert not ref[part].any() and not got[part].any()
+            continue
+        if name == "wk" and not rope:
+            assert np.abs(ref[part]).max() < 1e-12 and np.abs(got[part]).max() < 1e-6
+            continue
+        assert np.abs(ref[part]).max() > 1e-3, name
+        assert max_rel(got[part], ref[part]) < 1e-5, (name, max_rel(got[part], ref[part]))
