@@ -22,7 +22,7 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "AvgPool2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock",
+    "AvgPool2D", "BatchNorm2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock",
     "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
     "LSTM", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
@@ -65,7 +65,7 @@ def Ref(act: Activation) -> Activation:
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU) = range(1, 14)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D) = range(1, 15)
 
 
 class Layer:
@@ -146,6 +146,21 @@ def AvgPool2D(kernel, stride, padding, *in_channels):
     each window (padding not counted)."""
     return Layer(LAYER_AVGPOOL2D, kernel=kernel, stride=stride, padding=padding,
                  in_channels=in_channels[0] if in_channels else -1)
+
+
+def BatchNorm2D(*in_channels, eps=1e-5, momentum=0.1, affine=True):
+    """goneuron.BatchNorm2D (goneuron.go:211-218): NewBatchNorm2D(in, 1e-5,
+    0.1, true).  Training normalises each sample's channel planes by their own
+    statistics (one sample per Forward) and advances the running mean / var
+    once per sample; inference uses the running statistics.  The lazy form is
+    rejected: BatchNorm2D.Build has no error return, so Sequential.Build
+    (sequential.go:68-73) never resolves it."""
+    if not in_channels or in_channels[0] <= 0:
+        raise GNError(-1, "BatchNorm2D needs the channel count (the lazy form is never built)")
+    if eps < 0 or not (0 <= momentum <= 1):
+        raise GNError(-1, f"invalid eps {eps} / momentum {momentum}")
+    return Layer(LAYER_BATCHNORM2D, in_channels=int(in_channels[0]), eps=float(eps) if eps > 0 else 0.0,
+                 momentum=float(momentum), no_affine=int(not affine))
 
 
 def RMSNorm(*normalized_shape, eps=1e-5):
@@ -426,6 +441,17 @@ class Sequential:
         out = np.empty(n, np.float32)
         self._ck(lib().gn_model_layer_output(self.h, i, _fp(out), n))
         return out
+
+    def RunningStats(self, i):
+        """BatchNorm2D.GetRunningMean / GetRunningVar (batchnorm2d.go:837-838)."""
+        n = self.layers[i].desc.in_channels
+        m, v = np.empty(n, np.float32), np.empty(n, np.float32)
+        self._ck(lib().gn_model_get_running_stats(self.h, i, _fp(m), _fp(v), n))
+        return m, v
+
+    def SetRunningStats(self, i, mean, var):
+        m, v = _f32(mean).ravel(), _f32(var).ravel()
+        self._ck(lib().gn_model_set_running_stats(self.h, i, _fp(m), _fp(v), m.size))
 
     def LayerArgmax(self, i, n):
         out = np.empty(n, np.int32)

@@ -35,6 +35,7 @@ class LayerDesc(C.Structure):
         ("causal", C.c_int32), ("vocab", C.c_int32), ("dim", C.c_int32),
         ("return_sequences", C.c_int32), ("eps", C.c_float),
         ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
+        ("momentum", C.c_float), ("no_affine", C.c_int32),
     ]
 
 
@@ -87,6 +88,8 @@ SIGNATURES = {
     "gn_model_set_training": (C.c_int, [vp, C.c_int32]),
     "gn_model_layer_output": (C.c_int, [vp, C.c_int32, f32p, C.c_int64]),
     "gn_model_layer_argmax": (C.c_int, [vp, C.c_int32, i32p, C.c_int64]),
+    "gn_model_get_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
+    "gn_model_set_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
     "gn_dense_forward": (C.c_int, [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32]),
     "gn_dense_backward": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int32, C.c_int32,

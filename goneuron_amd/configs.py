@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, RMSNorm,
+from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, BatchNorm2D, RMSNorm,
                SwiGLU, Flatten, TransformerBlockExt, ActReLU, ActSwiGLU, ActGELU, NormLN, NormRMS,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
@@ -112,6 +112,8 @@ def product_layers(cfg):
             out.append(AvgPool2D(d["k"], d["s"], d["p"], d["inC"]))
         elif k == "rmsnorm":
             out.append(RMSNorm(d["n"]))
+        elif k == "batchnorm2d":
+            out.append(BatchNorm2D(d["C"]))
         elif k == "swiglu":
             out.append(SwiGLU(d["out"], d["in"]))
         elif k == "embedding":

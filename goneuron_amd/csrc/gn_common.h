@@ -128,6 +128,13 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
                               int B, hipStream_t st);
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st);
+// BatchNorm2D: training forward (per-plane stats st = mean, var, std; running
+// stats updated in sample order) or inference forward; training backward with
+// per-plane gamma / beta partial sums part [2][B*C] (part may be null).
+hipError_t launch_bn_fwd(const float *x, const float *gb, float *y, float *st, float *rm, float *rv,
+                         int B, int C, int HW, float eps, float mom, int training, hipStream_t s);
+hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const float *st, float *dx,
+                         float *part, int B, int C, int HW, hipStream_t s);
 hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
 hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
 

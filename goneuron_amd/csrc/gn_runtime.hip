@@ -527,6 +527,10 @@ struct LayerRT {
   float eps = 0.f;
   // SwiGLU: projections Z = [gate | up] and their gradients, [maxB, 2*out] each
   float *zbuf = nullptr, *dzbuf = nullptr;
+  // BatchNorm2D: C channels of HW; per-plane (mean, var, std), gamma / beta
+  // partial sums [2][maxB*C], running mean / var [C]
+  int C = 0, HW = 0;
+  float *bnst = nullptr, *bnpart = nullptr, *rmean = nullptr, *rvar = nullptr;
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -835,6 +839,18 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.pcount = R.D;
         R.out_len = len;
         break;
+      case GN_LAYER_BATCHNORM2D:  // batchnorm2d.go:103-135: gamma 1, beta 0 when affine
+        R.C = R.d.in_channels;
+        if (R.C <= 0 || len % R.C)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: BatchNorm2D channels %d do not divide input %d", i,
+                         R.C, len);
+        if (!(R.d.eps >= 0) || !(R.d.momentum >= 0 && R.d.momentum <= 1))
+          return set_err(c, GN_ERR_INVALID, "layer %d: BatchNorm2D eps < 0 or momentum outside [0,1]", i);
+        R.HW = len / R.C;
+        R.eps = R.d.eps > 0 ? R.d.eps : 1e-5f;  // the facade's eps (goneuron.go:216)
+        R.pcount = R.d.no_affine ? 0 : 2 * (int64_t)R.C;
+        R.out_len = len;
+        break;
       case GN_LAYER_SWIGLU:  // swiglu.go:73-100: [W | V], each out x in, no biases
         if (R.d.in_size != len)
           return set_err(c, GN_ERR_SHAPE, "layer %d: SwiGLU in %d != incoming %d", i, R.d.in_size, len);
@@ -968,6 +984,18 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
+    }
+    if (R.d.kind == GN_LAYER_BATCHNORM2D) {
+      if (R.pcount) std::fill(host.begin() + R.poff, host.begin() + R.poff + R.C, 1.0f);
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.C * 3, &R.bnst))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.C * 2, &R.bnpart))) return rc;
+      if ((rc = model_alloc(M.get(), R.C, &R.rmean))) return rc;
+      if ((rc = model_alloc(M.get(), R.C, &R.rvar))) return rc;
+      std::vector<float> ones(R.C, 1.0f);
+      HIP_OK(c, hipMemsetAsync(R.rmean, 0, R.C * sizeof(float), c->stream));
+      HIP_OK(c, hipMemcpyAsync(R.rvar, ones.data(), R.C * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+      HIP_OK(c, hipStreamSynchronize(c->stream));  // `ones` goes out of scope
     }
     if (R.d.kind == GN_LAYER_SWIGLU) {
       init_swiglu(host.data() + R.poff, R.d.in_size, R.d.out_size);
@@ -1402,6 +1430,12 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, launch_swiglu_fwd(R.zbuf, R.out, B, R.d.out_size, c->stream));
         break;
       }
+      case GN_LAYER_BATCHNORM2D: {  // running stats advance in training mode only
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_bn_fwd(cur, R.pcount ? M->params + R.poff : nullptr, R.out, R.bnst, R.rmean,
+                                R.rvar, B, R.C, R.HW, R.eps, R.d.momentum, M->training, c->stream));
+        break;
+      }
       case GN_LAYER_RMSNORM: {
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_rms_fwd(cur, M->params + R.poff, R.out, R.rmsv, B * (R.in_len / R.D), R.D,
@@ -1552,6 +1586,21 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         HIP_OK(c, dense_bwd_core(c, in, M->params + R.poff, R.dzbuf, M->grads + R.poff, nullptr, gin,
                                  B, R.d.in_size, 2 * R.d.out_size, scale, aux, deriv));
         is_dz = next_dz;
+        break;
+      }
+      case GN_LAYER_BATCHNORM2D: {  // batchnorm2d.go:611-660
+        KTimer kt(c, GN_KCLASS_OTHER);
+        const float *gb = R.pcount ? M->params + R.poff : nullptr;
+        HIP_OK(c, launch_bn_bwd(R.gout, in, gb, R.bnst, below ? below->gout : nullptr,
+                                R.pcount ? R.bnpart : nullptr, B, R.C, R.HW, c->stream));
+        if (R.pcount) {
+          float *G = M->grads + R.poff;
+          HIP_OK(c, launch_colsum(R.bnpart, B, R.C, R.C, scale, G, c->scratch, c->scratch_floats,
+                                  c->stream));
+          HIP_OK(c, launch_colsum(R.bnpart + (int64_t)B * R.C, B, R.C, R.C, scale, G + R.C, c->scratch,
+                                  c->scratch_floats, c->stream));
+        }
+        is_dz = false;
         break;
       }
       case GN_LAYER_RMSNORM: {  // rmsnorm.go:301-329: dx, then gamma += g * (x / rms)
@@ -1810,6 +1859,36 @@ extern "C" int gn_model_layer_output(gn_model *M, int32_t layer, float *dst, int
   HIP_OK(c, hipMemcpyAsync(dst, R.out, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
   return GN_OK;
+}
+
+static int running_stats_copy(gn_model *M, int32_t layer, float *mean, float *var, int32_t n,
+                              bool d2h) {
+  if (!M || layer < 0 || layer >= (int)M->L.size()) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  LayerRT &R = M->L[layer];
+  if (R.d.kind != GN_LAYER_BATCHNORM2D)
+    return set_err(c, GN_ERR_UNSUPPORTED, "layer %d is not BatchNorm2D", layer);
+  if (n != R.C || !mean || !var)
+    return set_err(c, GN_ERR_INVALID, "running stats hold %d channels, asked %d", R.C, n);
+  const size_t bytes = (size_t)n * sizeof(float);
+  const hipMemcpyKind k = d2h ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice;
+  HIP_OK(c, hipMemcpyAsync(d2h ? (void *)mean : (void *)R.rmean, d2h ? (void *)R.rmean : (void *)mean,
+                           bytes, k, c->stream));
+  HIP_OK(c, hipMemcpyAsync(d2h ? (void *)var : (void *)R.rvar, d2h ? (void *)R.rvar : (void *)var,
+                           bytes, k, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_model_get_running_stats(gn_model *M, int32_t layer, float *mean, float *var,
+                                          int32_t n) {
+  return running_stats_copy(M, layer, mean, var, n, true);
+}
+
+extern "C" int gn_model_set_running_stats(gn_model *M, int32_t layer, const float *mean,
+                                          const float *var, int32_t n) {
+  return running_stats_copy(M, layer, const_cast<float *>(mean), const_cast<float *>(var), n, false);
 }
 
 extern "C" int gn_model_layer_argmax(gn_model *M, int32_t layer, int32_t *dst, int64_t n) {

@@ -476,4 +476,151 @@ hipError_t launch_conv_dgrad(const float *gout, const float *out, const float *w
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// BatchNorm2D (batchnorm2d.go).  In the per-sample training path every
+// Forward sees one sample, so the statistics of plane (b, f) are that
+// sample's own: one wave per plane of HW values.  Forward: mean = sum *
+// (1/HW), var = sum (x - mean)^2 * (1/HW), std = float32(sqrt(float64(var +
+// eps))), y = gamma ((x - mean) * (1/std)) + beta (:320-400).  Backward
+// (:611-660): dx = g gamma / std - sum(g) gamma / HW / std - (x - mean)
+// sum(g (x - mean)) gamma / HW / std^3; per-plane partial sums of g (x -
+// mean) / std and g for the gamma / beta column sums.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bn_wsum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void bn_fwd_train_kernel(const float *__restrict__ x,
+                                                           const float *__restrict__ gb,
+                                                           float *__restrict__ y,
+                                                           float *__restrict__ st, int planes, int C,
+                                                           int HW, float eps) {
+  const int pl = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (pl >= planes) return;
+  const int f = pl % C;
+  const float *xr = x + (int64_t)pl * HW;
+  const float invN = 1.0f / (float)HW;
+  float s = 0.f;
+  for (int i = lane; i < HW; i += 64) s += xr[i];
+  const float mean = bn_wsum(s) * invN;
+  float ss = 0.f;
+  for (int i = lane; i < HW; i += 64) {
+    const float d = xr[i] - mean;
+    ss += d * d;
+  }
+  const float var = bn_wsum(ss) * invN;
+  const float std = (float)sqrt((double)(var + eps)), istd = 1.0f / std;
+  float *yr = y + (int64_t)pl * HW;
+  if (gb) {
+    const float g = gb[f], b = gb[C + f];
+    for (int i = lane; i < HW; i += 64) yr[i] = g * ((xr[i] - mean) * istd) + b;
+  } else {
+    for (int i = lane; i < HW; i += 64) yr[i] = (xr[i] - mean) * istd;
+  }
+  if (lane == 0) {
+    st[3 * pl] = mean;
+    st[3 * pl + 1] = var;
+    st[3 * pl + 2] = std;
+  }
+}
+
+// running stats: one update per sample in sample order, r = (1 - m) r + m stat
+// (batchnorm2d.go:337, 356), each product and sum rounded as in the reference
+__global__ __launch_bounds__(256) void bn_running_kernel(const float *__restrict__ st,
+                                                         float *__restrict__ rm,
+                                                         float *__restrict__ rv, int B, int C,
+                                                         float mom) {
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (f >= C) return;
+  const float om = 1.0f - mom;
+  float m = rm[f], v = rv[f];
+  for (int b = 0; b < B; ++b) {
+    const float *p = st + 3 * ((int64_t)b * C + f);
+    m = __fadd_rn(__fmul_rn(om, m), __fmul_rn(mom, p[0]));
+    v = __fadd_rn(__fmul_rn(om, v), __fmul_rn(mom, p[1]));
+  }
+  rm[f] = m;
+  rv[f] = v;
+}
+
+// inference (batchnorm2d.go:493-508): running stats, (x - mean) / std
+__global__ __launch_bounds__(256) void bn_fwd_eval_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ gb,
+                                                          const float *__restrict__ rm,
+                                                          const float *__restrict__ rv,
+                                                          float *__restrict__ y, int64_t total, int C,
+                                                          int HW, float eps) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * 256) {
+    const int f = (int)((e / HW) % C);
+    const float std = (float)sqrt((double)(rv[f] + eps));
+    const float norm = (x[e] - rm[f]) / std;
+    y[e] = gb ? gb[f] * norm + gb[C + f] : norm;
+  }
+}
+
+__global__ __launch_bounds__(256) void bn_bwd_kernel(const float *__restrict__ g,
+                                                     const float *__restrict__ x,
+                                                     const float *__restrict__ gb,
+                                                     const float *__restrict__ st,
+                                                     float *__restrict__ dx,
+                                                     float *__restrict__ part, int planes, int C,
+                                                     int HW) {
+  const int pl = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (pl >= planes) return;
+  const int f = pl % C;
+  const float *gr = g + (int64_t)pl * HW, *xr = x + (int64_t)pl * HW;
+  const float mean = st[3 * pl], std = st[3 * pl + 2];
+  float sg = 0.f, sgx = 0.f;
+  for (int i = lane; i < HW; i += 64) {
+    sg += gr[i];
+    sgx += gr[i] * (xr[i] - mean);
+  }
+  sg = bn_wsum(sg);
+  sgx = bn_wsum(sgx);
+  const float gm = gb ? gb[f] : 1.0f, m = (float)HW;
+  const float t1 = (sg * gm) / m / std, den = std * std * std, sgxg = sgx * gm;
+  float pg = 0.f;
+  for (int i = lane; i < HW; i += 64) {
+    const float diff = xr[i] - mean;
+    if (dx) dx[(int64_t)pl * HW + i] = (gr[i] * gm) / std - t1 - diff * sgxg / m / den;
+    pg += gr[i] * (diff / std);
+  }
+  pg = bn_wsum(pg);
+  if (part && lane == 0) {
+    part[pl] = pg;            // gamma: sum g (x - mean) / std
+    part[planes + pl] = sg;   // beta: sum g
+  }
+}
+
+hipError_t launch_bn_fwd(const float *x, const float *gb, float *y, float *st, float *rm, float *rv,
+                         int B, int C, int HW, float eps, float mom, int training, hipStream_t s) {
+  const int planes = B * C;
+  if (planes <= 0) return hipSuccess;
+  if (training) {
+    hipLaunchKernelGGL(bn_fwd_train_kernel, dim3((planes + 3) / 4), dim3(256), 0, s, x, gb, y, st,
+                       planes, C, HW, eps);
+    hipLaunchKernelGGL(bn_running_kernel, dim3((C + 255) / 256), dim3(256), 0, s, st, rm, rv, B, C,
+                       mom);
+  } else {
+    const int64_t total = (int64_t)planes * HW;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(bn_fwd_eval_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, gb, rm, rv, y,
+                       total, C, HW, eps);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const float *st, float *dx,
+                         float *part, int B, int C, int HW, hipStream_t s) {
+  const int planes = B * C;
+  if (planes <= 0) return hipSuccess;
+  hipLaunchKernelGGL(bn_bwd_kernel, dim3((planes + 3) / 4), dim3(256), 0, s, g, x, gb, st, dx, part,
+                     planes, C, HW);
+  return hipGetLastError();
+}
+
 }  // namespace gn

@@ -64,6 +64,7 @@ extern "C" {
 #define GN_LAYER_AVGPOOL2D 11    /* layer.NewAvgPool2D        avgpool2d.go:50 */
 #define GN_LAYER_RMSNORM 12      /* layer.NewRMSNorm          rmsnorm.go:49 */
 #define GN_LAYER_SWIGLU 13       /* layer.NewSwiGLU           swiglu.go:47 */
+#define GN_LAYER_BATCHNORM2D 14  /* layer.NewBatchNorm2D      batchnorm2d.go:70 */
 
 /* TransformerBlockExt options (layer.ActivationType, layer.NormType) */
 #define GN_BLOCK_ACT_RELU 0
@@ -91,6 +92,8 @@ typedef struct gn_layer_desc {
   int32_t block_act;    /* TransformerBlock ff1: GN_BLOCK_ACT_* (transformer.go:199-203) */
   int32_t block_norm;   /* TransformerBlock norms: GN_BLOCK_NORM_* (transformer.go:205-210) */
   int32_t use_rope;     /* TransformerBlock: rotary embeddings on Q and K (transformer.go:212-236) */
+  float momentum;       /* BatchNorm2D running-stat momentum, as given (the facade passes 0.1) */
+  int32_t no_affine;    /* BatchNorm2D without gamma / beta (NewBatchNorm2D affine = false) */
 } gn_layer_desc;
 
 typedef struct gn_adam_desc {   /* opt.NewAdam opt.go:117-126 */
@@ -177,6 +180,13 @@ int gn_model_set_training(gn_model *m, int32_t training);
  * (B x out_len), MaxPool2D argmax switches (B x out_len, int32). */
 int gn_model_layer_output(gn_model *m, int32_t layer, float *dst, int64_t n);
 int gn_model_layer_argmax(gn_model *m, int32_t layer, int32_t *dst, int64_t n);
+/* BatchNorm2D running statistics (C floats each) of `layer`:
+ * GetRunningMean / GetRunningVar (batchnorm2d.go:837-838) and, for restoring
+ * a checkpoint, writing them back (NamedParams running_mean / running_var,
+ * batchnorm2d.go:755-767). */
+int gn_model_get_running_stats(gn_model *m, int32_t layer, float *mean, float *var, int32_t n);
+int gn_model_set_running_stats(gn_model *m, int32_t layer, const float *mean, const float *var,
+                               int32_t n);
 
 /* ---- per-layer operators on device pointers -----------------------------
  * Batched stand-ins for the per-sample Layer.Forward / Backward calls and the

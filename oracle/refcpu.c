@@ -239,6 +239,9 @@ struct layer {
   struct layer *sub;       /* block: wQ, wK, wV, wOut, ff1, ff2 (Dense) */
   struct lnorm *ln;        /* block: norm1, norm2 (LayerNorm) */
   struct layer *rn;        /* block: norm1, norm2 (RMSNorm) */
+  /* BatchNorm2D */
+  float *runMean, *runVar, *bnMean, *bnVar, *bnStd;
+  int32_t bnN, bnHW;
   float *aq, *ak, *av, *scores, *fin, *gfin, *gq, *gk, *gv, *attOut, *res1, *n1, *ffOut, *res2,
       *blkOut, *gRes2, *gN1ff, *comb, *gRes1, *gInAtt, *tmpRow, *probs, *dpre;
 };
@@ -868,6 +871,157 @@ void gno_swiglu(const float *x, int32_t in, int32_t out, const float *params, fl
   memcpy(y, swiglu_forward(&L, x), sizeof(float) * out);
   if (g && gin && gparams) memcpy(gin, swiglu_backward(&L, g), sizeof(float) * in);
   free(L.inputBuf); free(L.preActBuf); free(L.outputBuf); free(L.gradInBuf); free(L.dzBuf);
+}
+
+/* BatchNorm2D batchnorm2d.go:103-135 (Build: gamma 1, beta 0, running mean 0,
+ * running var 1), :255-400 (training forward: per channel, sums over
+ * (sample, position) in groups of four, mean = sum * (1/n), variance of the
+ * differences the same way, std = float32(sqrt(float64(var + eps))), running
+ * stats (1 - m) r + m stat, y = gamma ((x - mean) * (1/std)) + beta),
+ * :493-508 (inference: running stats, (x - mean) / std), :611-660 (training
+ * backward).  In the per-sample training path each Forward sees one sample:
+ * N = 1 and the statistics are that sample's own. */
+static void bn_build(layer *L) {
+  int32_t C = L->spec.in_channels;
+  L->inC = C;
+  L->nparams = L->spec.no_affine ? 0 : 2 * (int64_t)C;
+  L->runMean = zalloc(C);
+  L->runVar = zalloc(C);
+  for (int32_t f = 0; f < C; f++) L->runVar[f] = 1.0f;
+  L->bnMean = zalloc(C);
+  L->bnVar = zalloc(C);
+  L->bnStd = zalloc(C);
+}
+static void bn_init(layer *L) {
+  for (int32_t f = 0; f < L->inC && L->nparams; f++) {
+    L->params[f] = 1.0f;
+    L->params[L->inC + f] = 0.0f;
+  }
+}
+static float bn_eps(const layer *L) { return L->spec.eps > 0 ? L->spec.eps : 1e-5f; }
+/* x holds N samples of C x HW */
+static const float *bn_forward_n(layer *L, const float *x, int32_t N, int32_t HW) {
+  int32_t C = L->inC, total = N * C * HW;
+  if (total > L->in_len) {
+    free(L->outputBuf); free(L->savedInput); free(L->gradInBuf);
+    L->outputBuf = zalloc(total);
+    L->savedInput = zalloc(total);
+    L->gradInBuf = zalloc(total);
+  }
+  L->in_len = L->out_len = total;
+  L->bnN = N;
+  L->bnHW = HW;
+  const float eps = bn_eps(L), mom = L->spec.momentum;
+  const float *gam = L->nparams ? L->params : NULL, *bet = L->nparams ? L->params + C : NULL;
+  if (!L->training) {
+    for (int32_t i = 0; i < N; i++)
+      for (int32_t f = 0; f < C; f++) {
+        const float *xr = x + ((int64_t)i * C + f) * HW;
+        float *o = L->outputBuf + ((int64_t)i * C + f) * HW;
+        float mean = L->runMean[f], std = (float)sqrt((double)(L->runVar[f] + eps));
+        for (int32_t s = 0; s < HW; s++) {
+          float norm = (xr[s] - mean) / std;
+          o[s] = gam ? gam[f] * norm + bet[f] : norm;
+        }
+      }
+    return L->outputBuf;
+  }
+  memcpy(L->savedInput, x, sizeof(float) * total);
+  float n = (float)(N * HW), invN = 1.0f / n;
+  for (int32_t f = 0; f < C; f++) {
+    float sum = 0.0f;
+    for (int32_t i = 0; i < N; i++) {
+      const float *p = x + ((int64_t)i * C + f) * HW;
+      int32_t s = 0;
+      for (; s <= HW - 4; s += 4) sum += p[s] + p[s + 1] + p[s + 2] + p[s + 3];
+      for (; s < HW; s++) sum += p[s];
+    }
+    float mean = sum * invN;
+    L->bnMean[f] = mean;
+    L->runMean[f] = (1 - mom) * L->runMean[f] + mom * mean;
+    float sumSq = 0.0f;
+    for (int32_t i = 0; i < N; i++) {
+      const float *p = x + ((int64_t)i * C + f) * HW;
+      int32_t s = 0;
+      for (; s <= HW - 4; s += 4) {
+        float d0 = p[s] - mean, d1 = p[s + 1] - mean, d2 = p[s + 2] - mean, d3 = p[s + 3] - mean;
+        sumSq += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+      }
+      for (; s < HW; s++) {
+        float d = p[s] - mean;
+        sumSq += d * d;
+      }
+    }
+    float var = sumSq * invN;
+    L->bnVar[f] = var;
+    L->bnStd[f] = (float)sqrt((double)(var + eps));
+    L->runVar[f] = (1 - mom) * L->runVar[f] + mom * var;
+  }
+  for (int32_t i = 0; i < N; i++)
+    for (int32_t f = 0; f < C; f++) {
+      const float *xr = x + ((int64_t)i * C + f) * HW;
+      float *o = L->outputBuf + ((int64_t)i * C + f) * HW;
+      float mean = L->bnMean[f], istd = 1.0f / L->bnStd[f];
+      for (int32_t s = 0; s < HW; s++) {
+        float norm = (xr[s] - mean) * istd;
+        o[s] = gam ? gam[f] * norm + bet[f] : norm;
+      }
+    }
+  return L->outputBuf;
+}
+static const float *bn_forward(layer *L, const float *x, int32_t total) {
+  return bn_forward_n(L, x, 1, total / L->inC);
+}
+static const float *bn_backward(layer *L, const float *grad) {
+  int32_t C = L->inC, N = L->bnN, HW = L->bnHW;
+  const float *x = L->savedInput;
+  float m = (float)(N * HW);
+  for (int32_t f = 0; f < C; f++) {
+    float mean = L->bnMean[f], std = L->bnStd[f], sumGrad = 0.0f, sumGX = 0.0f;
+    for (int32_t i = 0; i < N; i++)
+      for (int32_t s = 0; s < HW; s++) {
+        int64_t k = ((int64_t)i * C + f) * HW + s;
+        float diff = x[k] - mean;
+        sumGrad += grad[k];
+        sumGX += grad[k] * diff;
+      }
+    float g = L->nparams ? L->params[f] : 1.0f;
+    for (int32_t i = 0; i < N; i++)
+      for (int32_t s = 0; s < HW; s++) {
+        int64_t k = ((int64_t)i * C + f) * HW + s;
+        float diff = x[k] - mean, norm = diff / std, gi = grad[k] * g;
+        L->gradInBuf[k] = gi / std - (sumGrad * g) / m / std - diff * (sumGX * g) / m / (std * std * std);
+        if (L->nparams) {
+          L->grads[f] += grad[k] * norm;
+          L->grads[C + f] += grad[k];
+        }
+      }
+  }
+  return L->gradInBuf;
+}
+
+void gno_batchnorm2d(const float *x, int32_t N, int32_t C, int32_t HW, float eps, float momentum,
+                     int32_t affine, const float *gamma_beta, int32_t training, float *out,
+                     float *rm, float *rv, const float *g, float *gin, float *ggamma_beta) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_BATCHNORM2D;
+  L.spec.in_channels = C;
+  L.spec.eps = eps;
+  L.spec.momentum = momentum;
+  L.spec.no_affine = !affine;
+  bn_build(&L);
+  L.training = training;
+  L.params = (float *)gamma_beta;
+  L.grads = ggamma_beta;
+  memcpy(L.runMean, rm, sizeof(float) * C);
+  memcpy(L.runVar, rv, sizeof(float) * C);
+  memcpy(out, bn_forward_n(&L, x, N, HW), sizeof(float) * N * C * HW);
+  memcpy(rm, L.runMean, sizeof(float) * C);
+  memcpy(rv, L.runVar, sizeof(float) * C);
+  if (training && g && gin) memcpy(gin, bn_backward(&L, g), sizeof(float) * N * C * HW);
+  free(L.outputBuf); free(L.savedInput); free(L.gradInBuf);
+  free(L.runMean); free(L.runVar); free(L.bnMean); free(L.bnVar); free(L.bnStd);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1543,6 +1697,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_TRANSFORMER: tb_build(L); break;
     case GNO_LAYER_RMSNORM: rms_build(L); break;
     case GNO_LAYER_SWIGLU: swiglu_build(L); break;
+    case GNO_LAYER_BATCHNORM2D: bn_build(L); break;
     default: break;
   }
 }
@@ -1555,6 +1710,7 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_TRANSFORMER) tb_init(L);
   else if (L->kind == GNO_LAYER_RMSNORM) rms_init(L);
   else if (L->kind == GNO_LAYER_SWIGLU) swiglu_init(L);
+  else if (L->kind == GNO_LAYER_BATCHNORM2D) bn_init(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -1582,6 +1738,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
     case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
     case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
+    case GNO_LAYER_BATCHNORM2D: o = bn_forward(L, x, *len_io); break;
     default: o = x;
   }
   return o;
@@ -1601,6 +1758,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
     case GNO_LAYER_RMSNORM: return rms_backward(L, g);
     case GNO_LAYER_SWIGLU: return swiglu_backward(L, g);
+    case GNO_LAYER_BATCHNORM2D: return bn_backward(L, g);
     default: return g;
   }
 }
@@ -1658,6 +1816,9 @@ void gno_net_destroy(gno_net *n) {
     free(L->ids);
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_free(L);
     if (L->kind == GNO_LAYER_RMSNORM) free(L->tmpRow);
+    if (L->kind == GNO_LAYER_BATCHNORM2D) {
+      free(L->runMean); free(L->runVar); free(L->bnMean); free(L->bnVar); free(L->bnStd);
+    }
   }
   free(n->layers);
   free(n->params); free(n->grads); free(n->m); free(n->v); free(n->worker_grads); free(n->lossGrad);
@@ -1806,6 +1967,13 @@ int32_t gno_net_layer_argmax(gno_net *n, int32_t li, int32_t *dst, int32_t cap) 
   int32_t c = L->out_len < cap ? L->out_len : cap;
   memcpy(dst, L->argmax, sizeof(int32_t) * c);
   return c;
+}
+int32_t gno_net_layer_running_stats(gno_net *n, int32_t li, float *mean, float *var) {
+  layer *L = &n->layers[li];
+  if (L->kind != GNO_LAYER_BATCHNORM2D) return 0;
+  memcpy(mean, L->runMean, sizeof(float) * L->inC);
+  memcpy(var, L->runVar, sizeof(float) * L->inC);
+  return L->inC;
 }
 int32_t gno_net_layer_preact(gno_net *n, int32_t li, float *dst, int32_t cap) {
   layer *L = &n->layers[li];

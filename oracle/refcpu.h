@@ -21,6 +21,7 @@
  *   AvgPool2D                         internal/layer/avgpool2d.go:98-220,401-474,560-565
  *   RMSNorm                           internal/layer/rmsnorm.go:73-96,222-240,301-335
  *   SwiGLU                            internal/layer/swiglu.go:73-232
+ *   BatchNorm2D                       internal/layer/batchnorm2d.go:103-135,255-511,524-665
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -69,6 +70,7 @@ enum {
   GNO_LAYER_AVGPOOL2D = 11,
   GNO_LAYER_RMSNORM = 12,
   GNO_LAYER_SWIGLU = 13,
+  GNO_LAYER_BATCHNORM2D = 14,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -89,6 +91,8 @@ typedef struct gno_layer_spec {
   int32_t block_act;    /* TransformerBlock ff1: 0 ReLU, 1 SwiGLU, 2 GELU (transformer.go:199-203) */
   int32_t block_norm;   /* TransformerBlock norms: 0 LayerNorm, 1 RMSNorm (transformer.go:205-210) */
   int32_t use_rope;     /* TransformerBlock attention: rotary embeddings on Q and K */
+  float momentum;       /* BatchNorm2D running-stat momentum (the facade's 0.1) */
+  int32_t no_affine;    /* BatchNorm2D without gamma / beta */
 } gno_layer_spec;
 
 typedef struct gno_net gno_net;
@@ -153,6 +157,14 @@ void gno_swiglu(const float *x, int32_t in, int32_t out, const float *params, fl
                 const float *g, float *gin, float *gparams);
 /* applyRoPE over T tokens of nh heads of hd, in place (conj: the inverse). */
 void gno_rope(float *x, int32_t T, int32_t nh, int32_t hd, int32_t conj);
+/* BatchNorm2D of N samples of C channels x HW positions (x is N*C*HW) with
+ * the batch statistics (training, updating rm / rv) or the running ones; with
+ * g, gin (and ggamma / gbeta when affine) also the training backward. */
+void gno_batchnorm2d(const float *x, int32_t N, int32_t C, int32_t HW, float eps, float momentum,
+                     int32_t affine, const float *gamma_beta, int32_t training, float *out,
+                     float *rm, float *rv, const float *g, float *gin, float *ggamma_beta);
+/* Running mean / var of BatchNorm2D layer li (C each); returns C or 0. */
+int32_t gno_net_layer_running_stats(gno_net *n, int32_t li, float *mean, float *var);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

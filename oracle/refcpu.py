@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU = range(8)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU) = range(1, 14)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D) = range(1, 15)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -36,6 +36,7 @@ class LayerSpec(C.Structure):
         ("causal", C.c_int32), ("vocab", C.c_int32), ("dim", C.c_int32),
         ("return_sequences", C.c_int32), ("eps", C.c_float),
         ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
+        ("momentum", C.c_float), ("no_affine", C.c_int32),
     ]
 
 
@@ -107,6 +108,10 @@ def lib():
         L.gno_rmsnorm.restype = C.c_int32
         L.gno_swiglu.argtypes = [f32p, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p, f32p]
         L.gno_rope.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32]
+        L.gno_batchnorm2d.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_float,
+                                      C.c_int32, f32p, C.c_int32, f32p, f32p, f32p, f32p, f32p, f32p]
+        L.gno_net_layer_running_stats.argtypes = [C.c_void_p, C.c_int32, f32p, f32p]
+        L.gno_net_layer_running_stats.restype = C.c_int32
         _lib = L
     return _lib
 
@@ -214,6 +219,12 @@ class Net:
         n = lib().gno_net_layer_argmax(self.h, layer, iptr(a), cap)
         return a[:n].copy()
 
+    def running_stats(self, layer, cap=1 << 16):
+        m = np.empty(cap, np.float32)
+        v = np.empty(cap, np.float32)
+        n = lib().gno_net_layer_running_stats(self.h, layer, fptr(m), fptr(v))
+        return m[:n].copy(), v[:n].copy()
+
     def preact(self, layer, cap=1 << 20):
         a = np.empty(cap, np.float32)
         n = lib().gno_net_layer_preact(self.h, layer, fptr(a), cap)
@@ -275,6 +286,27 @@ def swiglu(x, out, params, g=None):
     gp = np.zeros(params.size, np.float32)
     lib().gno_swiglu(fptr(x), x.size, out, fptr(params), fptr(y), fptr(g), fptr(gin), fptr(gp))
     return y, gin, gp
+
+
+def batchnorm2d(x, N, C, HW, training=True, gamma_beta=None, rm=None, rv=None, g=None, eps=1e-5,
+                momentum=0.1):
+    """BatchNorm2D over N samples of C x HW.  Returns (out, rm, rv) or, with
+    g (training), (out, rm, rv, grad_in, grad_gamma_beta)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    affine = gamma_beta is not None
+    gb = np.ascontiguousarray(gamma_beta if affine else np.zeros(2 * C), np.float32)
+    rm = np.zeros(C, np.float32) if rm is None else np.array(rm, np.float32)
+    rv = np.ones(C, np.float32) if rv is None else np.array(rv, np.float32)
+    out = np.empty(x.size, np.float32)
+    gin = np.empty(x.size, np.float32)
+    ggb = np.zeros(2 * C, np.float32)
+    gg = None if g is None else np.ascontiguousarray(g, np.float32).ravel()
+    lib().gno_batchnorm2d(fptr(x), N, C, HW, eps, momentum, int(affine), fptr(gb), int(training),
+                          fptr(out), fptr(rm), fptr(rv), None if gg is None else fptr(gg),
+                          None if gg is None else fptr(gin), fptr(ggb))
+    if gg is None:
+        return out, rm, rv
+    return out, rm, rv, gin, ggb
 
 
 def rope(x, T, nh, hd, conj=False):

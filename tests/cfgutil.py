@@ -19,6 +19,9 @@ def oracle_specs(refcpu, cfg):
                                      stride=d["s"], padding=d["p"]))
         elif k == "flatten":
             specs.append(refcpu.spec(refcpu.LAYER_FLATTEN, in_size=d["n"]))
+        elif k == "batchnorm2d":
+            specs.append(refcpu.spec(refcpu.LAYER_BATCHNORM2D, in_channels=d["C"], momentum=0.1,
+                                     in_size=cfg["in_len"] if i == 0 else 0))
         elif k == "swiglu":
             specs.append(refcpu.spec(refcpu.LAYER_SWIGLU, in_size=d["in"], out_size=d["out"]))
         elif k == "rmsnorm":

@@ -382,6 +382,53 @@ def test_swiglu_net(gn, oracle, case):
         assert max_rel(got[b], ref) <= TOL, (b, max_rel(got[b], ref))
 
 
+_BN_CASES = {
+    # Conv2D (ReLU) -> BatchNorm2D -> MaxPool -> Flatten -> Dense softmax
+    "conv_bn_pool": (dict(B=24, in_len=3 * 12 * 12, classes=10, loss="ce", layers=[
+        {"kind": "conv2d", "inC": 3, "outC": 8, "k": 3, "s": 1, "p": 1, "act": "relu"},
+        {"kind": "batchnorm2d", "C": 8},
+        {"kind": "maxpool2d", "k": 2, "s": 2, "p": 0, "inC": 8},
+        {"kind": "flatten", "n": 8 * 6 * 6},
+        {"kind": "dense", "in": 8 * 6 * 6, "out": 10, "act": "softmax", "ptr": True}]), 1),
+    # BatchNorm2D as the first layer, 4 worker chunks (running stats in sample order)
+    "first_layer_w4": (dict(B=64, in_len=4 * 9 * 9, classes=6, loss="ce", layers=[
+        {"kind": "batchnorm2d", "C": 4},
+        {"kind": "flatten", "n": 4 * 81},
+        {"kind": "dense", "in": 4 * 81, "out": 6, "act": "softmax", "ptr": True}]), 4),
+    # 32 x 32 planes (more than one lane pass per wave), Dense ReLU head
+    "planes_32x32": (dict(B=16, in_len=3 * 32 * 32, classes=5, loss="mse", layers=[
+        {"kind": "conv2d", "inC": 3, "outC": 6, "k": 3, "s": 1, "p": 1, "act": "relu"},
+        {"kind": "batchnorm2d", "C": 6},
+        {"kind": "flatten", "n": 6 * 32 * 32},
+        {"kind": "dense", "in": 6 * 32 * 32, "out": 5, "act": "linear", "ptr": False}]), 1),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_BN_CASES))
+def test_batchnorm2d_net(gn, oracle, case):
+    """BatchNorm2D (batchnorm2d.go) in a net: gradients, Adam state and
+    weights over 3 steps; the running mean / var after them (one update per
+    sample, sample order); then inference on the running statistics against
+    the oracle's forward in eval mode."""
+    c, workers = _BN_CASES[case]
+    cfg = dict(num=15, name="bn_" + case, lr=1e-3, x="normal", **c)
+    model, net = _compare_step(gn, oracle, cfg, steps=3, workers=workers)
+    li = [d["kind"] for d in cfg["layers"]].index("batchnorm2d")
+    m_gpu, v_gpu = model.RunningStats(li)
+    m_ref, v_ref = net.running_stats(li)
+    assert max_rel(m_gpu, m_ref) <= TOL and max_rel(v_gpu, v_ref) <= TOL
+    x, _ = configs_inputs(cfg)
+    net.params[:] = model.Params()
+    net.set_training(False)
+    out = model.PredictBatch(x)
+    ref = np.stack([net.forward(x[b])[:out.shape[1]] for b in range(cfg["B"])])
+    assert max_rel(out, ref) <= TOL, max_rel(out, ref)
+    # writing the running statistics back (checkpoint restore) changes inference
+    model.SetRunningStats(li, m_gpu * 0, v_gpu * 0 + 4)
+    m2, v2 = model.RunningStats(li)
+    assert not m2.any() and (v2 == 4).all()
+
+
 def configs_inputs(cfg):
     from goneuron_amd import configs
     return configs.inputs(cfg)

@@ -342,6 +342,62 @@ def test_rope_known_answers_and_inverse(oracle):
     np.testing.assert_allclose(yr[:, :, hd // 2:], a * s + b * c, rtol=1e-5, atol=1e-5)
 
 
+def test_batchnorm2d_known_answers_and_fixture(oracle):
+    """batchnorm2d_test.go:8-30 ([1, 5 | 2, 6] -> [-1, 1 | -1, 1]), :86-115
+    (the input gradient of unit grads sums to 0); the PyTorch fixture
+    batchnorm2d_eval (2 x 3 x 4 x 4, batch statistics: track_running_stats
+    off, generate_references.py:262-283) with gamma 1, beta 0."""
+    out, _, _ = oracle.batchnorm2d([1, 5, 2, 6], 1, 2, 2)
+    np.testing.assert_allclose(out, [-1, 1, -1, 1], atol=1e-5)
+    _, _, _, gin, _ = oracle.batchnorm2d([1, 5, 2, 6], 1, 2, 2, g=np.ones(4, np.float32))
+    assert abs(float(gin.sum())) <= 1e-6
+    x = fx("batchnorm2d_eval", "input")
+    gb = np.array([1, 1, 1, 0, 0, 0], np.float32)
+    out, _, _ = oracle.batchnorm2d(x, 2, 3, 16, gamma_beta=gb)
+    np.testing.assert_allclose(out, fx("batchnorm2d_eval", "output"), rtol=1e-5, atol=1e-5)
+
+
+def test_batchnorm2d_backward_vs_autograd_and_running_stats(oracle):
+    """Training-mode gradients against torch autograd in float64 (the
+    reference's formula, batchnorm2d.go:640-655, is the exact one); running
+    statistics follow (1 - m) r + m stat with the *biased* variance
+    (batchnorm2d.go:351-356), one update per Forward; inference uses them
+    (:493-508)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(8)
+    N, C, HW = 3, 4, 9
+    x = (rng.normal(size=N * C * HW) * 2 + 0.5).astype(np.float32)
+    g = rng.normal(size=N * C * HW).astype(np.float32)
+    gb = np.concatenate([rng.uniform(0.5, 1.5, C), rng.normal(size=C)]).astype(np.float32)
+    out, rm, rv, gin, ggb = oracle.batchnorm2d(x, N, C, HW, gamma_beta=gb, g=g)
+    xt = torch.tensor(x.astype(np.float64).reshape(N, C, 3, 3), requires_grad=True)
+    gam = torch.tensor(gb[:C].astype(np.float64), requires_grad=True)
+    bet = torch.tensor(gb[C:].astype(np.float64), requires_grad=True)
+    y = torch.nn.functional.batch_norm(xt, None, None, gam, bet, training=True, eps=1e-5)
+    y.backward(torch.tensor(g.astype(np.float64).reshape(N, C, 3, 3)))
+    np.testing.assert_allclose(out, y.detach().numpy().ravel(), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(gin, xt.grad.numpy().ravel(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(ggb[:C], gam.grad.numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(ggb[C:], bet.grad.numpy(), rtol=1e-4, atol=1e-5)
+    xs = x.astype(np.float64).reshape(N, C, HW)
+    np.testing.assert_allclose(rm, 0.9 * 0 + 0.1 * xs.mean(axis=(0, 2)), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(rv, 0.9 * 1 + 0.1 * xs.var(axis=(0, 2)), rtol=1e-5, atol=1e-6)
+    # per-sample forwards: one update each, in order
+    rm2, rv2 = np.zeros(C), np.ones(C)
+    m_, v_ = np.zeros(C, np.float32), np.ones(C, np.float32)
+    for i in range(N):
+        _, m_, v_ = oracle.batchnorm2d(x[i * C * HW:(i + 1) * C * HW], 1, C, HW, gamma_beta=gb, rm=m_,
+                                       rv=v_)
+        rm2 = 0.9 * rm2 + 0.1 * xs[i].mean(axis=1)
+        rv2 = 0.9 * rv2 + 0.1 * xs[i].var(axis=1)
+    np.testing.assert_allclose(m_, rm2, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(v_, rv2, rtol=1e-5, atol=1e-6)
+    inf, _, _ = oracle.batchnorm2d(x, N, C, HW, training=False, gamma_beta=gb, rm=m_, rv=v_)
+    ref = (xs - rm2[None, :, None]) / np.sqrt(rv2[None, :, None] + 1e-5)
+    ref = ref * gb[:C].astype(np.float64)[None, :, None] + gb[C:].astype(np.float64)[None, :, None]
+    np.testing.assert_allclose(inf, ref.ravel(), rtol=1e-5, atol=1e-5)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
