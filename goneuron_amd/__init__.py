@@ -24,7 +24,7 @@ __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
     "AvgPool2D", "BatchNorm2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock",
     "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
-    "LSTM", "SequenceUnroller",
+    "LSTM", "GRU", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
     "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
 ]
@@ -65,7 +65,7 @@ def Ref(act: Activation) -> Activation:
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D) = range(1, 15)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER) = range(1, 16)
 
 
 class Layer:
@@ -230,14 +230,26 @@ class _LSTMSpec:
         self.out, self.inp = out, inp
 
 
+class _GRUSpec(_LSTMSpec):
+    pass
+
+
 def LSTM(out, *inp):
     return _LSTMSpec(out, inp[0] if inp else -1)
 
 
+def GRU(out, *inp):
+    """goneuron.GRU (goneuron.go:193-200): NewGRU(in, out), usable through
+    SequenceUnroller."""
+    return _GRUSpec(out, inp[0] if inp else -1)
+
+
 def SequenceUnroller(l, seq_len, return_sequences):
+    """goneuron.SequenceUnroller over an LSTM or a GRU (unroller.go:57-213)."""
     if not isinstance(l, _LSTMSpec):
-        raise GNError(-4, "SequenceUnroller is built for LSTM only")
-    return Layer(LAYER_LSTM_UNROLLER, in_size=l.inp, out_size=l.out, seq_len=seq_len,
+        raise GNError(-4, "SequenceUnroller is built for LSTM and GRU only")
+    kind = LAYER_GRU_UNROLLER if isinstance(l, _GRUSpec) else LAYER_LSTM_UNROLLER
+    return Layer(kind, in_size=l.inp, out_size=l.out, seq_len=seq_len,
                  return_sequences=int(return_sequences))
 
 

@@ -12,7 +12,7 @@ import numpy as np
 from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, BatchNorm2D, RMSNorm,
                SwiGLU, Flatten, TransformerBlockExt, ActReLU, ActSwiGLU, ActGELU, NormLN, NormRMS,
                Embedding,
-               PositionalEncoding, TransformerBlock, CLSPooling, LSTM, SequenceUnroller, ReLU,
+               PositionalEncoding, TransformerBlock, CLSPooling, LSTM, GRU, SequenceUnroller, ReLU,
                Sigmoid, Tanh, Linear, GELU, Softmax, LogSoftmax, Ref, NewSequential, fill_normal,
                fill_uniform, fill_class_ids)
 
@@ -66,6 +66,14 @@ def lstm(B=64, T=100, inp=64, hidden=256):
     return dict(num=5, name="lstm", B=B, loss="mse", lr=1e-3, x="normal", in_len=T * inp,
                 classes=None, targets="normal",
                 layers=[{"kind": "lstm", "in": inp, "hidden": hidden, "T": T},
+                        dense(hidden, 1, "linear")])
+
+
+def gru(B=64, T=100, inp=64, hidden=256):
+    """C5's shape with a GRU in the SequenceUnroller (not a BASELINE config)."""
+    return dict(num=6, name="gru", B=B, loss="mse", lr=1e-3, x="normal", in_len=T * inp,
+                classes=None, targets="normal",
+                layers=[{"kind": "gru", "in": inp, "hidden": hidden, "T": T},
                         dense(hidden, 1, "linear")])
 
 
@@ -132,6 +140,8 @@ def product_layers(cfg):
             out.append(CLSPooling(d["T"], d["dim"]))
         elif k == "lstm":
             out.append(SequenceUnroller(LSTM(d["hidden"], d["in"]), d["T"], False))
+        elif k == "gru":
+            out.append(SequenceUnroller(GRU(d["hidden"], d["in"]), d["T"], False))
         else:
             raise ValueError(k)
     # the first layer carries the per-sample input length (an LSTM carries its

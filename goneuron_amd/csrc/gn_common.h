@@ -138,6 +138,13 @@ hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const 
 hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
 hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
 
+// ---- SequenceUnroller(GRU) ----
+bool gru_supported(int H);
+hipError_t launch_gru_fwd(const float *xw, const float *WhT, float *pre, float *hprev, float *rh,
+                          float *out, int B, int T, int H, hipStream_t s);
+hipError_t launch_gru_bwd(const float *g, const float *pre, const float *hprev, const float *Wh,
+                          float *dG, int B, int T, int H, hipStream_t s);
+
 // ---- SequenceUnroller(LSTM) ----
 hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hipStream_t s);
 hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,

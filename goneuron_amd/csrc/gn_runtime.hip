@@ -531,6 +531,9 @@ struct LayerRT {
   // partial sums [2][maxB*C], running mean / var [C]
   int C = 0, HW = 0;
   float *bnst = nullptr, *bnpart = nullptr, *rmean = nullptr, *rvar = nullptr;
+  // SequenceUnroller(GRU): pre-activations [B*T][3H], h before each step and
+  // r * h_prev [B*T][H] (xw, WhT, Dg, S as for the LSTM, sized for 3 gates)
+  float *gpre = nullptr, *ghprev = nullptr, *grh = nullptr;
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -610,6 +613,13 @@ static void init_dense(float *p, int in, int out) {  // Dense.Build layer.go:300
   const int64_t nw = (int64_t)in * out;
   for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
   for (int i = 0; i < out; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
+}
+
+static void init_gru(float *p, int I, int H) {  // GRU.Build gru.go:120-147 (biases stay 0)
+  const float scale = (float)sqrt(2.0 / ((double)I + (double)H));
+  uint64_t s = (uint64_t)(I * 1000 + H * 100 + 242);
+  const int64_t n = (int64_t)3 * H * I + (int64_t)2 * H * H;
+  for (int64_t k = 0; k < n; ++k) p[k] = lcg_float(s) * 2 * scale - scale;
 }
 
 static void init_swiglu(float *p, int in, int out) {  // SwiGLU.Build swiglu.go:82-88
@@ -720,7 +730,8 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
 
   // Shape propagation (the reference infers per-sample lengths at forward time)
   int len = layers[0].in_size;
-  if (layers[0].kind == GN_LAYER_LSTM_UNROLLER) len = layers[0].in_size * layers[0].seq_len;
+  if (layers[0].kind == GN_LAYER_LSTM_UNROLLER || layers[0].kind == GN_LAYER_GRU_UNROLLER)
+    len = layers[0].in_size * layers[0].seq_len;
   if (len <= 0) return set_err(c, GN_ERR_INVALID, "first layer needs in_size (input length)");
   int64_t off = 0;
   for (int i = 0; i < nlayers; ++i) {
@@ -858,6 +869,21 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.pcount = 2 * (int64_t)R.d.in_size * R.d.out_size;
         R.out_len = R.d.out_size;
         break;
+      case GN_LAYER_GRU_UNROLLER:  // gru.go:110-167: [Wx 3H x I | Wh 2H x H | b 3H]
+        R.T = R.d.seq_len;
+        R.I = R.d.in_size;
+        R.H = R.d.out_size;
+        if (R.T <= 0 || R.I <= 0 || !gru_supported(R.H))
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(GRU) sizes (hidden <= 1024)", i);
+        if (R.d.return_sequences)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
+        if (i != 0)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: SequenceUnroller only as the first layer", i);
+        R.in_len = R.T * R.I;
+        len = R.in_len;
+        R.pcount = (int64_t)3 * R.H * R.I + (int64_t)2 * R.H * R.H + 3 * R.H;
+        R.out_len = R.H;
+        break;
       case GN_LAYER_LSTM_UNROLLER: {
         R.T = R.d.seq_len;
         R.I = R.d.in_size;
@@ -984,6 +1010,17 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
+    }
+    if (R.d.kind == GN_LAYER_GRU_UNROLLER) {
+      init_gru(host.data() + R.poff, R.I, R.H);
+      const size_t rows = (size_t)max_batch * R.T, H = R.H;
+      if ((rc = model_alloc(M.get(), 2 * H * H, &R.WhT))) return rc;
+      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.xw))) return rc;
+      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.gpre))) return rc;
+      if ((rc = model_alloc(M.get(), rows * H, &R.ghprev))) return rc;
+      if ((rc = model_alloc(M.get(), rows * H, &R.grh))) return rc;
+      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.Dg))) return rc;
+      if ((rc = model_alloc(M.get(), (size_t)max_batch * 3 * H, &R.S))) return rc;
     }
     if (R.d.kind == GN_LAYER_BATCHNORM2D) {
       if (R.pcount) std::fill(host.begin() + R.poff, host.begin() + R.poff + R.C, 1.0f);
@@ -1430,6 +1467,27 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, launch_swiglu_fwd(R.zbuf, R.out, B, R.d.out_size, c->stream));
         break;
       }
+      case GN_LAYER_GRU_UNROLLER: {
+        const int H = R.H, G3 = 3 * H;
+        const float *Wx = M->params + R.poff;
+        const float *Wh = Wx + (int64_t)G3 * R.I;
+        const float *bias = Wh + (int64_t)2 * H * H;
+        {
+          KTimer kt(c, GN_KCLASS_GEMM);
+          GemmArgs g{};  // xw[b*T + t] = b + Wx x_t (gru.go:194-210)
+          g.M = B * R.T; g.N = G3; g.K = R.I;
+          g.A = cur; g.lda = R.I;
+          g.B = Wx; g.ldb = R.I;
+          g.C = R.xw; g.ldc = G3; g.alpha = 1.0f;
+          g.bias = bias; g.act = F_IDENTITY;
+          g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+          HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, g, c->stream));
+        }
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_transpose(Wh, R.WhT, 2 * H, H, c->stream));
+        HIP_OK(c, launch_gru_fwd(R.xw, R.WhT, R.gpre, R.ghprev, R.grh, R.out, B, R.T, H, c->stream));
+        break;
+      }
       case GN_LAYER_BATCHNORM2D: {  // running stats advance in training mode only
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_bn_fwd(cur, R.pcount ? M->params + R.poff : nullptr, R.out, R.bnst, R.rmean,
@@ -1586,6 +1644,42 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         HIP_OK(c, dense_bwd_core(c, in, M->params + R.poff, R.dzbuf, M->grads + R.poff, nullptr, gin,
                                  B, R.d.in_size, 2 * R.d.out_size, scale, aux, deriv));
         is_dz = next_dz;
+        break;
+      }
+      case GN_LAYER_GRU_UNROLLER: {  // gru.go:347-510 per step, unroller.go:189-206
+        const int H = R.H, T = R.T, I = R.I, G3 = 3 * H;
+        const float *Wx = M->params + R.poff;
+        const float *Wh = Wx + (int64_t)G3 * I;
+        float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G3 * I, *gb = gWh + (int64_t)2 * H * H;
+        {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_gru_bwd(R.gout, R.gpre, R.ghprev, Wh, R.Dg, B, T, H, c->stream));
+          HIP_OK(c, launch_token_sum(R.Dg, R.S, B, T, G3, c->stream));
+          HIP_OK(c, launch_colsum(R.S, B, G3, G3, scale, gb, c->scratch, c->scratch_floats, c->stream));
+        }
+        KTimer kt(c, GN_KCLASS_GEMM);
+        GemmArgs a{};  // dWx = scale * (sum_t dG)^T x_last (inputBuf holds the last step's input)
+        a.M = G3; a.N = I; a.K = B;
+        a.A = R.S; a.lda = G3;
+        a.B = in + (int64_t)(T - 1) * I; a.ldb = T * I;
+        a.C = gWx; a.ldc = I; a.alpha = scale;
+        a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+        HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+        GemmArgs u{};  // dWh_u = scale * dU^T h_prev over (sample, step)
+        u.M = H; u.N = H; u.K = B * T;
+        u.A = R.Dg; u.lda = G3;
+        u.B = R.ghprev; u.ldb = H;
+        u.C = gWh; u.ldc = H; u.alpha = scale;
+        u.ws = c->scratch; u.ws_cap = c->scratch_floats;
+        HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, u, c->stream));
+        GemmArgs r{};  // dWh_r = scale * dC^T (r * h_prev): the candidate's use of the reset block
+        r.M = H; r.N = H; r.K = B * T;
+        r.A = R.Dg + 2 * H; r.lda = G3;
+        r.B = R.grh; r.ldb = H;
+        r.C = gWh + (int64_t)H * H; r.ldc = H; r.alpha = scale;
+        r.ws = c->scratch; r.ws_cap = c->scratch_floats;
+        HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, r, c->stream));
+        is_dz = false;
         break;
       }
       case GN_LAYER_BATCHNORM2D: {  // batchnorm2d.go:611-660

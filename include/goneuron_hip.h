@@ -65,6 +65,7 @@ extern "C" {
 #define GN_LAYER_RMSNORM 12      /* layer.NewRMSNorm          rmsnorm.go:49 */
 #define GN_LAYER_SWIGLU 13       /* layer.NewSwiGLU           swiglu.go:47 */
 #define GN_LAYER_BATCHNORM2D 14  /* layer.NewBatchNorm2D      batchnorm2d.go:70 */
+#define GN_LAYER_GRU_UNROLLER 15 /* SequenceUnroller(GRU)     unroller.go:57, gru.go:83 */
 
 /* TransformerBlockExt options (layer.ActivationType, layer.NormType) */
 #define GN_BLOCK_ACT_RELU 0

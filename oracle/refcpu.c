@@ -1025,6 +1025,163 @@ void gno_batchnorm2d(const float *x, int32_t N, int32_t C, int32_t HW, float eps
 }
 
 /* ------------------------------------------------------------------------ */
+/* GRU (gru.go) wrapped by SequenceUnroller (unroller.go)                     */
+/* ------------------------------------------------------------------------ */
+/* Build gru.go:110-167: params [Wx (3H x I) | Wh (2H x H) | b (3H)], gates
+ * (update, reset, candidate); one LCG stream seeded I*1000 + H*100 + 242 over
+ * Wx then Wh with the Xavier scale; biases 0.
+ * Forward gru.go:182-262: pre = b + Wx x (+ Wh_u h, Wh_r h for the first two
+ * gates); u = sig, r = sig; pre_c += Wh_r (r * h) — the candidate reuses the
+ * reset gate's recurrent block; h' = h + u (tanh(pre_c) - h).
+ * Backward gru.go:347-510 per step (the unroller runs t = T-1 .. 0 with a
+ * cumulative gradient, unroller.go:189-206): gates recomputed from the saved
+ * pre-activations; dU = dh (c - h_prev) u (1 - u), dC = dh (1 - u) (1 - c^2);
+ * the reset-gate delta is never computed (it stays 0); input-weight
+ * gradients use inputBuf, which holds the last step's input; dh_prev =
+ * Wh_u^T dU + Wh_r^T (dC r) + dh u is added to the step's gradient in place. */
+static void gru_build(layer *L) {
+  int32_t I = L->spec.in_size, H = L->spec.out_size, T = L->spec.seq_len;
+  L->H = H;
+  L->T = T;
+  L->nparams = (int64_t)3 * H * I + (int64_t)2 * H * H + 3 * H;
+  L->lstmIn = zalloc(I);                    /* inputBuf: the last step's input */
+  L->savedH = zalloc((int64_t)(T + 1) * H); /* h_0 = 0, h_1 .. h_T */
+  L->savedPre = zalloc((int64_t)T * 3 * H);
+  L->gateI = zalloc(H); L->gateF = zalloc(H); L->gateC = zalloc(H); /* u, r, c */
+  L->dI = zalloc(H); L->dC = zalloc(H); L->dx = zalloc(I); L->dhPrev = zalloc(H);
+  L->curGrad = zalloc(H);
+  L->dhNextU = zalloc(H);
+  L->gradInU = zalloc((int64_t)T * I);
+  L->outU = zalloc(H);
+  L->in_len = T * I;
+  L->out_len = H;
+}
+static void gru_init_params(layer *L) {
+  int32_t I = L->spec.in_size, H = L->H;
+  float scale = (float)sqrt(2.0 / ((double)I + (double)H));
+  float *wx = L->params, *wh = wx + (int64_t)3 * H * I, *b = wh + (int64_t)2 * H * H;
+  uint64_t rng = (uint64_t)(I * 1000 + H * 100 + 242);
+  for (int64_t i = 0; i < (int64_t)3 * H * I; i++) wx[i] = gno_rand_float(&rng) * 2 * scale - scale;
+  for (int64_t i = 0; i < (int64_t)2 * H * H; i++) wh[i] = gno_rand_float(&rng) * 2 * scale - scale;
+  for (int32_t i = 0; i < 3 * H; i++) b[i] = 0.0f;
+}
+static void gru_step_forward(layer *L, const float *x, int32_t t) {
+  int32_t I = L->spec.in_size, H = L->H;
+  const float *wx = L->params, *wh = wx + (int64_t)3 * H * I, *b = wh + (int64_t)2 * H * H;
+  const float *h = L->savedH + (int64_t)t * H;
+  float *hn = L->savedH + (int64_t)(t + 1) * H, *pre = L->savedPre + (int64_t)t * 3 * H;
+  memcpy(L->lstmIn, x, sizeof(float) * I);
+  memcpy(pre, b, sizeof(float) * 3 * H);
+  for (int32_t g = 0; g < 3; g++)
+    for (int32_t i = 0; i < H; i++) {
+      float sum = 0.0f;
+      for (int32_t j = 0; j < I; j++) sum += wx[((int64_t)g * H + i) * I + j] * x[j];
+      pre[g * H + i] += sum;
+    }
+  for (int32_t g = 0; g < 2; g++)
+    for (int32_t i = 0; i < H; i++) {
+      float sum = 0.0f;
+      for (int32_t j = 0; j < H; j++) sum += wh[((int64_t)g * H + i) * H + j] * h[j];
+      pre[g * H + i] += sum;
+    }
+  for (int32_t i = 0; i < H; i++) L->gateI[i] = sigmoid32(pre[i]);
+  for (int32_t i = 0; i < H; i++) L->gateF[i] = sigmoid32(pre[H + i]);
+  const float *whr = wh + (int64_t)H * H;
+  for (int32_t i = 0; i < H; i++) {
+    float sum = 0.0f;
+    for (int32_t j = 0; j < H; j++) sum += whr[(int64_t)i * H + j] * (L->gateF[j] * h[j]);
+    pre[2 * H + i] += sum;
+    L->gateC[i] = (float)tanh((double)pre[2 * H + i]);
+  }
+  for (int32_t i = 0; i < H; i++) hn[i] = h[i] + L->gateI[i] * (L->gateC[i] - h[i]);
+}
+static const float *gru_step_backward(layer *L, float *grad, int32_t t) {
+  int32_t I = L->spec.in_size, H = L->H;
+  const float *wx = L->params, *wh = wx + (int64_t)3 * H * I;
+  float *gwx = L->grads, *gwh = gwx + (int64_t)3 * H * I, *gb = gwh + (int64_t)2 * H * H;
+  const float *hp = L->savedH + (int64_t)t * H, *pre = L->savedPre + (int64_t)t * 3 * H;
+  const float *x = L->lstmIn, *whr = wh + (int64_t)H * H;
+  float *u = L->gateI, *r = L->gateF, *c = L->gateC, *dU = L->dI, *dCc = L->dC;
+  for (int32_t i = 0; i < H; i++) {
+    u[i] = sigmoid32(pre[i]);
+    r[i] = sigmoid32(pre[H + i]);
+    c[i] = (float)tanh((double)pre[2 * H + i]);
+  }
+  for (int32_t i = 0; i < H; i++) {
+    float dh = grad[i];
+    float dhc = dh * (1 - u[i]);
+    float du = dh * (c[i] - hp[i]);
+    dU[i] = du * u[i] * (1 - u[i]);
+    dCc[i] = dhc * (1 - c[i] * c[i]);
+  }
+  for (int32_t i = 0; i < H; i++) {
+    for (int32_t j = 0; j < I; j++) gwx[(int64_t)i * I + j] += dU[i] * x[j];
+    gb[i] += dU[i];
+  }
+  for (int32_t i = 0; i < H; i++) {
+    for (int32_t j = 0; j < I; j++) gwx[((int64_t)2 * H + i) * I + j] += dCc[i] * x[j];
+    gb[2 * H + i] += dCc[i];
+  }
+  for (int32_t i = 0; i < H; i++)
+    for (int32_t j = 0; j < H; j++) gwh[(int64_t)i * H + j] += dU[i] * hp[j];
+  for (int32_t i = 0; i < H; i++)
+    for (int32_t j = 0; j < H; j++) gwh[(int64_t)H * H + (int64_t)i * H + j] += dCc[i] * (r[j] * hp[j]);
+  for (int32_t i = 0; i < I; i++) {
+    float sum = 0.0f;
+    for (int32_t j = 0; j < H; j++) sum += wx[(int64_t)j * I + i] * dU[j];
+    for (int32_t j = 0; j < H; j++) sum += wx[((int64_t)2 * H + j) * I + i] * dCc[j];
+    L->dx[i] = sum;
+  }
+  for (int32_t i = 0; i < H; i++) {
+    float sum = 0.0f;
+    for (int32_t j = 0; j < H; j++) sum += wh[(int64_t)j * H + i] * dU[j];
+    for (int32_t j = 0; j < H; j++) sum += whr[(int64_t)j * H + i] * dCc[j] * r[j];
+    sum += grad[i] * u[i];
+    L->dhPrev[i] = sum;
+  }
+  for (int32_t i = 0; i < H; i++) grad[i] += L->dhPrev[i];
+  return L->dx;
+}
+static const float *gru_unroller_forward(layer *L, const float *x) {
+  int32_t I = L->spec.in_size, H = L->H;
+  for (int32_t i = 0; i < H; i++) L->savedH[i] = 0.0f; /* GRU.Reset (gru.go:171-180) */
+  for (int32_t t = 0; t < L->T; t++) gru_step_forward(L, x + (int64_t)t * I, t);
+  memcpy(L->outU, L->savedH + (int64_t)L->T * H, sizeof(float) * H);
+  return L->outU;
+}
+static const float *gru_unroller_backward(layer *L, const float *g) {
+  int32_t I = L->spec.in_size, H = L->H;
+  for (int32_t i = 0; i < H; i++) L->dhNextU[i] = 0.0f;
+  for (int32_t t = L->T - 1; t >= 0; t--) {
+    memcpy(L->curGrad, L->dhNextU, sizeof(float) * H);
+    if (t == L->T - 1)
+      for (int32_t i = 0; i < H; i++) L->curGrad[i] += g[i];
+    const float *dx = gru_step_backward(L, L->curGrad, t);
+    memcpy(L->gradInU + (int64_t)t * I, dx, sizeof(float) * I);
+    memcpy(L->dhNextU, L->curGrad, sizeof(float) * H);
+  }
+  return L->gradInU;
+}
+
+void gno_gru_sequence(const float *x, int32_t I, int32_t H, int32_t T, const float *params,
+                      float *out, const float *g, float *gin, float *gparams) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_GRU_UNROLLER;
+  L.spec.in_size = I;
+  L.spec.out_size = H;
+  L.spec.seq_len = T;
+  gru_build(&L);
+  L.params = (float *)params;
+  L.grads = gparams;
+  memcpy(out, gru_unroller_forward(&L, x), sizeof(float) * H);
+  if (g && gin && gparams) memcpy(gin, gru_unroller_backward(&L, g), sizeof(float) * T * I);
+  float *bufs[] = {L.lstmIn, L.savedH, L.savedPre, L.gateI, L.gateF, L.gateC, L.dI, L.dC, L.dx,
+                   L.dhPrev, L.curGrad, L.dhNextU, L.gradInU, L.outU};
+  for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) free(bufs[i]);
+}
+
+/* ------------------------------------------------------------------------ */
 /* LSTM (lstm.go) wrapped by SequenceUnroller (unroller.go)                  */
 /* ------------------------------------------------------------------------ */
 /* LSTM.Build lstm.go:144-256: params = [Wx (4H x in) | Wh (4H x H) | b (4H)],
@@ -1698,6 +1855,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_RMSNORM: rms_build(L); break;
     case GNO_LAYER_SWIGLU: swiglu_build(L); break;
     case GNO_LAYER_BATCHNORM2D: bn_build(L); break;
+    case GNO_LAYER_GRU_UNROLLER: gru_build(L); break;
     default: break;
   }
 }
@@ -1711,6 +1869,7 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_RMSNORM) rms_init(L);
   else if (L->kind == GNO_LAYER_SWIGLU) swiglu_init(L);
   else if (L->kind == GNO_LAYER_BATCHNORM2D) bn_init(L);
+  else if (L->kind == GNO_LAYER_GRU_UNROLLER) gru_init_params(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -1739,6 +1898,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
     case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
     case GNO_LAYER_BATCHNORM2D: o = bn_forward(L, x, *len_io); break;
+    case GNO_LAYER_GRU_UNROLLER: o = gru_unroller_forward(L, x); *len_io = L->H; break;
     default: o = x;
   }
   return o;
@@ -1759,6 +1919,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_RMSNORM: return rms_backward(L, g);
     case GNO_LAYER_SWIGLU: return swiglu_backward(L, g);
     case GNO_LAYER_BATCHNORM2D: return bn_backward(L, g);
+    case GNO_LAYER_GRU_UNROLLER: return gru_unroller_backward(L, g);
     default: return g;
   }
 }
@@ -1847,6 +2008,7 @@ static int32_t in_len_of(const gno_net *n) {
     case GNO_LAYER_DENSE: return L->spec.in_size;
     case GNO_LAYER_DROPOUT: return L->spec.in_size;
     case GNO_LAYER_LSTM_UNROLLER: return L->T * L->spec.in_size;
+    case GNO_LAYER_GRU_UNROLLER: return L->T * L->spec.in_size;
     case GNO_LAYER_EMBEDDING: return L->T;
     default: return L->spec.in_size;
   }

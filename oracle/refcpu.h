@@ -22,6 +22,7 @@
  *   RMSNorm                           internal/layer/rmsnorm.go:73-96,222-240,301-335
  *   SwiGLU                            internal/layer/swiglu.go:73-232
  *   BatchNorm2D                       internal/layer/batchnorm2d.go:103-135,255-511,524-665
+ *   GRU (in a SequenceUnroller)       internal/layer/gru.go:110-510, unroller.go:57-213
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -71,6 +72,7 @@ enum {
   GNO_LAYER_RMSNORM = 12,
   GNO_LAYER_SWIGLU = 13,
   GNO_LAYER_BATCHNORM2D = 14,
+  GNO_LAYER_GRU_UNROLLER = 15,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -165,6 +167,11 @@ void gno_batchnorm2d(const float *x, int32_t N, int32_t C, int32_t HW, float eps
                      float *rm, float *rv, const float *g, float *gin, float *ggamma_beta);
 /* Running mean / var of BatchNorm2D layer li (C each); returns C or 0. */
 int32_t gno_net_layer_running_stats(gno_net *n, int32_t li, float *mean, float *var);
+/* SequenceUnroller(GRU) of one sample (x: T x I) with params [Wx | Wh | b]:
+ * the last hidden state into out (H); with g, gin and gparams the backward
+ * (gin: T x I, gparams accumulates). */
+void gno_gru_sequence(const float *x, int32_t I, int32_t H, int32_t T, const float *params,
+                      float *out, const float *g, float *gin, float *gparams);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

@@ -21,7 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU = range(8)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D) = range(1, 15)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER) = range(1, 16)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -108,6 +108,8 @@ def lib():
         L.gno_rmsnorm.restype = C.c_int32
         L.gno_swiglu.argtypes = [f32p, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p, f32p]
         L.gno_rope.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32]
+        L.gno_gru_sequence.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p,
+                                       f32p]
         L.gno_batchnorm2d.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_float,
                                       C.c_int32, f32p, C.c_int32, f32p, f32p, f32p, f32p, f32p, f32p]
         L.gno_net_layer_running_stats.argtypes = [C.c_void_p, C.c_int32, f32p, f32p]
@@ -307,6 +309,22 @@ def batchnorm2d(x, N, C, HW, training=True, gamma_beta=None, rm=None, rv=None, g
     if gg is None:
         return out, rm, rv
     return out, rm, rv, gin, ggb
+
+
+def gru_sequence(x, I, H, T, params, g=None):
+    """SequenceUnroller(GRU) of one sample; returns h_T, or (h_T, grad_x,
+    grad_params) when g (dL/dh_T) is given."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    params = np.ascontiguousarray(params, np.float32).ravel()
+    out = np.empty(H, np.float32)
+    if g is None:
+        lib().gno_gru_sequence(fptr(x), I, H, T, fptr(params), fptr(out), None, None, None)
+        return out
+    g = np.ascontiguousarray(g, np.float32).ravel()
+    gin = np.empty(T * I, np.float32)
+    gp = np.zeros(params.size, np.float32)
+    lib().gno_gru_sequence(fptr(x), I, H, T, fptr(params), fptr(out), fptr(g), fptr(gin), fptr(gp))
+    return out, gin, gp
 
 
 def rope(x, T, nh, hd, conj=False):

@@ -47,6 +47,9 @@ def oracle_specs(refcpu, cfg):
                                      use_rope=int(bool(d.get("rope", False)))))
         elif k == "clspool":
             specs.append(refcpu.spec(refcpu.LAYER_CLSPOOL, seq_len=d["T"], dim=d["dim"]))
+        elif k == "gru":
+            specs.append(refcpu.spec(refcpu.LAYER_GRU_UNROLLER, in_size=d["in"], out_size=d["hidden"],
+                                     seq_len=d["T"]))
         elif k == "lstm":
             specs.append(refcpu.spec(refcpu.LAYER_LSTM_UNROLLER, in_size=d["in"], out_size=d["hidden"],
                                      seq_len=d["T"]))

@@ -429,6 +429,24 @@ def test_batchnorm2d_net(gn, oracle, case):
     assert not m2.any() and (v2 == 4).all()
 
 
+@pytest.mark.parametrize("B,T,inp,hidden,workers", [(7, 9, 5, 24, 1), (11, 12, 16, 64, 3),
+                                                    (64, 100, 64, 256, 4)])
+def test_gru_sequence(gn, oracle, B, T, inp, hidden, workers):
+    """SequenceUnroller(GRU) (gru.go, unroller.go) + Dense MSE: gradients of
+    [Wx | Wh | b] (the reset rows of Wx / b stay 0, the candidate's use of the
+    reset block lands in Wh_r), Adam state and weights over 2 steps; the last
+    case is C5's shape; then inference."""
+    from goneuron_amd import configs
+    cfg = configs.gru(B=B, T=T, inp=inp, hidden=hidden)
+    model, net = _compare_step(gn, oracle, cfg, steps=2, workers=workers)
+    x, _ = configs.inputs(cfg)
+    net.params[:] = model.Params()
+    net.set_training(False)
+    out = model.PredictBatch(x)
+    ref = np.stack([net.forward(x[b])[:out.shape[1]] for b in range(B)])
+    assert max_rel(out, ref) <= TOL, max_rel(out, ref)
+
+
 def configs_inputs(cfg):
     from goneuron_amd import configs
     return configs.inputs(cfg)

@@ -398,6 +398,129 @@ def test_batchnorm2d_backward_vs_autograd_and_running_stats(oracle):
     np.testing.assert_allclose(inf, ref.ravel(), rtol=1e-5, atol=1e-5)
 
 
+def _gru_np(x, I, H, T, p):
+    """float64 forward of the reference GRU (gru.go:182-262): candidate on the
+    reset gate's recurrent block; returns hs [T+1, H] and gates per step."""
+    p = p.astype(np.float64)
+    Wx = p[:3 * H * I].reshape(3 * H, I)
+    Wh = p[3 * H * I:3 * H * I + 2 * H * H].reshape(2 * H, H)
+    b = p[3 * H * I + 2 * H * H:]
+    xs = np.asarray(x, np.float64).reshape(T, I)
+    hs, gates = [np.zeros(H)], []
+    for t in range(T):
+        h = hs[-1]
+        pre = b + Wx @ xs[t]
+        pre[:2 * H] += Wh @ h
+        u, r = 1 / (1 + np.exp(-pre[:H])), 1 / (1 + np.exp(-pre[H:2 * H]))
+        c = np.tanh(pre[2 * H:] + Wh[H:] @ (r * h))
+        hs.append(h + u * (c - h))
+        gates.append((u, r, c))
+    return np.array(hs), gates
+
+
+def test_gru_params_init_and_single_step_autograd(oracle):
+    """gru_test.go:63-90 (3*8*4 + 2*8*8 + 3*8 parameters); Build's LCG stream
+    (seed I*1000 + H*100 + 242) over Wx then Wh, zero biases.  One step from
+    h0 = 0 (the reset gate cannot act, the last input is the only one) against
+    torch autograd in float64: the update-gate gradients are exact; the
+    candidate's are those of (1 - u) c, though the forward computes
+    h + u (c - h) — the backward follows the convention h' = (1 - u) c + u h
+    of the comment at gru.go:255-256."""
+    torch = pytest.importorskip("torch")
+    net = oracle.Net([oracle.spec(oracle.LAYER_GRU_UNROLLER, in_size=4, out_size=8, seq_len=3),
+                      oracle.spec(oracle.LAYER_DENSE, in_size=8, out_size=1, act=oracle.ACT_LINEAR)],
+                     oracle.LOSS_MSE)
+    assert net.layer_slice(0).stop == 3 * 8 * 4 + 2 * 8 * 8 + 3 * 8
+    seed, sc = 4 * 1000 + 8 * 100 + 242, np.float32(math.sqrt(2.0 / 12.0))
+    want = []
+    for _ in range(3 * 8 * 4 + 2 * 8 * 8):
+        seed = (seed * 6364136223846793005 + 1) & (2**64 - 1)
+        want.append(np.float32(seed >> 33) / np.float32(2**31) * np.float32(2) * sc - sc)
+    got = net.params[net.layer_slice(0)]
+    np.testing.assert_array_equal(got[:len(want)], np.array(want, np.float32))
+    assert not got[len(want):].any()
+    rng = np.random.default_rng(17)
+    I, H = 5, 6
+    p = (rng.normal(size=3 * H * I + 2 * H * H + 3 * H) * 0.5).astype(np.float32)
+    x = rng.normal(size=I).astype(np.float32)
+    g = rng.normal(size=H).astype(np.float32)
+    out, gin, gp = oracle.gru_sequence(x, I, H, 1, p, g=g)
+
+    def model(swap_candidate):
+        P = torch.tensor(p.astype(np.float64), requires_grad=True)
+        X = torch.tensor(x.astype(np.float64), requires_grad=True)
+        Wx = P[:3 * H * I].view(3 * H, I)
+        b = P[3 * H * I + 2 * H * H:]
+        pre = b + Wx @ X
+        u = torch.sigmoid(pre[:H])
+        c = torch.tanh(pre[2 * H:])          # r * h0 = 0: the reset gate cannot act
+        if swap_candidate:                   # the candidate weighted by (1 - u), u held fixed
+            hn = (1 - u.detach()) * c
+        else:
+            hn = u * c                       # h0 + u (c - h0) with h0 = 0
+        hn.backward(torch.tensor(g.astype(np.float64)))
+        return hn.detach().numpy(), P.grad.numpy(), X.grad.numpy()
+
+    h_true, gp_true, gx_true = model(False)
+    _, gp_swap, gx_swap = model(True)
+    np.testing.assert_allclose(out, h_true, rtol=1e-5, atol=1e-6)
+    # update gate: the exact gradient (dU = dh (c - h_prev) u (1 - u), gru.go:414-424)
+    sl_u = np.r_[0:H * I, 3 * H * I + 2 * H * H:3 * H * I + 2 * H * H + H]
+    np.testing.assert_allclose(gp[sl_u], gp_true[sl_u], rtol=1e-4, atol=1e-6)
+    # candidate: dh (1 - u) (1 - c^2) (gru.go:408-411, 426-430), the gradient of
+    # (1 - u) c although the forward computes h + u (c - h)
+    sl_c = np.r_[2 * H * I:3 * H * I, 3 * H * I + 2 * H * H + 2 * H:3 * H * I + 2 * H * H + 3 * H]
+    np.testing.assert_allclose(gp[sl_c], gp_swap[sl_c], rtol=1e-4, atol=1e-6)
+    assert not np.allclose(gp[sl_c], gp_true[sl_c], rtol=1e-3)
+    # input gradient: the update part of the exact one plus the candidate part of the swapped one
+    gx_u = gx_true - torch_gx_part(torch, p, x, g, I, H, "c", swap=False)
+    np.testing.assert_allclose(gin, gx_u + torch_gx_part(torch, p, x, g, I, H, "c", swap=True),
+                               rtol=1e-4, atol=1e-6)
+    # the reset gate gets nothing
+    assert not gp[H * I:2 * H * I].any()
+
+
+def torch_gx_part(torch, p, x, g, I, H, which, swap):
+    """d(g . h1)/dx through the candidate path only (u held fixed)."""
+    P = torch.tensor(p.astype(np.float64))
+    X = torch.tensor(x.astype(np.float64), requires_grad=True)
+    Wx = P[:3 * H * I].view(3 * H, I)
+    b = P[3 * H * I + 2 * H * H:]
+    u = torch.sigmoid(b[:H] + Wx[:H] @ X).detach()
+    c = torch.tanh(b[2 * H:] + Wx[2 * H:] @ X)
+    hn = ((1 - u) if swap else u) * c
+    hn.backward(torch.tensor(g.astype(np.float64)))
+    return X.grad.numpy()
+
+
+def test_gru_sequence_structure(oracle):
+    """T = 7: the forward equals the float64 restatement of gru.go:182-262
+    (candidate on the reset block); the reference backward's structure: the
+    reset gate's input weights and bias never receive gradient (its delta is
+    never computed), the update / candidate input-weight gradients are
+    outer products with the last step's input (inputBuf), the backward is
+    linear in the upstream gradient, and at T = 1 it matches the per-step
+    formula dh_prev = Wh_u^T dU + Wh_r^T (dC r) + dh u."""
+    rng = np.random.default_rng(23)
+    I, H, T = 4, 5, 7
+    p = (rng.normal(size=3 * H * I + 2 * H * H + 3 * H) * 0.5).astype(np.float32)
+    x = rng.normal(size=T * I).astype(np.float32)
+    g1, g2 = rng.normal(size=H).astype(np.float32), rng.normal(size=H).astype(np.float32)
+    out, gin1, gp1 = oracle.gru_sequence(x, I, H, T, p, g=g1)
+    hs, _ = _gru_np(x, I, H, T, p)
+    np.testing.assert_allclose(out, hs[-1], rtol=1e-5, atol=1e-6)
+    gWx = gp1[:3 * H * I].reshape(3 * H, I)
+    gb = gp1[3 * H * I + 2 * H * H:]
+    assert not gWx[H:2 * H].any() and not gb[H:2 * H].any()
+    xl = x[-I:].astype(np.float64)
+    for blk, bb in ((gWx[:H], gb[:H]), (gWx[2 * H:], gb[2 * H:])):
+        np.testing.assert_allclose(blk, np.outer(bb, xl), rtol=1e-4, atol=1e-6)
+    _, gin2, gp2 = oracle.gru_sequence(x, I, H, T, p, g=g2)
+    _, gin3, gp3 = oracle.gru_sequence(x, I, H, T, p, g=g1 + g2)
+    np.testing.assert_allclose(gp3, gp1 + gp2, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(gin3, gin1 + gin2, rtol=1e-4, atol=1e-5)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
