@@ -22,7 +22,7 @@ from ._lib import GNError, LayerDesc, AdamDesc, check, lib
 
 __all__ = [
     "NewSequential", "Sequential", "Dense", "DenseE", "Dropout", "Flatten", "Conv2D", "MaxPool2D",
-    "AvgPool2D", "BatchNorm2D", "RMSNorm", "SwiGLU", "Embedding", "PositionalEncoding", "TransformerBlock",
+    "AvgPool2D", "BatchNorm2D", "RMSNorm", "SwiGLU", "MoE", "Embedding", "PositionalEncoding", "TransformerBlock",
     "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
     "LSTM", "GRU", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
@@ -65,7 +65,7 @@ def Ref(act: Activation) -> Activation:
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER) = range(1, 16)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE) = range(1, 17)
 
 
 class Layer:
@@ -184,6 +184,20 @@ def SwiGLU(out, *in_size):
     if out <= 0:
         raise GNError(-1, f"invalid outSize {out}: must be > 0")
     return Layer(LAYER_SWIGLU, in_size=int(in_size[0]), out_size=int(out))
+
+
+def MoE(out, num_experts, k, *in_size):
+    """goneuron.MoE (goneuron.go:398-405): a Linear gating Dense and
+    num_experts Dense(in, out, LeakyReLU 0.1) experts, top-k routing by the
+    gate softmax, all parameters starting at 0 (moe.go:122-135).  Training
+    mode adds the RNG(42) gate noise and the load-balancing gradient.  The
+    lazy form is rejected (the input size must be known)."""
+    if not in_size or in_size[0] <= 0:
+        raise GNError(-1, "MoE needs an input size")
+    if out <= 0 or num_experts <= 0 or not (0 < k <= num_experts):
+        raise GNError(-1, f"invalid MoE sizes out={out} experts={num_experts} k={k}")
+    return Layer(LAYER_MOE, in_size=int(in_size[0]), out_size=int(out), num_experts=int(num_experts),
+                 top_k=int(k))
 
 
 def Embedding(num, dim):

@@ -36,6 +36,7 @@ class LayerDesc(C.Structure):
         ("return_sequences", C.c_int32), ("eps", C.c_float),
         ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
         ("momentum", C.c_float), ("no_affine", C.c_int32),
+        ("num_experts", C.c_int32), ("top_k", C.c_int32),
     ]
 
 

@@ -9,7 +9,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, BatchNorm2D, RMSNorm,
+from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, BatchNorm2D, MoE,
+               RMSNorm,
                SwiGLU, Flatten, TransformerBlockExt, ActReLU, ActSwiGLU, ActGELU, NormLN, NormRMS,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, GRU, SequenceUnroller, ReLU,
@@ -122,6 +123,8 @@ def product_layers(cfg):
             out.append(RMSNorm(d["n"]))
         elif k == "batchnorm2d":
             out.append(BatchNorm2D(d["C"]))
+        elif k == "moe":
+            out.append(MoE(d["out"], d["E"], d["k"], d["in"]))
         elif k == "swiglu":
             out.append(SwiGLU(d["out"], d["in"]))
         elif k == "embedding":

@@ -42,6 +42,7 @@ enum FwdKind : int32_t {
   F_SIGMOID = 2,
   F_TANH = 3,
   F_NAN = 4,      // scalar Activate of Softmax/LogSoftmax values (Conv2D only)
+  F_LEAKY = 5,    // *LeakyReLU with alpha 0.1 (the MoE experts)
 };
 
 struct GemmArgs {
@@ -137,6 +138,21 @@ hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const 
                          float *part, int B, int C, int HW, hipStream_t s);
 hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
 hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
+
+// ---- MoE ----
+constexpr int MOE_MAX_E = 64;  // experts routed by one thread's registers
+struct MoeRoute {
+  int B, E, K, training;
+  int chunk;              // worker chunk (streams 1 + b / chunk), 0: one stream
+  uint64_t base[65];      // noise stream states at the start of this forward
+};
+hipError_t launch_moe_route(const float *logits, float *prob, int32_t *act, const MoeRoute &rt,
+                            hipStream_t s);
+hipError_t launch_moe_combine(const float *eout, const float *prob, const int32_t *act, float *y,
+                              int B, int O, int E, int K, hipStream_t s);
+hipError_t launch_moe_backward_deltas(const float *g, const float *eout, const float *prob,
+                                      const int32_t *act, float *edz, float *dzg, int B, int O,
+                                      int E, int K, int training, hipStream_t s);
 
 // ---- SequenceUnroller(GRU) ----
 bool gru_supported(int H);

@@ -534,6 +534,13 @@ struct LayerRT {
   // SequenceUnroller(GRU): pre-activations [B*T][3H], h before each step and
   // r * h_prev [B*T][H] (xw, WhT, Dg, S as for the LSTM, sized for 3 gates)
   float *gpre = nullptr, *ghprev = nullptr, *grh = nullptr;
+  // MoE: E experts, top K; gate logits / probabilities / deltas [B][E], routes
+  // [B][K], expert outputs and deltas [E][B][O]; noise stream states (the
+  // network's own, then one per worker clone), advanced on the host
+  int E = 0, K = 0;
+  float *mlog = nullptr, *mprob = nullptr, *mdzg = nullptr, *meout = nullptr, *medz = nullptr;
+  int32_t *mact = nullptr;
+  std::vector<uint64_t> mrng;
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
@@ -869,6 +876,18 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.pcount = 2 * (int64_t)R.d.in_size * R.d.out_size;
         R.out_len = R.d.out_size;
         break;
+      case GN_LAYER_MOE:  // moe.go:47-138: [gating W (E x I), b | per expert W (O x I), b]
+        R.E = R.d.num_experts;
+        R.K = R.d.top_k;
+        if (R.d.in_size != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: MoE in %d != incoming %d", i, R.d.in_size, len);
+        if (R.d.out_size <= 0 || R.E <= 0 || R.E > MOE_MAX_E || R.K <= 0 || R.K > R.E)
+          return set_err(c, GN_ERR_INVALID, "layer %d: bad MoE sizes (experts <= %d, 0 < k <= experts)",
+                         i, MOE_MAX_E);
+        R.pcount = (int64_t)R.E * R.d.in_size + R.E +
+                   (int64_t)R.E * ((int64_t)R.d.out_size * R.d.in_size + R.d.out_size);
+        R.out_len = R.d.out_size;
+        break;
       case GN_LAYER_GRU_UNROLLER:  // gru.go:110-167: [Wx 3H x I | Wh 2H x H | b 3H]
         R.T = R.d.seq_len;
         R.I = R.d.in_size;
@@ -1010,6 +1029,20 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
+    }
+    if (R.d.kind == GN_LAYER_MOE) {
+      // parameters stay 0: Build rebinds the gating and expert layers to one
+      // fresh zero block (moe.go:122-135)
+      const size_t Bm = max_batch, E = R.E, O = R.d.out_size;
+      float *tmp = nullptr;
+      if ((rc = model_alloc(M.get(), Bm * E, &R.mlog))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * E, &R.mprob))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * E, &R.mdzg))) return rc;
+      if ((rc = model_alloc(M.get(), E * Bm * O, &R.meout))) return rc;
+      if ((rc = model_alloc(M.get(), E * Bm * O, &R.medz))) return rc;
+      if ((rc = model_alloc(M.get(), Bm * R.K, &tmp))) return rc;
+      R.mact = reinterpret_cast<int32_t *>(tmp);
+      R.mrng.assign(65, 42);  // NewRNG(42) in the layer and in every worker clone
     }
     if (R.d.kind == GN_LAYER_GRU_UNROLLER) {
       init_gru(host.data() + R.poff, R.I, R.H);
@@ -1467,6 +1500,40 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, launch_swiglu_fwd(R.zbuf, R.out, B, R.d.out_size, c->stream));
         break;
       }
+      case GN_LAYER_MOE: {
+        const int I = R.d.in_size, O = R.d.out_size, E = R.E, K = R.K;
+        const float *P = M->params + R.poff;
+        const int64_t e1 = (int64_t)O * I + O;
+        HIP_OK(c, gemm_nt(c, cur, P, P + (int64_t)E * I, R.mlog, B, E, I, EPI_BIAS_ACT, F_IDENTITY,
+                          nullptr));
+        MoeRoute rt{};
+        rt.B = B; rt.E = E; rt.K = K; rt.training = M->training;
+        const int W = std::min(M->workers, B);
+        if (M->workers > 1) rt.chunk = (B + W - 1) / W;  // trainBatchParallel chunks
+        for (int k = 0; k < 65; ++k) rt.base[k] = R.mrng[k];
+        {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_moe_route(R.mlog, R.mprob, R.mact, rt, c->stream));
+        }
+        for (int e = 0; e < E; ++e) {  // every expert on every sample; the route picks k of them
+          const float *We = P + (int64_t)E * I + E + e * e1;
+          HIP_OK(c, gemm_nt(c, cur, We, We + (int64_t)O * I, R.meout + (int64_t)e * B * O, B, O, I,
+                            EPI_BIAS_ACT, F_LEAKY, nullptr));
+        }
+        KTimer kt(c, GN_KCLASS_OTHER);
+        HIP_OK(c, launch_moe_combine(R.meout, R.mprob, R.mact, R.out, B, O, E, K, c->stream));
+        if (M->training) {  // E draws per sample on its stream
+          if (M->workers > 1) {
+            for (int w = 0; w < W; ++w) {
+              const int n = std::max(0, std::min(rt.chunk, B - w * rt.chunk));
+              for (int64_t d = 0; d < (int64_t)n * E; ++d) R.mrng[1 + w] = R.mrng[1 + w] * 6364136223846793005ull + 1;
+            }
+          } else {
+            for (int64_t d = 0; d < (int64_t)B * E; ++d) R.mrng[0] = R.mrng[0] * 6364136223846793005ull + 1;
+          }
+        }
+        break;
+      }
       case GN_LAYER_GRU_UNROLLER: {
         const int H = R.H, G3 = 3 * H;
         const float *Wx = M->params + R.poff;
@@ -1644,6 +1711,34 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         HIP_OK(c, dense_bwd_core(c, in, M->params + R.poff, R.dzbuf, M->grads + R.poff, nullptr, gin,
                                  B, R.d.in_size, 2 * R.d.out_size, scale, aux, deriv));
         is_dz = next_dz;
+        break;
+      }
+      case GN_LAYER_MOE: {  // moe.go:242-313
+        const int I = R.d.in_size, O = R.d.out_size, E = R.E, K = R.K;
+        const float *P = M->params + R.poff;
+        float *G = M->grads + R.poff;
+        const int64_t e1 = (int64_t)O * I + O;
+        {
+          KTimer kt(c, GN_KCLASS_OTHER);
+          HIP_OK(c, launch_moe_backward_deltas(R.gout, R.meout, R.mprob, R.mact, R.medz, R.mdzg, B, O, E,
+                                               K, M->training, c->stream));
+        }
+        // gating and expert Dense backward: W grads = scale dz^T x, b grads = scale colsum(dz)
+        HIP_OK(c, dense_bwd_core(c, in, P, R.mdzg, G, G + (int64_t)E * I, nullptr, B, I, E, scale,
+                                 nullptr, 0));
+        for (int e = 0; e < E; ++e) {
+          float *gW = G + (int64_t)E * I + E + e * e1;
+          HIP_OK(c, dense_bwd_core(c, in, nullptr, R.medz + (int64_t)e * B * O, gW, gW + (int64_t)O * I,
+                                   nullptr, B, I, O, scale, nullptr, 0));
+        }
+        if (below && below->gout) {  // dx = dz_gate Wg + sum_e dz_e W_e
+          float *gin = below->gout;
+          HIP_OK(c, gemm_nn(c, R.mdzg, P, gin, B, I, E, EPI_SCALE, 0, nullptr, 0));
+          for (int e = 0; e < E; ++e)
+            HIP_OK(c, gemm_nn(c, R.medz + (int64_t)e * B * O, P + (int64_t)E * I + E + e * e1, gin, B, I,
+                              O, EPI_BIAS_ADD, 0, gin, 0));
+        }
+        is_dz = false;
         break;
       }
       case GN_LAYER_GRU_UNROLLER: {  // gru.go:347-510 per step, unroller.go:189-206

@@ -59,6 +59,7 @@ __device__ __forceinline__ float apply_fwd(float v, int kind) {
     case F_SIGMOID: return 1.0f / (1.0f + (float)exp((double)(-v)));
     case F_TANH: return (float)tanh((double)v);
     case F_NAN: return __builtin_nanf("");
+    case F_LEAKY: return v > 0.0f ? v : 0.1f * v;
     default: return v;
   }
 }

@@ -66,6 +66,7 @@ extern "C" {
 #define GN_LAYER_SWIGLU 13       /* layer.NewSwiGLU           swiglu.go:47 */
 #define GN_LAYER_BATCHNORM2D 14  /* layer.NewBatchNorm2D      batchnorm2d.go:70 */
 #define GN_LAYER_GRU_UNROLLER 15 /* SequenceUnroller(GRU)     unroller.go:57, gru.go:83 */
+#define GN_LAYER_MOE 16          /* layer.NewMoE              moe.go:47 */
 
 /* TransformerBlockExt options (layer.ActivationType, layer.NormType) */
 #define GN_BLOCK_ACT_RELU 0
@@ -95,6 +96,8 @@ typedef struct gn_layer_desc {
   int32_t use_rope;     /* TransformerBlock: rotary embeddings on Q and K (transformer.go:212-236) */
   float momentum;       /* BatchNorm2D running-stat momentum, as given (the facade passes 0.1) */
   int32_t no_affine;    /* BatchNorm2D without gamma / beta (NewBatchNorm2D affine = false) */
+  int32_t num_experts;  /* MoE experts (<= 64) */
+  int32_t top_k;        /* MoE experts per sample */
 } gn_layer_desc;
 
 typedef struct gn_adam_desc {   /* opt.NewAdam opt.go:117-126 */

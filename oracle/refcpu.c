@@ -65,6 +65,7 @@ float gno_activate(int32_t act, float x) {
     case GNO_ACT_SOFTMAX:                                 /* :150-152 */
     case GNO_ACT_LOGSOFTMAX: return NAN;                  /* :192-194 */
     case GNO_ACT_LINEAR: return x;                        /* :345-347 */
+    case GNO_ACT_LEAKYRELU: return x > 0 ? x : 0.1f * x;  /* :74-79, alpha float32(0.1) */
     case GNO_ACT_GELU: {                                  /* :244-254 */
       float x3 = x * x * x;
       float arg = (float)0.7978845608028654 * (x + 0.044715f * x3);
@@ -89,6 +90,7 @@ float gno_derivative(int32_t act, float x) {
     case GNO_ACT_SOFTMAX:
     case GNO_ACT_LOGSOFTMAX: return NAN;                  /* :156-158, :198-200 */
     case GNO_ACT_LINEAR: return 1.0f;                     /* :350-352 */
+    case GNO_ACT_LEAKYRELU: return x > 0 ? 1.0f : 0.1f;   /* :83-88 */
     case GNO_ACT_GELU: {                                  /* :258-272, in float64 */
       double xd = (double)x, x2 = xd * xd, x3 = xd * x2;
       double arg = 0.7978845608028654 * (xd + 0.044715 * x3);
@@ -124,7 +126,7 @@ void gno_activate_batch(int32_t act, float *x, int32_t n) {
 
 /* cacheActivationType layer.go:183-205: pointer-only cases for Softmax and
  * LogSoftmax; everything else not listed is ActTypeNone. */
-enum { AT_NONE = 0, AT_RELU, AT_SIGMOID, AT_TANH, AT_SOFTMAX, AT_LOGSOFTMAX, AT_GELU };
+enum { AT_NONE = 0, AT_RELU, AT_SIGMOID, AT_TANH, AT_SOFTMAX, AT_LOGSOFTMAX, AT_GELU, AT_LEAKY };
 static int cache_act_type(int32_t act, int32_t is_ptr) {
   switch (act) {
     case GNO_ACT_RELU: return AT_RELU;
@@ -133,6 +135,7 @@ static int cache_act_type(int32_t act, int32_t is_ptr) {
     case GNO_ACT_SOFTMAX: return is_ptr ? AT_SOFTMAX : AT_NONE;
     case GNO_ACT_LOGSOFTMAX: return is_ptr ? AT_LOGSOFTMAX : AT_NONE;
     case GNO_ACT_GELU: return is_ptr ? AT_GELU : AT_NONE; /* only *activations.GELU */
+    case GNO_ACT_LEAKYRELU: return is_ptr ? AT_LEAKY : AT_NONE; /* only *activations.LeakyReLU */
     default: return AT_NONE;
   }
 }
@@ -242,6 +245,11 @@ struct layer {
   /* BatchNorm2D */
   float *runMean, *runVar, *bnMean, *bnVar, *bnStd;
   int32_t bnN, bnHW;
+  /* MoE: sub[0] gating, sub[1 + e] experts; one noise stream per worker clone */
+  float *moeLogits, *moeProbs, *moeW, *moeOut, *moeGate;
+  int32_t *moeActive;
+  uint64_t moeRng[64];
+  int32_t *curWorker; /* the net's active worker index */
   float *aq, *ak, *av, *scores, *fin, *gfin, *gq, *gk, *gv, *attOut, *res1, *n1, *ffOut, *res2,
       *blkOut, *gRes2, *gN1ff, *comb, *gRes1, *gInAtt, *tmpRow, *probs, *dpre;
 };
@@ -256,6 +264,7 @@ struct gno_net {
   float *worker_grads; /* workers x nparams when workers > 1 */
   float lr;
   int32_t timestep;
+  int32_t cur_worker; /* worker chunk being run (MoE noise streams) */
   float *lossGrad;
   int32_t max_width;
 };
@@ -1022,6 +1031,144 @@ void gno_batchnorm2d(const float *x, int32_t N, int32_t C, int32_t HW, float eps
   if (training && g && gin) memcpy(gin, bn_backward(&L, g), sizeof(float) * N * C * HW);
   free(L.outputBuf); free(L.savedInput); free(L.gradInBuf);
   free(L.runMean); free(L.runVar); free(L.bnMean); free(L.bnVar); free(L.bnStd);
+}
+
+static void dense_sub_build(layer *S, int32_t in, int32_t out, int32_t act);
+
+/* ------------------------------------------------------------------------ */
+/* MoE (moe.go)                                                               */
+/* ------------------------------------------------------------------------ */
+/* NewMoE / Build moe.go:47-138: gating Dense(in, E, Linear{}), E experts
+ * Dense(in, out, NewLeakyReLU(0.1)); Build rebinds all of them to one freshly
+ * allocated (zero) parameter block [gating W, b | expert 0 W, b | ...], so
+ * every MoE parameter starts at 0.  Forward moe.go:140-236: logits =
+ * gating(x); in training mode each logit gets (u*2 - 1)*0.05 from the
+ * instance's RNG(42) (never reset: the stream runs on across samples and
+ * steps; each trainBatchParallel worker clone owns its own, net.go:129-152);
+ * softmax with float64 exp; sort.Slice by descending probability (Go's
+ * pdqsort sorts <= 12 elements by insertion, which keeps ties in index
+ * order); out = sum over the top k (in that order) of expert_out * p.
+ * Backward moe.go:242-313: each active expert gets grad * p through its Dense
+ * backward; gate grad = grad . expert_out for active experts, + 0.2 (p - 1/E)
+ * for every expert in training mode; softmax backward; gating backward; the
+ * input gradient sums the experts' (in order) and the gating's. */
+static void moe_build(layer *L) {
+  int32_t I = L->spec.in_size, O = L->spec.out_size, E = L->spec.num_experts, K = L->spec.top_k;
+  L->sub = (layer *)calloc((size_t)E + 1, sizeof(layer));
+  dense_sub_build(&L->sub[0], I, E, GNO_ACT_LINEAR);
+  for (int32_t e = 0; e < E; e++) {
+    dense_sub_build(&L->sub[1 + e], I, O, GNO_ACT_LEAKYRELU);
+    L->sub[1 + e].spec.act_is_ptr = 1;
+    L->sub[1 + e].act_type = cache_act_type(GNO_ACT_LEAKYRELU, 1);
+  }
+  L->nparams = (int64_t)E * I + E + (int64_t)E * ((int64_t)O * I + O);
+  L->moeLogits = zalloc(E); L->moeProbs = zalloc(E); L->moeW = zalloc(K);
+  L->moeOut = zalloc((int64_t)E * O); L->moeGate = zalloc(E);
+  L->moeActive = (int32_t *)calloc((size_t)K, sizeof(int32_t));
+  L->outputBuf = zalloc(O); L->gradInBuf = zalloc(I); L->dzBuf = zalloc(O);
+  for (int w = 0; w < 64; w++) L->moeRng[w] = 42;
+  L->in_len = I;
+  L->out_len = O;
+}
+static void moe_bind(layer *L) {
+  int32_t I = L->spec.in_size, O = L->spec.out_size, E = L->spec.num_experts;
+  int64_t off = 0, g = (int64_t)E * I + E, e1 = (int64_t)O * I + O;
+  L->sub[0].params = L->params; L->sub[0].grads = L->grads; off = g;
+  for (int32_t e = 0; e < E; e++, off += e1) {
+    L->sub[1 + e].params = L->params + off;
+    L->sub[1 + e].grads = L->grads + off;
+  }
+}
+static void moe_init(layer *L) {
+  for (int64_t i = 0; i < L->nparams; i++) L->params[i] = 0.0f;
+}
+static const float *moe_forward(layer *L, const float *x) {
+  int32_t O = L->spec.out_size, E = L->spec.num_experts, K = L->spec.top_k;
+  int w = L->curWorker ? *L->curWorker : 0;
+  memcpy(L->moeLogits, dense_forward(&L->sub[0], x), sizeof(float) * E);
+  if (L->training)
+    for (int32_t i = 0; i < E; i++) L->moeLogits[i] += (gno_rand_float(&L->moeRng[w]) * 2 - 1) * 0.05f;
+  float mx = L->moeLogits[0];
+  for (int32_t i = 1; i < E; i++)
+    if (L->moeLogits[i] > mx) mx = L->moeLogits[i];
+  float sum = 0.0f;
+  for (int32_t i = 0; i < E; i++) {
+    L->moeProbs[i] = (float)exp((double)(L->moeLogits[i] - mx));
+    sum += L->moeProbs[i];
+  }
+  for (int32_t i = 0; i < E; i++) L->moeProbs[i] /= sum;
+  /* stable descending order by probability */
+  int32_t order[1024];
+  for (int32_t i = 0; i < E; i++) order[i] = i;
+  for (int32_t i = 1; i < E; i++)
+    for (int32_t j = i; j > 0 && L->moeProbs[order[j]] > L->moeProbs[order[j - 1]]; j--) {
+      int32_t t = order[j]; order[j] = order[j - 1]; order[j - 1] = t;
+    }
+  for (int32_t j = 0; j < O; j++) L->outputBuf[j] = 0.0f;
+  for (int32_t r = 0; r < K; r++) {
+    int32_t idx = order[r];
+    L->moeActive[r] = idx;
+    float wt = L->moeProbs[idx];
+    L->moeW[r] = wt;
+    const float *eo = dense_forward(&L->sub[1 + idx], x);
+    memcpy(L->moeOut + (int64_t)idx * O, eo, sizeof(float) * O);
+    for (int32_t j = 0; j < O; j++) L->outputBuf[j] += eo[j] * wt;
+  }
+  return L->outputBuf;
+}
+static const float *moe_backward(layer *L, const float *grad) {
+  int32_t I = L->spec.in_size, O = L->spec.out_size, E = L->spec.num_experts, K = L->spec.top_k;
+  for (int32_t i = 0; i < I; i++) L->gradInBuf[i] = 0.0f;
+  for (int32_t i = 0; i < E; i++) L->moeGate[i] = 0.0f;
+  for (int32_t r = 0; r < K; r++) {
+    int32_t idx = L->moeActive[r];
+    float wt = L->moeProbs[idx];
+    for (int32_t i = 0; i < O; i++) L->dzBuf[i] = grad[i] * wt;
+    const float *dx = dense_backward(&L->sub[1 + idx], L->dzBuf);
+    for (int32_t i = 0; i < I; i++) L->gradInBuf[i] += dx[i];
+    float dot = 0.0f;
+    for (int32_t i = 0; i < O; i++) dot += grad[i] * L->moeOut[(int64_t)idx * O + i];
+    L->moeGate[idx] = dot;
+  }
+  if (L->training) {
+    float lambda = 0.1f, target = 1.0f / (float)E;
+    for (int32_t i = 0; i < E; i++) L->moeGate[i] += 2 * lambda * (L->moeProbs[i] - target);
+  }
+  float sp = 0.0f;
+  for (int32_t i = 0; i < E; i++) sp += L->moeProbs[i] * L->moeGate[i];
+  for (int32_t i = 0; i < E; i++) L->moeGate[i] = L->moeProbs[i] * (L->moeGate[i] - sp);
+  const float *dg = dense_backward(&L->sub[0], L->moeGate);
+  for (int32_t i = 0; i < I; i++) L->gradInBuf[i] += dg[i];
+  return L->gradInBuf;
+}
+
+int32_t gno_moe(const float *x, int32_t I, int32_t O, int32_t E, int32_t K, const float *params,
+                int32_t training, uint64_t *rng, float *out, int32_t *active, const float *g,
+                float *gin, float *gparams) {
+  layer L;
+  memset(&L, 0, sizeof L);
+  L.kind = GNO_LAYER_MOE;
+  L.spec.in_size = I; L.spec.out_size = O; L.spec.num_experts = E; L.spec.top_k = K;
+  if (K <= 0 || K > E || E > 1024) return -1;
+  moe_build(&L);
+  L.training = training;
+  L.params = (float *)params;
+  L.grads = gparams;
+  moe_bind(&L);
+  L.moeRng[0] = *rng;
+  memcpy(out, moe_forward(&L, x), sizeof(float) * O);
+  memcpy(active, L.moeActive, sizeof(int32_t) * K);
+  *rng = L.moeRng[0];
+  if (g && gin && gparams) memcpy(gin, moe_backward(&L, g), sizeof(float) * I);
+  for (int32_t e = 0; e <= E; e++) {
+    layer *S = &L.sub[e];
+    free(S->inputBuf); free(S->preActBuf); free(S->outputBuf); free(S->savedOutput);
+    free(S->gradInBuf); free(S->dzBuf);
+  }
+  free(L.sub);
+  free(L.moeLogits); free(L.moeProbs); free(L.moeW); free(L.moeOut); free(L.moeGate);
+  free(L.moeActive); free(L.outputBuf); free(L.gradInBuf); free(L.dzBuf);
+  return K;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1856,6 +2003,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_SWIGLU: swiglu_build(L); break;
     case GNO_LAYER_BATCHNORM2D: bn_build(L); break;
     case GNO_LAYER_GRU_UNROLLER: gru_build(L); break;
+    case GNO_LAYER_MOE: moe_build(L); break;
     default: break;
   }
 }
@@ -1870,6 +2018,7 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_SWIGLU) swiglu_init(L);
   else if (L->kind == GNO_LAYER_BATCHNORM2D) bn_init(L);
   else if (L->kind == GNO_LAYER_GRU_UNROLLER) gru_init_params(L);
+  else if (L->kind == GNO_LAYER_MOE) moe_init(L);
 }
 static void layer_reset(layer *L) {
   if (L->kind == GNO_LAYER_DROPOUT) L->rng = 42;                                   /* dropout.go:399-401 */
@@ -1899,6 +2048,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
     case GNO_LAYER_BATCHNORM2D: o = bn_forward(L, x, *len_io); break;
     case GNO_LAYER_GRU_UNROLLER: o = gru_unroller_forward(L, x); *len_io = L->H; break;
+    case GNO_LAYER_MOE: o = moe_forward(L, x); *len_io = L->spec.out_size; break;
     default: o = x;
   }
   return o;
@@ -1920,6 +2070,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_SWIGLU: return swiglu_backward(L, g);
     case GNO_LAYER_BATCHNORM2D: return bn_backward(L, g);
     case GNO_LAYER_GRU_UNROLLER: return gru_unroller_backward(L, g);
+    case GNO_LAYER_MOE: return moe_backward(L, g);
     default: return g;
   }
 }
@@ -1956,6 +2107,10 @@ gno_net *gno_net_create(const gno_layer_spec *specs, int32_t nlayers, int32_t lo
     L->params = n->params + off;
     L->grads = n->grads + off;
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_bind(L);
+    if (L->kind == GNO_LAYER_MOE) {
+      moe_bind(L);
+      L->curWorker = &n->cur_worker;
+    }
     layer_init_params(L);
     off += L->nparams;
   }
@@ -1976,6 +2131,16 @@ void gno_net_destroy(gno_net *n) {
     for (size_t k = 0; k < sizeof lb / sizeof lb[0]; k++) free(lb[k]);
     free(L->ids);
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_free(L);
+    if (L->kind == GNO_LAYER_MOE) {
+      for (int32_t e = 0; e <= L->spec.num_experts; e++) {
+        layer *S = &L->sub[e];
+        free(S->inputBuf); free(S->preActBuf); free(S->outputBuf); free(S->savedOutput);
+        free(S->gradInBuf); free(S->dzBuf);
+      }
+      free(L->sub);
+      free(L->moeLogits); free(L->moeProbs); free(L->moeW); free(L->moeOut); free(L->moeGate);
+      free(L->moeActive);
+    }
     if (L->kind == GNO_LAYER_RMSNORM) free(L->tmpRow);
     if (L->kind == GNO_LAYER_BATCHNORM2D) {
       free(L->runMean); free(L->runVar); free(L->bnMean); free(L->bnVar); free(L->bnStd);
@@ -2019,6 +2184,7 @@ static void bind_grads(gno_net *n, float *buf) {
   for (int32_t i = 0; i < n->nlayers; i++) {
     n->layers[i].grads = buf + off;
     if (n->layers[i].kind == GNO_LAYER_TRANSFORMER) tb_bind(&n->layers[i]);
+    if (n->layers[i].kind == GNO_LAYER_MOE) moe_bind(&n->layers[i]);
     off += n->layers[i].nparams;
   }
 }
@@ -2075,6 +2241,7 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
     /* trainBatchSequential net.go:721-770 */
     float bs = (float)B, total = 0.0f;
     bind_grads(n, n->grads);
+    n->cur_worker = 0; /* the network's own layers */
     for (int32_t i = 0; i < B; i++)
       total += run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od);
     float inv = 1.0f / bs;
@@ -2094,6 +2261,7 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
     if (e > B) e = B;
     if (s >= e) continue;
     bind_grads(n, wg);
+    n->cur_worker = 1 + w; /* worker clone w (its layers keep their own state) */
     float local = 0.0f;
     for (int32_t i = s; i < e; i++) local += run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od);
     wl[w] = local;

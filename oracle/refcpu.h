@@ -23,6 +23,7 @@
  *   SwiGLU                            internal/layer/swiglu.go:73-232
  *   BatchNorm2D                       internal/layer/batchnorm2d.go:103-135,255-511,524-665
  *   GRU (in a SequenceUnroller)       internal/layer/gru.go:110-510, unroller.go:57-213
+ *   MoE                               internal/layer/moe.go:47-313, net.go:129-152 (worker clones)
  *   Flatten                           internal/layer/reshape.go:64-96
  *   LSTM                              internal/layer/lstm.go:144-751,1065-1101
  *   SequenceUnroller                  internal/layer/unroller.go:57-213
@@ -55,6 +56,7 @@ enum {
   GNO_ACT_LOGSOFTMAX = 5,
   GNO_ACT_LINEAR = 6,
   GNO_ACT_GELU = 7,
+  GNO_ACT_LEAKYRELU = 8, /* NewLeakyReLU(0.1): a pointer (ActTypeLeakyReLU) */
 };
 
 enum {
@@ -73,6 +75,7 @@ enum {
   GNO_LAYER_SWIGLU = 13,
   GNO_LAYER_BATCHNORM2D = 14,
   GNO_LAYER_GRU_UNROLLER = 15,
+  GNO_LAYER_MOE = 16,
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -95,6 +98,7 @@ typedef struct gno_layer_spec {
   int32_t use_rope;     /* TransformerBlock attention: rotary embeddings on Q and K */
   float momentum;       /* BatchNorm2D running-stat momentum (the facade's 0.1) */
   int32_t no_affine;    /* BatchNorm2D without gamma / beta */
+  int32_t num_experts, top_k; /* MoE */
 } gno_layer_spec;
 
 typedef struct gno_net gno_net;
@@ -172,6 +176,12 @@ int32_t gno_net_layer_running_stats(gno_net *n, int32_t li, float *mean, float *
  * (gin: T x I, gparams accumulates). */
 void gno_gru_sequence(const float *x, int32_t I, int32_t H, int32_t T, const float *params,
                       float *out, const float *g, float *gin, float *gparams);
+/* MoE of one sample with params [gating W, b | expert W, b ...]; *rng is the
+ * noise stream state (used and advanced in training mode); active gets the
+ * top-k expert ids in routing order; with g, gin and gparams the backward. */
+int32_t gno_moe(const float *x, int32_t I, int32_t O, int32_t E, int32_t K, const float *params,
+                int32_t training, uint64_t *rng, float *out, int32_t *active, const float *g,
+                float *gin, float *gparams);
 /* matMulOptimized: out[b,o] = bias[o] + sum_i in[b,i] w[o,i]. */
 void gno_matmul(const float *in, const float *w, const float *bias, float *out,
                 int32_t batch, int32_t in_size, int32_t out_size);

@@ -18,10 +18,11 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 
-ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU = range(8)
+(ACT_NIL, ACT_RELU, ACT_SIGMOID, ACT_TANH, ACT_SOFTMAX, ACT_LOGSOFTMAX, ACT_LINEAR, ACT_GELU,
+ ACT_LEAKYRELU) = range(9)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER) = range(1, 16)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE) = range(1, 17)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -37,6 +38,7 @@ class LayerSpec(C.Structure):
         ("return_sequences", C.c_int32), ("eps", C.c_float),
         ("block_act", C.c_int32), ("block_norm", C.c_int32), ("use_rope", C.c_int32),
         ("momentum", C.c_float), ("no_affine", C.c_int32),
+        ("num_experts", C.c_int32), ("top_k", C.c_int32),
     ]
 
 
@@ -108,6 +110,9 @@ def lib():
         L.gno_rmsnorm.restype = C.c_int32
         L.gno_swiglu.argtypes = [f32p, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p, f32p]
         L.gno_rope.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32]
+        L.gno_moe.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, f32p, C.c_int32,
+                              C.POINTER(C.c_uint64), f32p, i32p, f32p, f32p, f32p]
+        L.gno_moe.restype = C.c_int32
         L.gno_gru_sequence.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, f32p, f32p, f32p, f32p,
                                        f32p]
         L.gno_batchnorm2d.argtypes = [f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float, C.c_float,
@@ -325,6 +330,27 @@ def gru_sequence(x, I, H, T, params, g=None):
     gp = np.zeros(params.size, np.float32)
     lib().gno_gru_sequence(fptr(x), I, H, T, fptr(params), fptr(out), fptr(g), fptr(gin), fptr(gp))
     return out, gin, gp
+
+
+def moe(x, O, E, K, params, training=False, rng=42, g=None):
+    """MoE of one sample; returns (out, active, rng) or, with g,
+    (out, active, rng, grad_in, grad_params)."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    params = np.ascontiguousarray(params, np.float32).ravel()
+    st = C.c_uint64(rng)
+    out = np.empty(O, np.float32)
+    act = np.empty(K, np.int32)
+    gin = np.empty(x.size, np.float32)
+    gp = np.zeros(params.size, np.float32)
+    gg = None if g is None else np.ascontiguousarray(g, np.float32).ravel()
+    rc = lib().gno_moe(fptr(x), x.size, O, E, K, fptr(params), int(training), C.byref(st), fptr(out),
+                       iptr(act), None if gg is None else fptr(gg), None if gg is None else fptr(gin),
+                       fptr(gp))
+    if rc < 0:
+        raise ValueError("bad MoE sizes")
+    if gg is None:
+        return out, act, st.value
+    return out, act, st.value, gin, gp
 
 
 def rope(x, T, nh, hd, conj=False):

@@ -19,6 +19,9 @@ def oracle_specs(refcpu, cfg):
                                      stride=d["s"], padding=d["p"]))
         elif k == "flatten":
             specs.append(refcpu.spec(refcpu.LAYER_FLATTEN, in_size=d["n"]))
+        elif k == "moe":
+            specs.append(refcpu.spec(refcpu.LAYER_MOE, in_size=d["in"], out_size=d["out"],
+                                     num_experts=d["E"], top_k=d["k"]))
         elif k == "batchnorm2d":
             specs.append(refcpu.spec(refcpu.LAYER_BATCHNORM2D, in_channels=d["C"], momentum=0.1,
                                      in_size=cfg["in_len"] if i == 0 else 0))

@@ -447,6 +447,60 @@ def test_gru_sequence(gn, oracle, B, T, inp, hidden, workers):
     assert max_rel(out, ref) <= TOL, max_rel(out, ref)
 
 
+_MOE_CASES = {
+    # Dense -> MoE(8 experts, top 2) -> Dense softmax, W = 1 (the layer's own noise stream)
+    "e8k2": (dict(B=40, in_len=24, classes=6, loss="ce", layers=[
+        {"kind": "dense", "in": 24, "out": 32, "act": "relu", "ptr": False},
+        {"kind": "moe", "in": 32, "out": 20, "E": 8, "k": 2},
+        {"kind": "dense", "in": 20, "out": 6, "act": "softmax", "ptr": True}]), 1),
+    # MoE first, 4 worker chunks (one noise stream per worker clone), MSE
+    "e5k3_w4": (dict(B=64, in_len=16, classes=4, loss="mse", layers=[
+        {"kind": "moe", "in": 16, "out": 12, "E": 5, "k": 3},
+        {"kind": "dense", "in": 12, "out": 4, "act": "linear", "ptr": False}]), 4),
+    # 16 experts (ties impossible under the noise), top 4, wider
+    "e16k4": (dict(B=96, in_len=64, classes=10, loss="ce", layers=[
+        {"kind": "moe", "in": 64, "out": 48, "E": 16, "k": 4},
+        {"kind": "dense", "in": 48, "out": 10, "act": "softmax", "ptr": True}]), 1),
+}
+
+
+def _random_moe(cfg, scale=0.3, seed=5):
+    """Non-zero MoE parameters (the reference starts them at 0) so routing,
+    experts and gating all carry gradient."""
+    li = [d["kind"] for d in cfg["layers"]].index("moe")
+    d = cfg["layers"][li]
+
+    def f(p, sl):
+        rng = np.random.default_rng(seed)
+        p[sl] = (rng.normal(size=sl.stop - sl.start) * scale).astype(np.float32)
+        return p
+    return li, f
+
+
+@pytest.mark.parametrize("case", sorted(_MOE_CASES))
+@pytest.mark.parametrize("init", ["reference", "random"])
+def test_moe_net(gn, oracle, case, init):
+    """MoE (moe.go) in a net over 3 training steps: the noise streams run on
+    across steps (RNG(42) per layer / worker clone), routing, expert and gating
+    gradients, Adam state and weights against the oracle; then inference
+    (no noise) against the oracle's eval-mode forward."""
+    from goneuron_amd import configs
+    c, workers = _MOE_CASES[case]
+    cfg = dict(num=16, name="moe_" + case, lr=1e-3, x="normal", **c)
+    perturb = None
+    if init == "random":
+        li, f = _random_moe(cfg)
+        sl = oracle_net(oracle, cfg).layer_slice(li)
+        perturb = lambda p: f(p, sl)
+    model, net = _compare_step(gn, oracle, cfg, steps=3, workers=workers, perturb=perturb)
+    x, _ = configs_inputs(cfg)
+    net.params[:] = model.Params()
+    net.set_training(False)
+    out = model.PredictBatch(x)
+    ref = np.stack([net.forward(x[b])[:out.shape[1]] for b in range(cfg["B"])])
+    assert max_rel(out, ref) <= TOL, max_rel(out, ref)
+
+
 def configs_inputs(cfg):
     from goneuron_amd import configs
     return configs.inputs(cfg)

@@ -521,6 +521,77 @@ def test_gru_sequence_structure(oracle):
     np.testing.assert_allclose(gin3, gin1 + gin2, rtol=1e-4, atol=1e-5)
 
 
+def _moe_torch(torch, x, I, O, E, K, p, g, noise=None, lb=False):
+    """float64 MoE with the routing (top-k set and order) fixed by the
+    probabilities it computes: y = sum_r p_e leaky(W_e x + b_e); with lb the
+    load-balancing loss 0.1 sum (p - 1/E)^2 joins the objective."""
+    P = torch.tensor(p.astype(np.float64), requires_grad=True)
+    X = torch.tensor(x.astype(np.float64), requires_grad=True)
+    Wg, bg = P[:E * I].view(E, I), P[E * I:E * I + E]
+    logits = Wg @ X + bg
+    if noise is not None:
+        logits = logits + torch.tensor(noise)
+    pr = torch.softmax(logits, 0)
+    order = sorted(range(E), key=lambda e: -float(pr[e].detach()))[:K]  # stable: ties keep index order
+    y = torch.zeros(O, dtype=torch.float64)
+    base = E * I + E
+    for e in order:
+        W = P[base + e * (O * I + O):base + e * (O * I + O) + O * I].view(O, I)
+        b = P[base + e * (O * I + O) + O * I:base + (e + 1) * (O * I + O)]
+        z = W @ X + b
+        y = y + pr[e] * torch.where(z > 0, z, 0.1 * z)
+    obj = (y * torch.tensor(g.astype(np.float64))).sum()
+    if lb:
+        obj = obj + 0.1 * ((pr - 1.0 / E) ** 2).sum()
+    obj.backward()
+    return y.detach().numpy(), order, X.grad.numpy(), P.grad.numpy()
+
+
+def test_moe_init_routing_and_gradients(oracle):
+    """moe.go:47-138: every parameter starts at 0 (Build rebinds the gating
+    and expert Dense layers to one fresh zero block); routing keeps ties in
+    index order (sort.Slice sorts <= 12 elements by insertion); inference-mode
+    output and gradients equal torch autograd of sum_topk p_e leaky(W_e x +
+    b_e) with the top-k set held fixed (moe.go:242-313 is that gradient);
+    training mode adds RNG(42) noise (u*2-1)*0.05 to the logits and the
+    load-balancing gradient of 0.1 sum (p - 1/E)^2."""
+    torch = pytest.importorskip("torch")
+    I, O, E, K = 6, 5, 7, 3
+    net = oracle.Net([oracle.spec(oracle.LAYER_MOE, in_size=I, out_size=O, num_experts=E, top_k=K),
+                      oracle.spec(oracle.LAYER_DENSE, in_size=O, out_size=2, act=oracle.ACT_LINEAR)],
+                     oracle.LOSS_MSE)
+    sl = net.layer_slice(0)
+    assert sl.stop - sl.start == E * I + E + E * (O * I + O)
+    assert not net.params[sl].any()
+    n = E * I + E + E * (O * I + O)
+    # zero gating: equal probabilities, experts 0..K-1 in index order
+    x0 = np.ones(I, np.float32)
+    _, act, _ = oracle.moe(x0, O, E, K, np.zeros(n, np.float32))
+    assert list(act) == list(range(K))
+    rng = np.random.default_rng(31)
+    p = (rng.normal(size=n) * 0.5).astype(np.float32)
+    x = rng.normal(size=I).astype(np.float32)
+    g = rng.normal(size=O).astype(np.float32)
+    out, act, st, gin, gp = oracle.moe(x, O, E, K, p, training=False, g=g)
+    y, order, gx, gP = _moe_torch(torch, x, I, O, E, K, p, g)
+    assert list(act) == order and st == 42
+    np.testing.assert_allclose(out, y, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gin, gx, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(gp, gP, rtol=1e-4, atol=1e-6)
+    # training mode: noise from RNG(42), E draws per forward, and the lb gradient
+    seed, noise = 42, []
+    for _ in range(E):
+        seed = (seed * 6364136223846793005 + 1) & (2**64 - 1)
+        u = np.float32(seed >> 33) / np.float32(2**31)
+        noise.append(float((u * np.float32(2) - np.float32(1)) * np.float32(0.05)))
+    out, act, st, gin, gp = oracle.moe(x, O, E, K, p, training=True, g=g)
+    y, order, gx, gP = _moe_torch(torch, x, I, O, E, K, p, g, noise=np.array(noise), lb=True)
+    assert list(act) == order and st == seed
+    np.testing.assert_allclose(out, y, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gin, gx, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(gp, gP, rtol=1e-4, atol=1e-6)
+
+
 def test_maxpool_tie_first_wins(oracle):
     net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=16, in_channels=1, kernel=2, stride=2)],
                      oracle.LOSS_MSE)
