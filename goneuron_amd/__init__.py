@@ -26,7 +26,7 @@ __all__ = [
     "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
     "LSTM", "GRU", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
-    "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError",
+    "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError", "GGMLTypeF32", "GGMLTypeF16",
 ]
 
 # ---------------------------------------------------------------- activations
@@ -212,6 +212,9 @@ def TransformerBlock(dim, heads, seq_len, ff_dim, causal):
     return Layer(LAYER_TRANSFORMER, dim=dim, num_heads=heads, seq_len=seq_len, ff_dim=ff_dim,
                  causal=int(causal))
 
+
+# GGUF tensor types (gguf.go:57-66)
+GGMLTypeF32, GGMLTypeF16 = 0, 1
 
 # TransformerBlockExt options (goneuron.go:352-358, transformer.go:199-210)
 ActReLU, ActSwiGLU, ActGELU = 0, 1, 2
@@ -467,6 +470,31 @@ class Sequential:
         out = np.empty(n, np.float32)
         self._ck(lib().gn_model_layer_output(self.h, i, _fp(out), n))
         return out
+
+    # ---- checkpoints (net.go:1119-1392) ----
+    def SaveBinaryWeights(self, filename):
+        """Network.SaveBinaryWeights (net.go:1119-1214)."""
+        self._ck(lib().gn_model_save_binary_weights(self.h, str(filename).encode()))
+
+    def LoadBinaryWeights(self, filename):
+        """Reads a SaveBinaryWeights file into this model (names and sizes checked)."""
+        self._ck(lib().gn_model_load_binary_weights(self.h, str(filename).encode()))
+
+    def SaveGGUF(self, filename):
+        """Network.SaveGGUF (net.go:1217-1220): GGUF v3, F32 tensors."""
+        self.SaveGGUFExt(filename, GGMLTypeF32)
+
+    def SaveGGUFExt(self, filename, tensor_type):
+        """Network.SaveGGUFExt (net.go:1222-1392): F32 or F16 tensors."""
+        self._ck(lib().gn_model_save_gguf(self.h, str(filename).encode(), int(tensor_type)))
+
+    def SaveState(self, filename):
+        """Parameters, Adam moments and timestep, BatchNorm2D running stats and
+        MoE noise streams, for resuming training."""
+        self._ck(lib().gn_model_save_state(self.h, str(filename).encode()))
+
+    def LoadState(self, filename):
+        self._ck(lib().gn_model_load_state(self.h, str(filename).encode()))
 
     def RunningStats(self, i):
         """BatchNorm2D.GetRunningMean / GetRunningVar (batchnorm2d.go:837-838)."""

@@ -90,6 +90,12 @@ SIGNATURES = {
     "gn_model_layer_output": (C.c_int, [vp, C.c_int32, f32p, C.c_int64]),
     "gn_model_layer_argmax": (C.c_int, [vp, C.c_int32, i32p, C.c_int64]),
     "gn_model_get_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
+    "gn_model_set_adam": (C.c_int, [vp, f32p, f32p, C.c_int64, C.c_int64, C.c_int32]),
+    "gn_model_save_binary_weights": (C.c_int, [vp, C.c_char_p]),
+    "gn_model_load_binary_weights": (C.c_int, [vp, C.c_char_p]),
+    "gn_model_save_gguf": (C.c_int, [vp, C.c_char_p, C.c_int32]),
+    "gn_model_save_state": (C.c_int, [vp, C.c_char_p]),
+    "gn_model_load_state": (C.c_int, [vp, C.c_char_p]),
     "gn_model_set_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
     "gn_dense_forward": (C.c_int, [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32]),

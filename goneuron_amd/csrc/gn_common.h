@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/goneuron_hip.h"
 
@@ -217,5 +218,13 @@ hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const
 
 // ---- measurement probe ----
 hipError_t launch_mfma_probe(float *out, int blocks, int iters, hipStream_t s);
+
+// ---- model views for the checkpoint writers (gn_runtime.hip) ----
+int model_layer_count(gn_model *M);
+const gn_layer_desc *model_layer_desc(gn_model *M, int i);
+int model_loss_kind(gn_model *M);
+std::vector<uint64_t> *model_noise_streams(gn_model *M, int i);  // MoE, else null
+void model_set_timestep(gn_model *M, int t);
+int model_error(gn_model *M, int code, const char *fmt, ...);    // records and returns code
 
 }  // namespace gn

@@ -1178,6 +1178,16 @@ extern "C" int gn_model_get_adam(gn_model *M, float *mdst, float *vdst, int64_t 
   if (timestep) *timestep = M->timestep;
   return GN_OK;
 }
+extern "C" int gn_model_set_adam(gn_model *M, const float *msrc, const float *vsrc, int64_t off,
+                                 int64_t n, int32_t timestep) {
+  if (!M) return GN_ERR_INVALID;
+  if (timestep < 0) return set_err(M->ctx, GN_ERR_INVALID, "negative Adam timestep");
+  int rc = GN_OK;
+  if (msrc && (rc = arena_copy(M, M->m, const_cast<float *>(msrc), off, n, false))) return rc;
+  if (vsrc && (rc = arena_copy(M, M->v, const_cast<float *>(vsrc), off, n, false))) return rc;
+  M->timestep = timestep;
+  return GN_OK;
+}
 extern "C" int gn_model_arena(gn_model *M, float **p, float **g, float **m, float **v) {
   if (!M) return GN_ERR_INVALID;
   if (p) *p = M->params;
@@ -2092,3 +2102,24 @@ extern "C" int gn_model_layer_argmax(gn_model *M, int32_t layer, int32_t *dst, i
   HIP_OK(c, hipStreamSynchronize(c->stream));
   return GN_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Model views for the checkpoint writers (gn_checkpoint.hip)
+// ---------------------------------------------------------------------------
+namespace gn {
+int model_layer_count(gn_model *M) { return (int)M->L.size(); }
+const gn_layer_desc *model_layer_desc(gn_model *M, int i) { return &M->L[i].d; }
+int model_loss_kind(gn_model *M) { return M->loss_kind; }
+std::vector<uint64_t> *model_noise_streams(gn_model *M, int i) {
+  return M->L[i].d.kind == GN_LAYER_MOE ? &M->L[i].mrng : nullptr;
+}
+void model_set_timestep(gn_model *M, int t) { M->timestep = t; }
+int model_error(gn_model *M, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  return set_err(M->ctx, code, "%s", buf);
+}
+}  // namespace gn

@@ -152,6 +152,10 @@ int gn_model_set_params(gn_model *m, const float *src, int64_t offset, int64_t n
 int gn_model_get_grads(gn_model *m, float *dst, int64_t offset, int64_t n);
 int gn_model_get_adam(gn_model *m, float *m_dst, float *v_dst, int64_t offset, int64_t n,
                       int32_t *timestep);
+/* Restores Adam moments and the timestep (resume; the reference's
+ * Adam.NewStep / StepInPlace state, opt.go:237-335). */
+int gn_model_set_adam(gn_model *m, const float *m_src, const float *v_src, int64_t offset, int64_t n,
+                      int32_t timestep);
 /* Device pointers of the arena regions (for zero-copy callers). */
 int gn_model_arena(gn_model *m, float **params, float **grads, float **adam_m, float **adam_v);
 
@@ -191,6 +195,27 @@ int gn_model_layer_argmax(gn_model *m, int32_t layer, int32_t *dst, int64_t n);
 int gn_model_get_running_stats(gn_model *m, int32_t layer, float *mean, float *var, int32_t n);
 int gn_model_set_running_stats(gn_model *m, int32_t layer, const float *mean, const float *var,
                                int32_t n);
+
+/* ---- checkpoints: the formats either side of training ------------------
+ * Network.SaveBinaryWeights (net.go:1119-1214): "GONN", int32 version 1,
+ * int32 tensor count, then per tensor int32 name length, name, int32 rank,
+ * int32 shape[rank], int32 length, float32 data (little endian).  Tensors
+ * are each layer's NamedParams (or its flat Params) named
+ * layer_<i>_<ExtractLayerConfig type>_<name> (net.go:1425-1505). */
+int gn_model_save_binary_weights(gn_model *m, const char *path);
+/* Reads a SaveBinaryWeights file into this model's parameters and
+ * BatchNorm2D running statistics; every tensor's name and length must match.
+ * (The reference writes the format but has no reader.) */
+int gn_model_load_binary_weights(gn_model *m, const char *path);
+/* Network.SaveGGUF / SaveGGUFExt (net.go:1217-1392, gguf.go): GGUF v3 with
+ * F32 tensors (f16 = 0) or F16 (f16 = 1, Float32ToFloat16's truncation). */
+int gn_model_save_gguf(gn_model *m, const char *path, int32_t f16);
+/* The whole training state for resume: parameters, Adam moments and
+ * timestep, BatchNorm2D running statistics, MoE noise stream states.  No
+ * counterpart in the reference, whose gob Save (net.go:863-1006) keeps no
+ * Adam moments. */
+int gn_model_save_state(gn_model *m, const char *path);
+int gn_model_load_state(gn_model *m, const char *path);
 
 /* ---- per-layer operators on device pointers -----------------------------
  * Batched stand-ins for the per-sample Layer.Forward / Backward calls and the
