@@ -27,6 +27,14 @@
 // sums are added in split order by a second kernel that also applies the
 // epilogue.
 //
+// 128-wide tiles whose K ranges are whole stages run a four-wave variant
+// instead (gemm_f32_mfma_w4): one wave per 64 x 64 sub-tile over the whole K
+// range, operands fetched with direct global -> LDS loads (no staging
+// registers, no LDS store instructions), fragment reads and loads issued one
+// per MFMA.  With at least two tiles per CU it uses 32-deep stages so that two
+// blocks share a CU and one block's prologue, barriers and epilogue overlap
+// the other's MFMAs.
+//
 // Used by Dense forward (NT: X[B,in] * W[out,in]^T, fused bias + activation),
 // Dense dX (NN: dZ[B,out] * W[out,in], fused activation derivative of the layer
 // below) and Dense dW (TN: dZ^T X scaled by 1/B), the batched replacements of
@@ -256,6 +264,91 @@ __device__ __forceinline__ void read_frags(const float *S, int rowbase, int koff
   }
 }
 
+// Direct global -> LDS staging (gfx950 global_load_lds_dwordx4).  One wave
+// instruction writes its 64 lanes' 16 B contiguously from an LDS base held in
+// M0, so the LDS layout follows the lane order and is chosen through the
+// global address each lane fetches: float4 slot f = t + NT*j of a stage lands
+// at LDS float 4f.  No staging registers and no LDS store instructions; the
+// data is in LDS once the wave's vmcnt has drained past the load.
+//   K-contiguous operand: [R rows][64 k], unpadded; the 16 float4 chunks of
+//   row r are XOR-swizzled by r & 15 (slot f is row f >> 4, physical chunk
+//   f & 15, holding logical chunk (f & 15) ^ (r & 15)), so the b128 fragment
+//   reads of 16 consecutive rows hit 16 different bank groups.
+//   M/N-contiguous operand: [64 k][R rows], unpadded (its global layout).
+// Tile edges re-read the last valid row, as in load_tile_pipe (full K stages
+// only).
+typedef __attribute__((address_space(3))) void *lds_void_ptr;
+
+// XOR swizzle of the float4 chunks of K-contiguous row r (CH chunks per row):
+// any 8 consecutive rows (and any 16 when CH = 16) map a logical chunk to
+// distinct physical chunks, and with CH = 8 two rows 8 apart also differ, so
+// 16 consecutive rows of b128 reads cover all banks whether the LDS serves 8
+// or 16 lanes per pass.
+template <int CH>
+__device__ __forceinline__ int chunk_swz(int r) {
+  return CH == 16 ? (r & 15) : ((r & 7) ^ ((r >> 3) & 1));
+}
+
+template <int R, bool KC, int NTH = NT, int BKW = BK>
+__device__ __forceinline__ void load_tile_direct(const float *__restrict__ base, int ld, int rows,
+                                                 int r0, int k0, float *S) {
+  constexpr int CH = BKW / 4;  // float4 chunks per K-contiguous row
+  const int t = threadIdx.x;
+  const int wslot = __builtin_amdgcn_readfirstlane((t >> 6) * 64);  // the wave's first slot
+#pragma unroll
+  for (int j = 0; j < R * CH / NTH; ++j) {
+    const int f = t + NTH * j;
+    const float *src;
+    if (KC) {
+      const int r = f / CH, c = (f % CH) ^ chunk_swz<CH>(r);
+      src = base + (size_t)min(r0 + r, rows - 1) * ld + k0 + 4 * c;
+    } else {
+      const int k = f / (R / 4), r4 = (f % (R / 4)) << 2;
+      src = base + (size_t)(k0 + k) * ld + min(r0 + r4, rows - 4);
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)(S + 4 * (NTH * j + wslot)), 16, 0, 0);
+  }
+}
+
+// Fragment halves (MFMA steps koff .. koff+7 of each of the wave's T slabs)
+// from the direct layouts; pairwise rows for an M/N-contiguous operand at
+// T = 2, as in read_frags.
+template <int R, bool KC, int BKW = BK>
+__device__ __forceinline__ void read_frags_direct(const float *S, int rowbase, int koff, int l32,
+                                                  float (&a)[Tile<R>::T][8]) {
+  constexpr int T = Tile<R>::T, CH = BKW / 4;
+  if (KC) {
+    const int c0 = koff >> 2, sw = chunk_swz<CH>(l32);  // rowbase is a multiple of 16
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+      const float *src = S + (rowbase + i * 32 + l32) * BKW;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const floatx4 x = *reinterpret_cast<const floatx4 *>(src + 4 * ((c0 + q) ^ sw));
+        a[i][4 * q + 0] = x[0];
+        a[i][4 * q + 1] = x[1];
+        a[i][4 * q + 2] = x[2];
+        a[i][4 * q + 3] = x[3];
+      }
+    }
+  } else if (T == 2) {
+    const float *src = S + koff * R + rowbase + 2 * l32;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const float2 x = *reinterpret_cast<const float2 *>(src + s * R);
+      a[0][s] = x.x;
+      a[T - 1][s] = x.y;
+    }
+  } else {
+    const float *src = S + koff * R + rowbase + l32;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) a[0][s] = src[s * R];
+  }
+}
+
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= n only.
+#define GN_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x3F70 | ((n) & 15) | (((n) >> 4) << 14))
+
 // Block -> tile mapping.  Workgroups are dispatched round-robin over the 8
 // XCDs (each with its own L2), so consecutive block ids land on different
 // XCDs.  Remap so that each XCD receives a contiguous range of tile ids, and
@@ -293,6 +386,104 @@ __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, i
 
 // EPI_PARTIAL: split-K partial sums to the workspace (epilogue applied later).
 constexpr int EPI_PARTIAL = 3;
+
+// Epilogue of a block tile: accumulators -> C (or the split-K workspace).
+// v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
+// 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile; with PAIR_A /
+// PAIR_B the slabs of that operand hold every other row (read pairwise).
+template <int R, int EPI, bool PAIR_A, bool PAIR_B>
+__device__ __forceinline__ void gemm_store(const GemmArgs &p, const floatx16 (&acc)[Tile<R>::T][Tile<R>::T],
+                                           int m0, int n0, int wm, int wn, int half, int l32) {
+  constexpr int T = Tile<R>::T;
+  const int M = p.M, N = p.N;
+  auto col_of = [&](int j) { return n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32); };
+  auto row_of = [&](int i, int r) {
+    const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
+    return m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
+  };
+  // Every value the epilogue reads (bias, saved activations, residual rows)
+  // is loaded before the first store: the compiler cannot tell a store from
+  // an alias of them, so a load placed between stores would wait out its own
+  // round trip to L2, 64 times per lane.
+  float bcol[T];
+  float av[T][T][16];
+#pragma unroll
+  for (int j = 0; j < T; ++j) bcol[j] = 0.f;
+  if constexpr (EPI == EPI_BIAS_ACT || EPI == EPI_BIAS_ADD) {
+    if (p.bias) {
+#pragma unroll
+      for (int j = 0; j < T; ++j) bcol[j] = col_of(j) < N ? p.bias[col_of(j)] : 0.f;
+    }
+  }
+  const bool use_aux = (EPI == EPI_BIAS_ADD) || (EPI == EPI_DACT && p.act != D_ONE);
+  if (use_aux) {
+    // aux row of an output row: itself, or for EPI_DACT the last row of its
+    // group of aux_div rows (Q10), found with a multiply-high by
+    // ceil(2^32 / d), exact while rows * d < 2^32 (else the division).
+    const unsigned d = EPI == EPI_DACT && p.aux_div > 1 ? (unsigned)p.aux_div : 1u;
+    const bool magic_ok = (unsigned long long)M * d < (1ull << 32);
+    const unsigned magic = d > 1 ? (unsigned)(0xFFFFFFFFull / d + 1) : 0u;
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int j = 0; j < T; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row_of(i, r), col = col_of(j);
+          int ar = row;
+          if (d > 1) {
+            const unsigned q = magic_ok ? __umulhi((unsigned)row, magic) : (unsigned)row / d;
+            ar = (int)(q * d + d - 1);
+          }
+          av[i][j][r] = (row < M && col < N) ? p.aux[(size_t)ar * p.ldaux + col] : 0.f;
+        }
+  }
+  float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
+  auto store_all = [&](auto f) {
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        const int col = col_of(j);
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row_of(i, r);
+          if (row >= M) continue;
+          if (EPI == EPI_PARTIAL)
+            ws[(size_t)row * N + col] = acc[i][j][r];
+          else
+            p.C[(size_t)row * p.ldc + col] = f(acc[i][j][r], i, j, r);
+        }
+      }
+  };
+  // The activation is chosen once per block: identity and ReLU inline, the
+  // rest through an out-of-line call, so the 64-value-per-lane epilogue stays
+  // small (inlining the float64 sigmoid / tanh into it blew the code past the
+  // instruction cache).
+  if constexpr (EPI == EPI_BIAS_ACT) {
+    if (p.act == F_IDENTITY)
+      store_all([&](float v, int, int j, int) { return v + bcol[j]; });
+    else if (p.act == F_RELU)
+      store_all([&](float v, int, int j, int) {
+        const float z = v + bcol[j];
+        return z > 0.0f ? z : 0.0f;
+      });
+    else
+      store_all([&](float v, int, int j, int) { return apply_fwd_call(v + bcol[j], p.act); });
+  } else if constexpr (EPI == EPI_DACT) {
+    if (p.act == D_ONE)
+      store_all([&](float v, int, int, int) { return v * 1.0f; });
+    else if (p.act == D_RELU)
+      store_all([&](float v, int i, int j, int r) { return v * (av[i][j][r] > 0.0f ? 1.0f : 0.0f); });
+    else
+      store_all([&](float v, int i, int j, int r) { return v * apply_deriv_call(av[i][j][r], p.act); });
+  } else if constexpr (EPI == EPI_BIAS_ADD) {
+    store_all([&](float v, int i, int j, int r) { return v * p.alpha + bcol[j] + av[i][j][r]; });
+  } else {
+    store_all([&](float v, int, int, int) { return v * p.alpha; });
+  }
+}
 
 // R = 128 runs one block per CU (139 KB of LDS), so two waves per SIMD and
 // the full 256-register budget; R = 64 fits two blocks per CU.
@@ -478,73 +669,140 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     v[r4 + 3] += o.w;
   }
 
-  // v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
-  // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile; slab rows are
-  // every other row when the operand was read pairwise (read_frags).
-  constexpr bool PAIR_A = PIPE != 0 && !AK && T == 2, PAIR_B = PIPE != 0 && !BKC && T == 2;
-  float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
-  auto store_all = [&](auto f) {
+  gemm_store<R, EPI, PIPE != 0 && !AK && T == 2, PIPE != 0 && !BKC && T == 2>(p, acc, m0, n0, wm, wn,
+                                                                               half, l32);
+}
+
+// Four-wave variant for full K stages and R = 128: each wave owns a 64 x 64
+// sub-tile over the block's whole K range (no in-block K split, no
+// reduction), operands staged by direct global -> LDS loads two stages deep.
+// BKW = 32 keeps a block at 64 KB of LDS so two blocks share a CU: the two
+// waves on a SIMD then belong to different blocks and one block's MFMAs run
+// while the other waits at its barrier (one 8-wave block stalls both waves of
+// every SIMD at each barrier).  Lane half h feeds k = (BKW/2)h + s at MFMA
+// step s of a stage; the steps run in quarters of 8 whose fragments
+// alternate between two register sets; all quarters but the last run before
+// the stage's barrier:
+//   MFMAs q0 (reads q1) | ... | wait for the next stage's loads | barrier |
+//   next stage's q0 reads and the loads of the stage after next into the
+//   buffer just released | MFMAs of the last quarter.
+constexpr int NT4 = 256;
+
+template <int BKW, int NS, bool AK, bool BKC, int EPI>
+__global__ __launch_bounds__(NT4)
+__attribute__((amdgpu_waves_per_eu(NS * BKW <= 64 ? 2 : 1, NS * BKW <= 64 ? 2 : 1)))
+void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
+  constexpr int R = 128, T = 2;
+  constexpr int NL = R * BKW / 4 / NT4;  // direct loads per thread per operand stage
+  constexpr int QN = BKW / 16;           // quarters of 8 MFMA steps per stage
+  static_assert(QN == 2 || QN == 4, "stage depth");
+  __shared__ __attribute__((aligned(16))) float As[NS][R * BKW];
+  __shared__ __attribute__((aligned(16))) float Bs[NS][R * BKW];
+
+  int tm, tn;
+  tile_of_block(tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * R, n0 = tn * R;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int koff = half * (BKW / 2);
+  const int M = p.M, N = p.N;
+  const int kbeg = blockIdx.y * kchunk;
+  const int kend = min(p.K, kbeg + kchunk);
+  const int nk = (kend - kbeg) / BKW;  // >= 1, full stages (checked by the launcher)
+  const int mrow = wm * (R / 2), ncol = wn * (R / 2);
+
+  floatx16 acc[T][T];
 #pragma unroll
-    for (int i = 0; i < T; ++i)
+  for (int i = 0; i < T; ++i)
 #pragma unroll
-      for (int j = 0; j < T; ++j) {
-        const int col = n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32);
-        if (col >= N) continue;
+    for (int j = 0; j < T; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
-          const int row = m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
-          if (row >= M) continue;
-          if (EPI == EPI_PARTIAL)
-            ws[(size_t)row * N + col] = acc[i][j][r];
-          else
-            p.C[(size_t)row * p.ldc + col] = f(acc[i][j][r], row, col);
-        }
-      }
-  };
-  // The activation is chosen once per block: identity and ReLU inline, the
-  // rest through an out-of-line call, so the 64-value-per-lane epilogue stays
-  // small (inlining the float64 sigmoid / tanh into it blew the code past the
-  // instruction cache).
-  if constexpr (EPI == EPI_BIAS_ACT) {
-    const float *bias = p.bias;
-    if (p.act == F_IDENTITY)
-      store_all([&](float v, int, int col) { return v + (bias ? bias[col] : 0.f); });
-    else if (p.act == F_RELU)
-      store_all([&](float v, int, int col) {
-        const float z = v + (bias ? bias[col] : 0.f);
-        return z > 0.0f ? z : 0.0f;
-      });
-    else
-      store_all([&](float v, int, int col) {
-        return apply_fwd_call(v + (bias ? bias[col] : 0.f), p.act);
-      });
-  } else if constexpr (EPI == EPI_DACT) {
-    // aux row of an output row: itself, or the last row of its group of
-    // aux_div rows (Q10), found with a multiply-high by ceil(2^32 / d), exact
-    // while rows * d < 2^32 (else the division).
-    const float *aux = p.aux;
-    const int ldaux = p.ldaux;
-    const unsigned d = p.aux_div > 1 ? (unsigned)p.aux_div : 1u;
-    const bool magic_ok = (unsigned long long)M * d < (1ull << 32);
-    const unsigned magic = d > 1 ? (unsigned)(0xFFFFFFFFull / d + 1) : 0u;
-    auto saved = [&](int row, int col) {
-      int ar = row;
-      if (d > 1) {
-        const unsigned q = magic_ok ? __umulhi((unsigned)row, magic) : (unsigned)row / d;
-        ar = (int)(q * d + d - 1);
-      }
-      return aux[(size_t)ar * ldaux + col];
-    };
-    if (p.act == D_ONE)
-      store_all([&](float v, int, int) { return v * 1.0f; });
-    else if (p.act == D_RELU)
-      store_all([&](float v, int row, int col) { return v * (saved(row, col) > 0.0f ? 1.0f : 0.0f); });
-    else
-      store_all([&](float v, int row, int col) { return v * apply_deriv_call(saved(row, col), p.act); });
-  } else {
-    store_all([&](float v, int row, int col) { return epilogue(v, EPI, p, row, col); });
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int k1 = kbeg + min(st, nk - 1) * BKW;
+    load_tile_direct<R, AK, NT4, BKW>(p.A, p.lda, M, m0, k1, As[st]);
+    load_tile_direct<R, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k1, Bs[st]);
   }
+  GN_WAIT_VMCNT(2 * NL * (NS - 1));  // stage 0 has landed; later ones may be in flight
+  __syncthreads();
+  float fa[T][8], fb[T][8];
+  read_frags_direct<R, AK, BKW>(As[0], mrow, koff, l32, fa);
+  read_frags_direct<R, BKC, BKW>(Bs[0], ncol, koff, l32, fb);
+  constexpr int DSRH = (AK ? 2 * T : 8) + (BKC ? 2 * T : 8);
+  constexpr int NW = 2 * NL;
+  constexpr int MQ = 8 * T * T;  // MFMAs per quarter stage
+  auto mfma8 = [&](const float (&a)[T][8], const float (&b)[T][8]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < T; ++i)
+#pragma unroll
+        for (int j = 0; j < T; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+  };
+  int cur = 0;  // buffer of stage kt; stage kt + j sits in (cur + j) % NS
+  for (int kt = 0; kt < nk; ++kt) {
+    const int nxt = cur + 1 == NS ? 0 : cur + 1;
+    float ga[T][8], gb[T][8];
+    read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 8, l32, ga);
+    read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 8, l32, gb);
+    mfma8(fa, fb);
+    if constexpr (QN == 4) {
+      read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 16, l32, fa);
+      read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 16, l32, fb);
+      mfma8(ga, gb);
+      read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 24, l32, ga);
+      read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 24, l32, gb);
+      mfma8(fa, fb);
+    }
+    // group masks: 0x008 MFMA, 0x020 global load, 0x100 LDS read.  Each
+    // quarter's fragment reads go out one per MFMA among the first MFMAs of
+    // the quarter before (a single wave per SIMD issues in order: a run of
+    // reads leaves the matrix pipe idle), at most DSRH outstanding where a
+    // wait is needed (lgkmcnt counts to 15).
+#pragma unroll
+    for (int q = 0; q < QN - 1; ++q) {
+#pragma unroll
+      for (int r = 0; r < DSRH; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, MQ - DSRH, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs above the barrier
+    // this wave's loads of stage kt+1 are in LDS (those of kt+2 .. kt+NS-1
+    // may still be in flight)
+    GN_WAIT_VMCNT(2 * NL * (NS - 2));
+    __syncthreads();
+    read_frags_direct<R, AK, BKW>(As[nxt], mrow, koff, l32, fa);
+    read_frags_direct<R, BKC, BKW>(Bs[nxt], ncol, koff, l32, fb);
+    {
+      // stage kt+NS into stage kt's buffer, which every wave finished
+      // reading before this barrier
+      const int k2 = kbeg + min(kt + NS, nk - 1) * BKW;
+      load_tile_direct<R, AK, NT4, BKW>(p.A, p.lda, M, m0, k2, As[cur]);
+      load_tile_direct<R, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k2, Bs[cur]);
+    }
+    cur = nxt;
+    mfma8(ga, gb);
+    static_assert(DSRH + NW <= MQ, "one read or load per MFMA");
+#pragma unroll
+    for (int r = 0; r < DSRH; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, MQ - DSRH - NW, 0);
+  }
+  GN_WAIT_VMCNT(0);  // nothing may land after the block ends
+  gemm_store<R, EPI, !AK, !BKC>(p, acc, m0, n0, wm, wn, half, l32);
 }
 
 // Split-K reduction: partials summed in split order, then the epilogue.
@@ -579,7 +837,16 @@ template <int R, bool AK, bool BKC, int EPI>
 static hipError_t launch_t(bool vec, bool ktail, const GemmArgs &a, int tm, int tn, int splits,
                           int kchunk, hipStream_t s) {
   dim3 grid(tm * tn, splits), block(NT);
-  if (vec && !ktail)
+  if (R == 128 && vec && !ktail) {
+    // Four-wave kernels: two blocks per CU (32-deep stages, 64 KB of LDS)
+    // when there are at least two tiles per CU, else one (64-deep stages).
+    if (tm * tn * splits >= 512)
+      hipLaunchKernelGGL((gemm_f32_mfma_w4<32, 2, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
+                         kchunk);
+    else
+      hipLaunchKernelGGL((gemm_f32_mfma_w4<64, 2, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
+                         kchunk);
+  } else if (vec && !ktail)
     hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, 1>), grid, block, 0, s, a, tm, tn,
                        kchunk);
   else if (vec)
