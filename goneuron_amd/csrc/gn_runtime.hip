@@ -31,6 +31,7 @@ struct gn_ctx {
   hipDeviceProp_t props{};
   float *scratch = nullptr;  // colsum partials
   size_t scratch_floats = 0;
+  float *scratch_aux = nullptr;  // the same for kernels queued on `aux` (scratch_floats long)
   // kernel timing (gn_timing_enable)
   bool timing = false;
   struct Rec { int cls; hipEvent_t a, b; };
@@ -176,6 +177,12 @@ extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
     (void)hipStreamDestroy(c->aux);
     return GN_ERR_OOM;
   }
+  if (hipMalloc(&c->scratch_aux, c->scratch_floats * sizeof(float)) != hipSuccess) {
+    (void)hipFree(c->scratch);
+    (void)hipStreamDestroy(c->stream);
+    (void)hipStreamDestroy(c->aux);
+    return GN_ERR_OOM;
+  }
   *out = c.release();
   return GN_OK;
 }
@@ -187,6 +194,7 @@ extern "C" void gn_shutdown(gn_ctx *c) {
   (void)hipStreamSynchronize(c->aux);
   for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
   (void)hipFree(c->scratch);
+  (void)hipFree(c->scratch_aux);
   (void)hipStreamDestroy(c->stream);
   (void)hipStreamDestroy(c->aux);
   delete c;
@@ -367,13 +375,26 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
 }
 
 // gradW = scale * dz^T x ; gradB = scale * colsum(dz) ; gin = dz W (optionally * act'(aux))
+// With dz_ready, the parameter gradients go to ctx->aux (after dz_ready is
+// recorded on the main stream, with aux's own scratch) and run next to the dX
+// GEMM: the two GEMMs share the CUs, and each one's prologue and tail are
+// covered by the other's tiles.
 static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz,
                                  float *gW, float *gB, float *gin, int B, int in, int out_n,
-                                 float scale, const float *gin_aux, int gin_deriv) {
+                                 float scale, const float *gin_aux, int gin_deriv,
+                                 hipEvent_t dz_ready = nullptr) {
   hipError_t e;
+  hipStream_t ws = c->stream;
+  float *wscr = c->scratch;
+  if (dz_ready) {
+    if ((e = hipEventRecord(dz_ready, c->stream)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(c->aux, dz_ready, 0)) != hipSuccess) return e;
+    ws = c->aux;
+    wscr = c->scratch_aux;
+  }
   if (gB) {
-    KTimer kt(c, GN_KCLASS_OTHER);
-    e = launch_colsum(dz, B, out_n, out_n, scale, gB, c->scratch, c->scratch_floats, c->stream);
+    KTimer kt(c, GN_KCLASS_OTHER, ws);
+    e = launch_colsum(dz, B, out_n, out_n, scale, gB, wscr, c->scratch_floats, ws);
     if (e != hipSuccess) return e;
   }
   GemmArgs a{};
@@ -382,10 +403,10 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
   a.B = x; a.ldb = in;
   a.C = gW; a.ldc = in;
   a.alpha = scale;
-  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  a.ws = wscr; a.ws_cap = c->scratch_floats;
   {
-    KTimer kt(c, GN_KCLASS_GEMM);
-    e = launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
+    KTimer kt(c, GN_KCLASS_GEMM, ws);
+    e = launch_gemm('T', 'N', EPI_SCALE, a, ws);
   }
   if (e != hipSuccess) return e;
   if (gin) {
@@ -568,6 +589,7 @@ struct gn_model {
   // layer's backward is done, overlapping Adam with the rest of the backward
   bool overlap_adam = true;
   std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
+  std::vector<hipEvent_t> dz_ev;    // one per layer: its dz is ready (no timing)
 };
 
 // Adam coefficients of one Network.Step: Adam.NewStep increments the
@@ -609,6 +631,7 @@ extern "C" void gn_model_destroy(gn_model *M) {
   (void)hipStreamSynchronize(M->ctx->stream);
   (void)hipStreamSynchronize(M->ctx->aux);
   for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
+  for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
   for (void *p : M->owned) (void)hipFree(p);
   delete M;
 }
@@ -1619,6 +1642,13 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       M->sync_ev.push_back(e);
     }
   }
+  if (ac && (int)M->dz_ev.size() < n) {
+    while ((int)M->dz_ev.size() < n) {
+      hipEvent_t e;
+      HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      M->dz_ev.push_back(e);
+    }
+  }
   bool is_dz = true;  // gout of the current layer already holds dz
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
@@ -1644,8 +1674,11 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
             next_dz = true;
           }
         }
+        // with the per-layer Adam on aux (large models), dW and db run there
+        // next to dX; the layer's Adam is queued behind them.  The per-kernel
+        // timing pass keeps them on one stream, so each GEMM is timed alone.
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, gB, gin, B, R.d.in_size, R.d.out_size, scale,
-                                 aux, deriv));
+                                 aux, deriv, ac && gin && !c->timing ? M->dz_ev[i] : nullptr));
         is_dz = next_dz;
         break;
       }
