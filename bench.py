@@ -28,7 +28,7 @@ PEAK_HBM_GBPS = 8000.0
 # FETCH_SIZE (x2.000) and WRITE_SIZE (x1.000) passes, each scaled by what the
 # counter reads for a 1 GiB device-to-device copy (bench.py --copy-probe 1024).
 # Keyed by workload; a changed GEMM kernel needs a new measurement.
-GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2910.5e6}
+GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2861.0e6}
 
 
 def gemm_flops(cfg, B):
