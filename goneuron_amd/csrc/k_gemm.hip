@@ -391,28 +391,29 @@ constexpr int EPI_PARTIAL = 3;
 // v_mfma_f32_32x32x2_f32 result layout: lane l, accumulator r holds row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 tile; with PAIR_A /
 // PAIR_B the slabs of that operand hold every other row (read pairwise).
-template <int R, int EPI, bool PAIR_A, bool PAIR_B>
-__device__ __forceinline__ void gemm_store(const GemmArgs &p, const floatx16 (&acc)[Tile<R>::T][Tile<R>::T],
+template <int RM, int RN, int EPI, bool PAIR_A, bool PAIR_B>
+__device__ __forceinline__ void gemm_store(const GemmArgs &p,
+                                           const floatx16 (&acc)[Tile<RM>::T][Tile<RN>::T],
                                            int m0, int n0, int wm, int wn, int half, int l32) {
-  constexpr int T = Tile<R>::T;
+  constexpr int TM = Tile<RM>::T, TN = Tile<RN>::T;
   const int M = p.M, N = p.N;
-  auto col_of = [&](int j) { return n0 + wn * (R / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32); };
+  auto col_of = [&](int j) { return n0 + wn * (RN / 2) + (PAIR_B ? 2 * l32 + j : j * 32 + l32); };
   auto row_of = [&](int i, int r) {
     const int rr = (r >> 2) * 8 + half * 4 + (r & 3);
-    return m0 + wm * (R / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
+    return m0 + wm * (RM / 2) + (PAIR_A ? 2 * rr + i : i * 32 + rr);
   };
   // Every value the epilogue reads (bias, saved activations, residual rows)
   // is loaded before the first store: the compiler cannot tell a store from
   // an alias of them, so a load placed between stores would wait out its own
   // round trip to L2, 64 times per lane.
-  float bcol[T];
-  float av[T][T][16];
+  float bcol[TN];
+  float av[TM][TN][16];
 #pragma unroll
-  for (int j = 0; j < T; ++j) bcol[j] = 0.f;
+  for (int j = 0; j < TN; ++j) bcol[j] = 0.f;
   if constexpr (EPI == EPI_BIAS_ACT || EPI == EPI_BIAS_ADD) {
     if (p.bias) {
 #pragma unroll
-      for (int j = 0; j < T; ++j) bcol[j] = col_of(j) < N ? p.bias[col_of(j)] : 0.f;
+      for (int j = 0; j < TN; ++j) bcol[j] = col_of(j) < N ? p.bias[col_of(j)] : 0.f;
     }
   }
   const bool use_aux = (EPI == EPI_BIAS_ADD) || (EPI == EPI_DACT && p.act != D_ONE);
@@ -424,9 +425,9 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &p, const floatx16 (&a
     const bool magic_ok = (unsigned long long)M * d < (1ull << 32);
     const unsigned magic = d > 1 ? (unsigned)(0xFFFFFFFFull / d + 1) : 0u;
 #pragma unroll
-    for (int i = 0; i < T; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < T; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = row_of(i, r), col = col_of(j);
@@ -441,9 +442,9 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &p, const floatx16 (&a
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
   auto store_all = [&](auto f) {
 #pragma unroll
-    for (int i = 0; i < T; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < T; ++j) {
+      for (int j = 0; j < TN; ++j) {
         const int col = col_of(j);
         if (col >= N) continue;
 #pragma unroll
@@ -669,8 +670,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     v[r4 + 3] += o.w;
   }
 
-  gemm_store<R, EPI, PIPE != 0 && !AK && T == 2, PIPE != 0 && !BKC && T == 2>(p, acc, m0, n0, wm, wn,
-                                                                               half, l32);
+  gemm_store<R, R, EPI, PIPE != 0 && !AK && T == 2, PIPE != 0 && !BKC && T == 2>(p, acc, m0, n0, wm,
+                                                                                  wn, half, l32);
 }
 
 // Four-wave variant for full K stages and R = 128: each wave owns a 64 x 64
@@ -688,20 +689,22 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
 //   buffer just released | MFMAs of the last quarter.
 constexpr int NT4 = 256;
 
-template <int BKW, int NS, bool AK, bool BKC, int EPI>
+template <int BKW, int NS, int RN, bool AK, bool BKC, int EPI>
 __global__ __launch_bounds__(NT4)
-__attribute__((amdgpu_waves_per_eu(NS * BKW <= 64 ? 2 : 1, NS * BKW <= 64 ? 2 : 1)))
+__attribute__((amdgpu_waves_per_eu(NS * BKW * (128 + RN) <= 16384 ? 2 : 1,
+                                   NS * BKW * (128 + RN) <= 16384 ? 2 : 1)))
 void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
-  constexpr int R = 128, T = 2;
-  constexpr int NL = R * BKW / 4 / NT4;  // direct loads per thread per operand stage
-  constexpr int QN = BKW / 16;           // quarters of 8 MFMA steps per stage
+  constexpr int RM = 128, TM = 2, TN = RN / 64;
+  constexpr int NLA = RM * BKW / 4 / NT4, NLB = RN * BKW / 4 / NT4;  // direct loads per thread
+  constexpr int QN = BKW / 16;  // quarters of 8 MFMA steps per stage
   static_assert(QN == 2 || QN == 4, "stage depth");
-  __shared__ __attribute__((aligned(16))) float As[NS][R * BKW];
-  __shared__ __attribute__((aligned(16))) float Bs[NS][R * BKW];
+  static_assert(RN == 128 || RN == 64, "tile width");
+  __shared__ __attribute__((aligned(16))) float As[NS][RM * BKW];
+  __shared__ __attribute__((aligned(16))) float Bs[NS][RN * BKW];
 
   int tm, tn;
   tile_of_block(tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * R, n0 = tn * R;
+  const int m0 = tm * RM, n0 = tn * RN;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = w >> 1, wn = w & 1;
   const int half = lane >> 5, l32 = lane & 31;
@@ -710,52 +713,53 @@ void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   const int kbeg = blockIdx.y * kchunk;
   const int kend = min(p.K, kbeg + kchunk);
   const int nk = (kend - kbeg) / BKW;  // >= 1, full stages (checked by the launcher)
-  const int mrow = wm * (R / 2), ncol = wn * (R / 2);
+  const int mrow = wm * (RM / 2), ncol = wn * (RN / 2);
 
-  floatx16 acc[T][T];
+  floatx16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < T; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < T; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
 #pragma unroll
   for (int st = 0; st < NS; ++st) {
     const int k1 = kbeg + min(st, nk - 1) * BKW;
-    load_tile_direct<R, AK, NT4, BKW>(p.A, p.lda, M, m0, k1, As[st]);
-    load_tile_direct<R, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k1, Bs[st]);
+    load_tile_direct<RM, AK, NT4, BKW>(p.A, p.lda, M, m0, k1, As[st]);
+    load_tile_direct<RN, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k1, Bs[st]);
   }
-  GN_WAIT_VMCNT(2 * NL * (NS - 1));  // stage 0 has landed; later ones may be in flight
+  constexpr int NW = NLA + NLB;  // direct loads per thread per stage
+  GN_WAIT_VMCNT(NW * (NS - 1));  // stage 0 has landed; later ones may be in flight
   __syncthreads();
-  float fa[T][8], fb[T][8];
-  read_frags_direct<R, AK, BKW>(As[0], mrow, koff, l32, fa);
-  read_frags_direct<R, BKC, BKW>(Bs[0], ncol, koff, l32, fb);
-  constexpr int DSRH = (AK ? 2 * T : 8) + (BKC ? 2 * T : 8);
-  constexpr int NW = 2 * NL;
-  constexpr int MQ = 8 * T * T;  // MFMAs per quarter stage
-  auto mfma8 = [&](const float (&a)[T][8], const float (&b)[T][8]) {
+  float fa[TM][8], fb[TN][8];
+  read_frags_direct<RM, AK, BKW>(As[0], mrow, koff, l32, fa);
+  read_frags_direct<RN, BKC, BKW>(Bs[0], ncol, koff, l32, fb);
+  constexpr int DSRH = (AK ? 2 * TM : 8) + (BKC ? 2 * TN : 8);
+  constexpr int MQ = 8 * TM * TN;  // MFMAs per quarter stage
+  static_assert(DSRH <= MQ, "one read per MFMA");
+  auto mfma8 = [&](const float (&a)[TM][8], const float (&b)[TN][8]) {
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int i = 0; i < T; ++i)
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < T; ++j)
+        for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
   };
   int cur = 0;  // buffer of stage kt; stage kt + j sits in (cur + j) % NS
   for (int kt = 0; kt < nk; ++kt) {
     const int nxt = cur + 1 == NS ? 0 : cur + 1;
-    float ga[T][8], gb[T][8];
-    read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 8, l32, ga);
-    read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 8, l32, gb);
+    float ga[TM][8], gb[TN][8];
+    read_frags_direct<RM, AK, BKW>(As[cur], mrow, koff + 8, l32, ga);
+    read_frags_direct<RN, BKC, BKW>(Bs[cur], ncol, koff + 8, l32, gb);
     mfma8(fa, fb);
     if constexpr (QN == 4) {
-      read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 16, l32, fa);
-      read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 16, l32, fb);
+      read_frags_direct<RM, AK, BKW>(As[cur], mrow, koff + 16, l32, fa);
+      read_frags_direct<RN, BKC, BKW>(Bs[cur], ncol, koff + 16, l32, fb);
       mfma8(ga, gb);
-      read_frags_direct<R, AK, BKW>(As[cur], mrow, koff + 24, l32, ga);
-      read_frags_direct<R, BKC, BKW>(Bs[cur], ncol, koff + 24, l32, gb);
+      read_frags_direct<RM, AK, BKW>(As[cur], mrow, koff + 24, l32, ga);
+      read_frags_direct<RN, BKC, BKW>(Bs[cur], ncol, koff + 24, l32, gb);
       mfma8(fa, fb);
     }
     // group masks: 0x008 MFMA, 0x020 global load, 0x100 LDS read.  Each
@@ -775,34 +779,36 @@ void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs above the barrier
     // this wave's loads of stage kt+1 are in LDS (those of kt+2 .. kt+NS-1
     // may still be in flight)
-    GN_WAIT_VMCNT(2 * NL * (NS - 2));
+    GN_WAIT_VMCNT(NW * (NS - 2));
     __syncthreads();
-    read_frags_direct<R, AK, BKW>(As[nxt], mrow, koff, l32, fa);
-    read_frags_direct<R, BKC, BKW>(Bs[nxt], ncol, koff, l32, fb);
+    read_frags_direct<RM, AK, BKW>(As[nxt], mrow, koff, l32, fa);
+    read_frags_direct<RN, BKC, BKW>(Bs[nxt], ncol, koff, l32, fb);
     {
       // stage kt+NS into stage kt's buffer, which every wave finished
       // reading before this barrier
       const int k2 = kbeg + min(kt + NS, nk - 1) * BKW;
-      load_tile_direct<R, AK, NT4, BKW>(p.A, p.lda, M, m0, k2, As[cur]);
-      load_tile_direct<R, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k2, Bs[cur]);
+      load_tile_direct<RM, AK, NT4, BKW>(p.A, p.lda, M, m0, k2, As[cur]);
+      load_tile_direct<RN, BKC, NT4, BKW>(p.B, p.ldb, N, n0, k2, Bs[cur]);
     }
     cur = nxt;
     mfma8(ga, gb);
-    static_assert(DSRH + NW <= MQ, "one read or load per MFMA");
+    // reads and loads one per MFMA while MFMAs last, the remaining loads after
+    constexpr int NWM = NW < MQ - DSRH ? NW : MQ - DSRH;
 #pragma unroll
     for (int r = 0; r < DSRH; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 #pragma unroll
-    for (int q = 0; q < NW; ++q) {
+    for (int q = 0; q < NWM; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, MQ - DSRH - NW, 0);
+    if constexpr (NW > NWM) __builtin_amdgcn_sched_group_barrier(0x020, NW - NWM, 0);
+    if constexpr (MQ > DSRH + NWM) __builtin_amdgcn_sched_group_barrier(0x008, MQ - DSRH - NWM, 0);
   }
   GN_WAIT_VMCNT(0);  // nothing may land after the block ends
-  gemm_store<R, EPI, !AK, !BKC>(p, acc, m0, n0, wm, wn, half, l32);
+  gemm_store<RM, RN, EPI, !AK, !BKC && TN == 2>(p, acc, m0, n0, wm, wn, half, l32);
 }
 
 // Split-K reduction: partials summed in split order, then the epilogue.
@@ -841,10 +847,10 @@ static hipError_t launch_t(bool vec, bool ktail, const GemmArgs &a, int tm, int 
     // Four-wave kernels: two blocks per CU (32-deep stages, 64 KB of LDS)
     // when there are at least two tiles per CU, else one (64-deep stages).
     if (tm * tn * splits >= 512)
-      hipLaunchKernelGGL((gemm_f32_mfma_w4<32, 2, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
+      hipLaunchKernelGGL((gemm_f32_mfma_w4<32, 2, 128, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
                          kchunk);
     else
-      hipLaunchKernelGGL((gemm_f32_mfma_w4<64, 2, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
+      hipLaunchKernelGGL((gemm_f32_mfma_w4<64, 2, 128, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
                          kchunk);
   } else if (vec && !ktail)
     hipLaunchKernelGGL((gemm_f32_mfma<R, AK, BKC, true, EPI, 1>), grid, block, 0, s, a, tm, tn,
