@@ -546,11 +546,9 @@ __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict_
       }
 }
 
-// The same Gram with 16-byte staging loads, 32-wide K stages and the next
-// stage prefetched into registers while the current one runs on MFMA (H % 8
-// == 0, I % 4 == 0 and 16-byte aligned rows).  K runs over [dG | hPrev | x_last]:
-// the first 4H go to the dG accumulators, the rest (zero padded to a multiple
-// of 32) to the [x | hPrev] ones.
+// One 16-byte group of a Gram row: K runs over [dG | hPrev | x_last]; the first
+// 4H go to the dG accumulators, the rest (zero padded to a multiple of 32) to
+// the [x | hPrev] ones.
 __device__ __forceinline__ float4 gram_row4(const float *__restrict__ D,
                                             const float *__restrict__ hbuf,
                                             const float *__restrict__ x, int b, int t, int T,
@@ -564,16 +562,22 @@ __device__ __forceinline__ float4 gram_row4(const float *__restrict__ D,
   return make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-__global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restrict__ D,
+
+// The same Gram with 16-byte staging (H % 8 == 0, I % 4 == 0 and 16-byte aligned
+// rows), staged as float32: each K stage (32 wide) of the 64 u-rows and
+// 64 v-rows goes to LDS with 16-byte stores ([row][32 + 4], the pad keeps the
+// b128 reads of 16 consecutive rows on distinct banks), and lane l of a wave
+// takes k = 8*(l/16) + s at MFMA step s of a stage, so its 8 operand values of
+// a row are two b128 reads, widened to double as they are used (the products
+// and sums stay in float64).  The next stage is prefetched into registers
+// during the MFMAs; one barrier per stage.
+__global__ __launch_bounds__(256) void lstm_gram_v5_kernel(const float *__restrict__ D,
                                                            const float *__restrict__ hbuf,
                                                            const float *__restrict__ x,
                                                            double *__restrict__ Gm, ChainMap cm,
                                                            int I, int H, int nmax) {
-  constexpr int KS = 32;
-  // row pitch 80 doubles (640 B = 128 B mod 256 B): the four k-rows one
-  // operand read touches (16 lanes each, 128 B) fall in alternate bank halves
-  constexpr int GP = 80;
-  __shared__ double sv[KS][GP], su[KS][GP];
+  constexpr int KS = 32, GP = KS + 4;
+  __shared__ __attribute__((aligned(16))) float su[2][64 * GP], sv[2][64 * GP];
   const int ch = blockIdx.y;
   const int n = cm.len(ch);
   int lin = blockIdx.x, tv = 0;
@@ -586,24 +590,44 @@ __global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restri
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv >> 1, wn = wv & 1;
   const int G4 = 4 * H;
-  const int Kz = G4 + ((H + I + KS - 1) / KS) * KS;  // padded K
-  // staging: thread -> row rr (0..63), float4 column groups kq and kq + 16;
-  // a wave holds one kq, so each LDS store writes 64 consecutive doubles of a
-  // k-row (no bank conflicts)
-  const int rr = tid & 63, kq = (tid >> 6) * 4;
-  const int iv = tv * 64 + rr, iu = tu * 64 + rr;
-  const bool okv = iv < n, oku = iu < n;
-  int bv = 0, tvv = 0, bu = 0, tuu = 0;
-  if (okv) cm.at(ch, iv, bv, tvv);
-  if (oku) cm.at(ch, iu, bu, tuu);
-  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 rv[2], ru[2];
-  auto load = [&](int k0) {
+  const int Kz = G4 + ((H + I + KS - 1) / KS) * KS;  // padded K; G4 % KS == 0
+  const int nst = Kz / KS;
+  // staging: float4 slot f = tid + 256 j of a stage is row f >> 3, k 4 (f & 7)
+  int bu[2], tuu[2], bv[2], tvv[2];
+  bool oku[2], okv[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = k0 + kq + 16 * h;
-      rv[h] = okv ? gram_row4(D, hbuf, x, bv, tvv, cm.T, I, H, k) : z4;
-      ru[h] = oku ? gram_row4(D, hbuf, x, bu, tuu, cm.T, I, H, k) : z4;
+  for (int j = 0; j < 2; ++j) {
+    const int r = (tid + 256 * j) >> 3;
+    const int iu = tu * 64 + r, iv = tv * 64 + r;
+    oku[j] = iu < n;
+    okv[j] = iv < n;
+    bu[j] = tuu[j] = bv[j] = tvv[j] = 0;
+    if (oku[j]) cm.at(ch, iu, bu[j], tuu[j]);
+    if (okv[j]) cm.at(ch, iv, bv[j], tvv[j]);
+  }
+  float4 ru[2], rv[2];
+  auto load = [&](int k0) {
+    // explicit branches: a select between the row and a zero vector became a
+    // flat load through a pointer into private memory
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = k0 + 4 * ((tid + 256 * j) & 7);
+      if (oku[j])
+        ru[j] = gram_row4(D, hbuf, x, bu[j], tuu[j], cm.T, I, H, k);
+      else
+        ru[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (okv[j])
+        rv[j] = gram_row4(D, hbuf, x, bv[j], tvv[j], cm.T, I, H, k);
+      else
+        rv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int f = tid + 256 * j, o = (f >> 3) * GP + 4 * (f & 7);
+      *reinterpret_cast<float4 *>(&su[buf][o]) = ru[j];
+      *reinterpret_cast<float4 *>(&sv[buf][o]) = rv[j];
     }
   };
   d4v acc[2][2][2];
@@ -614,39 +638,47 @@ __global__ __launch_bounds__(256) void lstm_gram_v4_kernel(const float *__restri
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[q][i][j] = d4v{0.0, 0.0, 0.0, 0.0};
   load(0);
-  for (int k0 = 0; k0 < Kz; k0 += KS) {
-    __syncthreads();
+  store(0);
+  __syncthreads();
+  const int kl = 8 * (lane >> 4), m16 = lane & 15;
+  for (int st = 0; st < nst; ++st) {
+    const int cur = st & 1;
+    const bool more = st + 1 < nst;
+    if (more) load((st + 1) * KS);  // in flight during the MFMAs
+    float fa[2][8], fb[2][8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kk = kq + 16 * h;
-      sv[kk][rr] = rv[h].x; sv[kk + 1][rr] = rv[h].y; sv[kk + 2][rr] = rv[h].z; sv[kk + 3][rr] = rv[h].w;
-      su[kk][rr] = ru[h].x; su[kk + 1][rr] = ru[h].y; su[kk + 2][rr] = ru[h].z; su[kk + 3][rr] = ru[h].w;
+    for (int i = 0; i < 2; ++i) {
+      const float *pa = &su[cur][(wm * 32 + i * 16 + m16) * GP + kl];
+      const float *pb = &sv[cur][(wn * 32 + i * 16 + m16) * GP + kl];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(pa + 4 * h);
+        const float4 b4 = *reinterpret_cast<const float4 *>(pb + 4 * h);
+        fa[i][4 * h] = a4.x; fa[i][4 * h + 1] = a4.y; fa[i][4 * h + 2] = a4.z; fa[i][4 * h + 3] = a4.w;
+        fb[i][4 * h] = b4.x; fb[i][4 * h + 1] = b4.y; fb[i][4 * h + 2] = b4.z; fb[i][4 * h + 3] = b4.w;
+      }
     }
-    __syncthreads();
-    if (k0 + KS < Kz) load(k0 + KS);  // next stage in flight during the MFMAs
-    const int q = k0 < G4 ? 0 : 1;
+    const int q = st * KS < G4 ? 0 : 1;
 #pragma unroll
-    for (int ks = 0; ks < KS / 4; ++ks) {
-      const int k = ks * 4 + (lane >> 4);
-      double av[2], bvv[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) av[i] = su[k][wm * 32 + i * 16 + (lane & 15)];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bvv[j] = sv[k][wn * 32 + j * 16 + (lane & 15)];
+    for (int s = 0; s < 8; ++s) {
       if (q == 0) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[0][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bvv[j], acc[0][i][j], 0, 0, 0);
+            acc[0][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)fa[i][s], (double)fb[j][s],
+                                                                acc[0][i][j], 0, 0, 0);
       } else {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[1][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[i], bvv[j], acc[1][i][j], 0, 0, 0);
+            acc[1][i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)fa[i][s], (double)fb[j][s],
+                                                                acc[1][i][j], 0, 0, 0);
       }
     }
+    if (more) store(cur ^ 1);  // that buffer was last read before the previous barrier
+    __syncthreads();
   }
   double *Gc = Gm + (size_t)ch * nmax * nmax;
 #pragma unroll
@@ -964,11 +996,11 @@ hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const flo
   const int nmax = lstm_gram_pitch(cm.chunk * T);
   const int ntile = (nmax + 63) / 64;
   dim3 g(ntile * (ntile + 1) / 2, nchains);
-  const bool v4 = H % 8 == 0 && I % 4 == 0 &&
+  const bool vec = H % 8 == 0 && I % 4 == 0 &&
                   (((reinterpret_cast<uintptr_t>(D) | reinterpret_cast<uintptr_t>(hbuf) |
                      reinterpret_cast<uintptr_t>(x)) & 15) == 0);
-  if (v4)
-    hipLaunchKernelGGL(lstm_gram_v4_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+  if (vec)
+    hipLaunchKernelGGL(lstm_gram_v5_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
   else
     hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
   hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), 0, s, gram, coef, w, cm, nmax);
