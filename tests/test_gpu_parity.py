@@ -709,6 +709,32 @@ def test_wide_full_size_vs_torch(gn):
     assert max(perrs) <= TOL, perrs
 
 
+def test_overlapped_step_matches_serial(gn, dev):
+    """Models of at least 8 Mi parameters run the backward on two streams: the
+    dW GEMMs and bias sums next to the dX GEMMs, with the per-layer Adam
+    updates overlapped.  The per-kernel timing mode runs the same step with
+    every GEMM on one stream: loss, gradients and parameters must agree bit
+    for bit over two steps."""
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib
+    cfg = configs.wide(width=2048, classes=100, depth=2, B=256)
+    x, y = configs.inputs(cfg)
+    a = configs.build(cfg)
+    b = configs.build(cfg)
+    assert a.nparams >= 8 << 20
+    log(f"overlapped vs serial step, {a.nparams} params")
+    for _ in range(2):
+        la = a.TrainBatch(x, y)
+        assert lib().gn_timing_enable(dev.h, 1) == 0
+        try:
+            lb = b.TrainBatch(x, y)
+        finally:
+            assert lib().gn_timing_enable(dev.h, 0) == 0
+        assert la == lb
+        np.testing.assert_array_equal(a.Gradients(), b.Gradients())
+        np.testing.assert_array_equal(a.Params(), b.Params())
+
+
 # ------------------------------------------------------------------ error paths
 def test_errors_are_reported(gn, dev):
     from goneuron_amd import configs
