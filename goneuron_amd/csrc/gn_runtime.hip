@@ -985,7 +985,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       // parameters stay 0 (Q11); activations and gradients of the block
       const size_t rows = (size_t)max_batch * R.T, D = R.D, FF = R.FF;
       LayerRT::Tb &t = R.tb;
-      float **dbufs[] = {&t.Q, &t.K, &t.V, &t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2,
+      // Q, K, V in one block (their projections run as one batched GEMM)
+      if ((rc = model_alloc(M.get(), 3 * rows * D, &t.Q))) return rc;
+      t.K = t.Q + rows * D;
+      t.V = t.K + rows * D;
+      float **dbufs[] = {&t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2,
                          &t.GO, &t.GQ, &t.GK, &t.GV, &t.GX};
       for (float **b : dbufs)
         if ((rc = model_alloc(M.get(), rows * D, b))) return rc;
@@ -1305,10 +1309,22 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   const TbOff o = tb_offsets(D, FF, R.d.block_act, R.d.block_norm);
   const float *P = M->params + R.poff;
   LayerRT::Tb &t = R.tb;
-  // per-token projections: Q/K/V = X W^T + b (Dense with Linear activation)
-  HIP_OK(c, gemm_nt(c, X, P + o.wq, P + o.bq, t.Q, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
-  HIP_OK(c, gemm_nt(c, X, P + o.wk, P + o.bk, t.K, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
-  HIP_OK(c, gemm_nt(c, X, P + o.wv, P + o.bv, t.V, rows, D, D, EPI_BIAS_ACT, F_IDENTITY, nullptr));
+  // per-token projections: Q/K/V = X W^T + b (Dense with Linear activation),
+  // one launch for the three (equal strides between wQ, wK, wV, their biases
+  // and the Q, K, V buffers)
+  {
+    GemmArgs a{};
+    a.M = rows; a.N = D; a.K = D;
+    a.A = X; a.lda = D; a.B = P + o.wq; a.ldb = D;
+    a.C = t.Q; a.ldc = D; a.alpha = 1.f; a.bias = P + o.bq; a.act = F_IDENTITY;
+    a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+    a.nbatch = 3;
+    a.bstride_B = o.wk - o.wq;
+    a.bstride_bias = o.bk - o.bq;
+    a.bstride_C = t.K - t.Q;
+    KTimer kt(c, GN_KCLASS_GEMM);
+    HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream));
+  }
   {
     KTimer kt(c, GN_KCLASS_OTHER);
     if (R.d.use_rope) {  // transformer.go:457-461; the backward reads the rotated Q, K too

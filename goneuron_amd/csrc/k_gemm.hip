@@ -349,6 +349,16 @@ __device__ __forceinline__ void read_frags_direct(const float *S, int rowbase, i
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= n only.
 #define GN_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x3F70 | ((n) & 15) | (((n) >> 4) << 14))
 
+// Batched launches (gridDim.z > 1): the z-th GEMM's B, bias and C.
+__device__ __forceinline__ void batch_offsets(GemmArgs &p) {
+  if (gridDim.z > 1) {
+    const int64_t z = blockIdx.z;
+    p.B += z * p.bstride_B;
+    if (p.bias) p.bias += z * p.bstride_bias;
+    p.C += z * p.bstride_C;
+  }
+}
+
 // Block -> tile mapping.  Workgroups are dispatched round-robin over the 8
 // XCDs (each with its own L2), so consecutive block ids land on different
 // XCDs.  Remap so that each XCD receives a contiguous range of tile ids, and
@@ -498,6 +508,7 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   __shared__ __attribute__((aligned(16))) float As[2][TL::STAGE];
   __shared__ __attribute__((aligned(16))) float Bs[2][TL::STAGE];
 
+  batch_offsets(p);
   int tm, tn;
   tile_of_block(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * R, n0 = tn * R;
@@ -702,6 +713,7 @@ void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   __shared__ __attribute__((aligned(16))) float As[NS][RM * BKW];
   __shared__ __attribute__((aligned(16))) float Bs[NS][RN * BKW];
 
+  batch_offsets(p);
   int tm, tn;
   tile_of_block(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * RM, n0 = tn * RN;
@@ -842,7 +854,7 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int sp
 template <int R, bool AK, bool BKC, int EPI>
 static hipError_t launch_t(bool vec, bool ktail, const GemmArgs &a, int tm, int tn, int splits,
                           int kchunk, hipStream_t s) {
-  dim3 grid(tm * tn, splits), block(NT);
+  dim3 grid(tm * tn, splits, a.nbatch > 1 ? a.nbatch : 1), block(NT);
   if (R == 128 && vec && !ktail) {
     // Four-wave kernels: two blocks per CU (32-deep stages, 64 KB of LDS)
     // when there are at least two tiles per CU, else one (64-deep stages).
@@ -919,6 +931,19 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   if (splits > 1) {
     kchunk = ((a.K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (a.K + kchunk - 1) / kchunk;
+  }
+  if (a.nbatch > 1 && splits > 1) {
+    // split-K partials share one workspace: one launch per GEMM of the batch
+    for (int z = 0; z < a.nbatch; ++z) {
+      GemmArgs az = a;
+      az.nbatch = 1;
+      az.B += z * a.bstride_B;
+      if (az.bias) az.bias += z * a.bstride_bias;
+      az.C += z * a.bstride_C;
+      const hipError_t ez = launch_gemm(ta, tb, epi, az, s);
+      if (ez != hipSuccess) return ez;
+    }
+    return hipSuccess;
   }
   hipError_t e = big ? launch_r<128>(ta, tb, epi, vec, a, splits, kchunk, s)
                      : launch_r<64>(ta, tb, epi, vec, a, splits, kchunk, s);
