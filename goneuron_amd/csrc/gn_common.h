@@ -62,10 +62,10 @@ struct GemmArgs {
   float *ws;          // split-K workspace (may be null: no split)
   size_t ws_cap;      // floats
   int aux_div;        // EPI_DACT: > 1 reads aux row (row/aux_div)*aux_div + aux_div-1
-  // nbatch > 1: that many GEMMs sharing A, the z-th with B, bias and C
-  // advanced by z times these strides (floats)
+  // nbatch > 1: that many GEMMs, the z-th with A, B, bias and C advanced by
+  // z times these strides (floats; 0 shares the operand)
   int nbatch;
-  int64_t bstride_B, bstride_bias, bstride_C;
+  int64_t bstride_A, bstride_B, bstride_bias, bstride_C;
 };
 
 // EPI_SCALE    C = alpha*acc

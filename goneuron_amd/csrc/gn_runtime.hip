@@ -565,6 +565,7 @@ struct LayerRT {
   struct Tb {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
+    float *S3;  // token sums of gQ, gK, gV ([3][max batch][D])
     float *Z, *MG, *DZS;     // SwiGLU ff1: [gate | up] per token, token-0 mid grad, its dZ
     float *rcos, *rsin;      // RoPE angle tables [T][hd/2]
   } tb{};
@@ -998,6 +999,7 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), rows * 2, &t.st1))) return rc;
       if ((rc = model_alloc(M.get(), rows * 2, &t.st2))) return rc;
       if ((rc = model_alloc(M.get(), (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
+      if ((rc = model_alloc(M.get(), 3 * (size_t)max_batch * D, &t.S3))) return rc;
       if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
         if ((rc = model_alloc(M.get(), rows * 2 * FF, &t.Z))) return rc;
         if ((rc = model_alloc(M.get(), (size_t)max_batch * FF, &t.MG))) return rc;
@@ -1448,14 +1450,27 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     }
   }
   const float *gs[3] = {t.GQ, t.GK, t.GV};
-  const int64_t wo[3] = {o.wq, o.wk, o.wv}, bo[3] = {o.bq, o.bk, o.bv};
+  const int64_t bo[3] = {o.bq, o.bk, o.bv};
+  const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
   for (int k = 0; k < 3; ++k) {
-    {
-      KTimer kt(c, GN_KCLASS_OTHER);
-      HIP_OK(c, launch_token_sum(gs[k], t.S, B, T, D, c->stream));
-      HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + bo[k], cs, cap, c->stream));
-    }
-    HIP_OK(c, gemm_dw_last(c, t.S, X, G + wo[k], B, T, D, D, scale));
+    KTimer kt(c, GN_KCLASS_OTHER);
+    HIP_OK(c, launch_token_sum(gs[k], t.S3 + k * sst, B, T, D, c->stream));
+    HIP_OK(c, launch_colsum(t.S3 + k * sst, B, D, D, scale, G + bo[k], cs, cap, c->stream));
+  }
+  {
+    // dWq, dWk, dWv (Q10: token sums times the last token's input) in one
+    // launch: A strided over the token sums, B shared, C over the weights
+    GemmArgs a{};
+    a.M = D; a.N = D; a.K = B;
+    a.A = t.S3; a.lda = D;
+    a.B = X + (int64_t)(T - 1) * D; a.ldb = T * D;
+    a.C = G + o.wq; a.ldc = D; a.alpha = scale;
+    a.ws = cs; a.ws_cap = cap;
+    a.nbatch = 3;
+    a.bstride_A = sst;
+    a.bstride_C = o.wk - o.wq;
+    KTimer kt(c, GN_KCLASS_GEMM);
+    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
     HIP_OK(c, gemm_nn(c, t.GQ, P + o.wq, gin, rows, D, D, EPI_BIAS_ADD, 0, t.G2, 0));

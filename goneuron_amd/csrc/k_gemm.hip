@@ -349,10 +349,11 @@ __device__ __forceinline__ void read_frags_direct(const float *S, int rowbase, i
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= n only.
 #define GN_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x3F70 | ((n) & 15) | (((n) >> 4) << 14))
 
-// Batched launches (gridDim.z > 1): the z-th GEMM's B, bias and C.
+// Batched launches (gridDim.z > 1): the z-th GEMM's A, B, bias and C.
 __device__ __forceinline__ void batch_offsets(GemmArgs &p) {
   if (gridDim.z > 1) {
     const int64_t z = blockIdx.z;
+    p.A += z * p.bstride_A;
     p.B += z * p.bstride_B;
     if (p.bias) p.bias += z * p.bstride_bias;
     p.C += z * p.bstride_C;
@@ -932,11 +933,14 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
     kchunk = ((a.K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (a.K + kchunk - 1) / kchunk;
   }
-  if (a.nbatch > 1 && splits > 1) {
-    // split-K partials share one workspace: one launch per GEMM of the batch
+  const bool stride16 = ((a.bstride_A | a.bstride_B) & 3) == 0;
+  if (a.nbatch > 1 && (splits > 1 || !stride16)) {
+    // split-K partials share one workspace, and float4 legality is judged on
+    // the first member: one launch per GEMM of the batch
     for (int z = 0; z < a.nbatch; ++z) {
       GemmArgs az = a;
       az.nbatch = 1;
+      az.A += z * a.bstride_A;
       az.B += z * a.bstride_B;
       if (az.bias) az.bias += z * a.bstride_bias;
       az.C += z * a.bstride_C;
