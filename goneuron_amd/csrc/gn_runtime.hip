@@ -990,8 +990,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), 3 * rows * D, &t.Q))) return rc;
       t.K = t.Q + rows * D;
       t.V = t.K + rows * D;
-      float **dbufs[] = {&t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2,
-                         &t.GO, &t.GQ, &t.GK, &t.GV, &t.GX};
+      // gQ, gK, gV in one block too (their token sums run as one launch)
+      if ((rc = model_alloc(M.get(), 3 * rows * D, &t.GQ))) return rc;
+      t.GK = t.GQ + rows * D;
+      t.GV = t.GK + rows * D;
+      float **dbufs[] = {&t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2, &t.GO, &t.GX};
       for (float **b : dbufs)
         if ((rc = model_alloc(M.get(), rows * D, b))) return rc;
       if ((rc = model_alloc(M.get(), rows * FF, &t.MID))) return rc;
@@ -1449,13 +1452,15 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
       HIP_OK(c, launch_rope(t.GK, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
     }
   }
-  const float *gs[3] = {t.GQ, t.GK, t.GV};
   const int64_t bo[3] = {o.bq, o.bk, o.bv};
   const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
-  for (int k = 0; k < 3; ++k) {
+  {
     KTimer kt(c, GN_KCLASS_OTHER);
-    HIP_OK(c, launch_token_sum(gs[k], t.S3 + k * sst, B, T, D, c->stream));
-    HIP_OK(c, launch_colsum(t.S3 + k * sst, B, D, D, scale, G + bo[k], cs, cap, c->stream));
+    // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch over
+    // 3 * max batch samples (rows of samples >= B are stale and their sums unread)
+    HIP_OK(c, launch_token_sum(t.GQ, t.S3, 3 * M->maxB, T, D, c->stream));
+    for (int k = 0; k < 3; ++k)
+      HIP_OK(c, launch_colsum(t.S3 + k * sst, B, D, D, scale, G + bo[k], cs, cap, c->stream));
   }
   {
     // dWq, dWk, dWv (Q10: token sums times the last token's input) in one
