@@ -85,6 +85,10 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
 // db[o] = scale * sum_b dz[b*ld + o]
 hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
                          float *scratch, size_t scratch_cap, hipStream_t s);
+// up to 3 column sums of equal shape (dz[i] -> out[i]) in one launch pair
+hipError_t launch_colsum_multi(const float *const *dz, float *const *out, int n, int rows, int cols,
+                               int ld, float scale, float *scratch, size_t scratch_cap,
+                               hipStream_t s);
 
 // SwiGLU gating on Z = [gate | up] rows (2*out wide) and its backward into dZ
 hipError_t launch_swiglu_fwd(const float *Z, float *y, int B, int out, hipStream_t s);

@@ -1303,9 +1303,11 @@ static hipError_t tb_norm_bwd(gn_ctx *c, const LayerRT &R, const float *P, float
     e = launch_ln_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
   }
   if (e != hipSuccess) return e;
-  e = launch_colsum(t.GX, rows, D, D, scale, G + og, c->scratch, c->scratch_floats, c->stream);
-  if (e != hipSuccess || R.d.block_norm == GN_BLOCK_NORM_RMS) return e;
-  return launch_colsum(g, rows, D, D, scale, G + ob, c->scratch, c->scratch_floats, c->stream);
+  // gamma (and for LayerNorm beta) gradients in one launch pair
+  const float *src[2] = {t.GX, g};
+  float *dst[2] = {G + og, G + ob};
+  return launch_colsum_multi(src, dst, R.d.block_norm == GN_BLOCK_NORM_RMS ? 1 : 2, rows, D, D,
+                             scale, c->scratch, c->scratch_floats, c->stream);
 }
 
 static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
@@ -1459,8 +1461,9 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch over
     // 3 * max batch samples (rows of samples >= B are stale and their sums unread)
     HIP_OK(c, launch_token_sum(t.GQ, t.S3, 3 * M->maxB, T, D, c->stream));
-    for (int k = 0; k < 3; ++k)
-      HIP_OK(c, launch_colsum(t.S3 + k * sst, B, D, D, scale, G + bo[k], cs, cap, c->stream));
+    const float *src[3] = {t.S3, t.S3 + sst, t.S3 + 2 * sst};
+    float *dst[3] = {G + bo[0], G + bo[1], G + bo[2]};
+    HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
   }
   {
     // dWq, dWk, dWv (Q10: token sums times the last token's input) in one

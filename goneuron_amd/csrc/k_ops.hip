@@ -124,11 +124,20 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
 // averaged by grads *= 1/B, net.go:767-770).  Two passes: 64-column strips x
 // row chunks -> partials (one per chunk), then an in-order sum of partials.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(TPB) void colsum_partial(const float *__restrict__ dz, int rows,
-                                                      int cols, int ld, int rows_per_chunk,
-                                                      float *__restrict__ part, float scale,
-                                                      float *__restrict__ out) {
+// Up to three column sums of equal shape in one launch (blockIdx.z selects the
+// matrix); each member is summed exactly as a launch of its own.
+struct ColsumSet {
+  const float *dz[3];
+  float *out[3];
+};
+
+__global__ __launch_bounds__(TPB) void colsum_partial(ColsumSet set, int rows, int cols, int ld,
+                                                      int rows_per_chunk, float *__restrict__ part,
+                                                      float scale) {
   __shared__ float red[4][64];
+  const float *__restrict__ dz = set.dz[blockIdx.z];
+  float *__restrict__ out = set.out[blockIdx.z];
+  part += (size_t)blockIdx.z * gridDim.y * cols;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
   const int r0 = blockIdx.y * rows_per_chunk;
@@ -146,11 +155,13 @@ __global__ __launch_bounds__(TPB) void colsum_partial(const float *__restrict__ 
 }
 
 // One wave per column: lanes take the chunks, then a wave reduction.
-__global__ __launch_bounds__(TPB) void colsum_final(const float *__restrict__ part, int chunks,
-                                                    int cols, float scale, float *__restrict__ out) {
+__global__ __launch_bounds__(TPB) void colsum_final(ColsumSet set, const float *__restrict__ part,
+                                                    int chunks, int cols, float scale) {
   const int lane = threadIdx.x & 63;
   const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (col >= cols) return;
+  float *__restrict__ out = set.out[blockIdx.z];
+  part += (size_t)blockIdx.z * chunks * cols;
   float s = 0.f;
   for (int c = lane; c < chunks; c += 64) s += part[(size_t)c * cols + col];
 #pragma unroll
@@ -158,21 +169,44 @@ __global__ __launch_bounds__(TPB) void colsum_final(const float *__restrict__ pa
   if (lane == 0) out[col] = s * scale;
 }
 
-hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
-                         float *scratch, size_t scratch_cap, hipStream_t s) {
-  if (cols <= 0) return hipSuccess;
+static int colsum_chunks(int rows, int cols, size_t cap) {
   int chunks = (rows + 63) / 64;
   if (chunks > 64) chunks = 64;
-  if ((size_t)chunks * cols > scratch_cap) chunks = (int)(scratch_cap / cols);
-  if (chunks < 1) chunks = 1;
+  if ((size_t)chunks * cols > cap) chunks = (int)(cap / cols);
+  return chunks < 1 ? 1 : chunks;
+}
+
+hipError_t launch_colsum_multi(const float *const *dz, float *const *out, int n, int rows, int cols,
+                               int ld, float scale, float *scratch, size_t scratch_cap,
+                               hipStream_t s) {
+  if (cols <= 0 || n <= 0) return hipSuccess;
+  if (n > 3) return hipErrorInvalidValue;
+  const int chunks = colsum_chunks(rows, cols, scratch_cap);
+  if (n > 1 && chunks > 1 && (size_t)n * chunks * cols > scratch_cap) {
+    for (int i = 0; i < n; ++i) {  // partials of all members do not fit: one at a time
+      const hipError_t e = launch_colsum_multi(dz + i, out + i, 1, rows, cols, ld, scale, scratch,
+                                               scratch_cap, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  ColsumSet set{};
+  for (int i = 0; i < n; ++i) {
+    set.dz[i] = dz[i];
+    set.out[i] = out[i];
+  }
   const int rpc = (rows + chunks - 1) / chunks;
-  dim3 g1((cols + 63) / 64, chunks);
-  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, dz, rows, cols, ld, rpc, scratch, scale,
-                     out);
+  dim3 g1((cols + 63) / 64, chunks, n);
+  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, set, rows, cols, ld, rpc, scratch, scale);
   if (chunks > 1)
-    hipLaunchKernelGGL(colsum_final, dim3((cols + 3) / 4), dim3(TPB), 0, s, scratch, chunks, cols,
-                       scale, out);
+    hipLaunchKernelGGL(colsum_final, dim3((cols + 3) / 4, 1, n), dim3(TPB), 0, s, set, scratch,
+                       chunks, cols, scale);
   return hipGetLastError();
+}
+
+hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
+                         float *scratch, size_t scratch_cap, hipStream_t s) {
+  return launch_colsum_multi(&dz, &out, 1, rows, cols, ld, scale, scratch, scratch_cap, s);
 }
 
 // ---------------------------------------------------------------------------
