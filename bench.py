@@ -112,47 +112,6 @@ def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
                               "sample": f"{n1} of {B} samples fwd+bwd ({ts1:.2f} s) + Adam scaled by n/B"}}
 
 
-def mfma_probe():
-    """The fp32 MFMA rate the part sustains: gn_probe_mfma at 4, 8 and 16 waves
-    per CU and 4-11 ms per launch."""
-    import ctypes as C
-    import goneuron_amd as gn
-    from goneuron_amd._lib import lib, check
-    dev = gn.GetDefaultDevice()
-    for blocks, iters in ((512, 20000), (512, 20000), (1024, 20000), (1024, 20000), (512, 50000),
-                          (256, 100000)):
-        ms, tf = C.c_double(), C.c_double()
-        check(dev.h, lib().gn_probe_mfma(dev.h, blocks, iters, C.byref(ms), C.byref(tf)))
-        print(json.dumps({"mfma_probe_blocks": blocks, "iters": iters, "ms": ms.value,
-                          "tflops": tf.value, "frac_of_peak": tf.value / PEAK_FP32_MFMA_TFLOPS}),
-              flush=True)
-
-
-def library_sgemm():
-    """The vendor library (torch.mm, fp32) on the C3 forward shape: a practical
-    ceiling for the hand-written GEMM, run in a process of its own because
-    torch ships its own HIP runtime. The library never calls it."""
-    import torch
-    torch.backends.cuda.matmul.allow_tf32 = False
-    g = torch.Generator().manual_seed(0)
-    a = torch.randn(1024, 4096, generator=g).to("cuda:0")
-    b = torch.randn(4096, 4096, generator=g).to("cuda:0")
-    c = torch.empty(1024, 4096, device="cuda:0")
-    for _ in range(5):
-        torch.mm(a, b, out=c)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 50
-    e0.record()
-    for _ in range(reps):
-        torch.mm(a, b, out=c)
-    e1.record()
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    tf = 2 * 1024 * 4096 * 4096 / (ms * 1e-3) / 1e12
-    print(json.dumps({"library_sgemm": "torch.mm fp32 1024x4096 @ 4096x4096", "ms": ms,
-                      "tflops": tf, "frac_of_peak": tf / PEAK_FP32_MFMA_TFLOPS}), flush=True)
-
-
 def predict_bench(args, cfg, model, dev, dx, B, workers):
     """Inference throughput (f3): K forward passes in inference mode over the
     config's batch, inputs and outputs in HBM."""
@@ -200,11 +159,6 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="threads of the parallel CPU baseline (default min(B, cores, 16))")
-    ap.add_argument("--mfma-probe", action="store_true",
-                    help="only run the matrix-core probe (back-to-back fp32 MFMA at 2, 4 and 8 "
-                         "waves per SIMD, short and sustained) and print its rates")
-    ap.add_argument("--library-sgemm", action="store_true",
-                    help="only time torch.mm (fp32) on the C3 forward GEMM shape, as a reference point")
     ap.add_argument("--predict", action="store_true",
                     help="time the inference path instead (Sequential.PredictBatch: forward in "
                          "inference mode on HBM-resident inputs, gn_model_predict_device)")
@@ -219,12 +173,6 @@ def main():
 
     if args.copy_probe:
         copy_probe(args.copy_probe)
-        return
-    if args.mfma_probe:
-        mfma_probe()
-        return
-    if args.library_sgemm:
-        library_sgemm()
         return
 
     import ctypes as C
@@ -248,6 +196,9 @@ def main():
     dx, dy = dbuf(x), dbuf(y)
     if args.predict:
         predict_bench(args, cfg, model, dev, dx, B, workers)
+        check(dev.h, lib().gn_free(dev.h, dx))
+        check(dev.h, lib().gn_free(dev.h, dy))
+        model.Close()
         return
     step = lambda: check(dev.h, lib().gn_model_train_step_device(model.h, dx, dy, B))
     for _ in range(args.warmup):
@@ -343,6 +294,10 @@ def main():
         },
         "loss": loss.value,
     }
+    # explicit, ordered teardown: input buffers, the model, then (atexit) the device
+    check(dev.h, lib().gn_free(dev.h, dx))
+    check(dev.h, lib().gn_free(dev.h, dy))
+    model.Close()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget, workers, args.cpu_threads)
     else:

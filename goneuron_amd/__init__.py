@@ -13,7 +13,9 @@ Every step runs on the GPU (hand-written HIP kernels); there is no CPU path.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -328,6 +330,28 @@ class HIPDevice:
 
 
 _default = None
+_live_models = weakref.WeakSet()
+
+
+def _teardown():
+    """At interpreter exit: destroy every live model, then shut the default
+    device down, in that order and before module finalisation, so no HIP call
+    runs from a finalizer after the runtime has started to unload."""
+    global _default
+    for m in list(_live_models):
+        try:
+            m.Close()
+        except Exception:
+            pass
+    if _default is not None:
+        try:
+            _default.close()
+        except Exception:
+            pass
+        _default = None
+
+
+atexit.register(_teardown)
 
 
 def GetDefaultDevice() -> HIPDevice:
@@ -382,6 +406,7 @@ class Sequential:
                                                    C.byref(ad), max_batch, self.workers, C.byref(h)))
         self.h = h
         self.max_batch = max_batch
+        _live_models.add(self)
         n = C.c_int64()
         check(self.device.h, lib().gn_model_nparams(self.h, C.byref(n)))
         self.nparams = n.value
@@ -396,7 +421,26 @@ class Sequential:
         self.device = device
 
     def SetTraining(self, training):
+        """Network.SetTraining (net.go:187-193)."""
         self._ck(lib().gn_model_set_training(self.h, int(training)))
+
+    def IsTraining(self, i):
+        t = C.c_int32()
+        self._ck(lib().gn_model_get_training(self.h, i, C.byref(t)))
+        return bool(t.value)
+
+    def _reserve(self, B):
+        """Batch-sized buffers for B samples; every other piece of state stays."""
+        if B > self.max_batch:
+            self._ck(lib().gn_model_reserve(self.h, B))
+            self.max_batch = B
+
+    def SkippedSamples(self):
+        """Samples the last TrainBatch skipped (Embedding index out of range;
+        the reference's batch loop drops them, net.go:738-741)."""
+        n = C.c_int32()
+        self._ck(lib().gn_model_skipped_samples(self.h, C.byref(n)))
+        return n.value
 
     def TrainBatch(self, batchX, batchY) -> float:
         """Network.TrainBatch (net.go:412-436): fwd + bwd + Adam; returns mean loss."""
@@ -405,14 +449,15 @@ class Sequential:
         B = x.shape[0]
         if B == 0:
             return 0.0  # net.go:414-417
-        if B > self.max_batch:
-            self._create(B)
+        self._reserve(B)
         loss = C.c_float()
         self._ck(lib().gn_model_train_step(self.h, _fp(x), _fp(y), B, C.byref(loss)))
         return loss.value
 
     def Fit(self, trainX, trainY, epochs, batchSize, callbacks=()):
-        """Network.Fit (net.go:351-408) without callbacks' side effects."""
+        """Network.Fit (net.go:351-408) without callbacks' side effects: sets
+        training mode, then TrainBatch over the batches of every epoch."""
+        self.SetTraining(True)
         x = _f32(trainX)
         y = _f32(trainY)
         n = x.shape[0]
@@ -429,8 +474,7 @@ class Sequential:
     def PredictBatch(self, x):
         x = _f32(x)
         B = x.shape[0]
-        if B > self.max_batch:
-            self._create(B)
+        self._reserve(B)
         out = np.empty((B, self.out_size), np.float32)
         self._ck(lib().gn_model_predict(self.h, _fp(x), B, _fp(out)))
         return out

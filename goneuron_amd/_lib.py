@@ -87,6 +87,9 @@ SIGNATURES = {
     "gn_model_predict": (C.c_int, [vp, f32p, C.c_int32, f32p]),
     "gn_model_predict_device": (C.c_int, [vp, vp, C.c_int32, vp]),
     "gn_model_set_training": (C.c_int, [vp, C.c_int32]),
+    "gn_model_get_training": (C.c_int, [vp, C.c_int32, i32p]),
+    "gn_model_reserve": (C.c_int, [vp, C.c_int32]),
+    "gn_model_skipped_samples": (C.c_int, [vp, i32p]),
     "gn_model_layer_output": (C.c_int, [vp, C.c_int32, f32p, C.c_int64]),
     "gn_model_layer_argmax": (C.c_int, [vp, C.c_int32, i32p, C.c_int64]),
     "gn_model_get_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
@@ -110,7 +113,6 @@ SIGNATURES = {
     "gn_fill_class_ids": (C.c_int, [i32p, C.c_int64, C.c_int32, C.c_uint64]),
     "gn_timing_enable": (C.c_int, [vp, C.c_int]),
     "gn_timing_report": (C.c_int, [vp, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
-    "gn_probe_mfma": (C.c_int, [vp, C.c_int32, C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
 _lib = None

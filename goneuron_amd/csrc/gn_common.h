@@ -102,9 +102,17 @@ hipError_t launch_dact(const float *g, const float *out, float *dz, int64_t n, i
 // Output-layer row kernel: forward row activation (softmax/logsoftmax/none),
 // per-sample loss, loss gradient, and dz through the activation's Jacobian
 // (Q4).  z holds pre-activations [B,C]; out receives the activation output.
+// bad (may be null): samples the batch loop skips (an Embedding index error).
+// workers == 1: a bad sample adds no loss and no gradient (net.go:738-741);
+// workers > 1: a worker stops at its chunk's first bad sample and its chunk
+// loss is lost (net.go:641-644, 653-655).
 hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz, float *loss_rows,
-                           int B, int C, int row_act, int deriv, int loss_kind, hipStream_t s);
+                           int B, int C, int row_act, int deriv, int loss_kind, const int32_t *bad,
+                           int workers, hipStream_t s);
 enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMWISE = 3 };
+
+// dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
+hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);
 
 // Row activation only (forward/predict)
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s);
@@ -145,6 +153,9 @@ hipError_t launch_bn_fwd(const float *x, const float *gb, float *y, float *st, f
                          int B, int C, int HW, float eps, float mom, int training, hipStream_t s);
 hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const float *st, float *dx,
                          float *part, int B, int C, int HW, hipStream_t s);
+// inference-mode backward: dx = g * gamma / std(running var); no parameter gradient
+hipError_t launch_bn_bwd_eval(const float *g, const float *gb, const float *rv, float *dx, int B,
+                              int C, int HW, float eps, hipStream_t s);
 hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
 hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
 
@@ -197,14 +208,18 @@ hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, 
                               hipStream_t s);
 
 // ---- Transformer path ----
-hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int rows, int V,
-                        int D, int *err, hipStream_t s);
+// bad (may be null): per-sample flag, 1 when one of its ids lies outside [0, V)
+hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int B, int T, int V,
+                        int D, int32_t *bad, hipStream_t s);
 hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int TD, hipStream_t s);
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
-                             int D, int W, float scale, hipStream_t s);
+                             int D, int W, float scale, const int32_t *bad, hipStream_t s);
 hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
 hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipStream_t s);
 hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s);
+// nmem token sums in one launch: member m reads X + m*xstride, writes S + m*sstride
+hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N, int nmem,
+                                  int64_t xstride, int64_t sstride, hipStream_t s);
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
                          int rows, int N, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
@@ -224,8 +239,6 @@ hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
                            hipStream_t s);
 
-// ---- measurement probe ----
-hipError_t launch_mfma_probe(float *out, int blocks, int iters, hipStream_t s);
 
 // ---- model views for the checkpoint writers (gn_runtime.hip) ----
 int model_layer_count(gn_model *M);

@@ -237,32 +237,6 @@ extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
   return GN_OK;
 }
 
-extern "C" int gn_probe_mfma(gn_ctx *c, int32_t blocks, int32_t iters, double *ms, double *tflops) {
-  ENTRY(c);
-  if (blocks <= 0 || iters <= 0 || !ms || !tflops) return set_err(c, GN_ERR_INVALID, "bad probe args");
-  float *out = nullptr;
-  if (hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) != hipSuccess)
-    return set_err(c, GN_ERR_OOM, "probe buffer");
-  hipEvent_t a = nullptr, b = nullptr;
-  hipError_t e = hipEventCreate(&a);
-  if (e == hipSuccess) e = hipEventCreate(&b);
-  if (e == hipSuccess) e = launch_mfma_probe(out, blocks, 16, c->stream);  // warm-up
-  if (e == hipSuccess) e = hipEventRecord(a, c->stream);
-  if (e == hipSuccess) e = launch_mfma_probe(out, blocks, iters, c->stream);
-  if (e == hipSuccess) e = hipEventRecord(b, c->stream);
-  if (e == hipSuccess) e = hipEventSynchronize(b);
-  float t = 0.f;
-  if (e == hipSuccess) e = hipEventElapsedTime(&t, a, b);
-  if (a) (void)hipEventDestroy(a);
-  if (b) (void)hipEventDestroy(b);
-  (void)hipFree(out);
-  HIP_OK(c, e);
-  *ms = t;
-  // 4 waves per block, 4 MFMAs of 32x32x2 (4096 FLOP) per wave and iteration
-  *tflops = (double)blocks * 4 * 4 * 4096.0 * iters / (t * 1e-3) / 1e12;
-  return GN_OK;
-}
-
 extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *total_ms) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
@@ -542,7 +516,9 @@ struct LayerRT {
   // Embedding / PositionalEncoding / TransformerBlock / CLSPooling
   int V = 0, D = 0, NH = 0, FF = 0, causal = 0;
   int32_t *ids = nullptr;
-  int *err = nullptr;  // device error flag (Embedding: bad id; LSTM: cooperative wait timeout)
+  int32_t *bad = nullptr;  // Embedding: per-sample index-error flags [max batch]
+  int *err = nullptr;      // LSTM: cooperative wait timeout flag
+  int train = 1;           // training flag (SetTraining): Dropout, BatchNorm2D and MoE read it
   // RMSNorm over rows of D: per-row rms and g * x / rms for the gamma sums
   float *rmsv = nullptr, *gx = nullptr;
   float eps = 0.f;
@@ -583,9 +559,17 @@ struct gn_model {
   int timestep = 0;
   float *loss_rows = nullptr, *loss_dev = nullptr;
   float *xin = nullptr, *yin = nullptr;  // staging for host inputs
-  int training = 1;
   int last_B = 0;
-  std::vector<void *> owned;
+  bool last_predict = false;  // the last pass was an inference forward
+  int skipped = 0;            // samples the last training step skipped (Embedding index errors)
+  std::vector<void *> owned;   // state allocations (arena, tables, running statistics)
+  std::vector<void *> bowned;  // batch-sized buffers (rebuilt by gn_model_reserve)
+  // training flags of the trainBatchParallel worker clones: LightweightClone
+  // copies each layer's flag when the clone is made (dropout.go:410-418,
+  // batchnorm2d.go:786-808, moe.go:424) and Network.SetTraining never reaches
+  // the clones (net.go:187-193), so they keep it for the network's lifetime
+  std::vector<std::vector<char>> clone_train;
+  std::vector<char> eff;  // flags in effect for the current pass, per layer
   // train steps update each layer's parameters on ctx->aux as soon as that
   // layer's backward is done, overlapping Adam with the rest of the backward
   bool overlap_adam = true;
@@ -633,6 +617,7 @@ extern "C" void gn_model_destroy(gn_model *M) {
   (void)hipStreamSynchronize(M->ctx->aux);
   for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
+  for (void *p : M->bowned) (void)hipFree(p);
   for (void *p : M->owned) (void)hipFree(p);
   delete M;
 }
@@ -737,6 +722,163 @@ static TbOff tb_offsets(int D, int FF, int act = GN_BLOCK_ACT_RELU, int norm = G
 static void infer_hw(int channel_size, int &H, int &W) {
   H = (int)sqrt((double)channel_size);
   W = (H * H == channel_size) ? H : (H > 0 ? channel_size / H : 0);
+}
+
+static int model_balloc(gn_model *M, size_t floats, float **p) {
+  void *q = nullptr;
+  if (hipMalloc(&q, std::max<size_t>(floats, 1) * sizeof(float)) != hipSuccess) {
+    *p = nullptr;
+    return set_err(M->ctx, GN_ERR_OOM, "hipMalloc(%zu floats) failed", floats);
+  }
+  M->bowned.push_back(q);
+  *p = (float *)q;
+  return GN_OK;
+}
+
+static void free_batch(gn_model *M) {
+  for (void *p : M->bowned) (void)hipFree(p);
+  M->bowned.clear();
+  M->last_B = 0;
+}
+
+// Every buffer whose size follows the batch: layer outputs and output
+// gradients, the state layers save for their backward, staging for host
+// inputs.  Sized for M->maxB samples.
+static int alloc_batch(gn_model *M) {
+  gn_ctx *c = M->ctx;
+  const int nlayers = (int)M->L.size();
+  const int max_batch = M->maxB;
+  int rc;
+  for (int i = 0; i < nlayers; ++i) {
+    LayerRT &R = M->L[i];
+    if (R.d.kind == GN_LAYER_EMBEDDING) {
+      float *tmp = nullptr;
+      if ((rc = model_balloc(M, (size_t)max_batch * R.T, &tmp))) return rc;
+      R.ids = reinterpret_cast<int32_t *>(tmp);
+      if ((rc = model_balloc(M, (size_t)max_batch + 64, &tmp))) return rc;
+      R.bad = reinterpret_cast<int32_t *>(tmp);
+      HIP_OK(c, hipMemsetAsync(R.bad, 0, (size_t)max_batch * sizeof(int32_t), c->stream));
+    }
+    if (R.d.kind == GN_LAYER_TRANSFORMER) {
+      // activations and gradients of the block
+      const size_t rows = (size_t)max_batch * R.T, D = R.D, FF = R.FF;
+      LayerRT::Tb &t = R.tb;
+      // Q, K, V in one block (their projections run as one batched GEMM)
+      if ((rc = model_balloc(M, 3 * rows * D, &t.Q))) return rc;
+      t.K = t.Q + rows * D;
+      t.V = t.K + rows * D;
+      // gQ, gK, gV in one block too (their token sums run as one launch)
+      if ((rc = model_balloc(M, 3 * rows * D, &t.GQ))) return rc;
+      t.GK = t.GQ + rows * D;
+      t.GV = t.GK + rows * D;
+      float **dbufs[] = {&t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2, &t.GO, &t.GX};
+      for (float **b : dbufs)
+        if ((rc = model_balloc(M, rows * D, b))) return rc;
+      if ((rc = model_balloc(M, rows * FF, &t.MID))) return rc;
+      if ((rc = model_balloc(M, rows * FF, &t.DZ1))) return rc;
+      if ((rc = model_balloc(M, rows * 2, &t.st1))) return rc;
+      if ((rc = model_balloc(M, rows * 2, &t.st2))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
+      if ((rc = model_balloc(M, 3 * (size_t)max_batch * D, &t.S3))) return rc;
+      if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
+        if ((rc = model_balloc(M, rows * 2 * FF, &t.Z))) return rc;
+        if ((rc = model_balloc(M, (size_t)max_batch * FF, &t.MG))) return rc;
+        if ((rc = model_balloc(M, (size_t)max_batch * 2 * FF, &t.DZS))) return rc;
+      }
+    }
+    if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
+      const size_t Bm = max_batch, T = R.T, H = R.H;
+      if ((rc = model_balloc(M, Bm * T * H, &R.xw))) return rc;
+      if ((rc = model_balloc(M, Bm * T * H, &R.igb))) return rc;
+      if ((rc = model_balloc(M, Bm * T * H, &R.tcb))) return rc;
+      if ((rc = model_balloc(M, Bm * T * H, &R.cbuf))) return rc;
+      if ((rc = model_balloc(M, Bm * (T + 1) * H, &R.hbuf))) return rc;
+      if ((rc = model_balloc(M, Bm * (T + 1) * 4 * H, &R.Dg))) return rc;
+      if ((rc = model_balloc(M, Bm * 4 * H, &R.S))) return rc;
+      if ((rc = model_balloc(M, Bm * (T + 1), &R.wts))) return rc;
+      const int Wc = std::min(std::max(M->workers, 1), max_batch);
+      const size_t chunk = (max_batch + Wc - 1) / Wc;
+      const size_t nmax = (size_t)lstm_gram_pitch((int)(chunk * T));
+      const size_t nchains = (max_batch + chunk - 1) / chunk;
+      float *g = nullptr, *cf = nullptr;
+      if ((rc = model_balloc(M, 2 * nchains * nmax * nmax, &g))) return rc;
+      if ((rc = model_balloc(M, 2 * nchains * nmax, &cf))) return rc;
+      R.gram = reinterpret_cast<double *>(g);
+      R.coef = reinterpret_cast<double *>(cf);
+      R.lsync = nullptr;
+      R.err = nullptr;
+      R.lcoop = false;
+      R.lepoch = 0;
+      if (lstm_coop_eligible(max_batch, (int)H)) {
+        const size_t bytes = lstm_coop_sync_bytes(max_batch, (int)H);
+        float *sy = nullptr, *er = nullptr;
+        if ((rc = model_balloc(M, (bytes + 3) / 4, &sy))) return rc;
+        if ((rc = model_balloc(M, 64, &er))) return rc;
+        HIP_OK(c, hipMemsetAsync(sy, 0, bytes, c->stream));
+        HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
+        R.lsync = sy;
+        R.err = reinterpret_cast<int *>(er);
+        R.lcoop = true;
+      }
+    }
+    if (R.d.kind == GN_LAYER_MOE) {
+      const size_t Bm = max_batch, E = R.E, O = R.d.out_size;
+      float *tmp = nullptr;
+      if ((rc = model_balloc(M, Bm * E, &R.mlog))) return rc;
+      if ((rc = model_balloc(M, Bm * E, &R.mprob))) return rc;
+      if ((rc = model_balloc(M, Bm * E, &R.mdzg))) return rc;
+      if ((rc = model_balloc(M, E * Bm * O, &R.meout))) return rc;
+      if ((rc = model_balloc(M, E * Bm * O, &R.medz))) return rc;
+      if ((rc = model_balloc(M, Bm * R.K, &tmp))) return rc;
+      R.mact = reinterpret_cast<int32_t *>(tmp);
+    }
+    if (R.d.kind == GN_LAYER_GRU_UNROLLER) {
+      const size_t rows = (size_t)max_batch * R.T, H = R.H;
+      if ((rc = model_balloc(M, rows * 3 * H, &R.xw))) return rc;
+      if ((rc = model_balloc(M, rows * 3 * H, &R.gpre))) return rc;
+      if ((rc = model_balloc(M, rows * H, &R.ghprev))) return rc;
+      if ((rc = model_balloc(M, rows * H, &R.grh))) return rc;
+      if ((rc = model_balloc(M, rows * 3 * H, &R.Dg))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * 3 * H, &R.S))) return rc;
+    }
+    if (R.d.kind == GN_LAYER_BATCHNORM2D) {
+      if ((rc = model_balloc(M, (size_t)max_batch * R.C * 3, &R.bnst))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * R.C * 2, &R.bnpart))) return rc;
+    }
+    if (R.d.kind == GN_LAYER_SWIGLU) {
+      if ((rc = model_balloc(M, (size_t)max_batch * 2 * R.out_len, &R.zbuf))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * 2 * R.out_len, &R.dzbuf))) return rc;
+    }
+    if (R.d.kind == GN_LAYER_RMSNORM) {
+      if ((rc = model_balloc(M, (size_t)max_batch * (R.in_len / R.D), &R.rmsv))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * R.in_len, &R.gx))) return rc;
+    }
+    if (R.d.kind == GN_LAYER_MAXPOOL2D) {
+      float *am = nullptr;
+      if ((rc = model_balloc(M, (size_t)max_batch * R.out_len, &am))) return rc;
+      R.argmax = reinterpret_cast<int32_t *>(am);
+    }
+    if (R.d.kind == GN_LAYER_FLATTEN) {
+      // reshape.go:64-96: identity both ways; share the neighbours' buffers
+      R.out_alias = true;
+      R.gout_alias = true;
+      R.gout = i > 0 ? M->L[i - 1].gout : nullptr;
+      continue;
+    }
+    if ((rc = model_balloc(M, (size_t)max_batch * R.out_len, &R.out))) return rc;
+    if (R.d.kind == GN_LAYER_POSENC && i > 0) {
+      // PositionalEncoding.Backward returns its input gradient unchanged
+      // (transformer.go:112-118): share the buffer with the layer below
+      R.gout = M->L[i - 1].gout;
+      R.gout_alias = true;
+    } else if ((rc = model_balloc(M, (size_t)max_batch * R.out_len, &R.gout))) {
+      return rc;
+    }
+  }
+  if ((rc = model_balloc(M, (size_t)max_batch, &M->loss_rows))) return rc;
+  if ((rc = model_balloc(M, (size_t)max_batch * M->L[0].in_len, &M->xin))) return rc;
+  if ((rc = model_balloc(M, (size_t)max_batch * M->L.back().out_len, &M->yin))) return rc;
+  return GN_OK;
 }
 
 extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t nlayers,
@@ -965,132 +1107,57 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
   M->v = M->arena + 3 * M->region;
   HIP_OK(c, hipMemsetAsync(M->arena, 0, (size_t)M->region * 4 * sizeof(float), c->stream));
 
+  // Initial parameters (the reference's seeded LCG per layer) and the state
+  // that does not depend on the batch size; the batch-sized buffers follow in
+  // alloc_batch, which gn_model_reserve reruns for a larger batch.
   std::vector<float> host((size_t)std::max<int64_t>(off, 1), 0.f);
-  int maxw = 0;
   for (int i = 0; i < nlayers; ++i) {
     LayerRT &R = M->L[i];
-    maxw = std::max(maxw, std::max(R.in_len, R.out_len));
+    // training flags as the layers are constructed: Dropout and BatchNorm2D
+    // start in training mode (dropout.go:56, batchnorm2d.go:88), MoE does not
+    // (NewMoE leaves its flag false, moe.go:46-90)
+    R.train = R.d.kind == GN_LAYER_MOE ? 0 : 1;
     if (R.d.kind == GN_LAYER_DENSE) init_dense(host.data() + R.poff, R.d.in_size, R.d.out_size);
     if (R.d.kind == GN_LAYER_CONV2D) init_conv(host.data() + R.poff, R.cs.inC, R.cs.outC, R.cs.k);
-    if (R.d.kind == GN_LAYER_EMBEDDING) {
-      init_embedding(host.data() + R.poff, R.V, R.D);
-      float *tmp = nullptr;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.T, &tmp))) return rc;
-      R.ids = reinterpret_cast<int32_t *>(tmp);
-      if ((rc = model_alloc(M.get(), 64, &tmp))) return rc;
-      R.err = reinterpret_cast<int *>(tmp);
-      HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
-    }
+    if (R.d.kind == GN_LAYER_EMBEDDING) init_embedding(host.data() + R.poff, R.V, R.D);
     if (R.d.kind == GN_LAYER_POSENC) init_posenc(host.data() + R.poff, R.T, R.D);
-    if (R.d.kind == GN_LAYER_TRANSFORMER) {
-      // parameters stay 0 (Q11); activations and gradients of the block
-      const size_t rows = (size_t)max_batch * R.T, D = R.D, FF = R.FF;
+    if (R.d.kind == GN_LAYER_TRANSFORMER && R.d.use_rope) {
+      // parameters stay 0 (Q11); applyRoPE's angles (transformer.go:215-221)
+      // in float32, computed once
       LayerRT::Tb &t = R.tb;
-      // Q, K, V in one block (their projections run as one batched GEMM)
-      if ((rc = model_alloc(M.get(), 3 * rows * D, &t.Q))) return rc;
-      t.K = t.Q + rows * D;
-      t.V = t.K + rows * D;
-      // gQ, gK, gV in one block too (their token sums run as one launch)
-      if ((rc = model_alloc(M.get(), 3 * rows * D, &t.GQ))) return rc;
-      t.GK = t.GQ + rows * D;
-      t.GV = t.GK + rows * D;
-      float **dbufs[] = {&t.O, &t.RES1, &t.N1, &t.RES2, &t.G1, &t.COMB, &t.G2, &t.GO, &t.GX};
-      for (float **b : dbufs)
-        if ((rc = model_alloc(M.get(), rows * D, b))) return rc;
-      if ((rc = model_alloc(M.get(), rows * FF, &t.MID))) return rc;
-      if ((rc = model_alloc(M.get(), rows * FF, &t.DZ1))) return rc;
-      if ((rc = model_alloc(M.get(), rows * 2, &t.st1))) return rc;
-      if ((rc = model_alloc(M.get(), rows * 2, &t.st2))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
-      if ((rc = model_alloc(M.get(), 3 * (size_t)max_batch * D, &t.S3))) return rc;
-      if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
-        if ((rc = model_alloc(M.get(), rows * 2 * FF, &t.Z))) return rc;
-        if ((rc = model_alloc(M.get(), (size_t)max_batch * FF, &t.MG))) return rc;
-        if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * FF, &t.DZS))) return rc;
-      }
-      if (R.d.use_rope) {
-        // applyRoPE's angles (transformer.go:215-221) in float32, computed once
-        const int hd = R.D / R.NH, half = hd / 2;
-        std::vector<float> cs((size_t)R.T * std::max(half, 1)), sn(cs.size());
-        for (int tt = 0; tt < R.T; ++tt)
-          for (int k = 0; k < half; ++k) {
-            const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
-            const float m = (float)tt * theta;
-            cs[(size_t)tt * half + k] = (float)cos((double)m);
-            sn[(size_t)tt * half + k] = (float)sin((double)m);
-          }
-        if ((rc = model_alloc(M.get(), cs.size(), &t.rcos))) return rc;
-        if ((rc = model_alloc(M.get(), sn.size(), &t.rsin))) return rc;
-        HIP_OK(c, hipMemcpyAsync(t.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice,
-                                 c->stream));
-        HIP_OK(c, hipMemcpyAsync(t.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice,
-                                 c->stream));
-        // the host vectors go out of scope: finish the copies first
-        HIP_OK(c, hipStreamSynchronize(c->stream));
-      }
+      const int hd = R.D / R.NH, half = hd / 2;
+      std::vector<float> cs((size_t)R.T * std::max(half, 1)), sn(cs.size());
+      for (int tt = 0; tt < R.T; ++tt)
+        for (int k = 0; k < half; ++k) {
+          const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
+          const float m = (float)tt * theta;
+          cs[(size_t)tt * half + k] = (float)cos((double)m);
+          sn[(size_t)tt * half + k] = (float)sin((double)m);
+        }
+      if ((rc = model_alloc(M.get(), cs.size(), &t.rcos))) return rc;
+      if ((rc = model_alloc(M.get(), sn.size(), &t.rsin))) return rc;
+      HIP_OK(c, hipMemcpyAsync(t.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+      HIP_OK(c, hipMemcpyAsync(t.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+      // the host vectors go out of scope: finish the copies first
+      HIP_OK(c, hipStreamSynchronize(c->stream));
     }
     if (R.d.kind == GN_LAYER_LSTM_UNROLLER) {
       init_lstm(host.data() + R.poff, R.I, R.H);
-      const size_t Bm = max_batch, T = R.T, H = R.H;
-      if ((rc = model_alloc(M.get(), H * H, &R.WhT))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * T * H, &R.xw))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * T * H, &R.igb))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * T * H, &R.tcb))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * T * H, &R.cbuf))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * (T + 1) * H, &R.hbuf))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * (T + 1) * 4 * H, &R.Dg))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * 4 * H, &R.S))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * (T + 1), &R.wts))) return rc;
-      const int Wc = std::min(std::max(M->workers, 1), max_batch);
-      const size_t chunk = (max_batch + Wc - 1) / Wc;
-      const size_t nmax = (size_t)lstm_gram_pitch((int)(chunk * T));
-      const size_t nchains = (max_batch + chunk - 1) / chunk;
-      float *g = nullptr, *cf = nullptr;
-      if ((rc = model_alloc(M.get(), 2 * nchains * nmax * nmax, &g))) return rc;
-      if ((rc = model_alloc(M.get(), 2 * nchains * nmax, &cf))) return rc;
-      R.gram = reinterpret_cast<double *>(g);
-      R.coef = reinterpret_cast<double *>(cf);
-      if (lstm_coop_eligible(max_batch, (int)H)) {
-        const size_t bytes = lstm_coop_sync_bytes(max_batch, (int)H);
-        float *sy = nullptr, *er = nullptr;
-        if ((rc = model_alloc(M.get(), (bytes + 3) / 4, &sy))) return rc;
-        if ((rc = model_alloc(M.get(), 64, &er))) return rc;
-        HIP_OK(c, hipMemsetAsync(sy, 0, bytes, c->stream));
-        HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
-        R.lsync = sy;
-        R.err = reinterpret_cast<int *>(er);
-        R.lcoop = true;
-      }
+      if ((rc = model_alloc(M.get(), (size_t)R.H * R.H, &R.WhT))) return rc;
     }
     if (R.d.kind == GN_LAYER_MOE) {
       // parameters stay 0: Build rebinds the gating and expert layers to one
       // fresh zero block (moe.go:122-135)
-      const size_t Bm = max_batch, E = R.E, O = R.d.out_size;
-      float *tmp = nullptr;
-      if ((rc = model_alloc(M.get(), Bm * E, &R.mlog))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * E, &R.mprob))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * E, &R.mdzg))) return rc;
-      if ((rc = model_alloc(M.get(), E * Bm * O, &R.meout))) return rc;
-      if ((rc = model_alloc(M.get(), E * Bm * O, &R.medz))) return rc;
-      if ((rc = model_alloc(M.get(), Bm * R.K, &tmp))) return rc;
-      R.mact = reinterpret_cast<int32_t *>(tmp);
       R.mrng.assign(65, 42);  // NewRNG(42) in the layer and in every worker clone
     }
     if (R.d.kind == GN_LAYER_GRU_UNROLLER) {
       init_gru(host.data() + R.poff, R.I, R.H);
-      const size_t rows = (size_t)max_batch * R.T, H = R.H;
-      if ((rc = model_alloc(M.get(), 2 * H * H, &R.WhT))) return rc;
-      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.xw))) return rc;
-      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.gpre))) return rc;
-      if ((rc = model_alloc(M.get(), rows * H, &R.ghprev))) return rc;
-      if ((rc = model_alloc(M.get(), rows * H, &R.grh))) return rc;
-      if ((rc = model_alloc(M.get(), rows * 3 * H, &R.Dg))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * 3 * H, &R.S))) return rc;
+      if ((rc = model_alloc(M.get(), 2 * (size_t)R.H * R.H, &R.WhT))) return rc;
     }
     if (R.d.kind == GN_LAYER_BATCHNORM2D) {
       if (R.pcount) std::fill(host.begin() + R.poff, host.begin() + R.poff + R.C, 1.0f);
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.C * 3, &R.bnst))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.C * 2, &R.bnpart))) return rc;
       if ((rc = model_alloc(M.get(), R.C, &R.rmean))) return rc;
       if ((rc = model_alloc(M.get(), R.C, &R.rvar))) return rc;
       std::vector<float> ones(R.C, 1.0f);
@@ -1099,37 +1166,9 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
                                c->stream));
       HIP_OK(c, hipStreamSynchronize(c->stream));  // `ones` goes out of scope
     }
-    if (R.d.kind == GN_LAYER_SWIGLU) {
-      init_swiglu(host.data() + R.poff, R.d.in_size, R.d.out_size);
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * R.out_len, &R.zbuf))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * 2 * R.out_len, &R.dzbuf))) return rc;
-    }
-    if (R.d.kind == GN_LAYER_RMSNORM) {
+    if (R.d.kind == GN_LAYER_SWIGLU) init_swiglu(host.data() + R.poff, R.d.in_size, R.d.out_size);
+    if (R.d.kind == GN_LAYER_RMSNORM)
       std::fill(host.begin() + R.poff, host.begin() + R.poff + R.D, 1.0f);  // rmsnorm.go:80-82
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * (R.in_len / R.D), &R.rmsv))) return rc;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.in_len, &R.gx))) return rc;
-    }
-    if (R.d.kind == GN_LAYER_MAXPOOL2D) {
-      float *am = nullptr;
-      if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &am))) return rc;
-      R.argmax = reinterpret_cast<int32_t *>(am);
-    }
-    if (R.d.kind == GN_LAYER_FLATTEN) {
-      // reshape.go:64-96: identity both ways; share the neighbours' buffers
-      R.out_alias = true;
-      R.gout_alias = true;
-      R.gout = i > 0 ? M->L[i - 1].gout : nullptr;
-      continue;
-    }
-    if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.out))) return rc;
-    if (R.d.kind == GN_LAYER_POSENC && i > 0) {
-      // PositionalEncoding.Backward returns its input gradient unchanged
-      // (transformer.go:112-118): share the buffer with the layer below
-      R.gout = M->L[i - 1].gout;
-      R.gout_alias = true;
-    } else if ((rc = model_alloc(M.get(), (size_t)max_batch * R.out_len, &R.gout))) {
-      return rc;
-    }
     if (R.d.kind == GN_LAYER_DROPOUT) {
       // Q9: Dropout.Reset reseeds RNG(42) before every sample (dropout.go:399-401),
       // so one mask of the first `size` draws serves every sample and step.
@@ -1141,18 +1180,44 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), R.d.in_size, &R.mask))) return rc;
       HIP_OK(c, hipMemcpyAsync(R.mask, mk.data(), mk.size() * sizeof(float), hipMemcpyHostToDevice,
                                c->stream));
+      HIP_OK(c, hipStreamSynchronize(c->stream));  // `mk` goes out of scope
     }
   }
   HIP_OK(c, hipMemcpyAsync(M->params, host.data(), (size_t)off * sizeof(float),
                            hipMemcpyHostToDevice, c->stream));
-  if ((rc = model_alloc(M.get(), (size_t)max_batch, &M->loss_rows))) return rc;
   if ((rc = model_alloc(M.get(), 64, &M->loss_dev))) return rc;
-  if ((rc = model_alloc(M.get(), (size_t)max_batch * M->L[0].in_len, &M->xin))) return rc;
-  if ((rc = model_alloc(M.get(), (size_t)max_batch * M->L.back().out_len, &M->yin))) return rc;
   HIP_OK(c, hipMemsetAsync(M->loss_dev, 0, 64 * sizeof(float), c->stream));
+  if ((rc = alloc_batch(M.get()))) return rc;
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  (void)maxw;
   *out = M.release();
+  return GN_OK;
+}
+
+// Network.TrainBatch and PredictBatch take any batch size: a batch above the
+// size the buffers were made for rebuilds the batch-sized buffers (layer
+// outputs and gradients, saved state, staging) and keeps everything else —
+// parameters, gradients, Adam moments and timestep, BatchNorm2D running
+// statistics, MoE noise streams, training flags.
+extern "C" int gn_model_reserve(gn_model *M, int32_t max_batch) {
+  if (!M) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  if (max_batch <= 0) return set_err(c, GN_ERR_INVALID, "max_batch %d <= 0", max_batch);
+  if (max_batch <= M->maxB) return GN_OK;
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->aux));
+  const int old = M->maxB;
+  free_batch(M);
+  M->maxB = max_batch;
+  int rc = alloc_batch(M);
+  if (rc) {  // back to the old size; the caller's model stays usable
+    const std::string msg = c->err;
+    free_batch(M);
+    M->maxB = old;
+    if (alloc_batch(M)) return set_err(c, GN_ERR_OOM, "%s; restoring batch %d failed too", msg.c_str(), old);
+    return set_err(c, rc, "%s", msg.c_str());
+  }
+  HIP_OK(c, hipStreamSynchronize(c->stream));
   return GN_OK;
 }
 
@@ -1229,9 +1294,40 @@ extern "C" int gn_model_arena(gn_model *M, float **p, float **g, float **m, floa
   return GN_OK;
 }
 
+// Network.SetTraining (net.go:187-193): every layer of the network itself;
+// worker clones keep the flags they were made with.
 extern "C" int gn_model_set_training(gn_model *M, int32_t t) {
   if (!M) return GN_ERR_INVALID;
-  M->training = t ? 1 : 0;
+  for (LayerRT &R : M->L) R.train = t ? 1 : 0;
+  return GN_OK;
+}
+
+extern "C" int gn_model_get_training(gn_model *M, int32_t layer, int32_t *t) {
+  if (!M || !t || layer < 0 || layer >= (int)M->L.size()) return GN_ERR_INVALID;
+  *t = M->L[layer].train;
+  return GN_OK;
+}
+
+// Flags in effect for a pass over B samples: the network's own for inference
+// and for trainBatchSequential; for trainBatchParallel those of the worker
+// clones that run the chunks, clones being made (with the network's current
+// flags) the first time that many workers are needed (net.go:129-152).
+static int pass_flags(gn_model *M, int B, bool train) {
+  const int n = (int)M->L.size();
+  M->eff.assign(n, 0);
+  for (int i = 0; i < n; ++i) M->eff[i] = (char)M->L[i].train;
+  if (!train || M->workers <= 1) return GN_OK;
+  const int W = std::min(M->workers, B);
+  while ((int)M->clone_train.size() < W) M->clone_train.push_back(M->eff);
+  for (int i = 0; i < n; ++i) {
+    const char f = M->clone_train[0][i];
+    for (int w = 1; w < W; ++w)
+      if (M->clone_train[w][i] != f)
+        return set_err(M->ctx, GN_ERR_UNSUPPORTED,
+                       "layer %d: worker clones made at different times hold different training "
+                       "flags; chunks with mixed flags are not built", i);
+    M->eff[i] = f;
+  }
   return GN_OK;
 }
 
@@ -1458,9 +1554,9 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
   {
     KTimer kt(c, GN_KCLASS_OTHER);
-    // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch over
-    // 3 * max batch samples (rows of samples >= B are stale and their sums unread)
-    HIP_OK(c, launch_token_sum(t.GQ, t.S3, 3 * M->maxB, T, D, c->stream));
+    // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch,
+    // blockIdx.z picking the member, B samples each
+    HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, c->stream));
     const float *src[3] = {t.S3, t.S3 + sst, t.S3 + 2 * sst};
     float *dst[3] = {G + bo[0], G + bo[1], G + bo[2]};
     HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
@@ -1509,7 +1605,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         break;
       }
       case GN_LAYER_DROPOUT:
-        if (M->training)
+        if (M->eff[i])
           HIP_OK(c, launch_dropout(cur, R.mask, R.scale, R.out, B, R.out_len, c->stream));
         else
           HIP_OK(c, hipMemcpyAsync(R.out, cur, (size_t)B * R.out_len * sizeof(float),
@@ -1537,7 +1633,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       }
       case GN_LAYER_EMBEDDING: {
         KTimer kt(c, GN_KCLASS_OTHER);
-        HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B * R.T, R.V, R.D, R.err,
+        HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B, R.T, R.V, R.D, R.bad,
                                c->stream));
         break;
       }
@@ -1579,7 +1675,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         HIP_OK(c, gemm_nt(c, cur, P, P + (int64_t)E * I, R.mlog, B, E, I, EPI_BIAS_ACT, F_IDENTITY,
                           nullptr));
         MoeRoute rt{};
-        rt.B = B; rt.E = E; rt.K = K; rt.training = M->training;
+        rt.B = B; rt.E = E; rt.K = K; rt.training = M->eff[i];
         const int W = std::min(M->workers, B);
         if (M->workers > 1) rt.chunk = (B + W - 1) / W;  // trainBatchParallel chunks
         for (int k = 0; k < 65; ++k) rt.base[k] = R.mrng[k];
@@ -1594,7 +1690,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         }
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_moe_combine(R.meout, R.mprob, R.mact, R.out, B, O, E, K, c->stream));
-        if (M->training) {  // E draws per sample on its stream
+        if (M->eff[i]) {  // E draws per sample on its stream
           if (M->workers > 1) {
             for (int w = 0; w < W; ++w) {
               const int n = std::max(0, std::min(rt.chunk, B - w * rt.chunk));
@@ -1630,7 +1726,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_BATCHNORM2D: {  // running stats advance in training mode only
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_bn_fwd(cur, R.pcount ? M->params + R.poff : nullptr, R.out, R.bnst, R.rmean,
-                                R.rvar, B, R.C, R.HW, R.eps, R.d.momentum, M->training, c->stream));
+                                R.rvar, B, R.C, R.HW, R.eps, R.d.momentum, M->eff[i], c->stream));
         break;
       }
       case GN_LAYER_RMSNORM: {
@@ -1722,11 +1818,15 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_DROPOUT: {
-        // dropout.go:283-290; the training flag is on during TrainBatch
-        if (below && below->d.kind != GN_LAYER_FLATTEN)
+        // dropout.go:283-290 in training mode; out of it the gradient passes
+        // unchanged (dropout.go:241-247)
+        if (below && below->d.kind == GN_LAYER_FLATTEN)
+          return set_err(c, GN_ERR_UNSUPPORTED, "Flatten below Dropout");
+        if (below && M->eff[i])
           HIP_OK(c, launch_dropout(R.gout, R.mask, R.scale, below->gout, B, R.out_len, c->stream));
         else if (below)
-          return set_err(c, GN_ERR_UNSUPPORTED, "Flatten below Dropout");
+          HIP_OK(c, hipMemcpyAsync(below->gout, R.gout, (size_t)B * R.out_len * sizeof(float),
+                                   hipMemcpyDeviceToDevice, c->stream));
         is_dz = false;
         break;
       }
@@ -1803,7 +1903,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         {
           KTimer kt(c, GN_KCLASS_OTHER);
           HIP_OK(c, launch_moe_backward_deltas(R.gout, R.meout, R.mprob, R.mact, R.medz, R.mdzg, B, O, E,
-                                               K, M->training, c->stream));
+                                               K, M->eff[i], c->stream));
         }
         // gating and expert Dense backward: W grads = scale dz^T x, b grads = scale colsum(dz)
         HIP_OK(c, dense_bwd_core(c, in, P, R.mdzg, G, G + (int64_t)E * I, nullptr, B, I, E, scale,
@@ -1862,6 +1962,13 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_BATCHNORM2D: {  // batchnorm2d.go:611-660
         KTimer kt(c, GN_KCLASS_OTHER);
         const float *gb = R.pcount ? M->params + R.poff : nullptr;
+        if (!M->eff[i]) {  // inference-mode backward (batchnorm2d.go:525-551): no parameter gradient
+          if (R.pcount) HIP_OK(c, launch_fill(M->grads + R.poff, 0.0f, R.pcount, c->stream));
+          HIP_OK(c, launch_bn_bwd_eval(R.gout, gb, R.rvar, below ? below->gout : nullptr, B, R.C, R.HW,
+                                       R.eps, c->stream));
+          is_dz = false;
+          break;
+        }
         HIP_OK(c, launch_bn_bwd(R.gout, in, gb, R.bnst, below ? below->gout : nullptr,
                                 R.pcount ? R.bnpart : nullptr, B, R.C, R.HW, c->stream));
         if (R.pcount) {
@@ -1894,7 +2001,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_EMBEDDING: {  // Q12: last sample of each worker chunk only
         KTimer kt(c, GN_KCLASS_OTHER);
         HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
-                                    scale, c->stream));
+                                    scale, R.bad, c->stream));
         break;
       }
       case GN_LAYER_LSTM_UNROLLER: {
@@ -1972,12 +2079,16 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   gn_ctx *c = M->ctx;
   if (B <= 0 || B > M->maxB) return set_err(c, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
   if (!x || !y) return set_err(c, GN_ERR_INVALID, "null input");
-  int rc = model_forward(M, x, B, true);
+  int rc = pass_flags(M, B, true);
+  if (rc) return rc;
+  M->last_predict = false;
+  rc = model_forward(M, x, B, true);
   if (rc) return rc;
   LayerRT &O = M->L.back();
   int row_act = O.ap.row_act;
+  const int32_t *bad = M->L[0].d.kind == GN_LAYER_EMBEDDING ? M->L[0].bad : nullptr;
   HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
-                            O.ap.deriv, M->loss_kind, c->stream));
+                            O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
   HIP_OK(c, launch_loss_mean(M->loss_rows, B, M->workers, M->loss_dev, c->stream));
   // grads *= 1/B: float32 reciprocal (net.go:767-770), float32(1/float64(B))
   // for the W-worker path (net.go:703-706).
@@ -2030,23 +2141,66 @@ extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const flo
   return model_train_step(M, x, y, B);
 }
 
-// Device error flags, reported and cleared once the stream has drained:
-// out-of-range embedding ids (embedding.go:126-128 errors on them) and a
-// cooperative BPTT wait that timed out (its gradients are then invalid).
-static int check_embed_err(gn_model *M) {
+// Device flags, read once the stream has drained:
+//  - Embedding index errors (embedding.go:126-128): an inference pass fails
+//    (ForwardBatch returns the error, net.go:447-450); a training step skips
+//    the samples as the batch loop does and counts them (M->skipped);
+//  - a cooperative BPTT wait that timed out (its gradients are then invalid).
+static int check_flags(gn_model *M) {
   gn_ctx *c = M->ctx;
   if (M->L.empty()) return GN_OK;
   const LayerRT &R = M->L[0];
-  const bool emb = R.d.kind == GN_LAYER_EMBEDDING, lstm = R.d.kind == GN_LAYER_LSTM_UNROLLER;
-  if ((!emb && !lstm) || !R.err) return GN_OK;
-  int flag = 0;
-  HIP_OK(c, hipMemcpyAsync(&flag, R.err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
-  HIP_OK(c, hipStreamSynchronize(c->stream));
-  if (flag) {
-    HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
-    if (emb) return set_err(c, GN_ERR_INDEX, "embedding index out of bounds [0, %d)", R.V);
-    return set_err(c, GN_ERR_HIP, "LSTM cooperative BPTT: a workgroup wait timed out");
+  if (R.d.kind == GN_LAYER_LSTM_UNROLLER && R.err) {
+    int flag = 0;
+    HIP_OK(c, hipMemcpyAsync(&flag, R.err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    if (flag) {
+      HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
+      return set_err(c, GN_ERR_HIP, "LSTM cooperative BPTT: a workgroup wait timed out");
+    }
   }
+  if (R.d.kind == GN_LAYER_EMBEDDING && R.bad && M->last_B > 0) {
+    const int B = M->last_B;
+    std::vector<int32_t> f(B);
+    HIP_OK(c, hipMemcpyAsync(f.data(), R.bad, (size_t)B * sizeof(int32_t), hipMemcpyDeviceToHost,
+                             c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    int nbad = 0, nskip = 0;
+    for (int b = 0; b < B; ++b) nbad += f[b] ? 1 : 0;
+    if (M->last_predict) {
+      if (nbad)
+        return set_err(c, GN_ERR_INDEX, "embedding index out of bounds [0, %d) in %d of %d samples",
+                       R.V, nbad, B);
+      return GN_OK;
+    }
+    if (M->workers > 1) {  // a worker stops at its chunk's first bad sample
+      const int W = std::min(M->workers, B), chunk = (B + W - 1) / W;
+      for (int c0 = 0; c0 < B; c0 += chunk) {
+        const int c1 = std::min(B, c0 + chunk);
+        int b = c0;
+        while (b < c1 && !f[b]) ++b;
+        nskip += c1 - b;
+      }
+    } else {
+      nskip = nbad;
+    }
+    M->skipped = nskip;
+  }
+  return GN_OK;
+}
+
+// Samples the last training step skipped because an Embedding index was out
+// of range (the reference's batch loop drops them silently, net.go:738-741).
+extern "C" int gn_model_skipped_samples(gn_model *M, int32_t *n) {
+  if (!M || !n) return GN_ERR_INVALID;
+  gn_ctx *c = M->ctx;
+  ENTRY(c);
+  *n = 0;
+  if (M->last_predict) return GN_OK;
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  int rc = check_flags(M);
+  if (rc) return rc;
+  *n = M->skipped;
   return GN_OK;
 }
 
@@ -2071,7 +2225,7 @@ extern "C" int gn_model_train_step(gn_model *M, const float *x, const float *y, 
   if (rc) return rc;
   if (loss_out) return gn_model_read_loss(M, loss_out);
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  return check_embed_err(M);
+  return check_flags(M);
 }
 
 extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
@@ -2080,7 +2234,7 @@ extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
   ENTRY(c);
   HIP_OK(c, hipMemcpyAsync(loss, M->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  return check_embed_err(M);
+  return check_flags(M);
 }
 
 extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *out) {
@@ -2088,19 +2242,22 @@ extern "C" int gn_model_predict(gn_model *M, const float *x, int32_t B, float *o
   gn_ctx *c = M->ctx;
   ENTRY(c);
   if (B <= 0 || B > M->maxB || !x || !out) return set_err(c, GN_ERR_INVALID, "bad predict args");
-  const int saved = M->training;
-  M->training = 0;  // Sequential.Predict sets training=false (sequential.go:118-122)
+  // Sequential.Predict / PredictBatch set training=false and leave it so
+  // (sequential.go:118-122, 133-134): later training steps run that way too
+  for (LayerRT &R : M->L) R.train = 0;
+  int rc = pass_flags(M, B, false);
+  if (rc) return rc;
   HIP_OK(c, hipMemcpyAsync(M->xin, x, (size_t)B * M->L[0].in_len * sizeof(float),
                            hipMemcpyHostToDevice, c->stream));
-  int rc = model_forward(M, M->xin, B, false);
-  M->training = saved;
+  M->last_predict = true;
+  rc = model_forward(M, M->xin, B, false);
   if (rc) return rc;
   M->last_B = B;
   LayerRT &O = M->L.back();
   HIP_OK(c, hipMemcpyAsync(out, O.out, (size_t)B * O.out_len * sizeof(float),
                            hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  return check_embed_err(M);
+  return check_flags(M);
 }
 
 extern "C" int gn_model_predict_device(gn_model *M, const float *x, int32_t B, float *out) {
@@ -2108,10 +2265,11 @@ extern "C" int gn_model_predict_device(gn_model *M, const float *x, int32_t B, f
   gn_ctx *c = M->ctx;
   ENTRY(c);
   if (B <= 0 || B > M->maxB || !x || !out) return set_err(c, GN_ERR_INVALID, "bad predict args");
-  const int saved = M->training;
-  M->training = 0;
-  int rc = model_forward(M, x, B, false);
-  M->training = saved;
+  for (LayerRT &R : M->L) R.train = 0;  // ForwardBatch: SetTraining(false) (net.go:440)
+  int rc = pass_flags(M, B, false);
+  if (rc) return rc;
+  M->last_predict = true;
+  rc = model_forward(M, x, B, false);
   if (rc) return rc;
   M->last_B = B;
   LayerRT &O = M->L.back();
@@ -2167,10 +2325,13 @@ extern "C" int gn_model_layer_argmax(gn_model *M, int32_t layer, int32_t *dst, i
   gn_ctx *c = M->ctx;
   ENTRY(c);
   LayerRT &R = M->L[layer];
-  if (!R.argmax) return set_err(c, GN_ERR_UNSUPPORTED, "layer %d has no argmax switches", layer);
-  const int64_t have = (int64_t)M->last_B * R.out_len;
+  // MaxPool2D: the argmax switch of every output; MoE: the k experts each
+  // sample was routed to, in routing order
+  const int32_t *src = R.d.kind == GN_LAYER_MOE ? R.mact : R.argmax;
+  if (!src) return set_err(c, GN_ERR_UNSUPPORTED, "layer %d has no argmax switches or routes", layer);
+  const int64_t have = (int64_t)M->last_B * (R.d.kind == GN_LAYER_MOE ? R.K : R.out_len);
   if (n > have) return set_err(c, GN_ERR_INVALID, "asked %lld > %lld", (long long)n, (long long)have);
-  HIP_OK(c, hipMemcpyAsync(dst, R.argmax, n * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipMemcpyAsync(dst, src, n * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
   return GN_OK;
 }

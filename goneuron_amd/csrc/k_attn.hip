@@ -38,24 +38,33 @@ __device__ __forceinline__ float wmax(float v) {
 // ---------------------------------------------------------------------------
 // Embedding / PositionalEncoding / CLS
 // ---------------------------------------------------------------------------
-// out[r, :] = E[floor(x[r]), :] + (pe ? pe[r % T, :] : 0); ids[r] = index.
-// Out-of-range ids (an error in the reference, embedding.go:126-128) raise
-// *err and read row 0.
+// out[b, t, :] = E[floor(x[b, t]), :], ids[b, t] = that index; block row
+// blockIdx.y is sample b.  An index outside [0, V) makes Embedding.Forward
+// return an error (embedding.go:126-128), and the batch loop then skips the
+// sample (net.go:738-741, 641-644): every block of the sample checks its T ids
+// and block 0 records bad[b]; such a sample's rows read E[0] and are masked
+// out downstream.
 __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ x,
                                                     const float *__restrict__ E,
                                                     int32_t *__restrict__ ids,
-                                                    float *__restrict__ out, int rows, int V,
-                                                    int D, int *__restrict__ err) {
-  const int64_t n = (int64_t)rows * D;
+                                                    float *__restrict__ out, int T, int V, int D,
+                                                    int32_t *__restrict__ bad) {
+  const int b = blockIdx.y;
+  const float *xs = x + (int64_t)b * T;
+  int any = 0;
+  for (int t = threadIdx.x; t < T; t += 256) {
+    const int idx = (int)floor((double)xs[t]);
+    any |= (idx < 0 || idx >= V) ? 1 : 0;
+  }
+  any = __syncthreads_or(any);
+  if (bad && blockIdx.x == 0 && threadIdx.x == 0) bad[b] = any ? 1 : 0;
+  const int64_t n = (int64_t)T * D;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
-    const int r = (int)(e / D), d = (int)(e % D);
-    int idx = (int)floor((double)x[r]);
-    if (idx < 0 || idx >= V) {
-      if (d == 0) atomicOr(err, 1);
-      idx = 0;
-    }
-    if (d == 0) ids[r] = idx;
-    out[e] = E[(int64_t)idx * D + d];
+    const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
+    int idx = (int)floor((double)xs[t]);
+    if (idx < 0 || idx >= V) idx = 0;
+    if (d == 0) ids[(int64_t)b * T + t] = idx;
+    out[(int64_t)b * n + e] = E[(int64_t)idx * D + d];
   }
 }
 
@@ -66,29 +75,51 @@ __global__ __launch_bounds__(256) void pe_add_kernel(const float *__restrict__ x
     out[e] = x[e] + pe[e % TD];
 }
 
-// grad[E] = 0 (hipMemsetAsync before the launch), then the token rows of each
-// worker chunk's last sample are scatter-added in (chunk, token) order.  Block
-// l takes contributing row l: if l is the first row carrying its id it sums,
-// in order, every row with that id and writes the row of gradE; rows whose id
-// appeared earlier write nothing, so all writes are to distinct rows.
+// grad[E] = 0 (a fill before the launch), then the token rows of each worker
+// chunk's contributing sample are scatter-added in (chunk, token) order.
+// Embedding.Backward zeroes the gradient first (embedding.go:152-154), so the
+// contributing sample is the last one whose backward ran: the chunk's last
+// sample, or with skipped samples (bad[b]) the last valid one (sequential
+// loop, net.go:738-741) or the one before the chunk's first bad sample (a
+// worker returns at its first error, net.go:641-644); none if there is none.
+// Block l takes contributing row l: if l is the first row carrying its id it
+// sums, in order, every row with that id and writes the row of gradE; rows
+// whose id appeared earlier write nothing, so all writes are to distinct rows.
 constexpr int EG_MAXL = 2048;  // contributing rows held in LDS
-
-__device__ __forceinline__ int eg_sample(int l, int T, int chunk, int B) {
-  return min((l / T + 1) * chunk - 1, B - 1);
-}
 
 __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict__ g,
                                                          const int32_t *__restrict__ ids,
                                                          float *__restrict__ gradE, int B, int T,
-                                                         int D, int chunk, int L, float scale) {
+                                                         int D, int chunk, int L, float scale,
+                                                         const int32_t *__restrict__ bad, int par) {
   __shared__ int sid[EG_MAXL];
+  __shared__ int csamp[EG_MAXL];
   __shared__ int first;
-  const int l = blockIdx.x;
-  for (int e = threadIdx.x; e < L; e += 256)
-    sid[e] = ids[(int64_t)eg_sample(e, T, chunk, B) * T + e % T];
+  const int l = blockIdx.x, nch = L / T;
+  for (int w = threadIdx.x; w < nch; w += 256) {
+    const int c0 = w * chunk, c1 = min(B, c0 + chunk);
+    int sm = c1 - 1;
+    if (bad) {
+      if (par) {
+        int f = c0;
+        while (f < c1 && !bad[f]) ++f;
+        sm = f - 1;
+      } else {
+        while (sm >= c0 && bad[sm]) --sm;
+      }
+      if (sm < c0) sm = -1;
+    }
+    csamp[w] = sm;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < L; e += 256) {
+    const int sm = csamp[e / T];
+    sid[e] = sm < 0 ? -1 : ids[(int64_t)sm * T + e % T];
+  }
   if (threadIdx.x == 0) first = 1;
   __syncthreads();
   const int my = sid[l];
+  if (my < 0) return;  // uniform over the block
   for (int e = threadIdx.x; e < l; e += 256)
     if (sid[e] == my) first = 0;  // benign race: every writer stores 0
   __syncthreads();
@@ -96,7 +127,7 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
   for (int d = threadIdx.x; d < D; d += 256) {
     float acc = 0.f;
     for (int e = l; e < L; ++e)
-      if (sid[e] == my) acc += g[((int64_t)eg_sample(e, T, chunk, B) * T + e % T) * D + d];
+      if (sid[e] == my) acc += g[((int64_t)csamp[e / T] * T + e % T) * D + d];
     gradE[(int64_t)my * D + d] = acc * scale;
   }
 }
@@ -121,12 +152,16 @@ __global__ __launch_bounds__(256) void cls_bwd_kernel(const float *__restrict__ 
 
 // S[b, :] = sum_t X[b, t, :]   (per-sample token sums for the Q10 dW outer products)
 // Block = 64 columns x 16 token groups of sample blockIdx.y; partials added in LDS.
+// blockIdx.z selects a member of a batched launch (X, S advanced by xs, ss).
 __global__ __launch_bounds__(1024) void token_sum_kernel(const float *__restrict__ X,
-                                                         float *__restrict__ S, int B, int T, int N) {
+                                                         float *__restrict__ S, int B, int T, int N,
+                                                         int64_t xs, int64_t ss) {
   __shared__ float red[16][64];
   const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   const int64_t b = blockIdx.y;
+  X += blockIdx.z * xs;
+  S += blockIdx.z * ss;
   float s = 0.f;
   if (c < N) {
     const float *p = X + b * T * N + c;
@@ -515,10 +550,12 @@ static unsigned blocks_for(int64_t n) {
   return (unsigned)(b < 1 ? 1 : b);
 }
 
-hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int rows, int V,
-                        int D, int *err, hipStream_t s) {
-  hipLaunchKernelGGL(embed_kernel, dim3(blocks_for((int64_t)rows * D)), dim3(256), 0, s, x, E, ids,
-                     out, rows, V, D, err);
+hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int B, int T, int V,
+                        int D, int32_t *bad, hipStream_t s) {
+  if (B <= 0) return hipSuccess;
+  const int64_t n = (int64_t)T * D;
+  unsigned bx = (unsigned)std::min<int64_t>((n + 255) / 256, 64);
+  hipLaunchKernelGGL(embed_kernel, dim3(bx, B), dim3(256), 0, s, x, E, ids, out, T, V, D, bad);
   return hipGetLastError();
 }
 
@@ -529,16 +566,16 @@ hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int
 }
 
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
-                             int D, int W, float scale, hipStream_t s) {
+                             int D, int W, float scale, const int32_t *bad, hipStream_t s) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   const int chunk = (B + Wc - 1) / Wc;
   const int nsamp = (B + chunk - 1) / chunk;  // one contributing sample per chunk
   const int L = nsamp * T;
   if (L > EG_MAXL) return hipErrorInvalidValue;
-  hipError_t e = hipMemsetAsync(gradE, 0, (size_t)V * D * sizeof(float), s);
+  hipError_t e = launch_fill(gradE, 0.0f, (int64_t)V * D, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(embed_grad_kernel, dim3(L), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
-                     scale);
+                     scale, bad, W > 1 ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -555,7 +592,14 @@ hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipS
 }
 
 hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s) {
-  hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B), dim3(1024), 0, s, X, S, B, T, N);
+  return launch_token_sum_multi(X, S, B, T, N, 1, 0, 0, s);
+}
+
+hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N, int nmem,
+                                  int64_t xstride, int64_t sstride, hipStream_t s) {
+  if (B <= 0 || nmem <= 0) return hipSuccess;
+  hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B, nmem), dim3(1024), 0, s, X, S, B, T, N,
+                     xstride, sstride);
   return hipGetLastError();
 }
 

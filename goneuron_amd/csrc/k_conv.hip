@@ -614,6 +614,33 @@ hipError_t launch_bn_fwd(const float *x, const float *gb, float *y, float *st, f
   return hipGetLastError();
 }
 
+// inference-mode backward (batchnorm2d.go:525-551): dx = (g * gamma) / std of
+// the running variance; the parameters get no gradient
+__global__ __launch_bounds__(256) void bn_bwd_eval_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ gb,
+                                                          const float *__restrict__ rv,
+                                                          float *__restrict__ dx, int64_t total,
+                                                          int C, int HW, float eps) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * 256) {
+    const int f = (int)((e / HW) % C);
+    const float std = (float)sqrt((double)(rv[f] + eps));
+    const float gg = gb ? g[e] * gb[f] : g[e];
+    dx[e] = gg / std;
+  }
+}
+
+hipError_t launch_bn_bwd_eval(const float *g, const float *gb, const float *rv, float *dx, int B,
+                              int C, int HW, float eps, hipStream_t s) {
+  const int64_t total = (int64_t)B * C * HW;
+  if (total <= 0 || !dx) return hipSuccess;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(bn_bwd_eval_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, gb, rv, dx,
+                     total, C, HW, eps);
+  return hipGetLastError();
+}
+
 hipError_t launch_bn_bwd(const float *g, const float *x, const float *gb, const float *st, float *dx,
                          float *part, int B, int C, int HW, hipStream_t s) {
   const int planes = B * C;

@@ -331,14 +331,34 @@ static int row_threads(int C) { return C >= 4096 ? 1024 : TPB; }
 //   Softmax    dz_k = sum_i g_i p_i (d_ik - p_k) = p_k g_k - p_k sum_i g_i p_i  (layer.go:504-529)
 //   LogSoftmax dz_k = sum_i g_i (d_ik - exp(o_k)) = g_k - exp(o_k) sum_i g_i     (layer.go:530-560)
 //   otherwise  dz_k = g_k * Derivative                                          (layer.go:561-567)
+//
+// Samples the batch loop skips (bad[b], an Embedding index error) add no loss
+// and their dz row is 0, so no layer's gradient sees them: with workers == 1
+// only the bad sample itself (net.go:738-741); with workers > 1 the worker
+// returns at its chunk's first bad sample, so the rest of the chunk is
+// skipped too and the chunk's loss is never stored (net.go:641-644, 653-655).
 __global__ __launch_bounds__(1024) void out_rows_kernel(float *__restrict__ zo,
                                                        const float *__restrict__ y,
                                                        float *__restrict__ dz,
                                                        float *__restrict__ loss_rows, int C,
                                                        int row_act, int fwd, int deriv,
-                                                       int loss_kind) {
+                                                       int loss_kind,
+                                                       const int32_t *__restrict__ bad, int chunk) {
   __shared__ float sh[16];
   const int b = blockIdx.x, t = threadIdx.x, nt = blockDim.x;
+  bool valid = true, keep_loss = true;
+  if (bad) {
+    if (chunk > 0) {
+      const int c0 = (b / chunk) * chunk, c1 = min((int)gridDim.x, c0 + chunk);
+      for (int i = c0; i < c1; ++i)
+        if (bad[i]) {
+          keep_loss = false;
+          if (i <= b) valid = false;
+        }
+    } else {
+      valid = keep_loss = !bad[b];
+    }
+  }
   float *o = zo + (size_t)b * C;
   const float *yr = y + (size_t)b * C;
   float *d = dz + (size_t)b * C;
@@ -365,7 +385,7 @@ __global__ __launch_bounds__(1024) void out_rows_kernel(float *__restrict__ zo,
     }
     l = block_sum(l, sh);
   }
-  if (t == 0) loss_rows[b] = l;
+  if (t == 0) loss_rows[b] = keep_loss ? l : 0.0f;
   // Jacobian / derivative
   if (row_act == ROW_SOFTMAX) {
     float s1 = 0.f;
@@ -380,16 +400,38 @@ __global__ __launch_bounds__(1024) void out_rows_kernel(float *__restrict__ zo,
   } else {
     for (int i = t; i < C; i += nt) d[i] = d[i] * deriv_of(o[i], deriv);
   }
+  if (!valid) {
+    __syncthreads();
+    for (int i = t; i < C; i += nt) d[i] = 0.0f;
+  }
 }
 
 hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz, float *loss_rows,
-                           int B, int C, int row_act, int deriv, int loss_kind, hipStream_t s) {
+                           int B, int C, int row_act, int deriv, int loss_kind, const int32_t *bad,
+                           int workers, hipStream_t s) {
   (void)z;  // activation is computed in place on `out` (which holds z)
   if (B <= 0) return hipSuccess;
   // fwd kind for ROW_ELEMWISE rides in the high bits of row_act
   const int fwd = row_act >> 8;
+  const int W = workers < 1 ? 1 : (workers > B ? B : workers);
+  const int chunk = workers > 1 ? (B + W - 1) / W : 0;
   hipLaunchKernelGGL(out_rows_kernel, dim3(B), dim3(row_threads(C)), 0, s, out, y, dz, loss_rows, C,
-                     row_act & 0xff, fwd, deriv, loss_kind);
+                     row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  return hipGetLastError();
+}
+
+// dst[0, n) = v (a kernel, not a memset node: usable inside a captured graph)
+__global__ __launch_bounds__(TPB) void fill_kernel(float *__restrict__ dst, float v, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = v;
+}
+
+hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + TPB - 1) / TPB;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, dst, v, n);
   return hipGetLastError();
 }
 

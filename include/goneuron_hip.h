@@ -183,9 +183,30 @@ int gn_model_predict(gn_model *m, const float *x, int32_t B, float *out);
 /* The same with HBM-resident x (B x in_size) and output (B x out_size); no
  * host synchronisation (the device-side ForwardBatch of sequential.go:145-160). */
 int gn_model_predict_device(gn_model *m, const float *x_dev, int32_t B, float *out_dev);
+/* Network.SetTraining (net.go:187-193): sets the flag of every layer.  Layers
+ * start as the reference constructs them (Dropout and BatchNorm2D in training
+ * mode, MoE not: dropout.go:56, batchnorm2d.go:88, moe.go:46-90); Predict
+ * turns the flags off and leaves them off (sequential.go:118-134).  With
+ * workers > 1 a training step uses the flags of trainBatchParallel's worker
+ * clones, which copy the network's flags when first needed and keep them
+ * (net.go:129-152). */
 int gn_model_set_training(gn_model *m, int32_t training);
+int gn_model_get_training(gn_model *m, int32_t layer, int32_t *training);
+/* Network.TrainBatch / PredictBatch accept any batch size (net.go:412-436):
+ * grows the batch-sized buffers to max_batch samples, keeping parameters,
+ * gradients, Adam state, running statistics, noise streams and flags.  A
+ * smaller value is a no-op.  On failure the model keeps its old size. */
+int gn_model_reserve(gn_model *m, int32_t max_batch);
+/* Samples the last training step skipped because an Embedding index was out
+ * of range: the reference's batch loop drops such a sample (net.go:738-741;
+ * a trainBatchParallel worker drops the rest of its chunk and the chunk's
+ * loss, net.go:641-655) and the step still applies.  Inference passes report
+ * the same condition as GN_ERR_INDEX (ForwardBatch returns the error,
+ * net.go:447-450). */
+int gn_model_skipped_samples(gn_model *m, int32_t *count);
 /* Layer probes for parity tests: saved output of `layer` for the last batch
- * (B x out_len), MaxPool2D argmax switches (B x out_len, int32). */
+ * (B x out_len); int32 indices of the last batch: MaxPool2D argmax switches
+ * (B x out_len) or the MoE routes (B x k expert ids, routing order). */
 int gn_model_layer_output(gn_model *m, int32_t layer, float *dst, int64_t n);
 int gn_model_layer_argmax(gn_model *m, int32_t layer, int32_t *dst, int64_t n);
 /* BatchNorm2D running statistics (C floats each) of `layer`:
@@ -255,10 +276,6 @@ int gn_adam_step(gn_ctx *ctx, float *params, const float *grads, float *m, float
 #define GN_KCLASS_OTHER 2  /* row kernels, column sums, dropout, ... */
 int gn_timing_enable(gn_ctx *ctx, int enable);
 int gn_timing_report(gn_ctx *ctx, int kclass, int64_t *launches, double *total_ms);
-/* Matrix-core probe (measurement hook; no reference counterpart): `blocks`
- * workgroups of 4 wave64s issue `iters` x 4 back-to-back
- * v_mfma_f32_32x32x2_f32 each; returns the kernel time and its FLOP rate. */
-int gn_probe_mfma(gn_ctx *ctx, int32_t blocks, int32_t iters, double *ms, double *tflops);
 
 /* ---- synthetic inputs (host side; harness utility) ----------------------
  * The reference's LCG (layer.go:61-81): U[0,1) stream, N(0,1) by one

@@ -220,6 +220,7 @@ struct layer {
   float *grads;  /* view into the active grads buffer */
   int32_t in_len, out_len; /* per-sample sizes once known */
   int32_t training;
+  int32_t fwd_err; /* the last Forward returned an error (Embedding index out of range) */
   /* Dense */
   int32_t act_type;
   float *inputBuf, *preActBuf, *outputBuf, *savedOutput, *gradInBuf, *dzBuf;
@@ -248,6 +249,7 @@ struct layer {
   /* MoE: sub[0] gating, sub[1 + e] experts; one noise stream per worker clone */
   float *moeLogits, *moeProbs, *moeW, *moeOut, *moeGate;
   int32_t *moeActive;
+  int32_t *routeLog, routeLogN, routeLogCap; /* routes of every forward since the last reset */
   uint64_t moeRng[64];
   int32_t *curWorker; /* the net's active worker index */
   float *aq, *ak, *av, *scores, *fin, *gfin, *gq, *gk, *gv, *attOut, *res1, *n1, *ffOut, *res2,
@@ -265,6 +267,11 @@ struct gno_net {
   float lr;
   int32_t timestep;
   int32_t cur_worker; /* worker chunk being run (MoE noise streams) */
+  /* trainBatchParallel worker clones (net.go:129-152): LightweightClone copies
+   * each layer's training flag when the clone is made, and Network.SetTraining
+   * never reaches the pool, so a clone keeps its flags */
+  int32_t nclones;
+  int32_t *clone_training; /* nclones x nlayers */
   float *lossGrad;
   int32_t max_width;
 };
@@ -983,6 +990,22 @@ static const float *bn_forward(layer *L, const float *x, int32_t total) {
 }
 static const float *bn_backward(layer *L, const float *grad) {
   int32_t C = L->inC, N = L->bnN, HW = L->bnHW;
+  if (!L->training) {
+    /* batchnorm2d.go:525-551: g * gamma / std of the running variance; the
+     * parameters get no gradient */
+    const float eps = bn_eps(L);
+    for (int32_t i = 0; i < N; i++)
+      for (int32_t f = 0; f < C; f++) {
+        float std = (float)sqrt((double)(L->runVar[f] + eps));
+        for (int32_t s2 = 0; s2 < HW; s2++) {
+          int64_t k = ((int64_t)i * C + f) * HW + s2;
+          float g = grad[k];
+          if (L->nparams) g *= L->params[f];
+          L->gradInBuf[k] = g / std;
+        }
+      }
+    return L->gradInBuf;
+  }
   const float *x = L->savedInput;
   float m = (float)(N * HW);
   for (int32_t f = 0; f < C; f++) {
@@ -1108,6 +1131,7 @@ static const float *moe_forward(layer *L, const float *x) {
   for (int32_t r = 0; r < K; r++) {
     int32_t idx = order[r];
     L->moeActive[r] = idx;
+    if (L->routeLog && L->routeLogN < L->routeLogCap) L->routeLog[L->routeLogN++] = idx;
     float wt = L->moeProbs[idx];
     L->moeW[r] = wt;
     const float *eo = dense_forward(&L->sub[1 + idx], x);
@@ -1618,10 +1642,14 @@ static void emb_init(layer *L) {
   for (int64_t i = 0; i < L->nparams; i++) L->params[i] = scale * (2 * gno_rand_float(&rng) - 1);
 }
 static const float *emb_forward(layer *L, const float *x) {
+  L->fwd_err = 0;
   for (int32_t b = 0; b < L->T; b++) {
     int32_t idx = (int32_t)floor((double)x[b]);
     L->ids[b] = (int32_t)x[b];
-    if (idx < 0 || idx >= L->V) idx = 0; /* the reference errors out (sample skipped) */
+    if (idx < 0 || idx >= L->V) { /* Forward returns an error: the batch loop skips the sample */
+      L->fwd_err = 1;
+      return L->outputBuf;
+    }
     memcpy(L->outputBuf + (int64_t)b * L->D, L->params + (int64_t)idx * L->D, sizeof(float) * L->D);
   }
   return L->outputBuf;
@@ -2091,8 +2119,10 @@ gno_net *gno_net_create(const gno_layer_spec *specs, int32_t nlayers, int32_t lo
     layer *L = &n->layers[i];
     L->spec = specs[i];
     L->kind = specs[i].kind;
-    L->training = 1;
     layer_build(L);
+    /* as constructed: Dropout and BatchNorm2D in training mode (dropout.go:56,
+     * batchnorm2d.go:88), MoE not (NewMoE leaves the flag false) */
+    L->training = L->kind == GNO_LAYER_MOE ? 0 : 1;
     total += L->nparams;
   }
   n->nparams = total;
@@ -2140,6 +2170,7 @@ void gno_net_destroy(gno_net *n) {
       free(L->sub);
       free(L->moeLogits); free(L->moeProbs); free(L->moeW); free(L->moeOut); free(L->moeGate);
       free(L->moeActive);
+      free(L->routeLog);
     }
     if (L->kind == GNO_LAYER_RMSNORM) free(L->tmpRow);
     if (L->kind == GNO_LAYER_BATCHNORM2D) {
@@ -2148,6 +2179,7 @@ void gno_net_destroy(gno_net *n) {
   }
   free(n->layers);
   free(n->params); free(n->grads); free(n->m); free(n->v); free(n->worker_grads); free(n->lossGrad);
+  free(n->clone_training);
   free(n);
 }
 
@@ -2193,7 +2225,10 @@ static void bind_grads(gno_net *n, float *buf) {
 static const float *net_forward(gno_net *n, const float *x, int32_t in_len, int32_t *out_len) {
   const float *cur = x;
   int32_t len = in_len;
-  for (int32_t i = 0; i < n->nlayers; i++) cur = layer_forward(&n->layers[i], cur, &len);
+  for (int32_t i = 0; i < n->nlayers; i++) {
+    cur = layer_forward(&n->layers[i], cur, &len);
+    if (n->layers[i].fwd_err) return NULL; /* Network.Forward returns the error */
+  }
   *out_len = len;
   return cur;
 }
@@ -2206,6 +2241,7 @@ int32_t gno_net_forward(gno_net *n, const float *x, float *out) {
   for (int32_t i = 0; i < n->nlayers; i++) layer_reset(&n->layers[i]);
   int32_t ol;
   const float *o = net_forward(n, x, in_len_of(n), &ol);
+  if (!o) return -1;
   memcpy(out, o, sizeof(float) * ol);
   return ol;
 }
@@ -2215,16 +2251,18 @@ int32_t gno_net_out_size(const gno_net *n) {
   return L->out_len;
 }
 
-/* One sample: Reset all, Forward, loss.Forward, BackwardInPlace, Backward. */
-static float run_sample(gno_net *n, const float *x, const float *y, int32_t out_dim) {
+/* One sample: Reset all, Forward, loss.Forward, BackwardInPlace, Backward.
+ * Returns 0, or -1 when Forward failed (no loss, no backward). */
+static int run_sample(gno_net *n, const float *x, const float *y, int32_t out_dim, float *loss) {
   for (int32_t i = 0; i < n->nlayers; i++) layer_reset(&n->layers[i]);
   int32_t ol;
   const float *pred = net_forward(n, x, in_len_of(n), &ol);
   (void)out_dim;
-  float l = gno_loss_forward(n->loss_kind, pred, y, ol);
+  if (!pred) return -1;
+  *loss = gno_loss_forward(n->loss_kind, pred, y, ol);
   gno_loss_backward(n->loss_kind, pred, y, n->lossGrad, ol);
   net_backward(n, n->lossGrad);
-  return l;
+  return 0;
 }
 
 static int32_t target_dim(gno_net *n) {
@@ -2242,8 +2280,11 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
     float bs = (float)B, total = 0.0f;
     bind_grads(n, n->grads);
     n->cur_worker = 0; /* the network's own layers */
-    for (int32_t i = 0; i < B; i++)
-      total += run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od);
+    for (int32_t i = 0; i < B; i++) {
+      float l;
+      if (run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od, &l)) continue; /* net.go:738-741 */
+      total += l;
+    }
     float inv = 1.0f / bs;
     for (int64_t i = 0; i < n->nparams; i++) n->grads[i] *= inv;
     return total / bs;
@@ -2253,6 +2294,15 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
   if (B < W) W = B;
   int32_t chunk = (B + W - 1) / W;
   float wl[4096];
+  /* clones made now copy the network's current flags; older ones keep theirs */
+  if (n->nclones < W) {
+    n->clone_training = (int32_t *)realloc(n->clone_training, sizeof(int32_t) * W * n->nlayers);
+    for (int32_t w = n->nclones; w < W; w++)
+      for (int32_t i = 0; i < n->nlayers; i++) n->clone_training[w * n->nlayers + i] = n->layers[i].training;
+    n->nclones = W;
+  }
+  int32_t *master = (int32_t *)malloc(sizeof(int32_t) * n->nlayers);
+  for (int32_t i = 0; i < n->nlayers; i++) master[i] = n->layers[i].training;
   for (int32_t w = 0; w < W; w++) {
     float *wg = n->worker_grads + (int64_t)w * n->nparams;
     for (int64_t i = 0; i < n->nparams; i++) wg[i] = 0;
@@ -2262,10 +2312,20 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
     if (s >= e) continue;
     bind_grads(n, wg);
     n->cur_worker = 1 + w; /* worker clone w (its layers keep their own state) */
+    for (int32_t i = 0; i < n->nlayers; i++) n->layers[i].training = n->clone_training[w * n->nlayers + i];
     float local = 0.0f;
-    for (int32_t i = s; i < e; i++) local += run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od);
-    wl[w] = local;
+    int failed = 0;
+    for (int32_t i = s; i < e; i++) {
+      float l;
+      /* a worker returns at its first error: the rest of its chunk is skipped
+       * and its loss is never stored (net.go:641-644, 653-655) */
+      if (run_sample(n, x + (int64_t)i * in, y + (int64_t)i * od, od, &l)) { failed = 1; break; }
+      local += l;
+    }
+    wl[w] = failed ? 0.0f : local;
   }
+  for (int32_t i = 0; i < n->nlayers; i++) n->layers[i].training = master[i];
+  free(master);
   bind_grads(n, n->grads);
   for (int32_t w = 0; w < W; w++) {
     float *wg = n->worker_grads + (int64_t)w * n->nparams;
@@ -2289,6 +2349,23 @@ float gno_net_train_batch(gno_net *n, const float *x, const float *y, int32_t B)
   float l = gno_net_accumulate_batch(n, x, y, B);
   gno_net_step(n);
   return l;
+}
+
+/* MoE routes (k expert ids per forward, routing order) logged since the last
+ * call, which clears the log; returns the count. */
+int32_t gno_net_layer_routes(gno_net *n, int32_t li, int32_t *dst, int32_t cap) {
+  layer *L = &n->layers[li];
+  if (L->kind != GNO_LAYER_MOE) return 0;
+  if (!L->routeLog) {
+    L->routeLogCap = 1 << 20;
+    L->routeLog = (int32_t *)calloc((size_t)L->routeLogCap, sizeof(int32_t));
+    L->routeLogN = 0;
+    return 0;
+  }
+  int32_t c = L->routeLogN < cap ? L->routeLogN : cap;
+  memcpy(dst, L->routeLog, sizeof(int32_t) * c);
+  L->routeLogN = 0;
+  return c;
 }
 
 int32_t gno_net_layer_argmax(gno_net *n, int32_t li, int32_t *dst, int32_t cap) {

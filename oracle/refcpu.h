@@ -135,6 +135,9 @@ int32_t gno_net_out_size(const gno_net *n);
 /* Per-layer probes for unit tests: argmax of a MaxPool2D layer after the last
  * forward (count returned), last saved pre-activation of layer `layer`. */
 int32_t gno_net_layer_argmax(gno_net *n, int32_t layer, int32_t *dst, int32_t cap);
+/* MoE routes logged since the previous call (the first call starts the log
+ * and returns 0): k expert ids per forward in routing order. */
+int32_t gno_net_layer_routes(gno_net *n, int32_t layer, int32_t *dst, int32_t cap);
 int32_t gno_net_layer_preact(gno_net *n, int32_t layer, float *dst, int32_t cap);
 
 /* Stand-alone kernels of the reference (for golden-vector checks). */

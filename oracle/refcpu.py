@@ -89,6 +89,8 @@ def lib():
         L.gno_net_out_size.restype = C.c_int32
         L.gno_net_layer_argmax.argtypes = [C.c_void_p, C.c_int32, i32p, C.c_int32]
         L.gno_net_layer_argmax.restype = C.c_int32
+        L.gno_net_layer_routes.argtypes = [C.c_void_p, C.c_int32, i32p, C.c_int32]
+        L.gno_net_layer_routes.restype = C.c_int32
         L.gno_net_layer_preact.argtypes = [C.c_void_p, C.c_int32, f32p, C.c_int32]
         L.gno_net_layer_preact.restype = C.c_int32
         L.gno_activate_batch.argtypes = [C.c_int32, f32p, C.c_int32]
@@ -216,6 +218,8 @@ class Net:
         x = np.ascontiguousarray(x, np.float32)
         out = np.empty(out_cap, np.float32)
         n = lib().gno_net_forward(self.h, fptr(x), fptr(out))
+        if n < 0:
+            raise ValueError("Forward failed (embedding index out of range)")
         return out[:n].copy()
 
     def set_training(self, t):
@@ -224,6 +228,12 @@ class Net:
     def argmax(self, layer, cap=1 << 20):
         a = np.empty(cap, np.int32)
         n = lib().gno_net_layer_argmax(self.h, layer, iptr(a), cap)
+        return a[:n].copy()
+
+    def routes(self, layer, cap=1 << 20):
+        """MoE routes logged since the previous call (the first call starts the log)."""
+        a = np.empty(cap, np.int32)
+        n = lib().gno_net_layer_routes(self.h, layer, iptr(a), cap)
         return a[:n].copy()
 
     def running_stats(self, layer, cap=1 << 16):

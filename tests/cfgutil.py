@@ -82,3 +82,96 @@ def norm_rel(a, r):
     r = np.asarray(r, np.float64)
     den = np.linalg.norm(r)
     return float(np.linalg.norm(a - r) / den) if den else float(np.linalg.norm(a))
+
+
+def tensor_parts(cfg, net):
+    """(name, slice) of every parameter tensor of the flat arena, layer by
+    layer in the reference's Params() order, so tolerances apply per tensor
+    (gate blocks of recurrent weights, each block weight and bias, each
+    expert) rather than per layer."""
+    parts = []
+    for i, d in enumerate(cfg["layers"]):
+        sl = net.layer_slice(i)
+        o = sl.start
+
+        def add(name, n):
+            nonlocal o
+            parts.append((f"{i}:{d['kind']}.{name}", slice(o, o + n)))
+            o += n
+        k = d["kind"]
+        if k == "dense":
+            add("W", d["in"] * d["out"])
+            add("b", d["out"])
+        elif k == "conv2d":
+            add("W", d["outC"] * d["inC"] * d["k"] * d["k"])
+            add("b", d["outC"])
+        elif k == "lstm":
+            I, H = d["in"], d["hidden"]
+            for g in "ifgo":
+                add("Wx_" + g, H * I)
+            for g in "ifgo":
+                add("Wh_" + g, H * H)
+            for g in "ifgo":
+                add("b_" + g, H)
+        elif k == "gru":
+            I, H = d["in"], d["hidden"]
+            for g in "urc":
+                add("Wx_" + g, H * I)
+            for g in "ur":
+                add("Wh_" + g, H * H)
+            for g in "urc":
+                add("b_" + g, H)
+        elif k == "embedding":
+            add("E", d["vocab"] * d["dim"])
+        elif k == "posenc":
+            add("P", d["T"] * d["dim"])
+        elif k == "transformer":
+            D, FF = d["dim"], d["ff"]
+            for name in ("wq", "wk", "wv", "wo"):
+                add(name + ".W", D * D)
+                add(name + ".b", D)
+            for name in ("norm1", "norm2"):
+                add(name + ".gamma", D)
+                if d.get("norm", "ln") != "rms":
+                    add(name + ".beta", D)
+            if d.get("act", "relu") == "swiglu":
+                add("ff1.W", FF * D)
+                add("ff1.V", FF * D)
+            else:
+                add("ff1.W", FF * D)
+                add("ff1.b", FF)
+            add("ff2.W", D * FF)
+            add("ff2.b", D)
+        elif k == "rmsnorm":
+            add("gamma", d["n"])
+        elif k == "batchnorm2d":
+            add("gamma", d["C"])
+            add("beta", d["C"])
+        elif k == "swiglu":
+            add("W", d["in"] * d["out"])
+            add("V", d["in"] * d["out"])
+        elif k == "moe":
+            add("gate.W", d["E"] * d["in"])
+            add("gate.b", d["E"])
+            for e in range(d["E"]):
+                add(f"expert{e}.W", d["out"] * d["in"])
+                add(f"expert{e}.b", d["out"])
+        assert o == sl.stop, (i, k, o, sl)
+    return parts
+
+
+def sign_flips(p_new, p_old, r_new, g_ref, rel=1e-4, upd_rel=1e-2):
+    """Adam updates whose direction differs between two runs.  Returns the
+    count where the reference gradient is below rel * max|g| (sub-noise
+    gradients, where either sign is within rounding; the figure BASELINE asks
+    for) and the count where the reference update itself is larger than
+    upd_rel * max|update| (never expected: a real disagreement)."""
+    p_old = np.asarray(p_old, np.float64)
+    du = np.asarray(p_new, np.float64) - p_old
+    dr = np.asarray(r_new, np.float64) - p_old
+    if not dr.size:
+        return 0, 0
+    flips = np.sign(du) != np.sign(dr)
+    small_g = np.abs(g_ref) <= rel * np.abs(g_ref).max()
+    big_u = np.abs(dr) > upd_rel * np.abs(dr).max()
+    return int((flips & small_g).sum()), int((flips & big_u).sum())

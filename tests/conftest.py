@@ -17,3 +17,15 @@ def oracle():
     from oracle import refcpu
     refcpu.build()
     return refcpu
+
+
+@pytest.fixture(scope="session")
+def gn():
+    import goneuron_amd as gn
+    gn.GetDefaultDevice()
+    return gn
+
+
+@pytest.fixture(scope="session")
+def dev(gn):
+    return gn.GetDefaultDevice()

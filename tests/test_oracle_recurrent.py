@@ -1,0 +1,289 @@
+"""Pins the oracle's BPTT recursions (SequenceUnroller over LSTM and GRU, with a
+Dense head and MSE) against float64 torch autograd.
+
+Each torch model computes the reference's forward values and, through
+zero-valued terms of the form ``v - v.detach()`` (value 0, gradient that of
+``v``) or detached factors, exactly the gradient the reference's hand-written
+backward produces.  Only the quirks are written by hand; every per-step
+derivative (sigmoid', tanh', the cell chain, Wh^T dG, the Dense head, MSE) is
+autograd's.  Each test also shows that the textbook recurrence gives different
+gradients, so a dropped quirk fails it.
+
+LSTM (internal/layer/lstm.go, unroller.go):
+  Q13  only the input gate adds Wx x + Wh h to its bias (lstmComputeInputGates
+       loops over the first outSize rows, lstm.go:1065-1101); f, g, o keep the
+       bias as value, but the backward gives them the full LSTM's gradient
+       (lstm.go:560-606) -> pre = b + (z - z.detach()) on those gates;
+  Q10  the input-weight gradient uses inputBuf, the last step's input
+       (lstm.go:612-640) -> Wx x_t in value, Wx x_{T-1} in gradient;
+  Q15  LSTM.Backward adds dhPrev into the caller's gradient (lstm.go:727-730)
+       and the unroller carries that buffer to the previous step
+       (unroller.go:189-206): dh_{t-1} = dh_t + Wh^T dG -> h_t + (h_{t-1} -
+       h_{t-1}.detach());
+  Q14  clipGradients scales the layer's cumulative gradient to norm 1 after
+       every step (lstm.go:732-761): checked with the clip active by taking
+       autograd's per-step pre-activation gradients dG_t, forming each step's
+       contribution [dG x_last | dG h_{t-1} | dG] and clipping the running sum
+       (worker chain order: samples in order, steps T-1 .. 0).
+GRU (internal/layer/gru.go, unroller.go):
+  Q23  the candidate's delta weights dh by (1 - u) and the direct path by u
+       (gru.go:397-411, 519-520) while the forward is h + u (c - h);
+  Q24  the reset delta is never computed (gru.go:437-447): no gradient into the
+       reset gate; input weights use the last step's input (gru.go:433-454);
+       the candidate's use of the reset block reaches dh_prev as
+       Wh_r[j][i] dC[j] r[j] (row index j, gru.go:515-517);
+  carry dh_{t-1} = dh_t + dhPrev (gru.go:524-527, unroller.go:189-206).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from cfgutil import max_rel
+
+torch = pytest.importorskip("torch")
+
+
+def _det(v):
+    return v - v.detach()
+
+
+def _lstm_params(rng, I, H, scale=0.4):
+    n = 4 * H * I + 4 * H * H + 4 * H + H + 1
+    return (rng.normal(size=n) * scale).astype(np.float32)
+
+
+def _lstm_torch(p, x, y, I, H, T, reference=True, keep_pre=False):
+    """Mean MSE over the batch of SequenceUnroller(LSTM(I, H), T, last) ->
+    Dense(H, 1, Linear); returns (loss, flat gradient, pre-activation
+    gradients [T][B, 4H], hidden states [T + 1][B, H])."""
+    B = x.shape[0]
+    P = torch.tensor(p.astype(np.float64), requires_grad=True)
+    nwx, nwh = 4 * H * I, 4 * H * H
+    Wx = P[:nwx].view(4 * H, I)
+    Wh = P[nwx:nwx + nwh].view(4 * H, H)
+    b = P[nwx + nwh:nwx + nwh + 4 * H]
+    Wd = P[nwx + nwh + 4 * H:nwx + nwh + 5 * H].view(1, H)
+    bd = P[nwx + nwh + 5 * H:]
+    X = torch.tensor(x.astype(np.float64)).view(B, T, I)
+    xl = X[:, T - 1, :]
+    h = torch.zeros(B, H, dtype=torch.float64)
+    c = torch.zeros(B, H, dtype=torch.float64)
+    pres, hs = [], [h.detach().numpy().copy()]
+    for t in range(T):
+        xt = X[:, t, :]
+        if reference:
+            zx = xt @ Wx.detach().T + _det(xl @ Wx.T)          # Q10
+            z = zx + h @ Wh.T
+            z = torch.cat([z[:, :H], _det(z[:, H:])], dim=1)     # Q13
+        else:
+            z = xt @ Wx.T + h @ Wh.T
+        pre = b + z
+        if keep_pre:
+            pre.retain_grad()
+            pres.append(pre)
+        i = torch.sigmoid(pre[:, :H])
+        f = torch.sigmoid(pre[:, H:2 * H])
+        g = torch.tanh(pre[:, 2 * H:3 * H])
+        o = torch.sigmoid(pre[:, 3 * H:])
+        c = f * c + i * g
+        hn = o * torch.tanh(c)
+        if reference:
+            hn = hn + _det(h)                                    # Q15
+        h = hn
+        hs.append(h.detach().numpy().copy())
+    out = (h @ Wd.T + bd)[:, 0]
+    Y = torch.tensor(y.astype(np.float64)).view(B)
+    loss = ((out - Y) ** 2).sum() / B
+    loss.backward()
+    dpre = [q.grad.numpy() * B for q in pres]  # per-sample gradients (the loss is a batch mean)
+    return float(loss), P.grad.numpy(), dpre, hs
+
+
+def _lstm_net(oracle, I, H, T, workers=1):
+    return oracle.Net([oracle.spec(oracle.LAYER_LSTM_UNROLLER, in_size=I, out_size=H, seq_len=T),
+                       oracle.spec(oracle.LAYER_DENSE, in_size=H, out_size=1, act=oracle.ACT_LINEAR)],
+                      oracle.LOSS_MSE, workers=workers)
+
+
+def _lstm_parts(I, H):
+    nwx, nwh = 4 * H * I, 4 * H * H
+    parts = {}
+    for gi, gname in enumerate("ifgo"):
+        parts["Wx_" + gname] = np.s_[gi * H * I:(gi + 1) * H * I]
+        parts["Wh_" + gname] = np.s_[nwx + gi * H * H:nwx + (gi + 1) * H * H]
+        parts["b_" + gname] = np.s_[nwx + nwh + gi * H:nwx + nwh + (gi + 1) * H]
+    parts["dense_W"] = np.s_[nwx + nwh + 4 * H:nwx + nwh + 5 * H]
+    parts["dense_b"] = np.s_[nwx + nwh + 5 * H:nwx + nwh + 5 * H + 1]
+    return parts
+
+
+def _check_parts(got, ref, parts, tol=1e-4):
+    errs = {k: max_rel(got[s], ref[s]) for k, s in parts.items()}
+    bad = {k: e for k, e in errs.items() if e > tol}
+    assert not bad, bad
+    return errs
+
+
+@pytest.mark.parametrize("T,I,H,B", [(6, 5, 7, 3), (9, 4, 6, 2), (12, 3, 5, 1)])
+def test_lstm_bptt_vs_autograd_clip_inactive(oracle, T, I, H, B):
+    """Random parameters (every gate live, non-zero cell-gate bias), targets a
+    small step from the predictions so the cumulative gradient stays far
+    below the clip norm; every gate block of Wx, Wh, b and the Dense head to
+    1e-4 of float64 autograd."""
+    rng = np.random.default_rng(100 + T)
+    p = _lstm_params(rng, I, H)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    net = _lstm_net(oracle, I, H, T)
+    net.params[:] = p
+    # predictions first, then targets 1e-3 away
+    preds = np.array([net.forward(x[b])[0] for b in range(B)], np.float32)
+    y = (preds + 1e-3 * rng.choice([-1.0, 1.0], size=B)).astype(np.float32)
+    loss = net.accumulate_batch(x, y.reshape(B, 1), B)
+    g = net.grads.copy()
+    nl = 4 * H * (I + H) + 4 * H
+    assert np.linalg.norm(g[:nl]) * B < 0.05  # the clip never acts
+    l_ref, g_ref, _, _ = _lstm_torch(p, x, y, I, H, T)
+    assert abs(loss - l_ref) <= 1e-4 * abs(l_ref)
+    _check_parts(g, g_ref, _lstm_parts(I, H))
+    # the textbook LSTM (all gates from Wx x + Wh h, own-step inputs, no
+    # carried dh) gives other gradients: the quirks are what is pinned
+    _, g_std, _, _ = _lstm_torch(p, x, y, I, H, T, reference=False)
+    assert max_rel(g[:nl], g_std[:nl]) > 1e-2
+
+
+def _clip_chain(deltas):
+    """G <- clip(G + D_t) over a chain, in float64 (Q14): the running sum of the
+    contributions scaled to norm 1 whenever its norm exceeds 1."""
+    G = np.zeros_like(deltas[0])
+    for d in deltas:
+        G = G + d
+        n = math.sqrt(float(G @ G))
+        if n > 1:
+            G = G * (1.0 / n)
+    return G
+
+
+@pytest.mark.parametrize("workers", [1, 2, 3])
+def test_lstm_bptt_with_clip_active(oracle, workers):
+    """Large targets: the per-step clip acts.  The recursion's deltas come from
+    autograd (the clip never feeds back into it); each step contributes
+    [dG (x) x_{T-1} | dG (x) h_{t-1} | dG]; each worker chain clips its running
+    sum after every step; the chains are summed and averaged over B."""
+    T, I, H, B = 7, 4, 6, 6
+    rng = np.random.default_rng(77)
+    p = _lstm_params(rng, I, H, scale=0.5)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    y = (rng.normal(size=B) * 30).astype(np.float32)
+    net = _lstm_net(oracle, I, H, T, workers=workers)
+    net.params[:] = p
+    net.accumulate_batch(x, y.reshape(B, 1), B)
+    g = net.grads.copy()
+    _, g_ref, dpre, hs = _lstm_torch(p, x, y, I, H, T, keep_pre=True)
+    X = x.astype(np.float64).reshape(B, T, I)
+    W = min(workers, B)
+    chunk = (B + W - 1) // W
+    nl = 4 * H * (I + H) + 4 * H
+    total = np.zeros(nl)
+    active = 0
+    for c0 in range(0, B, chunk):
+        deltas = []
+        for bb in range(c0, min(B, c0 + chunk)):
+            for t in range(T - 1, -1, -1):
+                dg = dpre[t][bb]
+                deltas.append(np.concatenate([np.outer(dg, X[bb, T - 1]).ravel(),
+                                              np.outer(dg, hs[t][bb]).ravel(), dg]))
+        total += _clip_chain(deltas)
+        run = np.cumsum(np.stack(deltas), axis=0)
+        active += int((np.linalg.norm(run, axis=1) > 1).sum())
+    assert active > 0  # the clip acted somewhere in every configuration
+    ref = g_ref.copy()
+    ref[:nl] = total / B
+    _check_parts(g, ref, _lstm_parts(I, H))
+
+
+def _gru_params(rng, I, H, scale=0.4):
+    n = 3 * H * I + 2 * H * H + 3 * H + H + 1
+    return (rng.normal(size=n) * scale).astype(np.float32)
+
+
+def _gru_torch(p, x, y, I, H, T, reference=True):
+    """Mean MSE over the batch of SequenceUnroller(GRU(I, H), T, last) ->
+    Dense(H, 1, Linear)."""
+    B = x.shape[0]
+    P = torch.tensor(p.astype(np.float64), requires_grad=True)
+    nwx, nwh = 3 * H * I, 2 * H * H
+    Wx = P[:nwx].view(3 * H, I)
+    Wh = P[nwx:nwx + nwh].view(2 * H, H)
+    b = P[nwx + nwh:nwx + nwh + 3 * H]
+    Wd = P[nwx + nwh + 3 * H:nwx + nwh + 4 * H].view(1, H)
+    bd = P[nwx + nwh + 4 * H:]
+    Whu, Whr = Wh[:H], Wh[H:]
+    X = torch.tensor(x.astype(np.float64)).view(B, T, I)
+    xl = X[:, T - 1, :]
+    h = torch.zeros(B, H, dtype=torch.float64)
+    for t in range(T):
+        xt = X[:, t, :]
+        if reference:
+            zx = xt @ Wx.detach().T + _det(xl @ Wx.T)                      # last step's input
+            r = torch.sigmoid(b[H:2 * H] + zx[:, H:2 * H] + h @ Whr.T).detach()  # no reset delta
+            u = torch.sigmoid(b[:H] + zx[:, :H] + h @ Whu.T)
+            hd = h.detach()
+            pre_c = (b[2 * H:] + zx[:, 2 * H:] + (r * hd) @ Whr.T
+                     + r * _det(h @ Whr.detach().T))                           # r[j] on row j
+            c = torch.tanh(pre_c)
+            ud, cd = u.detach(), c.detach()
+            h = ((h + u * (c - h)).detach() + (1 - ud) * _det(c) + _det(u) * (cd - hd)
+                 + ud * _det(h) + _det(h))                                    # (1-u), u, carry
+        else:
+            zx = xt @ Wx.T
+            r = torch.sigmoid(b[H:2 * H] + zx[:, H:2 * H] + h @ Whr.T)
+            u = torch.sigmoid(b[:H] + zx[:, :H] + h @ Whu.T)
+            c = torch.tanh(b[2 * H:] + zx[:, 2 * H:] + (r * h) @ Whr.T)
+            h = h + u * (c - h)
+    out = (h @ Wd.T + bd)[:, 0]
+    Y = torch.tensor(y.astype(np.float64)).view(B)
+    loss = ((out - Y) ** 2).sum() / B
+    loss.backward()
+    return float(loss), P.grad.numpy()
+
+
+def _gru_parts(I, H):
+    nwx, nwh = 3 * H * I, 2 * H * H
+    parts = {}
+    for gi, gname in enumerate("urc"):
+        parts["Wx_" + gname] = np.s_[gi * H * I:(gi + 1) * H * I]
+        parts["b_" + gname] = np.s_[nwx + nwh + gi * H:nwx + nwh + (gi + 1) * H]
+    parts["Wh_u"] = np.s_[nwx:nwx + H * H]
+    parts["Wh_r"] = np.s_[nwx + H * H:nwx + nwh]
+    parts["dense_W"] = np.s_[nwx + nwh + 3 * H:nwx + nwh + 4 * H]
+    parts["dense_b"] = np.s_[nwx + nwh + 4 * H:nwx + nwh + 4 * H + 1]
+    return parts
+
+
+@pytest.mark.parametrize("T,I,H,B,workers", [(7, 4, 5, 3, 1), (11, 3, 8, 4, 2), (5, 6, 4, 1, 1)])
+def test_gru_bptt_vs_autograd(oracle, T, I, H, B, workers):
+    """T > 1 from random parameters: the Wh gradients (update block, and the
+    reset block through the candidate), the carried dh and the quirks against
+    float64 autograd, every block to 1e-4; the textbook GRU differs."""
+    rng = np.random.default_rng(200 + T)
+    p = _gru_params(rng, I, H)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    y = rng.normal(size=B).astype(np.float32)
+    net = oracle.Net([oracle.spec(oracle.LAYER_GRU_UNROLLER, in_size=I, out_size=H, seq_len=T),
+                      oracle.spec(oracle.LAYER_DENSE, in_size=H, out_size=1, act=oracle.ACT_LINEAR)],
+                     oracle.LOSS_MSE, workers=workers)
+    net.params[:] = p
+    loss = net.accumulate_batch(x, y.reshape(B, 1), B)
+    g = net.grads.copy()
+    l_ref, g_ref = _gru_torch(p, x, y, I, H, T)
+    assert abs(loss - l_ref) <= 1e-4 * abs(l_ref)
+    parts = _gru_parts(I, H)
+    # the reset gate's input weights and bias get nothing (both sides exactly 0)
+    for k in ("Wx_r", "b_r"):
+        assert not g[parts[k]].any() and not g_ref[parts[k]].any()
+        del parts[k]
+    _check_parts(g, g_ref, parts)
+    _, g_std = _gru_torch(p, x, y, I, H, T, reference=False)
+    nl = 3 * H * I + 2 * H * H + 3 * H
+    assert max_rel(g[:nl], g_std[:nl]) > 1e-2
