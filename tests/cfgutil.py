@@ -160,18 +160,20 @@ def tensor_parts(cfg, net):
     return parts
 
 
-def sign_flips(p_new, p_old, r_new, g_ref, rel=1e-4, upd_rel=1e-2):
-    """Adam updates whose direction differs between two runs.  Returns the
-    count where the reference gradient is below rel * max|g| (sub-noise
-    gradients, where either sign is within rounding; the figure BASELINE asks
-    for) and the count where the reference update itself is larger than
-    upd_rel * max|update| (never expected: a real disagreement)."""
+def adam_flips(p_new, p_old, r_new, m_ref, rel=1e-4):
+    """Adam updates whose direction differs between two runs.  A flip is
+    expected only where the reference's new first moment m is at noise level
+    (|m| <= rel * max|m| of the tensor: the sign of m, hence of the update, is
+    then within rounding; at the first step m = (1 - beta1) g, so this is the
+    sub-noise-gradient count BASELINE asks for).  Returns (mask of those
+    allowed flips, their count, count of flips elsewhere)."""
     p_old = np.asarray(p_old, np.float64)
     du = np.asarray(p_new, np.float64) - p_old
     dr = np.asarray(r_new, np.float64) - p_old
     if not dr.size:
-        return 0, 0
+        return np.zeros(0, bool), 0, 0
     flips = np.sign(du) != np.sign(dr)
-    small_g = np.abs(g_ref) <= rel * np.abs(g_ref).max()
-    big_u = np.abs(dr) > upd_rel * np.abs(dr).max()
-    return int((flips & small_g).sum()), int((flips & big_u).sum())
+    m_ref = np.asarray(m_ref, np.float64)
+    small = np.abs(m_ref) <= rel * np.abs(m_ref).max()
+    allowed = flips & small
+    return allowed, int(allowed.sum()), int((flips & ~small).sum())

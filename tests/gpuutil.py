@@ -5,7 +5,7 @@ import sys
 
 import numpy as np
 
-from cfgutil import max_rel, norm_rel, oracle_net, sign_flips, tensor_parts
+from cfgutil import adam_flips, max_rel, norm_rel, oracle_net, tensor_parts
 
 TOL = 1e-4
 
@@ -39,14 +39,29 @@ class DBuf:
             pass
 
 
-def compare_step(gn, oracle, cfg, steps=1, workers=1, perturb=None, setup=None, xy=None):
-    """perturb(params) -> params: optional replacement of the initial weights,
-    loaded into both implementations (e.g. non-zero TransformerBlock weights).
-    setup(model, net): called before the first step on both sides.
-    Every parameter tensor is checked on its own: gradient max|a-r|/max|r| and
-    updated weights ||a-r||/||r|| to 1e-4; Adam updates whose direction
-    differs are counted (allowed only where the reference gradient is below
-    1e-4 of its tensor's maximum)."""
+def compare_step(gn, oracle, cfg, steps=1, workers=1, perturb=None, setup=None, xy=None,
+                 arbiter=None):
+    """One model on the GPU and the oracle, step by step from the same weights.
+
+    perturb(params) -> params: replacement of the initial weights, loaded into
+    both (e.g. a non-zero TransformerBlock).  setup(model, net): called before
+    the first step.  xy: inputs other than the config's synthetic ones.
+
+    Every parameter tensor is checked on its own:
+      - gradient max|a - r| / max|r| <= 1e-4.  A tensor whose reference
+        gradient is numerically zero (max|r| <= 1e-6 of its layer's largest
+        gradient; e.g. the attention K projection without RoPE, whose token
+        sum of gK vanishes because softmax Jacobian rows sum to zero) must be
+        below that floor on the GPU too;
+      - with arbiter(params) -> float64 gradient (the exact answer), a tensor
+        that misses 1e-4 against the oracle passes if the GPU is within 1e-4
+        of the exact answer and no further from it than the oracle, i.e. the
+        difference is the oracle's (the reference's) own float32 rounding;
+      - updated weights ||a - r|| / ||r|| <= 1e-4 outside the Adam updates
+        whose direction legitimately differs (first moment at noise level);
+        those are counted, and flips anywhere else fail.  The updates of
+        numerically zero tensors are Adam-normalised rounding noise on both
+        sides and are not compared."""
     from goneuron_amd import configs
     log(f"model parity {cfg['name']} B={cfg['B']} steps={steps} W={workers}")
     x, y = configs.inputs(cfg) if xy is None else xy
@@ -55,6 +70,7 @@ def compare_step(gn, oracle, cfg, steps=1, workers=1, perturb=None, setup=None, 
     net = oracle_net(oracle, cfg, workers=workers)
     np.testing.assert_array_equal(model.Params(), net.params)  # LCG init is exact
     parts = tensor_parts(cfg, net)
+    layer_of = {name: int(name.split(":")[0]) for name, _ in parts}
     if perturb is not None:
         p = perturb(net.params.copy())
         net.params[:] = p
@@ -63,25 +79,56 @@ def compare_step(gn, oracle, cfg, steps=1, workers=1, perturb=None, setup=None, 
         setup(model, net)
     for s in range(steps):
         p_old = net.params.copy()
+        truth = arbiter(p_old) if arbiter is not None else None
         lg = model.TrainBatch(x, y)
         lo = net.accumulate_batch(x, y, B)
         g_gpu = model.Gradients()
         g_ref = net.grads.copy()
         assert abs(lg - lo) <= TOL * max(abs(lo), 1e-30), (s, lg, lo)
-        bad = {name: e for name, sl in parts if (e := max_rel(g_gpu[sl], g_ref[sl])) > TOL}
+        lmax = {i: float(np.abs(g_ref[net.layer_slice(i)]).max()) if net.layer_slice(i).stop >
+                net.layer_slice(i).start else 0.0 for i in set(layer_of.values())}
+        bad, zero, arb = {}, [], {}
+        for name, sl in parts:
+            floor = 1e-6 * lmax[layer_of[name]]
+            if float(np.abs(g_ref[sl]).max()) <= floor:
+                zero.append(name)
+                if float(np.abs(g_gpu[sl]).max()) > floor:
+                    bad[name] = ("numerically zero in the reference", float(np.abs(g_gpu[sl]).max()), floor)
+                continue
+            e = max_rel(g_gpu[sl], g_ref[sl])
+            if e <= TOL:
+                continue
+            if truth is not None:
+                e_gt, e_ot = max_rel(g_gpu[sl], truth[sl]), max_rel(g_ref[sl], truth[sl])
+                arb[name] = (e, e_gt, e_ot)
+                if e_gt <= TOL and e_gt <= e_ot:
+                    continue
+            bad[name] = e
+        if zero:
+            log(f"  step {s}: numerically zero in both: {zero}")
+        for name, (e, e_gt, e_ot) in arb.items():
+            log(f"  step {s}: {name}: gpu-oracle {e:.2e}, gpu-exact {e_gt:.2e}, oracle-exact {e_ot:.2e}")
         assert not bad, (s, bad)
         net.step()
         p_gpu = model.Params()
-        bad = {name: e for name, sl in parts if (e := norm_rel(p_gpu[sl], net.params[sl])) > TOL}
-        assert not bad, (s, bad)
-        small = big = 0
+        m_ref = net.adam_m
+        nflip, bad = 0, {}
         for name, sl in parts:
-            a, b_ = sign_flips(p_gpu[sl], p_old[sl], net.params[sl], g_ref[sl])
-            small += a
-            big += b_
-        log(f"  step {s}: {len(parts)} tensors within 1e-4; Adam direction flips "
-            f"{small} on sub-1e-4 gradients, {big} on updates above 1e-2 of the largest")
-        assert big == 0, (s, big)
+            if name in zero:
+                # Adam normalises the rounding noise of a numerically zero
+                # gradient to full-size steps of either sign: not comparable
+                continue
+            allowed, n_ok, n_bad = adam_flips(p_gpu[sl], p_old[sl], net.params[sl], m_ref[sl])
+            nflip += n_ok
+            if n_bad:
+                bad[name] = ("direction flips", n_bad)
+                continue
+            keep = ~allowed
+            if norm_rel(p_gpu[sl][keep], net.params[sl][keep]) > TOL:
+                bad[name] = norm_rel(p_gpu[sl][keep], net.params[sl][keep])
+        assert not bad, (s, bad)
+        log(f"  step {s}: {len(parts)} tensors checked; {nflip} Adam updates flipped where the "
+            f"first moment is at noise level")
         # keep the two runs on identical weights so each step is checked alone
         net.params[:] = p_gpu
     m_gpu, v_gpu, t = model.AdamState()

@@ -496,9 +496,13 @@ def test_lstm_full_config(gn, oracle, workers, steps, start):
     start (every gate live from the first step), each gate block of Wx, Wh
     and b checked on its own."""
     from goneuron_amd import configs
+    from recurrent_ref import lstm_clip_truth
     cfg = configs.lstm()
+    x, y = configs.inputs(cfg)
+    d = cfg["layers"][0]
+    exact = lambda p: lstm_clip_truth(p, x, y[:, 0], d["in"], d["hidden"], d["T"], workers)
     _compare_step(gn, oracle, cfg, steps=steps, workers=workers,
-                  perturb=_random_lstm(cfg) if start == "random" else None)
+                  perturb=_random_lstm(cfg) if start == "random" else None, arbiter=exact)
 
 
 @pytest.mark.parametrize("workers", [1, 3])
@@ -602,14 +606,21 @@ def test_gpt_full_config_random_block(gn, oracle):
 
 
 def test_gpt_embedding_index_error(gn, oracle):
+    """An out-of-range id fails inference (ForwardBatch returns the error) and
+    leaves the parameters alone; training skips the sample instead (see
+    test_gpu_semantics.py)."""
     from goneuron_amd import configs
     cfg = configs.gpt(B=2, T=4, vocab=10, dim=8, heads=2, ff=8)
     model = configs.build(cfg)
     x, y = configs.inputs(cfg)
     x[1, 2] = 10  # out of range
+    p0 = model.Params()
     with pytest.raises(gn.GNError) as e:
-        model.TrainBatch(x, y)
+        model.PredictBatch(x)
     assert e.value.code == -8
+    np.testing.assert_array_equal(model.Params(), p0)
+    model.TrainBatch(x, y)
+    assert model.SkippedSamples() == 1
 
 
 # ------------------------------------------------------------------ full-size C3 vs torch fp32

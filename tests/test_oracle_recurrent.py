@@ -42,62 +42,8 @@ import pytest
 from cfgutil import max_rel
 
 torch = pytest.importorskip("torch")
-
-
-def _det(v):
-    return v - v.detach()
-
-
-def _lstm_params(rng, I, H, scale=0.4):
-    n = 4 * H * I + 4 * H * H + 4 * H + H + 1
-    return (rng.normal(size=n) * scale).astype(np.float32)
-
-
-def _lstm_torch(p, x, y, I, H, T, reference=True, keep_pre=False):
-    """Mean MSE over the batch of SequenceUnroller(LSTM(I, H), T, last) ->
-    Dense(H, 1, Linear); returns (loss, flat gradient, pre-activation
-    gradients [T][B, 4H], hidden states [T + 1][B, H])."""
-    B = x.shape[0]
-    P = torch.tensor(p.astype(np.float64), requires_grad=True)
-    nwx, nwh = 4 * H * I, 4 * H * H
-    Wx = P[:nwx].view(4 * H, I)
-    Wh = P[nwx:nwx + nwh].view(4 * H, H)
-    b = P[nwx + nwh:nwx + nwh + 4 * H]
-    Wd = P[nwx + nwh + 4 * H:nwx + nwh + 5 * H].view(1, H)
-    bd = P[nwx + nwh + 5 * H:]
-    X = torch.tensor(x.astype(np.float64)).view(B, T, I)
-    xl = X[:, T - 1, :]
-    h = torch.zeros(B, H, dtype=torch.float64)
-    c = torch.zeros(B, H, dtype=torch.float64)
-    pres, hs = [], [h.detach().numpy().copy()]
-    for t in range(T):
-        xt = X[:, t, :]
-        if reference:
-            zx = xt @ Wx.detach().T + _det(xl @ Wx.T)          # Q10
-            z = zx + h @ Wh.T
-            z = torch.cat([z[:, :H], _det(z[:, H:])], dim=1)     # Q13
-        else:
-            z = xt @ Wx.T + h @ Wh.T
-        pre = b + z
-        if keep_pre:
-            pre.retain_grad()
-            pres.append(pre)
-        i = torch.sigmoid(pre[:, :H])
-        f = torch.sigmoid(pre[:, H:2 * H])
-        g = torch.tanh(pre[:, 2 * H:3 * H])
-        o = torch.sigmoid(pre[:, 3 * H:])
-        c = f * c + i * g
-        hn = o * torch.tanh(c)
-        if reference:
-            hn = hn + _det(h)                                    # Q15
-        h = hn
-        hs.append(h.detach().numpy().copy())
-    out = (h @ Wd.T + bd)[:, 0]
-    Y = torch.tensor(y.astype(np.float64)).view(B)
-    loss = ((out - Y) ** 2).sum() / B
-    loss.backward()
-    dpre = [q.grad.numpy() * B for q in pres]  # per-sample gradients (the loss is a batch mean)
-    return float(loss), P.grad.numpy(), dpre, hs
+from recurrent_ref import (_clip_chain, _gru_params, _gru_torch, _lstm_params,  # noqa: E402
+                           _lstm_torch)
 
 
 def _lstm_net(oracle, I, H, T, workers=1):
@@ -152,18 +98,6 @@ def test_lstm_bptt_vs_autograd_clip_inactive(oracle, T, I, H, B):
     assert max_rel(g[:nl], g_std[:nl]) > 1e-2
 
 
-def _clip_chain(deltas):
-    """G <- clip(G + D_t) over a chain, in float64 (Q14): the running sum of the
-    contributions scaled to norm 1 whenever its norm exceeds 1."""
-    G = np.zeros_like(deltas[0])
-    for d in deltas:
-        G = G + d
-        n = math.sqrt(float(G @ G))
-        if n > 1:
-            G = G * (1.0 / n)
-    return G
-
-
 @pytest.mark.parametrize("workers", [1, 2, 3])
 def test_lstm_bptt_with_clip_active(oracle, workers):
     """Large targets: the per-step clip acts.  The recursion's deltas come from
@@ -200,52 +134,6 @@ def test_lstm_bptt_with_clip_active(oracle, workers):
     ref = g_ref.copy()
     ref[:nl] = total / B
     _check_parts(g, ref, _lstm_parts(I, H))
-
-
-def _gru_params(rng, I, H, scale=0.4):
-    n = 3 * H * I + 2 * H * H + 3 * H + H + 1
-    return (rng.normal(size=n) * scale).astype(np.float32)
-
-
-def _gru_torch(p, x, y, I, H, T, reference=True):
-    """Mean MSE over the batch of SequenceUnroller(GRU(I, H), T, last) ->
-    Dense(H, 1, Linear)."""
-    B = x.shape[0]
-    P = torch.tensor(p.astype(np.float64), requires_grad=True)
-    nwx, nwh = 3 * H * I, 2 * H * H
-    Wx = P[:nwx].view(3 * H, I)
-    Wh = P[nwx:nwx + nwh].view(2 * H, H)
-    b = P[nwx + nwh:nwx + nwh + 3 * H]
-    Wd = P[nwx + nwh + 3 * H:nwx + nwh + 4 * H].view(1, H)
-    bd = P[nwx + nwh + 4 * H:]
-    Whu, Whr = Wh[:H], Wh[H:]
-    X = torch.tensor(x.astype(np.float64)).view(B, T, I)
-    xl = X[:, T - 1, :]
-    h = torch.zeros(B, H, dtype=torch.float64)
-    for t in range(T):
-        xt = X[:, t, :]
-        if reference:
-            zx = xt @ Wx.detach().T + _det(xl @ Wx.T)                      # last step's input
-            r = torch.sigmoid(b[H:2 * H] + zx[:, H:2 * H] + h @ Whr.T).detach()  # no reset delta
-            u = torch.sigmoid(b[:H] + zx[:, :H] + h @ Whu.T)
-            hd = h.detach()
-            pre_c = (b[2 * H:] + zx[:, 2 * H:] + (r * hd) @ Whr.T
-                     + r * _det(h @ Whr.detach().T))                           # r[j] on row j
-            c = torch.tanh(pre_c)
-            ud, cd = u.detach(), c.detach()
-            h = ((h + u * (c - h)).detach() + (1 - ud) * _det(c) + _det(u) * (cd - hd)
-                 + ud * _det(h) + _det(h))                                    # (1-u), u, carry
-        else:
-            zx = xt @ Wx.T
-            r = torch.sigmoid(b[H:2 * H] + zx[:, H:2 * H] + h @ Whr.T)
-            u = torch.sigmoid(b[:H] + zx[:, :H] + h @ Whu.T)
-            c = torch.tanh(b[2 * H:] + zx[:, 2 * H:] + (r * h) @ Whr.T)
-            h = h + u * (c - h)
-    out = (h @ Wd.T + bd)[:, 0]
-    Y = torch.tensor(y.astype(np.float64)).view(B)
-    loss = ((out - Y) ** 2).sum() / B
-    loss.backward()
-    return float(loss), P.grad.numpy()
 
 
 def _gru_parts(I, H):
