@@ -104,6 +104,8 @@ SIGNATURES = {
                                    C.c_int32]),
     "gn_dense_backward": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int32, C.c_int32,
                                     C.c_int32, C.c_int32, C.c_int32, C.c_float]),
+    "gn_dense_backward_noalloc": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, C.c_int32, C.c_int32,
+                                            C.c_int32, C.c_int32, C.c_int32, C.c_float]),
     "gn_gemm": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float, vp,
                           C.c_int32, vp, C.c_int32, vp, C.c_int32]),
     "gn_adam_step": (C.c_int, [vp, vp, vp, vp, vp, C.c_int64, C.c_float, C.c_float, C.c_float,

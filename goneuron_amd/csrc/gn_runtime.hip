@@ -15,12 +15,26 @@
 
 #include <algorithm>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "gn_common.h"
 
 using namespace gn;
+
+// Scratch of gn_dense_backward_noalloc, one copy per GPU for the process's
+// lifetime: dz (B x out, at most kNoAllocDz floats) followed by the partial
+// sums of the bias column sums and of split-K GEMMs.  In host code the name
+// only stands for the symbol: the device address comes from
+// hipGetSymbolAddress at gn_init (noalloc_ptr), per device.
+constexpr size_t kNoAllocFloats = (size_t)8 << 20;  // 32 MiB
+constexpr size_t kNoAllocDz = (size_t)4 << 20;      // dz part: 16 MiB
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+constexpr int kMaxDevices = 64;
+static float *noalloc_ptr[kMaxDevices];
+static std::mutex noalloc_mu;
 
 struct gn_ctx {
   int device = 0;
@@ -32,6 +46,7 @@ struct gn_ctx {
   float *scratch = nullptr;  // colsum partials
   size_t scratch_floats = 0;
   float *scratch_aux = nullptr;  // the same for kernels queued on `aux` (scratch_floats long)
+  float *noalloc = nullptr;      // this device's copy of `scratch` (gn_dense_backward_noalloc)
   // kernel timing (gn_timing_enable)
   bool timing = false;
   struct Rec { int cls; hipEvent_t a, b; };
@@ -165,6 +180,18 @@ extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
   c->device = device_ordinal;
   if (hipSetDevice(device_ordinal) != hipSuccess) return GN_ERR_HIP;
   if (hipGetDeviceProperties(&c->props, device_ordinal) != hipSuccess) return GN_ERR_HIP;
+  if (device_ordinal >= kMaxDevices) return GN_ERR_INVALID;
+  {
+    // once per device, with that device current: the address of its copy of
+    // the no-alloc scratch array
+    std::lock_guard<std::mutex> lk(noalloc_mu);
+    if (!noalloc_ptr[device_ordinal]) {
+      float *p = nullptr;
+      if (hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return GN_ERR_HIP;
+      noalloc_ptr[device_ordinal] = p;
+    }
+    c->noalloc = noalloc_ptr[device_ordinal];
+  }
   // both streams at the default priority
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return GN_ERR_HIP;
   if (hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking) != hipSuccess) {
@@ -353,22 +380,31 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
 // recorded on the main stream, with aux's own scratch) and run next to the dX
 // GEMM: the two GEMMs share the CUs, and each one's prologue and tail are
 // covered by the other's tiles.
+// ms / ms_cap: scratch of the kernels on the main stream (default: the
+// context's).
 static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz,
                                  float *gW, float *gB, float *gin, int B, int in, int out_n,
                                  float scale, const float *gin_aux, int gin_deriv,
-                                 hipEvent_t dz_ready = nullptr) {
+                                 hipEvent_t dz_ready = nullptr, float *ms = nullptr,
+                                 size_t ms_cap = 0) {
   hipError_t e;
+  if (!ms) {
+    ms = c->scratch;
+    ms_cap = c->scratch_floats;
+  }
   hipStream_t ws = c->stream;
-  float *wscr = c->scratch;
+  float *wscr = ms;
+  size_t wcap = ms_cap;
   if (dz_ready) {
     if ((e = hipEventRecord(dz_ready, c->stream)) != hipSuccess) return e;
     if ((e = hipStreamWaitEvent(c->aux, dz_ready, 0)) != hipSuccess) return e;
     ws = c->aux;
     wscr = c->scratch_aux;
+    wcap = c->scratch_floats;
   }
   if (gB) {
     KTimer kt(c, GN_KCLASS_OTHER, ws);
-    e = launch_colsum(dz, B, out_n, out_n, scale, gB, wscr, c->scratch_floats, ws);
+    e = launch_colsum(dz, B, out_n, out_n, scale, gB, wscr, wcap, ws);
     if (e != hipSuccess) return e;
   }
   GemmArgs a{};
@@ -377,7 +413,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
   a.B = x; a.ldb = in;
   a.C = gW; a.ldc = in;
   a.alpha = scale;
-  a.ws = wscr; a.ws_cap = c->scratch_floats;
+  a.ws = wscr; a.ws_cap = wcap;
   {
     KTimer kt(c, GN_KCLASS_GEMM, ws);
     e = launch_gemm('T', 'N', EPI_SCALE, a, ws);
@@ -390,7 +426,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
     d.B = W; d.ldb = in;
     d.C = gin; d.ldc = in;
     d.alpha = 1.f;
-    d.ws = c->scratch; d.ws_cap = c->scratch_floats;
+    d.ws = ms; d.ws_cap = ms_cap;
     KTimer kt(c, GN_KCLASS_GEMM);
     if (gin_aux) {
       d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv;
@@ -447,13 +483,10 @@ __global__ void jac_rows_kernel(const float *__restrict__ o, const float *__rest
     d[i] = logsm ? grow[i] - (float)exp((double)orow[i]) * s : grow[i] * orow[i] - orow[i] * s;
 }
 
-extern "C" int gn_dense_backward(gn_ctx *c, const float *x, const float *W, const float *out,
-                                 const float *gout, float *gradW, float *gradB, float *gin,
-                                 float *dz, int32_t B, int32_t in, int32_t out_n, int32_t act,
-                                 int32_t act_is_ptr, float scale) {
-  ENTRY(c);
-  if (!x || !W || !out || !gout || !gradW || !dz || B <= 0 || in <= 0 || out_n <= 0)
-    return set_err(c, GN_ERR_INVALID, "bad dense_backward args");
+static int dense_backward_op(gn_ctx *c, const float *x, const float *W, const float *out,
+                             const float *gout, float *gradW, float *gradB, float *gin, float *dz,
+                             int32_t B, int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr,
+                             float scale, float *ms, size_t ms_cap) {
   ActPlan ap;
   if (plan_act(act, act_is_ptr, ap)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
   if (ap.jac) {
@@ -463,8 +496,43 @@ extern "C" int gn_dense_backward(gn_ctx *c, const float *x, const float *W, cons
   } else {
     HIP_OK(c, launch_dact(gout, out, dz, (int64_t)B * out_n, ap.deriv, c->stream));
   }
-  HIP_OK(c, dense_bwd_core(c, x, W, dz, gradW, gradB, gin, B, in, out_n, scale, nullptr, 0));
+  HIP_OK(c, dense_bwd_core(c, x, W, dz, gradW, gradB, gin, B, in, out_n, scale, nullptr, 0, nullptr,
+                           ms, ms_cap));
   return GN_OK;
+}
+
+extern "C" int gn_dense_backward(gn_ctx *c, const float *x, const float *W, const float *out,
+                                 const float *gout, float *gradW, float *gradB, float *gin,
+                                 float *dz, int32_t B, int32_t in, int32_t out_n, int32_t act,
+                                 int32_t act_is_ptr, float scale) {
+  ENTRY(c);
+  if (!x || !W || !out || !gout || !gradW || !dz || B <= 0 || in <= 0 || out_n <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad dense_backward args");
+  return dense_backward_op(c, x, W, out, gout, gradW, gradB, gin, dz, B, in, out_n, act, act_is_ptr,
+                           scale, nullptr, 0);
+}
+
+// gn_dense_backward without the dz workspace and without the context's
+// scratch: dz and every partial sum live in this device's copy of `scratch`
+// (noalloc_ptr), so the call allocates nothing.  Calls that overlap on one
+// GPU (other streams, other contexts, other threads) share that array and
+// race; the array keeps the last call's contents, and nothing in it needs to
+// start at zero (every value is written before it is read).
+extern "C" int gn_dense_backward_noalloc(gn_ctx *c, const float *x, const float *W, const float *out,
+                                         const float *gout, float *gradW, float *gradB, float *gin,
+                                         int32_t B, int32_t in, int32_t out_n, int32_t act,
+                                         int32_t act_is_ptr, float scale) {
+  ENTRY(c);
+  if (!x || !W || !out || !gout || !gradW || B <= 0 || in <= 0 || out_n <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad dense_backward_noalloc args");
+  if ((size_t)B * (size_t)out_n > kNoAllocDz)
+    return set_err(c, GN_ERR_INVALID,
+                   "dense_backward_noalloc: B x out = %lld floats exceeds the static scratch limit of "
+                   "%zu floats (use gn_dense_backward with a workspace)",
+                   (long long)B * out_n, kNoAllocDz);
+  if (!c->noalloc) return set_err(c, GN_ERR_HIP, "no-alloc scratch address unavailable");
+  return dense_backward_op(c, x, W, out, gout, gradW, gradB, gin, c->noalloc, B, in, out_n, act,
+                           act_is_ptr, scale, c->noalloc + kNoAllocDz, kNoAllocFloats - kNoAllocDz);
 }
 
 extern "C" int gn_adam_step(gn_ctx *c, float *p, const float *g, float *m, float *v, int64_t n,

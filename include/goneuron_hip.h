@@ -254,6 +254,17 @@ int gn_dense_backward(gn_ctx *ctx, const float *x, const float *W, const float *
                       const float *gout, float *gradW, float *gradB, float *gin, float *dz_scratch,
                       int32_t B, int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr,
                       float scale);
+/* No counterpart in the reference: gn_dense_backward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments without the dz workspace;
+ * dz and the partial sums live in a static 32 MiB device array of the
+ * library (one per GPU, held until the process ends), so B x out_n may not
+ * exceed 4,194,304 floats (GN_ERR_INVALID otherwise).  The call allocates
+ * nothing.  Calls that overlap on one GPU share that array and race: the
+ * caller serialises them. */
+int gn_dense_backward_noalloc(gn_ctx *ctx, const float *x, const float *W, const float *out,
+                              const float *gout, float *gradW, float *gradB, float *gin, int32_t B,
+                              int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr, float scale);
 /* Generic fp32 MFMA GEMM: C[M,N] = alpha * op(A) op(B); trans flags as BLAS
  * (A is M x K row-major when transA == 0, K x M when 1; B is K x N when
  * transB == 0, N x K when 1).  Stands in for matMulMPSPersistent
