@@ -1,18 +1,24 @@
 """Throughput of GoNeuron's fp32 training step (forward + backward + Adam) on
-one MI355X, with the roofline fraction of the dominant kernel and the CPU
-reference path timed beside it.
+one MI355X, with the roofline fraction of every kernel and the CPU reference
+path timed beside it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wide]
 
-Prints ONE JSON line.  `value` is samples/s with inputs resident in HBM; the
-GEMM family's achieved TFLOP/s comes from HIP events recorded around every
-GEMM launch on the library's stream during the timed steps.
+Prints ONE JSON line.  `value` is samples/s of the headline workload (C3, the
+wide Dense stack, unless --config says otherwise) with inputs resident in HBM.
+The `configs` key holds the same measurements for the other four BASELINE
+configurations, so one run times all five.  Per-kernel rooflines come from
+HIP events the library records around each of its launches (on the stream the
+launch goes to), divided into the launch's algorithmic work (bytes for
+memory-bound kernels, FLOPs for matrix-core kernels) that the library states
+per launch site.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -21,28 +27,85 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix (and vector) peak
+PEAK_FP64_MFMA_TFLOPS = 78.6
 PEAK_HBM_GBPS = 8000.0
+# the CPU share of one GPU on the GPU boxes (their nproc shows the whole host)
+CPU_SHARE = 16
 
-# HBM bytes per training step moved by the GEMM family, from rocprofv3 --pmc
-# FETCH_SIZE (x2.000) and WRITE_SIZE (x1.000) passes, each scaled by what the
-# counter reads for a 1 GiB device-to-device copy (bench.py --copy-probe 1024).
-# Keyed by workload; a changed GEMM kernel needs a new measurement.
-GEMM_TRAFFIC_BYTES_PER_STEP = {"wide": 2861.0e6}
-
-
-def gemm_flops(cfg, B):
-    """Algorithmic GEMM FLOPs of one step: forward 2*B*in*out per Dense,
-    dW the same, dX for every Dense but the first (its dX is discarded)."""
-    f = 0
-    dense = [d for d in cfg["layers"] if d["kind"] == "dense"]
-    for i, d in enumerate(dense):
-        mac = B * d["in"] * d["out"]
-        f += 2 * mac + 2 * mac + (2 * mac if i > 0 else 0)
-    return f
+# HBM bytes per GEMM launch of the C3 step, from the FETCH_SIZE / WRITE_SIZE
+# rocprofv3 passes of this bench scaled by a copy kernel of known size
+# (bench.py --calibrate-copy); read from the committed summary.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "wide_gemm_adam_hbm_traffic.md")
 
 
-def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
+def gemm_traffic_per_launch():
+    """The `gemm_bytes_per_launch: N` line of the committed counter summary."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                m = re.match(r"\s*gemm_bytes_per_launch:\s*([0-9.eE+]+)", line)
+                if m:
+                    return float(m.group(1))
+    except OSError:
+        pass
+    return None
+
+
+def kernel_bound(name):
+    """(bound, peak, unit) a kernel is judged against."""
+    if name.startswith("gemm_") or name in ("attn_fwd", "attn_bwd", "conv_wgrad"):
+        return "mfma", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+    if name == "lstm_gram":
+        return "mfma_fp64", PEAK_FP64_MFMA_TFLOPS, "TFLOP/s"
+    if name in ("conv_fwd", "conv_dgrad", "lstm_fwd", "lstm_bptt", "gru_fwd", "gru_bwd"):
+        # fp32 VALU / latency-bound recurrences: FLOP rate against the fp32 peak
+        return "valu", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
+    return "hbm", PEAK_HBM_GBPS, "GB/s"
+
+
+def kernel_table(lib, dev, K):
+    """Per-kernel stats of the timed steps: launches and ms per step, achieved
+    rate, fraction of the bound's peak."""
+    import ctypes as C
+    from goneuron_amd._lib import KernelStat, check
+    cap = 256
+    arr = (KernelStat * cap)()
+    n = C.c_int32()
+    check(dev.h, lib.gn_timing_kernels(dev.h, arr, cap, C.byref(n)))
+    out = {}
+    for i in range(min(n.value, cap)):
+        st = arr[i]
+        name = st.name.decode()
+        bound, peak, unit = kernel_bound(name)
+        scale = 1e12 if unit == "TFLOP/s" else 1e9
+        ach = st.units / (st.ms * 1e-3) / scale if st.ms > 0 and st.units > 0 else None
+        out[name] = {"launches_per_step": st.launches / K, "ms_per_step": st.ms / K,
+                     "us_per_launch": 1e3 * st.ms / st.launches if st.launches else None,
+                     "bound": bound, "achieved": ach, "unit": unit, "peak": peak,
+                     "frac": ach / peak if ach else None,
+                     "units_per_launch": st.units / st.launches if st.launches else None}
+    return out
+
+
+def host_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": aff, "cpu_share": CPU_SHARE}
+
+
+def cpu_baseline(cfg, x, y, budget_s, threads):
     """The CPU oracle (C restatement of the reference's per-sample path) timed
     on the host, on a bounded sample, two ways:
       - parallel (the reported value): trainBatchParallel's structure
@@ -58,7 +121,7 @@ def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
     from cfgutil import oracle_net
     refcpu.build()
     B = cfg["B"]
-    T = threads or min(B, os.cpu_count() or 1, 16)
+    T = threads
     nets = [oracle_net(refcpu, cfg) for _ in range(T)]
     net = nets[0]
     # calibrate with one sample, then fill the budget
@@ -112,14 +175,122 @@ def cpu_baseline(cfg, x, y, budget_s=15.0, workers=1, threads=None):
                               "sample": f"{n1} of {B} samples fwd+bwd ({ts1:.2f} s) + Adam scaled by n/B"}}
 
 
-def predict_bench(args, cfg, model, dev, dx, B, workers):
+def dominant(kernels):
+    """The roofline entry of the kernel with the most time per step."""
+    if not kernels:
+        return None
+    name, k = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])
+    return {"kernel": name, "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
+            "unit": k["unit"], "frac": k["frac"], "ms_per_step": k["ms_per_step"]}
+
+
+def run_config(name, args, dev, with_cpu, cpu_budget, threads):
+    """One configuration: plain timed steps (value), the same steps with the
+    library's per-launch events (kernel table), Adam alone, the host-pointer
+    step (H2D included), and the CPU baseline."""
+    import ctypes as C
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib, check
+    L = lib()
+    cfg = configs.CONFIGS[name]()
+    B = cfg["B"]
+    x, y = configs.inputs(cfg)
+    workers = configs.gpu_workers(B)
+    model = configs.build(cfg, device=dev, workers=workers)
+
+    def dbuf(a):
+        p = C.c_void_p()
+        check(dev.h, L.gn_malloc(dev.h, a.nbytes, C.byref(p)))
+        check(dev.h, L.gn_memcpy_h2d(dev.h, p, a.ctypes.data, a.nbytes))
+        return p
+
+    dx, dy = dbuf(x), dbuf(y)
+    K = args.steps
+    step = lambda: check(dev.h, L.gn_model_train_step_device(model.h, dx, dy, B))
+    for _ in range(args.warmup):
+        step()
+    dev.sync()
+    # timed region: K steps, no instrumentation -> value
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    dev.sync()
+    elapsed = time.perf_counter() - t0
+    # the same K steps with a HIP event pair around every launch -> kernel table
+    check(dev.h, L.gn_timing_enable(dev.h, 1))
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    dev.sync()
+    elapsed_ev = time.perf_counter() - t0
+    kernels = kernel_table(L, dev, K)
+    check(dev.h, L.gn_timing_enable(dev.h, 0))
+    # Adam alone: Network.Step's full-arena update (gn_model_step), K launches
+    check(dev.h, L.gn_timing_enable(dev.h, 1))
+    for _ in range(K):
+        check(dev.h, L.gn_model_step(model.h))
+    dev.sync()
+    adam = kernel_table(L, dev, K).get("adam")
+    check(dev.h, L.gn_timing_enable(dev.h, 0))
+    loss = C.c_float()
+    check(dev.h, L.gn_model_read_loss(model.h, C.byref(loss)))
+    # end to end from host buffers: the step copies x and y over PCIe first
+    xh, yh = np.ascontiguousarray(x), np.ascontiguousarray(y)
+    fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+    hstep = lambda: check(dev.h, L.gn_model_train_step(model.h, fp(xh), fp(yh), B, None))
+    hstep()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        hstep()
+    dev.sync()
+    elapsed_h = time.perf_counter() - t0
+    # explicit, ordered teardown: input buffers, then the model
+    check(dev.h, L.gn_free(dev.h, dx))
+    check(dev.h, L.gn_free(dev.h, dy))
+    nparams = model.nparams
+    model.Close()
+    gemm = {k: v for k, v in kernels.items() if k.startswith("gemm_")}
+    g_ms = sum(v["ms_per_step"] for v in gemm.values()) * K
+    g_n = sum(v["launches_per_step"] for v in gemm.values()) * K
+    g_units = sum(v["units_per_launch"] * v["launches_per_step"] for v in gemm.values()) * K
+    res = {
+        "workload": name, "batch": B, "workers": workers, "params": nparams,
+        "value": B * K / elapsed, "unit": "samples/s", "ms_per_step": elapsed * 1e3 / K,
+        "instrumented_ms_per_step": elapsed_ev * 1e3 / K,
+        "kernels_per_step": sum(v["launches_per_step"] for v in kernels.values()),
+        "gemm": {"launches_per_step": g_n / K, "ms_per_step": g_ms / K,
+                 "flops_per_step": g_units / K,
+                 "achieved_tflops": g_units / (g_ms * 1e-3) / 1e12 if g_ms > 0 else None,
+                 "avg_launch_ms": g_ms / g_n if g_n else None},
+        "dominant": dominant(kernels),
+        "kernels": kernels,
+        "adam_alone": adam,
+        "h2d_step": {"value": B * K / elapsed_h, "unit": "samples/s", "ms_per_step": elapsed_h * 1e3 / K,
+                     "note": "gn_model_train_step from host buffers: H2D copy of x and y inside "
+                             "every step (never `value`)"},
+        "loss": loss.value,
+    }
+    if with_cpu:
+        res["cpu_baseline"] = cpu_baseline(cfg, x, y, cpu_budget, min(B, threads))
+    return res
+
+
+def predict_bench(args, dev):
     """Inference throughput (f3): K forward passes in inference mode over the
     config's batch, inputs and outputs in HBM."""
     import ctypes as C
+    from goneuron_amd import configs
     from goneuron_amd._lib import lib, check
-    out = C.c_void_p()
-    check(dev.h, lib().gn_malloc(dev.h, B * model.out_size * 4, C.byref(out)))
-    run = lambda: check(dev.h, lib().gn_model_predict_device(model.h, dx, B, out))
+    L = lib()
+    cfg = configs.CONFIGS[args.config]()
+    B = cfg["B"]
+    x, _ = configs.inputs(cfg)
+    model = configs.build(cfg, device=dev)
+    dx, out = C.c_void_p(), C.c_void_p()
+    check(dev.h, L.gn_malloc(dev.h, x.nbytes, C.byref(dx)))
+    check(dev.h, L.gn_memcpy_h2d(dev.h, dx, x.ctypes.data, x.nbytes))
+    check(dev.h, L.gn_malloc(dev.h, B * model.out_size * 4, C.byref(out)))
+    run = lambda: check(dev.h, L.gn_model_predict_device(model.h, dx, B, out))
     for _ in range(args.warmup):
         run()
     dev.sync()
@@ -133,11 +304,15 @@ def predict_bench(args, cfg, model, dev, dx, B, workers):
                       "ms_per_step": 1e3 * el / args.steps, "higher_is_better": True,
                       "dtype": "f32", "data": "synthetic",
                       "config": {"workload": cfg["name"], "batch": B, "mode": "inference"}}), flush=True)
-    check(dev.h, lib().gn_free(dev.h, out))
+    check(dev.h, L.gn_free(dev.h, dx))
+    check(dev.h, L.gn_free(dev.h, out))
+    model.Close()
 
 
-def copy_probe(mib):
-    """A copy kernel of known size: reads and writes mib MiB per launch."""
+def calibrate_copy(mib):
+    """A copy kernel of known size (reads and writes mib MiB per launch, 3
+    launches): the FETCH_SIZE / WRITE_SIZE counters of the traffic passes are
+    scaled by what they read for it."""
     import torch
     n = mib * (1 << 20) // 4
     a = torch.ones(n, device="cuda:0")
@@ -146,7 +321,7 @@ def copy_probe(mib):
     for _ in range(3):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_probe_bytes_per_launch": n * 4}), flush=True)
+    print(json.dumps({"copy_bytes_per_launch": n * 4}), flush=True)
 
 
 def main():
@@ -154,15 +329,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"])
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--cpu-threads", type=int, default=None,
-                    help="threads of the parallel CPU baseline (default min(B, cores, 16))")
+    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"],
+                    help="headline workload (the `value` of the line)")
+    ap.add_argument("--only", action="store_true", help="time the headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of CPU work per configuration's baseline")
     ap.add_argument("--predict", action="store_true",
                     help="time the inference path instead (Sequential.PredictBatch: forward in "
                          "inference mode on HBM-resident inputs, gn_model_predict_device)")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 3 times (the "
                          "calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -170,138 +346,63 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the data-parallel "
               "sharding across GPUs is a design (DESIGN.md), not built here.", file=sys.stderr)
         sys.exit(2)
-
-    if args.copy_probe:
-        copy_probe(args.copy_probe)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
         return
 
-    import ctypes as C
     import goneuron_amd as gn
     from goneuron_amd import configs
-    from goneuron_amd._lib import lib, check
-
-    cfg = configs.CONFIGS[args.config]()
-    B = cfg["B"]
     dev = gn.GetDefaultDevice()
-    x, y = configs.inputs(cfg)
-    workers = configs.gpu_workers(B)
-    model = configs.build(cfg, device=dev, workers=workers)
-
-    def dbuf(a):
-        p = C.c_void_p()
-        check(dev.h, lib().gn_malloc(dev.h, a.nbytes, C.byref(p)))
-        check(dev.h, lib().gn_memcpy_h2d(dev.h, p, a.ctypes.data, a.nbytes))
-        return p
-
-    dx, dy = dbuf(x), dbuf(y)
     if args.predict:
-        predict_bench(args, cfg, model, dev, dx, B, workers)
-        check(dev.h, lib().gn_free(dev.h, dx))
-        check(dev.h, lib().gn_free(dev.h, dy))
-        model.Close()
+        predict_bench(args, dev)
         return
-    step = lambda: check(dev.h, lib().gn_model_train_step_device(model.h, dx, dy, B))
-    for _ in range(args.warmup):
-        step()
-    dev.sync()
-    # timed region: K steps, no instrumentation -> value
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    dev.sync()
-    elapsed = time.perf_counter() - t0
-    # the same K steps again with a HIP event pair around every kernel launch
-    # on the library's stream -> per-class kernel time for the roofline
-    check(dev.h, lib().gn_timing_enable(dev.h, 1))
-    dev.sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    dev.sync()
-    elapsed_ev = time.perf_counter() - t0
-    res = {}
-
-    def report(classes):
-        for cls, name in classes:
-            n = C.c_int64()
-            ms = C.c_double()
-            check(dev.h, lib().gn_timing_report(dev.h, cls, C.byref(n), C.byref(ms)))
-            res[name] = (n.value, ms.value)
-
-    report(((0, "gemm"), (1, "adam_overlapped"), (2, "other")))
-    check(dev.h, lib().gn_timing_enable(dev.h, 0))
-    # Adam alone: in a train step each layer's update runs on a second stream
-    # while the backward pass continues; Network.Step's full-arena update
-    # (gn_model_step, one launch on the main stream) times the kernel by itself.
-    check(dev.h, lib().gn_timing_enable(dev.h, 1))
-    dev.sync()
-    for _ in range(args.steps):
-        check(dev.h, lib().gn_model_step(model.h))
-    dev.sync()
-    report(((1, "adam"),))
-    check(dev.h, lib().gn_timing_enable(dev.h, 0))
-    loss = C.c_float()
-    check(dev.h, lib().gn_model_read_loss(model.h, C.byref(loss)))
-
+    host = host_info()
+    threads = max(1, min(host["affinity"] or 1, CPU_SHARE))
+    head = run_config(args.config, args, dev, not args.no_cpu, args.cpu_budget, threads)
+    print(f"bench: {args.config} {head['value']:.0f} samples/s", file=sys.stderr, flush=True)
+    others = {}
+    if not args.only:
+        for name in ("mlp", "cnn", "wide", "gpt", "lstm"):
+            if name != args.config:
+                others[name] = run_config(name, args, dev, not args.no_cpu, args.cpu_budget, threads)
+                print(f"bench: {name} {others[name]['value']:.0f} samples/s", file=sys.stderr, flush=True)
+    cfg = configs.CONFIGS[args.config]()
     K = args.steps
-    samples_per_s = B * K / elapsed
-    ms_per_step = elapsed * 1e3 / K
-    flops = gemm_flops(cfg, B)
-    g_n, g_ms = res["gemm"]
-    a_n, a_ms = res["adam"]
-    gemm_tflops = flops * K / (g_ms * 1e-3) / 1e12 if g_ms > 0 else None
-    per_launch_flops = flops * K / g_n if g_n else None
-    adam_bytes = 28 * model.nparams  # per launch of the full-arena update
-    adam_gbps = adam_bytes * a_n / (a_ms * 1e-3) / 1e9 if a_ms > 0 else None
-    ao_n, ao_ms = res["adam_overlapped"]
-
+    g = head["gemm"]
+    traffic = gemm_traffic_per_launch() if args.config == "wide" else None
+    flops_per_launch = g["flops_per_step"] / g["launches_per_step"] if g["launches_per_step"] else None
     line = {
         "metric": "train samples/s (fwd+bwd+Adam) on 1 MI355X; % of fp32 MFMA / HBM roofline",
-        "value": samples_per_s,
+        "value": head["value"],
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (reference LCG, seeds 1000+cfg / 2000+cfg), reference LCG weight init",
-        "config": {"workload": cfg["name"], "batch": B, "workers": workers,
+        "config": {"workload": cfg["name"], "batch": head["batch"], "workers": head["workers"],
                    "layers": [d["kind"] + (f"{d['in']}->{d['out']}" if d["kind"] == "dense" else "")
                               for d in cfg["layers"]],
                    "loss": cfg["loss"], "optimizer": "Adam lr=1e-3"},
-        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": (gemm_tflops / PEAK_FP32_MFMA_TFLOPS) if gemm_tflops else None,
-                     "traffic": (GEMM_TRAFFIC_BYTES_PER_STEP[cfg["name"]] * K / g_n
-                                 if cfg["name"] in GEMM_TRAFFIC_BYTES_PER_STEP and g_n else None),
-                     "kernel": "gemm_f32_mfma (all instantiations)",
-                     "flops_per_launch": per_launch_flops,
-                     "avg_launch_ms": g_ms / g_n if g_n else None},
-        "kernels": {
-            "gemm": {"launches_per_step": g_n / K, "ms_per_step": g_ms / K},
-            "adam": {"launches": a_n, "ms_per_launch": a_ms / a_n if a_n else None,
-                     "bound": "hbm", "achieved_gbps": adam_gbps, "peak_gbps": PEAK_HBM_GBPS,
-                     "frac": adam_gbps / PEAK_HBM_GBPS if adam_gbps else None,
-                     "bytes_per_launch": adam_bytes,
-                     "measured": "full-arena update (gn_model_step) launched alone"},
-            "adam_in_step": {"launches_per_step": ao_n / K, "ms_per_step": ao_ms / K,
-                             "note": "per-layer updates on a second stream, overlapped with the "
-                                     "backward pass; durations include the sharing"},
-            "other": {"launches_per_step": res["other"][0] / K, "ms_per_step": res["other"][1] / K},
-            "instrumented_ms_per_step": elapsed_ev * 1e3 / K,
-        },
-        "loss": loss.value,
+        "roofline": {"bound": "mfma", "achieved": g["achieved_tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s",
+                     "frac": g["achieved_tflops"] / PEAK_FP32_MFMA_TFLOPS if g["achieved_tflops"] else None,
+                     "traffic": traffic,
+                     "kernel": "gemm_f32_mfma (all instantiations: gemm_fwd, gemm_dx, gemm_dw)",
+                     "flops_per_launch": flops_per_launch, "avg_launch_ms": g["avg_launch_ms"]},
+        "kernels": head["kernels"],
+        "adam_alone": head["adam_alone"],
+        "h2d_step": head["h2d_step"],
+        "instrumented_ms_per_step": head["instrumented_ms_per_step"],
+        "loss": head["loss"],
+        "host": dict(host, threads_used=min(head["batch"], threads)),
+        "cpu_baseline": head.get("cpu_baseline"),
+        "configs": others,
     }
-    # explicit, ordered teardown: input buffers, the model, then (atexit) the device
-    check(dev.h, lib().gn_free(dev.h, dx))
-    check(dev.h, lib().gn_free(dev.h, dy))
-    model.Close()
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, x, y, args.cpu_budget, workers, args.cpu_threads)
-    else:
-        line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
 
 

@@ -44,6 +44,11 @@ class AdamDesc(C.Structure):
     _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float)]
 
 
+class KernelStat(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("cls", C.c_int32), ("launches", C.c_int64), ("ms", C.c_double),
+                ("units", C.c_double)]
+
+
 class Info(C.Structure):
     _fields_ = [("arch", C.c_char * 64), ("cu_count", C.c_int32), ("hbm_bytes", C.c_int64),
                 ("peak_fp32_mfma_tflops", C.c_double), ("peak_hbm_gbps", C.c_double)]
@@ -115,6 +120,7 @@ SIGNATURES = {
     "gn_fill_class_ids": (C.c_int, [i32p, C.c_int64, C.c_int32, C.c_uint64]),
     "gn_timing_enable": (C.c_int, [vp, C.c_int]),
     "gn_timing_report": (C.c_int, [vp, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+    "gn_timing_kernels": (C.c_int, [vp, C.POINTER(KernelStat), C.c_int32, i32p]),
 }
 
 _lib = None

@@ -201,6 +201,12 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
                                 void *sync, int *err, unsigned *epoch, int B, int T, int H,
                                 int spin_limit, hipStream_t s);
 int lstm_gram_pitch(int n);
+// the two halves of launch_lstm_clip_weights: the chains' Gram matrices, then
+// the clip recursion over them into the per-step weights
+hipError_t launch_lstm_gram(const float *D, const float *hbuf, const float *x, double *gram, int B,
+                            int T, int I, int H, int W, hipStream_t s);
+hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
+                            hipStream_t s);
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
                                     double *coef, float *w, int B, int T, int I, int H, int W,
                                     hipStream_t s);
@@ -221,7 +227,7 @@ hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipSt
 hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N, int nmem,
                                   int64_t xstride, int64_t sstride, hipStream_t s);
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
-                         int rows, int N, hipStream_t s);
+                         int rows, int N, float eps, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
 // Rotary embedding of rows [rows, NH*hd] in place; position = row % T; cs/sn

@@ -49,7 +49,12 @@ struct gn_ctx {
   float *noalloc = nullptr;      // this device's copy of `scratch` (gn_dense_backward_noalloc)
   // kernel timing (gn_timing_enable)
   bool timing = false;
-  struct Rec { int cls; hipEvent_t a, b; };
+  struct Rec {
+    int cls;
+    const char *name;  // kernel (or fused launch group) name, static storage
+    double units;      // algorithmic bytes (memory-bound) or FLOPs (GEMM / MFMA) of the launch
+    hipEvent_t a, b;
+  };
   std::vector<Rec> recs;
   std::vector<hipEvent_t> pool;
   size_t pool_used = 0;
@@ -65,13 +70,18 @@ static hipEvent_t ev_get(gn_ctx *c) {
 }
 
 // Brackets the kernels launched in its scope with events when timing is on
-// (on the stream those kernels go to).
+// (on the stream those kernels go to), under a name with the launch's
+// algorithmic work: the bytes a memory-bound kernel must move (compulsory
+// reads and writes, fp32) or the FLOPs of a matrix-core kernel.
 struct KTimer {
   gn_ctx *c;
   int cls;
+  const char *name;
+  double units;
   hipStream_t st;
   hipEvent_t a = nullptr, b = nullptr;
-  KTimer(gn_ctx *c_, int cls_, hipStream_t st_ = nullptr) : c(c_), cls(cls_), st(st_ ? st_ : c_->stream) {
+  KTimer(gn_ctx *c_, int cls_, const char *name_, double units_, hipStream_t st_ = nullptr)
+      : c(c_), cls(cls_), name(name_), units(units_), st(st_ ? st_ : c_->stream) {
     if (c->timing) {
       a = ev_get(c);
       b = ev_get(c);
@@ -82,10 +92,27 @@ struct KTimer {
   ~KTimer() {
     if (a) {
       (void)hipEventRecord(b, st);
-      c->recs.push_back({cls, a, b});
+      c->recs.push_back({cls, name, units, a, b});
     }
   }
 };
+
+static double gemm_flops(const GemmArgs &g) {
+  return 2.0 * g.M * g.N * g.K * (g.nbatch > 1 ? g.nbatch : 1);
+}
+static double f4(double n) { return 4.0 * n; }  // bytes of n floats
+// attention FLOPs per launch: the score and value products over the (query,
+// key) pairs the mask keeps, 2 products forward, 4 backward (dP, dQ, dK, dV)
+static double attn_flops(int B, int T, int NH, int hd, int causal, bool bwd) {
+  const double pairs = causal ? 0.5 * T * (T + 1.0) : (double)T * T;
+  return (bwd ? 8.0 : 4.0) * hd * pairs * B * NH;
+}
+// per-sample token sums: read B x T x N, write B x N
+static double token_sum_bytes(int B, int T, int N) { return f4((double)B * T * N + (double)B * N); }
+// direct convolution work: 2 FLOPs per tap of every output
+static double conv_flops(const ConvShape &cs, int B) {
+  return 2.0 * B * cs.outC * cs.oH * cs.oW * cs.inC * cs.k * cs.k;
+}
 
 static int set_err(gn_ctx *c, int code, const char *fmt, ...) {
   if (c) {
@@ -282,6 +309,34 @@ extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *t
   return GN_OK;
 }
 
+// Per-name totals of the timed launches since the last gn_timing_enable, in
+// first-seen order: up to cap entries into out, the count into *n.
+extern "C" int gn_timing_kernels(gn_ctx *c, gn_kernel_stat *out, int32_t cap, int32_t *n) {
+  ENTRY(c);
+  if (!n || (cap > 0 && !out)) return set_err(c, GN_ERR_INVALID, "bad timing_kernels args");
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->aux));
+  std::vector<gn_kernel_stat> acc;
+  for (const auto &r : c->recs) {
+    float t = 0;
+    HIP_OK(c, hipEventElapsedTime(&t, r.a, r.b));
+    size_t k = 0;
+    while (k < acc.size() && (acc[k].cls != r.cls || strcmp(acc[k].name, r.name) != 0)) ++k;
+    if (k == acc.size()) {
+      gn_kernel_stat z{};
+      snprintf(z.name, sizeof z.name, "%s", r.name ? r.name : "?");
+      z.cls = r.cls;
+      acc.push_back(z);
+    }
+    acc[k].launches += 1;
+    acc[k].ms += t;
+    acc[k].units += r.units;
+  }
+  *n = (int32_t)acc.size();
+  for (int32_t i = 0; i < cap && i < (int32_t)acc.size(); ++i) out[i] = acc[i];
+  return GN_OK;
+}
+
 extern "C" int gn_malloc(gn_ctx *c, size_t bytes, void **dptr) {
   ENTRY(c);
   if (!dptr) return set_err(c, GN_ERR_INVALID, "dptr is null");
@@ -371,7 +426,7 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
   a.C = out; a.ldc = out_n;
   a.bias = b; a.act = fwd; a.alpha = 1.f;
   a.ws = c->scratch; a.ws_cap = c->scratch_floats;
-  KTimer kt(c, GN_KCLASS_GEMM);
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
   return launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream);
 }
 
@@ -403,7 +458,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
     wcap = c->scratch_floats;
   }
   if (gB) {
-    KTimer kt(c, GN_KCLASS_OTHER, ws);
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * out_n + out_n), ws);
     e = launch_colsum(dz, B, out_n, out_n, scale, gB, wscr, wcap, ws);
     if (e != hipSuccess) return e;
   }
@@ -415,7 +470,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
   a.alpha = scale;
   a.ws = wscr; a.ws_cap = wcap;
   {
-    KTimer kt(c, GN_KCLASS_GEMM, ws);
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a), ws);
     e = launch_gemm('T', 'N', EPI_SCALE, a, ws);
   }
   if (e != hipSuccess) return e;
@@ -427,7 +482,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
     d.C = gin; d.ldc = in;
     d.alpha = 1.f;
     d.ws = ms; d.ws_cap = ms_cap;
-    KTimer kt(c, GN_KCLASS_GEMM);
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
     if (gin_aux) {
       d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv;
       e = launch_gemm('N', 'N', EPI_DACT, d, c->stream);
@@ -1410,7 +1465,7 @@ static hipError_t gemm_nt(gn_ctx *c, const float *A, const float *Bw, const floa
   a.C = C; a.ldc = N; a.alpha = 1.f; a.bias = bias; a.act = act;
   a.aux = aux; a.ldaux = N;
   a.ws = c->scratch; a.ws_cap = c->scratch_floats;
-  KTimer kt(c, GN_KCLASS_GEMM);
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
   return launch_gemm('N', 'T', epi, a, c->stream);
 }
 
@@ -1423,7 +1478,7 @@ static hipError_t gemm_nn(gn_ctx *c, const float *A, const float *Wm, float *C, 
   a.C = C; a.ldc = N; a.alpha = 1.f; a.act = act;
   a.aux = aux; a.ldaux = N; a.aux_div = aux_div;
   a.ws = c->scratch; a.ws_cap = c->scratch_floats;
-  KTimer kt(c, GN_KCLASS_GEMM);
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
   return launch_gemm('N', 'N', epi, a, c->stream);
 }
 
@@ -1438,7 +1493,7 @@ static hipError_t gemm_dw_last(gn_ctx *c, const float *S, const float *X, float 
   a.B = X + (int64_t)(T - 1) * N; a.ldb = T * N;
   a.C = dW; a.ldc = N; a.alpha = scale;
   a.ws = c->scratch; a.ws_cap = c->scratch_floats;
-  KTimer kt(c, GN_KCLASS_GEMM);
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
   return launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
 }
 
@@ -1447,9 +1502,11 @@ static hipError_t gemm_dw_last(gn_ctx *c, const float *S, const float *X, float 
 static hipError_t tb_norm_fwd(gn_ctx *c, const LayerRT &R, const float *P, const TbOff &o, int k,
                               const float *x, float *y, float *st, int rows) {
   const float *g = P + (k == 0 ? o.g1 : o.g2), *be = P + (k == 0 ? o.be1 : o.be2);
-  KTimer kt(c, GN_KCLASS_OTHER);
-  if (R.d.block_norm == GN_BLOCK_NORM_RMS) return launch_rms_fwd(x, g, y, st, rows, R.D, 1e-5f, c->stream);
-  return launch_ln_fwd(x, g, be, y, st, rows, R.D, c->stream);
+  const bool rms = R.d.block_norm == GN_BLOCK_NORM_RMS;
+  // read x, write y and the per-row statistics
+  KTimer kt(c, GN_KCLASS_OTHER, rms ? "rms_fwd" : "ln_fwd", f4(2.0 * rows * R.D + (rms ? 1 : 2) * rows));
+  if (rms) return launch_rms_fwd(x, g, y, st, rows, R.D, 1e-5f, c->stream);
+  return launch_ln_fwd(x, g, be, y, st, rows, R.D, 1e-5f, c->stream);
 }
 
 // Block norm backward: dx into dx, gamma (and LayerNorm beta) gradients.
@@ -1459,19 +1516,24 @@ static hipError_t tb_norm_bwd(gn_ctx *c, const LayerRT &R, const float *P, float
   const int D = R.D;
   const int64_t og = k == 0 ? o.g1 : o.g2, ob = k == 0 ? o.be1 : o.be2;
   LayerRT::Tb &t = const_cast<LayerRT &>(R).tb;
-  KTimer kt(c, GN_KCLASS_OTHER);
+  const bool rms = R.d.block_norm == GN_BLOCK_NORM_RMS;
   hipError_t e;
-  if (R.d.block_norm == GN_BLOCK_NORM_RMS) {
-    e = launch_rms_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
-  } else {
-    e = launch_ln_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
+  {
+    // read g, x and the statistics, write dx and g * xhat
+    KTimer kt(c, GN_KCLASS_OTHER, rms ? "rms_bwd" : "ln_bwd", f4(4.0 * rows * D + (rms ? 1 : 2) * rows));
+    if (rms) {
+      e = launch_rms_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
+    } else {
+      e = launch_ln_bwd(g, x, P + og, st, dx, t.GX, rows, D, c->stream);
+    }
   }
   if (e != hipSuccess) return e;
   // gamma (and for LayerNorm beta) gradients in one launch pair
   const float *src[2] = {t.GX, g};
   float *dst[2] = {G + og, G + ob};
-  return launch_colsum_multi(src, dst, R.d.block_norm == GN_BLOCK_NORM_RMS ? 1 : 2, rows, D, D,
-                             scale, c->scratch, c->scratch_floats, c->stream);
+  const int nm = rms ? 1 : 2;
+  KTimer kt(c, GN_KCLASS_OTHER, "colsum", nm * f4((double)rows * D + D));
+  return launch_colsum_multi(src, dst, nm, rows, D, D, scale, c->scratch, c->scratch_floats, c->stream);
 }
 
 static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
@@ -1493,15 +1555,16 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
     a.bstride_B = o.wk - o.wq;
     a.bstride_bias = o.bk - o.bq;
     a.bstride_C = t.K - t.Q;
-    KTimer kt(c, GN_KCLASS_GEMM);
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
     HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream));
   }
+  if (R.d.use_rope) {  // transformer.go:457-461; the backward reads the rotated Q, K too
+    KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
+    HIP_OK(c, launch_rope(t.Q, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
+    HIP_OK(c, launch_rope(t.K, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
+  }
   {
-    KTimer kt(c, GN_KCLASS_OTHER);
-    if (R.d.use_rope) {  // transformer.go:457-461; the backward reads the rotated Q, K too
-      HIP_OK(c, launch_rope(t.Q, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
-      HIP_OK(c, launch_rope(t.K, t.rcos, t.rsin, rows, R.T, R.NH, D / R.NH, 0, c->stream));
-    }
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, R.T, R.NH, D / R.NH, R.causal, false));
     HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, c->stream));
   }
   // res1 = x + wOut(o): the residual add rides in the GEMM epilogue
@@ -1511,7 +1574,7 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
     // Z = [gate | up] for every token (one GEMM against [W | V]), MID = swish(gate) * up
     HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, nullptr, t.Z, rows, 2 * FF, D, EPI_BIAS_ACT, F_IDENTITY,
                       nullptr));
-    KTimer kt(c, GN_KCLASS_OTHER);
+    KTimer kt(c, GN_KCLASS_OTHER, "swiglu_fwd", f4(3.0 * rows * FF));
     HIP_OK(c, launch_swiglu_fwd(t.Z, t.MID, rows, FF, c->stream));
   } else {
     // ReLU, or GELU as a value activation: identity forward (ActTypeNone)
@@ -1535,10 +1598,13 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   // norm 2 (LayerNorm: Q18 formula; RMSNorm: Q19), gamma / beta column sums
   HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 1, R.gout, t.RES2, t.st2, t.G1, rows, scale));
   {
-    KTimer kt(c, GN_KCLASS_OTHER);
     // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
     // per-sample token sums S that the Q10 weight gradient needs anyway
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
     HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.b2, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.MID, G + o.w2, B, T, D, FF, scale));
@@ -1554,11 +1620,11 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     a.C = t.MG; a.ldc = FF; a.alpha = 1.f;
     a.ws = cs; a.ws_cap = cap;
     {
-      KTimer kt(c, GN_KCLASS_GEMM);
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
       HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
     }
     {
-      KTimer kt(c, GN_KCLASS_OTHER);
+      KTimer kt(c, GN_KCLASS_OTHER, "swiglu_bwd", f4(5.0 * B * FF));
       HIP_OK(c, launch_swiglu_bwd(t.MG, t.Z + (int64_t)(T - 1) * 2 * FF, T * 2 * FF, t.DZS, B, FF,
                                   c->stream));
     }
@@ -1570,7 +1636,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     w.C = G + o.w1; w.ldc = D; w.alpha = scale;
     w.ws = cs; w.ws_cap = cap;
     {
-      KTimer kt(c, GN_KCLASS_GEMM);
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(w));
       HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, w, c->stream));
     }
     // combined = dRES2, plus dZ [W; V] on each sample's token 0
@@ -1583,7 +1649,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     d.C = t.COMB; d.ldc = T * D; d.alpha = 1.f;
     d.aux = t.G1; d.ldaux = T * D;
     d.ws = cs; d.ws_cap = cap;
-    KTimer kt(c, GN_KCLASS_GEMM);
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
     HIP_OK(c, launch_gemm('N', 'N', EPI_BIAS_ADD, d, c->stream));
   } else {
     // ff1: dz1 = (dz2 W2) * act'(last token's pre-activation) (Q10); ReLU from
@@ -1591,8 +1657,11 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     const int dk = R.d.block_act == GN_BLOCK_ACT_GELU ? D_GELU : D_RELU;
     HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, dk, t.MID, T));
     {
-      KTimer kt(c, GN_KCLASS_OTHER);
+      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF));
       HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
+    }
+    {
+      KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * FF + FF));
       HIP_OK(c, launch_colsum(t.S, B, FF, FF, scale, G + o.b1, cs, cap, c->stream));
     }
     HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
@@ -1602,31 +1671,38 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   // norm 1
   HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));
   {
-    KTimer kt(c, GN_KCLASS_OTHER);
     // wOut (Linear): dz = dRES1
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
     HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.bo, cs, cap, c->stream));
   }
   HIP_OK(c, gemm_dw_last(c, t.S, t.O, G + o.wo, B, T, D, D, scale));
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
   {
-    KTimer kt(c, GN_KCLASS_OTHER);
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, R.NH, D / R.NH, R.causal, true));
     HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
                               c->stream));
-    if (R.d.use_rope) {  // transformer.go:660-664: conjugate rotation before wQ/wK
-      HIP_OK(c, launch_rope(t.GQ, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
-      HIP_OK(c, launch_rope(t.GK, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
-    }
+  }
+  if (R.d.use_rope) {  // transformer.go:660-664: conjugate rotation before wQ/wK
+    KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
+    HIP_OK(c, launch_rope(t.GQ, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
+    HIP_OK(c, launch_rope(t.GK, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
   }
   const int64_t bo[3] = {o.bq, o.bk, o.bv};
   const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
   {
-    KTimer kt(c, GN_KCLASS_OTHER);
     // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch,
     // blockIdx.z picking the member, B samples each
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, c->stream));
+  }
+  {
     const float *src[3] = {t.S3, t.S3 + sst, t.S3 + 2 * sst};
     float *dst[3] = {G + bo[0], G + bo[1], G + bo[2]};
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", 3 * f4((double)B * D + D));
     HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
   }
   {
@@ -1641,7 +1717,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     a.nbatch = 3;
     a.bstride_A = sst;
     a.bstride_C = o.wk - o.wq;
-    KTimer kt(c, GN_KCLASS_GEMM);
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
     HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
@@ -1673,9 +1749,10 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         break;
       }
       case GN_LAYER_DROPOUT:
-        if (M->eff[i])
+        if (M->eff[i]) {
+          KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * R.out_len + R.out_len));
           HIP_OK(c, launch_dropout(cur, R.mask, R.scale, R.out, B, R.out_len, c->stream));
-        else
+        } else
           HIP_OK(c, hipMemcpyAsync(R.out, cur, (size_t)B * R.out_len * sizeof(float),
                                    hipMemcpyDeviceToDevice, c->stream));
         break;
@@ -1685,33 +1762,33 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_CONV2D: {
         const float *W = M->params + R.poff;
         const float *b = W + (int64_t)R.cs.outC * R.cs.inC * R.cs.k * R.cs.k;
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "conv_fwd", conv_flops(R.cs, B));
         HIP_OK(c, launch_conv_fwd(cur, W, b, R.out, R.cs, B, R.cfwd, c->stream));
         break;
       }
-      case GN_LAYER_MAXPOOL2D: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+      case GN_LAYER_MAXPOOL2D: {  // read the input, write outputs and int32 switches
+        KTimer kt(c, GN_KCLASS_OTHER, "maxpool_fwd", f4((double)B * R.in_len + 2.0 * B * R.out_len));
         HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
         break;
       }
       case GN_LAYER_AVGPOOL2D: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "avgpool_fwd", f4((double)B * R.in_len + (double)B * R.out_len));
         HIP_OK(c, launch_avgpool_fwd(cur, R.out, R.ps, B, c->stream));
         break;
       }
-      case GN_LAYER_EMBEDDING: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+      case GN_LAYER_EMBEDDING: {  // read the ids and their rows, write rows and int32 ids
+        KTimer kt(c, GN_KCLASS_OTHER, "embed_fwd", f4(2.0 * B * R.T + 2.0 * B * R.T * R.D));
         HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B, R.T, R.V, R.D, R.bad,
                                c->stream));
         break;
       }
       case GN_LAYER_POSENC: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "pe_add", f4(2.0 * B * R.T * R.D + (double)R.T * R.D));
         HIP_OK(c, launch_pe_add(cur, M->params + R.poff, R.out, B, R.T * R.D, c->stream));
         break;
       }
       case GN_LAYER_CLSPOOL: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "cls_fwd", f4(2.0 * B * R.D));
         HIP_OK(c, launch_cls_fwd(cur, R.out, B, R.T * R.D, R.D, c->stream));
         break;
       }
@@ -1723,7 +1800,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_SWIGLU: {
         const int out2 = 2 * R.d.out_size;
         {
-          KTimer kt(c, GN_KCLASS_GEMM);
+          KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", 2.0 * B * out2 * R.d.in_size);
           GemmArgs g{};  // Z[b] = [W x_b | V x_b]
           g.M = B; g.N = out2; g.K = R.d.in_size;
           g.A = cur; g.lda = R.d.in_size;
@@ -1732,7 +1809,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
           g.ws = c->scratch; g.ws_cap = c->scratch_floats;
           HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
         }
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "swiglu_fwd", f4(3.0 * B * R.d.out_size));
         HIP_OK(c, launch_swiglu_fwd(R.zbuf, R.out, B, R.d.out_size, c->stream));
         break;
       }
@@ -1748,7 +1825,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         if (M->workers > 1) rt.chunk = (B + W - 1) / W;  // trainBatchParallel chunks
         for (int k = 0; k < 65; ++k) rt.base[k] = R.mrng[k];
         {
-          KTimer kt(c, GN_KCLASS_OTHER);
+          KTimer kt(c, GN_KCLASS_OTHER, "moe_route", f4(2.0 * B * E + (double)B * K));
           HIP_OK(c, launch_moe_route(R.mlog, R.mprob, R.mact, rt, c->stream));
         }
         for (int e = 0; e < E; ++e) {  // every expert on every sample; the route picks k of them
@@ -1756,7 +1833,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
           HIP_OK(c, gemm_nt(c, cur, We, We + (int64_t)O * I, R.meout + (int64_t)e * B * O, B, O, I,
                             EPI_BIAS_ACT, F_LEAKY, nullptr));
         }
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "moe_combine", f4((double)K * B * O + (double)B * O));
         HIP_OK(c, launch_moe_combine(R.meout, R.mprob, R.mact, R.out, B, O, E, K, c->stream));
         if (M->eff[i]) {  // E draws per sample on its stream
           if (M->workers > 1) {
@@ -1776,7 +1853,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         const float *Wh = Wx + (int64_t)G3 * R.I;
         const float *bias = Wh + (int64_t)2 * H * H;
         {
-          KTimer kt(c, GN_KCLASS_GEMM);
+          KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", 2.0 * B * R.T * G3 * R.I);
           GemmArgs g{};  // xw[b*T + t] = b + Wx x_t (gru.go:194-210)
           g.M = B * R.T; g.N = G3; g.K = R.I;
           g.A = cur; g.lda = R.I;
@@ -1786,19 +1863,23 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
           g.ws = c->scratch; g.ws_cap = c->scratch_floats;
           HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, g, c->stream));
         }
-        KTimer kt(c, GN_KCLASS_OTHER);
-        HIP_OK(c, launch_transpose(Wh, R.WhT, 2 * H, H, c->stream));
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "transpose", f4(4.0 * H * H));
+          HIP_OK(c, launch_transpose(Wh, R.WhT, 2 * H, H, c->stream));
+        }
+        // recurrence: the hidden-state products 2 x 3H x H per sample and step
+        KTimer kt(c, GN_KCLASS_OTHER, "gru_fwd", 2.0 * 3 * H * H * B * R.T);
         HIP_OK(c, launch_gru_fwd(R.xw, R.WhT, R.gpre, R.ghprev, R.grh, R.out, B, R.T, H, c->stream));
         break;
       }
       case GN_LAYER_BATCHNORM2D: {  // running stats advance in training mode only
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "bn_fwd", f4(2.0 * B * R.in_len + 3.0 * B * R.C));
         HIP_OK(c, launch_bn_fwd(cur, R.pcount ? M->params + R.poff : nullptr, R.out, R.bnst, R.rmean,
                                 R.rvar, B, R.C, R.HW, R.eps, R.d.momentum, M->eff[i], c->stream));
         break;
       }
       case GN_LAYER_RMSNORM: {
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "rms_fwd", f4(2.0 * B * R.in_len + (double)B * (R.in_len / R.D)));
         HIP_OK(c, launch_rms_fwd(cur, M->params + R.poff, R.out, R.rmsv, B * (R.in_len / R.D), R.D,
                                  R.eps, c->stream));
         break;
@@ -1808,7 +1889,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         const float *Wh = Wx + (int64_t)4 * R.H * R.I;
         const float *bias = Wh + (int64_t)4 * R.H * R.H;
         {
-          KTimer kt(c, GN_KCLASS_GEMM);
+          KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", 2.0 * B * R.T * R.H * R.I);
           GemmArgs g{};  // xw[b*T + t][i] = x[b, t, :] . Wx[i, :] (input-gate rows, Q13)
           g.M = B * R.T; g.N = R.H; g.K = R.I;
           g.A = cur; g.lda = R.I;
@@ -1817,8 +1898,12 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
           g.ws = c->scratch; g.ws_cap = c->scratch_floats;
           HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
         }
-        KTimer kt(c, GN_KCLASS_OTHER);
-        HIP_OK(c, launch_transpose(Wh, R.WhT, R.H, R.H, c->stream));
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "transpose", f4(2.0 * R.H * R.H));
+          HIP_OK(c, launch_transpose(Wh, R.WhT, R.H, R.H, c->stream));
+        }
+        // recurrence: Q13 leaves only the input gate with Wh h, 2 x H x H per sample and step
+        KTimer kt(c, GN_KCLASS_OTHER, "lstm_fwd", 2.0 * R.H * R.H * B * R.T);
         HIP_OK(c, launch_lstm_fwd(R.xw, R.WhT, bias, R.igb, R.tcb, R.cbuf, R.hbuf, R.out, B, R.T,
                                   R.H, c->stream));
         break;
@@ -1864,7 +1949,10 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         float *gW = M->grads + R.poff;
         float *gB = gW + (int64_t)R.d.in_size * R.d.out_size;
         float *dz = R.gout;
-        if (!is_dz) HIP_OK(c, launch_dact(R.gout, R.out, dz, (int64_t)B * R.out_len, R.ap.deriv, c->stream));
+        if (!is_dz) {  // read the gradient and the saved output, write dz
+          KTimer kt(c, GN_KCLASS_OTHER, "dact", f4(3.0 * B * R.out_len));
+          HIP_OK(c, launch_dact(R.gout, R.out, dz, (int64_t)B * R.out_len, R.ap.deriv, c->stream));
+        }
         float *gin = nullptr;
         const float *aux = nullptr;
         int deriv = 0;
@@ -1890,9 +1978,10 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         // unchanged (dropout.go:241-247)
         if (below && below->d.kind == GN_LAYER_FLATTEN)
           return set_err(c, GN_ERR_UNSUPPORTED, "Flatten below Dropout");
-        if (below && M->eff[i])
+        if (below && M->eff[i]) {
+          KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * R.out_len + R.out_len));
           HIP_OK(c, launch_dropout(R.gout, R.mask, R.scale, below->gout, B, R.out_len, c->stream));
-        else if (below)
+        } else if (below)
           HIP_OK(c, hipMemcpyAsync(below->gout, R.gout, (size_t)B * R.out_len * sizeof(float),
                                    hipMemcpyDeviceToDevice, c->stream));
         is_dz = false;
@@ -1901,15 +1990,15 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_FLATTEN:
         break;  // gout aliased by the layer above
       case GN_LAYER_MAXPOOL2D:
-        if (below && below->gout) {
-          KTimer kt(c, GN_KCLASS_OTHER);
+        if (below && below->gout) {  // read gradients and switches, write the input gradient
+          KTimer kt(c, GN_KCLASS_OTHER, "maxpool_bwd", f4(2.0 * B * R.out_len + (double)B * R.in_len));
           HIP_OK(c, launch_maxpool_bwd(R.gout, R.argmax, below->gout, R.ps, B, c->stream));
         }
         is_dz = false;
         break;
       case GN_LAYER_AVGPOOL2D:  // avgpool2d.go:401-474
         if (below && below->gout) {
-          KTimer kt(c, GN_KCLASS_OTHER);
+          KTimer kt(c, GN_KCLASS_OTHER, "avgpool_bwd", f4((double)B * R.out_len + (double)B * R.in_len));
           HIP_OK(c, launch_avgpool_bwd(R.gout, below->gout, R.ps, B, c->stream));
         }
         is_dz = false;
@@ -1919,17 +2008,22 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         // is applied to gout here, so it never receives a fused dz.
         if (is_dz && i != n - 1) return set_err(c, GN_ERR_UNSUPPORTED, "fused dz into Conv2D");
         const float *W = M->params + R.poff;
-        KTimer kt(c, GN_KCLASS_OTHER);
-        HIP_OK(c, launch_conv_wgrad(in, R.gout, R.out, M->grads + R.poff, R.cs, B, R.cderiv, scale,
-                                    c->scratch, c->scratch_floats, c->stream));
-        if (below && below->gout)
+        {  // dW and db: the taps plus the all-ones column
+          KTimer kt(c, GN_KCLASS_OTHER, "conv_wgrad",
+                    conv_flops(R.cs, B) + 2.0 * B * R.cs.outC * R.cs.oH * R.cs.oW);
+          HIP_OK(c, launch_conv_wgrad(in, R.gout, R.out, M->grads + R.poff, R.cs, B, R.cderiv, scale,
+                                      c->scratch, c->scratch_floats, c->stream));
+        }
+        if (below && below->gout) {
+          KTimer kt(c, GN_KCLASS_OTHER, "conv_dgrad", conv_flops(R.cs, B));
           HIP_OK(c, launch_conv_dgrad(R.gout, R.out, W, below->gout, R.cs, B, R.cderiv, c->stream));
+        }
         is_dz = false;
         break;
       }
       case GN_LAYER_CLSPOOL:
         if (below && below->gout) {  // transformer.go:1714-1723: row 0 gets g, the rest 0
-          KTimer kt(c, GN_KCLASS_OTHER);
+          KTimer kt(c, GN_KCLASS_OTHER, "cls_bwd", f4((double)B * R.D + (double)B * R.T * R.D));
           HIP_OK(c, launch_cls_bwd(R.gout, below->gout, B, R.T * R.D, R.D, c->stream));
         }
         is_dz = false;
@@ -1942,7 +2036,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       }
       case GN_LAYER_SWIGLU: {  // swiglu.go:196-232
         {
-          KTimer kt(c, GN_KCLASS_OTHER);
+          KTimer kt(c, GN_KCLASS_OTHER, "swiglu_bwd", f4(5.0 * B * R.d.out_size));
           HIP_OK(c, launch_swiglu_bwd(R.gout, R.zbuf, 2 * R.d.out_size, R.dzbuf, B, R.d.out_size,
                                       c->stream));
         }
@@ -1969,7 +2063,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         float *G = M->grads + R.poff;
         const int64_t e1 = (int64_t)O * I + O;
         {
-          KTimer kt(c, GN_KCLASS_OTHER);
+          KTimer kt(c, GN_KCLASS_OTHER, "moe_deltas", f4(2.0 * K * B * O + 3.0 * B * E));
           HIP_OK(c, launch_moe_backward_deltas(R.gout, R.meout, R.mprob, R.mact, R.medz, R.mdzg, B, O, E,
                                                K, M->eff[i], c->stream));
         }
@@ -1996,13 +2090,20 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const float *Wx = M->params + R.poff;
         const float *Wh = Wx + (int64_t)G3 * I;
         float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G3 * I, *gb = gWh + (int64_t)2 * H * H;
-        {
-          KTimer kt(c, GN_KCLASS_OTHER);
+        {  // the recursion: Wh products 2 x 2H x H per sample and step
+          KTimer kt(c, GN_KCLASS_OTHER, "gru_bwd", 2.0 * 2 * H * H * B * T);
           HIP_OK(c, launch_gru_bwd(R.gout, R.gpre, R.ghprev, Wh, R.Dg, B, T, H, c->stream));
+        }
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, G3));
           HIP_OK(c, launch_token_sum(R.Dg, R.S, B, T, G3, c->stream));
+        }
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * G3 + G3));
           HIP_OK(c, launch_colsum(R.S, B, G3, G3, scale, gb, c->scratch, c->scratch_floats, c->stream));
         }
-        KTimer kt(c, GN_KCLASS_GEMM);
+        KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw",
+                  2.0 * G3 * I * B + 2 * 2.0 * H * H * B * T);
         GemmArgs a{};  // dWx = scale * (sum_t dG)^T x_last (inputBuf holds the last step's input)
         a.M = G3; a.N = I; a.K = B;
         a.A = R.S; a.lda = G3;
@@ -2028,7 +2129,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_BATCHNORM2D: {  // batchnorm2d.go:611-660
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "bn_bwd", f4(3.0 * B * R.in_len + 2.0 * B * R.C));
         const float *gb = R.pcount ? M->params + R.poff : nullptr;
         if (!M->eff[i]) {  // inference-mode backward (batchnorm2d.go:525-551): no parameter gradient
           if (R.pcount) HIP_OK(c, launch_fill(M->grads + R.poff, 0.0f, R.pcount, c->stream));
@@ -2050,7 +2151,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_RMSNORM: {  // rmsnorm.go:301-329: dx, then gamma += g * (x / rms)
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "rms_bwd", f4(5.0 * B * R.in_len));
         const int rows = B * (R.in_len / R.D);
         HIP_OK(c, launch_rms_bwd(R.gout, in, M->params + R.poff, R.rmsv, below ? below->gout : nullptr,
                                  R.gx, rows, R.D, c->stream));
@@ -2060,14 +2161,17 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_POSENC: {  // gradW += g (transformer.go:112-118), summed over samples
-        KTimer kt(c, GN_KCLASS_OTHER);
+        KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * R.T * R.D + (double)R.T * R.D));
         HIP_OK(c, launch_colsum(R.gout, B, R.T * R.D, R.T * R.D, scale, M->grads + R.poff,
                                 c->scratch, c->scratch_floats, c->stream));
         is_dz = false;
         break;
       }
       case GN_LAYER_EMBEDDING: {  // Q12: last sample of each worker chunk only
-        KTimer kt(c, GN_KCLASS_OTHER);
+        // fill of the gradient table, then the contributing rows (one sample per chunk)
+        const int Wc = std::max(1, std::min(M->workers, B));
+        const int nch = (B + (B + Wc - 1) / Wc - 1) / ((B + Wc - 1) / Wc);
+        KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)R.V * R.D + 2.0 * nch * R.T * R.D));
         HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
                                     scale, R.bad, c->stream));
         break;
@@ -2078,8 +2182,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const float *Wh = Wx + (int64_t)G4 * I;
         const float *bias = Wh + (int64_t)G4 * H;
         float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
-        {
-          KTimer kt(c, GN_KCLASS_OTHER);
+        {  // BPTT: Wh^T dG, 2 x 4H x H per sample and step
+          KTimer kt(c, GN_KCLASS_OTHER, "lstm_bptt", 2.0 * G4 * H * B * T);
           bool done = false;
           if (R.lcoop && lstm_coop_eligible(B, H)) {
             const hipError_t e = launch_lstm_bwd_coop(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg,
@@ -2094,12 +2198,27 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           }
           if (!done)
             HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
-          HIP_OK(c, launch_lstm_clip_weights(R.Dg, R.hbuf, in, R.gram, R.coef, R.wts, B, T, I, H,
-                                             M->workers, c->stream));
+        }
+        // the clip chains: n = chunk x T steps each
+        const int Wc = std::max(1, std::min(M->workers, B)), chunk = (B + Wc - 1) / Wc;
+        const double nst = (double)chunk * T, nchain = (double)((B + chunk - 1) / chunk);
+        {  // Gram of the steps' contributions: n(n+1)/2 pairs, 2 (4H + H + I) FLOPs each, fp64
+          KTimer kt(c, GN_KCLASS_OTHER, "lstm_gram", nchain * nst * (nst + 1) * (5.0 * H + I));
+          HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream));
+        }
+        {  // the clip recursion reads each chain's Gram once
+          KTimer kt(c, GN_KCLASS_OTHER, "lstm_clip", nchain * 8.0 * nst * (nst + 1) / 2);
+          HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->stream));
+        }
+        {  // dG scaled in place by the step weights, plus the per-sample sums
+          KTimer kt(c, GN_KCLASS_OTHER, "lstm_weight", f4(2.0 * B * (T + 1) * G4 + (double)B * G4));
           HIP_OK(c, launch_lstm_weight(R.Dg, R.wts, R.S, B, T, H, c->stream));
+        }
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * G4 + G4));
           HIP_OK(c, launch_colsum(R.S, B, G4, G4, scale, gb, c->scratch, c->scratch_floats, c->stream));
         }
-        KTimer kt(c, GN_KCLASS_GEMM);
+        KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", 2.0 * G4 * I * B + 2.0 * G4 * H * B * (T + 1));
         GemmArgs a{};  // dWx = scale * S^T x_last
         a.M = G4; a.N = I; a.K = B;
         a.A = R.S; a.lda = G4;
@@ -2129,7 +2248,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       bool last = true;
       for (int j = 0; j < i; ++j)
         if (M->L[j].pcount > 0) last = false;
-      KTimer kt(c, GN_KCLASS_ADAM, c->aux);
+      KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, c->aux);
       HIP_OK(c, launch_adam(M->params + R.poff, M->grads + R.poff, M->m + R.poff, M->v + R.poff,
                             R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps,
                             c->aux, last ? 16384 : 256));
@@ -2155,9 +2274,15 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   LayerRT &O = M->L.back();
   int row_act = O.ap.row_act;
   const int32_t *bad = M->L[0].d.kind == GN_LAYER_EMBEDDING ? M->L[0].bad : nullptr;
-  HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
-                            O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
-  HIP_OK(c, launch_loss_mean(M->loss_rows, B, M->workers, M->loss_dev, c->stream));
+  {  // read z and y, write the activation output and dz, one loss per row
+    KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * O.out_len + B));
+    HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
+                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "loss_mean", f4((double)B + 1));
+    HIP_OK(c, launch_loss_mean(M->loss_rows, B, M->workers, M->loss_dev, c->stream));
+  }
   // grads *= 1/B: float32 reciprocal (net.go:767-770), float32(1/float64(B))
   // for the W-worker path (net.go:703-706).
   const float scale = M->workers > 1 ? (float)(1.0 / (double)B) : 1.0f / (float)B;
@@ -2172,7 +2297,7 @@ extern "C" int gn_model_step(gn_model *M) {
   gn_ctx *c = M->ctx;
   ENTRY(c);
   const AdamCoef a = adam_next(M);  // Adam.NewStep (opt.go:254-258)
-  KTimer kt(c, GN_KCLASS_ADAM);
+  KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * M->nparams);  // read p, g, m, v; write p, m, v
   HIP_OK(c, launch_adam(M->params, M->grads, M->m, M->v, M->nparams, a.efflr, a.b1, a.b2, a.omb1,
                         a.omb2, a.eps, c->stream));
   return GN_OK;

@@ -604,9 +604,9 @@ hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N,
 }
 
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
-                         int rows, int N, hipStream_t s) {
+                         int rows, int N, float eps, hipStream_t s) {
   hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gam, bet, y, stats,
-                     rows, N, 1e-5f);
+                     rows, N, eps);
   return hipGetLastError();
 }
 

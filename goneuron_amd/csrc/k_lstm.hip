@@ -987,9 +987,8 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
   return e;
 }
 
-hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
-                                    double *coef, float *w, int B, int T, int I, int H, int W,
-                                    hipStream_t s) {
+hipError_t launch_lstm_gram(const float *D, const float *hbuf, const float *x, double *gram, int B,
+                            int T, int I, int H, int W, hipStream_t s) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
@@ -1003,8 +1002,25 @@ hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const flo
     hipLaunchKernelGGL(lstm_gram_v5_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
   else
     hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
+                            hipStream_t s) {
+  const int Wc = W < 1 ? 1 : (W > B ? B : W);
+  ChainMap cm{T, (B + Wc - 1) / Wc, B};
+  const int nchains = (B + cm.chunk - 1) / cm.chunk;
+  const int nmax = lstm_gram_pitch(cm.chunk * T);
   hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), 0, s, gram, coef, w, cm, nmax);
   return hipGetLastError();
+}
+
+hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
+                                    double *coef, float *w, int B, int T, int I, int H, int W,
+                                    hipStream_t s) {
+  const hipError_t e = launch_lstm_gram(D, hbuf, x, gram, B, T, I, H, W, s);
+  if (e != hipSuccess) return e;
+  return launch_lstm_clip(gram, coef, w, B, T, W, s);
 }
 
 hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, int H,

@@ -287,6 +287,19 @@ int gn_adam_step(gn_ctx *ctx, float *params, const float *grads, float *m, float
 #define GN_KCLASS_OTHER 2  /* row kernels, column sums, dropout, ... */
 int gn_timing_enable(gn_ctx *ctx, int enable);
 int gn_timing_report(gn_ctx *ctx, int kclass, int64_t *launches, double *total_ms);
+/* Per kernel (or fused launch group) since the last enable: name, class,
+ * launch count, summed time and summed algorithmic work -- bytes moved for a
+ * memory-bound kernel (compulsory fp32 reads and writes), FLOPs for a GEMM /
+ * matrix-core kernel -- so units / time is its achieved GB/s or FLOP/s.
+ * Writes at most cap entries and the number of distinct names to *n. */
+typedef struct gn_kernel_stat {
+  char name[48];
+  int32_t cls;      /* GN_KCLASS_* */
+  int64_t launches;
+  double ms;
+  double units;
+} gn_kernel_stat;
+int gn_timing_kernels(gn_ctx *ctx, gn_kernel_stat *out, int32_t cap, int32_t *n);
 
 /* ---- synthetic inputs (host side; harness utility) ----------------------
  * The reference's LCG (layer.go:61-81): U[0,1) stream, N(0,1) by one
