@@ -111,6 +111,23 @@ SIGNATURES = {
                                     C.c_int32, C.c_int32, C.c_int32, C.c_float]),
     "gn_dense_backward_noalloc": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, C.c_int32, C.c_int32,
                                             C.c_int32, C.c_int32, C.c_int32, C.c_float]),
+    "gn_conv2d_forward": (C.c_int, [vp, vp, vp, vp] + [C.c_int32] * 9),
+    "gn_conv2d_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 9 + [C.c_float]),
+    "gn_maxpool2d_forward": (C.c_int, [vp, vp, vp, vp] + [C.c_int32] * 7),
+    "gn_maxpool2d_backward": (C.c_int, [vp, vp, vp, vp] + [C.c_int32] * 7),
+    "gn_dropout_forward": (C.c_int, [vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_float, C.c_int32]),
+    "gn_dropout_backward": (C.c_int, [vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_float, C.c_int32]),
+    "gn_softmax_ce_backward": (C.c_int, [vp, vp, vp, vp, vp] + [C.c_int32] * 5),
+    "gn_layernorm_forward": (C.c_int, [vp] + [vp] * 5 + [C.c_int32, C.c_int32, C.c_float]),
+    "gn_layernorm_backward": (C.c_int, [vp] + [vp] * 8 + [C.c_int32, C.c_int32, C.c_float]),
+    "gn_mha_workspace": (C.c_int, [C.c_int32] * 5 + [C.POINTER(C.c_int64)]),
+    "gn_mha_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 6),
+    "gn_mha_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 6 + [C.c_float]),
+    "gn_lstm_workspace": (C.c_int, [C.c_int32] * 5 + [C.POINTER(C.c_int64)]),
+    "gn_lstm_seq_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 4),
+    "gn_lstm_seq_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 5 + [C.c_float]),
+    "gn_embedding_forward": (C.c_int, [vp] + [vp] * 5 + [C.c_int32] * 4),
+    "gn_embedding_backward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 5 + [C.c_float]),
     "gn_gemm": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float, vp,
                           C.c_int32, vp, C.c_int32, vp, C.c_int32]),
     "gn_adam_step": (C.c_int, [vp, vp, vp, vp, vp, C.c_int64, C.c_float, C.c_float, C.c_float,

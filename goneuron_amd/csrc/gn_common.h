@@ -159,6 +159,26 @@ hipError_t launch_bn_bwd_eval(const float *g, const float *gb, const float *rv, 
 hipError_t launch_avgpool_fwd(const float *x, float *out, const PoolShape &s, int B, hipStream_t st);
 hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s, int B, hipStream_t st);
 
+// ---- the reference's LCG (layer.go:61-81) on the device ----
+constexpr uint64_t LCG_A = 6364136223846793005ull, LCG_C = 1ull;
+// state after n steps of s -> a s + c (binary powers of the affine map)
+__device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t n) {
+  uint64_t A = 1, C = 0, a = LCG_A, c = LCG_C;
+  while (n) {
+    if (n & 1) {
+      A *= a;
+      C = C * a + c;
+    }
+    c = c * (a + 1);
+    a *= a;
+    n >>= 1;
+  }
+  return A * s + C;
+}
+// Dropout's Q9 mask: element i is 0 when the (i+1)-th draw of RNG(42) is < p
+// (the stream is reset before every sample, dropout.go:138-150, 399-401)
+hipError_t launch_dropout_mask(float *mask, int n, float p, hipStream_t s);
+
 // ---- MoE ----
 constexpr int MOE_MAX_E = 64;  // experts routed by one thread's registers
 struct MoeRoute {

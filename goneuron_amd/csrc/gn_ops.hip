@@ -1,0 +1,607 @@
+// Per-layer operators on device pointers: batched stand-ins for the
+// per-sample Layer.Forward / Backward calls of the reference
+// (internal/layer/layer.go:84-132) and for the per-layer Metal entry points
+// they replace (internal/layer/metal.go:6-50), built from the kernels the
+// whole-model step uses.
+//
+// Conventions: B samples, each in the reference's flat per-sample layout,
+// row-major; parameter gradients are written (not accumulated) and scaled by
+// `scale` (1/B gives the batch average of Network.TrainBatch); an input
+// gradient is written when its pointer is not null.  Calls queue work on the
+// context's stream and return without synchronising.
+#include <math.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gn_ctx.h"
+
+namespace {
+
+int conv_shape(gn_ctx *c, ConvShape &cs, int B, int inC, int H, int W, int outC, int k, int stride,
+               int pad) {
+  if (B <= 0 || inC <= 0 || H <= 0 || W <= 0 || outC <= 0 || k <= 0 || stride <= 0 || pad < 0)
+    return set_err(c, GN_ERR_INVALID, "bad Conv2D geometry");
+  cs.inC = inC;
+  cs.outC = outC;
+  cs.k = k;
+  cs.stride = stride;
+  cs.pad = pad;
+  cs.H = H;
+  cs.W = W;
+  cs.oH = (H + 2 * pad - k) / stride + 1;
+  cs.oW = (W + 2 * pad - k) / stride + 1;
+  if (cs.oH <= 0 || cs.oW <= 0) return set_err(c, GN_ERR_SHAPE, "Conv2D output would be empty");
+  return GN_OK;
+}
+
+int pool_shape(gn_ctx *c, PoolShape &ps, int B, int C, int H, int W, int k, int stride, int pad) {
+  if (B <= 0 || C <= 0 || H <= 0 || W <= 0 || k <= 0 || stride <= 0 || pad < 0)
+    return set_err(c, GN_ERR_INVALID, "bad MaxPool2D geometry");
+  ps.C = C;
+  ps.k = k;
+  ps.stride = stride;
+  ps.pad = pad;
+  ps.H = H;
+  ps.W = W;
+  ps.oH = (H + 2 * pad - k) / stride + 1;
+  ps.oW = (W + 2 * pad - k) / stride + 1;
+  if (ps.oH <= 0 || ps.oW <= 0) return set_err(c, GN_ERR_SHAPE, "MaxPool2D output would be empty");
+  return GN_OK;
+}
+
+// regions of a caller workspace, each 64 floats (256 B) aligned
+struct Carve {
+  float *base;
+  size_t off = 0;
+  explicit Carve(float *b) : base(b) {}
+  float *take(size_t n) {
+    float *p = base ? base + off : nullptr;
+    off += (n + 63) / 64 * 64;
+    return p;
+  }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Conv2D (conv2d.go:716-1174): out = act(conv(x, W) + b), per sample NCHW;
+// params = [W (outC x inC x k x k) | b (outC)], the layer's Params() layout.
+// The backward forms dz = gout * act'(out), writes [dW | db] = scale * sums
+// over the batch and, when gin is set, the input gradient (col2im).
+// ---------------------------------------------------------------------------
+extern "C" int gn_conv2d_forward(gn_ctx *c, const float *x, const float *params, float *out,
+                                 int32_t B, int32_t inC, int32_t H, int32_t W, int32_t outC,
+                                 int32_t k, int32_t stride, int32_t pad, int32_t act) {
+  ENTRY(c);
+  ConvShape cs{};
+  int rc = conv_shape(c, cs, B, inC, H, W, outC, k, stride, pad);
+  if (rc) return rc;
+  if (!x || !params || !out) return set_err(c, GN_ERR_INVALID, "null pointer");
+  int fwd = 0, deriv = 0;
+  if (plan_scalar_act(act, fwd, deriv)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
+  KTimer kt(c, GN_KCLASS_OTHER, "conv_fwd", conv_flops(cs, B));
+  HIP_OK(c, launch_conv_fwd(x, params, params + (int64_t)outC * inC * k * k, out, cs, B, fwd, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_conv2d_backward(gn_ctx *c, const float *x, const float *params, const float *out,
+                                  const float *gout, float *grads, float *gin, int32_t B, int32_t inC,
+                                  int32_t H, int32_t W, int32_t outC, int32_t k, int32_t stride,
+                                  int32_t pad, int32_t act, float scale) {
+  ENTRY(c);
+  ConvShape cs{};
+  int rc = conv_shape(c, cs, B, inC, H, W, outC, k, stride, pad);
+  if (rc) return rc;
+  if (!x || !params || !out || !gout || !grads) return set_err(c, GN_ERR_INVALID, "null pointer");
+  int fwd = 0, deriv = 0;
+  if (plan_scalar_act(act, fwd, deriv)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "conv_wgrad", conv_flops(cs, B) + 2.0 * B * outC * cs.oH * cs.oW);
+    HIP_OK(c, launch_conv_wgrad(x, gout, out, grads, cs, B, deriv, scale, c->scratch, c->scratch_floats,
+                                c->stream));
+  }
+  if (gin) {
+    KTimer kt(c, GN_KCLASS_OTHER, "conv_dgrad", conv_flops(cs, B));
+    HIP_OK(c, launch_conv_dgrad(gout, out, params, gin, cs, B, deriv, c->stream));
+  }
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MaxPool2D (maxpool2d.go:106-410): strict-greater first maximum of each
+// window (padding never wins); argmax holds the flat input index (inside the
+// sample) of every output, int32.  The backward sums gout into the winners.
+// ---------------------------------------------------------------------------
+extern "C" int gn_maxpool2d_forward(gn_ctx *c, const float *x, float *out, int32_t *argmax, int32_t B,
+                                    int32_t C, int32_t H, int32_t W, int32_t k, int32_t stride,
+                                    int32_t pad) {
+  ENTRY(c);
+  PoolShape ps{};
+  int rc = pool_shape(c, ps, B, C, H, W, k, stride, pad);
+  if (rc) return rc;
+  if (!x || !out || !argmax) return set_err(c, GN_ERR_INVALID, "null pointer");
+  KTimer kt(c, GN_KCLASS_OTHER, "maxpool_fwd", f4((double)B * C * H * W + 2.0 * B * C * ps.oH * ps.oW));
+  HIP_OK(c, launch_maxpool_fwd(x, out, argmax, ps, B, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_maxpool2d_backward(gn_ctx *c, const float *gout, const int32_t *argmax, float *gin,
+                                     int32_t B, int32_t C, int32_t H, int32_t W, int32_t k,
+                                     int32_t stride, int32_t pad) {
+  ENTRY(c);
+  PoolShape ps{};
+  int rc = pool_shape(c, ps, B, C, H, W, k, stride, pad);
+  if (rc) return rc;
+  if (!gout || !argmax || !gin) return set_err(c, GN_ERR_INVALID, "null pointer");
+  KTimer kt(c, GN_KCLASS_OTHER, "maxpool_bwd", f4(2.0 * B * C * ps.oH * ps.oW + (double)B * C * H * W));
+  HIP_OK(c, launch_maxpool_bwd(gout, argmax, gin, ps, B, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Dropout (dropout.go:47-401).  Training: the mask is the first n draws of
+// RNG(42) against p, the same for every sample because Reset reseeds the
+// stream before each one (Q9), written to mask (n floats, 0 or 1);
+// out = x * mask / (1 - p).  Inference: out = x, and the gradient passes
+// unchanged.
+// ---------------------------------------------------------------------------
+extern "C" int gn_dropout_forward(gn_ctx *c, const float *x, float *out, float *mask, int32_t B,
+                                  int32_t n, float p, int32_t training) {
+  ENTRY(c);
+  if (!x || !out || B <= 0 || n <= 0 || (training && !mask)) return set_err(c, GN_ERR_INVALID, "bad dropout args");
+  if (!(p >= 0 && p <= 1)) return set_err(c, GN_ERR_INVALID, "dropout p %g outside [0, 1]", p);
+  if (!training) {
+    HIP_OK(c, hipMemcpyAsync(out, x, (size_t)B * n * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    return GN_OK;
+  }
+  HIP_OK(c, launch_dropout_mask(mask, n, p, c->stream));
+  const float keep = 1.0f - p;
+  KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * n + n));
+  HIP_OK(c, launch_dropout(x, mask, 1.0f / keep, out, B, n, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_dropout_backward(gn_ctx *c, const float *gout, const float *mask, float *gin,
+                                   int32_t B, int32_t n, float p, int32_t training) {
+  ENTRY(c);
+  if (!gout || !gin || B <= 0 || n <= 0 || (training && !mask))
+    return set_err(c, GN_ERR_INVALID, "bad dropout args");
+  if (!(p >= 0 && p <= 1)) return set_err(c, GN_ERR_INVALID, "dropout p %g outside [0, 1]", p);
+  if (!training) {
+    HIP_OK(c, hipMemcpyAsync(gin, gout, (size_t)B * n * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    return GN_OK;
+  }
+  const float keep = 1.0f - p;
+  KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * n + n));
+  HIP_OK(c, launch_dropout(gout, mask, 1.0f / keep, gin, B, n, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Output layer: activation + loss + loss gradient through the activation
+// (Dense's Softmax / LogSoftmax Jacobian, layer.go:504-567; loss.go:53-178).
+// zo holds the pre-activations of B rows of C and receives the activation
+// output; dz the gradient at the pre-activations; loss_rows the per-sample
+// losses.
+// ---------------------------------------------------------------------------
+extern "C" int gn_softmax_ce_backward(gn_ctx *c, float *zo, const float *y, float *dz, float *loss_rows,
+                                      int32_t B, int32_t C, int32_t act, int32_t act_is_ptr,
+                                      int32_t loss_kind) {
+  ENTRY(c);
+  if (!zo || !y || !dz || !loss_rows || B <= 0 || C <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad softmax_ce args");
+  if (loss_kind != GN_LOSS_MSE && loss_kind != GN_LOSS_CE)
+    return set_err(c, GN_ERR_INVALID, "unknown loss %d", loss_kind);
+  ActPlan ap;
+  if (plan_act(act, act_is_ptr, ap)) return set_err(c, GN_ERR_INVALID, "unknown activation %d", act);
+  KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * C + B));
+  HIP_OK(c, launch_out_rows(zo, y, zo, dz, loss_rows, B, C, ap.row_act, ap.deriv, loss_kind, nullptr, 1,
+                            c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm (layernorm.go:193-441) over rows of N: y = gamma (x - mean) / std
+// + beta with std = sqrt(var + eps) (eps 0 selects 1e-5); stats keeps (mean,
+// std) per row for the backward, whose dx follows the reference's formula
+// (its last term uses N std^2; Q18).  work: rows x N floats of scratch for
+// g * xhat.  dgamma / dbeta = scale * sums over the rows.
+// ---------------------------------------------------------------------------
+extern "C" int gn_layernorm_forward(gn_ctx *c, const float *x, const float *gamma, const float *beta,
+                                    float *y, float *stats, int32_t rows, int32_t N, float eps) {
+  ENTRY(c);
+  if (!x || !gamma || !beta || !y || !stats || rows <= 0 || N <= 0 || !(eps >= 0))
+    return set_err(c, GN_ERR_INVALID, "bad layernorm args");
+  KTimer kt(c, GN_KCLASS_OTHER, "ln_fwd", f4(2.0 * rows * N + 2.0 * rows));
+  HIP_OK(c, launch_ln_fwd(x, gamma, beta, y, stats, rows, N, eps > 0 ? eps : 1e-5f, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_layernorm_backward(gn_ctx *c, const float *g, const float *x, const float *gamma,
+                                     const float *stats, float *dx, float *dgamma, float *dbeta,
+                                     float *work, int32_t rows, int32_t N, float scale) {
+  ENTRY(c);
+  if (!g || !x || !gamma || !stats || !dx || !dgamma || !dbeta || !work || rows <= 0 || N <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad layernorm args");
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd", f4(4.0 * rows * N + 2.0 * rows));
+    HIP_OK(c, launch_ln_bwd(g, x, gamma, stats, dx, work, rows, N, c->stream));
+  }
+  const float *src[2] = {work, g};
+  float *dst[2] = {dgamma, dbeta};
+  KTimer kt(c, GN_KCLASS_OTHER, "colsum", 2 * f4((double)rows * N + N));
+  HIP_OK(c, launch_colsum_multi(src, dst, 2, rows, N, N, scale, c->scratch, c->scratch_floats, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MultiHeadAttention (transformer.go:277-690): x is B x T x D; params =
+// [wQ (W D x D, b D) | wK | wV | wOut].  Q, K, V are Linear Dense layers per
+// token (RoPE on Q, K when use_rope), scaled dot-product attention per head
+// (causal mask -1e9), out = wOut(attention).  The backward is the per-token
+// Dense backward of the reference (the weight gradients use the last token's
+// input, Q10), the attention backward, the conjugate rotation.  work holds
+// what the forward saves for the backward (gn_mha_workspace floats); the
+// forward and backward of one batch must share it and x.
+// ---------------------------------------------------------------------------
+namespace {
+struct MhaWork {
+  float *Q, *K, *V, *O, *GO, *GQ, *GK, *GV, *S, *S3, *rcos, *rsin;
+  size_t floats;
+};
+MhaWork mha_carve(float *w, int B, int T, int D, int NH, int rope) {
+  Carve cv(w);
+  MhaWork m{};
+  const size_t rows = (size_t)B * T;
+  m.Q = cv.take(3 * rows * D);
+  m.K = m.Q ? m.Q + rows * D : nullptr;
+  m.V = m.K ? m.K + rows * D : nullptr;
+  m.O = cv.take(rows * D);
+  m.GO = cv.take(rows * D);
+  m.GQ = cv.take(3 * rows * D);
+  m.GK = m.GQ ? m.GQ + rows * D : nullptr;
+  m.GV = m.GK ? m.GK + rows * D : nullptr;
+  m.S = cv.take((size_t)B * D);
+  m.S3 = cv.take(3 * (size_t)B * D);
+  const size_t half = (size_t)std::max(D / std::max(NH, 1) / 2, 1);
+  m.rcos = rope ? cv.take((size_t)T * half) : nullptr;
+  m.rsin = rope ? cv.take((size_t)T * half) : nullptr;
+  m.floats = cv.off;
+  return m;
+}
+int mha_check(gn_ctx *c, int B, int T, int D, int NH) {
+  if (B <= 0 || T <= 0 || D <= 0 || NH <= 0 || D % NH) return set_err(c, GN_ERR_INVALID, "bad MHA sizes");
+  if (!attn_supported(T, D, NH))
+    return set_err(c, GN_ERR_UNSUPPORTED, "attention needs T <= 128 and D / heads <= 32");
+  return GN_OK;
+}
+}  // namespace
+
+extern "C" int gn_mha_workspace(int32_t B, int32_t T, int32_t D, int32_t heads, int32_t use_rope,
+                                int64_t *floats) {
+  if (!floats || B <= 0 || T <= 0 || D <= 0 || heads <= 0) return GN_ERR_INVALID;
+  *floats = (int64_t)mha_carve(nullptr, B, T, D, heads, use_rope).floats;
+  return GN_OK;
+}
+
+extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
+                              int32_t B, int32_t T, int32_t D, int32_t heads, int32_t causal,
+                              int32_t use_rope) {
+  ENTRY(c);
+  int rc = mha_check(c, B, T, D, heads);
+  if (rc) return rc;
+  if (!x || !params || !out || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MhaWork m = mha_carve(work, B, T, D, heads, use_rope);
+  const int rows = B * T, hd = D / heads;
+  const int64_t nd = (int64_t)D * D + D;
+  {  // Q, K, V in one batched launch (weights, biases and outputs equally spaced)
+    GemmArgs a{};
+    a.M = rows; a.N = D; a.K = D;
+    a.A = x; a.lda = D; a.B = params; a.ldb = D;
+    a.C = m.Q; a.ldc = D; a.alpha = 1.f; a.bias = params + (int64_t)D * D; a.act = F_IDENTITY;
+    a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+    a.nbatch = 3;
+    a.bstride_B = nd;
+    a.bstride_bias = nd;
+    a.bstride_C = (int64_t)rows * D;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream));
+  }
+  if (use_rope) {  // applyRoPE's angles (transformer.go:215-221), float32 as the reference
+    const int half = hd / 2;
+    std::vector<float> cs((size_t)T * std::max(half, 1)), sn(cs.size());
+    for (int t = 0; t < T; ++t)
+      for (int k = 0; k < half; ++k) {
+        const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
+        const float mt = (float)t * theta;
+        cs[(size_t)t * half + k] = (float)cos((double)mt);
+        sn[(size_t)t * half + k] = (float)sin((double)mt);
+      }
+    HIP_OK(c, hipMemcpyAsync(m.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIP_OK(c, hipMemcpyAsync(m.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));  // the host tables go out of scope
+    KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
+    HIP_OK(c, launch_rope(m.Q, m.rcos, m.rsin, rows, T, heads, hd, 0, c->stream));
+    HIP_OK(c, launch_rope(m.K, m.rcos, m.rsin, rows, T, heads, hd, 0, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, T, heads, hd, causal, false));
+    HIP_OK(c, launch_attn_fwd(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, c->stream));
+  }
+  GemmArgs o{};
+  o.M = rows; o.N = D; o.K = D;
+  o.A = m.O; o.lda = D; o.B = params + 3 * nd; o.ldb = D;
+  o.C = out; o.ldc = D; o.alpha = 1.f; o.bias = params + 3 * nd + (int64_t)D * D; o.act = F_IDENTITY;
+  o.ws = c->scratch; o.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(o));
+  HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, o, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                               float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t D,
+                               int32_t heads, int32_t causal, int32_t use_rope, float scale) {
+  ENTRY(c);
+  int rc = mha_check(c, B, T, D, heads);
+  if (rc) return rc;
+  if (!x || !params || !gout || !grads || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MhaWork m = mha_carve(work, B, T, D, heads, use_rope);
+  const int rows = B * T, hd = D / heads;
+  const int64_t nd = (int64_t)D * D + D;
+  const float *Wo = params + 3 * nd;
+  float *G = grads;
+  float *cs = c->scratch;
+  const size_t cap = c->scratch_floats;
+  // wOut, a per-token Linear Dense: its bias gradient sums every token, which
+  // are the per-sample token sums its Q10 weight gradient uses too
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
+    HIP_OK(c, launch_token_sum(gout, m.S, B, T, D, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
+    HIP_OK(c, launch_colsum(m.S, B, D, D, scale, G + 3 * nd + (int64_t)D * D, cs, cap, c->stream));
+  }
+  {
+    GemmArgs a{};  // dWo = scale * S^T O_last
+    a.M = D; a.N = D; a.K = B;
+    a.A = m.S; a.lda = D;
+    a.B = m.O + (int64_t)(T - 1) * D; a.ldb = T * D;
+    a.C = G + 3 * nd; a.ldc = D; a.alpha = scale;
+    a.ws = cs; a.ws_cap = cap;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
+    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+  }
+  {
+    GemmArgs a{};  // GO = gout Wo
+    a.M = rows; a.N = D; a.K = D;
+    a.A = gout; a.lda = D; a.B = Wo; a.ldb = D;
+    a.C = m.GO; a.ldc = D; a.alpha = 1.f;
+    a.ws = cs; a.ws_cap = cap;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+    HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, heads, hd, causal, true));
+    HIP_OK(c, launch_attn_bwd(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, c->stream));
+  }
+  if (use_rope) {  // transformer.go:660-664: the conjugate rotation before wQ / wK
+    KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
+    HIP_OK(c, launch_rope(m.GQ, m.rcos, m.rsin, rows, T, heads, hd, 1, c->stream));
+    HIP_OK(c, launch_rope(m.GK, m.rcos, m.rsin, rows, T, heads, hd, 1, c->stream));
+  }
+  const int64_t sst = (int64_t)B * D;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D));
+    HIP_OK(c, launch_token_sum_multi(m.GQ, m.S3, B, T, D, 3, (int64_t)rows * D, sst, c->stream));
+  }
+  {
+    const float *src[3] = {m.S3, m.S3 + sst, m.S3 + 2 * sst};
+    float *dst[3] = {G + (int64_t)D * D, G + nd + (int64_t)D * D, G + 2 * nd + (int64_t)D * D};
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", 3 * f4((double)B * D + D));
+    HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
+  }
+  {
+    GemmArgs a{};  // dWq, dWk, dWv = scale * S3_m^T x_last in one launch
+    a.M = D; a.N = D; a.K = B;
+    a.A = m.S3; a.lda = D;
+    a.B = x + (int64_t)(T - 1) * D; a.ldb = T * D;
+    a.C = G; a.ldc = D; a.alpha = scale;
+    a.ws = cs; a.ws_cap = cap;
+    a.nbatch = 3;
+    a.bstride_A = sst;
+    a.bstride_C = nd;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
+    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+  }
+  if (gin) {  // gin = gQ Wq + gK Wk + gV Wv
+    const float *gq[3] = {m.GQ, m.GK, m.GV};
+    for (int i = 0; i < 3; ++i) {
+      GemmArgs a{};
+      a.M = rows; a.N = D; a.K = D;
+      a.A = gq[i]; a.lda = D; a.B = params + i * nd; a.ldb = D;
+      a.C = gin; a.ldc = D; a.alpha = 1.f;
+      a.aux = gin; a.ldaux = D;
+      a.ws = cs; a.ws_cap = cap;
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+      HIP_OK(c, launch_gemm('N', 'N', i == 0 ? EPI_SCALE : EPI_BIAS_ADD, a, c->stream));
+    }
+  }
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// SequenceUnroller(LSTM) (unroller.go:57-213, lstm.go:144-751) over a batch:
+// x is B x T x I, params = [Wx (4H x I) | Wh (4H x H) | b (4H)], gates i, f,
+// g, o; out = h_{T-1} (B x H).  The reference's quirks are kept: only the
+// input gate adds Wx x + Wh h (Q13); dWx uses the last step's input (Q10);
+// dh_{t-1} = dh_t + Wh^T dG (Q15); each worker chain's cumulative gradient is
+// clipped to norm 1 after every step (Q14, `workers` chains of ceil(B /
+// workers) samples, evaluated exactly through the chain's Gram matrix).  The
+// input gradient (gin, B x T x I) uses the unclipped deltas, as the
+// reference's dx does.  work holds what the forward saves (gn_lstm_workspace
+// floats for the same B, T, I, H, workers).
+// ---------------------------------------------------------------------------
+namespace {
+struct LstmWork {
+  float *WhT, *xw, *igb, *tcb, *cbuf, *hbuf, *Dg, *S, *wts;
+  double *gram, *coef;
+  size_t floats;
+};
+LstmWork lstm_carve(float *w, int B, int T, int I, int H, int workers) {
+  Carve cv(w);
+  LstmWork m{};
+  const size_t Bm = B, TT = T, HH = H;
+  m.WhT = cv.take(HH * HH);
+  m.xw = cv.take(Bm * TT * HH);
+  m.igb = cv.take(Bm * TT * HH);
+  m.tcb = cv.take(Bm * TT * HH);
+  m.cbuf = cv.take(Bm * TT * HH);
+  m.hbuf = cv.take(Bm * (TT + 1) * HH);
+  m.Dg = cv.take(Bm * (TT + 1) * 4 * HH);
+  m.S = cv.take(Bm * 4 * HH);
+  m.wts = cv.take(Bm * (TT + 1));
+  const int Wc = std::min(std::max(workers, 1), B);
+  const size_t chunk = (B + Wc - 1) / Wc;
+  const size_t nmax = (size_t)lstm_gram_pitch((int)(chunk * T));
+  const size_t nchains = (B + chunk - 1) / chunk;
+  m.gram = reinterpret_cast<double *>(cv.take(2 * nchains * nmax * nmax));
+  m.coef = reinterpret_cast<double *>(cv.take(2 * nchains * nmax));
+  m.floats = cv.off;
+  (void)I;
+  return m;
+}
+}  // namespace
+
+extern "C" int gn_lstm_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int32_t workers,
+                                 int64_t *floats) {
+  if (!floats || B <= 0 || T <= 0 || I <= 0 || H <= 0) return GN_ERR_INVALID;
+  *floats = (int64_t)lstm_carve(nullptr, B, T, I, H, workers).floats;
+  return GN_OK;
+}
+
+extern "C" int gn_lstm_seq_forward(gn_ctx *c, const float *x, const float *params, float *out,
+                                   float *work, int32_t B, int32_t T, int32_t I, int32_t H) {
+  ENTRY(c);
+  if (!x || !params || !out || !work || B <= 0 || T <= 0 || I <= 0 || H <= 0 || H > 1024)
+    return set_err(c, GN_ERR_INVALID, "bad LSTM args (hidden <= 1024)");
+  LstmWork m = lstm_carve(work, B, T, I, H, 1);
+  const float *Wx = params, *Wh = Wx + (int64_t)4 * H * I, *bias = Wh + (int64_t)4 * H * H;
+  {
+    GemmArgs g{};  // xw[b*T + t] = x_t . Wx_i (the input-gate rows, Q13)
+    g.M = B * T; g.N = H; g.K = I;
+    g.A = x; g.lda = I; g.B = Wx; g.ldb = I;
+    g.C = m.xw; g.ldc = H; g.alpha = 1.f;
+    g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(g));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "transpose", f4(2.0 * H * H));
+    HIP_OK(c, launch_transpose(Wh, m.WhT, H, H, c->stream));
+  }
+  KTimer kt(c, GN_KCLASS_OTHER, "lstm_fwd", 2.0 * H * H * B * T);
+  HIP_OK(c, launch_lstm_fwd(m.xw, m.WhT, bias, m.igb, m.tcb, m.cbuf, m.hbuf, out, B, T, H, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_lstm_seq_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                                    float *grads, float *gin, float *work, int32_t B, int32_t T,
+                                    int32_t I, int32_t H, int32_t workers, float scale) {
+  ENTRY(c);
+  if (!x || !params || !gout || !grads || !work || B <= 0 || T <= 0 || I <= 0 || H <= 0 || H > 1024)
+    return set_err(c, GN_ERR_INVALID, "bad LSTM args (hidden <= 1024)");
+  // the forward's saved state sits where the carve of the same sizes puts it;
+  // the Gram buffers (after it) are sized for `workers`
+  LstmWork m = lstm_carve(work, B, T, I, H, workers);
+  const int G4 = 4 * H;
+  const float *Wx = params, *Wh = Wx + (int64_t)G4 * I, *bias = Wh + (int64_t)G4 * H;
+  float *gWx = grads, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "lstm_bptt", 2.0 * G4 * H * B * T);
+    HIP_OK(c, launch_lstm_bwd(gout, m.igb, m.tcb, m.cbuf, Wh, bias, m.Dg, B, T, H, c->stream));
+  }
+  if (gin) {  // dx_t = Wx^T dG_t for every sample and step, before the clip weights touch dG
+    GemmArgs a{};
+    a.M = T; a.N = I; a.K = G4;
+    a.A = m.Dg; a.lda = G4; a.B = Wx; a.ldb = I;
+    a.C = gin; a.ldc = I; a.alpha = 1.f;
+    a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+    a.nbatch = B;
+    a.bstride_A = (int64_t)(T + 1) * G4;
+    a.bstride_C = (int64_t)T * I;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+    HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+  }
+  const int Wc = std::max(1, std::min(workers, B)), chunk = (B + Wc - 1) / Wc;
+  const double nst = (double)chunk * T, nchain = (double)((B + chunk - 1) / chunk);
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "lstm_gram", nchain * nst * (nst + 1) * (5.0 * H + I));
+    HIP_OK(c, launch_lstm_gram(m.Dg, m.hbuf, x, m.gram, B, T, I, H, workers, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "lstm_clip", nchain * 8.0 * nst * (nst + 1) / 2);
+    HIP_OK(c, launch_lstm_clip(m.gram, m.coef, m.wts, B, T, workers, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "lstm_weight", f4(2.0 * B * (T + 1) * G4 + (double)B * G4));
+    HIP_OK(c, launch_lstm_weight(m.Dg, m.wts, m.S, B, T, H, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * G4 + G4));
+    HIP_OK(c, launch_colsum(m.S, B, G4, G4, scale, gb, c->scratch, c->scratch_floats, c->stream));
+  }
+  GemmArgs a{};  // dWx = scale * S^T x_last
+  a.M = G4; a.N = I; a.K = B;
+  a.A = m.S; a.lda = G4;
+  a.B = x + (int64_t)(T - 1) * I; a.ldb = T * I;
+  a.C = gWx; a.ldc = I; a.alpha = scale;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  GemmArgs h{};  // dWh = scale * (w dG)^T hPrev, K over (sample, step)
+  h.M = G4; h.N = H; h.K = B * (T + 1);
+  h.A = m.Dg; h.lda = G4;
+  h.B = m.hbuf; h.ldb = H;
+  h.C = gWh; h.ldc = H; h.alpha = scale;
+  h.ws = c->scratch; h.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a) + gemm_flops(h));
+  HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+  HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, h, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Embedding (embedding.go:79-183): x holds B x T token ids as floats
+// (floor(x) is the index); out the rows of E (V x D); ids the int32 indices
+// for the backward; bad (optional, B ints) flags the samples with an index
+// outside [0, V) (the reference's Forward errors on them; their rows read
+// row 0 here).  The backward zeroes gradE and adds the rows of each worker
+// chunk's last sample (Embedding.Backward zeroes its gradient first, Q12;
+// `workers` chunks of ceil(B / workers); with bad, the last sample of the
+// chunk that the reference's loop would still run), times scale.
+// ---------------------------------------------------------------------------
+extern "C" int gn_embedding_forward(gn_ctx *c, const float *x, const float *E, float *out, int32_t *ids,
+                                    int32_t *bad, int32_t B, int32_t T, int32_t V, int32_t D) {
+  ENTRY(c);
+  if (!x || !E || !out || !ids || B <= 0 || T <= 0 || V <= 0 || D <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad embedding args");
+  KTimer kt(c, GN_KCLASS_OTHER, "embed_fwd", f4(2.0 * B * T + 2.0 * B * T * D));
+  HIP_OK(c, launch_embed(x, E, ids, out, B, T, V, D, bad, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_embedding_backward(gn_ctx *c, const float *gout, const int32_t *ids,
+                                     const int32_t *bad, float *gradE, int32_t B, int32_t T, int32_t V,
+                                     int32_t D, int32_t workers, float scale) {
+  ENTRY(c);
+  if (!gout || !ids || !gradE || B <= 0 || T <= 0 || V <= 0 || D <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad embedding args");
+  const int Wc = std::max(1, std::min(workers, B)), chunk = (B + Wc - 1) / Wc;
+  const int nch = (B + chunk - 1) / chunk;
+  KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)V * D + 2.0 * nch * T * D));
+  const hipError_t e = launch_embed_grad(gout, ids, gradE, V, B, T, D, workers, scale, bad, c->stream);
+  if (e == hipErrorInvalidValue)
+    return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed 2048", nch * T);
+  HIP_OK(c, e);
+  return GN_OK;
+}

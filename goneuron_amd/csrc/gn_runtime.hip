@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "gn_common.h"
+#include "gn_ctx.h"
 
 using namespace gn;
 
@@ -36,120 +37,6 @@ constexpr int kMaxDevices = 64;
 static float *noalloc_ptr[kMaxDevices];
 static std::mutex noalloc_mu;
 
-struct gn_ctx {
-  int device = 0;
-  hipStream_t stream = nullptr;
-  hipStream_t aux = nullptr;  // per-layer Adam updates, overlapped with the backward pass
-  std::string err;
-  int fail_next = 0;
-  hipDeviceProp_t props{};
-  float *scratch = nullptr;  // colsum partials
-  size_t scratch_floats = 0;
-  float *scratch_aux = nullptr;  // the same for kernels queued on `aux` (scratch_floats long)
-  float *noalloc = nullptr;      // this device's copy of `scratch` (gn_dense_backward_noalloc)
-  // kernel timing (gn_timing_enable)
-  bool timing = false;
-  struct Rec {
-    int cls;
-    const char *name;  // kernel (or fused launch group) name, static storage
-    double units;      // algorithmic bytes (memory-bound) or FLOPs (GEMM / MFMA) of the launch
-    hipEvent_t a, b;
-  };
-  std::vector<Rec> recs;
-  std::vector<hipEvent_t> pool;
-  size_t pool_used = 0;
-};
-
-static hipEvent_t ev_get(gn_ctx *c) {
-  if (c->pool_used == c->pool.size()) {
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
-    c->pool.push_back(e);
-  }
-  return c->pool[c->pool_used++];
-}
-
-// Brackets the kernels launched in its scope with events when timing is on
-// (on the stream those kernels go to), under a name with the launch's
-// algorithmic work: the bytes a memory-bound kernel must move (compulsory
-// reads and writes, fp32) or the FLOPs of a matrix-core kernel.
-struct KTimer {
-  gn_ctx *c;
-  int cls;
-  const char *name;
-  double units;
-  hipStream_t st;
-  hipEvent_t a = nullptr, b = nullptr;
-  KTimer(gn_ctx *c_, int cls_, const char *name_, double units_, hipStream_t st_ = nullptr)
-      : c(c_), cls(cls_), name(name_), units(units_), st(st_ ? st_ : c_->stream) {
-    if (c->timing) {
-      a = ev_get(c);
-      b = ev_get(c);
-      if (a && b) (void)hipEventRecord(a, st);
-      else a = b = nullptr;
-    }
-  }
-  ~KTimer() {
-    if (a) {
-      (void)hipEventRecord(b, st);
-      c->recs.push_back({cls, name, units, a, b});
-    }
-  }
-};
-
-static double gemm_flops(const GemmArgs &g) {
-  return 2.0 * g.M * g.N * g.K * (g.nbatch > 1 ? g.nbatch : 1);
-}
-static double f4(double n) { return 4.0 * n; }  // bytes of n floats
-// attention FLOPs per launch: the score and value products over the (query,
-// key) pairs the mask keeps, 2 products forward, 4 backward (dP, dQ, dK, dV)
-static double attn_flops(int B, int T, int NH, int hd, int causal, bool bwd) {
-  const double pairs = causal ? 0.5 * T * (T + 1.0) : (double)T * T;
-  return (bwd ? 8.0 : 4.0) * hd * pairs * B * NH;
-}
-// per-sample token sums: read B x T x N, write B x N
-static double token_sum_bytes(int B, int T, int N) { return f4((double)B * T * N + (double)B * N); }
-// direct convolution work: 2 FLOPs per tap of every output
-static double conv_flops(const ConvShape &cs, int B) {
-  return 2.0 * B * cs.outC * cs.oH * cs.oW * cs.inC * cs.k * cs.k;
-}
-
-static int set_err(gn_ctx *c, int code, const char *fmt, ...) {
-  if (c) {
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
-    va_end(ap);
-    c->err = buf;
-  }
-  return code;
-}
-
-#define HIP_OK(ctx, expr)                                                                  \
-  do {                                                                                     \
-    hipError_t e_ = (expr);                                                                \
-    if (e_ != hipSuccess)                                                                  \
-      return set_err((ctx), GN_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
-                     __FILE__, __LINE__);                                                  \
-  } while (0)
-
-static int check_fail(gn_ctx *c) {
-  if (c && c->fail_next) {
-    int code = c->fail_next;
-    c->fail_next = 0;
-    return set_err(c, code, "injected failure (gn_debug_fail_next)");
-  }
-  return GN_OK;
-}
-
-#define ENTRY(ctx)                              \
-  do {                                          \
-    if (!(ctx)) return GN_ERR_INVALID;          \
-    int f_ = check_fail(ctx);                   \
-    if (f_) return f_;                          \
-    (void)hipSetDevice((ctx)->device);          \
-  } while (0)
 
 // ---------------------------------------------------------------------------
 // LCG of the reference (layer.go:61-81) and synthetic data
@@ -378,45 +265,6 @@ extern "C" int gn_memset_zero(gn_ctx *c, void *dst, size_t bytes) {
 // ---------------------------------------------------------------------------
 // Per-layer operators
 // ---------------------------------------------------------------------------
-struct ActPlan {
-  int row_act;  // RowAct (with fwd kind in bits 8.. for ROW_ELEMWISE)
-  int fwd;      // FwdKind for elementwise forward
-  int deriv;    // DerivKind
-  bool jac;     // Softmax/LogSoftmax Jacobian backward
-};
-
-// cacheActivationType (layer.go:183-205) + the Activate/Derivative methods of
-// activations.go: pointer Softmax/LogSoftmax get the row activation and the
-// Jacobian; the values fall through to identity forward / NaN derivative.
-static int plan_act(int act, int is_ptr, ActPlan &p) {
-  p = ActPlan{ROW_NONE, F_IDENTITY, D_ONE, false};
-  switch (act) {
-    case GN_ACT_RELU: p.fwd = F_RELU; p.deriv = D_RELU; break;
-    case GN_ACT_SIGMOID: p.fwd = F_SIGMOID; p.deriv = D_SIGMOID; break;
-    case GN_ACT_TANH: p.fwd = F_TANH; p.deriv = D_TANH; break;
-    case GN_ACT_LINEAR: break;
-    case GN_ACT_GELU:
-      // only *activations.GELU is ActTypeGELU (layer.go:196-197); the value
-      // runs as ActTypeNone: identity forward, Derivative(preAct) backward,
-      // and the identity output is the pre-activation D_GELU needs
-      if (is_ptr) return GN_ERR_UNSUPPORTED;
-      p.deriv = D_GELU;
-      break;
-    case GN_ACT_SOFTMAX:
-    case GN_ACT_LOGSOFTMAX:
-      if (is_ptr) {
-        p.row_act = act == GN_ACT_SOFTMAX ? ROW_SOFTMAX : ROW_LOGSOFTMAX;
-        p.jac = true;
-      } else {
-        p.deriv = D_NAN;
-      }
-      break;
-    default: return GN_ERR_INVALID;  // nil activation: the reference panics in Derivative
-  }
-  if (p.row_act == ROW_NONE && p.fwd != F_IDENTITY) p.row_act = ROW_ELEMWISE | (p.fwd << 8);
-  return GN_OK;
-}
-
 static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const float *b, float *out,
                             int B, int in, int out_n, int fwd) {
   GemmArgs a{};
@@ -774,20 +622,6 @@ static void init_conv(float *p, int inC, int outC, int k) {  // Conv2D.Build con
   const int64_t nw = (int64_t)outC * inC * k * k;
   for (int64_t i = 0; i < nw; ++i) p[i] = lcg_float(s) * 2 * scale - scale;
   for (int i = 0; i < outC; ++i) p[nw + i] = lcg_float(s) * 0.2f - 0.1f;
-}
-
-// Conv2D calls the activation's scalar Activate / Derivative methods directly
-// (conv2d.go:950, :1140): Softmax/LogSoftmax give NaN there.
-static int plan_scalar_act(int act, int &fwd, int &deriv) {
-  switch (act) {
-    case GN_ACT_RELU: fwd = F_RELU; deriv = D_RELU; return GN_OK;
-    case GN_ACT_SIGMOID: fwd = F_SIGMOID; deriv = D_SIGMOID; return GN_OK;
-    case GN_ACT_TANH: fwd = F_TANH; deriv = D_TANH; return GN_OK;
-    case GN_ACT_LINEAR: fwd = F_IDENTITY; deriv = D_ONE; return GN_OK;
-    case GN_ACT_SOFTMAX:
-    case GN_ACT_LOGSOFTMAX: fwd = F_NAN; deriv = D_NAN; return GN_OK;
-    default: return GN_ERR_INVALID;
-  }
 }
 
 static void init_lstm(float *p, int in, int H) {  // LSTM.Build lstm.go:175-196

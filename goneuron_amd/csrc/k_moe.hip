@@ -15,22 +15,7 @@
 
 namespace gn {
 
-constexpr uint64_t LCG_A = 6364136223846793005ull, LCG_C = 1ull;
 
-// state after n steps of s -> a s + c (binary powers of the affine map)
-__device__ __forceinline__ uint64_t lcg_jump(uint64_t s, uint64_t n) {
-  uint64_t A = 1, C = 0, a = LCG_A, c = LCG_C;
-  while (n) {
-    if (n & 1) {
-      A *= a;
-      C = C * a + c;
-    }
-    c = c * (a + 1);
-    a *= a;
-    n >>= 1;
-  }
-  return A * s + C;
-}
 
 // One thread per sample: noisy logits (training), softmax, stable descending
 // order; writes probabilities [B][E] and the top-k ids [B][K].

@@ -420,6 +420,20 @@ hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(TPB) void dropout_mask_kernel(float *__restrict__ mask, int n, float p) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t s = lcg_jump(42, (uint64_t)i + 1);
+  const float u = (float)(s >> 33) / (float)(1u << 31);
+  mask[i] = u < p ? 0.0f : 1.0f;
+}
+
+hipError_t launch_dropout_mask(float *mask, int n, float p, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(dropout_mask_kernel, dim3((n + TPB - 1) / TPB), dim3(TPB), 0, s, mask, n, p);
+  return hipGetLastError();
+}
+
 // dst[0, n) = v (a kernel, not a memset node: usable inside a captured graph)
 __global__ __launch_bounds__(TPB) void fill_kernel(float *__restrict__ dst, float v, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;

@@ -265,6 +265,117 @@ int gn_dense_backward(gn_ctx *ctx, const float *x, const float *W, const float *
 int gn_dense_backward_noalloc(gn_ctx *ctx, const float *x, const float *W, const float *out,
                               const float *gout, float *gradW, float *gradB, float *gin, int32_t B,
                               int32_t in, int32_t out_n, int32_t act, int32_t act_is_ptr, float scale);
+
+/* Common to the operators below: B samples, each in the layer's flat
+ * per-sample layout (its InSize / OutSize), row-major; parameter gradients
+ * are written, not accumulated, and multiplied by `scale` (1/B gives the
+ * batch average of Network.TrainBatch); an input gradient is written when its
+ * pointer is not NULL.  Calls queue work on the context's stream. */
+
+/* Conv2D.ForwardWithArena (conv2d.go:716-960, Metal conv path metal.go:6-50):
+ * out = act(conv(x, W) + b) per sample, NCHW, params = [W (outC x inC x k x k)
+ * | b (outC)] as Conv2D.Params().  act: scalar GN_ACT_* (Softmax not allowed). */
+int gn_conv2d_forward(gn_ctx *ctx, const float *x, const float *params, float *out, int32_t B,
+                      int32_t inC, int32_t H, int32_t W, int32_t outC, int32_t k, int32_t stride,
+                      int32_t pad, int32_t act);
+/* Conv2D.Backward (conv2d.go:997-1236) over the batch: dz = gout * act'(out),
+ * grads = [dW | db] = scale * batch sums, gin = col2im(W^T dz). */
+int gn_conv2d_backward(gn_ctx *ctx, const float *x, const float *params, const float *out,
+                       const float *gout, float *grads, float *gin, int32_t B, int32_t inC,
+                       int32_t H, int32_t W, int32_t outC, int32_t k, int32_t stride, int32_t pad,
+                       int32_t act, float scale);
+/* MaxPool2D.ForwardWithArena (maxpool2d.go:106-226; MaxPool2DPersistent
+ * metal.go:343): first strict maximum of each window, padding never wins;
+ * argmax = the winner's flat index inside its sample (int32, one per output). */
+int gn_maxpool2d_forward(gn_ctx *ctx, const float *x, float *out, int32_t *argmax, int32_t B,
+                         int32_t C, int32_t H, int32_t W, int32_t k, int32_t stride, int32_t pad);
+/* MaxPool2D.Backward (maxpool2d.go:357-411): gin[i] = sum of gout over the
+ * outputs whose argmax is i (every gin element is written). */
+int gn_maxpool2d_backward(gn_ctx *ctx, const float *gout, const int32_t *argmax, float *gin,
+                          int32_t B, int32_t C, int32_t H, int32_t W, int32_t k, int32_t stride,
+                          int32_t pad);
+/* Dropout.ForwardWithArena (dropout.go:85-155): in training mode mask (n
+ * floats) receives the first n draws of RNG(42) against p (Reset reseeds the
+ * stream before every sample, dropout.go:399-401, so every sample shares it)
+ * and out = x * mask / (1 - p); in inference mode out = x. */
+int gn_dropout_forward(gn_ctx *ctx, const float *x, float *out, float *mask, int32_t B, int32_t n,
+                       float p, int32_t training);
+/* Dropout.Backward (dropout.go:241-293): gin = gout * mask / (1 - p) in
+ * training mode, gout otherwise. */
+int gn_dropout_backward(gn_ctx *ctx, const float *gout, const float *mask, float *gin, int32_t B,
+                        int32_t n, float p, int32_t training);
+/* Output layer and loss: zo (B x C pre-activations) receives act(zo) (Softmax
+ * / LogSoftmax rows when act_is_ptr, layer.go:183-205), loss_rows the
+ * per-sample loss (MSE / CrossEntropy Forward, loss.go:53-70, 120-145) and dz
+ * the gradient at the pre-activations (loss BackwardInPlace loss.go:91-112,
+ * 165-185, then Dense's activation backward layer.go:488-567, Softmax
+ * Jacobian included). */
+int gn_softmax_ce_backward(gn_ctx *ctx, float *zo, const float *y, float *dz, float *loss_rows,
+                           int32_t B, int32_t C, int32_t act, int32_t act_is_ptr, int32_t loss_kind);
+/* LayerNorm.ForwardWithArena (layernorm.go:193-306) over `rows` rows of N:
+ * y = gamma (x - mean) / std + beta, std = sqrt(var + eps) (eps 0 selects
+ * 1e-5); stats = (mean, std) per row, kept for the backward. */
+int gn_layernorm_forward(gn_ctx *ctx, const float *x, const float *gamma, const float *beta,
+                         float *y, float *stats, int32_t rows, int32_t N, float eps);
+/* LayerNorm.Backward (layernorm.go:334-441): dx by the reference's formula
+ * (its last term divides by N std^2), dgamma = scale * sum g * xhat, dbeta =
+ * scale * sum g; work = rows x N floats of scratch. */
+int gn_layernorm_backward(gn_ctx *ctx, const float *g, const float *x, const float *gamma,
+                          const float *stats, float *dx, float *dgamma, float *dbeta, float *work,
+                          int32_t rows, int32_t N, float scale);
+/* MultiHeadAttention (transformer.go:277-776): x is B x T x D, params = [wQ |
+ * wK | wV | wOut], each a Linear Dense (W D x D, b D).  work carries the
+ * forward's saved state to the backward: gn_mha_workspace floats, the same
+ * buffer and x for both calls.  Needs T <= 128 and D / heads <= 32
+ * (GN_ERR_UNSUPPORTED otherwise). */
+int gn_mha_workspace(int32_t B, int32_t T, int32_t D, int32_t heads, int32_t use_rope,
+                     int64_t *floats);
+/* MultiHeadAttention.ForwardWithArena (transformer.go:405-529): Q, K, V per
+ * token, RoPE on Q and K when use_rope (applyRoPE transformer.go:212-236),
+ * softmax(Q K^T / sqrt(hd)) V per head (causal mask -1e9), out = wOut(O). */
+int gn_mha_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work,
+                   int32_t B, int32_t T, int32_t D, int32_t heads, int32_t causal, int32_t use_rope);
+/* MultiHeadAttention.Backward (transformer.go:557-690): each projection's
+ * weight gradient uses its last token's input (the per-token Dense layers
+ * keep only the last Forward's input) and its bias gradient sums every
+ * token; conjugate rotation before wQ / wK; gin = sum of the three
+ * projections' input gradients. */
+int gn_mha_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout,
+                    float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t D,
+                    int32_t heads, int32_t causal, int32_t use_rope, float scale);
+/* SequenceUnroller(LSTM) with return_sequences false (unroller.go:57-213,
+ * lstm.go:144-753): x is B x T x I, params = [Wx (4H x I) | Wh (4H x H) | b
+ * (4H)], gates i, f, g, o; out = h_{T-1} (B x H); hidden <= 1024.  work:
+ * gn_lstm_workspace floats (the same B, T, I, H, workers for both calls). */
+int gn_lstm_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int32_t workers,
+                      int64_t *floats);
+/* LSTM.ForwardWithArena per step (lstm.go:276-442): only the input gate adds Wx x +
+ * Wh h to its bias (lstmComputeInputGates, lstm.go:1065-1101). */
+int gn_lstm_seq_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work,
+                        int32_t B, int32_t T, int32_t I, int32_t H);
+/* SequenceUnroller.Backward + LSTM.Backward per step (unroller.go:133-213,
+ * lstm.go:476-699, clipGradients 725-753): carried dh (dh_{t-1} = dh_t + Wh^T dG), dWx from the last
+ * step's input, each worker chain's cumulative gradient clipped to norm 1
+ * after every step (`workers` chains of ceil(B / workers) samples, as
+ * trainBatchParallel's chunks), gin_t = Wx^T dG_t (unclipped). */
+int gn_lstm_seq_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout,
+                         float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t I,
+                         int32_t H, int32_t workers, float scale);
+/* Embedding.ForwardWithArena (embedding.go:79-141): x = B x T ids as floats,
+ * out = rows of E (V x D), ids = the int32 indices for the backward; bad
+ * (optional, B ints) = 1 for a sample with an id outside [0, V), which the
+ * reference's Forward rejects (its output rows read row 0 here). */
+int gn_embedding_forward(gn_ctx *ctx, const float *x, const float *E, float *out, int32_t *ids,
+                         int32_t *bad, int32_t B, int32_t T, int32_t V, int32_t D);
+/* Embedding.Backward (embedding.go:147-183) over a batch: Backward zeroes the
+ * table's gradient before adding a sample's rows, so gradE = scale * the rows
+ * of the last sample of each worker chunk (`workers` chunks of ceil(B /
+ * workers); with bad, the last sample the reference's loop still reaches).
+ * At most 2048 contributing rows (chunks x T; GN_ERR_UNSUPPORTED beyond). */
+int gn_embedding_backward(gn_ctx *ctx, const float *gout, const int32_t *ids, const int32_t *bad,
+                          float *gradE, int32_t B, int32_t T, int32_t V, int32_t D, int32_t workers,
+                          float scale);
+
 /* Generic fp32 MFMA GEMM: C[M,N] = alpha * op(A) op(B); trans flags as BLAS
  * (A is M x K row-major when transA == 0, K x M when 1; B is K x N when
  * transB == 0, N x K when 1).  Stands in for matMulMPSPersistent

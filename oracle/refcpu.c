@@ -1937,6 +1937,70 @@ static const float *mha_backward(layer *L, const float *g) {
   return L->gInAtt;
 }
 
+/* MultiHeadAttention as a layer of its own (transformer.go:277-690): four
+ * Linear Dense projections wQ, wK, wV, wOut (each W [D][D] then b), called
+ * per token; Build rebinds them to fresh zero slices (transformer.go:354-380),
+ * so the layer starts at 0. */
+static void mha_build(layer *L) {
+  int32_t d = L->spec.dim, T = L->spec.seq_len;
+  L->D = d;
+  L->T = T;
+  L->NH = L->spec.num_heads;
+  L->sub = (layer *)calloc(4, sizeof(layer));
+  for (int i = 0; i < 4; i++) dense_sub_build(&L->sub[i], d, d, GNO_ACT_LINEAR);
+  L->nparams = 4 * ((int64_t)d * d + d);
+  int64_t td = (int64_t)T * d;
+  L->aq = zalloc(td); L->ak = zalloc(td); L->av = zalloc(td); L->scores = zalloc((int64_t)T * T);
+  L->fin = zalloc(td); L->gfin = zalloc(td); L->gq = zalloc(td); L->gk = zalloc(td); L->gv = zalloc(td);
+  L->attOut = zalloc(td); L->gInAtt = zalloc(td);
+  L->tmpRow = zalloc(T); L->probs = zalloc(T); L->dpre = zalloc(T);
+  L->in_len = L->out_len = (int32_t)td;
+}
+static void mha_bind(layer *L) {
+  int64_t nd = (int64_t)L->D * L->D + L->D;
+  for (int i = 0; i < 4; i++) {
+    L->sub[i].params = L->params + i * nd;
+    L->sub[i].grads = L->grads + i * nd;
+  }
+}
+static void mha_free(layer *L) {
+  for (int i = 0; i < 4 && L->sub; i++) {
+    layer *S = &L->sub[i];
+    free(S->inputBuf); free(S->preActBuf); free(S->outputBuf); free(S->savedOutput);
+    free(S->gradInBuf); free(S->dzBuf);
+  }
+  free(L->sub);
+  float *bufs[] = {L->aq, L->ak, L->av, L->scores, L->fin, L->gfin, L->gq, L->gk, L->gv,
+                   L->attOut, L->gInAtt, L->probs, L->dpre};
+  for (size_t k = 0; k < sizeof bufs / sizeof bufs[0]; k++) free(bufs[k]);
+}
+
+/* LayerNorm as a layer of its own (layernorm.go:43-441): rows of
+ * normalizedShape (spec.dim) of each sample (spec.in_size long), affine
+ * gamma 1 and beta 0 (layernorm.go:83-104), eps as given (spec.eps, 0 =
+ * 1e-5). */
+static void lnl_build(layer *L) {
+  int32_t N = L->spec.dim, rows = L->spec.in_size / (N > 0 ? N : 1);
+  L->ln = (lnorm *)calloc(1, sizeof(lnorm));
+  ln_build(L->ln, N, rows);
+  L->ln->eps = L->spec.eps > 0 ? L->spec.eps : 1e-5f;
+  L->nparams = 2 * (int64_t)N;
+  L->in_len = L->out_len = rows * N;
+}
+static void lnl_bind(layer *L) {
+  int32_t N = L->spec.dim;
+  L->ln->gamma = L->params;
+  L->ln->beta = L->params + N;
+  L->ln->ggamma = L->grads;
+  L->ln->gbeta = L->grads + N;
+}
+static void lnl_init(layer *L) {
+  for (int32_t i = 0; i < L->spec.dim; i++) {
+    L->params[i] = 1.0f;
+    L->params[L->spec.dim + i] = 0.0f;
+  }
+}
+
 /* TransformerBlock.ForwardWithArena (arena-less) transformer.go:1080-1184 */
 static const float *tb_norm_forward(layer *L, int k, const float *x) {
   return L->rn ? rms_forward(&L->rn[k], x, L->T * L->D) : ln_forward(&L->ln[k], x);
@@ -2027,6 +2091,8 @@ static void layer_build(layer *L) {
     case GNO_LAYER_POSENC: pe_build(L); break;
     case GNO_LAYER_CLSPOOL: cls_build(L); break;
     case GNO_LAYER_TRANSFORMER: tb_build(L); break;
+    case GNO_LAYER_MHA: mha_build(L); break;
+    case GNO_LAYER_LAYERNORM: lnl_build(L); break;
     case GNO_LAYER_RMSNORM: rms_build(L); break;
     case GNO_LAYER_SWIGLU: swiglu_build(L); break;
     case GNO_LAYER_BATCHNORM2D: bn_build(L); break;
@@ -2041,7 +2107,8 @@ static void layer_init_params(layer *L) {
   else if (L->kind == GNO_LAYER_LSTM_UNROLLER) lstm_init_params(L);
   else if (L->kind == GNO_LAYER_EMBEDDING) emb_init(L);
   else if (L->kind == GNO_LAYER_POSENC) pe_init(L);
-  else if (L->kind == GNO_LAYER_TRANSFORMER) tb_init(L);
+  else if (L->kind == GNO_LAYER_TRANSFORMER || L->kind == GNO_LAYER_MHA) tb_init(L);
+  else if (L->kind == GNO_LAYER_LAYERNORM) lnl_init(L);
   else if (L->kind == GNO_LAYER_RMSNORM) rms_init(L);
   else if (L->kind == GNO_LAYER_SWIGLU) swiglu_init(L);
   else if (L->kind == GNO_LAYER_BATCHNORM2D) bn_init(L);
@@ -2072,6 +2139,8 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_POSENC: o = pe_forward(L, x); break;
     case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
     case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
+    case GNO_LAYER_MHA: o = mha_forward(L, x); break;
+    case GNO_LAYER_LAYERNORM: o = ln_forward(L->ln, x); break;
     case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
     case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
     case GNO_LAYER_BATCHNORM2D: o = bn_forward(L, x, *len_io); break;
@@ -2094,6 +2163,8 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_POSENC: return pe_backward(L, g);
     case GNO_LAYER_CLSPOOL: return cls_backward(L, g);
     case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
+    case GNO_LAYER_MHA: return mha_backward(L, g);
+    case GNO_LAYER_LAYERNORM: return ln_backward(L->ln, g);
     case GNO_LAYER_RMSNORM: return rms_backward(L, g);
     case GNO_LAYER_SWIGLU: return swiglu_backward(L, g);
     case GNO_LAYER_BATCHNORM2D: return bn_backward(L, g);
@@ -2137,6 +2208,8 @@ gno_net *gno_net_create(const gno_layer_spec *specs, int32_t nlayers, int32_t lo
     L->params = n->params + off;
     L->grads = n->grads + off;
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_bind(L);
+    if (L->kind == GNO_LAYER_MHA) mha_bind(L);
+    if (L->kind == GNO_LAYER_LAYERNORM) lnl_bind(L);
     if (L->kind == GNO_LAYER_MOE) {
       moe_bind(L);
       L->curWorker = &n->cur_worker;
@@ -2161,6 +2234,11 @@ void gno_net_destroy(gno_net *n) {
     for (size_t k = 0; k < sizeof lb / sizeof lb[0]; k++) free(lb[k]);
     free(L->ids);
     if (L->kind == GNO_LAYER_TRANSFORMER) tb_free(L);
+    if (L->kind == GNO_LAYER_MHA) mha_free(L);
+    if (L->kind == GNO_LAYER_LAYERNORM) {
+      ln_free(L->ln);
+      free(L->ln);
+    }
     if (L->kind == GNO_LAYER_MOE) {
       for (int32_t e = 0; e <= L->spec.num_experts; e++) {
         layer *S = &L->sub[e];
@@ -2207,6 +2285,7 @@ static int32_t in_len_of(const gno_net *n) {
     case GNO_LAYER_LSTM_UNROLLER: return L->T * L->spec.in_size;
     case GNO_LAYER_GRU_UNROLLER: return L->T * L->spec.in_size;
     case GNO_LAYER_EMBEDDING: return L->T;
+    case GNO_LAYER_MHA: return L->T * L->D;
     default: return L->spec.in_size;
   }
 }
@@ -2216,6 +2295,8 @@ static void bind_grads(gno_net *n, float *buf) {
   for (int32_t i = 0; i < n->nlayers; i++) {
     n->layers[i].grads = buf + off;
     if (n->layers[i].kind == GNO_LAYER_TRANSFORMER) tb_bind(&n->layers[i]);
+    if (n->layers[i].kind == GNO_LAYER_MHA) mha_bind(&n->layers[i]);
+    if (n->layers[i].kind == GNO_LAYER_LAYERNORM) lnl_bind(&n->layers[i]);
     if (n->layers[i].kind == GNO_LAYER_MOE) moe_bind(&n->layers[i]);
     off += n->layers[i].nparams;
   }
@@ -2232,9 +2313,10 @@ static const float *net_forward(gno_net *n, const float *x, int32_t in_len, int3
   *out_len = len;
   return cur;
 }
-static void net_backward(gno_net *n, const float *g) {
+static const float *net_backward(gno_net *n, const float *g) {
   const float *cur = g;
   for (int32_t i = n->nlayers - 1; i >= 0; i--) cur = layer_backward(&n->layers[i], cur);
+  return cur;
 }
 
 int32_t gno_net_forward(gno_net *n, const float *x, float *out) {
@@ -2262,6 +2344,20 @@ static int run_sample(gno_net *n, const float *x, const float *y, int32_t out_di
   *loss = gno_loss_forward(n->loss_kind, pred, y, ol);
   gno_loss_backward(n->loss_kind, pred, y, n->lossGrad, ol);
   net_backward(n, n->lossGrad);
+  return 0;
+}
+
+/* The same with the output gradient given instead of a loss: the sample's
+ * output and input gradient are copied out (when out / gin are set). */
+static int run_sample_grad(gno_net *n, const float *x, const float *g, float *out, float *gin) {
+  for (int32_t i = 0; i < n->nlayers; i++) layer_reset(&n->layers[i]);
+  int32_t ol, il = in_len_of(n);
+  const float *pred = net_forward(n, x, il, &ol);
+  if (!pred) return -1;
+  if (out) memcpy(out, pred, sizeof(float) * ol);
+  memcpy(n->lossGrad, g, sizeof(float) * ol);
+  const float *gi = net_backward(n, n->lossGrad);
+  if (gin && gi) memcpy(gin, gi, sizeof(float) * il);
   return 0;
 }
 
@@ -2336,6 +2432,51 @@ float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32
   float total = 0.0f;
   for (int32_t w = 0; w < W; w++) total += wl[w];
   return total / (float)B;
+}
+
+/* A batch pass of the network with the output gradient of each sample given
+ * (gout, B x out) in place of a loss: per sample forward (outputs into out),
+ * backward from gout (input gradients into gin), the parameter gradients
+ * accumulated and averaged as in gno_net_accumulate_batch (same worker
+ * chunking).  For testing a layer alone with an arbitrary upstream gradient. */
+void gno_net_accumulate_grad(gno_net *n, const float *x, const float *gout, int32_t B, int32_t od,
+                             float *out, float *gin) {
+  int32_t in = in_len_of(n);
+  for (int64_t i = 0; i < n->nparams; i++) n->grads[i] = 0;
+  if (n->workers <= 1) {
+    float bs = (float)B;
+    bind_grads(n, n->grads);
+    n->cur_worker = 0;
+    for (int32_t i = 0; i < B; i++)
+      run_sample_grad(n, x + (int64_t)i * in, gout + (int64_t)i * od, out ? out + (int64_t)i * od : NULL,
+                      gin ? gin + (int64_t)i * in : NULL);
+    float inv = 1.0f / bs;
+    for (int64_t i = 0; i < n->nparams; i++) n->grads[i] *= inv;
+    return;
+  }
+  int32_t W = n->workers;
+  if (B < W) W = B;
+  int32_t chunk = (B + W - 1) / W;
+  for (int32_t w = 0; w < W; w++) {
+    float *wg = n->worker_grads + (int64_t)w * n->nparams;
+    for (int64_t i = 0; i < n->nparams; i++) wg[i] = 0;
+    int32_t s = w * chunk, e = s + chunk;
+    if (e > B) e = B;
+    if (s >= e) continue;
+    bind_grads(n, wg);
+    n->cur_worker = 1 + w;
+    for (int32_t i = s; i < e; i++)
+      if (run_sample_grad(n, x + (int64_t)i * in, gout + (int64_t)i * od,
+                          out ? out + (int64_t)i * od : NULL, gin ? gin + (int64_t)i * in : NULL))
+        break;
+  }
+  bind_grads(n, n->grads);
+  for (int32_t w = 0; w < W; w++) {
+    float *wg = n->worker_grads + (int64_t)w * n->nparams;
+    for (int64_t i = 0; i < n->nparams; i++) n->grads[i] += wg[i];
+  }
+  float inv = (float)(1.0 / (double)B);
+  for (int64_t i = 0; i < n->nparams; i++) n->grads[i] *= inv;
 }
 
 /* Network.Step net.go:260-284 -> Adam.NewStep + StepInPlace */

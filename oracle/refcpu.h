@@ -76,6 +76,8 @@ enum {
   GNO_LAYER_BATCHNORM2D = 14,
   GNO_LAYER_GRU_UNROLLER = 15,
   GNO_LAYER_MOE = 16,
+  GNO_LAYER_MHA = 17,       /* MultiHeadAttention alone (dim, num_heads, seq_len, causal, use_rope) */
+  GNO_LAYER_LAYERNORM = 18, /* LayerNorm alone (dim = normalizedShape, in_size = sample length, eps) */
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };
@@ -128,6 +130,14 @@ float gno_net_train_batch(gno_net *n, const float *x, const float *y, int32_t B)
  * gradient), for gradient parity checks. */
 float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32_t B);
 void gno_net_step(gno_net *n);
+/* A batch pass with each sample's output gradient given (gout, B x out)
+ * instead of a loss (od = output length per sample): outputs into out and
+ * input gradients into gin (either
+ * may be NULL); parameter gradients accumulated and averaged as by
+ * gno_net_accumulate_batch (same worker chunking).  For testing one layer
+ * against an arbitrary upstream gradient. */
+void gno_net_accumulate_grad(gno_net *n, const float *x, const float *gout, int32_t B, int32_t od,
+                             float *out, float *gin);
 /* Forward of one sample (training flag as set); writes out, returns out len. */
 int32_t gno_net_forward(gno_net *n, const float *x, float *out);
 void gno_net_set_training(gno_net *n, int32_t training);

@@ -22,7 +22,8 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
  ACT_LEAKYRELU) = range(9)
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE) = range(1, 17)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE, LAYER_MHA,
+ LAYER_LAYERNORM) = range(1, 19)
 LOSS_MSE, LOSS_CE = 1, 2
 
 
@@ -82,6 +83,7 @@ def lib():
         L.gno_net_accumulate_batch.argtypes = [C.c_void_p, f32p, f32p, C.c_int32]
         L.gno_net_accumulate_batch.restype = C.c_float
         L.gno_net_step.argtypes = [C.c_void_p]
+        L.gno_net_accumulate_grad.argtypes = [C.c_void_p, f32p, f32p, C.c_int32, C.c_int32, f32p, f32p]
         L.gno_net_forward.argtypes = [C.c_void_p, f32p, f32p]
         L.gno_net_forward.restype = C.c_int32
         L.gno_net_set_training.argtypes = [C.c_void_p, C.c_int32]
@@ -210,6 +212,16 @@ class Net:
         x = np.ascontiguousarray(x, np.float32)
         y = np.ascontiguousarray(y, np.float32)
         return lib().gno_net_accumulate_batch(self.h, fptr(x), fptr(y), B)
+
+    def accumulate_grad(self, x, gout, B, in_len, out_len):
+        """Batch pass with given output gradients: returns (outputs, input
+        gradients); self.grads holds the averaged parameter gradients."""
+        x = np.ascontiguousarray(x, np.float32)
+        gout = np.ascontiguousarray(gout, np.float32)
+        out = np.zeros((B, out_len), np.float32)
+        gin = np.zeros((B, in_len), np.float32)
+        lib().gno_net_accumulate_grad(self.h, fptr(x), fptr(gout), B, out_len, fptr(out), fptr(gin))
+        return out, gin
 
     def step(self):
         lib().gno_net_step(self.h)

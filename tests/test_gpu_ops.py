@@ -1,0 +1,314 @@
+"""GPU tests of the per-layer operators (the batched Layer.Forward / Backward
+entry points of the C ABI) against the oracle's single-layer networks.
+
+Each case builds a one-layer oracle network, runs its batch pass with given
+output gradients (gno_net_accumulate_grad: per-sample Forward and Backward,
+parameter gradients averaged over the batch, the worker chunks of
+trainBatchParallel when workers > 1), and runs the operator pair on the same
+inputs and parameters through ctypes.  Outputs, input gradients and every
+parameter tensor are compared per tensor at 1e-4 of the reference's largest
+magnitude (float32 summation order differs; integer results - argmax, ids,
+masks - bit-exact)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from cfgutil import max_rel
+from gpuutil import DBuf, TOL, log
+
+pytestmark = pytest.mark.gpu
+
+F = C.c_float
+
+
+def _zeros(dev, shape, dtype=np.float32):
+    return DBuf(dev, np.zeros(shape, dtype))
+
+
+def _lib():
+    from goneuron_amd._lib import check, lib
+    return lib(), check
+
+
+def _close(name, got, want, tol=TOL):
+    e = max_rel(got, want)
+    assert e <= tol, (name, e)
+
+
+# ---------------------------------------------------------------- Conv2D
+@pytest.mark.parametrize("B,inC,HW,outC,k,s,p,act", [
+    (8, 3, 32, 16, 3, 1, 1, 1),     # the CNN config's first layer
+    (5, 4, 11, 6, 5, 2, 2, 3),      # 5x5 stride 2, tanh
+    (3, 2, 9, 5, 3, 2, 0, 2),       # no padding, sigmoid
+    (4, 16, 16, 32, 3, 1, 1, 6)])   # linear
+def test_conv2d_ops(dev, oracle, B, inC, HW, outC, k, s, p, act):
+    L, check = _lib()
+    log(f"conv2d B={B} inC={inC} HW={HW} outC={outC} k={k} s={s} p={p} act={act}")
+    n_in = inC * HW * HW
+    net = oracle.Net([oracle.spec(oracle.LAYER_CONV2D, in_size=n_in, in_channels=inC, out_channels=outC,
+                                  kernel=k, stride=s, padding=p, act=act)], oracle.LOSS_MSE)
+    oH = (HW + 2 * p - k) // s + 1
+    n_out = outC * oH * oH
+    rng = np.random.default_rng(B * 7 + HW)
+    x = rng.normal(size=(B, n_in)).astype(np.float32)
+    g = rng.normal(size=(B, n_out)).astype(np.float32)
+    params = net.params.copy()
+    out_r, gin_r = net.accumulate_grad(x, g, B, n_in, n_out)
+    grads_r = net.grads.copy()
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, params), DBuf(dev, g)
+    dout, dgr, dgin = _zeros(dev, (B, n_out)), _zeros(dev, params.shape), _zeros(dev, (B, n_in))
+    check(dev.h, L.gn_conv2d_forward(dev.h, dx.p, dp.p, dout.p, B, inC, HW, HW, outC, k, s, p, act))
+    check(dev.h, L.gn_conv2d_backward(dev.h, dx.p, dp.p, dout.p, dg.p, dgr.p, dgin.p, B, inC, HW, HW,
+                                      outC, k, s, p, act, F(np.float32(1) / np.float32(B))))
+    nw = outC * inC * k * k
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    gr = dgr.get()
+    _close("dW", gr[:nw], grads_r[:nw])
+    _close("db", gr[nw:], grads_r[nw:])
+
+
+def test_conv2d_ops_reject_bad_geometry(dev):
+    L, _ = _lib()
+    rc = L.gn_conv2d_forward(dev.h, None, None, None, 1, 1, 2, 2, 1, 5, 1, 0, 1)
+    assert rc != 0
+    x, w, o = _zeros(dev, 4), _zeros(dev, 26), _zeros(dev, 4)
+    assert L.gn_conv2d_forward(dev.h, x.p, w.p, o.p, 1, 1, 2, 2, 1, 5, 1, 0, 1) == -5  # GN_ERR_SHAPE
+
+
+# ---------------------------------------------------------------- MaxPool2D
+@pytest.mark.parametrize("B,C_,HW,k,s,p", [(8, 16, 32, 2, 2, 0), (3, 4, 9, 3, 2, 1), (2, 3, 7, 3, 1, 1)])
+def test_maxpool2d_ops(dev, oracle, B, C_, HW, k, s, p):
+    L, check = _lib()
+    log(f"maxpool2d B={B} C={C_} HW={HW} k={k} s={s} p={p}")
+    n_in = C_ * HW * HW
+    net = oracle.Net([oracle.spec(oracle.LAYER_MAXPOOL2D, in_size=n_in, in_channels=C_, kernel=k,
+                                  stride=s, padding=p)], oracle.LOSS_MSE)
+    oH = (HW + 2 * p - k) // s + 1
+    n_out = C_ * oH * oH
+    rng = np.random.default_rng(HW * 3 + k)
+    # ties in a few windows: the first maximum wins
+    x = rng.integers(-3, 4, size=(B, n_in)).astype(np.float32)
+    g = rng.normal(size=(B, n_out)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, n_in, n_out)
+    am_last = net.argmax(0)
+    dx, dg = DBuf(dev, x), DBuf(dev, g)
+    dout, dam, dgin = _zeros(dev, (B, n_out)), _zeros(dev, (B, n_out), np.int32), _zeros(dev, (B, n_in))
+    check(dev.h, L.gn_maxpool2d_forward(dev.h, dx.p, dout.p, dam.p, B, C_, HW, HW, k, s, p))
+    check(dev.h, L.gn_maxpool2d_backward(dev.h, dg.p, dam.p, dgin.p, B, C_, HW, HW, k, s, p))
+    np.testing.assert_array_equal(dout.get(), out_r)
+    np.testing.assert_array_equal(dam.get()[-1], am_last[:n_out])
+    _close("gin", dgin.get(), gin_r, 1e-6)
+
+
+# ---------------------------------------------------------------- Dropout
+@pytest.mark.parametrize("B,n,p", [(16, 128, 0.2), (5, 1000, 0.5), (3, 77, 0.0)])
+@pytest.mark.parametrize("training", [1, 0])
+def test_dropout_ops(dev, oracle, B, n, p, training):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_DROPOUT, in_size=n, p=p)], oracle.LOSS_MSE)
+    net.set_training(training)
+    rng = np.random.default_rng(n)
+    x = rng.normal(size=(B, n)).astype(np.float32)
+    g = rng.normal(size=(B, n)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, n, n)
+    dx, dg = DBuf(dev, x), DBuf(dev, g)
+    dout, dmask, dgin = _zeros(dev, (B, n)), _zeros(dev, n), _zeros(dev, (B, n))
+    check(dev.h, L.gn_dropout_forward(dev.h, dx.p, dout.p, dmask.p, B, n, F(p), training))
+    check(dev.h, L.gn_dropout_backward(dev.h, dg.p, dmask.p, dgin.p, B, n, F(p), training))
+    np.testing.assert_array_equal(dout.get(), out_r)
+    np.testing.assert_array_equal(dgin.get(), gin_r)
+    if training:
+        m = dmask.get()
+        assert set(np.unique(m)) <= {0.0, 1.0}
+        np.testing.assert_array_equal(m == 0, out_r[0] == 0)  # x has no exact zeros
+
+
+# ---------------------------------------------------------------- output layer + loss
+@pytest.mark.parametrize("B,I,Cn,act,ptr,loss", [
+    (64, 32, 10, 4, 1, 2),   # pointer Softmax + CrossEntropy (the MLP head)
+    (17, 20, 7, 5, 1, 2),    # pointer LogSoftmax + CrossEntropy
+    (9, 12, 5, 6, 0, 1),     # Linear + MSE
+    (12, 16, 6, 2, 0, 1),    # Sigmoid + MSE
+    (8, 10, 4, 4, 0, 2)])    # value Softmax (identity forward, NaN derivative) + CE
+def test_softmax_ce_backward(dev, oracle, B, I, Cn, act, ptr, loss):
+    """The oracle's Dense(I, Cn) head with the loss: its averaged weight
+    gradient is scale * dz^T x, so dz from the operator (on the same
+    pre-activations) reproduces it; the mean of loss_rows is the batch loss."""
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_DENSE, in_size=I, out_size=Cn, act=act, act_is_ptr=ptr)],
+                     loss)
+    rng = np.random.default_rng(B * Cn)
+    x = rng.normal(size=(B, I)).astype(np.float32)
+    if loss == 2:
+        y = np.zeros((B, Cn), np.float32)
+        y[np.arange(B), rng.integers(0, Cn, size=B)] = 1
+    else:
+        y = rng.normal(size=(B, Cn)).astype(np.float32)
+    lo = net.accumulate_batch(x, y, B)
+    gr = net.grads.copy()
+    W, b = net.params[:Cn * I].reshape(Cn, I), net.params[Cn * I:]
+    dx, dW, db, dy = DBuf(dev, x), DBuf(dev, W.copy()), DBuf(dev, b.copy()), DBuf(dev, y)
+    dzo, ddz, dl = _zeros(dev, (B, Cn)), _zeros(dev, (B, Cn)), _zeros(dev, B)
+    check(dev.h, L.gn_dense_forward(dev.h, dx.p, dW.p, db.p, dzo.p, B, I, Cn, 6, 0))  # pre-activations
+    check(dev.h, L.gn_softmax_ce_backward(dev.h, dzo.p, dy.p, ddz.p, dl.p, B, Cn, act, ptr, loss))
+    dz = ddz.get().astype(np.float64)
+    rows = dl.get()
+    if act == 4 and not ptr:  # NaN derivative: every gradient NaN on both sides
+        assert np.isnan(dz).all() and np.isnan(gr).all()
+        assert abs(rows.mean() - lo) <= TOL * abs(lo)
+        return
+    assert abs(rows.astype(np.float64).mean() - lo) <= TOL * abs(lo), (rows.mean(), lo)
+    _close("dW", (dz.T @ x.astype(np.float64) / B).ravel(), gr[:Cn * I])
+    _close("db", dz.sum(0) / B, gr[Cn * I:])
+
+
+# ---------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("B,rows,N,eps", [(8, 16, 64, 1e-5), (3, 5, 10, 1e-3), (4, 1, 300, 0.0)])
+def test_layernorm_ops(dev, oracle, B, rows, N, eps):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_LAYERNORM, dim=N, in_size=rows * N, eps=eps)],
+                     oracle.LOSS_MSE)
+    rng = np.random.default_rng(rows * N)
+    p = np.concatenate([1 + 0.3 * rng.normal(size=N), 0.3 * rng.normal(size=N)]).astype(np.float32)
+    net.params[:] = p
+    x = (rng.normal(size=(B, rows * N)) * 2 + 0.5).astype(np.float32)
+    g = rng.normal(size=(B, rows * N)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, rows * N, rows * N)
+    gr = net.grads.copy()
+    R = B * rows
+    dx, dgam, dbet, dg = DBuf(dev, x), DBuf(dev, p[:N]), DBuf(dev, p[N:]), DBuf(dev, g)
+    dy, dst, ddx = _zeros(dev, (B, rows * N)), _zeros(dev, 2 * R), _zeros(dev, (B, rows * N))
+    dgg, dgb, dwk = _zeros(dev, N), _zeros(dev, N), _zeros(dev, (R, N))
+    check(dev.h, L.gn_layernorm_forward(dev.h, dx.p, dgam.p, dbet.p, dy.p, dst.p, R, N, F(eps)))
+    check(dev.h, L.gn_layernorm_backward(dev.h, dg.p, dx.p, dgam.p, dst.p, ddx.p, dgg.p, dgb.p, dwk.p,
+                                         R, N, F(np.float32(1) / np.float32(B))))
+    _close("out", dy.get(), out_r)
+    _close("gin", ddx.get(), gin_r)
+    _close("dgamma", dgg.get(), gr[:N])
+    _close("dbeta", dgb.get(), gr[N:])
+
+
+# ---------------------------------------------------------------- MultiHeadAttention
+@pytest.mark.parametrize("B,T,D,NH,causal,rope", [
+    (4, 16, 64, 4, 1, 0), (3, 32, 64, 2, 0, 0), (2, 12, 48, 3, 1, 1), (5, 8, 32, 1, 0, 1)])
+def test_mha_ops(dev, oracle, B, T, D, NH, causal, rope):
+    L, check = _lib()
+    log(f"mha B={B} T={T} D={D} heads={NH} causal={causal} rope={rope}")
+    net = oracle.Net([oracle.spec(oracle.LAYER_MHA, dim=D, num_heads=NH, seq_len=T, causal=causal,
+                                  use_rope=rope)], oracle.LOSS_MSE)
+    rng = np.random.default_rng(T * D + NH)
+    p = (rng.normal(size=net.n) * (0.5 / np.sqrt(D))).astype(np.float32)
+    net.params[:] = p
+    x = rng.normal(size=(B, T * D)).astype(np.float32)
+    g = rng.normal(size=(B, T * D)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, T * D, T * D)
+    gr = net.grads.copy()
+    ws = C.c_int64()
+    check(None, L.gn_mha_workspace(B, T, D, NH, rope, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = (_zeros(dev, (B, T * D)), _zeros(dev, p.shape), _zeros(dev, (B, T * D)),
+                            _zeros(dev, ws.value))
+    check(dev.h, L.gn_mha_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, D, NH, causal, rope))
+    check(dev.h, L.gn_mha_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, T, D, NH, causal,
+                                   rope, F(np.float32(1) / np.float32(B))))
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    got = dgr.get()
+    nd = D * D + D
+    scale = np.abs(gr).max()
+    for i, name in enumerate(("wQ", "wK", "wV", "wOut")):
+        for part, sl in (("W", slice(i * nd, i * nd + D * D)), ("b", slice(i * nd + D * D, (i + 1) * nd))):
+            ref = gr[sl]
+            if np.abs(ref).max() <= 1e-6 * scale:  # wK without RoPE: the softmax rows sum it to zero
+                assert np.abs(got[sl]).max() <= 1e-5 * scale, (name, part)
+                continue
+            _close(name + "." + part, got[sl], ref)
+
+
+def test_mha_ops_reject_unsupported(dev):
+    L, _ = _lib()
+    x = _zeros(dev, 8)
+    assert L.gn_mha_forward(dev.h, x.p, x.p, x.p, x.p, 1, 256, 64, 2, 0, 0) == -4  # GN_ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------- SequenceUnroller(LSTM)
+@pytest.mark.parametrize("B,T,I,H,workers,gscale", [
+    (6, 10, 8, 16, 1, 1e-3),   # clip inactive
+    (6, 10, 8, 16, 1, 3.0),    # clip active on one chain
+    (8, 7, 5, 12, 4, 3.0),     # four worker chains, clip active
+    (5, 12, 6, 32, 2, 0.3)])
+def test_lstm_seq_ops(dev, oracle, B, T, I, H, workers, gscale):
+    L, check = _lib()
+    log(f"lstm B={B} T={T} I={I} H={H} workers={workers} gscale={gscale}")
+    net = oracle.Net([oracle.spec(oracle.LAYER_LSTM_UNROLLER, in_size=I, out_size=H, seq_len=T)],
+                     oracle.LOSS_MSE, workers=workers)
+    rng = np.random.default_rng(T * H + workers)
+    p = (rng.normal(size=net.n) * 0.3).astype(np.float32)  # every gate live
+    net.params[:] = p
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    g = (rng.normal(size=(B, H)) * gscale).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, T * I, H)
+    gr = net.grads.copy()
+    ws = C.c_int64()
+    check(None, L.gn_lstm_workspace(B, T, I, H, workers, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = (_zeros(dev, (B, H)), _zeros(dev, p.shape), _zeros(dev, (B, T * I)),
+                            _zeros(dev, ws.value))
+    check(dev.h, L.gn_lstm_seq_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, I, H))
+    check(dev.h, L.gn_lstm_seq_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, T, I, H, workers,
+                                        F(np.float32(1) / np.float32(B))))
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    got = dgr.get()
+    nwx, nwh = 4 * H * I, 4 * H * H
+    for gi, gname in enumerate("ifgo"):
+        for part, sl in (("Wx", slice(gi * H * I, (gi + 1) * H * I)),
+                         ("Wh", slice(nwx + gi * H * H, nwx + (gi + 1) * H * H)),
+                         ("b", slice(nwx + nwh + gi * H, nwx + nwh + (gi + 1) * H))):
+            _close(part + "_" + gname, got[sl], gr[sl])
+
+
+# ---------------------------------------------------------------- Embedding
+@pytest.mark.parametrize("B,T,V,D,workers,bad", [
+    (8, 16, 100, 32, 1, False), (10, 6, 50, 16, 4, False), (9, 5, 40, 8, 3, True), (7, 4, 30, 8, 1, True)])
+def test_embedding_ops(dev, oracle, B, T, V, D, workers, bad):
+    """Forward rows bit-exact; the table gradient is the last sample of each
+    worker chunk (Backward zeroes it first).  With an out-of-range id in some
+    samples, `bad` flags them; the sequential loop skips them (continue) and
+    a worker stops at its first one."""
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_EMBEDDING, in_size=T, vocab=V, dim=D)], oracle.LOSS_MSE,
+                     workers=workers)
+    rng = np.random.default_rng(B * T + V)
+    ids = rng.integers(0, V, size=(B, T))
+    if bad:
+        ids[1, 2] = V + 3
+        ids[B - 1, 0] = -1
+    x = ids.astype(np.float32)
+    g = rng.normal(size=(B, T * D)).astype(np.float32)
+    E = net.params.copy()
+    out_r, _ = net.accumulate_grad(x, g, B, T, T * D)
+    gr = net.grads.copy()
+    dxb, dE, dg = DBuf(dev, x), DBuf(dev, E), DBuf(dev, g)
+    dout, dids, dbad, dgE = (_zeros(dev, (B, T * D)), _zeros(dev, (B, T), np.int32), _zeros(dev, B, np.int32),
+                             _zeros(dev, E.shape))
+    check(dev.h, L.gn_embedding_forward(dev.h, dxb.p, dE.p, dout.p, dids.p, dbad.p, B, T, V, D))
+    check(dev.h, L.gn_embedding_backward(dev.h, dg.p, dids.p, dbad.p, dgE.p, B, T, V, D, workers,
+                                         F(np.float32(1) / np.float32(B))))
+    flags = dbad.get()
+    want_bad = ((ids < 0) | (ids >= V)).any(1).astype(np.int32)
+    np.testing.assert_array_equal(flags, want_bad)
+    # samples the reference's loop runs: all good ones when sequential; in a
+    # worker chunk, those before its first bad sample
+    ok = want_bad == 0
+    if workers > 1:
+        chunk = -(-B // min(workers, B))
+        for c0 in range(0, B, chunk):
+            hit = np.nonzero(want_bad[c0:c0 + chunk])[0]
+            if hit.size:
+                ok[c0 + hit[0]:c0 + chunk] = False
+    np.testing.assert_array_equal(dout.get()[ok], out_r[ok])
+    np.testing.assert_array_equal(dids.get()[ok], ids[ok])
+    _close("gradE", dgE.get(), gr, 1e-6)

@@ -136,6 +136,31 @@ def test_lstm_bptt_with_clip_active(oracle, workers):
     _check_parts(g, ref, _lstm_parts(I, H))
 
 
+@pytest.mark.parametrize("T,I,H,B,workers", [(6, 5, 7, 3, 1), (8, 4, 6, 4, 2)])
+def test_lstm_input_gradient_vs_autograd(oracle, T, I, H, B, workers):
+    """The unroller's input gradient (lstm.go:642-663, unroller.go:189-206):
+    dx_t = Wx^T dG_t over all four gates with autograd's per-step
+    pre-activation gradients dG_t, the clip (which scales parameter
+    gradients only) acting or not.  The output gradient given to the oracle
+    is the per-sample MSE gradient 2 (pred - y) of the torch model's loss."""
+    rng = np.random.default_rng(300 + T)
+    p = _lstm_params(rng, I, H)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    y = (rng.normal(size=B) * 5).astype(np.float32)
+    net = _lstm_net(oracle, I, H, T, workers=workers)
+    net.params[:] = p
+    preds = np.array([net.forward(x[b])[0] for b in range(B)], np.float32)
+    gout = (2 * (preds - y)).astype(np.float32).reshape(B, 1)
+    _, gin = net.accumulate_grad(x, gout, B, T * I, 1)
+    _, _, dpre, _ = _lstm_torch(p, x, y, I, H, T, keep_pre=True)
+    Wx = p[:4 * H * I].astype(np.float64).reshape(4 * H, I)
+    ref = np.stack([np.stack([dpre[t][b] @ Wx for t in range(T)]) for b in range(B)]).reshape(B, T * I)
+    assert max_rel(gin, ref) <= 1e-4, max_rel(gin, ref)
+    # the input gate alone (a dropped gate sum) or the own-step weights differ
+    only_i = np.stack([np.stack([dpre[t][b][:H] @ Wx[:H] for t in range(T)]) for b in range(B)])
+    assert max_rel(gin, only_i.reshape(B, T * I)) > 1e-2
+
+
 def _gru_parts(I, H):
     nwx, nwh = 3 * H * I, 2 * H * H
     parts = {}
