@@ -54,11 +54,11 @@ def gemm_traffic_per_launch():
 
 def kernel_bound(name):
     """(bound, peak, unit) a kernel is judged against."""
-    if name.startswith("gemm_") or name in ("attn_fwd", "attn_bwd", "conv_wgrad"):
+    if name.startswith("gemm_") or name in ("attn_fwd", "attn_bwd", "conv_wgrad", "conv_dgrad"):
         return "mfma", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
     if name == "lstm_gram":
         return "mfma_fp64", PEAK_FP64_MFMA_TFLOPS, "TFLOP/s"
-    if name in ("conv_fwd", "conv_dgrad", "lstm_fwd", "lstm_bptt", "gru_fwd", "gru_bwd"):
+    if name in ("conv_fwd", "lstm_fwd", "lstm_bptt", "gru_fwd", "gru_bwd"):
         # fp32 VALU / latency-bound recurrences: FLOP rate against the fp32 peak
         return "valu", PEAK_FP32_MFMA_TFLOPS, "TFLOP/s"
     return "hbm", PEAK_HBM_GBPS, "GB/s"
@@ -192,7 +192,7 @@ def run_config(name, args, dev, with_cpu, cpu_budget, threads):
     from goneuron_amd import configs
     from goneuron_amd._lib import lib, check
     L = lib()
-    cfg = configs.CONFIGS[name]()
+    cfg = configs.get(name)
     B = cfg["B"]
     x, y = configs.inputs(cfg)
     workers = configs.gpu_workers(B)
@@ -282,7 +282,7 @@ def predict_bench(args, dev):
     from goneuron_amd import configs
     from goneuron_amd._lib import lib, check
     L = lib()
-    cfg = configs.CONFIGS[args.config]()
+    cfg = configs.get(args.config)
     B = cfg["B"]
     x, _ = configs.inputs(cfg)
     model = configs.build(cfg, device=dev)
@@ -329,8 +329,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm"],
-                    help="headline workload (the `value` of the line)")
+    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm", "gru", "cnn2"],
+                    help="headline workload (the `value` of the line); gru and cnn2 are not "
+                         "BASELINE configs")
     ap.add_argument("--only", action="store_true", help="time the headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
@@ -366,7 +367,7 @@ def main():
             if name != args.config:
                 others[name] = run_config(name, args, dev, not args.no_cpu, args.cpu_budget, threads)
                 print(f"bench: {name} {others[name]['value']:.0f} samples/s", file=sys.stderr, flush=True)
-    cfg = configs.CONFIGS[args.config]()
+    cfg = configs.get(args.config)
     K = args.steps
     g = head["gemm"]
     traffic = gemm_traffic_per_launch() if args.config == "wide" else None

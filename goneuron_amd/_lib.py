@@ -94,6 +94,8 @@ SIGNATURES = {
     "gn_model_set_training": (C.c_int, [vp, C.c_int32]),
     "gn_model_get_training": (C.c_int, [vp, C.c_int32, i32p]),
     "gn_model_reserve": (C.c_int, [vp, C.c_int32]),
+    "gn_model_set_graphs": (C.c_int, [vp, C.c_int32]),
+    "gn_model_graph_count": (C.c_int, [vp, i32p]),
     "gn_model_skipped_samples": (C.c_int, [vp, i32p]),
     "gn_model_layer_output": (C.c_int, [vp, C.c_int32, f32p, C.c_int64]),
     "gn_model_layer_argmax": (C.c_int, [vp, C.c_int32, i32p, C.c_int64]),

@@ -78,7 +78,25 @@ def gru(B=64, T=100, inp=64, hidden=256):
                         dense(hidden, 1, "linear")])
 
 
+def cnn2(B=128):
+    """C2 with a second 16 -> 16 Conv2D below the pooling (not a BASELINE
+    config): the second conv's input gradient runs every step."""
+    return dict(num=7, name="cnn2", B=B, loss="ce", lr=1e-3, x="normal", in_len=3 * 32 * 32,
+                classes=10,
+                layers=[{"kind": "conv2d", "inC": 3, "outC": 16, "k": 3, "s": 1, "p": 1, "act": "relu"},
+                        {"kind": "conv2d", "inC": 16, "outC": 16, "k": 3, "s": 1, "p": 1, "act": "relu"},
+                        {"kind": "maxpool2d", "k": 2, "s": 2, "p": 0, "inC": 16},
+                        {"kind": "flatten", "n": 4096},
+                        dense(4096, 10, "softmax", True)])
+
+
 CONFIGS = {"mlp": mlp, "cnn": cnn, "wide": wide, "gpt": gpt, "lstm": lstm}
+# further workloads bench.py times on request (--config), outside the default line
+EXTRA = {"gru": gru, "cnn2": cnn2}
+
+
+def get(name):
+    return (CONFIGS.get(name) or EXTRA[name])()
 
 
 def inputs(cfg, B=None):

@@ -546,7 +546,27 @@ struct gn_model {
   bool overlap_adam = true;
   std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
   std::vector<hipEvent_t> dz_ev;    // one per layer: its dz is ready (no timing)
+  // HIP graphs of the accumulate pass (forward, loss, backward) of small
+  // models, keyed by the input pointers, the batch and the training flags in
+  // effect: the first step with a key runs eagerly, the second is captured,
+  // later ones replay.  Adam runs after the graph as an ordinary launch (its
+  // coefficients change every step).
+  struct StepGraph {
+    const float *x, *y;
+    int B;
+    std::vector<char> eff;
+    hipGraphExec_t exec;
+  };
+  std::vector<StepGraph> graphs;
+  bool graph_on = true;   // gn_model_set_graphs
+  bool graph_ok = true;   // false once a capture failed: eager from then on
 };
+
+static void drop_graphs(gn_model *M) {
+  for (auto &g : M->graphs)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  M->graphs.clear();
+}
 
 // Adam coefficients of one Network.Step: Adam.NewStep increments the
 // timestep before the update, whose bias corrections use timestep + 1
@@ -586,6 +606,7 @@ extern "C" void gn_model_destroy(gn_model *M) {
   (void)hipSetDevice(M->ctx->device);
   (void)hipStreamSynchronize(M->ctx->stream);
   (void)hipStreamSynchronize(M->ctx->aux);
+  drop_graphs(M);
   for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
   for (void *p : M->bowned) (void)hipFree(p);
@@ -1164,6 +1185,7 @@ extern "C" int gn_model_reserve(gn_model *M, int32_t max_batch) {
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
   const int old = M->maxB;
+  drop_graphs(M);  // they hold the old batch buffers
   free_batch(M);
   M->maxB = max_batch;
   int rc = alloc_batch(M);
@@ -2137,6 +2159,65 @@ extern "C" int gn_model_step(gn_model *M) {
   return GN_OK;
 }
 
+// Steps whose launches can be replayed from a graph: no timing events, no
+// host-advanced per-step state (MoE gating noise streams, the LSTM's
+// cooperative BPTT epochs).
+static bool graph_eligible(const gn_model *M) {
+  if (!M->graph_on || !M->graph_ok || M->ctx->timing) return false;
+  for (const LayerRT &R : M->L)
+    if (R.d.kind == GN_LAYER_MOE || R.d.kind == GN_LAYER_LSTM_UNROLLER) return false;
+  return true;
+}
+
+static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B) {
+  gn_ctx *c = M->ctx;
+  if (B <= 0 || B > M->maxB) return set_err(c, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
+  if (!x || !y) return set_err(c, GN_ERR_INVALID, "null input");
+  int rc = pass_flags(M, B, true);
+  if (rc) return rc;
+  gn_model::StepGraph *g = nullptr;
+  for (auto &e : M->graphs)
+    if (e.x == x && e.y == y && e.B == B && e.eff == M->eff) g = &e;
+  if (g && g->exec) {  // replay: the host state the pass would have set
+    M->last_predict = false;
+    M->last_B = B;
+    HIP_OK(c, hipGraphLaunch(g->exec, c->stream));
+    return GN_OK;
+  }
+  if (!g) {  // first step with this key: eager (also settles every lazy set-up)
+    rc = model_accumulate(M, x, y, B);
+    if (rc) return rc;
+    if (M->graphs.size() >= 4) {  // keep the 4 newest keys
+      if (M->graphs.front().exec) (void)hipGraphExecDestroy(M->graphs.front().exec);
+      M->graphs.erase(M->graphs.begin());
+    }
+    M->graphs.push_back({x, y, B, M->eff, nullptr});
+    return GN_OK;
+  }
+  // second step with this key: capture the pass, then launch it
+  hipGraph_t graph = nullptr;
+  HIP_OK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  rc = model_accumulate(M, x, y, B);
+  hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  if (rc == GN_OK && e == hipSuccess && graph) {
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e == hipSuccess) {
+      g->exec = ex;
+      HIP_OK(c, hipGraphLaunch(ex, c->stream));
+      return GN_OK;
+    }
+  } else if (graph) {
+    (void)hipGraphDestroy(graph);
+  }
+  // the capture failed: nothing of it ran; this model stays eager from now on
+  (void)hipGetLastError();
+  M->graph_ok = false;
+  drop_graphs(M);
+  return model_accumulate(M, x, y, B);
+}
+
 // One training step: forward, loss, backward and Adam (Network.TrainBatch
 // followed by Network.Step).  Per-layer updates overlapped with the backward
 // pass pay off only when the update is long; small models update once at the
@@ -2144,7 +2225,7 @@ extern "C" int gn_model_step(gn_model *M) {
 constexpr int64_t kOverlapAdamMin = (int64_t)8 << 20;
 static int model_train_step(gn_model *M, const float *x, const float *y, int B) {
   if (!M->overlap_adam || M->nparams < kOverlapAdamMin) {
-    int rc = model_accumulate(M, x, y, B);
+    int rc = graph_eligible(M) ? accumulate_graphed(M, x, y, B) : model_accumulate(M, x, y, B);
     if (rc) return rc;
     return gn_model_step(M);
   }
@@ -2228,6 +2309,23 @@ extern "C" int gn_model_skipped_samples(gn_model *M, int32_t *n) {
   int rc = check_flags(M);
   if (rc) return rc;
   *n = M->skipped;
+  return GN_OK;
+}
+
+extern "C" int gn_model_set_graphs(gn_model *M, int32_t on) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
+  M->graph_on = on != 0;
+  if (!M->graph_on) drop_graphs(M);
+  return GN_OK;
+}
+
+extern "C" int gn_model_graph_count(gn_model *M, int32_t *n) {
+  if (!M || !n) return GN_ERR_INVALID;
+  int k = 0;
+  for (const auto &g : M->graphs) k += g.exec ? 1 : 0;
+  *n = k;
   return GN_OK;
 }
 

@@ -14,7 +14,9 @@
 // element sums the gradients of the windows whose argmax points at it, in
 // increasing output position -- the order the reference's scatter adds them.
 // Conv2D weight/bias gradients are an implicit GEMM over (sample, position)
-// reduced per block and then across blocks in a fixed order.
+// reduced per block and then across blocks in a fixed order.  The input
+// gradient (the transposed convolution of conv2d.go:1117-1168) is an implicit
+// GEMM over (oc, kh, kw) for stride 1, a per-element gather otherwise.
 #include "gn_common.h"
 
 #include <algorithm>
@@ -333,6 +335,92 @@ __global__ __launch_bounds__(CT) void conv2d_dgrad_kernel(const float *__restric
   }
 }
 
+// Conv2D input gradient on fp32 MFMA for stride 1: an implicit GEMM per block
+// (one sample, a band of input rows)
+//   gin[ic][pos] = sum over tap = (oc, kh, kw) of W[oc][ic][kh][kw] * dzcol[tap][pos],
+//   dzcol[(oc, kh, kw)][(ih, iw)] = dz[oc][ih + pad - kh][iw + pad - kw]
+// (zero outside the output plane).  The band's dz rows with a k - 1 halo on
+// each side (dz = gout * act'(out), zero padded) and W in tap-major order sit
+// in LDS; each wave takes 32 x 32 (channel, position) tiles over the whole K,
+// and the 32 lanes of a tile column store 32 consecutive positions of one
+// input plane.
+__global__ __launch_bounds__(CT) void conv2d_dgrad_mfma(const float *__restrict__ gout,
+                                                        const float *__restrict__ out,
+                                                        const float *__restrict__ w,
+                                                        float *__restrict__ gin, ConvShape s,
+                                                        int band_rows, int deriv) {
+  extern __shared__ float sm[];
+  const int bands = (s.H + band_rows - 1) / band_rows;
+  const int b = blockIdx.x / bands, band = blockIdx.x % bands;
+  const int ih0 = band * band_rows, R = min(s.H, ih0 + band_rows) - ih0;
+  const int k = s.k, km = k - 1, kk = k * k;
+  const int Rz = band_rows + km, Wz = s.W + km;
+  const int ntap = s.outC * kk, ntp = (ntap + 7) & ~7;   // K padded with zero taps
+  float *dzb = sm;                                         // [outC][Rz][Wz]
+  float *wt = dzb + s.outC * Rz * Wz;                      // [ntp][inC]
+  int *toff = reinterpret_cast<int *>(wt + ntp * s.inC);   // [ntp] LDS offset of a tap
+  const int osz = s.oH * s.oW;
+  const int oh0 = ih0 + s.pad - km, ow0 = s.pad - km;
+  for (int e = threadIdx.x; e < s.outC * Rz * Wz; e += CT) {
+    const int c = e % Wz, r = (e / Wz) % Rz, oc = e / (Wz * Rz);
+    const int oh = oh0 + r, ow = ow0 + c;
+    float v = 0.f;
+    if (oh >= 0 && oh < s.oH && ow >= 0 && ow < s.oW) {
+      const int64_t gi = ((int64_t)b * s.outC + oc) * osz + oh * s.oW + ow;
+      v = gout[gi] * act_deriv(out[gi], deriv);
+    }
+    dzb[e] = v;
+  }
+  for (int e = threadIdx.x; e < ntp * s.inC; e += CT) {
+    const int tap = e / s.inC, ic = e - tap * s.inC;
+    float v = 0.f;
+    if (tap < ntap) {
+      const int oc = tap / kk, kh = (tap / k) % k, kw = tap % k;
+      v = w[((oc * s.inC + ic) * k + kh) * k + kw];
+    }
+    wt[e] = v;
+  }
+  for (int t = threadIdx.x; t < ntp; t += CT) {
+    int o = 0;
+    if (t < ntap) {
+      const int oc = t / kk, kh = (t / k) % k, kw = t % k;
+      o = (oc * Rz + km - kh) * Wz + km - kw;
+    }
+    toff[t] = o;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int P = R * s.W;
+  const int mtiles = (s.inC + 31) / 32, ntiles = (P + 31) / 32;
+  const int64_t gbase = ((int64_t)b * s.inC * s.H + ih0) * s.W;  // (b, ic = 0, ih0, 0)
+  for (int tile = wv; tile < mtiles * ntiles; tile += CT / 64) {
+    const int mt = tile / ntiles, nt = tile - mt * ntiles;
+    const int ic = mt * 32 + (lane & 31);
+    const bool icv = ic < s.inC;
+    const int pos = nt * 32 + (lane & 31);
+    const int poff = pos < P ? (pos / s.W) * Wz + pos % s.W : 0;
+    cfx16 acc = cfx16{};
+    for (int q0 = 0; q0 < ntp; q0 += 8) {  // the operands of 4 MFMAs loaded ahead of them
+      float a[4], bv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = q0 + 2 * u + (lane >> 5);
+        a[u] = icv ? wt[q * s.inC + ic] : 0.f;
+        bv[u] = dzb[toff[q] + poff];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u], bv[u], acc, 0, 0, 0);
+    }
+    if (pos < P) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < s.inC) gin[gbase + (int64_t)row * s.H * s.W + pos] = acc[r];
+      }
+    }
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   int64_t b = (n + CT - 1) / CT;
   if (b > 65536) b = 65536;
@@ -470,6 +558,23 @@ hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out
 
 hipError_t launch_conv_dgrad(const float *gout, const float *out, const float *w, float *gin,
                              const ConvShape &s, int B, int deriv, hipStream_t st) {
+  if (s.stride == 1) {  // MFMA implicit GEMM: bands of input rows, >= 4 blocks per CU
+    const int km = s.k - 1, ntap = s.outC * s.k * s.k, ntp = (ntap + 7) & ~7;
+    auto lds = [&](int band) {
+      return ((size_t)s.outC * (band + km) * (s.W + km) + (size_t)ntp * s.inC + ntp) * sizeof(float);
+    };
+    int band = s.H;
+    while (band > 1 && (lds(band) > 32768 || (int64_t)B * ((s.H + band - 1) / band) < 1024))
+      band = (band + 1) / 2;
+    if (lds(band) <= 65536) {
+      const int64_t nblocks = (int64_t)B * ((s.H + band - 1) / band);
+      if (nblocks > 0x7fffffff) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(conv2d_dgrad_mfma, dim3((unsigned)nblocks), dim3(CT), lds(band), st, gout, out,
+                         w, gin, s, band, deriv);
+      return hipGetLastError();
+    }
+  }
+  // strided convolutions, and shapes whose band does not fit: per-element gather
   const int64_t n = (int64_t)B * s.inC * s.H * s.W;
   hipLaunchKernelGGL(conv2d_dgrad_kernel, dim3(grid_for(n)), dim3(CT), 0, st, gout, out, w, gin, s,
                      B, deriv);

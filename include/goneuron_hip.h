@@ -166,6 +166,18 @@ int gn_model_train_step(gn_model *m, const float *x, const float *y, int32_t B, 
 /* Same with HBM-resident x / y; the mean loss stays on the device (read it
  * with gn_model_read_loss).  No host synchronisation. */
 int gn_model_train_step_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
+/* No counterpart in the reference (launch-overhead control).  Training steps
+ * of models without MoE or LSTM layers replay their forward + loss + backward
+ * launches from a HIP graph: the first step for a given (x, y, B, training
+ * flags) runs eagerly, the second is captured, later ones replay it; Adam is
+ * launched after it as usual.  Same kernels, same results.  on = 0 turns it
+ * off (and frees the graphs), 1 back on (the default).  A model keeps at most
+ * 4 graphs; gn_model_reserve frees them.  A replay reads x and y at the
+ * addresses of the step it was captured from, which are the addresses its
+ * key matched. */
+int gn_model_set_graphs(gn_model *m, int32_t on);
+/* Number of captured step graphs the model holds. */
+int gn_model_graph_count(gn_model *m, int32_t *n);
 /* Test hook (no counterpart in the reference): polls per wait of the
  * cooperative LSTM BPTT kernel before it reports a timeout (default 2^18);
  * a negative value makes every wait time out at once, so the error path
