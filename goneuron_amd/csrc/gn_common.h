@@ -222,11 +222,22 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
                                 int spin_limit, hipStream_t s);
 int lstm_gram_pitch(int n);
 // the two halves of launch_lstm_clip_weights: the chains' Gram matrices, then
-// the clip recursion over them into the per-step weights
+// the clip recursion over them into the per-step weights.  They may also run
+// side by side (clip on another stream): with `cnt` (lstm_gram_counters
+// unsigned, zeroed once) the Gram kernel counts the finished tiles of each
+// column and the clip of launch number `epoch` (1, 2, ...) waits for them;
+// `started` (one unsigned per chain, zeroed once) receives `epoch` when a
+// chain's clip workgroup is resident, and launch_lstm_clip_gate, queued
+// before the Gram kernel, waits for that.  Waits are bounded by spin_limit
+// polls and set *err on a timeout.
 hipError_t launch_lstm_gram(const float *D, const float *hbuf, const float *x, double *gram, int B,
-                            int T, int I, int H, int W, hipStream_t s);
+                            int T, int I, int H, int W, hipStream_t s, unsigned *cnt = nullptr);
 hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
-                            hipStream_t s);
+                            hipStream_t s, const unsigned *cnt = nullptr, unsigned epoch = 0,
+                            unsigned *started = nullptr, int *err = nullptr, int spin_limit = 0);
+int lstm_gram_counters(int B, int T, int W);
+hipError_t launch_lstm_clip_gate(const unsigned *started, int B, int W, unsigned epoch, int *err,
+                                 int spin_limit, hipStream_t s);
 hipError_t launch_lstm_clip_weights(const float *D, const float *hbuf, const float *x, double *gram,
                                     double *coef, float *w, int B, int T, int I, int H, int W,
                                     hipStream_t s);

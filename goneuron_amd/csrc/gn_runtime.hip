@@ -481,8 +481,15 @@ struct LayerRT {
   float *igb = nullptr, *tcb = nullptr, *cbuf = nullptr, *hbuf = nullptr;
   float *Dg = nullptr, *S = nullptr, *wts = nullptr;
   double *gram = nullptr, *coef = nullptr;
-  void *lsync = nullptr;                         // cooperative BPTT flags + exchange
-  unsigned lepoch = 0;                           // its flag base
+  void *lsync = nullptr;                         // cooperative BPTT exchange words
+  unsigned lepoch = 0;                           // its tag base
+  // Gram / clip side by side: per-column tile counts, per-chain start flags,
+  // launch number since the counts were zeroed and the batch they were laid
+  // out for; events for the clip's stream
+  unsigned *gcnt = nullptr, *gstart = nullptr;
+  unsigned gepoch = 0;
+  int gB = 0;
+  hipEvent_t lev[2] = {nullptr, nullptr};
   bool lcoop = false;                            // cooperative BPTT usable
   // Embedding / PositionalEncoding / TransformerBlock / CLSPooling
   int V = 0, D = 0, NH = 0, FF = 0, causal = 0;
@@ -607,6 +614,9 @@ extern "C" void gn_model_destroy(gn_model *M) {
   (void)hipStreamSynchronize(M->ctx->stream);
   (void)hipStreamSynchronize(M->ctx->aux);
   drop_graphs(M);
+  for (LayerRT &R : M->L)
+    for (hipEvent_t e : R.lev)
+      if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
   for (void *p : M->bowned) (void)hipFree(p);
@@ -785,17 +795,29 @@ static int alloc_batch(gn_model *M) {
       R.coef = reinterpret_cast<double *>(cf);
       R.lsync = nullptr;
       R.err = nullptr;
+      {
+        const size_t ncnt = (size_t)lstm_gram_counters(max_batch, (int)T, M->workers) + nchains;
+        float *cb = nullptr, *er = nullptr;
+        if ((rc = model_balloc(M, ncnt, &cb))) return rc;
+        if ((rc = model_balloc(M, 64, &er))) return rc;
+        HIP_OK(c, hipMemsetAsync(cb, 0, ncnt * sizeof(unsigned), c->stream));
+        HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
+        R.gcnt = reinterpret_cast<unsigned *>(cb);
+        R.gstart = R.gcnt + lstm_gram_counters(max_batch, (int)T, M->workers);
+        R.err = reinterpret_cast<int *>(er);
+        R.gepoch = 0;
+        R.gB = 0;
+        for (hipEvent_t &e : R.lev)
+          if (!e) HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      }
       R.lcoop = false;
       R.lepoch = 0;
       if (lstm_coop_eligible(max_batch, (int)H)) {
         const size_t bytes = lstm_coop_sync_bytes(max_batch, (int)H);
-        float *sy = nullptr, *er = nullptr;
+        float *sy = nullptr;
         if ((rc = model_balloc(M, (bytes + 3) / 4, &sy))) return rc;
-        if ((rc = model_balloc(M, 64, &er))) return rc;
         HIP_OK(c, hipMemsetAsync(sy, 0, bytes, c->stream));
-        HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
         R.lsync = sy;
-        R.err = reinterpret_cast<int *>(er);
         R.lcoop = true;
       }
     }
@@ -2058,13 +2080,40 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         // the clip chains: n = chunk x T steps each
         const int Wc = std::max(1, std::min(M->workers, B)), chunk = (B + Wc - 1) / Wc;
         const double nst = (double)chunk * T, nchain = (double)((B + chunk - 1) / chunk);
-        {  // Gram of the steps' contributions: n(n+1)/2 pairs, 2 (4H + H + I) FLOPs each, fp64
-          KTimer kt(c, GN_KCLASS_OTHER, "lstm_gram", nchain * nst * (nst + 1) * (5.0 * H + I));
-          HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream));
-        }
-        {  // the clip recursion reads each chain's Gram once
-          KTimer kt(c, GN_KCLASS_OTHER, "lstm_clip", nchain * 8.0 * nst * (nst + 1) / 2);
-          HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->stream));
+        if (!c->timing && R.gcnt) {
+          // Gram and clip side by side: the clip (second stream) reads each
+          // column tile as soon as the Gram kernel has counted it; a gate
+          // queued before the Gram kernel holds it until every chain's clip
+          // workgroup is resident.  The tile counts' layout follows B.
+          if (R.gB != B) {  // counts and start flags of every chain the largest batch has
+            const int Wm = std::max(1, std::min(M->workers, M->maxB));
+            const int cm = (M->maxB + Wm - 1) / Wm;
+            const size_t ncnt = (size_t)lstm_gram_counters(M->maxB, T, M->workers) +
+                                (size_t)((M->maxB + cm - 1) / cm);
+            HIP_OK(c, hipMemsetAsync(R.gcnt, 0, ncnt * sizeof(unsigned), c->stream));
+            R.gepoch = 0;
+            R.gB = B;
+          }
+          const unsigned ep = ++R.gepoch;
+          HIP_OK(c, hipEventRecord(R.lev[0], c->stream));
+          HIP_OK(c, hipStreamWaitEvent(c->aux, R.lev[0], 0));
+          HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->aux, R.gcnt, ep,
+                                     R.gstart, R.err, M->lstm_spin_limit));
+          HIP_OK(c, hipEventRecord(R.lev[1], c->aux));
+          HIP_OK(c, launch_lstm_clip_gate(R.gstart, B, M->workers, ep, R.err, M->lstm_spin_limit,
+                                          c->stream));
+          HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream,
+                                     R.gcnt));
+          HIP_OK(c, hipStreamWaitEvent(c->stream, R.lev[1], 0));
+        } else {
+          {  // Gram of the steps' contributions: n(n+1)/2 pairs, 2 (4H + H + I) FLOPs each, fp64
+            KTimer kt(c, GN_KCLASS_OTHER, "lstm_gram", nchain * nst * (nst + 1) * (5.0 * H + I));
+            HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream));
+          }
+          {  // the clip recursion reads each chain's Gram once
+            KTimer kt(c, GN_KCLASS_OTHER, "lstm_clip", nchain * 8.0 * nst * (nst + 1) / 2);
+            HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->stream));
+          }
         }
         {  // dG scaled in place by the step weights, plus the per-sample sums
           KTimer kt(c, GN_KCLASS_OTHER, "lstm_weight", f4(2.0 * B * (T + 1) * G4 + (double)B * G4));
@@ -2264,7 +2313,8 @@ static int check_flags(gn_model *M) {
     HIP_OK(c, hipStreamSynchronize(c->stream));
     if (flag) {
       HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
-      return set_err(c, GN_ERR_HIP, "LSTM cooperative BPTT: a workgroup wait timed out");
+      return set_err(c, GN_ERR_HIP,
+                     "LSTM: a cross-workgroup wait timed out (BPTT exchange or Gram/clip overlap)");
     }
   }
   if (R.d.kind == GN_LAYER_EMBEDDING && R.bad && M->last_B > 0) {

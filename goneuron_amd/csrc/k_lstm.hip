@@ -184,6 +184,84 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
   if (own) out[(size_t)b * H + i] = hnew;
 }
 
+// The same recurrence with each thread's share of WhT in registers for the
+// whole sequence (at most LF_R rows x 4 columns per thread: H <= 256), so a
+// step reads no weights at all; the products are summed in the order
+// lstm_fwd_kernel uses, so the results are the same bit for bit.
+constexpr int LF_R = 16;
+__global__ __launch_bounds__(1024) void lstm_fwd_reg_kernel(const float *__restrict__ xw,
+                                                            const float *__restrict__ WhT,
+                                                            const float *__restrict__ bias,
+                                                            float *__restrict__ igb,
+                                                            float *__restrict__ tcb,
+                                                            float *__restrict__ cbuf,
+                                                            float *__restrict__ hbuf,
+                                                            float *__restrict__ out, int T, int H,
+                                                            int GB, int NQ) {
+  extern __shared__ float sm[];
+  float *hs = sm, *part = sm + ((H + 3) & ~3);  // part[NQ][H], 16-byte aligned
+  const int b = blockIdx.x;
+  const int i = threadIdx.x;
+  const int c = i % GB, q = i / GB;
+  const bool mv = q < NQ && 4 * c < H;
+  const int k0 = mv ? (H * q) / NQ : 0;
+  const int nk = mv ? (H * (q + 1)) / NQ - k0 : 0;  // <= LF_R (checked by the launcher)
+  float4 wr[LF_R];
+#pragma unroll
+  for (int e = 0; e < LF_R; ++e)
+    wr[e] = e < nk ? reinterpret_cast<const float4 *>(WhT)[(size_t)(k0 + e) * (H / 4) + c]
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  const bool own = i < H;
+  const float *xwb = xw + (size_t)b * T * H;
+  float bi = 0.f, fg = 0.f, gg = 0.f, og = 0.f, xwn = 0.f;
+  if (own) {
+    hs[i] = 0.f;
+    hbuf[(size_t)b * (T + 1) * H + i] = 0.f;
+    bi = bias[i];
+    fg = sigm(bias[H + i]);       // Q13: f, g, o pre-activations are the biases
+    gg = tanh32(bias[2 * H + i]);
+    og = sigm(bias[3 * H + i]);
+    xwn = xwb[i];
+  }
+  __syncthreads();
+  float cc = 0.f, hnew = 0.f;
+  for (int t = 0; t < T; ++t) {
+    const float xwc = xwn;
+    if (own && t + 1 < T) xwn = xwb[(size_t)(t + 1) * H + i];  // next step's, in flight
+    if (mv) {
+      float4 sacc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int e = 0; e < LF_R; ++e)
+        if (e < nk) {
+          const float x = hs[k0 + e];
+          sacc.x += wr[e].x * x;
+          sacc.y += wr[e].y * x;
+          sacc.z += wr[e].z * x;
+          sacc.w += wr[e].w * x;
+        }
+      *reinterpret_cast<float4 *>(part + q * H + 4 * c) = sacc;
+    }
+    __syncthreads();
+    if (own) {
+      float sh = 0.f;
+      for (int r = 0; r < NQ; ++r) sh += part[r * H + i];
+      const float a = (bi + xwc) + sh;  // bias, then Wx x, then Wh h (lstm.go:1065-1101)
+      const size_t o = ((size_t)b * T + t) * H + i;
+      const float ig = sigm(a);
+      cc = fg * cc + ig * gg;
+      const float tc = tanh32(cc);
+      hnew = og * tc;
+      igb[o] = ig;
+      tcb[o] = tc;
+      cbuf[o] = cc;
+      hbuf[((size_t)b * (T + 1) + t + 1) * H + i] = hnew;
+      hs[i] = hnew;
+    }
+    __syncthreads();
+  }
+  if (own) out[(size_t)b * H + i] = hnew;
+}
+
 // BPTT deltas, one workgroup per sample.  gh = dL/dh_{T-1} [B][H].
 // D [B][T+1][4H]: row t = (dI, dF, dC, dO) of step t; row T = 0 (padding that
 // lines D up with hbuf for the dWh GEMM).  dhPrev = Wh^T dG is split over NQ
@@ -264,18 +342,19 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
 // [m*U, (m+1)*U) of Wh (U = H / LC_KM) in LDS for the whole sequence, owns
 // those hidden units' state and gate deltas, and computes their dhPrev from
 // the group's full dG.  Per step each member publishes its units' dG through
-// an exchange buffer (double-buffered by step parity) and a flag (agent-scope
-// release / acquire), waits for the other members' flags, reads the full dG
-// and does its share of Wh^T dG from LDS.  All shared words are agent-scope
-// atomics (device-coherent loads and stores, no cache flushes); a member
-// waits for its exchange stores to complete before raising its flag, and
-// reads the exchange only after every flag of the step is up.  Every wait is
-// bounded by
-// spin_limit polls; a timeout sets *err and the kernel runs to its end
-// without further waits (results are then invalid and the caller reports
-// the error).  All workgroups must be resident together: launched
-// cooperatively, one per CU.  Workgroup ids map to XCDs round-robin, so a
-// group's members are given ids of one residue mod 8 (one XCD, one L2).
+// an exchange buffer (double-buffered by step parity) whose 64-bit words hold
+// a value and the step's tag together; a reader polls the words it needs
+// until each carries the step's tag.  Value and tag are one single-copy
+// atomic (agent-scope, relaxed) word, so a word with the right tag holds that
+// step's value: no separate flag, no wait for store completion, one memory
+// round trip per step.  Two buffers suffice: a member writes step s + 2 into
+// step s's buffer only after reading every member's step s + 1 words, which
+// each member wrote after it had read all of step s.  Every poll is bounded
+// by spin_limit; a timeout sets *err and the kernel runs to its end without
+// further waits (results are then invalid and the caller reports the error).
+// All workgroups must be resident together: launched cooperatively, one per
+// CU.  Workgroup ids map to XCDs round-robin, so a group's members are given
+// ids of one residue mod 8 (one XCD).
 constexpr int LC_KM = 8;
 constexpr int LC_SPG = 2;
 constexpr int LC_NT = 1024;
@@ -286,20 +365,26 @@ __host__ __device__ inline int lstm_coop_grid(int B) {
 }
 static inline size_t lstm_coop_lds(int H) {
   const int U = H / LC_KM;
-  return ((size_t)4 * H * (U + 4) + (size_t)LC_SPG * 4 * H + (size_t)(LC_NT / 64) * LC_SPG * U) *
+  return ((size_t)4 * H * (U + 4) + (size_t)LC_SPG * 4 * H + (size_t)(LC_NT / 64) * LC_SPG * U +
+          (size_t)2 * 3 * LC_SPG * U) *
          sizeof(float);
+}
+
+__device__ __forceinline__ unsigned long long lc_word(float v, unsigned tag) {
+  return ((unsigned long long)tag << 32) | (unsigned long long)__float_as_uint(v);
 }
 
 __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
     const float *__restrict__ gh, const float *__restrict__ igb, const float *__restrict__ tcb,
     const float *__restrict__ cbuf, const float *__restrict__ Wh, const float *__restrict__ bias,
-    float *__restrict__ D, unsigned *flags, float *X, int *err, int B, int T, int H, unsigned base,
+    float *__restrict__ D, unsigned long long *X, int *err, int B, int T, int H, unsigned base,
     int spin_limit) {
   extern __shared__ float sm[];
   const int U = H / LC_KM, UP = U + 4, G4 = 4 * H;
   float *Wsl = sm;                          // [4H][UP]: Wh[r][u0 + u]
   float *dGs = Wsl + (size_t)G4 * UP;       // [SPG][4H]: the group's dG of this step
   float *part = dGs + LC_SPG * G4;          // [waves][SPG][U]
+  float *gpre = part + (LC_NT / 64) * LC_SPG * U;  // [2][3][SPG * U]: owners' next saved gates
   const int wg = blockIdx.x, xcd = wg & 7, rest = wg >> 3;
   const int m = rest % LC_KM, g = (rest / LC_KM) * 8 + xcd;
   const int ngroups = lstm_coop_groups(B);
@@ -334,75 +419,101 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q) padrow[q * H + io] = 0.f;
   }
-  // partial products: thread (share, c4) sums rows of its share for units
-  // 4*c4 .. 4*c4+3 of both samples
-  const int C4 = U / 4;                     // 1, 2, 4 or 8: divides 64
-  const int c4 = tid % C4, share = tid / C4;
-  const int nshare = LC_NT / C4;
+  bool bad = spin_limit < 0;  // forced timeout (test hook): give up without polling
+  if (bad && tid == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Two roles with two barriers per step each, in separate loops (no
+  // control-flow merge inside a step, where the compiler would make wave 0
+  // wait for its stores): wave 0 holds the owner lanes; waves 1.. fetch the
+  // exchange and compute Wh^T dG.  A wait for a load also waits for every
+  // vector store issued before it, so the owners load nothing after their
+  // exchange stores within a step.
+  const int NO = LC_SPG * U;  // owner slots
+  if (wave == 0) {
+    for (int step = 0; step < T; ++step) {
+      const int t = T - 1 - step, par = t & 1;
+      const unsigned tag = base + (unsigned)step + 1u;
+      unsigned long long *xb = X + (size_t)par * Bp * G4 + (size_t)g * LC_SPG * G4;
+      if (own) {
+        // step 0's saved gates from the prologue, later ones prefetched into
+        // LDS by the other waves during the previous step
+        const float *gp = gpre + (size_t)par * 3 * NO;
+        const float ig = step ? gp[tid] : ign, tc = step ? gp[NO + tid] : tcn,
+                    cp = step ? gp[2 * NO + tid] : cpn;
+        const float did = ig * (1.0f - ig);
+        const float dc = cur * og * (1 - tc * tc) + dcn;
+        const float dv[4] = {dc * gg * did, dc * cp * dfd, dc * ig * dgd, cur * tc * dod};
+        dcn = dc * fg;
+        if (valid) {
+          float *row = D + ((size_t)bo * (T + 1) + t) * G4;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) row[q * H + io] = dv[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          __hip_atomic_store(xb + (size_t)so * G4 + q * H + io, lc_word(valid ? dv[q] : 0.f, tag),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();  // dGs filled
+      __syncthreads();  // partial sums written
+      if (own) {
+        float sum = 0.f;
+        for (int w = 1; w < LC_NT / 64; ++w) sum += part[(size_t)w * LC_SPG * U + so * U + uo];
+        cur += sum;
+      }
+    }
+    return;
+  }
+  // waves 1..: thread rt = tid - 64 = (share, c4) sums the rows of its share
+  // for units 4*c4 .. 4*c4+3 of both samples
+  const int rt = tid - 64;
+  constexpr int NRT = LC_NT - 64;
+  const int C4 = U / 4;                     // 1, 2, 4 or 8: divides 64 and NRT
+  const int c4 = rt % C4, share = rt / C4;
+  const int nshare = NRT / C4;
   const int rps = (G4 + nshare - 1) / nshare;
   const int r0 = min(share * rps, G4), r1 = min(r0 + rps, G4);
-  bool bad = false;
+  constexpr int MAXW = (LC_SPG * 4 * 256 + NRT - 1) / NRT;  // exchange words per thread, H <= 256
+  const int nw = LC_SPG * G4;
+  // prefetch role: thread rt < 3 * NO loads saved gate (rt / NO) of owner slot rt % NO
+  const int pk = rt / NO, ps = rt - pk * NO;
+  const int pb = g * LC_SPG + ps / U, pu = u0 + ps % U;
+  const bool pv = rt < 3 * NO && pb < B;
+  const float *psrc = pk == 0 ? igb : (pk == 1 ? tcb : cbuf);
+  const size_t pbase = (size_t)pb * T * H + pu;
   for (int step = 0; step < T; ++step) {
     const int t = T - 1 - step, par = t & 1;
-    if (own) {
-      const float ig = ign, tc = tcn, cp = cpn;
-      if (valid && t > 0) {
-        ign = igb[ob + (size_t)(t - 1) * H];
-        tcn = tcb[ob + (size_t)(t - 1) * H];
-        cpn = t > 1 ? cbuf[ob + (size_t)(t - 2) * H] : 0.f;
-      }
-      const float did = ig * (1.0f - ig);
-      const float dc = cur * og * (1 - tc * tc) + dcn;
-      const float dv[4] = {dc * gg * did, dc * cp * dfd, dc * ig * dgd, cur * tc * dod};
-      dcn = dc * fg;
-      float *xrow = X + ((size_t)par * Bp + bo) * G4;
-      if (valid) {
-        float *row = D + ((size_t)bo * (T + 1) + t) * G4;
+    const unsigned tag = base + (unsigned)step + 1u;
+    const unsigned long long *xb = X + (size_t)par * Bp * G4 + (size_t)g * LC_SPG * G4;
+    // the next step's saved gate (step t - 1: ig, tc of t - 1, c of t - 2)
+    const int tl = pk == 2 ? t - 2 : t - 1;
+    const float pre = pv && t > 0 && tl >= 0 ? psrc[pbase + (size_t)tl * H] : 0.f;
+    // all of this thread's words at once, then re-poll those without this step's tag
+    unsigned long long wv[MAXW];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) row[q * H + io] = dv[q];
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        __hip_atomic_store(xrow + q * H + io, valid ? dv[q] : 0.f, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      // the exchange stores must have completed (device-coherent) before the
-      // flag is raised: s_waitcnt vmcnt(0)
-      __builtin_amdgcn_s_waitcnt(0x0F70);
+    for (int k = 0; k < MAXW; ++k) {
+      const int idx = rt + k * NRT;
+      wv[k] = idx < nw ? __hip_atomic_load(xb + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0ull;
     }
-    __syncthreads();
-    if (wave == 0) {
-      const unsigned want = base + (unsigned)step + 1u;
-      if (lane == 0)
-        __hip_atomic_store(flags + g * LC_KM + m, want, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // lanes 0..KM-1 poll the members' flags together
-      if (!bad && spin_limit < 0) {  // forced timeout (test hook): give up without polling
-        bad = true;
-        if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (!bad) {
+    if (rt < 3 * NO) gpre[(size_t)(par ^ 1) * 3 * NO + rt] = pre;
+#pragma unroll
+    for (int k = 0; k < MAXW; ++k) {
+      const int idx = rt + k * NRT;
+      if (idx < nw) {
         int spins = 0;
-        while (true) {
-          bool ready = true;
-          if (lane < LC_KM)
-            ready = (int)(__hip_atomic_load(flags + g * LC_KM + lane, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT) - want) >= 0;
-          if (__all(ready)) break;
+        while (!bad && (unsigned)(wv[k] >> 32) != tag) {
           if (++spins > spin_limit) {
             bad = true;
-            if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
           }
           __builtin_amdgcn_s_sleep(1);
+          wv[k] = __hip_atomic_load(xb + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        dGs[idx] = __uint_as_float((unsigned)wv[k]);
       }
     }
-    __syncthreads();
-    for (int idx = tid; idx < LC_SPG * G4; idx += LC_NT) {
-      const int s = idx / G4;
-      dGs[idx] = __hip_atomic_load(X + ((size_t)par * Bp + g * LC_SPG + s) * G4 + (idx - s * G4),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
+    __syncthreads();  // dGs filled
     float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
     for (int r = r0; r < r1; ++r) {
       const float4 w = *reinterpret_cast<const float4 *>(Wsl + r * UP + 4 * c4);
@@ -421,12 +532,7 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
       *reinterpret_cast<float4 *>(p0) = a0;
       *reinterpret_cast<float4 *>(p0 + U) = a1;
     }
-    __syncthreads();
-    if (own) {
-      float sum = 0.f;
-      for (int w = 0; w < LC_NT / 64; ++w) sum += part[(size_t)w * LC_SPG * U + so * U + uo];
-      cur += sum;
-    }
+    __syncthreads();  // partial sums written
   }
 }
 
@@ -455,16 +561,45 @@ struct ChainMap {
 // result element i of lane l is row 4*i + l/16, column l%16.
 typedef double d4v __attribute__((ext_vector_type(4)));
 
+// A finished Gram tile is published by a count per (chain, 64-column tile):
+// every thread's stores are released at agent scope before the barrier, then
+// one release increment.  The counts only grow (launch e leaves column tv of
+// each chain at e * (tv + 1)), so they are never reset.
+__device__ __forceinline__ void gram_publish(unsigned *cnt, int ch, int tv, int nmax) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(cnt + (size_t)ch * ((nmax + 63) / 64) + tv, 1u, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits (bounded) until column tile tv of chain ch holds `want` tiles: relaxed
+// polls, then one acquire fence; on a timeout sets *err and returns (the
+// results are then invalid).
+__device__ __forceinline__ void gram_wait(const unsigned *cnt, int ch, int tv, int nmax,
+                                          unsigned want, int *err, int spin_limit) {
+  const unsigned *c = cnt + (size_t)ch * ((nmax + 63) / 64) + tv;
+  int spins = 0;
+  while ((int)(__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - want) < 0) {
+    if (++spins > spin_limit) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
 __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict__ D,
                                                         const float *__restrict__ hbuf,
                                                         const float *__restrict__ x,
                                                         double *__restrict__ Gm, ChainMap cm,
-                                                        int I, int H, int nmax) {
+                                                        int I, int H, int nmax, unsigned *cnt) {
   __shared__ double sv[16][64], su[16][64];
-  const int ch = blockIdx.y;
+  const int ch = blockIdx.x;  // chains vary fastest in dispatch order
   const int n = cm.len(ch);
   // tile (tv, tu) with tu <= tv from the linear block index
-  int lin = blockIdx.x, tv = 0;
+  int lin = blockIdx.y, tv = 0;
   while (lin > tv) {
     lin -= tv + 1;
     ++tv;
@@ -544,6 +679,7 @@ __global__ __launch_bounds__(256) void lstm_gram_kernel(const float *__restrict_
         const int v = tv * 64 + wn * 32 + j * 16 + (lane & 15);
         if (v < n && u <= v) Gc[(size_t)u * nmax + v] = acc[0][i][j][r] * (acc[1][i][j][r] + 1.0);
       }
+  if (cnt) gram_publish(cnt, ch, tv, nmax);
 }
 
 // One 16-byte group of a Gram row: K runs over [dG | hPrev | x_last]; the first
@@ -575,12 +711,12 @@ __global__ __launch_bounds__(256) void lstm_gram_v5_kernel(const float *__restri
                                                            const float *__restrict__ hbuf,
                                                            const float *__restrict__ x,
                                                            double *__restrict__ Gm, ChainMap cm,
-                                                           int I, int H, int nmax) {
+                                                           int I, int H, int nmax, unsigned *cnt) {
   constexpr int KS = 32, GP = KS + 4;
   __shared__ __attribute__((aligned(16))) float su[2][64 * GP], sv[2][64 * GP];
-  const int ch = blockIdx.y;
+  const int ch = blockIdx.x;  // chains vary fastest in dispatch order
   const int n = cm.len(ch);
-  int lin = blockIdx.x, tv = 0;
+  int lin = blockIdx.y, tv = 0;
   while (lin > tv) {
     lin -= tv + 1;
     ++tv;
@@ -691,6 +827,7 @@ __global__ __launch_bounds__(256) void lstm_gram_v5_kernel(const float *__restri
         const int v = tv * 64 + wn * 32 + j * 16 + (lane & 15);
         if (v < n && u <= v) Gc[(size_t)u * nmax + v] = acc[0][i][j][r] * (acc[1][i][j][r] + 1.0);
       }
+  if (cnt) gram_publish(cnt, ch, tv, nmax);
 }
 
 // Sequential clip of one chain from its Gram matrix; one workgroup per chain.
@@ -721,7 +858,9 @@ __device__ __forceinline__ double readlane_d(double x, int l) {
 __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__restrict__ Gm,
                                                         double *__restrict__ a,
                                                         float *__restrict__ w, ChainMap cm,
-                                                        int nmax) {
+                                                        int nmax, const unsigned *cnt,
+                                                        unsigned epoch, unsigned *started,
+                                                        int *err, int spin_limit) {
   // tile[buf][u][r] = <D_{v0+u}, D_{v0+r}> (u <= r) of the current / next block;
   // cross[u][r] = <D_{v0+u}, D_{v1+r}>: current block rows x next block columns
   __shared__ double tile[2][CLIP_BLK][CLIP_BLK + 1];
@@ -734,6 +873,12 @@ __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__rest
   double *ac = a + (size_t)ch * nmax;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int nblk = (n + CLIP_BLK - 1) / CLIP_BLK;
+  // run beside the Gram kernel: announce residency, then read each Gram
+  // column tile only once its count says this launch's tiles are stored
+  if (cnt) {
+    if (tid == 0) __hip_atomic_store(started + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (nblk > 0) gram_wait(cnt, ch, 0, nmax, epoch, err, spin_limit);
+  }
   {
     const int nb0 = min(CLIP_BLK, n);
     for (int e = tid; e < CLIP_BLK * CLIP_BLK; e += CLIP_NT) {
@@ -797,6 +942,7 @@ __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__rest
         bcast[1] = blkscale;
       }
     } else if (nb1 > 0) {
+      if (cnt) gram_wait(cnt, ch, k + 1, nmax, epoch * (unsigned)(k + 2), err, spin_limit);
       // meanwhile the other three waves prepare the next block: the part of
       // its s from blocks before this one (a's final up to this block's
       // rescale, applied below), its diagonal tile and the cross tile
@@ -909,6 +1055,11 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
   if (!lstm_fits(H)) return hipErrorInvalidValue;
   const LstmLayout L = lstm_layout(H, WhT);
   const size_t base = (size_t)(((H + 3) & ~3) + L.NQ * H) * sizeof(float);
+  if (L.v4 && (H + L.NQ - 1) / L.NQ <= LF_R) {  // every thread's WhT share fits its registers
+    hipLaunchKernelGGL(lstm_fwd_reg_kernel, dim3(B), dim3(1024), base, s, xw, WhT, bias, igb, tcb,
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
+    return hipGetLastError();
+  }
   // as many leading shares of WhT in LDS as fit 128 KB (whole float4 rows:
   // the V4 layout only; the copy needs 16-byte aligned WhT)
   int QL = 0;
@@ -954,21 +1105,19 @@ bool lstm_coop_eligible(int B, int H) {
 
 size_t lstm_coop_sync_bytes(int B, int H) {
   const int Bp = lstm_coop_groups(B) * LC_SPG;
-  return (size_t)lstm_coop_groups(B) * LC_KM * sizeof(unsigned) + 256 +
-         (size_t)2 * Bp * 4 * H * sizeof(float);
+  return (size_t)2 * Bp * 4 * H * sizeof(unsigned long long);
 }
 
-// sync: lstm_coop_sync_bytes(B, H) bytes, 256-byte aligned; flags first (their
-// values only ever grow: each launch passes base = the previous launch's last
-// flag value), then the exchange buffer.  err: device int, 0 on success.
+// sync: lstm_coop_sync_bytes(B, H) bytes, zeroed once at allocation: the
+// tagged exchange words (tags only ever grow: each launch passes base = the
+// previous launch's last tag, so no word of an earlier launch matches).
+// err: device int, 0 on success.
 hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *tcb,
                                 const float *cbuf, const float *Wh, const float *bias, float *D,
                                 void *sync, int *err, unsigned *epoch, int B, int T, int H,
                                 int spin_limit, hipStream_t s) {
   if (!lstm_coop_eligible(B, H)) return hipErrorInvalidValue;
-  unsigned *flags = reinterpret_cast<unsigned *>(sync);
-  float *X = reinterpret_cast<float *>(reinterpret_cast<char *>(sync) +
-                                       (((size_t)lstm_coop_groups(B) * LC_KM * sizeof(unsigned) + 255) & ~(size_t)255));
+  unsigned long long *X = reinterpret_cast<unsigned long long *>(sync);
   const size_t shm = lstm_coop_lds(H);
   static bool attr_set = false;
   if (!attr_set) {
@@ -979,7 +1128,7 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
   }
   unsigned base = *epoch;
   void *args[] = {(void *)&gh, (void *)&igb, (void *)&tcb, (void *)&cbuf, (void *)&Wh,
-                  (void *)&bias, (void *)&D, (void *)&flags, (void *)&X, (void *)&err,
+                  (void *)&bias, (void *)&D, (void *)&X, (void *)&err,
                   (void *)&B, (void *)&T, (void *)&H, (void *)&base, (void *)&spin_limit};
   hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(lstm_bwd_coop_kernel),
                                             dim3(lstm_coop_grid(B)), dim3(LC_NT), args, shm, s);
@@ -988,30 +1137,73 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
 }
 
 hipError_t launch_lstm_gram(const float *D, const float *hbuf, const float *x, double *gram, int B,
-                            int T, int I, int H, int W, hipStream_t s) {
+                            int T, int I, int H, int W, hipStream_t s, unsigned *cnt) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
   const int nmax = lstm_gram_pitch(cm.chunk * T);
   const int ntile = (nmax + 63) / 64;
-  dim3 g(ntile * (ntile + 1) / 2, nchains);
+  dim3 g(nchains, ntile * (ntile + 1) / 2);  // column tiles complete in order, all chains together
   const bool vec = H % 8 == 0 && I % 4 == 0 &&
                   (((reinterpret_cast<uintptr_t>(D) | reinterpret_cast<uintptr_t>(hbuf) |
                      reinterpret_cast<uintptr_t>(x)) & 15) == 0);
   if (vec)
-    hipLaunchKernelGGL(lstm_gram_v5_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+    hipLaunchKernelGGL(lstm_gram_v5_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax, cnt);
   else
-    hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax);
+    hipLaunchKernelGGL(lstm_gram_kernel, g, dim3(256), 0, s, D, hbuf, x, gram, cm, I, H, nmax, cnt);
+  return hipGetLastError();
+}
+
+// One thread: waits (bounded) until every chain's clip workgroup has started,
+// so the Gram kernel queued after it cannot fill the CUs first.  Only the
+// overlap depends on it: after spin_limit polls it lets the Gram kernel go.
+__global__ void lstm_clip_gate_kernel(const unsigned *started, int nchains, unsigned epoch,
+                                      int spin_limit) {
+  if (threadIdx.x != 0) return;
+  int spins = 0;
+  for (int ch = 0; ch < nchains; ++ch)
+    while (__hip_atomic_load(started + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+      if (++spins > spin_limit) return;
+      __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+int lstm_gram_counters(int B, int T, int W) {
+  const int Wc = W < 1 ? 1 : (W > B ? B : W);
+  const int chunk = (B + Wc - 1) / Wc, nchains = (B + chunk - 1) / chunk;
+  return nchains * ((lstm_gram_pitch(chunk * T) + 63) / 64);
+}
+
+hipError_t launch_lstm_clip_gate(const unsigned *started, int B, int W, unsigned epoch, int *err,
+                                 int spin_limit, hipStream_t s) {
+  const int Wc = W < 1 ? 1 : (W > B ? B : W);
+  const int chunk = (B + Wc - 1) / Wc, nchains = (B + chunk - 1) / chunk;
+  (void)err;
+  hipLaunchKernelGGL(lstm_clip_gate_kernel, dim3(1), dim3(64), 0, s, started, nchains, epoch,
+                     spin_limit < 0 ? 0 : spin_limit);
   return hipGetLastError();
 }
 
 hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
-                            hipStream_t s) {
+                            hipStream_t s, const unsigned *cnt, unsigned epoch, unsigned *started,
+                            int *err, int spin_limit) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
   const int nmax = lstm_gram_pitch(cm.chunk * T);
-  hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), 0, s, gram, coef, w, cm, nmax);
+  if (cnt && (!started || !err)) return hipErrorInvalidValue;
+  // beside the Gram kernel, unused dynamic LDS keeps its workgroups off the
+  // clip's CUs (their waves would take issue slots from the serial recursion)
+  const size_t pad = cnt ? (size_t)24 << 10 : 0;
+  static bool attr_set = false;
+  if (cnt && !attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_clip_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pad);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), pad, s, gram, coef, w, cm, nmax,
+                     cnt, epoch, started, err, spin_limit);
   return hipGetLastError();
 }
 
