@@ -566,6 +566,7 @@ struct gn_model {
   };
   std::vector<StepGraph> graphs;
   bool graph_on = true;   // gn_model_set_graphs
+  int emb = -1;           // the Embedding layer (its index-error flags mask samples), or -1
   bool graph_ok = true;   // false once a capture failed: eager from then on
 };
 
@@ -977,7 +978,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.D = R.d.dim;
         R.T = len;  // tokens per sample
         if (R.V <= 0 || R.D <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: bad Embedding", i);
-        if (i != 0) return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: Embedding only as the first layer", i);
+        // below another layer it reads floor() of that layer's outputs as ids
+        // and hands it a zero gradient (embedding.go:156-163)
+        if (M->emb >= 0)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: a second Embedding layer is not built", i);
+        M->emb = i;
         R.pcount = (int64_t)R.V * R.D;
         R.out_len = R.T * R.D;
         break;
@@ -1062,8 +1067,9 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
           return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(GRU) sizes (hidden <= 1024)", i);
         if (R.d.return_sequences)
           return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
-        if (i != 0)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: SequenceUnroller only as the first layer", i);
+        if (i != 0 && len != R.T * R.I)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: SequenceUnroller(GRU) takes %d x %d, gets %d", i,
+                         R.T, R.I, len);
         R.in_len = R.T * R.I;
         len = R.in_len;
         R.pcount = (int64_t)3 * R.H * R.I + (int64_t)2 * R.H * R.H + 3 * R.H;
@@ -1077,9 +1083,10 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
           return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(LSTM) sizes", i);
         if (R.d.return_sequences)
           return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
-        if (i != 0)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: SequenceUnroller only as the first layer", i);
-        R.in_len = R.T * R.I;  // the first layer's in_size is the per-step input size here
+        if (i != 0 && len != R.T * R.I)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: SequenceUnroller(LSTM) takes %d x %d, gets %d", i,
+                         R.T, R.I, len);
+        R.in_len = R.T * R.I;  // in_size is the per-step input size here
         len = R.in_len;
         R.pcount = (int64_t)4 * R.H * R.I + (int64_t)4 * R.H * R.H + 4 * R.H;
         R.out_len = R.H;
@@ -1093,8 +1100,10 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     off += R.pcount;
     len = R.out_len;
   }
-  if (M->L.back().d.kind != GN_LAYER_DENSE)
-    return set_err(c, GN_ERR_UNSUPPORTED, "the output layer must be Dense");
+  // any layer may be the output layer (Network.Forward hands its output to the
+  // loss, net.go:212-223); a non-Dense one gets dL/dy itself, with no
+  // activation applied by the loss kernel
+  if (M->L.back().d.kind != GN_LAYER_DENSE) M->L.back().ap = ActPlan{ROW_NONE, F_IDENTITY, D_ONE, false};
   M->nparams = off;
   M->region = (off + 63) / 64 * 64;
 
@@ -1972,6 +1981,15 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           KTimer kt(c, GN_KCLASS_OTHER, "gru_bwd", 2.0 * 2 * H * H * B * T);
           HIP_OK(c, launch_gru_bwd(R.gout, R.gpre, R.ghprev, Wh, R.Dg, B, T, H, c->stream));
         }
+        if (below && below->gout) {  // dx_t = Wx^T [dU | dR (never set, 0) | dC] (gru.go:481-500)
+          GemmArgs a{};
+          a.M = B * T; a.N = I; a.K = G3;
+          a.A = R.Dg; a.lda = G3; a.B = Wx; a.ldb = I;
+          a.C = below->gout; a.ldc = I; a.alpha = 1.f;
+          a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+          KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+          HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+        }
         {
           KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, G3));
           HIP_OK(c, launch_token_sum(R.Dg, R.S, B, T, G3, c->stream));
@@ -2052,6 +2070,9 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)R.V * R.D + 2.0 * nch * R.T * R.D));
         HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
                                     scale, R.bad, c->stream));
+        if (below && below->gout)  // indices carry no gradient (embedding.go:156-163)
+          HIP_OK(c, launch_fill(below->gout, 0.0f, (int64_t)B * R.T, c->stream));
+        is_dz = false;
         break;
       }
       case GN_LAYER_LSTM_UNROLLER: {
@@ -2077,6 +2098,23 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           if (!done)
             HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
         }
+        // Below another layer: its gradient dx_t = Wx^T dG_t from the unclipped
+        // deltas (lstm.go:642-663; the unroller stacks the steps,
+        // unroller.go:200-206), before lstm_weight scales dG in place
+        auto lstm_gin = [&]() -> int {
+          if (!below || !below->gout) return GN_OK;
+          GemmArgs a{};
+          a.M = T; a.N = I; a.K = G4;
+          a.A = R.Dg; a.lda = G4; a.B = Wx; a.ldb = I;
+          a.C = below->gout; a.ldc = I; a.alpha = 1.f;
+          a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+          a.nbatch = B;
+          a.bstride_A = (int64_t)(T + 1) * G4;
+          a.bstride_C = (int64_t)T * I;
+          KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+          HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+          return GN_OK;
+        };
         // the clip chains: n = chunk x T steps each
         const int Wc = std::max(1, std::min(M->workers, B)), chunk = (B + Wc - 1) / Wc;
         const double nst = (double)chunk * T, nchain = (double)((B + chunk - 1) / chunk);
@@ -2104,8 +2142,12 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
                                           c->stream));
           HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream,
                                      R.gcnt));
+          int rc = lstm_gin();  // beside the clip
+          if (rc) return rc;
           HIP_OK(c, hipStreamWaitEvent(c->stream, R.lev[1], 0));
         } else {
+          int rc = lstm_gin();
+          if (rc) return rc;
           {  // Gram of the steps' contributions: n(n+1)/2 pairs, 2 (4H + H + I) FLOPs each, fp64
             KTimer kt(c, GN_KCLASS_OTHER, "lstm_gram", nchain * nst * (nst + 1) * (5.0 * H + I));
             HIP_OK(c, launch_lstm_gram(R.Dg, R.hbuf, in, R.gram, B, T, I, H, M->workers, c->stream));
@@ -2178,7 +2220,7 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   if (rc) return rc;
   LayerRT &O = M->L.back();
   int row_act = O.ap.row_act;
-  const int32_t *bad = M->L[0].d.kind == GN_LAYER_EMBEDDING ? M->L[0].bad : nullptr;
+  const int32_t *bad = M->emb >= 0 ? M->L[M->emb].bad : nullptr;
   {  // read z and y, write the activation output and dz, one loss per row
     KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * O.out_len + B));
     HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
@@ -2306,18 +2348,20 @@ extern "C" int gn_model_train_step_device(gn_model *M, const float *x, const flo
 static int check_flags(gn_model *M) {
   gn_ctx *c = M->ctx;
   if (M->L.empty()) return GN_OK;
-  const LayerRT &R = M->L[0];
-  if (R.d.kind == GN_LAYER_LSTM_UNROLLER && R.err) {
-    int flag = 0;
-    HIP_OK(c, hipMemcpyAsync(&flag, R.err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
-    HIP_OK(c, hipStreamSynchronize(c->stream));
-    if (flag) {
-      HIP_OK(c, hipMemsetAsync(R.err, 0, sizeof(int), c->stream));
-      return set_err(c, GN_ERR_HIP,
-                     "LSTM: a cross-workgroup wait timed out (BPTT exchange or Gram/clip overlap)");
+  for (const LayerRT &Q : M->L)
+    if (Q.d.kind == GN_LAYER_LSTM_UNROLLER && Q.err) {
+      int flag = 0;
+      HIP_OK(c, hipMemcpyAsync(&flag, Q.err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+      HIP_OK(c, hipStreamSynchronize(c->stream));
+      if (flag) {
+        HIP_OK(c, hipMemsetAsync(Q.err, 0, sizeof(int), c->stream));
+        return set_err(c, GN_ERR_HIP,
+                       "LSTM: a cross-workgroup wait timed out (BPTT exchange or Gram/clip overlap)");
+      }
     }
-  }
-  if (R.d.kind == GN_LAYER_EMBEDDING && R.bad && M->last_B > 0) {
+  if (M->emb < 0) return GN_OK;
+  const LayerRT &R = M->L[M->emb];
+  if (R.bad && M->last_B > 0) {
     const int B = M->last_B;
     std::vector<int32_t> f(B);
     HIP_OK(c, hipMemcpyAsync(f.data(), R.bad, (size_t)B * sizeof(int32_t), hipMemcpyDeviceToHost,

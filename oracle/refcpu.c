@@ -2361,11 +2361,38 @@ static int run_sample_grad(gno_net *n, const float *x, const float *g, float *ou
   return 0;
 }
 
+/* Output length of the network, walked from the input length without running
+ * a forward: Conv2D and the pooling layers only learn their plane size from
+ * the first input they see (conv2d.go:716-740, maxpool2d.go:119-126), so
+ * their out_len is not known before that. */
 static int32_t target_dim(gno_net *n) {
-  /* output length of the last layer; for Dense it is out_size */
-  const layer *L = &n->layers[n->nlayers - 1];
-  if (L->kind == GNO_LAYER_DENSE) return L->spec.out_size;
-  return L->out_len;
+  int32_t len = in_len_of(n);
+  for (int32_t i = 0; i < n->nlayers; i++) {
+    const layer *L = &n->layers[i];
+    switch (L->kind) {
+      case GNO_LAYER_DENSE: len = L->spec.out_size; break;
+      case GNO_LAYER_FLATTEN: break;
+      case GNO_LAYER_CONV2D: {
+        const int32_t cs = len / L->inC;
+        const int32_t h = (int32_t)sqrt((double)cs), w = h * h == cs ? h : cs / h;
+        len = L->outC * ((h + 2 * L->pad - L->k) / L->stride + 1) * ((w + 2 * L->pad - L->k) / L->stride + 1);
+        break;
+      }
+      case GNO_LAYER_MAXPOOL2D:
+      case GNO_LAYER_AVGPOOL2D: {
+        const int32_t C = L->spec.in_channels > 0 ? L->spec.in_channels : 1;
+        const int32_t cs = len / C;
+        const int32_t h = (int32_t)sqrt((double)cs), w = h * h == cs ? h : cs / h;
+        const int32_t k = L->spec.kernel, st = L->spec.stride, pd = L->spec.padding;
+        len = C * ((h + 2 * pd - k) / st + 1) * ((w + 2 * pd - k) / st + 1);
+        break;
+      }
+      default:
+        if (L->out_len > 0) len = L->out_len;  /* fixed at Build, or shape-preserving */
+        break;
+    }
+  }
+  return len;
 }
 
 float gno_net_accumulate_batch(gno_net *n, const float *x, const float *y, int32_t B) {

@@ -38,8 +38,8 @@ def oracle_specs(refcpu, cfg):
             specs.append(refcpu.spec(refcpu.LAYER_MAXPOOL2D, in_channels=d["inC"], kernel=d["k"],
                                      stride=d["s"], padding=d["p"]))
         elif k == "embedding":
-            specs.append(refcpu.spec(refcpu.LAYER_EMBEDDING, in_size=cfg["in_len"], vocab=d["vocab"],
-                                     dim=d["dim"]))
+            specs.append(refcpu.spec(refcpu.LAYER_EMBEDDING, in_size=d.get("T", cfg["in_len"]),
+                                     vocab=d["vocab"], dim=d["dim"]))
         elif k == "posenc":
             specs.append(refcpu.spec(refcpu.LAYER_POSENC, seq_len=d["T"], dim=d["dim"]))
         elif k == "transformer":
