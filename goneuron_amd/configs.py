@@ -160,9 +160,9 @@ def product_layers(cfg):
         elif k == "clspool":
             out.append(CLSPooling(d["T"], d["dim"]))
         elif k == "lstm":
-            out.append(SequenceUnroller(LSTM(d["hidden"], d["in"]), d["T"], False))
+            out.append(SequenceUnroller(LSTM(d["hidden"], d["in"]), d["T"], d.get("seq", False)))
         elif k == "gru":
-            out.append(SequenceUnroller(GRU(d["hidden"], d["in"]), d["T"], False))
+            out.append(SequenceUnroller(GRU(d["hidden"], d["in"]), d["T"], d.get("seq", False)))
         else:
             raise ValueError(k)
     # the first layer carries the per-sample input length (an LSTM carries its

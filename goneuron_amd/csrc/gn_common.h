@@ -196,19 +196,22 @@ hipError_t launch_moe_backward_deltas(const float *g, const float *eout, const f
 
 // ---- SequenceUnroller(GRU) ----
 bool gru_supported(int H);
+// seq (returnSequences): out [B][T][H]; g dL/dh_t [B][T][H] (else [B][H])
 hipError_t launch_gru_fwd(const float *xw, const float *WhT, float *pre, float *hprev, float *rh,
-                          float *out, int B, int T, int H, hipStream_t s);
+                          float *out, int B, int T, int H, hipStream_t s, int seq = 0);
 hipError_t launch_gru_bwd(const float *g, const float *pre, const float *hprev, const float *Wh,
-                          float *dG, int B, int T, int H, hipStream_t s);
+                          float *dG, int B, int T, int H, hipStream_t s, int seq = 0);
 
 // ---- SequenceUnroller(LSTM) ----
 hipError_t launch_transpose(const float *in, float *out, int rows, int cols, hipStream_t s);
+// seq (returnSequences): out is [B][T][H] (every state); in the backward gh is
+// then dL/dh_t [B][T][H] instead of dL/dh_{T-1} [B][H]
 hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,
                            float *tcb, float *cbuf, float *hbuf, float *out, int B, int T, int H,
-                           hipStream_t s);
+                           hipStream_t s, int seq = 0);
 hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
                            const float *Wh, const float *bias, float *D, int B, int T, int H,
-                           hipStream_t s);
+                           hipStream_t s, int seq = 0);
 // Cooperative BPTT (see k_lstm.hip): eligibility, the sync buffer it needs
 // (flags + exchange, zeroed once at allocation), and the launch.  Returns an
 // error without launching when not eligible or when the cooperative launch is
@@ -219,7 +222,7 @@ size_t lstm_coop_sync_bytes(int B, int H);
 hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *tcb,
                                 const float *cbuf, const float *Wh, const float *bias, float *D,
                                 void *sync, int *err, unsigned *epoch, int B, int T, int H,
-                                int spin_limit, hipStream_t s);
+                                int spin_limit, hipStream_t s, int seq = 0);
 int lstm_gram_pitch(int n);
 // the two halves of launch_lstm_clip_weights: the chains' Gram matrices, then
 // the clip recursion over them into the per-step weights.  They may also run

@@ -1065,15 +1065,13 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.H = R.d.out_size;
         if (R.T <= 0 || R.I <= 0 || !gru_supported(R.H))
           return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(GRU) sizes (hidden <= 1024)", i);
-        if (R.d.return_sequences)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
         if (i != 0 && len != R.T * R.I)
           return set_err(c, GN_ERR_SHAPE, "layer %d: SequenceUnroller(GRU) takes %d x %d, gets %d", i,
                          R.T, R.I, len);
         R.in_len = R.T * R.I;
         len = R.in_len;
         R.pcount = (int64_t)3 * R.H * R.I + (int64_t)2 * R.H * R.H + 3 * R.H;
-        R.out_len = R.H;
+        R.out_len = R.d.return_sequences ? R.T * R.H : R.H;  // unroller.go:21-43
         break;
       case GN_LAYER_LSTM_UNROLLER: {
         R.T = R.d.seq_len;
@@ -1081,15 +1079,13 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.H = R.d.out_size;
         if (R.T <= 0 || R.I <= 0 || R.H <= 0 || R.H > 1024)
           return set_err(c, GN_ERR_INVALID, "layer %d: bad SequenceUnroller(LSTM) sizes", i);
-        if (R.d.return_sequences)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: returnSequences=true not built", i);
         if (i != 0 && len != R.T * R.I)
           return set_err(c, GN_ERR_SHAPE, "layer %d: SequenceUnroller(LSTM) takes %d x %d, gets %d", i,
                          R.T, R.I, len);
         R.in_len = R.T * R.I;  // in_size is the per-step input size here
         len = R.in_len;
         R.pcount = (int64_t)4 * R.H * R.I + (int64_t)4 * R.H * R.H + 4 * R.H;
-        R.out_len = R.H;
+        R.out_len = R.d.return_sequences ? R.T * R.H : R.H;  // unroller.go:21-43
         break;
       }
       default:
@@ -1756,7 +1752,8 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         }
         // recurrence: the hidden-state products 2 x 3H x H per sample and step
         KTimer kt(c, GN_KCLASS_OTHER, "gru_fwd", 2.0 * 3 * H * H * B * R.T);
-        HIP_OK(c, launch_gru_fwd(R.xw, R.WhT, R.gpre, R.ghprev, R.grh, R.out, B, R.T, H, c->stream));
+        HIP_OK(c, launch_gru_fwd(R.xw, R.WhT, R.gpre, R.ghprev, R.grh, R.out, B, R.T, H, c->stream,
+                                 R.d.return_sequences ? 1 : 0));
         break;
       }
       case GN_LAYER_BATCHNORM2D: {  // running stats advance in training mode only
@@ -1792,7 +1789,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         // recurrence: Q13 leaves only the input gate with Wh h, 2 x H x H per sample and step
         KTimer kt(c, GN_KCLASS_OTHER, "lstm_fwd", 2.0 * R.H * R.H * B * R.T);
         HIP_OK(c, launch_lstm_fwd(R.xw, R.WhT, bias, R.igb, R.tcb, R.cbuf, R.hbuf, R.out, B, R.T,
-                                  R.H, c->stream));
+                                  R.H, c->stream, R.d.return_sequences ? 1 : 0));
         break;
       }
       default:
@@ -1979,7 +1976,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         float *gWx = M->grads + R.poff, *gWh = gWx + (int64_t)G3 * I, *gb = gWh + (int64_t)2 * H * H;
         {  // the recursion: Wh products 2 x 2H x H per sample and step
           KTimer kt(c, GN_KCLASS_OTHER, "gru_bwd", 2.0 * 2 * H * H * B * T);
-          HIP_OK(c, launch_gru_bwd(R.gout, R.gpre, R.ghprev, Wh, R.Dg, B, T, H, c->stream));
+          HIP_OK(c, launch_gru_bwd(R.gout, R.gpre, R.ghprev, Wh, R.Dg, B, T, H, c->stream,
+                                   R.d.return_sequences ? 1 : 0));
         }
         if (below && below->gout) {  // dx_t = Wx^T [dU | dR (never set, 0) | dC] (gru.go:481-500)
           GemmArgs a{};
@@ -2087,7 +2085,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           if (R.lcoop && lstm_coop_eligible(B, H)) {
             const hipError_t e = launch_lstm_bwd_coop(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg,
                                                       R.lsync, R.err, &R.lepoch, B, T, H,
-                                                      M->lstm_spin_limit, c->stream);
+                                                      M->lstm_spin_limit, c->stream, R.d.return_sequences ? 1 : 0);
             if (e == hipSuccess) {
               done = true;
             } else {  // refused (e.g. fewer free CUs than workgroups): per-sample kernel from now on
@@ -2096,7 +2094,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
             }
           }
           if (!done)
-            HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream));
+            HIP_OK(c, launch_lstm_bwd(R.gout, R.igb, R.tcb, R.cbuf, Wh, bias, R.Dg, B, T, H, c->stream,
+                                      R.d.return_sequences ? 1 : 0));
         }
         // Below another layer: its gradient dx_t = Wx^T dG_t from the unclipped
         // deltas (lstm.go:642-663; the unroller stacks the steps,

@@ -33,7 +33,8 @@ __global__ __launch_bounds__(1024) void gru_fwd_kernel(const float *__restrict__
                                                        float *__restrict__ pre,
                                                        float *__restrict__ hprev,
                                                        float *__restrict__ rh,
-                                                       float *__restrict__ out, int T, int H) {
+                                                       float *__restrict__ out, int T, int H,
+                                                       int seq) {
   extern __shared__ float sm[];
   float *h = sm, *srh = sm + H;
   const int b = blockIdx.x, i = threadIdx.x;
@@ -69,10 +70,11 @@ __global__ __launch_bounds__(1024) void gru_fwd_kernel(const float *__restrict__
       pre[row * 3 * H + 2 * H + i] = pc;
       rh[row * H + i] = srh[i];
       h[i] = hi + u * (c - hi);  // every read of h[] this step happened before the barrier
+      if (seq) out[row * H + i] = h[i];  // returnSequences: every state, [B][T][H]
     }
     __syncthreads();
   }
-  if (act) out[(size_t)b * H + i] = h[i];
+  if (act && !seq) out[(size_t)b * H + i] = h[i];
 }
 
 // g [B][H] = dL/dh_T; Wh [2H][H] as stored; writes dG [B*T][3H].
@@ -80,15 +82,19 @@ __global__ __launch_bounds__(1024) void gru_bwd_kernel(const float *__restrict__
                                                        const float *__restrict__ pre,
                                                        const float *__restrict__ hprev,
                                                        const float *__restrict__ Wh,
-                                                       float *__restrict__ dG, int T, int H) {
+                                                       float *__restrict__ dG, int T, int H,
+                                                       int seq) {
   extern __shared__ float sm[];
   float *sdu = sm, *sdcr = sm + H;
   const int b = blockIdx.x, i = threadIdx.x;
   const bool act = i < H;
-  float dh = act ? g[(size_t)b * H + i] : 0.f;
+  // g: dL/dh_T [B][H], or with seq dL/dh_t [B][T][H] added to the carried
+  // gradient at every step (unroller.go:192-198)
+  float dh = act ? (seq ? g[((size_t)b * T + T - 1) * H + i] : g[(size_t)b * H + i]) : 0.f;
   for (int t = T - 1; t >= 0; --t) {
     const size_t row = (size_t)b * T + t;
     float u = 0.f;
+    if (act && seq && t < T - 1) dh += g[row * H + i];
     if (act) {
       u = gru_sig(pre[row * 3 * H + i]);
       const float r = gru_sig(pre[row * 3 * H + H + i]);
@@ -117,20 +123,20 @@ __global__ __launch_bounds__(1024) void gru_bwd_kernel(const float *__restrict__
 bool gru_supported(int H) { return H >= 1 && H <= 1024; }
 
 hipError_t launch_gru_fwd(const float *xw, const float *WhT, float *pre, float *hprev, float *rh,
-                          float *out, int B, int T, int H, hipStream_t s) {
+                          float *out, int B, int T, int H, hipStream_t s, int seq) {
   if (!gru_supported(H)) return hipErrorInvalidValue;
   const int threads = (H + 63) / 64 * 64;
   hipLaunchKernelGGL(gru_fwd_kernel, dim3(B), dim3(threads), 2 * H * sizeof(float), s, xw, WhT, pre,
-                     hprev, rh, out, T, H);
+                     hprev, rh, out, T, H, seq);
   return hipGetLastError();
 }
 
 hipError_t launch_gru_bwd(const float *g, const float *pre, const float *hprev, const float *Wh,
-                          float *dG, int B, int T, int H, hipStream_t s) {
+                          float *dG, int B, int T, int H, hipStream_t s, int seq) {
   if (!gru_supported(H)) return hipErrorInvalidValue;
   const int threads = (H + 63) / 64 * 64;
   hipLaunchKernelGGL(gru_bwd_kernel, dim3(B), dim3(threads), 2 * H * sizeof(float), s, g, pre, hprev,
-                     Wh, dG, T, H);
+                     Wh, dG, T, H, seq);
   return hipGetLastError();
 }
 

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
                                                         float *__restrict__ cbuf,
                                                         float *__restrict__ hbuf,
                                                         float *__restrict__ out, int T, int H,
-                                                        int GB, int NQ, int QL) {
+                                                        int GB, int NQ, int QL, int seq) {
   extern __shared__ float sm[];
   float *hs = sm, *part = sm + ((H + 3) & ~3);  // part[NQ][H], 16-byte aligned
   float *Wl = part + NQ * H;                    // WhT rows [0, H*QL/NQ), 16-byte aligned
@@ -178,10 +178,11 @@ __global__ __launch_bounds__(1024) void lstm_fwd_kernel(const float *__restrict_
       cbuf[o] = c;
       hbuf[((size_t)b * (T + 1) + t + 1) * H + i] = hnew;
       hs[i] = hnew;
+      if (seq) out[((size_t)b * T + t) * H + i] = hnew;  // returnSequences: every state
     }
     __syncthreads();
   }
-  if (own) out[(size_t)b * H + i] = hnew;
+  if (own && !seq) out[(size_t)b * H + i] = hnew;
 }
 
 // The same recurrence with each thread's share of WhT in registers for the
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(1024) void lstm_fwd_reg_kernel(const float *__restr
                                                             float *__restrict__ cbuf,
                                                             float *__restrict__ hbuf,
                                                             float *__restrict__ out, int T, int H,
-                                                            int GB, int NQ) {
+                                                            int GB, int NQ, int seq) {
   extern __shared__ float sm[];
   float *hs = sm, *part = sm + ((H + 3) & ~3);  // part[NQ][H], 16-byte aligned
   const int b = blockIdx.x;
@@ -256,10 +257,11 @@ __global__ __launch_bounds__(1024) void lstm_fwd_reg_kernel(const float *__restr
       cbuf[o] = cc;
       hbuf[((size_t)b * (T + 1) + t + 1) * H + i] = hnew;
       hs[i] = hnew;
+      if (seq) out[((size_t)b * T + t) * H + i] = hnew;  // returnSequences: every state
     }
     __syncthreads();
   }
-  if (own) out[(size_t)b * H + i] = hnew;
+  if (own && !seq) out[(size_t)b * H + i] = hnew;
 }
 
 // BPTT deltas, one workgroup per sample.  gh = dL/dh_{T-1} [B][H].
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
                                                         const float *__restrict__ Wh,
                                                         const float *__restrict__ bias,
                                                         float *__restrict__ D, int T, int H,
-                                                        int GB, int NQ) {
+                                                        int GB, int NQ, int seq) {
   extern __shared__ float dG[];  // 4H, then part[NQ][H]
   float *part = dG + 4 * H;
   const int b = blockIdx.x;
@@ -284,10 +286,12 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
   const int G4 = 4 * H;
   float *Db = D + (size_t)b * (T + 1) * G4;
   for (int k = threadIdx.x; k < G4; k += blockDim.x) Db[(size_t)T * G4 + k] = 0.f;
-  float cur = own ? gh[(size_t)b * H + i] : 0.f, dcn = 0.f;
-  float fg = 0.f, gg = 0.f, og = 0.f, dfd = 0.f, dgd = 0.f, dod = 0.f;
-  float ign = 0.f, tcn = 0.f, cpn = 0.f;  // step t's saved values, fetched one step early
+  // gh: dL/dh_{T-1} [B][H], or with seq (returnSequences) dL/dh_t [B][T][H],
+  // added to the carried gradient at every step (unroller.go:192-198)
   const size_t ob = (size_t)b * T * H + i;
+  float cur = own ? (seq ? gh[ob + (size_t)(T - 1) * H] : gh[(size_t)b * H + i]) : 0.f, dcn = 0.f;
+  float fg = 0.f, gg = 0.f, og = 0.f, dfd = 0.f, dgd = 0.f, dod = 0.f;
+  float ign = 0.f, tcn = 0.f, cpn = 0.f, gsn = 0.f;  // step t's saved values, fetched one step early
   if (own) {
     fg = sigm(bias[H + i]);
     gg = tanh32(bias[2 * H + i]);
@@ -302,10 +306,12 @@ __global__ __launch_bounds__(1024) void lstm_bwd_kernel(const float *__restrict_
   for (int t = T - 1; t >= 0; --t) {
     if (own) {
       const float ig = ign, tc = tcn, cp = cpn;
+      if (seq && t < T - 1) cur += gsn;
       if (t > 0) {
         ign = igb[ob + (size_t)(t - 1) * H];
         tcn = tcb[ob + (size_t)(t - 1) * H];
         cpn = t > 1 ? cbuf[ob + (size_t)(t - 2) * H] : 0.f;
+        if (seq) gsn = gh[ob + (size_t)(t - 1) * H];
       }
       const float did = ig * (1.0f - ig);
       const float dc = cur * og * (1 - tc * tc) + dcn;
@@ -366,7 +372,7 @@ __host__ __device__ inline int lstm_coop_grid(int B) {
 static inline size_t lstm_coop_lds(int H) {
   const int U = H / LC_KM;
   return ((size_t)4 * H * (U + 4) + (size_t)LC_SPG * 4 * H + (size_t)(LC_NT / 64) * LC_SPG * U +
-          (size_t)2 * 3 * LC_SPG * U) *
+          (size_t)2 * 4 * LC_SPG * U) *
          sizeof(float);
 }
 
@@ -378,13 +384,13 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
     const float *__restrict__ gh, const float *__restrict__ igb, const float *__restrict__ tcb,
     const float *__restrict__ cbuf, const float *__restrict__ Wh, const float *__restrict__ bias,
     float *__restrict__ D, unsigned long long *X, int *err, int B, int T, int H, unsigned base,
-    int spin_limit) {
+    int spin_limit, int seq) {
   extern __shared__ float sm[];
   const int U = H / LC_KM, UP = U + 4, G4 = 4 * H;
   float *Wsl = sm;                          // [4H][UP]: Wh[r][u0 + u]
   float *dGs = Wsl + (size_t)G4 * UP;       // [SPG][4H]: the group's dG of this step
   float *part = dGs + LC_SPG * G4;          // [waves][SPG][U]
-  float *gpre = part + (LC_NT / 64) * LC_SPG * U;  // [2][3][SPG * U]: owners' next saved gates
+  float *gpre = part + (LC_NT / 64) * LC_SPG * U;  // [2][4][SPG * U]: owners' next ig, tc, c, dL/dh
   const int wg = blockIdx.x, xcd = wg & 7, rest = wg >> 3;
   const int m = rest % LC_KM, g = (rest / LC_KM) * 8 + xcd;
   const int ngroups = lstm_coop_groups(B);
@@ -405,7 +411,7 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
   float ign = 0.f, tcn = 0.f, cpn = 0.f;
   const size_t ob = (size_t)bo * T * H + io;
   if (valid) {
-    cur = gh[(size_t)bo * H + io];
+    cur = seq ? gh[ob + (size_t)(T - 1) * H] : gh[(size_t)bo * H + io];
     fg = sigm(bias[H + io]);
     gg = tanh32(bias[2 * H + io]);
     og = sigm(bias[3 * H + io]);
@@ -436,9 +442,10 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
       if (own) {
         // step 0's saved gates from the prologue, later ones prefetched into
         // LDS by the other waves during the previous step
-        const float *gp = gpre + (size_t)par * 3 * NO;
+        const float *gp = gpre + (size_t)par * 4 * NO;
         const float ig = step ? gp[tid] : ign, tc = step ? gp[NO + tid] : tcn,
                     cp = step ? gp[2 * NO + tid] : cpn;
+        if (seq && step) cur += gp[3 * NO + tid];  // this step's own gradient (unroller.go:192-198)
         const float did = ig * (1.0f - ig);
         const float dc = cur * og * (1 - tc * tc) + dcn;
         const float dv[4] = {dc * gg * did, dc * cp * dfd, dc * ig * dgd, cur * tc * dod};
@@ -474,11 +481,12 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
   const int r0 = min(share * rps, G4), r1 = min(r0 + rps, G4);
   constexpr int MAXW = (LC_SPG * 4 * 256 + NRT - 1) / NRT;  // exchange words per thread, H <= 256
   const int nw = LC_SPG * G4;
-  // prefetch role: thread rt < 3 * NO loads saved gate (rt / NO) of owner slot rt % NO
+  // prefetch role: thread rt < NK * NO loads value (rt / NO) of owner slot rt % NO
+  const int NK = seq ? 4 : 3;
   const int pk = rt / NO, ps = rt - pk * NO;
   const int pb = g * LC_SPG + ps / U, pu = u0 + ps % U;
-  const bool pv = rt < 3 * NO && pb < B;
-  const float *psrc = pk == 0 ? igb : (pk == 1 ? tcb : cbuf);
+  const bool pv = rt < NK * NO && pb < B;
+  const float *psrc = pk == 0 ? igb : (pk == 1 ? tcb : (pk == 2 ? cbuf : gh));
   const size_t pbase = (size_t)pb * T * H + pu;
   for (int step = 0; step < T; ++step) {
     const int t = T - 1 - step, par = t & 1;
@@ -495,7 +503,7 @@ __global__ __launch_bounds__(LC_NT) void lstm_bwd_coop_kernel(
       wv[k] = idx < nw ? __hip_atomic_load(xb + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                        : 0ull;
     }
-    if (rt < 3 * NO) gpre[(size_t)(par ^ 1) * 3 * NO + rt] = pre;
+    if (rt < NK * NO) gpre[(size_t)(par ^ 1) * 4 * NO + rt] = pre;
 #pragma unroll
     for (int k = 0; k < MAXW; ++k) {
       const int idx = rt + k * NRT;
@@ -1051,13 +1059,13 @@ static bool lstm_fits(int H) { return H >= 1 && H <= 1024; }
 
 hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias, float *igb,
                            float *tcb, float *cbuf, float *hbuf, float *out, int B, int T, int H,
-                           hipStream_t s) {
+                           hipStream_t s, int seq) {
   if (!lstm_fits(H)) return hipErrorInvalidValue;
   const LstmLayout L = lstm_layout(H, WhT);
   const size_t base = (size_t)(((H + 3) & ~3) + L.NQ * H) * sizeof(float);
   if (L.v4 && (H + L.NQ - 1) / L.NQ <= LF_R) {  // every thread's WhT share fits its registers
     hipLaunchKernelGGL(lstm_fwd_reg_kernel, dim3(B), dim3(1024), base, s, xw, WhT, bias, igb, tcb,
-                       cbuf, hbuf, out, T, H, L.GB, L.NQ);
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ, seq);
     return hipGetLastError();
   }
   // as many leading shares of WhT in LDS as fit 128 KB (whole float4 rows:
@@ -1075,25 +1083,25 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
   }
   if (L.v4)
     hipLaunchKernelGGL(lstm_fwd_kernel<true>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
-                       cbuf, hbuf, out, T, H, L.GB, L.NQ, QL);
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ, QL, seq);
   else
     hipLaunchKernelGGL(lstm_fwd_kernel<false>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
-                       cbuf, hbuf, out, T, H, L.GB, L.NQ, 0);
+                       cbuf, hbuf, out, T, H, L.GB, L.NQ, 0, seq);
   return hipGetLastError();
 }
 
 hipError_t launch_lstm_bwd(const float *gh, const float *igb, const float *tcb, const float *cbuf,
                            const float *Wh, const float *bias, float *D, int B, int T, int H,
-                           hipStream_t s) {
+                           hipStream_t s, int seq) {
   if (!lstm_fits(H)) return hipErrorInvalidValue;
   const LstmLayout L = lstm_layout(H, Wh);
   const size_t shm = (size_t)(4 * H + L.NQ * H) * sizeof(float);
   if (L.v4)
     hipLaunchKernelGGL(lstm_bwd_kernel<true>, dim3(B), dim3(1024), shm, s, gh, igb, tcb, cbuf, Wh,
-                       bias, D, T, H, L.GB, L.NQ);
+                       bias, D, T, H, L.GB, L.NQ, seq);
   else
     hipLaunchKernelGGL(lstm_bwd_kernel<false>, dim3(B), dim3(1024), shm, s, gh, igb, tcb, cbuf, Wh,
-                       bias, D, T, H, L.GB, L.NQ);
+                       bias, D, T, H, L.GB, L.NQ, seq);
   return hipGetLastError();
 }
 
@@ -1115,7 +1123,7 @@ size_t lstm_coop_sync_bytes(int B, int H) {
 hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *tcb,
                                 const float *cbuf, const float *Wh, const float *bias, float *D,
                                 void *sync, int *err, unsigned *epoch, int B, int T, int H,
-                                int spin_limit, hipStream_t s) {
+                                int spin_limit, hipStream_t s, int seq) {
   if (!lstm_coop_eligible(B, H)) return hipErrorInvalidValue;
   unsigned long long *X = reinterpret_cast<unsigned long long *>(sync);
   const size_t shm = lstm_coop_lds(H);
@@ -1129,7 +1137,8 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
   unsigned base = *epoch;
   void *args[] = {(void *)&gh, (void *)&igb, (void *)&tcb, (void *)&cbuf, (void *)&Wh,
                   (void *)&bias, (void *)&D, (void *)&X, (void *)&err,
-                  (void *)&B, (void *)&T, (void *)&H, (void *)&base, (void *)&spin_limit};
+                  (void *)&B, (void *)&T, (void *)&H, (void *)&base, (void *)&spin_limit,
+                  (void *)&seq};
   hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(lstm_bwd_coop_kernel),
                                             dim3(lstm_coop_grid(B)), dim3(LC_NT), args, shm, s);
   if (e == hipSuccess) *epoch = base + (unsigned)T;

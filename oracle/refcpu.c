@@ -1223,9 +1223,9 @@ static void gru_build(layer *L) {
   L->curGrad = zalloc(H);
   L->dhNextU = zalloc(H);
   L->gradInU = zalloc((int64_t)T * I);
-  L->outU = zalloc(H);
+  L->out_len = L->spec.return_sequences ? T * H : H; /* unroller.go:21-43 OutSize */
+  L->outU = zalloc(L->out_len);
   L->in_len = T * I;
-  L->out_len = H;
 }
 static void gru_init_params(layer *L) {
   int32_t I = L->spec.in_size, H = L->H;
@@ -1317,7 +1317,10 @@ static const float *gru_unroller_forward(layer *L, const float *x) {
   int32_t I = L->spec.in_size, H = L->H;
   for (int32_t i = 0; i < H; i++) L->savedH[i] = 0.0f; /* GRU.Reset (gru.go:171-180) */
   for (int32_t t = 0; t < L->T; t++) gru_step_forward(L, x + (int64_t)t * I, t);
-  memcpy(L->outU, L->savedH + (int64_t)L->T * H, sizeof(float) * H);
+  if (L->spec.return_sequences) /* every step's state (unroller.go:115-119) */
+    memcpy(L->outU, L->savedH + H, sizeof(float) * (int64_t)L->T * H);
+  else
+    memcpy(L->outU, L->savedH + (int64_t)L->T * H, sizeof(float) * H);
   return L->outU;
 }
 static const float *gru_unroller_backward(layer *L, const float *g) {
@@ -1325,7 +1328,9 @@ static const float *gru_unroller_backward(layer *L, const float *g) {
   for (int32_t i = 0; i < H; i++) L->dhNextU[i] = 0.0f;
   for (int32_t t = L->T - 1; t >= 0; t--) {
     memcpy(L->curGrad, L->dhNextU, sizeof(float) * H);
-    if (t == L->T - 1)
+    if (L->spec.return_sequences) /* unroller.go:192-198: every step's gradient */
+      for (int32_t i = 0; i < H; i++) L->curGrad[i] += g[(int64_t)t * H + i];
+    else if (t == L->T - 1)
       for (int32_t i = 0; i < H; i++) L->curGrad[i] += g[i];
     const float *dx = gru_step_backward(L, L->curGrad, t);
     memcpy(L->gradInU + (int64_t)t * I, dx, sizeof(float) * I);
@@ -1375,9 +1380,9 @@ static void lstm_build(layer *L) {
   L->curGrad = zalloc(H);
   L->dhNextU = zalloc(H);
   L->gradInU = zalloc((int64_t)T * in);
-  L->outU = zalloc(H);
+  L->out_len = L->spec.return_sequences ? T * H : H; /* unroller.go:21-43 OutSize */
+  L->outU = zalloc(L->out_len);
   L->in_len = T * in;
-  L->out_len = H;
 }
 
 static void lstm_init_params(layer *L) {
@@ -1515,8 +1520,12 @@ static const float *lstm_step_backward(layer *L, float *grad) {
 static const float *unroller_forward(layer *L, const float *x) {
   int32_t in = L->spec.in_size;
   lstm_reset(L);
-  for (int32_t t = 0; t < L->T; t++) lstm_step_forward(L, x + (int64_t)t * in);
-  memcpy(L->outU, L->hiddenBuf, sizeof(float) * L->H);
+  for (int32_t t = 0; t < L->T; t++) {
+    lstm_step_forward(L, x + (int64_t)t * in);
+    if (L->spec.return_sequences) /* every step's state (unroller.go:115-119) */
+      memcpy(L->outU + (int64_t)t * L->H, L->hiddenBuf, sizeof(float) * L->H);
+  }
+  if (!L->spec.return_sequences) memcpy(L->outU, L->hiddenBuf, sizeof(float) * L->H);
   return L->outU;
 }
 
@@ -1526,7 +1535,9 @@ static const float *unroller_backward(layer *L, const float *grad) {
   for (int32_t i = 0; i < H; i++) L->dhNextU[i] = 0;
   for (int32_t t = L->T - 1; t >= 0; t--) {
     memcpy(L->curGrad, L->dhNextU, sizeof(float) * H);
-    if (t == L->T - 1)
+    if (L->spec.return_sequences) /* unroller.go:192-198: every step's gradient */
+      for (int32_t i = 0; i < H; i++) L->curGrad[i] += grad[(int64_t)t * H + i];
+    else if (t == L->T - 1)
       for (int32_t i = 0; i < H; i++) L->curGrad[i] += grad[i];
     const float *dx = lstm_step_backward(L, L->curGrad);
     memcpy(L->gradInU + (int64_t)t * in, dx, sizeof(float) * in);
@@ -2134,7 +2145,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_MAXPOOL2D: o = maxpool_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_AVGPOOL2D: o = avgpool_forward(L, x, *len_io); *len_io = L->out_len; break;
     case GNO_LAYER_FLATTEN: o = x; L->in_len = L->out_len = *len_io; break; /* reshape.go:64-80 */
-    case GNO_LAYER_LSTM_UNROLLER: o = unroller_forward(L, x); *len_io = L->H; break;
+    case GNO_LAYER_LSTM_UNROLLER: o = unroller_forward(L, x); *len_io = L->out_len; break;
     case GNO_LAYER_EMBEDDING: o = emb_forward(L, x); *len_io = L->out_len; break;
     case GNO_LAYER_POSENC: o = pe_forward(L, x); break;
     case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
@@ -2144,7 +2155,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_RMSNORM: o = rms_forward(L, x, *len_io); break;
     case GNO_LAYER_SWIGLU: o = swiglu_forward(L, x); *len_io = L->spec.out_size; break;
     case GNO_LAYER_BATCHNORM2D: o = bn_forward(L, x, *len_io); break;
-    case GNO_LAYER_GRU_UNROLLER: o = gru_unroller_forward(L, x); *len_io = L->H; break;
+    case GNO_LAYER_GRU_UNROLLER: o = gru_unroller_forward(L, x); *len_io = L->out_len; break;
     case GNO_LAYER_MOE: o = moe_forward(L, x); *len_io = L->spec.out_size; break;
     default: o = x;
   }

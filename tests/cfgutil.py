@@ -52,10 +52,10 @@ def oracle_specs(refcpu, cfg):
             specs.append(refcpu.spec(refcpu.LAYER_CLSPOOL, seq_len=d["T"], dim=d["dim"]))
         elif k == "gru":
             specs.append(refcpu.spec(refcpu.LAYER_GRU_UNROLLER, in_size=d["in"], out_size=d["hidden"],
-                                     seq_len=d["T"]))
+                                     seq_len=d["T"], return_sequences=int(d.get("seq", False))))
         elif k == "lstm":
             specs.append(refcpu.spec(refcpu.LAYER_LSTM_UNROLLER, in_size=d["in"], out_size=d["hidden"],
-                                     seq_len=d["T"]))
+                                     seq_len=d["T"], return_sequences=int(d.get("seq", False))))
         else:
             raise NotImplementedError(k)
     return specs

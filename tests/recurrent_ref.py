@@ -19,23 +19,25 @@ def _lstm_params(rng, I, H, scale=0.4):
     return (rng.normal(size=n) * scale).astype(np.float32)
 
 
-def _lstm_torch(p, x, y, I, H, T, reference=True, keep_pre=False):
+def _lstm_torch(p, x, y, I, H, T, reference=True, keep_pre=False, seq=False):
     """Mean MSE over the batch of SequenceUnroller(LSTM(I, H), T, last) ->
-    Dense(H, 1, Linear); returns (loss, flat gradient, pre-activation
-    gradients [T][B, 4H], hidden states [T + 1][B, H])."""
+    Dense(H, 1, Linear) (seq: returnSequences, the Dense reads all T states);
+    returns (loss, flat gradient, pre-activation gradients [T][B, 4H], hidden
+    states [T + 1][B, H])."""
     B = x.shape[0]
     P = torch.tensor(p.astype(np.float64), requires_grad=True)
     nwx, nwh = 4 * H * I, 4 * H * H
     Wx = P[:nwx].view(4 * H, I)
     Wh = P[nwx:nwx + nwh].view(4 * H, H)
     b = P[nwx + nwh:nwx + nwh + 4 * H]
-    Wd = P[nwx + nwh + 4 * H:nwx + nwh + 5 * H].view(1, H)
-    bd = P[nwx + nwh + 5 * H:]
+    nd = (T if seq else 1) * H
+    Wd = P[nwx + nwh + 4 * H:nwx + nwh + 4 * H + nd].view(1, nd)
+    bd = P[nwx + nwh + 4 * H + nd:]
     X = torch.tensor(x.astype(np.float64)).view(B, T, I)
     xl = X[:, T - 1, :]
     h = torch.zeros(B, H, dtype=torch.float64)
     c = torch.zeros(B, H, dtype=torch.float64)
-    pres, hs = [], [h.detach().numpy().copy()]
+    pres, hs, states = [], [h.detach().numpy().copy()], []
     for t in range(T):
         xt = X[:, t, :]
         if reference:
@@ -57,8 +59,9 @@ def _lstm_torch(p, x, y, I, H, T, reference=True, keep_pre=False):
         if reference:
             hn = hn + _det(h)                                    # Q15
         h = hn
+        states.append(h)
         hs.append(h.detach().numpy().copy())
-    out = (h @ Wd.T + bd)[:, 0]
+    out = ((torch.cat(states, 1) if seq else h) @ Wd.T + bd)[:, 0]
     Y = torch.tensor(y.astype(np.float64)).view(B)
     loss = ((out - Y) ** 2).sum() / B
     loss.backward()
@@ -83,18 +86,20 @@ def _gru_params(rng, I, H, scale=0.4):
     return (rng.normal(size=n) * scale).astype(np.float32)
 
 
-def _gru_torch(p, x, y, I, H, T, reference=True):
+def _gru_torch(p, x, y, I, H, T, reference=True, seq=False):
     """Mean MSE over the batch of SequenceUnroller(GRU(I, H), T, last) ->
-    Dense(H, 1, Linear)."""
+    Dense(H, 1, Linear) (seq: returnSequences, the Dense reads all T states)."""
     B = x.shape[0]
     P = torch.tensor(p.astype(np.float64), requires_grad=True)
     nwx, nwh = 3 * H * I, 2 * H * H
     Wx = P[:nwx].view(3 * H, I)
     Wh = P[nwx:nwx + nwh].view(2 * H, H)
     b = P[nwx + nwh:nwx + nwh + 3 * H]
-    Wd = P[nwx + nwh + 3 * H:nwx + nwh + 4 * H].view(1, H)
-    bd = P[nwx + nwh + 4 * H:]
+    nd = (T if seq else 1) * H
+    Wd = P[nwx + nwh + 3 * H:nwx + nwh + 3 * H + nd].view(1, nd)
+    bd = P[nwx + nwh + 3 * H + nd:]
     Whu, Whr = Wh[:H], Wh[H:]
+    states = []
     X = torch.tensor(x.astype(np.float64)).view(B, T, I)
     xl = X[:, T - 1, :]
     h = torch.zeros(B, H, dtype=torch.float64)
@@ -117,7 +122,8 @@ def _gru_torch(p, x, y, I, H, T, reference=True):
             u = torch.sigmoid(b[:H] + zx[:, :H] + h @ Whu.T)
             c = torch.tanh(b[2 * H:] + zx[:, 2 * H:] + (r * h) @ Whr.T)
             h = h + u * (c - h)
-    out = (h @ Wd.T + bd)[:, 0]
+        states.append(h)
+    out = ((torch.cat(states, 1) if seq else h) @ Wd.T + bd)[:, 0]
     Y = torch.tensor(y.astype(np.float64)).view(B)
     loss = ((out - Y) ** 2).sum() / B
     loss.backward()

@@ -1,12 +1,15 @@
 """GPU parity for layer arrangements the reference accepts beyond the benchmark
 configs: a SequenceUnroller (LSTM or GRU) or an Embedding below other layers,
-and output layers that are not Dense.
+unrollers that return every state, and output layers that are not Dense.
 
   - SequenceUnroller not first: it hands the layer below dx_t = Wx^T dG_t for
     every step (lstm.go:642-663, gru.go:481-500, stacked by
     unroller.go:200-206), from the unclipped deltas;
   - Embedding not first: floor() of the layer below's outputs are its ids, and
     the layer below gets a zero gradient (embedding.go:156-163);
+  - SequenceUnroller(returnSequences = true) outputs every step's state and
+    adds each step's own gradient to the carried one (unroller.go:115-119,
+    192-198);
   - a non-Dense output layer receives the loss gradient itself (Network.Forward
     hands its output to the loss, net.go:212-223).
 
@@ -75,6 +78,23 @@ def cases():
                                            {"kind": "flatten", "n": 15},
                                            _dense(15, 2, "linear")]),
                               ((_normal(rng, B, 4) * 3).astype(np.float32), _normal(rng, B, 2)))
+    # SequenceUnroller(returnSequences = true): every state out, every step's gradient in
+    out["lstm_seq"] = (dict(num=29, name="lstm_seq", B=B, loss="mse", lr=1e-3, x="normal", in_len=5 * 3,
+                            layers=[{"kind": "lstm", "in": 3, "hidden": 6, "T": 5, "seq": True},
+                                    _dense(30, 1, "linear")]),
+                       (_normal(rng, B, 15), _normal(rng, B, 1)))
+    # H = 32: the cooperative BPTT kernel with the per-step gradients; then a
+    # second unroller on the state sequence (examples/stock_prediction_bilstm stacks them)
+    out["lstm_seq_coop_stack"] = (dict(num=30, name="lstm_seq_coop_stack", B=8, loss="mse", lr=1e-3,
+                                       x="normal", in_len=7 * 4,
+                                       layers=[{"kind": "lstm", "in": 4, "hidden": 32, "T": 7, "seq": True},
+                                               {"kind": "lstm", "in": 32, "hidden": 8, "T": 7},
+                                               _dense(8, 2, "linear")]),
+                                  (_normal(rng, 8, 28), _normal(rng, 8, 2)))
+    out["gru_seq"] = (dict(num=31, name="gru_seq", B=B, loss="mse", lr=1e-3, x="normal", in_len=4 * 3,
+                           layers=[{"kind": "gru", "in": 3, "hidden": 5, "T": 4, "seq": True},
+                                   _dense(20, 2, "linear")]),
+                      (_normal(rng, B, 12), _normal(rng, B, 2)))
     # output layers that are not Dense
     out["dropout_out"] = (dict(num=26, name="dropout_out", B=B, loss="mse", lr=1e-3, x="normal", in_len=10,
                                layers=[_dense(10, 6, "relu"), {"kind": "dropout", "p": 0.3, "n": 6}]),

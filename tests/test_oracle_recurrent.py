@@ -200,3 +200,88 @@ def test_gru_bptt_vs_autograd(oracle, T, I, H, B, workers):
     _, g_std = _gru_torch(p, x, y, I, H, T, reference=False)
     nl = 3 * H * I + 2 * H * H + 3 * H
     assert max_rel(g[:nl], g_std[:nl]) > 1e-2
+
+
+def _seq_params(rng, n_rec, T, H, scale=0.4):
+    return (rng.normal(size=n_rec + T * H + 1) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("workers,big", [(1, False), (2, True)])
+def test_lstm_return_sequences_vs_autograd(oracle, workers, big):
+    """SequenceUnroller(LSTM, returnSequences = true) -> Dense(T H, 1): the
+    output is every step's state (unroller.go:115-119) and the backward adds
+    each step's own gradient to the carried one (unroller.go:192-198).  The
+    torch model's loss reads all T states, so autograd gives that injection;
+    with large targets (big) the per-step clip acts and is applied to
+    autograd's per-step deltas in the worker chains."""
+    T, I, H, B = 6, 3, 5, 4
+    rng = np.random.default_rng(400 + workers)
+    nrec = 4 * H * I + 4 * H * H + 4 * H
+    p = _seq_params(rng, nrec, T, H)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    net = oracle.Net([oracle.spec(oracle.LAYER_LSTM_UNROLLER, in_size=I, out_size=H, seq_len=T,
+                                  return_sequences=1),
+                      oracle.spec(oracle.LAYER_DENSE, in_size=T * H, out_size=1, act=oracle.ACT_LINEAR)],
+                     oracle.LOSS_MSE, workers=workers)
+    assert net.n == p.size
+    net.params[:] = p
+    preds = np.array([net.forward(x[b])[0] for b in range(B)], np.float32)
+    y = (preds + (rng.normal(size=B) * 30 if big else 1e-2 * rng.choice([-1.0, 1.0], size=B))).astype(np.float32)
+    loss = net.accumulate_batch(x, y.reshape(B, 1), B)
+    g = net.grads.copy()
+    l_ref, g_ref, dpre, hs = _lstm_torch(p, x, y, I, H, T, keep_pre=True, seq=True)
+    # (targets 1e-3 from float32 predictions: the loss itself is ~1e-6)
+    assert abs(loss - l_ref) <= 1e-4 * abs(l_ref) + 1e-9
+    if big:
+        X = x.astype(np.float64).reshape(B, T, I)
+        W = min(workers, B)
+        chunk = (B + W - 1) // W
+        total = np.zeros(nrec)
+        active = 0
+        for c0 in range(0, B, chunk):
+            deltas = []
+            for bb in range(c0, min(B, c0 + chunk)):
+                for t in range(T - 1, -1, -1):
+                    dg = dpre[t][bb]
+                    deltas.append(np.concatenate([np.outer(dg, X[bb, T - 1]).ravel(),
+                                                  np.outer(dg, hs[t][bb]).ravel(), dg]))
+            total += _clip_chain(deltas)
+            run = np.cumsum(np.stack(deltas), axis=0)
+            active += int((np.linalg.norm(run, axis=1) > 1).sum())
+        assert active > 0
+        g_ref = g_ref.copy()
+        g_ref[:nrec] = total / B
+    else:
+        assert np.linalg.norm(g[:nrec]) * B < 0.5  # the clip never acts (running norms stay below 1)
+    parts = {k: v for k, v in _lstm_parts(I, H).items() if not k.startswith("dense")}
+    parts["dense_W"] = np.s_[nrec:nrec + T * H]
+    parts["dense_b"] = np.s_[nrec + T * H:]
+    _check_parts(g, g_ref, parts)
+    # only the last state read (returnSequences = false) gives other gradients
+    _, g_last, _, _ = _lstm_torch(np.concatenate([p[:nrec], p[nrec + (T - 1) * H:]]), x, y, I, H, T)
+    assert max_rel(g[:nrec], g_last[:nrec]) > 1e-2
+
+
+def test_gru_return_sequences_vs_autograd(oracle):
+    T, I, H, B = 5, 4, 6, 3
+    rng = np.random.default_rng(500)
+    nrec = 3 * H * I + 2 * H * H + 3 * H
+    p = _seq_params(rng, nrec, T, H)
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    y = rng.normal(size=B).astype(np.float32)
+    net = oracle.Net([oracle.spec(oracle.LAYER_GRU_UNROLLER, in_size=I, out_size=H, seq_len=T,
+                                  return_sequences=1),
+                      oracle.spec(oracle.LAYER_DENSE, in_size=T * H, out_size=1, act=oracle.ACT_LINEAR)],
+                     oracle.LOSS_MSE)
+    net.params[:] = p
+    loss = net.accumulate_batch(x, y.reshape(B, 1), B)
+    g = net.grads.copy()
+    l_ref, g_ref = _gru_torch(p, x, y, I, H, T, seq=True)
+    assert abs(loss - l_ref) <= 1e-4 * abs(l_ref)
+    parts = {k: v for k, v in _gru_parts(I, H).items() if not k.startswith("dense")}
+    for k in ("Wx_r", "b_r"):
+        assert not g[parts[k]].any() and not g_ref[parts[k]].any()
+        del parts[k]
+    parts["dense_W"] = np.s_[nrec:nrec + T * H]
+    parts["dense_b"] = np.s_[nrec + T * H:]
+    _check_parts(g, g_ref, parts)
