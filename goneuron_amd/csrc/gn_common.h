@@ -109,6 +109,11 @@ hipError_t launch_dact(const float *g, const float *out, float *dz, int64_t n, i
 hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz, float *loss_rows,
                            int B, int C, int row_act, int deriv, int loss_kind, const int32_t *bad,
                            int workers, hipStream_t s);
+// launch_out_rows with each row in registers (rows of up to 16384 classes;
+// hipErrorNotSupported for longer ones)
+hipError_t launch_out_rows_reg(float *out, const float *y, float *dz, float *loss_rows, int B, int C,
+                               int row_act, int deriv, int loss_kind, const int32_t *bad, int workers,
+                               hipStream_t s);
 enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMWISE = 3 };
 
 // dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
@@ -117,8 +122,6 @@ hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);
 // Row activation only (forward/predict)
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s);
 
-// mean loss: loss = (sum_b rows[b] in sample order) / B
-hipError_t launch_loss_mean(const float *rows, int B, int workers, float *loss, hipStream_t s);
 
 // dropout: out = x*scale where mask else 0 (mask is per-feature, Q9)
 hipError_t launch_dropout(const float *x, const float *mask, float scale, float *out, int B, int n,

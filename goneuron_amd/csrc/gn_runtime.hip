@@ -535,7 +535,8 @@ struct gn_model {
   int64_t nparams = 0, region = 0;
   float *arena = nullptr, *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
   int timestep = 0;
-  float *loss_rows = nullptr, *loss_dev = nullptr;
+  float *loss_rows = nullptr;
+  int loss_B = 0;  // rows of loss_rows the last training pass wrote
   float *xin = nullptr, *yin = nullptr;  // staging for host inputs
   int last_B = 0;
   bool last_predict = false;  // the last pass was an inference forward
@@ -1190,8 +1191,7 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
   }
   HIP_OK(c, hipMemcpyAsync(M->params, host.data(), (size_t)off * sizeof(float),
                            hipMemcpyHostToDevice, c->stream));
-  if ((rc = model_alloc(M.get(), 64, &M->loss_dev))) return rc;
-  HIP_OK(c, hipMemsetAsync(M->loss_dev, 0, 64 * sizeof(float), c->stream));
+
   if ((rc = alloc_batch(M.get()))) return rc;
   HIP_OK(c, hipStreamSynchronize(c->stream));
   *out = M.release();
@@ -2220,15 +2220,20 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   LayerRT &O = M->L.back();
   int row_act = O.ap.row_act;
   const int32_t *bad = M->emb >= 0 ? M->L[M->emb].bad : nullptr;
-  {  // read z and y, write the activation output and dz, one loss per row
+  {  // read z and y, write the activation output and dz, one loss per row (the batch loss is
+     // summed from the rows when it is read, gn_model_read_loss)
     KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * O.out_len + B));
-    HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
-                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
+    const hipError_t e = launch_out_rows_reg(O.out, y, O.gout, M->loss_rows, B, O.out_len, row_act,
+                                             O.ap.deriv, M->loss_kind, bad, M->workers, c->stream);
+    if (e == hipErrorNotSupported) {  // rows longer than 16384 classes
+      (void)hipGetLastError();
+      HIP_OK(c, launch_out_rows(O.out, y, O.out, O.gout, M->loss_rows, B, O.out_len, row_act,
+                                O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
+    } else {
+      HIP_OK(c, e);
+    }
   }
-  {
-    KTimer kt(c, GN_KCLASS_OTHER, "loss_mean", f4((double)B + 1));
-    HIP_OK(c, launch_loss_mean(M->loss_rows, B, M->workers, M->loss_dev, c->stream));
-  }
+  M->loss_B = B;
   // grads *= 1/B: float32 reciprocal (net.go:767-770), float32(1/float64(B))
   // for the W-worker path (net.go:703-706).
   const float scale = M->workers > 1 ? (float)(1.0 / (double)B) : 1.0f / (float)B;
@@ -2271,6 +2276,7 @@ static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B
   if (g && g->exec) {  // replay: the host state the pass would have set
     M->last_predict = false;
     M->last_B = B;
+    M->loss_B = B;
     HIP_OK(c, hipGraphLaunch(g->exec, c->stream));
     return GN_OK;
   }
@@ -2450,8 +2456,24 @@ extern "C" int gn_model_read_loss(gn_model *M, float *loss) {
   if (!M || !loss) return GN_ERR_INVALID;
   gn_ctx *c = M->ctx;
   ENTRY(c);
-  HIP_OK(c, hipMemcpyAsync(loss, M->loss_dev, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  // the batch loss of the last training pass, summed as the batch loop does:
+  // running float32 sums per worker chunk, the chunks' sums in worker order,
+  // divided by float32(B) (net.go:650-716 with W workers, :734-784 with one)
+  const int B = M->loss_B;
+  *loss = 0.0f;
+  if (B <= 0) return GN_OK;
+  std::vector<float> rows(B);
+  HIP_OK(c, hipMemcpyAsync(rows.data(), M->loss_rows, (size_t)B * sizeof(float), hipMemcpyDeviceToHost,
+                           c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
+  const int W = std::max(1, std::min(M->workers, B)), chunk = M->workers > 1 ? (B + W - 1) / W : B;
+  float total = 0.0f;
+  for (int c0 = 0; c0 < B; c0 += chunk) {
+    float local = 0.0f;
+    for (int i = c0; i < std::min(B, c0 + chunk); ++i) local += rows[i];
+    total += local;
+  }
+  *loss = total / (float)B;
   return check_flags(M);
 }
 

@@ -420,6 +420,194 @@ hipError_t launch_out_rows(const float *z, const float *y, float *out, float *dz
   return hipGetLastError();
 }
 
+// The same row computation with each row held in registers (G threads per
+// row, up to OR_PER values each): one pass over z and y, one exp per element
+// for the row activation; rows of G = 64 threads are reduced by wave shuffles
+// (four rows per block), longer groups through LDS (one row per block).
+constexpr int OR_PER = 16;
+
+// The float64 transcendentals out of line: inlined into the 16-way unrolled
+// row loops they made the kernels ~60 KB of code, fetched again by every wave.
+__device__ __attribute__((noinline)) float or_exp_diff(float a, float b) {
+  return (float)exp((double)(a - b));
+}
+__device__ __attribute__((noinline)) float or_exp(float a) { return (float)exp((double)a); }
+__device__ __attribute__((noinline)) float or_log(float a) { return (float)log((double)a); }
+__device__ __attribute__((noinline)) float or_fwd(float v, int kind) { return fwd_of(v, kind); }
+__device__ __attribute__((noinline)) float or_deriv(float o, int kind) { return deriv_of(o, kind); }
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v, float *sh, int slot) {
+  v = wave_sum(v);
+  if (G == 64) return v;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[slot * 16 + w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < G / 64; ++i) s += sh[slot * 16 + i];
+  return s;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v, float *sh, int slot) {
+  v = wave_max(v);
+  if (G == 64) return v;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) sh[slot * 16 + w] = v;
+  __syncthreads();
+  float m = sh[slot * 16];
+  for (int i = 1; i < G / 64; ++i) m = fmaxf(m, sh[slot * 16 + i]);
+  return m;
+}
+
+template <int G, int NT>
+__global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo,
+                                                          const float *__restrict__ y,
+                                                          float *__restrict__ dz,
+                                                          float *__restrict__ loss_rows, int B,
+                                                          int C, int row_act, int fwd, int deriv,
+                                                          int loss_kind,
+                                                          const int32_t *__restrict__ bad, int chunk) {
+  __shared__ float sh[16 * (NT / G) + 16];
+  constexpr int RPB = NT / G;
+  const int r = threadIdx.x / G, t = threadIdx.x % G;
+  const int b = blockIdx.x * RPB + r;
+  const bool row_ok = b < B;
+  bool valid = true, keep_loss = true;
+  if (bad && row_ok) {
+    if (chunk > 0) {
+      const int c0 = (b / chunk) * chunk, c1 = min(B, c0 + chunk);
+      for (int i = c0; i < c1; ++i)
+        if (bad[i]) {
+          keep_loss = false;
+          if (i <= b) valid = false;
+        }
+    } else {
+      valid = keep_loss = !bad[b];
+    }
+  }
+  float o[OR_PER], yv[OR_PER], d[OR_PER];
+  const float *zr = zo + (size_t)(row_ok ? b : 0) * C, *yr = y + (size_t)(row_ok ? b : 0) * C;
+#pragma unroll
+  for (int k = 0; k < OR_PER; ++k) {
+    const int i = t + k * G;
+    const bool in = row_ok && i < C;
+    o[k] = in ? zr[i] : 0.f;
+    yv[k] = in ? yr[i] : 0.f;
+  }
+  // row activation (activations.go:161-183, 204-236)
+  if (row_act == ROW_SOFTMAX || row_act == ROW_LOGSOFTMAX) {
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) mx = fmaxf(mx, o[k]);
+    mx = group_max<G>(mx, sh, r);
+    float ef[OR_PER], sm = 0.f;
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k) {
+      ef[k] = t + k * G < C ? or_exp_diff(o[k], mx) : 0.f;
+      sm += ef[k];
+    }
+    sm = group_sum<G>(sm, sh, r);
+    if (row_act == ROW_SOFTMAX) {
+#pragma unroll
+      for (int k = 0; k < OR_PER; ++k) o[k] = ef[k] / sm;
+    } else {
+      const float ls = or_log(sm);
+#pragma unroll
+      for (int k = 0; k < OR_PER; ++k) o[k] = o[k] - mx - ls;
+    }
+  } else if (row_act == ROW_ELEMWISE) {
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) o[k] = or_fwd(o[k], fwd);
+  }
+  // loss and its gradient (loss.go:53-105, 120-178)
+  float l = 0.f;
+  if (loss_kind == GN_LOSS_MSE) {
+    const float factor = 2.0f / (float)C;
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k) {
+      const bool in = t + k * G < C;
+      const float df = o[k] - yv[k];
+      l += in ? df * df : 0.f;
+      d[k] = factor * df;
+    }
+    l = group_sum<G>(l, sh, r) / (float)C;
+  } else {
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k) {
+      if (t + k * G < C) {
+        float pv = o[k];
+        if (pv < 1e-10f) pv = 1e-10f;
+        l -= yv[k] * or_log(pv);
+      }
+      d[k] = o[k] - yv[k];
+    }
+    l = group_sum<G>(l, sh, r);
+  }
+  // the activation's Jacobian / derivative (layer.go:504-567)
+  if (row_act == ROW_SOFTMAX) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) s1 += d[k] * o[k];
+    s1 = group_sum<G>(s1, sh, r);
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k) d[k] = d[k] * o[k] - o[k] * s1;
+  } else if (row_act == ROW_LOGSOFTMAX) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) s1 += d[k];
+    s1 = group_sum<G>(s1, sh, r);
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) d[k] = d[k] - or_exp(o[k]) * s1;
+  } else {
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k)
+      if (t + k * G < C) d[k] = d[k] * or_deriv(o[k], deriv);
+  }
+  if (row_ok) {
+    float *orow = zo + (size_t)b * C, *drow = dz + (size_t)b * C;
+#pragma unroll
+    for (int k = 0; k < OR_PER; ++k) {
+      const int i = t + k * G;
+      if (i < C) {
+        orow[i] = o[k];
+        drow[i] = valid ? d[k] : 0.0f;
+      }
+    }
+    if (t == 0) loss_rows[b] = keep_loss ? l : 0.0f;
+  }
+}
+
+// launch_out_rows for rows that fit the register kernels (C <= 16384);
+// hipErrorNotSupported otherwise.
+hipError_t launch_out_rows_reg(float *out, const float *y, float *dz, float *loss_rows, int B, int C,
+                               int row_act, int deriv, int loss_kind, const int32_t *bad, int workers,
+                               hipStream_t s) {
+  if (B <= 0) return hipSuccess;
+  const int fwd = row_act >> 8;
+  const int W = workers < 1 ? 1 : (workers > B ? B : workers);
+  const int chunk = workers > 1 ? (B + W - 1) / W : 0;
+  if (C <= 256) {
+    hipLaunchKernelGGL((out_rows_reg_kernel<64, 256>), dim3((B + 3) / 4), dim3(256), 0, s, out, y, dz,
+                       loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  } else if (C <= 256 * OR_PER) {
+    hipLaunchKernelGGL((out_rows_reg_kernel<256, 256>), dim3(B), dim3(256), 0, s, out, y, dz,
+                       loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  } else if (C <= 1024 * OR_PER) {
+    hipLaunchKernelGGL((out_rows_reg_kernel<1024, 1024>), dim3(B), dim3(1024), 0, s, out, y, dz,
+                       loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  } else {
+    return hipErrorNotSupported;
+  }
+  return hipGetLastError();
+}
+
 __global__ __launch_bounds__(TPB) void dropout_mask_kernel(float *__restrict__ mask, int n, float p) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -459,31 +647,6 @@ hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) 
   if (B <= 0 || (row_act & 0xff) == ROW_NONE) return hipSuccess;
   hipLaunchKernelGGL(row_act_kernel, dim3(B), dim3(row_threads(C)), 0, s, out, C, row_act & 0xff,
                      row_act >> 8);
-  return hipGetLastError();
-}
-
-// Batch loss: the mean over the batch of the per-sample losses, summed per
-// worker chunk and then over the chunks in worker order (net.go:679-716;
-// one chunk for W = 1, net.go:744).  Each chunk is summed by a block-wide tree
-// (a different float32 order than the reference's running sum, well inside
-// the loss tolerance), the chunk sums in order by thread 0.
-__global__ __launch_bounds__(TPB) void loss_mean_kernel(const float *__restrict__ rows, int B,
-                                                        int W, float *__restrict__ loss) {
-  __shared__ float sh[16];
-  const int chunk = W > 1 ? (B + W - 1) / W : B;
-  float total = 0.f;
-  for (int c0 = 0; c0 < B; c0 += chunk) {
-    const int c1 = min(B, c0 + chunk);
-    float s = 0.f;
-    for (int i = c0 + threadIdx.x; i < c1; i += TPB) s += rows[i];
-    s = block_sum(s, sh);
-    total += s;
-  }
-  if (threadIdx.x == 0) *loss = total / (float)B;
-}
-
-hipError_t launch_loss_mean(const float *rows, int B, int W, float *loss, hipStream_t s) {
-  hipLaunchKernelGGL(loss_mean_kernel, dim3(1), dim3(TPB), 0, s, rows, B, W, loss);
   return hipGetLastError();
 }
 
