@@ -28,7 +28,7 @@ __all__ = [
     "TransformerBlockExt", "ActReLU", "ActSwiGLU", "ActGELU", "NormLN", "NormRMS", "CLSPooling",
     "LSTM", "GRU", "SequenceUnroller",
     "ReLU", "Sigmoid", "Tanh", "Softmax", "LogSoftmax", "Linear", "GELU", "Ref", "Adam", "MSE",
-    "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError", "GGMLTypeF32", "GGMLTypeF16",
+    "CrossEntropy", "HIPDevice", "GetDefaultDevice", "GNError", "GGMLTypeF32", "GGMLTypeF16", "Load",
 ]
 
 # ---------------------------------------------------------------- activations
@@ -515,7 +515,11 @@ class Sequential:
         self._ck(lib().gn_model_layer_output(self.h, i, _fp(out), n))
         return out
 
-    # ---- checkpoints (net.go:1119-1392) ----
+    # ---- checkpoints (net.go:863-1392) ----
+    def Save(self, filename):
+        """Network.Save (net.go:863-871): the "GONN" gob file net.Load reads."""
+        self._ck(lib().gn_model_save_gob(self.h, str(filename).encode()))
+
     def SaveBinaryWeights(self, filename):
         """Network.SaveBinaryWeights (net.go:1119-1214)."""
         self._ck(lib().gn_model_save_binary_weights(self.h, str(filename).encode()))
@@ -570,6 +574,40 @@ class Sequential:
 
 def NewSequential(*layers, device=None) -> Sequential:
     return Sequential(*layers, device=device)
+
+
+def Load(filename, in_len=0, max_batch=1024, workers=1, device=None):
+    """goneuron.Load (goneuron.go:491-497, net.Load net.go:875-1005): the model
+    a Save file describes, with its parameters, the saved loss and a fresh
+    Adam(0.001); returns (model, loss).  in_len is the per-sample input length,
+    needed when the first layer is not Dense or Dropout."""
+    device = device or GetDefaultDevice()
+    h = C.c_void_p()
+    lk = C.c_int32()
+    check(device.h, lib().gn_model_load_gob(device.h, str(filename).encode(), int(in_len), int(max_batch),
+                                            int(workers), C.byref(h), C.byref(lk)))
+    n = C.c_int32()
+    check(device.h, lib().gn_model_layer_count(h, C.byref(n)))
+    layers = []
+    for i in range(n.value):
+        d = LayerDesc()
+        check(device.h, lib().gn_model_layer_desc(h, i, C.byref(d)))
+        layer = Layer(d.kind)
+        layer.desc = d
+        layers.append(layer)
+    m = Sequential(*layers, device=device)
+    m.opt = Adam(0.001)
+    m.loss = CrossEntropy if lk.value == LOSS_CE else MSE
+    m.workers = int(workers)
+    m.h = h
+    m.max_batch = int(max_batch)
+    _live_models.add(m)
+    cnt = C.c_int64()
+    check(device.h, lib().gn_model_nparams(h, C.byref(cnt)))
+    m.nparams = cnt.value
+    check(device.h, lib().gn_model_out_size(h, C.byref(n)))
+    m.out_size = n.value
+    return m, m.loss
 
 
 # ---------------------------------------------------------------- synthetic data

@@ -79,6 +79,9 @@ SIGNATURES = {
     "gn_model_nparams": (C.c_int, [vp, C.POINTER(C.c_int64)]),
     "gn_model_layer_params": (C.c_int, [vp, C.c_int32, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
     "gn_model_out_size": (C.c_int, [vp, i32p]),
+    "gn_model_layer_count": (C.c_int, [vp, i32p]),
+    "gn_model_layer_desc": (C.c_int, [vp, C.c_int32, C.POINTER(LayerDesc)]),
+    "gn_model_loss_kind": (C.c_int, [vp, i32p]),
     "gn_model_get_params": (C.c_int, [vp, f32p, C.c_int64, C.c_int64]),
     "gn_model_set_params": (C.c_int, [vp, f32p, C.c_int64, C.c_int64]),
     "gn_model_get_grads": (C.c_int, [vp, f32p, C.c_int64, C.c_int64]),
@@ -106,6 +109,8 @@ SIGNATURES = {
     "gn_model_save_gguf": (C.c_int, [vp, C.c_char_p, C.c_int32]),
     "gn_model_save_state": (C.c_int, [vp, C.c_char_p]),
     "gn_model_load_state": (C.c_int, [vp, C.c_char_p]),
+    "gn_model_save_gob": (C.c_int, [vp, C.c_char_p]),
+    "gn_model_load_gob": (C.c_int, [vp, C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.POINTER(vp), i32p]),
     "gn_model_set_running_stats": (C.c_int, [vp, C.c_int32, f32p, f32p, C.c_int32]),
     "gn_dense_forward": (C.c_int, [vp, vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32]),

@@ -289,6 +289,10 @@ const gn_layer_desc *model_layer_desc(gn_model *M, int i);
 int model_loss_kind(gn_model *M);
 std::vector<uint64_t> *model_noise_streams(gn_model *M, int i);  // MoE, else null
 void model_set_timestep(gn_model *M, int t);
+int model_timestep(gn_model *M);
+const gn_adam_desc &model_adam(gn_model *M);
+bool model_master_dims(gn_model *M);  // a forward pass ran on the network's own layers
+void model_layer_geom(gn_model *M, int i, ConvShape *cs, PoolShape *ps, float *eps);
 int model_error(gn_model *M, int code, const char *fmt, ...);    // records and returns code
 
 }  // namespace gn

@@ -569,6 +569,11 @@ struct gn_model {
   bool graph_on = true;   // gn_model_set_graphs
   int emb = -1;           // the Embedding layer (its index-error flags mask samples), or -1
   bool graph_ok = true;   // false once a capture failed: eager from then on
+  // a forward pass ran on the network's own layers (Predict, or training with
+  // one worker; trainBatchParallel runs clones only, net.go:588-716): from
+  // then on its Conv2D / pooling layers know their input height and width
+  // (conv2d.go:746, maxpool2d.go:119-127), which ExtractLayerConfig reads
+  bool master_dims = false;
 };
 
 static void drop_graphs(gn_model *M) {
@@ -1246,6 +1251,25 @@ extern "C" int gn_model_out_size(gn_model *M, int32_t *n) {
   return GN_OK;
 }
 
+extern "C" int gn_model_layer_count(gn_model *M, int32_t *n) {
+  if (!M || !n) return GN_ERR_INVALID;
+  *n = (int32_t)M->L.size();
+  return GN_OK;
+}
+
+extern "C" int gn_model_layer_desc(gn_model *M, int32_t i, gn_layer_desc *d) {
+  if (!M || !d) return GN_ERR_INVALID;
+  if (i < 0 || i >= (int)M->L.size()) return set_err(M->ctx, GN_ERR_INVALID, "layer %d out of range", i);
+  *d = M->L[i].d;
+  return GN_OK;
+}
+
+extern "C" int gn_model_loss_kind(gn_model *M, int32_t *k) {
+  if (!M || !k) return GN_ERR_INVALID;
+  *k = M->loss_kind;
+  return GN_OK;
+}
+
 static int arena_copy(gn_model *M, float *region, float *host, int64_t off, int64_t n, bool d2h) {
   gn_ctx *c = M->ctx;
   ENTRY(c);
@@ -1615,6 +1639,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
 // `for_loss`: the output layer keeps pre-activations for the row kernel.
 static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
   gn_ctx *c = M->ctx;
+  if (!for_loss || M->workers <= 1) M->master_dims = true;
   const float *cur = x;
   const int n = (int)M->L.size();
   for (int i = 0; i < n; ++i) {
@@ -1860,12 +1885,11 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_DROPOUT: {
         // dropout.go:283-290 in training mode; out of it the gradient passes
         // unchanged (dropout.go:241-247)
-        if (below && below->d.kind == GN_LAYER_FLATTEN)
-          return set_err(c, GN_ERR_UNSUPPORTED, "Flatten below Dropout");
-        if (below && M->eff[i]) {
+        // (a Flatten first in the network has no gradient buffer: nothing below needs one)
+        if (below && below->gout && M->eff[i]) {
           KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * R.out_len + R.out_len));
           HIP_OK(c, launch_dropout(R.gout, R.mask, R.scale, below->gout, B, R.out_len, c->stream));
-        } else if (below)
+        } else if (below && below->gout)
           HIP_OK(c, hipMemcpyAsync(below->gout, R.gout, (size_t)B * R.out_len * sizeof(float),
                                    hipMemcpyDeviceToDevice, c->stream));
         is_dz = false;
@@ -2587,6 +2611,14 @@ std::vector<uint64_t> *model_noise_streams(gn_model *M, int i) {
   return M->L[i].d.kind == GN_LAYER_MOE ? &M->L[i].mrng : nullptr;
 }
 void model_set_timestep(gn_model *M, int t) { M->timestep = t; }
+int model_timestep(gn_model *M) { return M->timestep; }
+const gn_adam_desc &model_adam(gn_model *M) { return M->adam; }
+bool model_master_dims(gn_model *M) { return M->master_dims; }
+void model_layer_geom(gn_model *M, int i, ConvShape *cs, PoolShape *ps, float *eps) {
+  if (cs) *cs = M->L[i].cs;
+  if (ps) *ps = M->L[i].ps;
+  if (eps) *eps = M->L[i].eps;
+}
 int model_error(gn_model *M, int code, const char *fmt, ...) {
   char buf[512];
   va_list ap;

@@ -146,6 +146,10 @@ void gn_model_destroy(gn_model *m);
 int gn_model_nparams(gn_model *m, int64_t *n);
 int gn_model_layer_params(gn_model *m, int32_t layer, int64_t *offset, int64_t *count);
 int gn_model_out_size(gn_model *m, int32_t *n);
+/* The layers as built (a loaded model's descriptions) and the loss. */
+int gn_model_layer_count(gn_model *m, int32_t *n);
+int gn_model_layer_desc(gn_model *m, int32_t layer, gn_layer_desc *out);
+int gn_model_loss_kind(gn_model *m, int32_t *loss_kind);
 /* Network.Params / SetParams / Gradients (net.go:549-572, 787-846). */
 int gn_model_get_params(gn_model *m, float *dst, int64_t offset, int64_t n);
 int gn_model_set_params(gn_model *m, const float *src, int64_t offset, int64_t n);
@@ -249,6 +253,24 @@ int gn_model_save_gguf(gn_model *m, const char *path, int32_t f16);
  * Adam moments. */
 int gn_model_save_state(gn_model *m, const char *path);
 int gn_model_load_state(gn_model *m, const char *path);
+/* Network.Save (net.go:863-871, Encode :1008-1075): "GONN", int32 1, then a
+ * gob stream of int32(layers), the loss name, "Adam", one LayerConfig per
+ * layer (ExtractLayerConfig, net.go:1393-1505), the flat parameters and
+ * Adam's GobState (opt.go:262-322: its moments only when the network has at
+ * most 1000 parameters, opt.go:129-153).  Byte for byte what a Go process
+ * writes when Save is its first use of gob (gob numbers types per process). */
+int gn_model_save_gob(gn_model *m, const char *path);
+/* net.Load (net.go:875-1005): the reference's checks (magic, version, at
+ * most 1000 layers, at most 256M parameters, the parameter count), then its
+ * layers rebuilt with their saved parameters, value activations, the saved
+ * loss and a fresh Adam(0.001) (the reference never restores the saved
+ * optimizer state).  in_len is the input length per sample, needed when the
+ * first layer is not Dense or Dropout (0 = from the file).  loss_kind
+ * receives GN_LOSS_*.  Layer types, losses and optimizers this library does
+ * not build are GN_ERR_UNSUPPORTED, as is a saved parameter count that
+ * differs from the layer its config describes. */
+int gn_model_load_gob(gn_ctx *ctx, const char *path, int32_t in_len, int32_t max_batch, int32_t workers,
+                      gn_model **out, int32_t *loss_kind);
 
 /* ---- per-layer operators on device pointers -----------------------------
  * Batched stand-ins for the per-sample Layer.Forward / Backward calls and the

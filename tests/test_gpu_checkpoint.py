@@ -8,6 +8,8 @@ import struct
 import numpy as np
 import pytest
 
+import goformats
+
 pytestmark = pytest.mark.gpu
 
 
@@ -63,6 +65,8 @@ def test_binary_weights_layout_and_round_trip(gn, tmp_path):
     model.SaveBinaryWeights(path)
     ver, ts = _read_gonn(path)
     assert ver == 1
+    # byte for byte what net.go:1119-1214 writes for these tensors
+    assert open(path, "rb").read() == goformats.binary_weights([(n, s, d) for n, s, d in ts])
     assert [(n, s) for n, s, _ in ts] == [
         ("layer_0_Conv2D_weights", (3, 2, 3, 3)), ("layer_0_Conv2D_biases", (3,)),
         ("layer_1_BatchNorm2D_running_mean", (3,)), ("layer_1_BatchNorm2D_running_var", (3,)),
@@ -160,6 +164,29 @@ def test_gguf_export(gn, tmp_path, f16):
     assert ts[0][1] == (13, 16) and ts[1][1] == (8, 16) and ts[12][1] == (24, 16)
     assert ts[14][1] == (16, 24)
     assert all(t == f16 for _, _, t, _ in ts)
+    # byte for byte what net.go:1222-1392 writes: the same tensors as
+    # NamedParams (consecutive slices of the parameters, names before the
+    # GGUF mapping), header, metadata, 32-byte alignment, F16 truncation
+    named = [[("weights", (13, 16))], [("weights", (8, 16))],
+             [(f"mha_{w}_{b}", (16, 16) if b == "weights" else (16,)) for w in ("wQ", "wK", "wV", "wOut")
+              for b in ("weights", "biases")] +
+             [("norm1_gamma", (16,)), ("norm2_gamma", (16,)), ("ff1_w", (24, 16)), ("ff1_v", (24, 16)),
+              ("ff2_weights", (16, 24)), ("ff2_biases", (16,))],
+             ("flat", p[:0]), [("weights", (13, 16)), ("biases", (13,))]]
+    off, layer_tensors = 0, []
+    for lt in named:
+        if isinstance(lt, tuple):
+            layer_tensors.append(lt)
+            continue
+        cur = []
+        for n, shape in lt:
+            k = int(np.prod(shape))
+            cur.append((n, shape, p[off:off + k]))
+            off += k
+        layer_tensors.append(cur)
+    assert off == p.size
+    want = goformats.gguf(layer_tensors, 5, "loss.CrossEntropy", f16)
+    assert open(path, "rb").read() == want
     got = np.concatenate([d.astype(np.float32) for _, _, _, d in ts])
     if not f16:
         np.testing.assert_array_equal(got, p)

@@ -95,6 +95,16 @@ def cases():
                            layers=[{"kind": "gru", "in": 3, "hidden": 5, "T": 4, "seq": True},
                                    _dense(20, 2, "linear")]),
                       (_normal(rng, B, 12), _normal(rng, B, 2)))
+    # Conv2D -> MaxPool2D -> Flatten -> Dropout -> Dense: Dropout above a Flatten
+    out["flatten_dropout"] = (dict(num=32, name="flatten_dropout", B=B, loss="ce", lr=1e-3, x="normal",
+                                   in_len=2 * 6 * 6, classes=3,
+                                   layers=[{"kind": "conv2d", "inC": 2, "outC": 3, "k": 3, "s": 1, "p": 1,
+                                            "act": "relu"},
+                                           {"kind": "maxpool2d", "k": 2, "s": 2, "p": 0, "inC": 3},
+                                           {"kind": "flatten", "n": 27},
+                                           {"kind": "dropout", "p": 0.25, "n": 27},
+                                           _dense(27, 3, "softmax", True)]),
+                              (_normal(rng, B, 72), _onehot(rng, B, 3)))
     # output layers that are not Dense
     out["dropout_out"] = (dict(num=26, name="dropout_out", B=B, loss="mse", lr=1e-3, x="normal", in_len=10,
                                layers=[_dense(10, 6, "relu"), {"kind": "dropout", "p": 0.3, "n": 6}]),
