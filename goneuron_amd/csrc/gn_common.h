@@ -66,6 +66,11 @@ struct GemmArgs {
   // z times these strides (floats; 0 shares the operand)
   int nbatch;
   int64_t bstride_A, bstride_B, bstride_bias, bstride_C;
+  // nbatch_in > 1: members form [nbatch / nbatch_in][nbatch_in]; member
+  // z = zo * nbatch_in + zi is advanced by zo times the strides above plus zi
+  // times these (attention's (sample, head) pairs inside [B*T, D] matrices)
+  int nbatch_in;
+  int64_t istride_A, istride_B, istride_C;
 };
 
 // EPI_SCALE    C = alpha*acc
@@ -275,7 +280,16 @@ hipError_t launch_rms_fwd(const float *x, const float *gam, float *y, float *rms
                           float eps, hipStream_t s);
 hipError_t launch_rms_bwd(const float *g, const float *x, const float *gam, const float *rms,
                           float *dx, float *gx, int rows, int N, hipStream_t s);
-bool attn_supported(int T, int D, int NH);
+bool attn_supported(int T, int D, int NH);  // the fused kernels: T <= 128, D / NH <= 32
+// Attention of any T and head size through batched GEMMs over the (sample,
+// head) pairs and row kernels: the scores / probabilities and their
+// gradients are materialised in `S` (attn_gemm_floats(B, T, NH) floats)
+size_t attn_gemm_floats(int B, int T, int NH);
+hipError_t launch_attn_fwd_gemm(const float *Q, const float *K, const float *V, float *O, int B, int T,
+                                int D, int NH, int causal, float *S, hipStream_t s);
+hipError_t launch_attn_bwd_gemm(const float *Q, const float *K, const float *V, const float *GO,
+                                float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
+                                float *S, hipStream_t s);
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s);
 hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *GO,

@@ -247,7 +247,7 @@ extern "C" int gn_layernorm_backward(gn_ctx *c, const float *g, const float *x, 
 // ---------------------------------------------------------------------------
 namespace {
 struct MhaWork {
-  float *Q, *K, *V, *O, *GO, *GQ, *GK, *GV, *S, *S3, *rcos, *rsin;
+  float *Q, *K, *V, *O, *GO, *GQ, *GK, *GV, *S, *S3, *rcos, *rsin, *SC;
   size_t floats;
 };
 MhaWork mha_carve(float *w, int B, int T, int D, int NH, int rope) {
@@ -267,13 +267,13 @@ MhaWork mha_carve(float *w, int B, int T, int D, int NH, int rope) {
   const size_t half = (size_t)std::max(D / std::max(NH, 1) / 2, 1);
   m.rcos = rope ? cv.take((size_t)T * half) : nullptr;
   m.rsin = rope ? cv.take((size_t)T * half) : nullptr;
+  m.SC = attn_supported(T, D, NH) ? nullptr : cv.take(attn_gemm_floats(B, T, NH));
   m.floats = cv.off;
   return m;
 }
 int mha_check(gn_ctx *c, int B, int T, int D, int NH) {
   if (B <= 0 || T <= 0 || D <= 0 || NH <= 0 || D % NH) return set_err(c, GN_ERR_INVALID, "bad MHA sizes");
-  if (!attn_supported(T, D, NH))
-    return set_err(c, GN_ERR_UNSUPPORTED, "attention needs T <= 128 and D / heads <= 32");
+  if ((int64_t)B * NH > 65535) return set_err(c, GN_ERR_UNSUPPORTED, "batch x heads above 65535");
   return GN_OK;
 }
 }  // namespace
@@ -327,7 +327,10 @@ extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, fl
   }
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, T, heads, hd, causal, false));
-    HIP_OK(c, launch_attn_fwd(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, c->stream));
+    if (m.SC)
+      HIP_OK(c, launch_attn_fwd_gemm(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, m.SC, c->stream));
+    else
+      HIP_OK(c, launch_attn_fwd(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, c->stream));
   }
   GemmArgs o{};
   o.M = rows; o.N = D; o.K = D;
@@ -384,7 +387,11 @@ extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, c
   }
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, heads, hd, causal, true));
-    HIP_OK(c, launch_attn_bwd(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, c->stream));
+    if (m.SC)
+      HIP_OK(c, launch_attn_bwd_gemm(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, m.SC,
+                                     c->stream));
+    else
+      HIP_OK(c, launch_attn_bwd(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, c->stream));
   }
   if (use_rope) {  // transformer.go:660-664: the conjugate rotation before wQ / wK
     KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));

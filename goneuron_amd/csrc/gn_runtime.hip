@@ -522,6 +522,7 @@ struct LayerRT {
     float *S3;  // token sums of gQ, gK, gV ([3][max batch][D])
     float *Z, *MG, *DZS;     // SwiGLU ff1: [gate | up] per token, token-0 mid grad, its dZ
     float *rcos, *rsin;      // RoPE angle tables [T][hd/2]
+    float *SC;               // attention scores and their gradients (sizes the fused kernels do not hold)
   } tb{};
 };
 
@@ -775,6 +776,9 @@ static int alloc_batch(gn_model *M) {
       if ((rc = model_balloc(M, rows * 2, &t.st2))) return rc;
       if ((rc = model_balloc(M, (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
       if ((rc = model_balloc(M, 3 * (size_t)max_batch * D, &t.S3))) return rc;
+      if (!attn_supported(R.T, R.D, R.NH) &&
+          (rc = model_balloc(M, attn_gemm_floats(max_batch, R.T, R.NH), &t.SC)))
+        return rc;
       if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
         if ((rc = model_balloc(M, rows * 2 * FF, &t.Z))) return rc;
         if ((rc = model_balloc(M, (size_t)max_batch * FF, &t.MG))) return rc;
@@ -1008,8 +1012,10 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.causal = R.d.causal;
         if (R.T <= 0 || R.D <= 0 || R.FF <= 0 || R.T * R.D != len)
           return set_err(c, GN_ERR_SHAPE, "layer %d: TransformerBlock %dx%d != input %d", i, R.T, R.D, len);
-        if (!attn_supported(R.T, R.D, R.NH))
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: attention needs T <= 128, D/heads <= 32", i);
+        if (R.NH <= 0 || R.D % R.NH)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: dim %d is not a multiple of %d heads", i, R.D, R.NH);
+        if ((int64_t)max_batch * R.NH > 65535)
+          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: batch x heads above 65535", i);
         if (R.d.block_act < GN_BLOCK_ACT_RELU || R.d.block_act > GN_BLOCK_ACT_GELU ||
             R.d.block_norm < GN_BLOCK_NORM_LN || R.d.block_norm > GN_BLOCK_NORM_RMS)
           return set_err(c, GN_ERR_INVALID, "layer %d: unknown TransformerBlock act %d / norm %d", i,
@@ -1472,7 +1478,10 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   }
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, R.T, R.NH, D / R.NH, R.causal, false));
-    HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, c->stream));
+    if (t.SC)
+      HIP_OK(c, launch_attn_fwd_gemm(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, t.SC, c->stream));
+    else
+      HIP_OK(c, launch_attn_fwd(t.Q, t.K, t.V, t.O, B, R.T, D, R.NH, R.causal, c->stream));
   }
   // res1 = x + wOut(o): the residual add rides in the GEMM epilogue
   HIP_OK(c, gemm_nt(c, t.O, P + o.wo, P + o.bo, t.RES1, rows, D, D, EPI_BIAS_ADD, 0, X));
@@ -1590,8 +1599,12 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, R.NH, D / R.NH, R.causal, true));
-    HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
-                              c->stream));
+    if (t.SC)
+      HIP_OK(c, launch_attn_bwd_gemm(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal, t.SC,
+                                     c->stream));
+    else
+      HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
+                                c->stream));
   }
   if (R.d.use_rope) {  // transformer.go:660-664: conjugate rotation before wQ/wK
     KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));

@@ -648,6 +648,135 @@ bool attn_supported(int T, int D, int NH) {
   return NH > 0 && D % NH == 0 && T >= 1 && T <= AT_T && D / NH <= AT_HD;
 }
 
+// ---------------------------------------------------------------------------
+// Attention of any sequence length and head size (the fused kernels above
+// hold T <= 128 keys and 32-wide heads in LDS).  The scores of every (sample,
+// head) pair are materialised: S = Q_h K_h^T by one batched MFMA GEMM over
+// the B x NH pairs (each a T x hd slice of the [B*T, D] matrices), a row
+// kernel applies the mask, the scale and the reference's row softmax, and a
+// second batched GEMM forms O_h = P V_h.  The backward recomputes P, forms
+// dP = gO_h V_h^T, turns it into gradScore = P (dP - sum_k dP_k P_k) / sqrt(hd)
+// in a row kernel (masked entries 0, transformer.go:583-630), and takes
+// gQ = G K_h, gK = G^T Q_h, gV = P^T gO_h as three batched GEMMs.
+// ---------------------------------------------------------------------------
+
+// Row r of S (member r / T, query i = r % T): masked keys j > i take -1e9,
+// the rest s / sqrt(hd) (transformer.go:466-477); then activations.go:161-183:
+// row max, exp of (x - max) in float64 rounded to float32, float32 sum, divide.
+__global__ __launch_bounds__(256) void attn_softmax_rows(float *__restrict__ S, int64_t rows, int T,
+                                                         int causal, float scale) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int i = (int)(r % T);
+  float *row = S + r * T;
+  float mx = -__builtin_inff();
+  for (int j = lane; j < T; j += 64) {
+    const float v = (causal && j > i) ? -1e9f : row[j] / scale;
+    row[j] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = wmax(mx);
+  float sum = 0.f;
+  for (int j = lane; j < T; j += 64) {
+    const float e = (float)exp((double)(row[j] - mx));
+    row[j] = e;
+    sum += e;
+  }
+  sum = wsum(sum);
+  for (int j = lane; j < T; j += 64) row[j] = row[j] / sum;
+}
+
+// G (holding dP) <- P (dP - sum_k dP_k P_k) / sqrt(hd) on unmasked keys, 0 on
+// masked ones (their gradRow entries are never formed, transformer.go:595-606)
+__global__ __launch_bounds__(256) void attn_dscore_rows(const float *__restrict__ P, float *__restrict__ G,
+                                                        int64_t rows, int T, int causal, float scale) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const int i = (int)(r % T);
+  const float *p = P + r * T;
+  float *g = G + r * T;
+  float d = 0.f;
+  for (int j = lane; j < T; j += 64)
+    if (!(causal && j > i)) d += g[j] * p[j];
+  d = wsum(d);
+  for (int j = lane; j < T; j += 64) g[j] = (causal && j > i) ? 0.f : (p[j] * (g[j] - d)) / scale;
+}
+
+size_t attn_gemm_floats(int B, int T, int NH) { return 2 * (size_t)B * NH * T * T; }
+
+namespace {
+// One batched GEMM over the (sample, head) pairs.  Operands are either a
+// head slice of a [B*T, D] matrix (sample stride T*D, head stride hd, row
+// pitch D) or a T x T block of the score buffer (stride T*T per pair).
+struct HeadOp {
+  const float *p;
+  bool scores;
+};
+hipError_t pair_gemm(char ta, char tb, int M, int N, int K, HeadOp A, HeadOp Bm, float *C, bool c_scores,
+                     int B, int T, int D, int NH, hipStream_t s) {
+  const int hd = D / NH;
+  const int64_t TT = (int64_t)T * T;
+  GemmArgs a{};
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.alpha = 1.f;
+  a.nbatch = B * NH;
+  a.nbatch_in = NH;
+  auto set = [&](HeadOp o, const float *&ptr, int &ld, int64_t &bs, int64_t &is) {
+    ptr = o.p;
+    ld = o.scores ? T : D;
+    bs = o.scores ? NH * TT : (int64_t)T * D;
+    is = o.scores ? TT : hd;
+  };
+  set(A, a.A, a.lda, a.bstride_A, a.istride_A);
+  set(Bm, a.B, a.ldb, a.bstride_B, a.istride_B);
+  const float *cp = nullptr;
+  set(HeadOp{C, c_scores}, cp, a.ldc, a.bstride_C, a.istride_C);
+  a.C = C;
+  return launch_gemm(ta, tb, EPI_SCALE, a, s);
+}
+hipError_t softmax_scores(float *S, int B, int T, int NH, int hd, int causal, hipStream_t s) {
+  const int64_t rows = (int64_t)B * NH * T;
+  hipLaunchKernelGGL(attn_softmax_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, S, rows, T, causal,
+                     (float)sqrt((double)hd));
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attn_fwd_gemm(const float *Q, const float *K, const float *V, float *O, int B, int T,
+                                int D, int NH, int causal, float *S, hipStream_t s) {
+  if ((int64_t)B * NH > 65535) return hipErrorInvalidConfiguration;  // grid z
+  const int hd = D / NH;
+  hipError_t e = pair_gemm('N', 'T', T, T, hd, {Q, false}, {K, false}, S, true, B, T, D, NH, s);
+  if (e == hipSuccess) e = softmax_scores(S, B, T, NH, hd, causal, s);
+  if (e == hipSuccess) e = pair_gemm('N', 'N', T, hd, T, {S, true}, {V, false}, O, false, B, T, D, NH, s);
+  return e;
+}
+
+hipError_t launch_attn_bwd_gemm(const float *Q, const float *K, const float *V, const float *GO,
+                                float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
+                                float *S, hipStream_t s) {
+  if ((int64_t)B * NH > 65535) return hipErrorInvalidConfiguration;
+  const int hd = D / NH;
+  float *P = S, *G = S + (size_t)B * NH * T * T;
+  hipError_t e = pair_gemm('N', 'T', T, T, hd, {Q, false}, {K, false}, P, true, B, T, D, NH, s);
+  if (e == hipSuccess) e = softmax_scores(P, B, T, NH, hd, causal, s);
+  if (e == hipSuccess) e = pair_gemm('N', 'T', T, T, hd, {GO, false}, {V, false}, G, true, B, T, D, NH, s);
+  if (e == hipSuccess) {
+    const int64_t rows = (int64_t)B * NH * T;
+    hipLaunchKernelGGL(attn_dscore_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, P, G, rows, T,
+                       causal, (float)sqrt((double)hd));
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = pair_gemm('N', 'N', T, hd, T, {G, true}, {K, false}, GQ, false, B, T, D, NH, s);
+  if (e == hipSuccess) e = pair_gemm('T', 'N', T, hd, T, {G, true}, {Q, false}, GK, false, B, T, D, NH, s);
+  if (e == hipSuccess) e = pair_gemm('T', 'N', T, hd, T, {P, true}, {GO, false}, GV, false, B, T, D, NH, s);
+  return e;
+}
+
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s) {
   hipLaunchKernelGGL(attn_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, O, T, D, NH, causal);

@@ -352,11 +352,15 @@ __device__ __forceinline__ void read_frags_direct(const float *S, int rowbase, i
 // Batched launches (gridDim.z > 1): the z-th GEMM's A, B, bias and C.
 __device__ __forceinline__ void batch_offsets(GemmArgs &p) {
   if (gridDim.z > 1) {
-    const int64_t z = blockIdx.z;
-    p.A += z * p.bstride_A;
-    p.B += z * p.bstride_B;
+    int64_t z = blockIdx.z, zi = 0;
+    if (p.nbatch_in > 1) {
+      zi = z % p.nbatch_in;
+      z /= p.nbatch_in;
+    }
+    p.A += z * p.bstride_A + zi * p.istride_A;
+    p.B += z * p.bstride_B + zi * p.istride_B;
     if (p.bias) p.bias += z * p.bstride_bias;
-    p.C += z * p.bstride_C;
+    p.C += z * p.bstride_C + zi * p.istride_C;
   }
 }
 
@@ -919,10 +923,12 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   // those cannot fill the chip, split K (down to one K stage per split: a lone
   // tile runs at 1/256 of the chip).  Partials go to the workspace and are
   // summed in split order.
-  const int t128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-  const int t64 = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+  // two-level batches (many small members) count the tiles of all members
+  const int64_t nmem = (a.nbatch > 1 && a.nbatch_in > 1) ? a.nbatch : 1;
+  const int64_t t128 = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128) * nmem;
+  const int64_t t64 = ((a.M + 63) / 64) * (int64_t)((a.N + 63) / 64) * nmem;
   const bool big = t128 >= 160;
-  const int tiles = big ? t128 : t64;
+  const int tiles = (int)std::min<int64_t>(big ? t128 : t64, 1 << 30);
   int splits = 1;
   if (tiles < 160 && a.K >= 2 * BK && a.ws) {
     splits = std::min((256 + tiles - 1) / tiles, a.K / BK);
@@ -933,17 +939,20 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
     kchunk = ((a.K + splits - 1) / splits + BK - 1) / BK * BK;
     splits = (a.K + kchunk - 1) / kchunk;
   }
-  const bool stride16 = ((a.bstride_A | a.bstride_B) & 3) == 0;
+  const bool two = a.nbatch_in > 1;
+  const bool stride16 = ((a.bstride_A | a.bstride_B | (two ? a.istride_A | a.istride_B : 0)) & 3) == 0;
   if (a.nbatch > 1 && (splits > 1 || !stride16)) {
     // split-K partials share one workspace, and float4 legality is judged on
     // the first member: one launch per GEMM of the batch
     for (int z = 0; z < a.nbatch; ++z) {
+      const int64_t zo = two ? z / a.nbatch_in : z, zi = two ? z % a.nbatch_in : 0;
       GemmArgs az = a;
       az.nbatch = 1;
-      az.A += z * a.bstride_A;
-      az.B += z * a.bstride_B;
-      if (az.bias) az.bias += z * a.bstride_bias;
-      az.C += z * a.bstride_C;
+      az.nbatch_in = 0;
+      az.A += zo * a.bstride_A + zi * a.istride_A;
+      az.B += zo * a.bstride_B + zi * a.istride_B;
+      if (az.bias) az.bias += zo * a.bstride_bias;
+      az.C += zo * a.bstride_C + zi * a.istride_C;
       const hipError_t ez = launch_gemm(ta, tb, epi, az, s);
       if (ez != hipSuccess) return ez;
     }

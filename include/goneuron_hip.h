@@ -360,8 +360,10 @@ int gn_layernorm_backward(gn_ctx *ctx, const float *g, const float *x, const flo
 /* MultiHeadAttention (transformer.go:277-776): x is B x T x D, params = [wQ |
  * wK | wV | wOut], each a Linear Dense (W D x D, b D).  work carries the
  * forward's saved state to the backward: gn_mha_workspace floats, the same
- * buffer and x for both calls.  Needs T <= 128 and D / heads <= 32
- * (GN_ERR_UNSUPPORTED otherwise). */
+ * buffer and x for both calls.  Any T and head size: up to T = 128 and
+ * 32-wide heads in fused kernels, beyond that through batched GEMMs over the
+ * materialised B x heads x T x T scores (included in the workspace); B x heads
+ * must not exceed 65535. */
 int gn_mha_workspace(int32_t B, int32_t T, int32_t D, int32_t heads, int32_t use_rope,
                      int64_t *floats);
 /* MultiHeadAttention.ForwardWithArena (transformer.go:405-529): Q, K, V per

@@ -192,7 +192,9 @@ def test_layernorm_ops(dev, oracle, B, rows, N, eps):
 
 # ---------------------------------------------------------------- MultiHeadAttention
 @pytest.mark.parametrize("B,T,D,NH,causal,rope", [
-    (4, 16, 64, 4, 1, 0), (3, 32, 64, 2, 0, 0), (2, 12, 48, 3, 1, 1), (5, 8, 32, 1, 0, 1)])
+    (4, 16, 64, 4, 1, 0), (3, 32, 64, 2, 0, 0), (2, 12, 48, 3, 1, 1), (5, 8, 32, 1, 0, 1),
+    # beyond the fused kernels (T > 128 or heads wider than 32): the batched-GEMM path
+    (2, 136, 80, 2, 1, 0), (3, 40, 128, 2, 0, 1), (1, 200, 96, 3, 1, 1)])
 def test_mha_ops(dev, oracle, B, T, D, NH, causal, rope):
     L, check = _lib()
     log(f"mha B={B} T={T} D={D} heads={NH} causal={causal} rope={rope}")
@@ -228,9 +230,11 @@ def test_mha_ops(dev, oracle, B, T, D, NH, causal, rope):
 
 
 def test_mha_ops_reject_unsupported(dev):
+    """More (sample, head) pairs than one launch's grid holds: refused on the
+    host before any launch."""
     L, _ = _lib()
     x = _zeros(dev, 8)
-    assert L.gn_mha_forward(dev.h, x.p, x.p, x.p, x.p, 1, 256, 64, 2, 0, 0) == -4  # GN_ERR_UNSUPPORTED
+    assert L.gn_mha_forward(dev.h, x.p, x.p, x.p, x.p, 40000, 2, 64, 2, 0, 0) == -4  # GN_ERR_UNSUPPORTED
 
 
 # ---------------------------------------------------------------- SequenceUnroller(LSTM)

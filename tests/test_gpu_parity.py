@@ -548,10 +548,13 @@ def test_gpt_small_random_block(gn, oracle, workers):
     _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
 
 
-@pytest.mark.parametrize("T,dim,heads,causal", [(13, 30, 2, False), (33, 64, 2, True), (97, 16, 1, False)])
+@pytest.mark.parametrize("T,dim,heads,causal", [(13, 30, 2, False), (33, 64, 2, True), (97, 16, 1, False),
+                                                 (144, 64, 2, True), (24, 96, 2, False), (130, 40, 1, True)])
 def test_gpt_attention_shapes(gn, oracle, T, dim, heads, causal):
     """Odd sequence lengths and head dims (LDS zero padding), the non-causal
-    path and a block-crossing causal mask, with a random block."""
+    path and a block-crossing causal mask, with a random block.  T > 128 or
+    heads wider than 32 (the last three) take the batched-GEMM attention
+    (transformer.go:405-690 has no size limit)."""
     from goneuron_amd import configs
     cfg = configs.gpt(B=3, T=T, vocab=29, dim=dim, heads=heads, ff=24, causal=causal)
     _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg))
@@ -570,6 +573,14 @@ def test_gpt_block_ext(gn, oracle, act, norm, rope, causal, workers):
     cfg = configs.gpt(B=5, T=12, vocab=37, dim=32, heads=4, ff=48, act=act, norm=norm, rope=rope,
                       causal=causal)
     _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
+
+
+def test_gpt_block_ext_long(gn, oracle):
+    """SwiGLU, RMSNorm and RoPE over 160 tokens with 48-wide heads (the
+    batched-GEMM attention), causal, 2 steps with 2 workers."""
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=4, T=160, vocab=31, dim=96, heads=2, ff=64, act="swiglu", norm="rms", rope=True)
+    _compare_step(gn, oracle, cfg, steps=2, workers=2, perturb=_random_block(cfg, scale=0.1))
 
 
 def test_gpt_block_ext_c4_size(gn, oracle):
