@@ -153,6 +153,41 @@ __global__ __launch_bounds__(CT) void maxpool_bwd_kernel(const float *__restrict
   }
 }
 
+// Windows that tile the plane exactly (stride == k, no padding, H and W
+// multiples of k): every input lies in one window, so a thread per window
+// writes its k x k inputs: the window's gradient where the argmax points,
+// 0 elsewhere (the same values as the gather above).
+__global__ __launch_bounds__(CT) void maxpool_bwd_tiled_kernel(const float *__restrict__ gout,
+                                                               const int32_t *__restrict__ argmax,
+                                                               float *__restrict__ gin, PoolShape s,
+                                                               int64_t n) {
+  const int64_t o = (int64_t)blockIdx.x * CT + threadIdx.x;
+  if (o >= n) return;
+  const int osz = s.oH * s.oW;
+  const int64_t plane = o / osz;  // b * C + c
+  const int pos = (int)(o - plane * osz), oh = pos / s.oW, ow = pos - oh * s.oW;
+  const int c = (int)(plane % s.C);
+  const int am = argmax[o];
+  const float g = gout[o];
+  float *gp = gin + plane * s.H * s.W;
+  for (int kh = 0; kh < s.k; ++kh) {
+    const int ih = oh * s.k + kh;
+    const int rowi = (c * s.H + ih) * s.W;  // flat index inside the sample
+    if (s.k == 2) {
+      const int iw = ow * 2;
+      float2 v;
+      v.x = am == rowi + iw ? g : 0.0f;
+      v.y = am == rowi + iw + 1 ? g : 0.0f;
+      *reinterpret_cast<float2 *>(gp + ih * s.W + iw) = v;
+    } else {
+      for (int kw = 0; kw < s.k; ++kw) {
+        const int iw = ow * s.k + kw;
+        gp[ih * s.W + iw] = am == rowi + iw ? g : 0.0f;
+      }
+    }
+  }
+}
+
 // Conv2D weight + bias gradient partials.  Block (b, band): positions of one
 // band of output rows of one sample; dz = gout * act'(out) is formed on the
 // fly.  Output slot o < outC*inC*k*k is dW (oc, ic, kh, kw), the last outC
@@ -504,6 +539,14 @@ hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const
 
 hipError_t launch_maxpool_bwd(const float *gout, const int32_t *argmax, float *gin,
                               const PoolShape &s, int B, hipStream_t st) {
+  const bool tiled = s.stride == s.k && s.pad == 0 && s.H == s.oH * s.k && s.W == s.oW * s.k &&
+                     (s.k != 2 || s.W % 2 == 0);
+  if (tiled) {
+    const int64_t n = (int64_t)B * s.C * s.oH * s.oW;
+    hipLaunchKernelGGL(maxpool_bwd_tiled_kernel, dim3((unsigned)((n + CT - 1) / CT)), dim3(CT), 0, st,
+                       gout, argmax, gin, s, n);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(B * s.C), dim3(CT), 0, st, gout, argmax, gin, s);
   return hipGetLastError();
 }

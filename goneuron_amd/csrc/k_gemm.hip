@@ -861,9 +861,12 @@ static hipError_t launch_t(bool vec, bool ktail, const GemmArgs &a, int tm, int 
                           int kchunk, hipStream_t s) {
   dim3 grid(tm * tn, splits, a.nbatch > 1 ? a.nbatch : 1), block(NT);
   if (R == 128 && vec && !ktail) {
-    // Four-wave kernels: two blocks per CU (32-deep stages, 64 KB of LDS)
-    // when there are at least two tiles per CU, else one (64-deep stages).
-    if (tm * tn * splits >= 512)
+    // Four-wave kernels: 32-deep stages (64 KB of LDS) when there are at
+    // least two tiles per CU (two blocks share a CU) or the K range is at most
+    // four 64-deep stages (the transformer's K = 256 projections: +0.7 % on
+    // its step; at K = 1024 the C3 step lost 3 %); else 64-deep stages, one
+    // block per CU.
+    if (tm * tn * splits >= 512 || kchunk <= 256)
       hipLaunchKernelGGL((gemm_f32_mfma_w4<32, 2, 128, AK, BKC, EPI>), grid, dim3(NT4), 0, s, a, tm, tn,
                          kchunk);
     else

@@ -121,8 +121,10 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
 
 // ---------------------------------------------------------------------------
 // Bias gradient: db[o] = scale * sum_b dz[b, o]   (gradB += dz, layer.go:566;
-// averaged by grads *= 1/B, net.go:767-770).  Two passes: 64-column strips x
-// row chunks -> partials (one per chunk), then an in-order sum of partials.
+// averaged by grads *= 1/B, net.go:767-770).  Blocks over 32-column strips
+// (whole 128-byte lines) and, when the strips alone are too few to keep the
+// chip's loads in flight, row chunks whose partials a second pass adds in
+// chunk order.
 // ---------------------------------------------------------------------------
 // Up to three column sums of equal shape in one launch (blockIdx.z selects the
 // matrix); each member is summed exactly as a launch of its own.
@@ -131,49 +133,97 @@ struct ColsumSet {
   float *out[3];
 };
 
-__global__ __launch_bounds__(TPB) void colsum_partial(ColsumSet set, int rows, int cols, int ld,
-                                                      int rows_per_chunk, float *__restrict__ part,
-                                                      float scale) {
-  __shared__ float red[4][64];
+// Partials summed in chunk order, one thread per column (coalesced rows).
+__global__ __launch_bounds__(TPB) void colsum_final(ColsumSet set, const float *__restrict__ part,
+                                                    int chunks, int cols, float scale) {
+  const int col = blockIdx.x * TPB + threadIdx.x;
+  if (col >= cols) return;
+  float *__restrict__ out = set.out[blockIdx.z];
+  part += (size_t)blockIdx.z * chunks * cols + col;
+  float s = 0.f;
+  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols];
+  out[col] = s * scale;
+}
+
+// One block per 32-column strip and row chunk (blockIdx.y; a single chunk
+// writes the scaled sums, several write partials for colsum_final).  V4 (cols
+// and ld multiples of 4, 16-byte aligned rows): thread t takes columns
+// 4 (t % 8) .. +3 of the strip and rows t / 8, t / 8 + 32, ... of the chunk
+// (whole 128-byte lines, CS_U loads in flight); otherwise column t % 32 and
+// rows t / 32, t / 32 + 8, ....  Each thread's rows are summed in row order,
+// then the row lanes of a column in lane order.
+constexpr int CS_W = 32;  // columns per strip
+constexpr int CS_U = 8;   // loads in flight per thread
+template <bool V4>
+__global__ __launch_bounds__(TPB) void colsum_strip(ColsumSet set, int rows, int cols, int ld,
+                                                    int rows_per_chunk, float *__restrict__ part,
+                                                    float scale) {
+  constexpr int RL = V4 ? TPB / (CS_W / 4) : TPB / CS_W;  // row lanes
+  __shared__ float red[RL][CS_W + 1];
   const float *__restrict__ dz = set.dz[blockIdx.z];
   float *__restrict__ out = set.out[blockIdx.z];
-  part += (size_t)blockIdx.z * gridDim.y * cols;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
-  const int r0 = blockIdx.y * rows_per_chunk;
-  const int r1 = min(rows, r0 + rows_per_chunk);
-  float s = 0.f;
-  if (col < cols)
-    for (int r = r0 + w; r < r1; r += 4) s += dz[(size_t)r * ld + col];
-  red[w][lane] = s;
+  const int t = threadIdx.x, c0 = blockIdx.x * CS_W;
+  const int r0 = blockIdx.y * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
+  if (V4) {
+    const int q = t % (CS_W / 4), rl = t / (CS_W / 4), col = c0 + 4 * q;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (col < cols) {
+      const float *p = dz + col;
+      int r = r0 + rl;
+      for (; r + (CS_U - 1) * RL < r1; r += CS_U * RL) {
+        float4 v[CS_U];
+#pragma unroll
+        for (int u = 0; u < CS_U; ++u) v[u] = *reinterpret_cast<const float4 *>(p + (size_t)(r + u * RL) * ld);
+#pragma unroll
+        for (int u = 0; u < CS_U; ++u) {
+          s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w;
+        }
+      }
+      for (; r < r1; r += RL) {
+        const float4 a = *reinterpret_cast<const float4 *>(p + (size_t)r * ld);
+        s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
+      }
+    }
+    red[rl][4 * q + 0] = s.x;
+    red[rl][4 * q + 1] = s.y;
+    red[rl][4 * q + 2] = s.z;
+    red[rl][4 * q + 3] = s.w;
+  } else {
+    const int cl = t % CS_W, rl = t / CS_W, col = c0 + cl;
+    float s = 0.f;
+    if (col < cols) {
+      const float *p = dz + col;
+      int r = r0 + rl;
+      for (; r + (CS_U - 1) * RL < r1; r += CS_U * RL) {
+        float v[CS_U];
+#pragma unroll
+        for (int u = 0; u < CS_U; ++u) v[u] = p[(size_t)(r + u * RL) * ld];
+#pragma unroll
+        for (int u = 0; u < CS_U; ++u) s += v[u];
+      }
+      for (; r < r1; r += RL) s += p[(size_t)r * ld];
+    }
+    red[rl][cl] = s;
+  }
   __syncthreads();
-  if (w == 0 && col < cols) {
-    const float v = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-    if (gridDim.y == 1) out[col] = v * scale;  // a single chunk is the whole sum
-    else part[(size_t)blockIdx.y * cols + col] = v;
+  if (t < CS_W && c0 + t < cols) {
+    float v = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < RL; ++j) v += red[j][t];
+    if (gridDim.y == 1) out[c0 + t] = v * scale;
+    else part[((size_t)blockIdx.z * gridDim.y + blockIdx.y) * cols + c0 + t] = v;
   }
 }
 
-// One wave per column: lanes take the chunks, then a wave reduction.
-__global__ __launch_bounds__(TPB) void colsum_final(ColsumSet set, const float *__restrict__ part,
-                                                    int chunks, int cols, float scale) {
-  const int lane = threadIdx.x & 63;
-  const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (col >= cols) return;
-  float *__restrict__ out = set.out[blockIdx.z];
-  part += (size_t)blockIdx.z * chunks * cols;
-  float s = 0.f;
-  for (int c = lane; c < chunks; c += 64) s += part[(size_t)c * cols + col];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  if (lane == 0) out[col] = s * scale;
-}
-
-static int colsum_chunks(int rows, int cols, size_t cap) {
-  int chunks = (rows + 63) / 64;
+// Row chunks: enough blocks to keep loads in flight across the chip (about
+// 256 strip blocks in all), each chunk at least 256 rows; one chunk (a single
+// launch) when the strips alone give that many blocks or the rows are few.
+static int colsum_chunks(int rows, int cols, int n, size_t cap) {
+  const int64_t strips = (int64_t)((cols + CS_W - 1) / CS_W) * n;
+  int64_t chunks = std::min<int64_t>((256 + strips - 1) / strips, (rows + 255) / 256);
   if (chunks > 64) chunks = 64;
-  if ((size_t)chunks * cols > cap) chunks = (int)(cap / cols);
-  return chunks < 1 ? 1 : chunks;
+  if (chunks > 1 && (size_t)chunks * cols * n > cap) chunks = (int64_t)(cap / ((size_t)cols * n));
+  return chunks < 1 ? 1 : (int)chunks;
 }
 
 hipError_t launch_colsum_multi(const float *const *dz, float *const *out, int n, int rows, int cols,
@@ -181,7 +231,7 @@ hipError_t launch_colsum_multi(const float *const *dz, float *const *out, int n,
                                hipStream_t s) {
   if (cols <= 0 || n <= 0) return hipSuccess;
   if (n > 3) return hipErrorInvalidValue;
-  const int chunks = colsum_chunks(rows, cols, scratch_cap);
+  const int chunks = colsum_chunks(rows, cols, n, scratch_cap);
   if (n > 1 && chunks > 1 && (size_t)n * chunks * cols > scratch_cap) {
     for (int i = 0; i < n; ++i) {  // partials of all members do not fit: one at a time
       const hipError_t e = launch_colsum_multi(dz + i, out + i, 1, rows, cols, ld, scale, scratch,
@@ -191,16 +241,21 @@ hipError_t launch_colsum_multi(const float *const *dz, float *const *out, int n,
     return hipSuccess;
   }
   ColsumSet set{};
+  bool v4 = cols % 4 == 0 && ld % 4 == 0;
   for (int i = 0; i < n; ++i) {
     set.dz[i] = dz[i];
     set.out[i] = out[i];
+    v4 = v4 && (reinterpret_cast<uintptr_t>(dz[i]) & 15) == 0;
   }
   const int rpc = (rows + chunks - 1) / chunks;
-  dim3 g1((cols + 63) / 64, chunks, n);
-  hipLaunchKernelGGL(colsum_partial, g1, dim3(TPB), 0, s, set, rows, cols, ld, rpc, scratch, scale);
+  const dim3 g((cols + CS_W - 1) / CS_W, chunks, n);
+  if (v4)
+    hipLaunchKernelGGL(colsum_strip<true>, g, dim3(TPB), 0, s, set, rows, cols, ld, rpc, scratch, scale);
+  else
+    hipLaunchKernelGGL(colsum_strip<false>, g, dim3(TPB), 0, s, set, rows, cols, ld, rpc, scratch, scale);
   if (chunks > 1)
-    hipLaunchKernelGGL(colsum_final, dim3((cols + 3) / 4, 1, n), dim3(TPB), 0, s, set, scratch,
-                       chunks, cols, scale);
+    hipLaunchKernelGGL(colsum_final, dim3((cols + TPB - 1) / TPB, 1, n), dim3(TPB), 0, s, set,
+                       scratch, chunks, cols, scale);
   return hipGetLastError();
 }
 
