@@ -123,6 +123,8 @@ enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMW
 
 // dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
 hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);
+// out = ((r + p0) + p1) + p2 with p_j = p + j * pstride
+hipError_t launch_add3(const float *r, const float *p, int64_t pstride, float *out, int64_t n, hipStream_t s);
 
 // Row activation only (forward/predict)
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s);
@@ -260,6 +262,9 @@ hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, 
 hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int B, int T, int V,
                         int D, int32_t *bad, hipStream_t s);
 hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int TD, hipStream_t s);
+// Embedding then PositionalEncoding: out = the embedding rows, pe_out = out + pe[t]
+hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int32_t *ids, float *out,
+                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s);
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
                              int D, int W, float scale, const int32_t *bad, hipStream_t s);
 hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
@@ -270,6 +275,9 @@ hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N,
                                   int64_t xstride, int64_t sstride, hipStream_t s);
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
                          int rows, int N, float eps, hipStream_t s);
+hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam, const float *stats,
+                                float *dx, float *dgam, float *dbet, int rows, int N, float scale,
+                                float *ws, size_t ws_cap, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
 // Rotary embedding of rows [rows, NH*hd] in place; position = row % T; cs/sn

@@ -1431,6 +1431,15 @@ static hipError_t tb_norm_bwd(gn_ctx *c, const LayerRT &R, const float *P, float
   LayerRT::Tb &t = const_cast<LayerRT &>(R).tb;
   const bool rms = R.d.block_norm == GN_BLOCK_NORM_RMS;
   hipError_t e;
+  if (!rms) {
+    // read g, x and the statistics, write dx; gamma / beta sums from the
+    // kernel's per-block partials
+    KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd", f4(3.0 * rows * D + 2.0 * rows + 2.0 * D));
+    e = launch_ln_bwd_params(g, x, P + og, st, dx, G + og, G + ob, rows, D, scale, c->scratch,
+                             c->scratch_floats, c->stream);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   {
     // read g, x and the statistics, write dx and g * xhat
     KTimer kt(c, GN_KCLASS_OTHER, rms ? "rms_bwd" : "ln_bwd", f4(4.0 * rows * D + (rms ? 1 : 2) * rows));
@@ -1641,9 +1650,29 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
-    HIP_OK(c, gemm_nn(c, t.GQ, P + o.wq, gin, rows, D, D, EPI_BIAS_ADD, 0, t.G2, 0));
-    HIP_OK(c, gemm_nn(c, t.GK, P + o.wk, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
-    HIP_OK(c, gemm_nn(c, t.GV, P + o.wv, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
+    const int64_t pst = (int64_t)rows * D;
+    if ((size_t)3 * pst <= c->scratch_floats) {
+      // the three products in one batched launch into the scratch, then
+      // added to dRES1 in the order of three accumulating launches
+      GemmArgs a{};
+      a.M = rows; a.N = D; a.K = D;
+      a.A = t.GQ; a.lda = D; a.B = P + o.wq; a.ldb = D;
+      a.C = c->scratch; a.ldc = D; a.alpha = 1.f;
+      a.nbatch = 3;
+      a.bstride_A = t.GK - t.GQ;
+      a.bstride_B = o.wk - o.wq;
+      a.bstride_C = pst;
+      {
+        KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+        HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+      }
+      KTimer kt(c, GN_KCLASS_OTHER, "add3", f4(5.0 * pst));
+      HIP_OK(c, launch_add3(t.G2, c->scratch, pst, gin, pst, c->stream));
+    } else {
+      HIP_OK(c, gemm_nn(c, t.GQ, P + o.wq, gin, rows, D, D, EPI_BIAS_ADD, 0, t.G2, 0));
+      HIP_OK(c, gemm_nn(c, t.GK, P + o.wk, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
+      HIP_OK(c, gemm_nn(c, t.GV, P + o.wv, gin, rows, D, D, EPI_BIAS_ADD, 0, gin, 0));
+    }
   }
   return GN_OK;
 }
@@ -1654,6 +1683,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
   gn_ctx *c = M->ctx;
   if (!for_loss || M->workers <= 1) M->master_dims = true;
   const float *cur = x;
+  bool pe_done = false;  // the PositionalEncoding output was written with the embedding rows
   const int n = (int)M->L.size();
   for (int i = 0; i < n; ++i) {
     LayerRT &R = M->L[i];
@@ -1698,12 +1728,26 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         break;
       }
       case GN_LAYER_EMBEDDING: {  // read the ids and their rows, write rows and int32 ids
+        LayerRT *pe = i + 1 < n ? &M->L[i + 1] : nullptr;
+        if (pe && pe->d.kind == GN_LAYER_POSENC && pe->T == R.T && pe->D == R.D) {
+          // and the PositionalEncoding output in the same pass
+          KTimer kt(c, GN_KCLASS_OTHER, "embed_pe_fwd",
+                    f4(2.0 * B * R.T + 3.0 * B * R.T * R.D + (double)R.T * R.D));
+          HIP_OK(c, launch_embed_pe(cur, M->params + R.poff, M->params + pe->poff, R.ids, R.out, pe->out, B,
+                                    R.T, R.V, R.D, R.bad, c->stream));
+          pe_done = true;
+          break;
+        }
         KTimer kt(c, GN_KCLASS_OTHER, "embed_fwd", f4(2.0 * B * R.T + 2.0 * B * R.T * R.D));
         HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B, R.T, R.V, R.D, R.bad,
                                c->stream));
         break;
       }
       case GN_LAYER_POSENC: {
+        if (pe_done) {  // written with the embedding rows
+          pe_done = false;
+          break;
+        }
         KTimer kt(c, GN_KCLASS_OTHER, "pe_add", f4(2.0 * B * R.T * R.D + (double)R.T * R.D));
         HIP_OK(c, launch_pe_add(cur, M->params + R.poff, R.out, B, R.T * R.D, c->stream));
         break;

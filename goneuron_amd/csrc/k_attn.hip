@@ -68,6 +68,37 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ x,
   }
 }
 
+// Embedding followed by PositionalEncoding in one pass: the embedding rows
+// as embed_kernel writes them, and pe_out = those rows + P[t] (the
+// PositionalEncoding output, pe_add_kernel's values).
+__global__ __launch_bounds__(256) void embed_pe_kernel(const float *__restrict__ x,
+                                                       const float *__restrict__ E,
+                                                       const float *__restrict__ pe,
+                                                       int32_t *__restrict__ ids,
+                                                       float *__restrict__ out,
+                                                       float *__restrict__ pe_out, int T, int V,
+                                                       int D, int32_t *__restrict__ bad) {
+  const int b = blockIdx.y;
+  const float *xs = x + (int64_t)b * T;
+  int any = 0;
+  for (int t = threadIdx.x; t < T; t += 256) {
+    const int idx = (int)floor((double)xs[t]);
+    any |= (idx < 0 || idx >= V) ? 1 : 0;
+  }
+  any = __syncthreads_or(any);
+  if (bad && blockIdx.x == 0 && threadIdx.x == 0) bad[b] = any ? 1 : 0;
+  const int64_t n = (int64_t)T * D;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
+    int idx = (int)floor((double)xs[t]);
+    if (idx < 0 || idx >= V) idx = 0;
+    if (d == 0) ids[(int64_t)b * T + t] = idx;
+    const float v = E[(int64_t)idx * D + d];
+    out[(int64_t)b * n + e] = v;
+    pe_out[(int64_t)b * n + e] = v + pe[e];
+  }
+}
+
 __global__ __launch_bounds__(256) void pe_add_kernel(const float *__restrict__ x,
                                                      const float *__restrict__ pe,
                                                      float *__restrict__ out, int64_t n, int TD) {
@@ -75,8 +106,9 @@ __global__ __launch_bounds__(256) void pe_add_kernel(const float *__restrict__ x
     out[e] = x[e] + pe[e % TD];
 }
 
-// grad[E] = 0 (a fill before the launch), then the token rows of each worker
-// chunk's contributing sample are scatter-added in (chunk, token) order.
+// grad[E] = 0 except the rows the scatter writes (zeroing blocks), and the
+// token rows of each worker chunk's contributing sample scatter-added in
+// (chunk, token) order.
 // Embedding.Backward zeroes the gradient first (embedding.go:152-154), so the
 // contributing sample is the last one whose backward ran: the chunk's last
 // sample, or with skipped samples (bad[b]) the last valid one (sequential
@@ -87,14 +119,20 @@ __global__ __launch_bounds__(256) void pe_add_kernel(const float *__restrict__ x
 // whose id appeared earlier write nothing, so all writes are to distinct rows.
 constexpr int EG_MAXL = 2048;  // contributing rows held in LDS
 
+// Blocks L.. zero the rows of gradE that no contributing row writes, EG_ZR
+// rows each (the fill the reference's zeroing amounts to, without a launch of
+// its own).
+constexpr int EG_ZR = 32;
 __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict__ g,
                                                          const int32_t *__restrict__ ids,
                                                          float *__restrict__ gradE, int B, int T,
                                                          int D, int chunk, int L, float scale,
-                                                         const int32_t *__restrict__ bad, int par) {
+                                                         const int32_t *__restrict__ bad, int par,
+                                                         int V) {
   __shared__ int sid[EG_MAXL];
   __shared__ int csamp[EG_MAXL];
   __shared__ int first;
+  __shared__ int hit[EG_ZR];
   const int l = blockIdx.x, nch = L / T;
   for (int w = threadIdx.x; w < nch; w += 256) {
     const int c0 = w * chunk, c1 = min(B, c0 + chunk);
@@ -117,6 +155,22 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
     sid[e] = sm < 0 ? -1 : ids[(int64_t)sm * T + e % T];
   }
   if (threadIdx.x == 0) first = 1;
+  if (l >= L) {  // zeroing block: rows [z0, z1) minus the contributing ids
+    const int z0 = (l - L) * EG_ZR, z1 = min(V, z0 + EG_ZR);
+    if (threadIdx.x < EG_ZR) hit[threadIdx.x] = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < L; e += 256) {
+      const int id = sid[e];
+      if (id >= z0 && id < z1) hit[id - z0] = 1;  // every writer stores 1
+    }
+    __syncthreads();
+    const int64_t n = (int64_t)(z1 - z0) * D;
+    for (int64_t e = threadIdx.x; e < n; e += 256) {
+      const int r = (int)(e / D);
+      if (!hit[r]) gradE[(int64_t)z0 * D + e] = 0.0f;
+    }
+    return;
+  }
   __syncthreads();
   const int my = sid[l];
   if (my < 0) return;  // uniform over the block
@@ -233,6 +287,117 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
     v -= (diff * sgx) / (nf * std * std);
     dx[(int64_t)r * N + i] = v;
     gx[(int64_t)r * N + i] = gr[i] * (diff / std);
+  }
+}
+
+// The same dx, and instead of the g * xhat matrix, the block's own column
+// sums of g * xhat (gamma) and g (beta): block = 4 waves x LN_RW rows; a wave
+// loads its rows' g and x into registers at once (lane i holds columns i,
+// i + 64, ..., N <= 64 LN_MAXC), then finishes them row by row; the waves'
+// sums are added in wave order and written as one partial row pair
+// part[block][0 .. 2N) for ln_param_final.
+constexpr int LN_RW = 4, LN_MAXC = 8, LN_RPB = 4 * LN_RW;
+__global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ x,
+                                                          const float *__restrict__ gam,
+                                                          const float *__restrict__ stats,
+                                                          float *__restrict__ dx,
+                                                          float *__restrict__ part, int rows, int N) {
+  __shared__ float red[4][2][LN_MAXC * 64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rbase = blockIdx.x * LN_RPB + w * LN_RW;
+  float gv[LN_RW][LN_MAXC], xv[LN_RW][LN_MAXC], gm[LN_MAXC], mean[LN_RW], sd[LN_RW];
+#pragma unroll
+  for (int j = 0; j < LN_MAXC; ++j) {
+    const int i = lane + 64 * j;
+    gm[j] = i < N ? gam[i] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < LN_RW; ++q) {
+    const int r = min(rbase + q, rows - 1);
+    mean[q] = stats[2 * r];
+    sd[q] = stats[2 * r + 1];
+#pragma unroll
+    for (int j = 0; j < LN_MAXC; ++j) {
+      const int i = lane + 64 * j;
+      gv[q][j] = i < N ? g[(int64_t)r * N + i] : 0.f;
+      xv[q][j] = i < N ? x[(int64_t)r * N + i] : 0.f;
+    }
+  }
+  float pg[LN_MAXC], pb[LN_MAXC];
+#pragma unroll
+  for (int j = 0; j < LN_MAXC; ++j) pg[j] = pb[j] = 0.f;
+  const float nf = (float)N;
+#pragma unroll
+  for (int q = 0; q < LN_RW; ++q) {
+    const int r = rbase + q;
+    if (r >= rows) break;  // uniform over the wave
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int j = 0; j < LN_MAXC; ++j)
+      if (lane + 64 * j < N) {
+        const float gp = gv[q][j] * gm[j];
+        sg += gp;
+        sgx += gp * (xv[q][j] - mean[q]);
+      }
+    sg = wsum(sg);
+    sgx = wsum(sgx);
+    const float std = sd[q];
+#pragma unroll
+    for (int j = 0; j < LN_MAXC; ++j) {
+      const int i = lane + 64 * j;
+      if (i < N) {
+        const float diff = xv[q][j] - mean[q];
+        const float gi = gv[q][j], gp = gi * gm[j];
+        float v = (gp - sg / nf) / std;
+        v -= (diff * sgx) / (nf * std * std);
+        dx[(int64_t)r * N + i] = v;
+        pg[j] += gi * (diff / std);
+        pb[j] += gi;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < LN_MAXC; ++j) {
+    red[w][0][j * 64 + lane] = pg[j];
+    red[w][1][j * 64 + lane] = pb[j];
+  }
+  __syncthreads();
+  float *pp = part + (size_t)blockIdx.x * 2 * N;
+  for (int i = threadIdx.x; i < N; i += 256) {
+    pp[i] = (red[0][0][i] + red[1][0][i]) + (red[2][0][i] + red[3][0][i]);
+    pp[N + i] = (red[0][1][i] + red[1][1][i]) + (red[2][1][i] + red[3][1][i]);
+  }
+}
+
+// dgamma / dbeta: the blocks' partials summed per column of [gamma | beta]:
+// a block takes 64 columns (one per lane), its 4 waves every 4th partial in
+// block order, and the 4 sums are added in wave order, times scale.
+__global__ __launch_bounds__(256) void ln_param_final(const float *__restrict__ part, int nblk, int N,
+                                                      float scale, float *__restrict__ dgam,
+                                                      float *__restrict__ dbet) {
+  __shared__ float red[4][64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 64 + lane;
+  float s = 0.f;
+  if (c < 2 * N) {
+    int b = w;
+    for (; b + 12 < nblk; b += 16) {
+      const float v0 = part[(size_t)b * 2 * N + c], v1 = part[(size_t)(b + 4) * 2 * N + c];
+      const float v2 = part[(size_t)(b + 8) * 2 * N + c], v3 = part[(size_t)(b + 12) * 2 * N + c];
+      s += v0;
+      s += v1;
+      s += v2;
+      s += v3;
+    }
+    for (; b < nblk; b += 4) s += part[(size_t)b * 2 * N + c];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && c < 2 * N) {
+    const float v = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) * scale;
+    if (c < N) dgam[c] = v;
+    else dbet[c - N] = v;
   }
 }
 
@@ -559,6 +724,15 @@ hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out
   return hipGetLastError();
 }
 
+hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int32_t *ids, float *out,
+                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s) {
+  if (B <= 0) return hipSuccess;
+  const int64_t n = (int64_t)T * D;
+  unsigned bx = (unsigned)std::min<int64_t>((n + 255) / 256, 64);
+  hipLaunchKernelGGL(embed_pe_kernel, dim3(bx, B), dim3(256), 0, s, x, E, pe, ids, out, pe_out, T, V, D, bad);
+  return hipGetLastError();
+}
+
 hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int TD, hipStream_t s) {
   const int64_t n = (int64_t)B * TD;
   hipLaunchKernelGGL(pe_add_kernel, dim3(blocks_for(n)), dim3(256), 0, s, x, pe, out, n, TD);
@@ -572,10 +746,9 @@ hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, i
   const int nsamp = (B + chunk - 1) / chunk;  // one contributing sample per chunk
   const int L = nsamp * T;
   if (L > EG_MAXL) return hipErrorInvalidValue;
-  hipError_t e = launch_fill(gradE, 0.0f, (int64_t)V * D, s);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(embed_grad_kernel, dim3(L), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
-                     scale, bad, W > 1 ? 1 : 0);
+  const int zb = (V + EG_ZR - 1) / EG_ZR;
+  hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
+                     scale, bad, W > 1 ? 1 : 0, V);
   return hipGetLastError();
 }
 
@@ -607,6 +780,20 @@ hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, flo
                          int rows, int N, float eps, hipStream_t s) {
   hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gam, bet, y, stats,
                      rows, N, eps);
+  return hipGetLastError();
+}
+
+// dx plus the gamma / beta gradients (scaled) through per-block partials in
+// ws; hipErrorNotSupported when N or the partials do not fit.
+hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam, const float *stats,
+                                float *dx, float *dgam, float *dbet, int rows, int N, float scale,
+                                float *ws, size_t ws_cap, hipStream_t s) {
+  const int nblk = (rows + LN_RPB - 1) / LN_RPB;
+  if (N > 64 * LN_MAXC || (size_t)nblk * 2 * N > ws_cap) return hipErrorNotSupported;
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(256), 0, s, g, x, gam, stats, dx, ws, rows, N);
+  hipLaunchKernelGGL(ln_param_final, dim3((2 * N + 63) / 64), dim3(256), 0, s, ws, nblk, N, scale, dgam,
+                     dbet);
   return hipGetLastError();
 }
 

@@ -677,6 +677,27 @@ hipError_t launch_dropout_mask(float *mask, int n, float p, hipStream_t s) {
   return hipGetLastError();
 }
 
+// out = ((r + p[0]) + p[1]) + p[2], p[j] = p0 + j * pstride: three products
+// added to a residual gradient in the order three accumulating launches
+// would add them.
+__global__ __launch_bounds__(TPB) void add3_kernel(const float *__restrict__ r, const float *__restrict__ p,
+                                                   int64_t pstride, float *__restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v = r[i] + p[i];
+    v = p[pstride + i] + v;
+    out[i] = p[2 * pstride + i] + v;
+  }
+}
+
+hipError_t launch_add3(const float *r, const float *p, int64_t pstride, float *out, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  int64_t blocks = (n + TPB - 1) / TPB;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(add3_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, r, p, pstride, out, n);
+  return hipGetLastError();
+}
+
 // dst[0, n) = v (a kernel, not a memset node: usable inside a captured graph)
 __global__ __launch_bounds__(TPB) void fill_kernel(float *__restrict__ dst, float v, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
