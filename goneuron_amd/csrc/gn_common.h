@@ -62,6 +62,7 @@ struct GemmArgs {
   float *ws;          // split-K workspace (may be null: no split)
   size_t ws_cap;      // floats
   int aux_div;        // EPI_DACT: > 1 reads aux row (row/aux_div)*aux_div + aux_div-1
+  const float *colscale;  // EPI_DACT: per-column factor applied before act' (may be null)
   // nbatch > 1: that many GEMMs, the z-th with A, B, bias and C advanced by
   // z times these strides (floats; 0 shares the operand)
   int nbatch;
@@ -75,7 +76,8 @@ struct GemmArgs {
 
 // EPI_SCALE    C = alpha*acc
 // EPI_BIAS_ACT C = act(acc + bias[col])
-// EPI_DACT     C = acc * act'(aux[r', col])  (r' = row, or the last row of its group)
+// EPI_DACT     C = (acc * colscale[col]) * act'(aux[r', col])  (r' = row, or the last row of
+//              its group; no colscale: acc * act')
 // EPI_BIAS_ADD C = alpha*acc + bias[col] + aux[row, col]  (aux may alias C)
 enum GemmEpi : int { EPI_SCALE = 0, EPI_BIAS_ACT = 1, EPI_DACT = 2, EPI_BIAS_ADD = 4 };
 

@@ -289,7 +289,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
                                  float *gW, float *gB, float *gin, int B, int in, int out_n,
                                  float scale, const float *gin_aux, int gin_deriv,
                                  hipEvent_t dz_ready = nullptr, float *ms = nullptr,
-                                 size_t ms_cap = 0) {
+                                 size_t ms_cap = 0, const float *gin_colscale = nullptr) {
   hipError_t e;
   if (!ms) {
     ms = c->scratch;
@@ -332,7 +332,7 @@ static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, cons
     d.ws = ms; d.ws_cap = ms_cap;
     KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
     if (gin_aux) {
-      d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv;
+      d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv; d.colscale = gin_colscale;
       e = launch_gemm('N', 'N', EPI_DACT, d, c->stream);
     } else {
       e = launch_gemm('N', 'N', EPI_SCALE, d, c->stream);
@@ -469,6 +469,7 @@ struct LayerRT {
   bool gout_alias = false;
   ActPlan ap{};
   float *mask = nullptr;        // Dropout per-feature mask (Q9)
+  float *dfac = nullptr;        // Dropout per-feature backward factor: mask > 0 ? scale : 0
   float scale = 1.f;
   ConvShape cs{};               // Conv2D
   PoolShape ps{};               // MaxPool2D
@@ -1197,6 +1198,11 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
       if ((rc = model_alloc(M.get(), R.d.in_size, &R.mask))) return rc;
       HIP_OK(c, hipMemcpyAsync(R.mask, mk.data(), mk.size() * sizeof(float), hipMemcpyHostToDevice,
                                c->stream));
+      std::vector<float> fac(R.d.in_size);
+      for (int k = 0; k < R.d.in_size; ++k) fac[k] = mk[k] > 0.f ? R.scale : 0.f;
+      if ((rc = model_alloc(M.get(), R.d.in_size, &R.dfac))) return rc;
+      HIP_OK(c, hipMemcpyAsync(R.dfac, fac.data(), fac.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
       HIP_OK(c, hipStreamSynchronize(c->stream));  // `mk` goes out of scope
     }
   }
@@ -1904,6 +1910,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
     }
   }
   bool is_dz = true;  // gout of the current layer already holds dz
+  bool drop_done = false;  // the Dropout below was folded into the Dense above's dX epilogue
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
     const float *in = i == 0 ? x : M->L[i - 1].out;
@@ -1920,26 +1927,42 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           HIP_OK(c, launch_dact(R.gout, R.out, dz, (int64_t)B * R.out_len, R.ap.deriv, c->stream));
         }
         float *gin = nullptr;
-        const float *aux = nullptr;
+        const float *aux = nullptr, *cfac = nullptr;
         int deriv = 0;
         bool next_dz = false;
         if (below) {
           gin = below->gout;  // Flatten's gout aliases the buffer of the layer under it
+          LayerRT *b2 = i >= 2 ? &M->L[i - 2] : nullptr;
           if (below->d.kind == GN_LAYER_DENSE && !below->ap.jac) {
             aux = below->out;  // fuse act' of the layer below into the dX epilogue
             deriv = below->ap.deriv;
             next_dz = true;
+          } else if (below->d.kind == GN_LAYER_DROPOUT && M->eff[i - 1] && b2 &&
+                     b2->d.kind == GN_LAYER_DENSE && !b2->ap.jac && b2->gout) {
+            // Dense <- Dropout (training) <- Dense: the dropout factor and the
+            // lower layer's act' in the dX epilogue, straight into its dz
+            gin = b2->gout;
+            aux = b2->out;
+            deriv = b2->ap.deriv;
+            cfac = below->dfac;
+            next_dz = true;
+            drop_done = true;
           }
         }
         // with the per-layer Adam on aux (large models), dW and db run there
         // next to dX; the layer's Adam is queued behind them.  The per-kernel
         // timing pass keeps them on one stream, so each GEMM is timed alone.
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, gB, gin, B, R.d.in_size, R.d.out_size, scale,
-                                 aux, deriv, ac && gin && !c->timing ? M->dz_ev[i] : nullptr));
+                                 aux, deriv, ac && gin && !c->timing ? M->dz_ev[i] : nullptr, nullptr,
+                                 0, cfac));
         is_dz = next_dz;
         break;
       }
       case GN_LAYER_DROPOUT: {
+        if (drop_done) {  // applied by the dX epilogue of the Dense above
+          drop_done = false;
+          break;
+        }
         // dropout.go:283-290 in training mode; out of it the gradient passes
         // unchanged (dropout.go:241-247)
         // (a Flatten first in the network has no gradient buffer: nothing below needs one)

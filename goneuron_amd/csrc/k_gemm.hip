@@ -396,6 +396,8 @@ __device__ __forceinline__ float epilogue(float v, int epi, const GemmArgs &p, i
   if (epi == EPI_BIAS_ADD)
     return v * p.alpha + (p.bias ? p.bias[col] : 0.f) + p.aux[(size_t)row * p.ldaux + col];
   const int ar = p.aux_div > 1 ? (row / p.aux_div) * p.aux_div + p.aux_div - 1 : row;
+  if (p.colscale) v = v * p.colscale[col];
+  if (p.act == D_ONE) return v * 1.0f;
   return v * apply_deriv(p.aux[(size_t)ar * p.ldaux + col], p.act);
 }
 
@@ -430,6 +432,11 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &p,
 #pragma unroll
       for (int j = 0; j < TN; ++j) bcol[j] = col_of(j) < N ? p.bias[col_of(j)] : 0.f;
     }
+  }
+  const bool cscale = EPI == EPI_DACT && p.colscale;
+  if (cscale) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bcol[j] = col_of(j) < N ? p.colscale[col_of(j)] : 0.f;
   }
   const bool use_aux = (EPI == EPI_BIAS_ADD) || (EPI == EPI_DACT && p.act != D_ONE);
   if (use_aux) {
@@ -488,7 +495,14 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &p,
     else
       store_all([&](float v, int, int j, int) { return apply_fwd_call(v + bcol[j], p.act); });
   } else if constexpr (EPI == EPI_DACT) {
-    if (p.act == D_ONE)
+    if (cscale) {  // a Dropout between two Dense layers (dropout.go:283-290): its factor first
+      if (p.act == D_ONE)
+        store_all([&](float v, int, int j, int) { return (v * bcol[j]) * 1.0f; });
+      else if (p.act == D_RELU)
+        store_all([&](float v, int i, int j, int r) { return (v * bcol[j]) * (av[i][j][r] > 0.0f ? 1.0f : 0.0f); });
+      else
+        store_all([&](float v, int i, int j, int r) { return (v * bcol[j]) * apply_deriv_call(av[i][j][r], p.act); });
+    } else if (p.act == D_ONE)
       store_all([&](float v, int, int, int) { return v * 1.0f; });
     else if (p.act == D_RELU)
       store_all([&](float v, int i, int j, int r) { return v * (av[i][j][r] > 0.0f ? 1.0f : 0.0f); });
