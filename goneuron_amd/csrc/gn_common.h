@@ -247,9 +247,12 @@ int lstm_gram_pitch(int n);
 // polls and set *err on a timeout.
 hipError_t launch_lstm_gram(const float *D, const float *hbuf, const float *x, double *gram, int B,
                             int T, int I, int H, int W, hipStream_t s, unsigned *cnt = nullptr);
+// cnt set: beside the Gram kernel (may bail, see lstm_clip_kernel); cnt null
+// and bailed set: only the chains whose bailed flag holds `epoch`
 hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
                             hipStream_t s, const unsigned *cnt = nullptr, unsigned epoch = 0,
-                            unsigned *started = nullptr, int *err = nullptr, int spin_limit = 0);
+                            unsigned *started = nullptr, int *err = nullptr, int spin_limit = 0,
+                            unsigned *bailed = nullptr, int bail_limit = 2048);
 int lstm_gram_counters(int B, int T, int W);
 hipError_t launch_lstm_clip_gate(const unsigned *started, int B, int W, unsigned epoch, int *err,
                                  int spin_limit, hipStream_t s);

@@ -487,7 +487,7 @@ struct LayerRT {
   // Gram / clip side by side: per-column tile counts, per-chain start flags,
   // launch number since the counts were zeroed and the batch they were laid
   // out for; events for the clip's stream
-  unsigned *gcnt = nullptr, *gstart = nullptr;
+  unsigned *gcnt = nullptr, *gstart = nullptr, *gbail = nullptr;
   unsigned gepoch = 0;
   int gB = 0;
   hipEvent_t lev[2] = {nullptr, nullptr};
@@ -530,6 +530,7 @@ struct LayerRT {
 struct gn_model {
   gn_ctx *ctx = nullptr;
   int lstm_spin_limit = 1 << 18;  // polls per cooperative BPTT wait (see gn_debug_lstm_spin_limit)
+  int lstm_clip_bail = 2048;      // polls of the clip's wait for a Gram kernel beside it
   std::vector<LayerRT> L;
   int loss_kind = 0;
   gn_adam_desc adam{};
@@ -808,7 +809,8 @@ static int alloc_batch(gn_model *M) {
       R.lsync = nullptr;
       R.err = nullptr;
       {
-        const size_t ncnt = (size_t)lstm_gram_counters(max_batch, (int)T, M->workers) + nchains;
+        // tile counts, then per chain a start flag and a bail flag
+        const size_t ncnt = (size_t)lstm_gram_counters(max_batch, (int)T, M->workers) + 2 * nchains;
         float *cb = nullptr, *er = nullptr;
         if ((rc = model_balloc(M, ncnt, &cb))) return rc;
         if ((rc = model_balloc(M, 64, &er))) return rc;
@@ -816,6 +818,7 @@ static int alloc_batch(gn_model *M) {
         HIP_OK(c, hipMemsetAsync(er, 0, sizeof(int), c->stream));
         R.gcnt = reinterpret_cast<unsigned *>(cb);
         R.gstart = R.gcnt + lstm_gram_counters(max_batch, (int)T, M->workers);
+        R.gbail = R.gstart + nchains;
         R.err = reinterpret_cast<int *>(er);
         R.gepoch = 0;
         R.gB = 0;
@@ -2230,7 +2233,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
             const int Wm = std::max(1, std::min(M->workers, M->maxB));
             const int cm = (M->maxB + Wm - 1) / Wm;
             const size_t ncnt = (size_t)lstm_gram_counters(M->maxB, T, M->workers) +
-                                (size_t)((M->maxB + cm - 1) / cm);
+                                2 * (size_t)((M->maxB + cm - 1) / cm);
             HIP_OK(c, hipMemsetAsync(R.gcnt, 0, ncnt * sizeof(unsigned), c->stream));
             R.gepoch = 0;
             R.gB = B;
@@ -2239,7 +2242,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           HIP_OK(c, hipEventRecord(R.lev[0], c->stream));
           HIP_OK(c, hipStreamWaitEvent(c->aux, R.lev[0], 0));
           HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->aux, R.gcnt, ep,
-                                     R.gstart, R.err, M->lstm_spin_limit));
+                                     R.gstart, R.err, M->lstm_spin_limit, R.gbail, M->lstm_clip_bail));
           HIP_OK(c, hipEventRecord(R.lev[1], c->aux));
           HIP_OK(c, launch_lstm_clip_gate(R.gstart, B, M->workers, ep, R.err, M->lstm_spin_limit,
                                           c->stream));
@@ -2248,6 +2251,10 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           int rc = lstm_gin();  // beside the clip
           if (rc) return rc;
           HIP_OK(c, hipStreamWaitEvent(c->stream, R.lev[1], 0));
+          // the chains whose clip found no Gram kernel running beside it
+          // (streams run one after the other); returns at once otherwise
+          HIP_OK(c, launch_lstm_clip(R.gram, R.coef, R.wts, B, T, M->workers, c->stream, nullptr, ep,
+                                     nullptr, nullptr, 0, R.gbail));
         } else {
           int rc = lstm_gin();
           if (rc) return rc;
@@ -2535,6 +2542,12 @@ extern "C" int gn_model_graph_count(gn_model *M, int32_t *n) {
 extern "C" int gn_debug_lstm_spin_limit(gn_model *M, int32_t polls) {
   if (!M) return GN_ERR_INVALID;
   M->lstm_spin_limit = polls;
+  return GN_OK;
+}
+
+extern "C" int gn_debug_lstm_clip_bail(gn_model *M, int32_t polls) {
+  if (!M) return GN_ERR_INVALID;
+  M->lstm_clip_bail = polls;
   return GN_OK;
 }
 

@@ -863,12 +863,19 @@ __device__ __forceinline__ double readlane_d(double x, int l) {
   return __hiloint2double(hi, lo);
 }
 
+// Beside the Gram kernel (cnt set) nothing guarantees that the two kernels
+// run at the same time (a profiler or a busy device may run them one after
+// the other), so the wait for the first Gram column is short (bail_limit
+// polls, 2048 by default): without it the chain's workgroup records bailed[ch] = epoch and
+// ends; the launch queued after the Gram kernel and after this one (cnt
+// null, bailed set) then runs the chains that bailed and no others.
 __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__restrict__ Gm,
                                                         double *__restrict__ a,
                                                         float *__restrict__ w, ChainMap cm,
                                                         int nmax, const unsigned *cnt,
                                                         unsigned epoch, unsigned *started,
-                                                        int *err, int spin_limit) {
+                                                        unsigned *bailed, int *err, int spin_limit,
+                                                        int bail_limit) {
   // tile[buf][u][r] = <D_{v0+u}, D_{v0+r}> (u <= r) of the current / next block;
   // cross[u][r] = <D_{v0+u}, D_{v1+r}>: current block rows x next block columns
   __shared__ double tile[2][CLIP_BLK][CLIP_BLK + 1];
@@ -884,8 +891,28 @@ __global__ __launch_bounds__(CLIP_NT) void lstm_clip_kernel(const double *__rest
   // run beside the Gram kernel: announce residency, then read each Gram
   // column tile only once its count says this launch's tiles are stored
   if (cnt) {
-    if (tid == 0) __hip_atomic_store(started + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (nblk > 0) gram_wait(cnt, ch, 0, nmax, epoch, err, spin_limit);
+    __shared__ int go;
+    if (tid == 0) {
+      __hip_atomic_store(started + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned *c0 = cnt + (size_t)ch * ((nmax + 63) / 64);
+      const int limit = spin_limit < bail_limit ? spin_limit : bail_limit;
+      int spins = 0, ok = 1;
+      if (nblk > 0)
+        while ((int)(__hip_atomic_load(c0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0) {
+          if (++spins > limit) {
+            ok = 0;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+      if (!ok) __hip_atomic_store(bailed + ch, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      go = ok;
+    }
+    __syncthreads();
+    if (!go) return;  // the launch after the Gram kernel does this chain
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  } else if (bailed) {
+    if (__hip_atomic_load(bailed + ch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) return;
   }
   {
     const int nb0 = min(CLIP_BLK, n);
@@ -1195,12 +1222,12 @@ hipError_t launch_lstm_clip_gate(const unsigned *started, int B, int W, unsigned
 
 hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, int T, int W,
                             hipStream_t s, const unsigned *cnt, unsigned epoch, unsigned *started,
-                            int *err, int spin_limit) {
+                            int *err, int spin_limit, unsigned *bailed, int bail_limit) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   ChainMap cm{T, (B + Wc - 1) / Wc, B};
   const int nchains = (B + cm.chunk - 1) / cm.chunk;
   const int nmax = lstm_gram_pitch(cm.chunk * T);
-  if (cnt && (!started || !err)) return hipErrorInvalidValue;
+  if (cnt && (!started || !err || !bailed)) return hipErrorInvalidValue;
   // beside the Gram kernel, unused dynamic LDS keeps its workgroups off the
   // clip's CUs (their waves would take issue slots from the serial recursion)
   const size_t pad = cnt ? (size_t)24 << 10 : 0;
@@ -1212,7 +1239,7 @@ hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, i
     attr_set = true;
   }
   hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), pad, s, gram, coef, w, cm, nmax,
-                     cnt, epoch, started, err, spin_limit);
+                     cnt, epoch, started, bailed, err, spin_limit, bail_limit);
   return hipGetLastError();
 }
 

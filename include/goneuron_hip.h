@@ -188,6 +188,13 @@ int gn_model_graph_count(gn_model *m, int32_t *n);
  * (GN_ERR_HIP at the next gn_model_read_loss / gn_model_train_step) can be
  * tested without a fault. */
 int gn_debug_lstm_spin_limit(gn_model *model, int32_t polls);
+/* Test hook (no counterpart in the reference): polls of the LSTM clip
+ * kernel's wait for the Gram kernel it runs beside (default 2048).  When the
+ * two kernels do not run at the same time (a profiler, a busy device) the
+ * clip gives up after that many polls and a launch queued after the Gram
+ * kernel clips the chain instead; 0 forces that path, whose results equal
+ * the overlapped path's bit for bit. */
+int gn_debug_lstm_clip_bail(gn_model *model, int32_t polls);
 /* Forward + backward + average only (grads valid, no Adam step). */
 int gn_model_accumulate_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
 /* Network.Step (net.go:260-284): Adam.NewStep + StepInPlace on the arena. */

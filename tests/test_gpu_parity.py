@@ -541,6 +541,31 @@ def test_lstm_coop_timeout_is_reported(gn):
     model.TrainBatch(x, y)  # raises if the error were still pending
 
 
+@pytest.mark.parametrize("shape,workers", [((16, 20, 16, 64), 1), ((16, 20, 16, 64), 4),
+                                           ((64, 100, 64, 256), 4)])
+def test_lstm_clip_fallback_matches_overlap(gn, shape, workers):
+    """The clip kernel beside the Gram kernel gives up when no Gram kernel
+    runs beside it (streams run one after the other, as under a profiler; here
+    forced with a zero poll limit) and the launch queued after the Gram kernel
+    clips those chains: loss, gradients and parameters equal the overlapped
+    path's bit for bit over two steps."""
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib
+    B, T, inp, hidden = shape
+    cfg = configs.lstm(B=B, T=T, inp=inp, hidden=hidden)
+    x, y = configs.inputs(cfg)
+    a = configs.build(cfg, workers=workers)
+    b = configs.build(cfg, workers=workers)
+    assert lib().gn_debug_lstm_clip_bail(b.h, 0) == 0
+    for _ in range(2):
+        la, lb = a.TrainBatch(x, y), b.TrainBatch(x, y)
+        assert la == lb
+        np.testing.assert_array_equal(a.Gradients(), b.Gradients())
+        np.testing.assert_array_equal(a.Params(), b.Params())
+    a.Close()
+    b.Close()
+
+
 @pytest.mark.parametrize("workers", [1, 2])
 def test_gpt_small_random_block(gn, oracle, workers):
     from goneuron_amd import configs
