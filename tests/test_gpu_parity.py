@@ -153,6 +153,23 @@ def test_sigmoid_tanh_dense_epilogues(gn, oracle):
     _compare_step(gn, oracle, cfg, steps=1)
 
 
+@pytest.mark.parametrize("acts,workers,B", [(("sigmoid", "tanh"), 1, 37), (("tanh", "sigmoid"), 3, 300),
+                                            (("relu", "relu"), 4, 2048)])
+def test_dropout_between_dense_layers(gn, oracle, acts, workers, B):
+    """Dense <- Dropout (training) <- Dense: the dropout factor and the lower
+    layer's act' are applied in the upper layer's dX epilogue (no dropout
+    backward, no act' pass); sigmoid / tanh below take the out-of-line
+    derivative, 2048 x 640 runs unsplit GEMMs, 37 and 300 rows split ones;
+    odd widths (a dropped feature set that is not a multiple of 4)."""
+    from goneuron_amd.configs import dense
+    a1, a2 = acts
+    cfg = dict(num=7, name="drop", B=B, loss="mse", lr=1e-3, x="normal", in_len=45,
+               classes=None, targets="normal",
+               layers=[dense(45, 83, a1), dense(83, 640, a2), {"kind": "dropout", "p": 0.3, "n": 640},
+                       dense(640, 1, "linear")])
+    _compare_step(gn, oracle, cfg, steps=2, workers=workers)
+
+
 def test_odd_batch_and_sizes(gn, oracle):
     from goneuron_amd import configs
     cfg = configs.wide(width=72, classes=13, depth=2, B=19)
