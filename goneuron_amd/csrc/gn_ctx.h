@@ -19,7 +19,6 @@ struct gn_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   hipStream_t aux = nullptr;   // dW and bias sums next to the dX GEMMs (large models), LSTM clip
-  hipStream_t aux2 = nullptr;  // per-layer Adam updates, overlapped with the backward pass
   std::string err;
   int fail_next = 0;
   hipDeviceProp_t props{};

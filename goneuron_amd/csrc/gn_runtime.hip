@@ -106,29 +106,22 @@ extern "C" int gn_init(int device_ordinal, gn_ctx **out) {
     }
     c->noalloc = noalloc_ptr[device_ordinal];
   }
-  // all streams at the default priority
+  // both streams at the default priority
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return GN_ERR_HIP;
   if (hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking) != hipSuccess) {
     (void)hipStreamDestroy(c->stream);
-    return GN_ERR_HIP;
-  }
-  if (hipStreamCreateWithFlags(&c->aux2, hipStreamNonBlocking) != hipSuccess) {
-    (void)hipStreamDestroy(c->stream);
-    (void)hipStreamDestroy(c->aux);
     return GN_ERR_HIP;
   }
   c->scratch_floats = (size_t)16 << 20;  // 64 MiB: colsum partials, split-K partials
   if (hipMalloc(&c->scratch, c->scratch_floats * sizeof(float)) != hipSuccess) {
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->aux);
-    (void)hipStreamDestroy(c->aux2);
     return GN_ERR_OOM;
   }
   if (hipMalloc(&c->scratch_aux, c->scratch_floats * sizeof(float)) != hipSuccess) {
     (void)hipFree(c->scratch);
     (void)hipStreamDestroy(c->stream);
     (void)hipStreamDestroy(c->aux);
-    (void)hipStreamDestroy(c->aux2);
     return GN_ERR_OOM;
   }
   *out = c.release();
@@ -140,13 +133,11 @@ extern "C" void gn_shutdown(gn_ctx *c) {
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   (void)hipStreamSynchronize(c->aux);
-  (void)hipStreamSynchronize(c->aux2);
   for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
   (void)hipFree(c->scratch);
   (void)hipFree(c->scratch_aux);
   (void)hipStreamDestroy(c->stream);
   (void)hipStreamDestroy(c->aux);
-  (void)hipStreamDestroy(c->aux2);
   delete c;
 }
 
@@ -168,7 +159,6 @@ extern "C" int gn_sync(gn_ctx *c) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
-  HIP_OK(c, hipStreamSynchronize(c->aux2));
   return GN_OK;
 }
 
@@ -182,7 +172,6 @@ extern "C" int gn_timing_enable(gn_ctx *c, int enable) {
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
-  HIP_OK(c, hipStreamSynchronize(c->aux2));
   c->timing = enable != 0;
   c->recs.clear();
   c->pool_used = 0;
@@ -193,7 +182,6 @@ extern "C" int gn_timing_report(gn_ctx *c, int cls, int64_t *launches, double *t
   ENTRY(c);
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
-  HIP_OK(c, hipStreamSynchronize(c->aux2));
   int64_t n = 0;
   double ms = 0;
   for (const auto &r : c->recs) {
@@ -215,7 +203,6 @@ extern "C" int gn_timing_kernels(gn_ctx *c, gn_kernel_stat *out, int32_t cap, in
   if (!n || (cap > 0 && !out)) return set_err(c, GN_ERR_INVALID, "bad timing_kernels args");
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
-  HIP_OK(c, hipStreamSynchronize(c->aux2));
   std::vector<gn_kernel_stat> acc;
   for (const auto &r : c->recs) {
     float t = 0;
@@ -571,6 +558,10 @@ struct gn_model {
   std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
   std::vector<hipEvent_t> dz_ev;    // one per layer: its dz is ready (no timing)
   std::vector<hipEvent_t> dw_ev;    // one per layer: its dW and bias sums on ctx->aux are done
+  // the per-layer Adam updates run on a stream of the model's own, created by
+  // its first overlapped train step and destroyed with the model, so a
+  // context that later trains other models keeps two streams in use
+  hipStream_t adam_s = nullptr;
   // HIP graphs of the accumulate pass (forward, loss, backward) of small
   // models, keyed by the input pointers, the batch and the training flags in
   // effect: the first step with a key runs eagerly, the second is captured,
@@ -643,6 +634,10 @@ extern "C" void gn_model_destroy(gn_model *M) {
       if (e) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->sync_ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : M->dw_ev) (void)hipEventDestroy(e);
+  if (M->adam_s) {
+    (void)hipStreamSynchronize(M->adam_s);
+    (void)hipStreamDestroy(M->adam_s);
+  }
   for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
   for (void *p : M->bowned) (void)hipFree(p);
   for (void *p : M->owned) (void)hipFree(p);
@@ -1246,7 +1241,6 @@ extern "C" int gn_model_reserve(gn_model *M, int32_t max_batch) {
   if (max_batch <= M->maxB) return GN_OK;
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipStreamSynchronize(c->aux));
-  HIP_OK(c, hipStreamSynchronize(c->aux2));
   const int old = M->maxB;
   drop_graphs(M);  // they hold the old batch buffers
   free_batch(M);
@@ -1935,6 +1929,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       M->dw_ev.push_back(e);
     }
   }
+  if (ac && !M->adam_s)  // default priority, like the context's streams
+    HIP_OK(c, hipStreamCreateWithFlags(&M->adam_s, hipStreamNonBlocking));
   std::vector<char> dw_aux(n, 0);  // layer i's dW went to ctx->aux
   bool is_dz = true;  // gout of the current layer already holds dz
   bool drop_done = false;  // the Dropout below was folded into the Dense above's dX epilogue
@@ -1982,7 +1978,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const bool side = ac && gin && !c->timing;
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, gB, gin, B, R.d.in_size, R.d.out_size, scale,
                                  aux, deriv, side ? M->dz_ev[i] : nullptr, nullptr, 0, cfac));
-        if (side) {  // the layer's Adam (ctx->aux2) waits for its dW and bias sums
+        if (side) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
           dw_aux[i] = 1;
         }
@@ -2328,22 +2324,22 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       // Adam on its own stream: after the layer's dX (main stream) and dW
       // (ctx->aux), so the next layers' dW GEMMs do not queue behind it
       HIP_OK(c, hipEventRecord(M->sync_ev[i], c->stream));
-      HIP_OK(c, hipStreamWaitEvent(c->aux2, M->sync_ev[i], 0));
-      if (dw_aux[i]) HIP_OK(c, hipStreamWaitEvent(c->aux2, M->dw_ev[i], 0));
+      HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->sync_ev[i], 0));
+      if (dw_aux[i]) HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->dw_ev[i], 0));
       // While backward kernels still run, a 256-block grid (one block per CU
       // next to the GEMM's waves) keeps the update off their critical path;
       // the update of the first parameterised layer runs alone, at full width.
       bool last = true;
       for (int j = 0; j < i; ++j)
         if (M->L[j].pcount > 0) last = false;
-      KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, c->aux2);
+      KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, M->adam_s);
       HIP_OK(c, launch_adam(M->params + R.poff, M->grads + R.poff, M->m + R.poff, M->v + R.poff,
                             R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps,
-                            c->aux2, last ? 16384 : 256));
+                            M->adam_s, last ? 16384 : 256));
     }
   }
   if (ac) {  // every dW on ctx->aux precedes an update the step now waits for
-    HIP_OK(c, hipEventRecord(M->sync_ev[n], c->aux2));
+    HIP_OK(c, hipEventRecord(M->sync_ev[n], M->adam_s));
     HIP_OK(c, hipStreamWaitEvent(c->stream, M->sync_ev[n], 0));
   }
   return GN_OK;
