@@ -72,6 +72,13 @@ struct GemmArgs {
   // times these (attention's (sample, head) pairs inside [B*T, D] matrices)
   int nbatch_in;
   int64_t istride_A, istride_B, istride_C;
+  // EPI_BIAS_ACT with a Dropout above (training): also drop_out[row, col] =
+  // drop_mask[col] > 0 ? C[row, col] * drop_scale : 0 (the dropout kernel's
+  // expression), at pitch ldc; in the split-K reduction when K splits, else by
+  // a dropout launch after the GEMM.  nbatch <= 1.
+  float *drop_out;
+  const float *drop_mask;
+  float drop_scale;
 };
 
 // EPI_SCALE    C = alpha*acc
@@ -278,6 +285,17 @@ hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipSt
 // nmem token sums in one launch: member m reads X + m*xstride, writes S + m*sstride
 hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N, int nmem,
                                   int64_t xstride, int64_t sstride, hipStream_t s);
+// Up to three Linear layers' Q10 gradients from per-sample token sums:
+// dW[o][i] = scale * sum_b S[b][o] X[b][i], db[o] = scale * sum_b S[b][o]
+// (S pitch lds, X rows pitch ldx, dW M x N dense), b ascending.
+struct TokDwSet {
+  const float *S[3];
+  const float *X[3];
+  float *dW[3];
+  float *db[3];
+};
+hipError_t launch_tok_dw(const TokDwSet &set, int nmem, int B, int M, int N, int lds, int ldx,
+                         float scale, hipStream_t s);
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
                          int rows, int N, float eps, hipStream_t s);
 hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam, const float *stats,

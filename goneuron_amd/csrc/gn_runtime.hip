@@ -265,8 +265,11 @@ extern "C" int gn_memset_zero(gn_ctx *c, void *dst, size_t bytes) {
 // ---------------------------------------------------------------------------
 // Per-layer operators
 // ---------------------------------------------------------------------------
+// drop: a Dropout above the layer in training mode, whose output the GEMM
+// writes too (its split-K reduction, or a dropout launch right after it)
 static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const float *b, float *out,
-                            int B, int in, int out_n, int fwd) {
+                            int B, int in, int out_n, int fwd, float *drop_out = nullptr,
+                            const float *drop_mask = nullptr, float drop_scale = 0.f) {
   GemmArgs a{};
   a.M = B; a.N = out_n; a.K = in;
   a.A = x; a.lda = in;
@@ -274,6 +277,9 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
   a.C = out; a.ldc = out_n;
   a.bias = b; a.act = fwd; a.alpha = 1.f;
   a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  a.drop_out = drop_out;
+  a.drop_mask = drop_mask;
+  a.drop_scale = drop_scale;
   KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
   return launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream);
 }
@@ -1417,16 +1423,17 @@ static hipError_t gemm_nn(gn_ctx *c, const float *A, const float *Wm, float *C, 
 // Q10 weight gradient of a per-token Dense: dW[M,N] = scale * S^T Xlast, with
 // S [B, M] the per-sample token sums of dz and Xlast the last token's input
 // row of every sample (row stride T*N).
-static hipError_t gemm_dw_last(gn_ctx *c, const float *S, const float *X, float *dW, int B, int T,
-                               int M, int N, float scale) {
-  GemmArgs a{};
-  a.M = M; a.N = N; a.K = B;
-  a.A = S; a.lda = M;
-  a.B = X + (int64_t)(T - 1) * N; a.ldb = T * N;
-  a.C = dW; a.ldc = N; a.alpha = scale;
-  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
-  KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
-  return launch_gemm('T', 'N', EPI_SCALE, a, c->stream);
+// Q10 gradients of one Linear in the block: dW = scale * S^T x_last and
+// db = scale * colsum(S) from its per-sample token sums S [B][M], one launch
+static hipError_t tb_tok_dw(gn_ctx *c, const float *S, const float *X, float *dW, float *db, int B,
+                            int T, int M, int N, float scale) {
+  TokDwSet set{};
+  set.S[0] = S;
+  set.X[0] = X + (int64_t)(T - 1) * N;
+  set.dW[0] = dW;
+  set.db[0] = db;
+  KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", f4((double)B * M + (double)B * N + (double)M * N + M));
+  return launch_tok_dw(set, 1, B, M, N, M, T * N, scale, c->stream);
 }
 
 // Block norm k (0: norm1, 1: norm2) forward: LayerNorm (stats = mean, std)
@@ -1547,11 +1554,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
   }
-  {
-    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
-    HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.b2, cs, cap, c->stream));
-  }
-  HIP_OK(c, gemm_dw_last(c, t.S, t.MID, G + o.w2, B, T, D, FF, scale));
+  HIP_OK(c, tb_tok_dw(c, t.S, t.MID, G + o.w2, G + o.b2, B, T, D, FF, scale));
   if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
     // ff1 = SwiGLU called per token: its one saved entry (the last token's
     // input, gate and up) serves the first Backward (token 0); the later ones
@@ -1604,11 +1607,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
       KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF));
       HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
     }
-    {
-      KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * FF + FF));
-      HIP_OK(c, launch_colsum(t.S, B, FF, FF, scale, G + o.b1, cs, cap, c->stream));
-    }
-    HIP_OK(c, gemm_dw_last(c, t.S, t.N1, G + o.w1, B, T, FF, D, scale));
+    HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale));
     // combined = dRES2 + dz1 W1
     HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
   }
@@ -1619,11 +1618,7 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
   }
-  {
-    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
-    HIP_OK(c, launch_colsum(t.S, B, D, D, scale, G + o.bo, cs, cap, c->stream));
-  }
-  HIP_OK(c, gemm_dw_last(c, t.S, t.O, G + o.wo, B, T, D, D, scale));
+  HIP_OK(c, tb_tok_dw(c, t.S, t.O, G + o.wo, G + o.bo, B, T, D, D, scale));
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, R.NH, D / R.NH, R.causal, true));
@@ -1648,25 +1643,18 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, c->stream));
   }
   {
-    const float *src[3] = {t.S3, t.S3 + sst, t.S3 + 2 * sst};
-    float *dst[3] = {G + bo[0], G + bo[1], G + bo[2]};
-    KTimer kt(c, GN_KCLASS_OTHER, "colsum", 3 * f4((double)B * D + D));
-    HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
-  }
-  {
-    // dWq, dWk, dWv (Q10: token sums times the last token's input) in one
-    // launch: A strided over the token sums, B shared, C over the weights
-    GemmArgs a{};
-    a.M = D; a.N = D; a.K = B;
-    a.A = t.S3; a.lda = D;
-    a.B = X + (int64_t)(T - 1) * D; a.ldb = T * D;
-    a.C = G + o.wq; a.ldc = D; a.alpha = scale;
-    a.ws = cs; a.ws_cap = cap;
-    a.nbatch = 3;
-    a.bstride_A = sst;
-    a.bstride_C = o.wk - o.wq;
-    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
-    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+    // dWq, dWk, dWv and their biases (Q10: token sums times the last token's
+    // input, token sums summed over the batch) in one launch
+    TokDwSet set{};
+    const int64_t wo3[3] = {o.wq, o.wk, o.wv};
+    for (int z = 0; z < 3; ++z) {
+      set.S[z] = t.S3 + z * sst;
+      set.X[z] = X + (int64_t)(T - 1) * D;
+      set.dW[z] = G + wo3[z];
+      set.db[z] = G + bo[z];
+    }
+    KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", 3 * f4((double)B * D + (double)B * D + (double)D * D + D));
+    HIP_OK(c, launch_tok_dw(set, 3, B, D, D, D, T * D, scale, c->stream));
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
     const int64_t pst = (int64_t)rows * D;
@@ -1703,6 +1691,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
   if (!for_loss || M->workers <= 1) M->master_dims = true;
   const float *cur = x;
   bool pe_done = false;  // the PositionalEncoding output was written with the embedding rows
+  bool drop_done = false;  // the Dropout's output was written by the Dense GEMM below it
   const int n = (int)M->L.size();
   for (int i = 0; i < n; ++i) {
     LayerRT &R = M->L[i];
@@ -1713,13 +1702,23 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         const bool last = (i == n - 1);
         int fwd = R.ap.fwd;
         if (R.ap.jac || (last && for_loss)) fwd = F_IDENTITY;  // row kernel finishes it
-        HIP_OK(c, dense_fwd(c, cur, W, b, R.out, B, R.d.in_size, R.d.out_size, fwd));
+        // a Dropout above in training mode: its output from the GEMM's split-K
+        // reduction (dropout.go:85-130 per element, the same expression)
+        LayerRT *dr = !last && M->L[i + 1].d.kind == GN_LAYER_DROPOUT && M->eff[i + 1] &&
+                              M->L[i + 1].out_len == R.out_len
+                          ? &M->L[i + 1]
+                          : nullptr;
+        HIP_OK(c, dense_fwd(c, cur, W, b, R.out, B, R.d.in_size, R.d.out_size, fwd,
+                            dr ? dr->out : nullptr, dr ? dr->mask : nullptr, dr ? dr->scale : 0.f));
+        drop_done = dr != nullptr;
         if (last && !for_loss && R.ap.jac)
           HIP_OK(c, launch_row_act(R.out, B, R.out_len, R.ap.row_act, c->stream));
         break;
       }
       case GN_LAYER_DROPOUT:
-        if (M->eff[i]) {
+        if (drop_done) {
+          drop_done = false;
+        } else if (M->eff[i]) {
           KTimer kt(c, GN_KCLASS_OTHER, "dropout", f4(2.0 * B * R.out_len + R.out_len));
           HIP_OK(c, launch_dropout(cur, R.mask, R.scale, R.out, B, R.out_len, c->stream));
         } else

@@ -219,7 +219,16 @@ __global__ __launch_bounds__(1024) void token_sum_kernel(const float *__restrict
   float s = 0.f;
   if (c < N) {
     const float *p = X + b * T * N + c;
-    for (int t = grp; t < T; t += 16) s += p[(int64_t)t * N];
+    // eight tokens' loads in flight, added in token order
+    int t = grp;
+    for (; t + 7 * 16 < T; t += 8 * 16) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(t + 16 * u) * N];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; t < T; t += 16) s += p[(int64_t)t * N];
   }
   red[grp][lane] = s;
   __syncthreads();
@@ -229,6 +238,69 @@ __global__ __launch_bounds__(1024) void token_sum_kernel(const float *__restrict
     for (int g = 0; g < 16; ++g) v += red[g][lane];
     S[b * N + c] = v;
   }
+}
+
+// Q10 weight and bias gradients of a Linear in the block from the per-sample
+// token sums S [B][M] (pitch lds) and the last token's input rows X [B]
+// (pitch ldx): dW[o][i] = scale * sum_b S[b][o] X[b][i] and db[o] = scale *
+// sum_b S[b][o], b ascending (the K = B product and the column sum of one
+// launch).  Block = 16 rows o x 64 columns i; per chunk of 64 samples every
+// thread issues its S and X loads at once (one memory round trip), stages
+// them in LDS, then thread (g, i) accumulates rows 4g..4g+3.  blockIdx.z
+// selects the member.
+constexpr int TD_O = 16, TD_I = 64, TD_CB = 64;
+__global__ __launch_bounds__(256) void tok_dw_kernel(TokDwSet set, int B, int M, int N, int lds,
+                                                     int ldx, float scale) {
+  __shared__ float ss[TD_CB][TD_O];
+  __shared__ float xs[TD_CB][TD_I];
+  const float *__restrict__ S = set.S[blockIdx.z];
+  const float *__restrict__ X = set.X[blockIdx.z];
+  float *__restrict__ dW = set.dW[blockIdx.z];
+  float *__restrict__ db = set.db[blockIdx.z];
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int i0 = blockIdx.x * TD_I, o0 = blockIdx.y * TD_O;
+  const bool bias = blockIdx.x == 0 && tid < TD_O;
+  constexpr int NS = TD_CB * TD_O / 256, NX = TD_CB * TD_I / 256;  // 4 and 16 loads per thread
+  float acc[4] = {0.f, 0.f, 0.f, 0.f}, bs = 0.f;
+  for (int b0 = 0; b0 < B; b0 += TD_CB) {
+    const int nb = min(TD_CB, B - b0);
+    float sv[NS], xv[NX];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const int e = tid + 256 * q, bb = e / TD_O, oo = e % TD_O;
+      sv[q] = bb < nb && o0 + oo < M ? S[(size_t)(b0 + bb) * lds + o0 + oo] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < NX; ++q) {
+      const int bb = (tid >> 6) + 4 * q;
+      xv[q] = bb < nb && i0 + lane < N ? X[(size_t)(b0 + bb) * ldx + i0 + lane] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const int e = tid + 256 * q;
+      ss[e / TD_O][e % TD_O] = sv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < NX; ++q) xs[(tid >> 6) + 4 * q][lane] = xv[q];
+    __syncthreads();
+    for (int bb = 0; bb < nb; ++bb) {
+      const float x = xs[bb][lane];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] += ss[bb][4 * g + k] * x;
+    }
+    if (bias)
+      for (int bb = 0; bb < nb; ++bb) bs += ss[bb][tid];
+    __syncthreads();
+  }
+  const int i = i0 + lane;
+  if (i < N) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int o = o0 + 4 * g + k;
+      if (o < M) dW[(size_t)o * N + i] = acc[k] * scale;
+    }
+  }
+  if (bias && o0 + tid < M) db[o0 + tid] = bs * scale;
 }
 
 // ---------------------------------------------------------------------------
@@ -773,6 +845,15 @@ hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N,
   if (B <= 0 || nmem <= 0) return hipSuccess;
   hipLaunchKernelGGL(token_sum_kernel, dim3((N + 63) / 64, B, nmem), dim3(1024), 0, s, X, S, B, T, N,
                      xstride, sstride);
+  return hipGetLastError();
+}
+
+hipError_t launch_tok_dw(const TokDwSet &set, int nmem, int B, int M, int N, int lds, int ldx,
+                         float scale, hipStream_t s) {
+  if (nmem < 1 || nmem > 3) return hipErrorInvalidValue;
+  if (M <= 0 || N <= 0) return hipSuccess;
+  hipLaunchKernelGGL(tok_dw_kernel, dim3((N + TD_I - 1) / TD_I, (M + TD_O - 1) / TD_O, nmem), dim3(256), 0,
+                     s, set, B, M, N, lds, ldx, scale);
   return hipGetLastError();
 }
 

@@ -849,7 +849,9 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits,
     float v = p.ws[idx];
     for (int s = 1; s < splits; ++s) v += p.ws[s * MN + idx];
     const int row = (int)(idx / p.N), col = (int)(idx % p.N);
-    p.C[(size_t)row * p.ldc + col] = epilogue(v, epi, p, row, col);
+    const float y = epilogue(v, epi, p, row, col);
+    p.C[(size_t)row * p.ldc + col] = y;
+    if (p.drop_out) p.drop_out[(size_t)row * p.ldc + col] = p.drop_mask[col] > 0.f ? y * p.drop_scale : 0.0f;
   }
 }
 
@@ -866,7 +868,9 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int sp
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   if (lane == 0) {
     const int row = (int)(idx / p.N), col = (int)(idx % p.N);
-    p.C[(size_t)row * p.ldc + col] = epilogue(v, epi, p, row, col);
+    const float y = epilogue(v, epi, p, row, col);
+    p.C[(size_t)row * p.ldc + col] = y;
+    if (p.drop_out) p.drop_out[(size_t)row * p.ldc + col] = p.drop_mask[col] > 0.f ? y * p.drop_scale : 0.0f;
   }
 }
 
@@ -930,6 +934,7 @@ static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.drop_out && (epi != EPI_BIAS_ACT || a.nbatch > 1 || !a.drop_mask)) return hipErrorInvalidValue;
   // float4 staging needs 16 B aligned rows and the contiguous extent % 4 == 0
   const bool ak = (ta == 'N'), bk = (tb == 'T');
   bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0);
@@ -977,7 +982,12 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   }
   hipError_t e = big ? launch_r<128>(ta, tb, epi, vec, a, splits, kchunk, s)
                      : launch_r<64>(ta, tb, epi, vec, a, splits, kchunk, s);
-  if (e != hipSuccess || splits <= 1) return e;
+  if (e != hipSuccess) return e;
+  if (splits <= 1) {
+    if (!a.drop_out) return e;
+    if (a.ldc != a.N) return hipErrorInvalidValue;
+    return launch_dropout(a.C, a.drop_mask, a.drop_scale, a.drop_out, a.M, a.N, s);
+  }
   const size_t MN = (size_t)a.M * a.N;
   if (splits >= 16 && MN <= 65536) {
     const unsigned blocks = (unsigned)((MN + NT / 64 - 1) / (NT / 64));
