@@ -942,9 +942,10 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
   vec = vec && a.K > 0;  // the pipelined loop assumes at least one K stage
   // 128-wide tiles when they fill the 256 CUs, else 64-wide tiles; when even
-  // those cannot fill the chip, split K (down to one K stage per split: a lone
-  // tile runs at 1/256 of the chip).  Partials go to the workspace and are
-  // summed in split order.
+  // those cannot fill the chip and K has at least 8 stages, split K (down to
+  // one K stage per split: a lone tile runs at 1/256 of the chip).  Partials
+  // go to the workspace and are summed in split order.  Below 8 stages a tile
+  // is short and the reduce launch would cost more than the split saves.
   // two-level batches (many small members) count the tiles of all members
   const int64_t nmem = (a.nbatch > 1 && a.nbatch_in > 1) ? a.nbatch : 1;
   const int64_t t128 = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128) * nmem;
@@ -952,7 +953,7 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   const bool big = t128 >= 160;
   const int tiles = (int)std::min<int64_t>(big ? t128 : t64, 1 << 30);
   int splits = 1;
-  if (tiles < 160 && a.K >= 2 * BK && a.ws) {
+  if (tiles < 160 && a.K >= 8 * BK && a.ws) {
     splits = std::min((256 + tiles - 1) / tiles, a.K / BK);
     while (splits > 1 && (size_t)splits * a.M * a.N > a.ws_cap) --splits;
   }
