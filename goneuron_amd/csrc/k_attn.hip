@@ -164,10 +164,18 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
       if (id >= z0 && id < z1) hit[id - z0] = 1;  // every writer stores 1
     }
     __syncthreads();
-    const int64_t n = (int64_t)(z1 - z0) * D;
-    for (int64_t e = threadIdx.x; e < n; e += 256) {
-      const int r = (int)(e / D);
-      if (!hit[r]) gradE[(int64_t)z0 * D + e] = 0.0f;
+    float *base = gradE + (int64_t)z0 * D;
+    if ((D & 3) == 0 && (reinterpret_cast<uintptr_t>(base) & 15) == 0) {
+      // 16-byte stores, row and column from one 32-bit division per store
+      const int D4 = D >> 2, n4 = (z1 - z0) * D4;
+      for (int e = threadIdx.x; e < n4; e += 256) {
+        const int r = e / D4;
+        if (!hit[r]) reinterpret_cast<float4 *>(base)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    } else {
+      const int n = (z1 - z0) * D;
+      for (int e = threadIdx.x; e < n; e += 256)
+        if (!hit[e / D]) base[e] = 0.0f;
     }
     return;
   }

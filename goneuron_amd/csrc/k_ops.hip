@@ -596,7 +596,9 @@ __global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo
       if (t + k * G < C) {
         float pv = o[k];
         if (pv < 1e-10f) pv = 1e-10f;
-        l -= yv[k] * or_log(pv);
+        // a zero target adds 0 * log(pv) = +-0 to a sum that is never -0: the
+        // float64 log is needed only for the others (and a NaN output)
+        if (yv[k] != 0.f || pv != pv) l -= yv[k] * or_log(pv);
       }
       d[k] = o[k] - yv[k];
     }
