@@ -590,6 +590,15 @@ def test_gpt_small_random_block(gn, oracle, workers):
     _compare_step(gn, oracle, cfg, steps=2, workers=workers, perturb=_random_block(cfg))
 
 
+def test_gpt_batch_over_64_samples(gn, oracle):
+    """More than 64 samples: the Q10 weight and bias gradients of each Linear
+    sum the token sums in chunks of 64 samples (here 64 + 6), and the block's
+    widths (36 and 40) are not multiples of the 16 x 64 output blocks."""
+    from goneuron_amd import configs
+    cfg = configs.gpt(B=70, T=5, vocab=23, dim=36, heads=2, ff=40)
+    _compare_step(gn, oracle, cfg, steps=2, workers=1, perturb=_random_block(cfg))
+
+
 @pytest.mark.parametrize("T,dim,heads,causal", [(13, 30, 2, False), (33, 64, 2, True), (97, 16, 1, False),
                                                  (144, 64, 2, True), (24, 96, 2, False), (130, 40, 1, True)])
 def test_gpt_attention_shapes(gn, oracle, T, dim, heads, causal):
