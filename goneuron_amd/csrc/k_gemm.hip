@@ -950,7 +950,9 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   const int64_t nmem = (a.nbatch > 1 && a.nbatch_in > 1) ? a.nbatch : 1;
   const int64_t t128 = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128) * nmem;
   const int64_t t64 = ((a.M + 63) / 64) * (int64_t)((a.N + 63) / 64) * nmem;
-  const bool big = t128 >= 160;
+  // short K (at most four 64-deep stages) with four 64-wide tiles per CU:
+  // 64-wide tiles, whose blocks cover each other's prologue and epilogue
+  const bool big = t128 >= 160 && !(a.K <= 256 && t64 >= 1024);
   const int tiles = (int)std::min<int64_t>(big ? t128 : t64, 1 << 30);
   int splits = 1;
   if (tiles < 160 && a.K >= 8 * BK && a.ws) {
