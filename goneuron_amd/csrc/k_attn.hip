@@ -462,6 +462,14 @@ __global__ __launch_bounds__(256) void ln_param_final(const float *__restrict__ 
   float s = 0.f;
   if (c < 2 * N) {
     int b = w;
+    // sixteen partials in flight, added in the same order as below
+    for (; b + 60 < nblk; b += 64) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = part[(size_t)(b + 4 * u) * 2 * N + c];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += v[u];
+    }
     for (; b + 12 < nblk; b += 16) {
       const float v0 = part[(size_t)b * 2 * N + c], v1 = part[(size_t)(b + 4) * 2 * N + c];
       const float v2 = part[(size_t)(b + 8) * 2 * N + c], v3 = part[(size_t)(b + 12) * 2 * N + c];

@@ -847,7 +847,14 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits,
   const size_t MN = (size_t)p.M * p.N;
   for (size_t idx = (size_t)blockIdx.x * NT + threadIdx.x; idx < MN; idx += (size_t)gridDim.x * NT) {
     float v = p.ws[idx];
-    for (int s = 1; s < splits; ++s) v += p.ws[s * MN + idx];
+    for (int s = 1; s < splits; s += 8) {  // eight loads in flight, added in split order
+      float u8[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) u8[u] = s + u < splits ? p.ws[(s + u) * MN + idx] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s + u < splits) v += u8[u];
+    }
     const int row = (int)(idx / p.N), col = (int)(idx % p.N);
     const float y = epilogue(v, epi, p, row, col);
     p.C[(size_t)row * p.ldc + col] = y;

@@ -141,7 +141,14 @@ __global__ __launch_bounds__(TPB) void colsum_final(ColsumSet set, const float *
   float *__restrict__ out = set.out[blockIdx.z];
   part += (size_t)blockIdx.z * chunks * cols + col;
   float s = 0.f;
-  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols];
+  for (int c = 0; c < chunks; c += 8) {  // eight loads in flight, added in chunk order
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = c + u < chunks ? part[(size_t)(c + u) * cols] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (c + u < chunks) s += v[u];
+  }
   out[col] = s * scale;
 }
 
