@@ -329,7 +329,14 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_reduce(const float *__restric
   const int o = blockIdx.x * (CT / 64) + (threadIdx.x >> 6);
   if (o >= nslots) return;
   float s = 0.f;
-  for (int i = lane; i < nblocks; i += 64) s += part[(int64_t)i * nslots + o];
+  for (int i = lane; i < nblocks; i += 8 * 64) {  // eight loads in flight, added in block order
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = i + 64 * u < nblocks ? part[(int64_t)(i + 64 * u) * nslots + o] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i + 64 * u < nblocks) s += v[u];
+  }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
   if (lane == 0) grad[o] = s * scale;  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)

@@ -1048,10 +1048,26 @@ __global__ __launch_bounds__(256) void lstm_weight_kernel(float *__restrict__ D,
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int b = (int)(e / G4), k = (int)(e % G4);
     float s = 0.f;
-    for (int t = T - 1; t >= 0; --t) {
-      float *p = D + ((size_t)b * (T + 1) + t) * G4 + k;
-      const float d = *p * w[(size_t)b * (T + 1) + t];
-      *p = d;
+    float *col = D + (size_t)b * (T + 1) * G4 + k;
+    const float *wb = w + (size_t)b * (T + 1);
+    int t = T - 1;
+    for (; t >= 7; t -= 8) {  // eight steps' loads in flight, then the same order as below
+      float dv[8], wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        dv[u] = col[(size_t)(t - u) * G4];
+        wv[u] = wb[t - u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float d = dv[u] * wv[u];
+        col[(size_t)(t - u) * G4] = d;
+        s += d;
+      }
+    }
+    for (; t >= 0; --t) {
+      const float d = col[(size_t)t * G4] * wb[t];
+      col[(size_t)t * G4] = d;
       s += d;
     }
     S[(size_t)b * G4 + k] = s;
