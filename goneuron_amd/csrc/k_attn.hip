@@ -323,6 +323,43 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (r >= rows) return;
   const float *xr = x + (int64_t)r * N;
+  constexpr int LF_C = 8;  // up to 512 columns held in registers
+  if (N <= 64 * LF_C) {
+    // the row in registers, read once (its loads in flight together); the
+    // same sums in the same order as the loops below
+    float v[LF_C], gv[LF_C], bv[LF_C];
+#pragma unroll
+    for (int c = 0; c < LF_C; ++c) {
+      const int i = lane + 64 * c;
+      v[c] = i < N ? xr[i] : 0.f;
+      gv[c] = i < N ? gam[i] : 0.f;
+      bv[c] = i < N ? bet[i] : 0.f;
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < LF_C; ++c)
+      if (lane + 64 * c < N) s += v[c];
+    const float mean = wsum(s) / (float)N;
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < LF_C; ++c)
+      if (lane + 64 * c < N) {
+        const float d = v[c] - mean;
+        ss += d * d;
+      }
+    const float var = wsum(ss) / (float)N;
+    const float std = (float)sqrt((double)(var + eps));
+#pragma unroll
+    for (int c = 0; c < LF_C; ++c) {
+      const int i = lane + 64 * c;
+      if (i < N) y[(int64_t)r * N + i] = gv[c] * ((v[c] - mean) / std) + bv[c];
+    }
+    if (lane == 0) {
+      stats[2 * r] = mean;
+      stats[2 * r + 1] = std;
+    }
+    return;
+  }
   float s = 0.f;
   for (int i = lane; i < N; i += 64) s += xr[i];
   const float mean = wsum(s) / (float)N;
