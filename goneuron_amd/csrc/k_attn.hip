@@ -186,10 +186,29 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
     if (sid[e] == my) first = 0;  // benign race: every writer stores 0
   __syncthreads();
   if (!first) return;
+  // wave 0 lists the rows e >= l with this id, in ascending order (ballots
+  // over 64 rows at a time); every thread then sums only those rows
+  __shared__ int lst[EG_MAXL];
+  __shared__ int nl;
+  if (threadIdx.x < 64) {
+    int cnt = 0;
+    for (int base = l; base < L; base += 64) {
+      const int e = base + threadIdx.x;
+      const bool m = e < L && sid[e] == my;
+      const unsigned long long mask = __ballot(m);
+      if (m) lst[cnt + __popcll(mask & ((1ull << threadIdx.x) - 1ull))] = e;
+      cnt += __popcll(mask);
+    }
+    if (threadIdx.x == 0) nl = cnt;
+  }
+  __syncthreads();
+  const int n = nl;
   for (int d = threadIdx.x; d < D; d += 256) {
     float acc = 0.f;
-    for (int e = l; e < L; ++e)
-      if (sid[e] == my) acc += g[((int64_t)csamp[e / T] * T + e % T) * D + d];
+    for (int j = 0; j < n; ++j) {
+      const int e = lst[j];
+      acc += g[((int64_t)csamp[e / T] * T + e % T) * D + d];
+    }
     gradE[(int64_t)my * D + d] = acc * scale;
   }
 }
