@@ -4,10 +4,11 @@ path timed beside it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wide]
 
-Prints ONE JSON line.  `value` is samples/s of the headline workload (C3, the
-wide Dense stack, unless --config says otherwise) with inputs resident in HBM.
-The `configs` key holds the same measurements for the other four BASELINE
-configurations, so one run times all five.  Per-kernel rooflines come from
+Prints ONE JSON line last (under 4 KB).  `value` is samples/s of the headline
+workload (C3, the wide Dense stack, unless --config says otherwise) with inputs
+resident in HBM.  The `configs` key holds a short summary of the other four
+BASELINE configurations, so one run times all five; every configuration's
+full per-kernel table goes to gpurun_out/bench_detail.json.  Per-kernel rooflines come from
 HIP events the library records around each of its launches (on the stream the
 launch goes to), divided into the launch's algorithmic work (bytes for
 memory-bound kernels, FLOPs for matrix-core kernels) that the library states
@@ -32,6 +33,11 @@ PEAK_FP64_MFMA_TFLOPS = 78.6
 PEAK_HBM_GBPS = 8000.0
 # the CPU share of one GPU on the GPU boxes (their nproc shows the whole host)
 CPU_SHARE = 16
+# Network.TrainBatch goes parallel from 64 samples up (net.go:428-435)
+PARALLEL_THRESHOLD = 64
+# the driver keeps the tail of stdout; the final line stays well inside it
+MAX_LINE_BYTES = 4096
+DETAIL_PATH = os.path.join(ROOT, "gpurun_out", "bench_detail.json")
 
 # HBM bytes per GEMM launch of the C3 step, from the FETCH_SIZE / WRITE_SIZE
 # rocprofv3 passes of this bench scaled by a copy kernel of known size
@@ -113,7 +119,9 @@ def cpu_baseline(cfg, x, y, budget_s, threads):
         state and gradient arena, as LightweightClone) running its own
         contiguous chunk; then the serial sum of the T gradient arenas and one
         Adam pass, per batch;
-      - single thread: trainBatchSequential (net.go:721-784).
+      - single thread: trainBatchSequential (net.go:721-784), the reported
+        value for batches below 64 samples, which the reference never runs
+        in parallel (net.go:428-435).
     samples/s = samples / (sample time + per-batch time * samples / B)."""
     import threading
     from oracle import refcpu
@@ -122,7 +130,7 @@ def cpu_baseline(cfg, x, y, budget_s, threads):
     refcpu.build()
     B = cfg["B"]
     T = threads
-    nets = [oracle_net(refcpu, cfg) for _ in range(T)]
+    nets = [oracle_net(refcpu, cfg) for _ in range(T if B >= PARALLEL_THRESHOLD else 1)]
     net = nets[0]
     # calibrate with one sample, then fill the budget
     t0 = time.perf_counter()
@@ -152,6 +160,15 @@ def cpu_baseline(cfg, x, y, budget_s, threads):
         for h in th:
             h.join()
 
+    if B < PARALLEL_THRESHOLD:
+        # the reference trains batches below 64 samples sequentially on one
+        # goroutine (Network.TrainBatch, net.go:428-435): the 1-thread figure
+        # is the baseline
+        del nets
+        return {"value": single, "unit": "samples/s", "cores": 1, "kind": "port",
+                "sample": f"oracle/refcpu (C restatement, -O2 -ffp-contract=off), trainBatchSequential "
+                          f"(B = {B} < 64): {n1} of {B} samples fwd+bwd ({ts1:.2f} s) + one Adam pass "
+                          f"({ta:.3f} s) scaled by n/B"}
     run_all(1)  # first touch of every worker's buffers, untimed
     acc = np.zeros_like(net.grads)
     acc += 1.0
@@ -167,10 +184,10 @@ def cpu_baseline(cfg, x, y, budget_s, threads):
     par = done / (tp + (tsum + ta) * done / B)
     del nets
     return {"value": par, "unit": "samples/s", "cores": T, "kind": "port",
-            "sample": f"oracle/refcpu (C restatement of the per-sample path, -O2 -ffp-contract=off): "
+            "sample": f"oracle/refcpu (C restatement, -O2 -ffp-contract=off), trainBatchParallel shape: "
                       f"{T} threads x {npt} samples of their own chunks of the {B}-sample batch "
-                      f"({tp:.2f} s), plus per batch the sum of {T} gradient arenas ({tsum:.3f} s) and one "
-                      f"Adam pass over {net.n} params ({ta:.3f} s) scaled by samples/B",
+                      f"({tp:.2f} s) + per batch the sum of {T} gradient arenas ({tsum:.3f} s) and one "
+                      f"Adam pass ({ta:.3f} s) scaled by samples/B",
             "single_thread": {"value": single, "cores": 1,
                               "sample": f"{n1} of {B} samples fwd+bwd ({ts1:.2f} s) + Adam scaled by n/B"}}
 
@@ -368,43 +385,97 @@ def main():
                 others[name] = run_config(name, args, dev, not args.no_cpu, args.cpu_budget, threads)
                 print(f"bench: {name} {others[name]['value']:.0f} samples/s", file=sys.stderr, flush=True)
     cfg = configs.get(args.config)
-    K = args.steps
-    g = head["gemm"]
     traffic = gemm_traffic_per_launch() if args.config == "wide" else None
-    flops_per_launch = g["flops_per_step"] / g["launches_per_step"] if g["launches_per_step"] else None
-    line = {
+    write_detail({"host": dict(host, threads_used=min(head["batch"], threads)),
+                  "headline": head, "configs": others})
+    line = final_line(args, cfg, head, others, host, traffic)
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > MAX_LINE_BYTES:  # never expected: drop the per-config map first
+        line.pop("configs", None)
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
+
+
+def _r(v, nd=4):
+    """A float rounded to nd significant digits (None passes through)."""
+    if v is None:
+        return None
+    return float(f"{v:.{nd}g}")
+
+
+def summarize(res):
+    """What the final line keeps of one configuration: throughput, the
+    dominant kernel's roofline fraction and the CPU baseline's value."""
+    d = res.get("dominant") or {}
+    cb = res.get("cpu_baseline") or {}
+    return {"value": _r(res["value"]), "ms_per_step": _r(res["ms_per_step"]),
+            "batch": res["batch"], "workers": res["workers"],
+            "kernels_per_step": _r(res.get("kernels_per_step"), 3),
+            "dominant": d.get("kernel"), "dominant_bound": d.get("bound"),
+            "dominant_frac": _r(d.get("frac"), 3),
+            "cpu_baseline": _r(cb.get("value")), "cpu_cores": cb.get("cores")}
+
+
+def final_line(args, cfg, head, others, host, traffic):
+    """The one JSON line the driver parses, kept under MAX_LINE_BYTES: the
+    headline workload's value, roofline and CPU baseline, plus a short entry
+    per other configuration.  Full per-kernel tables go to DETAIL_PATH."""
+    g = head["gemm"]
+    if g["launches_per_step"] and g["achieved_tflops"]:
+        # GEMM family of the step: every launch of the fp32 MFMA GEMM kernels
+        roof = {"bound": "mfma", "achieved": _r(g["achieved_tflops"]), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": _r(g["achieved_tflops"] / PEAK_FP32_MFMA_TFLOPS),
+                "traffic": traffic,
+                "kernel": "gemm_f32_mfma (gemm_fwd, gemm_dx, gemm_dw)",
+                "flops_per_launch": _r(g["flops_per_step"] / g["launches_per_step"]),
+                "avg_launch_ms": _r(g["avg_launch_ms"]),
+                "launches_per_step": g["launches_per_step"]}
+    else:
+        d = head.get("dominant") or {}
+        roof = {"bound": "hbm" if d.get("bound") == "hbm" else "mfma", "achieved": _r(d.get("achieved")),
+                "peak": d.get("peak"), "unit": d.get("unit"), "frac": _r(d.get("frac")),
+                "traffic": None, "kernel": d.get("kernel")}
+    cb = head.get("cpu_baseline")
+    if cb is not None:
+        cb = {"value": _r(cb["value"]), "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
+              "sample": cb["sample"][:300],
+              "single_thread": _r((cb.get("single_thread") or {}).get("value", cb["value"]))}
+    adam = head.get("adam_alone") or {}
+    return {
         "metric": "train samples/s (fwd+bwd+Adam) on 1 MI355X; % of fp32 MFMA / HBM roofline",
-        "value": head["value"],
+        "value": _r(head["value"], 6),
         "unit": "samples/s",
         "n_gpus": 1,
-        "steps": K,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["ms_per_step"],
+        "ms_per_step": _r(head["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (reference LCG, seeds 1000+cfg / 2000+cfg), reference LCG weight init",
+        "data": "synthetic (reference LCG inputs, seeds 1000+cfg / 2000+cfg; reference LCG weight init)",
         "config": {"workload": cfg["name"], "batch": head["batch"], "workers": head["workers"],
-                   "layers": [d["kind"] + (f"{d['in']}->{d['out']}" if d["kind"] == "dense" else "")
-                              for d in cfg["layers"]],
-                   "loss": cfg["loss"], "optimizer": "Adam lr=1e-3"},
-        "roofline": {"bound": "mfma", "achieved": g["achieved_tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s",
-                     "frac": g["achieved_tflops"] / PEAK_FP32_MFMA_TFLOPS if g["achieved_tflops"] else None,
-                     "traffic": traffic,
-                     "kernel": "gemm_f32_mfma (all instantiations: gemm_fwd, gemm_dx, gemm_dw)",
-                     "flops_per_launch": flops_per_launch, "avg_launch_ms": g["avg_launch_ms"]},
-        "kernels": head["kernels"],
-        "adam_alone": head["adam_alone"],
-        "h2d_step": head["h2d_step"],
-        "instrumented_ms_per_step": head["instrumented_ms_per_step"],
-        "loss": head["loss"],
-        "host": dict(host, threads_used=min(head["batch"], threads)),
-        "cpu_baseline": head.get("cpu_baseline"),
-        "configs": others,
+                   "params": head["params"], "loss": cfg["loss"], "optimizer": "Adam lr=1e-3"},
+        "roofline": roof,
+        "adam": {"achieved": _r(adam.get("achieved")), "unit": "GB/s", "peak": PEAK_HBM_GBPS,
+                 "frac": _r(adam.get("frac"))},
+        "h2d_ms_per_step": _r(head["h2d_step"]["ms_per_step"]),
+        "cpu_baseline": cb,
+        "host": {"cpu_model": (host.get("cpu_model") or "")[:60], "threads": min(head["batch"], CPU_SHARE,
+                                                                                 host.get("affinity") or 1)},
+        "configs": {k: summarize(v) for k, v in others.items()},
+        "detail": os.path.relpath(DETAIL_PATH, ROOT),
     }
-    print(json.dumps(line), flush=True)
+
+
+def write_detail(obj):
+    """Full per-kernel tables of every configuration (not part of the line)."""
+    try:
+        os.makedirs(os.path.dirname(DETAIL_PATH), exist_ok=True)
+        with open(DETAIL_PATH, "w") as fh:
+            json.dump(obj, fh, indent=1)
+    except OSError as e:
+        print(f"bench: could not write {DETAIL_PATH}: {e}", file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":

@@ -568,6 +568,9 @@ struct gn_model {
   // its first overlapped train step and destroyed with the model, so a
   // context that later trains other models keeps two streams in use
   hipStream_t adam_s = nullptr;
+  // per-layer updates launched by the current overlapped step: a step that
+  // fails after one of them keeps its timestep (those layers hold step t)
+  int step_updates = 0;
   // HIP graphs of the accumulate pass (forward, loss, backward) of small
   // models, keyed by the input pointers, the batch and the training flags in
   // effect: the first step with a key runs eagerly, the second is captured,
@@ -2332,6 +2335,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       for (int j = 0; j < i; ++j)
         if (M->L[j].pcount > 0) last = false;
       KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, M->adam_s);
+      ++M->step_updates;
       HIP_OK(c, launch_adam(M->params + R.poff, M->grads + R.poff, M->m + R.poff, M->v + R.poff,
                             R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps,
                             M->adam_s, last ? 16384 : 256));
@@ -2465,8 +2469,14 @@ static int model_train_step(gn_model *M, const float *x, const float *y, int B) 
   if (B <= 0 || B > M->maxB) return set_err(M->ctx, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
   const int saved = M->timestep;
   const AdamCoef a = adam_next(M);
+  M->step_updates = 0;
   int rc = model_accumulate(M, x, y, B, &a);
-  if (rc) M->timestep = saved;
+  // Failed before any layer was updated: the step did not happen.  Failed
+  // after some layers' updates were launched: those layers hold step t and
+  // the others do not, so the parameters are inconsistent (the caller
+  // reloads a checkpoint); the timestep stays at t so a retry does not apply
+  // bias correction t a second time to the updated layers.
+  if (rc && M->step_updates == 0) M->timestep = saved;
   return rc;
 }
 

@@ -22,7 +22,27 @@
 // dWh = (w dG)^T hPrev, db = sum w dG.
 #include "gn_common.h"
 
+#include <atomic>
+
 namespace gn {
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) holds per device and per
+// kernel.  set[d] is the largest size already set on device d for one kernel:
+// a later launch that needs more LDS (a larger H) sets it again.
+static constexpr int kAttrDevices = 64;
+static hipError_t ensure_lds_attr(const void *fn, int bytes, std::atomic<int> (&set)[kAttrDevices]) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kAttrDevices) return hipErrorInvalidDevice;
+  if (set[dev].load(std::memory_order_relaxed) >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return e;
+  int cur = set[dev].load(std::memory_order_relaxed);
+  while (cur < bytes && !set[dev].compare_exchange_weak(cur, bytes)) {
+  }
+  return hipSuccess;
+}
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + (float)exp((double)(-x))); }
 __device__ __forceinline__ float tanh32(float x) { return (float)tanh((double)x); }
@@ -1117,12 +1137,12 @@ hipError_t launch_lstm_fwd(const float *xw, const float *WhT, const float *bias,
   if (L.v4 && H % 4 == 0)
     while (QL < L.NQ && (size_t)(H * (QL + 1) / L.NQ) * H * sizeof(float) <= (128u << 10)) ++QL;
   const size_t shm = base + (size_t)(H * QL / L.NQ) * H * sizeof(float);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_fwd_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 << 10);
+  static std::atomic<int> attr_v4[kAttrDevices], attr_v1[kAttrDevices];
+  {
+    const hipError_t e =
+        L.v4 ? ensure_lds_attr(reinterpret_cast<const void *>(lstm_fwd_kernel<true>), (int)shm, attr_v4)
+             : ensure_lds_attr(reinterpret_cast<const void *>(lstm_fwd_kernel<false>), (int)shm, attr_v1);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   if (L.v4)
     hipLaunchKernelGGL(lstm_fwd_kernel<true>, dim3(B), dim3(1024), shm, s, xw, WhT, bias, igb, tcb,
@@ -1170,12 +1190,11 @@ hipError_t launch_lstm_bwd_coop(const float *gh, const float *igb, const float *
   if (!lstm_coop_eligible(B, H)) return hipErrorInvalidValue;
   unsigned long long *X = reinterpret_cast<unsigned long long *>(sync);
   const size_t shm = lstm_coop_lds(H);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_bwd_coop_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  static std::atomic<int> attr_set[kAttrDevices];
+  {
+    const hipError_t e =
+        ensure_lds_attr(reinterpret_cast<const void *>(lstm_bwd_coop_kernel), (int)shm, attr_set);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   unsigned base = *epoch;
   void *args[] = {(void *)&gh, (void *)&igb, (void *)&tcb, (void *)&cbuf, (void *)&Wh,
@@ -1247,12 +1266,11 @@ hipError_t launch_lstm_clip(const double *gram, double *coef, float *w, int B, i
   // beside the Gram kernel, unused dynamic LDS keeps its workgroups off the
   // clip's CUs (their waves would take issue slots from the serial recursion)
   const size_t pad = cnt ? (size_t)24 << 10 : 0;
-  static bool attr_set = false;
-  if (cnt && !attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(lstm_clip_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pad);
+  static std::atomic<int> attr_set[kAttrDevices];
+  if (cnt) {
+    const hipError_t e =
+        ensure_lds_attr(reinterpret_cast<const void *>(lstm_clip_kernel), (int)pad, attr_set);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   hipLaunchKernelGGL(lstm_clip_kernel, dim3(nchains), dim3(CLIP_NT), pad, s, gram, coef, w, cm, nmax,
                      cnt, epoch, started, bailed, err, spin_limit, bail_limit);

@@ -165,7 +165,13 @@ int gn_model_arena(gn_model *m, float **params, float **grads, float **adam_m, f
 
 /* Network.TrainBatch (net.go:412-436): one fwd+bwd over B samples, gradient
  * average, Adam step.  Host inputs: x is B x in_size, y is B x out_size
- * (row major, the [][]float32 batches flattened).  loss_out may be NULL. */
+ * (row major, the [][]float32 batches flattened).  loss_out may be NULL.
+ * On failure: a step that failed before any parameter was updated leaves
+ * the model as it was.  Large models update each layer as soon as its
+ * backward is done; a step of such a model that fails after some layers
+ * were updated leaves those at step t and the others at t-1 (reload a
+ * checkpoint), with the Adam timestep at t, so a retry never applies bias
+ * correction t twice. */
 int gn_model_train_step(gn_model *m, const float *x, const float *y, int32_t B, float *loss_out);
 /* Same with HBM-resident x / y; the mean loss stays on the device (read it
  * with gn_model_read_loss).  No host synchronisation. */
