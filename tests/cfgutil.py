@@ -177,3 +177,33 @@ def adam_flips(p_new, p_old, r_new, m_ref, rel=1e-4):
     small = np.abs(m_ref) <= rel * np.abs(m_ref).max()
     allowed = flips & small
     return allowed, int(allowed.sum()), int((flips & ~small).sum())
+
+
+def adam_update_bound(g, m_old, v_old, tau, timestep, lr=1e-3, b1=0.9, b2=0.999, eps=1e-8):
+    """Largest change of each Adam update (opt.go:207-258, Q1: t = timestep+1)
+    that a gradient change of at most tau per element can cause, from the
+    moments m_old, v_old before the step.  Per element the update is
+        effLR * u(g),  u(g) = (b1 m + (1-b1) g) / (sqrt(b2 v + (1-b2) g^2) + eps),
+    one function of g, whose extremes on [g - tau, g + tau] lie at the ends
+    or where u'(g) = 0, i.e. g* = (1-b1) b2 v / (b1 m (1-b2)) (eps left out
+    there; it shifts the extreme by a relative 1e-8 of the update).
+    Elements whose gradient is small next to tau get a large bound: Adam
+    normalises each element, so their updates move by up to a full step
+    under rounding-level gradient changes."""
+    g = np.asarray(g, np.float64)
+    m = np.asarray(m_old, np.float64)
+    v = np.asarray(v_old, np.float64)
+    ts = timestep + 1
+    efflr = lr * np.sqrt(1.0 - b2 ** ts) / (1.0 - b1 ** ts)
+
+    def u(x):
+        return (b1 * m + (1.0 - b1) * x) / (np.sqrt(b2 * v + (1.0 - b2) * x * x) + eps)
+
+    u0 = u(g)
+    dev = np.maximum(np.abs(u(g - tau) - u0), np.abs(u(g + tau) - u0))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        gs = (1.0 - b1) * b2 * v / (b1 * m * (1.0 - b2))
+    inside = np.isfinite(gs) & (np.abs(gs - g) <= tau)
+    if inside.any():
+        dev = np.where(inside, np.maximum(dev, np.abs(u(np.where(inside, gs, g)) - u0)), dev)
+    return efflr * dev * (1.0 + 1e-6)

@@ -488,6 +488,27 @@ def configs_inputs(cfg):
     return configs.inputs(cfg)
 
 
+# C5 tensors per test allowed to pass through the float64 arbiter rather
+# than against the oracle directly: none (every C5 tensor of every case has
+# been within 1e-4 of the oracle); the arbiter stays to report the errors of
+# a tensor that misses.
+LSTM_ARBITER_MAX = 0
+
+
+def _record_arbiter(case, steps, rec):
+    """Arbiter decisions of one C5 case, printed and appended to
+    gpurun_out/lstm_arbiter.jsonl when that folder exists."""
+    import json
+    import os
+    line = {"case": case, "steps": steps, "tensors_per_step": 12, "asked": len(rec),
+            "passed_by_arbiter": sum(r["passed_by_arbiter"] for r in rec), "records": rec}
+    print("lstm arbiter: " + json.dumps(line), flush=True)
+    out = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
+    if os.path.isdir(out):
+        with open(os.path.join(out, "lstm_arbiter.jsonl"), "a") as fh:
+            fh.write(json.dumps(line) + "\n")
+
+
 def _random_lstm(cfg, scale=0.08, seed=31):
     """Small random LSTM parameters with non-zero biases in every gate, so the
     first step already has live i, f, g, o deltas, non-zero h_prev and c_prev
@@ -518,8 +539,14 @@ def test_lstm_full_config(gn, oracle, workers, steps, start):
     x, y = configs.inputs(cfg)
     d = cfg["layers"][0]
     exact = lambda p: lstm_clip_truth(p, x, y[:, 0], d["in"], d["hidden"], d["T"], workers)
+    rec = []
     _compare_step(gn, oracle, cfg, steps=steps, workers=workers,
-                  perturb=_random_lstm(cfg) if start == "random" else None, arbiter=exact)
+                  perturb=_random_lstm(cfg) if start == "random" else None, arbiter=exact, record=rec)
+    # the tensors (of 12 per step) that pass only because the GPU is at least
+    # as close to the float64 answer as the oracle: written out and bounded
+    passed = [r for r in rec if r["passed_by_arbiter"]]
+    _record_arbiter(f"W={workers} start={start}", steps, rec)
+    assert len(passed) <= LSTM_ARBITER_MAX, passed
 
 
 @pytest.mark.parametrize("workers", [1, 3])
@@ -665,6 +692,16 @@ def test_gpt_full_config_random_block(gn, oracle):
     from goneuron_amd import configs
     cfg = configs.gpt()
     _compare_step(gn, oracle, cfg, steps=1, perturb=_random_block(cfg, scale=0.05))
+
+
+def test_gpt_full_config_reference_start(gn, oracle):
+    """C4 at BASELINE size from the reference's own start, the benchmarked
+    one: every TransformerBlock parameter 0 (Q11), so the first step trains
+    the embedding's last sample (Q12), the positional table, the block's
+    biases and the output layer, and the second step starts from a non-zero
+    block.  Two steps, every tensor checked on its own."""
+    from goneuron_amd import configs
+    _compare_step(gn, oracle, configs.gpt(), steps=2)
 
 
 def test_gpt_embedding_index_error(gn, oracle):

@@ -1268,3 +1268,41 @@ def test_gpt_grads_vs_torch_autograd(oracle, act, norm, rope, causal):
             continue
         assert np.abs(ref[part]).max() > 1e-3, name
         assert max_rel(got[part], ref[part]) < 1e-5, (name, max_rel(got[part], ref[part]))
+
+
+@pytest.mark.parametrize("timestep", [1, 2, 7])
+def test_adam_update_bound_is_sound_and_tight(oracle, timestep):
+    """The propagated tolerance the GPU parity tests allow an Adam update
+    (cfgutil.adam_update_bound): over random gradient changes of at most tau
+    per element, the oracle's own Adam (opt.go:207-258) never moves an update
+    by more than the bound, and the worst change comes close to it."""
+    from cfgutil import adam_update_bound
+    rng = np.random.default_rng(40 + timestep)
+    n = 4096
+    # gradients spanning six decades, so some are at the tolerance's scale
+    g = (rng.normal(size=n) * 10.0 ** rng.uniform(-6, 0, n)).astype(np.float32)
+    m0 = (rng.normal(size=n) * 1e-3 * (timestep > 1)).astype(np.float32)
+    v0 = (np.abs(rng.normal(size=n)) * 1e-6 * (timestep > 1)).astype(np.float32)
+    p0 = rng.normal(size=n).astype(np.float32) * np.float32(0.05)
+    tau = 1e-4 * float(np.abs(g).max())
+
+    def run(gg):
+        p, m, v = p0.copy(), m0.copy(), v0.copy()
+        oracle.adam_step(p, gg.astype(np.float32), m, v, 1e-3, 0.9, 0.999, 1e-8, timestep)
+        return p, m, v
+
+    p_ref, m_ref, v_ref = run(g)
+    bnd = adam_update_bound(g, m0, v0, tau, timestep)
+    worst = np.zeros(n)
+    for k in range(24):
+        d = rng.uniform(-1, 1, n) if k < 20 else np.full(n, (-1.0) ** k)
+        p, _, _ = run(g + (d * tau).astype(np.float32))
+        dp = np.abs(p.astype(np.float64) - p_ref)
+        # float32 rounding of the update itself: a few ulps of the weight and
+        # of the update
+        rnd = 4 * np.spacing(np.abs(p_ref)).astype(np.float64) + 1e-6 * np.abs(p_ref - p0)
+        assert (dp <= bnd * 1.001 + rnd).all()
+        worst = np.maximum(worst, dp)
+    big = bnd > 1e-6
+    assert big.any()
+    assert np.median(worst[big] / bnd[big]) > 0.3
