@@ -67,7 +67,8 @@ def Ref(act: Activation) -> Activation:
 # ---------------------------------------------------------------- layers
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
- LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE) = range(1, 17)
+ LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE, LAYER_MHA,
+ LAYER_LAYERNORM, LAYER_GAP1D) = range(1, 20)
 
 
 class Layer:
@@ -175,6 +176,41 @@ def RMSNorm(*normalized_shape, eps=1e-5):
     if eps < 0:
         raise GNError(-1, f"invalid eps {eps}: must be >= 0")
     return Layer(LAYER_RMSNORM, dim=int(normalized_shape[0]), eps=float(eps) if eps > 0 else 0.0)
+
+
+def LayerNorm(*normalized_shape, eps=1e-5):
+    """goneuron.LayerNorm (goneuron.go:220-227) -> layer.NewLayerNorm(in, 1e-5,
+    true): y = gamma (x - mean) / sqrt(var + eps) + beta over rows of
+    normalizedShape, gamma 1 and beta 0 at the start (layernorm.go:57-118).
+    The lazy form LayerNorm() is rejected: LayerNorm.Build has no error
+    return, so Sequential.Build (sequential.go:68-73) never resolves it."""
+    if not normalized_shape or normalized_shape[0] <= 0:
+        raise GNError(-1, "LayerNorm needs normalizedShape > 0 (the lazy form is never built)")
+    if eps < 0:
+        raise GNError(-1, f"invalid eps {eps}: must be >= 0")
+    return Layer(LAYER_LAYERNORM, dim=int(normalized_shape[0]), eps=float(eps) if eps > 0 else 0.0)
+
+
+def MultiHeadAttention(num_heads, seq_len, causal, *dim):
+    """goneuron.MultiHeadAttention (goneuron.go:369-376) ->
+    layer.NewMultiHeadAttentionE(dim, numHeads, seqLen, causal): per-token
+    wQ, wK, wV, wOut Linear Dense layers around scaled dot-product attention,
+    all parameters starting at 0 (Build rebinds them to a fresh zero buffer,
+    transformer.go:318-394).  Without dim the layer takes input / seq_len."""
+    if num_heads <= 0 or seq_len <= 0:
+        raise GNError(-1, f"invalid numHeads {num_heads} / seqLen {seq_len}")
+    d = int(dim[0]) if dim else -1
+    if d != -1 and (d <= 0 or d % num_heads):
+        raise GNError(-1, f"dim {d} must be positive and divisible by numHeads {num_heads}")
+    return Layer(LAYER_MHA, dim=d, num_heads=int(num_heads), seq_len=int(seq_len), causal=int(causal))
+
+
+def GlobalAveragePooling1D(seq_len, dim):
+    """goneuron.GlobalAveragePooling1D (goneuron.go:378-381): the mean over the
+    seq_len rows of dim (transformer.go:1524-1600)."""
+    if seq_len <= 0 or dim <= 0:
+        raise GNError(-1, f"invalid seqLen {seq_len} / dim {dim}")
+    return Layer(LAYER_GAP1D, seq_len=int(seq_len), dim=int(dim))
 
 
 def SwiGLU(out, *in_size):

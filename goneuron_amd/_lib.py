@@ -132,8 +132,8 @@ SIGNATURES = {
     "gn_mha_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 6),
     "gn_mha_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 6 + [C.c_float]),
     "gn_lstm_workspace": (C.c_int, [C.c_int32] * 5 + [C.POINTER(C.c_int64)]),
-    "gn_lstm_seq_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 4),
-    "gn_lstm_seq_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 5 + [C.c_float]),
+    "gn_lstm_seq_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 5),
+    "gn_lstm_seq_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 5 + [C.c_float, C.c_int32]),
     "gn_embedding_forward": (C.c_int, [vp] + [vp] * 5 + [C.c_int32] * 4),
     "gn_embedding_backward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 5 + [C.c_float]),
     "gn_gemm": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float, vp,

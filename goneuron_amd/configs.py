@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 
 from . import (CrossEntropy, MSE, Adam, Dense, Dropout, Conv2D, MaxPool2D, AvgPool2D, BatchNorm2D, MoE,
-               RMSNorm,
+               RMSNorm, LayerNorm, MultiHeadAttention, GlobalAveragePooling1D,
                SwiGLU, Flatten, TransformerBlockExt, ActReLU, ActSwiGLU, ActGELU, NormLN, NormRMS,
                Embedding,
                PositionalEncoding, TransformerBlock, CLSPooling, LSTM, GRU, SequenceUnroller, ReLU,
@@ -139,6 +139,12 @@ def product_layers(cfg):
             out.append(AvgPool2D(d["k"], d["s"], d["p"], d["inC"]))
         elif k == "rmsnorm":
             out.append(RMSNorm(d["n"]))
+        elif k == "layernorm":
+            out.append(LayerNorm(d["n"]))
+        elif k == "mha":
+            out.append(MultiHeadAttention(d["heads"], d["T"], d["causal"], d["dim"]))
+        elif k == "gap1d":
+            out.append(GlobalAveragePooling1D(d["T"], d["dim"]))
         elif k == "batchnorm2d":
             out.append(BatchNorm2D(d["C"]))
         elif k == "moe":

@@ -48,6 +48,7 @@ const char *layer_type(int kind) {
     case GN_LAYER_EMBEDDING: return "Embedding";
     case GN_LAYER_FLATTEN: return "Flatten";
     case GN_LAYER_BATCHNORM2D: return "BatchNorm2D";
+    case GN_LAYER_LAYERNORM: return "LayerNorm";
     default: return "Unknown";
   }
 }
@@ -87,6 +88,15 @@ void layer_tensors(gn_model *M, int i, int64_t poff, int64_t pcount, std::vector
     case GN_LAYER_EMBEDDING: b.add("weights", {d.vocab, d.dim}); return;  // embedding.go:248-256
     case GN_LAYER_POSENC: b.add("weights", {d.seq_len, (int64_t)pcount / d.seq_len}); return;
     case GN_LAYER_RMSNORM: b.add("gamma", {d.dim}); return;  // rmsnorm.go:434-442
+    case GN_LAYER_LAYERNORM:                                  // layernorm.go:533-550
+      b.add("gamma", {d.dim});
+      b.add("beta", {d.dim});
+      return;
+    case GN_LAYER_MHA: {  // transformer.go:786-801; pcount = 4 (D^2 + D)
+      const int64_t D = (int64_t)((sqrt(1.0 + (double)pcount) - 1.0) / 2.0 + 0.5);
+      for (const char *w : {"wQ_", "wK_", "wV_", "wOut_"}) b.dense(w, D, D);
+      return;
+    }
     case GN_LAYER_SWIGLU:                                     // swiglu.go:295-308
       b.add("w", {d.out_size, d.in_size});
       b.add("v", {d.out_size, d.in_size});
@@ -909,7 +919,7 @@ extern "C" int gn_model_save_gob(gn_model *M, const char *path) {
     float eps = 0;
     model_layer_geom(M, i, &cs, &ps, &eps);
     // ExtractLayerConfig (net.go:1426-1505)
-    int64_t in = -1, out = -1, k = 0, st = 0, pad = 0, inC = 0, outC = 0;
+    int64_t in = -1, out = -1, k = 0, st = 0, pad = 0, inC = 0, outC = 0, ns = 0;
     float prob = 0, e = 0;
     bool affine = false;
     std::string act;
@@ -938,6 +948,9 @@ extern "C" int gn_model_save_gob(gn_model *M, const char *path) {
       case GN_LAYER_EMBEDDING:
         in = d.vocab, out = d.dim;
         break;
+      case GN_LAYER_LAYERNORM:  // net.go:1469-1473
+        ns = d.dim, e = eps, affine = true;
+        break;
       default:
         break;
     }
@@ -957,6 +970,7 @@ extern "C" int gn_model_save_gob(gn_model *M, const char *path) {
     f.f(11, prob);
     f.f(12, e);
     f.b(13, affine);
+    f.i(14, ns);
     f.end();
     s.message(m);
   }
@@ -1094,7 +1108,12 @@ extern "C" int gn_model_load_gob(gn_ctx *c, const char *path, int32_t in_len, in
       d.kind = GN_LAYER_EMBEDDING, d.vocab = narrow(g.in_size), d.dim = narrow(g.out_size);
     } else if (g.type == "Flatten") {
       d.kind = GN_LAYER_FLATTEN;
-    } else if (g.type == "LSTM" || g.type == "GRU" || g.type == "LayerNorm" || g.type == "RBF") {
+    } else if (g.type == "LayerNorm") {  // net.go:1544-1547: NewLayerNorm(NormalizedShape, Eps, Affine)
+      if (!g.affine)
+        return set_err(c, GN_ERR_UNSUPPORTED, "layer %lld: LayerNorm without affine parameters is not built",
+                       (long long)i);
+      d.kind = GN_LAYER_LAYERNORM, d.dim = narrow(g.normalized_shape), d.eps = g.eps;
+    } else if (g.type == "LSTM" || g.type == "GRU" || g.type == "RBF") {
       return set_err(c, GN_ERR_UNSUPPORTED, "failed to create layer: %s is not built by this library",
                      g.type.c_str());
     } else {
@@ -1108,6 +1127,7 @@ extern "C" int gn_model_load_gob(gn_ctx *c, const char *path, int32_t in_len, in
       want = (int64_t)d.out_channels * d.in_channels * d.kernel * d.kernel + d.out_channels;
     else if (d.kind == GN_LAYER_BATCHNORM2D) want = d.no_affine ? 0 : 2 * (int64_t)d.in_channels;
     else if (d.kind == GN_LAYER_EMBEDDING) want = (int64_t)d.vocab * d.dim;
+    else if (d.kind == GN_LAYER_LAYERNORM) want = 2 * (int64_t)d.dim;
     if (want != (int64_t)g.params.size())
       return set_err(c, GN_ERR_UNSUPPORTED,
                      "layer %lld (%s): the file holds %zu parameters, the layer its config describes %lld",

@@ -137,6 +137,9 @@ hipError_t launch_add3(const float *r, const float *p, int64_t pstride, float *o
 
 // Row activation only (forward/predict)
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s);
+// dz of a hidden Softmax / LogSoftmax row activation from its output gradient
+hipError_t launch_row_jac(const float *g, const float *out, float *dz, int B, int C, int row_act,
+                          hipStream_t s);
 
 
 // dropout: out = x*scale where mask else 0 (mask is per-feature, Q9)
@@ -271,16 +274,22 @@ hipError_t launch_lstm_weight(float *D, const float *w, float *S, int B, int T, 
 
 // ---- Transformer path ----
 // bad (may be null): per-sample flag, 1 when one of its ids lies outside [0, V)
+// bad_or: only set flags (a later Embedding of the network adds its samples)
 hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int B, int T, int V,
-                        int D, int32_t *bad, hipStream_t s);
+                        int D, int32_t *bad, hipStream_t s, bool bad_or = false);
 hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int TD, hipStream_t s);
 // Embedding then PositionalEncoding: out = the embedding rows, pe_out = out + pe[t]
 hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int32_t *ids, float *out,
-                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s);
+                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s,
+                           bool bad_or = false);
+// ws (may be null below 2048 contributing rows): 2 x contributing rows ints
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
-                             int D, int W, float scale, const int32_t *bad, hipStream_t s);
+                             int D, int W, float scale, const int32_t *bad, hipStream_t s,
+                             float *ws = nullptr, size_t ws_floats = 0);
 hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
 hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipStream_t s);
+hipError_t launch_gap1d_fwd(const float *x, float *out, int B, int T, int D, hipStream_t s);
+hipError_t launch_gap1d_bwd(const float *g, float *gin, int B, int T, int D, hipStream_t s);
 hipError_t launch_token_sum(const float *X, float *S, int B, int T, int N, hipStream_t s);
 // nmem token sums in one launch: member m reads X + m*xstride, writes S + m*sstride
 hipError_t launch_token_sum_multi(const float *X, float *S, int B, int T, int N, int nmem,

@@ -184,3 +184,18 @@ inline int plan_scalar_act(int act, int &fwd, int &deriv) {
 }
 
 
+
+// MultiHeadAttention buffers of one batch (gn_ops.hip): Q, K, V (and GQ, GK,
+// GV) equally spaced, token sums S [B][D] and S3 (three blocks s3_stride
+// apart), RoPE tables [T][hd/2], materialised scores when the fused kernels
+// do not hold the shape.
+struct MhaBufs {
+  float *Q, *K, *V, *O, *GO, *GQ, *GK, *GV, *S, *S3, *rcos, *rsin, *SC;
+  int64_t s3_stride;
+};
+void rope_tables(int T, int hd, std::vector<float> &cs, std::vector<float> &sn);
+int mha_forward_impl(gn_ctx *c, const float *x, const float *params, float *out, const MhaBufs &m,
+                     int B, int T, int D, int NH, int causal, int rope);
+int mha_backward_impl(gn_ctx *c, const float *x, const float *params, const float *gout, float *grads,
+                      float *gin, const MhaBufs &m, int B, int T, int D, int NH, int causal, int rope,
+                      float scale);

@@ -246,13 +246,9 @@ extern "C" int gn_layernorm_backward(gn_ctx *c, const float *g, const float *x, 
 // forward and backward of one batch must share it and x.
 // ---------------------------------------------------------------------------
 namespace {
-struct MhaWork {
-  float *Q, *K, *V, *O, *GO, *GQ, *GK, *GV, *S, *S3, *rcos, *rsin, *SC;
-  size_t floats;
-};
-MhaWork mha_carve(float *w, int B, int T, int D, int NH, int rope) {
+MhaBufs mha_carve(float *w, int B, int T, int D, int NH, int rope, size_t *floats) {
   Carve cv(w);
-  MhaWork m{};
+  MhaBufs m{};
   const size_t rows = (size_t)B * T;
   m.Q = cv.take(3 * rows * D);
   m.K = m.Q ? m.Q + rows * D : nullptr;
@@ -264,38 +260,42 @@ MhaWork mha_carve(float *w, int B, int T, int D, int NH, int rope) {
   m.GV = m.GK ? m.GK + rows * D : nullptr;
   m.S = cv.take((size_t)B * D);
   m.S3 = cv.take(3 * (size_t)B * D);
+  m.s3_stride = (int64_t)B * D;
   const size_t half = (size_t)std::max(D / std::max(NH, 1) / 2, 1);
   m.rcos = rope ? cv.take((size_t)T * half) : nullptr;
   m.rsin = rope ? cv.take((size_t)T * half) : nullptr;
   m.SC = attn_supported(T, D, NH) ? nullptr : cv.take(attn_gemm_floats(B, T, NH));
-  m.floats = cv.off;
+  if (floats) *floats = cv.off;
   return m;
 }
 int mha_check(gn_ctx *c, int B, int T, int D, int NH) {
   if (B <= 0 || T <= 0 || D <= 0 || NH <= 0 || D % NH) return set_err(c, GN_ERR_INVALID, "bad MHA sizes");
-  if ((int64_t)B * NH > 65535) return set_err(c, GN_ERR_UNSUPPORTED, "batch x heads above 65535");
   return GN_OK;
 }
 }  // namespace
 
-extern "C" int gn_mha_workspace(int32_t B, int32_t T, int32_t D, int32_t heads, int32_t use_rope,
-                                int64_t *floats) {
-  if (!floats || B <= 0 || T <= 0 || D <= 0 || heads <= 0) return GN_ERR_INVALID;
-  *floats = (int64_t)mha_carve(nullptr, B, T, D, heads, use_rope).floats;
-  return GN_OK;
+// applyRoPE's angles (transformer.go:215-221) in float32, as the reference
+void rope_tables(int T, int hd, std::vector<float> &cs, std::vector<float> &sn) {
+  const int half = hd / 2;
+  cs.assign((size_t)T * std::max(half, 1), 0.f);
+  sn.assign(cs.size(), 0.f);
+  for (int t = 0; t < T; ++t)
+    for (int k = 0; k < half; ++k) {
+      const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
+      const float mt = (float)t * theta;
+      cs[(size_t)t * half + k] = (float)cos((double)mt);
+      sn[(size_t)t * half + k] = (float)sin((double)mt);
+    }
 }
 
-extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
-                              int32_t B, int32_t T, int32_t D, int32_t heads, int32_t causal,
-                              int32_t use_rope) {
-  ENTRY(c);
-  int rc = mha_check(c, B, T, D, heads);
-  if (rc) return rc;
-  if (!x || !params || !out || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
-  MhaWork m = mha_carve(work, B, T, D, heads, use_rope);
-  const int rows = B * T, hd = D / heads;
+// The MultiHeadAttention forward over B samples (transformer.go:405-527):
+// Q, K, V projections in one batched GEMM (their weights, biases and output
+// buffers equally spaced), RoPE, attention, out = wOut(attention).
+int mha_forward_impl(gn_ctx *c, const float *x, const float *params, float *out, const MhaBufs &m,
+                     int B, int T, int D, int NH, int causal, int rope) {
+  const int rows = B * T, hd = D / NH;
   const int64_t nd = (int64_t)D * D + D;
-  {  // Q, K, V in one batched launch (weights, biases and outputs equally spaced)
+  {
     GemmArgs a{};
     a.M = rows; a.N = D; a.K = D;
     a.A = x; a.lda = D; a.B = params; a.ldb = D;
@@ -304,33 +304,21 @@ extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, fl
     a.nbatch = 3;
     a.bstride_B = nd;
     a.bstride_bias = nd;
-    a.bstride_C = (int64_t)rows * D;
+    a.bstride_C = m.K - m.Q;
     KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
     HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream));
   }
-  if (use_rope) {  // applyRoPE's angles (transformer.go:215-221), float32 as the reference
-    const int half = hd / 2;
-    std::vector<float> cs((size_t)T * std::max(half, 1)), sn(cs.size());
-    for (int t = 0; t < T; ++t)
-      for (int k = 0; k < half; ++k) {
-        const float theta = (float)pow(10000.0, -(double)(2 * k) / (double)hd);
-        const float mt = (float)t * theta;
-        cs[(size_t)t * half + k] = (float)cos((double)mt);
-        sn[(size_t)t * half + k] = (float)sin((double)mt);
-      }
-    HIP_OK(c, hipMemcpyAsync(m.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
-    HIP_OK(c, hipMemcpyAsync(m.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
-    HIP_OK(c, hipStreamSynchronize(c->stream));  // the host tables go out of scope
+  if (rope) {
     KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
-    HIP_OK(c, launch_rope(m.Q, m.rcos, m.rsin, rows, T, heads, hd, 0, c->stream));
-    HIP_OK(c, launch_rope(m.K, m.rcos, m.rsin, rows, T, heads, hd, 0, c->stream));
+    HIP_OK(c, launch_rope(m.Q, m.rcos, m.rsin, rows, T, NH, hd, 0, c->stream));
+    HIP_OK(c, launch_rope(m.K, m.rcos, m.rsin, rows, T, NH, hd, 0, c->stream));
   }
   {
-    KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, T, heads, hd, causal, false));
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_fwd", attn_flops(B, T, NH, hd, causal, false));
     if (m.SC)
-      HIP_OK(c, launch_attn_fwd_gemm(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, m.SC, c->stream));
+      HIP_OK(c, launch_attn_fwd_gemm(m.Q, m.K, m.V, m.O, B, T, D, NH, causal, m.SC, c->stream));
     else
-      HIP_OK(c, launch_attn_fwd(m.Q, m.K, m.V, m.O, B, T, D, heads, causal, c->stream));
+      HIP_OK(c, launch_attn_fwd(m.Q, m.K, m.V, m.O, B, T, D, NH, causal, c->stream));
   }
   GemmArgs o{};
   o.M = rows; o.N = D; o.K = D;
@@ -342,87 +330,72 @@ extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, fl
   return GN_OK;
 }
 
-extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
-                               float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t D,
-                               int32_t heads, int32_t causal, int32_t use_rope, float scale) {
-  ENTRY(c);
-  int rc = mha_check(c, B, T, D, heads);
-  if (rc) return rc;
-  if (!x || !params || !gout || !grads || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
-  MhaWork m = mha_carve(work, B, T, D, heads, use_rope);
-  const int rows = B * T, hd = D / heads;
+// The MultiHeadAttention backward (transformer.go:557-690): wOut, the
+// attention, the conjugate rotation, then wQ, wK, wV, each a per-token Linear
+// Dense whose weight gradient uses the last token's input (Q10) and whose
+// bias gradient sums every token: both from the per-sample token sums, one
+// launch per Linear (three for Q, K, V together).  gin (may be null) = gQ Wq
+// + gK Wk + gV Wv.
+int mha_backward_impl(gn_ctx *c, const float *x, const float *params, const float *gout, float *grads,
+                      float *gin, const MhaBufs &m, int B, int T, int D, int NH, int causal, int rope,
+                      float scale) {
+  const int rows = B * T, hd = D / NH;
   const int64_t nd = (int64_t)D * D + D;
-  const float *Wo = params + 3 * nd;
   float *G = grads;
   float *cs = c->scratch;
   const size_t cap = c->scratch_floats;
-  // wOut, a per-token Linear Dense: its bias gradient sums every token, which
-  // are the per-sample token sums its Q10 weight gradient uses too
   {
     KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
     HIP_OK(c, launch_token_sum(gout, m.S, B, T, D, c->stream));
   }
   {
-    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * D + D));
-    HIP_OK(c, launch_colsum(m.S, B, D, D, scale, G + 3 * nd + (int64_t)D * D, cs, cap, c->stream));
-  }
-  {
-    GemmArgs a{};  // dWo = scale * S^T O_last
-    a.M = D; a.N = D; a.K = B;
-    a.A = m.S; a.lda = D;
-    a.B = m.O + (int64_t)(T - 1) * D; a.ldb = T * D;
-    a.C = G + 3 * nd; a.ldc = D; a.alpha = scale;
-    a.ws = cs; a.ws_cap = cap;
-    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
-    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+    TokDwSet set{};  // dWo = scale S^T O_last, dbo = scale colsum(S)
+    set.S[0] = m.S;
+    set.X[0] = m.O + (int64_t)(T - 1) * D;
+    set.dW[0] = G + 3 * nd;
+    set.db[0] = G + 3 * nd + (int64_t)D * D;
+    KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", f4(2.0 * B * D + (double)D * D + D));
+    HIP_OK(c, launch_tok_dw(set, 1, B, D, D, D, T * D, scale, c->stream));
   }
   {
     GemmArgs a{};  // GO = gout Wo
     a.M = rows; a.N = D; a.K = D;
-    a.A = gout; a.lda = D; a.B = Wo; a.ldb = D;
+    a.A = gout; a.lda = D; a.B = params + 3 * nd; a.ldb = D;
     a.C = m.GO; a.ldc = D; a.alpha = 1.f;
     a.ws = cs; a.ws_cap = cap;
     KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
     HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
   }
   {
-    KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, heads, hd, causal, true));
+    KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, NH, hd, causal, true));
     if (m.SC)
-      HIP_OK(c, launch_attn_bwd_gemm(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, m.SC,
+      HIP_OK(c, launch_attn_bwd_gemm(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, NH, causal, m.SC,
                                      c->stream));
     else
-      HIP_OK(c, launch_attn_bwd(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, heads, causal, c->stream));
+      HIP_OK(c, launch_attn_bwd(m.Q, m.K, m.V, m.GO, m.GQ, m.GK, m.GV, B, T, D, NH, causal, c->stream));
   }
-  if (use_rope) {  // transformer.go:660-664: the conjugate rotation before wQ / wK
+  if (rope) {  // transformer.go:660-664: the conjugate rotation before wQ / wK
     KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
-    HIP_OK(c, launch_rope(m.GQ, m.rcos, m.rsin, rows, T, heads, hd, 1, c->stream));
-    HIP_OK(c, launch_rope(m.GK, m.rcos, m.rsin, rows, T, heads, hd, 1, c->stream));
+    HIP_OK(c, launch_rope(m.GQ, m.rcos, m.rsin, rows, T, NH, hd, 1, c->stream));
+    HIP_OK(c, launch_rope(m.GK, m.rcos, m.rsin, rows, T, NH, hd, 1, c->stream));
   }
-  const int64_t sst = (int64_t)B * D;
+  const int64_t sst = m.s3_stride;
   {
     KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D));
-    HIP_OK(c, launch_token_sum_multi(m.GQ, m.S3, B, T, D, 3, (int64_t)rows * D, sst, c->stream));
+    HIP_OK(c, launch_token_sum_multi(m.GQ, m.S3, B, T, D, 3, m.GK - m.GQ, sst, c->stream));
   }
   {
-    const float *src[3] = {m.S3, m.S3 + sst, m.S3 + 2 * sst};
-    float *dst[3] = {G + (int64_t)D * D, G + nd + (int64_t)D * D, G + 2 * nd + (int64_t)D * D};
-    KTimer kt(c, GN_KCLASS_OTHER, "colsum", 3 * f4((double)B * D + D));
-    HIP_OK(c, launch_colsum_multi(src, dst, 3, B, D, D, scale, cs, cap, c->stream));
+    TokDwSet set{};
+    for (int z = 0; z < 3; ++z) {
+      set.S[z] = m.S3 + z * sst;
+      set.X[z] = x + (int64_t)(T - 1) * D;
+      set.dW[z] = G + z * nd;
+      set.db[z] = G + z * nd + (int64_t)D * D;
+    }
+    KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", 3 * f4(2.0 * B * D + (double)D * D + D));
+    HIP_OK(c, launch_tok_dw(set, 3, B, D, D, D, T * D, scale, c->stream));
   }
-  {
-    GemmArgs a{};  // dWq, dWk, dWv = scale * S3_m^T x_last in one launch
-    a.M = D; a.N = D; a.K = B;
-    a.A = m.S3; a.lda = D;
-    a.B = x + (int64_t)(T - 1) * D; a.ldb = T * D;
-    a.C = G; a.ldc = D; a.alpha = scale;
-    a.ws = cs; a.ws_cap = cap;
-    a.nbatch = 3;
-    a.bstride_A = sst;
-    a.bstride_C = nd;
-    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a));
-    HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
-  }
-  if (gin) {  // gin = gQ Wq + gK Wk + gV Wv
+  if (gin) {
     const float *gq[3] = {m.GQ, m.GK, m.GV};
     for (int i = 0; i < 3; ++i) {
       GemmArgs a{};
@@ -438,6 +411,44 @@ extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, c
   return GN_OK;
 }
 
+extern "C" int gn_mha_workspace(int32_t B, int32_t T, int32_t D, int32_t heads, int32_t use_rope,
+                                int64_t *floats) {
+  if (!floats || B <= 0 || T <= 0 || D <= 0 || heads <= 0) return GN_ERR_INVALID;
+  size_t n = 0;
+  mha_carve(nullptr, B, T, D, heads, use_rope, &n);
+  *floats = (int64_t)n;
+  return GN_OK;
+}
+
+extern "C" int gn_mha_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
+                              int32_t B, int32_t T, int32_t D, int32_t heads, int32_t causal,
+                              int32_t use_rope) {
+  ENTRY(c);
+  int rc = mha_check(c, B, T, D, heads);
+  if (rc) return rc;
+  if (!x || !params || !out || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MhaBufs m = mha_carve(work, B, T, D, heads, use_rope, nullptr);
+  if (use_rope) {
+    std::vector<float> cs, sn;
+    rope_tables(T, D / heads, cs, sn);
+    HIP_OK(c, hipMemcpyAsync(m.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIP_OK(c, hipMemcpyAsync(m.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIP_OK(c, hipStreamSynchronize(c->stream));  // the host tables go out of scope
+  }
+  return mha_forward_impl(c, x, params, out, m, B, T, D, heads, causal, use_rope);
+}
+
+extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                               float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t D,
+                               int32_t heads, int32_t causal, int32_t use_rope, float scale) {
+  ENTRY(c);
+  int rc = mha_check(c, B, T, D, heads);
+  if (rc) return rc;
+  if (!x || !params || !gout || !grads || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MhaBufs m = mha_carve(work, B, T, D, heads, use_rope, nullptr);
+  return mha_backward_impl(c, x, params, gout, grads, gin, m, B, T, D, heads, causal, use_rope, scale);
+}
+
 // ---------------------------------------------------------------------------
 // SequenceUnroller(LSTM) (unroller.go:57-213, lstm.go:144-751) over a batch:
 // x is B x T x I, params = [Wx (4H x I) | Wh (4H x H) | b (4H)], gates i, f,
@@ -447,7 +458,8 @@ extern "C" int gn_mha_backward(gn_ctx *c, const float *x, const float *params, c
 // clipped to norm 1 after every step (Q14, `workers` chains of ceil(B /
 // workers) samples, evaluated exactly through the chain's Gram matrix).  The
 // input gradient (gin, B x T x I) uses the unclipped deltas, as the
-// reference's dx does.  work holds what the forward saves (gn_lstm_workspace
+// reference's dx does.  With return_sequences, out and gout are B x T x H,
+// every step's h (unroller.go:85-127, 158-188).  work holds what the forward saves (gn_lstm_workspace
 // floats for the same B, T, I, H, workers).
 // ---------------------------------------------------------------------------
 namespace {
@@ -489,7 +501,8 @@ extern "C" int gn_lstm_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int
 }
 
 extern "C" int gn_lstm_seq_forward(gn_ctx *c, const float *x, const float *params, float *out,
-                                   float *work, int32_t B, int32_t T, int32_t I, int32_t H) {
+                                   float *work, int32_t B, int32_t T, int32_t I, int32_t H,
+                                   int32_t return_sequences) {
   ENTRY(c);
   if (!x || !params || !out || !work || B <= 0 || T <= 0 || I <= 0 || H <= 0 || H > 1024)
     return set_err(c, GN_ERR_INVALID, "bad LSTM args (hidden <= 1024)");
@@ -509,13 +522,15 @@ extern "C" int gn_lstm_seq_forward(gn_ctx *c, const float *x, const float *param
     HIP_OK(c, launch_transpose(Wh, m.WhT, H, H, c->stream));
   }
   KTimer kt(c, GN_KCLASS_OTHER, "lstm_fwd", 2.0 * H * H * B * T);
-  HIP_OK(c, launch_lstm_fwd(m.xw, m.WhT, bias, m.igb, m.tcb, m.cbuf, m.hbuf, out, B, T, H, c->stream));
+  HIP_OK(c, launch_lstm_fwd(m.xw, m.WhT, bias, m.igb, m.tcb, m.cbuf, m.hbuf, out, B, T, H, c->stream,
+                            return_sequences ? 1 : 0));
   return GN_OK;
 }
 
 extern "C" int gn_lstm_seq_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
                                     float *grads, float *gin, float *work, int32_t B, int32_t T,
-                                    int32_t I, int32_t H, int32_t workers, float scale) {
+                                    int32_t I, int32_t H, int32_t workers, float scale,
+                                    int32_t return_sequences) {
   ENTRY(c);
   if (!x || !params || !gout || !grads || !work || B <= 0 || T <= 0 || I <= 0 || H <= 0 || H > 1024)
     return set_err(c, GN_ERR_INVALID, "bad LSTM args (hidden <= 1024)");
@@ -527,7 +542,8 @@ extern "C" int gn_lstm_seq_backward(gn_ctx *c, const float *x, const float *para
   float *gWx = grads, *gWh = gWx + (int64_t)G4 * I, *gb = gWh + (int64_t)G4 * H;
   {
     KTimer kt(c, GN_KCLASS_OTHER, "lstm_bptt", 2.0 * G4 * H * B * T);
-    HIP_OK(c, launch_lstm_bwd(gout, m.igb, m.tcb, m.cbuf, Wh, bias, m.Dg, B, T, H, c->stream));
+    HIP_OK(c, launch_lstm_bwd(gout, m.igb, m.tcb, m.cbuf, Wh, bias, m.Dg, B, T, H, c->stream,
+                              return_sequences ? 1 : 0));
   }
   if (gin) {  // dx_t = Wx^T dG_t for every sample and step, before the clip weights touch dG
     GemmArgs a{};
@@ -606,9 +622,10 @@ extern "C" int gn_embedding_backward(gn_ctx *c, const float *gout, const int32_t
   const int Wc = std::max(1, std::min(workers, B)), chunk = (B + Wc - 1) / Wc;
   const int nch = (B + chunk - 1) / chunk;
   KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)V * D + 2.0 * nch * T * D));
-  const hipError_t e = launch_embed_grad(gout, ids, gradE, V, B, T, D, workers, scale, bad, c->stream);
-  if (e == hipErrorInvalidValue)
-    return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed 2048", nch * T);
-  HIP_OK(c, e);
+  if ((size_t)2 * nch * T > c->scratch_floats)
+    return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed the scratch",
+                   nch * T);
+  HIP_OK(c, launch_embed_grad(gout, ids, gradE, V, B, T, D, workers, scale, bad, c->stream, c->scratch,
+                              c->scratch_floats));
   return GN_OK;
 }

@@ -887,6 +887,31 @@ static int alloc_batch(gn_model *M) {
       if ((rc = model_balloc(M, (size_t)max_batch * (R.in_len / R.D), &R.rmsv))) return rc;
       if ((rc = model_balloc(M, (size_t)max_batch * R.in_len, &R.gx))) return rc;
     }
+    if (R.d.kind == GN_LAYER_LAYERNORM) {
+      // per-row (mean, std); g * xhat for the gamma sums when the one-pass
+      // backward does not fit the scratch; an input-gradient sink when the
+      // layer is first (the backward kernels always write dx)
+      if ((rc = model_balloc(M, (size_t)max_batch * (R.in_len / R.D) * 2, &R.rmsv))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * R.in_len, &R.gx))) return rc;
+      if (i == 0 && (rc = model_balloc(M, (size_t)max_batch * R.in_len, &R.zbuf))) return rc;
+    }
+    if (R.d.kind == GN_LAYER_MHA) {
+      const size_t rows = (size_t)max_batch * R.T, D = R.D;
+      LayerRT::Tb &t = R.tb;
+      if ((rc = model_balloc(M, 3 * rows * D, &t.Q))) return rc;
+      t.K = t.Q + rows * D;
+      t.V = t.K + rows * D;
+      if ((rc = model_balloc(M, 3 * rows * D, &t.GQ))) return rc;
+      t.GK = t.GQ + rows * D;
+      t.GV = t.GK + rows * D;
+      if ((rc = model_balloc(M, rows * D, &t.O))) return rc;
+      if ((rc = model_balloc(M, rows * D, &t.GO))) return rc;
+      if ((rc = model_balloc(M, (size_t)max_batch * D, &t.S))) return rc;
+      if ((rc = model_balloc(M, 3 * (size_t)max_batch * D, &t.S3))) return rc;
+      if (!attn_supported(R.T, R.D, R.NH) &&
+          (rc = model_balloc(M, attn_gemm_floats(max_batch, R.T, R.NH), &t.SC)))
+        return rc;
+    }
     if (R.d.kind == GN_LAYER_MAXPOOL2D) {
       float *am = nullptr;
       if ((rc = model_balloc(M, (size_t)max_batch * R.out_len, &am))) return rc;
@@ -952,8 +977,6 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         if (R.d.out_size <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: Dense out <= 0", i);
         if (plan_act(R.d.act, R.d.act_is_ptr, R.ap))
           return set_err(c, GN_ERR_INVALID, "layer %d: activation %d not supported", i, R.d.act);
-        if (R.ap.jac && i != nlayers - 1)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: Softmax/LogSoftmax only on the output layer", i);
         R.pcount = (int64_t)R.d.in_size * R.d.out_size + R.d.out_size;
         R.out_len = R.d.out_size;
         break;
@@ -1012,10 +1035,9 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         R.T = len;  // tokens per sample
         if (R.V <= 0 || R.D <= 0) return set_err(c, GN_ERR_INVALID, "layer %d: bad Embedding", i);
         // below another layer it reads floor() of that layer's outputs as ids
-        // and hands it a zero gradient (embedding.go:156-163)
-        if (M->emb >= 0)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: a second Embedding layer is not built", i);
-        M->emb = i;
+        // and hands it a zero gradient (embedding.go:156-163); the first
+        // Embedding's per-sample index-error flags cover every Embedding
+        if (M->emb < 0) M->emb = i;
         R.pcount = (int64_t)R.V * R.D;
         R.out_len = R.T * R.D;
         break;
@@ -1037,8 +1059,6 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
           return set_err(c, GN_ERR_SHAPE, "layer %d: TransformerBlock %dx%d != input %d", i, R.T, R.D, len);
         if (R.NH <= 0 || R.D % R.NH)
           return set_err(c, GN_ERR_SHAPE, "layer %d: dim %d is not a multiple of %d heads", i, R.D, R.NH);
-        if ((int64_t)max_batch * R.NH > 65535)
-          return set_err(c, GN_ERR_UNSUPPORTED, "layer %d: batch x heads above 65535", i);
         if (R.d.block_act < GN_BLOCK_ACT_RELU || R.d.block_act > GN_BLOCK_ACT_GELU ||
             R.d.block_norm < GN_BLOCK_NORM_LN || R.d.block_norm > GN_BLOCK_NORM_RMS)
           return set_err(c, GN_ERR_INVALID, "layer %d: unknown TransformerBlock act %d / norm %d", i,
@@ -1052,6 +1072,36 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
         if (R.T <= 0 || R.D <= 0 || R.T * R.D != len)
           return set_err(c, GN_ERR_SHAPE, "layer %d: CLSPooling %dx%d != input %d", i, R.T, R.D, len);
         R.out_len = R.D;
+        break;
+      case GN_LAYER_GAP1D:  // transformer.go:1524-1600: mean over the seq_len rows of dim
+        R.T = R.d.seq_len;
+        R.D = R.d.dim;
+        if (R.T <= 0 || R.D <= 0 || R.T * R.D != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: GlobalAveragePooling1D %dx%d != input %d", i, R.T,
+                         R.D, len);
+        R.out_len = R.D;
+        break;
+      case GN_LAYER_MHA:  // transformer.go:318-394: dim = input / seq_len when not given
+        R.T = R.d.seq_len;
+        R.D = R.d.dim > 0 ? R.d.dim : (R.T > 0 ? len / R.T : 0);
+        R.NH = R.d.num_heads;
+        R.causal = R.d.causal;
+        if (R.T <= 0 || R.D <= 0 || R.T * R.D != len)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: MultiHeadAttention %dx%d != input %d", i, R.T, R.D, len);
+        if (R.NH <= 0 || R.D % R.NH)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: dim %d is not a multiple of %d heads", i, R.D, R.NH);
+        R.pcount = 4 * ((int64_t)R.D * R.D + R.D);
+        R.out_len = len;
+        break;
+      case GN_LAYER_LAYERNORM:  // layernorm.go:193-304: rows of normalizedShape
+        R.D = R.d.dim;
+        if (R.D <= 0 || len % R.D)
+          return set_err(c, GN_ERR_SHAPE, "layer %d: LayerNorm normalizedShape %d does not divide input %d",
+                         i, R.D, len);
+        if (!(R.d.eps >= 0)) return set_err(c, GN_ERR_INVALID, "layer %d: LayerNorm eps < 0", i);
+        R.eps = R.d.eps > 0 ? R.d.eps : 1e-5f;  // the facade's eps (goneuron.go:220-227)
+        R.pcount = 2 * (int64_t)R.D;               // [gamma | beta] (layernorm.go:83-118)
+        R.out_len = len;
         break;
       case GN_LAYER_RMSNORM:  // rmsnorm.go:222-240: rows of normalizedShape
         R.D = R.d.dim;
@@ -1209,6 +1259,21 @@ extern "C" int gn_model_create(gn_ctx *c, const gn_layer_desc *layers, int32_t n
     if (R.d.kind == GN_LAYER_SWIGLU) init_swiglu(host.data() + R.poff, R.d.in_size, R.d.out_size);
     if (R.d.kind == GN_LAYER_RMSNORM)
       std::fill(host.begin() + R.poff, host.begin() + R.poff + R.D, 1.0f);  // rmsnorm.go:80-82
+    if (R.d.kind == GN_LAYER_LAYERNORM)  // gamma 1, beta 0 (layernorm.go:83-118)
+      std::fill(host.begin() + R.poff, host.begin() + R.poff + R.D, 1.0f);
+    if (R.d.kind == GN_LAYER_MHA && R.d.use_rope) {
+      // parameters stay 0 (Build rebinds wQ, wK, wV, wOut to a fresh zero
+      // buffer, transformer.go:367-379); the rotary angles once
+      std::vector<float> cs, sn;
+      rope_tables(R.T, R.D / R.NH, cs, sn);
+      if ((rc = model_alloc(M.get(), cs.size(), &R.tb.rcos))) return rc;
+      if ((rc = model_alloc(M.get(), sn.size(), &R.tb.rsin))) return rc;
+      HIP_OK(c, hipMemcpyAsync(R.tb.rcos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+      HIP_OK(c, hipMemcpyAsync(R.tb.rsin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice,
+                               c->stream));
+      HIP_OK(c, hipStreamSynchronize(c->stream));  // the host tables go out of scope
+    }
     if (R.d.kind == GN_LAYER_DROPOUT) {
       // Q9: Dropout.Reset reseeds RNG(42) before every sample (dropout.go:399-401),
       // so one mask of the first `size` draws serves every sample and step.
@@ -1393,6 +1458,13 @@ static int pass_flags(gn_model *M, int B, bool train) {
     M->eff[i] = f;
   }
   return GN_OK;
+}
+
+// A standalone MultiHeadAttention's buffers, sized for the model's max batch
+static MhaBufs mha_bufs(const gn_model *M, const LayerRT &R) {
+  const LayerRT::Tb &t = R.tb;
+  return MhaBufs{t.Q, t.K, t.V, t.O, t.GO, t.GQ, t.GK, t.GV, t.S, t.S3, t.rcos, t.rsin, t.SC,
+                 (int64_t)M->maxB * R.D};
 }
 
 // ---------------------------------------------------------------------------
@@ -1707,15 +1779,17 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         if (R.ap.jac || (last && for_loss)) fwd = F_IDENTITY;  // row kernel finishes it
         // a Dropout above in training mode: its output from the GEMM's split-K
         // reduction (dropout.go:85-130 per element, the same expression)
-        LayerRT *dr = !last && M->L[i + 1].d.kind == GN_LAYER_DROPOUT && M->eff[i + 1] &&
+        LayerRT *dr = !last && !R.ap.jac && M->L[i + 1].d.kind == GN_LAYER_DROPOUT && M->eff[i + 1] &&
                               M->L[i + 1].out_len == R.out_len
                           ? &M->L[i + 1]
                           : nullptr;
         HIP_OK(c, dense_fwd(c, cur, W, b, R.out, B, R.d.in_size, R.d.out_size, fwd,
                             dr ? dr->out : nullptr, dr ? dr->mask : nullptr, dr ? dr->scale : 0.f));
         drop_done = dr != nullptr;
-        if (last && !for_loss && R.ap.jac)
+        if (R.ap.jac && !(last && for_loss)) {  // the loss kernel finishes the output layer's rows
+          KTimer kt(c, GN_KCLASS_OTHER, "row_act", f4(2.0 * B * R.out_len));
           HIP_OK(c, launch_row_act(R.out, B, R.out_len, R.ap.row_act, c->stream));
+        }
         break;
       }
       case GN_LAYER_DROPOUT:
@@ -1755,13 +1829,13 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
           KTimer kt(c, GN_KCLASS_OTHER, "embed_pe_fwd",
                     f4(2.0 * B * R.T + 3.0 * B * R.T * R.D + (double)R.T * R.D));
           HIP_OK(c, launch_embed_pe(cur, M->params + R.poff, M->params + pe->poff, R.ids, R.out, pe->out, B,
-                                    R.T, R.V, R.D, R.bad, c->stream));
+                                    R.T, R.V, R.D, M->L[M->emb].bad, c->stream, i != M->emb));
           pe_done = true;
           break;
         }
         KTimer kt(c, GN_KCLASS_OTHER, "embed_fwd", f4(2.0 * B * R.T + 2.0 * B * R.T * R.D));
-        HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B, R.T, R.V, R.D, R.bad,
-                               c->stream));
+        HIP_OK(c, launch_embed(cur, M->params + R.poff, R.ids, R.out, B, R.T, R.V, R.D, M->L[M->emb].bad,
+                               c->stream, i != M->emb));
         break;
       }
       case GN_LAYER_POSENC: {
@@ -1781,6 +1855,24 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_TRANSFORMER: {
         int r = tb_forward(M, R, cur, B);
         if (r) return r;
+        break;
+      }
+      case GN_LAYER_MHA: {
+        int r = mha_forward_impl(c, cur, M->params + R.poff, R.out, mha_bufs(M, R), B, R.T, R.D, R.NH,
+                                 R.causal, R.d.use_rope);
+        if (r) return r;
+        break;
+      }
+      case GN_LAYER_LAYERNORM: {
+        const int rows = B * (R.in_len / R.D);
+        KTimer kt(c, GN_KCLASS_OTHER, "ln_fwd", f4(2.0 * rows * R.D + 2.0 * rows));
+        HIP_OK(c, launch_ln_fwd(cur, M->params + R.poff, M->params + R.poff + R.D, R.out, R.rmsv, rows, R.D,
+                                R.eps, c->stream));
+        break;
+      }
+      case GN_LAYER_GAP1D: {
+        KTimer kt(c, GN_KCLASS_OTHER, "gap1d_fwd", f4((double)B * R.T * R.D + (double)B * R.D));
+        HIP_OK(c, launch_gap1d_fwd(cur, R.out, B, R.T, R.D, c->stream));
         break;
       }
       case GN_LAYER_SWIGLU: {
@@ -1947,7 +2039,10 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         float *gW = M->grads + R.poff;
         float *gB = gW + (int64_t)R.d.in_size * R.d.out_size;
         float *dz = R.gout;
-        if (!is_dz) {  // read the gradient and the saved output, write dz
+        if (!is_dz && R.ap.jac) {  // a hidden Softmax / LogSoftmax: the row Jacobian (layer.go:504-560)
+          KTimer kt(c, GN_KCLASS_OTHER, "row_jac", f4(3.0 * B * R.out_len));
+          HIP_OK(c, launch_row_jac(R.gout, R.out, dz, B, R.out_len, R.ap.row_act, c->stream));
+        } else if (!is_dz) {  // read the gradient and the saved output, write dz
           KTimer kt(c, GN_KCLASS_OTHER, "dact", f4(3.0 * B * R.out_len));
           HIP_OK(c, launch_dact(R.gout, R.out, dz, (int64_t)B * R.out_len, R.ap.deriv, c->stream));
         }
@@ -2051,6 +2146,49 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         is_dz = false;
         break;
       }
+      case GN_LAYER_MHA: {
+        int r = mha_backward_impl(c, in, M->params + R.poff, R.gout, M->grads + R.poff,
+                                  below ? below->gout : nullptr, mha_bufs(M, R), B, R.T, R.D, R.NH, R.causal,
+                                  R.d.use_rope, scale);
+        if (r) return r;
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_LAYERNORM: {  // layernorm.go:334-441 (Q18), gamma / beta sums over the rows
+        const int rows = B * (R.in_len / R.D), N = R.D;
+        const float *gam = M->params + R.poff;
+        float *dg = M->grads + R.poff, *db = dg + N;
+        float *dx = below && below->gout ? below->gout : R.zbuf;
+        hipError_t e;
+        {
+          KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd", f4(3.0 * rows * N + 2.0 * rows + 2.0 * N));
+          e = launch_ln_bwd_params(R.gout, in, gam, R.rmsv, dx, dg, db, rows, N, scale, c->scratch,
+                                   c->scratch_floats, c->stream);
+        }
+        if (e == hipErrorNotSupported) {  // partials beyond the scratch: g * xhat, then column sums
+          (void)hipGetLastError();
+          {
+            KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd", f4(4.0 * rows * N + 2.0 * rows));
+            HIP_OK(c, launch_ln_bwd(R.gout, in, gam, R.rmsv, dx, R.gx, rows, N, c->stream));
+          }
+          const float *src[2] = {R.gx, R.gout};
+          float *dst[2] = {dg, db};
+          KTimer kt(c, GN_KCLASS_OTHER, "colsum", 2 * f4((double)rows * N + N));
+          HIP_OK(c, launch_colsum_multi(src, dst, 2, rows, N, N, scale, c->scratch, c->scratch_floats,
+                                        c->stream));
+        } else {
+          HIP_OK(c, e);
+        }
+        is_dz = false;
+        break;
+      }
+      case GN_LAYER_GAP1D:
+        if (below && below->gout) {
+          KTimer kt(c, GN_KCLASS_OTHER, "gap1d_bwd", f4((double)B * R.D + (double)B * R.T * R.D));
+          HIP_OK(c, launch_gap1d_bwd(R.gout, below->gout, B, R.T, R.D, c->stream));
+        }
+        is_dz = false;
+        break;
       case GN_LAYER_SWIGLU: {  // swiglu.go:196-232
         {
           KTimer kt(c, GN_KCLASS_OTHER, "swiglu_bwd", f4(5.0 * B * R.d.out_size));
@@ -2199,8 +2337,11 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const int Wc = std::max(1, std::min(M->workers, B));
         const int nch = (B + (B + Wc - 1) / Wc - 1) / ((B + Wc - 1) / Wc);
         KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)R.V * R.D + 2.0 * nch * R.T * R.D));
+        if ((size_t)2 * nch * R.T > c->scratch_floats)
+          return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed the scratch",
+                         nch * R.T);
         HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
-                                    scale, R.bad, c->stream));
+                                    scale, M->L[M->emb].bad, c->stream, c->scratch, c->scratch_floats));
         if (below && below->gout)  // indices carry no gradient (embedding.go:156-163)
           HIP_OK(c, launch_fill(below->gout, 0.0f, (int64_t)B * R.T, c->stream));
         is_dz = false;

@@ -16,6 +16,8 @@
 //    std^3 in the last term);
 //  - Embedding.Backward zeroes the whole gradient before scattering, so only
 //    the last sample of each worker chunk contributes (embedding.go:152-154).
+#include <algorithm>
+
 #include "gn_common.h"
 
 namespace gn {
@@ -42,13 +44,14 @@ __device__ __forceinline__ float wmax(float v) {
 // blockIdx.y is sample b.  An index outside [0, V) makes Embedding.Forward
 // return an error (embedding.go:126-128), and the batch loop then skips the
 // sample (net.go:738-741, 641-644): every block of the sample checks its T ids
-// and block 0 records bad[b]; such a sample's rows read E[0] and are masked
-// out downstream.
+// and block 0 records bad[b] (with bad_or, a later Embedding of the network,
+// only sets it, so the flag covers every Embedding); such a sample's rows
+// read E[0] and are masked out downstream.
 __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ x,
                                                     const float *__restrict__ E,
                                                     int32_t *__restrict__ ids,
                                                     float *__restrict__ out, int T, int V, int D,
-                                                    int32_t *__restrict__ bad) {
+                                                    int32_t *__restrict__ bad, int bad_or) {
   const int b = blockIdx.y;
   const float *xs = x + (int64_t)b * T;
   int any = 0;
@@ -57,7 +60,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ x,
     any |= (idx < 0 || idx >= V) ? 1 : 0;
   }
   any = __syncthreads_or(any);
-  if (bad && blockIdx.x == 0 && threadIdx.x == 0) bad[b] = any ? 1 : 0;
+  if (bad && blockIdx.x == 0 && threadIdx.x == 0 && (any || !bad_or)) bad[b] = any ? 1 : 0;
   const int64_t n = (int64_t)T * D;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(256) void embed_pe_kernel(const float *__restrict__
                                                        int32_t *__restrict__ ids,
                                                        float *__restrict__ out,
                                                        float *__restrict__ pe_out, int T, int V,
-                                                       int D, int32_t *__restrict__ bad) {
+                                                       int D, int32_t *__restrict__ bad, int bad_or) {
   const int b = blockIdx.y;
   const float *xs = x + (int64_t)b * T;
   int any = 0;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void embed_pe_kernel(const float *__restrict__
     any |= (idx < 0 || idx >= V) ? 1 : 0;
   }
   any = __syncthreads_or(any);
-  if (bad && blockIdx.x == 0 && threadIdx.x == 0) bad[b] = any ? 1 : 0;
+  if (bad && blockIdx.x == 0 && threadIdx.x == 0 && (any || !bad_or)) bad[b] = any ? 1 : 0;
   const int64_t n = (int64_t)T * D;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int t = (int)(e / D), d = (int)(e - (int64_t)t * D);
@@ -210,6 +213,101 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
       acc += g[((int64_t)csamp[e / T] * T + e % T) * D + d];
     }
     gradE[(int64_t)my * D + d] = acc * scale;
+  }
+}
+
+// More than EG_MAXL contributing rows: the same sums, with the contributing
+// sample of every chunk and the id of every row in a global list that
+// embed_grad_prep writes first, and each block's matching rows gathered into
+// LDS EG_MAXL at a time (the running sum is kept in gradE between batches, so
+// the additions keep their order).
+__global__ __launch_bounds__(256) void embed_grad_prep(const int32_t *__restrict__ ids, int B, int T,
+                                                       int chunk, int L, const int32_t *__restrict__ bad,
+                                                       int par, int *__restrict__ sid) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= L) return;
+  const int w = e / T, c0 = w * chunk, c1 = min(B, c0 + chunk);
+  int sm = c1 - 1;
+  if (bad) {
+    if (par) {
+      int f = c0;
+      while (f < c1 && !bad[f]) ++f;
+      sm = f - 1;
+    } else {
+      while (sm >= c0 && bad[sm]) --sm;
+    }
+    if (sm < c0) sm = -1;
+  }
+  sid[e] = sm < 0 ? -1 : ids[(int64_t)sm * T + e % T];
+  sid[L + e] = sm;  // the row's sample (-1: none)
+}
+
+__global__ __launch_bounds__(256) void embed_grad_global_kernel(const float *__restrict__ g,
+                                                                const int *__restrict__ sid,
+                                                                float *__restrict__ gradE, int T, int D,
+                                                                int L, float scale, int V) {
+  __shared__ int first;
+  __shared__ int hit[EG_ZR];
+  __shared__ int lst[EG_MAXL];
+  __shared__ int nl;
+  const int l = blockIdx.x;
+  const int *samp = sid + L;
+  if (l >= L) {  // zeroing block
+    const int z0 = (l - L) * EG_ZR, z1 = min(V, z0 + EG_ZR);
+    if (threadIdx.x < EG_ZR) hit[threadIdx.x] = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < L; e += 256) {
+      const int id = sid[e];
+      if (id >= z0 && id < z1) hit[id - z0] = 1;
+    }
+    __syncthreads();
+    float *base = gradE + (int64_t)z0 * D;
+    const int n = (z1 - z0) * D;
+    for (int e = threadIdx.x; e < n; e += 256)
+      if (!hit[e / D]) base[e] = 0.0f;
+    return;
+  }
+  const int my = sid[l];
+  if (my < 0) return;  // uniform over the block
+  if (threadIdx.x == 0) first = 1;
+  __syncthreads();
+  for (int e = threadIdx.x; e < l; e += 256)
+    if (sid[e] == my) first = 0;
+  __syncthreads();
+  if (!first) return;
+  float *row = gradE + (int64_t)my * D;
+  bool started = false;
+  for (int pos = l; pos < L;) {
+    // wave 0 lists the next matching rows (ascending, at most EG_MAXL - 64
+    // per batch so a ballot never overflows), every thread adds them
+    if (threadIdx.x < 64) {
+      int cnt = 0, base = pos;
+      for (; base < L && cnt <= EG_MAXL - 64; base += 64) {
+        const int e = base + threadIdx.x;
+        const bool m = e < L && sid[e] == my;
+        const unsigned long long mask = __ballot(m);
+        if (m) lst[cnt + __popcll(mask & ((1ull << threadIdx.x) - 1ull))] = e;
+        cnt += __popcll(mask);
+      }
+      if (threadIdx.x == 0) {
+        nl = cnt;
+        first = base;  // where the next batch starts
+      }
+    }
+    __syncthreads();
+    const int n = nl;
+    const int next = first;
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float acc = started ? row[d] : 0.f;
+      for (int j = 0; j < n; ++j) {
+        const int e = lst[j];
+        acc += g[((int64_t)samp[e] * T + e % T) * D + d];
+      }
+      row[d] = next >= L ? acc * scale : acc;
+    }
+    started = true;
+    pos = next;
+    __syncthreads();
   }
 }
 
@@ -860,20 +958,23 @@ static unsigned blocks_for(int64_t n) {
 }
 
 hipError_t launch_embed(const float *x, const float *E, int32_t *ids, float *out, int B, int T, int V,
-                        int D, int32_t *bad, hipStream_t s) {
+                        int D, int32_t *bad, hipStream_t s, bool bad_or) {
   if (B <= 0) return hipSuccess;
   const int64_t n = (int64_t)T * D;
   unsigned bx = (unsigned)std::min<int64_t>((n + 255) / 256, 64);
-  hipLaunchKernelGGL(embed_kernel, dim3(bx, B), dim3(256), 0, s, x, E, ids, out, T, V, D, bad);
+  hipLaunchKernelGGL(embed_kernel, dim3(bx, B), dim3(256), 0, s, x, E, ids, out, T, V, D, bad,
+                     bad_or ? 1 : 0);
   return hipGetLastError();
 }
 
 hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int32_t *ids, float *out,
-                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s) {
+                           float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s,
+                           bool bad_or) {
   if (B <= 0) return hipSuccess;
   const int64_t n = (int64_t)T * D;
   unsigned bx = (unsigned)std::min<int64_t>((n + 255) / 256, 64);
-  hipLaunchKernelGGL(embed_pe_kernel, dim3(bx, B), dim3(256), 0, s, x, E, pe, ids, out, pe_out, T, V, D, bad);
+  hipLaunchKernelGGL(embed_pe_kernel, dim3(bx, B), dim3(256), 0, s, x, E, pe, ids, out, pe_out, T, V, D, bad,
+                     bad_or ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -884,13 +985,23 @@ hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int
 }
 
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
-                             int D, int W, float scale, const int32_t *bad, hipStream_t s) {
+                             int D, int W, float scale, const int32_t *bad, hipStream_t s, float *ws,
+                             size_t ws_floats) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   const int chunk = (B + Wc - 1) / Wc;
   const int nsamp = (B + chunk - 1) / chunk;  // one contributing sample per chunk
   const int L = nsamp * T;
-  if (L > EG_MAXL) return hipErrorInvalidValue;
   const int zb = (V + EG_ZR - 1) / EG_ZR;
+  if (L > EG_MAXL) {
+    // the row lists in the caller's workspace: 2 L ints
+    if (!ws || ws_floats < (size_t)2 * L) return hipErrorInvalidValue;
+    int *sid = reinterpret_cast<int *>(ws);
+    hipLaunchKernelGGL(embed_grad_prep, dim3((L + 255) / 256), dim3(256), 0, s, ids, B, T, chunk, L, bad,
+                       W > 1 ? 1 : 0, sid);
+    hipLaunchKernelGGL(embed_grad_global_kernel, dim3(L + zb), dim3(256), 0, s, g, sid, gradE, T, D, L,
+                       scale, V);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
                      scale, bad, W > 1 ? 1 : 0, V);
   return hipGetLastError();
@@ -1076,7 +1187,21 @@ hipError_t pair_gemm(char ta, char tb, int M, int N, int K, HeadOp A, HeadOp Bm,
   const float *cp = nullptr;
   set(HeadOp{C, c_scores}, cp, a.ldc, a.bstride_C, a.istride_C);
   a.C = C;
-  return launch_gemm(ta, tb, EPI_SCALE, a, s);
+  // the batch index is the grid's z dimension (at most 65535): samples in
+  // chunks whose (sample, head) pairs fit it, each chunk's operands advanced
+  // by whole samples
+  const int per = std::max(1, 65535 / NH);
+  for (int b0 = 0; b0 < B; b0 += per) {
+    const int nb = std::min(per, B - b0);
+    GemmArgs c = a;
+    c.nbatch = nb * NH;
+    c.A = a.A + (int64_t)b0 * a.bstride_A;
+    c.B = a.B + (int64_t)b0 * a.bstride_B;
+    c.C = a.C + (int64_t)b0 * a.bstride_C;
+    const hipError_t e = launch_gemm(ta, tb, EPI_SCALE, c, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 hipError_t softmax_scores(float *S, int B, int T, int NH, int hd, int causal, hipStream_t s) {
   const int64_t rows = (int64_t)B * NH * T;
@@ -1088,7 +1213,6 @@ hipError_t softmax_scores(float *S, int B, int T, int NH, int hd, int causal, hi
 
 hipError_t launch_attn_fwd_gemm(const float *Q, const float *K, const float *V, float *O, int B, int T,
                                 int D, int NH, int causal, float *S, hipStream_t s) {
-  if ((int64_t)B * NH > 65535) return hipErrorInvalidConfiguration;  // grid z
   const int hd = D / NH;
   hipError_t e = pair_gemm('N', 'T', T, T, hd, {Q, false}, {K, false}, S, true, B, T, D, NH, s);
   if (e == hipSuccess) e = softmax_scores(S, B, T, NH, hd, causal, s);
@@ -1099,7 +1223,6 @@ hipError_t launch_attn_fwd_gemm(const float *Q, const float *K, const float *V, 
 hipError_t launch_attn_bwd_gemm(const float *Q, const float *K, const float *V, const float *GO,
                                 float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
                                 float *S, hipStream_t s) {
-  if ((int64_t)B * NH > 65535) return hipErrorInvalidConfiguration;
   const int hd = D / NH;
   float *P = S, *G = S + (size_t)B * NH * T * T;
   hipError_t e = pair_gemm('N', 'T', T, T, hd, {Q, false}, {K, false}, P, true, B, T, D, NH, s);
@@ -1115,6 +1238,49 @@ hipError_t launch_attn_bwd_gemm(const float *Q, const float *K, const float *V, 
   if (e == hipSuccess) e = pair_gemm('T', 'N', T, hd, T, {G, true}, {Q, false}, GK, false, B, T, D, NH, s);
   if (e == hipSuccess) e = pair_gemm('T', 'N', T, hd, T, {P, true}, {GO, false}, GV, false, B, T, D, NH, s);
   return e;
+}
+
+// GlobalAveragePooling1D (transformer.go:1541-1600): out[b][i] = (sum over
+// s of x[b][s][i], in increasing s, float32) / float32(T); the backward
+// gives every position g[b][i] / float32(T).
+__global__ __launch_bounds__(256) void gap1d_fwd_kernel(const float *__restrict__ x, float *__restrict__ out,
+                                                        int64_t BD, int T, int D) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= BD) return;
+  const int64_t b = e / D, i = e - b * D;
+  const float *p = x + b * T * D + i;
+  float sum = 0.f;
+  int s = 0;
+  for (; s + 4 <= T; s += 4) {  // four loads in flight, added in order
+    const float v0 = p[(int64_t)s * D], v1 = p[(int64_t)(s + 1) * D], v2 = p[(int64_t)(s + 2) * D],
+                v3 = p[(int64_t)(s + 3) * D];
+    sum += v0;
+    sum += v1;
+    sum += v2;
+    sum += v3;
+  }
+  for (; s < T; ++s) sum += p[(int64_t)s * D];
+  out[e] = sum / (float)T;
+}
+
+__global__ __launch_bounds__(256) void gap1d_bwd_kernel(const float *__restrict__ g, float *__restrict__ gin,
+                                                        int64_t n, int T, int D) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t TD = (int64_t)T * D, b = e / TD, i = e % D;
+  gin[e] = g[b * D + i] / (float)T;
+}
+
+hipError_t launch_gap1d_fwd(const float *x, float *out, int B, int T, int D, hipStream_t s) {
+  const int64_t BD = (int64_t)B * D;
+  hipLaunchKernelGGL(gap1d_fwd_kernel, dim3((unsigned)((BD + 255) / 256)), dim3(256), 0, s, x, out, BD, T, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_gap1d_bwd(const float *g, float *gin, int B, int T, int D, hipStream_t s) {
+  const int64_t n = (int64_t)B * T * D;
+  hipLaunchKernelGGL(gap1d_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, gin, n, T, D);
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,

@@ -728,6 +728,39 @@ __global__ __launch_bounds__(1024) void row_act_kernel(float *__restrict__ x, in
   row_activate(x + (size_t)blockIdx.x * C, C, row_act, fwd, sh);
 }
 
+// A hidden Softmax / LogSoftmax Dense's dz from the gradient g of its output
+// o (layer.go:504-560), per row, g and dz may alias:
+//   Softmax    dz_k = sum_i g_i o_i (d_ik - o_k) = g_k o_k - o_k sum_i g_i o_i
+//   LogSoftmax dz_k = sum_i g_i (d_ik - exp(o_k)) = g_k - exp(o_k) sum_i g_i
+__global__ __launch_bounds__(1024) void row_jac_kernel(const float *g, const float *__restrict__ o,
+                                                       float *dz, int C, int row_act) {
+  __shared__ float sh[16];
+  const int t = threadIdx.x, nt = blockDim.x;
+  const size_t off = (size_t)blockIdx.x * C;
+  g += off;
+  o += off;
+  dz += off;
+  float s1 = 0.f;
+  if (row_act == ROW_SOFTMAX)
+    for (int i = t; i < C; i += nt) s1 += g[i] * o[i];
+  else
+    for (int i = t; i < C; i += nt) s1 += g[i];
+  s1 = block_sum(s1, sh);
+  if (row_act == ROW_SOFTMAX)
+    for (int i = t; i < C; i += nt) dz[i] = g[i] * o[i] - o[i] * s1;
+  else
+    for (int i = t; i < C; i += nt) dz[i] = g[i] - (float)exp((double)o[i]) * s1;
+}
+
+hipError_t launch_row_jac(const float *g, const float *out, float *dz, int B, int C, int row_act,
+                          hipStream_t s) {
+  row_act &= 0xff;
+  if (B <= 0) return hipSuccess;
+  if (row_act != ROW_SOFTMAX && row_act != ROW_LOGSOFTMAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(row_jac_kernel, dim3(B), dim3(row_threads(C)), 0, s, g, out, dz, C, row_act);
+  return hipGetLastError();
+}
+
 hipError_t launch_row_act(float *out, int B, int C, int row_act, hipStream_t s) {
   if (B <= 0 || (row_act & 0xff) == ROW_NONE) return hipSuccess;
   hipLaunchKernelGGL(row_act_kernel, dim3(B), dim3(row_threads(C)), 0, s, out, C, row_act & 0xff,

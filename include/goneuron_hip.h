@@ -67,6 +67,11 @@ extern "C" {
 #define GN_LAYER_BATCHNORM2D 14  /* layer.NewBatchNorm2D      batchnorm2d.go:70 */
 #define GN_LAYER_GRU_UNROLLER 15 /* SequenceUnroller(GRU)     unroller.go:57, gru.go:83 */
 #define GN_LAYER_MOE 16          /* layer.NewMoE              moe.go:47 */
+#define GN_LAYER_MHA 17          /* layer.NewMultiHeadAttentionE transformer.go:283 (dim, num_heads,
+                                    seq_len, causal; parameters start at 0, transformer.go:367-379) */
+#define GN_LAYER_LAYERNORM 18    /* layer.NewLayerNorm        layernorm.go:57 (dim = normalizedShape,
+                                    eps; gamma 1, beta 0) */
+#define GN_LAYER_GAP1D 19        /* layer.NewGlobalAveragePooling1D transformer.go:1524 (seq_len, dim) */
 
 /* TransformerBlockExt options (layer.ActivationType, layer.NormType) */
 #define GN_BLOCK_ACT_RELU 0
@@ -90,7 +95,7 @@ typedef struct gn_layer_desc {
   float p;              /* Dropout probability */
   int32_t seq_len, num_heads, ff_dim, causal, vocab, dim; /* RMSNorm: dim = normalizedShape */
   int32_t return_sequences;
-  float eps;            /* RMSNorm eps; 0 selects the facade's 1e-5 (goneuron.go:234) */
+  float eps;            /* RMSNorm / LayerNorm eps; 0 selects the facade's 1e-5 (goneuron.go:220-236) */
   int32_t block_act;    /* TransformerBlock ff1: GN_BLOCK_ACT_* (transformer.go:199-203) */
   int32_t block_norm;   /* TransformerBlock norms: GN_BLOCK_NORM_* (transformer.go:205-210) */
   int32_t use_rope;     /* TransformerBlock: rotary embeddings on Q and K (transformer.go:212-236) */
@@ -401,15 +406,17 @@ int gn_lstm_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int32_t worker
 /* LSTM.ForwardWithArena per step (lstm.go:276-442): only the input gate adds Wx x +
  * Wh h to its bias (lstmComputeInputGates, lstm.go:1065-1101). */
 int gn_lstm_seq_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work,
-                        int32_t B, int32_t T, int32_t I, int32_t H);
+                        int32_t B, int32_t T, int32_t I, int32_t H, int32_t return_sequences);
 /* SequenceUnroller.Backward + LSTM.Backward per step (unroller.go:133-213,
  * lstm.go:476-699, clipGradients 725-753): carried dh (dh_{t-1} = dh_t + Wh^T dG), dWx from the last
  * step's input, each worker chain's cumulative gradient clipped to norm 1
  * after every step (`workers` chains of ceil(B / workers) samples, as
- * trainBatchParallel's chunks), gin_t = Wx^T dG_t (unclipped). */
+ * trainBatchParallel's chunks), gin_t = Wx^T dG_t (unclipped).  return_sequences
+ * (NewSequenceUnroller's flag, unroller.go:21-43): out / gout hold every step's
+ * h (B x T x H) instead of the last (B x H). */
 int gn_lstm_seq_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout,
                          float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t I,
-                         int32_t H, int32_t workers, float scale);
+                         int32_t H, int32_t workers, float scale, int32_t return_sequences);
 /* Embedding.ForwardWithArena (embedding.go:79-141): x = B x T ids as floats,
  * out = rows of E (V x D), ids = the int32 indices for the backward; bad
  * (optional, B ints) = 1 for a sample with an id outside [0, V), which the

@@ -1718,6 +1718,31 @@ static const float *cls_backward(layer *L, const float *g) {
   return L->gradInBuf;
 }
 
+/* GlobalAveragePooling1D transformer.go:1524-1600: out[i] = (sum over s of
+ * x[s*dim+i], increasing s, float32) / float32(seqLen); Backward gives every
+ * position grad[i] / float32(seqLen). */
+static void gap1d_build(layer *L) {
+  L->T = L->spec.seq_len;
+  L->D = L->spec.dim;
+  L->outputBuf = zalloc(L->D);
+  L->gradInBuf = zalloc((int64_t)L->T * L->D);
+  L->in_len = L->T * L->D;
+  L->out_len = L->D;
+}
+static const float *gap1d_forward(layer *L, const float *x) {
+  for (int32_t i = 0; i < L->D; i++) {
+    float sum = 0.0f;
+    for (int32_t s = 0; s < L->T; s++) sum += x[(int64_t)s * L->D + i];
+    L->outputBuf[i] = sum / (float)L->T;
+  }
+  return L->outputBuf;
+}
+static const float *gap1d_backward(layer *L, const float *g) {
+  for (int32_t s = 0; s < L->T; s++)
+    for (int32_t i = 0; i < L->D; i++) L->gradInBuf[(int64_t)s * L->D + i] = g[i] / (float)L->T;
+  return L->gradInBuf;
+}
+
 /* ------------------------------------------------------------------------ */
 /* TransformerBlock (transformer.go:908-1279) with MultiHeadAttention        */
 /* (:318-690).  Sub-layer flat order: wQ, wK, wV, wOut (W then b), norm1     */
@@ -2101,6 +2126,7 @@ static void layer_build(layer *L) {
     case GNO_LAYER_EMBEDDING: emb_build(L); break;
     case GNO_LAYER_POSENC: pe_build(L); break;
     case GNO_LAYER_CLSPOOL: cls_build(L); break;
+    case GNO_LAYER_GAP1D: gap1d_build(L); break;
     case GNO_LAYER_TRANSFORMER: tb_build(L); break;
     case GNO_LAYER_MHA: mha_build(L); break;
     case GNO_LAYER_LAYERNORM: lnl_build(L); break;
@@ -2149,6 +2175,7 @@ static const float *layer_forward(layer *L, const float *x, int32_t *len_io) {
     case GNO_LAYER_EMBEDDING: o = emb_forward(L, x); *len_io = L->out_len; break;
     case GNO_LAYER_POSENC: o = pe_forward(L, x); break;
     case GNO_LAYER_CLSPOOL: o = cls_forward(L, x); *len_io = L->D; break;
+    case GNO_LAYER_GAP1D: o = gap1d_forward(L, x); *len_io = L->D; break;
     case GNO_LAYER_TRANSFORMER: o = tb_forward(L, x); break;
     case GNO_LAYER_MHA: o = mha_forward(L, x); break;
     case GNO_LAYER_LAYERNORM: o = ln_forward(L->ln, x); break;
@@ -2173,6 +2200,7 @@ static const float *layer_backward(layer *L, const float *g) {
     case GNO_LAYER_EMBEDDING: return emb_backward(L, g);
     case GNO_LAYER_POSENC: return pe_backward(L, g);
     case GNO_LAYER_CLSPOOL: return cls_backward(L, g);
+    case GNO_LAYER_GAP1D: return gap1d_backward(L, g);
     case GNO_LAYER_TRANSFORMER: return tb_backward(L, g);
     case GNO_LAYER_MHA: return mha_backward(L, g);
     case GNO_LAYER_LAYERNORM: return ln_backward(L->ln, g);
@@ -2297,6 +2325,8 @@ static int32_t in_len_of(const gno_net *n) {
     case GNO_LAYER_GRU_UNROLLER: return L->T * L->spec.in_size;
     case GNO_LAYER_EMBEDDING: return L->T;
     case GNO_LAYER_MHA: return L->T * L->D;
+    case GNO_LAYER_GAP1D: return L->T * L->D;
+    case GNO_LAYER_CLSPOOL: return L->T * L->D;
     default: return L->spec.in_size;
   }
 }

@@ -78,6 +78,7 @@ enum {
   GNO_LAYER_MOE = 16,
   GNO_LAYER_MHA = 17,       /* MultiHeadAttention alone (dim, num_heads, seq_len, causal, use_rope) */
   GNO_LAYER_LAYERNORM = 18, /* LayerNorm alone (dim = normalizedShape, in_size = sample length, eps) */
+  GNO_LAYER_GAP1D = 19,     /* GlobalAveragePooling1D (seq_len, dim) */
 };
 
 enum { GNO_LOSS_MSE = 1, GNO_LOSS_CE = 2 };

@@ -23,7 +23,7 @@ _LIB_PATH = os.path.join(_HERE, "librefcpu.so")
 (LAYER_DENSE, LAYER_DROPOUT, LAYER_CONV2D, LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_EMBEDDING,
  LAYER_POSENC, LAYER_TRANSFORMER, LAYER_CLSPOOL, LAYER_LSTM_UNROLLER, LAYER_AVGPOOL2D,
  LAYER_RMSNORM, LAYER_SWIGLU, LAYER_BATCHNORM2D, LAYER_GRU_UNROLLER, LAYER_MOE, LAYER_MHA,
- LAYER_LAYERNORM) = range(1, 19)
+ LAYER_LAYERNORM, LAYER_GAP1D) = range(1, 20)
 LOSS_MSE, LOSS_CE = 1, 2
 
 

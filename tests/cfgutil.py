@@ -30,6 +30,13 @@ def oracle_specs(refcpu, cfg):
         elif k == "rmsnorm":
             specs.append(refcpu.spec(refcpu.LAYER_RMSNORM, dim=d["n"],
                                      in_size=cfg["in_len"] if i == 0 else 0))
+        elif k == "layernorm":  # "len": the per-sample input length (rows of n)
+            specs.append(refcpu.spec(refcpu.LAYER_LAYERNORM, dim=d["n"], in_size=d["len"]))
+        elif k == "mha":
+            specs.append(refcpu.spec(refcpu.LAYER_MHA, dim=d["dim"], num_heads=d["heads"], seq_len=d["T"],
+                                     causal=int(d["causal"]), use_rope=0))
+        elif k == "gap1d":
+            specs.append(refcpu.spec(refcpu.LAYER_GAP1D, seq_len=d["T"], dim=d["dim"]))
         elif k == "conv2d":
             specs.append(refcpu.spec(refcpu.LAYER_CONV2D, in_size=cfg["in_len"], in_channels=d["inC"],
                                      out_channels=d["outC"], kernel=d["k"], stride=d["s"],
@@ -144,6 +151,13 @@ def tensor_parts(cfg, net):
             add("ff2.b", D)
         elif k == "rmsnorm":
             add("gamma", d["n"])
+        elif k == "layernorm":
+            add("gamma", d["n"])
+            add("beta", d["n"])
+        elif k == "mha":
+            for name in ("wq", "wk", "wv", "wo"):
+                add(name + ".W", d["dim"] * d["dim"])
+                add(name + ".b", d["dim"])
         elif k == "batchnorm2d":
             add("gamma", d["C"])
             add("beta", d["C"])

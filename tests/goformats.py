@@ -328,10 +328,11 @@ ADAM_STATE = ("struct", "adamGobState", [
 
 # kind codes of goneuron_hip.h
 DENSE, DROPOUT, CONV2D, MAXPOOL2D, FLATTEN, EMBEDDING, POSENC, TRANSFORMER, CLSPOOL, LSTM, AVGPOOL2D, \
-    RMSNORM, SWIGLU, BATCHNORM2D, GRU, MOE = range(1, 17)
+    RMSNORM, SWIGLU, BATCHNORM2D, GRU, MOE, MHA, LAYERNORM, GAP1D = range(1, 20)
 ACT_NAMES = {2: "Sigmoid", 3: "Tanh", 4: "Softmax", 5: "LogSoftmax", 6: "Linear", 7: "GELU"}
 TYPE_NAMES = {DENSE: "Dense", CONV2D: "Conv2D", DROPOUT: "Dropout", MAXPOOL2D: "MaxPool2D",
-              AVGPOOL2D: "AvgPool2D", EMBEDDING: "Embedding", FLATTEN: "Flatten", BATCHNORM2D: "BatchNorm2D"}
+              AVGPOOL2D: "AvgPool2D", EMBEDDING: "Embedding", FLATTEN: "Flatten", BATCHNORM2D: "BatchNorm2D",
+              LAYERNORM: "LayerNorm"}
 
 
 def f32(x):
@@ -362,6 +363,8 @@ def layer_config(L, params, dims_known):
         cfg.update(InChannels=ch, KernelSize=L["k"], Stride=L["s"], Padding=L["p"])
     elif k == EMBEDDING:
         cfg.update(InSize=L["vocab"], OutSize=L["dim"])
+    elif k == LAYERNORM:  # net.go:1469-1473
+        cfg.update(NormalizedShape=L["n"], Eps=f32(L["eps"]), Affine=True)
     return cfg
 
 

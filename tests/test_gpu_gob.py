@@ -74,6 +74,13 @@ def geometry(cfg):
         elif k == "lstm":
             L = dict(kind=G.LSTM)
             n = d["hidden"]
+        elif k == "layernorm":
+            L = dict(kind=G.LAYERNORM, n=d["n"], eps=1e-5)
+        elif k == "mha":
+            L = dict(kind=G.MHA)
+        elif k == "gap1d":
+            L = dict(kind=G.GAP1D)
+            n = d["dim"]
         else:
             raise ValueError(k)
         out.append(L)
@@ -111,7 +118,25 @@ def _lstm(B=4):
                         {"kind": "dense", "in": 4, "out": 1, "act": "linear", "ptr": False}])
 
 
-MODELS = {"cnn_all": _cnn_all, "mlp_big": _mlp_big, "emb": _emb, "lstm": _lstm}
+def _norm(B=8):
+    # a Tanh output: CreateLayer rebuilds activations as values, which for
+    # Softmax would predict the identity (net.go:1512-1588)
+    return dict(num=55, name="gob_norm", B=B, loss="ce", lr=1e-3, x="normal", in_len=12, classes=3,
+                layers=[{"kind": "dense", "in": 12, "out": 8, "act": "relu", "ptr": False},
+                        {"kind": "layernorm", "n": 4, "len": 8},
+                        {"kind": "dense", "in": 8, "out": 3, "act": "tanh", "ptr": False}])
+
+
+def _attn(B=4):
+    return dict(num=56, name="gob_attn", B=B, loss="mse", lr=1e-3, x="normal", in_len=3 * 4, classes=None,
+                targets="normal",
+                layers=[{"kind": "mha", "heads": 2, "T": 3, "causal": True, "dim": 4},
+                        {"kind": "gap1d", "T": 3, "dim": 4},
+                        {"kind": "dense", "in": 4, "out": 1, "act": "linear", "ptr": False}])
+
+
+MODELS = {"cnn_all": _cnn_all, "mlp_big": _mlp_big, "emb": _emb, "lstm": _lstm, "norm": _norm,
+          "attn": _attn}
 
 
 def expected_file(cfg, model, dims_known, types=None):
@@ -168,12 +193,14 @@ def _expected_descs(cfg, dims_known):
             out.append((G.DROPOUT, dict(in_size=c["InSize"])))
         elif t == "Embedding":
             out.append((G.EMBEDDING, dict(vocab=c["InSize"], dim=c["OutSize"])))
+        elif t == "LayerNorm":
+            out.append((G.LAYERNORM, dict(dim=c["NormalizedShape"])))
         else:
             out.append((G.FLATTEN, {}))
     return out
 
 
-@pytest.mark.parametrize("name", ["cnn_all", "mlp_big", "emb"])
+@pytest.mark.parametrize("name", ["cnn_all", "mlp_big", "emb", "norm"])
 def test_load_rebuilds_the_network(gn, tmp_path, name):
     """Saved after training with four workers (sizes unknown to the network's
     own layers), loaded back: the layers CreateLayer builds, the parameters,

@@ -229,40 +229,84 @@ def test_mha_ops(dev, oracle, B, T, D, NH, causal, rope):
             _close(name + "." + part, got[sl], ref)
 
 
-def test_mha_ops_reject_unsupported(dev):
-    """More (sample, head) pairs than one launch's grid holds: refused on the
-    host before any launch."""
-    L, _ = _lib()
-    x = _zeros(dev, 8)
-    assert L.gn_mha_forward(dev.h, x.p, x.p, x.p, x.p, 40000, 2, 64, 2, 0, 0) == -4  # GN_ERR_UNSUPPORTED
+@pytest.mark.parametrize("D,NH,T", [(128, 2, 2), (64, 2, 4)])
+def test_mha_ops_beyond_grid_limit(dev, oracle, D, NH, T):
+    """More (sample, head) pairs than a grid dimension holds (33,000 samples x
+    2 heads): the batched-GEMM path (heads 64 wide) runs the pairs in chunks,
+    the fused path (heads 32 wide) takes them on the grid's x dimension.  The
+    batch repeats 10 distinct samples 3,300 times, so every output row equals
+    its distinct sample's and the batch-averaged gradients equal the 10-sample
+    batch's, which the oracle computes."""
+    L, check = _lib()
+    nd, reps = 10, 3300
+    B = nd * reps
+    log(f"mha B={B} T={T} D={D} heads={NH}: {B * NH} (sample, head) pairs")
+    net = oracle.Net([oracle.spec(oracle.LAYER_MHA, dim=D, num_heads=NH, seq_len=T, causal=1, use_rope=0)],
+                     oracle.LOSS_MSE)
+    rng = np.random.default_rng(D + T)
+    p = (rng.normal(size=net.n) * (0.5 / np.sqrt(D))).astype(np.float32)
+    net.params[:] = p
+    x0 = rng.normal(size=(nd, T * D)).astype(np.float32)
+    g0 = rng.normal(size=(nd, T * D)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x0, g0, nd, T * D, T * D)
+    gr = net.grads.copy()
+    x, g = np.tile(x0, (reps, 1)), np.tile(g0, (reps, 1))
+    ws = C.c_int64()
+    check(None, L.gn_mha_workspace(B, T, D, NH, 0, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = (_zeros(dev, (B, T * D)), _zeros(dev, p.shape), _zeros(dev, (B, T * D)),
+                            _zeros(dev, ws.value))
+    check(dev.h, L.gn_mha_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, D, NH, 1, 0))
+    check(dev.h, L.gn_mha_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, T, D, NH, 1, 0,
+                                   F(np.float32(1) / np.float32(B))))
+    out, gin = dout.get().reshape(reps, nd, T * D), dgin.get().reshape(reps, nd, T * D)
+    for r in (0, reps // 2, reps - 1):  # first, middle and last copies (the last chunk of pairs)
+        _close(f"out[{r}]", out[r], out_r)
+        _close(f"gin[{r}]", gin[r], gin_r)
+    # the parameter gradients sum B = 33,000 per-sample terms in float32, in
+    # sample order as the reference's batch loop does: that sum's own
+    # rounding reaches about B * 2^-24 of its value (the 10-sample oracle sum
+    # has almost none), so that is the tolerance here
+    gtol = max(TOL, B * 2.0 ** -24)
+    got = dgr.get()
+    nd4 = D * D + D
+    for i, name in enumerate(("wQ", "wK", "wV", "wOut")):
+        for part, sl in (("W", slice(i * nd4, i * nd4 + D * D)), ("b", slice(i * nd4 + D * D, (i + 1) * nd4))):
+            ref = gr[sl]
+            if np.abs(ref).max() <= 1e-6 * np.abs(gr).max():
+                continue
+            _close(name + "." + part, got[sl], ref, gtol)
 
 
 # ---------------------------------------------------------------- SequenceUnroller(LSTM)
-@pytest.mark.parametrize("B,T,I,H,workers,gscale", [
-    (6, 10, 8, 16, 1, 1e-3),   # clip inactive
-    (6, 10, 8, 16, 1, 3.0),    # clip active on one chain
-    (8, 7, 5, 12, 4, 3.0),     # four worker chains, clip active
-    (5, 12, 6, 32, 2, 0.3)])
-def test_lstm_seq_ops(dev, oracle, B, T, I, H, workers, gscale):
+@pytest.mark.parametrize("B,T,I,H,workers,gscale,seq", [
+    (6, 10, 8, 16, 1, 1e-3, 0),   # clip inactive
+    (6, 10, 8, 16, 1, 3.0, 0),    # clip active on one chain
+    (8, 7, 5, 12, 4, 3.0, 0),     # four worker chains, clip active
+    (5, 12, 6, 32, 2, 0.3, 0),
+    (6, 9, 8, 16, 1, 0.5, 1),     # returnSequences: every step's h out, a gradient per step in
+    (7, 6, 5, 24, 3, 2.0, 1)])
+def test_lstm_seq_ops(dev, oracle, B, T, I, H, workers, gscale, seq):
     L, check = _lib()
-    log(f"lstm B={B} T={T} I={I} H={H} workers={workers} gscale={gscale}")
-    net = oracle.Net([oracle.spec(oracle.LAYER_LSTM_UNROLLER, in_size=I, out_size=H, seq_len=T)],
-                     oracle.LOSS_MSE, workers=workers)
+    log(f"lstm B={B} T={T} I={I} H={H} workers={workers} gscale={gscale} seq={seq}")
+    net = oracle.Net([oracle.spec(oracle.LAYER_LSTM_UNROLLER, in_size=I, out_size=H, seq_len=T,
+                                  return_sequences=seq)], oracle.LOSS_MSE, workers=workers)
     rng = np.random.default_rng(T * H + workers)
     p = (rng.normal(size=net.n) * 0.3).astype(np.float32)  # every gate live
     net.params[:] = p
     x = rng.normal(size=(B, T * I)).astype(np.float32)
-    g = (rng.normal(size=(B, H)) * gscale).astype(np.float32)
-    out_r, gin_r = net.accumulate_grad(x, g, B, T * I, H)
+    OL = T * H if seq else H
+    g = (rng.normal(size=(B, OL)) * gscale).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, T * I, OL)
     gr = net.grads.copy()
     ws = C.c_int64()
     check(None, L.gn_lstm_workspace(B, T, I, H, workers, C.byref(ws)))
     dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
-    dout, dgr, dgin, dwk = (_zeros(dev, (B, H)), _zeros(dev, p.shape), _zeros(dev, (B, T * I)),
+    dout, dgr, dgin, dwk = (_zeros(dev, (B, OL)), _zeros(dev, p.shape), _zeros(dev, (B, T * I)),
                             _zeros(dev, ws.value))
-    check(dev.h, L.gn_lstm_seq_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, I, H))
+    check(dev.h, L.gn_lstm_seq_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, I, H, seq))
     check(dev.h, L.gn_lstm_seq_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, T, I, H, workers,
-                                        F(np.float32(1) / np.float32(B))))
+                                        F(np.float32(1) / np.float32(B)), seq))
     _close("out", dout.get(), out_r)
     _close("gin", dgin.get(), gin_r)
     got = dgr.get()
@@ -276,7 +320,9 @@ def test_lstm_seq_ops(dev, oracle, B, T, I, H, workers, gscale):
 
 # ---------------------------------------------------------------- Embedding
 @pytest.mark.parametrize("B,T,V,D,workers,bad", [
-    (8, 16, 100, 32, 1, False), (10, 6, 50, 16, 4, False), (9, 5, 40, 8, 3, True), (7, 4, 30, 8, 1, True)])
+    (8, 16, 100, 32, 1, False), (10, 6, 50, 16, 4, False), (9, 5, 40, 8, 3, True), (7, 4, 30, 8, 1, True),
+    # more than 2048 contributing rows (64 worker chunks x 40 tokens): the global row lists
+    (64, 40, 700, 24, 64, False), (128, 40, 300, 20, 64, True)])
 def test_embedding_ops(dev, oracle, B, T, V, D, workers, bad):
     """Forward rows bit-exact; the table gradient is the last sample of each
     worker chunk (Backward zeroes it first).  With an out-of-range id in some

@@ -125,3 +125,22 @@ def test_layernorm_layer_vs_formula(oracle, rows, N, B, eps):
     assert max_rel(gin.reshape(-1, N), dx) <= 1e-4
     assert max_rel(net.grads[:N], (G * xh).sum(0) / B) <= 1e-4
     assert max_rel(net.grads[N:], G.sum(0) / B) <= 1e-4
+
+
+def test_global_average_pooling_1d_closed_form(oracle):
+    """GlobalAveragePooling1D (transformer.go:1541-1600): the float32 sum over
+    the rows in order, divided by float32(seqLen); the backward spreads
+    grad / seqLen over every row."""
+    T, D, B = 7, 5, 3
+    rng = np.random.default_rng(77)
+    net = oracle.Net([oracle.spec(oracle.LAYER_GAP1D, seq_len=T, dim=D)], oracle.LOSS_MSE)
+    x = rng.normal(size=(B, T * D)).astype(np.float32)
+    g = rng.normal(size=(B, D)).astype(np.float32)
+    out, gin = net.accumulate_grad(x, g, B, T * D, D)
+    for b in range(B):
+        acc = np.zeros(D, np.float32)
+        for s in range(T):
+            acc = (acc + x[b, s * D:(s + 1) * D]).astype(np.float32)
+        np.testing.assert_array_equal(out[b], (acc / np.float32(T)).astype(np.float32))
+        np.testing.assert_array_equal(gin[b], np.tile((g[b] / np.float32(T)).astype(np.float32), T))
+    np.testing.assert_allclose(out, x.reshape(B, T, D).mean(axis=1), rtol=1e-6, atol=1e-6)
