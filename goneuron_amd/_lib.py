@@ -136,6 +136,21 @@ SIGNATURES = {
     "gn_lstm_seq_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 5 + [C.c_float, C.c_int32]),
     "gn_embedding_forward": (C.c_int, [vp] + [vp] * 5 + [C.c_int32] * 4),
     "gn_embedding_backward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 5 + [C.c_float]),
+    "gn_avgpool2d_forward": (C.c_int, [vp] + [vp] * 2 + [C.c_int32] * 7),
+    "gn_avgpool2d_backward": (C.c_int, [vp] + [vp] * 2 + [C.c_int32] * 7),
+    "gn_rmsnorm_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32, C.c_int32, C.c_float]),
+    "gn_rmsnorm_backward": (C.c_int, [vp] + [vp] * 7 + [C.c_int32, C.c_int32, C.c_float]),
+    "gn_swiglu_workspace": (C.c_int, [C.c_int32, C.c_int32, C.POINTER(C.c_int64)]),
+    "gn_swiglu_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 3),
+    "gn_swiglu_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 3 + [C.c_float]),
+    "gn_batchnorm2d_forward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 3 + [C.c_float, C.c_float, C.c_int32]),
+    "gn_batchnorm2d_backward": (C.c_int, [vp] + [vp] * 8 + [C.c_int32] * 3 + [C.c_float, C.c_int32, C.c_float]),
+    "gn_gru_workspace": (C.c_int, [C.c_int32] * 4 + [C.POINTER(C.c_int64)]),
+    "gn_gru_seq_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 5),
+    "gn_gru_seq_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 4 + [C.c_float, C.c_int32]),
+    "gn_moe_workspace": (C.c_int, [C.c_int32] * 5 + [C.POINTER(C.c_int64)]),
+    "gn_moe_forward": (C.c_int, [vp] + [vp] * 4 + [C.c_int32] * 6 + [C.POINTER(C.c_uint64)]),
+    "gn_moe_backward": (C.c_int, [vp] + [vp] * 6 + [C.c_int32] * 6 + [C.c_float]),
     "gn_gemm": (C.c_int, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float, vp,
                           C.c_int32, vp, C.c_int32, vp, C.c_int32]),
     "gn_adam_step": (C.c_int, [vp, vp, vp, vp, vp, C.c_int64, C.c_float, C.c_float, C.c_float,

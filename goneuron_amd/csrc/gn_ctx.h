@@ -199,3 +199,10 @@ int mha_forward_impl(gn_ctx *c, const float *x, const float *params, float *out,
 int mha_backward_impl(gn_ctx *c, const float *x, const float *params, const float *gout, float *grads,
                       float *gin, const MhaBufs &m, int B, int T, int D, int NH, int causal, int rope,
                       float scale);
+
+// gradW = scale * dz^T x ; gradB = scale * colsum(dz) (gB may be null) ;
+// gin = dz W (optionally * act'(gin_aux)), gin may be null (gn_runtime.hip)
+hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz, float *gW,
+                          float *gB, float *gin, int B, int in, int out_n, float scale,
+                          const float *gin_aux, int gin_deriv, hipEvent_t dz_ready = nullptr,
+                          float *ms = nullptr, size_t ms_cap = 0, const float *gin_colscale = nullptr);

@@ -629,3 +629,416 @@ extern "C" int gn_embedding_backward(gn_ctx *c, const float *gout, const int32_t
                               c->scratch_floats));
   return GN_OK;
 }
+
+// ---------------------------------------------------------------------------
+// AvgPool2D (avgpool2d.go:137-474): per sample C x H x W, windows k x k with
+// stride and zero padding; the mean counts only the positions inside the
+// input (count_include_pad false).  The backward spreads each output
+// gradient over its window's positions.
+// ---------------------------------------------------------------------------
+extern "C" int gn_avgpool2d_forward(gn_ctx *c, const float *x, float *out, int32_t B, int32_t C, int32_t H,
+                                    int32_t W, int32_t k, int32_t stride, int32_t pad) {
+  ENTRY(c);
+  PoolShape ps{};
+  int rc = pool_shape(c, ps, B, C, H, W, k, stride, pad);
+  if (rc) return rc;
+  if (!x || !out) return set_err(c, GN_ERR_INVALID, "null pointer");
+  KTimer kt(c, GN_KCLASS_OTHER, "avgpool_fwd", f4((double)B * C * H * W + (double)B * C * ps.oH * ps.oW));
+  HIP_OK(c, launch_avgpool_fwd(x, out, ps, B, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_avgpool2d_backward(gn_ctx *c, const float *gout, float *gin, int32_t B, int32_t C,
+                                     int32_t H, int32_t W, int32_t k, int32_t stride, int32_t pad) {
+  ENTRY(c);
+  PoolShape ps{};
+  int rc = pool_shape(c, ps, B, C, H, W, k, stride, pad);
+  if (rc) return rc;
+  if (!gout || !gin) return set_err(c, GN_ERR_INVALID, "null pointer");
+  KTimer kt(c, GN_KCLASS_OTHER, "avgpool_bwd", f4((double)B * C * ps.oH * ps.oW + (double)B * C * H * W));
+  HIP_OK(c, launch_avgpool_bwd(gout, gin, ps, B, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (rmsnorm.go:222-329) over rows of N: y = gamma x / rms, rms =
+// sqrt(mean(x^2) + eps) (eps 0 selects 1e-5); the backward is the
+// reference's formula (its projection term is scaled by gamma_j, Q19).
+// work: rows x N floats (g x / rms for the gamma sums).
+// ---------------------------------------------------------------------------
+extern "C" int gn_rmsnorm_forward(gn_ctx *c, const float *x, const float *gamma, float *y, float *rms,
+                                  int32_t rows, int32_t N, float eps) {
+  ENTRY(c);
+  if (!x || !gamma || !y || !rms || rows <= 0 || N <= 0 || !(eps >= 0))
+    return set_err(c, GN_ERR_INVALID, "bad rmsnorm args");
+  KTimer kt(c, GN_KCLASS_OTHER, "rms_fwd", f4(2.0 * rows * N + rows));
+  HIP_OK(c, launch_rms_fwd(x, gamma, y, rms, rows, N, eps > 0 ? eps : 1e-5f, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_rmsnorm_backward(gn_ctx *c, const float *g, const float *x, const float *gamma,
+                                   const float *rms, float *dx, float *dgamma, float *work, int32_t rows,
+                                   int32_t N, float scale) {
+  ENTRY(c);
+  if (!g || !x || !gamma || !rms || !dgamma || !work || rows <= 0 || N <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad rmsnorm args");
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "rms_bwd", f4(4.0 * rows * N + rows));
+    HIP_OK(c, launch_rms_bwd(g, x, gamma, rms, dx, work, rows, N, c->stream));
+  }
+  KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)rows * N + N));
+  HIP_OK(c, launch_colsum(work, rows, N, N, scale, dgamma, c->scratch, c->scratch_floats, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU (swiglu.go:103-232): params = [W (out x in) | V (out x in)], no
+// biases; y = swish(W x) * (V x).  work: gn_swiglu_workspace floats (the
+// projections Z = [W x | V x] and their gradients); forward and backward of
+// one batch share it.
+// ---------------------------------------------------------------------------
+extern "C" int gn_swiglu_workspace(int32_t B, int32_t out, int64_t *floats) {
+  if (!floats || B <= 0 || out <= 0) return GN_ERR_INVALID;
+  *floats = 4 * (int64_t)B * out;
+  return GN_OK;
+}
+
+extern "C" int gn_swiglu_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
+                                 int32_t B, int32_t in, int32_t out_size) {
+  ENTRY(c);
+  if (!x || !params || !out || !work || B <= 0 || in <= 0 || out_size <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad swiglu args");
+  const int out2 = 2 * out_size;
+  {
+    GemmArgs g{};  // Z[b] = [W x_b | V x_b]
+    g.M = B; g.N = out2; g.K = in;
+    g.A = x; g.lda = in;
+    g.B = params; g.ldb = in;
+    g.C = work; g.ldc = out2; g.alpha = 1.0f;
+    g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(g));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_SCALE, g, c->stream));
+  }
+  KTimer kt(c, GN_KCLASS_OTHER, "swiglu_fwd", f4(3.0 * B * out_size));
+  HIP_OK(c, launch_swiglu_fwd(work, out, B, out_size, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_swiglu_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                                  float *grads, float *gin, float *work, int32_t B, int32_t in,
+                                  int32_t out_size, float scale) {
+  ENTRY(c);
+  if (!x || !params || !gout || !grads || !work || B <= 0 || in <= 0 || out_size <= 0)
+    return set_err(c, GN_ERR_INVALID, "bad swiglu args");
+  float *Z = work, *dZ = work + 2 * (int64_t)B * out_size;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "swiglu_bwd", f4(5.0 * B * out_size));
+    HIP_OK(c, launch_swiglu_bwd(gout, Z, 2 * out_size, dZ, B, out_size, c->stream));
+  }
+  // [dW | dV] = scale dZ^T x, gin = dZ [W; V]
+  HIP_OK(c, dense_bwd_core(c, x, params, dZ, grads, nullptr, gin, B, in, 2 * out_size, scale, nullptr, 0));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// BatchNorm2D (batchnorm2d.go:255-666): x is B x C x HW; params = [gamma |
+// beta] or null (affine = false).  Training (Q22): each sample normalised by
+// its own per-channel statistics (one sample per Forward in the reference's
+// per-sample loop), the running mean / var advanced once per sample in sample
+// order (biased variance, momentum as given); stats keeps (mean, var, std)
+// per (sample, channel) for the backward.  Inference: the running
+// statistics.  The backward writes [dgamma | dbeta] = scale * sums (zero in
+// inference mode, where only dx flows, batchnorm2d.go:525-551); work: 2 B C
+// floats.
+// ---------------------------------------------------------------------------
+extern "C" int gn_batchnorm2d_forward(gn_ctx *c, const float *x, const float *params, float *out,
+                                      float *stats, float *running_mean, float *running_var, int32_t B,
+                                      int32_t C, int32_t HW, float eps, float momentum, int32_t training) {
+  ENTRY(c);
+  if (!x || !out || !stats || !running_mean || !running_var || B <= 0 || C <= 0 || HW <= 0 || !(eps >= 0) ||
+      !(momentum >= 0 && momentum <= 1))
+    return set_err(c, GN_ERR_INVALID, "bad batchnorm2d args");
+  KTimer kt(c, GN_KCLASS_OTHER, "bn_fwd", f4(2.0 * B * C * HW + 3.0 * B * C));
+  HIP_OK(c, launch_bn_fwd(x, params, out, stats, running_mean, running_var, B, C, HW, eps > 0 ? eps : 1e-5f,
+                          momentum, training ? 1 : 0, c->stream));
+  return GN_OK;
+}
+
+extern "C" int gn_batchnorm2d_backward(gn_ctx *c, const float *gout, const float *x, const float *params,
+                                       const float *stats, const float *running_var, float *grads, float *gin,
+                                       float *work, int32_t B, int32_t C, int32_t HW, float eps,
+                                       int32_t training, float scale) {
+  ENTRY(c);
+  if (!gout || !x || !stats || !running_var || !work || B <= 0 || C <= 0 || HW <= 0 || (params && !grads))
+    return set_err(c, GN_ERR_INVALID, "bad batchnorm2d args");
+  KTimer kt(c, GN_KCLASS_OTHER, "bn_bwd", f4(3.0 * B * C * HW + 2.0 * B * C));
+  if (!training) {
+    if (params) HIP_OK(c, launch_fill(grads, 0.0f, 2 * (int64_t)C, c->stream));
+    if (gin)
+      HIP_OK(c, launch_bn_bwd_eval(gout, params, running_var, gin, B, C, HW, eps > 0 ? eps : 1e-5f,
+                                   c->stream));
+    return GN_OK;
+  }
+  HIP_OK(c, launch_bn_bwd(gout, x, params, stats, gin, params ? work : nullptr, B, C, HW, c->stream));
+  if (params) {
+    HIP_OK(c, launch_colsum(work, B, C, C, scale, grads, c->scratch, c->scratch_floats, c->stream));
+    HIP_OK(c, launch_colsum(work + (int64_t)B * C, B, C, C, scale, grads + C, c->scratch, c->scratch_floats,
+                            c->stream));
+  }
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// SequenceUnroller(GRU) (unroller.go:57-213, gru.go:192-703) over a batch: x
+// is B x T x I, params = [Wx (3H x I) | Wh (2H x H) | b (3H)], gates u, r, c.
+// The reference's quirks are kept: h' = h + u (c - h) forward but a backward
+// that weights the candidate by (1 - u) and the direct path by u (Q23), no
+// reset-gate delta (Q24), dWx from the last step's input, gradients carried
+// as dh_{t-1} = dh_t + dh_prev.  return_sequences: out / gout hold every
+// step's h.  work: gn_gru_workspace floats, shared by the forward and
+// backward of one batch.
+// ---------------------------------------------------------------------------
+namespace {
+struct GruWork {
+  float *WhT, *xw, *pre, *hprev, *rh, *Dg, *S;
+  size_t floats;
+};
+GruWork gru_carve(float *w, int B, int T, int H) {
+  Carve cv(w);
+  GruWork m{};
+  const size_t rows = (size_t)B * T;
+  m.WhT = cv.take(2 * (size_t)H * H);
+  m.xw = cv.take(rows * 3 * H);
+  m.pre = cv.take(rows * 3 * H);
+  m.hprev = cv.take(rows * H);
+  m.rh = cv.take(rows * H);
+  m.Dg = cv.take(rows * 3 * H);
+  m.S = cv.take((size_t)B * 3 * H);
+  m.floats = cv.off;
+  return m;
+}
+}  // namespace
+
+extern "C" int gn_gru_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int64_t *floats) {
+  if (!floats || B <= 0 || T <= 0 || I <= 0 || H <= 0) return GN_ERR_INVALID;
+  *floats = (int64_t)gru_carve(nullptr, B, T, H).floats;
+  return GN_OK;
+}
+
+extern "C" int gn_gru_seq_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
+                                  int32_t B, int32_t T, int32_t I, int32_t H, int32_t return_sequences) {
+  ENTRY(c);
+  if (!x || !params || !out || !work || B <= 0 || T <= 0 || I <= 0 || !gru_supported(H))
+    return set_err(c, GN_ERR_INVALID, "bad GRU args (hidden <= 1024)");
+  GruWork m = gru_carve(work, B, T, H);
+  const int G3 = 3 * H;
+  const float *Wx = params, *Wh = Wx + (int64_t)G3 * I, *bias = Wh + (int64_t)2 * H * H;
+  {
+    GemmArgs g{};  // xw[b*T + t] = b + Wx x_t (gru.go:194-210)
+    g.M = B * T; g.N = G3; g.K = I;
+    g.A = x; g.lda = I; g.B = Wx; g.ldb = I;
+    g.C = m.xw; g.ldc = G3; g.alpha = 1.0f;
+    g.bias = bias; g.act = F_IDENTITY;
+    g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(g));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, g, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "transpose", f4(4.0 * H * H));
+    HIP_OK(c, launch_transpose(Wh, m.WhT, 2 * H, H, c->stream));
+  }
+  KTimer kt(c, GN_KCLASS_OTHER, "gru_fwd", 2.0 * 3 * H * H * B * T);
+  HIP_OK(c, launch_gru_fwd(m.xw, m.WhT, m.pre, m.hprev, m.rh, out, B, T, H, c->stream,
+                           return_sequences ? 1 : 0));
+  return GN_OK;
+}
+
+extern "C" int gn_gru_seq_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                                   float *grads, float *gin, float *work, int32_t B, int32_t T, int32_t I,
+                                   int32_t H, float scale, int32_t return_sequences) {
+  ENTRY(c);
+  if (!x || !params || !gout || !grads || !work || B <= 0 || T <= 0 || I <= 0 || !gru_supported(H))
+    return set_err(c, GN_ERR_INVALID, "bad GRU args (hidden <= 1024)");
+  GruWork m = gru_carve(work, B, T, H);
+  const int G3 = 3 * H;
+  const float *Wx = params, *Wh = Wx + (int64_t)G3 * I;
+  float *gWx = grads, *gWh = gWx + (int64_t)G3 * I, *gb = gWh + (int64_t)2 * H * H;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "gru_bwd", 2.0 * 2 * H * H * B * T);
+    HIP_OK(c, launch_gru_bwd(gout, m.pre, m.hprev, Wh, m.Dg, B, T, H, c->stream, return_sequences ? 1 : 0));
+  }
+  if (gin) {  // dx_t = Wx^T [dU | dR (never set, 0) | dC] (gru.go:481-500)
+    GemmArgs a{};
+    a.M = B * T; a.N = I; a.K = G3;
+    a.A = m.Dg; a.lda = G3; a.B = Wx; a.ldb = I;
+    a.C = gin; a.ldc = I; a.alpha = 1.f;
+    a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+    HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, G3));
+    HIP_OK(c, launch_token_sum(m.Dg, m.S, B, T, G3, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * G3 + G3));
+    HIP_OK(c, launch_colsum(m.S, B, G3, G3, scale, gb, c->scratch, c->scratch_floats, c->stream));
+  }
+  GemmArgs a{};  // dWx = scale * (sum_t dG)^T x_last
+  a.M = G3; a.N = I; a.K = B;
+  a.A = m.S; a.lda = G3;
+  a.B = x + (int64_t)(T - 1) * I; a.ldb = T * I;
+  a.C = gWx; a.ldc = I; a.alpha = scale;
+  a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+  GemmArgs u{};  // dWh_u = scale * dU^T h_prev over (sample, step)
+  u.M = H; u.N = H; u.K = B * T;
+  u.A = m.Dg; u.lda = G3;
+  u.B = m.hprev; u.ldb = H;
+  u.C = gWh; u.ldc = H; u.alpha = scale;
+  u.ws = c->scratch; u.ws_cap = c->scratch_floats;
+  GemmArgs r{};  // dWh_r = scale * dC^T (r * h_prev): the candidate's use of the reset block
+  r.M = H; r.N = H; r.K = B * T;
+  r.A = m.Dg + 2 * H; r.lda = G3;
+  r.B = m.rh; r.ldb = H;
+  r.C = gWh + (int64_t)H * H; r.ldc = H; r.alpha = scale;
+  r.ws = c->scratch; r.ws_cap = c->scratch_floats;
+  KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a) + gemm_flops(u) + gemm_flops(r));
+  HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, a, c->stream));
+  HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, u, c->stream));
+  HIP_OK(c, launch_gemm('T', 'N', EPI_SCALE, r, c->stream));
+  return GN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MoE (moe.go:140-313): params = [gating W (E x I), b (E) | per expert W (O x
+// I), b (O)]; a Linear gating Dense, E Dense(LeakyReLU 0.1) experts, the top
+// K by gate softmax combined with their probabilities (ties keep index
+// order).  training adds the layer's RNG gate noise: *noise is that stream's
+// state (NewRNG(42) at construction), advanced by E draws per sample, and
+// the load-balancing gradient in the backward.  All experts run on every
+// sample; the route picks K of them.  work: gn_moe_workspace floats, shared
+// by the forward and backward of one batch.
+// ---------------------------------------------------------------------------
+namespace {
+struct MoeWork {
+  float *logits, *prob, *dzg, *eout, *edz;
+  int32_t *act;
+  size_t floats;
+};
+MoeWork moe_carve(float *w, int B, int I, int O, int E, int K) {
+  Carve cv(w);
+  MoeWork m{};
+  m.logits = cv.take((size_t)B * E);
+  m.prob = cv.take((size_t)B * E);
+  m.dzg = cv.take((size_t)B * E);
+  m.eout = cv.take((size_t)E * B * O);
+  m.edz = cv.take((size_t)E * B * O);
+  m.act = reinterpret_cast<int32_t *>(cv.take((size_t)B * K));
+  m.floats = cv.off;
+  (void)I;
+  return m;
+}
+int moe_check(gn_ctx *c, int B, int I, int O, int E, int K) {
+  if (B <= 0 || I <= 0 || O <= 0 || E <= 0 || E > MOE_MAX_E || K <= 0 || K > E)
+    return set_err(c, GN_ERR_INVALID, "bad MoE sizes (experts <= %d, 0 < k <= experts)", MOE_MAX_E);
+  return GN_OK;
+}
+}  // namespace
+
+extern "C" int gn_moe_workspace(int32_t B, int32_t I, int32_t O, int32_t E, int32_t K, int64_t *floats) {
+  if (!floats || B <= 0 || I <= 0 || O <= 0 || E <= 0 || K <= 0) return GN_ERR_INVALID;
+  *floats = (int64_t)moe_carve(nullptr, B, I, O, E, K).floats;
+  return GN_OK;
+}
+
+extern "C" int gn_moe_forward(gn_ctx *c, const float *x, const float *params, float *out, float *work,
+                              int32_t B, int32_t I, int32_t O, int32_t E, int32_t K, int32_t training,
+                              uint64_t *noise) {
+  ENTRY(c);
+  int rc = moe_check(c, B, I, O, E, K);
+  if (rc) return rc;
+  if (!x || !params || !out || !work || (training && !noise)) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MoeWork m = moe_carve(work, B, I, O, E, K);
+  const int64_t e1 = (int64_t)O * I + O;
+  {
+    GemmArgs g{};  // gate logits = Wg x + bg
+    g.M = B; g.N = E; g.K = I;
+    g.A = x; g.lda = I; g.B = params; g.ldb = I;
+    g.C = m.logits; g.ldc = E; g.alpha = 1.f; g.bias = params + (int64_t)E * I; g.act = F_IDENTITY;
+    g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(g));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, g, c->stream));
+  }
+  MoeRoute rt{};
+  rt.B = B; rt.E = E; rt.K = K; rt.training = training ? 1 : 0;
+  rt.chunk = 0;
+  rt.base[0] = training ? *noise : 42;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "moe_route", f4(2.0 * B * E + (double)B * K));
+    HIP_OK(c, launch_moe_route(m.logits, m.prob, m.act, rt, c->stream));
+  }
+  for (int e = 0; e < E; ++e) {
+    const float *We = params + (int64_t)E * I + E + e * e1;
+    GemmArgs g{};
+    g.M = B; g.N = O; g.K = I;
+    g.A = x; g.lda = I; g.B = We; g.ldb = I;
+    g.C = m.eout + (int64_t)e * B * O; g.ldc = O; g.alpha = 1.f; g.bias = We + (int64_t)O * I;
+    g.act = F_LEAKY;
+    g.ws = c->scratch; g.ws_cap = c->scratch_floats;
+    KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(g));
+    HIP_OK(c, launch_gemm('N', 'T', EPI_BIAS_ACT, g, c->stream));
+  }
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "moe_combine", f4((double)K * B * O + (double)B * O));
+    HIP_OK(c, launch_moe_combine(m.eout, m.prob, m.act, out, B, O, E, K, c->stream));
+  }
+  if (training)  // E draws per sample on the layer's stream
+    for (int64_t d = 0; d < (int64_t)B * E; ++d) *noise = *noise * 6364136223846793005ull + 1;
+  return GN_OK;
+}
+
+extern "C" int gn_moe_backward(gn_ctx *c, const float *x, const float *params, const float *gout,
+                               float *grads, float *gin, float *work, int32_t B, int32_t I, int32_t O,
+                               int32_t E, int32_t K, int32_t training, float scale) {
+  ENTRY(c);
+  int rc = moe_check(c, B, I, O, E, K);
+  if (rc) return rc;
+  if (!x || !params || !gout || !grads || !work) return set_err(c, GN_ERR_INVALID, "null pointer");
+  MoeWork m = moe_carve(work, B, I, O, E, K);
+  const int64_t e1 = (int64_t)O * I + O;
+  {
+    KTimer kt(c, GN_KCLASS_OTHER, "moe_deltas", f4(2.0 * K * B * O + 3.0 * B * E));
+    HIP_OK(c, launch_moe_backward_deltas(gout, m.eout, m.prob, m.act, m.edz, m.dzg, B, O, E, K,
+                                         training ? 1 : 0, c->stream));
+  }
+  // gating and expert Dense backward: W grads = scale dz^T x, b grads = scale colsum(dz)
+  HIP_OK(c, dense_bwd_core(c, x, params, m.dzg, grads, grads + (int64_t)E * I, nullptr, B, I, E, scale,
+                           nullptr, 0));
+  for (int e = 0; e < E; ++e) {
+    float *gW = grads + (int64_t)E * I + E + e * e1;
+    HIP_OK(c, dense_bwd_core(c, x, nullptr, m.edz + (int64_t)e * B * O, gW, gW + (int64_t)O * I, nullptr, B,
+                             I, O, scale, nullptr, 0));
+  }
+  if (gin) {  // dx = dz_gate Wg + sum_e dz_e W_e
+    GemmArgs a{};
+    a.M = B; a.N = I; a.K = E;
+    a.A = m.dzg; a.lda = E; a.B = params; a.ldb = I;
+    a.C = gin; a.ldc = I; a.alpha = 1.f;
+    a.ws = c->scratch; a.ws_cap = c->scratch_floats;
+    {
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+      HIP_OK(c, launch_gemm('N', 'N', EPI_SCALE, a, c->stream));
+    }
+    for (int e = 0; e < E; ++e) {
+      GemmArgs d{};
+      d.M = B; d.N = I; d.K = O;
+      d.A = m.edz + (int64_t)e * B * O; d.lda = O; d.B = params + (int64_t)E * I + E + e * e1; d.ldb = I;
+      d.C = gin; d.ldc = I; d.alpha = 1.f;
+      d.aux = gin; d.ldaux = I;
+      d.ws = c->scratch; d.ws_cap = c->scratch_floats;
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
+      HIP_OK(c, launch_gemm('N', 'N', EPI_BIAS_ADD, d, c->stream));
+    }
+  }
+  return GN_OK;
+}

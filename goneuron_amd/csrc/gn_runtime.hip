@@ -291,11 +291,10 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
 // covered by the other's tiles.
 // ms / ms_cap: scratch of the kernels on the main stream (default: the
 // context's).
-static hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz,
-                                 float *gW, float *gB, float *gin, int B, int in, int out_n,
-                                 float scale, const float *gin_aux, int gin_deriv,
-                                 hipEvent_t dz_ready = nullptr, float *ms = nullptr,
-                                 size_t ms_cap = 0, const float *gin_colscale = nullptr) {
+hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz, float *gW,
+                          float *gB, float *gin, int B, int in, int out_n, float scale,
+                          const float *gin_aux, int gin_deriv, hipEvent_t dz_ready, float *ms,
+                          size_t ms_cap, const float *gin_colscale) {
   hipError_t e;
   if (!ms) {
     ms = c->scratch;

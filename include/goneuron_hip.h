@@ -427,10 +427,74 @@ int gn_embedding_forward(gn_ctx *ctx, const float *x, const float *E, float *out
  * table's gradient before adding a sample's rows, so gradE = scale * the rows
  * of the last sample of each worker chunk (`workers` chunks of ceil(B /
  * workers); with bad, the last sample the reference's loop still reaches).
- * At most 2048 contributing rows (chunks x T; GN_ERR_UNSUPPORTED beyond). */
+ * Contributing rows (chunks x T) above 2048 take a list in the context's
+ * scratch (2 ints per row; GN_ERR_UNSUPPORTED beyond 8M rows). */
 int gn_embedding_backward(gn_ctx *ctx, const float *gout, const int32_t *ids, const int32_t *bad,
                           float *gradE, int32_t B, int32_t T, int32_t V, int32_t D, int32_t workers,
                           float scale);
+
+/* AvgPool2D.ForwardWithArena / Backward (avgpool2d.go:137-474): B samples of
+ * C x H x W, k x k windows, stride, zero padding not counted in the mean. */
+int gn_avgpool2d_forward(gn_ctx *ctx, const float *x, float *out, int32_t B, int32_t C, int32_t H,
+                         int32_t W, int32_t k, int32_t stride, int32_t pad);
+int gn_avgpool2d_backward(gn_ctx *ctx, const float *gout, float *gin, int32_t B, int32_t C, int32_t H,
+                          int32_t W, int32_t k, int32_t stride, int32_t pad);
+/* RMSNorm.ForwardWithArena / Backward (rmsnorm.go:222-329) over `rows` rows of
+ * N: y = gamma x / rms, rms per row for the backward (eps 0 selects 1e-5);
+ * dx (may be NULL) follows the reference's formula; dgamma = scale * sums;
+ * work: rows x N floats. */
+int gn_rmsnorm_forward(gn_ctx *ctx, const float *x, const float *gamma, float *y, float *rms,
+                       int32_t rows, int32_t N, float eps);
+int gn_rmsnorm_backward(gn_ctx *ctx, const float *g, const float *x, const float *gamma, const float *rms,
+                        float *dx, float *dgamma, float *work, int32_t rows, int32_t N, float scale);
+/* SwiGLU.ForwardWithArena / Backward (swiglu.go:103-232): params = [W | V]
+ * (out x in each, no biases), y = swish(W x) * (V x); grads = [dW | dV]
+ * written (scale * sums); gin may be NULL; work: gn_swiglu_workspace floats
+ * shared by the forward and backward of one batch. */
+int gn_swiglu_workspace(int32_t B, int32_t out, int64_t *floats);
+int gn_swiglu_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work, int32_t B,
+                      int32_t in, int32_t out_size);
+int gn_swiglu_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout, float *grads,
+                       float *gin, float *work, int32_t B, int32_t in, int32_t out_size, float scale);
+/* BatchNorm2D.ForwardWithArena / Backward (batchnorm2d.go:255-666): B samples
+ * of C x HW; params = [gamma | beta] or NULL (affine = false).  training:
+ * each sample normalised by its own channel statistics (the reference runs one
+ * sample per Forward), running mean / var advanced once per sample in sample
+ * order; stats = 3 B C floats (mean, var, std) for the backward.  Inference
+ * uses the running statistics; its backward gives dx only and zero parameter
+ * gradients (batchnorm2d.go:525-551).  work: 2 B C floats. */
+int gn_batchnorm2d_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *stats,
+                           float *running_mean, float *running_var, int32_t B, int32_t C, int32_t HW,
+                           float eps, float momentum, int32_t training);
+int gn_batchnorm2d_backward(gn_ctx *ctx, const float *gout, const float *x, const float *params,
+                            const float *stats, const float *running_var, float *grads, float *gin,
+                            float *work, int32_t B, int32_t C, int32_t HW, float eps, int32_t training,
+                            float scale);
+/* SequenceUnroller(GRU) forward / backward (unroller.go:57-213,
+ * gru.go:192-703): x = B x T x I, params = [Wx (3H x I) | Wh (2H x H) | b
+ * (3H)], the reference's quirks kept (candidate weighted by 1 - u in the
+ * backward, no reset-gate delta, dWx from the last step's input, carried dh);
+ * return_sequences: out / gout hold every step's h.  work: gn_gru_workspace
+ * floats, shared by the forward and backward of one batch. */
+int gn_gru_workspace(int32_t B, int32_t T, int32_t I, int32_t H, int64_t *floats);
+int gn_gru_seq_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work, int32_t B,
+                       int32_t T, int32_t I, int32_t H, int32_t return_sequences);
+int gn_gru_seq_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout, float *grads,
+                        float *gin, float *work, int32_t B, int32_t T, int32_t I, int32_t H, float scale,
+                        int32_t return_sequences);
+/* MoE.ForwardWithArena / Backward (moe.go:140-313): params = [gating W (E x
+ * I), b | per expert W (O x I), b]; the top K experts by gate softmax
+ * (stable in index order for ties), LeakyReLU(0.1) experts.  training adds
+ * the layer's RNG gate noise: *noise is the stream's state (42 at
+ * construction), advanced by E draws per sample; and the load-balancing
+ * gradient.  work: gn_moe_workspace floats, shared by the forward and
+ * backward of one batch. */
+int gn_moe_workspace(int32_t B, int32_t I, int32_t O, int32_t E, int32_t K, int64_t *floats);
+int gn_moe_forward(gn_ctx *ctx, const float *x, const float *params, float *out, float *work, int32_t B,
+                   int32_t I, int32_t O, int32_t E, int32_t K, int32_t training, uint64_t *noise);
+int gn_moe_backward(gn_ctx *ctx, const float *x, const float *params, const float *gout, float *grads,
+                    float *gin, float *work, int32_t B, int32_t I, int32_t O, int32_t E, int32_t K,
+                    int32_t training, float scale);
 
 /* Generic fp32 MFMA GEMM: C[M,N] = alpha * op(A) op(B); trans flags as BLAS
  * (A is M x K row-major when transA == 0, K x M when 1; B is K x N when

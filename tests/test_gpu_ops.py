@@ -362,3 +362,201 @@ def test_embedding_ops(dev, oracle, B, T, V, D, workers, bad):
     np.testing.assert_array_equal(dout.get()[ok], out_r[ok])
     np.testing.assert_array_equal(dids.get()[ok], ids[ok])
     _close("gradE", dgE.get(), gr, 1e-6)
+
+
+# ---------------------------------------------------------------- AvgPool2D
+@pytest.mark.parametrize("B,C,HW,k,s,p", [(4, 3, 8, 2, 2, 0), (3, 2, 9, 3, 2, 1), (5, 4, 7, 3, 1, 1)])
+def test_avgpool2d_ops(dev, oracle, B, C, HW, k, s, p):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_AVGPOOL2D, in_channels=C, kernel=k, stride=s, padding=p,
+                                  in_size=C * HW * HW)], oracle.LOSS_MSE)
+    o = (HW + 2 * p - k) // s + 1
+    rng = np.random.default_rng(B * C + HW)
+    x = rng.normal(size=(B, C * HW * HW)).astype(np.float32)
+    g = rng.normal(size=(B, C * o * o)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, C * HW * HW, C * o * o)
+    dx, dg = DBuf(dev, x), DBuf(dev, g)
+    dout, dgin = _zeros(dev, (B, C * o * o)), _zeros(dev, (B, C * HW * HW))
+    check(dev.h, L.gn_avgpool2d_forward(dev.h, dx.p, dout.p, B, C, HW, HW, k, s, p))
+    check(dev.h, L.gn_avgpool2d_backward(dev.h, dg.p, dgin.p, B, C, HW, HW, k, s, p))
+    _close("out", dout.get(), out_r, 1e-6)
+    _close("gin", dgin.get(), gin_r, 1e-6)
+
+
+# ---------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("B,rows,N", [(4, 3, 16), (6, 1, 100), (2, 5, 33)])
+def test_rmsnorm_ops(dev, oracle, B, rows, N):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_RMSNORM, dim=N, in_size=rows * N)], oracle.LOSS_MSE)
+    rng = np.random.default_rng(rows * N + B)
+    p = (1 + 0.3 * rng.normal(size=N)).astype(np.float32)  # gamma away from 1 (Q19 differs there)
+    net.params[:] = p
+    x = (rng.normal(size=(B, rows * N)) + 0.2).astype(np.float32)
+    g = rng.normal(size=(B, rows * N)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, rows * N, rows * N)
+    gr = net.grads.copy()
+    R = B * rows
+    dx, dgam, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dy, drms, ddx, dgg, dwk = (_zeros(dev, (B, rows * N)), _zeros(dev, R), _zeros(dev, (B, rows * N)),
+                               _zeros(dev, N), _zeros(dev, (R, N)))
+    check(dev.h, L.gn_rmsnorm_forward(dev.h, dx.p, dgam.p, dy.p, drms.p, R, N, F(1e-5)))
+    check(dev.h, L.gn_rmsnorm_backward(dev.h, dg.p, dx.p, dgam.p, drms.p, ddx.p, dgg.p, dwk.p, R, N,
+                                       F(np.float32(1) / np.float32(B))))
+    _close("out", dy.get(), out_r)
+    _close("gin", ddx.get(), gin_r)
+    _close("dgamma", dgg.get(), gr)
+
+
+# ---------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("B,I,O", [(8, 16, 12), (5, 33, 7), (64, 128, 96)])
+def test_swiglu_ops(dev, oracle, B, I, O):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_SWIGLU, in_size=I, out_size=O)], oracle.LOSS_MSE)
+    rng = np.random.default_rng(I * O + B)
+    p = net.params.copy()  # the reference's init
+    x = rng.normal(size=(B, I)).astype(np.float32)
+    g = rng.normal(size=(B, O)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, I, O)
+    gr = net.grads.copy()
+    ws = C.c_int64()
+    check(None, L.gn_swiglu_workspace(B, O, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = _zeros(dev, (B, O)), _zeros(dev, p.shape), _zeros(dev, (B, I)), _zeros(dev, ws.value)
+    check(dev.h, L.gn_swiglu_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, I, O))
+    check(dev.h, L.gn_swiglu_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, I, O,
+                                      F(np.float32(1) / np.float32(B))))
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    got = dgr.get()
+    _close("dW", got[:I * O], gr[:I * O])
+    _close("dV", got[I * O:], gr[I * O:])
+
+
+# ---------------------------------------------------------------- BatchNorm2D
+@pytest.mark.parametrize("B,Cc,HW,affine,training", [(4, 3, 25, True, True), (6, 8, 16, False, True),
+                                                      (3, 5, 36, True, False)])
+def test_batchnorm2d_ops(dev, oracle, B, Cc, HW, affine, training):
+    """Training: per-sample statistics (Q22) and the running statistics
+    advanced per sample in sample order; inference: the running statistics,
+    dx only."""
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_BATCHNORM2D, in_channels=Cc, momentum=0.1, in_size=Cc * HW,
+                                  no_affine=int(not affine))], oracle.LOSS_MSE)
+    rng = np.random.default_rng(B * Cc + HW)
+    if affine:
+        p = np.concatenate([1 + 0.2 * rng.normal(size=Cc), 0.2 * rng.normal(size=Cc)]).astype(np.float32)
+        net.params[:] = p
+    x = (rng.normal(size=(B, Cc * HW)) * 1.5 + 0.3).astype(np.float32)
+    g = rng.normal(size=(B, Cc * HW)).astype(np.float32)
+    rm0, rv0 = np.zeros(Cc, np.float32), np.ones(Cc, np.float32)
+    if not training:
+        # running statistics from a training pass first, on both sides
+        net.accumulate_grad(x[::-1].copy(), g, B, Cc * HW, Cc * HW)
+        rm0, rv0 = net.running_stats(0)
+        net.set_training(False)
+    out_r, gin_r = net.accumulate_grad(x, g, B, Cc * HW, Cc * HW)
+    gr = net.grads.copy()
+    rm_r, rv_r = net.running_stats(0)
+    dx, dg = DBuf(dev, x), DBuf(dev, g)
+    dp = DBuf(dev, p) if affine else None
+    drm, drv = DBuf(dev, rm0), DBuf(dev, rv0)
+    dout, dst, dgin, dwk = (_zeros(dev, (B, Cc * HW)), _zeros(dev, 3 * B * Cc), _zeros(dev, (B, Cc * HW)),
+                            _zeros(dev, 2 * B * Cc))
+    dgr = _zeros(dev, 2 * Cc) if affine else None
+    pp = dp.p if affine else None
+    check(dev.h, L.gn_batchnorm2d_forward(dev.h, dx.p, pp, dout.p, dst.p, drm.p, drv.p, B, Cc, HW, F(1e-5),
+                                          F(0.1), int(training)))
+    check(dev.h, L.gn_batchnorm2d_backward(dev.h, dg.p, dx.p, pp, dst.p, drv.p, dgr.p if affine else None,
+                                           dgin.p, dwk.p, B, Cc, HW, F(1e-5), int(training),
+                                           F(np.float32(1) / np.float32(B))))
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    _close("running_mean", drm.get(), rm_r, 1e-5)
+    _close("running_var", drv.get(), rv_r, 1e-5)
+    if affine:
+        got = dgr.get()
+        if training:
+            _close("dgamma", got[:Cc], gr[:Cc])
+            _close("dbeta", got[Cc:], gr[Cc:])
+        else:
+            assert not got.any()
+
+
+# ---------------------------------------------------------------- SequenceUnroller(GRU)
+@pytest.mark.parametrize("B,T,I,H,seq", [(6, 8, 5, 12, 0), (4, 5, 7, 32, 1), (9, 12, 16, 64, 0)])
+def test_gru_seq_ops(dev, oracle, B, T, I, H, seq):
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_GRU_UNROLLER, in_size=I, out_size=H, seq_len=T,
+                                  return_sequences=seq)], oracle.LOSS_MSE)
+    rng = np.random.default_rng(T * H + I)
+    p = (rng.normal(size=net.n) * 0.2).astype(np.float32)
+    net.params[:] = p
+    x = rng.normal(size=(B, T * I)).astype(np.float32)
+    OL = T * H if seq else H
+    g = rng.normal(size=(B, OL)).astype(np.float32)
+    out_r, gin_r = net.accumulate_grad(x, g, B, T * I, OL)
+    gr = net.grads.copy()
+    ws = C.c_int64()
+    check(None, L.gn_gru_workspace(B, T, I, H, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = (_zeros(dev, (B, OL)), _zeros(dev, p.shape), _zeros(dev, (B, T * I)),
+                            _zeros(dev, ws.value))
+    check(dev.h, L.gn_gru_seq_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, T, I, H, seq))
+    check(dev.h, L.gn_gru_seq_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, T, I, H,
+                                       F(np.float32(1) / np.float32(B)), seq))
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    got = dgr.get()
+    nwx, nwh = 3 * H * I, 2 * H * H
+    for gi, gname in enumerate("urc"):
+        sl = slice(gi * H * I, (gi + 1) * H * I)
+        if gname == "r":  # Q24: the reset gate's input weights get no gradient
+            assert not got[sl].any() and not gr[sl].any()
+            continue
+        _close("Wx_" + gname, got[sl], gr[sl])
+    for gi, gname in enumerate("ur"):
+        sl = slice(nwx + gi * H * H, nwx + (gi + 1) * H * H)
+        _close("Wh_" + gname, got[sl], gr[sl])
+    _close("b", got[nwx + nwh:], gr[nwx + nwh:])
+
+
+# ---------------------------------------------------------------- MoE
+@pytest.mark.parametrize("B,I,O,E,K,training", [(8, 10, 6, 4, 2, True), (12, 16, 8, 8, 3, False),
+                                                 (5, 7, 5, 3, 1, True)])
+def test_moe_ops(dev, oracle, B, I, O, E, K, training):
+    """Routes bit-exact (gate noise from the layer's RNG(42) stream in
+    training, the stream advanced by E draws per sample)."""
+    L, check = _lib()
+    net = oracle.Net([oracle.spec(oracle.LAYER_MOE, in_size=I, out_size=O, num_experts=E, top_k=K)],
+                     oracle.LOSS_MSE)
+    net.set_training(training)
+    rng = np.random.default_rng(B * E + K)
+    p = (rng.normal(size=net.n) * 0.4).astype(np.float32)  # the reference starts at 0: live experts
+    net.params[:] = p
+    x = rng.normal(size=(B, I)).astype(np.float32)
+    g = rng.normal(size=(B, O)).astype(np.float32)
+    net.routes(0)
+    out_r, gin_r = net.accumulate_grad(x, g, B, I, O)
+    gr = net.grads.copy()
+    routes_r = net.routes(0).reshape(B, K)
+    ws = C.c_int64()
+    check(None, L.gn_moe_workspace(B, I, O, E, K, C.byref(ws)))
+    dx, dp, dg = DBuf(dev, x), DBuf(dev, p), DBuf(dev, g)
+    dout, dgr, dgin, dwk = _zeros(dev, (B, O)), _zeros(dev, p.shape), _zeros(dev, (B, I)), _zeros(dev, ws.value)
+    noise = C.c_uint64(42)
+    check(dev.h, L.gn_moe_forward(dev.h, dx.p, dp.p, dout.p, dwk.p, B, I, O, E, K, int(training),
+                                  C.byref(noise)))
+    check(dev.h, L.gn_moe_backward(dev.h, dx.p, dp.p, dg.p, dgr.p, dgin.p, dwk.p, B, I, O, E, K, int(training),
+                                   F(np.float32(1) / np.float32(B))))
+    s = 42
+    if training:
+        for _ in range(B * E):
+            s = (s * 6364136223846793005 + 1) % (1 << 64)
+    assert noise.value == s
+    # the routes sit at the end of the workspace, after the float regions
+    wk = dwk.get()
+    off = sum(-(-n // 64) * 64 for n in (B * E, B * E, B * E, E * B * O, E * B * O))
+    np.testing.assert_array_equal(wk[off:off + B * K].view(np.int32).reshape(B, K), routes_r)
+    _close("out", dout.get(), out_r)
+    _close("gin", dgin.get(), gin_r)
+    _close("grads", dgr.get(), gr)
