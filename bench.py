@@ -346,8 +346,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="wide", choices=["mlp", "cnn", "wide", "gpt", "lstm", "gru", "cnn2"],
-                    help="headline workload (the `value` of the line); gru and cnn2 are not "
+    ap.add_argument("--config", default="wide",
+                    choices=["mlp", "cnn", "wide", "gpt", "lstm", "gru", "cnn2", "gpt_long"],
+                    help="headline workload (the `value` of the line); gru, cnn2 and gpt_long are not "
                          "BASELINE configs")
     ap.add_argument("--only", action="store_true", help="time the headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")

@@ -90,9 +90,18 @@ def cnn2(B=128):
                         dense(4096, 10, "softmax", True)])
 
 
+def gpt_long(B=16):
+    """C4 with sequences of 256 tokens (not a BASELINE config): beyond the
+    fused attention kernels' 128, so attention runs as batched GEMMs over the
+    (sample, head) pairs with materialised scores."""
+    cfg = gpt(B=B, T=256)
+    cfg.update(num=8, name="gpt_long")
+    return cfg
+
+
 CONFIGS = {"mlp": mlp, "cnn": cnn, "wide": wide, "gpt": gpt, "lstm": lstm}
 # further workloads bench.py times on request (--config), outside the default line
-EXTRA = {"gru": gru, "cnn2": cnn2}
+EXTRA = {"gru": gru, "cnn2": cnn2, "gpt_long": gpt_long}
 
 
 def get(name):
