@@ -129,6 +129,20 @@ hipError_t launch_out_rows_reg(float *out, const float *y, float *dz, float *los
                                int row_act, int deriv, int loss_kind, const int32_t *bad, int workers,
                                hipStream_t s);
 enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMWISE = 3 };
+// The output Dense layer of a training pass with few outputs as two kernels:
+// tail_fwd = the forward GEMM (bias included) + launch_out_rows_reg's rows;
+// tail_bwd = dW (scale dz^T x), db (scale colsum dz), dX (dz W with the dX
+// GEMM's epilogue: cfac, then act' of aux) and, when gB_below is given, the
+// bias gradient of the Dense whose dz that dX is (scale colsum gin).
+// Supported: 1 <= C <= 32 outputs, in % 4 == 0, x and W 16-byte aligned
+// (hipErrorInvalidValue otherwise).
+bool tail_supported(int C, int in);
+hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, const float *y, float *out,
+                           float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
+                           int loss_kind, const int32_t *bad, int workers, hipStream_t s);
+hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
+                           const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
+                           int C, float scale, hipStream_t s);
 
 // dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
 hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);

@@ -560,6 +560,11 @@ struct gn_model {
   // train steps update each layer's parameters on ctx->aux as soon as that
   // layer's backward is done, overlapping Adam with the rest of the backward
   bool overlap_adam = true;
+  // the output Dense layer of training passes as the two fused kernels of
+  // launch_tail_fwd / launch_tail_bwd when it qualifies (gn_debug_fused_tail);
+  // tail_now: the current pass uses them
+  bool tail_on = true;
+  bool tail_now = false;
   std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
   std::vector<hipEvent_t> dz_ev;    // one per layer: its dz is ready (no timing)
   std::vector<hipEvent_t> dw_ev;    // one per layer: its dW and bias sums on ctx->aux are done
@@ -1774,6 +1779,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         const float *W = M->params + R.poff;
         const float *b = W + (int64_t)R.d.in_size * R.d.out_size;
         const bool last = (i == n - 1);
+        if (last && for_loss && M->tail_now) break;  // launch_tail_fwd computes z with the loss rows
         int fwd = R.ap.fwd;
         if (R.ap.jac || (last && for_loss)) fwd = F_IDENTITY;  // row kernel finishes it
         // a Dropout above in training mode: its output from the GEMM's split-K
@@ -2027,6 +2033,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   std::vector<char> dw_aux(n, 0);  // layer i's dW went to ctx->aux
   bool is_dz = true;  // gout of the current layer already holds dz
   bool drop_done = false;  // the Dropout below was folded into the Dense above's dX epilogue
+  int bias_done = -1;      // a Dense layer whose bias gradient launch_tail_bwd wrote
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
     const float *in = i == 0 ? x : M->L[i - 1].out;
@@ -2071,9 +2078,25 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         // with the per-layer Adam on aux (large models), dW and db run there
         // next to dX; the layer's Adam is queued behind them.  The per-kernel
         // timing pass keeps them on one stream, so each GEMM is timed alone.
+        if (i == n - 1 && M->tail_now) {
+          // every gradient of the output layer in one kernel, and the bias
+          // gradient of the Dense whose dz its dX is
+          LayerRT *dn = next_dz ? (gin == below->gout ? below : &M->L[i - 2]) : nullptr;
+          float *gb_below = dn ? M->grads + dn->poff + (int64_t)dn->d.in_size * dn->d.out_size : nullptr;
+          const int C = R.d.out_size, nin = R.d.in_size;
+          KTimer kt(c, GN_KCLASS_OTHER, "tail_bwd",
+                    f4(2.0 * B * nin + 2.0 * C * nin + B * C + C + (gin ? (aux ? 2.0 : 1.0) * B * nin : 0.0) +
+                       (gb_below ? nin : 0)));
+          HIP_OK(c, launch_tail_bwd(in, W, dz, gW, gB, gin, aux, deriv, cfac, gb_below, B, nin, C, scale,
+                                    c->stream));
+          bias_done = dn ? (int)(dn - &M->L[0]) : -1;
+          is_dz = next_dz;
+          break;
+        }
         const bool side = ac && gin && !c->timing;
-        HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, gB, gin, B, R.d.in_size, R.d.out_size, scale,
-                                 aux, deriv, side ? M->dz_ev[i] : nullptr, nullptr, 0, cfac));
+        HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, i == bias_done ? nullptr : gB, gin, B, R.d.in_size,
+                                 R.d.out_size, scale, aux, deriv, side ? M->dz_ev[i] : nullptr, nullptr, 0,
+                                 cfac));
         if (side) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
           dw_aux[i] = 1;
@@ -2488,6 +2511,19 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   return GN_OK;
 }
 
+// The fused output-layer kernels serve a training pass when the output layer
+// is a Dense with few outputs whose products are small enough that the
+// GEMMs' launches, not their work, would set their time.
+constexpr double kTailMaxMacs = 16.0 * (1 << 20);
+static bool tail_eligible(const gn_model *M, const float *in_ptr, int B) {
+  const LayerRT &O = M->L.back();
+  if (!M->tail_on || O.d.kind != GN_LAYER_DENSE || !O.gout) return false;
+  const int C = O.d.out_size, in = O.d.in_size;
+  if (!tail_supported(C, in) || (double)B * in * C > kTailMaxMacs) return false;
+  const float *W = M->params + O.poff;
+  return ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(in_ptr)) & 15) == 0;
+}
+
 static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
                             const AdamCoef *ac = nullptr) {
   gn_ctx *c = M->ctx;
@@ -2496,13 +2532,25 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   int rc = pass_flags(M, B, true);
   if (rc) return rc;
   M->last_predict = false;
+  LayerRT &O = M->L.back();
+  const int n = (int)M->L.size();
+  int below = n - 2;  // Flatten aliases its input
+  while (below >= 0 && M->L[below].d.kind == GN_LAYER_FLATTEN) --below;
+  const float *oin = below >= 0 ? M->L[below].out : x;  // the output layer's input
+  M->tail_now = tail_eligible(M, oin, B);
   rc = model_forward(M, x, B, true);
   if (rc) return rc;
-  LayerRT &O = M->L.back();
   int row_act = O.ap.row_act;
   const int32_t *bad = M->emb >= 0 ? M->L[M->emb].bad : nullptr;
-  {  // read z and y, write the activation output and dz, one loss per row (the batch loss is
-     // summed from the rows when it is read, gn_model_read_loss)
+  if (M->tail_now) {  // read x, W and y; write the activation output, dz and the row losses
+    const float *W = M->params + O.poff;
+    const int in = O.d.in_size, C = O.d.out_size;
+    KTimer kt(c, GN_KCLASS_OTHER, "tail_fwd",
+              f4((double)B * in + (double)C * in + C + 3.0 * B * C + B));
+    HIP_OK(c, launch_tail_fwd(oin, W, W + (int64_t)in * C, y, O.out, O.gout, M->loss_rows, B, in, C, row_act,
+                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
+  } else {  // read z and y, write the activation output and dz, one loss per row (the batch loss is
+            // summed from the rows when it is read, gn_model_read_loss)
     KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * O.out_len + B));
     const hipError_t e = launch_out_rows_reg(O.out, y, O.gout, M->loss_rows, B, O.out_len, row_act,
                                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream);
@@ -2718,6 +2766,15 @@ extern "C" int gn_model_graph_count(gn_model *M, int32_t *n) {
 extern "C" int gn_debug_lstm_spin_limit(gn_model *M, int32_t polls) {
   if (!M) return GN_ERR_INVALID;
   M->lstm_spin_limit = polls;
+  return GN_OK;
+}
+
+extern "C" int gn_debug_fused_tail(gn_model *M, int32_t on) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
+  M->tail_on = on != 0;
+  drop_graphs(M);  // captured passes hold the other path
   return GN_OK;
 }
 

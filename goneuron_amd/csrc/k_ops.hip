@@ -523,66 +523,59 @@ __device__ __forceinline__ float group_max(float v, float *sh, int slot) {
   return m;
 }
 
-template <int G, int NT>
-__global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo,
-                                                          const float *__restrict__ y,
-                                                          float *__restrict__ dz,
-                                                          float *__restrict__ loss_rows, int B,
-                                                          int C, int row_act, int fwd, int deriv,
-                                                          int loss_kind,
-                                                          const int32_t *__restrict__ bad, int chunk) {
-  __shared__ float sh[16 * (NT / G) + 16];
-  constexpr int RPB = NT / G;
-  const int r = threadIdx.x / G, t = threadIdx.x % G;
-  const int b = blockIdx.x * RPB + r;
-  const bool row_ok = b < B;
-  bool valid = true, keep_loss = true;
-  if (bad && row_ok) {
-    if (chunk > 0) {
-      const int c0 = (b / chunk) * chunk, c1 = min(B, c0 + chunk);
-      for (int i = c0; i < c1; ++i)
-        if (bad[i]) {
-          keep_loss = false;
-          if (i <= b) valid = false;
-        }
-    } else {
-      valid = keep_loss = !bad[b];
-    }
+// The validity of row b under the W-worker split (net.go:412-436): `valid`
+// keeps its gradient (no bad sample at or before it in its worker's chunk),
+// `keep_loss` its loss (no bad sample in the chunk); without a chunk split
+// only the row's own flag counts.
+__device__ __forceinline__ void row_validity(const int32_t *__restrict__ bad, int b, int B, int chunk,
+                                             bool &valid, bool &keep_loss) {
+  valid = keep_loss = true;
+  if (!bad) return;
+  if (chunk > 0) {
+    const int c0 = (b / chunk) * chunk, c1 = min(B, c0 + chunk);
+    for (int i = c0; i < c1; ++i)
+      if (bad[i]) {
+        keep_loss = false;
+        if (i <= b) valid = false;
+      }
+  } else {
+    valid = keep_loss = !bad[b];
   }
-  float o[OR_PER], yv[OR_PER], d[OR_PER];
-  const float *zr = zo + (size_t)(row_ok ? b : 0) * C, *yr = y + (size_t)(row_ok ? b : 0) * C;
-#pragma unroll
-  for (int k = 0; k < OR_PER; ++k) {
-    const int i = t + k * G;
-    const bool in = row_ok && i < C;
-    o[k] = in ? zr[i] : 0.f;
-    yv[k] = in ? yr[i] : 0.f;
-  }
+}
+
+// One output row held in registers by a group of G threads (PER values each,
+// element t + k*G): the row activation, the loss and the loss gradient through
+// the activation's Jacobian / derivative.  o holds z on entry and the
+// activation output on return; d receives dz.  Returns the row's loss.
+template <int G, int PER>
+__device__ __forceinline__ float out_row_math(float (&o)[PER], const float (&yv)[PER], float (&d)[PER],
+                                              int t, int C, int row_act, int fwd, int deriv,
+                                              int loss_kind, float *sh, int r) {
   // row activation (activations.go:161-183, 204-236)
   if (row_act == ROW_SOFTMAX || row_act == ROW_LOGSOFTMAX) {
     float mx = -__builtin_inff();
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) mx = fmaxf(mx, o[k]);
     mx = group_max<G>(mx, sh, r);
-    float ef[OR_PER], sm = 0.f;
+    float ef[PER], sm = 0.f;
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k) {
+    for (int k = 0; k < PER; ++k) {
       ef[k] = t + k * G < C ? or_exp_diff(o[k], mx) : 0.f;
       sm += ef[k];
     }
     sm = group_sum<G>(sm, sh, r);
     if (row_act == ROW_SOFTMAX) {
 #pragma unroll
-      for (int k = 0; k < OR_PER; ++k) o[k] = ef[k] / sm;
+      for (int k = 0; k < PER; ++k) o[k] = ef[k] / sm;
     } else {
       const float ls = or_log(sm);
 #pragma unroll
-      for (int k = 0; k < OR_PER; ++k) o[k] = o[k] - mx - ls;
+      for (int k = 0; k < PER; ++k) o[k] = o[k] - mx - ls;
     }
   } else if (row_act == ROW_ELEMWISE) {
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) o[k] = or_fwd(o[k], fwd);
   }
   // loss and its gradient (loss.go:53-105, 120-178)
@@ -590,7 +583,7 @@ __global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo
   if (loss_kind == GN_LOSS_MSE) {
     const float factor = 2.0f / (float)C;
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k) {
+    for (int k = 0; k < PER; ++k) {
       const bool in = t + k * G < C;
       const float df = o[k] - yv[k];
       l += in ? df * df : 0.f;
@@ -599,7 +592,7 @@ __global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo
     l = group_sum<G>(l, sh, r) / (float)C;
   } else {
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k) {
+    for (int k = 0; k < PER; ++k) {
       if (t + k * G < C) {
         float pv = o[k];
         if (pv < 1e-10f) pv = 1e-10f;
@@ -615,25 +608,53 @@ __global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo
   if (row_act == ROW_SOFTMAX) {
     float s1 = 0.f;
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) s1 += d[k] * o[k];
     s1 = group_sum<G>(s1, sh, r);
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k) d[k] = d[k] * o[k] - o[k] * s1;
+    for (int k = 0; k < PER; ++k) d[k] = d[k] * o[k] - o[k] * s1;
   } else if (row_act == ROW_LOGSOFTMAX) {
     float s1 = 0.f;
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) s1 += d[k];
     s1 = group_sum<G>(s1, sh, r);
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) d[k] = d[k] - or_exp(o[k]) * s1;
   } else {
 #pragma unroll
-    for (int k = 0; k < OR_PER; ++k)
+    for (int k = 0; k < PER; ++k)
       if (t + k * G < C) d[k] = d[k] * or_deriv(o[k], deriv);
   }
+  return l;
+}
+
+template <int G, int NT>
+__global__ __launch_bounds__(NT) void out_rows_reg_kernel(float *__restrict__ zo,
+                                                          const float *__restrict__ y,
+                                                          float *__restrict__ dz,
+                                                          float *__restrict__ loss_rows, int B,
+                                                          int C, int row_act, int fwd, int deriv,
+                                                          int loss_kind,
+                                                          const int32_t *__restrict__ bad, int chunk) {
+  __shared__ float sh[16 * (NT / G) + 16];
+  constexpr int RPB = NT / G;
+  const int r = threadIdx.x / G, t = threadIdx.x % G;
+  const int b = blockIdx.x * RPB + r;
+  const bool row_ok = b < B;
+  bool valid = true, keep_loss = true;
+  if (row_ok) row_validity(bad, b, B, chunk, valid, keep_loss);
+  float o[OR_PER], yv[OR_PER], d[OR_PER];
+  const float *zr = zo + (size_t)(row_ok ? b : 0) * C, *yr = y + (size_t)(row_ok ? b : 0) * C;
+#pragma unroll
+  for (int k = 0; k < OR_PER; ++k) {
+    const int i = t + k * G;
+    const bool in = row_ok && i < C;
+    o[k] = in ? zr[i] : 0.f;
+    yv[k] = in ? yr[i] : 0.f;
+  }
+  const float l = out_row_math<G, OR_PER>(o, yv, d, t, C, row_act, fwd, deriv, loss_kind, sh, r);
   if (row_ok) {
     float *orow = zo + (size_t)b * C, *drow = dz + (size_t)b * C;
 #pragma unroll
@@ -669,6 +690,275 @@ hipError_t launch_out_rows_reg(float *out, const float *y, float *dz, float *los
   } else {
     return hipErrorNotSupported;
   }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The output Dense layer of a training pass when it has few outputs
+// (C <= TAIL_MAXC): two kernels instead of the forward GEMM, the loss rows,
+// the dW GEMM, the bias sums and the dX GEMM, whose launches cost more than
+// their work at these sizes.
+// ---------------------------------------------------------------------------
+
+// Sums of 64 values over the 64 lanes of a wave: v[j] of every lane summed,
+// the total of value j left in lane j (a halving butterfly: 63 shuffles
+// instead of 64 x 6; the tree is fixed, so the sums are deterministic).
+template <int OFF, int N>
+__device__ __forceinline__ void lane_sums_step(float (&v)[64], int lane) {
+  const bool up = (lane & OFF) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float send = up ? v[i] : v[i + N / 2];
+    const float keep = up ? v[i + N / 2] : v[i];
+    v[i] = keep + __shfl_xor(send, OFF, 64);
+  }
+}
+__device__ __forceinline__ float lane_sums(float (&v)[64], int lane) {
+  lane_sums_step<32, 64>(v, lane);
+  lane_sums_step<16, 32>(v, lane);
+  lane_sums_step<8, 16>(v, lane);
+  lane_sums_step<4, 8>(v, lane);
+  lane_sums_step<2, 4>(v, lane);
+  lane_sums_step<1, 2>(v, lane);
+  return v[0];
+}
+
+// Forward (z = x W^T + b, layer.go:405-470) fused with the loss rows: a block
+// of NT threads takes RB rows (RB * CM = 64), its threads split K in float4
+// steps (W's rows are read once per block), the waves' partial sums meet in
+// LDS in wave order, and wave w then runs out_row_math on row w (and w + NW)
+// with one element per lane; targets are loaded before the K loop.  Rows
+// past B are computed on the last row and not stored.
+template <int CM, int RB, int NT>
+__global__ __launch_bounds__(NT) void tail_fwd_kernel(
+    const float *__restrict__ x, const float *__restrict__ W, const float *__restrict__ bias,
+    const float *__restrict__ y, float *__restrict__ out, float *__restrict__ dz,
+    float *__restrict__ loss_rows, int B, int in, int C, int row_act, int fwd, int deriv,
+    int loss_kind, const int32_t *__restrict__ bad, int chunk) {
+  static_assert(CM * RB == 64, "one partial sum per lane");
+  constexpr int NW = NT / 64, RPW = (RB + NW - 1) / NW;
+  __shared__ float red[NW][64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int b0 = blockIdx.x * RB;
+  const bool in_row = lane < C;
+  float yreg[RPW];
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int r = w + q * NW, b = b0 + r;
+    yreg[q] = r < RB && b < B && in_row ? y[(size_t)b * C + lane] : 0.f;
+  }
+  const float bv = in_row ? bias[lane] : 0.f;
+  const int in4 = in >> 2;
+  const float4 *__restrict__ W4 = reinterpret_cast<const float4 *>(W);
+  const float4 *xr[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+    xr[r] = reinterpret_cast<const float4 *>(x + (size_t)min(b0 + r, B - 1) * in);
+  float acc[64];
+#pragma unroll
+  for (int j = 0; j < 64; ++j) acc[j] = 0.f;
+#pragma unroll(CM <= 4 ? 2 : 1)
+  for (int k4 = t; k4 < in4; k4 += NT) {
+    float4 wv[CM], xv[RB];
+#pragma unroll
+    for (int o = 0; o < CM; ++o) wv[o] = o < C ? W4[(size_t)o * in4 + k4] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) xv[r] = xr[r][k4];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int o = 0; o < CM; ++o) {
+        float a = acc[r * CM + o];
+        a += xv[r].x * wv[o].x;
+        a += xv[r].y * wv[o].y;
+        a += xv[r].z * wv[o].z;
+        a += xv[r].w * wv[o].w;
+        acc[r * CM + o] = a;
+      }
+  }
+  red[w][lane] = lane_sums(acc, lane);  // lane j: row j / CM, output j % CM
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int r = w + q * NW;
+    if (r >= RB) break;
+    const int b = b0 + r;
+    const bool row_ok = b < B;
+    const int j = r * CM + lane;
+    float z = 0.f;
+    if (in_row) {
+      z = red[0][j];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) z += red[v][j];
+      z += bv;
+    }
+    float o[1] = {z}, yv[1] = {yreg[q]}, d[1];
+    bool valid = true, keep_loss = true;
+    if (row_ok) row_validity(bad, b, B, chunk, valid, keep_loss);
+    const float l = out_row_math<64, 1>(o, yv, d, lane, C, row_act, fwd, deriv, loss_kind, nullptr, 0);
+    if (row_ok) {
+      if (in_row) {
+        out[(size_t)b * C + lane] = o[0];
+        dz[(size_t)b * C + lane] = valid ? d[0] : 0.0f;
+      }
+      if (lane == 0) loss_rows[b] = keep_loss ? l : 0.0f;
+    }
+  }
+}
+
+// Backward of the same layer: gW = scale dz^T x, gB = scale colsum(dz) and
+// gin = dz W with the dX GEMM's epilogue (a Dropout's factor, then act' of
+// the layer below from its saved output), plus, when that layer is a Dense
+// whose dz gin is, its bias gradient gB_below = scale colsum(gin).  A block
+// of NT / 64 waves owns 64 columns of x / gin over every row (lane = column);
+// the rows go in 64-row chunks whose dz rows are staged in LDS (zero past C),
+// each wave taking 64 / (NT / 64) consecutive rows of a chunk with their x
+// (and saved-output) loads issued together; the waves' partial sums meet in
+// a fixed LDS tree.
+// gB comes from block 0.
+constexpr int TAIL_MAXC = 32;
+constexpr int TAIL_ROWS = 64;
+template <int CM, int NT>
+__global__ __launch_bounds__(NT) void tail_bwd_kernel(
+    const float *__restrict__ x, const float *__restrict__ W, const float *__restrict__ dz,
+    float *__restrict__ gW, float *__restrict__ gB, float *__restrict__ gin,
+    const float *__restrict__ aux, int deriv, const float *__restrict__ cfac,
+    float *__restrict__ gB_below, int B, int in, int C, float scale) {
+  constexpr int NW = NT / 64, RPW = TAIL_ROWS / NW;
+  __shared__ float dzs[TAIL_ROWS * CM];
+  __shared__ float part[NW / 2][CM + 1][64];  // the tree's upper halves (row CM: gin sums)
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  const bool cok = col < in;
+  const int cc = cok ? col : in - 1;
+  const bool daux = gin && aux && deriv != D_ONE;
+  float wcol[CM], acc[CM + 1];  // acc[CM]: this wave's sum of gin
+#pragma unroll
+  for (int o = 0; o < CM; ++o) {
+    wcol[o] = o < C ? W[(size_t)o * in + cc] : 0.f;
+    acc[o] = 0.f;
+  }
+  acc[CM] = 0.f;
+  const float cf = cfac ? cfac[cc] : 1.0f;
+  for (int r0 = 0; r0 < B; r0 += TAIL_ROWS) {
+    const int nr = min(TAIL_ROWS, B - r0);
+    __syncthreads();
+    for (int i = t; i < TAIL_ROWS * CM; i += NT) {
+      const int r = i / CM, o = i % CM;
+      dzs[i] = r < nr && o < C ? dz[(size_t)(r0 + r) * C + o] : 0.f;
+    }
+    __syncthreads();
+    float xv[RPW], av[RPW];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rr = w * RPW + q;
+      const int r = r0 + min(rr, nr - 1);
+      xv[q] = x[(size_t)r * in + cc];
+      av[q] = daux ? aux[(size_t)r * in + cc] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rr = w * RPW + q;
+      if (rr >= nr) break;
+      const float *dr = dzs + rr * CM;
+      float sd = 0.f;
+#pragma unroll
+      for (int o = 0; o < CM; ++o) {
+        const float dv = dr[o];
+        acc[o] += dv * xv[q];
+        sd += dv * wcol[o];
+      }
+      if (gin) {
+        float g = sd;
+        if (aux) {  // the dX GEMM's EPI_DACT epilogue
+          if (cfac) g = g * cf;
+          g = deriv == D_ONE ? g * 1.0f : g * deriv_of(av[q], deriv);
+        } else {
+          g = g * 1.0f;  // EPI_SCALE with alpha 1
+        }
+        if (cok) gin[(size_t)(r0 + rr) * in + col] = g;
+        acc[CM] += g;
+      }
+    }
+  }
+  // wave w adds wave w + h's sums, h = 8, 4, 2, 1
+#pragma unroll
+  for (int h = NW / 2; h >= 1; h >>= 1) {
+    __syncthreads();
+    if (w >= h && w < 2 * h) {
+#pragma unroll
+      for (int o = 0; o <= CM; ++o) part[w - h][o][lane] = acc[o];
+    }
+    __syncthreads();
+    if (w < h) {
+#pragma unroll
+      for (int o = 0; o <= CM; ++o) acc[o] += part[w][o][lane];
+    }
+  }
+  if (w == 0 && cok) {
+#pragma unroll
+    for (int o = 0; o < CM; ++o)
+      if (o < C) gW[(size_t)o * in + col] = acc[o] * scale;
+    if (gB_below) gB_below[col] = acc[CM] * scale;
+  }
+  if (gB && blockIdx.x == 0) {  // NT / 32 row ranges per output, added in order
+    constexpr int P = NT / TAIL_MAXC;
+    __syncthreads();
+    float *bs = &part[0][0][0];
+    const int per = (B + P - 1) / P;
+    if (t < P * C) {
+      const int o = t % C, q = t / C;
+      float s = 0.f;
+      for (int r = q * per; r < min(B, (q + 1) * per); ++r) s += dz[(size_t)r * C + o];
+      bs[q * TAIL_MAXC + o] = s;
+    }
+    __syncthreads();
+    if (t < C) {
+      float s = bs[t];
+      for (int q = 1; q < P; ++q) s += bs[q * TAIL_MAXC + t];
+      gB[t] = s * scale;
+    }
+  }
+}
+
+bool tail_supported(int C, int in) { return C >= 1 && C <= TAIL_MAXC && in >= 1 && in % 4 == 0; }
+
+hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, const float *y, float *out,
+                           float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
+                           int loss_kind, const int32_t *bad, int workers, hipStream_t s) {
+  if (B <= 0) return hipSuccess;
+  if (!tail_supported(C, in) || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(W) & 15))
+    return hipErrorInvalidValue;
+  const int fwd = row_act >> 8;
+  const int Wk = workers < 1 ? 1 : (workers > B ? B : workers);
+  const int chunk = workers > 1 ? (B + Wk - 1) / Wk : 0;
+  if (C <= 4)
+    hipLaunchKernelGGL((tail_fwd_kernel<4, 16, 512>), dim3((B + 15) / 16), dim3(512), 0, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  else if (C <= 16)
+    hipLaunchKernelGGL((tail_fwd_kernel<16, 4, 512>), dim3((B + 3) / 4), dim3(512), 0, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  else
+    hipLaunchKernelGGL((tail_fwd_kernel<32, 2, 512>), dim3((B + 1) / 2), dim3(512), 0, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  return hipGetLastError();
+}
+
+hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
+                           const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
+                           int C, float scale, hipStream_t s) {
+  if (B <= 0) return hipSuccess;
+  if (!tail_supported(C, in)) return hipErrorInvalidValue;
+  const dim3 g((in + 63) / 64);
+  if (C <= 4)
+    hipLaunchKernelGGL((tail_bwd_kernel<4, 1024>), g, dim3(1024), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
+                       gB_below, B, in, C, scale);
+  else if (C <= 16)
+    hipLaunchKernelGGL((tail_bwd_kernel<16, 1024>), g, dim3(1024), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
+                       gB_below, B, in, C, scale);
+  else
+    hipLaunchKernelGGL((tail_bwd_kernel<32, 512>), g, dim3(512), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
+                       gB_below, B, in, C, scale);
   return hipGetLastError();
 }
 

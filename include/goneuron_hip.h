@@ -206,6 +206,12 @@ int gn_debug_lstm_spin_limit(gn_model *model, int32_t polls);
  * kernel clips the chain instead; 0 forces that path, whose results equal
  * the overlapped path's bit for bit. */
 int gn_debug_lstm_clip_bail(gn_model *model, int32_t polls);
+/* Test hook (no counterpart in the reference): on = 0 makes training passes
+ * run the output Dense layer through its GEMMs, loss-row and column-sum
+ * kernels even where it qualifies for the two fused output-layer kernels
+ * (at most 32 outputs, input width a multiple of 4); 1 (the default) allows
+ * them.  Both paths compute the same step to float32 rounding. */
+int gn_debug_fused_tail(gn_model *model, int32_t on);
 /* Forward + backward + average only (grads valid, no Adam step). */
 int gn_model_accumulate_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
 /* Network.Step (net.go:260-284): Adam.NewStep + StepInPlace on the arena. */
