@@ -140,9 +140,13 @@ bool tail_supported(int C, int in);
 hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, const float *y, float *out,
                            float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
                            int loss_kind, const int32_t *bad, int workers, hipStream_t s);
+// pool_arg / pool_gin: gin is the gradient of a Flatten over a 2x2 stride-2
+// MaxPool2D with pH x pW input planes (even); the values go through the
+// pool's switches straight into pool_gin, its input gradient (gin unused).
 hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
                            const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
-                           int C, float scale, hipStream_t s);
+                           int C, float scale, hipStream_t s, const int32_t *pool_arg = nullptr,
+                           float *pool_gin = nullptr, int pH = 0, int pW = 0);
 
 // dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
 hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);
@@ -170,8 +174,12 @@ struct ConvShape {
 struct PoolShape {
   int C, k, stride, pad, H, W, oH, oW;
 };
+// pool_out / pool_arg: a 2x2 stride-2 MaxPool2D over the conv output computed
+// in the same pass (conv_fwd_pool_fusable shapes only)
 hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, float *out,
-                           const ConvShape &s, int B, int fwd, hipStream_t st);
+                           const ConvShape &s, int B, int fwd, hipStream_t st, float *pool_out = nullptr,
+                           int32_t *pool_arg = nullptr);
+bool conv_fwd_pool_fusable(const ConvShape &s, const PoolShape &p, int B);
 // grad = [dW | db] (scaled), dz = gout * act'(out) formed on the fly
 hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
                              const ConvShape &s, int B, int deriv, float scale, float *ws,

@@ -1771,6 +1771,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
   const float *cur = x;
   bool pe_done = false;  // the PositionalEncoding output was written with the embedding rows
   bool drop_done = false;  // the Dropout's output was written by the Dense GEMM below it
+  bool pool_done = false;  // the MaxPool2D's outputs were written by the Conv2D below it
   const int n = (int)M->L.size();
   for (int i = 0; i < n; ++i) {
     LayerRT &R = M->L[i];
@@ -1813,11 +1814,20 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
       case GN_LAYER_CONV2D: {
         const float *W = M->params + R.poff;
         const float *b = W + (int64_t)R.cs.outC * R.cs.inC * R.cs.k * R.cs.k;
+        // a 2x2 stride-2 MaxPool2D above: its outputs and switches in the same pass
+        LayerRT *pl = i + 1 < n && M->L[i + 1].d.kind == GN_LAYER_MAXPOOL2D ? &M->L[i + 1] : nullptr;
+        if (pl && !conv_fwd_pool_fusable(R.cs, pl->ps, B)) pl = nullptr;
         KTimer kt(c, GN_KCLASS_OTHER, "conv_fwd", conv_flops(R.cs, B));
-        HIP_OK(c, launch_conv_fwd(cur, W, b, R.out, R.cs, B, R.cfwd, c->stream));
+        HIP_OK(c, launch_conv_fwd(cur, W, b, R.out, R.cs, B, R.cfwd, c->stream, pl ? pl->out : nullptr,
+                                  pl ? pl->argmax : nullptr));
+        pool_done = pl != nullptr;
         break;
       }
       case GN_LAYER_MAXPOOL2D: {  // read the input, write outputs and int32 switches
+        if (pool_done) {
+          pool_done = false;
+          break;
+        }
         KTimer kt(c, GN_KCLASS_OTHER, "maxpool_fwd", f4((double)B * R.in_len + 2.0 * B * R.out_len));
         HIP_OK(c, launch_maxpool_fwd(cur, R.out, R.argmax, R.ps, B, c->stream));
         break;
@@ -2034,6 +2044,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   bool is_dz = true;  // gout of the current layer already holds dz
   bool drop_done = false;  // the Dropout below was folded into the Dense above's dX epilogue
   int bias_done = -1;      // a Dense layer whose bias gradient launch_tail_bwd wrote
+  int pool_bwd_done = -1;  // a MaxPool2D whose input gradient launch_tail_bwd wrote
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
     const float *in = i == 0 ? x : M->L[i - 1].out;
@@ -2084,11 +2095,24 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           LayerRT *dn = next_dz ? (gin == below->gout ? below : &M->L[i - 2]) : nullptr;
           float *gb_below = dn ? M->grads + dn->poff + (int64_t)dn->d.in_size * dn->d.out_size : nullptr;
           const int C = R.d.out_size, nin = R.d.in_size;
+          // Flatten over a 2x2 stride-2 MaxPool2D whose windows tile its
+          // input: the pool's backward through its switches in the same pass
+          LayerRT *pl = i >= 3 && below->d.kind == GN_LAYER_FLATTEN && M->L[i - 2].d.kind == GN_LAYER_MAXPOOL2D
+                            ? &M->L[i - 2]
+                            : nullptr;
+          if (pl) {
+            const PoolShape &q = pl->ps;
+            const bool tiled = q.k == 2 && q.stride == 2 && q.pad == 0 && q.H % 2 == 0 && q.W % 2 == 0 &&
+                               q.oH == q.H / 2 && q.oW == q.W / 2 && q.C * q.oH * q.oW == nin;
+            if (!tiled || !M->L[i - 3].gout || aux || cfac || next_dz) pl = nullptr;
+          }
           KTimer kt(c, GN_KCLASS_OTHER, "tail_bwd",
                     f4(2.0 * B * nin + 2.0 * C * nin + B * C + C + (gin ? (aux ? 2.0 : 1.0) * B * nin : 0.0) +
-                       (gb_below ? nin : 0)));
+                       (gb_below ? nin : 0) + (pl ? 4.0 * B * nin : 0.0)));
           HIP_OK(c, launch_tail_bwd(in, W, dz, gW, gB, gin, aux, deriv, cfac, gb_below, B, nin, C, scale,
-                                    c->stream));
+                                    c->stream, pl ? pl->argmax : nullptr, pl ? M->L[i - 3].gout : nullptr,
+                                    pl ? pl->ps.H : 0, pl ? pl->ps.W : 0));
+          pool_bwd_done = pl ? i - 2 : -1;
           bias_done = dn ? (int)(dn - &M->L[0]) : -1;
           is_dz = next_dz;
           break;
@@ -2124,6 +2148,10 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
       case GN_LAYER_FLATTEN:
         break;  // gout aliased by the layer above
       case GN_LAYER_MAXPOOL2D:
+        if (i == pool_bwd_done) {
+          is_dz = false;
+          break;
+        }
         if (below && below->gout) {  // read gradients and switches, write the input gradient
           KTimer kt(c, GN_KCLASS_OTHER, "maxpool_bwd", f4(2.0 * B * R.out_len + (double)B * R.in_len));
           HIP_OK(c, launch_maxpool_bwd(R.gout, R.argmax, below->gout, R.ps, B, c->stream));

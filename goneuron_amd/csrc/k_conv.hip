@@ -463,6 +463,134 @@ __global__ __launch_bounds__(CT) void conv2d_dgrad_mfma(const float *__restrict_
   }
 }
 
+// k3 s1 p1 with INC input channels (conv2D3x3Optimized): a thread per output
+// position -- or per 2x2 quad of positions when a 2x2 / stride-2 MaxPool2D
+// follows and tiles the plane -- and per group of OCG output channels.  The
+// input window is read once into registers and serves every channel of the
+// group; each output keeps conv2d_fwd_kernel's expressions, so the results
+// are the same bit for bit.  With POOL the quad's four activations are
+// scanned in (kh, kw) order with a strict '>' from -Inf (maxpool_fwd_kernel),
+// writing the pooled value and its flat index inside the sample.
+// the float64 activations out of line: inlined once per output they made
+// the kernel ~12k instructions, fetched again by every wave
+__device__ __noinline__ float act_fwd_call(float v, int kind) { return act_fwd(v, kind); }
+
+template <int INC, int OCG, bool POOL>
+__global__ __launch_bounds__(CT) void conv3_fwd_group_kernel(const float *__restrict__ x,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ bias,
+                                                             float *__restrict__ out, ConvShape s, int B,
+                                                             int fwd, float *__restrict__ pout,
+                                                             int32_t *__restrict__ parg) {
+  constexpr int Q = POOL ? 2 : 1;  // positions per side
+  constexpr int R = Q + 2;         // window rows and columns
+  const int H = s.H, W = s.W;      // = oH, oW
+  const int qh = H / Q, qw = W / Q, per = qh * qw;
+  const int groups = s.outC / OCG;
+  // blockIdx.y = sample * groups + channel group: uniform, so the weights
+  // and the bias come through scalar loads
+  const int q = blockIdx.x * CT + threadIdx.x;
+  if (q >= per) return;
+  const int g = blockIdx.y % groups, b = blockIdx.y / groups;
+  const int y0 = (q / qw) * Q, x0 = (q % qw) * Q;
+  const float *xs = x + (int64_t)b * INC * H * W;
+  // the window, zero outside the plane: clamped addresses and a select (no
+  // branch around each load)
+  float win[INC][R][R];
+#pragma unroll
+  for (int ic = 0; ic < INC; ++ic)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int c = 0; c < R; ++c) {
+        const int ih = y0 - 1 + r, iw = x0 - 1 + c;
+        const bool inb = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        const float v = xs[(ic * H + min(max(ih, 0), H - 1)) * W + min(max(iw, 0), W - 1)];
+        win[ic][r][c] = inb ? v : 0.f;
+      }
+#pragma unroll 1
+  for (int j = 0; j < OCG; ++j) {
+    const int oc = g * OCG + j;
+    const float *wk = w + oc * INC * 9;
+    const float bo = bias[oc];
+    float mv = -__builtin_inff();
+    int mi = -1;
+#pragma unroll
+    for (int dy = 0; dy < Q; ++dy)
+#pragma unroll
+      for (int dx = 0; dx < Q; ++dx) {
+        const int oh = y0 + dy, ow = x0 + dx;
+        float p = 0.0f;
+        if (oh >= 1 && oh < H - 1) {
+#pragma unroll
+          for (int ic = 0; ic < INC; ++ic) {
+            const float *k9 = wk + ic * 9;
+            p += k9[0] * win[ic][dy][dx] + k9[1] * win[ic][dy][dx + 1] + k9[2] * win[ic][dy][dx + 2];
+            p += k9[3] * win[ic][dy + 1][dx] + k9[4] * win[ic][dy + 1][dx + 1] + k9[5] * win[ic][dy + 1][dx + 2];
+            p += k9[6] * win[ic][dy + 2][dx] + k9[7] * win[ic][dy + 2][dx + 1] + k9[8] * win[ic][dy + 2][dx + 2];
+          }
+          if (ow < 1 || ow >= W - 1) p = 0.0f;  // Q7: the interior-row edge columns keep 0
+        } else {  // first and last rows: taps in (ic, kh, kw) order, those outside skipped
+#pragma unroll
+          for (int ic = 0; ic < INC; ++ic)
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+              const int ih = oh + kh - 1;
+#pragma unroll
+              for (int kw = 0; kw < 3; ++kw) {
+                const int iw = ow + kw - 1;
+                const bool ok = ih >= 0 && ih < H && iw >= 0 && iw < W;
+                const float t = p + wk[(ic * 3 + kh) * 3 + kw] * win[ic][dy + kh][dx + kw];
+                p = ok ? t : p;
+              }
+            }
+        }
+        const float z = p + bo;
+        const float v = fwd == F_RELU ? (z > 0.0f ? z : 0.0f) : fwd == F_IDENTITY ? z : act_fwd_call(z, fwd);
+        const int e = (oc * H + oh) * W + ow;  // flat index inside the sample
+        out[(int64_t)b * s.outC * H * W + e] = v;
+        if (POOL && v > mv) {
+          mv = v;
+          mi = e;
+        }
+      }
+    if (POOL) {
+      const int64_t po = ((int64_t)b * s.outC + oc) * per + q;
+      pout[po] = mv;
+      parg[po] = mi;
+    }
+  }
+}
+
+template <int INC>
+static hipError_t conv3_fwd_inc(const float *x, const float *w, const float *bias, float *out,
+                                const ConvShape &s, int B, int fwd, float *pout, int32_t *parg,
+                                hipStream_t st) {
+  const bool pool = pout != nullptr;
+  const int per = pool ? (s.H / 2) * (s.W / 2) : s.H * s.W;
+  const int ocg = s.outC % 4 == 0 ? 4 : 1;
+  const dim3 grid((per + CT - 1) / CT, B * (s.outC / ocg));
+  if (pool && ocg == 4)
+    hipLaunchKernelGGL((conv3_fwd_group_kernel<INC, 4, true>), dim3(grid), dim3(CT), 0, st, x, w, bias, out, s, B,
+                       fwd, pout, parg);
+  else if (pool)
+    hipLaunchKernelGGL((conv3_fwd_group_kernel<INC, 1, true>), dim3(grid), dim3(CT), 0, st, x, w, bias, out, s, B,
+                       fwd, pout, parg);
+  else if (ocg == 4)
+    hipLaunchKernelGGL((conv3_fwd_group_kernel<INC, 4, false>), dim3(grid), dim3(CT), 0, st, x, w, bias, out, s, B,
+                       fwd, pout, parg);
+  else
+    hipLaunchKernelGGL((conv3_fwd_group_kernel<INC, 1, false>), dim3(grid), dim3(CT), 0, st, x, w, bias, out, s, B,
+                       fwd, pout, parg);
+  return hipGetLastError();
+}
+
+bool conv_fwd_pool_fusable(const ConvShape &s, const PoolShape &p, int B) {
+  return (int64_t)B * s.outC <= 65535 && s.k == 3 && s.stride == 1 && s.pad == 1 && s.inC >= 1 && s.inC <= 4 && p.k == 2 && p.stride == 2 &&
+         p.pad == 0 && p.C == s.outC && p.H == s.oH && p.W == s.oW && s.oH % 2 == 0 && s.oW % 2 == 0 &&
+         p.oH == s.oH / 2 && p.oW == s.oW / 2 && (int64_t)s.outC * s.oH * s.oW < (1ll << 31);
+}
+
 static unsigned grid_for(int64_t n) {
   int64_t b = (n + CT - 1) / CT;
   if (b > 65536) b = 65536;
@@ -470,7 +598,21 @@ static unsigned grid_for(int64_t n) {
 }
 
 hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, float *out,
-                           const ConvShape &s, int B, int fwd, hipStream_t st) {
+                           const ConvShape &s, int B, int fwd, hipStream_t st, float *pool_out,
+                           int32_t *pool_arg) {
+  if (pool_out && !(pool_arg && s.k == 3 && s.stride == 1 && s.pad == 1 && s.inC <= 4 && s.oH % 2 == 0 &&
+                    s.oW % 2 == 0))
+    return hipErrorInvalidValue;
+  if (s.k == 3 && s.stride == 1 && s.pad == 1 && s.inC >= 1 && s.inC <= 4 && s.oH == s.H && s.oW == s.W &&
+      (int64_t)s.outC * s.oH * s.oW < (1ll << 31) && (int64_t)B * s.outC <= 65535) {
+    switch (s.inC) {
+      case 1: return conv3_fwd_inc<1>(x, w, bias, out, s, B, fwd, pool_out, pool_arg, st);
+      case 2: return conv3_fwd_inc<2>(x, w, bias, out, s, B, fwd, pool_out, pool_arg, st);
+      case 3: return conv3_fwd_inc<3>(x, w, bias, out, s, B, fwd, pool_out, pool_arg, st);
+      default: return conv3_fwd_inc<4>(x, w, bias, out, s, B, fwd, pool_out, pool_arg, st);
+    }
+  }
+  if (pool_out) return hipErrorInvalidValue;
   const int osz = s.oH * s.oW;
   const int gx = std::min((osz + CT - 1) / CT, 64);
   hipLaunchKernelGGL(conv2d_fwd_kernel, dim3(gx, B * s.outC), dim3(CT), 0, st, x, w, bias, out, s, B,

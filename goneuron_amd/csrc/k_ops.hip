@@ -818,12 +818,17 @@ __global__ __launch_bounds__(NT) void tail_fwd_kernel(
 // gB comes from block 0.
 constexpr int TAIL_MAXC = 32;
 constexpr int TAIL_ROWS = 64;
-template <int CM, int NT>
+// With POOL, gin is the gradient of a Flatten over a 2x2 stride-2 MaxPool2D
+// whose windows tile its pH x pW input planes: instead of gin, each value goes
+// to the input position its switch names and the window's other three
+// positions get 0 (maxpool_bwd_kernel for non-overlapping windows), into pgin.
+template <int CM, int NT, bool POOL>
 __global__ __launch_bounds__(NT) void tail_bwd_kernel(
     const float *__restrict__ x, const float *__restrict__ W, const float *__restrict__ dz,
     float *__restrict__ gW, float *__restrict__ gB, float *__restrict__ gin,
     const float *__restrict__ aux, int deriv, const float *__restrict__ cfac,
-    float *__restrict__ gB_below, int B, int in, int C, float scale) {
+    float *__restrict__ gB_below, int B, int in, int C, float scale, const int32_t *__restrict__ parg,
+    float *__restrict__ pgin, int pH, int pW) {
   constexpr int NW = NT / 64, RPW = TAIL_ROWS / NW;
   __shared__ float dzs[TAIL_ROWS * CM];
   __shared__ float part[NW / 2][CM + 1][64];  // the tree's upper halves (row CM: gin sums)
@@ -840,6 +845,12 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
   }
   acc[CM] = 0.f;
   const float cf = cfac ? cfac[cc] : 1.0f;
+  int pe0 = 0;  // POOL: flat index of the column's window corner in the pooled layer's input
+  if (POOL) {
+    const int ow = pW / 2, osz = (pH / 2) * ow;
+    const int c = cc / osz, ph = (cc % osz) / ow, pw = cc % ow;
+    pe0 = (c * pH + 2 * ph) * pW + 2 * pw;
+  }
   for (int r0 = 0; r0 < B; r0 += TAIL_ROWS) {
     const int nr = min(TAIL_ROWS, B - r0);
     __syncthreads();
@@ -849,12 +860,14 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
     }
     __syncthreads();
     float xv[RPW], av[RPW];
+    int am[RPW];
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
       const int rr = w * RPW + q;
       const int r = r0 + min(rr, nr - 1);
       xv[q] = x[(size_t)r * in + cc];
       av[q] = daux ? aux[(size_t)r * in + cc] : 0.f;
+      am[q] = POOL ? parg[(size_t)r * in + cc] : 0;
     }
 #pragma unroll
     for (int q = 0; q < RPW; ++q) {
@@ -868,7 +881,7 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
         acc[o] += dv * xv[q];
         sd += dv * wcol[o];
       }
-      if (gin) {
+      if (gin || POOL) {
         float g = sd;
         if (aux) {  // the dX GEMM's EPI_DACT epilogue
           if (cfac) g = g * cf;
@@ -876,7 +889,20 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
         } else {
           g = g * 1.0f;  // EPI_SCALE with alpha 1
         }
-        if (cok) gin[(size_t)(r0 + rr) * in + col] = g;
+        if (POOL) {
+          if (cok) {
+            float *dst = pgin + (size_t)(r0 + rr) * 4 * in;
+#pragma unroll
+            for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+              for (int dx = 0; dx < 2; ++dx) {
+                const int e = pe0 + dy * pW + dx;
+                dst[e] = am[q] == e ? g : 0.0f;
+              }
+          }
+        } else if (cok) {
+          gin[(size_t)(r0 + rr) * in + col] = g;
+        }
         acc[CM] += g;
       }
     }
@@ -946,19 +972,28 @@ hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, co
 
 hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
                            const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
-                           int C, float scale, hipStream_t s) {
+                           int C, float scale, hipStream_t s, const int32_t *pool_arg, float *pool_gin, int pH,
+                           int pW) {
   if (B <= 0) return hipSuccess;
   if (!tail_supported(C, in)) return hipErrorInvalidValue;
+  const bool pool = pool_gin != nullptr;
+  if (pool && (!pool_arg || aux || cfac || gB_below || pH < 2 || pW < 2 || pH % 2 || pW % 2 ||
+               in % ((pH / 2) * (pW / 2)) != 0))
+    return hipErrorInvalidValue;
   const dim3 g((in + 63) / 64);
-  if (C <= 4)
-    hipLaunchKernelGGL((tail_bwd_kernel<4, 1024>), g, dim3(1024), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
-                       gB_below, B, in, C, scale);
-  else if (C <= 16)
-    hipLaunchKernelGGL((tail_bwd_kernel<16, 1024>), g, dim3(1024), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
-                       gB_below, B, in, C, scale);
-  else
-    hipLaunchKernelGGL((tail_bwd_kernel<32, 512>), g, dim3(512), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac,
-                       gB_below, B, in, C, scale);
+#define TAIL_BWD(CM_, NT_, P_)                                                                                  \
+  hipLaunchKernelGGL((tail_bwd_kernel<CM_, NT_, P_>), g, dim3(NT_), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac, \
+                     gB_below, B, in, C, scale, pool_arg, pool_gin, pH, pW)
+  if (pool) {
+    if (C <= 4) TAIL_BWD(4, 512, true);
+    else if (C <= 16) TAIL_BWD(16, 512, true);
+    else TAIL_BWD(32, 512, true);
+  } else {
+    if (C <= 4) TAIL_BWD(4, 1024, false);
+    else if (C <= 16) TAIL_BWD(16, 1024, false);
+    else TAIL_BWD(32, 512, false);
+  }
+#undef TAIL_BWD
   return hipGetLastError();
 }
 
