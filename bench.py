@@ -344,8 +344,10 @@ def calibrate_copy(mib):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 200 steps: the small configurations' steps (tens of us) are then timed
+    # in steady state; at 20 the host's launch rate, not the GPU, set them
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="wide",
                     choices=["mlp", "cnn", "wide", "gpt", "lstm", "gru", "cnn2", "gpt_long"],
                     help="headline workload (the `value` of the line); gru, cnn2 and gpt_long are not "

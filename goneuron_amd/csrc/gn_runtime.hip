@@ -572,6 +572,14 @@ struct gn_model {
   // its first overlapped train step and destroyed with the model, so a
   // context that later trains other models keeps two streams in use
   hipStream_t adam_s = nullptr;
+  // the backward's parameter-gradient kernels (Dense dW and bias sums, the
+  // transformer block's token sums and Q10 weight gradients) on ctx->aux
+  // beside the input-gradient chain: always in steps with per-layer Adam
+  // updates, elsewhere only when gn_debug_side_streams asks (as branches of a
+  // captured C4 step they cost more than they overlap: 459 vs 392 us per
+  // step); fork_ev / join_ev branch aux off the main stream and back
+  bool side_ok = false;
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   // per-layer updates launched by the current overlapped step: a step that
   // fails after one of them keeps its timestep (those layers hold step t)
   int step_updates = 0;
@@ -579,7 +587,9 @@ struct gn_model {
   // models, keyed by the input pointers, the batch and the training flags in
   // effect: the first step with a key runs eagerly, the second is captured,
   // later ones replay.  Adam runs after the graph as an ordinary launch (its
-  // coefficients change every step).
+  // coefficients change every step; an update inside the graph with its
+  // coefficients from a device table measured no faster: 36.7 vs 36.4 us per
+  // C1 step).
   struct StepGraph {
     const float *x, *y;
     int B;
@@ -610,13 +620,13 @@ struct AdamCoef {
   float efflr, b1, b2, omb1, omb2, eps;
 };
 
-static AdamCoef adam_next(gn_model *M) {
-  M->timestep++;
+// Adam.NewStep (opt.go:254-258) for the step that takes the timestep to t
+static AdamCoef adam_coef(const gn_model *M, int t) {
   AdamCoef a;
   a.b1 = M->adam.beta1;
   a.b2 = M->adam.beta2;
   a.eps = M->adam.eps;
-  const double ts = (double)(M->timestep + 1);
+  const double ts = (double)(t + 1);
   const float bias1 = (float)(1.0 - pow((double)a.b1, ts));
   const float bias2 = (float)(1.0 - pow((double)a.b2, ts));
   a.efflr = M->adam.lr * (float)sqrt((double)bias2) / bias1;
@@ -624,6 +634,12 @@ static AdamCoef adam_next(gn_model *M) {
   a.omb2 = 1.0f - a.b2;
   return a;
 }
+
+static AdamCoef adam_next(gn_model *M) {
+  M->timestep++;
+  return adam_coef(M, M->timestep);
+}
+
 
 static int model_alloc(gn_model *M, size_t floats, float **p) {
   void *q = nullptr;
@@ -652,6 +668,8 @@ extern "C" void gn_model_destroy(gn_model *M) {
     (void)hipStreamDestroy(M->adam_s);
   }
   for (hipEvent_t e : M->dz_ev) (void)hipEventDestroy(e);
+  if (M->fork_ev) (void)hipEventDestroy(M->fork_ev);
+  if (M->join_ev) (void)hipEventDestroy(M->join_ev);
   for (void *p : M->bowned) (void)hipFree(p);
   for (void *p : M->owned) (void)hipFree(p);
   delete M;
@@ -1505,14 +1523,14 @@ static hipError_t gemm_nn(gn_ctx *c, const float *A, const float *Wm, float *C, 
 // Q10 gradients of one Linear in the block: dW = scale * S^T x_last and
 // db = scale * colsum(S) from its per-sample token sums S [B][M], one launch
 static hipError_t tb_tok_dw(gn_ctx *c, const float *S, const float *X, float *dW, float *db, int B,
-                            int T, int M, int N, float scale) {
+                            int T, int M, int N, float scale, hipStream_t st) {
   TokDwSet set{};
   set.S[0] = S;
   set.X[0] = X + (int64_t)(T - 1) * N;
   set.dW[0] = dW;
   set.db[0] = db;
-  KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", f4((double)B * M + (double)B * N + (double)M * N + M));
-  return launch_tok_dw(set, 1, B, M, N, M, T * N, scale, c->stream);
+  KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", f4((double)B * M + (double)B * N + (double)M * N + M), st);
+  return launch_tok_dw(set, 1, B, M, N, M, T * N, scale, st);
 }
 
 // Block norm k (0: norm1, 1: norm2) forward: LayerNorm (stats = mean, std)
@@ -1616,8 +1634,19 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
   return GN_OK;
 }
 
-static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int B, float scale) {
+// side: a stream for the parameter-gradient kernels (token sums and the Q10
+// weight gradients read what the main stream has written and write only S,
+// S3 and this layer's gradients), branched off the main stream after each
+// input they read; null runs them on the main stream.
+static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int B, float scale,
+                       hipStream_t side) {
   gn_ctx *c = M->ctx;
+  const hipStream_t ss = side ? side : c->stream;
+  auto fork = [&]() -> hipError_t {
+    if (!side) return hipSuccess;
+    const hipError_t e = hipEventRecord(M->fork_ev, c->stream);
+    return e != hipSuccess ? e : hipStreamWaitEvent(side, M->fork_ev, 0);
+  };
   const int D = R.D, FF = R.FF, T = R.T, rows = B * T;
   const TbOff o = tb_offsets(D, FF, R.d.block_act, R.d.block_norm);
   const float *P = M->params + R.poff;
@@ -1627,13 +1656,14 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   const size_t cap = c->scratch_floats;
   // norm 2 (LayerNorm: Q18 formula; RMSNorm: Q19), gamma / beta column sums
   HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 1, R.gout, t.RES2, t.st2, t.G1, rows, scale));
+  HIP_OK(c, fork());
   {
     // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
     // per-sample token sums S that the Q10 weight gradient needs anyway
-    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
-    HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, c->stream));
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
+    HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, ss));
   }
-  HIP_OK(c, tb_tok_dw(c, t.S, t.MID, G + o.w2, G + o.b2, B, T, D, FF, scale));
+  HIP_OK(c, tb_tok_dw(c, t.S, t.MID, G + o.w2, G + o.b2, B, T, D, FF, scale, ss));
   if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
     // ff1 = SwiGLU called per token: its one saved entry (the last token's
     // input, gate and up) serves the first Backward (token 0); the later ones
@@ -1682,22 +1712,24 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     // its output, GELU (identity forward) from MID, which is the pre-activation
     const int dk = R.d.block_act == GN_BLOCK_ACT_GELU ? D_GELU : D_RELU;
     HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, dk, t.MID, T));
+    HIP_OK(c, fork());
     {
-      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF));
-      HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, c->stream));
+      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF), ss);
+      HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, ss));
     }
-    HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale));
+    HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale, ss));
     // combined = dRES2 + dz1 W1
     HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
   }
   // norm 1
   HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));
+  HIP_OK(c, fork());
   {
     // wOut (Linear): dz = dRES1
-    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D));
-    HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, c->stream));
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
+    HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, ss));
   }
-  HIP_OK(c, tb_tok_dw(c, t.S, t.O, G + o.wo, G + o.bo, B, T, D, D, scale));
+  HIP_OK(c, tb_tok_dw(c, t.S, t.O, G + o.wo, G + o.bo, B, T, D, D, scale, ss));
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, R.NH, D / R.NH, R.causal, true));
@@ -1715,11 +1747,12 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   }
   const int64_t bo[3] = {o.bq, o.bk, o.bv};
   const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
+  HIP_OK(c, fork());
   {
     // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch,
     // blockIdx.z picking the member, B samples each
-    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D));
-    HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, c->stream));
+    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D), ss);
+    HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, ss));
   }
   {
     // dWq, dWk, dWv and their biases (Q10: token sums times the last token's
@@ -1732,8 +1765,8 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
       set.dW[z] = G + wo3[z];
       set.db[z] = G + bo[z];
     }
-    KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", 3 * f4((double)B * D + (double)B * D + (double)D * D + D));
-    HIP_OK(c, launch_tok_dw(set, 3, B, D, D, D, T * D, scale, c->stream));
+    KTimer kt(c, GN_KCLASS_OTHER, "tok_dw", 3 * f4((double)B * D + (double)B * D + (double)D * D + D), ss);
+    HIP_OK(c, launch_tok_dw(set, 3, B, D, D, D, T * D, scale, ss));
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
     const int64_t pst = (int64_t)rows * D;
@@ -2017,27 +2050,22 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
 static int model_backward(gn_model *M, const float *x, int B, float scale, const AdamCoef *ac) {
   gn_ctx *c = M->ctx;
   const int n = (int)M->L.size();
-  if (ac && (int)M->sync_ev.size() < n + 1) {
-    while ((int)M->sync_ev.size() < n + 1) {
+  // parameter gradients on ctx->aux beside the input-gradient chain (the
+  // per-kernel timing pass keeps one stream, so each kernel is timed alone)
+  const bool side = !c->timing && (ac || M->side_ok);
+  auto grow = [&](std::vector<hipEvent_t> &v, int want) -> int {
+    while ((int)v.size() < want) {
       hipEvent_t e;
       HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
-      M->sync_ev.push_back(e);
+      v.push_back(e);
     }
-  }
-  if (ac && (int)M->dz_ev.size() < n) {
-    while ((int)M->dz_ev.size() < n) {
-      hipEvent_t e;
-      HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
-      M->dz_ev.push_back(e);
-    }
-  }
-  if (ac && (int)M->dw_ev.size() < n) {
-    while ((int)M->dw_ev.size() < n) {
-      hipEvent_t e;
-      HIP_OK(c, hipEventCreateWithFlags(&e, hipEventDisableTiming));
-      M->dw_ev.push_back(e);
-    }
-  }
+    return GN_OK;
+  };
+  if (ac && grow(M->sync_ev, n + 1)) return GN_ERR_HIP;
+  if (side && (grow(M->dz_ev, n) || grow(M->dw_ev, n))) return GN_ERR_HIP;
+  if (side && !M->fork_ev) HIP_OK(c, hipEventCreateWithFlags(&M->fork_ev, hipEventDisableTiming));
+  if (side && !M->join_ev) HIP_OK(c, hipEventCreateWithFlags(&M->join_ev, hipEventDisableTiming));
+  bool aux_used = false;
   if (ac && !M->adam_s)  // default priority, like the context's streams
     HIP_OK(c, hipStreamCreateWithFlags(&M->adam_s, hipStreamNonBlocking));
   std::vector<char> dw_aux(n, 0);  // layer i's dW went to ctx->aux
@@ -2117,13 +2145,14 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
           is_dz = next_dz;
           break;
         }
-        const bool side = ac && gin && !c->timing;
+        const bool sd = side && gin;
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, i == bias_done ? nullptr : gB, gin, B, R.d.in_size,
-                                 R.d.out_size, scale, aux, deriv, side ? M->dz_ev[i] : nullptr, nullptr, 0,
+                                 R.d.out_size, scale, aux, deriv, sd ? M->dz_ev[i] : nullptr, nullptr, 0,
                                  cfac));
-        if (side) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
+        if (sd) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
           dw_aux[i] = 1;
+          aux_used = true;
         }
         is_dz = next_dz;
         break;
@@ -2191,8 +2220,13 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         is_dz = false;
         break;
       case GN_LAYER_TRANSFORMER: {
-        int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale);
+        int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale, side ? c->aux : nullptr);
         if (r) return r;
+        if (side) {  // the layer's Adam (M->adam_s) waits for its weight gradients
+          HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
+          dw_aux[i] = 1;
+          aux_used = true;
+        }
         is_dz = false;
         break;
       }
@@ -2535,6 +2569,9 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   if (ac) {  // every dW on ctx->aux precedes an update the step now waits for
     HIP_OK(c, hipEventRecord(M->sync_ev[n], M->adam_s));
     HIP_OK(c, hipStreamWaitEvent(c->stream, M->sync_ev[n], 0));
+  } else if (aux_used) {  // the pass ends when aux's gradients are done (a captured pass rejoins here)
+    HIP_OK(c, hipEventRecord(M->join_ev, c->aux));
+    HIP_OK(c, hipStreamWaitEvent(c->stream, M->join_ev, 0));
   }
   return GN_OK;
 }
@@ -2803,6 +2840,16 @@ extern "C" int gn_debug_fused_tail(gn_model *M, int32_t on) {
   HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
   M->tail_on = on != 0;
   drop_graphs(M);  // captured passes hold the other path
+  return GN_OK;
+}
+
+extern "C" int gn_debug_side_streams(gn_model *M, int32_t on) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
+  HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->aux));
+  M->side_ok = on != 0;
+  drop_graphs(M);  // captured passes hold the other arrangement
   return GN_OK;
 }
 

@@ -261,25 +261,51 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
   const int osz = s.oH * s.oW;
   const int Rin = (band_rows - 1) * s.stride + s.k;  // input rows one band touches
   const int Wp = s.W + 2 * s.pad;
-  float *dz = sm;                                    // [outC][Pp]
-  float *xb = dz + s.outC * Pp;                      // [inC][Rin][Wp]
+  // dz [Pp][ocs], ocs = outC rounded up to odd: the 32 lanes of an MFMA
+  // operand read read consecutive channels of one position, and the staging
+  // writes (consecutive positions) fall in distinct banks
+  const int ocs = s.outC | 1;
+  float *dz = sm;
+  float *xb = dz + ocs * Pp;                         // [inC][Rin][Wp]
   int *poff = reinterpret_cast<int *>(xb + s.inC * Rin * Wp);  // [Pp] LDS offset of a position
   float *red = reinterpret_cast<float *>(poff + Pp);           // [4][32*32]
-  for (int e = threadIdx.x; e < s.outC * Pp; e += CT) {
-    const int oc = e / Pp, q = e % Pp;
-    float v = 0.f;
-    if (q < P) {
-      const int64_t gi = ((int64_t)b * s.outC + oc) * osz + oh0 * s.oW + q;
-      v = gout[gi] * act_deriv(out[gi], deriv);
+  // staged 8 elements per thread at a time, every load issued before the
+  // first is used (a load per iteration waited out its own round trip)
+  constexpr int SU = 8;
+  const int ndz = s.outC * Pp;
+  for (int e0 = threadIdx.x; e0 < ndz; e0 += CT * SU) {
+    float gv[SU], ov[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int e = e0 + u * CT;
+      const int oc = e / Pp, q = e - oc * Pp;
+      const bool ld = e < ndz && q < P;
+      const int64_t gi = ld ? ((int64_t)b * s.outC + oc) * osz + oh0 * s.oW + q : 0;
+      gv[u] = ld ? gout[gi] : 0.f;
+      ov[u] = ld ? out[gi] : 0.f;
     }
-    dz[e] = v;
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int e = e0 + u * CT;
+      const int q = e % Pp;
+      if (e < ndz) dz[q * ocs + e / Pp] = q < P ? gv[u] * act_deriv(ov[u], deriv) : 0.f;
+    }
   }
   const int ih0 = oh0 * s.stride - s.pad;
   const float *xs = x + (int64_t)b * s.inC * s.H * s.W;
-  for (int e = threadIdx.x; e < s.inC * Rin * Wp; e += CT) {
-    const int c = e % Wp, r = (e / Wp) % Rin, ic = e / (Wp * Rin);
-    const int ih = ih0 + r, iw = c - s.pad;
-    xb[e] = (ih >= 0 && ih < s.H && iw >= 0 && iw < s.W) ? xs[(ic * s.H + ih) * s.W + iw] : 0.f;
+  const int nxb = s.inC * Rin * Wp;
+  for (int e0 = threadIdx.x; e0 < nxb; e0 += CT * SU) {
+    float xv[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int e = e0 + u * CT;
+      const int c = e % Wp, r = (e / Wp) % Rin, ic = e / (Wp * Rin);
+      const int ih = ih0 + r, iw = c - s.pad;
+      xv[u] = e < nxb && ih >= 0 && ih < s.H && iw >= 0 && iw < s.W ? xs[(ic * s.H + ih) * s.W + iw] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < SU; ++u)
+      if (e0 + u * CT < nxb) xb[e0 + u * CT] = xv[u];
   }
   for (int q = threadIdx.x; q < Pp; q += CT)
     poff[q] = q < P ? (q / s.oW) * s.stride * Wp + (q % s.oW) * s.stride : 0;
@@ -300,12 +326,21 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
       } else if (tap == ntap) {
         toff = -2;
       }
+      // 8 steps' operands read from LDS before their 8 MFMAs, so the reads'
+      // latencies overlap (one step at a time, each waited out its own)
       cfx16 acc = cfx16{};
-      for (int q0 = kb; q0 < ke; q0 += 2) {
-        const int q = q0 + (lane >> 5);
-        const float a = oc < s.outC ? dz[oc * Pp + q] : 0.f;
-        const float bv = toff >= 0 ? xb[toff + poff[q]] : (toff == -2 && q < P ? 1.f : 0.f);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
+      const int nst = (ke - kb) / 2;
+      for (int s0 = 0; s0 < nst; s0 += 8) {
+        float av[8], bv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool ok = s0 + u < nst;
+          const int q = kb + 2 * (s0 + u) + (lane >> 5);
+          av[u] = ok && oc < s.outC ? dz[q * ocs + oc] : 0.f;
+          bv[u] = !ok ? 0.f : toff >= 0 ? xb[toff + poff[q]] : (toff == -2 && q < P ? 1.f : 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], bv[u], acc, 0, 0, 0);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -720,7 +755,7 @@ hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out
   // in 64 KiB of LDS
   auto mfma_lds = [&](int band) {
     const int P = band * s.oW, Pp = (P + 1) & ~1, Rin = (band - 1) * s.stride + s.k;
-    return ((size_t)s.outC * Pp + (size_t)s.inC * Rin * Wp + Pp + 4 * 1024) * sizeof(float);
+    return ((size_t)(s.outC | 1) * Pp + (size_t)s.inC * Rin * Wp + Pp + 4 * 1024) * sizeof(float);
   };
   int band = s.oH;
   while (band > 1 && mfma_lds(band) > 32768) band = (band + 1) / 2;

@@ -39,11 +39,10 @@ __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, flo
 // run near the HBM limit.
 constexpr int ADAM_U = 4;
 
-__global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
-                                                   const float *__restrict__ g,
-                                                   float *__restrict__ m, float *__restrict__ v,
-                                                   int64_t n, float efflr, float b1, float b2,
-                                                   float omb1, float omb2, float eps) {
+__device__ __forceinline__ void adam_range(float *__restrict__ p, const float *__restrict__ g,
+                                           float *__restrict__ m, float *__restrict__ v, int64_t n,
+                                           float efflr, float b1, float b2, float omb1, float omb2,
+                                           float eps) {
   typedef float f4v __attribute__((ext_vector_type(4)));
   const int64_t n4 = n >> 2;
   const int64_t stride = (int64_t)gridDim.x * TPB * ADAM_U;
@@ -86,6 +85,13 @@ __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p,
     const int64_t i = (n4 << 2) + threadIdx.x;
     if (i < n) adam1(p[i], g[i], m[i], v[i], efflr, b1, b2, omb1, omb2, eps);
   }
+}
+
+__global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p, const float *__restrict__ g,
+                                                   float *__restrict__ m, float *__restrict__ v, int64_t n,
+                                                   float efflr, float b1, float b2, float omb1, float omb2,
+                                                   float eps) {
+  adam_range(p, g, m, v, n, efflr, b1, b2, omb1, omb2, eps);
 }
 
 hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,

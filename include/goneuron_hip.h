@@ -212,6 +212,13 @@ int gn_debug_lstm_clip_bail(gn_model *model, int32_t polls);
  * (at most 32 outputs, input width a multiple of 4); 1 (the default) allows
  * them.  Both paths compute the same step to float32 rounding. */
 int gn_debug_fused_tail(gn_model *model, int32_t on);
+/* Test hook (no counterpart in the reference): on = 1 runs the backward's
+ * parameter-gradient kernels (Dense dW and bias sums, the transformer
+ * block's token sums and weight gradients) on a second stream beside the
+ * input-gradient kernels, as steps with per-layer Adam updates (models of
+ * at least 8 Mi parameters) always do; 0 (the default) keeps them on the
+ * main stream otherwise.  Both give the same step bit for bit. */
+int gn_debug_side_streams(gn_model *model, int32_t on);
 /* Forward + backward + average only (grads valid, no Adam step). */
 int gn_model_accumulate_device(gn_model *m, const float *x_dev, const float *y_dev, int32_t B);
 /* Network.Step (net.go:260-284): Adam.NewStep + StepInPlace on the arena. */

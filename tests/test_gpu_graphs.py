@@ -126,3 +126,34 @@ def test_no_graph_for_lstm_and_moe(gn, dev):
     check(dev.h, L.gn_model_graph_count(m.h, C.byref(n)))
     assert n.value == 0
     m.Close()
+
+
+def test_graph_adam_timestep_moved(gn, dev):
+    """A timestep moved from the host between replays (a checkpoint restore,
+    gn_model_set_adam, far ahead and back): the update after each replayed
+    pass takes its bias corrections from the model's timestep, so every step
+    equals the eager model's bit for bit."""
+    from goneuron_amd import configs
+    from goneuron_amd._lib import check, lib
+    L = lib()
+    cfg = configs.mlp()
+    x, y = configs.inputs(cfg)
+    g = configs.build(cfg, device=dev)
+    e = configs.build(cfg, device=dev)
+    check(dev.h, L.gn_model_set_graphs(e.h, 0))
+    for step in range(12):
+        if step in (4, 8):
+            t = 5000 if step == 4 else 7
+            for m in (g, e):
+                check(dev.h, L.gn_model_set_adam(m.h, None, None, 0, 0, t))
+        lg, le = g.TrainBatch(x, y), e.TrainBatch(x, y)
+        assert lg == le, (step, lg, le)
+        sg, se = _state(g), _state(e)
+        for part, a, b in zip(("params", "grads", "m", "v"), sg[:4], se[:4]):
+            np.testing.assert_array_equal(a, b, err_msg=f"step {step} {part}")
+        assert sg[4] == se[4]
+    n = C.c_int32()
+    check(dev.h, L.gn_model_graph_count(g.h, C.byref(n)))
+    assert n.value == 1
+    g.Close()
+    e.Close()

@@ -818,6 +818,38 @@ def test_overlapped_step_matches_serial(gn, dev):
         np.testing.assert_array_equal(a.Params(), b.Params())
 
 
+@pytest.mark.parametrize("shape", ["small", "full", "swiglu"])
+def test_side_streams_match_serial(gn, shape):
+    """With gn_debug_side_streams(1) the backward's parameter-gradient
+    kernels (the transformer block's token sums and weight gradients, the
+    output Dense layer's dW and bias sums) run on a second stream beside the
+    input-gradient kernels, branched off after each input they read and
+    joined at the end of the pass, also inside the captured step graphs (the
+    arrangement of steps with per-layer Adam updates).  On the main stream
+    (the default here) loss, gradients and parameters must agree bit for bit
+    over four steps (the first eager, then captured and replayed)."""
+    from goneuron_amd import configs
+    from goneuron_amd._lib import lib
+    cfg = {"small": lambda: configs.gpt(B=6, T=16, vocab=50, dim=32, heads=4, ff=48),
+           "full": configs.gpt,
+           "swiglu": lambda: configs.gpt(B=4, T=8, vocab=30, dim=16, heads=2, ff=24, act="swiglu")}[shape]()
+    x, y = configs.inputs(cfg)
+    a = configs.build(cfg, workers=1)
+    b = configs.build(cfg, workers=1)
+    p = _random_block(cfg)(a.Params())
+    a.SetParams(p)
+    b.SetParams(p)
+    assert lib().gn_debug_side_streams(a.h, 1) == 0
+    log(f"side streams vs serial, {shape}")
+    for _ in range(4):
+        la, lb = a.TrainBatch(x, y), b.TrainBatch(x, y)
+        assert la == lb
+        np.testing.assert_array_equal(a.Gradients(), b.Gradients())
+        np.testing.assert_array_equal(a.Params(), b.Params())
+    a.Close()
+    b.Close()
+
+
 # ------------------------------------------------------------------ error paths
 def test_errors_are_reported(gn, dev):
     from goneuron_amd import configs
