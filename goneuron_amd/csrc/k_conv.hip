@@ -244,8 +244,9 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_partial(const float *__restri
 // tap = (ic, kh, kw) plus one all-ones column that yields the bias gradient.
 // dz and the block's input rows (zero padded by `pad` on every side) sit in
 // LDS; each of the 4 waves takes a quarter of the positions and the waves'
-// 32x32 results are added in LDS in wave order.
+// 16 x 32 results are added in LDS in wave order.
 typedef float cfx16 __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict__ x,
                                                         const float *__restrict__ gout,
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
   const int b = blockIdx.x / bands, band = blockIdx.x % bands;
   const int oh0 = band * band_rows, oh1 = min(s.oH, oh0 + band_rows);
   const int P = (oh1 - oh0) * s.oW;
-  const int Pp = (P + 1) & ~1;
+  const int Pp = (P + 3) & ~3;  // whole 4-position MFMA steps
   const int osz = s.oH * s.oW;
   const int Rin = (band_rows - 1) * s.stride + s.k;  // input rows one band touches
   const int Wp = s.W + 2 * s.pad;
@@ -271,24 +272,23 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
   float *red = reinterpret_cast<float *>(poff + Pp);           // [4][32*32]
   // staged 8 elements per thread at a time, every load issued before the
   // first is used (a load per iteration waited out its own round trip)
+  // (a thread per position, channels in groups: no index divisions)
   constexpr int SU = 8;
-  const int ndz = s.outC * Pp;
-  for (int e0 = threadIdx.x; e0 < ndz; e0 += CT * SU) {
-    float gv[SU], ov[SU];
+  for (int q = threadIdx.x; q < Pp; q += CT) {
+    const bool qv = q < P;
+    const int64_t base = (int64_t)b * s.outC * osz + oh0 * s.oW + q;
+    for (int oc0 = 0; oc0 < s.outC; oc0 += SU) {
+      float gv[SU], ov[SU];
 #pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int e = e0 + u * CT;
-      const int oc = e / Pp, q = e - oc * Pp;
-      const bool ld = e < ndz && q < P;
-      const int64_t gi = ld ? ((int64_t)b * s.outC + oc) * osz + oh0 * s.oW + q : 0;
-      gv[u] = ld ? gout[gi] : 0.f;
-      ov[u] = ld ? out[gi] : 0.f;
-    }
+      for (int u = 0; u < SU; ++u) {
+        const bool ld = qv && oc0 + u < s.outC;
+        const int64_t gi = base + (int64_t)(oc0 + u) * osz;
+        gv[u] = ld ? gout[gi] : 0.f;
+        ov[u] = ld ? out[gi] : 0.f;
+      }
 #pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int e = e0 + u * CT;
-      const int q = e % Pp;
-      if (e < ndz) dz[q * ocs + e / Pp] = q < P ? gv[u] * act_deriv(ov[u], deriv) : 0.f;
+      for (int u = 0; u < SU; ++u)
+        if (oc0 + u < s.outC) dz[q * ocs + oc0 + u] = qv ? gv[u] * act_deriv(ov[u], deriv) : 0.f;
     }
   }
   const int ih0 = oh0 * s.stride - s.pad;
@@ -313,42 +313,59 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int ntap = s.inC * s.k * s.k;
   const int nw = s.outC * ntap, nslots = nw + s.outC;
-  const int kq = ((Pp / 2 + 3) / 4) * 2;  // positions per wave (even)
+  const int kq = ((Pp / 4 + 3) / 4) * 4;  // positions per wave (whole MFMA steps)
   const int kb = w * kq, ke = min(Pp, kb + kq);
-  for (int mt = 0; mt * 32 < s.outC; ++mt)
-    for (int nt = 0; nt * 32 <= ntap; ++nt) {
-      const int oc = mt * 32 + (lane & 31);
-      const int tap = nt * 32 + (lane & 31);
-      int toff = -1;  // -1: zero column, -2: ones column (bias)
-      if (tap < ntap) {
-        const int kw = tap % s.k, kh = (tap / s.k) % s.k, ic = tap / (s.k * s.k);
-        toff = (ic * Rin + kh) * Wp + kw;
-      } else if (tap == ntap) {
-        toff = -2;
+  const int i16 = lane & 15, k4 = lane >> 4;
+  // v_mfma_f32_16x16x4f32: A[i = l%16][k = l/16] (channel, position), B[k][j = l%16]
+  // (position, tap; tap ntap is the all-ones bias column); result register r
+  // of lane l is channel 4*(l/16) + r, tap l%16.  Two 16-wide tap tiles per
+  // pass share the channel operand.
+  for (int mt = 0; mt * 16 < s.outC; ++mt)
+    for (int nt = 0; nt * 16 <= ntap; nt += 2) {
+      const int oc = mt * 16 + i16;
+      int toff[2];  // -1: zero column, -2: ones column (bias)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int tap = (nt + h) * 16 + i16;
+        toff[h] = -1;
+        if (tap < ntap) {
+          const int kw = tap % s.k, kh = (tap / s.k) % s.k, ic = tap / (s.k * s.k);
+          toff[h] = (ic * Rin + kh) * Wp + kw;
+        } else if (tap == ntap) {
+          toff[h] = -2;
+        }
       }
-      // 8 steps' operands read from LDS before their 8 MFMAs, so the reads'
-      // latencies overlap (one step at a time, each waited out its own)
-      cfx16 acc = cfx16{};
-      const int nst = (ke - kb) / 2;
+      // 8 steps' operands read from LDS before their MFMAs, so the reads'
+      // latencies overlap
+      f4v acc0 = f4v{0.f, 0.f, 0.f, 0.f}, acc1 = f4v{0.f, 0.f, 0.f, 0.f};
+      const int nst = (ke - kb) / 4;
       for (int s0 = 0; s0 < nst; s0 += 8) {
-        float av[8], bv[8];
+        float av[8], bv0[8], bv1[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const bool ok = s0 + u < nst;
-          const int q = kb + 2 * (s0 + u) + (lane >> 5);
+          const int q = kb + 4 * (s0 + u) + k4;
+          const int po = ok ? poff[q] : 0;
           av[u] = ok && oc < s.outC ? dz[q * ocs + oc] : 0.f;
-          bv[u] = !ok ? 0.f : toff >= 0 ? xb[toff + poff[q]] : (toff == -2 && q < P ? 1.f : 0.f);
+          bv0[u] = !ok ? 0.f : toff[0] >= 0 ? xb[toff[0] + po] : (toff[0] == -2 && q < P ? 1.f : 0.f);
+          bv1[u] = !ok ? 0.f : toff[1] >= 0 ? xb[toff[1] + po] : (toff[1] == -2 && q < P ? 1.f : 0.f);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], bv[u], acc, 0, 0, 0);
+        for (int u = 0; u < 8; ++u) {
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv0[u], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv1[u], acc1, 0, 0, 0);
+        }
       }
+      // the 4 waves' 16 x 32 results added in LDS in wave order
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        red[w * 1024 + (8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * 32 + (lane & 31)] = acc[r];
+      for (int r = 0; r < 4; ++r) {
+        red[w * 512 + (4 * k4 + r) * 32 + i16] = acc0[r];
+        red[w * 512 + (4 * k4 + r) * 32 + 16 + i16] = acc1[r];
+      }
       __syncthreads();
-      for (int e = threadIdx.x; e < 1024; e += CT) {
-        const int o = mt * 32 + e / 32, t = nt * 32 + e % 32;
-        const float v = (red[e] + red[1024 + e]) + (red[2048 + e] + red[3072 + e]);
+      for (int e = threadIdx.x; e < 512; e += CT) {
+        const int o = mt * 16 + e / 32, t = nt * 16 + e % 32;
+        const float v = (red[e] + red[512 + e]) + (red[1024 + e] + red[1536 + e]);
         if (o < s.outC && t < ntap) part[(int64_t)blockIdx.x * nslots + o * ntap + t] = v;
         else if (o < s.outC && t == ntap) part[(int64_t)blockIdx.x * nslots + nw + o] = v;
       }
@@ -754,7 +771,7 @@ hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out
   // MFMA path: bands of output rows whose dz tile, input rows and tables fit
   // in 64 KiB of LDS
   auto mfma_lds = [&](int band) {
-    const int P = band * s.oW, Pp = (P + 1) & ~1, Rin = (band - 1) * s.stride + s.k;
+    const int P = band * s.oW, Pp = (P + 3) & ~3, Rin = (band - 1) * s.stride + s.k;
     return ((size_t)(s.outC | 1) * Pp + (size_t)s.inC * Rin * Wp + Pp + 4 * 1024) * sizeof(float);
   };
   int band = s.oH;
