@@ -79,6 +79,10 @@ struct GemmArgs {
   float *drop_out;
   const float *drop_mask;
   float drop_scale;
+  // non-null: when K splits, only the partial sums are written to ws (the
+  // reduce and epilogue are left to the caller) and *defer_splits receives
+  // the split count; it receives 1 when the GEMM ran whole (with epilogue)
+  int *defer_splits;
 };
 
 // EPI_SCALE    C = alpha*acc
@@ -137,9 +141,25 @@ enum RowAct : int { ROW_NONE = 0, ROW_SOFTMAX = 1, ROW_LOGSOFTMAX = 2, ROW_ELEMW
 // Supported: 1 <= C <= 32 outputs, in % 4 == 0, x and W 16-byte aligned
 // (hipErrorInvalidValue otherwise).
 bool tail_supported(int C, int in);
+// The rows of x may come from a GEMM whose K split was not reduced
+// (GemmArgs::defer_splits): x[r][c] = act(sum_s ws[s][r][c] + bias[c]) in
+// split order (gemm_splitk_reduce's sum and epilogue), written to xo, and
+// when a Dropout follows in training, dout = mask[c] > 0 ? x * scale : 0 is
+// written too and is the layer's input.
+struct TailSplitIn {
+  const float *ws = nullptr;  // null: x is read as given
+  int splits = 0;
+  const float *bias = nullptr;
+  int act = 0;
+  float *xo = nullptr;
+  float *dout = nullptr;
+  const float *mask = nullptr;
+  float scale = 0.f;
+};
 hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, const float *y, float *out,
                            float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
-                           int loss_kind, const int32_t *bad, int workers, hipStream_t s);
+                           int loss_kind, const int32_t *bad, int workers, hipStream_t s,
+                           const TailSplitIn &sp = TailSplitIn());
 // pool_arg / pool_gin: gin is the gradient of a Flatten over a 2x2 stride-2
 // MaxPool2D with pH x pW input planes (even); the values go through the
 // pool's switches straight into pool_gin, its input gradient (gin unused).

@@ -267,9 +267,11 @@ extern "C" int gn_memset_zero(gn_ctx *c, void *dst, size_t bytes) {
 // ---------------------------------------------------------------------------
 // drop: a Dropout above the layer in training mode, whose output the GEMM
 // writes too (its split-K reduction, or a dropout launch right after it)
+// defer: when non-null and K splits, only the partial sums are written (to
+// the context's scratch) and *defer receives the split count (else 1)
 static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const float *b, float *out,
                             int B, int in, int out_n, int fwd, float *drop_out = nullptr,
-                            const float *drop_mask = nullptr, float drop_scale = 0.f) {
+                            const float *drop_mask = nullptr, float drop_scale = 0.f, int *defer = nullptr) {
   GemmArgs a{};
   a.M = B; a.N = out_n; a.K = in;
   a.A = x; a.lda = in;
@@ -280,6 +282,7 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
   a.drop_out = drop_out;
   a.drop_mask = drop_mask;
   a.drop_scale = drop_scale;
+  a.defer_splits = defer;
   KTimer kt(c, GN_KCLASS_GEMM, "gemm_fwd", gemm_flops(a));
   return launch_gemm('N', 'T', EPI_BIAS_ACT, a, c->stream);
 }
@@ -565,6 +568,8 @@ struct gn_model {
   // tail_now: the current pass uses them
   bool tail_on = true;
   bool tail_now = false;
+  int tail_src = -1;     // the Dense whose output (or Dropout above it) the output layer reads
+  TailSplitIn tail_sp;   // its deferred split-K partials in the current pass (ws null: none)
   std::vector<hipEvent_t> sync_ev;  // one per layer + 1 (no timing)
   std::vector<hipEvent_t> dz_ev;    // one per layer: its dz is ready (no timing)
   std::vector<hipEvent_t> dw_ev;    // one per layer: its dW and bias sums on ctx->aux are done
@@ -1822,8 +1827,24 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
                               M->L[i + 1].out_len == R.out_len
                           ? &M->L[i + 1]
                           : nullptr;
+        // the Dense that feeds the fused output kernels leaves its split-K
+        // reduce (and epilogue, and Dropout) to them
+        const bool feed = for_loss && M->tail_now && i == M->tail_src && !R.ap.jac;
+        int splits = 1;
         HIP_OK(c, dense_fwd(c, cur, W, b, R.out, B, R.d.in_size, R.d.out_size, fwd,
-                            dr ? dr->out : nullptr, dr ? dr->mask : nullptr, dr ? dr->scale : 0.f));
+                            dr ? dr->out : nullptr, dr ? dr->mask : nullptr, dr ? dr->scale : 0.f,
+                            feed ? &splits : nullptr));
+        if (feed && splits > 1) {
+          TailSplitIn &sp = M->tail_sp;
+          sp.ws = c->scratch;
+          sp.splits = splits;
+          sp.bias = b;
+          sp.act = fwd;
+          sp.xo = R.out;
+          sp.dout = dr ? dr->out : nullptr;
+          sp.mask = dr ? dr->mask : nullptr;
+          sp.scale = dr ? dr->scale : 0.f;
+        }
         drop_done = dr != nullptr;
         if (R.ap.jac && !(last && for_loss)) {  // the loss kernel finishes the output layer's rows
           KTimer kt(c, GN_KCLASS_OTHER, "row_act", f4(2.0 * B * R.out_len));
@@ -2603,6 +2624,20 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
   while (below >= 0 && M->L[below].d.kind == GN_LAYER_FLATTEN) --below;
   const float *oin = below >= 0 ? M->L[below].out : x;  // the output layer's input
   M->tail_now = tail_eligible(M, oin, B);
+  // the Dense that writes that input: itself, or below a training Dropout
+  // whose output its GEMM writes (model_forward's fusion)
+  M->tail_src = -1;
+  M->tail_sp = TailSplitIn();
+  if (M->tail_now && below >= 0) {
+    int src = below;
+    if (M->L[src].d.kind == GN_LAYER_DROPOUT && src >= 1 && M->eff[src] &&
+        M->L[src - 1].d.kind == GN_LAYER_DENSE && M->L[src - 1].out_len == M->L[src].out_len)
+      --src;
+    const int rb = O.d.out_size <= 4 ? 16 : O.d.out_size <= 16 ? 4 : 2;
+    if (M->L[src].d.kind == GN_LAYER_DENSE && !M->L[src].ap.jac &&
+        (size_t)rb * O.d.in_size * sizeof(float) <= 65536)
+      M->tail_src = src;
+  }
   rc = model_forward(M, x, B, true);
   if (rc) return rc;
   int row_act = O.ap.row_act;
@@ -2613,7 +2648,7 @@ static int model_accumulate(gn_model *M, const float *x, const float *y, int B,
     KTimer kt(c, GN_KCLASS_OTHER, "tail_fwd",
               f4((double)B * in + (double)C * in + C + 3.0 * B * C + B));
     HIP_OK(c, launch_tail_fwd(oin, W, W + (int64_t)in * C, y, O.out, O.gout, M->loss_rows, B, in, C, row_act,
-                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream));
+                              O.ap.deriv, M->loss_kind, bad, M->workers, c->stream, M->tail_sp));
   } else {  // read z and y, write the activation output and dz, one loss per row (the batch loss is
             // summed from the rows when it is read, gn_model_read_loss)
     KTimer kt(c, GN_KCLASS_OTHER, "out_rows", f4(4.0 * B * O.out_len + B));

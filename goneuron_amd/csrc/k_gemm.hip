@@ -973,6 +973,7 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   }
   const bool two = a.nbatch_in > 1;
   const bool stride16 = ((a.bstride_A | a.bstride_B | (two ? a.istride_A | a.istride_B : 0)) & 3) == 0;
+  if (a.defer_splits && a.nbatch > 1) return hipErrorInvalidValue;
   if (a.nbatch > 1 && (splits > 1 || !stride16)) {
     // split-K partials share one workspace, and float4 legality is judged on
     // the first member: one launch per GEMM of the batch
@@ -993,6 +994,10 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   hipError_t e = big ? launch_r<128>(ta, tb, epi, vec, a, splits, kchunk, s)
                      : launch_r<64>(ta, tb, epi, vec, a, splits, kchunk, s);
   if (e != hipSuccess) return e;
+  if (a.defer_splits) {
+    *a.defer_splits = splits;
+    if (splits > 1) return hipGetLastError();  // partials only: the caller reduces
+  }
   if (splits <= 1) {
     if (!a.drop_out) return e;
     if (a.ldc != a.N) return hipErrorInvalidValue;

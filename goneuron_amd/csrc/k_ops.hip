@@ -740,13 +740,46 @@ __global__ __launch_bounds__(NT) void tail_fwd_kernel(
     const float *__restrict__ x, const float *__restrict__ W, const float *__restrict__ bias,
     const float *__restrict__ y, float *__restrict__ out, float *__restrict__ dz,
     float *__restrict__ loss_rows, int B, int in, int C, int row_act, int fwd, int deriv,
-    int loss_kind, const int32_t *__restrict__ bad, int chunk) {
+    int loss_kind, const int32_t *__restrict__ bad, int chunk, TailSplitIn sp) {
   static_assert(CM * RB == 64, "one partial sum per lane");
   constexpr int NW = NT / 64, RPW = (RB + NW - 1) / NW;
   __shared__ float red[NW][64];
+  extern __shared__ float4 xs4[];  // sp.ws: the block's RB input rows
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int b0 = blockIdx.x * RB;
   const bool in_row = lane < C;
+  if (sp.ws) {
+    // the layer below's split-K partials summed in split order, its bias and
+    // activation, the Dropout above it: gemm_splitk_reduce's values, written
+    // out for the backward and kept in LDS as this layer's input
+    float *xs = reinterpret_cast<float *>(xs4);
+    const size_t MN = (size_t)B * in;
+    for (int e = t; e < RB * in; e += NT) {
+      const int r = e / in, c = e - r * in, b = b0 + r;
+      float xv = 0.f;
+      if (b < B) {
+        const size_t idx = (size_t)b * in + c;
+        float v = sp.ws[idx];
+        for (int s0 = 1; s0 < sp.splits; s0 += 8) {  // eight loads in flight, added in split order
+          float u8[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) u8[u] = s0 + u < sp.splits ? sp.ws[(s0 + u) * MN + idx] : 0.f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (s0 + u < sp.splits) v += u8[u];
+        }
+        const float yv = fwd_of(v + sp.bias[c], sp.act);
+        sp.xo[idx] = yv;
+        xv = yv;
+        if (sp.dout) {
+          xv = sp.mask[c] > 0.f ? yv * sp.scale : 0.0f;
+          sp.dout[idx] = xv;
+        }
+      }
+      xs[e] = xv;
+    }
+    __syncthreads();
+  }
   float yreg[RPW];
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
@@ -769,7 +802,7 @@ __global__ __launch_bounds__(NT) void tail_fwd_kernel(
 #pragma unroll
     for (int o = 0; o < CM; ++o) wv[o] = o < C ? W4[(size_t)o * in4 + k4] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int r = 0; r < RB; ++r) xv[r] = xr[r][k4];
+    for (int r = 0; r < RB; ++r) xv[r] = sp.ws ? xs4[r * in4 + k4] : xr[r][k4];
 #pragma unroll
     for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -957,22 +990,27 @@ bool tail_supported(int C, int in) { return C >= 1 && C <= TAIL_MAXC && in >= 1 
 
 hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, const float *y, float *out,
                            float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
-                           int loss_kind, const int32_t *bad, int workers, hipStream_t s) {
+                           int loss_kind, const int32_t *bad, int workers, hipStream_t s, const TailSplitIn &sp) {
   if (B <= 0) return hipSuccess;
-  if (!tail_supported(C, in) || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(W) & 15))
+  if (!tail_supported(C, in) || (reinterpret_cast<uintptr_t>(W) & 15) ||
+      (!sp.ws && (reinterpret_cast<uintptr_t>(x) & 15)))
     return hipErrorInvalidValue;
   const int fwd = row_act >> 8;
   const int Wk = workers < 1 ? 1 : (workers > B ? B : workers);
   const int chunk = workers > 1 ? (B + Wk - 1) / Wk : 0;
+  const int rb = C <= 4 ? 16 : C <= 16 ? 4 : 2;
+  const size_t lds = sp.ws ? (size_t)rb * in * sizeof(float) : 0;
+  if (lds > 65536 || (sp.ws && (!sp.bias || !sp.xo || (sp.dout && !sp.mask) || sp.splits < 1)))
+    return hipErrorInvalidValue;
   if (C <= 4)
-    hipLaunchKernelGGL((tail_fwd_kernel<4, 16, 512>), dim3((B + 15) / 16), dim3(512), 0, s, x, W, bias, y, out,
-                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+    hipLaunchKernelGGL((tail_fwd_kernel<4, 16, 512>), dim3((B + 15) / 16), dim3(512), lds, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk, sp);
   else if (C <= 16)
-    hipLaunchKernelGGL((tail_fwd_kernel<16, 4, 512>), dim3((B + 3) / 4), dim3(512), 0, s, x, W, bias, y, out,
-                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+    hipLaunchKernelGGL((tail_fwd_kernel<16, 4, 512>), dim3((B + 3) / 4), dim3(512), lds, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk, sp);
   else
-    hipLaunchKernelGGL((tail_fwd_kernel<32, 2, 512>), dim3((B + 1) / 2), dim3(512), 0, s, x, W, bias, y, out,
-                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+    hipLaunchKernelGGL((tail_fwd_kernel<32, 2, 512>), dim3((B + 1) / 2), dim3(512), lds, s, x, W, bias, y, out,
+                       dz, loss_rows, B, in, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk, sp);
   return hipGetLastError();
 }
 

@@ -16,7 +16,9 @@ Each case:
   - compares the two paths' loss and gradients with each other (to 1e-5:
     both are float32 products over the same terms in different orders).
 
-The cases cover the three kernel shapes (outputs <= 4, <= 16, <= 32), a batch
+The cases cover the three kernel shapes (outputs <= 4, <= 16, <= 32), the
+split-K partials of the Dense below summed by the output kernel (with and
+without a Dropout between), a batch
 that leaves the last block of rows partial, batches beyond one 64-row chunk
 of the backward, each kind of layer below (a Dense with its act', a Dropout
 over a Dense, a Flatten over pooling) and Embedding index errors under a
@@ -72,6 +74,13 @@ def cases():
     out["sigmoid_out"] = (dict(num=44, name="sigmoid_out", B=B, loss="mse", lr=1e-3, x="normal", in_len=8,
                                layers=[_dense(8, 24, "relu"), _dense(24, 5, "sigmoid")]),
                           1, (rng.normal(size=(B, 8)).astype(np.float32),
+                              rng.uniform(size=(B, 5)).astype(np.float32)))
+    # a Dense below with K = 1024 (its GEMM splits K): the output kernel sums
+    # the partials, applies the bias and tanh, and writes that layer's output
+    B = 40
+    out["split_below"] = (dict(num=46, name="split_below", B=B, loss="mse", lr=1e-3, x="normal", in_len=1024,
+                               layers=[_dense(1024, 48, "tanh"), _dense(48, 5, "sigmoid")]),
+                          3, (rng.normal(size=(B, 1024)).astype(np.float32),
                               rng.uniform(size=(B, 5)).astype(np.float32)))
     # C2's layers at a small batch: the input gradient goes to a Flatten over MaxPool2D
     out["cnn_small"] = (configs.cnn(B=9), 1, None)
