@@ -160,13 +160,16 @@ hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, co
                            float *dz, float *loss_rows, int B, int in, int C, int row_act, int deriv,
                            int loss_kind, const int32_t *bad, int workers, hipStream_t s,
                            const TailSplitIn &sp = TailSplitIn());
+// xb / gWb / inb: gin is the dz of a Dense with input xb (B x inb); its
+// weight gradient gWb = scale gin^T xb is summed here too (rows in order).
 // pool_arg / pool_gin: gin is the gradient of a Flatten over a 2x2 stride-2
 // MaxPool2D with pH x pW input planes (even); the values go through the
 // pool's switches straight into pool_gin, its input gradient (gin unused).
 hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
                            const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
                            int C, float scale, hipStream_t s, const int32_t *pool_arg = nullptr,
-                           float *pool_gin = nullptr, int pH = 0, int pW = 0);
+                           float *pool_gin = nullptr, int pH = 0, int pW = 0, const float *xb = nullptr,
+                           float *gWb = nullptr, int inb = 0);
 
 // dst[0, n) = v by a kernel (no memset node, so it can sit in a captured graph)
 hipError_t launch_fill(float *dst, float v, int64_t n, hipStream_t s);

@@ -205,4 +205,5 @@ int mha_backward_impl(gn_ctx *c, const float *x, const float *params, const floa
 hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz, float *gW,
                           float *gB, float *gin, int B, int in, int out_n, float scale,
                           const float *gin_aux, int gin_deriv, hipEvent_t dz_ready = nullptr,
-                          float *ms = nullptr, size_t ms_cap = 0, const float *gin_colscale = nullptr);
+                          float *ms = nullptr, size_t ms_cap = 0, const float *gin_colscale = nullptr,
+                          bool skip_dw = false);

@@ -297,7 +297,7 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
 hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz, float *gW,
                           float *gB, float *gin, int B, int in, int out_n, float scale,
                           const float *gin_aux, int gin_deriv, hipEvent_t dz_ready, float *ms,
-                          size_t ms_cap, const float *gin_colscale) {
+                          size_t ms_cap, const float *gin_colscale, bool skip_dw) {
   hipError_t e;
   if (!ms) {
     ms = c->scratch;
@@ -325,11 +325,11 @@ hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float
   a.C = gW; a.ldc = in;
   a.alpha = scale;
   a.ws = wscr; a.ws_cap = wcap;
-  {
+  if (!skip_dw) {
     KTimer kt(c, GN_KCLASS_GEMM, "gemm_dw", gemm_flops(a), ws);
     e = launch_gemm('T', 'N', EPI_SCALE, a, ws);
+    if (e != hipSuccess) return e;
   }
-  if (e != hipSuccess) return e;
   if (gin) {
     GemmArgs d{};
     d.M = B; d.N = in; d.K = out_n;
@@ -2068,6 +2068,10 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
 // With `ac`, each layer's parameters get their Adam update on ctx->aux once
 // the layer's backward kernels are queued (no later kernel of the backward
 // reads them), and the main stream waits for all updates at the end.
+// products (multiply-adds) up to which the fused output-layer kernels take a
+// Dense layer's GEMM work
+constexpr double kTailMaxMacs = 16.0 * (1 << 20);
+
 static int model_backward(gn_model *M, const float *x, int B, float scale, const AdamCoef *ac) {
   gn_ctx *c = M->ctx;
   const int n = (int)M->L.size();
@@ -2093,6 +2097,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   bool is_dz = true;  // gout of the current layer already holds dz
   bool drop_done = false;  // the Dropout below was folded into the Dense above's dX epilogue
   int bias_done = -1;      // a Dense layer whose bias gradient launch_tail_bwd wrote
+  int dw_done = -1;        // ... and whose weight gradient it wrote
   int pool_bwd_done = -1;  // a MaxPool2D whose input gradient launch_tail_bwd wrote
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
@@ -2155,21 +2160,33 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
                                q.oH == q.H / 2 && q.oW == q.W / 2 && q.C * q.oH * q.oW == nin;
             if (!tiled || !M->L[i - 3].gout || aux || cfac || next_dz) pl = nullptr;
           }
+          // the weight gradient of that Dense too, when it is small enough
+          // that its GEMM's launch, not its work, would set its time
+          const int dni = dn ? (int)(dn - &M->L[0]) : -1;
+          const bool dwb = dn && (double)B * dn->d.in_size * dn->d.out_size <= kTailMaxMacs;
+          const float *xdn = dni > 0 ? M->L[dni - 1].out : x;
           KTimer kt(c, GN_KCLASS_OTHER, "tail_bwd",
                     f4(2.0 * B * nin + 2.0 * C * nin + B * C + C + (gin ? (aux ? 2.0 : 1.0) * B * nin : 0.0) +
-                       (gb_below ? nin : 0) + (pl ? 4.0 * B * nin : 0.0)));
+                       (gb_below ? nin : 0) + (pl ? 4.0 * B * nin : 0.0) +
+                       (dwb ? (double)B * dn->d.in_size + (double)dn->d.in_size * dn->d.out_size : 0.0)));
           HIP_OK(c, launch_tail_bwd(in, W, dz, gW, gB, gin, aux, deriv, cfac, gb_below, B, nin, C, scale,
                                     c->stream, pl ? pl->argmax : nullptr, pl ? M->L[i - 3].gout : nullptr,
-                                    pl ? pl->ps.H : 0, pl ? pl->ps.W : 0));
+                                    pl ? pl->ps.H : 0, pl ? pl->ps.W : 0, dwb ? xdn : nullptr,
+                                    dwb ? M->grads + dn->poff : nullptr, dwb ? dn->d.in_size : 0));
+          dw_done = dwb ? dni : -1;
           pool_bwd_done = pl ? i - 2 : -1;
           bias_done = dn ? (int)(dn - &M->L[0]) : -1;
           is_dz = next_dz;
           break;
         }
-        const bool sd = side && gin;
+        if (i == dw_done && i == bias_done && !gin) {  // every gradient of the layer is written
+          is_dz = next_dz;
+          break;
+        }
+        const bool sd = side && gin && i != dw_done;
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, i == bias_done ? nullptr : gB, gin, B, R.d.in_size,
                                  R.d.out_size, scale, aux, deriv, sd ? M->dz_ev[i] : nullptr, nullptr, 0,
-                                 cfac));
+                                 cfac, i == dw_done));
         if (sd) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
           dw_aux[i] = 1;
@@ -2599,8 +2616,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
 
 // The fused output-layer kernels serve a training pass when the output layer
 // is a Dense with few outputs whose products are small enough that the
-// GEMMs' launches, not their work, would set their time.
-constexpr double kTailMaxMacs = 16.0 * (1 << 20);
+// GEMMs' launches, not their work, would set their time (kTailMaxMacs).
 static bool tail_eligible(const gn_model *M, const float *in_ptr, int B) {
   const LayerRT &O = M->L.back();
   if (!M->tail_on || O.d.kind != GN_LAYER_DENSE || !O.gout) return false;

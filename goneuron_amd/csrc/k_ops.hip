@@ -867,10 +867,23 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
     float *__restrict__ gW, float *__restrict__ gB, float *__restrict__ gin,
     const float *__restrict__ aux, int deriv, const float *__restrict__ cfac,
     float *__restrict__ gB_below, int B, int in, int C, float scale, const int32_t *__restrict__ parg,
-    float *__restrict__ pgin, int pH, int pW) {
-  constexpr int NW = NT / 64, RPW = TAIL_ROWS / NW;
+    float *__restrict__ pgin, int pH, int pW, const float *__restrict__ xb, float *__restrict__ gWb,
+    int inb) {
+  constexpr int NW = NT / 64, RPW = TAIL_ROWS / NW, OPT = 64 * 64 / NT;  // OPT: staged x values per thread
   __shared__ float dzs[TAIL_ROWS * CM];
   __shared__ float part[NW / 2][CM + 1][64];  // the tree's upper halves (row CM: gin sums)
+  extern __shared__ float gx_sh[];  // gWb: a chunk's gin rows [64][64], then its input rows [64][64]
+  float *gsh = gx_sh, *xsh = gx_sh + 64 * 64;
+  // gWb: blockIdx.y picks 64 input columns of the Dense below, whose weight
+  // gradient gWb = scale gin^T xb the block sums for its 64 gin columns
+  // (rows in order); the layer's own outputs come from the blocks of row 0
+  const bool main_blk = blockIdx.y == 0;
+  const int kc0 = blockIdx.y * 64;
+  // waves 0-3 each own one 32 x 32 quarter of the 64 x 64 tile on fp32 MFMA
+  // (v_mfma_f32_32x32x2f32: A[i = l%32][k = l/32], B[k = l/32][j = l%32];
+  // result register r of lane l is row 8(r/4) + 4(l/32) + r%4, column l%32)
+  typedef float tfx16 __attribute__((ext_vector_type(16)));
+  tfx16 accb = tfx16{};
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int col = blockIdx.x * 64 + lane;
   const bool cok = col < in;
@@ -928,7 +941,9 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
         } else {
           g = g * 1.0f;  // EPI_SCALE with alpha 1
         }
-        if (POOL) {
+        if (gWb) gsh[rr * 64 + lane] = g;
+        if (!main_blk) {
+        } else if (POOL) {
           if (cok) {
             float *dst = pgin + (size_t)(r0 + rr) * 4 * in;
 #pragma unroll
@@ -945,7 +960,39 @@ __global__ __launch_bounds__(NT) void tail_bwd_kernel(
         acc[CM] += g;
       }
     }
+    if (gWb) {  // this chunk's rows of gin^T xb for the block's 64 x 64 tile
+      if (nr & 1) gsh[nr * 64 + (t & 63)] = 0.f;  // the odd last row's MFMA partner
+      __syncthreads();
+      float xr[OPT];
+#pragma unroll
+      for (int o = 0; o < OPT; ++o) {
+        const int e = t + o * NT, rr = e >> 6, kk = e & 63;
+        xr[o] = rr < nr && kc0 + kk < inb ? xb[(size_t)(r0 + rr) * inb + kc0 + kk] : 0.f;
+      }
+#pragma unroll
+      for (int o = 0; o < OPT; ++o) xsh[t + o * NT] = xr[o];
+      __syncthreads();
+      if (w < 4) {  // rows past nr hold zeros on both sides
+        const int jt = w >> 1, kt = w & 1;
+        for (int rr = 0; rr < nr; rr += 2) {
+          const int r = rr + (lane >> 5);
+          const float a = gsh[r * 64 + 32 * jt + (lane & 31)];
+          const float b = xsh[r * 64 + 32 * kt + (lane & 31)];
+          accb = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, accb, 0, 0, 0);
+        }
+      }
+    }
   }
+  if (gWb && w < 4) {
+    const int jt = w >> 1, kt = w & 1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = blockIdx.x * 64 + 32 * jt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int kk = kc0 + 32 * kt + (lane & 31);
+      if (j < in && kk < inb) gWb[(size_t)j * inb + kk] = accb[r] * scale;
+    }
+  }
+  if (!main_blk) return;
   // wave w adds wave w + h's sums, h = 8, 4, 2, 1
 #pragma unroll
   for (int h = NW / 2; h >= 1; h >>= 1) {
@@ -1017,24 +1064,26 @@ hipError_t launch_tail_fwd(const float *x, const float *W, const float *bias, co
 hipError_t launch_tail_bwd(const float *x, const float *W, const float *dz, float *gW, float *gB, float *gin,
                            const float *aux, int deriv, const float *cfac, float *gB_below, int B, int in,
                            int C, float scale, hipStream_t s, const int32_t *pool_arg, float *pool_gin, int pH,
-                           int pW) {
+                           int pW, const float *xb, float *gWb, int inb) {
   if (B <= 0) return hipSuccess;
   if (!tail_supported(C, in)) return hipErrorInvalidValue;
   const bool pool = pool_gin != nullptr;
   if (pool && (!pool_arg || aux || cfac || gB_below || pH < 2 || pW < 2 || pH % 2 || pW % 2 ||
                in % ((pH / 2) * (pW / 2)) != 0))
     return hipErrorInvalidValue;
-  const dim3 g((in + 63) / 64);
-#define TAIL_BWD(CM_, NT_, P_)                                                                                  \
-  hipLaunchKernelGGL((tail_bwd_kernel<CM_, NT_, P_>), g, dim3(NT_), 0, s, x, W, dz, gW, gB, gin, aux, deriv, cfac, \
-                     gB_below, B, in, C, scale, pool_arg, pool_gin, pH, pW)
+  if (gWb && (!xb || inb < 1 || pool || !gin)) return hipErrorInvalidValue;
+  const dim3 g((in + 63) / 64, gWb ? (inb + 63) / 64 : 1);
+  const size_t lds = gWb ? 2 * 64 * 64 * sizeof(float) : 0;
+#define TAIL_BWD(CM_, NT_, P_)                                                                                    \
+  hipLaunchKernelGGL((tail_bwd_kernel<CM_, NT_, P_>), g, dim3(NT_), lds, s, x, W, dz, gW, gB, gin, aux, deriv,   \
+                     cfac, gB_below, B, in, C, scale, pool_arg, pool_gin, pH, pW, xb, gWb, inb)
   if (pool) {
     if (C <= 4) TAIL_BWD(4, 512, true);
     else if (C <= 16) TAIL_BWD(16, 512, true);
     else TAIL_BWD(32, 512, true);
   } else {
     if (C <= 4) TAIL_BWD(4, 1024, false);
-    else if (C <= 16) TAIL_BWD(16, 1024, false);
+    else if (C <= 16) TAIL_BWD(16, 512, false);
     else TAIL_BWD(32, 512, false);
   }
 #undef TAIL_BWD

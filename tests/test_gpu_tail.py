@@ -5,8 +5,8 @@ input width that is a multiple of 4 runs that layer as two kernels: the
 forward product fused with the loss rows (activation, loss, loss gradient
 through the Jacobian / derivative, layer.go:405-470 + loss.go), and one
 backward kernel for dW, db and dX with the dX GEMM's epilogue (a Dropout's
-factor, act' of the layer below), which also sums the bias gradient of a
-Dense whose dz that dX is.
+factor, act' of the layer below), which also sums the bias and weight
+gradients of a Dense whose dz that dX is.
 
 Each case:
   - runs two training steps against the oracle (gpuutil.compare_step, every
@@ -82,6 +82,14 @@ def cases():
                                layers=[_dense(1024, 48, "tanh"), _dense(48, 5, "sigmoid")]),
                           3, (rng.normal(size=(B, 1024)).astype(np.float32),
                               rng.uniform(size=(B, 5)).astype(np.float32)))
+    # three Dense layers: the middle one's weight gradient comes from the
+    # output kernel, its input gradient from its own dX GEMM
+    B = 70
+    out["three_dense"] = (dict(num=47, name="three_dense", B=B, loss="ce", lr=1e-3, x="normal", in_len=10,
+                               classes=3,
+                               layers=[_dense(10, 16, "relu"), _dense(16, 24, "tanh"),
+                                       _dense(24, 3, "softmax", True)]),
+                          2, (rng.normal(size=(B, 10)).astype(np.float32), _onehot(rng, B, 3)))
     # C2's layers at a small batch: the input gradient goes to a Flatten over MaxPool2D
     out["cnn_small"] = (configs.cnn(B=9), 1, None)
     # Embedding index errors under two workers: the skipped samples' rows and chunk losses
