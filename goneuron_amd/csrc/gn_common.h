@@ -327,10 +327,14 @@ hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int
 hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int32_t *ids, float *out,
                            float *pe_out, int B, int T, int V, int D, int32_t *bad, hipStream_t s,
                            bool bad_or = false);
-// ws (may be null below 2048 contributing rows): 2 x contributing rows ints
+// ws (may be null below 2048 contributing rows): 2 x contributing rows ints.
+// pe_grad (may be null; only where embed_grad_takes_pe): the gradient of a
+// PositionalEncoding above the Embedding (the same gradient rows summed over
+// the samples, times scale), written by the same launch.
+bool embed_grad_takes_pe(int B, int T, int W);
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
                              int D, int W, float scale, const int32_t *bad, hipStream_t s,
-                             float *ws = nullptr, size_t ws_floats = 0);
+                             float *ws = nullptr, size_t ws_floats = 0, float *pe_grad = nullptr);
 hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
 hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipStream_t s);
 hipError_t launch_gap1d_fwd(const float *x, float *out, int B, int T, int D, hipStream_t s);
@@ -350,11 +354,52 @@ struct TokDwSet {
 };
 hipError_t launch_tok_dw(const TokDwSet &set, int nmem, int B, int M, int N, int lds, int ldx,
                          float scale, hipStream_t s);
+// The parameter gradients of a transformer block's backward in one launch:
+// up to six Linear layers' Q10 gradients (tok_dw's products; the token sums
+// of sample b are S[b * np * ps + o] for np = 1, or the sum of np per-row-block
+// partial rows S[(b * np + j) * ps + o], j ascending) and up to two
+// LayerNorms' gamma / beta gradients from their backward's block partials
+// (ln_param_final's sums).  launch_tb_params fills `start` (LayerNorm jobs'
+// blocks first, then the Linear jobs').
+struct TbParamJob {
+  const float *S;
+  int np;
+  int64_t ps;
+  const float *X;  // the last token's input row of sample 0; sample b at X + b * ldx
+  int64_t ldx;
+  float *dW, *db;
+  int M, N;
+};
+struct TbLnJob {
+  const float *part;  // nblk rows of [dgamma partial | dbeta partial], 2N each
+  int nblk, N;
+  float *dgam, *dbet;
+};
+constexpr int TBP_MAXLIN = 6, TBP_MAXLN = 2;
+struct TbParamSet {
+  TbParamJob lin[TBP_MAXLIN];
+  TbLnJob ln[TBP_MAXLN];
+  int nlin, nln;
+  int start[TBP_MAXLIN + TBP_MAXLN + 1];
+};
+hipError_t launch_tb_params(TbParamSet &set, int B, float scale, hipStream_t s);
+// cls (may be null): rows r with r % clsT == 0 are also written as row r / clsT of cls
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
-                         int rows, int N, float eps, hipStream_t s);
+                         int rows, int N, float eps, hipStream_t s, float *cls = nullptr, int clsT = 0);
 hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam, const float *stats,
                                 float *dx, float *dgam, float *dbet, int rows, int N, float scale,
                                 float *ws, size_t ws_cap, hipStream_t s);
+// LayerNorm backward, dx and per-block partials only: part [ln_bwd_blocks(rows)][2N]
+// (dgamma | dbeta, unscaled; a TbLnJob sums them), tsum (may be null) [blocks][N]
+// the blocks' column sums of dx (ln_bwd_rows_per_block() rows each).  gpool (may
+// be null, then g is read): a CLSPooling's gradient, row r / poolT for rows r
+// with r % poolT == 0, zero elsewhere.
+int ln_bwd_blocks(int rows);
+int ln_bwd_rows_per_block();
+bool ln_bwd_part_supported(int N);
+hipError_t launch_ln_bwd_part(const float *g, const float *gpool, int poolT, const float *x,
+                              const float *gam, const float *stats, float *dx, float *part, float *tsum,
+                              int rows, int N, hipStream_t s);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
 // Rotary embedding of rows [rows, NH*hd] in place; position = row % T; cs/sn
@@ -377,9 +422,10 @@ hipError_t launch_attn_bwd_gemm(const float *Q, const float *K, const float *V, 
                                 float *S, hipStream_t s);
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s);
+// TS (may be null): the per-sample token sums of gQ, gK, gV ([B][D] each, member m at TS + m * tss)
 hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *GO,
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
-                           hipStream_t s);
+                           hipStream_t s, float *TS = nullptr, int64_t tss = 0);
 
 
 // ---- model views for the checkpoint writers (gn_runtime.hip) ----

@@ -529,6 +529,11 @@ struct LayerRT {
     float *Q, *K, *V, *O, *RES1, *N1, *MID, *RES2, *st1, *st2;
     float *G1, *DZ1, *COMB, *G2, *GO, *GQ, *GK, *GV, *GX, *S;
     float *S3;  // token sums of gQ, gK, gV ([3][max batch][D])
+    // LayerNorm backward block partials of norm 1 / norm 2: [blocks][2D]
+    // (dgamma | dbeta) and [blocks][D] (column sums of dx, the token sums of
+    // wOut's / ff2's dz); null when the norms are RMSNorm or the rows of a
+    // block can span two samples
+    float *LP1, *LP2, *TS1, *TS2;
     float *Z, *MG, *DZS;     // SwiGLU ff1: [gate | up] per token, token-0 mid grad, its dZ
     float *rcos, *rsin;      // RoPE angle tables [T][hd/2]
     float *SC;               // attention scores and their gradients (sizes the fused kernels do not hold)
@@ -824,6 +829,14 @@ static int alloc_batch(gn_model *M) {
       if ((rc = model_balloc(M, rows * 2, &t.st2))) return rc;
       if ((rc = model_balloc(M, (size_t)max_batch * std::max(D, FF), &t.S))) return rc;
       if ((rc = model_balloc(M, 3 * (size_t)max_batch * D, &t.S3))) return rc;
+      if (R.d.block_norm != GN_BLOCK_NORM_RMS && ln_bwd_part_supported(R.D) &&
+          R.T % ln_bwd_rows_per_block() == 0) {
+        const size_t nb = (size_t)ln_bwd_blocks((int)rows);
+        if ((rc = model_balloc(M, nb * 2 * D, &t.LP1))) return rc;
+        if ((rc = model_balloc(M, nb * 2 * D, &t.LP2))) return rc;
+        if ((rc = model_balloc(M, nb * D, &t.TS1))) return rc;
+        if ((rc = model_balloc(M, nb * D, &t.TS2))) return rc;
+      }
       if (!attn_supported(R.T, R.D, R.NH) &&
           (rc = model_balloc(M, attn_gemm_floats(max_batch, R.T, R.NH), &t.SC)))
         return rc;
@@ -935,6 +948,14 @@ static int alloc_batch(gn_model *M) {
       if ((rc = model_balloc(M, rows * D, &t.GO))) return rc;
       if ((rc = model_balloc(M, (size_t)max_batch * D, &t.S))) return rc;
       if ((rc = model_balloc(M, 3 * (size_t)max_batch * D, &t.S3))) return rc;
+      if (R.d.block_norm != GN_BLOCK_NORM_RMS && ln_bwd_part_supported(R.D) &&
+          R.T % ln_bwd_rows_per_block() == 0) {
+        const size_t nb = (size_t)ln_bwd_blocks((int)rows);
+        if ((rc = model_balloc(M, nb * 2 * D, &t.LP1))) return rc;
+        if ((rc = model_balloc(M, nb * 2 * D, &t.LP2))) return rc;
+        if ((rc = model_balloc(M, nb * D, &t.TS1))) return rc;
+        if ((rc = model_balloc(M, nb * D, &t.TS2))) return rc;
+      }
       if (!attn_supported(R.T, R.D, R.NH) &&
           (rc = model_balloc(M, attn_gemm_floats(max_batch, R.T, R.NH), &t.SC)))
         return rc;
@@ -1540,14 +1561,30 @@ static hipError_t tb_tok_dw(gn_ctx *c, const float *S, const float *X, float *dW
 
 // Block norm k (0: norm1, 1: norm2) forward: LayerNorm (stats = mean, std)
 // or RMSNorm(dim, 1e-5) (stats = rms), transformer.go:928-934.
+// cls (LayerNorm only, may be null): token 0 of every sample also written
+// there (the output of a CLSPooling above the block).
 static hipError_t tb_norm_fwd(gn_ctx *c, const LayerRT &R, const float *P, const TbOff &o, int k,
-                              const float *x, float *y, float *st, int rows) {
+                              const float *x, float *y, float *st, int rows, float *cls = nullptr) {
   const float *g = P + (k == 0 ? o.g1 : o.g2), *be = P + (k == 0 ? o.be1 : o.be2);
   const bool rms = R.d.block_norm == GN_BLOCK_NORM_RMS;
   // read x, write y and the per-row statistics
-  KTimer kt(c, GN_KCLASS_OTHER, rms ? "rms_fwd" : "ln_fwd", f4(2.0 * rows * R.D + (rms ? 1 : 2) * rows));
+  KTimer kt(c, GN_KCLASS_OTHER, rms ? "rms_fwd" : "ln_fwd",
+            f4(2.0 * rows * R.D + (rms ? 1 : 2) * rows + (cls ? (double)rows / R.T * R.D : 0.0)));
   if (rms) return launch_rms_fwd(x, g, y, st, rows, R.D, 1e-5f, c->stream);
-  return launch_ln_fwd(x, g, be, y, st, rows, R.D, 1e-5f, c->stream);
+  return launch_ln_fwd(x, g, be, y, st, rows, R.D, 1e-5f, c->stream, cls, R.T);
+}
+
+// The block's norms run the one-pass LayerNorm backward with its partials
+// kept (t.LP*, t.TS*): the block's parameter gradients then come from one
+// tb_param_kernel launch, and a CLSPooling above the block needs no
+// gradient scatter (the norm-2 backward reads the pooled rows).
+static bool tb_fused_params(const LayerRT &R) { return R.tb.LP1 != nullptr; }
+// A CLSPooling above a block whose last norm is a LayerNorm: the norm's
+// forward writes the pooled rows, and with the fused parameter path its
+// backward reads the pooled gradient (no cls_fwd / cls_bwd launch).
+static bool tb_cls_fusable(const LayerRT &R, const LayerRT &up) {
+  return up.d.kind == GN_LAYER_CLSPOOL && R.d.kind == GN_LAYER_TRANSFORMER &&
+         R.d.block_norm != GN_BLOCK_NORM_RMS && up.T == R.T && up.D == R.D && tb_fused_params(R);
 }
 
 // Block norm backward: dx into dx, gamma (and LayerNorm beta) gradients.
@@ -1586,7 +1623,8 @@ static hipError_t tb_norm_bwd(gn_ctx *c, const LayerRT &R, const float *P, float
   return launch_colsum_multi(src, dst, nm, rows, D, D, scale, c->scratch, c->scratch_floats, c->stream);
 }
 
-static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
+// cls (may be null): the output of a CLSPooling above, written by norm 2
+static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B, float *cls) {
   gn_ctx *c = M->ctx;
   const int D = R.D, FF = R.FF, rows = B * R.T;
   const TbOff o = tb_offsets(D, FF, R.d.block_act, R.d.block_norm);
@@ -1635,7 +1673,7 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
     HIP_OK(c, gemm_nt(c, t.N1, P + o.w1, P + o.b1, t.MID, rows, FF, D, EPI_BIAS_ACT, f, nullptr));
   }
   HIP_OK(c, gemm_nt(c, t.MID, P + o.w2, P + o.b2, t.RES2, rows, D, FF, EPI_BIAS_ADD, 0, t.N1));
-  HIP_OK(c, tb_norm_fwd(c, R, P, o, 1, t.RES2, R.out, t.st2, rows));
+  HIP_OK(c, tb_norm_fwd(c, R, P, o, 1, t.RES2, R.out, t.st2, rows, cls));
   return GN_OK;
 }
 
@@ -1643,8 +1681,11 @@ static int tb_forward(gn_model *M, LayerRT &R, const float *X, int B) {
 // weight gradients read what the main stream has written and write only S,
 // S3 and this layer's gradients), branched off the main stream after each
 // input they read; null runs them on the main stream.
+// gpool (fused parameter path only, may be null): the gradient of a
+// CLSPooling above the block, read by the norm-2 backward in place of a
+// scattered R.gout.
 static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int B, float scale,
-                       hipStream_t side) {
+                       hipStream_t side, const float *gpool) {
   gn_ctx *c = M->ctx;
   const hipStream_t ss = side ? side : c->stream;
   auto fork = [&]() -> hipError_t {
@@ -1659,16 +1700,48 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   LayerRT::Tb &t = R.tb;
   float *cs = c->scratch;
   const size_t cap = c->scratch_floats;
+  const bool fused = tb_fused_params(R);
+  if (gpool && !fused) return set_err(c, GN_ERR_INVALID, "pooled gradient without the fused block backward");
+  // fused: the parameter-gradient jobs, run as one launch once their inputs exist
+  TbParamSet pset{};
+  double pbytes = 0;
+  const int nblk = ln_bwd_blocks(rows), np = T / ln_bwd_rows_per_block();
+  auto lin_job = [&](const float *S, int snp, int64_t sps, const float *Xl, int Mo, int Ni, int64_t wo,
+                     int64_t bo) {
+    TbParamJob &j = pset.lin[pset.nlin++];
+    j.S = S; j.np = snp; j.ps = sps;
+    j.X = Xl + (int64_t)(T - 1) * Ni; j.ldx = (int64_t)T * Ni;
+    j.dW = G + wo; j.db = G + bo; j.M = Mo; j.N = Ni;
+    pbytes += f4((double)B * snp * Mo + (double)B * Ni + (double)Mo * Ni + Mo);
+  };
+  auto norm_bwd_fused = [&](int k, const float *g, const float *gp, const float *x, const float *st,
+                            float *dx, float *lp, float *ts) -> hipError_t {
+    KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd",
+              f4((gp ? 2.0 : 3.0) * rows * D + 2.0 * rows + (double)nblk * 3 * D));
+    const hipError_t e = launch_ln_bwd_part(gp ? nullptr : g, gp, T, x, P + (k == 0 ? o.g1 : o.g2), st, dx, lp,
+                                            ts, rows, D, c->stream);
+    TbLnJob &j = pset.ln[pset.nln++];
+    j.part = lp; j.nblk = nblk; j.N = D;
+    j.dgam = G + (k == 0 ? o.g1 : o.g2); j.dbet = G + (k == 0 ? o.be1 : o.be2);
+    pbytes += f4((double)nblk * 2 * D + 2.0 * D);
+    return e;
+  };
   // norm 2 (LayerNorm: Q18 formula; RMSNorm: Q19), gamma / beta column sums
-  HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 1, R.gout, t.RES2, t.st2, t.G1, rows, scale));
-  HIP_OK(c, fork());
-  {
-    // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
-    // per-sample token sums S that the Q10 weight gradient needs anyway
-    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
-    HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, ss));
+  if (fused) {
+    HIP_OK(c, norm_bwd_fused(1, R.gout, gpool, t.RES2, t.st2, t.G1, t.LP2, t.TS2));
+    // ff2 (Linear): dz2 = dRES2, its token sums from the norm's block partials
+    lin_job(t.TS2, np, D, t.MID, D, FF, o.w2, o.b2);
+  } else {
+    HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 1, R.gout, t.RES2, t.st2, t.G1, rows, scale));
+    HIP_OK(c, fork());
+    {
+      // ff2 (Linear): dz2 = dRES2; the bias gradient sums every token, i.e. the
+      // per-sample token sums S that the Q10 weight gradient needs anyway
+      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
+      HIP_OK(c, launch_token_sum(t.G1, t.S, B, T, D, ss));
+    }
+    HIP_OK(c, tb_tok_dw(c, t.S, t.MID, G + o.w2, G + o.b2, B, T, D, FF, scale, ss));
   }
-  HIP_OK(c, tb_tok_dw(c, t.S, t.MID, G + o.w2, G + o.b2, B, T, D, FF, scale, ss));
   if (R.d.block_act == GN_BLOCK_ACT_SWIGLU) {
     // ff1 = SwiGLU called per token: its one saved entry (the last token's
     // input, gate and up) serves the first Backward (token 0); the later ones
@@ -1722,28 +1795,40 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
       KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF), ss);
       HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, ss));
     }
-    HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale, ss));
+    if (fused)
+      lin_job(t.S, 1, FF, t.N1, FF, D, o.w1, o.b1);
+    else
+      HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale, ss));
     // combined = dRES2 + dz1 W1
     HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
   }
   // norm 1
-  HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));
-  HIP_OK(c, fork());
-  {
-    // wOut (Linear): dz = dRES1
-    KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
-    HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, ss));
+  if (fused) {
+    HIP_OK(c, norm_bwd_fused(0, t.COMB, nullptr, t.RES1, t.st1, t.G2, t.LP1, t.TS1));
+    lin_job(t.TS1, np, D, t.O, D, D, o.wo, o.bo);  // wOut (Linear): dz = dRES1
+  } else {
+    HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));
+    HIP_OK(c, fork());
+    {
+      // wOut (Linear): dz = dRES1
+      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, D), ss);
+      HIP_OK(c, launch_token_sum(t.G2, t.S, B, T, D, ss));
+    }
+    HIP_OK(c, tb_tok_dw(c, t.S, t.O, G + o.wo, G + o.bo, B, T, D, D, scale, ss));
   }
-  HIP_OK(c, tb_tok_dw(c, t.S, t.O, G + o.wo, G + o.bo, B, T, D, D, scale, ss));
   HIP_OK(c, gemm_nn(c, t.G2, P + o.wo, t.GO, rows, D, D, EPI_SCALE, 0, nullptr, 0));
+  const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
+  // the fused attention backward forms the token sums of gQ, gK, gV itself
+  // (not when RoPE rotates gQ and gK after it)
+  const bool attn_sums = fused && !t.SC && !R.d.use_rope;
   {
     KTimer kt(c, GN_KCLASS_OTHER, "attn_bwd", attn_flops(B, T, R.NH, D / R.NH, R.causal, true));
     if (t.SC)
       HIP_OK(c, launch_attn_bwd_gemm(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal, t.SC,
                                      c->stream));
     else
-      HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal,
-                                c->stream));
+      HIP_OK(c, launch_attn_bwd(t.Q, t.K, t.V, t.GO, t.GQ, t.GK, t.GV, B, T, D, R.NH, R.causal, c->stream,
+                                attn_sums ? t.S3 : nullptr, sst));
   }
   if (R.d.use_rope) {  // transformer.go:660-664: conjugate rotation before wQ/wK
     KTimer kt(c, GN_KCLASS_OTHER, "rope", 2 * f4(2.0 * rows * D));
@@ -1751,19 +1836,24 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     HIP_OK(c, launch_rope(t.GK, t.rcos, t.rsin, rows, T, R.NH, D / R.NH, 1, c->stream));
   }
   const int64_t bo[3] = {o.bq, o.bk, o.bv};
-  const int64_t sst = (int64_t)M->maxB * D;  // stride of the three token-sum blocks
+  const int64_t wo3[3] = {o.wq, o.wk, o.wv};
   HIP_OK(c, fork());
-  {
+  if (!attn_sums) {
     // gQ, gK, gV are one [3][max batch][T][D] block: one token-sum launch,
     // blockIdx.z picking the member, B samples each
     KTimer kt(c, GN_KCLASS_OTHER, "token_sum", 3 * token_sum_bytes(B, T, D), ss);
     HIP_OK(c, launch_token_sum_multi(t.GQ, t.S3, B, T, D, 3, t.GK - t.GQ, sst, ss));
   }
-  {
+  if (fused) {
+    // dWq, dWk, dWv and their biases join the jobs: every parameter gradient
+    // of the block in one launch
+    for (int z = 0; z < 3; ++z) lin_job(t.S3 + z * sst, 1, D, X, D, D, wo3[z], bo[z]);
+    KTimer kt(c, GN_KCLASS_OTHER, "tb_params", pbytes, ss);
+    HIP_OK(c, launch_tb_params(pset, B, scale, ss));
+  } else {
     // dWq, dWk, dWv and their biases (Q10: token sums times the last token's
     // input, token sums summed over the batch) in one launch
     TokDwSet set{};
-    const int64_t wo3[3] = {o.wq, o.wk, o.wv};
     for (int z = 0; z < 3; ++z) {
       set.S[z] = t.S3 + z * sst;
       set.X[z] = X + (int64_t)(T - 1) * D;
@@ -1810,6 +1900,7 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
   bool pe_done = false;  // the PositionalEncoding output was written with the embedding rows
   bool drop_done = false;  // the Dropout's output was written by the Dense GEMM below it
   bool pool_done = false;  // the MaxPool2D's outputs were written by the Conv2D below it
+  bool cls_done = false;   // the CLSPooling's output was written by the block below it
   const int n = (int)M->L.size();
   for (int i = 0; i < n; ++i) {
     LayerRT &R = M->L[i];
@@ -1917,12 +2008,23 @@ static int model_forward(gn_model *M, const float *x, int B, bool for_loss) {
         break;
       }
       case GN_LAYER_CLSPOOL: {
+        if (cls_done) {
+          cls_done = false;
+          break;
+        }
         KTimer kt(c, GN_KCLASS_OTHER, "cls_fwd", f4(2.0 * B * R.D));
         HIP_OK(c, launch_cls_fwd(cur, R.out, B, R.T * R.D, R.D, c->stream));
         break;
       }
       case GN_LAYER_TRANSFORMER: {
-        int r = tb_forward(M, R, cur, B);
+        // a CLSPooling above gets token 0 of each sample from the block's last norm
+        LayerRT *up = i + 1 < n ? &M->L[i + 1] : nullptr;
+        float *cls = nullptr;
+        if (up && tb_cls_fusable(R, *up)) {
+          cls = up->out;
+          cls_done = true;
+        }
+        int r = tb_forward(M, R, cur, B, cls);
         if (r) return r;
         break;
       }
@@ -2099,6 +2201,8 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
   int bias_done = -1;      // a Dense layer whose bias gradient launch_tail_bwd wrote
   int dw_done = -1;        // ... and whose weight gradient it wrote
   int pool_bwd_done = -1;  // a MaxPool2D whose input gradient launch_tail_bwd wrote
+  const float *cls_gpool = nullptr;  // a CLSPooling's gradient left for the block below
+  float *pe_grad = nullptr;  // a PositionalEncoding's gradient left for the Embedding below
   for (int i = n - 1; i >= 0; --i) {
     LayerRT &R = M->L[i];
     const float *in = i == 0 ? x : M->L[i - 1].out;
@@ -2251,14 +2355,19 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_CLSPOOL:
-        if (below && below->gout) {  // transformer.go:1714-1723: row 0 gets g, the rest 0
+        if (below && tb_cls_fusable(*below, R)) {
+          cls_gpool = R.gout;  // the block's norm-2 backward reads it
+        } else if (below && below->gout) {  // transformer.go:1714-1723: row 0 gets g, the rest 0
           KTimer kt(c, GN_KCLASS_OTHER, "cls_bwd", f4((double)B * R.D + (double)B * R.T * R.D));
           HIP_OK(c, launch_cls_bwd(R.gout, below->gout, B, R.T * R.D, R.D, c->stream));
         }
         is_dz = false;
         break;
       case GN_LAYER_TRANSFORMER: {
-        int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale, side ? c->aux : nullptr);
+        const float *gpool = cls_gpool;
+        cls_gpool = nullptr;
+        int r = tb_backward(M, R, in, below ? below->gout : nullptr, B, scale, side ? c->aux : nullptr,
+                            gpool);
         if (r) return r;
         if (side) {  // the layer's Adam (M->adam_s) waits for its weight gradients
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
@@ -2448,6 +2557,12 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         break;
       }
       case GN_LAYER_POSENC: {  // gradW += g (transformer.go:112-118), summed over samples
+        if (below && below->d.kind == GN_LAYER_EMBEDDING && below->T == R.T && below->D == R.D &&
+            embed_grad_takes_pe(B, R.T, M->workers)) {
+          pe_grad = M->grads + R.poff;  // summed by the Embedding's gradient launch
+          is_dz = false;
+          break;
+        }
         KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * R.T * R.D + (double)R.T * R.D));
         HIP_OK(c, launch_colsum(R.gout, B, R.T * R.D, R.T * R.D, scale, M->grads + R.poff,
                                 c->scratch, c->scratch_floats, c->stream));
@@ -2458,12 +2573,16 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         // fill of the gradient table, then the contributing rows (one sample per chunk)
         const int Wc = std::max(1, std::min(M->workers, B));
         const int nch = (B + (B + Wc - 1) / Wc - 1) / ((B + Wc - 1) / Wc);
-        KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", f4((double)R.V * R.D + 2.0 * nch * R.T * R.D));
+        float *peg = pe_grad;
+        pe_grad = nullptr;
+        KTimer kt(c, GN_KCLASS_OTHER, "embed_grad",
+                  f4((double)R.V * R.D + 2.0 * nch * R.T * R.D +
+                     (peg ? (double)B * R.T * R.D + (double)R.T * R.D : 0.0)));
         if ((size_t)2 * nch * R.T > c->scratch_floats)
           return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed the scratch",
                          nch * R.T);
         HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
-                                    scale, M->L[M->emb].bad, c->stream, c->scratch, c->scratch_floats));
+                                    scale, M->L[M->emb].bad, c->stream, c->scratch, c->scratch_floats, peg));
         if (below && below->gout)  // indices carry no gradient (embedding.go:156-163)
           HIP_OK(c, launch_fill(below->gout, 0.0f, (int64_t)B * R.T, c->stream));
         is_dz = false;

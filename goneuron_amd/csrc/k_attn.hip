@@ -126,17 +126,38 @@ constexpr int EG_MAXL = 2048;  // contributing rows held in LDS
 // rows each (the fill the reference's zeroing amounts to, without a launch of
 // its own).
 constexpr int EG_ZR = 32;
+// Blocks past those (pe_grad not null): a PositionalEncoding's gradient below
+// which this Embedding sits, pe_grad[e] = scale * sum over the B samples of
+// g[b][e], b ascending (the same gradient rows; transformer.go:112-118), 256
+// columns e of the T x D table per block.
 __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict__ g,
                                                          const int32_t *__restrict__ ids,
                                                          float *__restrict__ gradE, int B, int T,
                                                          int D, int chunk, int L, float scale,
                                                          const int32_t *__restrict__ bad, int par,
-                                                         int V) {
+                                                         int V, float *__restrict__ pe_grad) {
   __shared__ int sid[EG_MAXL];
   __shared__ int csamp[EG_MAXL];
   __shared__ int first;
   __shared__ int hit[EG_ZR];
   const int l = blockIdx.x, nch = L / T;
+  const int zb = (V + EG_ZR - 1) / EG_ZR;
+  if (l >= L + zb) {  // PositionalEncoding block (uniform over the block)
+    const int64_t n = (int64_t)T * D, e = (int64_t)(l - L - zb) * 256 + threadIdx.x;
+    if (e >= n) return;
+    float acc = 0.f;
+    int b = 0;
+    for (; b + 15 < B; b += 16) {  // sixteen rows in flight, added in order
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = g[(int64_t)(b + u) * n + e];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc += v[u];
+    }
+    for (; b < B; ++b) acc += g[(int64_t)b * n + e];
+    pe_grad[e] = acc * scale;
+    return;
+  }
   for (int w = threadIdx.x; w < nch; w += 256) {
     const int c0 = w * chunk, c1 = min(B, c0 + chunk);
     int sm = c1 - 1;
@@ -374,26 +395,46 @@ __global__ __launch_bounds__(1024) void token_sum_kernel(const float *__restrict
 // them in LDS, then thread (g, i) accumulates rows 4g..4g+3.  blockIdx.z
 // selects the member.
 constexpr int TD_O = 16, TD_I = 64, TD_CB = 64;
-__global__ __launch_bounds__(256) void tok_dw_kernel(TokDwSet set, int B, int M, int N, int lds,
-                                                     int ldx, float scale) {
-  __shared__ float ss[TD_CB][TD_O];
-  __shared__ float xs[TD_CB][TD_I];
-  const float *__restrict__ S = set.S[blockIdx.z];
-  const float *__restrict__ X = set.X[blockIdx.z];
-  float *__restrict__ dW = set.dW[blockIdx.z];
-  float *__restrict__ db = set.db[blockIdx.z];
+struct TdShared {
+  float ss[TD_CB][TD_O];
+  float xs[TD_CB][TD_I];
+};
+// One 16 x 64 block (by, bx) of a Q10 gradient.  The token sum of sample b
+// is S[b * np * ps + o] when np = 1, or the np partial rows S[(b * np + j) *
+// ps + o], j ascending, when the producer left per-row-block partials (a
+// LayerNorm backward block of 16 token rows, np = T / 16).
+__device__ __forceinline__ void tok_dw_block(TdShared &sh, const float *__restrict__ S, int np,
+                                             int64_t ps, const float *__restrict__ X, int64_t ldx,
+                                             float *__restrict__ dW, float *__restrict__ db, int B,
+                                             int M, int N, float scale, int bx, int by) {
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
-  const int i0 = blockIdx.x * TD_I, o0 = blockIdx.y * TD_O;
-  const bool bias = blockIdx.x == 0 && tid < TD_O;
+  const int i0 = bx * TD_I, o0 = by * TD_O;
+  const bool bias = bx == 0 && tid < TD_O;
   constexpr int NS = TD_CB * TD_O / 256, NX = TD_CB * TD_I / 256;  // 4 and 16 loads per thread
   float acc[4] = {0.f, 0.f, 0.f, 0.f}, bs = 0.f;
   for (int b0 = 0; b0 < B; b0 += TD_CB) {
     const int nb = min(TD_CB, B - b0);
     float sv[NS], xv[NX];
+    const float *sp[NS];
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       const int e = tid + 256 * q, bb = e / TD_O, oo = e % TD_O;
-      sv[q] = bb < nb && o0 + oo < M ? S[(size_t)(b0 + bb) * lds + o0 + oo] : 0.f;
+      sp[q] = bb < nb && o0 + oo < M ? S + (size_t)(b0 + bb) * np * ps + o0 + oo : nullptr;
+      sv[q] = sp[q] ? sp[q][0] : 0.f;
+    }
+    // the further partials eight per element at a time, all elements' loads in
+    // flight together, each element's partials added in order
+    for (int j = 1; j < np; j += 8) {
+      float u[NS][8];
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) u[q][k] = sp[q] && j + k < np ? sp[q][(size_t)(j + k) * ps] : 0.f;
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (j + k < np) sv[q] += u[q][k];
     }
 #pragma unroll
     for (int q = 0; q < NX; ++q) {
@@ -403,18 +444,18 @@ __global__ __launch_bounds__(256) void tok_dw_kernel(TokDwSet set, int B, int M,
 #pragma unroll
     for (int q = 0; q < NS; ++q) {
       const int e = tid + 256 * q;
-      ss[e / TD_O][e % TD_O] = sv[q];
+      sh.ss[e / TD_O][e % TD_O] = sv[q];
     }
 #pragma unroll
-    for (int q = 0; q < NX; ++q) xs[(tid >> 6) + 4 * q][lane] = xv[q];
+    for (int q = 0; q < NX; ++q) sh.xs[(tid >> 6) + 4 * q][lane] = xv[q];
     __syncthreads();
     for (int bb = 0; bb < nb; ++bb) {
-      const float x = xs[bb][lane];
+      const float x = sh.xs[bb][lane];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc[k] += ss[bb][4 * g + k] * x;
+      for (int k = 0; k < 4; ++k) acc[k] += sh.ss[bb][4 * g + k] * x;
     }
     if (bias)
-      for (int bb = 0; bb < nb; ++bb) bs += ss[bb][tid];
+      for (int bb = 0; bb < nb; ++bb) bs += sh.ss[bb][tid];
     __syncthreads();
   }
   const int i = i0 + lane;
@@ -428,18 +469,29 @@ __global__ __launch_bounds__(256) void tok_dw_kernel(TokDwSet set, int B, int M,
   if (bias && o0 + tid < M) db[o0 + tid] = bs * scale;
 }
 
+__global__ __launch_bounds__(256) void tok_dw_kernel(TokDwSet set, int B, int M, int N, int lds,
+                                                     int ldx, float scale) {
+  __shared__ TdShared sh;
+  const int z = blockIdx.z;
+  tok_dw_block(sh, set.S[z], 1, lds, set.X[z], ldx, set.dW[z], set.db[z], B, M, N, scale, blockIdx.x,
+               blockIdx.y);
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm over rows of N (one wave64 per row)
 // ---------------------------------------------------------------------------
+// cls (may be null): rows r with r % clsT == 0 are also written to row r /
+// clsT of cls (a CLSPooling above the LayerNorm, transformer.go:1679-1725).
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x,
                                                      const float *__restrict__ gam,
                                                      const float *__restrict__ bet,
                                                      float *__restrict__ y,
                                                      float *__restrict__ stats, int rows, int N,
-                                                     float eps) {
+                                                     float eps, float *__restrict__ cls, int clsT) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (r >= rows) return;
   const float *xr = x + (int64_t)r * N;
+  float *crow = cls && r % clsT == 0 ? cls + (int64_t)(r / clsT) * N : nullptr;
   constexpr int LF_C = 8;  // up to 512 columns held in registers
   if (N <= 64 * LF_C) {
     // the row in registers, read once (its loads in flight together); the
@@ -469,7 +521,11 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
 #pragma unroll
     for (int c = 0; c < LF_C; ++c) {
       const int i = lane + 64 * c;
-      if (i < N) y[(int64_t)r * N + i] = gv[c] * ((v[c] - mean) / std) + bv[c];
+      if (i < N) {
+        const float o = gv[c] * ((v[c] - mean) / std) + bv[c];
+        y[(int64_t)r * N + i] = o;
+        if (crow) crow[i] = o;
+      }
     }
     if (lane == 0) {
       stats[2 * r] = mean;
@@ -487,7 +543,11 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
   }
   const float var = wsum(ss) / (float)N;
   const float std = (float)sqrt((double)(var + eps));
-  for (int i = lane; i < N; i += 64) y[(int64_t)r * N + i] = gam[i] * ((xr[i] - mean) / std) + bet[i];
+  for (int i = lane; i < N; i += 64) {
+    const float o = gam[i] * ((xr[i] - mean) / std) + bet[i];
+    y[(int64_t)r * N + i] = o;
+    if (crow) crow[i] = o;
+  }
   if (lane == 0) {
     stats[2 * r] = mean;
     stats[2 * r + 1] = std;
@@ -530,14 +590,21 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 // i + 64, ..., N <= 64 LN_MAXC), then finishes them row by row; the waves'
 // sums are added in wave order and written as one partial row pair
 // part[block][0 .. 2N) for ln_param_final.
+// gpool (may be null; then g is read): the gradient of a CLSPooling above,
+// row r / poolT of gpool for rows r with r % poolT == 0 and zero for the rest
+// (cls_bwd_kernel's rows, not materialised).  tsum (may be null): the
+// block's column sums of dx, tsum[block][0 .. N), the per-row-block partials
+// of the token sums that a Linear's Q10 gradient below needs.
 constexpr int LN_RW = 4, LN_MAXC = 8, LN_RPB = 4 * LN_RW;
 __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ gpool, int poolT,
                                                           const float *__restrict__ x,
                                                           const float *__restrict__ gam,
                                                           const float *__restrict__ stats,
                                                           float *__restrict__ dx,
-                                                          float *__restrict__ part, int rows, int N) {
-  __shared__ float red[4][2][LN_MAXC * 64];
+                                                          float *__restrict__ part,
+                                                          float *__restrict__ tsum, int rows, int N) {
+  __shared__ float red[4][3][LN_MAXC * 64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int rbase = blockIdx.x * LN_RPB + w * LN_RW;
   float gv[LN_RW][LN_MAXC], xv[LN_RW][LN_MAXC], gm[LN_MAXC], mean[LN_RW], sd[LN_RW];
@@ -551,16 +618,18 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
     const int r = min(rbase + q, rows - 1);
     mean[q] = stats[2 * r];
     sd[q] = stats[2 * r + 1];
+    const float *grow =
+        gpool ? (r % poolT == 0 ? gpool + (int64_t)(r / poolT) * N : nullptr) : g + (int64_t)r * N;
 #pragma unroll
     for (int j = 0; j < LN_MAXC; ++j) {
       const int i = lane + 64 * j;
-      gv[q][j] = i < N ? g[(int64_t)r * N + i] : 0.f;
+      gv[q][j] = i < N && grow ? grow[i] : 0.f;
       xv[q][j] = i < N ? x[(int64_t)r * N + i] : 0.f;
     }
   }
-  float pg[LN_MAXC], pb[LN_MAXC];
+  float pg[LN_MAXC], pb[LN_MAXC], pd[LN_MAXC];
 #pragma unroll
-  for (int j = 0; j < LN_MAXC; ++j) pg[j] = pb[j] = 0.f;
+  for (int j = 0; j < LN_MAXC; ++j) pg[j] = pb[j] = pd[j] = 0.f;
   const float nf = (float)N;
 #pragma unroll
   for (int q = 0; q < LN_RW; ++q) {
@@ -588,6 +657,7 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
         dx[(int64_t)r * N + i] = v;
         pg[j] += gi * (diff / std);
         pb[j] += gi;
+        pd[j] += v;
       }
     }
   }
@@ -595,28 +665,37 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
   for (int j = 0; j < LN_MAXC; ++j) {
     red[w][0][j * 64 + lane] = pg[j];
     red[w][1][j * 64 + lane] = pb[j];
+    if (tsum) red[w][2][j * 64 + lane] = pd[j];
   }
   __syncthreads();
   float *pp = part + (size_t)blockIdx.x * 2 * N;
   for (int i = threadIdx.x; i < N; i += 256) {
     pp[i] = (red[0][0][i] + red[1][0][i]) + (red[2][0][i] + red[3][0][i]);
     pp[N + i] = (red[0][1][i] + red[1][1][i]) + (red[2][1][i] + red[3][1][i]);
+    if (tsum)
+      tsum[(size_t)blockIdx.x * N + i] = (red[0][2][i] + red[1][2][i]) + (red[2][2][i] + red[3][2][i]);
   }
 }
 
 // dgamma / dbeta: the blocks' partials summed per column of [gamma | beta]:
 // a block takes 64 columns (one per lane), its 4 waves every 4th partial in
 // block order, and the 4 sums are added in wave order, times scale.
-__global__ __launch_bounds__(256) void ln_param_final(const float *__restrict__ part, int nblk, int N,
-                                                      float scale, float *__restrict__ dgam,
-                                                      float *__restrict__ dbet) {
-  __shared__ float red[4][64];
+__device__ __forceinline__ void ln_param_block(float (&red)[4][64], const float *__restrict__ part,
+                                               int nblk, int N, float scale, float *__restrict__ dgam,
+                                               float *__restrict__ dbet, int bx) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = blockIdx.x * 64 + lane;
+  const int c = bx * 64 + lane;
   float s = 0.f;
   if (c < 2 * N) {
     int b = w;
-    // sixteen partials in flight, added in the same order as below
+    // 32 or 16 partials in flight, added in the same order as below
+    for (; b + 124 < nblk; b += 128) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) v[u] = part[(size_t)(b + 4 * u) * 2 * N + c];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) s += v[u];
+    }
     for (; b + 60 < nblk; b += 64) {
       float v[16];
 #pragma unroll
@@ -640,6 +719,36 @@ __global__ __launch_bounds__(256) void ln_param_final(const float *__restrict__ 
     const float v = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) * scale;
     if (c < N) dgam[c] = v;
     else dbet[c - N] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void ln_param_final(const float *__restrict__ part, int nblk, int N,
+                                                      float scale, float *__restrict__ dgam,
+                                                      float *__restrict__ dbet) {
+  __shared__ float red[4][64];
+  ln_param_block(red, part, nblk, N, scale, dgam, dbet, blockIdx.x);
+}
+
+// A transformer block's parameter gradients in one launch: the blocks of
+// every LayerNorm job (ln_param_block, the longest chains of loads, so they
+// are dispatched first) and then of every Q10 Linear job (tok_dw_block), job
+// j owning blocks [start[j], start[j + 1]).
+__global__ __launch_bounds__(256) void tb_param_kernel(TbParamSet set, int B, float scale) {
+  __shared__ union {
+    TdShared td;
+    float red[4][64];
+  } sh;
+  const int bid = blockIdx.x, nj = set.nlin + set.nln;
+  int j = 0;
+  while (j + 1 < nj && bid >= set.start[j + 1]) ++j;
+  const int lb = bid - set.start[j];
+  if (j < set.nln) {
+    const TbLnJob &q = set.ln[j];
+    ln_param_block(sh.red, q.part, q.nblk, q.N, scale, q.dgam, q.dbet, lb);
+  } else {
+    const TbParamJob &p = set.lin[j - set.nln];
+    const int nbx = (p.N + TD_I - 1) / TD_I;
+    tok_dw_block(sh.td, p.S, p.np, p.ps, p.X, p.ldx, p.dW, p.db, B, p.M, p.N, scale, lb % nbx, lb / nbx);
   }
 }
 
@@ -869,6 +978,31 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__
   store_t(O, o, b, h, T, D, hd, w, lane);
 }
 
+// 16 values per lane summed over the 32 lanes of each half-wave (a halving
+// butterfly over lane bits 4..1, then lane bit 0): lane l ends with the total
+// of value (l & 31) >> 1 of its half.
+template <int OFF, int N>
+__device__ __forceinline__ void half_sums_step(float (&v)[16], int lane) {
+  const bool up = (lane & OFF) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float send = up ? v[i] : v[i + N / 2];
+    const float keep = up ? v[i + N / 2] : v[i];
+    v[i] = keep + __shfl_xor(send, OFF, 64);
+  }
+}
+__device__ __forceinline__ float half_sums(float (&v)[16], int lane) {
+  half_sums_step<16, 16>(v, lane);
+  half_sums_step<8, 8>(v, lane);
+  half_sums_step<4, 4>(v, lane);
+  half_sums_step<2, 2>(v, lane);
+  return v[0] + __shfl_xor(v[0], 1, 64);
+}
+
+// TS (may be null): the per-sample token sums of gQ, gK and gV (member m at
+// TS + m * tss, [B][D]) for the Q10 gradients of the three projections: each
+// wave's sums over its 32 queries (keys) meet in LDS and are added in wave
+// order.
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__ Q,
                                                        const float *__restrict__ K,
                                                        const float *__restrict__ V,
@@ -876,9 +1010,11 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__
                                                        float *__restrict__ GQ,
                                                        float *__restrict__ GK,
                                                        float *__restrict__ GV, int T, int D,
-                                                       int NH, int causal) {
+                                                       int NH, int causal, float *__restrict__ TS,
+                                                       int64_t tss) {
   __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP], sg[AT_T * AT_HP];
   __shared__ float sp[AT_T * AT_SP];  // P^T, then dS^T, as [j][i]
+  __shared__ float tred[3][4][AT_HD];  // token-sum partials per member and wave
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -923,11 +1059,19 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__
     for (int jt = 0; jt < 4; ++jt)
       if (!(causal && jt > w) && 32 * jt < T) mm_keys(acc, sk, ds[jt], jt, lane);
     store_t(GQ, acc, b, h, T, D, hd, w, lane);
+    if (TS) {  // sum over the wave's queries i < T of each d
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = i < T ? acc[r] : 0.f;
+      const float s = half_sums(v, lane);
+      const int rr = (lane & 31) >> 1;
+      if ((lane & 1) == 0) tred[0][w][mrow(rr, lane)] = s;
+    }
   }
   // the key-side products sum over queries of every wave: P^T and then dS^T
   // go through LDS as [j][i], and wave w takes keys j in [32w, 32w+32)
   const int j0 = 32 * w;
-  auto keyside = [&](const float *Yq, float *G) {
+  auto keyside = [&](const float *Yq, float *G, int m) {
     fx16 acc = fx16{};
     // X[j][d] = sum_i Zt[j][i] Yq[i][d]; Zt[j][i] = 0 for i < j under the mask
     for (int ii = causal ? j0 : 0; ii < T; ii += 2) {
@@ -935,10 +1079,16 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__
       const float bv = Yq[(ii + (lane >> 5)) * AT_HP + (lane & 31)];
       acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
     }
+    float s = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int j = j0 + mrow(r, lane), d = lane & 31;
       if (j < T && d < hd) G[((int64_t)b * T + j) * D + h * hd + d] = acc[r];
+      s += j < T ? acc[r] : 0.f;
+    }
+    if (TS) {  // sum over the wave's keys j < T of d = lane % 32
+      s += __shfl_xor(s, 32, 64);
+      if (lane < 32) tred[m][w][lane] = s;
     }
   };
 #pragma unroll
@@ -946,14 +1096,21 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__
 #pragma unroll
     for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = pt[jt][r];
   __syncthreads();
-  keyside(sg, GV);  // gV_j = sum_i p_ij gO_i
+  keyside(sg, GV, 2);  // gV_j = sum_i p_ij gO_i
   __syncthreads();
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = ds[jt][r];
   __syncthreads();
-  keyside(sq, GK);  // gK_j = sum_i dS_ij q_i
+  keyside(sq, GK, 1);  // gK_j = sum_i dS_ij q_i
+  if (TS) {
+    __syncthreads();
+    const int m = threadIdx.x >> 5, d = threadIdx.x & 31;
+    if (m < 3 && d < hd)
+      TS[m * tss + (int64_t)b * D + h * hd + d] =
+          ((tred[m][0][d] + tred[m][1][d]) + tred[m][2][d]) + tred[m][3][d];
+  }
 }
 
 static unsigned blocks_for(int64_t n) {
@@ -989,14 +1146,22 @@ hipError_t launch_pe_add(const float *x, const float *pe, float *out, int B, int
   return hipGetLastError();
 }
 
-hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
-                             int D, int W, float scale, const int32_t *bad, hipStream_t s, float *ws,
-                             size_t ws_floats) {
+static int embed_grad_rows(int B, int T, int W) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   const int chunk = (B + Wc - 1) / Wc;
-  const int nsamp = (B + chunk - 1) / chunk;  // one contributing sample per chunk
-  const int L = nsamp * T;
+  return ((B + chunk - 1) / chunk) * T;  // one contributing sample per chunk
+}
+
+bool embed_grad_takes_pe(int B, int T, int W) { return B > 0 && embed_grad_rows(B, T, W) <= EG_MAXL; }
+
+hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
+                             int D, int W, float scale, const int32_t *bad, hipStream_t s, float *ws,
+                             size_t ws_floats, float *pe_grad) {
+  const int Wc = W < 1 ? 1 : (W > B ? B : W);
+  const int chunk = (B + Wc - 1) / Wc;
+  const int L = embed_grad_rows(B, T, W);
   const int zb = (V + EG_ZR - 1) / EG_ZR;
+  if (pe_grad && !embed_grad_takes_pe(B, T, W)) return hipErrorInvalidValue;
   if (L > EG_MAXL) {
     // the row lists in the caller's workspace: 2 L ints
     if (!ws || ws_floats < (size_t)2 * L) return hipErrorInvalidValue;
@@ -1007,8 +1172,9 @@ hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, i
                        scale, V);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
-                     scale, bad, W > 1 ? 1 : 0, V);
+  const int pb = pe_grad ? (int)(((int64_t)T * D + 255) / 256) : 0;
+  hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb + pb), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
+                     scale, bad, W > 1 ? 1 : 0, V, pe_grad);
   return hipGetLastError();
 }
 
@@ -1046,9 +1212,10 @@ hipError_t launch_tok_dw(const TokDwSet &set, int nmem, int B, int M, int N, int
 }
 
 hipError_t launch_ln_fwd(const float *x, const float *gam, const float *bet, float *y, float *stats,
-                         int rows, int N, float eps, hipStream_t s) {
+                         int rows, int N, float eps, hipStream_t s, float *cls, int clsT) {
+  if (cls && clsT < 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(ln_fwd_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, x, gam, bet, y, stats,
-                     rows, N, eps);
+                     rows, N, eps, cls, clsT);
   return hipGetLastError();
 }
 
@@ -1060,9 +1227,47 @@ hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam
   const int nblk = (rows + LN_RPB - 1) / LN_RPB;
   if (N > 64 * LN_MAXC || (size_t)nblk * 2 * N > ws_cap) return hipErrorNotSupported;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(256), 0, s, g, x, gam, stats, dx, ws, rows, N);
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(256), 0, s, g, nullptr, 1, x, gam, stats, dx, ws,
+                     nullptr, rows, N);
   hipLaunchKernelGGL(ln_param_final, dim3((2 * N + 63) / 64), dim3(256), 0, s, ws, nblk, N, scale, dgam,
                      dbet);
+  return hipGetLastError();
+}
+
+int ln_bwd_blocks(int rows) { return (rows + LN_RPB - 1) / LN_RPB; }
+int ln_bwd_rows_per_block() { return LN_RPB; }
+bool ln_bwd_part_supported(int N) { return N >= 1 && N <= 64 * LN_MAXC; }
+
+hipError_t launch_ln_bwd_part(const float *g, const float *gpool, int poolT, const float *x,
+                              const float *gam, const float *stats, float *dx, float *part, float *tsum,
+                              int rows, int N, hipStream_t s) {
+  if (!ln_bwd_part_supported(N) || (!g && !gpool) || (gpool && poolT < 1) || !part)
+    return hipErrorInvalidValue;
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(ln_bwd_blocks(rows)), dim3(256), 0, s, g, gpool,
+                     gpool ? poolT : 1, x, gam, stats, dx, part, tsum, rows, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_tb_params(TbParamSet &set, int B, float scale, hipStream_t s) {
+  if (set.nlin < 0 || set.nlin > TBP_MAXLIN || set.nln < 0 || set.nln > TBP_MAXLN)
+    return hipErrorInvalidValue;
+  int n = 0, j = 0;
+  for (int k = 0; k < set.nln; ++k, ++j) {
+    const TbLnJob &q = set.ln[k];
+    if (q.N < 0 || q.nblk < 1 || !q.part || !q.dgam || !q.dbet) return hipErrorInvalidValue;
+    set.start[j] = n;
+    n += (2 * q.N + 63) / 64;
+  }
+  for (int k = 0; k < set.nlin; ++k, ++j) {
+    const TbParamJob &p = set.lin[k];
+    if (p.M < 0 || p.N < 0 || p.np < 1 || !p.S || !p.X || !p.dW || !p.db) return hipErrorInvalidValue;
+    set.start[j] = n;
+    n += ((p.N + TD_I - 1) / TD_I) * ((p.M + TD_O - 1) / TD_O);
+  }
+  set.start[j] = n;
+  if (n == 0 || B <= 0) return hipSuccess;
+  hipLaunchKernelGGL(tb_param_kernel, dim3(n), dim3(256), 0, s, set, B, scale);
   return hipGetLastError();
 }
 
@@ -1296,9 +1501,9 @@ hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float
 
 hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *GO,
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
-                           hipStream_t s) {
+                           hipStream_t s, float *TS, int64_t tss) {
   hipLaunchKernelGGL(attn_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, GO, GQ, GK, GV, T, D,
-                     NH, causal);
+                     NH, causal, TS, tss);
   return hipGetLastError();
 }
 
