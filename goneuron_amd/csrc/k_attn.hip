@@ -24,7 +24,6 @@ namespace gn {
 
 constexpr int AT_T = 128;   // max sequence length held in LDS
 constexpr int AT_HD = 32;   // max head dim held in LDS
-constexpr int AT_HP = AT_HD + 1;
 
 __device__ __forceinline__ float wsum(float v) {
 #pragma unroll
@@ -819,289 +818,391 @@ __global__ __launch_bounds__(256) void rms_bwd_kernel(const float *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Causal multi-head attention on fp32 MFMA, one workgroup per (sample, head).
-// Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd); T <= 128 and
-// hd <= 32 are held in LDS (zero-padded to 128 x 32).  Wave w owns queries
-// i in [32w, 32w+32) and works on transposed scores S^T[j][i] = k_j . q_i, so
-// each lane holds one query's column: the softmax over keys j is a reduction
-// inside the lane plus one exchange with lane l^32, and the probabilities stay
-// in registers in exactly the order the next MFMA consumes them (below).  The
-// backward pass recomputes them from Q and K instead of storing B*NH*T*T.
-// v_mfma_f32_32x32x2_f32 operands: A[m = l%32][k = l/32], B[k = l/32][n = l%32];
-// result register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-// A product X[.][i] = sum_j Y[.][j] Z[j][i] whose Z^T comes from such a result
-// takes, at MFMA step s, key j = 8*(s/4) + 4*(l/32) + s%4 of the 32-key tile:
-// lane l then supplies Z register s as its B operand.
+// Causal multi-head attention on fp32 MFMA, one workgroup of 4 waves per
+// (sample, head).  Q/K/V/O are [B*T, D] with head h in columns [h*hd,
+// (h+1)*hd); T <= 128 and hd <= 32 are held in LDS, staged [t][d] (zero
+// padded to 128 x 32) at a 16-byte-aligned pitch (A16_HP, read as float4).
+// The tokens are cut into eight 16-token tiles: wave w owns query tiles w and
+// 7 - w, and in the backward's key-side products key tiles w and 7 - w, so
+// under the causal mask every wave works 9 of the 36 live tile pairs (a wave
+// per 32 queries, the first layout, gave one wave 4 of 10 tile pairs and
+// another 1: forward 13.5 -> 10.6 us, backward 32.1 -> 23.6 us on C4's shape).
+// The backward recomputes the probabilities from Q and K instead of storing
+// B*NH*T*T.
+// v_mfma_f32_16x16x4_f32: A[m = l%16][k = l/16], B[k = l/16][n = l%16],
+// result register r of lane l is row 4*(l/16) + r, column l%16.
+// Scores are formed transposed, S^T = K Q^T, so lane l holds query l%16 of
+// its tile and keys 4*(l/16) + r; a product over keys (P V, dS K) then takes
+// at step s of key tile kt key 16 kt + 4*(l/16) + s, i.e. the lane's own
+// register s as its B operand, and the matching row of V (K) from LDS.
 // ---------------------------------------------------------------------------
-typedef float fx16 __attribute__((ext_vector_type(16)));
-constexpr int AT_SP = AT_T + 1;  // row pitch of the T x T LDS matrix
+typedef float fx4 __attribute__((ext_vector_type(4)));
+constexpr int A16_HP = 36;   // [t][d] pitch: rows 16-byte aligned, float4 reads conflict-free
+constexpr int A16_SP = 132;  // [key][query] pitch of the P^T / dS^T matrix
 
-__device__ __forceinline__ int mrow(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+__device__ __forceinline__ fx4 mfma16(float a, float b, const fx4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
-// Stage rows [0, 128) x cols [0, 32) of head h into LDS (pitch AT_HP), zero
-// padded.  With hd, D and the head offset multiples of 4 every thread issues
-// its four 16-byte loads before any store; otherwise element by element.
-__device__ __forceinline__ void stage_head(float *dst, const float *__restrict__ src, int b, int h,
-                                           int T, int D, int hd) {
-  if ((hd & 3) == 0 && (D & 3) == 0 && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
-    float4 v[4];
+// Rows [0, 128) x cols [0, 32) of head h of N matrices, zero padded, at
+// pitch A16_HP; with hd, D and the pointers multiples of 4 floats every
+// thread issues all its 16-byte loads (4 per matrix) before any store.
+template <int N>
+__device__ __forceinline__ void stage16(float *const (&dst)[N], const float *const (&src)[N], int b, int h,
+                                        int T, int D, int hd) {
+  bool vec = (hd & 3) == 0 && (D & 3) == 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int f = threadIdx.x + 256 * q;  // 128 rows x 8 float4
-      const int t = f >> 3, d = (f & 7) << 2;
-      v[q] = (t < T && d < hd)
-                 ? *reinterpret_cast<const float4 *>(src + ((int64_t)b * T + t) * D + h * hd + d)
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+  for (int m = 0; m < N; ++m) vec = vec && (reinterpret_cast<uintptr_t>(src[m]) & 15) == 0;
+  if (vec) {
+    float4 v[N][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int f = threadIdx.x + 256 * q;
-      float *o = dst + (f >> 3) * AT_HP + ((f & 7) << 2);
-      o[0] = v[q].x;
-      o[1] = v[q].y;
-      o[2] = v[q].z;
-      o[3] = v[q].w;
-    }
+    for (int m = 0; m < N; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int f = threadIdx.x + 256 * q;  // 128 rows x 8 float4
+        const int t = f >> 3, d = (f & 7) << 2;
+        v[m][q] = (t < T && d < hd)
+                      ? *reinterpret_cast<const float4 *>(src[m] + ((int64_t)b * T + t) * D + h * hd + d)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+    for (int m = 0; m < N; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int f = threadIdx.x + 256 * q;
+        *reinterpret_cast<float4 *>(dst[m] + (f >> 3) * A16_HP + ((f & 7) << 2)) = v[m][q];
+      }
     return;
   }
-  for (int e = threadIdx.x; e < AT_T * AT_HD; e += 256) {
-    const int t = e / AT_HD, d = e % AT_HD;
-    dst[t * AT_HP + d] = (t < T && d < hd) ? src[((int64_t)b * T + t) * D + h * hd + d] : 0.f;
+  for (int m = 0; m < N; ++m)
+    for (int e = threadIdx.x; e < AT_T * AT_HD; e += 256) {
+      const int t = e / AT_HD, d = e % AT_HD;
+      dst[m][t * A16_HP + d] = (t < T && d < hd) ? src[m][((int64_t)b * T + t) * D + h * hd + d] : 0.f;
+    }
+}
+
+// The lane's 8 head-dim values of row `row` that the B operand of a 32-deep
+// score product takes: d = 4*(l/16) + s (steps 0-3) and 16 + 4*(l/16) + s.
+__device__ __forceinline__ void rows16(float4 (&r)[2], const float *s, int row, int lane) {
+  const float4 *p = reinterpret_cast<const float4 *>(s + row * A16_HP + 4 * (lane >> 4));
+  r[0] = p[0];
+  r[1] = p[4];
+}
+
+// X^T tile: acc[r] = sum_d Y[16 yt + 4*(l/16) + r][d] * Z[row of zb][d] (Y rows
+// from LDS, the lane's Z row in zb), k order d = 4*(l/16) + s, then + 16.
+__device__ __forceinline__ fx4 tile_t(const float *sy, const float4 (&zb)[2], int yt, int lane) {
+  float4 yb[2];
+  rows16(yb, sy, 16 * yt + (lane & 15), lane);
+  fx4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mfma16(yb[0].x, zb[0].x, acc);
+  acc = mfma16(yb[0].y, zb[0].y, acc);
+  acc = mfma16(yb[0].z, zb[0].z, acc);
+  acc = mfma16(yb[0].w, zb[0].w, acc);
+  acc = mfma16(yb[1].x, zb[1].x, acc);
+  acc = mfma16(yb[1].y, zb[1].y, acc);
+  acc = mfma16(yb[1].z, zb[1].z, acc);
+  acc = mfma16(yb[1].w, zb[1].w, acc);
+  return acc;
+}
+
+// o[half][r] += sum over the 16 keys of tile kt of Y[j][16 half + l%16] * Zt[j]
+// (Zt the lane's transposed-score registers): the head-dim-major product
+// O^T[d][i] = sum_j Y[j][d] Z[i][j].
+__device__ __forceinline__ void keys_t(fx4 (&o)[2], const float *sy, const fx4 &zt, int kt, int lane) {
+  const int j0 = 16 * kt + 4 * (lane >> 4), d = lane & 15;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    o[0] = mfma16(sy[(j0 + s) * A16_HP + d], zt[s], o[0]);
+    o[1] = mfma16(sy[(j0 + s) * A16_HP + 16 + d], zt[s], o[1]);
   }
 }
 
-// acc += A_rows[32 rows from r0] . B_rows[32 rows from c0]^T over k in [0, 32),
-// both stored [row][k] at pitch AT_HP (the padding columns are zero).
-__device__ __forceinline__ void mm_nt(fx16 &acc, const float *A, const float *Bm, int r0, int c0,
-                                      int lane) {
-#pragma unroll
-  for (int k = 0; k < AT_HD; k += 2) {
-    const float a = A[(r0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
-    const float b = Bm[(c0 + (lane & 31)) * AT_HP + k + (lane >> 5)];
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
-  }
-}
-
-// acc[d][i] += sum over the 32 keys of tile jt of Y[j][d] * Zt[j][i], with Y in
-// LDS ([j][d], pitch AT_HP) and Zt the transposed-score-layout registers.
-__device__ __forceinline__ void mm_keys(fx16 &acc, const float *Y, const fx16 &Zt, int jt, int lane) {
-#pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    const int j = 32 * jt + 8 * (s >> 2) + 4 * (lane >> 5) + (s & 3);
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Y[j * AT_HP + (lane & 31)], Zt[s], acc, 0, 0, 0);
-  }
-}
-
-// Probabilities P^T[j][i] of the wave's 32 queries in registers: scores /
-// sqrt(hd), -1e9 on causal-masked entries (as the reference), columns j >= T do
-// not exist; row softmax (activations.go:161-183) with a float32 exp: the
-// reference rounds a float64 exp to float32, expf is within 1 ulp of that and
-// the float64 exp of 64 entries per lane dominated the kernel.  The divisions
-// by sqrt(hd) and by the row sum are products with the reciprocal (within an
-// ulp of the quotient; 128 IEEE divisions per lane had cost a quarter of the
-// kernel: 17.8 -> 13.5 us forward, 36.7 -> 31.1 us backward on C4's shape).
-// Tiles jt > w are fully masked under the causal mask and are left at 0.
-__device__ __forceinline__ void attn_probs(fx16 (&pt)[4], const float *sq, const float *sk, int T,
-                                           int causal, float scale, int w, int lane) {
-  const int i = 32 * w + (lane & 31);
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-    pt[jt] = fx16{};
-    if (!(causal && jt > w)) mm_nt(pt[jt], sk, sq, 32 * jt, 32 * w, lane);
-  }
-  const float inv_scale = 1.0f / scale;
+// Softmax of the scores of query i = 16 qt + l%16 over the key tiles kt <=
+// klim (the rest are fully masked and contribute exact zeros): scores /
+// sqrt(hd), -1e9 on causal-masked entries (as the reference), keys j >= T
+// absent; float32 exp, products with the reciprocals of sqrt(hd) and of the
+// row sum (attn_probs' arithmetic).
+__device__ __forceinline__ void probs16(fx4 (&st)[8], int qt, int klim, int T, int causal,
+                                        float inv_scale, int lane) {
+  const int i = 16 * qt + (lane & 15);
   float mx = -__builtin_inff();
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int kt = 0; kt < 8; ++kt) {
+    if (kt > klim) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 32 * jt + mrow(r, lane);
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * kt + 4 * (lane >> 4) + r;
       float sc;
       if (j >= T) sc = -__builtin_inff();
       else if (causal && j > i) sc = -1e9f;
-      else sc = pt[jt][r] * inv_scale;
-      pt[jt][r] = sc;
+      else sc = st[kt][r] * inv_scale;
+      st[kt][r] = sc;
       mx = fmaxf(mx, sc);
     }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
   float sum = 0.f;
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int kt = 0; kt < 8; ++kt) {
+    if (kt > klim) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 32 * jt + mrow(r, lane);
-      const float e = j < T ? expf(pt[jt][r] - mx) : 0.f;
-      pt[jt][r] = e;
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * kt + 4 * (lane >> 4) + r;
+      const float e = j < T ? expf(st[kt][r] - mx) : 0.f;
+      st[kt][r] = e;
       sum += e;
     }
+  }
+  sum += __shfl_xor(sum, 16, 64);
   sum += __shfl_xor(sum, 32, 64);
   const float inv_sum = 1.0f / sum;
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int kt = 0; kt < 8; ++kt) {
+    if (kt > klim) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) pt[jt][r] = pt[jt][r] * inv_sum;
+    for (int r = 0; r < 4; ++r) st[kt][r] = st[kt][r] * inv_sum;
+  }
 }
 
-// Store a [d][i] (transposed) accumulator as head-h columns of G [B*T, D].
-__device__ __forceinline__ void store_t(float *G, const fx16 &v, int b, int h, int T, int D, int hd,
-                                        int w, int lane) {
-  const int i = 32 * w + (lane & 31);
+// Store a head-dim-major accumulator pair (O^T[d][i]: lane l, register r is d
+// = 4*(l/16) + r + 16 half, query i = l%16 of tile qt) as head-h columns of G.
+__device__ __forceinline__ void store16_t(float *G, const fx4 (&v)[2], int b, int h, int T, int D, int hd,
+                                          int qt, int lane) {
+  const int i = 16 * qt + (lane & 15);
   if (i >= T) return;
+  float *row = G + ((int64_t)b * T + i) * D + h * hd;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int d = mrow(r, lane);
-    if (d < hd) G[((int64_t)b * T + i) * D + h * hd + d] = v[r];
+  for (int half = 0; half < 2; ++half) {
+    const int d0 = 16 * half + 4 * (lane >> 4);
+    if (d0 + 3 < hd && ((reinterpret_cast<uintptr_t>(row + d0) & 15) == 0)) {
+      *reinterpret_cast<float4 *>(row + d0) = make_float4(v[half][0], v[half][1], v[half][2], v[half][3]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (d0 + r < hd) row[d0 + r] = v[half][r];
+    }
   }
 }
 
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const float *__restrict__ Q,
-                                                       const float *__restrict__ K,
-                                                       const float *__restrict__ V,
-                                                       float *__restrict__ O, int T, int D,
-                                                       int NH, int causal) {
-  __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP];
+__global__ __launch_bounds__(256) void attn16_fwd_kernel(const float *__restrict__ Q,
+                                                         const float *__restrict__ K,
+                                                         const float *__restrict__ V,
+                                                         float *__restrict__ O, int T, int D, int NH,
+                                                         int causal) {
+  __shared__ __align__(16) float sq[AT_T * A16_HP];
+  __shared__ __align__(16) float sk[AT_T * A16_HP];
+  __shared__ __align__(16) float sv[AT_T * A16_HP];
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  stage_head(sq, Q, b, h, T, D, hd);
-  stage_head(sk, K, b, h, T, D, hd);
-  stage_head(sv, V, b, h, T, D, hd);
-  __syncthreads();
-  const float scale = (float)sqrt((double)hd);
-  fx16 pt[4];
-  attn_probs(pt, sq, sk, T, causal, scale, w, lane);
-  // O^T[d][i] = sum_j V[j][d] P[i][j]
-  fx16 o = fx16{};
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-    if (!(causal && jt > w) && 32 * jt < T) mm_keys(o, sv, pt[jt], jt, lane);
-  store_t(O, o, b, h, T, D, hd, w, lane);
-}
-
-// 16 values per lane summed over the 32 lanes of each half-wave (a halving
-// butterfly over lane bits 4..1, then lane bit 0): lane l ends with the total
-// of value (l & 31) >> 1 of its half.
-template <int OFF, int N>
-__device__ __forceinline__ void half_sums_step(float (&v)[16], int lane) {
-  const bool up = (lane & OFF) != 0;
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) {
-    const float send = up ? v[i] : v[i + N / 2];
-    const float keep = up ? v[i + N / 2] : v[i];
-    v[i] = keep + __shfl_xor(send, OFF, 64);
-  }
-}
-__device__ __forceinline__ float half_sums(float (&v)[16], int lane) {
-  half_sums_step<16, 16>(v, lane);
-  half_sums_step<8, 8>(v, lane);
-  half_sums_step<4, 4>(v, lane);
-  half_sums_step<2, 2>(v, lane);
-  return v[0] + __shfl_xor(v[0], 1, 64);
-}
-
-// TS (may be null): the per-sample token sums of gQ, gK and gV (member m at
-// TS + m * tss, [B][D]) for the Q10 gradients of the three projections: each
-// wave's sums over its 32 queries (keys) meet in LDS and are added in wave
-// order.
-__global__ __launch_bounds__(256) void attn_bwd_kernel(const float *__restrict__ Q,
-                                                       const float *__restrict__ K,
-                                                       const float *__restrict__ V,
-                                                       const float *__restrict__ GO,
-                                                       float *__restrict__ GQ,
-                                                       float *__restrict__ GK,
-                                                       float *__restrict__ GV, int T, int D,
-                                                       int NH, int causal, float *__restrict__ TS,
-                                                       int64_t tss) {
-  __shared__ float sq[AT_T * AT_HP], sk[AT_T * AT_HP], sv[AT_T * AT_HP], sg[AT_T * AT_HP];
-  __shared__ float sp[AT_T * AT_SP];  // P^T, then dS^T, as [j][i]
-  __shared__ float tred[3][4][AT_HD];  // token-sum partials per member and wave
-  const int b = blockIdx.x / NH, h = blockIdx.x % NH;
-  const int hd = D / NH;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  stage_head(sq, Q, b, h, T, D, hd);
-  stage_head(sk, K, b, h, T, D, hd);
-  stage_head(sv, V, b, h, T, D, hd);
-  stage_head(sg, GO, b, h, T, D, hd);
-  __syncthreads();
-  const float scale = (float)sqrt((double)hd), inv_scale = 1.0f / scale;
-  const int i = 32 * w + (lane & 31);
-  fx16 pt[4];
-  attn_probs(pt, sq, sk, T, causal, scale, w, lane);
-  // dP^T[j][i] = v_j . gO_i ; r_i = sum_j dP_ij p_ij ; dS = (dP p - p r) / sqrt(hd)
-  fx16 ds[4];
-  float rs = 0.f;
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt) {
-    ds[jt] = fx16{};
-    if (!(causal && jt > w)) mm_nt(ds[jt], sv, sg, 32 * jt, 32 * w, lane);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 32 * jt + mrow(r, lane);
-      const bool live = j < T && !(causal && j > i);
-      if (!live) ds[jt][r] = 0.f;
-      rs += ds[jt][r] * pt[jt][r];
-    }
-  }
-  rs += __shfl_xor(rs, 32, 64);
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 32 * jt + mrow(r, lane);
-      const bool live = j < T && !(causal && j > i);
-      const float p = pt[jt][r];
-      ds[jt][r] = live ? (ds[jt][r] * p - p * rs) * inv_scale : 0.f;
-    }
-  // gQ^T[d][i] = sum_j K[j][d] dS[i][j]
   {
-    fx16 acc = fx16{};
+    float *const dst[3] = {sq, sk, sv};
+    const float *const src[3] = {Q, K, V};
+    stage16<3>(dst, src, b, h, T, D, hd);
+  }
+  __syncthreads();
+  const float inv_scale = 1.0f / (float)sqrt((double)hd);
+  const int nt = (T + 15) >> 4;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-      if (!(causal && jt > w) && 32 * jt < T) mm_keys(acc, sk, ds[jt], jt, lane);
-    store_t(GQ, acc, b, h, T, D, hd, w, lane);
-    if (TS) {  // sum over the wave's queries i < T of each d
-      float v[16];
+  for (int u = 0; u < 2; ++u) {
+    const int qt = u ? 7 - w : w;
+    if (qt >= nt) continue;
+    const int klim = causal ? qt : nt - 1;
+    float4 qb[2];
+    rows16(qb, sq, 16 * qt + (lane & 15), lane);
+    fx4 st[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[r] = i < T ? acc[r] : 0.f;
-      const float s = half_sums(v, lane);
-      const int rr = (lane & 31) >> 1;
-      if ((lane & 1) == 0) tred[0][w][mrow(rr, lane)] = s;
+    for (int kt = 0; kt < 8; ++kt)
+      if (kt <= klim) st[kt] = tile_t(sk, qb, kt, lane);
+    probs16(st, qt, klim, T, causal, inv_scale, lane);
+    // O^T[d][i] = sum_j V[j][d] P[i][j]
+    fx4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+      if (kt <= klim) keys_t(o, sv, st[kt], kt, lane);
+    store16_t(O, o, b, h, T, D, hd, qt, lane);
+  }
+}
+
+// Backward, same tiles: query side (wave w: query tiles w, 7 - w) recomputes
+// P, forms dP^T = V gO^T, r_i = sum_j dP_ij p_ij and dS = (dP p - p r) /
+// sqrt(hd), writes gQ = dS K and leaves P^T (then dS^T) in LDS as [j][i]; key
+// side (wave w: key tiles w, 7 - w) sums gV_j = sum_i p_ij gO_i and gK_j =
+// sum_i dS_ij q_i over the live query tiles.  TS (may be null): the
+// per-sample token sums of gQ, gK and gV (member m at TS + m * tss, [B][D])
+// for the Q10 gradients of the three projections: each wave's sums over its
+// queries (keys) meet in LDS and are added in wave order.
+__global__ __launch_bounds__(256) void attn16_bwd_kernel(const float *__restrict__ Q,
+                                                         const float *__restrict__ K,
+                                                         const float *__restrict__ V,
+                                                         const float *__restrict__ GO,
+                                                         float *__restrict__ GQ,
+                                                         float *__restrict__ GK,
+                                                         float *__restrict__ GV, int T, int D,
+                                                         int NH, int causal, float *__restrict__ TS,
+                                                         int64_t tss) {
+  __shared__ __align__(16) float sq[AT_T * A16_HP];
+  __shared__ __align__(16) float sk[AT_T * A16_HP];
+  __shared__ __align__(16) float sv[AT_T * A16_HP];
+  __shared__ __align__(16) float sg[AT_T * A16_HP];
+  __shared__ __align__(16) float sp[AT_T * A16_SP];  // P^T, then dS^T, as [j][i]
+  __shared__ float tred[3][4][AT_HD];
+  const int b = blockIdx.x / NH, h = blockIdx.x % NH;
+  const int hd = D / NH;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  {
+    float *const dst[4] = {sq, sk, sv, sg};
+    const float *const src[4] = {Q, K, V, GO};
+    stage16<4>(dst, src, b, h, T, D, hd);
+  }
+  __syncthreads();
+  const float inv_scale = 1.0f / (float)sqrt((double)hd);
+  const int nt = (T + 15) >> 4;
+  fx4 dsk[2][8];  // dS^T of the wave's two query tiles, kept for the gK pass
+  float tq[8];    // gQ token-sum partials: value v = 4 half + r, d = 4*(l/16) + r + 16 half
+#pragma unroll
+  for (int v = 0; v < 8; ++v) tq[v] = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int qt = u ? 7 - w : w;
+    if (qt >= nt) continue;
+    const int klim = causal ? qt : nt - 1;
+    const int i = 16 * qt + (lane & 15);
+    float4 qb[2], gb[2];
+    rows16(qb, sq, i, lane);
+    rows16(gb, sg, i, lane);
+    fx4 pt[8];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+      if (kt <= klim) {
+        pt[kt] = tile_t(sk, qb, kt, lane);
+        dsk[u][kt] = tile_t(sv, gb, kt, lane);  // dP^T[j][i] = v_j . gO_i
+      }
+    probs16(pt, qt, klim, T, causal, inv_scale, lane);
+    float rs = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt > klim) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * kt + 4 * (lane >> 4) + r;
+        const bool live = j < T && !(causal && j > i);
+        if (!live) dsk[u][kt][r] = 0.f;
+        rs += dsk[u][kt][r] * pt[kt][r];
+      }
+    }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt > klim) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * kt + 4 * (lane >> 4) + r;
+        const bool live = j < T && !(causal && j > i);
+        const float p = pt[kt][r];
+        dsk[u][kt][r] = live && i < T ? (dsk[u][kt][r] * p - p * rs) * inv_scale : 0.f;
+        sp[j * A16_SP + i] = i < T ? p : 0.f;
+      }
+    }
+    // gQ^T[d][i] = sum_j K[j][d] dS[i][j]
+    fx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+      if (kt <= klim) keys_t(acc, sk, dsk[u][kt], kt, lane);
+    store16_t(GQ, acc, b, h, T, D, hd, qt, lane);
+    if (TS && i < T) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) tq[v] += acc[v >> 2][v & 3];
     }
   }
-  // the key-side products sum over queries of every wave: P^T and then dS^T
-  // go through LDS as [j][i], and wave w takes keys j in [32w, 32w+32)
-  const int j0 = 32 * w;
-  auto keyside = [&](const float *Yq, float *G, int m) {
-    fx16 acc = fx16{};
-    // X[j][d] = sum_i Zt[j][i] Yq[i][d]; Zt[j][i] = 0 for i < j under the mask
-    for (int ii = causal ? j0 : 0; ii < T; ii += 2) {
-      const float a = sp[(j0 + (lane & 31)) * AT_SP + ii + (lane >> 5)];
-      const float bv = Yq[(ii + (lane >> 5)) * AT_HP + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bv, acc, 0, 0, 0);
-    }
-    float s = 0.f;
+  if (TS) {
+    // sum over the 16 queries of each lane group (lane bits 0-3): halving
+    // butterfly, lane l ends with value ((l >> 1) & 7)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = j0 + mrow(r, lane), d = lane & 31;
-      if (j < T && d < hd) G[((int64_t)b * T + j) * D + h * hd + d] = acc[r];
-      s += j < T ? acc[r] : 0.f;
+    for (int v = 0; v < 4; ++v) {
+      const bool up = (lane & 8) != 0;
+      const float send = up ? tq[v] : tq[v + 4], keep = up ? tq[v + 4] : tq[v];
+      tq[v] = keep + __shfl_xor(send, 8, 64);
     }
-    if (TS) {  // sum over the wave's keys j < T of d = lane % 32
-      s += __shfl_xor(s, 32, 64);
-      if (lane < 32) tred[m][w][lane] = s;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const bool up = (lane & 4) != 0;
+      const float send = up ? tq[v] : tq[v + 2], keep = up ? tq[v + 2] : tq[v];
+      tq[v] = keep + __shfl_xor(send, 4, 64);
+    }
+    {
+      const bool up = (lane & 2) != 0;
+      const float send = up ? tq[0] : tq[1], keep = up ? tq[1] : tq[0];
+      tq[0] = keep + __shfl_xor(send, 2, 64);
+    }
+    const float s = tq[0] + __shfl_xor(tq[0], 1, 64);
+    const int v = (lane >> 1) & 7, d = 4 * (lane >> 4) + (v & 3) + 16 * (v >> 2);
+    if ((lane & 1) == 0) tred[0][w][d] = s;
+  }
+  __syncthreads();
+  // key side: wave w takes key tiles w and 7 - w; X[j][d] = sum_i Zt[j][i] Yq[i][d]
+  // over the live query tiles (Zt[j][i] = 0 for i < j under the mask)
+  auto keyside = [&](const float *Yq, float *G, int m) {
+    float ts[2] = {0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int kt = u ? 7 - w : w;
+      if (kt >= nt) continue;
+      fx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      const float *zrow = sp + (16 * kt + (lane & 15)) * A16_SP + 4 * (lane >> 4);
+      for (int qt = causal ? kt : 0; qt < nt; ++qt) {
+        const float4 z = *reinterpret_cast<const float4 *>(zrow + 16 * qt);
+        const float *y = Yq + (16 * qt + 4 * (lane >> 4)) * A16_HP + (lane & 15);
+        acc[0] = mfma16(z.x, y[0], acc[0]);
+        acc[1] = mfma16(z.x, y[16], acc[1]);
+        acc[0] = mfma16(z.y, y[A16_HP], acc[0]);
+        acc[1] = mfma16(z.y, y[A16_HP + 16], acc[1]);
+        acc[0] = mfma16(z.z, y[2 * A16_HP], acc[0]);
+        acc[1] = mfma16(z.z, y[2 * A16_HP + 16], acc[1]);
+        acc[0] = mfma16(z.w, y[3 * A16_HP], acc[0]);
+        acc[1] = mfma16(z.w, y[3 * A16_HP + 16], acc[1]);
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int d = 16 * half + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * kt + 4 * (lane >> 4) + r;
+          if (j < T) {
+            if (d < hd) G[((int64_t)b * T + j) * D + h * hd + d] = acc[half][r];
+            ts[half] += acc[half][r];
+          }
+        }
+      }
+    }
+    if (TS) {  // sum over the wave's keys of d = 16 half + l%16
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float s = ts[half];
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        if (lane < 16) tred[m][w][16 * half + lane] = s;
+      }
     }
   };
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = pt[jt][r];
-  __syncthreads();
   keyside(sg, GV, 2);  // gV_j = sum_i p_ij gO_i
   __syncthreads();
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int u = 0; u < 2; ++u) {
+    const int qt = u ? 7 - w : w;
+    if (qt >= nt) continue;
+    const int klim = causal ? qt : nt - 1;
+    const int i = 16 * qt + (lane & 15);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sp[(32 * jt + mrow(r, lane)) * AT_SP + i] = ds[jt][r];
+    for (int kt = 0; kt < 8; ++kt) {
+      if (kt > klim) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sp[(16 * kt + 4 * (lane >> 4) + r) * A16_SP + i] = dsk[u][kt][r];
+    }
+  }
   __syncthreads();
   keyside(sq, GK, 1);  // gK_j = sum_i dS_ij q_i
   if (TS) {
@@ -1495,14 +1596,16 @@ hipError_t launch_gap1d_bwd(const float *g, float *gin, int B, int T, int D, hip
 
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s) {
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, O, T, D, NH, causal);
+  if (!attn_supported(T, D, NH)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attn16_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, O, T, D, NH, causal);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const float *GO,
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
                            hipStream_t s, float *TS, int64_t tss) {
-  hipLaunchKernelGGL(attn_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, GO, GQ, GK, GV, T, D,
+  if (!attn_supported(T, D, NH)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attn16_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, GO, GQ, GK, GV, T, D,
                      NH, causal, TS, tss);
   return hipGetLastError();
 }
