@@ -393,13 +393,16 @@ hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam
 // (dgamma | dbeta, unscaled; a TbLnJob sums them), tsum (may be null) [blocks][N]
 // the blocks' column sums of dx (ln_bwd_rows_per_block() rows each).  gpool (may
 // be null, then g is read): a CLSPooling's gradient, row r / poolT for rows r
-// with r % poolT == 0, zero elsewhere.
+// with r % poolT == 0, zero elsewhere.  tsx (may be null): the same launch
+// also writes tss[b][c] = sum_t tsx[b][t][c] (tsB samples of tsT x tsN), the
+// per-sample token sums of another matrix.
 int ln_bwd_blocks(int rows);
 int ln_bwd_rows_per_block();
 bool ln_bwd_part_supported(int N);
 hipError_t launch_ln_bwd_part(const float *g, const float *gpool, int poolT, const float *x,
                               const float *gam, const float *stats, float *dx, float *part, float *tsum,
-                              int rows, int N, hipStream_t s);
+                              int rows, int N, hipStream_t s, const float *tsx = nullptr,
+                              float *tss = nullptr, int tsB = 0, int tsT = 0, int tsN = 0);
 hipError_t launch_ln_bwd(const float *g, const float *x, const float *gam, const float *stats,
                          float *dx, float *gx, int rows, int N, hipStream_t s);
 // Rotary embedding of rows [rows, NH*hd] in place; position = row % T; cs/sn

@@ -1714,12 +1714,14 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     j.dW = G + wo; j.db = G + bo; j.M = Mo; j.N = Ni;
     pbytes += f4((double)B * snp * Mo + (double)B * Ni + (double)Mo * Ni + Mo);
   };
+  // tsx (may be null): a [B][T][FF] matrix whose token sums the same launch writes to t.S
   auto norm_bwd_fused = [&](int k, const float *g, const float *gp, const float *x, const float *st,
-                            float *dx, float *lp, float *ts) -> hipError_t {
+                            float *dx, float *lp, float *ts, const float *tsx = nullptr) -> hipError_t {
     KTimer kt(c, GN_KCLASS_OTHER, "ln_bwd",
-              f4((gp ? 2.0 : 3.0) * rows * D + 2.0 * rows + (double)nblk * 3 * D));
+              f4((gp ? 2.0 : 3.0) * rows * D + 2.0 * rows + (double)nblk * 3 * D) +
+                  (tsx ? token_sum_bytes(B, T, FF) : 0.0));
     const hipError_t e = launch_ln_bwd_part(gp ? nullptr : g, gp, T, x, P + (k == 0 ? o.g1 : o.g2), st, dx, lp,
-                                            ts, rows, D, c->stream);
+                                            ts, rows, D, c->stream, tsx, t.S, B, T, FF);
     TbLnJob &j = pset.ln[pset.nln++];
     j.part = lp; j.nblk = nblk; j.N = D;
     j.dgam = G + (k == 0 ? o.g1 : o.g2); j.dbet = G + (k == 0 ? o.be1 : o.be2);
@@ -1790,21 +1792,24 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
     // its output, GELU (identity forward) from MID, which is the pre-activation
     const int dk = R.d.block_act == GN_BLOCK_ACT_GELU ? D_GELU : D_RELU;
     HIP_OK(c, gemm_nn(c, t.G1, P + o.w2, t.DZ1, rows, FF, D, EPI_DACT, dk, t.MID, T));
-    HIP_OK(c, fork());
-    {
-      KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF), ss);
-      HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, ss));
-    }
-    if (fused)
+    if (fused) {
+      // the token sums of dz1 come with the norm-1 backward's launch below
       lin_job(t.S, 1, FF, t.N1, FF, D, o.w1, o.b1);
-    else
+    } else {
+      HIP_OK(c, fork());
+      {
+        KTimer kt(c, GN_KCLASS_OTHER, "token_sum", token_sum_bytes(B, T, FF), ss);
+        HIP_OK(c, launch_token_sum(t.DZ1, t.S, B, T, FF, ss));
+      }
       HIP_OK(c, tb_tok_dw(c, t.S, t.N1, G + o.w1, G + o.b1, B, T, FF, D, scale, ss));
+    }
     // combined = dRES2 + dz1 W1
     HIP_OK(c, gemm_nn(c, t.DZ1, P + o.w1, t.COMB, rows, D, FF, EPI_BIAS_ADD, 0, t.G1, 0));
   }
   // norm 1
   if (fused) {
-    HIP_OK(c, norm_bwd_fused(0, t.COMB, nullptr, t.RES1, t.st1, t.G2, t.LP1, t.TS1));
+    HIP_OK(c, norm_bwd_fused(0, t.COMB, nullptr, t.RES1, t.st1, t.G2, t.LP1, t.TS1,
+                             R.d.block_act == GN_BLOCK_ACT_SWIGLU ? nullptr : t.DZ1));
     lin_job(t.TS1, np, D, t.O, D, D, o.wo, o.bo);  // wOut (Linear): dz = dRES1
   } else {
     HIP_OK(c, tb_norm_bwd(c, R, P, G, o, 0, t.COMB, t.RES1, t.st1, t.G2, rows, scale));

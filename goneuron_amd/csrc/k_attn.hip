@@ -594,6 +594,16 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 // (cls_bwd_kernel's rows, not materialised).  tsum (may be null): the
 // block's column sums of dx, tsum[block][0 .. N), the per-row-block partials
 // of the token sums that a Linear's Q10 gradient below needs.
+// Blocks from nln on (ts.X not null): per-sample token sums of another
+// matrix, ts.S[b][c] = sum_t ts.X[b][t][c] (a block per sample and 64
+// columns, its 4 waves every 4th token with eight loads in flight, the wave
+// sums added in wave order), work that would otherwise take a launch of its
+// own.
+struct LnTokSum {
+  const float *X;
+  float *S;
+  int T, N;
+};
 constexpr int LN_RW = 4, LN_MAXC = 8, LN_RPB = 4 * LN_RW;
 __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restrict__ g,
                                                           const float *__restrict__ gpool, int poolT,
@@ -602,9 +612,32 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
                                                           const float *__restrict__ stats,
                                                           float *__restrict__ dx,
                                                           float *__restrict__ part,
-                                                          float *__restrict__ tsum, int rows, int N) {
+                                                          float *__restrict__ tsum, int rows, int N,
+                                                          int nln, LnTokSum ts) {
   __shared__ float red[4][3][LN_MAXC * 64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if ((int)blockIdx.x >= nln) {  // token-sum block (uniform over the block)
+    const int nc = (ts.N + 63) >> 6, tb = blockIdx.x - nln;
+    const int b = tb / nc, c = (tb % nc) * 64 + lane;
+    float acc = 0.f;
+    if (c < ts.N) {
+      const float *p = ts.X + (int64_t)b * ts.T * ts.N + c;
+      int t = w;
+      for (; t + 28 < ts.T; t += 32) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(t + 4 * u) * ts.N];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+      }
+      for (; t < ts.T; t += 4) acc += p[(int64_t)t * ts.N];
+    }
+    red[w][0][lane] = acc;
+    __syncthreads();
+    if (w == 0 && c < ts.N)
+      ts.S[(int64_t)b * ts.N + c] = ((red[0][0][lane] + red[1][0][lane]) + red[2][0][lane]) + red[3][0][lane];
+    return;
+  }
   const int rbase = blockIdx.x * LN_RPB + w * LN_RW;
   float gv[LN_RW][LN_MAXC], xv[LN_RW][LN_MAXC], gm[LN_MAXC], mean[LN_RW], sd[LN_RW];
 #pragma unroll
@@ -1329,7 +1362,7 @@ hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam
   if (N > 64 * LN_MAXC || (size_t)nblk * 2 * N > ws_cap) return hipErrorNotSupported;
   if (rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(256), 0, s, g, nullptr, 1, x, gam, stats, dx, ws,
-                     nullptr, rows, N);
+                     nullptr, rows, N, nblk, LnTokSum{});
   hipLaunchKernelGGL(ln_param_final, dim3((2 * N + 63) / 64), dim3(256), 0, s, ws, nblk, N, scale, dgam,
                      dbet);
   return hipGetLastError();
@@ -1341,12 +1374,16 @@ bool ln_bwd_part_supported(int N) { return N >= 1 && N <= 64 * LN_MAXC; }
 
 hipError_t launch_ln_bwd_part(const float *g, const float *gpool, int poolT, const float *x,
                               const float *gam, const float *stats, float *dx, float *part, float *tsum,
-                              int rows, int N, hipStream_t s) {
+                              int rows, int N, hipStream_t s, const float *tsx, float *tss, int tsB, int tsT,
+                              int tsN) {
   if (!ln_bwd_part_supported(N) || (!g && !gpool) || (gpool && poolT < 1) || !part)
     return hipErrorInvalidValue;
+  if (tsx && (!tss || tsB < 0 || tsT < 1 || tsN < 1)) return hipErrorInvalidValue;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(ln_bwd_blocks(rows)), dim3(256), 0, s, g, gpool,
-                     gpool ? poolT : 1, x, gam, stats, dx, part, tsum, rows, N);
+  const int nln = ln_bwd_blocks(rows);
+  const int nts = tsx ? tsB * ((tsN + 63) / 64) : 0;
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nln + nts), dim3(256), 0, s, g, gpool, gpool ? poolT : 1, x, gam,
+                     stats, dx, part, tsum, rows, N, nln, LnTokSum{tsx, tss, tsT, tsN});
   return hipGetLastError();
 }
 
