@@ -446,20 +446,36 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &p,
     const unsigned d = EPI == EPI_DACT && p.aux_div > 1 ? (unsigned)p.aux_div : 1u;
     const bool magic_ok = (unsigned long long)M * d < (1ull << 32);
     const unsigned magic = d > 1 ? (unsigned)(0xFFFFFFFFull / d + 1) : 0u;
+    const int mlast = min(m0 + RM, M) - 1;
+    if (d > 1 && (unsigned)m0 / d == (unsigned)mlast / d) {
+      // the block's rows share one aux row (a tile inside one sample's
+      // tokens): one load per column instead of one per element
+      const size_t ar = (size_t)((unsigned)m0 / d * d + d - 1);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const int col = col_of(j);
+        const float a = col < N ? p.aux[ar * p.ldaux + col] : 0.f;
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = row_of(i, r), col = col_of(j);
-          int ar = row;
-          if (d > 1) {
-            const unsigned q = magic_ok ? __umulhi((unsigned)row, magic) : (unsigned)row / d;
-            ar = (int)(q * d + d - 1);
+          for (int r = 0; r < 16; ++r) av[i][j][r] = a;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = row_of(i, r), col = col_of(j);
+            int ar = row;
+            if (d > 1) {
+              const unsigned q = magic_ok ? __umulhi((unsigned)row, magic) : (unsigned)row / d;
+              ar = (int)(q * d + d - 1);
+            }
+            av[i][j][r] = (row < M && col < N) ? p.aux[(size_t)ar * p.ldaux + col] : 0.f;
           }
-          av[i][j][r] = (row < M && col < N) ? p.aux[(size_t)ar * p.ldaux + col] : 0.f;
-        }
+    }
   }
   float *ws = EPI == EPI_PARTIAL ? p.ws + (size_t)blockIdx.y * M * N : nullptr;
   auto store_all = [&](auto f) {
