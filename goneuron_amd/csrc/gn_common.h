@@ -83,7 +83,16 @@ struct GemmArgs {
   // reduce and epilogue are left to the caller) and *defer_splits receives
   // the split count; it receives 1 when the GEMM ran whole (with epilogue)
   int *defer_splits;
+  // kseg > 0 (a multiple of 64, nbatch <= 1, 64-wide tiles): the K range is
+  // cut into segments of kseg, segment s of op(A) / op(B) starting seg_A /
+  // seg_B floats after segment 0 (a sum of products A_s B_s over operands
+  // that are not adjacent in memory, in one launch); launch_gemm returns
+  // hipErrorNotSupported where its plan cannot take them.  kseg_dA / kseg_dB
+  // are filled by launch_gemm.
+  int kseg;
+  int64_t seg_A, seg_B, kseg_dA, kseg_dB;
 };
+bool gemm_segments_ok(const GemmArgs &a);  // launch_gemm can take a's K segments
 
 // EPI_SCALE    C = alpha*acc
 // EPI_BIAS_ACT C = act(acc + bias[col])

@@ -1870,7 +1870,28 @@ static int tb_backward(gn_model *M, LayerRT &R, const float *X, float *gin, int 
   }
   if (gin) {  // gIn = dRES1 + gQ Wq + gK Wk + gV Wv
     const int64_t pst = (int64_t)rows * D;
-    if ((size_t)3 * pst <= c->scratch_floats) {
+    hipError_t eg = hipErrorNotSupported;
+    {
+      // one GEMM over K = 3D in three segments (gQ | gK | gV against Wq; Wk;
+      // Wv) with dRES1 added in the epilogue
+      GemmArgs a{};
+      a.M = rows; a.N = D; a.K = 3 * D;
+      a.A = t.GQ; a.lda = D; a.B = P + o.wq; a.ldb = D;
+      a.C = gin; a.ldc = D; a.alpha = 1.f;
+      a.aux = t.G2; a.ldaux = D;
+      a.kseg = D;
+      a.seg_A = t.GK - t.GQ;
+      a.seg_B = o.wk - o.wq;
+      a.ws = cs; a.ws_cap = cap;
+      if (gemm_segments_ok(a)) {
+        KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(a));
+        eg = launch_gemm('N', 'N', EPI_BIAS_ADD, a, c->stream);
+      }
+    }
+    if (eg == hipSuccess) {
+    } else if (eg != hipErrorNotSupported) {
+      HIP_OK(c, eg);
+    } else if ((size_t)3 * pst <= c->scratch_floats) {
       // the three products in one batched launch into the scratch, then
       // added to dRES1 in the order of three accumulating launches
       GemmArgs a{};

@@ -558,6 +558,9 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
   const int kbeg = blockIdx.y * kchunk;
   const int kend = min(p.K, kbeg + kchunk);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  // operand bases of the K stage starting at k (segmented K: the stage's segment)
+  auto opA = [&](int k) -> const float * { return p.kseg ? p.A + (int64_t)(k / p.kseg) * p.kseg_dA : p.A; };
+  auto opB = [&](int k) -> const float * { return p.kseg ? p.B + (int64_t)(k / p.kseg) * p.kseg_dB : p.B; };
 
   floatx16 acc[T][T];
 #pragma unroll
@@ -582,14 +585,14 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     constexpr bool KT = PIPE == 2;
     const int mrow = wm * (R / 2), ncol = wn * (R / 2);
     floatx4 ra[TL::NLD], rb[TL::NLD];
-    load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, kbeg, ra);
-    load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+    load_tile_pipe<R, AK, KT>(opA(kbeg), p.lda, M, kend, m0, kbeg, ra);
+    load_tile_pipe<R, BKC, KT>(opB(kbeg), p.ldb, N, kend, n0, kbeg, rb);
     store_tile_pipe<R, AK, KT>(As[0], ra, kbeg, kend);
     store_tile_pipe<R, BKC, KT>(Bs[0], rb, kbeg, kend);
     {
       const int k1 = kbeg + min(1, nk - 1) * BK;
-      load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, k1, ra);
-      load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, k1, rb);
+      load_tile_pipe<R, AK, KT>(opA(k1), p.lda, M, kend, m0, k1, ra);
+      load_tile_pipe<R, BKC, KT>(opB(k1), p.ldb, N, kend, n0, k1, rb);
     }
     __syncthreads();
     float f0a[T][8], f0b[T][8];
@@ -637,8 +640,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
       read_frags<R, BKC>(Bs[cur ^ 1], ncol, koff, l32, f0b);
       {
         const int k2 = kbeg + min(kt + 2, nk - 1) * BK;
-        load_tile_pipe<R, AK, KT>(p.A, p.lda, M, kend, m0, k2, ra);
-        load_tile_pipe<R, BKC, KT>(p.B, p.ldb, N, kend, n0, k2, rb);
+        load_tile_pipe<R, AK, KT>(opA(k2), p.lda, M, kend, m0, k2, ra);
+        load_tile_pipe<R, BKC, KT>(opB(k2), p.ldb, N, kend, n0, k2, rb);
       }
 #pragma unroll
       for (int s = 4; s < 8; ++s)
@@ -658,8 +661,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
     __syncthreads();
   } else {
     float4 ra[TL::NLD], rb[TL::NLD];
-    load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg, ra);
-    load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg, rb);
+    load_tile<R, AK, VEC>(opA(kbeg), p.lda, M, kend, m0, kbeg, ra);
+    load_tile<R, BKC, VEC>(opB(kbeg), p.ldb, N, kend, n0, kbeg, rb);
     store_tile<R, AK>(As[0], ra);
     store_tile<R, BKC>(Bs[0], rb);
     __syncthreads();
@@ -667,8 +670,8 @@ void gemm_f32_mfma(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
       const int cur = kt & 1;
       const bool more = kt + 1 < nk;
       if (more) {
-        load_tile<R, AK, VEC>(p.A, p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
-        load_tile<R, BKC, VEC>(p.B, p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
+        load_tile<R, AK, VEC>(opA(kbeg + (kt + 1) * BK), p.lda, M, kend, m0, kbeg + (kt + 1) * BK, ra);
+        load_tile<R, BKC, VEC>(opB(kbeg + (kt + 1) * BK), p.ldb, N, kend, n0, kbeg + (kt + 1) * BK, rb);
       }
       float a[T][16], b[T][16];
 #pragma unroll
@@ -955,12 +958,36 @@ static hipError_t launch_r(char ta, char tb, int epi, bool vec, const GemmArgs &
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t s) {
-  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+// The tile plan of launch_gemm takes 128-wide tiles (four-wave kernels,
+// which load whole K ranges) when they fill the chip; a segmented K needs the
+// 64-wide plan.
+static bool plan_big(const GemmArgs &a) {
+  const int64_t nmem = (a.nbatch > 1 && a.nbatch_in > 1) ? a.nbatch : 1;
+  const int64_t t128 = ((a.M + 127) / 128) * (int64_t)((a.N + 127) / 128) * nmem;
+  const int64_t t64 = ((a.M + 63) / 64) * (int64_t)((a.N + 63) / 64) * nmem;
+  return t128 >= 160 && !(a.K <= 256 && t64 >= 1024);
+}
+
+bool gemm_segments_ok(const GemmArgs &a) {
+  return a.kseg > 0 && a.kseg % BK == 0 && a.nbatch <= 1 && !a.defer_splits && !a.drop_out && !plan_big(a);
+}
+
+hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a0, hipStream_t s) {
+  if (a0.M <= 0 || a0.N <= 0) return hipSuccess;
+  GemmArgs a = a0;
+  if (a.kseg > 0) {
+    // the stage loaders of the eight-wave kernel step to segment k / kseg
+    if (!gemm_segments_ok(a)) return hipErrorNotSupported;
+    a.kseg_dA = a.seg_A - (ta == 'N' ? (int64_t)a.kseg : (int64_t)a.kseg * a.lda);
+    a.kseg_dB = a.seg_B - (tb == 'T' ? (int64_t)a.kseg : (int64_t)a.kseg * a.ldb);
+  } else {
+    a.kseg = 0;
+  }
   if (a.drop_out && (epi != EPI_BIAS_ACT || a.nbatch > 1 || !a.drop_mask)) return hipErrorInvalidValue;
   // float4 staging needs 16 B aligned rows and the contiguous extent % 4 == 0
   const bool ak = (ta == 'N'), bk = (tb == 'T');
-  bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0);
+  bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 4 == 0) && (a.ldb % 4 == 0) &&
+             ((a.seg_A | a.seg_B) & 3) == 0;
   vec = vec && (ak ? (a.K % 4 == 0) : (a.M % 4 == 0));
   vec = vec && (bk ? (a.K % 4 == 0) : (a.N % 4 == 0));
   vec = vec && a.K > 0;  // the pipelined loop assumes at least one K stage
@@ -975,7 +1002,8 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a, hipStream_t
   const int64_t t64 = ((a.M + 63) / 64) * (int64_t)((a.N + 63) / 64) * nmem;
   // short K (at most four 64-deep stages) with four 64-wide tiles per CU:
   // 64-wide tiles, whose blocks cover each other's prologue and epilogue
-  const bool big = t128 >= 160 && !(a.K <= 256 && t64 >= 1024);
+  const bool big = plan_big(a);
+  if (a.kseg > 0 && big) return hipErrorNotSupported;  // the four-wave kernels load whole K ranges
   const int tiles = (int)std::min<int64_t>(big ? t128 : t64, 1 << 30);
   int splits = 1;
   if (tiles < 160 && a.K >= 8 * BK && a.ws) {
