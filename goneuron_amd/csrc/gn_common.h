@@ -91,6 +91,14 @@ struct GemmArgs {
   // are filled by launch_gemm.
   int kseg;
   int64_t seg_A, seg_B, kseg_dA, kseg_dB;
+  // cs_src set: when K splits, the split-K reduction launch also writes the
+  // column sums cs_dst[c] = cs_scale * sum_r cs_src[r][c] (cs_rows x cs_cols,
+  // dense) and sets *cs_done to 1 (else 0: the caller sums them itself)
+  const float *cs_src;
+  float *cs_dst;
+  int cs_rows, cs_cols;
+  float cs_scale;
+  int *cs_done;
 };
 bool gemm_segments_ok(const GemmArgs &a);  // launch_gemm can take a's K segments
 

@@ -206,4 +206,4 @@ hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float
                           float *gB, float *gin, int B, int in, int out_n, float scale,
                           const float *gin_aux, int gin_deriv, hipEvent_t dz_ready = nullptr,
                           float *ms = nullptr, size_t ms_cap = 0, const float *gin_colscale = nullptr,
-                          bool skip_dw = false);
+                          bool skip_dw = false, bool bias_main = false);

@@ -297,7 +297,7 @@ static hipError_t dense_fwd(gn_ctx *c, const float *x, const float *W, const flo
 hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float *dz, float *gW,
                           float *gB, float *gin, int B, int in, int out_n, float scale,
                           const float *gin_aux, int gin_deriv, hipEvent_t dz_ready, float *ms,
-                          size_t ms_cap, const float *gin_colscale, bool skip_dw) {
+                          size_t ms_cap, const float *gin_colscale, bool skip_dw, bool bias_main) {
   hipError_t e;
   if (!ms) {
     ms = c->scratch;
@@ -313,7 +313,11 @@ hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float
     wscr = c->scratch_aux;
     wcap = c->scratch_floats;
   }
-  if (gB) {
+  // bias_main: the bias sums may ride on the dX GEMM's split-K reduction
+  // launch (below) on the main stream; without it (steps with per-layer
+  // updates, which wait for them on the second stream) they run here
+  const bool cs_in_dx = gB && gin && bias_main;
+  if (gB && !cs_in_dx) {
     KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * out_n + out_n), ws);
     e = launch_colsum(dz, B, out_n, out_n, scale, gB, wscr, wcap, ws);
     if (e != hipSuccess) return e;
@@ -338,12 +342,24 @@ hipError_t dense_bwd_core(gn_ctx *c, const float *x, const float *W, const float
     d.C = gin; d.ldc = in;
     d.alpha = 1.f;
     d.ws = ms; d.ws_cap = ms_cap;
-    KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
-    if (gin_aux) {
-      d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv; d.colscale = gin_colscale;
-      e = launch_gemm('N', 'N', EPI_DACT, d, c->stream);
-    } else {
-      e = launch_gemm('N', 'N', EPI_SCALE, d, c->stream);
+    int cs_done = 0;
+    if (cs_in_dx) {
+      d.cs_src = dz; d.cs_dst = gB; d.cs_rows = B; d.cs_cols = out_n; d.cs_scale = scale;
+      d.cs_done = &cs_done;
+    }
+    {
+      KTimer kt(c, GN_KCLASS_GEMM, "gemm_dx", gemm_flops(d));
+      if (gin_aux) {
+        d.aux = gin_aux; d.ldaux = in; d.act = gin_deriv; d.colscale = gin_colscale;
+        e = launch_gemm('N', 'N', EPI_DACT, d, c->stream);
+      } else {
+        e = launch_gemm('N', 'N', EPI_SCALE, d, c->stream);
+      }
+    }
+    if (e != hipSuccess) return e;
+    if (cs_in_dx && !cs_done) {
+      KTimer kt(c, GN_KCLASS_OTHER, "colsum", f4((double)B * out_n + out_n));
+      e = launch_colsum(dz, B, out_n, out_n, scale, gB, ms, ms_cap, c->stream);
     }
   }
   return e;
@@ -2316,7 +2332,7 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const bool sd = side && gin && i != dw_done;
         HIP_OK(c, dense_bwd_core(c, in, W, dz, gW, i == bias_done ? nullptr : gB, gin, B, R.d.in_size,
                                  R.d.out_size, scale, aux, deriv, sd ? M->dz_ev[i] : nullptr, nullptr, 0,
-                                 cfac, i == dw_done));
+                                 cfac, i == dw_done, !ac));
         if (sd) {  // the layer's Adam (M->adam_s) waits for its dW and bias sums
           HIP_OK(c, hipEventRecord(M->dw_ev[i], c->aux));
           dw_aux[i] = 1;

@@ -862,9 +862,33 @@ void gemm_f32_mfma_w4(GemmArgs p, int tiles_m, int tiles_n, int kchunk) {
 }
 
 // Split-K reduction: partials summed in split order, then the epilogue.
-__global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits, int epi) {
+// Blocks from nred on (p.cs_src set): the column sums cs_dst[c] = cs_scale *
+// sum_r cs_src[r][c], rows in order with eight loads in flight, one thread
+// per column (a bias gradient that would otherwise take a launch).
+__device__ __forceinline__ void reduce_side_colsum(const GemmArgs &p, int cb) {
+  const int c = cb * NT + threadIdx.x;
+  if (c >= p.cs_cols) return;
+  const float *src = p.cs_src + c;
+  float v = 0.f;
+  int r = 0;
+  for (; r + 7 < p.cs_rows; r += 8) {
+    float u8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) u8[u] = src[(size_t)(r + u) * p.cs_cols];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += u8[u];
+  }
+  for (; r < p.cs_rows; ++r) v += src[(size_t)r * p.cs_cols];
+  p.cs_dst[c] = v * p.cs_scale;
+}
+
+__global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits, int epi, int nred) {
+  if ((int)blockIdx.x >= nred) {
+    reduce_side_colsum(p, blockIdx.x - nred);
+    return;
+  }
   const size_t MN = (size_t)p.M * p.N;
-  for (size_t idx = (size_t)blockIdx.x * NT + threadIdx.x; idx < MN; idx += (size_t)gridDim.x * NT) {
+  for (size_t idx = (size_t)blockIdx.x * NT + threadIdx.x; idx < MN; idx += (size_t)nred * NT) {
     float v = p.ws[idx];
     for (int s = 1; s < splits; s += 8) {  // eight loads in flight, added in split order
       float u8[8];
@@ -883,7 +907,11 @@ __global__ __launch_bounds__(NT) void gemm_splitk_reduce(GemmArgs p, int splits,
 
 // Small outputs with many splits: one wave per element, lanes over the splits
 // (a fixed tree order), so the sum is not a chain of `splits` dependent loads.
-__global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int splits, int epi) {
+__global__ __launch_bounds__(NT) void gemm_splitk_reduce_wave(GemmArgs p, int splits, int epi, int nred) {
+  if ((int)blockIdx.x >= nred) {
+    reduce_side_colsum(p, blockIdx.x - nred);
+    return;
+  }
   const size_t MN = (size_t)p.M * p.N;
   const size_t idx = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1048,13 +1076,15 @@ hipError_t launch_gemm(char ta, char tb, int epi, const GemmArgs &a0, hipStream_
     return launch_dropout(a.C, a.drop_mask, a.drop_scale, a.drop_out, a.M, a.N, s);
   }
   const size_t MN = (size_t)a.M * a.N;
+  const unsigned csb = a.cs_src && a.cs_dst && a.cs_cols > 0 ? (unsigned)((a.cs_cols + NT - 1) / NT) : 0u;
   if (splits >= 16 && MN <= 65536) {
     const unsigned blocks = (unsigned)((MN + NT / 64 - 1) / (NT / 64));
-    hipLaunchKernelGGL(gemm_splitk_reduce_wave, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+    hipLaunchKernelGGL(gemm_splitk_reduce_wave, dim3(blocks + csb), dim3(NT), 0, s, a, splits, epi, (int)blocks);
   } else {
     const unsigned blocks = (unsigned)std::min<size_t>((MN + NT - 1) / NT, 4096);
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks), dim3(NT), 0, s, a, splits, epi);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(blocks + csb), dim3(NT), 0, s, a, splits, epi, (int)blocks);
   }
+  if (a.cs_done) *a.cs_done = csb > 0 ? 1 : 0;
   return hipGetLastError();
 }
 

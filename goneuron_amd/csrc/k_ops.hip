@@ -500,6 +500,10 @@ __device__ __attribute__((noinline)) float or_exp_diff(float a, float b) {
   return (float)exp((double)(a - b));
 }
 __device__ __attribute__((noinline)) float or_exp(float a) { return (float)exp((double)a); }
+// Inline forms for the wide-row kernels (8 values per thread): eight
+// independent float64 exps interleave instead of running as eight calls.
+__device__ __forceinline__ float or_exp_diff_i(float a, float b) { return (float)exp((double)(a - b)); }
+__device__ __forceinline__ float or_exp_i(float a) { return (float)exp((double)a); }
 __device__ __attribute__((noinline)) float or_log(float a) { return (float)log((double)a); }
 __device__ __attribute__((noinline)) float or_fwd(float v, int kind) { return fwd_of(v, kind); }
 __device__ __attribute__((noinline)) float or_deriv(float o, int kind) { return deriv_of(o, kind); }
@@ -567,7 +571,10 @@ __device__ __forceinline__ float out_row_math(float (&o)[PER], const float (&yv)
     float ef[PER], sm = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-      ef[k] = t + k * G < C ? or_exp_diff(o[k], mx) : 0.f;
+      if constexpr (PER >= 8)
+        ef[k] = t + k * G < C ? or_exp_diff_i(o[k], mx) : 0.f;
+      else
+        ef[k] = t + k * G < C ? or_exp_diff(o[k], mx) : 0.f;
       sm += ef[k];
     }
     sm = group_sum<G>(sm, sh, r);
@@ -627,7 +634,7 @@ __device__ __forceinline__ float out_row_math(float (&o)[PER], const float (&yv)
     s1 = group_sum<G>(s1, sh, r);
 #pragma unroll
     for (int k = 0; k < PER; ++k)
-      if (t + k * G < C) d[k] = d[k] - or_exp(o[k]) * s1;
+      if (t + k * G < C) d[k] = d[k] - (PER >= 8 ? or_exp_i(o[k]) : or_exp(o[k])) * s1;
   } else {
 #pragma unroll
     for (int k = 0; k < PER; ++k)
