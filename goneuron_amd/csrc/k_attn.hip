@@ -584,11 +584,12 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ g
 }
 
 // The same dx, and instead of the g * xhat matrix, the block's own column
-// sums of g * xhat (gamma) and g (beta): block = 4 waves x LN_RW rows; a wave
-// loads its rows' g and x into registers at once (lane i holds columns i,
-// i + 64, ..., N <= 64 LN_MAXC), then finishes them row by row; the waves'
-// sums are added in wave order and written as one partial row pair
-// part[block][0 .. 2N) for ln_param_final.
+// sums of g * xhat (gamma) and g (beta): block = 8 waves x 2 rows (two waves
+// per SIMD: with 4 waves x 4 rows one wave per SIMD had waited out every
+// load); a wave loads its rows' g and x into registers at once (lane i holds
+// columns i, i + 64, ..., N <= 64 LN_MAXC), then finishes them row by row;
+// the waves' sums are added in a fixed tree and written as one partial row
+// pair part[block][0 .. 2N) for ln_param_final.
 // gpool (may be null; then g is read): the gradient of a CLSPooling above,
 // row r / poolT of gpool for rows r with r % poolT == 0 and zero for the rest
 // (cls_bwd_kernel's rows, not materialised).  tsum (may be null): the
@@ -604,8 +605,8 @@ struct LnTokSum {
   float *S;
   int T, N;
 };
-constexpr int LN_RW = 4, LN_MAXC = 8, LN_RPB = 4 * LN_RW;
-__global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restrict__ g,
+constexpr int LN_RW = 2, LN_WV = 8, LN_MAXC = 8, LN_RPB = LN_WV * LN_RW, LN_NT = 64 * LN_WV;
+__global__ __launch_bounds__(LN_NT) void ln_bwd_part_kernel(const float *__restrict__ g,
                                                           const float *__restrict__ gpool, int poolT,
                                                           const float *__restrict__ x,
                                                           const float *__restrict__ gam,
@@ -614,8 +615,12 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
                                                           float *__restrict__ part,
                                                           float *__restrict__ tsum, int rows, int N,
                                                           int nln, LnTokSum ts) {
-  __shared__ float red[4][3][LN_MAXC * 64];
+  __shared__ float red[LN_WV][3][LN_MAXC * 64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // the waves' partial sums v[0..7] added in a fixed tree
+  auto tree8 = [](float v0, float v1, float v2, float v3, float v4, float v5, float v6, float v7) {
+    return ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7));
+  };
   if ((int)blockIdx.x >= nln) {  // token-sum block (uniform over the block)
     const int nc = (ts.N + 63) >> 6, tb = blockIdx.x - nln;
     const int b = tb / nc, c = (tb % nc) * 64 + lane;
@@ -623,19 +628,20 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
     if (c < ts.N) {
       const float *p = ts.X + (int64_t)b * ts.T * ts.N + c;
       int t = w;
-      for (; t + 28 < ts.T; t += 32) {
+      for (; t + 7 * LN_WV < ts.T; t += 8 * LN_WV) {
         float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(t + 4 * u) * ts.N];
+        for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(t + LN_WV * u) * ts.N];
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += v[u];
       }
-      for (; t < ts.T; t += 4) acc += p[(int64_t)t * ts.N];
+      for (; t < ts.T; t += LN_WV) acc += p[(int64_t)t * ts.N];
     }
     red[w][0][lane] = acc;
     __syncthreads();
     if (w == 0 && c < ts.N)
-      ts.S[(int64_t)b * ts.N + c] = ((red[0][0][lane] + red[1][0][lane]) + red[2][0][lane]) + red[3][0][lane];
+      ts.S[(int64_t)b * ts.N + c] = tree8(red[0][0][lane], red[1][0][lane], red[2][0][lane], red[3][0][lane],
+                                          red[4][0][lane], red[5][0][lane], red[6][0][lane], red[7][0][lane]);
     return;
   }
   const int rbase = blockIdx.x * LN_RPB + w * LN_RW;
@@ -701,11 +707,13 @@ __global__ __launch_bounds__(256) void ln_bwd_part_kernel(const float *__restric
   }
   __syncthreads();
   float *pp = part + (size_t)blockIdx.x * 2 * N;
-  for (int i = threadIdx.x; i < N; i += 256) {
-    pp[i] = (red[0][0][i] + red[1][0][i]) + (red[2][0][i] + red[3][0][i]);
-    pp[N + i] = (red[0][1][i] + red[1][1][i]) + (red[2][1][i] + red[3][1][i]);
-    if (tsum)
-      tsum[(size_t)blockIdx.x * N + i] = (red[0][2][i] + red[1][2][i]) + (red[2][2][i] + red[3][2][i]);
+  for (int i = threadIdx.x; i < N; i += LN_NT) {
+#define LN_RED(k) tree8(red[0][k][i], red[1][k][i], red[2][k][i], red[3][k][i], red[4][k][i], red[5][k][i], \
+                        red[6][k][i], red[7][k][i])
+    pp[i] = LN_RED(0);
+    pp[N + i] = LN_RED(1);
+    if (tsum) tsum[(size_t)blockIdx.x * N + i] = LN_RED(2);
+#undef LN_RED
   }
 }
 
@@ -1361,7 +1369,7 @@ hipError_t launch_ln_bwd_params(const float *g, const float *x, const float *gam
   const int nblk = (rows + LN_RPB - 1) / LN_RPB;
   if (N > 64 * LN_MAXC || (size_t)nblk * 2 * N > ws_cap) return hipErrorNotSupported;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(256), 0, s, g, nullptr, 1, x, gam, stats, dx, ws,
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nblk), dim3(LN_NT), 0, s, g, nullptr, 1, x, gam, stats, dx, ws,
                      nullptr, rows, N, nblk, LnTokSum{});
   hipLaunchKernelGGL(ln_param_final, dim3((2 * N + 63) / 64), dim3(256), 0, s, ws, nblk, N, scale, dgam,
                      dbet);
@@ -1382,7 +1390,7 @@ hipError_t launch_ln_bwd_part(const float *g, const float *gpool, int poolT, con
   if (rows <= 0) return hipSuccess;
   const int nln = ln_bwd_blocks(rows);
   const int nts = tsx ? tsB * ((tsN + 63) / 64) : 0;
-  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nln + nts), dim3(256), 0, s, g, gpool, gpool ? poolT : 1, x, gam,
+  hipLaunchKernelGGL(ln_bwd_part_kernel, dim3(nln + nts), dim3(LN_NT), 0, s, g, gpool, gpool ? poolT : 1, x, gam,
                      stats, dx, part, tsum, rows, N, nln, LnTokSum{tsx, tss, tsT, tsN});
   return hipGetLastError();
 }
