@@ -859,15 +859,17 @@ __global__ __launch_bounds__(256) void rms_bwd_kernel(const float *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Causal multi-head attention on fp32 MFMA, one workgroup of 4 waves per
-// (sample, head).  Q/K/V/O are [B*T, D] with head h in columns [h*hd,
-// (h+1)*hd); T <= 128 and hd <= 32 are held in LDS, staged [t][d] (zero
-// padded to 128 x 32) at a 16-byte-aligned pitch (A16_HP, read as float4).
-// The tokens are cut into eight 16-token tiles: wave w owns query tiles w and
-// 7 - w, and in the backward's key-side products key tiles w and 7 - w, so
-// under the causal mask every wave works 9 of the 36 live tile pairs (a wave
-// per 32 queries, the first layout, gave one wave 4 of 10 tile pairs and
-// another 1: forward 13.5 -> 10.6 us, backward 32.1 -> 23.6 us on C4's shape).
+// Causal multi-head attention on fp32 MFMA, one workgroup per (sample,
+// head).  Q/K/V/O are [B*T, D] with head h in columns [h*hd, (h+1)*hd);
+// T <= 128 and hd <= 32 are held in LDS, staged [t][d] (zero padded to
+// 128 x 32) at a 16-byte-aligned pitch (A16_HP, read as float4).  The tokens
+// are cut into eight 16-token tiles, and each SIMD owns query tiles s and
+// 7 - s (in the backward's key-side products key tiles s and 7 - s), so under
+// the causal mask every SIMD works 9 of the 36 live tile pairs: with 8 waves
+// per workgroup one tile per wave, two waves per SIMD (tile_of).  A wave per
+// 32 queries, the first layout, gave one wave 4 of 10 tile pairs and another
+// 1; balanced tiles took C4's forward 13.5 -> 10.6 us and backward 32.1 ->
+// 23.6 us with 4 waves, and the second wave per SIMD to 9.3 and 19.2 us.
 // The backward recomputes the probabilities from Q and K instead of storing
 // B*NH*T*T.
 // v_mfma_f32_16x16x4_f32: A[m = l%16][k = l/16], B[k = l/16][n = l%16],
@@ -888,19 +890,20 @@ __device__ __forceinline__ fx4 mfma16(float a, float b, const fx4 &c) {
 // Rows [0, 128) x cols [0, 32) of head h of N matrices, zero padded, at
 // pitch A16_HP; with hd, D and the pointers multiples of 4 floats every
 // thread issues all its 16-byte loads (4 per matrix) before any store.
-template <int N>
+template <int N, int NT>
 __device__ __forceinline__ void stage16(float *const (&dst)[N], const float *const (&src)[N], int b, int h,
                                         int T, int D, int hd) {
+  constexpr int PQ = 1024 / NT;  // float4 per thread per matrix (128 rows x 8 float4)
   bool vec = (hd & 3) == 0 && (D & 3) == 0;
 #pragma unroll
   for (int m = 0; m < N; ++m) vec = vec && (reinterpret_cast<uintptr_t>(src[m]) & 15) == 0;
   if (vec) {
-    float4 v[N][4];
+    float4 v[N][PQ];
 #pragma unroll
     for (int m = 0; m < N; ++m)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int f = threadIdx.x + 256 * q;  // 128 rows x 8 float4
+      for (int q = 0; q < PQ; ++q) {
+        const int f = threadIdx.x + NT * q;
         const int t = f >> 3, d = (f & 7) << 2;
         v[m][q] = (t < T && d < hd)
                       ? *reinterpret_cast<const float4 *>(src[m] + ((int64_t)b * T + t) * D + h * hd + d)
@@ -909,14 +912,14 @@ __device__ __forceinline__ void stage16(float *const (&dst)[N], const float *con
 #pragma unroll
     for (int m = 0; m < N; ++m)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int f = threadIdx.x + 256 * q;
+      for (int q = 0; q < PQ; ++q) {
+        const int f = threadIdx.x + NT * q;
         *reinterpret_cast<float4 *>(dst[m] + (f >> 3) * A16_HP + ((f & 7) << 2)) = v[m][q];
       }
     return;
   }
   for (int m = 0; m < N; ++m)
-    for (int e = threadIdx.x; e < AT_T * AT_HD; e += 256) {
+    for (int e = threadIdx.x; e < AT_T * AT_HD; e += NT) {
       const int t = e / AT_HD, d = e % AT_HD;
       dst[m][t * A16_HP + d] = (t < T && d < hd) ? src[m][((int64_t)b * T + t) * D + h * hd + d] : 0.f;
     }
@@ -1027,11 +1030,21 @@ __device__ __forceinline__ void store16_t(float *G, const fx4 (&v)[2], int b, in
   }
 }
 
-__global__ __launch_bounds__(256) void attn16_fwd_kernel(const float *__restrict__ Q,
-                                                         const float *__restrict__ K,
-                                                         const float *__restrict__ V,
-                                                         float *__restrict__ O, int T, int D, int NH,
-                                                         int causal) {
+// Query (key) tile u of wave w: with 4 waves tiles w and 7 - w; with 8 waves
+// (two per SIMD, waves w and w + 4 on one SIMD) tile w for w < 4 and 11 - w
+// after, so each SIMD again works tiles s and 7 - s.
+template <int NW>
+__device__ __forceinline__ int tile_of(int w, int u) {
+  return NW == 4 ? (u ? 7 - w : w) : (w < 4 ? w : 11 - w);
+}
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn16_fwd_kernel(const float *__restrict__ Q,
+                                                             const float *__restrict__ K,
+                                                             const float *__restrict__ V,
+                                                             float *__restrict__ O, int T, int D, int NH,
+                                                             int causal) {
+  constexpr int NU = 8 / NW;
   __shared__ __align__(16) float sq[AT_T * A16_HP];
   __shared__ __align__(16) float sk[AT_T * A16_HP];
   __shared__ __align__(16) float sv[AT_T * A16_HP];
@@ -1041,14 +1054,14 @@ __global__ __launch_bounds__(256) void attn16_fwd_kernel(const float *__restrict
   {
     float *const dst[3] = {sq, sk, sv};
     const float *const src[3] = {Q, K, V};
-    stage16<3>(dst, src, b, h, T, D, hd);
+    stage16<3, 64 * NW>(dst, src, b, h, T, D, hd);
   }
   __syncthreads();
   const float inv_scale = 1.0f / (float)sqrt((double)hd);
   const int nt = (T + 15) >> 4;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int qt = u ? 7 - w : w;
+  for (int u = 0; u < NU; ++u) {
+    const int qt = tile_of<NW>(w, u);
     if (qt >= nt) continue;
     const int klim = causal ? qt : nt - 1;
     float4 qb[2];
@@ -1075,39 +1088,41 @@ __global__ __launch_bounds__(256) void attn16_fwd_kernel(const float *__restrict
 // per-sample token sums of gQ, gK and gV (member m at TS + m * tss, [B][D])
 // for the Q10 gradients of the three projections: each wave's sums over its
 // queries (keys) meet in LDS and are added in wave order.
-__global__ __launch_bounds__(256) void attn16_bwd_kernel(const float *__restrict__ Q,
-                                                         const float *__restrict__ K,
-                                                         const float *__restrict__ V,
-                                                         const float *__restrict__ GO,
-                                                         float *__restrict__ GQ,
-                                                         float *__restrict__ GK,
-                                                         float *__restrict__ GV, int T, int D,
-                                                         int NH, int causal, float *__restrict__ TS,
-                                                         int64_t tss) {
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void attn16_bwd_kernel(const float *__restrict__ Q,
+                                                             const float *__restrict__ K,
+                                                             const float *__restrict__ V,
+                                                             const float *__restrict__ GO,
+                                                             float *__restrict__ GQ,
+                                                             float *__restrict__ GK,
+                                                             float *__restrict__ GV, int T, int D,
+                                                             int NH, int causal, float *__restrict__ TS,
+                                                             int64_t tss) {
+  constexpr int NU = 8 / NW;
   __shared__ __align__(16) float sq[AT_T * A16_HP];
   __shared__ __align__(16) float sk[AT_T * A16_HP];
   __shared__ __align__(16) float sv[AT_T * A16_HP];
   __shared__ __align__(16) float sg[AT_T * A16_HP];
   __shared__ __align__(16) float sp[AT_T * A16_SP];  // P^T, then dS^T, as [j][i]
-  __shared__ float tred[3][4][AT_HD];
+  __shared__ float tred[3][NW][AT_HD];
   const int b = blockIdx.x / NH, h = blockIdx.x % NH;
   const int hd = D / NH;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   {
     float *const dst[4] = {sq, sk, sv, sg};
     const float *const src[4] = {Q, K, V, GO};
-    stage16<4>(dst, src, b, h, T, D, hd);
+    stage16<4, 64 * NW>(dst, src, b, h, T, D, hd);
   }
   __syncthreads();
   const float inv_scale = 1.0f / (float)sqrt((double)hd);
   const int nt = (T + 15) >> 4;
-  fx4 dsk[2][8];  // dS^T of the wave's two query tiles, kept for the gK pass
+  fx4 dsk[NU][8];  // dS^T of the wave's query tiles, kept for the gK pass
   float tq[8];    // gQ token-sum partials: value v = 4 half + r, d = 4*(l/16) + r + 16 half
 #pragma unroll
   for (int v = 0; v < 8; ++v) tq[v] = 0.f;
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int qt = u ? 7 - w : w;
+  for (int u = 0; u < NU; ++u) {
+    const int qt = tile_of<NW>(w, u);
     if (qt >= nt) continue;
     const int klim = causal ? qt : nt - 1;
     const int i = 16 * qt + (lane & 15);
@@ -1189,8 +1204,8 @@ __global__ __launch_bounds__(256) void attn16_bwd_kernel(const float *__restrict
   auto keyside = [&](const float *Yq, float *G, int m) {
     float ts[2] = {0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int kt = u ? 7 - w : w;
+    for (int u = 0; u < NU; ++u) {
+      const int kt = tile_of<NW>(w, u);
       if (kt >= nt) continue;
       fx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
       const float *zrow = sp + (16 * kt + (lane & 15)) * A16_SP + 4 * (lane >> 4);
@@ -1232,8 +1247,8 @@ __global__ __launch_bounds__(256) void attn16_bwd_kernel(const float *__restrict
   keyside(sg, GV, 2);  // gV_j = sum_i p_ij gO_i
   __syncthreads();
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int qt = u ? 7 - w : w;
+  for (int u = 0; u < NU; ++u) {
+    const int qt = tile_of<NW>(w, u);
     if (qt >= nt) continue;
     const int klim = causal ? qt : nt - 1;
     const int i = 16 * qt + (lane & 15);
@@ -1249,11 +1264,16 @@ __global__ __launch_bounds__(256) void attn16_bwd_kernel(const float *__restrict
   if (TS) {
     __syncthreads();
     const int m = threadIdx.x >> 5, d = threadIdx.x & 31;
-    if (m < 3 && d < hd)
-      TS[m * tss + (int64_t)b * D + h * hd + d] =
-          ((tred[m][0][d] + tred[m][1][d]) + tred[m][2][d]) + tred[m][3][d];
+    if (m < 3 && d < hd) {
+      float v = tred[m][0][d];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) v += tred[m][q][d];
+      TS[m * tss + (int64_t)b * D + h * hd + d] = v;
+    }
   }
 }
+
+constexpr int kAttnWaves = 8;  // waves per attention workgroup
 
 static unsigned blocks_for(int64_t n) {
   int64_t b = (n + 255) / 256;
@@ -1642,7 +1662,8 @@ hipError_t launch_gap1d_bwd(const float *g, float *gin, int B, int T, int D, hip
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, float *O, int B, int T,
                            int D, int NH, int causal, hipStream_t s) {
   if (!attn_supported(T, D, NH)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn16_fwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, O, T, D, NH, causal);
+  hipLaunchKernelGGL(attn16_fwd_kernel<kAttnWaves>, dim3(B * NH), dim3(64 * kAttnWaves), 0, s, Q, K, V, O, T, D,
+                     NH, causal);
   return hipGetLastError();
 }
 
@@ -1650,8 +1671,8 @@ hipError_t launch_attn_bwd(const float *Q, const float *K, const float *V, const
                            float *GQ, float *GK, float *GV, int B, int T, int D, int NH, int causal,
                            hipStream_t s, float *TS, int64_t tss) {
   if (!attn_supported(T, D, NH)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn16_bwd_kernel, dim3(B * NH), dim3(256), 0, s, Q, K, V, GO, GQ, GK, GV, T, D,
-                     NH, causal, TS, tss);
+  hipLaunchKernelGGL(attn16_bwd_kernel<kAttnWaves>, dim3(B * NH), dim3(64 * kAttnWaves), 0, s, Q, K, V, GO, GQ,
+                     GK, GV, T, D, NH, causal, TS, tss);
   return hipGetLastError();
 }
 
