@@ -500,10 +500,12 @@ __device__ __attribute__((noinline)) float or_exp_diff(float a, float b) {
   return (float)exp((double)(a - b));
 }
 __device__ __attribute__((noinline)) float or_exp(float a) { return (float)exp((double)a); }
-// Inline forms for the wide-row kernels (8 values per thread): eight
-// independent float64 exps interleave instead of running as eight calls.
-__device__ __forceinline__ float or_exp_diff_i(float a, float b) { return (float)exp((double)(a - b)); }
-__device__ __forceinline__ float or_exp_i(float a) { return (float)exp((double)a); }
+// The wide-row kernels (up to 16 values per thread, thousands of classes)
+// take the float32 exp, within 1 ulp of the reference's float64 exp rounded
+// to float32 (as the attention softmax does): 16 float64 exps per thread had
+// set the row kernel's time.
+__device__ __forceinline__ float or_exp_diff_i(float a, float b) { return expf(a - b); }
+__device__ __forceinline__ float or_exp_i(float a) { return expf(a); }
 __device__ __attribute__((noinline)) float or_log(float a) { return (float)log((double)a); }
 __device__ __attribute__((noinline)) float or_fwd(float v, int kind) { return fwd_of(v, kind); }
 __device__ __attribute__((noinline)) float or_deriv(float o, int kind) { return deriv_of(o, kind); }
