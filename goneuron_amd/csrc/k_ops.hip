@@ -33,17 +33,23 @@ __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, flo
   p = p - efflr * mi / (__builtin_sqrtf(vi) + eps);
 }
 
-// Each thread handles ADAM_U float4 groups per iteration (spaced one block
-// apart, so every load instruction stays coalesced) and issues all 4*ADAM_U
-// loads before the arithmetic, which keeps enough bytes in flight per CU to
-// run near the HBM limit.
+// Each thread handles U float4 groups per iteration (spaced one block apart,
+// so every load instruction stays coalesced) and issues all 4*U loads before
+// the arithmetic, which keeps enough bytes in flight per CU to run near the
+// HBM limit: U = 4 for arenas above 8 Mi parameters (C3: 5.92 TB/s; U = 1
+// 5.22), U = 1 below when the grid is not capped, where one pass of single
+// groups finishes sooner (C4's 4.9 M parameters: 22.1 vs 23.8 us in a
+// scratch harness).
 constexpr int ADAM_U = 4;
+constexpr int64_t kAdamSmall = 8 << 20;
 
+template <int U>
 __device__ __forceinline__ void adam_range(float *__restrict__ p, const float *__restrict__ g,
                                            float *__restrict__ m, float *__restrict__ v, int64_t n,
                                            float efflr, float b1, float b2, float omb1, float omb2,
                                            float eps) {
   typedef float f4v __attribute__((ext_vector_type(4)));
+  constexpr int ADAM_U = U;
   const int64_t n4 = n >> 2;
   const int64_t stride = (int64_t)gridDim.x * TPB * ADAM_U;
   f4v *p4 = reinterpret_cast<f4v *>(p);
@@ -87,11 +93,12 @@ __device__ __forceinline__ void adam_range(float *__restrict__ p, const float *_
   }
 }
 
+template <int U>
 __global__ __launch_bounds__(TPB) void adam_kernel(float *__restrict__ p, const float *__restrict__ g,
                                                    float *__restrict__ m, float *__restrict__ v, int64_t n,
                                                    float efflr, float b1, float b2, float omb1, float omb2,
                                                    float eps) {
-  adam_range(p, g, m, v, n, efflr, b1, b2, omb1, omb2, eps);
+  adam_range<U>(p, g, m, v, n, efflr, b1, b2, omb1, omb2, eps);
 }
 
 hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, float efflr,
@@ -107,7 +114,7 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
     return hipErrorInvalidValue;
   if (mis) {
     const int64_t head = std::min<int64_t>(n, (int64_t)((16 - mis) / 4));
-    hipLaunchKernelGGL(adam_kernel, dim3(1), dim3(TPB), 0, s, p, g, m, v, head, efflr, b1, b2, omb1,
+    hipLaunchKernelGGL(adam_kernel<1>, dim3(1), dim3(TPB), 0, s, p, g, m, v, head, efflr, b1, b2, omb1,
                        omb2, eps);
     p += head;
     g += head;
@@ -117,11 +124,17 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
     if (n <= 0) return hipGetLastError();
   }
   const int64_t n4 = n >> 2;
-  int64_t blocks = (n4 + TPB * ADAM_U - 1) / (TPB * ADAM_U);
+  // single groups only where they make one pass (not under a block cap)
+  const int u = n <= kAdamSmall && (n4 + TPB - 1) / TPB <= max_blocks ? 1 : ADAM_U;
+  int64_t blocks = (n4 + TPB * u - 1) / (TPB * u);
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(adam_kernel, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
-                     b1, b2, omb1, omb2, eps);
+  if (u == 1)
+    hipLaunchKernelGGL(adam_kernel<1>, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
+                       b1, b2, omb1, omb2, eps);
+  else
+    hipLaunchKernelGGL(adam_kernel<ADAM_U>, dim3((unsigned)blocks), dim3(TPB), 0, s, p, g, m, v, n, efflr,
+                       b1, b2, omb1, omb2, eps);
   return hipGetLastError();
 }
 
