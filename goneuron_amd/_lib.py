@@ -70,6 +70,7 @@ SIGNATURES = {
     "gn_debug_lstm_spin_limit": (C.c_int, [vp, C.c_int32]),
     "gn_debug_lstm_clip_bail": (C.c_int, [vp, C.c_int32]),
     "gn_debug_fused_tail": (C.c_int, [vp, C.c_int32]),
+    "gn_debug_step_update": (C.c_int, [vp, C.c_int32]),
     "gn_debug_side_streams": (C.c_int, [vp, C.c_int32]),
     "gn_malloc": (C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
     "gn_free": (C.c_int, [vp, vp]),

@@ -117,6 +117,44 @@ hipError_t launch_adam(float *p, const float *g, float *m, float *v, int64_t n, 
                        float b1, float b2, float omb1, float omb2, float eps, hipStream_t s,
                        int max_blocks = 16384);
 
+// Adam.StepInPlace for one parameter, opt.go:244-251:
+//   m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; p -= effLR*m/(sqrt(v)+eps)
+// The library is built with -ffp-contract=off, so every product and sum is
+// rounded on its own; '/' and sqrtf are IEEE correctly rounded under
+// -fhip-fp32-correctly-rounded-divide-sqrt (== float32(math.Sqrt(float64(v)))).
+__device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float efflr, float b1,
+                                      float b2, float omb1, float omb2, float eps) {
+  const float mi = b1 * m + omb1 * g;
+  const float vi = b2 * v + omb2 * g * g;
+  m = mi;
+  v = vi;
+  p = p - efflr * mi / (__builtin_sqrtf(vi) + eps);
+}
+
+// Network.Step's update carried by the kernel that writes a step's last
+// gradients (no Adam launch of its own).  A gradient at gp in the arena's
+// gradient region has its parameter, first and second moment at gp - stride,
+// gp + stride and gp + 2 stride (the arena is [params | grads | m | v]).
+struct AdamStep {
+  float efflr, b1, b2, omb1, omb2, eps;
+  int64_t stride;  // 0: no update
+  // launch_conv_wgrad_reduce: extra blocks update the gradients
+  // [rest + r0[i], rest + r1[i]) (final, their parameters read by no later
+  // kernel of the step)
+  float *rest;
+  int64_t r0[2], r1[2];
+};
+
+// the update of the parameter whose gradient g was just stored at gp
+__device__ __forceinline__ void adam_at(float *gp, float g, const AdamStep &a) {
+  float *pp = gp - a.stride, *mp = gp + a.stride, *vp = gp + 2 * a.stride;
+  float p = *pp, m = *mp, v = *vp;
+  adam1(p, g, m, v, a.efflr, a.b1, a.b2, a.omb1, a.omb2, a.eps);
+  *pp = p;
+  *mp = m;
+  *vp = v;
+}
+
 // db[o] = scale * sum_b dz[b*ld + o]
 hipError_t launch_colsum(const float *dz, int rows, int cols, int ld, float scale, float *out,
                          float *scratch, size_t scratch_cap, hipStream_t s);
@@ -221,9 +259,20 @@ hipError_t launch_conv_fwd(const float *x, const float *w, const float *bias, fl
                            int32_t *pool_arg = nullptr);
 bool conv_fwd_pool_fusable(const ConvShape &s, const PoolShape &p, int B);
 // grad = [dW | db] (scaled), dz = gout * act'(out) formed on the fly
+// red: only the partial sums are launched; red receives the reduction's
+// arguments for launch_conv_wgrad_reduce
+struct ConvWgradReduce {
+  const float *ws;
+  int nblocks, nslots;
+  float scale;
+  float *grad;
+};
 hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
                              const ConvShape &s, int B, int deriv, float scale, float *ws,
-                             size_t ws_cap, hipStream_t st);
+                             size_t ws_cap, hipStream_t st, ConvWgradReduce *red = nullptr);
+// the deferred reduction, with the step's update of every gradient it writes
+// and of upd.rest's ranges (extra blocks); upd null: the reduction alone
+hipError_t launch_conv_wgrad_reduce(const ConvWgradReduce &red, const AdamStep *upd, hipStream_t st);
 hipError_t launch_conv_dgrad(const float *gout, const float *out, const float *w, float *gin,
                              const ConvShape &s, int B, int deriv, hipStream_t st);
 hipError_t launch_maxpool_fwd(const float *x, float *out, int32_t *argmax, const PoolShape &s,

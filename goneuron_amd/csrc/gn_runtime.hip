@@ -14,6 +14,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -612,20 +613,38 @@ struct gn_model {
   // HIP graphs of the accumulate pass (forward, loss, backward) of small
   // models, keyed by the input pointers, the batch and the training flags in
   // effect: the first step with a key runs eagerly, the second is captured,
-  // later ones replay.  Adam runs after the graph as an ordinary launch (its
-  // coefficients change every step; an update inside the graph with its
-  // coefficients from a device table measured no faster: 36.7 vs 36.4 us per
-  // C1 step).
+  // later ones replay.  Adam (or the launch carrying it, upd_fn) runs after
+  // the graph as an ordinary launch (its coefficients change every step; an
+  // update inside the graph with its coefficients from a device table
+  // measured no faster: 36.7 vs 36.4 us per C1 step).
   struct StepGraph {
     const float *x, *y;
     int B;
     std::vector<char> eff;
     hipGraphExec_t exec;
+    bool upd;  // captured for a train step (upd_want)
+    std::function<hipError_t(const AdamStep &)> upd_fn;  // the launch it left out, or none
+    const char *upd_name;
+    double upd_units;
   };
   std::vector<StepGraph> graphs;
   bool graph_on = true;   // gn_model_set_graphs
   int emb = -1;           // the Embedding layer (its index-error flags mask samples), or -1
   bool graph_ok = true;   // false once a capture failed: eager from then on
+  // Train steps of small models: when the backward's last launch can carry
+  // Network.Step's update (the weight-gradient reduction of a first Conv2D:
+  // each gradient it writes is updated by the lane that writes it, extra
+  // blocks update every other layer), the pass leaves it out and the step
+  // launches it with the update's coefficients after the pass or its graph:
+  // no Adam launch of its own (C2 63.7 -> 60.3 us per step, same box).
+  // upd_want asks the current pass for it; upd_fn, upd_name, upd_units
+  // describe the launch left out (null: none, the step launches Adam).
+  // gn_debug_step_update.
+  bool upd_on = true;
+  bool upd_want = false;
+  std::function<hipError_t(const AdamStep &)> upd_fn;
+  const char *upd_name = nullptr;
+  double upd_units = 0;
   // a forward pass ran on the network's own layers (Predict, or training with
   // one worker; trainBatchParallel runs clones only, net.go:588-716): from
   // then on its Conv2D / pooling layers know their input height and width
@@ -2384,10 +2403,33 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         if (is_dz && i != n - 1) return set_err(c, GN_ERR_UNSUPPORTED, "fused dz into Conv2D");
         const float *W = M->params + R.poff;
         {  // dW and db: the taps plus the all-ones column
-          KTimer kt(c, GN_KCLASS_OTHER, "conv_wgrad",
-                    conv_flops(R.cs, B) + 2.0 * B * R.cs.outC * R.cs.oH * R.cs.oW);
-          HIP_OK(c, launch_conv_wgrad(in, R.gout, R.out, M->grads + R.poff, R.cs, B, R.cderiv, scale,
-                                      c->scratch, c->scratch_floats, c->stream));
+          // the first layer's reduction is the backward's last launch: with
+          // the step's update it is left out, and carries the update of every
+          // other layer in extra blocks
+          ConvWgradReduce red{};
+          const bool defer = M->upd_want && !below;
+          {
+            KTimer kt(c, GN_KCLASS_OTHER, "conv_wgrad",
+                      conv_flops(R.cs, B) + 2.0 * B * R.cs.outC * R.cs.oH * R.cs.oW);
+            HIP_OK(c, launch_conv_wgrad(in, R.gout, R.out, M->grads + R.poff, R.cs, B, R.cderiv, scale,
+                                        c->scratch, c->scratch_floats, c->stream, defer ? &red : nullptr));
+          }
+          if (defer) {
+            hipStream_t st = c->stream;
+            float *rest = M->grads;
+            const int64_t c0 = R.poff, c1 = R.poff + red.nslots, np = M->nparams;
+            M->upd_fn = [=](const AdamStep &a) {
+              AdamStep u = a;
+              u.rest = rest;
+              u.r0[0] = 0;
+              u.r1[0] = c0;
+              u.r0[1] = c1;
+              u.r1[1] = np;
+              return launch_conv_wgrad_reduce(red, &u, st);
+            };
+            M->upd_name = "wgrad_reduce_adam";
+            M->upd_units = 4.0 * ((double)red.nblocks * red.nslots + red.nslots) + 28.0 * M->nparams;
+          }
         }
         if (below && below->gout) {
           KTimer kt(c, GN_KCLASS_OTHER, "conv_dgrad", conv_flops(R.cs, B));
@@ -2878,12 +2920,15 @@ static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B
   if (rc) return rc;
   gn_model::StepGraph *g = nullptr;
   for (auto &e : M->graphs)
-    if (e.x == x && e.y == y && e.B == B && e.eff == M->eff) g = &e;
+    if (e.x == x && e.y == y && e.B == B && e.eff == M->eff && e.upd == M->upd_want) g = &e;
   if (g && g->exec) {  // replay: the host state the pass would have set
     M->last_predict = false;
     M->last_B = B;
     M->loss_B = B;
     HIP_OK(c, hipGraphLaunch(g->exec, c->stream));
+    M->upd_fn = g->upd_fn;
+    M->upd_name = g->upd_name;
+    M->upd_units = g->upd_units;
     return GN_OK;
   }
   if (!g) {  // first step with this key: eager (also settles every lazy set-up)
@@ -2893,7 +2938,7 @@ static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B
       if (M->graphs.front().exec) (void)hipGraphExecDestroy(M->graphs.front().exec);
       M->graphs.erase(M->graphs.begin());
     }
-    M->graphs.push_back({x, y, B, M->eff, nullptr});
+    M->graphs.push_back({x, y, B, M->eff, nullptr, M->upd_want, nullptr, nullptr, 0.0});
     return GN_OK;
   }
   // second step with this key: capture the pass, then launch it
@@ -2907,6 +2952,9 @@ static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B
     (void)hipGraphDestroy(graph);
     if (e == hipSuccess) {
       g->exec = ex;
+      g->upd_fn = M->upd_fn;  // the launch the captured pass left out (or none)
+      g->upd_name = M->upd_name;
+      g->upd_units = M->upd_units;
       HIP_OK(c, hipGraphLaunch(ex, c->stream));
       return GN_OK;
     }
@@ -2927,9 +2975,29 @@ static int accumulate_graphed(gn_model *M, const float *x, const float *y, int B
 constexpr int64_t kOverlapAdamMin = (int64_t)8 << 20;
 static int model_train_step(gn_model *M, const float *x, const float *y, int B) {
   if (!M->overlap_adam || M->nparams < kOverlapAdamMin) {
+    M->upd_want = M->upd_on;
+    M->upd_fn = nullptr;
     int rc = graph_eligible(M) ? accumulate_graphed(M, x, y, B) : model_accumulate(M, x, y, B);
+    M->upd_want = false;
     if (rc) return rc;
-    return gn_model_step(M);
+    if (!M->upd_fn) return gn_model_step(M);
+    // the backward's last launch, left out of the pass, with Network.Step's
+    // update (Adam.NewStep, opt.go:254-258, then StepInPlace per parameter)
+    gn_ctx *c = M->ctx;
+    const AdamCoef a = adam_next(M);
+    AdamStep u{};
+    u.efflr = a.efflr;
+    u.b1 = a.b1;
+    u.b2 = a.b2;
+    u.omb1 = a.omb1;
+    u.omb2 = a.omb2;
+    u.eps = a.eps;
+    u.stride = M->region;
+    KTimer kt(c, GN_KCLASS_OTHER, M->upd_name, M->upd_units);
+    const hipError_t e = M->upd_fn(u);
+    M->upd_fn = nullptr;
+    HIP_OK(c, e);
+    return GN_OK;
   }
   if (B <= 0 || B > M->maxB) return set_err(M->ctx, GN_ERR_INVALID, "batch %d outside [1,%d]", B, M->maxB);
   const int saved = M->timestep;
@@ -3051,6 +3119,15 @@ extern "C" int gn_debug_fused_tail(gn_model *M, int32_t on) {
   ENTRY(M->ctx);
   HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
   M->tail_on = on != 0;
+  drop_graphs(M);  // captured passes hold the other path
+  return GN_OK;
+}
+
+extern "C" int gn_debug_step_update(gn_model *M, int32_t on) {
+  if (!M) return GN_ERR_INVALID;
+  ENTRY(M->ctx);
+  HIP_OK(M->ctx, hipStreamSynchronize(M->ctx->stream));
+  M->upd_on = on != 0;
   drop_graphs(M);  // captured passes hold the other path
   return GN_OK;
 }

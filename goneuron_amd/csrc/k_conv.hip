@@ -373,10 +373,23 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_mfma(const float *__restrict_
     }
 }
 
-// One wave per slot: lanes take the blocks, then a wave reduction.
+// One wave per slot: lanes take the blocks, then a wave reduction.  With the
+// step's update (ad.stride), each slot's gradient is updated by the lane that
+// writes it, and blocks from nred on update ad.rest's ranges.
 __global__ __launch_bounds__(CT) void conv2d_wgrad_reduce(const float *__restrict__ part,
                                                           int nblocks, int nslots, float scale,
-                                                          float *__restrict__ grad) {
+                                                          float *__restrict__ grad, int nred,
+                                                          AdamStep ad) {
+  if ((int)blockIdx.x >= nred) {
+    const int64_t step = (int64_t)(gridDim.x - nred) * CT;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float *g = ad.rest;
+      for (int64_t i = ad.r0[r] + (int64_t)(blockIdx.x - nred) * CT + threadIdx.x; i < ad.r1[r]; i += step)
+        adam_at(g + i, g[i], ad);
+    }
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int o = blockIdx.x * (CT / 64) + (threadIdx.x >> 6);
   if (o >= nslots) return;
@@ -391,7 +404,10 @@ __global__ __launch_bounds__(CT) void conv2d_wgrad_reduce(const float *__restric
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
-  if (lane == 0) grad[o] = s * scale;  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)
+  if (lane == 0) {  // grad = [dW | db], the Conv2D arena layout (conv2d.go:121-125)
+    grad[o] = s * scale;
+    if (ad.stride) adam_at(grad + o, s * scale, ad);
+  }
 }
 
 // dX gather: gin[b, ic, ih, iw] = sum over (oc, kh, kw) of dz * w, dz formed
@@ -763,9 +779,28 @@ hipError_t launch_avgpool_bwd(const float *gout, float *gin, const PoolShape &s,
   return hipGetLastError();
 }
 
+hipError_t launch_conv_wgrad_reduce(const ConvWgradReduce &red, const AdamStep *upd, hipStream_t st) {
+  AdamStep ad{};
+  int extra = 0;
+  if (upd) {
+    ad = *upd;
+    if (ad.stride <= 0) return hipErrorInvalidValue;
+    int64_t n = 0;
+    for (int r = 0; r < 2; ++r) {
+      if (ad.r1[r] < ad.r0[r] || (ad.r1[r] > ad.r0[r] && !ad.rest)) return hipErrorInvalidValue;
+      n += ad.r1[r] - ad.r0[r];
+    }
+    extra = (int)std::min<int64_t>((n + 4 * CT - 1) / (4 * CT), 1024);  // ~4 parameters per thread
+  }
+  const int nred = (red.nslots + 3) / 4;
+  hipLaunchKernelGGL(conv2d_wgrad_reduce, dim3(nred + extra), dim3(CT), 0, st, red.ws, red.nblocks, red.nslots,
+                     red.scale, red.grad, nred, ad);
+  return hipGetLastError();
+}
+
 hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out, float *grad,
                              const ConvShape &s, int B, int deriv, float scale, float *ws,
-                             size_t ws_cap, hipStream_t st) {
+                             size_t ws_cap, hipStream_t st, ConvWgradReduce *red) {
   const int nslots = s.outC * s.inC * s.k * s.k + s.outC;
   const int Wp = s.W + 2 * s.pad;
   // MFMA path: bands of output rows whose dz tile, input rows and tables fit
@@ -782,8 +817,12 @@ hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out
     if ((size_t)nblocks * nslots > ws_cap) return hipErrorInvalidValue;
     hipLaunchKernelGGL(conv2d_wgrad_mfma, dim3(nblocks), dim3(CT), mfma_lds(band), st, x, gout, out,
                        ws, s, band, deriv);
+    if (red) {
+      *red = ConvWgradReduce{ws, nblocks, nslots, scale, grad};
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(conv2d_wgrad_reduce, dim3((nslots + 3) / 4), dim3(CT), 0, st, ws, nblocks,
-                       nslots, scale, grad);
+                       nslots, scale, grad, (nslots + 3) / 4, AdamStep{});
     return hipGetLastError();
   }
   // scalar path for shapes whose input rows do not fit: dz tile <= 32 KiB
@@ -795,8 +834,12 @@ hipError_t launch_conv_wgrad(const float *x, const float *gout, const float *out
   const size_t shm = (size_t)s.outC * band * s.oW * sizeof(float);
   hipLaunchKernelGGL(conv2d_wgrad_partial, dim3(nblocks), dim3(CT), shm, st, x, gout, out, ws, s,
                      band, deriv);
+  if (red) {
+    *red = ConvWgradReduce{ws, nblocks, nslots, scale, grad};
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(conv2d_wgrad_reduce, dim3((nslots + 3) / 4), dim3(CT), 0, st, ws, nblocks,
-                     nslots, scale, grad);
+                     nslots, scale, grad, (nslots + 3) / 4, AdamStep{});
   return hipGetLastError();
 }
 

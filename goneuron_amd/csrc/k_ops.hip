@@ -17,22 +17,9 @@ namespace gn {
 constexpr int TPB = 256;
 
 // ---------------------------------------------------------------------------
-// Adam.StepInPlace, opt.go:244-251:
-//   m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; p -= effLR*m/(sqrt(v)+eps)
-// 28 bytes of HBM traffic per parameter (read p,g,m,v; write p,m,v).
+// Adam.StepInPlace over the arena (adam1, opt.go:244-251): 28 bytes of HBM
+// traffic per parameter (read p,g,m,v; write p,m,v).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float efflr, float b1,
-                                      float b2, float omb1, float omb2, float eps) {
-  // -ffp-contract=off keeps every product and sum separately rounded;
-  // '/' and sqrtf are IEEE correctly rounded under
-  // -fhip-fp32-correctly-rounded-divide-sqrt (== float32(math.Sqrt(float64(v))))
-  const float mi = b1 * m + omb1 * g;
-  const float vi = b2 * v + omb2 * g * g;
-  m = mi;
-  v = vi;
-  p = p - efflr * mi / (__builtin_sqrtf(vi) + eps);
-}
-
 // Each thread handles U float4 groups per iteration (spaced one block apart,
 // so every load instruction stays coalesced) and issues all 4*U loads before
 // the arithmetic, which keeps enough bytes in flight per CU to run near the

@@ -212,6 +212,13 @@ int gn_debug_lstm_clip_bail(gn_model *model, int32_t polls);
  * (at most 32 outputs, input width a multiple of 4); 1 (the default) allows
  * them.  Both paths compute the same step to float32 rounding. */
 int gn_debug_fused_tail(gn_model *model, int32_t on);
+/* Test hook (no counterpart in the reference): on = 0 makes train steps of
+ * small models (under 8 Mi parameters) run Network.Step's Adam update as a
+ * launch of its own after the backward; 1 (the default) lets the backward's
+ * last launch carry it where that launch writes the step's last gradients
+ * (a first Conv2D's weight-gradient reduction).  Both give the same step bit
+ * for bit. */
+int gn_debug_step_update(gn_model *model, int32_t on);
 /* Test hook (no counterpart in the reference): on = 1 runs the backward's
  * parameter-gradient kernels (Dense dW and bias sums, the transformer
  * block's token sums and weight gradients) on a second stream beside the
