@@ -95,6 +95,20 @@ def kernel_table(lib, dev, K):
     return out
 
 
+def add_floors(kernels, launch_us):
+    """Each kernel against the shortest time it could take: the longer of an
+    empty launch (launch_us, timed like the kernels) and its algorithmic bytes
+    or FLOPs at the bound's peak.  floor_frac near 1: the kernel is at its
+    floor (for the small kernels of C1, C2 and C4 the launch sets it)."""
+    if not launch_us:
+        return
+    for k in kernels.values():
+        scale = 1e12 if k["unit"] == "TFLOP/s" else 1e9
+        work = (k.get("units_per_launch") or 0.0) / (k["peak"] * scale) * 1e6
+        k["floor_us"] = max(launch_us, work)
+        k["floor_frac"] = k["floor_us"] / k["us_per_launch"] if k.get("us_per_launch") else None
+
+
 def host_info():
     model = None
     try:
@@ -209,7 +223,8 @@ def dominant(kernels):
         return None
     name, k = max(kernels.items(), key=lambda kv: kv[1]["ms_per_step"])
     return {"kernel": name, "bound": k["bound"], "achieved": k["achieved"], "peak": k["peak"],
-            "unit": k["unit"], "frac": k["frac"], "ms_per_step": k["ms_per_step"]}
+            "unit": k["unit"], "frac": k["frac"], "ms_per_step": k["ms_per_step"],
+            "floor_frac": k.get("floor_frac")}
 
 
 def run_config(name, args, dev, with_cpu, cpu_budget, threads):
@@ -260,6 +275,13 @@ def run_config(name, args, dev, with_cpu, cpu_budget, threads):
     dev.sync()
     adam = kernel_table(L, dev, K).get("adam")
     check(dev.h, L.gn_timing_enable(dev.h, 0))
+    # the launch floor, timed the same way: K empty 256-block launches
+    check(dev.h, L.gn_timing_enable(dev.h, 1))
+    check(dev.h, L.gn_timing_floor(dev.h, 256, K))
+    dev.sync()
+    floor = kernel_table(L, dev, K).get("floor") or {}
+    check(dev.h, L.gn_timing_enable(dev.h, 0))
+    add_floors(kernels, floor.get("us_per_launch"))
     loss = C.c_float()
     check(dev.h, L.gn_model_read_loss(model.h, C.byref(loss)))
     # end to end from host buffers: the step copies x and y over PCIe first
@@ -293,6 +315,7 @@ def run_config(name, args, dev, with_cpu, cpu_budget, threads):
         "dominant": dominant(kernels),
         "kernels": kernels,
         "adam_alone": adam,
+        "launch_floor_us": floor.get("us_per_launch"),
         "h2d_step": {"value": B * K / elapsed_h, "unit": "samples/s", "ms_per_step": elapsed_h * 1e3 / K,
                      "note": "gn_model_train_step from host buffers: H2D copy of x and y inside "
                              "every step (never `value`)"},
@@ -428,6 +451,7 @@ def summarize(res):
             "kernels_per_step": _r(res.get("kernels_per_step"), 3),
             "dominant": d.get("kernel"), "dominant_bound": d.get("bound"),
             "dominant_frac": _r(d.get("frac"), 3),
+            "dominant_floor_frac": _r(d.get("floor_frac"), 3),
             "cpu_baseline": _r(cb.get("value")), "cpu_cores": cb.get("cores")}
 
 

@@ -164,6 +164,7 @@ SIGNATURES = {
     "gn_timing_enable": (C.c_int, [vp, C.c_int]),
     "gn_timing_report": (C.c_int, [vp, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     "gn_timing_kernels": (C.c_int, [vp, C.POINTER(KernelStat), C.c_int32, i32p]),
+    "gn_timing_floor": (C.c_int, [vp, C.c_int32, C.c_int32]),
 }
 
 _lib = None

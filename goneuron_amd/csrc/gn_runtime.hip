@@ -225,6 +225,19 @@ extern "C" int gn_timing_kernels(gn_ctx *c, gn_kernel_stat *out, int32_t cap, in
   return GN_OK;
 }
 
+__global__ void floor_kernel() {}
+
+extern "C" int gn_timing_floor(gn_ctx *c, int32_t blocks, int32_t reps) {
+  ENTRY(c);
+  if (blocks < 1 || reps < 0) return set_err(c, GN_ERR_INVALID, "bad timing_floor args");
+  for (int32_t r = 0; r < reps; ++r) {
+    KTimer kt(c, GN_KCLASS_OTHER, "floor", 0.0);
+    hipLaunchKernelGGL(floor_kernel, dim3((unsigned)blocks), dim3(256), 0, c->stream);
+    HIP_OK(c, hipGetLastError());
+  }
+  return GN_OK;
+}
+
 extern "C" int gn_malloc(gn_ctx *c, size_t bytes, void **dptr) {
   ENTRY(c);
   if (!dptr) return set_err(c, GN_ERR_INVALID, "dptr is null");

@@ -551,6 +551,10 @@ typedef struct gn_kernel_stat {
   double units;
 } gn_kernel_stat;
 int gn_timing_kernels(gn_ctx *ctx, gn_kernel_stat *out, int32_t cap, int32_t *n);
+/* The launch floor the per-kernel times are read against: reps launches of an
+ * empty kernel of `blocks` 256-thread workgroups on the context stream, timed
+ * like every library launch (recorded as "floor" while timing is enabled). */
+int gn_timing_floor(gn_ctx *ctx, int32_t blocks, int32_t reps);
 
 /* ---- synthetic inputs (host side; harness utility) ----------------------
  * The reference's LCG (layer.go:61-81): U[0,1) stream, N(0,1) by one
