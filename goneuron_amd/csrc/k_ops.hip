@@ -699,6 +699,9 @@ hipError_t launch_out_rows_reg(float *out, const float *y, float *dz, float *los
   } else if (C <= 256 * OR_PER) {
     hipLaunchKernelGGL((out_rows_reg_kernel<256, 256>), dim3(B), dim3(256), 0, s, out, y, dz,
                        loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
+  } else if (C <= 512 * OR_PER) {
+    hipLaunchKernelGGL((out_rows_reg_kernel<512, 512>), dim3(B), dim3(512), 0, s, out, y, dz,
+                       loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
   } else if (C <= 1024 * OR_PER) {
     hipLaunchKernelGGL((out_rows_reg_kernel<1024, 1024>), dim3(B), dim3(1024), 0, s, out, y, dz,
                        loss_rows, B, C, row_act & 0xff, fwd, deriv, loss_kind, bad, chunk);
