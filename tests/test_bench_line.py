@@ -16,6 +16,7 @@ def fake_result(name, nkernels=40, B=1024, with_cpu=True):
                        "achieved": 123.456789, "unit": "TFLOP/s" if i < 3 else "GB/s",
                        "peak": 157.3 if i < 3 else 8000.0, "frac": 0.78485436,
                        "units_per_launch": 28791291904.0}
+    bench.add_floors(kernels, 6.1234567)
     res = {"workload": name, "batch": B, "workers": 4, "params": 71222248,
            "value": 311220.123456789, "unit": "samples/s", "ms_per_step": 3.29023456789,
            "instrumented_ms_per_step": 3.4, "kernels_per_step": 37.0,
@@ -64,3 +65,16 @@ def test_final_line_without_gemms_uses_dominant_kernel():
     assert line["roofline"]["kernel"] == head["dominant"]["kernel"]
     assert line["cpu_baseline"] is None
     assert len(json.dumps(line)) < bench.MAX_LINE_BYTES
+
+
+def test_kernel_floor_is_the_longer_of_launch_and_work():
+    """floor_us = max(empty-launch time, work at the bound's peak), floor_frac
+    = floor_us / the kernel's time; no floors without a launch figure."""
+    k = {"tiny": {"unit": "GB/s", "peak": 8000.0, "units_per_launch": 8e6, "us_per_launch": 10.0},
+         "big": {"unit": "TFLOP/s", "peak": 157.3, "units_per_launch": 157.3e6 * 200, "us_per_launch": 250.0}}
+    bench.add_floors(k, 6.0)
+    assert k["tiny"]["floor_us"] == 6.0 and abs(k["tiny"]["floor_frac"] - 0.6) < 1e-12  # 1 us of bytes < launch
+    assert abs(k["big"]["floor_us"] - 200.0) < 1e-9 and abs(k["big"]["floor_frac"] - 0.8) < 1e-12
+    k2 = {"x": {"unit": "GB/s", "peak": 8000.0, "units_per_launch": 1.0, "us_per_launch": 5.0}}
+    bench.add_floors(k2, None)
+    assert "floor_us" not in k2["x"]
