@@ -2802,22 +2802,29 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         return set_err(c, GN_ERR_UNSUPPORTED, "layer kind %d", R.d.kind);
     }
     if (ac && R.pcount > 0) {
-      // Adam on its own stream: after the layer's dX (main stream) and dW
-      // (ctx->aux), so the next layers' dW GEMMs do not queue behind it
-      HIP_OK(c, hipEventRecord(M->sync_ev[i], c->stream));
-      HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->sync_ev[i], 0));
-      if (dw_aux[i]) HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->dw_ev[i], 0));
       // While backward kernels still run, a 256-block grid (one block per CU
       // next to the GEMM's waves) keeps the update off their critical path;
-      // the update of the first parameterised layer runs alone, at full width.
+      // the update of the first parameterised layer runs at full width.
       bool last = true;
       for (int j = 0; j < i; ++j)
         if (M->L[j].pcount > 0) last = false;
-      KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, M->adam_s);
+      // Adam on its own stream: after the layer's dX (main stream) and dW
+      // (ctx->aux), so the next layers' dW GEMMs do not queue behind it.  The
+      // first layer's update, whose gradients all come from the main stream,
+      // follows them there, beside the end of the update before it.
+      hipStream_t us = M->adam_s;
+      if (last && !dw_aux[i]) {
+        us = c->stream;
+      } else {
+        HIP_OK(c, hipEventRecord(M->sync_ev[i], c->stream));
+        HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->sync_ev[i], 0));
+        if (dw_aux[i]) HIP_OK(c, hipStreamWaitEvent(M->adam_s, M->dw_ev[i], 0));
+      }
+      KTimer kt(c, GN_KCLASS_ADAM, "adam", 28.0 * R.pcount, us);
       ++M->step_updates;
       HIP_OK(c, launch_adam(M->params + R.poff, M->grads + R.poff, M->m + R.poff, M->v + R.poff,
-                            R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps,
-                            M->adam_s, last ? 16384 : 256));
+                            R.pcount, ac->efflr, ac->b1, ac->b2, ac->omb1, ac->omb2, ac->eps, us,
+                            last ? 16384 : 256));
     }
   }
   if (ac) {  // every dW on ctx->aux precedes an update the step now waits for
