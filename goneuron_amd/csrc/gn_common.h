@@ -398,9 +398,14 @@ hipError_t launch_embed_pe(const float *x, const float *E, const float *pe, int3
 // PositionalEncoding above the Embedding (the same gradient rows summed over
 // the samples, times scale), written by the same launch.
 bool embed_grad_takes_pe(int B, int T, int W);
+// upd: the step's Adam update carried by the launch (its rows, the zeroed
+// rows with g = 0, the PositionalEncoding's gradient, and upd->rest's float4
+// ranges by extra blocks); only where embed_grad_upd_ok.
+bool embed_grad_upd_ok(int B, int T, int D, int W, const float *gradE, const float *rest, int64_t stride);
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
                              int D, int W, float scale, const int32_t *bad, hipStream_t s,
-                             float *ws = nullptr, size_t ws_floats = 0, float *pe_grad = nullptr);
+                             float *ws = nullptr, size_t ws_floats = 0, float *pe_grad = nullptr,
+                             const AdamStep *upd = nullptr);
 hipError_t launch_cls_fwd(const float *x, float *out, int B, int TD, int D, hipStream_t s);
 hipError_t launch_cls_bwd(const float *g, float *gin, int B, int TD, int D, hipStream_t s);
 hipError_t launch_gap1d_fwd(const float *x, float *out, int B, int T, int D, hipStream_t s);

@@ -645,11 +645,12 @@ struct gn_model {
   int emb = -1;           // the Embedding layer (its index-error flags mask samples), or -1
   bool graph_ok = true;   // false once a capture failed: eager from then on
   // Train steps of small models: when the backward's last launch can carry
-  // Network.Step's update (the weight-gradient reduction of a first Conv2D:
-  // each gradient it writes is updated by the lane that writes it, extra
-  // blocks update every other layer), the pass leaves it out and the step
-  // launches it with the update's coefficients after the pass or its graph:
-  // no Adam launch of its own (C2 63.7 -> 60.3 us per step, same box).
+  // Network.Step's update (the weight-gradient reduction of a first Conv2D,
+  // or the gradient launch of a first Embedding: each gradient it writes is
+  // updated by the thread that writes it, extra blocks update every other
+  // layer), the pass leaves it out and the step launches it with the
+  // update's coefficients after the pass or its graph: no Adam launch of its
+  // own (C2 63.7 -> 60.3 us per step, same box).
   // upd_want asks the current pass for it; upd_fn, upd_name, upd_units
   // describe the launch left out (null: none, the step launches Adam).
   // gn_debug_step_update.
@@ -2672,14 +2673,53 @@ static int model_backward(gn_model *M, const float *x, int B, float scale, const
         const int nch = (B + (B + Wc - 1) / Wc - 1) / ((B + Wc - 1) / Wc);
         float *peg = pe_grad;
         pe_grad = nullptr;
-        KTimer kt(c, GN_KCLASS_OTHER, "embed_grad",
-                  f4((double)R.V * R.D + 2.0 * nch * R.T * R.D +
-                     (peg ? (double)B * R.T * R.D + (double)R.T * R.D : 0.0)));
+        const double units = f4((double)R.V * R.D + 2.0 * nch * R.T * R.D +
+                                (peg ? (double)B * R.T * R.D + (double)R.T * R.D : 0.0));
         if ((size_t)2 * nch * R.T > c->scratch_floats)
           return set_err(c, GN_ERR_UNSUPPORTED, "embedding backward: %d contributing rows exceed the scratch",
                          nch * R.T);
-        HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers,
-                                    scale, M->L[M->emb].bad, c->stream, c->scratch, c->scratch_floats, peg));
+        // a first Embedding's gradient launch is the backward's last: with
+        // the step's update it is left out and carries the update (its own
+        // rows and the PositionalEncoding's inline, every other layer in
+        // extra blocks over at most two float4-aligned ranges)
+        int64_t rr0[2] = {0, 0}, rr1[2] = {0, 0};
+        bool defer = M->upd_want && !below &&
+                     embed_grad_upd_ok(B, R.T, R.D, M->workers, M->grads + R.poff, M->grads, M->region);
+        if (defer) {
+          int64_t lo = R.poff, hi = R.poff + (int64_t)R.V * R.D;  // covered inline
+          if (peg) {
+            const int64_t p0 = peg - M->grads, p1 = p0 + (int64_t)R.T * R.D;
+            if (p0 == hi) hi = p1;
+            else if (p1 == lo) lo = p0;
+            else defer = false;
+          }
+          const int64_t end = (M->nparams + 3) / 4 * 4;  // the region's zero padding past nparams is inert
+          rr0[0] = 0, rr1[0] = lo, rr0[1] = hi, rr1[1] = end;
+          if ((lo & 3) || (hi & 3) || end > M->region) defer = false;
+        }
+        if (defer) {
+          const float *g = R.gout;
+          const int32_t *ids = R.ids, *bad = M->L[M->emb].bad;
+          float *gE = M->grads + R.poff, *rest = M->grads, *ws = c->scratch;
+          const size_t wsf = c->scratch_floats;
+          const int V = R.V, T = R.T, D = R.D, W = M->workers;
+          hipStream_t st = c->stream;
+          M->upd_fn = [=](const AdamStep &a) {
+            AdamStep u = a;
+            u.rest = rest;
+            for (int r = 0; r < 2; ++r) {
+              u.r0[r] = rr0[r];
+              u.r1[r] = rr1[r];
+            }
+            return launch_embed_grad(g, ids, gE, V, B, T, D, W, scale, bad, st, ws, wsf, peg, &u);
+          };
+          M->upd_name = "embed_grad_adam";
+          M->upd_units = units + 28.0 * M->nparams;
+        } else {
+          KTimer kt(c, GN_KCLASS_OTHER, "embed_grad", units);
+          HIP_OK(c, launch_embed_grad(R.gout, R.ids, M->grads + R.poff, R.V, B, R.T, R.D, M->workers, scale,
+                                      M->L[M->emb].bad, c->stream, c->scratch, c->scratch_floats, peg));
+        }
         if (below && below->gout)  // indices carry no gradient (embedding.go:156-163)
           HIP_OK(c, launch_fill(below->gout, 0.0f, (int64_t)B * R.T, c->stream));
         is_dz = false;

@@ -129,18 +129,49 @@ constexpr int EG_ZR = 32;
 // which this Embedding sits, pe_grad[e] = scale * sum over the B samples of
 // g[b][e], b ascending (the same gradient rows; transformer.go:112-118), 256
 // columns e of the T x D table per block.
+// With the step's update (ad.stride; launch_embed_grad's upd): every
+// gradient written here is updated by the thread that writes it (the zeroed
+// rows too, with g = 0), and blocks past the PositionalEncoding's update the
+// float4 groups of ad.rest's ranges (every other layer, whose gradients are
+// final and whose parameters no later kernel of the step reads).
+__device__ __forceinline__ void adam_g4(float4 *g4, float4 gv, const AdamStep &ad, float4 p, float4 m,
+                                        float4 v) {
+  adam1(p.x, gv.x, m.x, v.x, ad.efflr, ad.b1, ad.b2, ad.omb1, ad.omb2, ad.eps);
+  adam1(p.y, gv.y, m.y, v.y, ad.efflr, ad.b1, ad.b2, ad.omb1, ad.omb2, ad.eps);
+  adam1(p.z, gv.z, m.z, v.z, ad.efflr, ad.b1, ad.b2, ad.omb1, ad.omb2, ad.eps);
+  adam1(p.w, gv.w, m.w, v.w, ad.efflr, ad.b1, ad.b2, ad.omb1, ad.omb2, ad.eps);
+  const int64_t s4 = ad.stride >> 2;
+  g4[-s4] = p;
+  g4[s4] = m;
+  g4[2 * s4] = v;
+}
+
 __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict__ g,
                                                          const int32_t *__restrict__ ids,
                                                          float *__restrict__ gradE, int B, int T,
                                                          int D, int chunk, int L, float scale,
                                                          const int32_t *__restrict__ bad, int par,
-                                                         int V, float *__restrict__ pe_grad) {
+                                                         int V, float *__restrict__ pe_grad, AdamStep ad,
+                                                         int pb) {
   __shared__ int sid[EG_MAXL];
   __shared__ int csamp[EG_MAXL];
   __shared__ int first;
   __shared__ int hit[EG_ZR];
   const int l = blockIdx.x, nch = L / T;
   const int zb = (V + EG_ZR - 1) / EG_ZR;
+  if (l >= L + zb + pb) {  // update blocks: one float4 group of ad.rest's ranges per thread and pass
+    const int nb = gridDim.x - (L + zb + pb), bi = l - (L + zb + pb);
+    const int64_t s4 = ad.stride >> 2;
+    for (int r = 0; r < 2; ++r) {
+      float4 *g4 = reinterpret_cast<float4 *>(ad.rest);
+      for (int64_t i = (ad.r0[r] >> 2) + (int64_t)bi * 256 + threadIdx.x; i < (ad.r1[r] >> 2);
+           i += (int64_t)nb * 256) {
+        const float4 gv = g4[i], p = g4[i - s4], m = g4[i + s4], v = g4[i + 2 * s4];
+        adam_g4(g4 + i, gv, ad, p, m, v);
+      }
+    }
+    return;
+  }
   if (l >= L + zb) {  // PositionalEncoding block (uniform over the block)
     const int64_t n = (int64_t)T * D, e = (int64_t)(l - L - zb) * 256 + threadIdx.x;
     if (e >= n) return;
@@ -155,6 +186,7 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
     }
     for (; b < B; ++b) acc += g[(int64_t)b * n + e];
     pe_grad[e] = acc * scale;
+    if (ad.stride) adam_at(pe_grad + e, acc * scale, ad);
     return;
   }
   for (int w = threadIdx.x; w < nch; w += 256) {
@@ -191,9 +223,36 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
     if ((D & 3) == 0 && (reinterpret_cast<uintptr_t>(base) & 15) == 0) {
       // 16-byte stores, row and column from one 32-bit division per store
       const int D4 = D >> 2, n4 = (z1 - z0) * D4;
-      for (int e = threadIdx.x; e < n4; e += 256) {
-        const int r = e / D4;
-        if (!hit[r]) reinterpret_cast<float4 *>(base)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 *b4 = reinterpret_cast<float4 *>(base);
+      if (ad.stride) {  // zero gradients and their update; a thread's p, m, v loads go out together
+        constexpr int ZG = EG_ZR * 256 / 4 / 256;  // float4 groups per thread at D <= 256
+        const int64_t s4 = ad.stride >> 2;
+        for (int e0 = threadIdx.x; e0 < n4; e0 += ZG * 256) {
+          float4 p[ZG], m[ZG], v[ZG];
+#pragma unroll
+          for (int u = 0; u < ZG; ++u) {
+            const int e = e0 + u * 256;
+            if (e < n4 && !hit[e / D4]) {
+              p[u] = b4[e - s4];
+              m[u] = b4[e + s4];
+              v[u] = b4[e + 2 * s4];
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < ZG; ++u) {
+            const int e = e0 + u * 256;
+            if (e < n4 && !hit[e / D4]) {
+              const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+              b4[e] = z;
+              adam_g4(b4 + e, z, ad, p[u], m[u], v[u]);
+            }
+          }
+        }
+      } else {
+        for (int e = threadIdx.x; e < n4; e += 256) {
+          const int r = e / D4;
+          if (!hit[r]) b4[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
     } else {
       const int n = (z1 - z0) * D;
@@ -233,6 +292,7 @@ __global__ __launch_bounds__(256) void embed_grad_kernel(const float *__restrict
       acc += g[((int64_t)csamp[e / T] * T + e % T) * D + d];
     }
     gradE[(int64_t)my * D + d] = acc * scale;
+    if (ad.stride) adam_at(gradE + (int64_t)my * D + d, acc * scale, ad);
   }
 }
 
@@ -1316,14 +1376,31 @@ static int embed_grad_rows(int B, int T, int W) {
 
 bool embed_grad_takes_pe(int B, int T, int W) { return B > 0 && embed_grad_rows(B, T, W) <= EG_MAXL; }
 
+bool embed_grad_upd_ok(int B, int T, int D, int W, const float *gradE, const float *rest, int64_t stride) {
+  return B > 0 && embed_grad_rows(B, T, W) <= EG_MAXL && D % 4 == 0 && D <= 256 && stride > 0 &&
+         stride % 4 == 0 && ((reinterpret_cast<uintptr_t>(gradE) | reinterpret_cast<uintptr_t>(rest)) & 15) == 0;
+}
+
 hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, int V, int B, int T,
                              int D, int W, float scale, const int32_t *bad, hipStream_t s, float *ws,
-                             size_t ws_floats, float *pe_grad) {
+                             size_t ws_floats, float *pe_grad, const AdamStep *upd) {
   const int Wc = W < 1 ? 1 : (W > B ? B : W);
   const int chunk = (B + Wc - 1) / Wc;
   const int L = embed_grad_rows(B, T, W);
   const int zb = (V + EG_ZR - 1) / EG_ZR;
   if (pe_grad && !embed_grad_takes_pe(B, T, W)) return hipErrorInvalidValue;
+  AdamStep ad{};
+  int nrest = 0;
+  if (upd) {
+    ad = *upd;
+    if (!embed_grad_upd_ok(B, T, D, W, gradE, ad.rest, ad.stride)) return hipErrorInvalidValue;
+    int64_t n4 = 0;
+    for (int r = 0; r < 2; ++r) {
+      if (ad.r1[r] < ad.r0[r] || ((ad.r0[r] | ad.r1[r]) & 3)) return hipErrorInvalidValue;
+      n4 += (ad.r1[r] - ad.r0[r]) >> 2;
+    }
+    nrest = (int)std::min<int64_t>((n4 + 255) / 256, 16384);
+  }
   if (L > EG_MAXL) {
     // the row lists in the caller's workspace: 2 L ints
     if (!ws || ws_floats < (size_t)2 * L) return hipErrorInvalidValue;
@@ -1335,8 +1412,8 @@ hipError_t launch_embed_grad(const float *g, const int32_t *ids, float *gradE, i
     return hipGetLastError();
   }
   const int pb = pe_grad ? (int)(((int64_t)T * D + 255) / 256) : 0;
-  hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb + pb), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk, L,
-                     scale, bad, W > 1 ? 1 : 0, V, pe_grad);
+  hipLaunchKernelGGL(embed_grad_kernel, dim3(L + zb + pb + nrest), dim3(256), 0, s, g, ids, gradE, B, T, D, chunk,
+                     L, scale, bad, W > 1 ? 1 : 0, V, pe_grad, ad, pb);
   return hipGetLastError();
 }
 

@@ -1,20 +1,22 @@
 """GPU: Network.Step's update carried by the backward's last launch.
 
 A train step of a small model (under 8 Mi parameters) whose backward ends in
-the weight-gradient reduction of a first Conv2D runs the Adam update
-(Adam.NewStep + StepInPlace, opt.go:237-258) in that launch instead of a
-launch of its own: each gradient the reduction writes is updated by the lane
-that writes it, and extra blocks of the launch update every other layer
-(their gradients are final and no later kernel of the step reads their
-parameters).  Other models keep the update as its own launch.
+the weight-gradient reduction of a first Conv2D, or in the gradient launch of
+a first Embedding, runs the Adam update (Adam.NewStep + StepInPlace,
+opt.go:237-258) in that launch instead of a launch of its own: each gradient
+the launch writes is updated by the thread that writes it (an Embedding's
+zeroed rows with g = 0, a PositionalEncoding's gradient summed by the same
+launch too), and extra blocks of the launch update every other layer (their
+gradients are final and no later kernel of the step reads their parameters).
+Other models keep the update as its own launch.
 
 Each case trains two copies of a model from the same weights for four steps
 (the first eager, the second captured into a graph, the others replayed),
 one as above and one with gn_debug_step_update(0) (the update always as its
 own launch), and requires parameters, gradients and Adam moments to be equal
 bit for bit after every step; the per-launch timing records show which path
-ran.  The oracle parity of these steps is covered by the model tests (C2 and
-the two-conv CNN go through the same train step).
+ran.  The oracle parity of these steps is covered by the model tests (C2, C4
+and the two-conv CNN go through the same train step).
 """
 import numpy as np
 import pytest
@@ -45,6 +47,10 @@ def cases():
                                        "act": "tanh"},
                                       {"kind": "flatten", "n": 64}, _dense(64, 1, "linear")]), 1,
                          "wgrad_reduce_adam")
+    # a first Embedding (+ PositionalEncoding) under a transformer block: the
+    # Embedding's gradient launch carries the update (C4's shape, small)
+    out["gpt_small"] = (configs.gpt(B=4, T=32, vocab=37, dim=32, heads=2, ff=48), 1, "embed_grad_adam")
+    out["gpt_w2"] = (configs.gpt(B=6, T=16, vocab=29, dim=64, heads=4, ff=40), 2, "embed_grad_adam")
     # models whose backward ends elsewhere: the update keeps its own launch
     out["mlp_w4"] = (configs.mlp(), 4, None)
     out["three_dense"] = (dict(num=47, name="three_dense", B=70, loss="ce", lr=1e-3, x="normal", in_len=10,
